@@ -1,0 +1,197 @@
+/*
+ * warpgbm_amd -- C ABI of the MI355X (gfx950) hot path of WarpGBM.
+ *
+ * All pointers are device pointers (HIP global memory) unless stated
+ * otherwise; `stream` is a hipStream_t passed as void* (NULL = default
+ * stream).  Every call is asynchronous on `stream` and returns 0 on success,
+ * a hipError_t value on a HIP failure, or WGBM_EINVAL / WGBM_ENOMEM; the
+ * message is available from wgbm_last_error() (thread-local).  Calls never
+ * print, and they validate shapes and ranges before launching anything.
+ *
+ * Arithmetic contract (see the reference semantics cited at each entry):
+ *  - histogram gradient sums are exact sums of the residuals quantised to
+ *    q = rint(r * 2^s) with a power-of-two scale chosen from max|r| of the
+ *    call (at most 28 significant bits per value), rounded once to float32;
+ *    counts are exact.  Results do not depend on row order or launch shape.
+ *  - split gains/directions are bit-identical to a sequential float32 scan.
+ *  - predictions add trees in tree order (deterministic).
+ */
+#ifndef WARPGBM_AMD_H
+#define WARPGBM_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WGBM_EINVAL 1000
+#define WGBM_ENOMEM 1001
+
+/* Library version string. */
+const char* wgbm_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char* wgbm_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Reference-compatible operators.  Each replaces one function bound by the
+ * reference's pybind module (warpgbm/cuda/node_kernel.cpp:41-47).
+ * ------------------------------------------------------------------------ */
+
+/* compute_histogram3 -- replaces launch_histogram_kernel_cuda_configurable
+ * (warpgbm/cuda/histogram_kernel.cu:63-104, bound at node_kernel.cpp:43).
+ * For each position p < n_samples, row s = sample_indices[p], era
+ * e = era_indices[s] (ignored when num_eras == 1), and each output feature
+ * f < n_feats with code b = bin_indices[s * n_feats_master + feature_indices[f]]:
+ * if 0 <= b < num_bins:  grad_hist[e,f,b] += residual[s];  hess_hist[e,f,b] += 1.
+ * grad_hist / hess_hist: float32 [num_eras, n_feats, num_bins], ACCUMULATED
+ * into (the caller zeroes them, as the reference's caller does).  Rows whose
+ * era is outside [0, num_eras) are skipped.  threads_per_block and
+ * rows_per_thread are accepted for signature compatibility and ignored. */
+int wgbm_compute_histogram3(const int8_t* bin_indices, int64_t n_rows, int64_t n_feats_master,
+                            const float* residuals, const int32_t* sample_indices,
+                            int64_t n_samples, const int32_t* feature_indices, int64_t n_feats,
+                            const int32_t* era_indices, int32_t num_eras, float* grad_hist,
+                            float* hess_hist, int32_t num_bins, int32_t threads_per_block,
+                            int32_t rows_per_thread, void* stream);
+
+/* compute_split -- replaces launch_directional_split_kernel
+ * (warpgbm/cuda/best_split_kernel.cu:61-88, bound at node_kernel.cpp:42).
+ * G, H: float32 [num_eras, n_feats, num_bins]; per_era_gain and
+ * per_era_direction: float32 [num_eras, n_feats, num_bins - 1], overwritten.
+ * min_split_gain is accepted and unused, as in the reference kernel. */
+int wgbm_compute_split(const float* G, const float* H, int32_t num_eras, int32_t n_feats,
+                       int32_t num_bins, float min_split_gain, float min_child_samples,
+                       float eps, float* per_era_gain, float* per_era_direction,
+                       int32_t threads, void* stream);
+
+/* custom_cuda_binner -- replaces launch_bin_column_kernel
+ * (warpgbm/cuda/binner.cu:27-52, bound at node_kernel.cpp:44).
+ * bin_indices[i] = number of leading edges with X[i] >= edge (NaN -> 0). */
+int wgbm_custom_cuda_binner(const float* X, int64_t n, const float* bin_edges, int32_t n_edges,
+                            int8_t* bin_indices, void* stream);
+
+/* predict_forest -- replaces predict_with_forest (warpgbm/cuda/predict.cu:48-76,
+ * bound at node_kernel.cpp:45).  tree_tensor: float32 [n_trees, max_nodes, 6]
+ * rows (feature, bin, left, right, is_leaf, leaf_value) as written by the
+ * reference's flatten_tree; out[i] += learning_rate * leaf, trees added in
+ * tree order.  A walk that leaves the table contributes NaN. */
+int wgbm_predict_forest(const int8_t* bin_indices, int64_t n, int64_t n_feats,
+                        const float* tree_tensor, int64_t n_trees, int64_t max_nodes,
+                        float learning_rate, float* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Batched entry points (no single reference counterpart; each batches the
+ * per-node / per-feature / per-tree reference calls named in its comment).
+ * ------------------------------------------------------------------------ */
+
+/* Multi-segment histogram: the positions order[seg[k] .. seg[k+1]) are the
+ * rows of segment k (a node; cf. the per-node sample_indices of
+ * warpgbm/core.py:551-562).  codes: int8 [n_rows, stride] row-major,
+ * features 0..n_feats-1.  G, H: float32 [n_seg, n_feats, num_bins],
+ * accumulated into.  seg is a device int64 array [n_seg + 1]; n_pos is
+ * seg[n_seg] (known to the caller). */
+int wgbm_histogram_segments(const int8_t* codes, int64_t n_rows, int64_t stride, int32_t n_feats,
+                            const float* residuals, const int32_t* order, const int64_t* seg,
+                            int32_t n_seg, int64_t n_pos, int32_t num_bins, float* G, float* H,
+                            void* stream);
+
+/* Quantile edges (the torch.quantile call of warpgbm/core.py:529-534) from
+ * columns already sorted ascending (NaN last): sorted float32 [n_feats, n];
+ * q float32 [nq]; edges float32 [n_feats, nq]. */
+int wgbm_quantile_edges(const float* sorted, int64_t n, int32_t n_feats, const float* q,
+                        int32_t nq, float* edges, void* stream);
+
+/* Batched binner (the per-feature loop of warpgbm/core.py:527-538 and
+ * 908-913 in one launch).  X float32 [n, n_feats] with row stride x_stride
+ * (elements); edges float32 [n_feats, n_edges] sorted per feature.  Writes
+ * codes_rm int8 [n, codes_stride] (padding bytes = -1) and, if codes_cm is
+ * not NULL, codes_cm int8 [n_feats, n] (column-major copy). */
+int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride,
+                    const float* edges, int32_t n_edges, int8_t* codes_rm, int64_t codes_stride,
+                    int8_t* codes_cm, void* stream);
+
+/* Pre-binned int8 input (warpgbm/core.py:502-505): copy [n, n_feats] with
+ * row stride x_stride bytes into the padded row-major and column-major
+ * layouts used by wgbm_bin_matrix. */
+int wgbm_copy_prebinned(const int8_t* X, int64_t n, int32_t n_feats, int64_t x_stride,
+                        int8_t* codes_rm, int64_t codes_stride, int8_t* codes_cm, void* stream);
+
+/* Single-launch ensemble inference over heap-ordered trees (replaces the
+ * per-tree launches of warpgbm/core.py:1010-1026 and the single launch of
+ * :928-930).  Tree t = round * K + k, node h has children 2h+1 / 2h+2;
+ * feat[t*H + h] >= 0 splits on that feature (left if code <= bin), -1 is a
+ * leaf with value leaf[t*H + h].  out float32 [n, K] row-major, pre-filled
+ * with the initial scores; tree contributions added round by round. */
+int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, const int32_t* feat,
+                      const int32_t* bin, const float* leaf, int32_t n_rounds, int32_t K,
+                      int32_t H, int32_t max_depth, float learning_rate, float* out,
+                      void* stream);
+
+/* In-place row softmax of float32 [n, K] (warpgbm/metrics.py:12-15). */
+int wgbm_softmax_rows(float* x, int64_t n, int32_t K, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Level-wise boosting engine (the caller of the four operators:
+ * warpgbm/core.py grow_forest 692-744, grow_forest_multiclass 746-818,
+ * grow_tree 597-658).
+ * ------------------------------------------------------------------------ */
+typedef struct wgbm_engine wgbm_engine;
+
+typedef struct wgbm_engine_config {
+  int64_t n_rows;
+  int32_t n_feats;
+  int64_t codes_stride;       /* multiple of 16, >= n_feats */
+  int32_t num_bins;           /* 2..127 */
+  int32_t num_eras;
+  int32_t max_depth;
+  int32_t n_trees;            /* 1 (regression) or K (softmax) */
+  int32_t objective;          /* 0 regression, 1 softmax */
+  float min_child_weight;
+  float min_split_gain;
+  float l2_reg;
+  float learning_rate;
+  const int8_t* codes_rm;     /* [n_rows, codes_stride] */
+  const int8_t* codes_cm;     /* [n_feats, n_rows] */
+  const int32_t* root_order;  /* [n_rows] row ids sorted by era, ascending inside */
+  const int64_t* era_start;   /* [num_eras + 1] */
+} wgbm_engine_config;
+
+/* Heap-ordered record of the trees grown in one round; H = 2^(max_depth+1)-1.
+ * feat: split feature, -1 leaf, -2 absent; count: rows in the node;
+ * gain: per-era gains of the chosen split [n_trees, H, num_eras]. */
+typedef struct wgbm_tree_record {
+  int32_t* feat;   /* [n_trees, H] */
+  int32_t* bin;    /* [n_trees, H] */
+  float* leaf;     /* [n_trees, H] */
+  int64_t* count;  /* [n_trees, H] */
+  float* gain;     /* [n_trees, H, num_eras] */
+  int32_t H;
+} wgbm_tree_record;
+
+int wgbm_engine_create(wgbm_engine** out, const wgbm_engine_config* cfg);
+/* One boosting round.  target: float32 y [n_rows] (regression) or int32
+ * labels [n_rows] (softmax); pred: float32 [n_rows] or [n_rows, K],
+ * updated in place; feat_sel: int32 [n_sel] features of this round's trees
+ * (colsample_bytree subset, local order). */
+int wgbm_engine_round(wgbm_engine* eng, const void* target, float* pred, const int32_t* feat_sel,
+                      int32_t n_sel, const wgbm_tree_record* rec, void* stream);
+/* Tuning knobs: key 1 = histogram tile rows (0 = automatic). */
+int wgbm_engine_set_tuning(wgbm_engine* eng, int32_t key, int64_t value);
+void wgbm_engine_destroy(wgbm_engine* eng);
+
+/* ------------------------------------------------------------------------
+ * Instrumentation: HIP-event timing of selected kernels (tags
+ * "hist_tiles", "engine_hist_tiles").  Reading synchronises the events.
+ * ------------------------------------------------------------------------ */
+void wgbm_timer_enable(int32_t on);
+int wgbm_timer_read(const char* tag, double* total_ms, int64_t* count);
+void wgbm_timer_reset(void);
+/* Free the library's scratch buffers (all devices / streams). */
+void wgbm_release_scratch(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WARPGBM_AMD_H */

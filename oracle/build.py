@@ -1,0 +1,30 @@
+"""Build the oracle's C helpers (test infrastructure): gcc -> oracle/_build/liboracle.so.
+
+The reference's own native code (warpgbm/cuda/*.cu) is CUDA and needs nvcc,
+which this image lacks, so there is no oracle/_ref build: the oracle is the
+restatement in this package, pinned by the checks in tests/test_oracle_pins.py.
+"""
+from __future__ import annotations
+
+import subprocess
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+SRC = HERE / "csrc" / "oracle.c"
+OUT = HERE / "_build" / "liboracle.so"
+
+
+def build() -> Path:
+    OUT.parent.mkdir(parents=True, exist_ok=True)
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = ["gcc", "-O2", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
+           "-std=c11", str(SRC), "-o", str(tmp), "-lm"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{r.stderr}")
+    tmp.replace(OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build())

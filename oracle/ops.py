@@ -1,0 +1,300 @@
+"""numpy restatements of WarpGBM's native operators (CPU oracle; test-only).
+
+Conventions
+* float32 arithmetic is done with numpy float32 arrays/scalars; every
+  operation rounds to float32 (x86-64 SSE, no extended precision, no FMA).
+* "exact" histograms use the arithmetic of the HIP library: each residual is
+  quantised to q = rint(r * 2^s) (exact scaling by a power of two), sums of q
+  are exact integers, and a float32 value is produced once by rounding
+  ldexp(sum, -s).  The shift s comes from max|r| (see shift_from_absmax).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+
+
+# --------------------------------------------------------------------------- quantisation
+def qbits_for_rows(n: int) -> int:
+    """Significant bits per quantised residual for up to n rows: keeps
+    |sum q| < 2^53 (so sums convert to float64 exactly); at most 28."""
+    bl = int(n).bit_length()
+    return int(min(28, max(8, 52 - bl)))
+
+
+def shift_from_absmax(m, qbits: int) -> int:
+    """s such that max|r| * 2^s < 2^qbits: with m = f * 2^e, f in [0.5, 1)."""
+    m = F32(m)
+    if not (m > 0):
+        return 0
+    _, e = np.frexp(m)
+    return int(qbits - int(e))
+
+
+def quantise(r: np.ndarray, s: int) -> np.ndarray:
+    """q = rint(r * 2^s) as int64 (ties to even); r * 2^s is exact in float32."""
+    return np.rint(np.ldexp(np.asarray(r, dtype=F32), s)).astype(np.int64)
+
+
+def dequantise(Q, s: int) -> np.ndarray:
+    """float32(ldexp(Q, -s)): one rounding of an exact value (|Q| < 2^53)."""
+    return np.ldexp(np.asarray(Q, dtype=np.int64).astype(np.float64), -s).astype(F32)
+
+
+def leaf_value(sq: int, count: int, s: int) -> np.float32:
+    """Node mean of the quantised residuals: float32(ldexp(sq, -s) / count),
+    float64 arithmetic (the reference's residual[node_indices].mean(),
+    warpgbm/core.py:599 and :614)."""
+    return F32(np.ldexp(np.float64(sq), -s) / np.float64(count))
+
+
+# --------------------------------------------------------------------------- histogram
+def histogram_exact_q(codes, q, rows, feats, era, E: int, B: int):
+    """Exact integer histogram (restates warpgbm/cuda/histogram_kernel.cu:33-59
+    with integer sums): Q[e, f, b] = sum of q[s], C[e, f, b] = number of s,
+    over s in rows with e = era[s] (all 0 when E == 1) and
+    b = codes[s, feats[f]] in [0, B).  codes: int8 [N, >=max(feats)+1]."""
+    rows = np.asarray(rows, dtype=np.int64)
+    feats = np.asarray(feats, dtype=np.int64)
+    F = len(feats)
+    Q = np.zeros((E, F, B), dtype=np.int64)
+    C = np.zeros((E, F, B), dtype=np.int64)
+    if len(rows) == 0:
+        return Q, C
+    qs = np.asarray(q, dtype=np.int64)[rows]
+    es = np.zeros(len(rows), np.int64) if E == 1 else np.asarray(era, np.int64)[rows]
+    ok_e = (es >= 0) & (es < E)
+    for fi, f in enumerate(feats):
+        b = np.asarray(codes[rows, f], dtype=np.int64)
+        ok = ok_e & (b >= 0) & (b < B)
+        idx = es[ok] * B + b[ok]
+        # float64 weights: every partial sum is an integer below 2^53, hence exact
+        Q[:, fi, :] = np.rint(np.bincount(idx, weights=qs[ok].astype(np.float64),
+                                          minlength=E * B)).astype(np.int64).reshape(E, B)
+        C[:, fi, :] = np.bincount(idx, minlength=E * B).reshape(E, B)
+    return Q, C
+
+
+def histogram_exact(codes, resid, rows, feats, era, E: int, B: int, qbits=None):
+    """float32 G, H of one compute_histogram3 call in the HIP library's
+    arithmetic: scale from max|resid| over ``rows``, exact sums, one rounding."""
+    rows = np.asarray(rows, dtype=np.int64)
+    r = np.asarray(resid, dtype=F32)
+    m = np.max(np.abs(r[rows])) if len(rows) else F32(0)
+    s = shift_from_absmax(m, qbits_for_rows(max(len(rows), 1)) if qbits is None else qbits)
+    Q, C = histogram_exact_q(codes, quantise(r, s), rows, feats, era, E, B)
+    return dequantise(Q, s), C.astype(F32)
+
+
+def histogram_f32_seq(codes, resid, rows, feats, era, E: int, B: int):
+    """Literal restatement of histogram_kernel.cu:33-59 with the float32
+    atomics applied in ascending position order (one of the orders the
+    reference's atomics can produce): G += residual, H += 1.0f."""
+    rows = np.asarray(rows, dtype=np.int64)
+    feats = np.asarray(feats, dtype=np.int64)
+    F = len(feats)
+    G = np.zeros((E, F, B), dtype=F32)
+    H = np.zeros((E, F, B), dtype=F32)
+    r = np.asarray(resid, dtype=F32)
+    es = np.zeros(len(rows), np.int64) if E == 1 else np.asarray(era, np.int64)[rows]
+    for fi, f in enumerate(feats):
+        b = np.asarray(codes[rows, f], dtype=np.int64)
+        ok = (b >= 0) & (b < B) & (es >= 0) & (es < E)
+        # np.add.at is unbuffered and applies the adds in index order, in float32
+        np.add.at(G[:, fi, :], (es[ok], b[ok]), r[rows[ok]])
+        np.add.at(H[:, fi, :], (es[ok], b[ok]), F32(1.0))
+    return G, H
+
+
+# --------------------------------------------------------------------------- split
+def split_scan(G, H, min_child_samples, eps):
+    """Per-era gain and direction, warpgbm/cuda/best_split_kernel.cu:25-54:
+    sequential float32 totals over bins, then a sequential float32 prefix over
+    b < B-1.  Vectorised over (era, feature).  Returns gain, dir [E, F, B-1]."""
+    G = np.asarray(G, dtype=F32)
+    H = np.asarray(H, dtype=F32)
+    E, F, B = G.shape
+    mcw = F32(min_child_samples)
+    eps = F32(eps)
+    Gt = np.zeros((E, F), F32)
+    Ht = np.zeros((E, F), F32)
+    for b in range(B):
+        Gt = Gt + G[:, :, b]
+        Ht = Ht + H[:, :, b]
+    tot = (Gt * Gt) / (Ht + eps)
+    GL = np.zeros((E, F), F32)
+    HL = np.zeros((E, F), F32)
+    gain = np.zeros((E, F, B - 1), F32)
+    dirn = np.zeros((E, F, B - 1), F32)
+    for b in range(B - 1):
+        GL = GL + G[:, :, b]
+        HL = HL + H[:, :, b]
+        GR = Gt - GL
+        HR = Ht - HL
+        ok = (HL >= mcw) & (HR >= mcw)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            g = (GL * GL) / (HL + eps) + (GR * GR) / (HR + eps) - tot
+            lv = GL / (HL + eps)
+            rv = GR / (HR + eps)
+        gain[:, :, b] = np.where(ok, g, F32(0))
+        dirn[:, :, b] = np.where(ok, np.where(lv > rv, F32(1), F32(-1)), F32(0))
+    return gain, dirn
+
+
+def des_criterion(gain, dirn):
+    """(crit, agree) over [F, B-1] from per-era arrays (warpgbm/core.py:577-583).
+    E == 1: crit = gain[0].  E > 1: crit = float32(sum_e gain_e / E) with the
+    era sum in float64, sequential in era order; agree = |sum_e dir_e|, an
+    exact integer (the reference's |mean_e dir| is that integer over E)."""
+    gain = np.asarray(gain, dtype=F32)
+    E = gain.shape[0]
+    if E == 1:
+        return gain[0].copy(), None
+    acc = np.zeros(gain.shape[1:], np.float64)
+    for e in range(E):  # sequential era order
+        acc = acc + gain[e].astype(np.float64)
+    crit = (acc / np.float64(E)).astype(F32)
+    agree = np.abs(np.rint(np.asarray(dirn, dtype=np.float64)).astype(np.int64).sum(axis=0))
+    return crit, agree
+
+
+def des_select(gain, dirn, min_split_gain):
+    """Best (local feature, bin) or (-1, -1), warpgbm/core.py:577-594:
+    mask = crit > min_split_gain (and agree == max agree when E > 1);
+    first flat index of the masked maximum (torch.argmax takes the first)."""
+    crit, agree = des_criterion(gain, dirn)
+    msg = F32(min_split_gain)
+    mask = crit > msg
+    if agree is not None:
+        mask &= agree == agree.max()
+    if not mask.any():
+        return -1, -1
+    masked = np.where(mask, crit, F32(-np.inf))
+    idx = int(np.argmax(masked.reshape(-1)))  # first maximum
+    nb = gain.shape[2]
+    return idx // nb, idx % nb
+
+
+# --------------------------------------------------------------------------- binning
+def bin_column(x, edges):
+    """warpgbm/cuda/binner.cu:17-23: bin = number of LEADING edges with
+    x >= edge (the linear scan stops at the first failure; NaN x -> 0)."""
+    x = np.asarray(x, dtype=F32)
+    e = np.asarray(edges, dtype=F32)
+    if e.size == 0:
+        return np.zeros(x.shape, np.int8)
+    ge = x[:, None] >= e[None, :]
+    return np.cumprod(ge, axis=1).sum(axis=1).astype(np.int8)
+
+
+def quantile_levels(num_bins: int) -> np.ndarray:
+    """torch.linspace(0, 1, B + 1)[1:-1] in float32 (warpgbm/core.py:529-531),
+    via torch's own CPU linspace."""
+    import torch
+
+    return torch.linspace(0, 1, num_bins + 1, dtype=torch.float32)[1:-1].numpy().copy()
+
+
+def quantile_edges_sorted(s, q):
+    """torch.quantile(x, q) (linear interpolation) from ascending-sorted x,
+    float32: rank = q*(n-1); lo = floor, hi = ceil; w = rank - lo;
+    d = b - a; edge = w < 0.5 ? fma(w, d, a) : fma(w - 1, d, b) (torch's lerp
+    is evaluated with fused multiply-adds); NaN anywhere -> all NaN.  The
+    fused multiply-add needs C (numpy has none): see csrc/oracle.c."""
+    from . import clib
+
+    return clib.quantile_sorted(s, q)
+
+
+def quantile_edges(X, num_bins: int) -> np.ndarray:
+    """[F, B-1] edges of every column of X (NaN sorts last, as in torch.sort)."""
+    X = np.asarray(X, dtype=F32)
+    q = quantile_levels(num_bins)
+    out = np.empty((X.shape[1], num_bins - 1), F32)
+    for f in range(X.shape[1]):
+        out[f] = quantile_edges_sorted(np.sort(X[:, f]), q)
+    return out
+
+
+def bin_matrix(X, edges) -> np.ndarray:
+    X = np.asarray(X, dtype=F32)
+    out = np.empty(X.shape, np.int8)
+    for f in range(X.shape[1]):
+        out[:, f] = bin_column(X[:, f], edges[f])
+    return out
+
+
+# --------------------------------------------------------------------------- inference
+def flatten_tree(tree, max_nodes: int) -> np.ndarray:
+    """Pre-order table (feature, bin, left, right, is_leaf, leaf_value),
+    NaN-filled (warpgbm/core.py:1215-1252)."""
+    flat = np.full((max_nodes, 6), np.nan, dtype=F32)
+    counter = [0]
+
+    def walk(node):
+        i = counter[0]
+        counter[0] += 1
+        if "leaf_value" in node:
+            flat[i, 4] = 1.0
+            flat[i, 5] = node["leaf_value"]
+            return
+        flat[i, 0] = node["feature"]
+        flat[i, 1] = node["bin"]
+        flat[i, 4] = 0.0
+        flat[i, 2] = counter[0]
+        walk(node["left"])
+        flat[i, 3] = counter[0]
+        walk(node["right"])
+
+    walk(tree)
+    return flat
+
+
+def predict_table(codes, table, lr, out):
+    """warpgbm/cuda/predict.cu:23-44 with the trees added in tree order:
+    out[i] = out[i] + float32(lr * leaf_t), t = 0..T-1.  Returns a new array."""
+    codes = np.asarray(codes)
+    table = np.asarray(table, dtype=F32)
+    out = np.array(out, dtype=F32, copy=True)
+    lr = F32(lr)
+    N = codes.shape[0]
+    T, M, _ = table.shape
+    for t in range(T):
+        node = np.zeros(N, np.int64)
+        leafv = np.full(N, np.nan, F32)
+        active = np.ones(N, bool)
+        for _ in range(M + 1):
+            nd = table[t, node]
+            is_leaf = active & (nd[:, 4] > F32(0.5))
+            leafv[is_leaf] = nd[is_leaf, 5]
+            active &= ~is_leaf
+            if not active.any():
+                break
+            feat = nd[:, 0].astype(np.int64)
+            sb = nd[:, 1].astype(np.int64)
+            c = codes[np.arange(N), np.clip(feat, 0, codes.shape[1] - 1)].astype(np.int64)
+            nxt = np.where(c <= sb, nd[:, 2], nd[:, 3]).astype(np.int64)
+            node = np.where(active, nxt, node)
+        out = out + lr * leafv
+    return out.astype(F32)
+
+
+def predict_tree_dict(codes, tree) -> np.ndarray:
+    """Leaf value reached by every row (recursive dict walk, code <= bin -> left)."""
+    codes = np.asarray(codes)
+    N = codes.shape[0]
+    out = np.empty(N, F32)
+
+    def walk(node, idx):
+        if len(idx) == 0:
+            return
+        if "leaf_value" in node:
+            out[idx] = F32(node["leaf_value"])
+            return
+        go = codes[idx, int(node["feature"])].astype(np.int64) <= int(node["bin"])
+        walk(node["left"], idx[go])
+        walk(node["right"], idx[~go])
+
+    walk(tree, np.arange(N))
+    return out

@@ -1,0 +1,106 @@
+"""Host-side error behaviour of the estimator, mirroring the reference's
+host-forceable checks (warpgbm/core.py:83-143, 216-291, 353-356, 983-984,
+1054-1055, 1118-1119).  CPU only: every check fires before device work."""
+import numpy as np
+import pytest
+
+from warpgbm_amd import WarpGBM
+from warpgbm_amd.core import _dict_to_heap, _heap_to_dict, _preorder_internal
+
+
+@pytest.mark.parametrize("kw,exc", [
+    ({"objective": "ranking"}, ValueError),
+    ({"num_bins": 1}, ValueError),
+    ({"num_bins": 128}, ValueError),
+    ({"num_bins": 10.0}, TypeError),
+    ({"max_depth": 0}, ValueError),
+    ({"learning_rate": 0.0}, ValueError),
+    ({"learning_rate": 1.5}, ValueError),
+    ({"learning_rate": "0.1"}, TypeError),
+    ({"n_estimators": 0}, ValueError),
+    ({"min_child_weight": 0}, ValueError),
+    ({"min_split_gain": -1.0}, ValueError),
+    ({"threads_per_block": 48}, ValueError),
+    ({"rows_per_thread": 17}, ValueError),
+    ({"L2_reg": -1e-3}, ValueError),
+    ({"colsample_bytree": 0.0}, ValueError),
+    ({"colsample_bytree": 1.01}, ValueError),
+])
+def test_hyperparameter_validation(kw, exc):
+    with pytest.raises(exc):
+        WarpGBM(**kw)
+
+
+def test_constructor_needs_no_gpu():
+    m = WarpGBM(num_bins=32, max_depth=5)
+    assert m.forest == [{} for _ in range(100)] and not m._is_fitted
+
+
+@pytest.mark.parametrize("args,exc,msg", [
+    (([[1.0]], np.zeros(1)), TypeError, "numpy arrays"),
+    ((np.zeros(3), np.zeros(3)), ValueError, "2-dimensional"),
+    ((np.zeros((3, 2)), np.zeros((3, 1))), ValueError, "1-dimensional"),
+    ((np.zeros((3, 2)), np.zeros(4)), ValueError, "same number of rows"),
+])
+def test_fit_argument_validation(args, exc, msg):
+    with pytest.raises(exc, match=msg):
+        WarpGBM().fit(*args)
+
+
+def test_fit_era_and_eval_validation():
+    X, y = np.zeros((4, 2)), np.zeros(4)
+    with pytest.raises(TypeError, match="era_id must be a numpy array"):
+        WarpGBM().fit(X, y, era_id=[0, 0, 1, 1])
+    with pytest.raises(ValueError, match="same length"):
+        WarpGBM().fit(X, y, era_id=np.zeros(3))
+    with pytest.raises(ValueError, match="must all be defined"):
+        WarpGBM().fit(X, y, X_eval=X)
+    with pytest.raises(ValueError, match="eval_every_n_trees"):
+        WarpGBM().fit(X, y, X_eval=X, y_eval=y, eval_every_n_trees=0)
+    with pytest.raises(ValueError, match="early_stopping_rounds"):
+        WarpGBM().fit(X, y, X_eval=X, y_eval=y, eval_every_n_trees=1, early_stopping_rounds=-2)
+    with pytest.raises(ValueError, match="Invalid eval_metric"):
+        WarpGBM().fit(X, y, X_eval=X, y_eval=y, eval_every_n_trees=1, eval_metric="auc")
+
+
+def test_binary_requires_two_classes():
+    with pytest.raises(ValueError, match="exactly 2 classes"):
+        WarpGBM(objective="binary").fit(np.zeros((6, 2)), np.array([0, 1, 2, 0, 1, 2]))
+
+
+def test_unfitted_errors():
+    m = WarpGBM()
+    with pytest.raises(ValueError, match="predict_proba only available"):
+        m.predict_proba(np.zeros((2, 2)))
+    with pytest.raises(ValueError, match="Cannot save unfitted"):
+        m.save_model("/tmp/never.pkl")
+    with pytest.raises(ValueError, match="not been fitted"):
+        m.get_feature_importance()
+    with pytest.raises(ValueError, match="not been fitted"):
+        m.get_per_era_feature_importance()
+
+
+def test_heap_dict_round_trip_and_preorder():
+    tree = {"feature": 3, "bin": 5,
+            "left": {"feature": 1, "bin": 0, "left": {"leaf_value": 1.5, "samples": 2},
+                     "right": {"leaf_value": -0.25, "samples": 3}},
+            "right": {"leaf_value": 2.0, "samples": 7}}
+    H = 7
+    f, b, v = _dict_to_heap(tree, H)
+    assert f.tolist() == [3, 1, -1, -1, -1, -1, -1]
+    cnt = np.array([12, 5, 7, 2, 3, 0, 0])
+    back = _heap_to_dict(f, b, v, cnt)
+    assert back == tree
+    assert _preorder_internal(np.array([3, 1, 2, -1, -1, -1, -1])) == [0, 1, 2]
+    assert _preorder_internal(np.array([0, -1, 4, -1, -1, 5, -1])) == [0, 2, 5]
+
+
+def test_flatten_tree_matches_reference_layout():
+    tree = {"feature": 3, "bin": 5, "left": {"leaf_value": 1.5, "samples": 2},
+            "right": {"feature": 0, "bin": 1, "left": {"leaf_value": 0.5, "samples": 1},
+                      "right": {"leaf_value": -1.0, "samples": 1}}}
+    flat = WarpGBM().flatten_tree(tree, 8).numpy()
+    assert flat[0, :5].tolist() == [3, 5, 1, 2, 0]
+    assert flat[1, 4:].tolist() == [1.0, 1.5]
+    assert flat[2, :5].tolist() == [0, 1, 3, 4, 0]
+    assert np.isnan(flat[5:]).all()

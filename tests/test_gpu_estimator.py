@@ -1,0 +1,146 @@
+"""End-to-end parity of the estimator (level-wise native engine on the GPU)
+with the oracle's restatement of the reference's recursive tree growth.
+
+Bar: identical tree dicts (features, bins, leaf values as floats, sample
+counts), identical predictions and importances (bit-exact), for regression
+softmax multiclass, era-aware DES, colsample subsets,
+warm start and save/load."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gbm, ops
+from tests.conftest import c1_data, print_case
+from warpgbm_amd import WarpGBM
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def bits(a):
+    return np.asarray(a, dtype=F32).view(np.uint32)
+
+
+def oracle_codes(model, X):
+    """Codes the oracle bins X to, with edges the oracle computes itself."""
+    edges = ops.quantile_edges(X, model.num_bins)
+    got = torch.as_tensor(model.bin_edges).cpu().numpy()
+    assert np.array_equal(bits(got), bits(edges)), "bin edges differ"
+    return ops.bin_matrix(X, edges)
+
+
+def test_c1_regression_bit_exact(gpu):
+    print_case("estimator", "C1 regression")
+    X, y = c1_data()
+    m = WarpGBM(num_bins=32, max_depth=5, n_estimators=20, learning_rate=0.1)
+    m.fit(X, y)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(num_bins=32, max_depth=5, n_estimators=20, learning_rate=0.1,
+                     min_child_weight=20, min_split_gain=0.0, L2_reg=1e-6).fit_codes(codes, y)
+    assert m.base_prediction == float(ref.base)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    p = m.predict(X)
+    assert np.array_equal(bits(p), bits(ref.predict_codes(codes)))
+    assert np.array_equal(bits(p), bits(ref.train_preds))
+    assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
+    assert np.corrcoef(p, y)[0, 1] > 0.9
+
+
+def test_multiclass_bit_exact(gpu):
+    print_case("estimator", "multiclass K=4")
+    rng = np.random.default_rng(1)
+    N, F, K = 6000, 12, 4
+    means = rng.standard_normal((K, F)) * 1.5
+    labels = rng.integers(0, K, N)
+    X = (means[labels] + rng.standard_normal((N, F))).astype(F32)
+    y = np.array(["a", "b", "c", "d"])[labels]
+    m = WarpGBM(objective="multiclass", num_bins=16, max_depth=4, n_estimators=8,
+                learning_rate=0.3, min_child_weight=10)
+    m.fit(X, y)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(objective="multiclass", num_bins=16, max_depth=4, n_estimators=8,
+                     learning_rate=0.3, min_child_weight=10).fit_codes(codes, labels)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"round {i} differs"
+    proba = m.predict_proba(X)
+    assert np.array_equal(bits(proba), bits(ref.predict_codes(codes)))
+    assert np.allclose(proba.sum(axis=1), 1.0, atol=1e-5)
+    assert (m.predict(X) == y).mean() > 0.8
+
+
+def test_era_des_prebinned_bit_exact(gpu):
+    print_case("estimator", "DES E=6 prebinned")
+    rng = np.random.default_rng(2)
+    N, F, E = 6000, 30, 6
+    X = rng.integers(0, 5, (N, F)).astype(np.int8)
+    era = np.repeat(np.arange(E), N // E)
+    sign = np.where(rng.random((E, 10)) < 0.5, -1.0, 1.0)
+    sign[:, :5] = 1.0  # features 0-4 consistent across eras, 5-9 flip
+    score = ((X[:, :10] - 2) * sign[era]).sum(axis=1) + rng.standard_normal(N)
+    y = np.digitize(score, np.quantile(score, [0.2, 0.4, 0.6, 0.8])) / 4.0
+    m = WarpGBM(num_bins=5, max_depth=4, n_estimators=6, learning_rate=0.5)
+    m.fit(X, y.astype(F32), era_id=era)
+    ref = gbm.Forest(num_bins=5, max_depth=4, n_estimators=6, learning_rate=0.5).fit_codes(
+        X, y.astype(F32), era_id=era)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
+    assert m.per_era_feature_importance_.shape == (E, F)
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
+
+
+def test_colsample_subsets_bit_exact(gpu):
+    print_case("estimator", "colsample 0.5")
+    X, y = c1_data(n=5000, f=40, seed=3)
+    m = WarpGBM(num_bins=16, max_depth=4, n_estimators=10, colsample_bytree=0.5,
+                random_state=7)
+    m.fit(X, y)
+    assert len(m.feature_subsets_) == 10 and all(len(s) == 20 for s in m.feature_subsets_)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(num_bins=16, max_depth=4, n_estimators=10).fit_codes(
+        codes, y, feat_sets=m.feature_subsets_)
+    for a, b in zip(m.forest, ref.forest):
+        assert a == b
+    m2 = WarpGBM(num_bins=16, max_depth=4, n_estimators=10, colsample_bytree=0.5,
+                 random_state=7).fit(X, y)
+    assert np.array_equal(m2.predict(X), m.predict(X))
+
+
+def test_warm_start_and_save_load(gpu, tmp_path):
+    print_case("estimator", "warm start / save-load")
+    X, y = c1_data(n=4000, f=20, seed=4)
+    full = WarpGBM(num_bins=16, max_depth=3, n_estimators=12).fit(X, y)
+    part = WarpGBM(num_bins=16, max_depth=3, n_estimators=6, warm_start=True).fit(X, y)
+    part.n_estimators = 12
+    part.fit(X, y)
+    assert part._trees_trained == 12
+    assert np.array_equal(bits(part.predict(X)), bits(full.predict(X)))
+    path = tmp_path / "m.pkl"
+    full.save_model(str(path))
+    loaded = WarpGBM().load_model(str(path))
+    assert np.array_equal(bits(loaded.predict(X)), bits(full.predict(X)))
+
+
+def test_eval_and_early_stopping(gpu):
+    print_case("estimator", "eval set")
+    X, y = c1_data(n=4000, f=20, seed=5)
+    m = WarpGBM(num_bins=16, max_depth=3, n_estimators=30, learning_rate=0.3)
+    m.fit(X[:3000], y[:3000], X_eval=X[3000:], y_eval=y[3000:], eval_every_n_trees=2,
+          early_stopping_rounds=2, eval_metric="mse")
+    assert len(m.eval_loss) >= 1 and len(m.training_loss) >= 1
+    assert m.training_loss[-1] < m.training_loss[0]
+    # eval predictions tracked during training equal predict() on the eval set
+    p = m.predict(X[3000:])
+    assert abs(((y[3000:] - p) ** 2).mean() - m.eval_loss[-1]) < 1e-4 * (1 + m.eval_loss[-1])
+
+
+def test_binary_objective(gpu):
+    print_case("estimator", "binary")
+    rng = np.random.default_rng(6)
+    X = rng.standard_normal((3000, 8)).astype(F32)
+    y = (X[:, 0] + 0.5 * X[:, 1] > 0).astype(np.int64)
+    m = WarpGBM(objective="binary", num_bins=16, max_depth=3, n_estimators=20,
+                learning_rate=0.3).fit(X, y)
+    assert m.predict_proba(X).shape == (3000, 2)
+    assert (m.predict(X) == y).mean() > 0.9

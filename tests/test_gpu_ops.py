@@ -1,0 +1,233 @@
+"""GPU parity of the reference-compatible ops (warpgbm_amd.node_kernel, i.e.
+the C ABI) and the batched entry points against the CPU oracle.
+
+Bar: bit-exact for codes, counts, histogram sums (the oracle reproduces the
+library's exact-sum arithmetic), split gains/directions and predictions; the
+literal float32 restatement of the reference histogram (sequential atomics)
+agrees within the float32 accumulation bound, stated in the test."""
+import math
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import clib, ops
+from tests.conftest import print_case
+from warpgbm_amd import device as D
+from warpgbm_amd import node_kernel
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+dev = torch.device("cuda:0")
+
+
+def t(a, dtype=None):
+    x = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        x = x.to(dtype)
+    return x.to(dev)
+
+
+def bits(a):
+    return np.asarray(a, dtype=F32).view(np.uint32)
+
+
+HIST_CASES = [
+    # name, N, Fm, B, E, n_rows_used, n_feats_used, code range
+    ("c1_like_unaligned_stride", 10000, 50, 32, 1, None, None, (0, 32)),
+    ("gathered_subset_negative_codes", 20000, 64, 32, 1, 7000, 40, (-3, 36)),
+    ("eras_3", 12000, 48, 16, 3, 9000, 48, (0, 16)),
+    ("eras_500_small_bins", 30000, 40, 5, 500, None, None, (0, 5)),
+    ("b2", 5000, 33, 2, 1, None, None, (-1, 3)),
+    ("b33_v16_edge", 6000, 100, 33, 2, 4000, 100, (0, 33)),
+    ("b34_v8", 6000, 100, 34, 1, None, None, (0, 34)),
+    ("b67_v8_edge", 4000, 70, 67, 1, None, 55, (0, 67)),
+    ("b68_v4", 4000, 70, 68, 1, None, None, (-5, 70)),
+    ("b127", 8000, 130, 127, 2, None, None, (-128, 127)),
+    ("wide_1000", 60000, 1000, 32, 1, 50000, 1000, (0, 32)),
+]
+
+
+@pytest.mark.parametrize("case", HIST_CASES, ids=[c[0] for c in HIST_CASES])
+def test_compute_histogram3_bit_exact(gpu, case):
+    name, N, Fm, B, E, nr, nf, (lo, hi) = case
+    print_case("compute_histogram3", name)
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    codes = rng.integers(lo, hi, (N, Fm)).astype(np.int8)
+    resid = (rng.standard_normal(N) * np.exp(rng.uniform(-3, 2, N))).astype(F32)
+    rows = np.arange(N) if nr is None else np.sort(rng.choice(N, nr, replace=False))
+    feats = np.arange(Fm) if nf is None else rng.permutation(Fm)[:nf]
+    era = rng.integers(0, E, N).astype(np.int32)
+    G = torch.zeros((E, len(feats), B), device=dev)
+    H = torch.zeros_like(G)
+    node_kernel.compute_histogram3(t(codes), t(resid), t(rows, torch.int32),
+                                   t(feats, torch.int32), t(era), G, H, B, 64, 4)
+    Gr, Hr = ops.histogram_exact(codes, resid, rows, feats, era, E, B)
+    assert np.array_equal(H.cpu().numpy(), Hr)
+    assert np.array_equal(bits(G.cpu().numpy()), bits(Gr))
+    if N * len(feats) <= 2_000_000:
+        # the literal reference restatement (float32 atomics in row order)
+        Gs, Hs = ops.histogram_f32_seq(codes, resid, rows, feats, era, E, B)
+        assert np.array_equal(Hs, Hr)
+        absum = np.zeros_like(Gs, dtype=np.float64)
+        rws = rows
+        es = era[rws] if E > 1 else np.zeros(len(rws), np.int64)
+        for fi, f in enumerate(feats):
+            b = codes[rws, f].astype(np.int64)
+            ok = (b >= 0) & (b < B)
+            np.add.at(absum[:, fi, :], (es[ok], b[ok]), np.abs(resid[rws[ok]]).astype(np.float64))
+        # |float32 sequential sum - exact| <= count * 2^-24 * sum|r|; the quantised
+        # exact sum is within 2^-20 * sum|r| of the true sum (28-bit residuals)
+        tol = (Hs.astype(np.float64) * 2.0**-23 + 2.0**-20) * absum + 1e-30
+        assert np.all(np.abs(G.cpu().numpy().astype(np.float64) - Gs) <= tol)
+
+
+def test_compute_histogram3_accumulates_and_handles_empty(gpu):
+    print_case("compute_histogram3", "accumulate/empty")
+    rng = np.random.default_rng(1)
+    N, Fm, B = 3000, 20, 8
+    codes = rng.integers(0, B, (N, Fm)).astype(np.int8)
+    resid = rng.standard_normal(N).astype(F32)
+    era = np.zeros(N, np.int32)
+    feats = np.arange(Fm)
+    G = torch.full((1, Fm, B), 2.5, device=dev)
+    H = torch.full((1, Fm, B), 1.0, device=dev)
+    node_kernel.compute_histogram3(t(codes), t(resid), t(np.arange(0), torch.int32),
+                                   t(feats, torch.int32), t(era), G, H, B)
+    assert torch.all(G == 2.5) and torch.all(H == 1.0)
+    node_kernel.compute_histogram3(t(codes), t(resid), t(np.arange(N), torch.int32),
+                                   t(feats, torch.int32), t(era), G, H, B)
+    Gr, Hr = ops.histogram_exact(codes, resid, np.arange(N), feats, era, 1, B)
+    assert np.array_equal(bits(G.cpu().numpy()), bits(Gr + F32(2.5)))
+    assert np.array_equal(H.cpu().numpy(), Hr + F32(1.0))
+
+
+def test_compute_histogram3_rejects_bad_input(gpu):
+    codes = torch.zeros((10, 4), dtype=torch.int8, device=dev)
+    r = torch.zeros(10, device=dev)
+    rows = torch.arange(10, dtype=torch.int32, device=dev)
+    feats = torch.arange(4, dtype=torch.int32, device=dev)
+    era = torch.zeros(10, dtype=torch.int32, device=dev)
+    G = torch.zeros((1, 4, 8), device=dev)
+    with pytest.raises(RuntimeError, match="dtype"):
+        node_kernel.compute_histogram3(codes, r.double(), rows, feats, era, G, G.clone(), 8)
+    with pytest.raises(RuntimeError, match="num_bins"):
+        node_kernel.compute_histogram3(codes, r, rows, feats, era, G, G.clone(), 9)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        node_kernel.compute_histogram3(codes.cpu(), r, rows, feats, era, G, G.clone(), 8)
+
+
+@pytest.mark.parametrize("E,F,B", [(1, 300, 32), (4, 50, 2), (7, 33, 17), (1, 5, 127)])
+def test_compute_split_bit_exact(gpu, E, F, B):
+    print_case("compute_split", E, F, B)
+    rng = np.random.default_rng(E * 1000 + F)
+    H = rng.integers(0, 60, (E, F, B)).astype(F32)
+    H[:, ::7, :] = 0  # masked features
+    G = (rng.standard_normal((E, F, B)) * np.sqrt(H + 1)).astype(F32)
+    ge = torch.empty((E, F, B - 1), device=dev)
+    de = torch.empty_like(ge)
+    node_kernel.compute_split(t(G), t(H), 0.0, 20, 1e-6, ge, de, 128)
+    gr, dr = ops.split_scan(G, H, 20, 1e-6)
+    assert np.array_equal(bits(ge.cpu().numpy()), bits(gr))
+    assert np.array_equal(de.cpu().numpy(), dr)
+
+
+def test_custom_cuda_binner_bit_exact(gpu):
+    print_case("custom_cuda_binner")
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(100003).astype(F32)
+    x[::101] = np.nan
+    for edges in (np.sort(rng.standard_normal(31)).astype(F32), rng.standard_normal(9).astype(F32),
+                  np.full(5, np.nan, F32), np.zeros(0, F32)):
+        x[:len(edges)] = edges
+        out = torch.empty(len(x), dtype=torch.int8, device=dev)
+        node_kernel.custom_cuda_binner(t(x), t(edges), out)
+        assert np.array_equal(out.cpu().numpy(), ops.bin_column(x, edges))
+
+
+def _random_tree(rng, depth, max_depth, F, B):
+    if depth == max_depth or rng.random() < 0.2:
+        return {"leaf_value": float(F32(rng.standard_normal())), "samples": 1}
+    return {"feature": int(rng.integers(F)), "bin": int(rng.integers(-1, B)),
+            "left": _random_tree(rng, depth + 1, max_depth, F, B),
+            "right": _random_tree(rng, depth + 1, max_depth, F, B)}
+
+
+def test_predict_forest_bit_exact(gpu):
+    print_case("predict_forest")
+    rng = np.random.default_rng(4)
+    N, F, B, D_ = 20000, 37, 16, 6
+    codes = rng.integers(-2, B, (N, F)).astype(np.int8)
+    trees = [_random_tree(rng, 0, D_, F, B) for _ in range(25)]
+    table = np.stack([ops.flatten_tree(tr, 2 ** (D_ + 1)) for tr in trees])
+    out = torch.full((N,), 0.75, device=dev)
+    node_kernel.predict_forest(t(codes), t(table), 0.1, out)
+    ref = ops.predict_table(codes, table, 0.1, np.full(N, F32(0.75)))
+    assert np.array_equal(bits(out.cpu().numpy()), bits(ref))
+
+
+def test_histogram_segments_bit_exact(gpu):
+    print_case("histogram_segments", "16 nodes")
+    rng = np.random.default_rng(5)
+    N, F, B, S = 40000, 200, 32, 16
+    stride = D.codes_stride(F)
+    codes = np.full((N, stride), -1, np.int8)
+    codes[:, :F] = rng.integers(0, B, (N, F))
+    resid = rng.standard_normal(N).astype(F32)
+    node = rng.integers(0, S, N)
+    order = np.argsort(node, kind="stable").astype(np.int32)
+    seg = np.zeros(S + 1, np.int64)
+    seg[1:] = np.cumsum(np.bincount(node, minlength=S))
+    G = torch.zeros((S, F, B), device=dev)
+    H = torch.zeros_like(G)
+    from warpgbm_amd import _lib
+
+    lib = _lib.load()
+    rc = lib.wgbm_histogram_segments(t(codes).data_ptr(), N, stride, F, t(resid).data_ptr(),
+                                     t(order).data_ptr(), t(seg).data_ptr(), S, N, B,
+                                     G.data_ptr(), H.data_ptr(),
+                                     _lib.current_stream_ptr(dev))
+    _lib.check(rc, "histogram_segments")
+    s = ops.shift_from_absmax(np.max(np.abs(resid)), ops.qbits_for_rows(N))
+    q = ops.quantise(resid, s)
+    Gc, Hc = G.cpu().numpy(), H.cpu().numpy()
+    for k in range(S):
+        Q, C = ops.histogram_exact_q(codes, q, order[seg[k]:seg[k + 1]], np.arange(F), None, 1, B)
+        assert np.array_equal(Hc[k], C[0].astype(F32))
+        assert np.array_equal(bits(Gc[k]), bits(ops.dequantise(Q[0], s)))
+
+
+def test_quantile_edges_and_bin_matrix(gpu):
+    print_case("quantile_edges/bin_matrix")
+    rng = np.random.default_rng(6)
+    N, F, B = 20001, 70, 32
+    X = (rng.standard_normal((N, F)) * rng.uniform(0.01, 50, F)).astype(F32)
+    X[:, 3] = np.round(X[:, 3])  # ties
+    X[::997, 5] = np.nan          # NaN column -> all edges NaN -> all codes 0
+    Xd = D.upload_float(X, dev)
+    edges = D.quantile_edges(Xd, B).cpu().numpy()
+    ref_edges = ops.quantile_edges(X, B)
+    assert np.array_equal(bits(edges), bits(ref_edges))
+    ref_torch = torch.quantile(torch.from_numpy(X[:, :4]), torch.from_numpy(ops.quantile_levels(B)),
+                               dim=0).numpy().T
+    assert np.array_equal(bits(edges[:4]), bits(ref_torch))
+    codes = D.bin_matrix(Xd, torch.from_numpy(edges), with_cm=True)
+    rm = codes.rm.cpu().numpy()
+    cm = codes.cm.cpu().numpy()
+    ref = ops.bin_matrix(X, edges)
+    assert np.array_equal(rm[:, :F], ref)
+    assert np.all(rm[:, F:] == -1)
+    assert np.array_equal(cm, ref.T)
+    assert np.all(ref[:, 5] == 0)
+
+
+def test_copy_prebinned(gpu):
+    print_case("copy_prebinned")
+    rng = np.random.default_rng(7)
+    X = rng.integers(-3, 5, (5000, 300)).astype(np.int64)
+    c = D.upload_prebinned(X, dev, with_cm=True)
+    rm = c.rm.cpu().numpy()
+    assert np.array_equal(rm[:, :300], X.astype(np.int8))
+    assert np.all(rm[:, 300:] == -1)
+    assert np.array_equal(c.cm.cpu().numpy(), X.astype(np.int8).T)

@@ -1,0 +1,441 @@
+"""Pins of the CPU oracle (oracle/) against things other than itself.
+
+The reference ships no golden vectors or known-answer tests for this path
+(its tests are statistical thresholds on a CUDA GPU), so each oracle function
+is checked here against brute force on tiny inputs, a library routine the
+reference itself calls (torch.quantile, torch.bucketize, torch.linspace),
+closed forms, and invariants chosen so that a dropped term, wrong sign,
+off-by-one bin or transposed index fails.
+
+  ops.bin_column            brute-force linear scan; torch.bucketize(right=True)
+  ops.quantile_edges_sorted torch.quantile (CPU) bit-exact
+  ops.quantile_levels       k / B within 1 ulp; torch.linspace
+  ops.quantise/dequantise   lossless for |r| >= max|r|/16; error <= 2^-(s+1)
+  ops.histogram_exact_q     brute-force integer dict; count invariants;
+                            child + sibling == parent
+  ops.histogram_exact       |G - fsum(r)| <= n 2^-(s+1) + ulp; vs f32 sequential
+  ops.histogram_f32_seq     per-row float32 loop
+  ops.split_scan            scalar float32 loop; hand KAT; gain >= 0 identity
+  ops.des_select            hand-built DES cases; first-index ties
+  ops.predict_table         recursive dict walk; stump closed form
+  gbm.Forest / TreeGrower   planted split found; leaf = group mean; train
+                            preds == predict; min_child respected
+  clib.expf / softmax       numpy float64 exp within 2 ulp; rows sum to 1
+"""
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import clib, gbm, ops
+
+F32 = np.float32
+
+
+# --------------------------------------------------------------------------- binning
+def _brute_bin(x, edges):
+    out = []
+    for v in x:
+        b = 0
+        while b < len(edges) and v >= edges[b]:
+            b += 1
+        out.append(b)
+    return np.array(out, np.int8)
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_bin_column_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(300).astype(F32)
+    x[::17] = np.nan
+    e = np.sort(rng.standard_normal(rng.integers(1, 20)).astype(F32))
+    e_unsorted = rng.standard_normal(9).astype(F32)
+    e_nan = e.copy()
+    e_nan[len(e) // 2] = np.nan
+    x[5] = e[0]  # equality goes right (x >= edge)
+    for edges in (e, e_unsorted, e_nan, np.full(4, np.nan, F32), np.array([1.0, 1.0, 1.0], F32)):
+        assert np.array_equal(ops.bin_column(x, edges), _brute_bin(x, edges))
+
+
+def test_bin_column_matches_bucketize_and_nan_rule():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(10000).astype(F32)
+    e = np.sort(rng.standard_normal(31).astype(F32))
+    x[:31] = e  # exact hits
+    ref = torch.bucketize(torch.from_numpy(x), torch.from_numpy(e), right=True).numpy()
+    assert np.array_equal(ops.bin_column(x, e), ref.astype(np.int8))
+    xn = np.array([np.nan], F32)
+    assert ops.bin_column(xn, e)[0] == 0  # reference: NaN -> 0 (bucketize would say 31)
+
+
+# --------------------------------------------------------------------------- quantile
+@pytest.mark.parametrize("B", [2, 5, 10, 32, 127])
+def test_quantile_edges_bit_exact_vs_torch_quantile(B):
+    rng = np.random.default_rng(B)
+    q = ops.quantile_levels(B)
+    for n in (1, 2, 3, 7, 100, 999, 5000):
+        for kind in ("normal", "ties", "tiny"):
+            if kind == "normal":
+                col = rng.standard_normal(n).astype(F32)
+            elif kind == "ties":
+                col = rng.integers(0, 4, n).astype(F32)
+            else:
+                col = (rng.standard_normal(n) * 1e-30).astype(F32)
+            ref = torch.quantile(torch.from_numpy(col), torch.from_numpy(q)).numpy()
+            got = ops.quantile_edges_sorted(np.sort(col), q)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (n, kind)
+
+
+def test_quantile_edges_many_random_columns_bit_exact():
+    rng = np.random.default_rng(123)
+    q = ops.quantile_levels(32)
+    X = (rng.standard_normal((4096, 64)) * rng.uniform(0.1, 100, 64)).astype(F32)
+    ref = torch.quantile(torch.from_numpy(X), torch.from_numpy(q), dim=0).numpy().T
+    got = ops.quantile_edges(X, 32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_quantile_nan_column_all_nan():
+    col = np.array([0.5, np.nan, -1.0, 2.0], F32)
+    q = ops.quantile_levels(4)
+    ref = torch.quantile(torch.from_numpy(col), torch.from_numpy(q)).numpy()
+    got = ops.quantile_edges_sorted(np.sort(col), q)
+    assert np.isnan(ref).all() and np.isnan(got).all()
+
+
+def test_quantile_levels():
+    for B in (2, 3, 10, 32, 127):
+        q = ops.quantile_levels(B)
+        assert q.dtype == F32 and len(q) == B - 1
+        k = np.arange(1, B, dtype=np.float64) / B
+        assert np.all(np.abs(q.astype(np.float64) - k) <= np.spacing(F32(1.0)))
+
+
+# --------------------------------------------------------------------------- quantisation
+def test_quantise_lossless_and_bounded():
+    rng = np.random.default_rng(0)
+    r = (rng.standard_normal(100000) * 3).astype(F32)
+    r[0] = 0.0
+    r[1] = -np.max(np.abs(r)) * 1.0
+    m = np.max(np.abs(r))
+    for n in (10, 10**6, 2**24):
+        qb = ops.qbits_for_rows(n)
+        s = ops.shift_from_absmax(m, qb)
+        q = ops.quantise(r, s)
+        assert np.max(np.abs(q)) <= 2**qb
+        back = np.ldexp(q.astype(np.float64), -s)
+        assert np.all(np.abs(back - r.astype(np.float64)) <= 2.0 ** (-s - 1))
+        # r * 2^s is an integer (lossless) once |r| >= max|r| * 2^(24 - qbits)
+        big = np.abs(r) >= m * 2.0 ** (24 - qb)
+        assert np.array_equal(back[big], r[big].astype(np.float64))
+        assert n * 2**qb < 2**53
+    assert ops.shift_from_absmax(0.0, 28) == 0
+    assert ops.qbits_for_rows(10**6) == 28
+
+
+# --------------------------------------------------------------------------- histograms
+def _tiny_hist_case(seed, E=3, B=6, N=80, Fm=7):
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(-2, B + 2, (N, Fm)).astype(np.int8)  # out-of-range both sides
+    r = rng.standard_normal(N).astype(F32)
+    rows = rng.choice(N, N // 2, replace=False)
+    feats = rng.permutation(Fm)[:5]
+    era = rng.integers(0, E, N).astype(np.int32)
+    return codes, r, rows, feats, era, E, B
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_histogram_exact_q_brute_force(seed):
+    codes, r, rows, feats, era, E, B = _tiny_hist_case(seed)
+    q = ops.quantise(r, 20)
+    Q, C = ops.histogram_exact_q(codes, q, rows, feats, era, E, B)
+    Qb = np.zeros_like(Q)
+    Cb = np.zeros_like(C)
+    for s in rows:
+        for fi, f in enumerate(feats):
+            b = int(codes[s, f])
+            if 0 <= b < B:
+                Qb[era[s], fi, b] += int(q[s])
+                Cb[era[s], fi, b] += 1
+    assert np.array_equal(Q, Qb) and np.array_equal(C, Cb)
+    # the C restatement agrees with the numpy one
+    Q2, C2 = clib.hist_exact_q(codes, q, rows, feats, era, E, B)
+    assert np.array_equal(Q, Q2) and np.array_equal(C, C2)
+
+
+def test_histogram_invariants_and_subtraction():
+    rng = np.random.default_rng(5)
+    N, Fm, B, E = 2000, 9, 8, 4
+    codes = rng.integers(0, B, (N, Fm)).astype(np.int8)
+    r = rng.standard_normal(N).astype(F32)
+    era = rng.integers(0, E, N).astype(np.int32)
+    q = ops.quantise(r, 22)
+    rows = np.arange(N)
+    Q, C = ops.histogram_exact_q(codes, q, rows, np.arange(Fm), era, E, B)
+    # every feature sees every row once: per-era totals equal across features
+    for e in range(E):
+        assert np.all(C[e].sum(axis=1) == np.count_nonzero(era == e))
+        assert np.all(Q[e].sum(axis=1) == q[era == e].sum())
+    left = rows[codes[:, 3] <= 4]
+    right = rows[codes[:, 3] > 4]
+    QL, CL = ops.histogram_exact_q(codes, q, left, np.arange(Fm), era, E, B)
+    QR, CR = ops.histogram_exact_q(codes, q, right, np.arange(Fm), era, E, B)
+    assert np.array_equal(QL + QR, Q) and np.array_equal(CL + CR, C)
+
+
+def test_histogram_exact_vs_true_sum_and_f32_sequential():
+    rng = np.random.default_rng(11)
+    N, Fm, B = 5000, 6, 16
+    codes = rng.integers(0, B, (N, Fm)).astype(np.int8)
+    r = (rng.standard_normal(N) * np.exp(rng.uniform(-6, 3, N))).astype(F32)
+    rows = rng.permutation(N)[:4000]
+    G, H = ops.histogram_exact(codes, r, rows, np.arange(Fm), None, 1, B)
+    Gs, Hs = ops.histogram_f32_seq(codes, r, rows, np.arange(Fm), np.zeros(N, np.int32), 1, B)
+    assert np.array_equal(H, Hs)
+    s = ops.shift_from_absmax(np.max(np.abs(r[rows])), ops.qbits_for_rows(len(rows)))
+    for f in range(Fm):
+        for b in range(B):
+            sel = rows[codes[rows, f] == b]
+            true = math.fsum(float(v) for v in r[sel])
+            bound = len(sel) * 2.0 ** (-s - 1) + float(np.spacing(np.abs(G[0, f, b])))
+            assert abs(float(G[0, f, b]) - true) <= bound
+            # float32 sequential accumulation error bound ~ n * eps * sum|r|
+            absum = math.fsum(abs(float(v)) for v in r[sel])
+            assert abs(float(Gs[0, f, b]) - true) <= len(sel) * 2**-24 * absum + 1e-30
+
+
+def test_histogram_f32_seq_matches_row_loop():
+    codes, r, rows, feats, era, E, B = _tiny_hist_case(9)
+    G, H = ops.histogram_f32_seq(codes, r, rows, feats, era, E, B)
+    Gb = np.zeros_like(G)
+    Hb = np.zeros_like(H)
+    for fi, f in enumerate(feats):
+        for s in rows:  # ascending position order
+            b = int(codes[s, f])
+            if 0 <= b < B:
+                Gb[era[s], fi, b] = F32(Gb[era[s], fi, b] + r[s])
+                Hb[era[s], fi, b] = F32(Hb[era[s], fi, b] + F32(1))
+    assert np.array_equal(G, Gb) and np.array_equal(H, Hb)
+
+
+# --------------------------------------------------------------------------- split
+def _scalar_split(G, H, mcw, eps):
+    E, F, B = G.shape
+    gain = np.zeros((E, F, B - 1), F32)
+    dirn = np.zeros((E, F, B - 1), F32)
+    mcw, eps = F32(mcw), F32(eps)
+    for e in range(E):
+        for f in range(F):
+            gt = F32(0)
+            ht = F32(0)
+            for b in range(B):
+                gt = F32(gt + G[e, f, b])
+                ht = F32(ht + H[e, f, b])
+            gl = F32(0)
+            hl = F32(0)
+            for b in range(B - 1):
+                gl = F32(gl + G[e, f, b])
+                hl = F32(hl + H[e, f, b])
+                gr = F32(gt - gl)
+                hr = F32(ht - hl)
+                if hl >= mcw and hr >= mcw:
+                    a1 = F32(F32(gl * gl) / F32(hl + eps))
+                    a2 = F32(F32(gr * gr) / F32(hr + eps))
+                    a3 = F32(F32(gt * gt) / F32(ht + eps))
+                    gain[e, f, b] = F32(F32(a1 + a2) - a3)
+                    lv = F32(gl / F32(hl + eps))
+                    rv = F32(gr / F32(hr + eps))
+                    dirn[e, f, b] = 1.0 if lv > rv else -1.0
+    return gain, dirn
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_split_scan_vs_scalar_loop(seed):
+    rng = np.random.default_rng(seed)
+    E, F, B = 3, 7, 9
+    H = rng.integers(0, 30, (E, F, B)).astype(F32)
+    G = (rng.standard_normal((E, F, B)) * H).astype(F32)
+    gain, dirn = ops.split_scan(G, H, 20, 1e-6)
+    g2, d2 = _scalar_split(G, H, 20, 1e-6)
+    assert np.array_equal(gain.view(np.uint32), g2.view(np.uint32))
+    assert np.array_equal(dirn, d2)
+
+
+def test_split_scan_hand_kat():
+    # one era, one feature, 3 bins: G = [3, -1, 4], H = [2, 1, 5], eps = 0, mcw = 1
+    G = np.array([[[3.0, -1.0, 4.0]]], F32)
+    H = np.array([[[2.0, 1.0, 5.0]]], F32)
+    gain, dirn = ops.split_scan(G, H, 1, 0.0)
+    # b=0: L=(3,2) R=(3,6): 9/2 + 9/6 - 36/8 = 1.5 ; left mean 1.5 > right 0.5 -> +1
+    # b=1: L=(2,3) R=(4,5): 4/3 + 16/5 - 36/8 = 1/30 ; 0.667 < 0.8 -> -1
+    exact = [Fraction(9, 2) + Fraction(9, 6) - Fraction(36, 8),
+             Fraction(4, 3) + Fraction(16, 5) - Fraction(36, 8)]
+    for b in range(2):
+        assert abs(float(gain[0, 0, b]) - float(exact[b])) <= 4 * np.spacing(F32(4.5))
+    assert dirn[0, 0].tolist() == [1.0, -1.0]
+    # min_child masking: with mcw = 3 the first threshold (HL = 2) is masked
+    gain, dirn = ops.split_scan(G, H, 3, 0.0)
+    assert gain[0, 0, 0] == 0 and dirn[0, 0, 0] == 0 and gain[0, 0, 1] != 0
+
+
+def test_split_gain_nonnegative_identity():
+    # with eps = 0 the split gain GL^2/HL + GR^2/HR - G^2/H >= 0 (Cauchy-Schwarz)
+    rng = np.random.default_rng(3)
+    H = rng.integers(1, 50, (2, 40, 12)).astype(F32)
+    G = (rng.standard_normal((2, 40, 12)) * 10).astype(F32)
+    gain, _ = ops.split_scan(G, H, 1, 0.0)
+    tot = np.abs(G.sum(axis=2)) ** 2 / H.sum(axis=2)
+    assert np.all(gain >= -1e-4 * (1 + tot[:, :, None]))
+
+
+# --------------------------------------------------------------------------- DES selection
+def test_des_select_e1_argmax_first_index():
+    gain = np.array([[[0.5, 2.0, 2.0], [2.0, 1.0, 0.0]]], F32)
+    dirn = np.sign(gain)
+    assert ops.des_select(gain, dirn, 0.0) == (0, 1)  # first of the three 2.0s
+    assert ops.des_select(gain, dirn, 5.0) == (-1, -1)
+    assert ops.des_select(np.zeros((1, 2, 3), F32), np.zeros((1, 2, 3), F32), 0.0) == (-1, -1)
+
+
+def test_des_select_prefers_consistent_direction():
+    # feature 0: large gains but directions disagree across eras;
+    # feature 1: smaller gains, same direction in all eras -> feature 1 wins
+    gain = np.array([[[9.0], [1.0]], [[9.0], [1.0]], [[9.0], [1.0]]], F32)
+    dirn = np.array([[[1.0], [1.0]], [[-1.0], [1.0]], [[1.0], [1.0]]], F32)
+    assert ops.des_select(gain, dirn, 0.0) == (1, 0)
+    # the max-agreement candidates all fail min_split_gain -> leaf, even
+    # though feature 0 passes it
+    assert ops.des_select(gain, dirn, 2.0) == (-1, -1)
+    # a masked era (dir 0, gain 0) dilutes both means equally
+    dirn2 = dirn.copy()
+    dirn2[0, 1, 0] = 0.0
+    gain2 = gain.copy()
+    gain2[0, 1, 0] = 0.0
+    # agree: f0 |1-1+1| = 1, f1 |0+1+1| = 2 -> f1 still
+    assert ops.des_select(gain2, dirn2, 0.0) == (1, 0)
+
+
+def test_des_criterion_mean_is_float64_sequential():
+    rng = np.random.default_rng(1)
+    gain = rng.standard_normal((500, 3, 4)).astype(F32)
+    crit, agree = ops.des_criterion(gain, np.sign(gain))
+    exact = np.array([[math.fsum(gain[:, f, b].astype(float)) / 500 for b in range(4)]
+                      for f in range(3)])
+    assert np.all(np.abs(crit - exact) <= 2 * np.spacing(np.abs(crit).astype(F32)) + 1e-12)
+    assert agree.dtype == np.int64
+
+
+# --------------------------------------------------------------------------- predict
+def _random_tree(rng, depth, max_depth, F, B):
+    if depth == max_depth or rng.random() < 0.25:
+        return {"leaf_value": float(F32(rng.standard_normal())), "samples": 1}
+    return {"feature": int(rng.integers(F)), "bin": int(rng.integers(-1, B)),
+            "left": _random_tree(rng, depth + 1, max_depth, F, B),
+            "right": _random_tree(rng, depth + 1, max_depth, F, B)}
+
+
+def test_predict_table_vs_dict_walk():
+    rng = np.random.default_rng(2)
+    F, B, D = 6, 8, 4
+    codes = rng.integers(-1, B, (500, F)).astype(np.int8)
+    trees = [_random_tree(rng, 0, D, F, B) for _ in range(7)]
+    table = np.stack([ops.flatten_tree(t, 2 ** (D + 1)) for t in trees])
+    lr = 0.3
+    base = np.full(500, F32(0.25), F32)
+    got = ops.predict_table(codes, table, lr, base)
+    exp = base.copy()
+    for t in trees:
+        exp = exp + F32(lr) * ops.predict_tree_dict(codes, t)
+    assert np.array_equal(got, exp)
+
+
+def test_predict_stump_closed_form():
+    codes = np.array([[0], [3], [4], [9]], np.int8)
+    stump = {"feature": 0, "bin": 3, "left": {"leaf_value": -2.0, "samples": 2},
+             "right": {"leaf_value": 5.0, "samples": 2}}
+    table = ops.flatten_tree(stump, 4)[None]
+    assert table[0, 0, 2] == 1 and table[0, 0, 3] == 2  # pre-order ids
+    got = ops.predict_table(codes, table, 0.5, np.zeros(4, F32))
+    assert got.tolist() == [-1.0, -1.0, 2.5, 2.5]
+
+
+# --------------------------------------------------------------------------- tree growth
+def test_gbm_finds_planted_split_and_group_means():
+    rng = np.random.default_rng(4)
+    N, F, B = 3000, 5, 16
+    codes = rng.integers(0, B, (N, F)).astype(np.int8)
+    y = np.where(codes[:, 2] <= 6, -3.0, 4.0).astype(F32) + F32(0.01) * rng.standard_normal(N).astype(F32)
+    f = gbm.Forest(num_bins=B, max_depth=1, n_estimators=1, learning_rate=1.0,
+                   min_child_weight=20).fit_codes(codes, y)
+    t = f.forest[0]
+    assert (t["feature"], t["bin"]) == (2, 6)
+    r = y - f.base
+    for side, sel in (("left", codes[:, 2] <= 6), ("right", codes[:, 2] > 6)):
+        assert abs(t[side]["leaf_value"] - float(np.mean(r[sel], dtype=np.float64))) < 1e-5
+        assert t[side]["samples"] == int(sel.sum())
+
+
+def test_gbm_invariants_regression():
+    rng = np.random.default_rng(8)
+    N, F, B = 4000, 8, 12
+    codes = rng.integers(0, B, (N, F)).astype(np.int8)
+    y = (codes[:, 0] * 0.3 - codes[:, 5] * 0.2 + rng.standard_normal(N)).astype(F32)
+    era = rng.integers(0, 3, N)
+    f = gbm.Forest(num_bins=B, max_depth=4, n_estimators=5, learning_rate=0.2,
+                   min_child_weight=30).fit_codes(codes, y, era_id=era)
+    assert np.array_equal(f.predict_codes(codes), f.train_preds)
+
+    def check(node, rows):
+        if "leaf_value" in node:
+            assert node["samples"] == len(rows)
+            return 1
+        go = codes[rows, node["feature"]] <= node["bin"]
+        # every era with rows on both sides satisfies min_child (count >= 30)
+        # for at least one era (the split had positive gain somewhere)
+        okl = [np.count_nonzero(era[rows[go]] == e) >= 30 for e in range(3)]
+        okr = [np.count_nonzero(era[rows[~go]] == e) >= 30 for e in range(3)]
+        assert any(a and b for a, b in zip(okl, okr))
+        return check(node["left"], rows[go]) + check(node["right"], rows[~go])
+
+    for t in f.forest:
+        assert check(t, np.arange(N)) <= 2 ** 4
+    assert f.feature_importance[0] > 0 and f.feature_importance[5] > 0
+
+
+def test_gbm_multiclass_invariants():
+    rng = np.random.default_rng(6)
+    N, F, B, K = 1500, 6, 10, 3
+    codes = rng.integers(0, B, (N, F)).astype(np.int8)
+    labels = (codes[:, 1] * K // B).astype(np.int32)
+    f = gbm.Forest(objective="multiclass", num_bins=B, max_depth=3, n_estimators=4,
+                   learning_rate=0.5, min_child_weight=10).fit_codes(codes, labels)
+    p = f.predict_codes(codes)
+    assert np.allclose(p.sum(axis=1), 1.0, atol=1e-6)
+    assert (np.argmax(p, axis=1) == labels).mean() > 0.9
+    res = clib.softmax_residual(f.train_scores, labels)
+    assert np.allclose(res.sum(axis=0), 0.0, atol=1e-6)
+
+
+# --------------------------------------------------------------------------- exp / softmax
+def test_expf_accuracy():
+    x = np.concatenate([np.linspace(-103, 88, 200001, dtype=F32),
+                        np.array([0.0, -0.0, -1e-30, 1e-30, -87.3, -88.0, -100.0], F32)])
+    got = clib.expf(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    ulp = np.spacing(ref.astype(F32)).astype(np.float64)
+    norm = ref >= np.finfo(F32).tiny
+    assert np.all(np.abs(got - ref)[norm] <= 2 * ulp[norm])
+    assert np.all(np.abs(got - ref)[~norm] <= 2 * 2.0 ** -149)
+    assert clib.expf(np.array([-200.0], F32))[0] == 0.0
+
+
+def test_softmax_rows_sum_to_one():
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal((1000, 7)) * 20).astype(F32)
+    p = clib.softmax_rows(x)
+    ref = np.exp(x - x.max(axis=1, keepdims=True))
+    ref /= ref.sum(axis=1, keepdims=True)
+    assert np.allclose(p.sum(axis=1), 1.0, atol=1e-6)
+    assert np.allclose(p, ref, rtol=1e-5, atol=1e-7)

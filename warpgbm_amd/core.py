@@ -1,0 +1,757 @@
+"""WarpGBM estimator on the MI355X hot path.
+
+Same public API as the reference estimator (warpgbm/core.py:14-1252):
+``WarpGBM(objective, num_bins, max_depth, learning_rate, n_estimators,
+min_child_weight, min_split_gain, threads_per_block, rows_per_thread, L2_reg,
+device, colsample_bytree, random_state, warm_start)`` with ``fit``,
+``predict``, ``predict_proba``, importance getters, ``save_model`` /
+``load_model`` and ``flatten_tree``; the fitted forest uses the reference's
+nested-dict tree format.
+
+What differs is how the trees are grown: the native level-wise engine builds
+every node of a depth (and all K class trees of a softmax round) per launch
+sequence, with no host synchronisation inside a round, instead of the
+reference's recursive per-node Python loop.  The trees are the same: the
+residual is fixed per tree (core.py:719), each node's decision depends only
+on its own rows, and histogram sums are exact (see include/warpgbm_amd.h).
+"""
+from __future__ import annotations
+
+import gc
+import pickle
+
+import numpy as np
+import torch
+from sklearn.base import BaseEstimator, RegressorMixin
+from sklearn.preprocessing import LabelEncoder
+
+from . import device as D
+from . import node_kernel
+from .metrics import accuracy_torch, log_loss_torch, rmsle_torch, softmax
+
+
+class WarpGBM(BaseEstimator, RegressorMixin):
+    def __init__(
+        self,
+        objective="regression",
+        num_bins=10,
+        max_depth=3,
+        learning_rate=0.1,
+        n_estimators=100,
+        min_child_weight=20,
+        min_split_gain=0.0,
+        threads_per_block=64,
+        rows_per_thread=4,
+        L2_reg=1e-6,
+        device="cuda",
+        colsample_bytree=1.0,
+        random_state=None,
+        warm_start=False,
+    ):
+        self._validate_hyperparams(
+            objective=objective,
+            num_bins=num_bins,
+            max_depth=max_depth,
+            learning_rate=learning_rate,
+            n_estimators=n_estimators,
+            min_child_weight=min_child_weight,
+            min_split_gain=min_split_gain,
+            threads_per_block=threads_per_block,
+            rows_per_thread=rows_per_thread,
+            L2_reg=L2_reg,
+            colsample_bytree=colsample_bytree,
+        )
+        self.objective = objective
+        self.num_bins = num_bins
+        self.max_depth = max_depth
+        self.learning_rate = learning_rate
+        self.n_estimators = n_estimators
+        self.min_child_weight = min_child_weight
+        self.min_split_gain = min_split_gain
+        # CUDA launch-shape knobs of the reference; accepted and validated,
+        # no effect on the HIP kernels
+        self.threads_per_block = threads_per_block
+        self.rows_per_thread = rows_per_thread
+        self.L2_reg = L2_reg
+        self.device = device
+        self.colsample_bytree = colsample_bytree
+        self.random_state = random_state
+        self.warm_start = warm_start
+        self.forest = [{} for _ in range(self.n_estimators)]
+        self.bin_edges = None
+        self.base_prediction = None
+        self.unique_eras = None
+        self.num_classes = None
+        self.classes_ = None
+        self.num_features = None
+        self.num_samples = None
+        self.label_encoder = None
+        self.feature_importance_ = None
+        self.per_era_feature_importance_ = None
+        self._is_fitted = False
+        self._trees_trained = 0
+        self._heap = None  # device heap tables of the fitted forest (cache)
+
+    # ------------------------------------------------------------------ validation
+    def _validate_hyperparams(self, **kwargs):
+        """Same checks and messages as warpgbm/core.py:83-143."""
+        if kwargs["objective"] not in ["regression", "multiclass", "binary"]:
+            raise ValueError(
+                f"objective must be 'regression', 'binary', or 'multiclass', got {kwargs['objective']}."
+            )
+        int_params = ["num_bins", "max_depth", "n_estimators", "min_child_weight",
+                      "threads_per_block", "rows_per_thread"]
+        float_params = ["learning_rate", "min_split_gain", "L2_reg", "colsample_bytree"]
+        for param in int_params:
+            if not isinstance(kwargs[param], int):
+                raise TypeError(f"{param} must be an integer, got {type(kwargs[param])}.")
+        for param in float_params:
+            if not isinstance(kwargs[param], (float, int)):
+                raise TypeError(f"{param} must be a float, got {type(kwargs[param])}.")
+        if not (2 <= kwargs["num_bins"] <= 127):
+            raise ValueError("num_bins must be between 2 and 127 inclusive.")
+        if kwargs["max_depth"] < 1:
+            raise ValueError("max_depth must be at least 1.")
+        if not (0.0 < kwargs["learning_rate"] <= 1.0):
+            raise ValueError("learning_rate must be in (0.0, 1.0].")
+        if kwargs["n_estimators"] <= 0:
+            raise ValueError("n_estimators must be positive.")
+        if kwargs["min_child_weight"] < 1:
+            raise ValueError("min_child_weight must be a positive integer.")
+        if kwargs["min_split_gain"] < 0:
+            raise ValueError("min_split_gain must be non-negative.")
+        if kwargs["threads_per_block"] <= 0 or kwargs["threads_per_block"] % 32 != 0:
+            raise ValueError("threads_per_block should be a positive multiple of 32 (warp size).")
+        if not (1 <= kwargs["rows_per_thread"] <= 16):
+            raise ValueError("rows_per_thread must be positive between 1 and 16 inclusive.")
+        if kwargs["L2_reg"] < 0:
+            raise ValueError("L2_reg must be non-negative.")
+        if kwargs["colsample_bytree"] <= 0 or kwargs["colsample_bytree"] > 1:
+            raise ValueError(
+                f"Invalid colsample_bytree: {kwargs['colsample_bytree']}. Must be a float value > 0 and <= 1."
+            )
+
+    def validate_fit_params(self, X, y, era_id, X_eval, y_eval, eval_every_n_trees,
+                            early_stopping_rounds, eval_metric):
+        """Same checks and messages as warpgbm/core.py:216-291."""
+        if not isinstance(X, np.ndarray) or not isinstance(y, np.ndarray):
+            raise TypeError("X and y must be numpy arrays.")
+        if X.ndim != 2:
+            raise ValueError(f"X must be 2-dimensional, got shape {X.shape}")
+        if y.ndim != 1:
+            raise ValueError(f"y must be 1-dimensional, got shape {y.shape}")
+        if X.shape[0] != y.shape[0]:
+            raise ValueError(
+                f"X and y must have the same number of rows. Got {X.shape[0]} and {y.shape[0]}.")
+        if era_id is not None:
+            if not isinstance(era_id, np.ndarray):
+                raise TypeError("era_id must be a numpy array.")
+            if era_id.ndim != 1:
+                raise ValueError(f"era_id must be 1-dimensional, got shape {era_id.shape}")
+            if len(era_id) != len(y):
+                raise ValueError(
+                    f"era_id must have same length as y. Got {len(era_id)} and {len(y)}.")
+        eval_args = [X_eval, y_eval, eval_every_n_trees]
+        if any(arg is not None for arg in eval_args):
+            if X_eval is None or y_eval is None or eval_every_n_trees is None:
+                raise ValueError(
+                    "If using eval set, X_eval, y_eval, and eval_every_n_trees must all be defined.")
+            if not isinstance(X_eval, np.ndarray) or not isinstance(y_eval, np.ndarray):
+                raise TypeError("X_eval and y_eval must be numpy arrays.")
+            if X_eval.ndim != 2:
+                raise ValueError(f"X_eval must be 2-dimensional, got shape {X_eval.shape}")
+            if y_eval.ndim != 1:
+                raise ValueError(f"y_eval must be 1-dimensional, got shape {y_eval.shape}")
+            if X_eval.shape[0] != y_eval.shape[0]:
+                raise ValueError(
+                    f"X_eval and y_eval must have same number of rows. Got {X_eval.shape[0]} and {y_eval.shape[0]}.")
+            if not isinstance(eval_every_n_trees, int) or eval_every_n_trees <= 0:
+                raise ValueError(
+                    f"eval_every_n_trees must be a positive integer, got {eval_every_n_trees}.")
+            if early_stopping_rounds is not None:
+                if not isinstance(early_stopping_rounds, int) or early_stopping_rounds <= 0:
+                    raise ValueError(
+                        f"early_stopping_rounds must be a positive integer, got {early_stopping_rounds}.")
+            else:
+                early_stopping_rounds = self.n_estimators + 1
+            valid_metrics = ["mse", "corr", "rmsle", "logloss", "accuracy"]
+            if eval_metric not in valid_metrics:
+                raise ValueError(f"Invalid eval_metric: {eval_metric}. Choose from {valid_metrics}.")
+        return early_stopping_rounds
+
+    # ------------------------------------------------------------------ fit
+    def fit(self, X, y, era_id=None, X_eval=None, y_eval=None, eval_every_n_trees=None,
+            early_stopping_rounds=None, eval_metric="mse"):
+        early_stopping_rounds = self.validate_fit_params(
+            X, y, era_id, X_eval, y_eval, eval_every_n_trees, early_stopping_rounds, eval_metric)
+        # colsample_bytree feature subsets come from this generator (host RNG,
+        # reproducible for a given random_state)
+        seed = self.random_state if self.random_state is not None else int(
+            np.random.SeedSequence().generate_state(1)[0])
+        self._gen = torch.Generator().manual_seed(int(seed))
+        if self.random_state is not None:
+            np.random.seed(self.random_state)
+
+        if not self.warm_start or not self._is_fitted:
+            self._is_fitted = False
+            self._trees_trained = 0
+            self.forest = [{} for _ in range(self.n_estimators)] if self.objective == "regression" else []
+            self.training_loss = []
+            self.eval_loss = []
+        else:
+            if X.shape[1] != self.num_features:
+                raise ValueError(
+                    f"X has {X.shape[1]} features, but model was trained with {self.num_features} features.")
+            if self._trees_trained >= self.n_estimators:
+                print(f"Model already has {self._trees_trained} trees (n_estimators={self.n_estimators}). No additional training needed.")
+                return self
+
+        if era_id is None:
+            era_id = np.ones(X.shape[0], dtype="int32")
+        self.feature_subsets_ = []
+
+        if self.objective in ("multiclass", "binary"):
+            if not self.warm_start or not self._is_fitted:
+                self.label_encoder = LabelEncoder()
+                y_encoded = self.label_encoder.fit_transform(y)
+                self.classes_ = self.label_encoder.classes_
+                self.num_classes = len(self.classes_)
+            else:
+                y_encoded = self.label_encoder.transform(y)
+            if self.objective == "binary" and self.num_classes != 2:
+                raise ValueError(f"binary objective requires exactly 2 classes, got {self.num_classes}")
+            if self.objective == "multiclass" and self.num_classes < 2:
+                raise ValueError(f"multiclass objective requires at least 2 classes, got {self.num_classes}")
+            return self._fit_classification(X, y_encoded, era_id, X_eval, y_eval,
+                                            eval_every_n_trees, early_stopping_rounds, eval_metric)
+        return self._fit_regression(X, y, era_id, X_eval, y_eval, eval_every_n_trees,
+                                    early_stopping_rounds, eval_metric)
+
+    def preprocess_gpu_data(self, X_np, Y_np, era_id_np):
+        """Codes, era layout and targets on the device (warpgbm/core.py:487-541)."""
+        self.num_samples, self.num_features = X_np.shape
+        dev = torch.device(self.device)
+        is_integer_type = np.issubdtype(X_np.dtype, np.integer)
+        max_vals = X_np.max(axis=0) if X_np.shape[0] else np.zeros(X_np.shape[1])
+        if is_integer_type and np.all(max_vals < self.num_bins):
+            print("Detected pre-binned integer input — skipping quantile binning.")
+            codes = D.upload_prebinned(X_np, dev, with_cm=True)
+            bin_edges = torch.arange(1, self.num_bins, dtype=torch.float32).repeat(
+                self.num_features, 1).to(dev)
+        else:
+            print("quantile binning.")
+            Xd = D.upload_float(X_np, dev)
+            bin_edges = D.quantile_edges(Xd, self.num_bins)
+            codes = D.bin_matrix(Xd, bin_edges, with_cm=True)
+            del Xd
+        uniq, inv, order, start = D.era_layout(era_id_np)
+        self.unique_eras = uniq
+        self.num_eras = len(uniq)
+        self._era_inv = inv
+        root_order = torch.from_numpy(order).to(dev)
+        era_start = torch.from_numpy(start).to(dev)
+        Y_gpu = torch.from_numpy(np.asarray(Y_np)).type(torch.float32).to(dev)
+        return codes, root_order, era_start, bin_edges, Y_gpu
+
+    def _new_engine(self, codes, root_order, era_start, n_trees, objective):
+        return D.Engine(codes, root_order, era_start, self.num_bins, self.num_eras,
+                        self.max_depth, n_trees, objective, self.min_child_weight,
+                        self.min_split_gain, self.L2_reg, self.learning_rate)
+
+    def _feature_subset(self, dev):
+        """Features of one round: randperm(F)[:k], k = max(1, int(colsample * F))
+        (warpgbm/core.py:702-703, 721-722, 777-778); the subsets drawn in the
+        last fit are kept in ``feature_subsets_``."""
+        F = self.num_features
+        if self.colsample_bytree < 1.0:
+            k = max(1, int(self.colsample_bytree * F))
+            sel = torch.randperm(F, generator=self._gen, dtype=torch.int64)[:k]
+        else:
+            sel = torch.arange(F, dtype=torch.int64)
+        self.feature_subsets_.append(sel.numpy().astype(np.int32))
+        return sel.to(torch.int32).to(dev)
+
+    def _alloc_records(self, n_rounds, n_trees, dev):
+        H = (1 << (self.max_depth + 1)) - 1
+        return {
+            "feat": torch.empty((n_rounds, n_trees, H), dtype=torch.int32, device=dev),
+            "bin": torch.empty((n_rounds, n_trees, H), dtype=torch.int32, device=dev),
+            "leaf": torch.empty((n_rounds, n_trees, H), dtype=torch.float32, device=dev),
+            "count": torch.empty((n_rounds, n_trees, H), dtype=torch.int64, device=dev),
+            "gain": torch.empty((n_rounds, n_trees, H, self.num_eras), dtype=torch.float32,
+                                device=dev),
+        }
+
+    def _fit_regression(self, X, y, era_id, X_eval, y_eval, eval_every_n_trees,
+                        early_stopping_rounds, eval_metric):
+        dev = torch.device(self.device)
+        codes, root_order, era_start, self.bin_edges, Y_gpu = self.preprocess_gpu_data(X, y, era_id)
+        start_iter = self._trees_trained if (self.warm_start and self._is_fitted) else 0
+        if start_iter > 0:
+            # rebuild the training predictions from the existing trees; trees
+            # are added in order, exactly as during training
+            preds = torch.full((self.num_samples,), np.float32(self.base_prediction),
+                               dtype=torch.float32, device=dev)
+            self._predict_codes_into(codes, preds.view(-1, 1), self.forest[:start_iter])
+        else:
+            # mean of the float32 targets, float64 accumulation, one rounding
+            # (the reference's Y_gpu.mean().item(), core.py:387)
+            self.base_prediction = float(np.float32(
+                np.mean(np.asarray(y, dtype=np.float32), dtype=np.float64)))
+            preds = torch.full((self.num_samples,), np.float32(self.base_prediction),
+                               dtype=torch.float32, device=dev)
+        self._setup_eval(X_eval, y_eval, eval_every_n_trees, early_stopping_rounds, eval_metric,
+                         classification=False)
+        if not hasattr(self, "training_loss") or not self.warm_start or not self._is_fitted:
+            self.training_loss = []
+            self.eval_loss = []
+            self.per_era_feature_importance_ = np.zeros((self.num_eras, self.num_features),
+                                                        dtype=np.float32)
+        if len(self.forest) < self.n_estimators:
+            self.forest.extend([{} for _ in range(self.n_estimators - len(self.forest))])
+        eng = self._new_engine(codes, root_order, era_start, 1, 0)
+        n_new = self.n_estimators - start_iter
+        rec = self._alloc_records(n_new, 1, dev)
+        self.stop = False
+        eval_pred = None
+        if self._eval is not None:
+            eval_pred = torch.full((self._eval["codes"].n, 1), np.float32(self.base_prediction),
+                                   dtype=torch.float32, device=dev)
+            if start_iter > 0:
+                self._predict_codes_into(self._eval["codes"], eval_pred, self.forest[:start_iter])
+        done = 0
+        with torch.no_grad():
+            for j in range(n_new):
+                i = start_iter + j
+                feat_sel = self._feature_subset(dev)
+                eng.round(Y_gpu, preds, feat_sel, {k: v[j] for k, v in rec.items()})
+                done = j + 1
+                if self._eval is not None:
+                    D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
+                                   rec["leaf"][j], 1, 1, self.max_depth, self.learning_rate,
+                                   eval_pred)
+                    self._compute_eval_regression(i, Y_gpu, preds, eval_pred[:, 0])
+                    if self.stop:
+                        break
+        eng.close()
+        self._absorb_records(rec, done, start_iter, classification=False)
+        self.feature_importance_ = self.per_era_feature_importance_.sum(axis=0)
+        self._is_fitted = True
+        self._heap = None
+        print(f"Finished training forest. Total trees: {self._trees_trained}")
+        del codes
+        gc.collect()
+        return self
+
+    def _fit_classification(self, X, y_encoded, era_id, X_eval, y_eval, eval_every_n_trees,
+                            early_stopping_rounds, eval_metric):
+        dev = torch.device(self.device)
+        codes, root_order, era_start, self.bin_edges, _ = self.preprocess_gpu_data(X, y_encoded, era_id)
+        K = self.num_classes
+        labels = torch.from_numpy(np.asarray(y_encoded).astype(np.int32)).to(dev)
+        start_iter = self._trees_trained if (self.warm_start and self._is_fitted) else 0
+        init = self._class_prior_logits(np.asarray(y_encoded))
+        scores = torch.from_numpy(np.tile(init, (self.num_samples, 1))).to(dev)
+        if start_iter > 0:
+            self._predict_codes_into(codes, scores, self.forest[:start_iter])
+        self._setup_eval(X_eval, y_eval, eval_every_n_trees, early_stopping_rounds, eval_metric,
+                         classification=True)
+        if not hasattr(self, "training_loss") or not self.warm_start or not self._is_fitted:
+            self.training_loss = []
+            self.eval_loss = []
+            self.per_era_feature_importance_ = np.zeros((self.num_eras, self.num_features),
+                                                        dtype=np.float32)
+            self.forest = []
+        eng = self._new_engine(codes, root_order, era_start, K, 1)
+        n_new = self.n_estimators - start_iter
+        rec = self._alloc_records(n_new, K, dev)
+        self.stop = False
+        eval_scores = None
+        if self._eval is not None:
+            eval_scores = torch.from_numpy(
+                np.tile(self._uniform_prior_logits(), (self._eval["codes"].n, 1))).to(dev)
+            if start_iter > 0:
+                self._predict_codes_into(self._eval["codes"], eval_scores, self.forest[:start_iter])
+        done = 0
+        with torch.no_grad():
+            for j in range(n_new):
+                i = start_iter + j
+                feat_sel = self._feature_subset(dev)
+                eng.round(labels, scores, feat_sel, {k: v[j] for k, v in rec.items()})
+                done = j + 1
+                if self._eval is not None:
+                    D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
+                                   rec["leaf"][j], 1, K, self.max_depth, self.learning_rate,
+                                   eval_scores)
+                    self._compute_eval_multiclass(i, labels, scores, eval_scores)
+                    if self.stop:
+                        break
+        eng.close()
+        self._absorb_records(rec, done, start_iter, classification=True)
+        self.feature_importance_ = self.per_era_feature_importance_.sum(axis=0)
+        self._is_fitted = True
+        self._heap = None
+        print(f"Finished training multiclass forest. Total rounds: {self._trees_trained} "
+              f"({self._trees_trained * self.num_classes} trees)")
+        del codes
+        gc.collect()
+        return self
+
+    # ------------------------------------------------------------------ priors
+    def _class_prior_logits(self, y_encoded):
+        """log(prior_k + 1e-10) with prior_k the class frequency in float32
+        (warpgbm/core.py:452-456)."""
+        K = self.num_classes
+        n = np.float32(len(y_encoded))
+        out = np.zeros(K, dtype=np.float32)
+        for k in range(K):
+            p = np.float32(np.count_nonzero(y_encoded == k)) / n
+            if p > 0:
+                out[k] = np.float32(np.log(np.float64(np.float32(p + np.float32(1e-10)))))
+        return out
+
+    def _uniform_prior_logits(self):
+        """log(float32(1/K + 1e-10)) for every class: the prior predict_proba
+        starts from (warpgbm/core.py:1003-1007)."""
+        K = self.num_classes
+        v = np.float32(np.log(np.float64(np.float32(1.0 / K + 1e-10))))
+        return np.full(K, v, dtype=np.float32)
+
+    # ------------------------------------------------------------------ eval
+    def _setup_eval(self, X_eval, y_eval, eval_every_n_trees, early_stopping_rounds, eval_metric,
+                    classification):
+        if X_eval is None or y_eval is None:
+            self._eval = None
+            self.eval_every_n_trees = None
+            self.early_stopping_rounds = None
+            return
+        dev = torch.device(self.device)
+        codes = self.bin_inference_data(X_eval)
+        if classification:
+            y_enc = self.label_encoder.transform(y_eval)
+            ye = torch.from_numpy(np.asarray(y_enc).astype(np.int32)).to(dev)
+            self.eval_metric = eval_metric if eval_metric != "mse" else "logloss"
+        else:
+            ye = torch.from_numpy(np.asarray(y_eval)).to(torch.float32).to(dev)
+            self.eval_metric = eval_metric
+        self._eval = {"codes": codes, "y": ye}
+        self.eval_every_n_trees = eval_every_n_trees
+        self.early_stopping_rounds = early_stopping_rounds
+
+    def get_eval_metric(self, y_true, y_pred):
+        if self.eval_metric == "mse":
+            return ((y_true - y_pred) ** 2).mean().item()
+        elif self.eval_metric == "corr":
+            return 1 - torch.corrcoef(torch.vstack([y_true, y_pred]))[0, 1].item()
+        elif self.eval_metric == "rmsle":
+            return rmsle_torch(y_true, y_pred).item()
+        else:
+            raise ValueError(f"Invalid eval_metric: {self.eval_metric}.")
+
+    def _compute_eval_regression(self, i, Y_gpu, preds, eval_preds):
+        """warpgbm/core.py:670-690."""
+        train_loss = ((Y_gpu - preds) ** 2).mean().item()
+        self.training_loss.append(train_loss)
+        if i % self.eval_every_n_trees == 0:
+            eval_loss = self.get_eval_metric(self._eval["y"], eval_preds)
+            self.eval_loss.append(eval_loss)
+            if len(self.eval_loss) > self.early_stopping_rounds:
+                if self.eval_loss[-(self.early_stopping_rounds + 1)] < self.eval_loss[-1]:
+                    self.stop = True
+            print(f"🌲 Tree {i+1}/{self.n_estimators} | Train MSE: {train_loss:.6f} | "
+                  f"Eval {self.eval_metric}: {eval_loss:.6f}")
+
+    def _compute_eval_multiclass(self, i, labels, scores, eval_scores):
+        """warpgbm/core.py:820-853."""
+        train_loss = log_loss_torch(labels, softmax(scores, dim=1)).item()
+        self.training_loss.append(train_loss)
+        if i % self.eval_every_n_trees == 0:
+            probs = eval_scores.clone()
+            D.softmax_rows(probs)
+            if self.eval_metric == "accuracy":
+                eval_loss = 1.0 - accuracy_torch(self._eval["y"], torch.argmax(probs, dim=1)).item()
+            else:
+                eval_loss = log_loss_torch(self._eval["y"], probs).item()
+            self.eval_loss.append(eval_loss)
+            if len(self.eval_loss) > self.early_stopping_rounds:
+                if self.eval_loss[-(self.early_stopping_rounds + 1)] < self.eval_loss[-1]:
+                    self.stop = True
+            print(f"🌲 Round {i+1}/{self.n_estimators} ({self.num_classes} trees) | "
+                  f"Train LogLoss: {train_loss:.6f} | Eval {self.eval_metric}: {eval_loss:.6f}")
+
+    # ------------------------------------------------------------------ records -> forest
+    def _absorb_records(self, rec, done, start_iter, classification):
+        """Convert the engine's heap records of ``done`` rounds into reference
+        tree dicts and accumulate importance in the reference's order: per
+        tree, internal nodes in depth-first pre-order, float32 adds
+        (warpgbm/core.py:624-627)."""
+        host = {k: v[:done].cpu().numpy() for k, v in rec.items()}
+        imp = self.per_era_feature_importance_
+        for j in range(done):
+            trees = []
+            for t in range(host["feat"].shape[1]):
+                tree = _heap_to_dict(host["feat"][j, t], host["bin"][j, t], host["leaf"][j, t],
+                                     host["count"][j, t])
+                for h in _preorder_internal(host["feat"][j, t]):
+                    imp[:, host["feat"][j, t, h]] += host["gain"][j, t, h]
+                trees.append(tree)
+            if classification:
+                self.forest.append(trees)
+            else:
+                self.forest[start_iter + j] = trees[0]
+        self._trees_trained = start_iter + done
+
+    # ------------------------------------------------------------------ binning at predict time
+    def bin_data_with_existing_edges(self, X_np):
+        dev = torch.device(self.device)
+        Xd = D.upload_float(X_np, dev)
+        codes = D.bin_matrix(Xd, torch.as_tensor(self.bin_edges), with_cm=False)
+        del Xd
+        return codes
+
+    def bin_inference_data(self, X_np):
+        """Codes for new data (warpgbm/core.py:934-955)."""
+        is_integer_type = np.issubdtype(X_np.dtype, np.integer)
+        is_prebinned = False
+        if is_integer_type and X_np.shape[1] == self.num_features:
+            max_vals = X_np.max(axis=0)
+            if np.all(max_vals < self.num_bins):
+                print("Detected pre-binned input at predict-time — skipping binning.")
+                is_prebinned = True
+        if is_prebinned:
+            return D.upload_prebinned(X_np, torch.device(self.device), with_cm=False)
+        return self.bin_data_with_existing_edges(X_np)
+
+    # ------------------------------------------------------------------ inference
+    def _heap_tables(self, rounds):
+        """Device heap tables [n_trees, H] of a list of rounds (tree dicts, or
+        lists of K tree dicts); empty trees are skipped like the reference's
+        ``if tree`` filters."""
+        H = (1 << (self.max_depth + 1)) - 1
+        K = 1 if self.objective == "regression" else self.num_classes
+        rows = []
+        for r in rounds:
+            trees = [r] if self.objective == "regression" else list(r)
+            if not trees or not all(trees):
+                continue
+            rows.append([_dict_to_heap(t, H) for t in trees])
+        n = len(rows)
+        feat = np.full((max(n, 1), K, H), -1, np.int32)
+        bin_ = np.zeros((max(n, 1), K, H), np.int32)
+        leaf = np.zeros((max(n, 1), K, H), np.float32)
+        for j, trees in enumerate(rows):
+            for k, (f, b, v) in enumerate(trees):
+                feat[j, k], bin_[j, k], leaf[j, k] = f, b, v
+        dev = torch.device(self.device)
+        return (torch.from_numpy(feat).to(dev), torch.from_numpy(bin_).to(dev),
+                torch.from_numpy(leaf).to(dev), n)
+
+    def _predict_codes_into(self, codes, out, rounds):
+        feat, bin_, leaf, n = self._heap_tables(rounds)
+        if n:
+            D.predict_heap(codes, feat, bin_, leaf, n, out.shape[1], self.max_depth,
+                           self.learning_rate, out)
+
+    def _cached_heap(self):
+        if self._heap is None:
+            self._heap = self._heap_tables(self.forest)
+        return self._heap
+
+    def predict_binned(self, codes):
+        out = torch.full((codes.n, 1), np.float32(self.base_prediction), dtype=torch.float32,
+                         device=torch.device(self.device))
+        feat, bin_, leaf, n = self._cached_heap()
+        if n:
+            D.predict_heap(codes, feat, bin_, leaf, n, 1, self.max_depth, self.learning_rate, out)
+        return out[:, 0]
+
+    def predict_proba_binned(self, codes):
+        dev = torch.device(self.device)
+        scores = torch.from_numpy(np.tile(self._uniform_prior_logits(), (codes.n, 1))).to(dev)
+        feat, bin_, leaf, n = self._cached_heap()
+        if n:
+            D.predict_heap(codes, feat, bin_, leaf, n, self.num_classes, self.max_depth,
+                           self.learning_rate, scores)
+        D.softmax_rows(scores)
+        return scores
+
+    def predict(self, X_np):
+        """Regression values, or class labels for classification (warpgbm/core.py:957-974)."""
+        if self.objective in ("multiclass", "binary"):
+            probs = self.predict_proba(X_np)
+            return self.label_encoder.inverse_transform(np.argmax(probs, axis=1))
+        codes = self.bin_inference_data(X_np)
+        preds = self.predict_binned(codes).cpu().numpy()
+        del codes
+        return preds
+
+    def predict_proba(self, X_np):
+        """Class probabilities (warpgbm/core.py:976-989)."""
+        if self.objective not in ["multiclass", "binary"]:
+            raise ValueError("predict_proba only available for classification objectives")
+        codes = self.bin_inference_data(X_np)
+        probs = self.predict_proba_binned(codes).cpu().numpy()
+        del codes
+        return probs
+
+    # ------------------------------------------------------------------ reference op helpers
+    def compute_histograms(self, sample_indices, feature_indices, residual, bin_indices,
+                           era_indices):
+        """Per-node histograms through the reference op (warpgbm/core.py:543-563)."""
+        E = int(era_indices.max().item()) + 1 if era_indices.numel() else 1
+        g = torch.zeros((E, len(feature_indices), self.num_bins), device=residual.device)
+        h = torch.zeros_like(g)
+        node_kernel.compute_histogram3(bin_indices, residual, sample_indices, feature_indices,
+                                       era_indices, g, h, self.num_bins, self.threads_per_block,
+                                       self.rows_per_thread)
+        return g, h
+
+    # ------------------------------------------------------------------ importance
+    def get_feature_importance(self, importance_type="gain", normalize=True):
+        """warpgbm/core.py:1032-1065."""
+        if self.feature_importance_ is None:
+            raise ValueError("Model has not been fitted yet.")
+        if importance_type != "gain":
+            raise ValueError(f"importance_type '{importance_type}' not supported. Use 'gain'.")
+        importance = self.feature_importance_.copy()
+        if normalize and importance.sum() > 0:
+            importance = importance / importance.sum()
+        return importance
+
+    def get_per_era_feature_importance(self, normalize=True):
+        """warpgbm/core.py:1067-1101."""
+        if self.per_era_feature_importance_ is None:
+            raise ValueError("Model has not been fitted yet.")
+        importance = self.per_era_feature_importance_.copy()
+        if normalize:
+            for era_idx in range(importance.shape[0]):
+                era_sum = importance[era_idx].sum()
+                if era_sum > 0:
+                    importance[era_idx] /= era_sum
+        return importance
+
+    # ------------------------------------------------------------------ persistence
+    def save_model(self, path):
+        """Pickle the model state with the reference's keys (warpgbm/core.py:1103-1155)."""
+        if not self._is_fitted:
+            raise ValueError("Cannot save unfitted model. Call fit() first.")
+        state = {
+            "objective": self.objective,
+            "num_bins": self.num_bins,
+            "max_depth": self.max_depth,
+            "learning_rate": self.learning_rate,
+            "n_estimators": self.n_estimators,
+            "min_child_weight": self.min_child_weight,
+            "min_split_gain": self.min_split_gain,
+            "L2_reg": self.L2_reg,
+            "colsample_bytree": self.colsample_bytree,
+            "random_state": self.random_state,
+            "warm_start": self.warm_start,
+            "forest": self.forest,
+            "bin_edges": torch.as_tensor(self.bin_edges).detach().cpu(),
+            "base_prediction": self.base_prediction,
+            "num_features": self.num_features,
+            "num_classes": self.num_classes,
+            "classes_": self.classes_,
+            "label_encoder": self.label_encoder,
+            "feature_importance_": self.feature_importance_,
+            "per_era_feature_importance_": self.per_era_feature_importance_,
+            "_is_fitted": self._is_fitted,
+            "_trees_trained": self._trees_trained,
+            "training_loss": getattr(self, "training_loss", []),
+            "eval_loss": getattr(self, "eval_loss", []),
+        }
+        with open(path, "wb") as f:
+            pickle.dump(state, f)
+        print(f"Model saved to {path}")
+
+    def load_model(self, path):
+        """Restore a model written by :meth:`save_model` (warpgbm/core.py:1157-1213).
+        Only load files you trust: the format is a pickle, as in the reference."""
+        with open(path, "rb") as f:
+            state = pickle.load(f)
+        for k in ["objective", "num_bins", "max_depth", "learning_rate", "n_estimators",
+                  "min_child_weight", "min_split_gain", "L2_reg", "colsample_bytree",
+                  "random_state", "warm_start", "forest", "bin_edges", "base_prediction",
+                  "num_features", "num_classes", "classes_", "label_encoder",
+                  "feature_importance_", "per_era_feature_importance_", "_is_fitted",
+                  "_trees_trained"]:
+            setattr(self, k, state[k])
+        self.training_loss = state.get("training_loss", [])
+        self.eval_loss = state.get("eval_loss", [])
+        if self.per_era_feature_importance_ is not None:
+            self.num_eras = self.per_era_feature_importance_.shape[0]
+        self._heap = None
+        print(f"Model loaded from {path} ({self._trees_trained} trees)")
+        return self
+
+    def flatten_tree(self, tree, max_nodes):
+        """Pre-order table [max_nodes, 6] of (feature, bin, left, right, is_leaf,
+        leaf_value), NaN-filled (the reference's predict table format,
+        warpgbm/core.py:1215-1252)."""
+        flat = torch.full((max_nodes, 6), float("nan"), dtype=torch.float32)
+        counter = [0]
+
+        def walk(node):
+            i = counter[0]
+            counter[0] += 1
+            if "leaf_value" in node:
+                flat[i, 4] = 1.0
+                flat[i, 5] = float(node["leaf_value"])
+                return
+            flat[i, 0] = float(node["feature"])
+            flat[i, 1] = float(node["bin"])
+            flat[i, 4] = 0.0
+            flat[i, 2] = counter[0]
+            walk(node["left"])
+            flat[i, 3] = counter[0]
+            walk(node["right"])
+
+        walk(tree)
+        return flat
+
+
+# ---------------------------------------------------------------------- tree helpers
+def _heap_to_dict(feat, bin_, leaf, count, h=0):
+    """Reference tree dict from heap arrays (feat -1 leaf, >= 0 split)."""
+    f = int(feat[h])
+    if f < 0:
+        return {"leaf_value": float(leaf[h]), "samples": int(count[h])}
+    return {
+        "feature": f,
+        "bin": int(bin_[h]),
+        "left": _heap_to_dict(feat, bin_, leaf, count, 2 * h + 1),
+        "right": _heap_to_dict(feat, bin_, leaf, count, 2 * h + 2),
+    }
+
+
+def _preorder_internal(feat):
+    """Heap indices of split nodes in depth-first pre-order (left first)."""
+    out, stack = [], [0]
+    while stack:
+        h = stack.pop()
+        if h < len(feat) and feat[h] >= 0:
+            out.append(h)
+            stack.append(2 * h + 2)
+            stack.append(2 * h + 1)
+    return out
+
+
+def _dict_to_heap(tree, H):
+    feat = np.full(H, -1, np.int32)
+    bin_ = np.zeros(H, np.int32)
+    leaf = np.zeros(H, np.float32)
+
+    def walk(node, h):
+        if h >= H:
+            raise ValueError("tree deeper than max_depth")
+        if "leaf_value" in node:
+            leaf[h] = np.float32(node["leaf_value"])
+            return
+        feat[h] = int(node["feature"])
+        bin_[h] = int(node["bin"])
+        walk(node["left"], 2 * h + 1)
+        walk(node["right"], 2 * h + 2)
+
+    walk(tree, 0)
+    return feat, bin_, leaf

@@ -1,0 +1,349 @@
+// extern "C" boundary of the library (declared in include/warpgbm_amd.h).
+#include <algorithm>
+
+#include "../../include/warpgbm_amd.h"
+#include "common.hpp"
+#include "engine.hpp"
+#include "kernels.hpp"
+
+const char* wgbm_last_error_impl();
+
+using namespace wgbm;
+
+static inline hipStream_t S(void* s) { return (hipStream_t)s; }
+static inline unsigned nblocks(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+extern "C" {
+
+const char* wgbm_version(void) { return "warpgbm_amd 0.1.0 (gfx950)"; }
+const char* wgbm_last_error(void) { return wgbm_last_error_impl(); }
+
+// ---------------------------------------------------------------------------
+// shared histogram pipeline: shift -> (era sort) -> tiles -> partials -> f32
+// ---------------------------------------------------------------------------
+static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t stride,
+                              int32_t n_hist_feats, const float* resid, const int32_t* rows,
+                              int64_t n_pos, const int64_t* seg_dev, int32_t n_seg,
+                              const int32_t* era, int32_t num_eras, const int32_t* feat_idx,
+                              int32_t n_out_feats, int32_t num_bins, float* G, float* H,
+                              hipStream_t st) {
+  const int V = hist_pick_v(num_bins);
+  const int n_chunks = (n_hist_feats + 16 * V - 1) / (16 * V);
+  // scratch layout (slot 0: small control words)
+  uint32_t* absmax = (uint32_t*)scratch_get(st, 256, 0);
+  WGBM_REQUIRE(absmax, "scratch allocation failed");
+  int32_t* shift = (int32_t*)(absmax + 16);
+  int32_t* n_tiles = shift + 16;
+  WGBM_CHECK((hipError_t)fill_u32(absmax, 1, 0u, st));
+  if (n_pos > 0) {
+    hipLaunchKernelGGL(absmax_kernel, dim3(std::min<int64_t>(nblocks(n_pos, 256), 2048)),
+                       dim3(256), 0, st, resid, rows, n_pos, absmax);
+    WGBM_LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL(shift_from_absmax_kernel, dim3(1), dim3(64), 0, st, absmax, 1,
+                     wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1)), shift);
+  WGBM_LAUNCH_CHECK();
+
+  // segments: explicit (seg_dev), by era (sort rows by era), or a single one
+  const int32_t* order = rows;
+  const int64_t* seg = seg_dev;
+  int n_keys = n_seg;
+  if (!seg_dev && num_eras > 1) {
+    int64_t* counts = (int64_t*)scratch_get(st, sizeof(int64_t) * (3 * (size_t)num_eras + 2), 1);
+    int32_t* sorted = (int32_t*)scratch_get(st, sizeof(int32_t) * std::max<int64_t>(n_pos, 1), 2);
+    WGBM_REQUIRE(counts && sorted, "scratch allocation failed");
+    int64_t* starts = counts + num_eras;
+    unsigned long long* cursor = (unsigned long long*)(starts + num_eras + 1);
+    if (fill_u64(counts, num_eras, 0, st)) return WGBM_EINVAL;
+    const unsigned g = std::min<int64_t>(nblocks(std::max<int64_t>(n_pos, 1), 256), 2048);
+    hipLaunchKernelGGL(era_count_kernel, dim3(g), dim3(256), 0, st, rows, n_pos, era, num_eras,
+                       counts);
+    WGBM_LAUNCH_CHECK();
+    hipLaunchKernelGGL(exclusive_scan_i64_kernel, dim3(1), dim3(1), 0, st, counts, num_eras,
+                       starts);
+    WGBM_LAUNCH_CHECK();
+    WGBM_CHECK(hipMemcpyAsync(cursor, starts, sizeof(int64_t) * num_eras,
+                              hipMemcpyDeviceToDevice, st));
+    hipLaunchKernelGGL(era_scatter_kernel, dim3(g), dim3(256), 0, st, rows, n_pos, era, num_eras,
+                       cursor, sorted);
+    WGBM_LAUNCH_CHECK();
+    order = sorted;
+    seg = starts;
+    n_keys = num_eras;
+  } else if (!seg_dev) {
+    n_keys = 1;
+  }
+
+  // tiles: ~4 workgroups per CU over the whole call
+  int64_t tiles_target = std::max<int64_t>(1, 1024 / n_chunks);
+  int64_t R = (n_pos + tiles_target - 1) / tiles_target;
+  R = std::min<int64_t>(std::max<int64_t>((R + 255) / 256 * 256, 1024), WGBM_MAX_TILE_ROWS);
+  const int64_t max_tiles = n_pos / R + n_keys + 1;
+  Tile* tiles = (Tile*)scratch_get(st, sizeof(Tile) * max_tiles, 3);
+  int32_t* kts = (int32_t*)scratch_get(st, sizeof(int32_t) * ((size_t)n_keys + 1), 4);
+  const int64_t words = max_tiles * n_chunks * 16 * V * num_bins;
+  int64_t* part_q = (int64_t*)scratch_get(st, sizeof(int64_t) * words, 5);
+  int32_t* part_c = (int32_t*)scratch_get(st, sizeof(int32_t) * words, 6);
+  WGBM_REQUIRE(tiles && kts && part_q && part_c, "scratch allocation failed (%lld words)",
+               (long long)words);
+  hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, seg, n_pos, n_keys,
+                     (const int32_t*)nullptr, (int32_t)R, (int32_t)max_tiles, tiles, kts, n_tiles);
+  WGBM_LAUNCH_CHECK();
+  HistLaunch a;
+  a.codes = codes;
+  a.n_rows = n_rows;
+  a.stride = stride;
+  a.n_feats = n_hist_feats;
+  a.resid = resid;
+  a.resid_tree_stride = 0;
+  a.order = order;
+  a.tiles = tiles;
+  a.n_tiles = n_tiles;
+  a.keys_per_tree = n_keys;
+  a.shifts = shift;
+  a.num_bins = num_bins;
+  a.part_q = part_q;
+  a.part_c = part_c;
+  a.V = V;
+  a.n_chunks = n_chunks;
+  a.max_tiles = (int32_t)max_tiles;
+  void* tm = timer_begin("hist_tiles", st);
+  int r = launch_hist_tiles(a, st);
+  timer_end(tm, st);
+  if (r) return r;
+  const int64_t fin = (int64_t)n_keys * n_out_feats * num_bins;
+  if (fin > 0) {
+    hipLaunchKernelGGL(hist_finalize_f32_kernel, dim3(nblocks(fin, 256)), dim3(256), 0, st, part_q,
+                       part_c, kts, n_keys, n_chunks, V, num_bins, feat_idx, n_out_feats, shift,
+                       absmax, n_tiles, G, H);
+    WGBM_LAUNCH_CHECK();
+  }
+  return 0;
+}
+
+int wgbm_compute_histogram3(const int8_t* bin_indices, int64_t n_rows, int64_t n_feats_master,
+                            const float* residuals, const int32_t* sample_indices,
+                            int64_t n_samples, const int32_t* feature_indices, int64_t n_feats,
+                            const int32_t* era_indices, int32_t num_eras, float* grad_hist,
+                            float* hess_hist, int32_t num_bins, int32_t threads_per_block,
+                            int32_t rows_per_thread, void* stream) {
+  (void)threads_per_block;
+  (void)rows_per_thread;
+  WGBM_REQUIRE(num_bins >= 1 && num_bins <= 127, "num_bins must be in [1, 127], got %d", num_bins);
+  WGBM_REQUIRE(num_eras >= 1, "num_eras must be >= 1");
+  WGBM_REQUIRE(n_rows >= 0 && n_feats_master >= 1 && n_feats >= 0 && n_samples >= 0,
+               "negative size");
+  WGBM_REQUIRE(n_feats_master < (int64_t(1) << 31) && n_feats < (int64_t(1) << 31),
+               "too many features");
+  WGBM_REQUIRE(n_samples == 0 || (bin_indices && residuals && sample_indices),
+               "null input pointer");
+  WGBM_REQUIRE(n_feats == 0 || (feature_indices && grad_hist && hess_hist), "null output pointer");
+  WGBM_REQUIRE(num_eras == 1 || era_indices, "era_indices required when num_eras > 1");
+  if (n_feats == 0) return 0;
+  return histogram_pipeline(bin_indices, n_rows, n_feats_master, (int32_t)n_feats_master,
+                            residuals, sample_indices, n_samples, nullptr, 1, era_indices,
+                            num_eras, feature_indices, (int32_t)n_feats, num_bins, grad_hist,
+                            hess_hist, S(stream));
+}
+
+int wgbm_histogram_segments(const int8_t* codes, int64_t n_rows, int64_t stride, int32_t n_feats,
+                            const float* residuals, const int32_t* order, const int64_t* seg,
+                            int32_t n_seg, int64_t n_pos, int32_t num_bins, float* G, float* H,
+                            void* stream) {
+  WGBM_REQUIRE(num_bins >= 1 && num_bins <= 127, "num_bins must be in [1, 127]");
+  WGBM_REQUIRE(n_seg >= 1 && seg && codes && residuals && G && H, "bad segment arguments");
+  WGBM_REQUIRE(stride >= n_feats && n_feats >= 1, "stride must be >= n_feats >= 1");
+  return histogram_pipeline(codes, n_rows, stride, n_feats, residuals, order, n_pos, seg, n_seg,
+                            nullptr, 1, nullptr, n_feats, num_bins, G, H, S(stream));
+}
+
+int wgbm_compute_split(const float* G, const float* H, int32_t num_eras, int32_t n_feats,
+                       int32_t num_bins, float min_split_gain, float min_child_samples,
+                       float eps, float* per_era_gain, float* per_era_direction,
+                       int32_t threads, void* stream) {
+  (void)min_split_gain;
+  (void)threads;
+  WGBM_REQUIRE(num_eras >= 1 && n_feats >= 0 && num_bins >= 2, "bad split shape");
+  const int64_t n = (int64_t)num_eras * n_feats;
+  if (n == 0) return 0;
+  WGBM_REQUIRE(G && H && per_era_gain && per_era_direction, "null pointer");
+  hipLaunchKernelGGL(split_f32_kernel, dim3(nblocks(n, 256)), dim3(256), 0, S(stream), G, H,
+                     num_eras, n_feats, num_bins, min_child_samples, eps, per_era_gain,
+                     per_era_direction);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+int wgbm_custom_cuda_binner(const float* X, int64_t n, const float* bin_edges, int32_t n_edges,
+                            int8_t* bin_indices, void* stream) {
+  WGBM_REQUIRE(n >= 0 && n_edges >= 0, "negative size");
+  if (n == 0) return 0;
+  WGBM_REQUIRE(X && bin_indices && (n_edges == 0 || bin_edges), "null pointer");
+  hipLaunchKernelGGL(bin_column_kernel, dim3(nblocks(n, 256)), dim3(256), 0, S(stream), X, n,
+                     bin_edges, n_edges, bin_indices);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+int wgbm_predict_forest(const int8_t* bin_indices, int64_t n, int64_t n_feats,
+                        const float* tree_tensor, int64_t n_trees, int64_t max_nodes,
+                        float learning_rate, float* out, void* stream) {
+  WGBM_REQUIRE(n >= 0 && n_feats >= 0 && n_trees >= 0 && max_nodes >= 1, "bad predict shape");
+  if (n == 0) return 0;
+  WGBM_REQUIRE(bin_indices && out && (n_trees == 0 || tree_tensor), "null pointer");
+  hipLaunchKernelGGL(predict_table_kernel, dim3(nblocks(n, 256)), dim3(256), 0, S(stream),
+                     bin_indices, n, n_feats, tree_tensor, n_trees, max_nodes, learning_rate, out);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+int wgbm_quantile_edges(const float* sorted, int64_t n, int32_t n_feats, const float* q,
+                        int32_t nq, float* edges, void* stream) {
+  WGBM_REQUIRE(n >= 1 && n_feats >= 0 && nq >= 0, "bad quantile shape");
+  WGBM_REQUIRE(n <= (int64_t(1) << 24), "quantile input too large (n > 2^24), as torch.quantile");
+  const int64_t tot = (int64_t)n_feats * nq;
+  if (tot == 0) return 0;
+  WGBM_REQUIRE(sorted && q && edges, "null pointer");
+  hipLaunchKernelGGL(quantile_edges_kernel, dim3(nblocks(tot, 256)), dim3(256), 0, S(stream),
+                     sorted, n, n_feats, q, nq, edges);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride,
+                    const float* edges, int32_t n_edges, int8_t* codes_rm, int64_t codes_stride,
+                    int8_t* codes_cm, void* stream) {
+  WGBM_REQUIRE(n >= 0 && n_feats >= 1 && x_stride >= n_feats && codes_stride >= n_feats,
+               "bad bin_matrix shape");
+  WGBM_REQUIRE(n_edges >= 0 && n_edges <= 126, "n_edges must be in [0, 126]");
+  if (n == 0) return 0;
+  WGBM_REQUIRE(X && codes_rm && (n_edges == 0 || edges), "null pointer");
+  const size_t lds = sizeof(float) * 64 * std::max(n_edges, 1);
+  dim3 grid(nblocks(n, 64), nblocks(n_feats, 64));
+  hipLaunchKernelGGL(bin_matrix_kernel, grid, dim3(256), lds, S(stream), X, n, n_feats, x_stride,
+                     edges, n_edges, codes_rm, codes_stride, codes_cm);
+  WGBM_LAUNCH_CHECK();
+  const int64_t covered = (int64_t)grid.y * 64;
+  if (codes_stride > covered) {
+    const int64_t tot = n * (codes_stride - covered);
+    hipLaunchKernelGGL(pad_codes_kernel, dim3(nblocks(tot, 256)), dim3(256), 0, S(stream),
+                       codes_rm, n, codes_stride, (int32_t)covered);
+    WGBM_LAUNCH_CHECK();
+  }
+  return 0;
+}
+
+int wgbm_copy_prebinned(const int8_t* X, int64_t n, int32_t n_feats, int64_t x_stride,
+                        int8_t* codes_rm, int64_t codes_stride, int8_t* codes_cm, void* stream) {
+  WGBM_REQUIRE(n >= 0 && n_feats >= 1 && x_stride >= n_feats && codes_stride >= n_feats,
+               "bad copy_prebinned shape");
+  if (n == 0) return 0;
+  WGBM_REQUIRE(X && codes_rm, "null pointer");
+  dim3 grid(nblocks(n, 64), nblocks(n_feats, 64));
+  hipLaunchKernelGGL(copy_prebinned_kernel, grid, dim3(256), 0, S(stream), X, n, n_feats,
+                     x_stride, codes_rm, codes_stride, codes_cm);
+  WGBM_LAUNCH_CHECK();
+  const int64_t covered = (int64_t)grid.y * 64;
+  if (codes_stride > covered) {
+    const int64_t tot = n * (codes_stride - covered);
+    hipLaunchKernelGGL(pad_codes_kernel, dim3(nblocks(tot, 256)), dim3(256), 0, S(stream),
+                       codes_rm, n, codes_stride, (int32_t)covered);
+    WGBM_LAUNCH_CHECK();
+  }
+  return 0;
+}
+
+int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, const int32_t* feat,
+                      const int32_t* bin, const float* leaf, int32_t n_rounds, int32_t K,
+                      int32_t H, int32_t max_depth, float learning_rate, float* out,
+                      void* stream) {
+  WGBM_REQUIRE(n >= 0 && K >= 1 && n_rounds >= 0 && max_depth >= 0 && max_depth <= 20,
+               "bad predict_heap shape");
+  WGBM_REQUIRE(H == (1 << (max_depth + 1)) - 1, "H must be 2^(max_depth+1)-1");
+  if (n == 0) return 0;
+  WGBM_REQUIRE(codes && out && (n_rounds == 0 || (feat && bin && leaf)), "null pointer");
+  hipLaunchKernelGGL(predict_heap_kernel, dim3(nblocks(n * K, 256)), dim3(256), 0, S(stream),
+                     codes, n, codes_stride, feat, bin, leaf, n_rounds, K, H, max_depth,
+                     learning_rate, out);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+int wgbm_softmax_rows(float* x, int64_t n, int32_t K, void* stream) {
+  WGBM_REQUIRE(n >= 0 && K >= 1, "bad softmax shape");
+  if (n == 0) return 0;
+  WGBM_REQUIRE(x, "null pointer");
+  hipLaunchKernelGGL(softmax_rows_kernel, dim3(nblocks(n, 256)), dim3(256), 0, S(stream), x, n, K);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// engine
+// ---------------------------------------------------------------------------
+struct wgbm_engine {
+  Engine* e;
+};
+
+int wgbm_engine_create(wgbm_engine** out, const wgbm_engine_config* cfg) {
+  WGBM_REQUIRE(out && cfg, "null pointer");
+  EngineConfig c;
+  c.n_rows = cfg->n_rows;
+  c.n_feats = cfg->n_feats;
+  c.stride = cfg->codes_stride;
+  c.num_bins = cfg->num_bins;
+  c.num_eras = cfg->num_eras;
+  c.max_depth = cfg->max_depth;
+  c.n_trees = cfg->n_trees;
+  c.objective = cfg->objective;
+  c.min_child_weight = cfg->min_child_weight;
+  c.min_split_gain = cfg->min_split_gain;
+  c.l2_reg = cfg->l2_reg;
+  c.learning_rate = cfg->learning_rate;
+  c.codes_rm = cfg->codes_rm;
+  c.codes_cm = cfg->codes_cm;
+  c.root_order = cfg->root_order;
+  c.era_start = cfg->era_start;
+  Engine* e = nullptr;
+  int r = engine_create(&e, c);
+  if (r) return r;
+  *out = new wgbm_engine{e};
+  return 0;
+}
+
+int wgbm_engine_round(wgbm_engine* eng, const void* target, float* pred, const int32_t* feat_sel,
+                      int32_t n_sel, const wgbm_tree_record* rec, void* stream) {
+  WGBM_REQUIRE(eng && rec, "null pointer");
+  TreeRecord r;
+  r.feat = rec->feat;
+  r.bin = rec->bin;
+  r.leaf = rec->leaf;
+  r.count = rec->count;
+  r.gain = rec->gain;
+  r.H = rec->H;
+  WGBM_REQUIRE(r.feat && r.bin && r.leaf && r.count && r.gain, "null record pointer");
+  return engine_round(eng->e, target, pred, feat_sel, n_sel, r, S(stream));
+}
+
+int wgbm_engine_set_tuning(wgbm_engine* eng, int32_t key, int64_t value) {
+  WGBM_REQUIRE(eng, "null engine");
+  return engine_set_tuning(eng->e, key, value);
+}
+
+void wgbm_engine_destroy(wgbm_engine* eng) {
+  if (!eng) return;
+  engine_destroy(eng->e);
+  delete eng;
+}
+
+void wgbm_timer_enable(int32_t on) { timer_enable(on); }
+int wgbm_timer_read(const char* tag, double* total_ms, int64_t* count) {
+  long c = 0;
+  int r = timer_read(tag, total_ms, &c);
+  *count = c;
+  return r;
+}
+void wgbm_timer_reset(void) { timer_reset(); }
+void wgbm_release_scratch(void) { scratch_release_all(); }
+
+}  // extern "C"

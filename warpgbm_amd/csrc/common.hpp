@@ -1,0 +1,145 @@
+// Shared device/host helpers for the warpgbm_amd HIP kernels (gfx950 / CDNA4).
+//
+// Arithmetic conventions used by every kernel in this library:
+//
+// * Histogram sums are EXACT.  A residual r (f32) is quantised once per call
+//   (or once per tree in the engine) to an integer q = rint(r * 2^s), where the
+//   shift s is chosen from M = max|r| so that |q| <= 2^qbits (qbits <= 28).
+//   Because multiplying by a power of two is exact, q carries every bit of r
+//   for |r| >= M/16.  Integer sums are associative, so the histogram is
+//   independent of the order in which rows are visited (no float atomics).
+//   A float sum is produced once, by rounding the exact integer sum:
+//       G = (float) ldexp((double) Q, -s)         (|Q| < 2^53, so exact in double)
+// * Row counts are exact integers (the reference's "hess" histogram is a row
+//   count: histogram_kernel.cu:44 adds 1.0f per row).
+// * Inside a workgroup the (q, 1) pair is packed into ONE 64-bit LDS word,
+//       P = q * 2^WGBM_CBITS + 1,
+//   so a single ds_add_u64 updates both the gradient sum and the count.
+//   With at most WGBM_MAX_TILE_ROWS rows per tile the count field never
+//   carries into the sum field and the sum never overflows.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define WGBM_CBITS 18
+#define WGBM_CMASK ((1ll << WGBM_CBITS) - 1)
+#define WGBM_QBITS_MAX 28
+#define WGBM_MAX_TILE_ROWS 65536
+
+// 3rd dword of a raw buffer resource descriptor for gfx9-family parts
+// (DATA_FORMAT = 32-bit, untyped raw access).
+#define WGBM_RSRC_DW3 0x00020000
+
+#define WGBM_CHECK(expr)                                                        \
+  do {                                                                          \
+    hipError_t _e = (expr);                                                     \
+    if (_e != hipSuccess) {                                                     \
+      wgbm_set_error("%s:%d: %s -> %s", __FILE__, __LINE__, #expr,              \
+                     hipGetErrorString(_e));                                    \
+      return (int)_e;                                                           \
+    }                                                                           \
+  } while (0)
+
+#define WGBM_REQUIRE(cond, ...)                                                 \
+  do {                                                                          \
+    if (!(cond)) {                                                              \
+      wgbm_set_error(__VA_ARGS__);                                              \
+      return WGBM_EINVAL;                                                       \
+    }                                                                           \
+  } while (0)
+
+#define WGBM_LAUNCH_CHECK()                                                     \
+  do {                                                                          \
+    hipError_t _e = hipGetLastError();                                          \
+    if (_e != hipSuccess) {                                                     \
+      wgbm_set_error("%s:%d: kernel launch failed: %s", __FILE__, __LINE__,     \
+                     hipGetErrorString(_e));                                    \
+      return (int)_e;                                                           \
+    }                                                                           \
+  } while (0)
+
+#ifndef WGBM_EINVAL
+#define WGBM_EINVAL 1000
+#define WGBM_ENOMEM 1001
+#endif
+
+void wgbm_set_error(const char* fmt, ...);
+
+// ---------------------------------------------------------------------------
+// quantisation helpers (bit-identical on host and device: only exact ops)
+// ---------------------------------------------------------------------------
+__host__ __device__ inline int wgbm_shift_from_absmax(float m, int qbits) {
+  if (!(m > 0.0f)) return 0;           // all-zero residual: q == 0 for every row
+  int e;
+  frexpf(m, &e);                       // m = f * 2^e, f in [0.5, 1)  =>  m < 2^e
+  return qbits - e;
+}
+
+__host__ __device__ inline int32_t wgbm_quantise(float r, int s) {
+  return (int32_t)rintf(ldexpf(r, s));
+}
+
+__host__ __device__ inline float wgbm_dequantise(int64_t q, int s) {
+  return (float)ldexp((double)q, -s);
+}
+
+// qbits for a problem with up to n rows: keeps |sum q| < 2^53 so that the
+// int64 -> double step of wgbm_dequantise is exact.
+__host__ inline int wgbm_qbits_for_rows(int64_t n) {
+  int bl = 0;
+  while ((int64_t(1) << bl) <= n && bl < 62) ++bl;   // bit length of n
+  int q = 52 - bl;
+  return q < WGBM_QBITS_MAX ? (q < 8 ? 8 : q) : WGBM_QBITS_MAX;
+}
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+__device__ inline __amdgpu_buffer_rsrc_t wgbm_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)bytes, WGBM_RSRC_DW3);
+}
+
+// Order-preserving encoding of a non-negative float's magnitude as uint32
+// (for atomicMax over |r|).  NaN maps above +inf and is reported as an error.
+__device__ inline uint32_t wgbm_abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+
+template <typename T>
+__device__ inline T wgbm_wave_sum(T v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ inline uint32_t wgbm_wave_max_u32(uint32_t v) {
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t w = __shfl_xor(v, o, 64);
+    v = v > w ? v : w;
+  }
+  return v;
+}
+
+// Deterministic exp for softmax (x <= 0 expected, any finite x accepted).
+// Cody-Waite reduction x = k*ln2 + r with a two-part ln2, then the degree-7
+// Taylor polynomial of e^r on |r| <= ln2/2 (truncation < 6e-9 relative),
+// evaluated in Horner form with explicit fmaf; scaling by 2^k with ldexpf.
+// Only IEEE-exact primitives are used, so host and device agree bit for bit.
+__host__ __device__ inline float wgbm_expf(float x) {
+  if (x != x) return x;
+  if (x < -104.0f) return 0.0f;
+  if (x > 88.5f) return __builtin_inff();
+  const float log2e = 1.44269504088896341f;
+  const float ln2_hi = 0.693145751953125f;        // 15 significant bits: k*ln2_hi is exact
+  const float ln2_lo = 1.42860682030941723212e-6f;  // ln 2 - ln2_hi
+  float k = rintf(x * log2e);
+  float r = fmaf(k, -ln2_hi, x);
+  r = fmaf(k, -ln2_lo, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)k);
+}

@@ -1,0 +1,127 @@
+// Level-wise tree engine (internal C++ interface).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.hpp"
+
+namespace wgbm {
+
+// Tree record in heap order (node h has children 2h+1, 2h+2), per tree of a
+// round: H = 2^(max_depth+1) - 1 slots.  feat: global split feature, -1 leaf,
+// -2 absent.  gain: per-era split gains [H][E] (importance bookkeeping).
+struct TreeRecord {
+  int32_t* feat;
+  int32_t* bin;
+  float* leaf;
+  int64_t* count;
+  float* gain;
+  int32_t H;
+};
+
+struct EngineConfig {
+  int64_t n_rows;
+  int32_t n_feats;
+  int64_t stride;          // row stride of codes_rm (bytes)
+  int32_t num_bins;
+  int32_t num_eras;
+  int32_t max_depth;
+  int32_t n_trees;         // trees grown together per round (1 or K)
+  int32_t objective;       // 0 regression, 1 softmax
+  float min_child_weight;
+  float min_split_gain;
+  float l2_reg;
+  float learning_rate;
+  const int8_t* codes_rm;  // [n_rows, stride]
+  const int8_t* codes_cm;  // [n_feats, n_rows]
+  const int32_t* root_order;  // [n_rows] rows sorted by era (ascending row id inside)
+  const int64_t* era_start;   // [E + 1]
+};
+
+struct Engine;
+int engine_create(Engine** out, const EngineConfig& cfg);
+void engine_destroy(Engine* e);
+// One boosting round.  target: float y [n] (regression) or int32 labels
+// (softmax).  pred: [n] or [n, K] row-major, updated in place.
+int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat_sel,
+                 int32_t n_sel, const TreeRecord& rec, hipStream_t st);
+int engine_set_tuning(Engine* e, int key, int64_t value);
+
+// kernels (engine_kernels.hip)
+__global__ void residual_regression_kernel(const float* y, const float* pred, int64_t n,
+                                           float* r, uint32_t* absmax);
+__global__ void residual_softmax_kernel(const float* logits, const int32_t* label, int64_t n,
+                                        int32_t K, float* r, uint32_t* absmax);
+__global__ void root_setup_kernel(const int32_t* root_order, int64_t n, int32_t T,
+                                  const int64_t* era_start, int32_t E, int32_t* order,
+                                  int64_t* seg, int32_t* present);
+__global__ void segment_totals_kernel(const Tile* tiles, const int32_t* n_tiles,
+                                      const int32_t* order, const float* resid, int64_t n,
+                                      const int32_t* shifts, int32_t keys_per_tree,
+                                      int64_t* tot_q, int64_t* tot_c);
+__global__ void level_finish_kernel(int32_t depth, int32_t max_depth, int32_t T, int32_t E,
+                                    const int32_t* present, const int32_t* split_l,
+                                    const int32_t* split_b, const float* split_gain_era,
+                                    const int32_t* feat_sel, const int64_t* tot_q,
+                                    const int64_t* tot_c, const int32_t* shifts,
+                                    float* leaf_val, TreeRecord rec);
+__global__ void partition_count_kernel(
+    const Tile* tiles, const int32_t* n_tiles, const int32_t* order, int32_t E, int32_t nodes,
+    int32_t max_split_depth_ok, const int32_t* split_l, const int32_t* split_b,
+    const int32_t* feat_sel, const int8_t* codes_cm, int64_t n, const float* resid,
+    const int32_t* shifts, const float* leaf_val, float lr, float* pred, int64_t pstride,
+    int64_t pcol, uint8_t* dirbit, int32_t* tile_left, int64_t* tot_q_next,
+    int64_t* tot_c_next);
+__global__ void partition_scan_kernel(int32_t T, int32_t nodes, int32_t E, const int64_t* seg,
+                                      const Tile* tiles, const int32_t* key_tile_start,
+                                      const int32_t* tile_left, const int32_t* split_l,
+                                      int64_t* Lk, int64_t* tile_lbase, int64_t* tile_rbase,
+                                      int64_t* seg_next, int32_t* present_next,
+                                      int32_t* key_list_next);
+__global__ void partition_scatter_kernel(const Tile* tiles, const int32_t* n_tiles,
+                                         const int32_t* order, int32_t E,
+                                         const int32_t* split_l, const uint8_t* dirbit,
+                                         const int64_t* tile_lbase, const int64_t* tile_rbase,
+                                         int32_t* order_next);
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v);
+
+// split kernels (split.hip)
+__global__ void split_f32_kernel(const float* G, const float* H, int32_t E, int32_t F,
+                                 int32_t B, float mcw, float eps, float* gain_out,
+                                 float* dir_out);
+__global__ void split_level_e1_kernel(const int64_t* hq, const int32_t* hc, int32_t F,
+                                      int32_t B, const int32_t* feat_sel, int32_t n_sel,
+                                      int32_t nodes_in_level, const int32_t* present,
+                                      const int32_t* shifts, float mcw, float eps,
+                                      float min_split_gain, int32_t* split_l, int32_t* split_b,
+                                      float* split_gain);
+__global__ void split_level_scan_kernel(const int64_t* hq, const int32_t* hc, int32_t F,
+                                        int32_t B, int32_t E, const int32_t* feat_sel,
+                                        int32_t n_sel, int32_t nodes_in_level, int32_t n_tn,
+                                        const int32_t* present, const int32_t* shifts,
+                                        float mcw, float eps, float* gain, int8_t* dir);
+__global__ void des_select_kernel(const float* gain, const int8_t* dir, int32_t B, int32_t E,
+                                  int32_t n_sel, const int32_t* present, float min_split_gain,
+                                  int32_t* split_l, int32_t* split_b, float* split_gain_era);
+
+// binning / predict kernels
+__global__ void bin_column_kernel(const float* x, int64_t n, const float* edges,
+                                  int32_t n_edges, int8_t* out);
+__global__ void bin_matrix_kernel(const float* X, int64_t n, int32_t F, int64_t xs,
+                                  const float* edges, int32_t n_edges, int8_t* codes_rm,
+                                  int64_t S, int8_t* codes_cm);
+__global__ void pad_codes_kernel(int8_t* codes_rm, int64_t n, int64_t S, int32_t from);
+__global__ void copy_prebinned_kernel(const int8_t* X, int64_t n, int32_t F, int64_t xs,
+                                      int8_t* codes_rm, int64_t S, int8_t* codes_cm);
+__global__ void quantile_edges_kernel(const float* sorted, int64_t n, int32_t F,
+                                      const float* q, int32_t nq, float* edges);
+__global__ void predict_table_kernel(const int8_t* codes, int64_t n, int64_t F,
+                                     const float* table, int64_t T, int64_t M, float lr,
+                                     float* out);
+__global__ void predict_heap_kernel(const int8_t* codes, int64_t n, int64_t S,
+                                    const int32_t* feat, const int32_t* bin, const float* leaf,
+                                    int32_t n_rounds, int32_t K, int32_t H, int32_t max_depth,
+                                    float lr, float* out);
+__global__ void softmax_rows_kernel(float* x, int64_t n, int32_t K);
+
+}  // namespace wgbm

@@ -1,0 +1,364 @@
+// Level-wise tree engine: host orchestration of one boosting round.
+//
+// The reference grows each tree depth-first with a host round trip per node
+// (warpgbm/core.py:597-658: .item() at :594, :606, :627, boolean-mask
+// compaction at :630).  The tree it builds does not depend on the visiting
+// order: the residual is fixed for the whole tree (core.py:719) and each
+// node's decision depends only on its own rows.  So the engine grows all
+// nodes of a depth at once, for all trees of a round (the K class trees of a
+// softmax round share their gradients, core.py:772), with every launch queued
+// on one stream and no host synchronisation inside a round:
+//   residuals -> shifts -> root segments/totals ->
+//   for depth d: histograms of the smaller children (+ siblings by
+//   subtraction) -> split/DES -> leaf values + record -> partition.
+#include <algorithm>
+#include <vector>
+
+#include "common.hpp"
+#include "engine.hpp"
+#include "kernels.hpp"
+
+namespace wgbm {
+
+struct Engine {
+  EngineConfig c;
+  int V = 16, n_chunks = 1, qbits = 28;
+  int H = 1;
+  int part_tile_rows = 2048;
+  int64_t hist_tile_rows = 0;  // 0: automatic
+  int64_t n_keys_max = 0, max_ptiles = 0, max_htiles = 0;
+  // buffers
+  float* resid = nullptr;
+  uint32_t* absmax = nullptr;
+  int32_t* shifts = nullptr;
+  int32_t* order[2] = {nullptr, nullptr};
+  int64_t* seg[2] = {nullptr, nullptr};
+  int64_t* totq[2] = {nullptr, nullptr};
+  int64_t* totc[2] = {nullptr, nullptr};
+  int32_t* present[2] = {nullptr, nullptr};
+  int32_t* key_list[2] = {nullptr, nullptr};
+  uint8_t* dirbit = nullptr;
+  Tile* ptiles = nullptr;
+  int32_t* pkts = nullptr;
+  int32_t* pn = nullptr;
+  int32_t* tile_left = nullptr;
+  int64_t* lbase = nullptr;
+  int64_t* rbase = nullptr;
+  int64_t* Lk = nullptr;
+  Tile* htiles = nullptr;
+  int32_t* hkts = nullptr;
+  int32_t* hn = nullptr;
+  int64_t* part_q = nullptr;
+  int32_t* part_c = nullptr;
+  int64_t part_words = 0;
+  int64_t* hq[2] = {nullptr, nullptr};
+  int32_t* hc[2] = {nullptr, nullptr};
+  float* sgain = nullptr;
+  int8_t* sdir = nullptr;
+  int32_t* split_l = nullptr;
+  int32_t* split_b = nullptr;
+  float* split_gain = nullptr;
+  float* leaf_val = nullptr;
+  std::vector<void*> allocs;
+};
+
+template <typename T>
+static int dalloc(Engine* e, T** p, int64_t n) {
+  if (n < 1) n = 1;
+  void* q = nullptr;
+  hipError_t err = hipMalloc(&q, (size_t)n * sizeof(T));
+  if (err != hipSuccess) {
+    wgbm_set_error("engine: hipMalloc of %lld bytes failed: %s", (long long)(n * sizeof(T)),
+                   hipGetErrorString(err));
+    return WGBM_ENOMEM;
+  }
+  e->allocs.push_back(q);
+  *p = (T*)q;
+  return 0;
+}
+
+#define E_ALLOC(ptr, n)                      \
+  do {                                       \
+    int _r = dalloc(e, &(ptr), (int64_t)(n)); \
+    if (_r) {                                \
+      engine_destroy(e);                     \
+      return _r;                             \
+    }                                        \
+  } while (0)
+
+void engine_destroy(Engine* e) {
+  if (!e) return;
+  for (void* p : e->allocs) (void)hipFree(p);
+  delete e;
+}
+
+int engine_create(Engine** out, const EngineConfig& cfg) {
+  WGBM_REQUIRE(cfg.n_rows > 0 && cfg.n_rows < (int64_t(1) << 31), "engine: n_rows out of range");
+  WGBM_REQUIRE(cfg.n_feats > 0, "engine: n_feats must be positive");
+  WGBM_REQUIRE(cfg.stride >= cfg.n_feats && cfg.stride % 16 == 0,
+               "engine: codes stride must be >= n_feats and a multiple of 16");
+  WGBM_REQUIRE(cfg.num_bins >= 2 && cfg.num_bins <= 127, "engine: num_bins must be in [2, 127]");
+  WGBM_REQUIRE(cfg.num_eras >= 1, "engine: num_eras must be >= 1");
+  WGBM_REQUIRE(cfg.max_depth >= 1 && cfg.max_depth <= 20, "engine: max_depth must be in [1, 20]");
+  WGBM_REQUIRE(cfg.n_trees >= 1, "engine: n_trees must be >= 1");
+  WGBM_REQUIRE(cfg.objective == 0 || cfg.objective == 1, "engine: bad objective");
+  WGBM_REQUIRE(cfg.objective == 1 || cfg.n_trees == 1, "engine: regression grows one tree per round");
+  WGBM_REQUIRE(cfg.codes_rm && cfg.codes_cm && cfg.root_order && cfg.era_start,
+               "engine: null input pointer");
+  Engine* e = new Engine();
+  e->c = cfg;
+  const int64_t T = cfg.n_trees, N = cfg.n_rows, E = cfg.num_eras, F = cfg.n_feats,
+                B = cfg.num_bins;
+  const int D = cfg.max_depth;
+  e->V = hist_pick_v(cfg.num_bins);
+  e->n_chunks = (int)((F + 16 * e->V - 1) / (16 * e->V));
+  e->qbits = wgbm_qbits_for_rows(N);
+  e->H = (1 << (D + 1)) - 1;
+  const int64_t nodes_max = int64_t(1) << D;
+  e->n_keys_max = T * nodes_max * E;
+  const int64_t hist_nodes_max = int64_t(1) << (D - 1);  // deepest level with histograms
+  E_ALLOC(e->resid, T * N);
+  E_ALLOC(e->absmax, T);
+  E_ALLOC(e->shifts, T);
+  for (int k = 0; k < 2; ++k) {
+    E_ALLOC(e->order[k], T * N);
+    E_ALLOC(e->seg[k], e->n_keys_max + 1);
+    E_ALLOC(e->totq[k], e->n_keys_max);
+    E_ALLOC(e->totc[k], e->n_keys_max);
+    E_ALLOC(e->present[k], T * nodes_max);
+    E_ALLOC(e->key_list[k], e->n_keys_max);
+    E_ALLOC(e->hq[k], T * hist_nodes_max * E * F * B);
+    E_ALLOC(e->hc[k], T * hist_nodes_max * E * F * B);
+  }
+  E_ALLOC(e->dirbit, T * N);
+  e->max_ptiles = T * N / e->part_tile_rows + e->n_keys_max + 1;
+  E_ALLOC(e->ptiles, e->max_ptiles);
+  E_ALLOC(e->pkts, e->n_keys_max + 1);
+  E_ALLOC(e->pn, 1);
+  E_ALLOC(e->tile_left, e->max_ptiles);
+  E_ALLOC(e->lbase, e->max_ptiles);
+  E_ALLOC(e->rbase, e->max_ptiles);
+  E_ALLOC(e->Lk, e->n_keys_max);
+  E_ALLOC(e->hkts, e->n_keys_max + 1);
+  E_ALLOC(e->hn, 1);
+  if (E > 1) {
+    E_ALLOC(e->sgain, T * hist_nodes_max * E * F * (B - 1));
+    E_ALLOC(e->sdir, T * hist_nodes_max * E * F * (B - 1));
+  }
+  E_ALLOC(e->split_l, T * nodes_max);
+  E_ALLOC(e->split_b, T * nodes_max);
+  E_ALLOC(e->split_gain, T * nodes_max * E);
+  E_ALLOC(e->leaf_val, T * nodes_max);
+  *out = e;
+  return 0;
+}
+
+int engine_set_tuning(Engine* e, int key, int64_t value) {
+  if (key == 1) {
+    WGBM_REQUIRE(value == 0 || (value >= 256 && value <= WGBM_MAX_TILE_ROWS),
+                 "hist tile rows must be 0 or in [256, %d]", WGBM_MAX_TILE_ROWS);
+    e->hist_tile_rows = value;
+    return 0;
+  }
+  wgbm_set_error("engine_set_tuning: unknown key %d", key);
+  return WGBM_EINVAL;
+}
+
+// histogram tile rows for a level: enough tiles for ~4 workgroups per CU
+static int64_t pick_tile_rows(const Engine* e, int64_t rows_bound) {
+  if (e->hist_tile_rows > 0) return e->hist_tile_rows;
+  const int64_t target_wg = 256 * 4;
+  int64_t tiles = std::max<int64_t>(1, target_wg / e->n_chunks);
+  int64_t r = (rows_bound + tiles - 1) / tiles;
+  r = (r + 255) / 256 * 256;
+  return std::min<int64_t>(std::max<int64_t>(r, 1024), WGBM_MAX_TILE_ROWS);
+}
+
+static int ensure_partials(Engine* e, int64_t max_tiles) {
+  const int64_t words = max_tiles * e->n_chunks * 16 * e->V * e->c.num_bins;
+  if (words <= e->part_words) return 0;
+  if (e->part_q) {
+    // partial buffers are only reused within the stream; grow after a sync
+    WGBM_CHECK(hipDeviceSynchronize());
+    for (auto it = e->allocs.begin(); it != e->allocs.end();) {
+      if (*it == e->part_q || *it == e->part_c) {
+        (void)hipFree(*it);
+        it = e->allocs.erase(it);
+      } else {
+        ++it;
+      }
+    }
+    e->part_q = nullptr;
+    e->part_c = nullptr;
+  }
+  int r = dalloc(e, &e->part_q, words);
+  if (r) return r;
+  r = dalloc(e, &e->part_c, words);
+  if (r) return r;
+  e->part_words = words;
+  return 0;
+}
+
+static inline unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat_sel,
+                 int32_t n_sel, const TreeRecord& rec, hipStream_t st) {
+  const EngineConfig& c = e->c;
+  WGBM_REQUIRE(target && pred && feat_sel, "engine_round: null pointer");
+  WGBM_REQUIRE(n_sel >= 1 && n_sel <= c.n_feats, "engine_round: n_sel out of range");
+  WGBM_REQUIRE(rec.H == e->H, "engine_round: record has H=%d, expected %d", rec.H, e->H);
+  const int T = c.n_trees, E = c.num_eras, F = c.n_feats, B = c.num_bins, D = c.max_depth;
+  const int64_t N = c.n_rows;
+
+  // residuals and quantisation shifts
+  WGBM_CHECK((hipError_t)fill_u32(e->absmax, T, 0u, st));
+  if (c.objective == 0) {
+    hipLaunchKernelGGL(residual_regression_kernel, dim3(std::min<int64_t>(blocks_for(N, 256), 4096)),
+                       dim3(256), 0, st, (const float*)target, pred, N, e->resid, e->absmax);
+  } else {
+    hipLaunchKernelGGL(residual_softmax_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, st,
+                       pred, (const int32_t*)target, N, T, e->resid, e->absmax);
+  }
+  WGBM_LAUNCH_CHECK();
+  hipLaunchKernelGGL(shift_from_absmax_kernel, dim3(1), dim3(256), 0, st, e->absmax, T, e->qbits,
+                     e->shifts);
+  WGBM_LAUNCH_CHECK();
+
+  // root segments and totals
+  int cur = 0;
+  hipLaunchKernelGGL(root_setup_kernel, dim3(blocks_for(std::max<int64_t>((int64_t)T * N, T * E), 256)),
+                     dim3(256), 0, st, c.root_order, N, T, c.era_start, E, e->order[0],
+                     e->seg[0], e->present[0]);
+  WGBM_LAUNCH_CHECK();
+  if (fill_u64(e->totq[0], (int64_t)T * E, 0, st) || fill_u64(e->totc[0], (int64_t)T * E, 0, st))
+    return WGBM_EINVAL;
+  hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[0], (int64_t)0, T * E,
+                     (const int32_t*)nullptr, e->part_tile_rows, (int32_t)e->max_ptiles, e->ptiles,
+                     e->pkts, e->pn);
+  WGBM_LAUNCH_CHECK();
+  hipLaunchKernelGGL(segment_totals_kernel, dim3((unsigned)e->max_ptiles), dim3(256), 0, st,
+                     e->ptiles, e->pn, e->order[0], e->resid, N, e->shifts, E, e->totq[0],
+                     e->totc[0]);
+  WGBM_LAUNCH_CHECK();
+
+  const float mcw = c.min_child_weight, eps = c.l2_reg, msg = c.min_split_gain;
+  for (int d = 0; d <= D; ++d) {
+    const int nodes = 1 << d;
+    const int n_tn = T * nodes;
+    const int n_keys = n_tn * E;
+    const int hcur = d & 1, hprev = hcur ^ 1;
+    if (d < D) {
+      // ---- histograms of the computed segments
+      const int n_list = d == 0 ? n_keys : T * (nodes / 2) * E;
+      const int32_t* list = d == 0 ? nullptr : e->key_list[cur];
+      const int64_t rows_bound = d == 0 ? (int64_t)T * N : ((int64_t)T * N) / 2;
+      const int64_t R = pick_tile_rows(e, rows_bound);
+      const int64_t max_tiles = rows_bound / R + n_list + 1;
+      int r = ensure_partials(e, max_tiles);
+      if (r) return r;
+      if (max_tiles > e->max_htiles) {
+        if (e->htiles) {
+          WGBM_CHECK(hipDeviceSynchronize());
+          for (auto it = e->allocs.begin(); it != e->allocs.end(); ++it)
+            if (*it == e->htiles) {
+              (void)hipFree(*it);
+              e->allocs.erase(it);
+              break;
+            }
+          e->htiles = nullptr;
+        }
+        r = dalloc(e, &e->htiles, max_tiles);
+        if (r) return r;
+        e->max_htiles = max_tiles;
+      }
+      hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur], (int64_t)0,
+                         n_list, list, (int32_t)R, (int32_t)max_tiles, e->htiles, e->hkts, e->hn);
+      WGBM_LAUNCH_CHECK();
+      HistLaunch a;
+      a.codes = c.codes_rm;
+      a.n_rows = N;
+      a.stride = c.stride;
+      a.n_feats = F;
+      a.resid = e->resid;
+      a.resid_tree_stride = N;
+      a.order = e->order[cur];
+      a.tiles = e->htiles;
+      a.n_tiles = e->hn;
+      a.keys_per_tree = nodes * E;
+      a.shifts = e->shifts;
+      a.num_bins = B;
+      a.part_q = e->part_q;
+      a.part_c = e->part_c;
+      a.V = e->V;
+      a.n_chunks = e->n_chunks;
+      a.max_tiles = (int32_t)max_tiles;
+      void* tm = timer_begin("engine_hist_tiles", st);
+      r = launch_hist_tiles(a, st);
+      timer_end(tm, st);
+      if (r) return r;
+      const int64_t fin = (int64_t)n_list * F * B;
+      hipLaunchKernelGGL(hist_finalize_level_kernel, dim3(blocks_for(fin, 256)), dim3(256), 0, st,
+                         e->part_q, e->part_c, e->hkts, list, n_list, e->n_chunks, e->V, B, F, E,
+                         nodes, d, e->hq[hprev], e->hc[hprev], e->hn, e->hq[hcur], e->hc[hcur]);
+      WGBM_LAUNCH_CHECK();
+      // ---- split search + DES selection
+      if (E == 1) {
+        hipLaunchKernelGGL(split_level_e1_kernel, dim3(n_tn), dim3(256), 0, st, e->hq[hcur],
+                           e->hc[hcur], F, B, feat_sel, n_sel, nodes, e->present[cur], e->shifts,
+                           mcw, eps, msg, e->split_l, e->split_b, e->split_gain);
+        WGBM_LAUNCH_CHECK();
+      } else {
+        const int64_t ns = (int64_t)n_tn * E * n_sel;
+        hipLaunchKernelGGL(split_level_scan_kernel, dim3(blocks_for(ns, 256)), dim3(256), 0, st,
+                           e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, n_sel, nodes, n_tn,
+                           e->present[cur], e->shifts, mcw, eps, e->sgain, e->sdir);
+        WGBM_LAUNCH_CHECK();
+        hipLaunchKernelGGL(des_select_kernel, dim3(n_tn), dim3(1024), 0, st, e->sgain, e->sdir, B,
+                           E, n_sel, e->present[cur], msg, e->split_l, e->split_b, e->split_gain);
+        WGBM_LAUNCH_CHECK();
+      }
+    } else {
+      hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st,
+                         e->split_l, (int64_t)n_tn, -1);
+      WGBM_LAUNCH_CHECK();
+    }
+    // ---- leaf values and the tree record of this depth
+    hipLaunchKernelGGL(level_finish_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st, d, D, T,
+                       E, e->present[cur], e->split_l, e->split_b, e->split_gain, feat_sel,
+                       e->totq[cur], e->totc[cur], e->shifts, e->leaf_val, rec);
+    WGBM_LAUNCH_CHECK();
+    // ---- partition (or final leaf update)
+    const int nxt = cur ^ 1;
+    hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur], (int64_t)0,
+                       n_keys, (const int32_t*)nullptr, e->part_tile_rows, (int32_t)e->max_ptiles,
+                       e->ptiles, e->pkts, e->pn);
+    WGBM_LAUNCH_CHECK();
+    if (d < D) {
+      if (fill_u64(e->totq[nxt], (int64_t)n_keys * 2, 0, st) ||
+          fill_u64(e->totc[nxt], (int64_t)n_keys * 2, 0, st))
+        return WGBM_EINVAL;
+    }
+    const int64_t pstride = c.objective == 0 ? 1 : T;
+    const int64_t pcol = c.objective == 0 ? 0 : 1;
+    hipLaunchKernelGGL(partition_count_kernel, dim3((unsigned)e->max_ptiles), dim3(256), 0, st,
+                       e->ptiles, e->pn, e->order[cur], E, nodes, d < D ? 1 : 0, e->split_l,
+                       e->split_b, feat_sel, c.codes_cm, N, e->resid, e->shifts, e->leaf_val,
+                       c.learning_rate, pred, pstride, pcol, e->dirbit, e->tile_left,
+                       e->totq[nxt], e->totc[nxt]);
+    WGBM_LAUNCH_CHECK();
+    if (d < D) {
+      hipLaunchKernelGGL(partition_scan_kernel, dim3(1), dim3(1024), 0, st, T, nodes, E,
+                         e->seg[cur], e->ptiles, e->pkts, e->tile_left, e->split_l, e->Lk,
+                         e->lbase, e->rbase, e->seg[nxt], e->present[nxt], e->key_list[nxt]);
+      WGBM_LAUNCH_CHECK();
+      hipLaunchKernelGGL(partition_scatter_kernel, dim3((unsigned)e->max_ptiles), dim3(256), 0, st,
+                         e->ptiles, e->pn, e->order[cur], E, e->split_l, e->dirbit, e->lbase,
+                         e->rbase, e->order[nxt]);
+      WGBM_LAUNCH_CHECK();
+    }
+    cur = nxt;
+  }
+  return 0;
+}
+
+}  // namespace wgbm

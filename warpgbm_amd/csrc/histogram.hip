@@ -1,0 +1,458 @@
+// Histogram building: per (segment, feature, bin) exact residual sums and row counts.
+//
+// Reference semantics (warpgbm/cuda/histogram_kernel.cu:16-59): for every row
+// s of a node and every feature f, with e = era[s] and b = codes[s, feat[f]],
+// if 0 <= b < B:  G[e,f,b] += residual[s];  H[e,f,b] += 1.
+//
+// MI355X design
+// * Rows are processed in TILES; every tile lies inside one SEGMENT (a run of
+//   the row-order array that shares one histogram: a node, or a (node, era)
+//   pair).  One workgroup = one tile x one chunk of 16*V features.
+// * A wave reads 4 rows at a time; the 16 lanes of a row ("slots") each load V
+//   consecutive code bytes with one buffer load (16 B for V = 16), so a wave
+//   touches 4 x 256 contiguous bytes per instruction.
+// * The workgroup histogram lives in LDS as packed 64-bit words
+//   (q * 2^18 + 1: exact gradient sum and row count in one ds_add_u64).  Word
+//   (j, b, slot) sits at index (j*(B+1) + b)*16 + slot: the slot owns its V
+//   features, so the 16 lanes of a row always address 16 different 8-byte bank
+//   pairs whatever the bin values are -- there are no data-dependent bank
+//   conflicts, only the unavoidable 4-way sharing between the 4 rows.
+//   Bin B is a trash row for out-of-range codes (negative pre-binned codes and
+//   features beyond the end of the row), which keeps the inner loop branch-free.
+// * Each tile writes its partial histogram (exact int64 sum, int32 count) in
+//   the LDS layout; a finalize kernel sums the tiles of a segment (integers, so
+//   in any order) and rounds once to float32.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace wgbm {
+
+// --------------------------------------------------------------------------
+// tile accumulation
+// --------------------------------------------------------------------------
+template <int V>
+struct CodeVec;
+template <>
+struct CodeVec<16> {
+  uint32_t w[4];
+};
+template <>
+struct CodeVec<8> {
+  uint32_t w[2];
+};
+template <>
+struct CodeVec<4> {
+  uint32_t w[1];
+};
+
+template <int V, int MODE>
+__device__ inline CodeVec<V> load_codes(const int8_t* __restrict__ codes,
+                                        __amdgpu_buffer_rsrc_t rs, int64_t off,
+                                        bool valid, int n_valid_bytes) {
+  CodeVec<V> v;
+  if (MODE == kLoadBuffer) {
+    // bounds-checked raw buffer load: an offset past the buffer returns zeros
+    const int o = valid ? (int)off : 0x7fffffff;
+    if constexpr (V == 16) {
+      auto x = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0);
+      v.w[0] = x[0]; v.w[1] = x[1]; v.w[2] = x[2]; v.w[3] = x[3];
+    } else if constexpr (V == 8) {
+      auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, 0);
+      v.w[0] = x[0]; v.w[1] = x[1];
+    } else {
+      v.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, 0);
+    }
+  } else if (MODE == kLoadGlobalAligned) {
+    // row stride and chunk offsets are multiples of V bytes: aligned vector
+    // loads that never run past the row (f_base + V <= stride)
+    typedef uint32_t u32v __attribute__((ext_vector_type(V / 4)));
+    if (valid) {
+      u32v x = __builtin_nontemporal_load(reinterpret_cast<const u32v*>(codes + off));
+#pragma unroll
+      for (int k = 0; k < V / 4; ++k) v.w[k] = x[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < V / 4; ++k) v.w[k] = 0;
+    }
+  } else {
+    // byte loads for unaligned strides; only bytes of real features are read
+#pragma unroll
+    for (int k = 0; k < V / 4; ++k) v.w[k] = 0;
+    if (valid) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        if (j < n_valid_bytes) {
+          uint32_t b = (uint8_t)codes[off + j];
+          v.w[j >> 2] |= b << (8 * (j & 3));
+        }
+      }
+    }
+  }
+  return v;
+}
+
+// One workgroup: tile blockIdx.y x feature chunk blockIdx.x.
+// residual for the tile's tree t = key / keys_per_tree is resid + t*resid_tree_stride
+template <int V, int MODE>
+__global__ __launch_bounds__(512) void hist_tiles_kernel(
+    const int8_t* __restrict__ codes, int64_t n_rows, int64_t stride, int32_t n_feats,
+    const float* __restrict__ resid, int64_t resid_tree_stride,
+    const int32_t* __restrict__ order, const Tile* __restrict__ tiles,
+    const int32_t* __restrict__ n_tiles, int32_t keys_per_tree,
+    const int32_t* __restrict__ shifts, int32_t num_bins,
+    int64_t* __restrict__ part_q, int32_t* __restrict__ part_c) {
+  extern __shared__ unsigned long long lds[];
+  const int n_chunks = (n_feats + 16 * V - 1) / (16 * V);
+  const int tile_id = blockIdx.x / n_chunks;
+  const int chunk = blockIdx.x - tile_id * n_chunks;
+  if (tile_id >= *n_tiles) return;
+  const Tile tl = tiles[tile_id];
+  const int Bp = num_bins + 1;
+  const int nent = V * Bp * 16;
+  for (int i = threadIdx.x; i < nent; i += blockDim.x) lds[i] = 0ull;
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int slot = lane & 15;
+  const int sub = lane >> 4;
+  const int f_base = chunk * 16 * V + slot * V;
+  const bool f_valid = f_base < n_feats;
+  const int tree = tl.key / keys_per_tree;
+  const float* __restrict__ r_t = resid + (int64_t)tree * resid_tree_stride;
+  const int s = shifts[tree];
+  const uint32_t rs_bytes = (MODE == kLoadBuffer) ? (uint32_t)(n_rows * stride) : 0u;
+  const __amdgpu_buffer_rsrc_t rs = wgbm_rsrc(codes, rs_bytes);
+  unsigned long long* my = lds + slot;
+  // bytes of this lane's vector that lie beyond the last feature are forced to
+  // 0xff, which the clamp below sends to the trash bin
+  const int n_valid_bytes = f_valid ? (n_feats - f_base < V ? n_feats - f_base : V) : 0;
+  uint32_t force[V / 4];
+#pragma unroll
+  for (int k = 0; k < V / 4; ++k) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (4 * k + q >= n_valid_bytes) m |= 0xffu << (8 * q);
+    force[k] = m;
+  }
+
+  constexpr int U = 4;  // rows in flight per lane
+  const int64_t step = (int64_t)nwaves * 4;
+  int64_t p = tl.begin + wave * 4 + sub;
+  for (; p < tl.end; p += step * U) {
+    CodeVec<V> cv[U];
+    unsigned long long pk[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t pu = p + u * step;
+      const bool ok = pu < tl.end;
+      const int64_t row = ok ? (order ? (int64_t)order[pu] : pu) : 0;
+      const float r = ok ? r_t[row] : 0.0f;
+      const int64_t q = (int64_t)wgbm_quantise(r, s);
+      // rows beyond the tile add 0 to the trash... they are masked by code below
+      pk[u] = ok ? (unsigned long long)(q * (int64_t)(1 << WGBM_CBITS) + 1) : 0ull;
+      cv[u] = load_codes<V, MODE>(codes, rs, row * stride + f_base, ok && f_valid, n_valid_bytes);
+#pragma unroll
+      for (int k = 0; k < V / 4; ++k) cv[u].w[k] |= force[k];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        uint32_t c = (cv[u].w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+        // out-of-range code (incl. negative int8, read as >= 128) -> trash bin
+        c = c < (uint32_t)num_bins ? c : (uint32_t)num_bins;
+        atomicAdd(my + (j * Bp + (int)c) * 16, pk[u]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // flush in LDS order: part[tile][chunk][j][b][slot] (trash row dropped)
+  const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
+  const int64_t chunk_off = (int64_t)tile_id * tile_words + (int64_t)chunk * 16 * V * num_bins;
+  const int nout = V * num_bins * 16;
+  for (int i = threadIdx.x; i < nout; i += blockDim.x) {
+    const int sl = i & 15;
+    const int jb = i >> 4;          // j*B + b
+    const int j = jb / num_bins;
+    const int b = jb - j * num_bins;
+    const unsigned long long P = lds[(j * Bp + b) * 16 + sl];
+    const int64_t C = (int64_t)(P & (unsigned long long)WGBM_CMASK);
+    const int64_t Q = ((int64_t)P - C) / (int64_t)(1 << WGBM_CBITS);
+    part_q[chunk_off + i] = Q;
+    part_c[chunk_off + i] = (int32_t)C;
+  }
+}
+
+// index of feature f, bin b inside one tile's partial block
+__device__ inline int64_t part_index(int f, int b, int V, int num_bins) {
+  const int chunk = f / (16 * V);
+  const int fl = f - chunk * 16 * V;
+  const int sl = fl / V;
+  const int j = fl - sl * V;
+  return (int64_t)chunk * 16 * V * num_bins + ((int64_t)(j * num_bins + b) << 4) + sl;
+}
+
+// --------------------------------------------------------------------------
+// finalize for the reference-compatible entry point:
+// G_out[e, fo, b] += float(sum over tiles of key e of Q[feat[fo], b]) (and H)
+// --------------------------------------------------------------------------
+__global__ void hist_finalize_f32_kernel(const int64_t* __restrict__ part_q,
+                                         const int32_t* __restrict__ part_c,
+                                         const int32_t* __restrict__ key_tile_start,
+                                         int32_t n_keys, int32_t n_chunks, int32_t V,
+                                         int32_t num_bins, const int32_t* __restrict__ feat_idx,
+                                         int32_t n_out_feats, const int32_t* __restrict__ shifts,
+                                         const uint32_t* __restrict__ absmax_bits,
+                                         const int32_t* __restrict__ n_tiles,
+                                         float* __restrict__ G, float* __restrict__ H) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)n_keys * n_out_feats * num_bins;
+  if (gid >= total) return;
+  const int b = (int)(gid % num_bins);
+  const int fo = (int)((gid / num_bins) % n_out_feats);
+  const int e = (int)(gid / ((int64_t)num_bins * n_out_feats));
+  const int f = feat_idx ? feat_idx[fo] : fo;
+  const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
+  const int64_t idx = part_index(f, b, V, num_bins);
+  int64_t Q = 0, C = 0;
+  const int t_end = key_tile_start[e + 1] < *n_tiles ? key_tile_start[e + 1] : *n_tiles;
+  for (int t = key_tile_start[e]; t < t_end; ++t) {
+    Q += part_q[(int64_t)t * tile_words + idx];
+    C += part_c[(int64_t)t * tile_words + idx];
+  }
+  const bool bad = (*absmax_bits) >= 0x7f800000u;  // non-finite residual seen
+  const float g = bad ? __builtin_nanf("") : wgbm_dequantise(Q, shifts[0]);
+  G[gid] = G[gid] + g;
+  H[gid] = H[gid] + (float)C;
+}
+
+// --------------------------------------------------------------------------
+// finalize for the level-wise engine: exact int64 sums into the level arrays,
+// plus the sibling histogram as (parent - computed child), also exact.
+//   computed key k = (tree, node, era) with node = 2*parent + side
+//   hq/hc layout: [tree][node][era][F][B]
+// --------------------------------------------------------------------------
+__global__ void hist_finalize_level_kernel(
+    const int64_t* __restrict__ part_q, const int32_t* __restrict__ part_c,
+    const int32_t* __restrict__ key_tile_start, const int32_t* __restrict__ key_list,
+    int32_t n_list, int32_t n_chunks, int32_t V, int32_t num_bins,
+    int32_t n_feats, int32_t num_eras, int32_t nodes_in_level, int32_t depth,
+    const int64_t* __restrict__ parent_q, const int32_t* __restrict__ parent_c,
+    const int32_t* __restrict__ n_tiles, int64_t* __restrict__ hq, int32_t* __restrict__ hc) {
+  const int64_t per_key = (int64_t)n_feats * num_bins;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int kk = (int)(gid / per_key);
+  if (kk >= n_list) return;
+  const int key = key_list ? key_list[kk] : kk;
+  if (key < 0) return;
+  const int fb = (int)(gid - (int64_t)kk * per_key);
+  const int f = fb / num_bins;
+  const int b = fb - f * num_bins;
+  const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
+  const int64_t idx = part_index(f, b, V, num_bins);
+  int64_t Q = 0, C = 0;
+  const int t_end = key_tile_start[kk + 1] < *n_tiles ? key_tile_start[kk + 1] : *n_tiles;
+  for (int t = key_tile_start[kk]; t < t_end; ++t) {
+    Q += part_q[(int64_t)t * tile_words + idx];
+    C += part_c[(int64_t)t * tile_words + idx];
+  }
+  const int64_t out = (int64_t)key * per_key + fb;
+  hq[out] = Q;
+  hc[out] = (int32_t)C;
+  if (depth > 0) {
+    // key = ((tree*nodes + node)*E + era)
+    const int era = key % num_eras;
+    const int tn = key / num_eras;
+    const int node = tn % nodes_in_level;
+    const int tree = tn / nodes_in_level;
+    const int sib = node ^ 1;
+    const int parent = node >> 1;
+    const int64_t pkey = ((int64_t)tree * (nodes_in_level >> 1) + parent) * num_eras + era;
+    const int64_t skey = ((int64_t)tree * nodes_in_level + sib) * num_eras + era;
+    hq[skey * per_key + fb] = parent_q[pkey * per_key + fb] - Q;
+    hc[skey * per_key + fb] = parent_c[pkey * per_key + fb] - (int32_t)C;
+  }
+}
+
+// --------------------------------------------------------------------------
+// max |residual| over the rows of a call (ABI path)
+// --------------------------------------------------------------------------
+__global__ void absmax_kernel(const float* __restrict__ resid, const int32_t* __restrict__ rows,
+                              int64_t n, uint32_t* __restrict__ out_bits) {
+  uint32_t m = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = rows ? (int64_t)rows[i] : i;
+    const uint32_t b = wgbm_abs_bits(resid[r]);
+    m = b > m ? b : m;
+  }
+  m = wgbm_wave_max_u32(m);
+  if ((threadIdx.x & 63) == 0) atomicMax(out_bits, m);
+}
+
+__global__ void shift_from_absmax_kernel(const uint32_t* __restrict__ bits, int32_t n, int32_t qbits,
+                                         int32_t* __restrict__ shifts) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t b = bits[i];
+  shifts[i] = b >= 0x7f800000u ? 0 : wgbm_shift_from_absmax(__uint_as_float(b), qbits);
+}
+
+// --------------------------------------------------------------------------
+// tile planner: one workgroup scans segment lengths and emits tiles of at most
+// tile_rows rows that never cross a segment.  keys: either all n_keys (list ==
+// nullptr) or the first *n_list entries of key_list.  seg: int64 [n_keys+1]
+// (nullptr => a single segment [0, total)).
+// --------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void plan_tiles_kernel(
+    const int64_t* __restrict__ seg, int64_t total, int32_t n_keys,
+    const int32_t* __restrict__ key_list, int32_t tile_rows,
+    int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
+    int32_t* __restrict__ n_tiles) {
+  __shared__ int32_t wsum[16];
+  __shared__ int32_t carry;
+  const int nk = n_keys;  // entries of key_list (or keys 0..n_keys-1)
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int base = 0; base < nk; base += blockDim.x) {
+    const int i = base + threadIdx.x;
+    int key = 0, nt = 0;
+    int64_t b0 = 0, b1 = 0;
+    if (i < nk) {
+      key = key_list ? key_list[i] : i;
+      if (key >= 0) {
+        b0 = seg ? seg[key] : 0;
+        b1 = seg ? seg[key + 1] : total;
+        nt = (int)((b1 - b0 + tile_rows - 1) / tile_rows);
+      }
+    }
+    // block exclusive scan of nt
+    int x = nt;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int o = 1; o < 64; o <<= 1) {
+      int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();
+    int wpre = 0;
+    for (int k = 0; k < w; ++k) wpre += wsum[k];
+    const int excl = carry + wpre + x - nt;
+    if (i < nk) {
+      key_tile_start[i] = excl;
+      for (int t = 0; t < nt; ++t) {
+        const int id = excl + t;
+        if (id < max_tiles) {
+          Tile tl;
+          tl.key = key;
+          tl.begin = b0 + (int64_t)t * tile_rows;
+          tl.end = tl.begin + tile_rows < b1 ? tl.begin + tile_rows : b1;
+          tiles[id] = tl;
+        }
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == blockDim.x - 1) carry = excl + nt;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    key_tile_start[nk] = carry;
+    *n_tiles = carry < max_tiles ? carry : max_tiles;
+  }
+}
+
+// --------------------------------------------------------------------------
+// era sort for the ABI path: rows -> era-grouped positions
+// --------------------------------------------------------------------------
+__global__ void era_count_kernel(const int32_t* __restrict__ rows, int64_t n,
+                                 const int32_t* __restrict__ era, int32_t num_eras,
+                                 int64_t* __restrict__ counts) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int e = era[rows ? rows[i] : i];
+    if (e >= 0 && e < num_eras) atomicAdd((unsigned long long*)&counts[e], 1ull);
+  }
+}
+
+__global__ void exclusive_scan_i64_kernel(const int64_t* __restrict__ in, int32_t n,
+                                          int64_t* __restrict__ out) {
+  // single thread; n is the number of eras (small)
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    int64_t acc = 0;
+    for (int i = 0; i < n; ++i) {
+      out[i] = acc;
+      acc += in[i];
+    }
+    out[n] = acc;
+  }
+}
+
+__global__ void era_scatter_kernel(const int32_t* __restrict__ rows, int64_t n,
+                                   const int32_t* __restrict__ era, int32_t num_eras,
+                                   unsigned long long* __restrict__ cursor,
+                                   int32_t* __restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t r = rows ? rows[i] : (int32_t)i;
+    const int e = era[r];
+    if (e >= 0 && e < num_eras) out[atomicAdd(&cursor[e], 1ull)] = r;
+  }
+}
+
+// --------------------------------------------------------------------------
+// host launch helpers
+// --------------------------------------------------------------------------
+int hist_pick_v(int num_bins) {
+  const int bp = num_bins + 1;
+  if (16 * bp <= 544) return 16;  // num_bins <= 33
+  if (8 * bp <= 544) return 8;    // num_bins <= 67
+  return 4;
+}
+
+size_t hist_lds_bytes(int V, int num_bins) { return (size_t)V * (num_bins + 1) * 16 * 8; }
+
+template <int V, int MODE>
+static int launch_tiles_t(const HistLaunch& a, hipStream_t st) {
+  static bool attr_set = false;
+  const size_t lds = hist_lds_bytes(V, a.num_bins);
+  if (!attr_set) {
+    WGBM_CHECK(hipFuncSetAttribute((const void*)hist_tiles_kernel<V, MODE>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr_set = true;
+  }
+  dim3 grid((unsigned)((int64_t)a.n_chunks * a.max_tiles));
+  hipLaunchKernelGGL((hist_tiles_kernel<V, MODE>), grid, dim3(512), lds, st, a.codes, a.n_rows,
+                     a.stride, a.n_feats, a.resid, a.resid_tree_stride, a.order, a.tiles,
+                     a.n_tiles, a.keys_per_tree, a.shifts, a.num_bins, a.part_q, a.part_c);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+int hist_load_mode(int64_t n_rows, int64_t stride, int V) {
+  if (n_rows * stride < ((int64_t)1 << 31) && stride % 4 == 0) return kLoadBuffer;
+  if (stride % V == 0) return kLoadGlobalAligned;
+  return kLoadBytes;
+}
+
+int launch_hist_tiles(const HistLaunch& a, hipStream_t st) {
+  const int mode = hist_load_mode(a.n_rows, a.stride, a.V);
+#define WGBM_DISPATCH(VV)                                                   \
+  if (a.V == VV) {                                                          \
+    if (mode == kLoadBuffer) return launch_tiles_t<VV, kLoadBuffer>(a, st); \
+    if (mode == kLoadGlobalAligned)                                         \
+      return launch_tiles_t<VV, kLoadGlobalAligned>(a, st);                 \
+    return launch_tiles_t<VV, kLoadBytes>(a, st);                           \
+  }
+  WGBM_DISPATCH(16)
+  WGBM_DISPATCH(8)
+  WGBM_DISPATCH(4)
+#undef WGBM_DISPATCH
+  wgbm_set_error("launch_hist_tiles: bad V=%d", a.V);
+  return WGBM_EINVAL;
+}
+
+}  // namespace wgbm

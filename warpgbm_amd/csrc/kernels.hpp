@@ -1,0 +1,87 @@
+// Internal (C++) declarations shared by the kernel translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wgbm {
+
+// A run of row-order positions [begin, end) that all belong to segment `key`.
+struct Tile {
+  int32_t key;
+  int32_t pad;
+  int64_t begin;
+  int64_t end;
+};
+
+enum { kLoadBuffer = 0, kLoadGlobalAligned = 1, kLoadBytes = 2 };
+
+struct HistLaunch {
+  const int8_t* codes;
+  int64_t n_rows;
+  int64_t stride;
+  int32_t n_feats;
+  const float* resid;
+  int64_t resid_tree_stride;
+  const int32_t* order;
+  const Tile* tiles;
+  const int32_t* n_tiles;
+  int32_t keys_per_tree;
+  const int32_t* shifts;
+  int32_t num_bins;
+  int64_t* part_q;
+  int32_t* part_c;
+  int32_t V;
+  int32_t n_chunks;
+  int32_t max_tiles;
+};
+
+int hist_pick_v(int num_bins);
+size_t hist_lds_bytes(int V, int num_bins);
+int hist_load_mode(int64_t n_rows, int64_t stride, int V);
+int launch_hist_tiles(const HistLaunch& a, hipStream_t st);
+
+// kernels launched directly from other translation units
+__global__ void hist_finalize_f32_kernel(const int64_t* part_q, const int32_t* part_c,
+                                         const int32_t* key_tile_start, int32_t n_keys,
+                                         int32_t n_chunks, int32_t V, int32_t num_bins,
+                                         const int32_t* feat_idx, int32_t n_out_feats,
+                                         const int32_t* shifts, const uint32_t* absmax_bits,
+                                         const int32_t* n_tiles, float* G, float* H);
+__global__ void hist_finalize_level_kernel(
+    const int64_t* part_q, const int32_t* part_c, const int32_t* key_tile_start,
+    const int32_t* key_list, int32_t n_list, int32_t n_chunks, int32_t V,
+    int32_t num_bins, int32_t n_feats, int32_t num_eras, int32_t nodes_in_level, int32_t depth,
+    const int64_t* parent_q, const int32_t* parent_c, const int32_t* n_tiles, int64_t* hq,
+    int32_t* hc);
+__global__ void absmax_kernel(const float* resid, const int32_t* rows, int64_t n,
+                              uint32_t* out_bits);
+__global__ void shift_from_absmax_kernel(const uint32_t* bits, int32_t n, int32_t qbits,
+                                         int32_t* shifts);
+__global__ void plan_tiles_kernel(const int64_t* seg, int64_t total, int32_t n_keys,
+                                  const int32_t* key_list, int32_t tile_rows, int32_t max_tiles, Tile* tiles,
+                                  int32_t* key_tile_start, int32_t* n_tiles);
+__global__ void era_count_kernel(const int32_t* rows, int64_t n, const int32_t* era,
+                                 int32_t num_eras, int64_t* counts);
+__global__ void exclusive_scan_i64_kernel(const int64_t* in, int32_t n, int64_t* out);
+__global__ void era_scatter_kernel(const int32_t* rows, int64_t n, const int32_t* era,
+                                   int32_t num_eras, unsigned long long* cursor, int32_t* out);
+
+// generic fills (graph-safe replacement for memset)
+__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v);
+__global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v);
+int fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t st);
+int fill_u64(void* p, int64_t n, unsigned long long v, hipStream_t st);
+
+// per-device scratch arena owned by the library (grow-only, stream-keyed)
+void* scratch_get(hipStream_t st, size_t bytes, int slot);
+void scratch_release_all();
+
+// optional HIP-event timers around selected kernels
+bool timer_enabled();
+void* timer_begin(const char* tag, hipStream_t st);
+void timer_end(void* h, hipStream_t st);
+void timer_enable(int on);
+int timer_read(const char* tag, double* total_ms, long* count);
+void timer_reset();
+
+}  // namespace wgbm

@@ -1,0 +1,189 @@
+"""Device-side building blocks of the estimator: ingestion and binning, era
+bookkeeping, the level-wise engine and ensemble inference.
+
+Everything here runs the HIP library through its C ABI; torch only provides
+device memory, copies and the stream.  Calling any of it without the built
+library (or without a GPU) raises -- there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+
+
+def _stream(dev) -> int:
+    return _lib.current_stream_ptr(dev)
+
+
+def codes_stride(n_feats: int) -> int:
+    """Row stride (bytes) of the int8 code matrix: a multiple of 16, and of 128
+    once a row spans several cache lines, so that the 256-byte feature chunks
+    read by one histogram workgroup never straddle a row boundary."""
+    if n_feats <= 128:
+        return (n_feats + 15) // 16 * 16
+    return (n_feats + 127) // 128 * 128
+
+
+def quantile_levels(num_bins: int) -> torch.Tensor:
+    """``torch.linspace(0, 1, num_bins + 1)[1:-1]`` in float32 (warpgbm/core.py:529-531)."""
+    return torch.linspace(0, 1, num_bins + 1, dtype=torch.float32)[1:-1].contiguous()
+
+
+@dataclass
+class Codes:
+    """Binned matrix on the device: row-major (padded) and column-major copies."""
+    rm: torch.Tensor        # int8 [n, stride]
+    cm: torch.Tensor | None  # int8 [F, n]
+    n: int
+    n_feats: int
+    stride: int
+
+
+def _alloc_codes(n: int, F: int, dev, with_cm: bool) -> Codes:
+    S = codes_stride(F)
+    rm = torch.empty((n, S), dtype=torch.int8, device=dev)
+    cm = torch.empty((F, n), dtype=torch.int8, device=dev) if with_cm else None
+    return Codes(rm, cm, n, F, S)
+
+
+def upload_prebinned(X: np.ndarray, dev, with_cm: bool) -> Codes:
+    """Integer input whose columns are all < num_bins is used as codes directly
+    (warpgbm/core.py:499-517); values are cast to int8 like the reference's
+    ``bin_indices[:, f] = torch.as_tensor(X[:, f])``."""
+    n, F = X.shape
+    x8 = torch.from_numpy(np.ascontiguousarray(X).astype(np.int8, copy=False)).to(dev)
+    c = _alloc_codes(n, F, dev, with_cm)
+    lib = _lib.load()
+    rc = lib.wgbm_copy_prebinned(x8.data_ptr(), n, F, F, c.rm.data_ptr(), c.stride,
+                                 c.cm.data_ptr() if c.cm is not None else None, _stream(dev))
+    _lib.check(rc, "copy_prebinned")
+    return c
+
+
+def upload_float(X: np.ndarray, dev) -> torch.Tensor:
+    """float32 [n, F] contiguous copy of X on the device (float64 input is
+    rounded to float32 first, as ``torch.as_tensor(..., dtype=float32)``)."""
+    return torch.from_numpy(np.ascontiguousarray(X, dtype=np.float32)).to(dev)
+
+
+def quantile_edges(Xd: torch.Tensor, num_bins: int, chunk: int = 256) -> torch.Tensor:
+    """Per-feature quantile edges [F, num_bins - 1] (the torch.quantile call of
+    warpgbm/core.py:529-534).  Columns are sorted on the device, then the
+    edge formula runs in the HIP kernel ``wgbm_quantile_edges``."""
+    n, F = Xd.shape
+    if n > (1 << 24):
+        raise ValueError("quantile() input tensor is too large (more than 2^24 rows per feature)")
+    dev = Xd.device
+    q = quantile_levels(num_bins).to(dev)
+    nq = num_bins - 1
+    edges = torch.empty((F, nq), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    for f0 in range(0, F, chunk):
+        f1 = min(F, f0 + chunk)
+        cols = Xd[:, f0:f1].t().contiguous()
+        srt = torch.sort(cols, dim=1).values
+        rc = lib.wgbm_quantile_edges(srt.data_ptr(), n, f1 - f0, q.data_ptr(), nq,
+                                     edges[f0:f1].data_ptr(), _stream(dev))
+        _lib.check(rc, "quantile_edges")
+        del cols, srt
+    return edges
+
+
+def bin_matrix(Xd: torch.Tensor, edges: torch.Tensor, with_cm: bool) -> Codes:
+    """All columns binned in one launch (the per-feature binner loop of
+    warpgbm/core.py:527-538 and :908-913)."""
+    n, F = Xd.shape
+    edges = edges.to(device=Xd.device, dtype=torch.float32).contiguous()
+    if edges.shape[0] != F:
+        raise ValueError(f"edges for {edges.shape[0]} features, X has {F}")
+    c = _alloc_codes(n, F, Xd.device, with_cm)
+    lib = _lib.load()
+    rc = lib.wgbm_bin_matrix(Xd.data_ptr(), n, F, F, edges.data_ptr(), edges.shape[1],
+                             c.rm.data_ptr(), c.stride,
+                             c.cm.data_ptr() if c.cm is not None else None, _stream(Xd.device))
+    _lib.check(rc, "bin_matrix")
+    return c
+
+
+def era_layout(era_id: np.ndarray):
+    """Sorted unique eras, era index per row, rows sorted by era (stable) and
+    era offsets (warpgbm/core.py:540: torch.unique(..., return_inverse=True))."""
+    uniq, inv = np.unique(np.asarray(era_id), return_inverse=True)
+    inv = inv.astype(np.int32).reshape(-1)
+    order = np.argsort(inv, kind="stable").astype(np.int32)
+    counts = np.bincount(inv, minlength=len(uniq)).astype(np.int64)
+    start = np.zeros(len(uniq) + 1, dtype=np.int64)
+    np.cumsum(counts, out=start[1:])
+    return uniq, inv, order, start
+
+
+class Engine:
+    """Owner of a native level-wise engine (``wgbm_engine_*``)."""
+
+    def __init__(self, codes: Codes, root_order: torch.Tensor, era_start: torch.Tensor,
+                 num_bins: int, num_eras: int, max_depth: int, n_trees: int, objective: int,
+                 min_child_weight: float, min_split_gain: float, l2_reg: float,
+                 learning_rate: float):
+        self.lib = _lib.load()
+        self._keep = (codes, root_order, era_start)
+        cfg = _lib.EngineConfig(
+            n_rows=codes.n, n_feats=codes.n_feats, codes_stride=codes.stride, num_bins=num_bins,
+            num_eras=num_eras, max_depth=max_depth, n_trees=n_trees, objective=objective,
+            min_child_weight=float(min_child_weight), min_split_gain=float(min_split_gain),
+            l2_reg=float(l2_reg), learning_rate=float(learning_rate),
+            codes_rm=codes.rm.data_ptr(), codes_cm=codes.cm.data_ptr(),
+            root_order=root_order.data_ptr(), era_start=era_start.data_ptr())
+        h = C.c_void_p()
+        _lib.check(self.lib.wgbm_engine_create(C.byref(h), C.byref(cfg)), "engine_create")
+        self.h = h
+        self.H = (1 << (max_depth + 1)) - 1
+        self.n_trees = n_trees
+        self.num_eras = num_eras
+
+    def set_tuning(self, key: int, value: int) -> None:
+        _lib.check(self.lib.wgbm_engine_set_tuning(self.h, key, value), "engine_set_tuning")
+
+    def round(self, target: torch.Tensor, pred: torch.Tensor, feat_sel: torch.Tensor,
+              rec: dict) -> None:
+        r = _lib.TreeRecord(feat=rec["feat"].data_ptr(), bin=rec["bin"].data_ptr(),
+                            leaf=rec["leaf"].data_ptr(), count=rec["count"].data_ptr(),
+                            gain=rec["gain"].data_ptr(), H=self.H)
+        rc = self.lib.wgbm_engine_round(self.h, target.data_ptr(), pred.data_ptr(),
+                                        feat_sel.data_ptr(), feat_sel.numel(), C.byref(r),
+                                        _stream(pred.device))
+        _lib.check(rc, "engine_round")
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            self.lib.wgbm_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def predict_heap(codes: Codes, feat: torch.Tensor, bin_: torch.Tensor, leaf: torch.Tensor,
+                 n_rounds: int, K: int, max_depth: int, learning_rate: float,
+                 out: torch.Tensor) -> None:
+    """Add the contributions of ``n_rounds`` rounds of K heap-ordered trees to
+    ``out`` [n, K] (one launch; cf. warpgbm/core.py:917-932, 991-1030)."""
+    H = (1 << (max_depth + 1)) - 1
+    lib = _lib.load()
+    rc = lib.wgbm_predict_heap(codes.rm.data_ptr(), codes.n, codes.stride, feat.data_ptr(),
+                               bin_.data_ptr(), leaf.data_ptr(), n_rounds, K, H, max_depth,
+                               float(learning_rate), out.data_ptr(), _stream(out.device))
+    _lib.check(rc, "predict_heap")
+
+
+def softmax_rows(x: torch.Tensor) -> None:
+    lib = _lib.load()
+    n, K = x.shape
+    _lib.check(lib.wgbm_softmax_rows(x.data_ptr(), n, K, _stream(x.device)), "softmax_rows")
