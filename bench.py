@@ -120,7 +120,7 @@ def main():
     step()
     torch.cuda.synchronize()
     assert torch.all(H1.sum(dim=2) == N), "root histogram counts are wrong"
-    assert torch.equal(H16.sum(dim=0), H1), "16-node counts do not add up to the root"
+    assert torch.equal(H16.sum(dim=0), H1[0]), "16-node counts do not add up to the root"
     lib.wgbm_timer_reset()
     lib.wgbm_timer_enable(1)
     e0 = torch.cuda.Event(enable_timing=True)

@@ -125,14 +125,25 @@ def test_warm_start_and_save_load(gpu, tmp_path):
 def test_eval_and_early_stopping(gpu):
     print_case("estimator", "eval set")
     X, y = c1_data(n=4000, f=20, seed=5)
-    m = WarpGBM(num_bins=16, max_depth=3, n_estimators=30, learning_rate=0.3)
+    # 31 trees: evaluation runs at i = 0, 2, ..., 30, so the last one sees all trees
+    m = WarpGBM(num_bins=16, max_depth=3, n_estimators=31, learning_rate=0.3)
     m.fit(X[:3000], y[:3000], X_eval=X[3000:], y_eval=y[3000:], eval_every_n_trees=2,
           early_stopping_rounds=2, eval_metric="mse")
-    assert len(m.eval_loss) >= 1 and len(m.training_loss) >= 1
+    assert len(m.training_loss) == m._trees_trained
     assert m.training_loss[-1] < m.training_loss[0]
-    # eval predictions tracked during training equal predict() on the eval set
-    p = m.predict(X[3000:])
-    assert abs(((y[3000:] - p) ** 2).mean() - m.eval_loss[-1]) < 1e-4 * (1 + m.eval_loss[-1])
+    if m._trees_trained == 31:
+        # eval predictions tracked during training equal predict() on the eval set
+        p = m.predict(X[3000:])
+        assert abs(float(((y[3000:] - p) ** 2).mean()) - m.eval_loss[-1]) <= 1e-5 * m.eval_loss[-1]
+    else:
+        # stopped early: the last eval loss rose against the one esr evaluations before
+        assert m.eval_loss[-3] < m.eval_loss[-1]
+    # early stopping triggers on a metric that gets worse: 1 - corr on a shuffled target
+    rng = np.random.default_rng(0)
+    m2 = WarpGBM(num_bins=16, max_depth=3, n_estimators=60, learning_rate=1.0)
+    m2.fit(X[:3000], y[:3000], X_eval=X[3000:], y_eval=rng.permutation(y[3000:]),
+           eval_every_n_trees=1, early_stopping_rounds=3, eval_metric="corr")
+    assert m2._trees_trained < 60
 
 
 def test_binary_objective(gpu):
