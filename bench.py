@@ -89,7 +89,13 @@ def main():
     N, F, B = args.rows, args.feats, 32
     print(f"[bench] generating C2 inputs {N}x{F}", file=sys.stderr, flush=True)
     codes_h, grad_h, node_h = c2_inputs(N, F)
-    codes = torch.from_numpy(codes_h).to(dev)
+    # the library's code layout: rows padded to a 128-byte multiple with -1
+    # (what the binner writes); algorithmic bytes still count F bytes per row
+    from warpgbm_amd.device import codes_stride
+
+    S = codes_stride(F)
+    codes = torch.full((N, S), -1, dtype=torch.int8, device=dev)
+    codes[:, :F] = torch.from_numpy(codes_h).to(dev)
     grad = torch.from_numpy(grad_h).to(dev)
     order16_h = np.argsort(node_h, kind="stable").astype(np.int32)
     seg16_h = np.zeros(17, np.int64)
@@ -104,10 +110,10 @@ def main():
     stream = _lib.current_stream_ptr(dev)
 
     def step():
-        _lib.check(lib.wgbm_histogram_segments(codes.data_ptr(), N, F, F, grad.data_ptr(), None,
+        _lib.check(lib.wgbm_histogram_segments(codes.data_ptr(), N, S, F, grad.data_ptr(), None,
                                                seg1.data_ptr(), 1, N, B, G1.data_ptr(),
                                                H1.data_ptr(), stream), "hist root")
-        _lib.check(lib.wgbm_histogram_segments(codes.data_ptr(), N, F, F, grad.data_ptr(),
+        _lib.check(lib.wgbm_histogram_segments(codes.data_ptr(), N, S, F, grad.data_ptr(),
                                                order16.data_ptr(), seg16.data_ptr(), 16, N, B,
                                                G16.data_ptr(), H16.data_ptr(), stream),
                    "hist 16 nodes")
@@ -205,7 +211,7 @@ def main():
         "dtype": "int8 codes / int64 exact sums",
         "data": "synthetic (numpy default_rng(0), BASELINE configs C2/C3)",
         "config": {"workload": f"C2 histogram: root + 16 nodes, {N}x{F} int8, 32 bins, 1 era",
-                   "rows": N, "features": F, "bins": B, "nodes": [1, 16]},
+                   "rows": N, "features": F, "bins": B, "nodes": [1, 16], "row_stride": S},
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(k_achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(k_achieved / HBM_PEAK_GBS, 4),

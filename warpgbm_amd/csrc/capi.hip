@@ -29,19 +29,20 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
                               hipStream_t st) {
   const int V = hist_pick_v(num_bins);
   const int n_chunks = (n_hist_feats + 16 * V - 1) / (16 * V);
-  // scratch layout (slot 0: small control words)
-  uint32_t* absmax = (uint32_t*)scratch_get(st, 256, 0);
-  WGBM_REQUIRE(absmax, "scratch allocation failed");
-  int32_t* shift = (int32_t*)(absmax + 16);
-  int32_t* n_tiles = shift + 16;
-  WGBM_CHECK((hipError_t)fill_u32(absmax, 1, 0u, st));
-  if (n_pos > 0) {
-    hipLaunchKernelGGL(absmax_kernel, dim3(std::min<int64_t>(nblocks(n_pos, 256), 2048)),
-                       dim3(256), 0, st, resid, rows, n_pos, absmax);
-    WGBM_LAUNCH_CHECK();
-  }
-  hipLaunchKernelGGL(shift_from_absmax_kernel, dim3(1), dim3(64), 0, st, absmax, 1,
-                     wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1)), shift);
+  // scratch layout (slot 0: control words and the per-block maxima)
+  constexpr int kAbsBlocks = 512;
+  uint32_t* ctl = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (64 + kAbsBlocks), 0);
+  WGBM_REQUIRE(ctl, "scratch allocation failed");
+  uint32_t* absmax = ctl;
+  int32_t* shift = (int32_t*)(ctl + 16);
+  int32_t* n_tiles = (int32_t*)(ctl + 32);
+  uint32_t* abs_part = ctl + 64;
+  const int n_abs = (int)std::max<int64_t>(1, std::min<int64_t>(nblocks(n_pos, 256), kAbsBlocks));
+  hipLaunchKernelGGL(absmax_partial_kernel, dim3(n_abs), dim3(256), 0, st, resid, rows, n_pos,
+                     abs_part);
+  WGBM_LAUNCH_CHECK();
+  hipLaunchKernelGGL(absmax_finish_kernel, dim3(1), dim3(256), 0, st, abs_part, n_abs,
+                     wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1)), absmax, shift);
   WGBM_LAUNCH_CHECK();
 
   // segments: explicit (seg_dev), by era (sort rows by era), or a single one
@@ -74,18 +75,18 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
     n_keys = 1;
   }
 
-  // tiles: ~4 workgroups per CU over the whole call
-  int64_t tiles_target = std::max<int64_t>(1, 1024 / n_chunks);
+  // tiles: ~2 workgroups per CU over the whole call
+  int64_t tiles_target = std::max<int64_t>(1, kHistTargetWG / n_chunks);
   int64_t R = (n_pos + tiles_target - 1) / tiles_target;
   R = std::min<int64_t>(std::max<int64_t>((R + 255) / 256 * 256, 1024), WGBM_MAX_TILE_ROWS);
   const int64_t max_tiles = n_pos / R + n_keys + 1;
   Tile* tiles = (Tile*)scratch_get(st, sizeof(Tile) * max_tiles, 3);
   int32_t* kts = (int32_t*)scratch_get(st, sizeof(int32_t) * ((size_t)n_keys + 1), 4);
-  const int64_t words = max_tiles * n_chunks * 16 * V * num_bins;
-  int64_t* part_q = (int64_t*)scratch_get(st, sizeof(int64_t) * words, 5);
-  int32_t* part_c = (int32_t*)scratch_get(st, sizeof(int32_t) * words, 6);
-  WGBM_REQUIRE(tiles && kts && part_q && part_c, "scratch allocation failed (%lld words)",
-               (long long)words);
+  const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
+  const int64_t words = max_tiles * tile_words;
+  unsigned long long* part =
+      (unsigned long long*)scratch_get(st, sizeof(unsigned long long) * words, 5);
+  WGBM_REQUIRE(tiles && kts && part, "scratch allocation failed (%lld words)", (long long)words);
   hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, seg, n_pos, n_keys,
                      (const int32_t*)nullptr, (int32_t)R, (int32_t)max_tiles, tiles, kts, n_tiles);
   WGBM_LAUNCH_CHECK();
@@ -102,8 +103,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   a.keys_per_tree = n_keys;
   a.shifts = shift;
   a.num_bins = num_bins;
-  a.part_q = part_q;
-  a.part_c = part_c;
+  a.part = part;
   a.V = V;
   a.n_chunks = n_chunks;
   a.max_tiles = (int32_t)max_tiles;
@@ -111,11 +111,26 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   int r = launch_hist_tiles(a, st);
   timer_end(tm, st);
   if (r) return r;
-  const int64_t fin = (int64_t)n_keys * n_out_feats * num_bins;
-  if (fin > 0) {
-    hipLaunchKernelGGL(hist_finalize_f32_kernel, dim3(nblocks(fin, 256)), dim3(256), 0, st, part_q,
-                       part_c, kts, n_keys, n_chunks, V, num_bins, feat_idx, n_out_feats, shift,
-                       absmax, n_tiles, G, H);
+  const unsigned fin_wg = (unsigned)(n_keys * ((tile_words + 31) / 32));
+  if (!feat_idx) {
+    // identity feature map: finalize straight into the (accumulated) outputs
+    hipLaunchKernelGGL(hist_finalize_f32_kernel, dim3(fin_wg), dim3(256), 0, st, part,
+                       kts, n_keys, n_chunks, V, num_bins, n_hist_feats, shift, absmax, n_tiles,
+                       1, G, H);
+    WGBM_LAUNCH_CHECK();
+  } else {
+    // full-width histogram in scratch, then the requested features
+    const int64_t full = (int64_t)n_keys * n_hist_feats * num_bins;
+    float* Gf = (float*)scratch_get(st, sizeof(float) * 2 * full, 7);
+    WGBM_REQUIRE(Gf, "scratch allocation failed");
+    float* Hf = Gf + full;
+    hipLaunchKernelGGL(hist_finalize_f32_kernel, dim3(fin_wg), dim3(256), 0, st, part,
+                       kts, n_keys, n_chunks, V, num_bins, n_hist_feats, shift, absmax, n_tiles,
+                       0, Gf, Hf);
+    WGBM_LAUNCH_CHECK();
+    const int64_t nout = (int64_t)n_keys * n_out_feats * num_bins;
+    hipLaunchKernelGGL(hist_gather_features_kernel, dim3(nblocks(nout, 256)), dim3(256), 0, st, Gf,
+                       Hf, n_keys, n_hist_feats, num_bins, feat_idx, n_out_feats, G, H);
     WGBM_LAUNCH_CHECK();
   }
   return 0;

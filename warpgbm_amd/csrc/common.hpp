@@ -118,6 +118,20 @@ __device__ inline uint32_t wgbm_wave_max_u32(uint32_t v) {
   return v;
 }
 
+// block-wide max (blockDim.x a multiple of 64, at most 1024); result valid in
+// every thread
+__device__ inline uint32_t wgbm_block_max_u32(uint32_t v) {
+  __shared__ uint32_t s_red[16];
+  v = wgbm_wave_max_u32(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) s_red[w] = v;
+  __syncthreads();
+  uint32_t m = 0;
+  for (int k = 0; k < (int)(blockDim.x >> 6); ++k) m = s_red[k] > m ? s_red[k] : m;
+  __syncthreads();
+  return m;
+}
+
 // Deterministic exp for softmax (x <= 0 expected, any finite x accepted).
 // Cody-Waite reduction x = k*ln2 + r with a two-part ln2, then the degree-7
 // Taylor polynomial of e^r on |r| <= ln2/2 (truncation < 6e-9 relative),

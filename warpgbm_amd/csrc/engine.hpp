@@ -49,9 +49,9 @@ int engine_set_tuning(Engine* e, int key, int64_t value);
 
 // kernels (engine_kernels.hip)
 __global__ void residual_regression_kernel(const float* y, const float* pred, int64_t n,
-                                           float* r, uint32_t* absmax);
+                                           float* r, uint32_t* partial);
 __global__ void residual_softmax_kernel(const float* logits, const int32_t* label, int64_t n,
-                                        int32_t K, float* r, uint32_t* absmax);
+                                        int32_t K, float* r, uint32_t* partial);
 __global__ void root_setup_kernel(const int32_t* root_order, int64_t n, int32_t T,
                                   const int64_t* era_start, int32_t E, int32_t* order,
                                   int64_t* seg, int32_t* present);

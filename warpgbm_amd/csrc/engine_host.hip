@@ -20,6 +20,8 @@
 
 namespace wgbm {
 
+constexpr int kResidBlocks = 1024;  // workgroups of the residual kernels
+
 struct Engine {
   EngineConfig c;
   int V = 16, n_chunks = 1, qbits = 28;
@@ -48,8 +50,8 @@ struct Engine {
   Tile* htiles = nullptr;
   int32_t* hkts = nullptr;
   int32_t* hn = nullptr;
-  int64_t* part_q = nullptr;
-  int32_t* part_c = nullptr;
+  unsigned long long* part = nullptr;
+  uint32_t* abs_part = nullptr;
   int64_t part_words = 0;
   int64_t* hq[2] = {nullptr, nullptr};
   int32_t* hc[2] = {nullptr, nullptr};
@@ -119,6 +121,7 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   const int64_t hist_nodes_max = int64_t(1) << (D - 1);  // deepest level with histograms
   E_ALLOC(e->resid, T * N);
   E_ALLOC(e->absmax, T);
+  E_ALLOC(e->abs_part, T * kResidBlocks);
   E_ALLOC(e->shifts, T);
   for (int k = 0; k < 2; ++k) {
     E_ALLOC(e->order[k], T * N);
@@ -164,10 +167,10 @@ int engine_set_tuning(Engine* e, int key, int64_t value) {
   return WGBM_EINVAL;
 }
 
-// histogram tile rows for a level: enough tiles for ~4 workgroups per CU
+// histogram tile rows for a level: enough tiles for ~2 workgroups per CU
 static int64_t pick_tile_rows(const Engine* e, int64_t rows_bound) {
   if (e->hist_tile_rows > 0) return e->hist_tile_rows;
-  const int64_t target_wg = 256 * 4;
+  const int64_t target_wg = kHistTargetWG;
   int64_t tiles = std::max<int64_t>(1, target_wg / e->n_chunks);
   int64_t r = (rows_bound + tiles - 1) / tiles;
   r = (r + 255) / 256 * 256;
@@ -177,23 +180,18 @@ static int64_t pick_tile_rows(const Engine* e, int64_t rows_bound) {
 static int ensure_partials(Engine* e, int64_t max_tiles) {
   const int64_t words = max_tiles * e->n_chunks * 16 * e->V * e->c.num_bins;
   if (words <= e->part_words) return 0;
-  if (e->part_q) {
+  if (e->part) {
     // partial buffers are only reused within the stream; grow after a sync
     WGBM_CHECK(hipDeviceSynchronize());
-    for (auto it = e->allocs.begin(); it != e->allocs.end();) {
-      if (*it == e->part_q || *it == e->part_c) {
+    for (auto it = e->allocs.begin(); it != e->allocs.end(); ++it)
+      if (*it == e->part) {
         (void)hipFree(*it);
-        it = e->allocs.erase(it);
-      } else {
-        ++it;
+        e->allocs.erase(it);
+        break;
       }
-    }
-    e->part_q = nullptr;
-    e->part_c = nullptr;
+    e->part = nullptr;
   }
-  int r = dalloc(e, &e->part_q, words);
-  if (r) return r;
-  r = dalloc(e, &e->part_c, words);
+  int r = dalloc(e, &e->part, words);
   if (r) return r;
   e->part_words = words;
   return 0;
@@ -210,18 +208,19 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   const int T = c.n_trees, E = c.num_eras, F = c.n_feats, B = c.num_bins, D = c.max_depth;
   const int64_t N = c.n_rows;
 
-  // residuals and quantisation shifts
-  WGBM_CHECK((hipError_t)fill_u32(e->absmax, T, 0u, st));
+  // residuals and quantisation shifts (per-workgroup maxima, then one
+  // workgroup per tree reduces them)
+  const int nres = (int)std::max<int64_t>(1, std::min<int64_t>(blocks_for(N, 256), kResidBlocks));
   if (c.objective == 0) {
-    hipLaunchKernelGGL(residual_regression_kernel, dim3(std::min<int64_t>(blocks_for(N, 256), 4096)),
-                       dim3(256), 0, st, (const float*)target, pred, N, e->resid, e->absmax);
+    hipLaunchKernelGGL(residual_regression_kernel, dim3(nres), dim3(256), 0, st,
+                       (const float*)target, pred, N, e->resid, e->abs_part);
   } else {
-    hipLaunchKernelGGL(residual_softmax_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, st,
-                       pred, (const int32_t*)target, N, T, e->resid, e->absmax);
+    hipLaunchKernelGGL(residual_softmax_kernel, dim3(nres), dim3(256), 0, st, pred,
+                       (const int32_t*)target, N, T, e->resid, e->abs_part);
   }
   WGBM_LAUNCH_CHECK();
-  hipLaunchKernelGGL(shift_from_absmax_kernel, dim3(1), dim3(256), 0, st, e->absmax, T, e->qbits,
-                     e->shifts);
+  hipLaunchKernelGGL(absmax_finish_kernel, dim3(T), dim3(256), 0, st, e->abs_part, nres, e->qbits,
+                     e->absmax, e->shifts);
   WGBM_LAUNCH_CHECK();
 
   // root segments and totals
@@ -287,8 +286,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       a.keys_per_tree = nodes * E;
       a.shifts = e->shifts;
       a.num_bins = B;
-      a.part_q = e->part_q;
-      a.part_c = e->part_c;
+      a.part = e->part;
       a.V = e->V;
       a.n_chunks = e->n_chunks;
       a.max_tiles = (int32_t)max_tiles;
@@ -296,9 +294,10 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       r = launch_hist_tiles(a, st);
       timer_end(tm, st);
       if (r) return r;
-      const int64_t fin = (int64_t)n_list * F * B;
-      hipLaunchKernelGGL(hist_finalize_level_kernel, dim3(blocks_for(fin, 256)), dim3(256), 0, st,
-                         e->part_q, e->part_c, e->hkts, list, n_list, e->n_chunks, e->V, B, F, E,
+      const int64_t tile_words = (int64_t)e->n_chunks * 16 * e->V * B;
+      const unsigned fin_wg = (unsigned)(n_list * ((tile_words + 31) / 32));
+      hipLaunchKernelGGL(hist_finalize_level_kernel, dim3(fin_wg), dim3(256), 0, st,
+                         e->part, e->hkts, list, n_list, e->n_chunks, e->V, B, F, E,
                          nodes, d, e->hq[hprev], e->hc[hprev], e->hn, e->hq[hcur], e->hc[hcur]);
       WGBM_LAUNCH_CHECK();
       // ---- split search + DES selection

@@ -17,10 +17,10 @@ namespace wgbm {
 // ---------------------------------------------------------------------------
 // residuals
 // ---------------------------------------------------------------------------
-// regression: r = y - pred (warpgbm/core.py:719)
+// regression: r = y - pred (warpgbm/core.py:719); partial[block] = max |r|
 __global__ void residual_regression_kernel(const float* __restrict__ y,
                                            const float* __restrict__ pred, int64_t n,
-                                           float* __restrict__ r, uint32_t* __restrict__ absmax) {
+                                           float* __restrict__ r, uint32_t* __restrict__ partial) {
   uint32_t m = 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -29,35 +29,42 @@ __global__ void residual_regression_kernel(const float* __restrict__ y,
     const uint32_t b = wgbm_abs_bits(v);
     m = b > m ? b : m;
   }
-  m = wgbm_wave_max_u32(m);
-  if ((threadIdx.x & 63) == 0) atomicMax(absmax, m);
+  m = wgbm_block_max_u32(m);
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
 // softmax: p = softmax(F[i, :]); residual_k = -(p_k - onehot_k)
-// (warpgbm/core.py:186-214 and :782; metrics.py:12-15)
+// (warpgbm/core.py:186-214 and :782; metrics.py:12-15).
+// partial[k * gridDim.x + block] = max_i |residual_k|
 __global__ void residual_softmax_kernel(const float* __restrict__ logits,
                                         const int32_t* __restrict__ label, int64_t n, int32_t K,
                                         float* __restrict__ r /* [K][n] */,
-                                        uint32_t* __restrict__ absmax /* [K] */) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool ok = i < n;
-  const float* x = logits + (ok ? i : 0) * K;
-  const int lab = ok ? label[i] : -1;
-  float m = x[0];
-  for (int k = 1; k < K; ++k) m = x[k] > m ? x[k] : m;
-  float s = 0.0f;
-  for (int k = 0; k < K; ++k) s = s + wgbm_expf(x[k] - m);
-  for (int k = 0; k < K; ++k) {
-    const float p = wgbm_expf(x[k] - m) / s;
-    const float g = p - (k == lab ? 1.0f : 0.0f);
-    const float v = -g;
-    uint32_t b = 0;
-    if (ok) {
-      r[(int64_t)k * n + i] = v;
-      b = wgbm_abs_bits(v);
+                                        uint32_t* __restrict__ partial) {
+  for (int k0 = 0; k0 < K; k0 += 8) {
+    // up to 8 class maxima per pass over the rows
+    uint32_t m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+      const float* x = logits + i * K;
+      const int lab = label[i];
+      float mx = x[0];
+      for (int k = 1; k < K; ++k) mx = x[k] > mx ? x[k] : mx;
+      float s = 0.0f;
+      for (int k = 0; k < K; ++k) s = s + wgbm_expf(x[k] - mx);
+      for (int kk = 0; kk < 8 && k0 + kk < K; ++kk) {
+        const int k = k0 + kk;
+        const float p = wgbm_expf(x[k] - mx) / s;
+        const float g = p - (k == lab ? 1.0f : 0.0f);
+        const float v = -g;
+        r[(int64_t)k * n + i] = v;
+        const uint32_t b = wgbm_abs_bits(v);
+        m[kk] = b > m[kk] ? b : m[kk];
+      }
     }
-    b = wgbm_wave_max_u32(b);
-    if ((threadIdx.x & 63) == 0) atomicMax(absmax + k, b);
+    for (int kk = 0; kk < 8 && k0 + kk < K; ++kk) {
+      const uint32_t bm = wgbm_block_max_u32(m[kk]);
+      if (threadIdx.x == 0) partial[(int64_t)(k0 + kk) * gridDim.x + blockIdx.x] = bm;
+    }
   }
 }
 

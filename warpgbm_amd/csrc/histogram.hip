@@ -52,15 +52,16 @@ __device__ inline CodeVec<V> load_codes(const int8_t* __restrict__ codes,
   CodeVec<V> v;
   if (MODE == kLoadBuffer) {
     // bounds-checked raw buffer load: an offset past the buffer returns zeros
+    // codes are streamed once: non-temporal loads (cache policy bit "nt")
     const int o = valid ? (int)off : 0x7fffffff;
     if constexpr (V == 16) {
-      auto x = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0);
+      auto x = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, kAuxNT);
       v.w[0] = x[0]; v.w[1] = x[1]; v.w[2] = x[2]; v.w[3] = x[3];
     } else if constexpr (V == 8) {
-      auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, 0);
+      auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, kAuxNT);
       v.w[0] = x[0]; v.w[1] = x[1];
     } else {
-      v.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, 0);
+      v.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, kAuxNT);
     }
   } else if (MODE == kLoadGlobalAligned) {
     // row stride and chunk offsets are multiples of V bytes: aligned vector
@@ -91,17 +92,19 @@ __device__ inline CodeVec<V> load_codes(const int8_t* __restrict__ codes,
   return v;
 }
 
-// One workgroup: tile blockIdx.y x feature chunk blockIdx.x.
-// residual for the tile's tree t = key / keys_per_tree is resid + t*resid_tree_stride
-template <int V, int MODE>
-__global__ __launch_bounds__(512) void hist_tiles_kernel(
+// One workgroup (kHistThreads threads) = one tile x one chunk of 16*V features.
+// residual for the tile's tree t = key / keys_per_tree is resid + t*resid_tree_stride.
+// BT > 0 fixes num_bins at compile time (LDS offsets become immediates).
+template <int V, int MODE, int BT>
+__global__ __launch_bounds__(kHistThreads) void hist_tiles_kernel(
     const int8_t* __restrict__ codes, int64_t n_rows, int64_t stride, int32_t n_feats,
     const float* __restrict__ resid, int64_t resid_tree_stride,
     const int32_t* __restrict__ order, const Tile* __restrict__ tiles,
     const int32_t* __restrict__ n_tiles, int32_t keys_per_tree,
-    const int32_t* __restrict__ shifts, int32_t num_bins,
-    int64_t* __restrict__ part_q, int32_t* __restrict__ part_c) {
+    const int32_t* __restrict__ shifts, int32_t num_bins_rt,
+    unsigned long long* __restrict__ part) {
   extern __shared__ unsigned long long lds[];
+  const int num_bins = BT > 0 ? BT : num_bins_rt;
   const int n_chunks = (n_feats + 16 * V - 1) / (16 * V);
   const int tile_id = blockIdx.x / n_chunks;
   const int chunk = blockIdx.x - tile_id * n_chunks;
@@ -109,12 +112,12 @@ __global__ __launch_bounds__(512) void hist_tiles_kernel(
   const Tile tl = tiles[tile_id];
   const int Bp = num_bins + 1;
   const int nent = V * Bp * 16;
-  for (int i = threadIdx.x; i < nent; i += blockDim.x) lds[i] = 0ull;
+  for (int i = threadIdx.x; i < nent; i += kHistThreads) lds[i] = 0ull;
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int nwaves = blockDim.x >> 6;
+  constexpr int nwaves = kHistThreads / 64;
   const int slot = lane & 15;
   const int sub = lane >> 4;
   const int f_base = chunk * 16 * V + slot * V;
@@ -138,30 +141,42 @@ __global__ __launch_bounds__(512) void hist_tiles_kernel(
     force[k] = m;
   }
 
-  constexpr int U = 4;  // rows in flight per lane
+  // software pipeline: the loads of batch k+1 are in flight while batch k is
+  // added into LDS.  Each lane handles rows p, p + step, ..., p + (U-1)*step.
+  constexpr int U = 4;
   const int64_t step = (int64_t)nwaves * 4;
+  CodeVec<V> cv[U];
+  float rv[U];
+  auto issue = [&](int64_t p0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t pu = p0 + u * step;
+      const bool ok = pu < tl.end;
+      const int64_t row = ok ? (order ? (int64_t)order[pu] : pu) : 0;
+      rv[u] = ok ? r_t[row] : 0.0f;
+      cv[u] = load_codes<V, MODE>(codes, rs, row * stride + f_base, ok && f_valid, n_valid_bytes);
+    }
+  };
   int64_t p = tl.begin + wave * 4 + sub;
+  if (p < tl.end) issue(p);
   for (; p < tl.end; p += step * U) {
-    CodeVec<V> cv[U];
+    CodeVec<V> cw[U];
     unsigned long long pk[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t pu = p + u * step;
-      const bool ok = pu < tl.end;
-      const int64_t row = ok ? (order ? (int64_t)order[pu] : pu) : 0;
-      const float r = ok ? r_t[row] : 0.0f;
-      const int64_t q = (int64_t)wgbm_quantise(r, s);
-      // rows beyond the tile add 0 to the trash... they are masked by code below
-      pk[u] = ok ? (unsigned long long)(q * (int64_t)(1 << WGBM_CBITS) + 1) : 0ull;
-      cv[u] = load_codes<V, MODE>(codes, rs, row * stride + f_base, ok && f_valid, n_valid_bytes);
 #pragma unroll
-      for (int k = 0; k < V / 4; ++k) cv[u].w[k] |= force[k];
+      for (int k = 0; k < V / 4; ++k) cw[u].w[k] = cv[u].w[k] | force[k];
+      const int64_t q = (int64_t)wgbm_quantise(rv[u], s);
+      // rows past the tile end add 0 (their codes read as zeros)
+      pk[u] = (p + u * step < tl.end) ? (unsigned long long)(q * (int64_t)(1 << WGBM_CBITS) + 1)
+                                      : 0ull;
     }
+    if (p + step * U < tl.end) issue(p + step * U);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        uint32_t c = (cv[u].w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+        uint32_t c = (cw[u].w[j >> 2] >> (8 * (j & 3))) & 0xffu;
         // out-of-range code (incl. negative int8, read as >= 128) -> trash bin
         c = c < (uint32_t)num_bins ? c : (uint32_t)num_bins;
         atomicAdd(my + (j * Bp + (int)c) * 16, pk[u]);
@@ -170,64 +185,125 @@ __global__ __launch_bounds__(512) void hist_tiles_kernel(
   }
   __syncthreads();
 
-  // flush in LDS order: part[tile][chunk][j][b][slot] (trash row dropped)
+  // flush in LDS order: part[tile][chunk][j][b][slot] (trash row dropped); the
+  // packed word (sum * 2^18 + count) is stored as is and unpacked by finalize
   const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
   const int64_t chunk_off = (int64_t)tile_id * tile_words + (int64_t)chunk * 16 * V * num_bins;
   const int nout = V * num_bins * 16;
-  for (int i = threadIdx.x; i < nout; i += blockDim.x) {
+  for (int i = threadIdx.x; i < nout; i += kHistThreads) {
     const int sl = i & 15;
-    const int jb = i >> 4;          // j*B + b
+    const int jb = i >> 4;  // j*B + b
     const int j = jb / num_bins;
     const int b = jb - j * num_bins;
-    const unsigned long long P = lds[(j * Bp + b) * 16 + sl];
-    const int64_t C = (int64_t)(P & (unsigned long long)WGBM_CMASK);
-    const int64_t Q = ((int64_t)P - C) / (int64_t)(1 << WGBM_CBITS);
-    part_q[chunk_off + i] = Q;
-    part_c[chunk_off + i] = (int32_t)C;
+    part[chunk_off + i] = lds[(j * Bp + b) * 16 + sl];
   }
 }
 
-// index of feature f, bin b inside one tile's partial block
-__device__ inline int64_t part_index(int f, int b, int V, int num_bins) {
-  const int chunk = f / (16 * V);
-  const int fl = f - chunk * 16 * V;
-  const int sl = fl / V;
-  const int j = fl - sl * V;
-  return (int64_t)chunk * 16 * V * num_bins + ((int64_t)(j * num_bins + b) << 4) + sl;
+// unpack a packed tile word into (exact sum, count)
+__device__ inline void unpack_word(unsigned long long P, int64_t& Q, int64_t& C) {
+  C = (int64_t)(P & (unsigned long long)WGBM_CMASK);
+  Q = ((int64_t)P - C) / (int64_t)(1 << WGBM_CBITS);
+}
+
+// partial-layout index i (within one tile) -> (feature, bin)
+__device__ inline void part_feature_bin(int64_t i, int V, int num_bins, int& f, int& b) {
+  const int per_chunk = 16 * V * num_bins;
+  const int chunk = (int)(i / per_chunk);
+  const int r = (int)(i - (int64_t)chunk * per_chunk);
+  const int sl = r & 15;
+  const int jb = r >> 4;
+  const int j = jb / num_bins;
+  b = jb - j * num_bins;
+  f = chunk * 16 * V + sl * V + j;
 }
 
 // --------------------------------------------------------------------------
-// finalize for the reference-compatible entry point:
-// G_out[e, fo, b] += float(sum over tiles of key e of Q[feat[fo], b]) (and H)
+// finalize (f32): for every segment k and every (feature, bin) of the tile
+// layout, sum the tiles of k (integers) and write
+//   G[k, f, b] (+)= float(sum * 2^-s),  H[k, f, b] (+)= count.
+// Threads walk the partials in their memory order, so reads are coalesced.
+// accumulate = 0 overwrites (scratch output), 1 adds (reference semantics).
 // --------------------------------------------------------------------------
-__global__ void hist_finalize_f32_kernel(const int64_t* __restrict__ part_q,
-                                         const int32_t* __restrict__ part_c,
-                                         const int32_t* __restrict__ key_tile_start,
-                                         int32_t n_keys, int32_t n_chunks, int32_t V,
-                                         int32_t num_bins, const int32_t* __restrict__ feat_idx,
-                                         int32_t n_out_feats, const int32_t* __restrict__ shifts,
-                                         const uint32_t* __restrict__ absmax_bits,
-                                         const int32_t* __restrict__ n_tiles,
-                                         float* __restrict__ G, float* __restrict__ H) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)n_keys * n_out_feats * num_bins;
-  if (gid >= total) return;
-  const int b = (int)(gid % num_bins);
-  const int fo = (int)((gid / num_bins) % n_out_feats);
-  const int e = (int)(gid / ((int64_t)num_bins * n_out_feats));
-  const int f = feat_idx ? feat_idx[fo] : fo;
+// A workgroup of 256 threads covers 32 consecutive partial words of one
+// segment; its 8 thread groups each sum every 8th tile and the groups are
+// combined in LDS (integer sums, so the split does not change the result).
+constexpr int kFinWords = 32, kFinSplit = 8;
+
+__device__ inline void finalize_sum(const unsigned long long* __restrict__ part, int64_t tile_words,
+                                    int64_t i, bool ok, int t0, int t1, int64_t& Q, int64_t& C) {
+  __shared__ int64_t sq[kFinSplit][kFinWords];
+  __shared__ int64_t sc[kFinSplit][kFinWords];
+  const int w = threadIdx.x % kFinWords;
+  const int g = threadIdx.x / kFinWords;
+  int64_t q = 0, c = 0;
+  if (ok)
+    for (int t = t0 + g; t < t1; t += kFinSplit) {
+      int64_t a, b;
+      unpack_word(part[(int64_t)t * tile_words + i], a, b);
+      q += a;
+      c += b;
+    }
+  sq[g][w] = q;
+  sc[g][w] = c;
+  __syncthreads();
+  Q = 0;
+  C = 0;
+  for (int k = 0; k < kFinSplit; ++k) {
+    Q += sq[k][w];
+    C += sc[k][w];
+  }
+}
+
+__global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
+    const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
+    int32_t n_keys, int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
+    const int32_t* __restrict__ shifts, const uint32_t* __restrict__ absmax_bits,
+    const int32_t* __restrict__ n_tiles, int32_t accumulate, float* __restrict__ G,
+    float* __restrict__ H) {
   const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
-  const int64_t idx = part_index(f, b, V, num_bins);
-  int64_t Q = 0, C = 0;
-  const int t_end = key_tile_start[e + 1] < *n_tiles ? key_tile_start[e + 1] : *n_tiles;
-  for (int t = key_tile_start[e]; t < t_end; ++t) {
-    Q += part_q[(int64_t)t * tile_words + idx];
-    C += part_c[(int64_t)t * tile_words + idx];
+  const int64_t wpk = (tile_words + kFinWords - 1) / kFinWords;  // workgroups per segment
+  const int k = (int)(blockIdx.x / wpk);
+  const int64_t i = (blockIdx.x - (int64_t)k * wpk) * kFinWords + threadIdx.x % kFinWords;
+  const bool ok = k < n_keys && i < tile_words;
+  int t0 = 0, t1 = 0;
+  if (k < n_keys) {
+    t0 = key_tile_start[k];
+    t1 = key_tile_start[k + 1] < *n_tiles ? key_tile_start[k + 1] : *n_tiles;
   }
+  int64_t Q, C;
+  finalize_sum(part, tile_words, i, ok, t0, t1, Q, C);
+  if (!ok || threadIdx.x >= kFinWords) return;
+  int f, b;
+  part_feature_bin(i, V, num_bins, f, b);
+  if (f >= n_feats) return;
   const bool bad = (*absmax_bits) >= 0x7f800000u;  // non-finite residual seen
   const float g = bad ? __builtin_nanf("") : wgbm_dequantise(Q, shifts[0]);
-  G[gid] = G[gid] + g;
-  H[gid] = H[gid] + (float)C;
+  const int64_t o = ((int64_t)k * n_feats + f) * num_bins + b;
+  if (accumulate) {
+    G[o] = G[o] + g;
+    H[o] = H[o] + (float)C;
+  } else {
+    G[o] = g;
+    H[o] = (float)C;
+  }
+}
+
+// out[e, fo, b] += full[e, feat[fo], b]  (feature selection of compute_histogram3)
+__global__ void hist_gather_features_kernel(const float* __restrict__ Gf,
+                                            const float* __restrict__ Hf, int32_t n_keys,
+                                            int32_t n_feats_full, int32_t num_bins,
+                                            const int32_t* __restrict__ feat_idx,
+                                            int32_t n_out, float* __restrict__ G,
+                                            float* __restrict__ H) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)n_keys * n_out * num_bins) return;
+  const int b = (int)(gid % num_bins);
+  const int fo = (int)((gid / num_bins) % n_out);
+  const int k = (int)(gid / ((int64_t)num_bins * n_out));
+  const int f = feat_idx[fo];
+  const int64_t src = ((int64_t)k * n_feats_full + f) * num_bins + b;
+  G[gid] = G[gid] + Gf[src];
+  H[gid] = H[gid] + Hf[src];
 }
 
 // --------------------------------------------------------------------------
@@ -236,33 +312,32 @@ __global__ void hist_finalize_f32_kernel(const int64_t* __restrict__ part_q,
 //   computed key k = (tree, node, era) with node = 2*parent + side
 //   hq/hc layout: [tree][node][era][F][B]
 // --------------------------------------------------------------------------
-__global__ void hist_finalize_level_kernel(
-    const int64_t* __restrict__ part_q, const int32_t* __restrict__ part_c,
-    const int32_t* __restrict__ key_tile_start, const int32_t* __restrict__ key_list,
-    int32_t n_list, int32_t n_chunks, int32_t V, int32_t num_bins,
-    int32_t n_feats, int32_t num_eras, int32_t nodes_in_level, int32_t depth,
+__global__ __launch_bounds__(256) void hist_finalize_level_kernel(
+    const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
+    const int32_t* __restrict__ key_list, int32_t n_list, int32_t n_chunks, int32_t V,
+    int32_t num_bins, int32_t n_feats, int32_t num_eras, int32_t nodes_in_level, int32_t depth,
     const int64_t* __restrict__ parent_q, const int32_t* __restrict__ parent_c,
     const int32_t* __restrict__ n_tiles, int64_t* __restrict__ hq, int32_t* __restrict__ hc) {
-  const int64_t per_key = (int64_t)n_feats * num_bins;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int kk = (int)(gid / per_key);
-  if (kk >= n_list) return;
-  const int key = key_list ? key_list[kk] : kk;
-  if (key < 0) return;
-  const int fb = (int)(gid - (int64_t)kk * per_key);
-  const int f = fb / num_bins;
-  const int b = fb - f * num_bins;
   const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
-  const int64_t idx = part_index(f, b, V, num_bins);
-  int64_t Q = 0, C = 0;
-  const int t_end = key_tile_start[kk + 1] < *n_tiles ? key_tile_start[kk + 1] : *n_tiles;
-  for (int t = key_tile_start[kk]; t < t_end; ++t) {
-    Q += part_q[(int64_t)t * tile_words + idx];
-    C += part_c[(int64_t)t * tile_words + idx];
-  }
-  const int64_t out = (int64_t)key * per_key + fb;
-  hq[out] = Q;
-  hc[out] = (int32_t)C;
+  const int64_t wpk = (tile_words + kFinWords - 1) / kFinWords;
+  const int kk = (int)(blockIdx.x / wpk);
+  if (kk >= n_list) return;  // uniform per workgroup
+  const int key = key_list ? key_list[kk] : kk;
+  if (key < 0) return;  // uniform per workgroup
+  const int64_t i = (blockIdx.x - (int64_t)kk * wpk) * kFinWords + threadIdx.x % kFinWords;
+  const bool ok = i < tile_words;
+  const int t0 = key_tile_start[kk];
+  const int t1 = key_tile_start[kk + 1] < *n_tiles ? key_tile_start[kk + 1] : *n_tiles;
+  int64_t Q, C;
+  finalize_sum(part, tile_words, i, ok, t0, t1, Q, C);
+  if (!ok || threadIdx.x >= kFinWords) return;
+  int f, b;
+  part_feature_bin(i, V, num_bins, f, b);
+  if (f >= n_feats) return;
+  const int64_t per_key = (int64_t)n_feats * num_bins;
+  const int64_t fb = (int64_t)f * num_bins + b;
+  hq[(int64_t)key * per_key + fb] = Q;
+  hc[(int64_t)key * per_key + fb] = (int32_t)C;
   if (depth > 0) {
     // key = ((tree*nodes + node)*E + era)
     const int era = key % num_eras;
@@ -281,8 +356,9 @@ __global__ void hist_finalize_level_kernel(
 // --------------------------------------------------------------------------
 // max |residual| over the rows of a call (ABI path)
 // --------------------------------------------------------------------------
-__global__ void absmax_kernel(const float* __restrict__ resid, const int32_t* __restrict__ rows,
-                              int64_t n, uint32_t* __restrict__ out_bits) {
+__global__ void absmax_partial_kernel(const float* __restrict__ resid,
+                                      const int32_t* __restrict__ rows, int64_t n,
+                                      uint32_t* __restrict__ partial) {
   uint32_t m = 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -290,16 +366,27 @@ __global__ void absmax_kernel(const float* __restrict__ resid, const int32_t* __
     const uint32_t b = wgbm_abs_bits(resid[r]);
     m = b > m ? b : m;
   }
-  m = wgbm_wave_max_u32(m);
-  if ((threadIdx.x & 63) == 0) atomicMax(out_bits, m);
+  m = wgbm_block_max_u32(m);
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
-__global__ void shift_from_absmax_kernel(const uint32_t* __restrict__ bits, int32_t n, int32_t qbits,
-                                         int32_t* __restrict__ shifts) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const uint32_t b = bits[i];
-  shifts[i] = b >= 0x7f800000u ? 0 : wgbm_shift_from_absmax(__uint_as_float(b), qbits);
+// one workgroup per independent maximum t: reduce partial[t*n_part ...] and
+// turn it into the quantisation shift (0 for an all-zero or non-finite input;
+// absmax_bits keeps the raw maximum so a NaN/inf input can be reported)
+__global__ void absmax_finish_kernel(const uint32_t* __restrict__ partial, int32_t n_part,
+                                     int32_t qbits, uint32_t* __restrict__ absmax_bits,
+                                     int32_t* __restrict__ shifts) {
+  const int t = blockIdx.x;
+  uint32_t m = 0;
+  for (int i = threadIdx.x; i < n_part; i += blockDim.x) {
+    const uint32_t b = partial[(int64_t)t * n_part + i];
+    m = b > m ? b : m;
+  }
+  m = wgbm_block_max_u32(m);
+  if (threadIdx.x == 0) {
+    absmax_bits[t] = m;
+    shifts[t] = m >= 0x7f800000u ? 0 : wgbm_shift_from_absmax(__uint_as_float(m), qbits);
+  }
 }
 
 // --------------------------------------------------------------------------
@@ -318,23 +405,22 @@ __global__ __launch_bounds__(1024) void plan_tiles_kernel(
   const int nk = n_keys;  // entries of key_list (or keys 0..n_keys-1)
   if (threadIdx.x == 0) carry = 0;
   __syncthreads();
+  // phase 1: exclusive scan of the tile counts -> key_tile_start
   for (int base = 0; base < nk; base += blockDim.x) {
     const int i = base + threadIdx.x;
-    int key = 0, nt = 0;
-    int64_t b0 = 0, b1 = 0;
+    int nt = 0;
     if (i < nk) {
-      key = key_list ? key_list[i] : i;
+      const int key = key_list ? key_list[i] : i;
       if (key >= 0) {
-        b0 = seg ? seg[key] : 0;
-        b1 = seg ? seg[key + 1] : total;
+        const int64_t b0 = seg ? seg[key] : 0;
+        const int64_t b1 = seg ? seg[key + 1] : total;
         nt = (int)((b1 - b0 + tile_rows - 1) / tile_rows);
       }
     }
-    // block exclusive scan of nt
     int x = nt;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     for (int o = 1; o < 64; o <<= 1) {
-      int y = __shfl_up(x, o, 64);
+      const int y = __shfl_up(x, o, 64);
       if (lane >= o) x += y;
     }
     if (lane == 63) wsum[w] = x;
@@ -342,26 +428,33 @@ __global__ __launch_bounds__(1024) void plan_tiles_kernel(
     int wpre = 0;
     for (int k = 0; k < w; ++k) wpre += wsum[k];
     const int excl = carry + wpre + x - nt;
-    if (i < nk) {
-      key_tile_start[i] = excl;
-      for (int t = 0; t < nt; ++t) {
-        const int id = excl + t;
-        if (id < max_tiles) {
-          Tile tl;
-          tl.key = key;
-          tl.begin = b0 + (int64_t)t * tile_rows;
-          tl.end = tl.begin + tile_rows < b1 ? tl.begin + tile_rows : b1;
-          tiles[id] = tl;
-        }
-      }
-    }
+    if (i < nk) key_tile_start[i] = excl;
     __syncthreads();
     if (threadIdx.x == blockDim.x - 1) carry = excl + nt;
     __syncthreads();
   }
+  const int ntot = carry < max_tiles ? carry : max_tiles;
   if (threadIdx.x == 0) {
     key_tile_start[nk] = carry;
-    *n_tiles = carry < max_tiles ? carry : max_tiles;
+    *n_tiles = ntot;
+  }
+  __syncthreads();
+  // phase 2: every tile finds its entry (last i with key_tile_start[i] <= id)
+  for (int id = threadIdx.x; id < ntot; id += blockDim.x) {
+    int lo = 0, hi = nk - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (key_tile_start[mid] <= id) lo = mid; else hi = mid - 1;
+    }
+    const int key = key_list ? key_list[lo] : lo;
+    const int64_t b0 = seg ? seg[key] : 0;
+    const int64_t b1 = seg ? seg[key + 1] : total;
+    Tile tl;
+    tl.key = key;
+    tl.pad = 0;
+    tl.begin = b0 + (int64_t)(id - key_tile_start[lo]) * tile_rows;
+    tl.end = tl.begin + tile_rows < b1 ? tl.begin + tile_rows : b1;
+    tiles[id] = tl;
   }
 }
 
@@ -415,19 +508,19 @@ int hist_pick_v(int num_bins) {
 
 size_t hist_lds_bytes(int V, int num_bins) { return (size_t)V * (num_bins + 1) * 16 * 8; }
 
-template <int V, int MODE>
+template <int V, int MODE, int BT>
 static int launch_tiles_t(const HistLaunch& a, hipStream_t st) {
   static bool attr_set = false;
   const size_t lds = hist_lds_bytes(V, a.num_bins);
   if (!attr_set) {
-    WGBM_CHECK(hipFuncSetAttribute((const void*)hist_tiles_kernel<V, MODE>,
+    WGBM_CHECK(hipFuncSetAttribute((const void*)hist_tiles_kernel<V, MODE, BT>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     attr_set = true;
   }
   dim3 grid((unsigned)((int64_t)a.n_chunks * a.max_tiles));
-  hipLaunchKernelGGL((hist_tiles_kernel<V, MODE>), grid, dim3(512), lds, st, a.codes, a.n_rows,
-                     a.stride, a.n_feats, a.resid, a.resid_tree_stride, a.order, a.tiles,
-                     a.n_tiles, a.keys_per_tree, a.shifts, a.num_bins, a.part_q, a.part_c);
+  hipLaunchKernelGGL((hist_tiles_kernel<V, MODE, BT>), grid, dim3(kHistThreads), lds, st, a.codes,
+                     a.n_rows, a.stride, a.n_feats, a.resid, a.resid_tree_stride, a.order, a.tiles,
+                     a.n_tiles, a.keys_per_tree, a.shifts, a.num_bins, a.part);
   WGBM_LAUNCH_CHECK();
   return 0;
 }
@@ -440,12 +533,16 @@ int hist_load_mode(int64_t n_rows, int64_t stride, int V) {
 
 int launch_hist_tiles(const HistLaunch& a, hipStream_t st) {
   const int mode = hist_load_mode(a.n_rows, a.stride, a.V);
-#define WGBM_DISPATCH(VV)                                                   \
-  if (a.V == VV) {                                                          \
-    if (mode == kLoadBuffer) return launch_tiles_t<VV, kLoadBuffer>(a, st); \
-    if (mode == kLoadGlobalAligned)                                         \
-      return launch_tiles_t<VV, kLoadGlobalAligned>(a, st);                 \
-    return launch_tiles_t<VV, kLoadBytes>(a, st);                           \
+  if (a.V == 16 && a.num_bins == 32) {
+    if (mode == kLoadBuffer) return launch_tiles_t<16, kLoadBuffer, 32>(a, st);
+    if (mode == kLoadGlobalAligned) return launch_tiles_t<16, kLoadGlobalAligned, 32>(a, st);
+  }
+#define WGBM_DISPATCH(VV)                                                      \
+  if (a.V == VV) {                                                             \
+    if (mode == kLoadBuffer) return launch_tiles_t<VV, kLoadBuffer, 0>(a, st); \
+    if (mode == kLoadGlobalAligned)                                            \
+      return launch_tiles_t<VV, kLoadGlobalAligned, 0>(a, st);                 \
+    return launch_tiles_t<VV, kLoadBytes, 0>(a, st);                           \
   }
   WGBM_DISPATCH(16)
   WGBM_DISPATCH(8)

@@ -15,6 +15,13 @@ struct Tile {
 
 enum { kLoadBuffer = 0, kLoadGlobalAligned = 1, kLoadBytes = 2 };
 
+// threads per histogram workgroup (16 waves; two workgroups fit one CU's LDS)
+constexpr int kHistThreads = 1024;
+// cache-policy bits of a buffer load: non-temporal (streamed once)
+constexpr int kAuxNT = 2;
+// histogram workgroups per launch the tile sizes aim for (2 per CU)
+constexpr int kHistTargetWG = 512;
+
 struct HistLaunch {
   const int8_t* codes;
   int64_t n_rows;
@@ -28,8 +35,7 @@ struct HistLaunch {
   int32_t keys_per_tree;
   const int32_t* shifts;
   int32_t num_bins;
-  int64_t* part_q;
-  int32_t* part_c;
+  unsigned long long* part;  // packed tile partials (sum * 2^18 + count)
   int32_t V;
   int32_t n_chunks;
   int32_t max_tiles;
@@ -41,22 +47,25 @@ int hist_load_mode(int64_t n_rows, int64_t stride, int V);
 int launch_hist_tiles(const HistLaunch& a, hipStream_t st);
 
 // kernels launched directly from other translation units
-__global__ void hist_finalize_f32_kernel(const int64_t* part_q, const int32_t* part_c,
+__global__ void hist_finalize_f32_kernel(const unsigned long long* part,
                                          const int32_t* key_tile_start, int32_t n_keys,
                                          int32_t n_chunks, int32_t V, int32_t num_bins,
-                                         const int32_t* feat_idx, int32_t n_out_feats,
-                                         const int32_t* shifts, const uint32_t* absmax_bits,
-                                         const int32_t* n_tiles, float* G, float* H);
+                                         int32_t n_feats, const int32_t* shifts,
+                                         const uint32_t* absmax_bits, const int32_t* n_tiles,
+                                         int32_t accumulate, float* G, float* H);
+__global__ void hist_gather_features_kernel(const float* Gf, const float* Hf, int32_t n_keys,
+                                            int32_t n_feats_full, int32_t num_bins,
+                                            const int32_t* feat_idx, int32_t n_out, float* G,
+                                            float* H);
 __global__ void hist_finalize_level_kernel(
-    const int64_t* part_q, const int32_t* part_c, const int32_t* key_tile_start,
-    const int32_t* key_list, int32_t n_list, int32_t n_chunks, int32_t V,
-    int32_t num_bins, int32_t n_feats, int32_t num_eras, int32_t nodes_in_level, int32_t depth,
-    const int64_t* parent_q, const int32_t* parent_c, const int32_t* n_tiles, int64_t* hq,
-    int32_t* hc);
-__global__ void absmax_kernel(const float* resid, const int32_t* rows, int64_t n,
-                              uint32_t* out_bits);
-__global__ void shift_from_absmax_kernel(const uint32_t* bits, int32_t n, int32_t qbits,
-                                         int32_t* shifts);
+    const unsigned long long* part, const int32_t* key_tile_start, const int32_t* key_list,
+    int32_t n_list, int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
+    int32_t num_eras, int32_t nodes_in_level, int32_t depth, const int64_t* parent_q,
+    const int32_t* parent_c, const int32_t* n_tiles, int64_t* hq, int32_t* hc);
+__global__ void absmax_partial_kernel(const float* resid, const int32_t* rows, int64_t n,
+                                      uint32_t* partial);
+__global__ void absmax_finish_kernel(const uint32_t* partial, int32_t n_part, int32_t qbits,
+                                     uint32_t* absmax_bits, int32_t* shifts);
 __global__ void plan_tiles_kernel(const int64_t* seg, int64_t total, int32_t n_keys,
                                   const int32_t* key_list, int32_t tile_rows, int32_t max_tiles, Tile* tiles,
                                   int32_t* key_tile_start, int32_t* n_tiles);
