@@ -1,6 +1,6 @@
 """Benchmark of the WarpGBM hot path on one MI355X.
 
-Metric (BASELINE.json): histogram GB/s (% HBM peak) + train/infer seconds,
+Metric: histogram GB/s (% HBM peak) + train/infer seconds,
 1M x 1K, 100 trees, depth 5.
 
 * value: whole-op throughput of the histogram build on config C2
@@ -53,6 +53,38 @@ def c3_inputs(rows, feats, seed):
     return X, y.astype(np.float32)
 
 
+def c4_inputs(rows=500_000, feats=2000, eras=500, seed=0):
+    """Config C4: int8 codes in {0..4}, 500 contiguous equal eras; target = per-era
+    5-quantile bucket of a score built from 50 features, 25 of which flip sign in
+    half of the eras."""
+    rng = np.random.default_rng(seed)
+    X = rng.integers(0, 5, (rows, feats), dtype=np.int8)
+    era = np.repeat(np.arange(eras), rows // eras)
+    c = rng.standard_normal(50)
+    s = np.ones((eras, 50))
+    flip = rng.random((eras, 25)) < 0.5
+    s[:, 25:] = np.where(flip, -1.0, 1.0)
+    score = ((X[:, :50].astype(np.float32) - 2) * (c * s[era])).sum(axis=1) + rng.standard_normal(rows)
+    y = np.empty(rows, np.float32)
+    for e in range(eras):
+        sl = slice(e * (rows // eras), (e + 1) * (rows // eras))
+        q = np.quantile(score[sl], [0.2, 0.4, 0.6, 0.8])
+        y[sl] = np.digitize(score[sl], q) / 4.0
+    return X, y, era
+
+
+def c5_inputs(rows_per_class=20_000, feats=100, K=10, seed=0):
+    """Config C5: 10 Gaussian clusters in 30 informative dims (means ~N(0, 1.5^2),
+    unit variance) plus 70 noise dims."""
+    means = np.random.default_rng(100).normal(0, 1.5, (K, 30))  # one distribution
+    rng = np.random.default_rng(seed)
+    lab = np.repeat(np.arange(K), rows_per_class)
+    X = np.empty((len(lab), feats), np.float32)
+    X[:, :30] = means[lab] + rng.standard_normal((len(lab), 30))
+    X[:, 30:] = rng.standard_normal((len(lab), feats - 30))
+    return X, lab
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -74,6 +106,9 @@ def main():
     ap.add_argument("--e2e-rows", type=int, default=1_000_000)
     ap.add_argument("--e2e-trees", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--extra", default="", help="comma list of extra end-to-end configs: c4,c5")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 1 GiB device copy (calibrates HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -86,6 +121,15 @@ def main():
 
     lib = _lib.load()
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        # a plain copy of known size: 2^30 bytes read, 2^30 bytes written
+        src = torch.ones(1 << 30, dtype=torch.int8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
     N, F, B = args.rows, args.feats, 32
     print(f"[bench] generating C2 inputs {N}x{F}", file=sys.stderr, flush=True)
     codes_h, grad_h, node_h = c2_inputs(N, F)
@@ -197,6 +241,13 @@ def main():
         print(f"[bench] C3 train {train_s:.2f} s, infer {infer_s:.2f} s, corr {corr:.4f}",
               file=sys.stderr, flush=True)
 
+    # HBM bytes per hist_tiles launch from the committed rocprofv3 PMC summary
+    # (FETCH_SIZE / WRITE_SIZE runs of this same workload, scaled by a copy of
+    # known size); null when that summary is absent
+    traffic = None
+    tpath = ROOT / "profiles" / "hist_c2_traffic.json"
+    if tpath.exists() and N == 1_000_000 and F == 1000:
+        traffic = round(json.loads(tpath.read_text())["traffic_bytes_per_dispatch"])
     out = {
         "metric": "histogram GB/s (% HBM peak) + train/infer sec, 1M×1K 100 trees depth 5",
         "value": round(gbs, 2),
@@ -209,18 +260,61 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 codes / int64 exact sums",
-        "data": "synthetic (numpy default_rng(0), BASELINE configs C2/C3)",
+        "data": "synthetic (numpy default_rng(0); C2 histogram and C3 end-to-end workloads)",
         "config": {"workload": f"C2 histogram: root + 16 nodes, {N}x{F} int8, 32 bins, 1 era",
                    "rows": N, "features": F, "bins": B, "nodes": [1, 16], "row_stride": S},
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(k_achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(k_achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "hist_tiles_kernel<16,0>",
+                     "traffic": traffic, "kernel": "hist_tiles_kernel<16,0,32>",
                      "kernel_ms": round(k_ms, 4)},
         "cpu_baseline": cpu,
     }
     out.update(e2e)
+    for cfg in [c for c in args.extra.split(",") if c]:
+        out.update(run_extra(cfg))
     print(json.dumps(out))
+
+
+def run_extra(cfg):
+    """End-to-end seconds of configs C4 (era-aware DES) and C5 (softmax)."""
+    import torch
+
+    from warpgbm_amd import WarpGBM
+
+    if cfg == "c4":
+        print("[bench] generating C4 inputs", file=sys.stderr, flush=True)
+        X, y, era = c4_inputs()
+        m = WarpGBM(num_bins=5, max_depth=8, n_estimators=100, learning_rate=0.1)
+        t0 = time.perf_counter()
+        m.fit(X, y, era_id=era)
+        torch.cuda.synchronize()
+        tr = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        p = m.predict(X)
+        inf = time.perf_counter() - t0
+        corr = float(np.corrcoef(p, y)[0, 1])
+        print(f"[bench] C4 train {tr:.2f} s, infer {inf:.2f} s, in-sample corr {corr:.4f}",
+              file=sys.stderr, flush=True)
+        return {"c4_train_s": round(tr, 3), "c4_infer_s": round(inf, 3), "c4_corr": round(corr, 4)}
+    if cfg == "c5":
+        print("[bench] generating C5 inputs", file=sys.stderr, flush=True)
+        X, lab = c5_inputs()
+        Xt, labt = c5_inputs(rows_per_class=100_000, seed=1)
+        m = WarpGBM(objective="multiclass", num_bins=32, max_depth=6, n_estimators=200,
+                    learning_rate=0.1)
+        t0 = time.perf_counter()
+        m.fit(X, lab)
+        torch.cuda.synchronize()
+        tr = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        proba = m.predict_proba(Xt)
+        inf = time.perf_counter() - t0
+        acc = float((np.argmax(proba, axis=1) == labt).mean())
+        print(f"[bench] C5 train {tr:.2f} s, predict_proba {inf:.2f} s, acc {acc:.4f}",
+              file=sys.stderr, flush=True)
+        return {"c5_train_s": round(tr, 3), "c5_infer_s": round(inf, 3), "c5_acc": round(acc, 4)}
+    raise SystemExit(f"unknown extra config {cfg}")
 
 
 if __name__ == "__main__":

@@ -27,7 +27,7 @@ def gpu():
 
 
 def c1_data(n=10000, f=50, seed=0):
-    """X ~ N(0,1) float32, y = X.w (10 nonzero) + 0.1 N(0,1)."""
+    """Config C1: X ~ N(0,1) float32, y = X.w (10 nonzero) + 0.1 N(0,1), 10k x 50."""
     rng = np.random.default_rng(seed)
     X = rng.standard_normal((n, f), dtype=np.float32)
     w = np.zeros(f, np.float32)

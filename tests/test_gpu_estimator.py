@@ -3,7 +3,7 @@ with the oracle's restatement of the reference's recursive tree growth.
 
 Bar: identical tree dicts (features, bins, leaf values as floats, sample
 counts), identical predictions and importances (bit-exact), for regression
-softmax multiclass, era-aware DES, colsample subsets,
+(config C1: 10k x 50, 32 bins, depth 5, 20 trees), softmax multiclass, era-aware DES, colsample subsets,
 warm start and save/load."""
 import numpy as np
 import pytest

@@ -10,7 +10,7 @@ off-by-one bin or transposed index fails.
   ops.bin_column            brute-force linear scan; torch.bucketize(right=True)
   ops.quantile_edges_sorted torch.quantile (CPU) bit-exact
   ops.quantile_levels       k / B within 1 ulp; torch.linspace
-  ops.quantise/dequantise   lossless for |r| >= max|r|/16; error <= 2^-(s+1)
+  ops.quantise/dequantise   lossless for |r| >= max|r|*2^(24-qbits); error <= 2^-(s+1)
   ops.histogram_exact_q     brute-force integer dict; count invariants;
                             child + sibling == parent
   ops.histogram_exact       |G - fsum(r)| <= n 2^-(s+1) + ulp; vs f32 sequential
