@@ -102,6 +102,14 @@ int wgbm_histogram_segments(const int8_t* codes, int64_t n_rows, int64_t stride,
 int wgbm_quantile_edges(const float* sorted, int64_t n, int32_t n_feats, const float* q,
                         int32_t nq, float* edges, void* stream);
 
+/* Quantile edges of every column of X float32 [n, n_feats] (row stride
+ * x_stride elements) without sorting: the order statistics torch.quantile
+ * interpolates between are found by radix selection (4 passes over an
+ * order-preserving key of each column), then interpolated as above.
+ * Bit-identical to torch.quantile(X[:, f], q); n <= 2^24. */
+int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride,
+                               const float* q, int32_t nq, float* edges, void* stream);
+
 /* Batched binner (the per-feature loop of warpgbm/core.py:527-538 and
  * 908-913 in one launch).  X float32 [n, n_feats] with row stride x_stride
  * (elements); edges float32 [n_feats, n_edges] sorted per feature.  Writes

@@ -239,3 +239,45 @@ def test_copy_prebinned(gpu):
     assert np.array_equal(rm[:, :300], X.astype(np.int8))
     assert np.all(rm[:, 300:] == -1)
     assert np.array_equal(c.cm.cpu().numpy(), X.astype(np.int8).T)
+
+
+@pytest.mark.parametrize("B", [2, 5, 32, 127])
+def test_native_quantile_selection_bit_exact(gpu, B):
+    """Radix-selection edges equal torch.quantile / the oracle for tiny columns,
+    heavy ties, constant columns, NaN columns and many targets."""
+    print_case("quantile_edges_matrix", B)
+    rng = np.random.default_rng(B)
+    cols = []
+    for n in (1, 2, 3, 7, 64, 1000, 20011):
+        X = np.empty((n, 6), F32)
+        X[:, 0] = rng.standard_normal(n)
+        X[:, 1] = rng.integers(-2, 3, n)                       # heavy ties
+        X[:, 2] = 3.5                                          # constant
+        X[:, 3] = (rng.standard_normal(n) * 1e-35)             # subnormal range
+        X[:, 4] = np.abs(rng.standard_normal(n)) * 1e30        # large
+        X[:, 5] = rng.standard_normal(n)
+        if n > 5:
+            X[n // 2, 5] = np.nan                              # NaN column -> all NaN
+        Xd = D.upload_float(X, dev)
+        got = D.quantile_edges(Xd, B).cpu().numpy()
+        ref = ops.quantile_edges(X, B)
+        assert np.array_equal(bits(got), bits(ref)), n
+        tq = torch.quantile(torch.from_numpy(X[:, :5]), torch.from_numpy(ops.quantile_levels(B)),
+                            dim=0).numpy().T
+        assert np.array_equal(bits(got[:5]), bits(tq)), n
+        # sorted-input entry point agrees too
+        srt = torch.sort(Xd.t().contiguous(), dim=1).values
+        got2 = D.quantile_edges_sorted(srt, B).cpu().numpy()
+        assert np.array_equal(bits(got2[:5]), bits(ref[:5])), n
+
+
+def test_staged_upload_exact(gpu):
+    """The pinned, multi-threaded upload reproduces X (float64 input rounded
+    to float32) exactly, including a ragged last chunk."""
+    print_case("upload_float")
+    rng = np.random.default_rng(9)
+    X = rng.standard_normal((300_001, 230))           # float64: converted while staging
+    Xd = D.upload_float(X, dev)
+    assert torch.equal(Xd.cpu(), torch.from_numpy(X.astype(np.float32)))
+    X32 = rng.standard_normal((250_000, 300), dtype=np.float32)
+    assert torch.equal(D.upload_float(X32, dev).cpu(), torch.from_numpy(X32))

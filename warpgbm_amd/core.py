@@ -25,9 +25,33 @@ import torch
 from sklearn.base import BaseEstimator, RegressorMixin
 from sklearn.preprocessing import LabelEncoder
 
+import os
+import time
+
 from . import device as D
 from . import node_kernel
 from .metrics import accuracy_torch, log_loss_torch, rmsle_torch, softmax
+
+_TIMING = os.environ.get("WGBM_TIMING", "") not in ("", "0")
+
+
+class _Phases:
+    """Wall-clock phase timer for fit (printed when WGBM_TIMING=1)."""
+
+    def __init__(self):
+        self.t = time.perf_counter()
+        self.items = []
+
+    def mark(self, name):
+        if _TIMING:
+            torch.cuda.synchronize()
+            now = time.perf_counter()
+            self.items.append((name, now - self.t))
+            self.t = now
+
+    def report(self):
+        if _TIMING:
+            print("fit phases: " + ", ".join(f"{n} {dt * 1e3:.1f} ms" for n, dt in self.items))
 
 
 class WarpGBM(BaseEstimator, RegressorMixin):
@@ -209,6 +233,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         if era_id is None:
             era_id = np.ones(X.shape[0], dtype="int32")
         self.feature_subsets_ = []
+        self._phases = _Phases()
 
         if self.objective in ("multiclass", "binary"):
             if not self.warm_start or not self._is_fitted:
@@ -231,9 +256,12 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         """Codes, era layout and targets on the device (warpgbm/core.py:487-541)."""
         self.num_samples, self.num_features = X_np.shape
         dev = torch.device(self.device)
+        ph = self._phases
         is_integer_type = np.issubdtype(X_np.dtype, np.integer)
-        max_vals = X_np.max(axis=0) if X_np.shape[0] else np.zeros(X_np.shape[1])
-        if is_integer_type and np.all(max_vals < self.num_bins):
+        # column maxima only matter for integer input (the pre-binned test)
+        prebinned = is_integer_type and (
+            X_np.shape[0] == 0 or bool(np.all(X_np.max(axis=0) < self.num_bins)))
+        if prebinned:
             print("Detected pre-binned integer input — skipping quantile binning.")
             codes = D.upload_prebinned(X_np, dev, with_cm=True)
             bin_edges = torch.arange(1, self.num_bins, dtype=torch.float32).repeat(
@@ -241,9 +269,13 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         else:
             print("quantile binning.")
             Xd = D.upload_float(X_np, dev)
+            ph.mark("upload")
             bin_edges = D.quantile_edges(Xd, self.num_bins)
+            ph.mark("edges")
             codes = D.bin_matrix(Xd, bin_edges, with_cm=True)
+            ph.mark("bin")
             del Xd
+        ph.mark("codes")
         uniq, inv, order, start = D.era_layout(era_id_np)
         self.unique_eras = uniq
         self.num_eras = len(uniq)
@@ -251,6 +283,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         root_order = torch.from_numpy(order).to(dev)
         era_start = torch.from_numpy(start).to(dev)
         Y_gpu = torch.from_numpy(np.asarray(Y_np)).type(torch.float32).to(dev)
+        ph.mark("eras+targets")
         return codes, root_order, era_start, bin_edges, Y_gpu
 
     def _new_engine(self, codes, root_order, era_start, n_trees, objective):
@@ -333,8 +366,11 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                     self._compute_eval_regression(i, Y_gpu, preds, eval_pred[:, 0])
                     if self.stop:
                         break
+        self._phases.mark("rounds")
         eng.close()
         self._absorb_records(rec, done, start_iter, classification=False)
+        self._phases.mark("records")
+        self._phases.report()
         self.feature_importance_ = self.per_era_feature_importance_.sum(axis=0)
         self._is_fitted = True
         self._heap = None
@@ -386,8 +422,11 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                     self._compute_eval_multiclass(i, labels, scores, eval_scores)
                     if self.stop:
                         break
+        self._phases.mark("rounds")
         eng.close()
         self._absorb_records(rec, done, start_iter, classification=True)
+        self._phases.mark("records")
+        self._phases.report()
         self.feature_importance_ = self.per_era_feature_importance_.sum(axis=0)
         self._is_fitted = True
         self._heap = None

@@ -158,4 +158,171 @@ __global__ void quantile_edges_kernel(const float* __restrict__ sorted, int64_t 
   edges[gid] = w < 0.5f ? fmaf(w, d, a) : fmaf(w - 1.0f, d, b);
 }
 
+
+// ---------------------------------------------------------------------------
+// Native quantile edges: the order statistics torch.quantile interpolates
+// between, found by radix selection instead of a sort.
+//
+// keys: order-preserving uint32 encoding of the float32 values, column-major
+// [F][n] (NaN -> 0xffffffff, i.e. after +inf, as in torch.sort).  For each
+// feature one workgroup selects the ranks lo_j = floor(q_j (n-1)) and
+// hi_j = ceil(q_j (n-1)) with four passes over the column, one byte of the
+// key per pass: pass 1 histograms the top byte of every key; pass k
+// histograms byte k of the keys whose top k-1 bytes equal a target's known
+// prefix.  The selected keys are decoded and interpolated exactly as in
+// quantile_edges_kernel.
+// ---------------------------------------------------------------------------
+__device__ inline uint32_t float_to_key(float x) {
+  uint32_t u = __float_as_uint(x);
+  if (x != x) return 0xffffffffu;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ inline float key_to_float(uint32_t k) {
+  const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+// X [n, F] float32 (row stride xs) -> keys [F, n]; 64 x 64 tiles through LDS
+__global__ __launch_bounds__(256) void transpose_keys_kernel(const float* __restrict__ X,
+                                                             int64_t n, int32_t F, int64_t xs,
+                                                             uint32_t* __restrict__ keys) {
+  __shared__ uint32_t t[64][65];
+  const int64_t r0 = (int64_t)blockIdx.x * 64;
+  const int f0 = blockIdx.y * 64;
+  const int c = threadIdx.x & 63;
+  for (int k = threadIdx.x >> 6; k < 64; k += 4) {
+    const int64_t r = r0 + k;
+    t[k][c] = (r < n && f0 + c < F) ? float_to_key(X[r * xs + f0 + c]) : 0u;
+  }
+  __syncthreads();
+  for (int k = threadIdx.x >> 6; k < 64; k += 4) {
+    const int f = f0 + k;
+    const int64_t r = r0 + c;
+    if (f < F && r < n) keys[(int64_t)f * n + r] = t[c][k];
+  }
+}
+
+constexpr int kSelThreads = 1024;
+constexpr int kSelMaxTargets = 256;   // 2 * 126 ranks at most (num_bins <= 127)
+constexpr int kSelGroup = 48;         // distinct prefixes histogrammed per column pass
+
+__global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
+    const uint32_t* __restrict__ keys, int64_t n, int32_t F, const float* __restrict__ q,
+    int32_t nq, float* __restrict__ edges) {
+  __shared__ uint32_t hist[kSelGroup][256];        // 48 KB
+  __shared__ uint32_t tprefix[kSelMaxTargets];      // known key bits of each target
+  __shared__ int64_t trank[kSelMaxTargets];         // rank still to find within the prefix
+  __shared__ uint32_t dist[kSelMaxTargets];         // distinct prefixes of this pass (sorted)
+  __shared__ int s_nd, s_nan;
+  const int f = blockIdx.x;
+  if (f >= F) return;
+  const uint32_t* col = keys + (int64_t)f * n;
+  const int nt = 2 * nq;
+  const int64_t last = n - 1;
+  for (int t = threadIdx.x; t < nt; t += kSelThreads) {
+    const float rank = q[t >> 1] * (float)last;
+    int64_t r = (t & 1) ? (int64_t)ceilf(rank) : (int64_t)rank;
+    r = r < 0 ? 0 : (r > last ? last : r);
+    trank[t] = r;
+    tprefix[t] = 0;
+  }
+  if (threadIdx.x == 0) s_nan = 0;
+  // pass 1: histogram of the top byte (per-wave copies in hist rows 0..15)
+  for (int i = threadIdx.x; i < 16 * 256; i += kSelThreads) (&hist[0][0])[i] = 0;
+  __syncthreads();
+  {
+    const int w = threadIdx.x >> 6;
+    int nan_local = 0;
+    for (int64_t i = threadIdx.x; i < n; i += kSelThreads) {
+      const uint32_t k = col[i];
+      nan_local += k == 0xffffffffu;
+      atomicAdd(&hist[w][k >> 24], 1u);
+    }
+    if (nan_local) atomicAdd(&s_nan, nan_local);
+  }
+  __syncthreads();
+  if (s_nan) {  // torch.quantile: a NaN anywhere makes every quantile NaN
+    for (int j = threadIdx.x; j < nq; j += kSelThreads)
+      edges[(int64_t)f * nq + j] = __builtin_nanf("");
+    return;
+  }
+  for (int b = threadIdx.x; b < 256; b += kSelThreads) {
+    uint32_t s = 0;
+    for (int w = 0; w < 16; ++w) s += hist[w][b];
+    hist[16][b] = s;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < nt; t += kSelThreads) {
+    int64_t r = trank[t];
+    int b = 0;
+    while (r >= (int64_t)hist[16][b]) r -= hist[16][b++];
+    tprefix[t] = (uint32_t)b;
+    trank[t] = r;
+  }
+  __syncthreads();
+  // passes 2..4: next byte of the keys that share a target's prefix
+  for (int pass = 1; pass < 4; ++pass) {
+    const int sh = 32 - 8 * pass;  // prefix = key >> sh
+    if (threadIdx.x == 0) {
+      // sorted distinct prefixes (insertion sort of <= 252 values)
+      int nd = 0;
+      for (int t = 0; t < nt; ++t) {
+        const uint32_t v = tprefix[t];
+        int pos = nd;
+        while (pos > 0 && dist[pos - 1] > v) --pos;
+        if (pos > 0 && dist[pos - 1] == v) continue;
+        for (int m = nd; m > pos; --m) dist[m] = dist[m - 1];
+        dist[pos] = v;
+        ++nd;
+      }
+      s_nd = nd;
+    }
+    __syncthreads();
+    const int nd = s_nd;
+    for (int g0 = 0; g0 < nd; g0 += kSelGroup) {
+      const int gn = nd - g0 < kSelGroup ? nd - g0 : kSelGroup;
+      for (int i = threadIdx.x; i < gn * 256; i += kSelThreads) (&hist[0][0])[i] = 0;
+      __syncthreads();
+      const uint32_t lo_p = dist[g0], hi_p = dist[g0 + gn - 1];
+      for (int64_t i = threadIdx.x; i < n; i += kSelThreads) {
+        const uint32_t k = col[i];
+        const uint32_t pre = k >> sh;
+        if (pre < lo_p || pre > hi_p) continue;
+        int lo = g0, hi = g0 + gn - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (dist[mid] < pre) lo = mid + 1; else hi = mid;
+        }
+        if (dist[lo] == pre) atomicAdd(&hist[lo - g0][(k >> (sh - 8)) & 255u], 1u);
+      }
+      __syncthreads();
+      for (int t = threadIdx.x; t < nt; t += kSelThreads) {
+        int lo = g0, hi = g0 + gn - 1;
+        const uint32_t pre = tprefix[t];
+        if (pre < dist[g0] || pre > dist[g0 + gn - 1]) continue;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (dist[mid] < pre) lo = mid + 1; else hi = mid;
+        }
+        int64_t r = trank[t];
+        int b = 0;
+        while (b < 255 && r >= (int64_t)hist[lo - g0][b]) r -= hist[lo - g0][b++];
+        tprefix[t] = (pre << 8) | (uint32_t)b;
+        trank[t] = r;
+      }
+      __syncthreads();
+    }
+  }
+  // interpolate (torch.quantile, linear): see quantile_edges_kernel
+  for (int j = threadIdx.x; j < nq; j += kSelThreads) {
+    const float rank = q[j] * (float)last;
+    const int64_t lo = (int64_t)rank;
+    const float w = rank - (float)lo;
+    const float a = key_to_float(tprefix[2 * j]);
+    const float b = key_to_float(tprefix[2 * j + 1]);
+    const float d = b - a;
+    edges[(int64_t)f * nq + j] = w < 0.5f ? fmaf(w, d, a) : fmaf(w - 1.0f, d, b);
+  }
+}
+
 }  // namespace wgbm

@@ -225,6 +225,30 @@ int wgbm_quantile_edges(const float* sorted, int64_t n, int32_t n_feats, const f
   return 0;
 }
 
+int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride,
+                               const float* q, int32_t nq, float* edges, void* stream) {
+  WGBM_REQUIRE(n >= 1 && n_feats >= 0 && nq >= 0 && nq <= 126 && x_stride >= n_feats,
+               "bad quantile shape");
+  WGBM_REQUIRE(n <= (int64_t(1) << 24), "quantile input too large (n > 2^24), as torch.quantile");
+  if ((int64_t)n_feats * nq == 0) return 0;
+  WGBM_REQUIRE(X && q && edges, "null pointer");
+  hipStream_t st = S(stream);
+  // column-major keys of up to `chunk` features at a time (bounded scratch)
+  const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n_feats, (int64_t(1) << 28) / n));
+  uint32_t* keys = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (size_t)(chunk * n), 8);
+  WGBM_REQUIRE(keys, "scratch allocation failed");
+  for (int64_t f0 = 0; f0 < n_feats; f0 += chunk) {
+    const int32_t fc = (int32_t)std::min<int64_t>(chunk, n_feats - f0);
+    dim3 tg(nblocks(n, 64), nblocks(fc, 64));
+    hipLaunchKernelGGL(transpose_keys_kernel, tg, dim3(256), 0, st, X + f0, n, fc, x_stride, keys);
+    WGBM_LAUNCH_CHECK();
+    hipLaunchKernelGGL(quantile_select_kernel, dim3(fc), dim3(1024), 0, st, keys, n, fc, q, nq,
+                       edges + f0 * nq);
+    WGBM_LAUNCH_CHECK();
+  }
+  return 0;
+}
+
 int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride,
                     const float* edges, int32_t n_edges, int8_t* codes_rm, int64_t codes_stride,
                     int8_t* codes_cm, void* stream) {

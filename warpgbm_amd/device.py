@@ -8,6 +8,9 @@ library (or without a GPU) raises -- there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes as C
+import concurrent.futures as cf
+import os
+import threading
 from dataclasses import dataclass
 
 import numpy as np
@@ -65,16 +68,74 @@ def upload_prebinned(X: np.ndarray, dev, with_cm: bool) -> Codes:
     return c
 
 
+_STAGE_BYTES = 64 << 20   # one pinned staging buffer
+_STAGE_COUNT = 4          # buffers in rotation
+_stage_lock = threading.Lock()
+_stage_bufs: list = []
+_pool = None
+
+
+def _staging():
+    """Reusable pinned host buffers (allocated pinned, never registered)."""
+    global _pool
+    with _stage_lock:
+        if not _stage_bufs:
+            for _ in range(_STAGE_COUNT):
+                _stage_bufs.append(torch.empty(_STAGE_BYTES, dtype=torch.uint8, pin_memory=True))
+        if _pool is None:
+            _pool = cf.ThreadPoolExecutor(max(1, min(8, os.cpu_count() or 1)))
+    return _stage_bufs, _pool
+
+
 def upload_float(X: np.ndarray, dev) -> torch.Tensor:
     """float32 [n, F] contiguous copy of X on the device (float64 input is
-    rounded to float32 first, as ``torch.as_tensor(..., dtype=float32)``)."""
-    return torch.from_numpy(np.ascontiguousarray(X, dtype=np.float32)).to(dev)
+    rounded to float32 first, as ``torch.as_tensor(..., dtype=float32)``).
+
+    Large inputs are streamed through pinned staging buffers: host threads
+    fill one buffer (converting the dtype on the way) while the DMA engine
+    copies the previous ones on a side stream."""
+    X = np.asarray(X)
+    n, F = X.shape
+    row_bytes = 4 * max(F, 1)
+    if n * row_bytes < 4 * _STAGE_BYTES or not X.flags.c_contiguous:
+        return torch.from_numpy(np.ascontiguousarray(X, dtype=np.float32)).to(dev)
+    out = torch.empty((n, F), dtype=torch.float32, device=dev)
+    bufs, pool = _staging()
+    rows_per = max(1, _STAGE_BYTES // row_bytes)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    events = [None] * len(bufs)
+    nthreads = pool._max_workers
+
+    def fill(dst, lo, hi):
+        np.copyto(dst[lo:hi], X[r0 + lo:r0 + hi], casting="same_kind")
+
+    for i, r0 in enumerate(range(0, n, rows_per)):
+        r1 = min(n, r0 + rows_per)
+        k = i % len(bufs)
+        if events[k] is not None:
+            events[k].synchronize()  # the DMA that used this buffer has finished
+        host = bufs[k][: (r1 - r0) * row_bytes].view(torch.float32).view(r1 - r0, F)
+        dst = host.numpy()
+        step = max(1, (r1 - r0 + nthreads - 1) // nthreads)
+        list(pool.map(lambda a: fill(dst, a, min(a + step, r1 - r0)), range(0, r1 - r0, step)))
+        with torch.cuda.stream(side):
+            out[r0:r1].copy_(host, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(side)
+        events[k] = ev
+    torch.cuda.current_stream(dev).wait_stream(side)
+    out.record_stream(side)
+    for ev in events:
+        if ev is not None:
+            ev.synchronize()  # buffers are reused by the next upload
+    return out
 
 
-def quantile_edges(Xd: torch.Tensor, num_bins: int, chunk: int = 256) -> torch.Tensor:
+def quantile_edges(Xd: torch.Tensor, num_bins: int) -> torch.Tensor:
     """Per-feature quantile edges [F, num_bins - 1] (the torch.quantile call of
-    warpgbm/core.py:529-534).  Columns are sorted on the device, then the
-    edge formula runs in the HIP kernel ``wgbm_quantile_edges``."""
+    warpgbm/core.py:529-534), by radix selection on the device
+    (``wgbm_quantile_edges_matrix``)."""
     n, F = Xd.shape
     if n > (1 << 24):
         raise ValueError("quantile() input tensor is too large (more than 2^24 rows per feature)")
@@ -83,14 +144,21 @@ def quantile_edges(Xd: torch.Tensor, num_bins: int, chunk: int = 256) -> torch.T
     nq = num_bins - 1
     edges = torch.empty((F, nq), dtype=torch.float32, device=dev)
     lib = _lib.load()
-    for f0 in range(0, F, chunk):
-        f1 = min(F, f0 + chunk)
-        cols = Xd[:, f0:f1].t().contiguous()
-        srt = torch.sort(cols, dim=1).values
-        rc = lib.wgbm_quantile_edges(srt.data_ptr(), n, f1 - f0, q.data_ptr(), nq,
-                                     edges[f0:f1].data_ptr(), _stream(dev))
-        _lib.check(rc, "quantile_edges")
-        del cols, srt
+    rc = lib.wgbm_quantile_edges_matrix(Xd.data_ptr(), n, F, F, q.data_ptr(), nq,
+                                        edges.data_ptr(), _stream(dev))
+    _lib.check(rc, "quantile_edges_matrix")
+    return edges
+
+
+def quantile_edges_sorted(sorted_cols: torch.Tensor, num_bins: int) -> torch.Tensor:
+    """Edges from columns already sorted ascending, [F, n] (``wgbm_quantile_edges``)."""
+    F, n = sorted_cols.shape
+    dev = sorted_cols.device
+    q = quantile_levels(num_bins).to(dev)
+    edges = torch.empty((F, num_bins - 1), dtype=torch.float32, device=dev)
+    rc = _lib.load().wgbm_quantile_edges(sorted_cols.data_ptr(), n, F, q.data_ptr(),
+                                         num_bins - 1, edges.data_ptr(), _stream(dev))
+    _lib.check(rc, "quantile_edges")
     return edges
 
 
