@@ -28,7 +28,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
                               int32_t n_out_feats, int32_t num_bins, float* G, float* H,
                               hipStream_t st) {
   const int V = hist_pick_v(num_bins);
-  const int n_chunks = (n_hist_feats + 16 * V - 1) / (16 * V);
+  const int n_chunks = (n_hist_feats + kHistSlots * V - 1) / (kHistSlots * V);
   // scratch layout (slot 0: control words and the per-block maxima)
   constexpr int kAbsBlocks = 512;
   uint32_t* ctl = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (64 + kAbsBlocks), 0);
@@ -82,7 +82,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   const int64_t max_tiles = n_pos / R + n_keys + 1;
   Tile* tiles = (Tile*)scratch_get(st, sizeof(Tile) * max_tiles, 3);
   int32_t* kts = (int32_t*)scratch_get(st, sizeof(int32_t) * ((size_t)n_keys + 1), 4);
-  const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
+  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
   const int64_t words = max_tiles * tile_words;
   unsigned long long* part =
       (unsigned long long*)scratch_get(st, sizeof(unsigned long long) * words, 5);
@@ -97,11 +97,11 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   a.n_feats = n_hist_feats;
   a.resid = resid;
   a.resid_tree_stride = 0;
+  a.shifts = shift;
   a.order = order;
   a.tiles = tiles;
   a.n_tiles = n_tiles;
   a.keys_per_tree = n_keys;
-  a.shifts = shift;
   a.num_bins = num_bins;
   a.part = part;
   a.V = V;

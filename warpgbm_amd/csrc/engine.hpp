@@ -74,7 +74,8 @@ __global__ void partition_count_kernel(
     int64_t* tot_c_next);
 __global__ void partition_scan_kernel(int32_t T, int32_t nodes, int32_t E, const int64_t* seg,
                                       const Tile* tiles, const int32_t* key_tile_start,
-                                      const int32_t* tile_left, const int32_t* split_l,
+                                      const int32_t* n_tiles, const int32_t* tile_left,
+                                      const int32_t* split_l,
                                       int64_t* Lk, int64_t* tile_lbase, int64_t* tile_rbase,
                                       int64_t* seg_next, int32_t* present_next,
                                       int32_t* key_list_next);
@@ -93,8 +94,9 @@ __global__ void split_level_e1_kernel(const int64_t* hq, const int32_t* hc, int3
                                       int32_t B, const int32_t* feat_sel, int32_t n_sel,
                                       int32_t nodes_in_level, const int32_t* present,
                                       const int32_t* shifts, float mcw, float eps,
-                                      float min_split_gain, int32_t* split_l, int32_t* split_b,
-                                      float* split_gain);
+                                      float min_split_gain, unsigned long long* best);
+__global__ void split_decode_kernel(const unsigned long long* best, int32_t n_tn, int32_t B,
+                                    int32_t* split_l, int32_t* split_b, float* split_gain);
 __global__ void split_level_scan_kernel(const int64_t* hq, const int32_t* hc, int32_t F,
                                         int32_t B, int32_t E, const int32_t* feat_sel,
                                         int32_t n_sel, int32_t nodes_in_level, int32_t n_tn,

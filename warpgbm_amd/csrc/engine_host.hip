@@ -61,6 +61,7 @@ struct Engine {
   int32_t* split_b = nullptr;
   float* split_gain = nullptr;
   float* leaf_val = nullptr;
+  unsigned long long* best = nullptr;
   std::vector<void*> allocs;
 };
 
@@ -113,7 +114,7 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
                 B = cfg.num_bins;
   const int D = cfg.max_depth;
   e->V = hist_pick_v(cfg.num_bins);
-  e->n_chunks = (int)((F + 16 * e->V - 1) / (16 * e->V));
+  e->n_chunks = (int)((F + kHistSlots * e->V - 1) / (kHistSlots * e->V));
   e->qbits = wgbm_qbits_for_rows(N);
   e->H = (1 << (D + 1)) - 1;
   const int64_t nodes_max = int64_t(1) << D;
@@ -152,6 +153,7 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->split_b, T * nodes_max);
   E_ALLOC(e->split_gain, T * nodes_max * E);
   E_ALLOC(e->leaf_val, T * nodes_max);
+  E_ALLOC(e->best, T * nodes_max);
   *out = e;
   return 0;
 }
@@ -178,7 +180,7 @@ static int64_t pick_tile_rows(const Engine* e, int64_t rows_bound) {
 }
 
 static int ensure_partials(Engine* e, int64_t max_tiles) {
-  const int64_t words = max_tiles * e->n_chunks * 16 * e->V * e->c.num_bins;
+  const int64_t words = max_tiles * e->n_chunks * kHistSlots * e->V * e->c.num_bins;
   if (words <= e->part_words) return 0;
   if (e->part) {
     // partial buffers are only reused within the stream; grow after a sync
@@ -280,11 +282,11 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       a.n_feats = F;
       a.resid = e->resid;
       a.resid_tree_stride = N;
+      a.shifts = e->shifts;
       a.order = e->order[cur];
       a.tiles = e->htiles;
       a.n_tiles = e->hn;
       a.keys_per_tree = nodes * E;
-      a.shifts = e->shifts;
       a.num_bins = B;
       a.part = e->part;
       a.V = e->V;
@@ -294,7 +296,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       r = launch_hist_tiles(a, st);
       timer_end(tm, st);
       if (r) return r;
-      const int64_t tile_words = (int64_t)e->n_chunks * 16 * e->V * B;
+      const int64_t tile_words = (int64_t)e->n_chunks * kHistSlots * e->V * B;
       const unsigned fin_wg = (unsigned)(n_list * ((tile_words + 31) / 32));
       hipLaunchKernelGGL(hist_finalize_level_kernel, dim3(fin_wg), dim3(256), 0, st,
                          e->part, e->hkts, list, n_list, e->n_chunks, e->V, B, F, E,
@@ -302,9 +304,14 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       WGBM_LAUNCH_CHECK();
       // ---- split search + DES selection
       if (E == 1) {
-        hipLaunchKernelGGL(split_level_e1_kernel, dim3(n_tn), dim3(256), 0, st, e->hq[hcur],
-                           e->hc[hcur], F, B, feat_sel, n_sel, nodes, e->present[cur], e->shifts,
-                           mcw, eps, msg, e->split_l, e->split_b, e->split_gain);
+        if (fill_u64(e->best, n_tn, 0ull, st)) return WGBM_EINVAL;
+        const int bpn = (n_sel + 255) / 256;
+        hipLaunchKernelGGL(split_level_e1_kernel, dim3((unsigned)(n_tn * bpn)), dim3(256), 0, st,
+                           e->hq[hcur], e->hc[hcur], F, B, feat_sel, n_sel, nodes,
+                           e->present[cur], e->shifts, mcw, eps, msg, e->best);
+        WGBM_LAUNCH_CHECK();
+        hipLaunchKernelGGL(split_decode_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st,
+                           e->best, n_tn, B, e->split_l, e->split_b, e->split_gain);
         WGBM_LAUNCH_CHECK();
       } else {
         const int64_t ns = (int64_t)n_tn * E * n_sel;
@@ -347,7 +354,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     WGBM_LAUNCH_CHECK();
     if (d < D) {
       hipLaunchKernelGGL(partition_scan_kernel, dim3(1), dim3(1024), 0, st, T, nodes, E,
-                         e->seg[cur], e->ptiles, e->pkts, e->tile_left, e->split_l, e->Lk,
+                         e->seg[cur], e->ptiles, e->pkts, e->pn, e->tile_left, e->split_l, e->Lk,
                          e->lbase, e->rbase, e->seg[nxt], e->present[nxt], e->key_list[nxt]);
       WGBM_LAUNCH_CHECK();
       hipLaunchKernelGGL(partition_scatter_kernel, dim3((unsigned)e->max_ptiles), dim3(256), 0, st,

@@ -274,26 +274,39 @@ __device__ inline int64_t block_excl_scan(int64_t v, int64_t* wsum /*[16]*/, int
 __global__ __launch_bounds__(1024) void partition_scan_kernel(
     int32_t T, int32_t nodes, int32_t E, const int64_t* __restrict__ seg,
     const Tile* __restrict__ tiles, const int32_t* __restrict__ key_tile_start,
-    const int32_t* __restrict__ tile_left, const int32_t* __restrict__ split_l,
-    int64_t* __restrict__ Lk, int64_t* __restrict__ tile_lbase, int64_t* __restrict__ tile_rbase,
+    const int32_t* __restrict__ n_tiles_dev, const int32_t* __restrict__ tile_left,
+    const int32_t* __restrict__ split_l, int64_t* __restrict__ Lk,
+    int64_t* __restrict__ tile_lbase, int64_t* __restrict__ tile_rbase,
     int64_t* __restrict__ seg_next, int32_t* __restrict__ present_next,
     int32_t* __restrict__ key_list_next) {
   __shared__ int64_t wsum[16];
   const int n_keys = T * nodes * E;
-  // phase 1: lefts per segment, left-prefix per tile (stored in tile_lbase)
+  const int n_tiles = *n_tiles_dev;
+  // phase 1: exclusive scan of the left counts over all tiles (tiles of a
+  // segment are consecutive), kept in tile_lbase for now
+  int64_t carry = 0;
+  for (int base = 0; base < n_tiles; base += blockDim.x) {
+    const int t = base + threadIdx.x;
+    const int64_t v = t < n_tiles ? tile_left[t] : 0;
+    int64_t tot;
+    const int64_t ex = block_excl_scan(v, wsum, &tot);
+    if (t < n_tiles) tile_lbase[t] = carry + ex;
+    carry += tot;
+  }
+  __syncthreads();
+  // lefts per segment: difference of the scan at its first tile and the next
+  // segment's first tile
   for (int k = threadIdx.x; k < n_keys; k += blockDim.x) {
-    int64_t acc = 0;
-    for (int tt = key_tile_start[k]; tt < key_tile_start[k + 1]; ++tt) {
-      tile_lbase[tt] = acc;
-      acc += tile_left[tt];
-    }
-    Lk[k] = acc;
+    const int t0 = key_tile_start[k], t1 = key_tile_start[k + 1];
+    const int64_t a = t0 < n_tiles ? tile_lbase[t0] : carry;
+    const int64_t b = t1 < n_tiles ? tile_lbase[t1] : carry;
+    Lk[k] = t1 > t0 ? b - a : 0;
   }
   __syncthreads();
   // phase 2: exclusive scan of next-level segment sizes
   const int nodes2 = 2 * nodes;
   const int n_next = T * nodes2 * E;
-  int64_t carry = 0;
+  carry = 0;
   for (int base = 0; base < n_next; base += blockDim.x) {
     const int k2 = base + threadIdx.x;
     int64_t sz = 0;
@@ -316,8 +329,15 @@ __global__ __launch_bounds__(1024) void partition_scan_kernel(
   }
   if (threadIdx.x == 0) seg_next[n_next] = carry;
   __syncthreads();
-  // phase 3: per-tile output bases
-  for (int k = threadIdx.x; k < n_keys; k += blockDim.x) {
+  // phase 3: per-tile output bases (one thread per tile).  The left prefix
+  // inside the segment is taken first (into tile_rbase) for every tile, since
+  // the bases then overwrite the scan the prefixes are read from.
+  for (int tt = threadIdx.x; tt < n_tiles; tt += blockDim.x)
+    tile_rbase[tt] = tile_lbase[tt] - tile_lbase[key_tile_start[tiles[tt].key]];
+  __syncthreads();
+  for (int tt = threadIdx.x; tt < n_tiles; tt += blockDim.x) {
+    const Tile tl = tiles[tt];
+    const int k = tl.key;
     const int tn = k / E;
     if (split_l[tn] < 0) continue;
     const int e = k - tn * E;
@@ -325,12 +345,10 @@ __global__ __launch_bounds__(1024) void partition_scan_kernel(
     const int node = tn - t * nodes;
     const int64_t kl = ((int64_t)t * nodes2 + 2 * node) * E + e;
     const int64_t kr = kl + E;
-    for (int tt = key_tile_start[k]; tt < key_tile_start[k + 1]; ++tt) {
-      const int64_t lpre = tile_lbase[tt];
-      const int64_t before = tiles[tt].begin - seg[k];
-      tile_lbase[tt] = seg_next[kl] + lpre;
-      tile_rbase[tt] = seg_next[kr] + (before - lpre);
-    }
+    const int64_t lpre = tile_rbase[tt];
+    const int64_t before = tl.begin - seg[k];
+    tile_lbase[tt] = seg_next[kl] + lpre;
+    tile_rbase[tt] = seg_next[kr] + (before - lpre);
   }
   // phase 4: presence and the histogram key list of the next level
   for (int tn = threadIdx.x; tn < T * nodes; tn += blockDim.x) {

@@ -7,16 +7,18 @@
 // MI355X design
 // * Rows are processed in TILES; every tile lies inside one SEGMENT (a run of
 //   the row-order array that shares one histogram: a node, or a (node, era)
-//   pair).  One workgroup = one tile x one chunk of 16*V features.
-// * A wave reads 4 rows at a time; the 16 lanes of a row ("slots") each load V
-//   consecutive code bytes with one buffer load (16 B for V = 16), so a wave
-//   touches 4 x 256 contiguous bytes per instruction.
+//   pair).  One workgroup = one tile x one chunk of 64*V features.
+// * Lane l of every wave owns the V consecutive features chunk*64*V + l*V ..
+//   + V-1 and reads their codes with one V-byte buffer load per row, so one
+//   load instruction covers 64*V contiguous bytes of one row.  A wave works
+//   on one row at a time: the row index and its residual are wave-uniform
+//   (scalar loads), and the software pipeline keeps U rows of loads in flight
+//   per wave.
 // * The workgroup histogram lives in LDS as packed 64-bit words
 //   (q * 2^18 + 1: exact gradient sum and row count in one ds_add_u64).  Word
-//   (j, b, slot) sits at index (j*(B+1) + b)*16 + slot: the slot owns its V
-//   features, so the 16 lanes of a row always address 16 different 8-byte bank
-//   pairs whatever the bin values are -- there are no data-dependent bank
-//   conflicts, only the unavoidable 4-way sharing between the 4 rows.
+//   (j, b, lane) sits at index (j*(B+1) + b)*64 + lane: every lane updates its
+//   own column, so the 64 lanes of an atomic never share an address or a
+//   bank pair whatever the bin values are (no address or bank conflicts).
 //   Bin B is a trash row for out-of-range codes (negative pre-binned codes and
 //   features beyond the end of the row), which keeps the inner loop branch-free.
 // * Each tile writes its partial histogram (exact int64 sum, int32 count) in
@@ -30,172 +32,174 @@ namespace wgbm {
 // --------------------------------------------------------------------------
 // tile accumulation
 // --------------------------------------------------------------------------
-template <int V>
-struct CodeVec;
-template <>
-struct CodeVec<16> {
-  uint32_t w[4];
-};
-template <>
-struct CodeVec<8> {
-  uint32_t w[2];
-};
-template <>
-struct CodeVec<4> {
-  uint32_t w[1];
-};
-
-template <int V, int MODE>
-__device__ inline CodeVec<V> load_codes(const int8_t* __restrict__ codes,
-                                        __amdgpu_buffer_rsrc_t rs, int64_t off,
-                                        bool valid, int n_valid_bytes) {
-  CodeVec<V> v;
-  if (MODE == kLoadBuffer) {
-    // bounds-checked raw buffer load: an offset past the buffer returns zeros
-    // codes are streamed once: non-temporal loads (cache policy bit "nt")
-    const int o = valid ? (int)off : 0x7fffffff;
-    if constexpr (V == 16) {
-      auto x = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, kAuxNT);
-      v.w[0] = x[0]; v.w[1] = x[1]; v.w[2] = x[2]; v.w[3] = x[3];
-    } else if constexpr (V == 8) {
-      auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, kAuxNT);
-      v.w[0] = x[0]; v.w[1] = x[1];
-    } else {
-      v.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, kAuxNT);
-    }
-  } else if (MODE == kLoadGlobalAligned) {
-    // row stride and chunk offsets are multiples of V bytes: aligned vector
-    // loads that never run past the row (f_base + V <= stride)
-    typedef uint32_t u32v __attribute__((ext_vector_type(V / 4)));
-    if (valid) {
-      u32v x = __builtin_nontemporal_load(reinterpret_cast<const u32v*>(codes + off));
-#pragma unroll
-      for (int k = 0; k < V / 4; ++k) v.w[k] = x[k];
-    } else {
-#pragma unroll
-      for (int k = 0; k < V / 4; ++k) v.w[k] = 0;
-    }
-  } else {
-    // byte loads for unaligned strides; only bytes of real features are read
-#pragma unroll
-    for (int k = 0; k < V / 4; ++k) v.w[k] = 0;
-    if (valid) {
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        if (j < n_valid_bytes) {
-          uint32_t b = (uint8_t)codes[off + j];
-          v.w[j >> 2] |= b << (8 * (j & 3));
-        }
-      }
-    }
-  }
-  return v;
-}
-
-// One workgroup (kHistThreads threads) = one tile x one chunk of 16*V features.
-// residual for the tile's tree t = key / keys_per_tree is resid + t*resid_tree_stride.
-// BT > 0 fixes num_bins at compile time (LDS offsets become immediates).
-template <int V, int MODE, int BT>
-__global__ __launch_bounds__(kHistThreads) void hist_tiles_kernel(
+// One workgroup (kHistThreads threads) = one tile x one chunk of 64*V features.
+// The residuals of the tile's tree t = key / keys_per_tree are
+// resid + t*resid_tree_stride, quantised with shifts[t].  BT > 0 fixes
+// num_bins at compile time (LDS offsets become immediates).  GATHER: the rows
+// of positions p are order[p] (else p).
+//
+// The kernel is bound by the LDS atomic unit (one 64-lane ds_add_u64 per row
+// and feature quad); everything else is arranged to keep that unit fed:
+// 8 waves per SIMD (two workgroups per CU, at most 64 VGPRs), row ids and
+// residuals as wave-uniform scalar loads, the row offset in the scalar
+// offset of the code load, and a branch-free add.
+template <int V, int MODE, int BT, bool GATHER>
+__global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void hist_tiles_kernel(
     const int8_t* __restrict__ codes, int64_t n_rows, int64_t stride, int32_t n_feats,
     const float* __restrict__ resid, int64_t resid_tree_stride,
-    const int32_t* __restrict__ order, const Tile* __restrict__ tiles,
-    const int32_t* __restrict__ n_tiles, int32_t keys_per_tree,
-    const int32_t* __restrict__ shifts, int32_t num_bins_rt,
-    unsigned long long* __restrict__ part) {
+    const int32_t* __restrict__ shifts, const int32_t* __restrict__ order,
+    const Tile* __restrict__ tiles, const int32_t* __restrict__ n_tiles, int32_t keys_per_tree,
+    int32_t num_bins_rt, unsigned long long* __restrict__ part) {
   extern __shared__ unsigned long long lds[];
+  constexpr int CW = kHistSlots * V;  // features per chunk
   const int num_bins = BT > 0 ? BT : num_bins_rt;
-  const int n_chunks = (n_feats + 16 * V - 1) / (16 * V);
+  const int n_chunks = (n_feats + CW - 1) / CW;
   const int tile_id = blockIdx.x / n_chunks;
   const int chunk = blockIdx.x - tile_id * n_chunks;
   if (tile_id >= *n_tiles) return;
   const Tile tl = tiles[tile_id];
   const int Bp = num_bins + 1;
-  const int nent = V * Bp * 16;
+  const int nent = V * Bp * kHistSlots;
   for (int i = threadIdx.x; i < nent; i += kHistThreads) lds[i] = 0ull;
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   constexpr int nwaves = kHistThreads / 64;
-  const int slot = lane & 15;
-  const int sub = lane >> 4;
-  const int f_base = chunk * 16 * V + slot * V;
-  const bool f_valid = f_base < n_feats;
+  const int f_base = chunk * CW + lane * V;
   const int tree = tl.key / keys_per_tree;
   const float* __restrict__ r_t = resid + (int64_t)tree * resid_tree_stride;
   const int s = shifts[tree];
+  const int32_t* __restrict__ ord = GATHER ? order + tl.begin : nullptr;
+  const int n = (int)(tl.end - tl.begin);  // a tile has at most 65536 rows
+  // A lane past the last feature reads bytes of its row all the same (offset
+  // 0) and adds them to its own words, which belong to no feature and are
+  // never read back; the clamp below keeps every address inside the lane's
+  // column (padding bytes and other out-of-range codes go to the trash bin B).
+  const int voff = f_base < n_feats ? f_base : 0;
+  const int n_valid_bytes = f_base < n_feats ? (n_feats - f_base < V ? n_feats - f_base : V) : 0;
   const uint32_t rs_bytes = (MODE == kLoadBuffer) ? (uint32_t)(n_rows * stride) : 0u;
   const __amdgpu_buffer_rsrc_t rs = wgbm_rsrc(codes, rs_bytes);
-  unsigned long long* my = lds + slot;
-  // bytes of this lane's vector that lie beyond the last feature are forced to
-  // 0xff, which the clamp below sends to the trash bin
-  const int n_valid_bytes = f_valid ? (n_feats - f_base < V ? n_feats - f_base : V) : 0;
-  uint32_t force[V / 4];
-#pragma unroll
-  for (int k = 0; k < V / 4; ++k) {
-    uint32_t m = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (4 * k + q >= n_valid_bytes) m |= 0xffu << (8 * q);
-    force[k] = m;
-  }
+  unsigned long long* my = lds + lane;
 
-  // software pipeline: the loads of batch k+1 are in flight while batch k is
-  // added into LDS.  Each lane handles rows p, p + step, ..., p + (U-1)*step.
-  constexpr int U = 4;
-  const int64_t step = (int64_t)nwaves * 4;
-  CodeVec<V> cv[U];
-  float rv[U];
-  auto issue = [&](int64_t p0) {
+  // software pipeline: wave w takes the row groups [i, i + U) with
+  // i = (w + k*nwaves)*U (tile-relative).  Two register sets alternate: the
+  // loads of group k+1 are in flight while group k is added into LDS.  The
+  // loop is unrolled twice so that neither set is ever copied (a copy would
+  // wait for every outstanding load).  Positions past the tile end (last
+  // group only) repeat the tile's last row and add nothing.
+  constexpr int U = 8;
+  constexpr int step = nwaves * U;
+  struct Group {
+    uint32_t c[U];
+    float r[U];
+  };
+  Group ga, gb;
+  const int row0 = (int)tl.begin;  // row ids fit 31 bits (checked by the launcher)
+  auto issue = [&](Group& g, int i0) {
+    int rows[U];
+    if (GATHER) {
+      if (i0 + U <= n) {
+        // full group: the U row ids are one contiguous (scalar) read of order
+        int32_t ids[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) ids[u] = ord[i0 + u];
+#pragma unroll
+        for (int u = 0; u < U; ++u) rows[u] = ids[u];
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) rows[u] = ord[i0 + u < n ? i0 + u : n - 1];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) rows[u] = row0 + (i0 + u < n ? i0 + u : n - 1);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t pu = p0 + u * step;
-      const bool ok = pu < tl.end;
-      const int64_t row = ok ? (order ? (int64_t)order[pu] : pu) : 0;
-      rv[u] = ok ? r_t[row] : 0.0f;
-      cv[u] = load_codes<V, MODE>(codes, rs, row * stride + f_base, ok && f_valid, n_valid_bytes);
+      g.r[u] = r_t[rows[u]];
+      if (MODE == kLoadBuffer) {
+        const int so = rows[u] * (int)stride;  // n_rows * stride < 2^31 in this mode
+        if constexpr (V == 4)
+          g.c[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, so, kAuxNT);
+        else if constexpr (V == 2)
+          g.c[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, voff, so, kAuxNT);
+        else
+          g.c[u] = __builtin_amdgcn_raw_buffer_load_b8(rs, voff, so, kAuxNT);
+      } else if (MODE == kLoadGlobalAligned) {
+        // row stride and chunk offsets are multiples of V bytes: aligned loads
+        // that never run past the row (voff + V <= stride)
+        const int8_t* src = codes + (int64_t)rows[u] * stride + voff;
+        if constexpr (V == 4)
+          g.c[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
+        else if constexpr (V == 2)
+          g.c[u] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(src));
+        else
+          g.c[u] = __builtin_nontemporal_load(reinterpret_cast<const uint8_t*>(src));
+      } else {
+        // byte loads for unaligned strides; only bytes of real features are read
+        const int8_t* src = codes + (int64_t)rows[u] * stride + voff;
+        uint32_t w8 = 0;
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+          if (j < n_valid_bytes) w8 |= (uint32_t)(uint8_t)src[j] << (8 * j);
+        g.c[u] = w8;
+      }
     }
   };
-  int64_t p = tl.begin + wave * 4 + sub;
-  if (p < tl.end) issue(p);
-  for (; p < tl.end; p += step * U) {
-    CodeVec<V> cw[U];
-    unsigned long long pk[U];
+  // branch-free: positions past the tile end add the word 0 (no sum, no
+  // count), selected with a wave-uniform condition where the word is used
+  auto add = [&](const Group& g, int i0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int k = 0; k < V / 4; ++k) cw[u].w[k] = cv[u].w[k] | force[k];
-      const int64_t q = (int64_t)wgbm_quantise(rv[u], s);
-      // rows past the tile end add 0 (their codes read as zeros)
-      pk[u] = (p + u * step < tl.end) ? (unsigned long long)(q * (int64_t)(1 << WGBM_CBITS) + 1)
-                                      : 0ull;
-    }
-    if (p + step * U < tl.end) issue(p + step * U);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
+      const int64_t q = (int64_t)wgbm_quantise(g.r[u], s);
+      const unsigned long long w =
+          i0 + u < n ? (unsigned long long)(q * (int64_t)(1 << WGBM_CBITS) + 1) : 0ull;
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        uint32_t c = (cw[u].w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+        uint32_t c = (g.c[u] >> (8 * j)) & 0xffu;
         // out-of-range code (incl. negative int8, read as >= 128) -> trash bin
         c = c < (uint32_t)num_bins ? c : (uint32_t)num_bins;
-        atomicAdd(my + (j * Bp + (int)c) * 16, pk[u]);
+        atomicAdd(my + (j * Bp + (int)c) * kHistSlots, w);
       }
+      // one row at a time: hoisting the next rows' work above these atomics
+      // only raises register pressure (the LDS unit is the bottleneck)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  int i = wave * U;
+  if (i < n) {
+    issue(ga, i);
+    // steady state without conditional loads, so that every add waits for
+    // exactly its own group (the other group's loads stay in flight)
+    while (i + 2 * step < n) {
+      issue(gb, i + step);
+      add(ga, i);
+      issue(ga, i + 2 * step);
+      add(gb, i + step);
+      i += 2 * step;
+    }
+    if (i + step < n) {
+      issue(gb, i + step);
+      add(ga, i);
+      add(gb, i + step);
+    } else {
+      add(ga, i);
     }
   }
   __syncthreads();
 
-  // flush in LDS order: part[tile][chunk][j][b][slot] (trash row dropped); the
+  // flush in LDS order: part[tile][chunk][j][b][lane] (trash row dropped); the
   // packed word (sum * 2^18 + count) is stored as is and unpacked by finalize
-  const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
-  const int64_t chunk_off = (int64_t)tile_id * tile_words + (int64_t)chunk * 16 * V * num_bins;
-  const int nout = V * num_bins * 16;
-  for (int i = threadIdx.x; i < nout; i += kHistThreads) {
-    const int sl = i & 15;
-    const int jb = i >> 4;  // j*B + b
+  const int64_t tile_words = (int64_t)n_chunks * CW * num_bins;
+  const int64_t chunk_off = (int64_t)tile_id * tile_words + (int64_t)chunk * CW * num_bins;
+  const int nout = V * num_bins * kHistSlots;
+  for (int k = threadIdx.x; k < nout; k += kHistThreads) {
+    const int sl = k & (kHistSlots - 1);
+    const int jb = k / kHistSlots;  // j*B + b
     const int j = jb / num_bins;
     const int b = jb - j * num_bins;
-    part[chunk_off + i] = lds[(j * Bp + b) * 16 + sl];
+    part[chunk_off + k] = lds[(j * Bp + b) * kHistSlots + sl];
   }
 }
 
@@ -207,14 +211,14 @@ __device__ inline void unpack_word(unsigned long long P, int64_t& Q, int64_t& C)
 
 // partial-layout index i (within one tile) -> (feature, bin)
 __device__ inline void part_feature_bin(int64_t i, int V, int num_bins, int& f, int& b) {
-  const int per_chunk = 16 * V * num_bins;
+  const int per_chunk = kHistSlots * V * num_bins;
   const int chunk = (int)(i / per_chunk);
   const int r = (int)(i - (int64_t)chunk * per_chunk);
-  const int sl = r & 15;
-  const int jb = r >> 4;
+  const int sl = r & (kHistSlots - 1);
+  const int jb = r / kHistSlots;
   const int j = jb / num_bins;
   b = jb - j * num_bins;
-  f = chunk * 16 * V + sl * V + j;
+  f = chunk * kHistSlots * V + sl * V + j;
 }
 
 // --------------------------------------------------------------------------
@@ -260,7 +264,7 @@ __global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
     const int32_t* __restrict__ shifts, const uint32_t* __restrict__ absmax_bits,
     const int32_t* __restrict__ n_tiles, int32_t accumulate, float* __restrict__ G,
     float* __restrict__ H) {
-  const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
+  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
   const int64_t wpk = (tile_words + kFinWords - 1) / kFinWords;  // workgroups per segment
   const int k = (int)(blockIdx.x / wpk);
   const int64_t i = (blockIdx.x - (int64_t)k * wpk) * kFinWords + threadIdx.x % kFinWords;
@@ -318,7 +322,7 @@ __global__ __launch_bounds__(256) void hist_finalize_level_kernel(
     int32_t num_bins, int32_t n_feats, int32_t num_eras, int32_t nodes_in_level, int32_t depth,
     const int64_t* __restrict__ parent_q, const int32_t* __restrict__ parent_c,
     const int32_t* __restrict__ n_tiles, int64_t* __restrict__ hq, int32_t* __restrict__ hc) {
-  const int64_t tile_words = (int64_t)n_chunks * 16 * V * num_bins;
+  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
   const int64_t wpk = (tile_words + kFinWords - 1) / kFinWords;
   const int kk = (int)(blockIdx.x / wpk);
   if (kk >= n_list) return;  // uniform per workgroup
@@ -499,30 +503,40 @@ __global__ void era_scatter_kernel(const int32_t* __restrict__ rows, int64_t n,
 // --------------------------------------------------------------------------
 // host launch helpers
 // --------------------------------------------------------------------------
+// features per lane: the largest V in {4, 2, 1} whose LDS histogram
+// V*(B+1)*64 words stays within 68 KiB, so that two workgroups fit a CU
 int hist_pick_v(int num_bins) {
   const int bp = num_bins + 1;
-  if (16 * bp <= 544) return 16;  // num_bins <= 33
-  if (8 * bp <= 544) return 8;    // num_bins <= 67
-  return 4;
+  if (4 * bp <= 136) return 4;  // num_bins <= 33
+  if (2 * bp <= 136) return 2;  // num_bins <= 67
+  return 1;
 }
 
-size_t hist_lds_bytes(int V, int num_bins) { return (size_t)V * (num_bins + 1) * 16 * 8; }
+size_t hist_lds_bytes(int V, int num_bins) {
+  return (size_t)V * (num_bins + 1) * kHistSlots * 8;
+}
 
-template <int V, int MODE, int BT>
+template <int V, int MODE, int BT, bool GATHER>
 static int launch_tiles_t(const HistLaunch& a, hipStream_t st) {
   static bool attr_set = false;
   const size_t lds = hist_lds_bytes(V, a.num_bins);
   if (!attr_set) {
-    WGBM_CHECK(hipFuncSetAttribute((const void*)hist_tiles_kernel<V, MODE, BT>,
+    WGBM_CHECK(hipFuncSetAttribute((const void*)hist_tiles_kernel<V, MODE, BT, GATHER>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     attr_set = true;
   }
   dim3 grid((unsigned)((int64_t)a.n_chunks * a.max_tiles));
-  hipLaunchKernelGGL((hist_tiles_kernel<V, MODE, BT>), grid, dim3(kHistThreads), lds, st, a.codes,
-                     a.n_rows, a.stride, a.n_feats, a.resid, a.resid_tree_stride, a.order, a.tiles,
-                     a.n_tiles, a.keys_per_tree, a.shifts, a.num_bins, a.part);
+  hipLaunchKernelGGL((hist_tiles_kernel<V, MODE, BT, GATHER>), grid, dim3(kHistThreads), lds, st,
+                     a.codes, a.n_rows, a.stride, a.n_feats, a.resid, a.resid_tree_stride,
+                     a.shifts, a.order, a.tiles, a.n_tiles, a.keys_per_tree, a.num_bins, a.part);
   WGBM_LAUNCH_CHECK();
   return 0;
+}
+
+template <int V, int MODE, int BT>
+static int launch_tiles_g(const HistLaunch& a, hipStream_t st) {
+  return a.order ? launch_tiles_t<V, MODE, BT, true>(a, st)
+                 : launch_tiles_t<V, MODE, BT, false>(a, st);
 }
 
 int hist_load_mode(int64_t n_rows, int64_t stride, int V) {
@@ -532,21 +546,22 @@ int hist_load_mode(int64_t n_rows, int64_t stride, int V) {
 }
 
 int launch_hist_tiles(const HistLaunch& a, hipStream_t st) {
+  WGBM_REQUIRE(a.n_rows < ((int64_t)1 << 31), "histogram: at most 2^31 - 1 rows");
   const int mode = hist_load_mode(a.n_rows, a.stride, a.V);
-  if (a.V == 16 && a.num_bins == 32) {
-    if (mode == kLoadBuffer) return launch_tiles_t<16, kLoadBuffer, 32>(a, st);
-    if (mode == kLoadGlobalAligned) return launch_tiles_t<16, kLoadGlobalAligned, 32>(a, st);
+  if (a.V == 4 && a.num_bins == 32) {
+    if (mode == kLoadBuffer) return launch_tiles_g<4, kLoadBuffer, 32>(a, st);
+    if (mode == kLoadGlobalAligned) return launch_tiles_g<4, kLoadGlobalAligned, 32>(a, st);
   }
 #define WGBM_DISPATCH(VV)                                                      \
   if (a.V == VV) {                                                             \
-    if (mode == kLoadBuffer) return launch_tiles_t<VV, kLoadBuffer, 0>(a, st); \
+    if (mode == kLoadBuffer) return launch_tiles_g<VV, kLoadBuffer, 0>(a, st); \
     if (mode == kLoadGlobalAligned)                                            \
-      return launch_tiles_t<VV, kLoadGlobalAligned, 0>(a, st);                 \
-    return launch_tiles_t<VV, kLoadBytes, 0>(a, st);                           \
+      return launch_tiles_g<VV, kLoadGlobalAligned, 0>(a, st);                 \
+    return launch_tiles_g<VV, kLoadBytes, 0>(a, st);                           \
   }
-  WGBM_DISPATCH(16)
-  WGBM_DISPATCH(8)
   WGBM_DISPATCH(4)
+  WGBM_DISPATCH(2)
+  WGBM_DISPATCH(1)
 #undef WGBM_DISPATCH
   wgbm_set_error("launch_hist_tiles: bad V=%d", a.V);
   return WGBM_EINVAL;

@@ -17,6 +17,8 @@ enum { kLoadBuffer = 0, kLoadGlobalAligned = 1, kLoadBytes = 2 };
 
 // threads per histogram workgroup (16 waves; two workgroups fit one CU's LDS)
 constexpr int kHistThreads = 1024;
+// lanes of a histogram row: lane l owns the V features chunk*64*V + l*V + j
+constexpr int kHistSlots = 64;
 // cache-policy bits of a buffer load: non-temporal (streamed once)
 constexpr int kAuxNT = 2;
 // histogram workgroups per launch the tile sizes aim for (2 per CU)
@@ -27,13 +29,13 @@ struct HistLaunch {
   int64_t n_rows;
   int64_t stride;
   int32_t n_feats;
-  const float* resid;
+  const float* resid;                // residuals [tree][row]
   int64_t resid_tree_stride;
+  const int32_t* shifts;             // quantisation shift per tree
   const int32_t* order;
   const Tile* tiles;
   const int32_t* n_tiles;
   int32_t keys_per_tree;
-  const int32_t* shifts;
   int32_t num_bins;
   unsigned long long* part;  // packed tile partials (sum * 2^18 + count)
   int32_t V;

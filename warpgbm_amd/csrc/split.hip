@@ -80,7 +80,7 @@ __global__ void split_f32_kernel(const float* __restrict__ G, const float* __res
 }
 
 // ---------------------------------------------------------------------------
-// engine: E == 1, fused scan + selection.  One workgroup per (tree, node).
+// engine: E == 1, fused scan + selection.
 //   hq/hc: [tree][node][F][B] exact sums; feat_sel: local -> global feature
 // outputs per (tree, node): split_l (local feature or -1), split_b, best gain
 // ---------------------------------------------------------------------------
@@ -88,25 +88,35 @@ __device__ inline bool better(float g, int i, float bg, int bi) {
   return g > bg || (g == bg && i < bi);
 }
 
+// order-preserving map of float bits to uint32 (and back)
+__device__ inline uint32_t gain_key(float g) {
+  const uint32_t u = __float_as_uint(g);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ inline float gain_from_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// One lane per (tree-node, local feature); the node's best candidate is kept
+// as a packed key  gain_key(gain) << 32 | (0xffffffff - flat index)  updated
+// with a 64-bit atomicMax, so the larger gain wins and, on equal gains, the
+// smaller flat index (torch.argmax takes the first).  Integer atomics make
+// the result independent of execution order.  best[tn] == 0: no split (every
+// real key is nonzero: gain_key(-inf) = 0x007fffff).
 __global__ __launch_bounds__(256) void split_level_e1_kernel(
     const int64_t* __restrict__ hq, const int32_t* __restrict__ hc, int32_t F, int32_t B,
     const int32_t* __restrict__ feat_sel, int32_t n_sel, int32_t nodes_in_level,
     const int32_t* __restrict__ present, const int32_t* __restrict__ shifts, float mcw,
-    float eps, float min_split_gain, int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
-    float* __restrict__ split_gain) {
-  const int tn = blockIdx.x;
-  if (!present[tn]) {
-    if (threadIdx.x == 0) {
-      split_l[tn] = -1;
-      split_b[tn] = -1;
-    }
-    return;
-  }
+    float eps, float min_split_gain, unsigned long long* __restrict__ best) {
+  const int blocks_per_node = (n_sel + 255) / 256;
+  const int tn = blockIdx.x / blocks_per_node;
+  const int l = (blockIdx.x - tn * blocks_per_node) * 256 + threadIdx.x;
+  if (!present[tn]) return;  // uniform per workgroup
   const int tree = tn / nodes_in_level;
   const int s = shifts[tree];
   float bg = -__builtin_inff();
   int bi = 0x7fffffff;
-  for (int l = threadIdx.x; l < n_sel; l += blockDim.x) {
+  if (l < n_sel) {
     const int f = feat_sel[l];
     const int64_t base = ((int64_t)tn * F + f) * B;
     const int64_t* q = hq + base;
@@ -123,7 +133,6 @@ __global__ __launch_bounds__(256) void split_level_e1_kernel(
           }
         });
   }
-  // workgroup argmax
   for (int o = 32; o > 0; o >>= 1) {
     const float og = __shfl_xor(bg, o, 64);
     const int oi = __shfl_xor(bi, o, 64);
@@ -132,29 +141,29 @@ __global__ __launch_bounds__(256) void split_level_e1_kernel(
       bi = oi;
     }
   }
-  __shared__ float sg[4];
-  __shared__ int si[4];
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    sg[w] = bg;
-    si[w] = bi;
+  if ((threadIdx.x & 63) == 0 && bi != 0x7fffffff) {
+    const unsigned long long key = ((unsigned long long)gain_key(bg) << 32) |
+                                   (unsigned long long)(0xffffffffu - (uint32_t)bi);
+    atomicMax(best + tn, key);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int k = 1; k < (int)(blockDim.x >> 6); ++k)
-      if (better(sg[k], si[k], bg, bi)) {
-        bg = sg[k];
-        bi = si[k];
-      }
-    if (bi == 0x7fffffff) {
-      split_l[tn] = -1;
-      split_b[tn] = -1;
-    } else {
-      split_l[tn] = bi / (B - 1);
-      split_b[tn] = bi % (B - 1);
-      split_gain[tn] = bg;
-    }
+}
+
+// decode the packed best keys of a level into (local feature, bin, gain)
+__global__ void split_decode_kernel(const unsigned long long* __restrict__ best, int32_t n_tn,
+                                    int32_t B, int32_t* __restrict__ split_l,
+                                    int32_t* __restrict__ split_b, float* __restrict__ split_gain) {
+  const int tn = blockIdx.x * blockDim.x + threadIdx.x;
+  if (tn >= n_tn) return;
+  const unsigned long long k = best[tn];
+  if (k == 0ull) {
+    split_l[tn] = -1;
+    split_b[tn] = -1;
+    return;
   }
+  const int idx = (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
+  split_l[tn] = idx / (B - 1);
+  split_b[tn] = idx % (B - 1);
+  split_gain[tn] = gain_from_key((uint32_t)(k >> 32));
 }
 
 // ---------------------------------------------------------------------------
