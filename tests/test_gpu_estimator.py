@@ -90,6 +90,45 @@ def test_era_des_prebinned_bit_exact(gpu):
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
 
 
+def test_era_des_colsample_uneven_eras_bit_exact(gpu):
+    """Direct era path (every era fits one LDS tile): uneven era sizes, eras
+    that are empty at deeper nodes, a feature subset per tree, a generic bin
+    count and the smallest min_child_weight."""
+    print_case("estimator", "DES E=7 uneven colsample")
+    rng = np.random.default_rng(5)
+    sizes = np.array([900, 40, 1500, 7, 600, 1200, 253])
+    E, N, F = len(sizes), int(sizes.sum()), 23
+    era = np.repeat(np.arange(E), sizes)
+    X = rng.integers(0, 12, (N, F)).astype(np.int8)
+    score = (X[:, :6] - 5.5).sum(axis=1) * np.where(era % 2 == 0, 1.0, -0.5) + rng.standard_normal(N)
+    y = (score / 10.0).astype(F32)
+    kw = dict(num_bins=12, max_depth=5, n_estimators=5, learning_rate=0.3, min_child_weight=1)
+    m = WarpGBM(colsample_bytree=0.6, random_state=11, **kw)
+    m.fit(X, y, era_id=era)
+    ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era, feat_sets=m.feature_subsets_)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
+
+
+def test_era_des_large_eras_histogram_path_bit_exact(gpu):
+    """Eras larger than one LDS tile (65536 rows) take the per-era histogram
+    path (tile partials, exact sibling subtraction, era accumulation)."""
+    print_case("estimator", "DES E=2 large eras")
+    rng = np.random.default_rng(6)
+    N, F, E = 140_000, 8, 2
+    era = np.repeat(np.arange(E), N // E)
+    X = rng.integers(0, 8, (N, F)).astype(np.int8)
+    score = (X[:, 0] - 3.5) + np.where(era == 0, 1.0, -1.0) * (X[:, 1] - 3.5) + rng.standard_normal(N)
+    y = (score / 4.0).astype(F32)
+    kw = dict(num_bins=8, max_depth=3, n_estimators=3, learning_rate=0.5)
+    m = WarpGBM(**kw).fit(X, y, era_id=era)
+    ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
+
+
 def test_colsample_subsets_bit_exact(gpu):
     print_case("estimator", "colsample 0.5")
     X, y = c1_data(n=5000, f=40, seed=3)

@@ -97,14 +97,31 @@ __global__ void split_level_e1_kernel(const int64_t* hq, const int32_t* hc, int3
                                       float min_split_gain, unsigned long long* best);
 __global__ void split_decode_kernel(const unsigned long long* best, int32_t n_tn, int32_t B,
                                     int32_t* split_l, int32_t* split_b, float* split_gain);
-__global__ void split_level_scan_kernel(const int64_t* hq, const int32_t* hc, int32_t F,
-                                        int32_t B, int32_t E, const int32_t* feat_sel,
-                                        int32_t n_sel, int32_t nodes_in_level, int32_t n_tn,
-                                        const int32_t* present, const int32_t* shifts,
-                                        float mcw, float eps, float* gain, int8_t* dir);
-__global__ void des_select_kernel(const float* gain, const int8_t* dir, int32_t B, int32_t E,
-                                  int32_t n_sel, const int32_t* present, float min_split_gain,
-                                  int32_t* split_l, int32_t* split_b, float* split_gain_era);
+__global__ void des_accumulate_kernel(const int64_t* hq, const int32_t* hc, int32_t F, int32_t B,
+                                      int32_t E, const int32_t* feat_sel, int32_t n_sel,
+                                      int32_t nodes_in_level, int32_t n_tn,
+                                      const int32_t* present, const int32_t* shifts, float mcw,
+                                      float eps, float* crit, int32_t* agree, int32_t* agree_max);
+__global__ void des_pick_kernel(const float* crit, const int32_t* agree, const int32_t* agree_max,
+                                const int32_t* present, int32_t n_tn, int64_t ncand,
+                                float min_split_gain, unsigned long long* best);
+__global__ void des_finish_kernel(const unsigned long long* best, const int64_t* hq,
+                                  const int32_t* hc, int32_t F, int32_t B, int32_t E,
+                                  const int32_t* feat_sel, int32_t nodes_in_level, int32_t n_tn,
+                                  const int32_t* shifts, float mcw, float eps, const float* staged,
+                                  int32_t n_sel, int32_t* split_l, int32_t* split_b,
+                                  float* split_gain_era);
+__global__ void des_combine_kernel(const float* gain, const int8_t* dir, int32_t E, int32_t n_tn,
+                                   int64_t ncand, const int32_t* present, float* crit,
+                                   int32_t* agree, int32_t* agree_max);
+__global__ void local_scatter_kernel(const int32_t* feat_sel, int32_t n_sel, int32_t F,
+                                     int32_t* local_of);
+int launch_des_era(int V, int B, dim3 grid, hipStream_t st, const int8_t* codes, int64_t stride,
+                   int32_t F, const float* resid, int64_t resid_tree_stride, const int32_t* shifts,
+                   const int32_t* order, const int64_t* seg, int32_t E, int32_t nodes_in_level,
+                   const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
+                   float eps, float* gain, int8_t* dir);
+
 
 // binning / predict kernels
 __global__ void bin_column_kernel(const float* x, int64_t n, const float* edges,

@@ -55,8 +55,15 @@ struct Engine {
   int64_t part_words = 0;
   int64_t* hq[2] = {nullptr, nullptr};
   int32_t* hc[2] = {nullptr, nullptr};
-  float* sgain = nullptr;
-  int8_t* sdir = nullptr;
+  float* crit = nullptr;         // E > 1: per-candidate era-mean gain [tn][n_sel*(B-1)]
+  int32_t* agree = nullptr;      // E > 1: per-candidate |sum of directions|
+  int32_t* agree_max = nullptr;  // E > 1: per-node max agree
+  // E > 1 with every era <= 65536 rows: per-era gains straight from LDS
+  // histograms of every (node, era) segment (no per-era histogram arrays)
+  bool des_direct = false;
+  float* sgain = nullptr;       // staged per-era gains [tn][E][n_sel][B-1]
+  int8_t* sdir = nullptr;       // staged per-era directions
+  int32_t* local_of = nullptr;  // [F] local index in the round's subset, or -1
   int32_t* split_l = nullptr;
   int32_t* split_b = nullptr;
   float* split_gain = nullptr;
@@ -124,6 +131,20 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->absmax, T);
   E_ALLOC(e->abs_part, T * kResidBlocks);
   E_ALLOC(e->shifts, T);
+  if (E > 1) {
+    // the direct era path needs every (node, era) segment to fit one LDS
+    // histogram (counts < 2^18 per bin): all eras at most 65536 rows
+    std::vector<int64_t> es((size_t)E + 1);
+    if (hipMemcpy(es.data(), cfg.era_start, sizeof(int64_t) * (E + 1), hipMemcpyDeviceToHost) !=
+        hipSuccess) {
+      wgbm_set_error("engine: cannot read era_start");
+      engine_destroy(e);
+      return WGBM_EINVAL;
+    }
+    int64_t mx = 0;
+    for (int64_t k = 0; k < E; ++k) mx = std::max<int64_t>(mx, es[k + 1] - es[k]);
+    e->des_direct = mx <= WGBM_MAX_TILE_ROWS;
+  }
   for (int k = 0; k < 2; ++k) {
     E_ALLOC(e->order[k], T * N);
     E_ALLOC(e->seg[k], e->n_keys_max + 1);
@@ -131,8 +152,15 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     E_ALLOC(e->totc[k], e->n_keys_max);
     E_ALLOC(e->present[k], T * nodes_max);
     E_ALLOC(e->key_list[k], e->n_keys_max);
-    E_ALLOC(e->hq[k], T * hist_nodes_max * E * F * B);
-    E_ALLOC(e->hc[k], T * hist_nodes_max * E * F * B);
+    if (!e->des_direct) {
+      E_ALLOC(e->hq[k], T * hist_nodes_max * E * F * B);
+      E_ALLOC(e->hc[k], T * hist_nodes_max * E * F * B);
+    }
+  }
+  if (e->des_direct) {
+    E_ALLOC(e->sgain, T * hist_nodes_max * E * F * (B - 1));
+    E_ALLOC(e->sdir, T * hist_nodes_max * E * F * (B - 1));
+    E_ALLOC(e->local_of, F);
   }
   E_ALLOC(e->dirbit, T * N);
   e->max_ptiles = T * N / e->part_tile_rows + e->n_keys_max + 1;
@@ -146,8 +174,9 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->hkts, e->n_keys_max + 1);
   E_ALLOC(e->hn, 1);
   if (E > 1) {
-    E_ALLOC(e->sgain, T * hist_nodes_max * E * F * (B - 1));
-    E_ALLOC(e->sdir, T * hist_nodes_max * E * F * (B - 1));
+    E_ALLOC(e->crit, T * hist_nodes_max * F * (B - 1));
+    E_ALLOC(e->agree, T * hist_nodes_max * F * (B - 1));
+    E_ALLOC(e->agree_max, T * nodes_max);
   }
   E_ALLOC(e->split_l, T * nodes_max);
   E_ALLOC(e->split_b, T * nodes_max);
@@ -242,13 +271,47 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                      e->totc[0]);
   WGBM_LAUNCH_CHECK();
 
+  if (e->des_direct) {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks_for(F, 256)), dim3(256), 0, st, e->local_of,
+                       (int64_t)F, -1);
+    WGBM_LAUNCH_CHECK();
+    hipLaunchKernelGGL(local_scatter_kernel, dim3(blocks_for(n_sel, 256)), dim3(256), 0, st,
+                       feat_sel, n_sel, F, e->local_of);
+    WGBM_LAUNCH_CHECK();
+  }
+
   const float mcw = c.min_child_weight, eps = c.l2_reg, msg = c.min_split_gain;
   for (int d = 0; d <= D; ++d) {
     const int nodes = 1 << d;
     const int n_tn = T * nodes;
     const int n_keys = n_tn * E;
     const int hcur = d & 1, hprev = hcur ^ 1;
-    if (d < D) {
+    if (d < D && e->des_direct) {
+      // ---- E > 1, direct: per-era gains of every (node, era) segment
+      const int64_t ncand = (int64_t)n_sel * (B - 1);
+      int r = launch_des_era(e->V, B, dim3((unsigned)((int64_t)n_keys * e->n_chunks)), st,
+                             c.codes_rm, c.stride, F, e->resid, N, e->shifts, e->order[cur],
+                             e->seg[cur], E, nodes, e->present[cur], e->local_of, n_sel, mcw, eps,
+                             e->sgain, e->sdir);
+      if (r) return r;
+      if (fill_u64(e->best, n_tn, 0ull, st)) return WGBM_EINVAL;
+      hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st,
+                         e->agree_max, (int64_t)n_tn, 0);
+      WGBM_LAUNCH_CHECK();
+      hipLaunchKernelGGL(des_combine_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)),
+                         dim3(256), 0, st, e->sgain, e->sdir, E, n_tn, ncand, e->present[cur],
+                         e->crit, e->agree, e->agree_max);
+      WGBM_LAUNCH_CHECK();
+      hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)), dim3(256),
+                         0, st, e->crit, e->agree, e->agree_max, e->present[cur], n_tn, ncand, msg,
+                         e->best);
+      WGBM_LAUNCH_CHECK();
+      hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)n_tn * E, 256)), dim3(256), 0,
+                         st, e->best, (const int64_t*)nullptr, (const int32_t*)nullptr, F, B, E,
+                         feat_sel, nodes, n_tn, e->shifts, mcw, eps, e->sgain, n_sel, e->split_l,
+                         e->split_b, e->split_gain);
+      WGBM_LAUNCH_CHECK();
+    } else if (d < D) {
       // ---- histograms of the computed segments
       const int n_list = d == 0 ? n_keys : T * (nodes / 2) * E;
       const int32_t* list = d == 0 ? nullptr : e->key_list[cur];
@@ -314,13 +377,25 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                            e->best, n_tn, B, e->split_l, e->split_b, e->split_gain);
         WGBM_LAUNCH_CHECK();
       } else {
-        const int64_t ns = (int64_t)n_tn * E * n_sel;
-        hipLaunchKernelGGL(split_level_scan_kernel, dim3(blocks_for(ns, 256)), dim3(256), 0, st,
-                           e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, n_sel, nodes, n_tn,
-                           e->present[cur], e->shifts, mcw, eps, e->sgain, e->sdir);
+        const int64_t ncand = (int64_t)n_sel * (B - 1);
+        const int64_t nacc = (int64_t)n_tn * n_sel * ((B - 1 + kDesChunk - 1) / kDesChunk);
+        if (fill_u64(e->best, n_tn, 0ull, st)) return WGBM_EINVAL;
+        hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st,
+                           e->agree_max, (int64_t)n_tn, 0);
         WGBM_LAUNCH_CHECK();
-        hipLaunchKernelGGL(des_select_kernel, dim3(n_tn), dim3(1024), 0, st, e->sgain, e->sdir, B,
-                           E, n_sel, e->present[cur], msg, e->split_l, e->split_b, e->split_gain);
+        hipLaunchKernelGGL(des_accumulate_kernel, dim3(blocks_for(nacc, 128)), dim3(128), 0, st,
+                           e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, n_sel, nodes, n_tn,
+                           e->present[cur], e->shifts, mcw, eps, e->crit, e->agree,
+                           e->agree_max);
+        WGBM_LAUNCH_CHECK();
+        hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)),
+                           dim3(256), 0, st, e->crit, e->agree, e->agree_max, e->present[cur],
+                           n_tn, ncand, msg, e->best);
+        WGBM_LAUNCH_CHECK();
+        hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)n_tn * E, 256)), dim3(256),
+                           0, st, e->best, e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, nodes,
+                           n_tn, e->shifts, mcw, eps, (const float*)nullptr, n_sel, e->split_l,
+                           e->split_b, e->split_gain);
         WGBM_LAUNCH_CHECK();
       }
     } else {
@@ -329,7 +404,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       WGBM_LAUNCH_CHECK();
     }
     // ---- leaf values and the tree record of this depth
-    hipLaunchKernelGGL(level_finish_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st, d, D, T,
+    hipLaunchKernelGGL(level_finish_kernel, dim3((unsigned)n_tn), dim3(64), 0, st, d, D, T,
                        E, e->present[cur], e->split_l, e->split_b, e->split_gain, feat_sel,
                        e->totq[cur], e->totc[cur], e->shifts, e->leaf_val, rec);
     WGBM_LAUNCH_CHECK();

@@ -117,48 +117,55 @@ __global__ __launch_bounds__(256) void segment_totals_kernel(
 //   leaf value = mean of the node's residuals (warpgbm/core.py:599, :614),
 //   computed from the exact quantised sum: float(ldexp(Sq, -s) / count)
 // ---------------------------------------------------------------------------
-__global__ void level_finish_kernel(int32_t depth, int32_t max_depth, int32_t T, int32_t E,
-                                    const int32_t* __restrict__ present,
-                                    const int32_t* __restrict__ split_l,
-                                    const int32_t* __restrict__ split_b,
-                                    const float* __restrict__ split_gain_era,
-                                    const int32_t* __restrict__ feat_sel,
-                                    const int64_t* __restrict__ tot_q,
-                                    const int64_t* __restrict__ tot_c,
-                                    const int32_t* __restrict__ shifts,
-                                    float* __restrict__ leaf_val, TreeRecord rec) {
+__global__ __launch_bounds__(64) void level_finish_kernel(
+    int32_t depth, int32_t max_depth, int32_t T, int32_t E, const int32_t* __restrict__ present,
+    const int32_t* __restrict__ split_l, const int32_t* __restrict__ split_b,
+    const float* __restrict__ split_gain_era, const int32_t* __restrict__ feat_sel,
+    const int64_t* __restrict__ tot_q, const int64_t* __restrict__ tot_c,
+    const int32_t* __restrict__ shifts, float* __restrict__ leaf_val, TreeRecord rec) {
+  // one wave per (tree, node); the eras are spread over the lanes
   const int nodes = 1 << depth;
-  const int tn = blockIdx.x * blockDim.x + threadIdx.x;
+  const int tn = blockIdx.x;
+  const int lane = threadIdx.x;
   if (tn >= T * nodes) return;
   const int t = tn / nodes;
   const int node = tn - t * nodes;
   const int64_t h = (int64_t)t * rec.H + (nodes - 1) + node;
   if (!present[tn]) {
-    rec.feat[h] = -2;
-    rec.bin[h] = -1;
-    rec.leaf[h] = 0.0f;
-    rec.count[h] = 0;
+    if (lane == 0) {
+      rec.feat[h] = -2;
+      rec.bin[h] = -1;
+      rec.leaf[h] = 0.0f;
+      rec.count[h] = 0;
+    }
     return;
   }
   int64_t sq = 0, sc = 0;
-  for (int e = 0; e < E; ++e) {
+  for (int e = lane; e < E; e += 64) {
     sq += tot_q[(int64_t)tn * E + e];
     sc += tot_c[(int64_t)tn * E + e];
   }
-  rec.count[h] = sc;
-  const int l = depth < max_depth ? split_l[tn] : -1;
-  if (l >= 0) {
-    rec.feat[h] = feat_sel[l];
-    rec.bin[h] = split_b[tn];
-    rec.leaf[h] = 0.0f;
-    for (int e = 0; e < E; ++e) rec.gain[h * E + e] = split_gain_era[(int64_t)tn * E + e];
-  } else {
-    const float v = (float)(ldexp((double)sq, -shifts[t]) / (double)sc);
-    leaf_val[tn] = v;
-    rec.feat[h] = -1;
-    rec.bin[h] = -1;
-    rec.leaf[h] = v;
+  for (int o = 32; o > 0; o >>= 1) {
+    sq += __shfl_xor(sq, o, 64);
+    sc += __shfl_xor(sc, o, 64);
   }
+  const int l = depth < max_depth ? split_l[tn] : -1;
+  if (lane == 0) {
+    rec.count[h] = sc;
+    if (l >= 0) {
+      rec.feat[h] = feat_sel[l];
+      rec.bin[h] = split_b[tn];
+      rec.leaf[h] = 0.0f;
+    } else {
+      const float v = (float)(ldexp((double)sq, -shifts[t]) / (double)sc);
+      leaf_val[tn] = v;
+      rec.feat[h] = -1;
+      rec.bin[h] = -1;
+      rec.leaf[h] = v;
+    }
+  }
+  if (l >= 0)
+    for (int e = lane; e < E; e += 64) rec.gain[h * E + e] = split_gain_era[(int64_t)tn * E + e];
 }
 
 // ---------------------------------------------------------------------------

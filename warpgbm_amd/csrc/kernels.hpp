@@ -19,6 +19,8 @@ enum { kLoadBuffer = 0, kLoadGlobalAligned = 1, kLoadBytes = 2 };
 constexpr int kHistThreads = 1024;
 // lanes of a histogram row: lane l owns the V features chunk*64*V + l*V + j
 constexpr int kHistSlots = 64;
+// split candidates (bins) per lane of the era-accumulating DES scan
+constexpr int kDesChunk = 8;
 // cache-policy bits of a buffer load: non-temporal (streamed once)
 constexpr int kAuxNT = 2;
 // histogram workgroups per launch the tile sizes aim for (2 per CU)

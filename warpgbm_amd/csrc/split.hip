@@ -167,135 +167,377 @@ __global__ void split_decode_kernel(const unsigned long long* __restrict__ best,
 }
 
 // ---------------------------------------------------------------------------
-// engine: E > 1.  (1) per-era scan, one lane per (tree-node, era, local feature)
-//   writes gain/dir into [tn][E][n_sel][B-1]
+// engine: E > 1, without per-era gain/direction arrays.
+//  (1) des_accumulate: one lane per (tree-node, local feature, chunk of up to
+//      kDesChunk split bins) walks the eras in order and keeps, per candidate,
+//      sum_e double(gain_e) and sum_e dir_e (the per-era values are exactly
+//      those of the sequential scan above).  Writes crit = float(sum / E) and
+//      agree = |sum dir| per candidate and the node's max agree (atomicMax).
+//  (2) des_pick: among candidates with agree == max agree and crit >
+//      min_split_gain, the largest crit (first flat index on ties), through a
+//      packed 64-bit atomicMax key as in the E == 1 path.
+//  (3) des_finish: decodes the pick and recomputes the chosen split's per-era
+//      gains for the tree record.
 // ---------------------------------------------------------------------------
-__global__ void split_level_scan_kernel(const int64_t* __restrict__ hq,
-                                        const int32_t* __restrict__ hc, int32_t F, int32_t B,
-                                        int32_t E, const int32_t* __restrict__ feat_sel,
-                                        int32_t n_sel, int32_t nodes_in_level, int32_t n_tn,
-                                        const int32_t* __restrict__ present,
-                                        const int32_t* __restrict__ shifts, float mcw, float eps,
-                                        float* __restrict__ gain, int8_t* __restrict__ dir) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)n_tn * E * n_sel;
-  if (gid >= total) return;
-  const int l = (int)(gid % n_sel);
-  const int e = (int)((gid / n_sel) % E);
-  const int tn = (int)(gid / ((int64_t)n_sel * E));
-  if (!present[tn]) return;
-  const int s = shifts[tn / nodes_in_level];
-  const int f = feat_sel[l];
-  const int64_t base = (((int64_t)tn * E + e) * F + f) * B;
-  const int64_t* q = hq + base;
-  const int32_t* c = hc + base;
-  float* go = gain + gid * (B - 1);
-  int8_t* dout = dir + gid * (B - 1);
-  scan_bins(
-      B, mcw, eps, [&](int b) { return wgbm_dequantise(q[b], s); },
-      [&](int b) { return (float)c[b]; },
-      [&](int b, float gn, float d) {
-        go[b] = gn;
-        dout[b] = (int8_t)d;
-      });
+// wave-level max into *dst when the wave's active lanes share one target;
+// otherwise one atomic per lane
+__device__ inline void atomic_max_grouped_i32(int32_t* base, int key, bool active, int v) {
+  const int k0 = __builtin_amdgcn_readfirstlane(key);
+  const bool uniform = __all(!active || key == k0);
+  if (uniform) {
+    int m = active ? v : -1;
+    for (int o = 32; o > 0; o >>= 1) {
+      const int y = __shfl_xor(m, o, 64);
+      m = y > m ? y : m;
+    }
+    if ((threadIdx.x & 63) == 0 && m >= 0) atomicMax(base + k0, m);
+  } else if (active) {
+    atomicMax(base + key, v);
+  }
 }
 
-// (2) DES selection, one workgroup per (tree, node)
-__global__ __launch_bounds__(1024) void des_select_kernel(
-    const float* __restrict__ gain, const int8_t* __restrict__ dir, int32_t B, int32_t E,
-    int32_t n_sel, const int32_t* __restrict__ present, float min_split_gain,
-    int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
-    float* __restrict__ split_gain_era /* [tn][E] */) {
-  const int tn = blockIdx.x;
-  if (!present[tn]) {
-    if (threadIdx.x == 0) {
+__device__ inline void atomic_max_grouped_u64(unsigned long long* base, int key, bool active,
+                                              unsigned long long v) {
+  const int k0 = __builtin_amdgcn_readfirstlane(key);
+  const bool uniform = __all(!active || key == k0);
+  if (uniform) {
+    unsigned long long m = active ? v : 0ull;
+    for (int o = 32; o > 0; o >>= 1) {
+      const unsigned long long y = __shfl_xor(m, o, 64);
+      m = y > m ? y : m;
+    }
+    if ((threadIdx.x & 63) == 0 && m != 0ull) atomicMax(base + k0, m);
+  } else if (active) {
+    atomicMax(base + key, v);
+  }
+}
+
+__global__ __launch_bounds__(128) void des_accumulate_kernel(
+    const int64_t* __restrict__ hq, const int32_t* __restrict__ hc, int32_t F, int32_t B,
+    int32_t E, const int32_t* __restrict__ feat_sel, int32_t n_sel, int32_t nodes_in_level,
+    int32_t n_tn, const int32_t* __restrict__ present, const int32_t* __restrict__ shifts,
+    float mcw, float eps, float* __restrict__ crit, int32_t* __restrict__ agree,
+    int32_t* __restrict__ agree_max) {
+  const int nb = B - 1;
+  const int nch = (nb + kDesChunk - 1) / kDesChunk;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)n_tn * n_sel * nch;
+  int tn = 0, l = 0, ch = 0;
+  bool active = gid < total;
+  if (active) {
+    ch = (int)(gid % nch);
+    l = (int)((gid / nch) % n_sel);
+    tn = (int)(gid / ((int64_t)nch * n_sel));
+    active = present[tn] != 0;
+  }
+  int amax = 0;
+  if (active) {
+    const int s = shifts[tn / nodes_in_level];
+    const int f = feat_sel[l];
+    const int b0 = ch * kDesChunk;
+    double gs[kDesChunk];
+    int ds[kDesChunk];
+#pragma unroll
+    for (int k = 0; k < kDesChunk; ++k) {
+      gs[k] = 0.0;
+      ds[k] = 0;
+    }
+    for (int e = 0; e < E; ++e) {
+      const int64_t base = (((int64_t)tn * E + e) * F + f) * B;
+      const int64_t* q = hq + base;
+      const int32_t* c = hc + base;
+      // the float operations of scan_bins, in the same order
+      float Gt = 0.0f, Ht = 0.0f;
+      for (int b = 0; b < B; ++b) {
+        Gt = Gt + wgbm_dequantise(q[b], s);
+        Ht = Ht + (float)c[b];
+      }
+      const float tot = (Gt * Gt) / (Ht + eps);
+      float GL = 0.0f, HL = 0.0f;
+      for (int b = 0; b < b0; ++b) {
+        GL = GL + wgbm_dequantise(q[b], s);
+        HL = HL + (float)c[b];
+      }
+#pragma unroll
+      for (int k = 0; k < kDesChunk; ++k) {
+        const int b = b0 + k;
+        if (b < nb) {
+          GL = GL + wgbm_dequantise(q[b], s);
+          HL = HL + (float)c[b];
+          const float GR = Gt - GL;
+          const float HR = Ht - HL;
+          float gain = 0.0f;
+          int dir = 0;
+          if (HL >= mcw && HR >= mcw) {
+            gain = (GL * GL) / (HL + eps) + (GR * GR) / (HR + eps) - tot;
+            const float lv = GL / (HL + eps);
+            const float rv = GR / (HR + eps);
+            dir = lv > rv ? 1 : -1;
+          }
+          gs[k] += (double)gain;
+          ds[k] += dir;
+        }
+      }
+    }
+    const int64_t ncand = (int64_t)n_sel * nb;
+#pragma unroll
+    for (int k = 0; k < kDesChunk; ++k) {
+      const int b = b0 + k;
+      if (b < nb) {
+        const int64_t o = (int64_t)tn * ncand + (int64_t)l * nb + b;
+        crit[o] = (float)(gs[k] / (double)E);
+        const int a = ds[k] < 0 ? -ds[k] : ds[k];
+        agree[o] = a;
+        amax = a > amax ? a : amax;
+      }
+    }
+  }
+  atomic_max_grouped_i32(agree_max, tn, active, amax);
+}
+
+__global__ __launch_bounds__(256) void des_pick_kernel(
+    const float* __restrict__ crit, const int32_t* __restrict__ agree,
+    const int32_t* __restrict__ agree_max, const int32_t* __restrict__ present, int32_t n_tn,
+    int64_t ncand, float min_split_gain, unsigned long long* __restrict__ best) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int tn = 0;
+  bool ok = gid < (int64_t)n_tn * ncand;
+  unsigned long long key = 0ull;
+  if (ok) {
+    tn = (int)(gid / ncand);
+    const int cand = (int)(gid - (int64_t)tn * ncand);
+    const float cr = crit[gid];
+    ok = present[tn] && agree[gid] == agree_max[tn] && cr > min_split_gain;
+    if (ok)
+      key = ((unsigned long long)gain_key(cr) << 32) |
+            (unsigned long long)(0xffffffffu - (uint32_t)cand);
+  }
+  atomic_max_grouped_u64(best, tn, ok, key);
+}
+
+// one lane per (tree-node, era): split_l / split_b from the pick and the
+// chosen split's gain in every era (record gain [tn][E])
+__global__ void des_finish_kernel(const unsigned long long* __restrict__ best,
+                                  const int64_t* __restrict__ hq, const int32_t* __restrict__ hc,
+                                  int32_t F, int32_t B, int32_t E,
+                                  const int32_t* __restrict__ feat_sel, int32_t nodes_in_level,
+                                  int32_t n_tn, const int32_t* __restrict__ shifts, float mcw,
+                                  float eps, const float* __restrict__ staged, int32_t n_sel,
+                                  int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
+                                  float* __restrict__ split_gain_era) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)n_tn * E) return;
+  const int tn = (int)(gid / E);
+  const int e = (int)(gid - (int64_t)tn * E);
+  const unsigned long long k = best[tn];
+  if (k == 0ull) {
+    if (e == 0) {
       split_l[tn] = -1;
       split_b[tn] = -1;
     }
     return;
   }
   const int nb = B - 1;
-  const int64_t ncand = (int64_t)n_sel * nb;
-  const float* g0 = gain + (int64_t)tn * E * ncand;
-  const int8_t* d0 = dir + (int64_t)tn * E * ncand;
-  __shared__ int red_i[16];
-  __shared__ float red_g[16];
-  __shared__ int s_max_agree;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int idx = (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
+  const int l = idx / nb, bsel = idx - (idx / nb) * nb;
+  if (e == 0) {
+    split_l[tn] = l;
+    split_b[tn] = bsel;
+  }
+  if (staged) {
+    // staged per-era gains [tn][E][n_sel][B-1]
+    split_gain_era[gid] = staged[((int64_t)tn * E + e) * ((int64_t)n_sel * nb) + idx];
+    return;
+  }
+  const int s = shifts[tn / nodes_in_level];
+  const int64_t base = (((int64_t)tn * E + e) * F + feat_sel[l]) * B;
+  const int64_t* q = hq + base;
+  const int32_t* c = hc + base;
+  float g_sel = 0.0f;
+  scan_bins(
+      B, mcw, eps, [&](int b) { return wgbm_dequantise(q[b], s); },
+      [&](int b) { return (float)c[b]; },
+      [&](int b, float gn, float d) {
+        (void)d;
+        if (b == bsel) g_sel = gn;
+      });
+  split_gain_era[gid] = g_sel;
+}
 
-  // pass 1: max over all candidates of |sum_e dir|
-  int amax = 0;
-  for (int64_t c = threadIdx.x; c < ncand; c += blockDim.x) {
-    int ds = 0;
-    for (int e = 0; e < E; ++e) ds += d0[(int64_t)e * ncand + c];
-    ds = ds < 0 ? -ds : ds;
-    amax = ds > amax ? ds : amax;
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    const int y = __shfl_xor(amax, o, 64);
-    amax = y > amax ? y : amax;
-  }
-  if (lane == 0) red_i[w] = amax;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int m = 0;
-    for (int k = 0; k < nw; ++k) m = red_i[k] > m ? red_i[k] : m;
-    s_max_agree = m;
-  }
-  __syncthreads();
-  const int max_agree = s_max_agree;
+// ---------------------------------------------------------------------------
+// engine: E > 1 when every (node, era) segment fits one tile (<= 65536 rows):
+// per-era gains straight from an LDS histogram, without materialising the
+// per-era histograms.
+//   des_era: one workgroup per (tree-node, era, chunk of 64*V features) builds
+//     the segment's histogram in LDS (packed q * 2^18 + 1 words, lane-owned
+//     columns as in the tile histogram) and writes every candidate's gain and
+//     direction for that era: staged gain / dir [tn][E][n_sel][B-1].
+//   des_combine: crit / agree per candidate from the staged values, the era
+//     sum in double in era order (same values and order as des_accumulate).
+// ---------------------------------------------------------------------------
+constexpr int kDesEraThreads = 256;
+
+template <int V, int BT>
+__global__ __launch_bounds__(kDesEraThreads) void des_era_kernel(
+    const int8_t* __restrict__ codes, int64_t stride, int32_t F,
+    const float* __restrict__ resid, int64_t resid_tree_stride,
+    const int32_t* __restrict__ shifts, const int32_t* __restrict__ order,
+    const int64_t* __restrict__ seg, int32_t E, int32_t nodes_in_level,
+    const int32_t* __restrict__ present, const int32_t* __restrict__ local_of, int32_t n_sel,
+    int32_t num_bins_rt, float mcw, float eps, float* __restrict__ gain,
+    int8_t* __restrict__ dir) {
+  extern __shared__ unsigned long long lds[];
+  constexpr int CW = kHistSlots * V;
+  constexpr int nwaves = kDesEraThreads / 64;
+  const int B = BT > 0 ? BT : num_bins_rt;
+  const int Bp = B + 1;
+  const int nb = B - 1;
+  const int n_chunks = (F + CW - 1) / CW;
+  const int key = blockIdx.x / n_chunks;
+  const int chunk = blockIdx.x - key * n_chunks;
+  const int tn = key / E;
+  if (!present[tn]) return;  // uniform per workgroup
+  for (int i = threadIdx.x; i < V * Bp * kHistSlots; i += kDesEraThreads) lds[i] = 0ull;
   __syncthreads();
 
-  // pass 2: argmax of crit over candidates with agree == max and crit > msg
-  float bg = -__builtin_inff();
-  int bi = 0x7fffffff;
-  for (int64_t c = threadIdx.x; c < ncand; c += blockDim.x) {
-    int ds = 0;
-    for (int e = 0; e < E; ++e) ds += d0[(int64_t)e * ncand + c];
-    ds = ds < 0 ? -ds : ds;
-    if (ds != max_agree) continue;
+  const int64_t begin = seg[key];
+  const int n = (int)(seg[key + 1] - begin);  // <= 65536 (checked by the engine)
+  const int tree = tn / nodes_in_level;
+  const int s = shifts[tree];
+  const float* __restrict__ r_t = resid + (int64_t)tree * resid_tree_stride;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int f_base = chunk * CW + lane * V;
+  // lanes past the last feature read offset 0 of the row; their words are
+  // never evaluated (see the tile histogram)
+  const int voff = f_base < F ? f_base : 0;
+  unsigned long long* my = lds + lane;
+  auto add_row = [&](int row) {
+    const int64_t q = (int64_t)wgbm_quantise(r_t[row], s);
+    const unsigned long long w = (unsigned long long)(q * (int64_t)(1 << WGBM_CBITS) + 1);
+    const int8_t* src = codes + (int64_t)row * stride + voff;
+    uint32_t cw;
+    if constexpr (V == 4)
+      cw = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
+    else if constexpr (V == 2)
+      cw = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(src));
+    else
+      cw = __builtin_nontemporal_load(reinterpret_cast<const uint8_t*>(src));
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      uint32_t c = (cw >> (8 * j)) & 0xffu;
+      c = c < (uint32_t)B ? c : (uint32_t)B;  // out-of-range code -> trash bin
+      atomicAdd(my + (j * Bp + (int)c) * kHistSlots, w);
+    }
+  };
+  // four rows per wave and step (wave-uniform), loads issued together
+  int i = wave;
+  for (; i + 3 * nwaves < n; i += 4 * nwaves) {
+    int rows[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rows[u] = order[begin + i + u * nwaves];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) add_row(rows[u]);
+  }
+  for (; i < n; i += nwaves) add_row(order[begin + i]);
+  __syncthreads();
+
+  // candidates of this era: thread per feature of the chunk
+  for (int fs = threadIdx.x; fs < CW; fs += kDesEraThreads) {
+    const int f = chunk * CW + fs;
+    if (f >= F) continue;
+    const int l = local_of[f];
+    if (l < 0) continue;
+    const unsigned long long* col = lds + (fs % V) * Bp * kHistSlots + fs / V;
+    const int64_t out = ((int64_t)key * n_sel + l) * nb;
+    scan_bins(
+        B, mcw, eps,
+        [&](int b) { return wgbm_dequantise((int64_t)col[b * kHistSlots] >> WGBM_CBITS, s); },
+        [&](int b) { return (float)(int32_t)(col[b * kHistSlots] & (unsigned long long)WGBM_CMASK); },
+        [&](int b, float gn, float d) {
+          gain[out + b] = gn;
+          dir[out + b] = (int8_t)d;
+        });
+  }
+}
+
+__global__ __launch_bounds__(256) void des_combine_kernel(
+    const float* __restrict__ gain, const int8_t* __restrict__ dir, int32_t E, int32_t n_tn,
+    int64_t ncand, const int32_t* __restrict__ present, float* __restrict__ crit,
+    int32_t* __restrict__ agree, int32_t* __restrict__ agree_max) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int tn = 0;
+  bool active = gid < (int64_t)n_tn * ncand;
+  int a = 0;
+  if (active) {
+    tn = (int)(gid / ncand);
+    active = present[tn] != 0;
+  }
+  if (active) {
+    const int64_t c = gid - (int64_t)tn * ncand;
+    const float* g = gain + (int64_t)tn * E * ncand + c;
+    const int8_t* dd = dir + (int64_t)tn * E * ncand + c;
     double acc = 0.0;
-    for (int e = 0; e < E; ++e) acc += (double)g0[(int64_t)e * ncand + c];
-    const float crit = (float)(acc / (double)E);
-    if (crit > min_split_gain && better(crit, (int)c, bg, bi)) {
-      bg = crit;
-      bi = (int)c;
+    int ds = 0;
+    int e = 0;
+    for (; e + 4 <= E; e += 4) {
+      const float g0 = g[(int64_t)e * ncand], g1 = g[(int64_t)(e + 1) * ncand];
+      const float g2 = g[(int64_t)(e + 2) * ncand], g3 = g[(int64_t)(e + 3) * ncand];
+      ds += dd[(int64_t)e * ncand] + dd[(int64_t)(e + 1) * ncand] + dd[(int64_t)(e + 2) * ncand] +
+            dd[(int64_t)(e + 3) * ncand];
+      acc += (double)g0;  // sequential era order
+      acc += (double)g1;
+      acc += (double)g2;
+      acc += (double)g3;
     }
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    const float og = __shfl_xor(bg, o, 64);
-    const int oi = __shfl_xor(bi, o, 64);
-    if (better(og, oi, bg, bi)) {
-      bg = og;
-      bi = oi;
+    for (; e < E; ++e) {
+      acc += (double)g[(int64_t)e * ncand];
+      ds += dd[(int64_t)e * ncand];
     }
+    crit[gid] = (float)(acc / (double)E);
+    a = ds < 0 ? -ds : ds;
+    agree[gid] = a;
   }
-  if (lane == 0) {
-    red_g[w] = bg;
-    red_i[w] = bi;
+  atomic_max_grouped_i32(agree_max, tn, active, a);
+}
+
+// local index of every feature of the round's subset (local_of is -1 elsewhere)
+__global__ void local_scatter_kernel(const int32_t* __restrict__ feat_sel, int32_t n_sel,
+                                     int32_t F, int32_t* __restrict__ local_of) {
+  const int l = blockIdx.x * blockDim.x + threadIdx.x;
+  if (l < n_sel) {
+    const int f = feat_sel[l];
+    if (f >= 0 && f < F) local_of[f] = l;
   }
-  __syncthreads();
-  __shared__ int s_best;
-  if (threadIdx.x == 0) {
-    for (int k = 1; k < nw; ++k)
-      if (better(red_g[k], red_i[k], bg, bi)) {
-        bg = red_g[k];
-        bi = red_i[k];
-      }
-    s_best = bi;
-    if (bi == 0x7fffffff) {
-      split_l[tn] = -1;
-      split_b[tn] = -1;
-    } else {
-      split_l[tn] = bi / nb;
-      split_b[tn] = bi % nb;
-    }
-  }
-  __syncthreads();
-  const int best = s_best;
-  if (best != 0x7fffffff)
-    for (int e = threadIdx.x; e < E; e += blockDim.x)
-      split_gain_era[(int64_t)tn * E + e] = g0[(int64_t)e * ncand + best];
+}
+
+int launch_des_era(int V, int B, dim3 grid, hipStream_t st, const int8_t* codes, int64_t stride,
+                   int32_t F, const float* resid, int64_t resid_tree_stride, const int32_t* shifts,
+                   const int32_t* order, const int64_t* seg, int32_t E, int32_t nodes_in_level,
+                   const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
+                   float eps, float* gain, int8_t* dir) {
+  const size_t lds = (size_t)V * (B + 1) * kHistSlots * 8;
+#define WGBM_DES_ERA(VV, BB)                                                                   \
+  do {                                                                                         \
+    static bool attr = false;                                                                  \
+    if (!attr) {                                                                               \
+      WGBM_CHECK(hipFuncSetAttribute((const void*)des_era_kernel<VV, BB>,                       \
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024)); \
+      attr = true;                                                                             \
+    }                                                                                          \
+    hipLaunchKernelGGL((des_era_kernel<VV, BB>), grid, dim3(kDesEraThreads), lds, st, codes,   \
+                       stride, F, resid, resid_tree_stride, shifts, order, seg, E,             \
+                       nodes_in_level, present, local_of, n_sel, B, mcw, eps, gain, dir);      \
+    WGBM_LAUNCH_CHECK();                                                                       \
+    return 0;                                                                                  \
+  } while (0)
+  if (V == 4 && B == 5) WGBM_DES_ERA(4, 5);
+  if (V == 4) WGBM_DES_ERA(4, 0);
+  if (V == 2) WGBM_DES_ERA(2, 0);
+  if (V == 1) WGBM_DES_ERA(1, 0);
+#undef WGBM_DES_ERA
+  wgbm_set_error("launch_des_era: bad V=%d", V);
+  return WGBM_EINVAL;
 }
 
 }  // namespace wgbm
