@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 from warpgbm_amd import WarpGBM
-from warpgbm_amd.core import _dict_to_heap, _heap_to_dict, _preorder_internal
+from warpgbm_amd.core import _dict_to_heap, _heap_to_dict_lists, _preorder_heap
 
 
 @pytest.mark.parametrize("kw,exc", [
@@ -89,10 +89,22 @@ def test_heap_dict_round_trip_and_preorder():
     f, b, v = _dict_to_heap(tree, H)
     assert f.tolist() == [3, 1, -1, -1, -1, -1, -1]
     cnt = np.array([12, 5, 7, 2, 3, 0, 0])
-    back = _heap_to_dict(f, b, v, cnt)
+    back = _heap_to_dict_lists(f.tolist(), b.tolist(), v.tolist(), cnt.tolist())
     assert back == tree
-    assert _preorder_internal(np.array([3, 1, 2, -1, -1, -1, -1])) == [0, 1, 2]
-    assert _preorder_internal(np.array([0, -1, 4, -1, -1, 5, -1])) == [0, 2, 5]
+    assert _preorder_heap(7).tolist() == [0, 1, 3, 4, 2, 5, 6]
+
+    def internal(feat):
+        return [int(h) for h in _preorder_heap(len(feat)) if feat[h] >= 0]
+
+    assert internal([3, 1, 2, -1, -1, -1, -1]) == [0, 1, 2]
+    # engine records mark nodes below a leaf as absent (-2)
+    feat = [0, -1, 4, -2, -2, -1, -1]
+    assert internal(feat) == [0, 2]
+    assert _heap_to_dict_lists(feat, [2, 0, 1, 0, 0, 0, 0], [0.0, 1.0, 0.0, 0.0, 0.0, -3.5, 2.0],
+                               [9, 4, 5, 0, 0, 4, 1]) == {
+        "feature": 0, "bin": 2, "left": {"leaf_value": 1.0, "samples": 4},
+        "right": {"feature": 4, "bin": 1, "left": {"leaf_value": -3.5, "samples": 4},
+                  "right": {"leaf_value": 2.0, "samples": 1}}}
 
 
 def test_flatten_tree_matches_reference_layout():

@@ -525,15 +525,21 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         tree, internal nodes in depth-first pre-order, float32 adds
         (warpgbm/core.py:624-627)."""
         host = {k: v[:done].cpu().numpy() for k, v in rec.items()}
-        imp = self.per_era_feature_importance_
+        feat = host["feat"]  # [done, n_trees, H]
+        n_trees, H = feat.shape[1], feat.shape[2]
+        # importance: every internal node of every tree, trees in order and
+        # nodes in pre-order; np.add.at applies repeated indices one after the
+        # other, so the float32 adds happen in exactly that sequence
+        po = _preorder_heap(H)
+        fp = feat[:, :, po]
+        internal = fp >= 0
+        np.add.at(self.per_era_feature_importance_.T, fp[internal],
+                  host["gain"][:, :, po, :][internal])
+        fl, bl = feat.tolist(), host["bin"].tolist()
+        ll, cl = host["leaf"].tolist(), host["count"].tolist()
         for j in range(done):
-            trees = []
-            for t in range(host["feat"].shape[1]):
-                tree = _heap_to_dict(host["feat"][j, t], host["bin"][j, t], host["leaf"][j, t],
-                                     host["count"][j, t])
-                for h in _preorder_internal(host["feat"][j, t]):
-                    imp[:, host["feat"][j, t, h]] += host["gain"][j, t, h]
-                trees.append(tree)
+            trees = [_heap_to_dict_lists(fl[j][t], bl[j][t], ll[j][t], cl[j][t])
+                     for t in range(n_trees)]
             if classification:
                 self.forest.append(trees)
             else:
@@ -751,29 +757,32 @@ class WarpGBM(BaseEstimator, RegressorMixin):
 
 
 # ---------------------------------------------------------------------- tree helpers
-def _heap_to_dict(feat, bin_, leaf, count, h=0):
-    """Reference tree dict from heap arrays (feat -1 leaf, >= 0 split)."""
-    f = int(feat[h])
-    if f < 0:
-        return {"leaf_value": float(leaf[h]), "samples": int(count[h])}
-    return {
-        "feature": f,
-        "bin": int(bin_[h]),
-        "left": _heap_to_dict(feat, bin_, leaf, count, 2 * h + 1),
-        "right": _heap_to_dict(feat, bin_, leaf, count, 2 * h + 2),
-    }
+def _heap_to_dict_lists(feat, bin_, leaf, count):
+    """Reference tree dict from one heap record given as Python lists (feat
+    -1 leaf, -2 absent, >= 0 split; children of h at 2h+1 / 2h+2), built
+    bottom-up."""
+    H = len(feat)
+    nodes = [None] * H
+    for h in range(H - 1, -1, -1):
+        f = feat[h]
+        if f >= 0:
+            nodes[h] = {"feature": f, "bin": bin_[h], "left": nodes[2 * h + 1],
+                        "right": nodes[2 * h + 2]}
+        elif f == -1:
+            nodes[h] = {"leaf_value": leaf[h], "samples": count[h]}
+    return nodes[0]
 
 
-def _preorder_internal(feat):
-    """Heap indices of split nodes in depth-first pre-order (left first)."""
+def _preorder_heap(H):
+    """All heap indices < H in depth-first pre-order (left first)."""
     out, stack = [], [0]
     while stack:
         h = stack.pop()
-        if h < len(feat) and feat[h] >= 0:
+        if h < H:
             out.append(h)
             stack.append(2 * h + 2)
             stack.append(2 * h + 1)
-    return out
+    return np.asarray(out, dtype=np.int64)
 
 
 def _dict_to_heap(tree, H):

@@ -157,3 +157,69 @@ __host__ __device__ inline float wgbm_expf(float x) {
   p = fmaf(p, r, 1.0f);
   return ldexpf(p, (int)k);
 }
+
+// ---------------------------------------------------------------------------
+// workgroup scans (blockDim.x == 1024, 16 waves)
+// ---------------------------------------------------------------------------
+// exclusive scan of one value per thread; *total = sum over the workgroup
+__device__ inline int64_t wgbm_block_excl_scan(int64_t v, int64_t* wsum /*[16]*/,
+                                               int64_t* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int64_t x = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+  int64_t pre = 0, tot = 0;
+  for (int k = 0; k < 16; ++k) {
+    if (k < w) pre += wsum[k];
+    tot += wsum[k];
+  }
+  __syncthreads();
+  *total = tot;
+  return pre + x - v;
+}
+
+// Exclusive scan of n values get(i) by one workgroup, kScanK * 1024 values
+// per step: the step's values are read coalesced into LDS (buf, kScanK *
+// 1024 words), every thread scans kScanK consecutive ones, the thread totals
+// are scanned across the workgroup, and put(i, prefix) is written coalesced.
+// Returns the total.
+constexpr int kScanK = 4;
+template <typename Get, typename Put>
+__device__ inline int64_t wgbm_block_scan_tiled(int n, Get get, Put put, int64_t* wsum,
+                                                int64_t* buf) {
+  const int t = threadIdx.x;
+  constexpr int kStep = kScanK * 1024;
+  int64_t carry = 0;
+  for (int base = 0; base < n; base += kStep) {
+#pragma unroll
+    for (int j = 0; j < kScanK; ++j) {
+      const int i = base + j * 1024 + t;
+      buf[j * 1024 + t] = i < n ? get(i) : 0;
+    }
+    __syncthreads();
+    int64_t run = 0;
+#pragma unroll
+    for (int m = 0; m < kScanK; ++m) run += buf[t * kScanK + m];
+    int64_t tot;
+    int64_t ex = carry + wgbm_block_excl_scan(run, wsum, &tot);
+#pragma unroll
+    for (int m = 0; m < kScanK; ++m) {
+      const int64_t v = buf[t * kScanK + m];
+      buf[t * kScanK + m] = ex;
+      ex += v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kScanK; ++j) {
+      const int i = base + j * 1024 + t;
+      if (i < n) put(i, buf[j * 1024 + t]);
+    }
+    carry += tot;
+    __syncthreads();
+  }
+  return carry;
+}

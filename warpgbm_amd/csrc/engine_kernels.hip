@@ -252,26 +252,6 @@ __global__ __launch_bounds__(256) void partition_count_kernel(
   }
 }
 
-// block-wide exclusive scan helper (blockDim.x == 1024, 16 waves)
-__device__ inline int64_t block_excl_scan(int64_t v, int64_t* wsum /*[16]*/, int64_t* total) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int64_t x = v;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int64_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  if (lane == 63) wsum[w] = x;
-  __syncthreads();
-  int64_t pre = 0, tot = 0;
-  for (int k = 0; k < 16; ++k) {
-    if (k < w) pre += wsum[k];
-    tot += wsum[k];
-  }
-  __syncthreads();
-  *total = tot;
-  return pre + x - v;
-}
-
 // ---------------------------------------------------------------------------
 // partition, pass 2 (one workgroup of 1024): segment sizes of the next level,
 // their offsets, per-tile output bases, next-level presence and the list of
@@ -287,54 +267,42 @@ __global__ __launch_bounds__(1024) void partition_scan_kernel(
     int64_t* __restrict__ seg_next, int32_t* __restrict__ present_next,
     int32_t* __restrict__ key_list_next) {
   __shared__ int64_t wsum[16];
+  __shared__ int64_t sbuf[kScanK * 1024];
   const int n_keys = T * nodes * E;
   const int n_tiles = *n_tiles_dev;
   // phase 1: exclusive scan of the left counts over all tiles (tiles of a
   // segment are consecutive), kept in tile_lbase for now
-  int64_t carry = 0;
-  for (int base = 0; base < n_tiles; base += blockDim.x) {
-    const int t = base + threadIdx.x;
-    const int64_t v = t < n_tiles ? tile_left[t] : 0;
-    int64_t tot;
-    const int64_t ex = block_excl_scan(v, wsum, &tot);
-    if (t < n_tiles) tile_lbase[t] = carry + ex;
-    carry += tot;
-  }
+  const int64_t lefts = wgbm_block_scan_tiled(
+      n_tiles, [&](int t) { return (int64_t)tile_left[t]; },
+      [&](int t, int64_t v) { tile_lbase[t] = v; }, wsum, sbuf);
   __syncthreads();
   // lefts per segment: difference of the scan at its first tile and the next
   // segment's first tile
   for (int k = threadIdx.x; k < n_keys; k += blockDim.x) {
     const int t0 = key_tile_start[k], t1 = key_tile_start[k + 1];
-    const int64_t a = t0 < n_tiles ? tile_lbase[t0] : carry;
-    const int64_t b = t1 < n_tiles ? tile_lbase[t1] : carry;
+    const int64_t a = t0 < n_tiles ? tile_lbase[t0] : lefts;
+    const int64_t b = t1 < n_tiles ? tile_lbase[t1] : lefts;
     Lk[k] = t1 > t0 ? b - a : 0;
   }
   __syncthreads();
   // phase 2: exclusive scan of next-level segment sizes
   const int nodes2 = 2 * nodes;
   const int n_next = T * nodes2 * E;
-  carry = 0;
-  for (int base = 0; base < n_next; base += blockDim.x) {
-    const int k2 = base + threadIdx.x;
-    int64_t sz = 0;
-    if (k2 < n_next) {
-      const int e = k2 % E;
-      const int tc = k2 / E;
-      const int t = tc / nodes2;
-      const int c = tc - t * nodes2;
-      const int tn = t * nodes + (c >> 1);
-      if (split_l[tn] >= 0) {
+  const int64_t total_next = wgbm_block_scan_tiled(
+      n_next,
+      [&](int k2) -> int64_t {
+        const int e = k2 % E;
+        const int tc = k2 / E;
+        const int t = tc / nodes2;
+        const int c = tc - t * nodes2;
+        const int tn = t * nodes + (c >> 1);
+        if (split_l[tn] < 0) return 0;
         const int k = tn * E + e;
         const int64_t cnt = seg[k + 1] - seg[k];
-        sz = (c & 1) ? cnt - Lk[k] : Lk[k];
-      }
-    }
-    int64_t tot;
-    const int64_t ex = block_excl_scan(sz, wsum, &tot);
-    if (k2 < n_next) seg_next[k2] = carry + ex;
-    carry += tot;
-  }
-  if (threadIdx.x == 0) seg_next[n_next] = carry;
+        return (c & 1) ? cnt - Lk[k] : Lk[k];
+      },
+      [&](int k2, int64_t v) { seg_next[k2] = v; }, wsum, sbuf);
+  if (threadIdx.x == 0) seg_next[n_next] = total_next;
   __syncthreads();
   // phase 3: per-tile output bases (one thread per tile).  The left prefix
   // inside the segment is taken first (into tile_rbase) for every tile, since
@@ -357,27 +325,36 @@ __global__ __launch_bounds__(1024) void partition_scan_kernel(
     tile_lbase[tt] = seg_next[kl] + lpre;
     tile_rbase[tt] = seg_next[kr] + (before - lpre);
   }
-  // phase 4: presence and the histogram key list of the next level
-  for (int tn = threadIdx.x; tn < T * nodes; tn += blockDim.x) {
+  // phase 4: presence and the histogram key list of the next level; one wave
+  // per (tree, node), the eras spread over its lanes
+  const int lane = threadIdx.x & 63;
+  for (int tn = threadIdx.x >> 6; tn < T * nodes; tn += blockDim.x >> 6) {
     const bool sp = split_l[tn] >= 0;
     const int t = tn / nodes;
     const int node = tn - t * nodes;
-    present_next[t * nodes2 + 2 * node] = sp;
-    present_next[t * nodes2 + 2 * node + 1] = sp;
+    if (lane == 0) {
+      present_next[t * nodes2 + 2 * node] = sp;
+      present_next[t * nodes2 + 2 * node + 1] = sp;
+    }
     int64_t ls = 0, tot = 0;
     if (sp)
-      for (int e = 0; e < E; ++e) {
+      for (int e = lane; e < E; e += 64) {
         const int k = tn * E + e;
         ls += Lk[k];
         tot += seg[k + 1] - seg[k];
       }
+    for (int o = 32; o > 0; o >>= 1) {
+      ls += __shfl_xor(ls, o, 64);
+      tot += __shfl_xor(tot, o, 64);
+    }
     const int side = (ls <= tot - ls) ? 0 : 1;
-    for (int e = 0; e < E; ++e)
+    for (int e = lane; e < E; e += 64)
       key_list_next[tn * E + e] =
           sp ? (int32_t)(((int64_t)t * nodes2 + 2 * node + side) * E + e) : -1;
   }
 }
 
+// ---------------------------------------------------------------------------
 // partition, pass 3: stable scatter of the rows of split nodes
 __global__ __launch_bounds__(256) void partition_scatter_kernel(
     const Tile* __restrict__ tiles, const int32_t* __restrict__ n_tiles,

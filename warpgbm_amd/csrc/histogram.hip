@@ -400,65 +400,76 @@ __global__ void absmax_finish_kernel(const uint32_t* __restrict__ partial, int32
 // (nullptr => a single segment [0, total)).
 // --------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void plan_tiles_kernel(
-    const int64_t* __restrict__ seg, int64_t total, int32_t n_keys,
+    const int64_t* __restrict__ seg, int64_t total_rows, int32_t n_keys,
     const int32_t* __restrict__ key_list, int32_t tile_rows,
     int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
     int32_t* __restrict__ n_tiles) {
-  __shared__ int32_t wsum[16];
-  __shared__ int32_t carry;
+  __shared__ int64_t wsum[16];
+  __shared__ int64_t sbuf[kScanK * 1024];
   const int nk = n_keys;  // entries of key_list (or keys 0..n_keys-1)
-  if (threadIdx.x == 0) carry = 0;
-  __syncthreads();
+  auto bounds = [&](int i, int& key, int64_t& b0, int64_t& b1) {
+    key = key_list ? key_list[i] : i;
+    b0 = (key >= 0 && seg) ? seg[key] : 0;
+    b1 = key < 0 ? 0 : (seg ? seg[key + 1] : total_rows);
+  };
   // phase 1: exclusive scan of the tile counts -> key_tile_start
-  for (int base = 0; base < nk; base += blockDim.x) {
-    const int i = base + threadIdx.x;
-    int nt = 0;
-    if (i < nk) {
-      const int key = key_list ? key_list[i] : i;
-      if (key >= 0) {
-        const int64_t b0 = seg ? seg[key] : 0;
-        const int64_t b1 = seg ? seg[key + 1] : total;
-        nt = (int)((b1 - b0 + tile_rows - 1) / tile_rows);
-      }
-    }
-    int x = nt;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(x, o, 64);
-      if (lane >= o) x += y;
-    }
-    if (lane == 63) wsum[w] = x;
-    __syncthreads();
-    int wpre = 0;
-    for (int k = 0; k < w; ++k) wpre += wsum[k];
-    const int excl = carry + wpre + x - nt;
-    if (i < nk) key_tile_start[i] = excl;
-    __syncthreads();
-    if (threadIdx.x == blockDim.x - 1) carry = excl + nt;
-    __syncthreads();
-  }
-  const int ntot = carry < max_tiles ? carry : max_tiles;
+  const int64_t total = wgbm_block_scan_tiled(
+      nk,
+      [&](int i) -> int64_t {
+        int key;
+        int64_t b0, b1;
+        bounds(i, key, b0, b1);
+        return key < 0 ? 0 : (b1 - b0 + tile_rows - 1) / tile_rows;
+      },
+      [&](int i, int64_t v) { key_tile_start[i] = (int32_t)v; }, wsum, sbuf);
+  const int ntot = total < max_tiles ? (int)total : max_tiles;
   if (threadIdx.x == 0) {
-    key_tile_start[nk] = carry;
+    key_tile_start[nk] = (int32_t)total;
     *n_tiles = ntot;
   }
   __syncthreads();
-  // phase 2: every tile finds its entry (last i with key_tile_start[i] <= id)
-  for (int id = threadIdx.x; id < ntot; id += blockDim.x) {
-    int lo = 0, hi = nk - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (key_tile_start[mid] <= id) lo = mid; else hi = mid - 1;
-    }
-    const int key = key_list ? key_list[lo] : lo;
-    const int64_t b0 = seg ? seg[key] : 0;
-    const int64_t b1 = seg ? seg[key + 1] : total;
+  // phase 2: every entry writes its own tiles (ids below the tile limit);
+  // entries with many tiles are written by the whole workgroup afterwards
+  constexpr int kMaxBig = 256, kSmall = 8;
+  __shared__ int big[kMaxBig];
+  __shared__ int n_big;
+  if (threadIdx.x == 0) n_big = 0;
+  __syncthreads();
+  auto write_tile = [&](int key, int64_t b0, int64_t b1, int first, int j) {
     Tile tl;
     tl.key = key;
     tl.pad = 0;
-    tl.begin = b0 + (int64_t)(id - key_tile_start[lo]) * tile_rows;
+    tl.begin = b0 + (int64_t)j * tile_rows;
     tl.end = tl.begin + tile_rows < b1 ? tl.begin + tile_rows : b1;
-    tiles[id] = tl;
+    tiles[first + j] = tl;
+  };
+  for (int i = threadIdx.x; i < nk; i += blockDim.x) {
+    int key;
+    int64_t b0, b1;
+    bounds(i, key, b0, b1);
+    if (key < 0) continue;
+    const int first = key_tile_start[i];
+    const int nt = key_tile_start[i + 1] - first;
+    if (nt > kSmall) {
+      const int slot = atomicAdd(&n_big, 1);
+      if (slot < kMaxBig) {
+        big[slot] = i;
+        continue;
+      }
+    }
+    for (int j = 0; j < nt && first + j < ntot; ++j) write_tile(key, b0, b1, first, j);
+  }
+  __syncthreads();
+  const int nb = n_big < kMaxBig ? n_big : kMaxBig;
+  for (int k = 0; k < nb; ++k) {
+    const int i = big[k];
+    int key;
+    int64_t b0, b1;
+    bounds(i, key, b0, b1);
+    const int first = key_tile_start[i];
+    const int nt = key_tile_start[i + 1] - first;
+    for (int j = threadIdx.x; j < nt && first + j < ntot; j += blockDim.x)
+      write_tile(key, b0, b1, first, j);
   }
 }
 
