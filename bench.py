@@ -22,6 +22,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import platform
@@ -171,6 +172,12 @@ def main():
     torch.cuda.synchronize()
     assert torch.all(H1.sum(dim=2) == N), "root histogram counts are wrong"
     assert torch.equal(H16.sum(dim=0), H1[0]), "16-node counts do not add up to the root"
+    # ceiling of the kernel's LDS stage: 64-bit LDS atomic adds per second in
+    # the same LDS layout with no global traffic (measured live)
+    lds_peak = C.c_double(0.0)
+    _lib.check(lib.wgbm_probe_lds_atomics(512, 500, C.byref(lds_peak), stream), "lds probe")
+    lds_peak = lds_peak.value
+    print(f"[bench] LDS atomic probe: {lds_peak:.3e} 64-bit adds/s", file=sys.stderr, flush=True)
     lib.wgbm_timer_reset()
     lib.wgbm_timer_enable(1)
     e0 = torch.cuda.Event(enable_timing=True)
@@ -266,8 +273,14 @@ def main():
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(k_achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(k_achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "hist_tiles_kernel<16,0,32>",
-                     "kernel_ms": round(k_ms, 4)},
+                     "traffic": traffic, "kernel": "hist_tiles_kernel<4,0,32,*>",
+                     "kernel_ms": round(k_ms, 4),
+                     # the binding unit in practice: one 64-bit LDS atomic per
+                     # (row, feature); peak = wgbm_probe_lds_atomics, measured
+                     # above on this GPU
+                     "lds_atomics": {"updates": N * F, "achieved_per_s": round(N * F / (k_ms * 1e-3)),
+                                     "peak_per_s": round(lds_peak),
+                                     "frac": round(N * F / (k_ms * 1e-3) / lds_peak, 4)}},
         "cpu_baseline": cpu,
     }
     out.update(e2e)

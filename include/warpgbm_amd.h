@@ -195,6 +195,10 @@ void wgbm_engine_destroy(wgbm_engine* eng);
 void wgbm_timer_enable(int32_t on);
 int wgbm_timer_read(const char* tag, double* total_ms, int64_t* count);
 void wgbm_timer_reset(void);
+/* Rate of 64-bit LDS atomic adds (per second, whole GPU) in the tile
+ * histogram's LDS layout with synthetic bins and no global traffic: the
+ * ceiling of the histogram kernel's LDS stage.  Synchronises `stream`. */
+int wgbm_probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, void* stream);
 /* Free the library's scratch buffers (all devices / streams). */
 void wgbm_release_scratch(void);
 

@@ -14,6 +14,7 @@ import torch
 
 from oracle import clib, ops
 from tests.conftest import print_case
+from warpgbm_amd import _lib
 from warpgbm_amd import device as D
 from warpgbm_amd import node_kernel
 
@@ -281,3 +282,15 @@ def test_staged_upload_exact(gpu):
     assert torch.equal(Xd.cpu(), torch.from_numpy(X.astype(np.float32)))
     X32 = rng.standard_normal((250_000, 300), dtype=np.float32)
     assert torch.equal(D.upload_float(X32, dev).cpu(), torch.from_numpy(X32))
+
+
+def test_lds_atomic_probe(gpu):
+    """The instrumentation probe runs and reports a plausible whole-GPU rate
+    of 64-bit LDS atomic adds (between 1e11 and 1e14 per second)."""
+    import ctypes
+
+    print_case("probe", "lds atomics")
+    rate = ctypes.c_double(0.0)
+    _lib.check(gpu.wgbm_probe_lds_atomics(64, 50, ctypes.byref(rate), _lib.current_stream_ptr()),
+               "probe")
+    assert 1e11 < rate.value < 1e14

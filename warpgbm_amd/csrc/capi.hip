@@ -15,6 +15,12 @@ static inline unsigned nblocks(int64_t n, int bs) { return (unsigned)((n + bs - 
 
 extern "C" {
 
+int wgbm_probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, void* stream) {
+  WGBM_REQUIRE(blocks >= 1 && blocks <= (1 << 16) && iters >= 1 && ops_per_s,
+               "probe_lds_atomics: bad arguments");
+  return probe_lds_atomics(blocks, iters, ops_per_s, S(stream));
+}
+
 const char* wgbm_version(void) { return "warpgbm_amd 0.1.0 (gfx950)"; }
 const char* wgbm_last_error(void) { return wgbm_last_error_impl(); }
 

@@ -73,11 +73,14 @@ void hist_tiles_kernel(
   const int s = shifts[tree];
   const int32_t* __restrict__ ord = GATHER ? order + tl.begin : nullptr;
   const int n = (int)(tl.end - tl.begin);  // a tile has at most 65536 rows
-  // A lane past the last feature reads bytes of its row all the same (offset
-  // 0) and adds them to its own words, which belong to no feature and are
-  // never read back; the clamp below keeps every address inside the lane's
-  // column (padding bytes and other out-of-range codes go to the trash bin B).
-  const int voff = f_base < n_feats ? f_base : 0;
+  // A lane past the last feature adds whatever it reads to its own words,
+  // which belong to no feature and are never read back; the clamp below keeps
+  // every address inside the lane's column (padding bytes and other
+  // out-of-range codes go to the trash bin B).  It reads nothing new: an
+  // out-of-range buffer offset (returns zeros without a memory access), or
+  // the last real feature's offset, whose line the wave fetches anyway.
+  const int vlast = (n_feats - 1) / V * V;
+  const int voff = f_base < n_feats ? f_base : (MODE == kLoadBuffer ? 0x7fffffff : vlast);
   const int n_valid_bytes = f_base < n_feats ? (n_feats - f_base < V ? n_feats - f_base : V) : 0;
   const uint32_t rs_bytes = (MODE == kLoadBuffer) ? (uint32_t)(n_rows * stride) : 0u;
   const __amdgpu_buffer_rsrc_t rs = wgbm_rsrc(codes, rs_bytes);
@@ -509,6 +512,63 @@ __global__ void era_scatter_kernel(const int32_t* __restrict__ rows, int64_t n,
     const int e = era[r];
     if (e >= 0 && e < num_eras) out[atomicAdd(&cursor[e], 1ull)] = r;
   }
+}
+
+// --------------------------------------------------------------------------
+// instrumentation: the LDS atomic rate of the tile histogram's layout alone.
+// Same LDS words as hist_tiles_kernel<4, *, 32> (4 features per lane, 33 bins,
+// 64 lane-owned columns) and the same packed 64-bit adds; every lane cycles
+// through 16 precomputed (feature, bin) words, so the loop is the atomics
+// alone (no global traffic, no address arithmetic).
+// --------------------------------------------------------------------------
+__global__ __launch_bounds__(kHistThreads) void lds_atomic_probe_kernel(
+    int32_t iters, unsigned long long* __restrict__ sink) {
+  extern __shared__ unsigned long long lds[];
+  constexpr int V = 4, Bp = 33;
+  for (int i = threadIdx.x; i < V * Bp * kHistSlots; i += kHistThreads) lds[i] = 0ull;
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  uint32_t h = threadIdx.x * 2654435761u + blockIdx.x * 97u + 1u;
+  unsigned long long* addr[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    h ^= h << 13;
+    h ^= h >> 17;
+    h ^= h << 5;
+    addr[k] = lds + lane + ((k & 3) * Bp + (int)(h & 31u)) * kHistSlots;
+  }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) atomicAdd(addr[k], (unsigned long long)(2 * it + 1));
+  }
+  __syncthreads();
+  // keep the result observable
+  if (threadIdx.x < 64) sink[blockIdx.x * 64 + threadIdx.x] = lds[threadIdx.x];
+}
+
+int probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, hipStream_t st) {
+  const size_t lds = (size_t)4 * 33 * kHistSlots * 8;
+  WGBM_CHECK(hipFuncSetAttribute((const void*)lds_atomic_probe_kernel,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  unsigned long long* sink = (unsigned long long*)scratch_get(st, sizeof(unsigned long long) * 64 * (size_t)blocks, 9);
+  WGBM_REQUIRE(sink, "scratch allocation failed");
+  hipEvent_t a, b;
+  WGBM_CHECK(hipEventCreate(&a));
+  WGBM_CHECK(hipEventCreate(&b));
+  // one untimed launch, then the timed one
+  hipLaunchKernelGGL(lds_atomic_probe_kernel, dim3(blocks), dim3(kHistThreads), lds, st, iters, sink);
+  WGBM_LAUNCH_CHECK();
+  WGBM_CHECK(hipEventRecord(a, st));
+  hipLaunchKernelGGL(lds_atomic_probe_kernel, dim3(blocks), dim3(kHistThreads), lds, st, iters, sink);
+  WGBM_LAUNCH_CHECK();
+  WGBM_CHECK(hipEventRecord(b, st));
+  WGBM_CHECK(hipEventSynchronize(b));
+  float ms = 0.0f;
+  WGBM_CHECK(hipEventElapsedTime(&ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  *ops_per_s = (double)blocks * kHistThreads * iters * 16 / (ms * 1e-3);
+  return 0;
 }
 
 // --------------------------------------------------------------------------

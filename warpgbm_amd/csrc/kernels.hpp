@@ -49,6 +49,7 @@ int hist_pick_v(int num_bins);
 size_t hist_lds_bytes(int V, int num_bins);
 int hist_load_mode(int64_t n_rows, int64_t stride, int V);
 int launch_hist_tiles(const HistLaunch& a, hipStream_t st);
+int probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, hipStream_t st);
 
 // kernels launched directly from other translation units
 __global__ void hist_finalize_f32_kernel(const unsigned long long* part,

@@ -408,9 +408,9 @@ __global__ __launch_bounds__(kDesEraThreads) void des_era_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int f_base = chunk * CW + lane * V;
-  // lanes past the last feature read offset 0 of the row; their words are
-  // never evaluated (see the tile histogram)
-  const int voff = f_base < F ? f_base : 0;
+  // lanes past the last feature re-read the last real feature's bytes (a line
+  // the wave fetches anyway); their words are never evaluated
+  const int voff = f_base < F ? f_base : (F - 1) / V * V;
   unsigned long long* my = lds + lane;
   auto add_row = [&](int row) {
     const int64_t q = (int64_t)wgbm_quantise(r_t[row], s);
