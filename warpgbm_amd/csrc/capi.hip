@@ -47,9 +47,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   hipLaunchKernelGGL(absmax_partial_kernel, dim3(n_abs), dim3(256), 0, st, resid, rows, n_pos,
                      abs_part);
   WGBM_LAUNCH_CHECK();
-  hipLaunchKernelGGL(absmax_finish_kernel, dim3(1), dim3(256), 0, st, abs_part, n_abs,
-                     wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1)), absmax, shift);
-  WGBM_LAUNCH_CHECK();
+  // (the per-block maxima are reduced to the shift by the tile planner below)
 
   // segments: explicit (seg_dev), by era (sort rows by era), or a single one
   const int32_t* order = rows;
@@ -94,7 +92,9 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
       (unsigned long long*)scratch_get(st, sizeof(unsigned long long) * words, 5);
   WGBM_REQUIRE(tiles && kts && part, "scratch allocation failed (%lld words)", (long long)words);
   hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, seg, n_pos, n_keys,
-                     (const int32_t*)nullptr, (int32_t)R, (int32_t)max_tiles, tiles, kts, n_tiles);
+                     (const int32_t*)nullptr, (int32_t)R, (int32_t)max_tiles, tiles, kts, n_tiles,
+                     abs_part, n_abs, wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1)), absmax,
+                     shift);
   WGBM_LAUNCH_CHECK();
   HistLaunch a;
   a.codes = codes;
@@ -117,23 +117,22 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   int r = launch_hist_tiles(a, st);
   timer_end(tm, st);
   if (r) return r;
-  const unsigned fin_wg = (unsigned)(n_keys * ((tile_words + 31) / 32));
+  // tiles per segment (finalize's tile split): the planner's estimate
+  const int64_t tiles_per_key = std::max<int64_t>(1, (n_pos + R - 1) / R / std::max(n_keys, 1));
   if (!feat_idx) {
     // identity feature map: finalize straight into the (accumulated) outputs
-    hipLaunchKernelGGL(hist_finalize_f32_kernel, dim3(fin_wg), dim3(256), 0, st, part,
-                       kts, n_keys, n_chunks, V, num_bins, n_hist_feats, shift, absmax, n_tiles,
-                       1, G, H);
-    WGBM_LAUNCH_CHECK();
+    r = launch_finalize_f32(tiles_per_key, part, kts, n_keys, n_chunks, V, num_bins, n_hist_feats,
+                            shift, absmax, n_tiles, 1, G, H, st);
+    if (r) return r;
   } else {
     // full-width histogram in scratch, then the requested features
     const int64_t full = (int64_t)n_keys * n_hist_feats * num_bins;
     float* Gf = (float*)scratch_get(st, sizeof(float) * 2 * full, 7);
     WGBM_REQUIRE(Gf, "scratch allocation failed");
     float* Hf = Gf + full;
-    hipLaunchKernelGGL(hist_finalize_f32_kernel, dim3(fin_wg), dim3(256), 0, st, part,
-                       kts, n_keys, n_chunks, V, num_bins, n_hist_feats, shift, absmax, n_tiles,
-                       0, Gf, Hf);
-    WGBM_LAUNCH_CHECK();
+    r = launch_finalize_f32(tiles_per_key, part, kts, n_keys, n_chunks, V, num_bins, n_hist_feats,
+                            shift, absmax, n_tiles, 0, Gf, Hf, st);
+    if (r) return r;
     const int64_t nout = (int64_t)n_keys * n_out_feats * num_bins;
     hipLaunchKernelGGL(hist_gather_features_kernel, dim3(nblocks(nout, 256)), dim3(256), 0, st, Gf,
                        Hf, n_keys, n_hist_feats, num_bins, feat_idx, n_out_feats, G, H);

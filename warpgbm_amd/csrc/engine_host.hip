@@ -264,7 +264,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     return WGBM_EINVAL;
   hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[0], (int64_t)0, T * E,
                      (const int32_t*)nullptr, e->part_tile_rows, (int32_t)e->max_ptiles, e->ptiles,
-                     e->pkts, e->pn);
+                     e->pkts, e->pn, (const uint32_t*)nullptr, 0, 0, (uint32_t*)nullptr,
+                     (int32_t*)nullptr);
   WGBM_LAUNCH_CHECK();
   hipLaunchKernelGGL(segment_totals_kernel, dim3((unsigned)e->max_ptiles), dim3(256), 0, st,
                      e->ptiles, e->pn, e->order[0], e->resid, N, e->shifts, E, e->totq[0],
@@ -336,7 +337,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         e->max_htiles = max_tiles;
       }
       hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur], (int64_t)0,
-                         n_list, list, (int32_t)R, (int32_t)max_tiles, e->htiles, e->hkts, e->hn);
+                         n_list, list, (int32_t)R, (int32_t)max_tiles, e->htiles, e->hkts, e->hn,
+                         (const uint32_t*)nullptr, 0, 0, (uint32_t*)nullptr, (int32_t*)nullptr);
       WGBM_LAUNCH_CHECK();
       HistLaunch a;
       a.codes = c.codes_rm;
@@ -359,12 +361,11 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       r = launch_hist_tiles(a, st);
       timer_end(tm, st);
       if (r) return r;
-      const int64_t tile_words = (int64_t)e->n_chunks * kHistSlots * e->V * B;
-      const unsigned fin_wg = (unsigned)(n_list * ((tile_words + 31) / 32));
-      hipLaunchKernelGGL(hist_finalize_level_kernel, dim3(fin_wg), dim3(256), 0, st,
-                         e->part, e->hkts, list, n_list, e->n_chunks, e->V, B, F, E,
-                         nodes, d, e->hq[hprev], e->hc[hprev], e->hn, e->hq[hcur], e->hc[hcur]);
-      WGBM_LAUNCH_CHECK();
+      const int64_t tiles_per_key = std::max<int64_t>(1, rows_bound / R / std::max(n_list, 1));
+      r = launch_finalize_level(tiles_per_key, e->part, e->hkts, list, n_list, e->n_chunks, e->V,
+                                B, F, E, nodes, d, e->hq[hprev], e->hc[hprev], e->hn, e->hq[hcur],
+                                e->hc[hcur], st);
+      if (r) return r;
       // ---- split search + DES selection
       if (E == 1) {
         if (fill_u64(e->best, n_tn, 0ull, st)) return WGBM_EINVAL;
@@ -412,7 +413,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     const int nxt = cur ^ 1;
     hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur], (int64_t)0,
                        n_keys, (const int32_t*)nullptr, e->part_tile_rows, (int32_t)e->max_ptiles,
-                       e->ptiles, e->pkts, e->pn);
+                       e->ptiles, e->pkts, e->pn, (const uint32_t*)nullptr, 0, 0,
+                       (uint32_t*)nullptr, (int32_t*)nullptr);
     WGBM_LAUNCH_CHECK();
     if (d < D) {
       if (fill_u64(e->totq[nxt], (int64_t)n_keys * 2, 0, st) ||

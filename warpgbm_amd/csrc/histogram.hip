@@ -70,7 +70,12 @@ void hist_tiles_kernel(
   const int f_base = chunk * CW + lane * V;
   const int tree = tl.key / keys_per_tree;
   const float* __restrict__ r_t = resid + (int64_t)tree * resid_tree_stride;
-  const int s = shifts[tree];
+  // Shifts lie in [0, 177]; clamping consumes the loaded value here, so the
+  // wait for the (scalar) load happens once before the loop rather than at
+  // the top of every iteration, where it would also drain the wave's
+  // outstanding LDS atomics (both share one counter).
+  const int s_raw = shifts[tree];
+  const int s = s_raw < 0 ? 0 : (s_raw > 255 ? 255 : s_raw);
   const int32_t* __restrict__ ord = GATHER ? order + tl.begin : nullptr;
   const int n = (int)(tl.end - tl.begin);  // a tile has at most 65536 rows
   // A lane past the last feature adds whatever it reads to its own words,
@@ -95,32 +100,32 @@ void hist_tiles_kernel(
   constexpr int U = 8;
   constexpr int step = nwaves * U;
   struct Group {
-    uint32_t c[U];
-    float r[U];
+    uint32_t c[U];  // codes of rows 0..U-1 of the group (all lanes)
+    float r;        // lane u < U: residual of row u
   };
   Group ga, gb;
   const int row0 = (int)tl.begin;  // row ids fit 31 bits (checked by the launcher)
+  const int ul = lane & (U - 1);
+  // GATHER: lane u < U holds order[i0 + u] of the next group to issue; read
+  // one issue ahead so that turning it into scalar row ids never waits
+  int32_t ids = 0;
+  auto load_ids = [&](int i0) {
+    if constexpr (GATHER) {
+      const int iu = i0 + ul < n ? i0 + ul : n - 1;
+      ids = ord[iu];
+    }
+  };
   auto issue = [&](Group& g, int i0) {
     int rows[U];
-    if (GATHER) {
-      if (i0 + U <= n) {
-        // full group: the U row ids are one contiguous (scalar) read of order
-        int32_t ids[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) ids[u] = ord[i0 + u];
-#pragma unroll
-        for (int u = 0; u < U; ++u) rows[u] = ids[u];
-      } else {
-#pragma unroll
-        for (int u = 0; u < U; ++u) rows[u] = ord[i0 + u < n ? i0 + u : n - 1];
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < U; ++u) rows[u] = row0 + (i0 + u < n ? i0 + u : n - 1);
-    }
+    for (int u = 0; u < U; ++u)
+      rows[u] = GATHER ? __builtin_amdgcn_readlane(ids, u) : row0 + (i0 + u < n ? i0 + u : n - 1);
+    // residuals: one vector load per group (lane u < U reads row u's)
+    const int my_row = GATHER ? ids : row0 + (i0 + ul < n ? i0 + ul : n - 1);
+    g.r = r_t[my_row];
+    if constexpr (GATHER) load_ids(i0 + step);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      g.r[u] = r_t[rows[u]];
       if (MODE == kLoadBuffer) {
         const int so = rows[u] * (int)stride;  // n_rows * stride < 2^31 in this mode
         if constexpr (V == 4)
@@ -153,11 +158,17 @@ void hist_tiles_kernel(
   // branch-free: positions past the tile end add the word 0 (no sum, no
   // count), selected with a wave-uniform condition where the word is used
   auto add = [&](const Group& g, int i0) {
+    // the group's packed words, quantised once (lane u < U: row u) and
+    // broadcast row by row
+    const int64_t qv = (int64_t)wgbm_quantise(g.r, s);
+    const uint64_t pv = (uint64_t)(qv * (int64_t)(1 << WGBM_CBITS) + 1);
+    const uint32_t plo = (uint32_t)pv, phi = (uint32_t)(pv >> 32);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t q = (int64_t)wgbm_quantise(g.r[u], s);
-      const unsigned long long w =
-          i0 + u < n ? (unsigned long long)(q * (int64_t)(1 << WGBM_CBITS) + 1) : 0ull;
+      // readlane returns int: widen through uint32_t (no sign extension)
+      const uint64_t wu = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(phi, u) << 32) |
+                          (uint64_t)(uint32_t)__builtin_amdgcn_readlane(plo, u);
+      const unsigned long long w = i0 + u < n ? (unsigned long long)wu : 0ull;
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         uint32_t c = (g.c[u] >> (8 * j)) & 0xffu;
@@ -172,6 +183,7 @@ void hist_tiles_kernel(
   };
   int i = wave * U;
   if (i < n) {
+    load_ids(i);
     issue(ga, i);
     // steady state without conditional loads, so that every add waits for
     // exactly its own group (the other group's loads stay in flight)
@@ -231,20 +243,22 @@ __device__ inline void part_feature_bin(int64_t i, int V, int num_bins, int& f, 
 // Threads walk the partials in their memory order, so reads are coalesced.
 // accumulate = 0 overwrites (scratch output), 1 adds (reference semantics).
 // --------------------------------------------------------------------------
-// A workgroup of 256 threads covers 32 consecutive partial words of one
-// segment; its 8 thread groups each sum every 8th tile and the groups are
-// combined in LDS (integer sums, so the split does not change the result).
-constexpr int kFinWords = 32, kFinSplit = 8;
-
+// A workgroup of 256 threads covers FW consecutive partial words of one
+// segment; its 256/FW thread groups each sum every (256/FW)-th tile and the
+// groups are combined in LDS (integer sums, so the split does not change the
+// result).  Few tiles per segment -> wide FW (long coalesced runs, few
+// workgroups); many tiles -> narrow FW (more parallel tile reads).
+template <int FW>
 __device__ inline void finalize_sum(const unsigned long long* __restrict__ part, int64_t tile_words,
                                     int64_t i, bool ok, int t0, int t1, int64_t& Q, int64_t& C) {
-  __shared__ int64_t sq[kFinSplit][kFinWords];
-  __shared__ int64_t sc[kFinSplit][kFinWords];
-  const int w = threadIdx.x % kFinWords;
-  const int g = threadIdx.x / kFinWords;
+  constexpr int SPLIT = 256 / FW;
+  __shared__ int64_t sq[SPLIT][FW];
+  __shared__ int64_t sc[SPLIT][FW];
+  const int w = threadIdx.x % FW;
+  const int g = threadIdx.x / FW;
   int64_t q = 0, c = 0;
   if (ok)
-    for (int t = t0 + g; t < t1; t += kFinSplit) {
+    for (int t = t0 + g; t < t1; t += SPLIT) {
       int64_t a, b;
       unpack_word(part[(int64_t)t * tile_words + i], a, b);
       q += a;
@@ -255,12 +269,13 @@ __device__ inline void finalize_sum(const unsigned long long* __restrict__ part,
   __syncthreads();
   Q = 0;
   C = 0;
-  for (int k = 0; k < kFinSplit; ++k) {
+  for (int k = 0; k < SPLIT; ++k) {
     Q += sq[k][w];
     C += sc[k][w];
   }
 }
 
+template <int FW>
 __global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
     const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
     int32_t n_keys, int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
@@ -268,9 +283,9 @@ __global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
     const int32_t* __restrict__ n_tiles, int32_t accumulate, float* __restrict__ G,
     float* __restrict__ H) {
   const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
-  const int64_t wpk = (tile_words + kFinWords - 1) / kFinWords;  // workgroups per segment
+  const int64_t wpk = (tile_words + FW - 1) / FW;  // workgroups per segment
   const int k = (int)(blockIdx.x / wpk);
-  const int64_t i = (blockIdx.x - (int64_t)k * wpk) * kFinWords + threadIdx.x % kFinWords;
+  const int64_t i = (blockIdx.x - (int64_t)k * wpk) * FW + threadIdx.x % FW;
   const bool ok = k < n_keys && i < tile_words;
   int t0 = 0, t1 = 0;
   if (k < n_keys) {
@@ -278,8 +293,8 @@ __global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
     t1 = key_tile_start[k + 1] < *n_tiles ? key_tile_start[k + 1] : *n_tiles;
   }
   int64_t Q, C;
-  finalize_sum(part, tile_words, i, ok, t0, t1, Q, C);
-  if (!ok || threadIdx.x >= kFinWords) return;
+  finalize_sum<FW>(part, tile_words, i, ok, t0, t1, Q, C);
+  if (!ok || threadIdx.x >= FW) return;
   int f, b;
   part_feature_bin(i, V, num_bins, f, b);
   if (f >= n_feats) return;
@@ -319,6 +334,7 @@ __global__ void hist_gather_features_kernel(const float* __restrict__ Gf,
 //   computed key k = (tree, node, era) with node = 2*parent + side
 //   hq/hc layout: [tree][node][era][F][B]
 // --------------------------------------------------------------------------
+template <int FW>
 __global__ __launch_bounds__(256) void hist_finalize_level_kernel(
     const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
     const int32_t* __restrict__ key_list, int32_t n_list, int32_t n_chunks, int32_t V,
@@ -326,18 +342,18 @@ __global__ __launch_bounds__(256) void hist_finalize_level_kernel(
     const int64_t* __restrict__ parent_q, const int32_t* __restrict__ parent_c,
     const int32_t* __restrict__ n_tiles, int64_t* __restrict__ hq, int32_t* __restrict__ hc) {
   const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
-  const int64_t wpk = (tile_words + kFinWords - 1) / kFinWords;
+  const int64_t wpk = (tile_words + FW - 1) / FW;
   const int kk = (int)(blockIdx.x / wpk);
   if (kk >= n_list) return;  // uniform per workgroup
   const int key = key_list ? key_list[kk] : kk;
   if (key < 0) return;  // uniform per workgroup
-  const int64_t i = (blockIdx.x - (int64_t)kk * wpk) * kFinWords + threadIdx.x % kFinWords;
+  const int64_t i = (blockIdx.x - (int64_t)kk * wpk) * FW + threadIdx.x % FW;
   const bool ok = i < tile_words;
   const int t0 = key_tile_start[kk];
   const int t1 = key_tile_start[kk + 1] < *n_tiles ? key_tile_start[kk + 1] : *n_tiles;
   int64_t Q, C;
-  finalize_sum(part, tile_words, i, ok, t0, t1, Q, C);
-  if (!ok || threadIdx.x >= kFinWords) return;
+  finalize_sum<FW>(part, tile_words, i, ok, t0, t1, Q, C);
+  if (!ok || threadIdx.x >= FW) return;
   int f, b;
   part_feature_bin(i, V, num_bins, f, b);
   if (f >= n_feats) return;
@@ -406,8 +422,20 @@ __global__ __launch_bounds__(1024) void plan_tiles_kernel(
     const int64_t* __restrict__ seg, int64_t total_rows, int32_t n_keys,
     const int32_t* __restrict__ key_list, int32_t tile_rows,
     int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
-    int32_t* __restrict__ n_tiles) {
+    int32_t* __restrict__ n_tiles, const uint32_t* __restrict__ abs_part, int32_t n_abs,
+    int32_t qbits, uint32_t* __restrict__ absmax_bits, int32_t* __restrict__ shift) {
   __shared__ int64_t wsum[16];
+  if (abs_part) {
+    // the quantisation shift of the call from the per-block maxima (what
+    // absmax_finish_kernel does for one tree), folded in to save a launch
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < n_abs; i += blockDim.x) m = abs_part[i] > m ? abs_part[i] : m;
+    m = wgbm_block_max_u32(m);
+    if (threadIdx.x == 0) {
+      *absmax_bits = m;
+      *shift = m >= 0x7f800000u ? 0 : wgbm_shift_from_absmax(__uint_as_float(m), qbits);
+    }
+  }
   __shared__ int64_t sbuf[kScanK * 1024];
   const int nk = n_keys;  // entries of key_list (or keys 0..n_keys-1)
   auto bounds = [&](int i, int& key, int64_t& b0, int64_t& b1) {
@@ -570,6 +598,62 @@ int probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, hipStrea
   *ops_per_s = (double)blocks * kHistThreads * iters * 16 / (ms * 1e-3);
   return 0;
 }
+
+// --------------------------------------------------------------------------
+// finalize launchers: words per workgroup from the expected tiles per segment
+// --------------------------------------------------------------------------
+int fin_words_for(int64_t tiles_per_key) {
+  if (tiles_per_key >= 32) return 32;   // 8-way tile split
+  if (tiles_per_key >= 16) return 64;   // 4-way
+  if (tiles_per_key >= 8) return 128;   // 2-way
+  return 256;                           // one group walks all tiles
+}
+
+#define WGBM_FIN_DISPATCH(FWV, LAUNCH) \
+  switch (FWV) {                       \
+    case 32: LAUNCH(32); break;        \
+    case 64: LAUNCH(64); break;        \
+    case 128: LAUNCH(128); break;      \
+    default: LAUNCH(256); break;       \
+  }
+
+int launch_finalize_f32(int64_t tiles_per_key, const unsigned long long* part,
+                        const int32_t* key_tile_start, int32_t n_keys, int32_t n_chunks, int32_t V,
+                        int32_t num_bins, int32_t n_feats, const int32_t* shifts,
+                        const uint32_t* absmax_bits, const int32_t* n_tiles, int32_t accumulate,
+                        float* G, float* H, hipStream_t st) {
+  const int fw = fin_words_for(tiles_per_key);
+  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
+  const unsigned wg = (unsigned)(n_keys * ((tile_words + fw - 1) / fw));
+#define WGBM_L(F)                                                                                 \
+  hipLaunchKernelGGL(hist_finalize_f32_kernel<F>, dim3(wg), dim3(256), 0, st, part, key_tile_start, \
+                     n_keys, n_chunks, V, num_bins, n_feats, shifts, absmax_bits, n_tiles,          \
+                     accumulate, G, H)
+  WGBM_FIN_DISPATCH(fw, WGBM_L)
+#undef WGBM_L
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
+                          const int32_t* key_tile_start, const int32_t* key_list, int32_t n_list,
+                          int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
+                          int32_t num_eras, int32_t nodes_in_level, int32_t depth,
+                          const int64_t* parent_q, const int32_t* parent_c, const int32_t* n_tiles,
+                          int64_t* hq, int32_t* hc, hipStream_t st) {
+  const int fw = fin_words_for(tiles_per_key);
+  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
+  const unsigned wg = (unsigned)(n_list * ((tile_words + fw - 1) / fw));
+#define WGBM_L(F)                                                                          \
+  hipLaunchKernelGGL(hist_finalize_level_kernel<F>, dim3(wg), dim3(256), 0, st, part,        \
+                     key_tile_start, key_list, n_list, n_chunks, V, num_bins, n_feats, num_eras, \
+                     nodes_in_level, depth, parent_q, parent_c, n_tiles, hq, hc)
+  WGBM_FIN_DISPATCH(fw, WGBM_L)
+#undef WGBM_L
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+#undef WGBM_FIN_DISPATCH
 
 // --------------------------------------------------------------------------
 // host launch helpers

@@ -52,28 +52,30 @@ int launch_hist_tiles(const HistLaunch& a, hipStream_t st);
 int probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, hipStream_t st);
 
 // kernels launched directly from other translation units
-__global__ void hist_finalize_f32_kernel(const unsigned long long* part,
-                                         const int32_t* key_tile_start, int32_t n_keys,
-                                         int32_t n_chunks, int32_t V, int32_t num_bins,
-                                         int32_t n_feats, const int32_t* shifts,
-                                         const uint32_t* absmax_bits, const int32_t* n_tiles,
-                                         int32_t accumulate, float* G, float* H);
+int launch_finalize_f32(int64_t tiles_per_key, const unsigned long long* part,
+                        const int32_t* key_tile_start, int32_t n_keys, int32_t n_chunks, int32_t V,
+                        int32_t num_bins, int32_t n_feats, const int32_t* shifts,
+                        const uint32_t* absmax_bits, const int32_t* n_tiles, int32_t accumulate,
+                        float* G, float* H, hipStream_t st);
 __global__ void hist_gather_features_kernel(const float* Gf, const float* Hf, int32_t n_keys,
                                             int32_t n_feats_full, int32_t num_bins,
                                             const int32_t* feat_idx, int32_t n_out, float* G,
                                             float* H);
-__global__ void hist_finalize_level_kernel(
-    const unsigned long long* part, const int32_t* key_tile_start, const int32_t* key_list,
-    int32_t n_list, int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
-    int32_t num_eras, int32_t nodes_in_level, int32_t depth, const int64_t* parent_q,
-    const int32_t* parent_c, const int32_t* n_tiles, int64_t* hq, int32_t* hc);
+int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
+                          const int32_t* key_tile_start, const int32_t* key_list, int32_t n_list,
+                          int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
+                          int32_t num_eras, int32_t nodes_in_level, int32_t depth,
+                          const int64_t* parent_q, const int32_t* parent_c, const int32_t* n_tiles,
+                          int64_t* hq, int32_t* hc, hipStream_t st);
 __global__ void absmax_partial_kernel(const float* resid, const int32_t* rows, int64_t n,
                                       uint32_t* partial);
 __global__ void absmax_finish_kernel(const uint32_t* partial, int32_t n_part, int32_t qbits,
                                      uint32_t* absmax_bits, int32_t* shifts);
 __global__ void plan_tiles_kernel(const int64_t* seg, int64_t total, int32_t n_keys,
                                   const int32_t* key_list, int32_t tile_rows, int32_t max_tiles, Tile* tiles,
-                                  int32_t* key_tile_start, int32_t* n_tiles);
+                                  int32_t* key_tile_start, int32_t* n_tiles,
+                                  const uint32_t* abs_part, int32_t n_abs, int32_t qbits,
+                                  uint32_t* absmax_bits, int32_t* shift);
 __global__ void era_count_kernel(const int32_t* rows, int64_t n, const int32_t* era,
                                  int32_t num_eras, int64_t* counts);
 __global__ void exclusive_scan_i64_kernel(const int64_t* in, int32_t n, int64_t* out);
