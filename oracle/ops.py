@@ -142,19 +142,36 @@ def split_scan(G, H, min_child_samples, eps):
     return gain, dirn
 
 
+DES_ERA_BLOCK = 32
+
+
+def era_sum_f64(gain):
+    """float64 sum over axis 0 of float32 per-era values in the DES order:
+    each block of 32 consecutive eras summed in era order, then the block
+    sums in block order."""
+    gain = np.asarray(gain, dtype=F32)
+    E = gain.shape[0]
+    acc = np.zeros(gain.shape[1:], np.float64)
+    for b0 in range(0, E, DES_ERA_BLOCK):
+        blk = np.zeros(gain.shape[1:], np.float64)
+        for e in range(b0, min(E, b0 + DES_ERA_BLOCK)):  # era order inside the block
+            blk = blk + gain[e].astype(np.float64)
+        acc = acc + blk  # block order
+    return acc
+
+
 def des_criterion(gain, dirn):
     """(crit, agree) over [F, B-1] from per-era arrays (warpgbm/core.py:577-583).
     E == 1: crit = gain[0].  E > 1: crit = float32(sum_e gain_e / E) with the
-    era sum in float64, sequential in era order; agree = |sum_e dir_e|, an
-    exact integer (the reference's |mean_e dir| is that integer over E)."""
+    era sum in float64 in two levels: the eras of each block of 32 consecutive
+    eras summed in era order, then the block sums in block order (for E <= 32
+    that is the plain sequential sum); agree = |sum_e dir_e|, an exact
+    integer (the reference's |mean_e dir| is that integer over E)."""
     gain = np.asarray(gain, dtype=F32)
     E = gain.shape[0]
     if E == 1:
         return gain[0].copy(), None
-    acc = np.zeros(gain.shape[1:], np.float64)
-    for e in range(E):  # sequential era order
-        acc = acc + gain[e].astype(np.float64)
-    crit = (acc / np.float64(E)).astype(F32)
+    crit = (era_sum_f64(gain) / np.float64(E)).astype(F32)
     agree = np.abs(np.rint(np.asarray(dirn, dtype=np.float64)).astype(np.int64).sum(axis=0))
     return crit, agree
 

@@ -317,6 +317,31 @@ def test_des_select_prefers_consistent_direction():
     assert ops.des_select(gain2, dirn2, 0.0) == (1, 0)
 
 
+def test_des_criterion_era_sum_order():
+    """E <= 32: the plain sequential float64 sum.  E > 32: 32-era blocks, each
+    summed in era order, then the block sums in order -- on values where the
+    two orders round differently (sequentially every 2^-53 is lost against
+    1.0; inside the second block they first add up exactly)."""
+    gain = np.zeros((40, 1, 1), F32)
+    gain[0] = 1.0
+    gain[1:32] = F32(2.0**-53)
+    gain[32] = F32(2.0**-50)
+    gain[33:40] = F32(2.0**-53)
+    seq = 0.0
+    for e in range(40):
+        seq = seq + float(gain[e, 0, 0])
+    assert seq == 1.0 + 2.0**-50
+    got = ops.era_sum_f64(gain)[0, 0]
+    assert got == 1.0 + 2.0**-49  # (1.0) + (2^-50 + 7 * 2^-53) = 1 + 15 * 2^-53, rounded
+    small = gain[:20]
+    s20 = 0.0
+    for e in range(20):
+        s20 = s20 + float(small[e, 0, 0])
+    assert ops.era_sum_f64(small)[0, 0] == s20
+    crit, _ = ops.des_criterion(gain, np.zeros_like(gain))
+    assert crit[0, 0] == np.float32(got / 40)
+
+
 def test_des_criterion_mean_is_float64_sequential():
     rng = np.random.default_rng(1)
     gain = rng.standard_normal((500, 3, 4)).astype(F32)

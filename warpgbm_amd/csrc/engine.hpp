@@ -109,16 +109,23 @@ __global__ void des_finish_kernel(const unsigned long long* best, const int64_t*
                                   const int32_t* hc, int32_t F, int32_t B, int32_t E,
                                   const int32_t* feat_sel, int32_t nodes_in_level, int32_t n_tn,
                                   const int32_t* shifts, float mcw, float eps, const float* staged,
-                                  int32_t n_sel, int32_t* split_l, int32_t* split_b,
-                                  float* split_gain_era);
-__global__ void des_combine_kernel(const float* gain, const int8_t* dir, int32_t E, int32_t n_tn,
-                                   int64_t ncand, const int32_t* present, float* crit,
-                                   int32_t* agree, int32_t* agree_max);
+                                  const int64_t* seg, int32_t n_sel, int32_t* split_l,
+                                  int32_t* split_b, float* split_gain_era);
+__global__ void des_alive_kernel(const int64_t* seg, int32_t E, int32_t n_tn, float mcw,
+                                 uint32_t* alive);
+__global__ void des_block_kernel(const float* gain, const int8_t* dir, int32_t E, int32_t n_tn,
+                                 int64_t ncand, const int32_t* present, const uint32_t* alive,
+                                 double* bsum, int32_t* bdir);
+__global__ void des_combine_kernel(const double* bsum, const int32_t* bdir, int32_t E,
+                                   int32_t n_tn, int64_t ncand, const int32_t* present,
+                                   const uint32_t* alive, float* crit, int32_t* agree,
+                                   int32_t* agree_max);
 __global__ void local_scatter_kernel(const int32_t* feat_sel, int32_t n_sel, int32_t F,
                                      int32_t* local_of);
-int launch_des_era(int V, int B, dim3 grid, hipStream_t st, const int8_t* codes, int64_t stride,
-                   int32_t F, const float* resid, int64_t resid_tree_stride, const int32_t* shifts,
-                   const int32_t* order, const int64_t* seg, int32_t E, int32_t nodes_in_level,
+int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* codes,
+                   int64_t stride, int32_t F, const float* resid, int64_t resid_tree_stride,
+                   const int32_t* shifts, const int32_t* order, const int64_t* seg, int32_t E,
+                   int32_t nodes_in_level,
                    const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
                    float eps, float* gain, int8_t* dir);
 

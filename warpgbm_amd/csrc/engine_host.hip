@@ -64,6 +64,9 @@ struct Engine {
   float* sgain = nullptr;       // staged per-era gains [tn][E][n_sel][B-1]
   int8_t* sdir = nullptr;       // staged per-era directions
   int32_t* local_of = nullptr;  // [F] local index in the round's subset, or -1
+  uint32_t* alive = nullptr;    // [tn][W] segments that can hold a split, W = ceil(E/32)
+  double* bsum = nullptr;       // [tn][W][n_sel*(B-1)] era-block gain sums
+  int32_t* bdir = nullptr;      // [tn][W][n_sel*(B-1)] era-block direction sums
   int32_t* split_l = nullptr;
   int32_t* split_b = nullptr;
   float* split_gain = nullptr;
@@ -161,6 +164,10 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     E_ALLOC(e->sgain, T * hist_nodes_max * E * F * (B - 1));
     E_ALLOC(e->sdir, T * hist_nodes_max * E * F * (B - 1));
     E_ALLOC(e->local_of, F);
+    const int64_t W = (E + kDesEraBlock - 1) / kDesEraBlock;
+    E_ALLOC(e->alive, T * hist_nodes_max * W);
+    E_ALLOC(e->bsum, T * hist_nodes_max * W * F * (B - 1));
+    E_ALLOC(e->bdir, T * hist_nodes_max * W * F * (B - 1));
   }
   E_ALLOC(e->dirbit, T * N);
   e->max_ptiles = T * N / e->part_tile_rows + e->n_keys_max + 1;
@@ -290,18 +297,25 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     if (d < D && e->des_direct) {
       // ---- E > 1, direct: per-era gains of every (node, era) segment
       const int64_t ncand = (int64_t)n_sel * (B - 1);
-      int r = launch_des_era(e->V, B, dim3((unsigned)((int64_t)n_keys * e->n_chunks)), st,
-                             c.codes_rm, c.stride, F, e->resid, N, e->shifts, e->order[cur],
-                             e->seg[cur], E, nodes, e->present[cur], e->local_of, n_sel, mcw, eps,
-                             e->sgain, e->sdir);
+      int r = launch_des_era(e->V, B, n_keys, st, c.codes_rm, c.stride, F, e->resid, N,
+                             e->shifts, e->order[cur], e->seg[cur], E, nodes, e->present[cur],
+                             e->local_of, n_sel, mcw, eps, e->sgain, e->sdir);
       if (r) return r;
       if (fill_u64(e->best, n_tn, 0ull, st)) return WGBM_EINVAL;
       hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st,
                          e->agree_max, (int64_t)n_tn, 0);
       WGBM_LAUNCH_CHECK();
-      hipLaunchKernelGGL(des_combine_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)),
+      const int64_t W = (E + kDesEraBlock - 1) / kDesEraBlock;
+      hipLaunchKernelGGL(des_alive_kernel, dim3(blocks_for((int64_t)n_tn * W, 256)), dim3(256), 0,
+                         st, e->seg[cur], E, n_tn, mcw, e->alive);
+      WGBM_LAUNCH_CHECK();
+      hipLaunchKernelGGL(des_block_kernel, dim3(blocks_for((int64_t)n_tn * W * ncand, 256)),
                          dim3(256), 0, st, e->sgain, e->sdir, E, n_tn, ncand, e->present[cur],
-                         e->crit, e->agree, e->agree_max);
+                         e->alive, e->bsum, e->bdir);
+      WGBM_LAUNCH_CHECK();
+      hipLaunchKernelGGL(des_combine_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)),
+                         dim3(256), 0, st, e->bsum, e->bdir, E, n_tn, ncand, e->present[cur],
+                         e->alive, e->crit, e->agree, e->agree_max);
       WGBM_LAUNCH_CHECK();
       hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)), dim3(256),
                          0, st, e->crit, e->agree, e->agree_max, e->present[cur], n_tn, ncand, msg,
@@ -309,8 +323,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       WGBM_LAUNCH_CHECK();
       hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)n_tn * E, 256)), dim3(256), 0,
                          st, e->best, (const int64_t*)nullptr, (const int32_t*)nullptr, F, B, E,
-                         feat_sel, nodes, n_tn, e->shifts, mcw, eps, e->sgain, n_sel, e->split_l,
-                         e->split_b, e->split_gain);
+                         feat_sel, nodes, n_tn, e->shifts, mcw, eps, e->sgain, e->seg[cur], n_sel,
+                         e->split_l, e->split_b, e->split_gain);
       WGBM_LAUNCH_CHECK();
     } else if (d < D) {
       // ---- histograms of the computed segments
@@ -395,8 +409,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         WGBM_LAUNCH_CHECK();
         hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)n_tn * E, 256)), dim3(256),
                            0, st, e->best, e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, nodes,
-                           n_tn, e->shifts, mcw, eps, (const float*)nullptr, n_sel, e->split_l,
-                           e->split_b, e->split_gain);
+                           n_tn, e->shifts, mcw, eps, (const float*)nullptr,
+                           (const int64_t*)nullptr, n_sel, e->split_l, e->split_b, e->split_gain);
         WGBM_LAUNCH_CHECK();
       }
     } else {

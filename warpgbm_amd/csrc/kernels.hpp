@@ -21,6 +21,9 @@ constexpr int kHistThreads = 1024;
 constexpr int kHistSlots = 64;
 // split candidates (bins) per lane of the era-accumulating DES scan
 constexpr int kDesChunk = 8;
+// eras per block of the DES era sum (float64: in era order inside a block,
+// then block sums in block order); also the width of a live-era mask word
+constexpr int kDesEraBlock = 32;
 // cache-policy bits of a buffer load: non-temporal (streamed once)
 constexpr int kAuxNT = 2;
 // histogram workgroups per launch the tile sizes aim for (2 per CU)

@@ -23,6 +23,8 @@
 // all candidates), and crit = float(sum_e double(gain_e) / E) with the era sum
 // taken sequentially in era order.
 #include <float.h>
+
+#include <algorithm>
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -86,6 +88,13 @@ __global__ void split_f32_kernel(const float* __restrict__ G, const float* __res
 // ---------------------------------------------------------------------------
 __device__ inline bool better(float g, int i, float bg, int bi) {
   return g > bg || (g == bg && i < bi);
+}
+
+// A (node, era) segment of n rows where every candidate split has gain 0 and
+// direction 0: HL >= mcw && HR >= mcw needs HL + HR >= 2*mcw, and HL + HR
+// counts at most the n rows (exact small integers in float).
+__device__ inline bool des_segment_dead(int64_t n, float mcw) {
+  return (float)n < 2.0f * mcw;
 }
 
 // order-preserving map of float bits to uint32 (and back)
@@ -242,6 +251,9 @@ __global__ __launch_bounds__(128) void des_accumulate_kernel(
       gs[k] = 0.0;
       ds[k] = 0;
     }
+    double bs[kDesChunk];  // current era block's sums
+#pragma unroll
+    for (int k = 0; k < kDesChunk; ++k) bs[k] = 0.0;
     for (int e = 0; e < E; ++e) {
       const int64_t base = (((int64_t)tn * E + e) * F + f) * B;
       const int64_t* q = hq + base;
@@ -274,8 +286,15 @@ __global__ __launch_bounds__(128) void des_accumulate_kernel(
             const float rv = GR / (HR + eps);
             dir = lv > rv ? 1 : -1;
           }
-          gs[k] += (double)gain;
+          bs[k] += (double)gain;  // era order inside the block
           ds[k] += dir;
+        }
+      }
+      if ((e + 1) % kDesEraBlock == 0 || e + 1 == E) {
+#pragma unroll
+        for (int k = 0; k < kDesChunk; ++k) {
+          gs[k] += bs[k];  // block order
+          bs[k] = 0.0;
         }
       }
     }
@@ -322,7 +341,8 @@ __global__ void des_finish_kernel(const unsigned long long* __restrict__ best,
                                   int32_t F, int32_t B, int32_t E,
                                   const int32_t* __restrict__ feat_sel, int32_t nodes_in_level,
                                   int32_t n_tn, const int32_t* __restrict__ shifts, float mcw,
-                                  float eps, const float* __restrict__ staged, int32_t n_sel,
+                                  float eps, const float* __restrict__ staged,
+                                  const int64_t* __restrict__ seg, int32_t n_sel,
                                   int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
                                   float* __restrict__ split_gain_era) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -345,8 +365,11 @@ __global__ void des_finish_kernel(const unsigned long long* __restrict__ best,
     split_b[tn] = bsel;
   }
   if (staged) {
-    // staged per-era gains [tn][E][n_sel][B-1]
-    split_gain_era[gid] = staged[((int64_t)tn * E + e) * ((int64_t)n_sel * nb) + idx];
+    // staged per-era gains [tn][E][n_sel][B-1]; none for dead segments
+    const int64_t k2 = (int64_t)tn * E + e;
+    split_gain_era[gid] = des_segment_dead(seg[k2 + 1] - seg[k2], mcw)
+                              ? 0.0f
+                              : staged[k2 * ((int64_t)n_sel * nb) + idx];
     return;
   }
   const int s = shifts[tn / nodes_in_level];
@@ -376,13 +399,14 @@ __global__ void des_finish_kernel(const unsigned long long* __restrict__ best,
 //     sum in double in era order (same values and order as des_accumulate).
 // ---------------------------------------------------------------------------
 constexpr int kDesEraThreads = 256;
+constexpr int kDesEraMaxWG = 4096;  // des_era grid bound (about 16 workgroups per CU)
 
 template <int V, int BT>
 __global__ __launch_bounds__(kDesEraThreads) void des_era_kernel(
     const int8_t* __restrict__ codes, int64_t stride, int32_t F,
     const float* __restrict__ resid, int64_t resid_tree_stride,
     const int32_t* __restrict__ shifts, const int32_t* __restrict__ order,
-    const int64_t* __restrict__ seg, int32_t E, int32_t nodes_in_level,
+    const int64_t* __restrict__ seg, int32_t E, int32_t n_keys, int32_t nodes_in_level,
     const int32_t* __restrict__ present, const int32_t* __restrict__ local_of, int32_t n_sel,
     int32_t num_bins_rt, float mcw, float eps, float* __restrict__ gain,
     int8_t* __restrict__ dir) {
@@ -393,18 +417,9 @@ __global__ __launch_bounds__(kDesEraThreads) void des_era_kernel(
   const int Bp = B + 1;
   const int nb = B - 1;
   const int n_chunks = (F + CW - 1) / CW;
-  const int key = blockIdx.x / n_chunks;
-  const int chunk = blockIdx.x - key * n_chunks;
-  const int tn = key / E;
-  if (!present[tn]) return;  // uniform per workgroup
-  for (int i = threadIdx.x; i < V * Bp * kHistSlots; i += kDesEraThreads) lds[i] = 0ull;
-  __syncthreads();
-
-  const int64_t begin = seg[key];
-  const int n = (int)(seg[key + 1] - begin);  // <= 65536 (checked by the engine)
-  const int tree = tn / nodes_in_level;
-  const int s = shifts[tree];
-  const float* __restrict__ r_t = resid + (int64_t)tree * resid_tree_stride;
+  const int slots = gridDim.x / n_chunks;  // workgroups per chunk; keys stride by it
+  const int slot = blockIdx.x / n_chunks;
+  const int chunk = blockIdx.x - slot * n_chunks;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int f_base = chunk * CW + lane * V;
@@ -412,59 +427,157 @@ __global__ __launch_bounds__(kDesEraThreads) void des_era_kernel(
   // the wave fetches anyway); their words are never evaluated
   const int voff = f_base < F ? f_base : (F - 1) / V * V;
   unsigned long long* my = lds + lane;
-  auto add_row = [&](int row) {
-    const int64_t q = (int64_t)wgbm_quantise(r_t[row], s);
-    const unsigned long long w = (unsigned long long)(q * (int64_t)(1 << WGBM_CBITS) + 1);
-    const int8_t* src = codes + (int64_t)row * stride + voff;
-    uint32_t cw;
-    if constexpr (V == 4)
-      cw = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
-    else if constexpr (V == 2)
-      cw = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(src));
-    else
-      cw = __builtin_nontemporal_load(reinterpret_cast<const uint8_t*>(src));
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
-      uint32_t c = (cw >> (8 * j)) & 0xffu;
-      c = c < (uint32_t)B ? c : (uint32_t)B;  // out-of-range code -> trash bin
-      atomicAdd(my + (j * Bp + (int)c) * kHistSlots, w);
-    }
-  };
-  // four rows per wave and step (wave-uniform), loads issued together
-  int i = wave;
-  for (; i + 3 * nwaves < n; i += 4 * nwaves) {
-    int rows[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) rows[u] = order[begin + i + u * nwaves];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) add_row(rows[u]);
-  }
-  for (; i < n; i += nwaves) add_row(order[begin + i]);
-  __syncthreads();
 
-  // candidates of this era: thread per feature of the chunk
-  for (int fs = threadIdx.x; fs < CW; fs += kDesEraThreads) {
-    const int f = chunk * CW + fs;
-    if (f >= F) continue;
-    const int l = local_of[f];
-    if (l < 0) continue;
-    const unsigned long long* col = lds + (fs % V) * Bp * kHistSlots + fs / V;
-    const int64_t out = ((int64_t)key * n_sel + l) * nb;
-    scan_bins(
-        B, mcw, eps,
-        [&](int b) { return wgbm_dequantise((int64_t)col[b * kHistSlots] >> WGBM_CBITS, s); },
-        [&](int b) { return (float)(int32_t)(col[b * kHistSlots] & (unsigned long long)WGBM_CMASK); },
-        [&](int b, float gn, float d) {
-          gain[out + b] = gn;
-          dir[out + b] = (int8_t)d;
-        });
+  // keys slot, slot + slots, ...: every wave classifies 64 of them at a time
+  // (one per lane) and the workgroup visits the live ones in order.  A key
+  // is skipped when its node is absent or the segment is dead (fewer than
+  // 2*min_child_weight rows: no candidate can split it, so every candidate
+  // has gain 0 and direction 0 there; des_combine and des_finish account for
+  // it without staged values).
+  for (int kb = slot; kb < n_keys; kb += 64 * slots) {
+    const int kl = kb + lane * slots;
+    bool live = false;
+    if (kl < n_keys) {
+      const int tnl = kl / E;
+      live = present[tnl] && !des_segment_dead(seg[kl + 1] - seg[kl], mcw);
+    }
+    uint64_t todo = __ballot(live);
+    while (todo) {
+      const int l0 = __builtin_ctzll(todo);
+      todo &= todo - 1;
+      const int key = kb + l0 * slots;
+      const int tn = key / E;
+      const int64_t begin = seg[key];
+      const int n = (int)(seg[key + 1] - begin);  // <= 65536 (checked by the engine)
+      const int tree = tn / nodes_in_level;
+      const int s = shifts[tree];
+      const float* __restrict__ r_t = resid + (int64_t)tree * resid_tree_stride;
+      for (int i = threadIdx.x; i < V * Bp * kHistSlots; i += kDesEraThreads) lds[i] = 0ull;
+      __syncthreads();
+      auto add_row = [&](int row) {
+        const int64_t q = (int64_t)wgbm_quantise(r_t[row], s);
+        const unsigned long long w = (unsigned long long)(q * (int64_t)(1 << WGBM_CBITS) + 1);
+        const int8_t* src = codes + (int64_t)row * stride + voff;
+        uint32_t cw;
+        if constexpr (V == 4)
+          cw = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
+        else if constexpr (V == 2)
+          cw = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(src));
+        else
+          cw = __builtin_nontemporal_load(reinterpret_cast<const uint8_t*>(src));
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          uint32_t c = (cw >> (8 * j)) & 0xffu;
+          c = c < (uint32_t)B ? c : (uint32_t)B;  // out-of-range code -> trash bin
+          atomicAdd(my + (j * Bp + (int)c) * kHistSlots, w);
+        }
+      };
+      // four rows per wave and step (wave-uniform), loads issued together
+      int i = wave;
+      for (; i + 3 * nwaves < n; i += 4 * nwaves) {
+        int rows[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) rows[u] = order[begin + i + u * nwaves];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) add_row(rows[u]);
+      }
+      for (; i < n; i += nwaves) add_row(order[begin + i]);
+      __syncthreads();
+
+      // candidates of this era: thread per feature of the chunk
+      for (int fs = threadIdx.x; fs < CW; fs += kDesEraThreads) {
+        const int f = chunk * CW + fs;
+        if (f >= F) continue;
+        const int l = local_of[f];
+        if (l < 0) continue;
+        const unsigned long long* col = lds + (fs % V) * Bp * kHistSlots + fs / V;
+        const int64_t out = ((int64_t)key * n_sel + l) * nb;
+        scan_bins(
+            B, mcw, eps,
+            [&](int b) { return wgbm_dequantise((int64_t)col[b * kHistSlots] >> WGBM_CBITS, s); },
+            [&](int b) {
+              return (float)(int32_t)(col[b * kHistSlots] & (unsigned long long)WGBM_CMASK);
+            },
+            [&](int b, float gn, float d) {
+              gain[out + b] = gn;
+              dir[out + b] = (int8_t)d;
+            });
+      }
+      __syncthreads();  // before the next key's histogram reuses the LDS
+    }
   }
 }
 
-__global__ __launch_bounds__(256) void des_combine_kernel(
+// live-era bit masks: bit (e % 32) of alive[tn * W + e / 32] is set when the
+// (tn, era e) segment can hold a split (not des_segment_dead); W = ceil(E/32)
+// (one mask word per era block)
+__global__ void des_alive_kernel(const int64_t* __restrict__ seg, int32_t E, int32_t n_tn,
+                                 float mcw, uint32_t* __restrict__ alive) {
+  static_assert(kDesEraBlock == 32, "one 32-bit mask word per era block");
+  const int W = (E + kDesEraBlock - 1) / kDesEraBlock;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)n_tn * W) return;
+  const int tn = (int)(gid / W);
+  const int w = (int)(gid - (int64_t)tn * W);
+  const int64_t* sg = seg + (int64_t)tn * E;
+  uint32_t m = 0;
+  for (int b = 0; b < kDesEraBlock; ++b) {
+    const int e = w * kDesEraBlock + b;
+    if (e < E && !des_segment_dead(sg[e + 1] - sg[e], mcw)) m |= 1u << b;
+  }
+  alive[gid] = m;
+}
+
+// Era sums in the DES order: float64, each block of kDesEraBlock consecutive
+// eras summed in era order (des_block_kernel, one lane per (node, block,
+// candidate)), then the block sums in block order (des_combine_kernel, one
+// lane per (node, candidate)).  Dead segments add gain 0 and direction 0
+// (acc + 0.0 == acc exactly): their staged values are never read, and a block
+// without a live era is skipped.
+__global__ __launch_bounds__(256) void des_block_kernel(
     const float* __restrict__ gain, const int8_t* __restrict__ dir, int32_t E, int32_t n_tn,
-    int64_t ncand, const int32_t* __restrict__ present, float* __restrict__ crit,
-    int32_t* __restrict__ agree, int32_t* __restrict__ agree_max) {
+    int64_t ncand, const int32_t* __restrict__ present, const uint32_t* __restrict__ alive,
+    double* __restrict__ bsum, int32_t* __restrict__ bdir) {
+  const int W = (E + kDesEraBlock - 1) / kDesEraBlock;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)n_tn * W * ncand) return;
+  const int64_t c = gid % ncand;
+  const int64_t tb = gid / ncand;  // tn * W + block
+  const int tn = (int)(tb / W);
+  const int blk = (int)(tb - (int64_t)tn * W);
+  if (!present[tn]) return;
+  const uint32_t m = alive[tb];
+  if (m == 0) return;
+  const int64_t base = ((int64_t)tn * E + (int64_t)blk * kDesEraBlock) * ncand + c;
+  double acc = 0.0;
+  int ds = 0;
+  constexpr int kHalf = kDesEraBlock / 2;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float gv[kHalf];
+    int dv[kHalf];
+#pragma unroll
+    for (int k = 0; k < kHalf; ++k) {
+      const int kk = h * kHalf + k;
+      const bool live = (m >> kk) & 1u;  // implies the era exists
+      gv[k] = live ? gain[base + (int64_t)kk * ncand] : 0.0f;
+      dv[k] = live ? (int)dir[base + (int64_t)kk * ncand] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kHalf; ++k) {
+      if ((m >> (h * kHalf + k)) & 1u) acc += (double)gv[k];  // era order
+      ds += dv[k];
+    }
+  }
+  bsum[gid] = acc;
+  bdir[gid] = ds;
+}
+
+__global__ __launch_bounds__(256) void des_combine_kernel(
+    const double* __restrict__ bsum, const int32_t* __restrict__ bdir, int32_t E, int32_t n_tn,
+    int64_t ncand, const int32_t* __restrict__ present, const uint32_t* __restrict__ alive,
+    float* __restrict__ crit, int32_t* __restrict__ agree, int32_t* __restrict__ agree_max) {
+  const int W = (E + kDesEraBlock - 1) / kDesEraBlock;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   int tn = 0;
   bool active = gid < (int64_t)n_tn * ncand;
@@ -475,24 +588,14 @@ __global__ __launch_bounds__(256) void des_combine_kernel(
   }
   if (active) {
     const int64_t c = gid - (int64_t)tn * ncand;
-    const float* g = gain + (int64_t)tn * E * ncand + c;
-    const int8_t* dd = dir + (int64_t)tn * E * ncand + c;
+    const uint32_t* al = alive + (int64_t)tn * W;
     double acc = 0.0;
     int ds = 0;
-    int e = 0;
-    for (; e + 4 <= E; e += 4) {
-      const float g0 = g[(int64_t)e * ncand], g1 = g[(int64_t)(e + 1) * ncand];
-      const float g2 = g[(int64_t)(e + 2) * ncand], g3 = g[(int64_t)(e + 3) * ncand];
-      ds += dd[(int64_t)e * ncand] + dd[(int64_t)(e + 1) * ncand] + dd[(int64_t)(e + 2) * ncand] +
-            dd[(int64_t)(e + 3) * ncand];
-      acc += (double)g0;  // sequential era order
-      acc += (double)g1;
-      acc += (double)g2;
-      acc += (double)g3;
-    }
-    for (; e < E; ++e) {
-      acc += (double)g[(int64_t)e * ncand];
-      ds += dd[(int64_t)e * ncand];
+    for (int b = 0; b < W; ++b) {
+      if (al[b] == 0) continue;
+      const int64_t o = ((int64_t)tn * W + b) * ncand + c;
+      acc += bsum[o];  // block order
+      ds += bdir[o];
     }
     crit[gid] = (float)(acc / (double)E);
     a = ds < 0 ? -ds : ds;
@@ -511,12 +614,17 @@ __global__ void local_scatter_kernel(const int32_t* __restrict__ feat_sel, int32
   }
 }
 
-int launch_des_era(int V, int B, dim3 grid, hipStream_t st, const int8_t* codes, int64_t stride,
-                   int32_t F, const float* resid, int64_t resid_tree_stride, const int32_t* shifts,
-                   const int32_t* order, const int64_t* seg, int32_t E, int32_t nodes_in_level,
+int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* codes,
+                   int64_t stride, int32_t F, const float* resid, int64_t resid_tree_stride,
+                   const int32_t* shifts, const int32_t* order, const int64_t* seg, int32_t E,
+                   int32_t nodes_in_level,
                    const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
                    float eps, float* gain, int8_t* dir) {
   const size_t lds = (size_t)V * (B + 1) * kHistSlots * 8;
+  // at most kDesEraMaxWG workgroups; each strides over the keys of its chunk
+  const int n_chunks = (F + kHistSlots * V - 1) / (kHistSlots * V);
+  const int slots = std::max(1, std::min(n_keys, kDesEraMaxWG / n_chunks));
+  const dim3 grid((unsigned)(slots * n_chunks));
 #define WGBM_DES_ERA(VV, BB)                                                                   \
   do {                                                                                         \
     static bool attr = false;                                                                  \
@@ -526,7 +634,7 @@ int launch_des_era(int V, int B, dim3 grid, hipStream_t st, const int8_t* codes,
       attr = true;                                                                             \
     }                                                                                          \
     hipLaunchKernelGGL((des_era_kernel<VV, BB>), grid, dim3(kDesEraThreads), lds, st, codes,   \
-                       stride, F, resid, resid_tree_stride, shifts, order, seg, E,             \
+                       stride, F, resid, resid_tree_stride, shifts, order, seg, E, n_keys,     \
                        nodes_in_level, present, local_of, n_sel, B, mcw, eps, gain, dir);      \
     WGBM_LAUNCH_CHECK();                                                                       \
     return 0;                                                                                  \
