@@ -402,7 +402,8 @@ constexpr int kDesEraThreads = 256;
 constexpr int kDesEraMaxWG = 4096;  // des_era grid bound (about 16 workgroups per CU)
 
 template <int V, int BT>
-__global__ __launch_bounds__(kDesEraThreads) void des_era_kernel(
+__global__ __launch_bounds__(kDesEraThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void des_era_kernel(
     const int8_t* __restrict__ codes, int64_t stride, int32_t F,
     const float* __restrict__ resid, int64_t resid_tree_stride,
     const int32_t* __restrict__ shifts, const int32_t* __restrict__ order,
@@ -454,34 +455,77 @@ __global__ __launch_bounds__(kDesEraThreads) void des_era_kernel(
       const float* __restrict__ r_t = resid + (int64_t)tree * resid_tree_stride;
       for (int i = threadIdx.x; i < V * Bp * kHistSlots; i += kDesEraThreads) lds[i] = 0ull;
       __syncthreads();
-      auto add_row = [&](int row) {
-        const int64_t q = (int64_t)wgbm_quantise(r_t[row], s);
-        const unsigned long long w = (unsigned long long)(q * (int64_t)(1 << WGBM_CBITS) + 1);
-        const int8_t* src = codes + (int64_t)row * stride + voff;
-        uint32_t cw;
-        if constexpr (V == 4)
-          cw = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
-        else if constexpr (V == 2)
-          cw = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(src));
-        else
-          cw = __builtin_nontemporal_load(reinterpret_cast<const uint8_t*>(src));
+      // software pipeline as in the tile histogram: wave w takes the row
+      // groups [i, i + U), i = (w + k*nwaves)*U; two register sets alternate
+      // so that the loads of the next group are in flight while this one is
+      // added; row ids and residuals are vector loads (lane u < U: row u of
+      // the group) broadcast with readlane; positions past the end read the
+      // segment's last row and add the word 0
+      constexpr int U = 8;
+      constexpr int step = nwaves * U;
+      const int ul = lane & (U - 1);
+      struct Group {
+        uint32_t c[U];
+        float r;
+      };
+      Group ga, gb;
+      int32_t ids = 0;  // lane u < U: order entry u of the next group to issue
+      auto load_ids = [&](int i0) { ids = order[begin + (i0 + ul < n ? i0 + ul : n - 1)]; };
+      auto issue = [&](Group& g, int i0) {
+        int rows[U];
 #pragma unroll
-        for (int j = 0; j < V; ++j) {
-          uint32_t c = (cw >> (8 * j)) & 0xffu;
-          c = c < (uint32_t)B ? c : (uint32_t)B;  // out-of-range code -> trash bin
-          atomicAdd(my + (j * Bp + (int)c) * kHistSlots, w);
+        for (int u = 0; u < U; ++u) rows[u] = __builtin_amdgcn_readlane(ids, u);
+        g.r = r_t[ids];
+        load_ids(i0 + step);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int8_t* src = codes + (int64_t)rows[u] * stride + voff;
+          if constexpr (V == 4)
+            g.c[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
+          else if constexpr (V == 2)
+            g.c[u] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(src));
+          else
+            g.c[u] = __builtin_nontemporal_load(reinterpret_cast<const uint8_t*>(src));
         }
       };
-      // four rows per wave and step (wave-uniform), loads issued together
-      int i = wave;
-      for (; i + 3 * nwaves < n; i += 4 * nwaves) {
-        int rows[4];
+      auto add = [&](const Group& g, int i0) {
+        const int64_t qv = (int64_t)wgbm_quantise(g.r, s);
+        const uint64_t pv = (uint64_t)(qv * (int64_t)(1 << WGBM_CBITS) + 1);
+        const uint32_t plo = (uint32_t)pv, phi = (uint32_t)(pv >> 32);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) rows[u] = order[begin + i + u * nwaves];
+        for (int u = 0; u < U; ++u) {
+          // readlane returns int: widen through uint32_t (no sign extension)
+          const uint64_t wu = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(phi, u) << 32) |
+                              (uint64_t)(uint32_t)__builtin_amdgcn_readlane(plo, u);
+          const unsigned long long w = i0 + u < n ? (unsigned long long)wu : 0ull;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) add_row(rows[u]);
+          for (int j = 0; j < V; ++j) {
+            uint32_t c = (g.c[u] >> (8 * j)) & 0xffu;
+            c = c < (uint32_t)B ? c : (uint32_t)B;  // out-of-range code -> trash bin
+            atomicAdd(my + (j * Bp + (int)c) * kHistSlots, w);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      int i = wave * U;
+      if (i < n) {
+        load_ids(i);
+        issue(ga, i);
+        while (i + 2 * step < n) {
+          issue(gb, i + step);
+          add(ga, i);
+          issue(ga, i + 2 * step);
+          add(gb, i + step);
+          i += 2 * step;
+        }
+        if (i + step < n) {
+          issue(gb, i + step);
+          add(ga, i);
+          add(gb, i + step);
+        } else {
+          add(ga, i);
+        }
       }
-      for (; i < n; i += nwaves) add_row(order[begin + i]);
       __syncthreads();
 
       // candidates of this era: thread per feature of the chunk
