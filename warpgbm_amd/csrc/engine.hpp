@@ -54,17 +54,21 @@ __global__ void residual_softmax_kernel(const float* logits, const int32_t* labe
                                         int32_t K, float* r, uint32_t* partial);
 __global__ void root_setup_kernel(const int32_t* root_order, int64_t n, int32_t T,
                                   const int64_t* era_start, int32_t E, int32_t* order,
-                                  int64_t* seg, int32_t* present);
+                                  int64_t* seg, int32_t* present, int64_t* tot_q,
+                                  int64_t* tot_c, unsigned long long* best, int32_t* agree_max);
 __global__ void segment_totals_kernel(const Tile* tiles, const int32_t* n_tiles,
                                       const int32_t* order, const float* resid, int64_t n,
                                       const int32_t* shifts, int32_t keys_per_tree,
                                       int64_t* tot_q, int64_t* tot_c);
 __global__ void level_finish_kernel(int32_t depth, int32_t max_depth, int32_t T, int32_t E,
-                                    const int32_t* present, const int32_t* split_l,
-                                    const int32_t* split_b, const float* split_gain_era,
+                                    int32_t B, const int32_t* present,
+                                    const unsigned long long* best, int32_t* split_l,
+                                    int32_t* split_b, const float* split_gain_era,
                                     const int32_t* feat_sel, const int64_t* tot_q,
                                     const int64_t* tot_c, const int32_t* shifts,
-                                    float* leaf_val, TreeRecord rec);
+                                    float* leaf_val, TreeRecord rec, int64_t* tot_q_next,
+                                    int64_t* tot_c_next, unsigned long long* best_next,
+                                    int32_t* agree_max_next);
 __global__ void partition_count_kernel(
     const Tile* tiles, const int32_t* n_tiles, const int32_t* order, int32_t E, int32_t nodes,
     int32_t max_split_depth_ok, const int32_t* split_l, const int32_t* split_b,
@@ -95,8 +99,6 @@ __global__ void split_level_e1_kernel(const int64_t* hq, const int32_t* hc, int3
                                       int32_t nodes_in_level, const int32_t* present,
                                       const int32_t* shifts, float mcw, float eps,
                                       float min_split_gain, unsigned long long* best);
-__global__ void split_decode_kernel(const unsigned long long* best, int32_t n_tn, int32_t B,
-                                    int32_t* split_l, int32_t* split_b, float* split_gain);
 __global__ void des_accumulate_kernel(const int64_t* hq, const int32_t* hc, int32_t F, int32_t B,
                                       int32_t E, const int32_t* feat_sel, int32_t n_sel,
                                       int32_t nodes_in_level, int32_t n_tn,

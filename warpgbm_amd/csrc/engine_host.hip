@@ -57,7 +57,7 @@ struct Engine {
   int32_t* hc[2] = {nullptr, nullptr};
   float* crit = nullptr;         // E > 1: per-candidate era-mean gain [tn][n_sel*(B-1)]
   int32_t* agree = nullptr;      // E > 1: per-candidate |sum of directions|
-  int32_t* agree_max = nullptr;  // E > 1: per-node max agree
+  int32_t* agree_max = nullptr;  // E > 1: per-node max agree, two depths (parity)
   // E > 1 with every era <= 65536 rows: per-era gains straight from LDS
   // histograms of every (node, era) segment (no per-era histogram arrays)
   bool des_direct = false;
@@ -71,7 +71,8 @@ struct Engine {
   int32_t* split_b = nullptr;
   float* split_gain = nullptr;
   float* leaf_val = nullptr;
-  unsigned long long* best = nullptr;
+  unsigned long long* best = nullptr;  // packed split picks, two depths (parity)
+  int64_t pick_stride = 0;             // words per depth in best / agree_max
   std::vector<void*> allocs;
 };
 
@@ -183,13 +184,14 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   if (E > 1) {
     E_ALLOC(e->crit, T * hist_nodes_max * F * (B - 1));
     E_ALLOC(e->agree, T * hist_nodes_max * F * (B - 1));
-    E_ALLOC(e->agree_max, T * nodes_max);
+    E_ALLOC(e->agree_max, 2 * T * nodes_max);
   }
   E_ALLOC(e->split_l, T * nodes_max);
   E_ALLOC(e->split_b, T * nodes_max);
   E_ALLOC(e->split_gain, T * nodes_max * E);
   E_ALLOC(e->leaf_val, T * nodes_max);
-  E_ALLOC(e->best, T * nodes_max);
+  E_ALLOC(e->best, 2 * T * nodes_max);
+  e->pick_stride = T * nodes_max;
   *out = e;
   return 0;
 }
@@ -265,10 +267,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   int cur = 0;
   hipLaunchKernelGGL(root_setup_kernel, dim3(blocks_for(std::max<int64_t>((int64_t)T * N, T * E), 256)),
                      dim3(256), 0, st, c.root_order, N, T, c.era_start, E, e->order[0],
-                     e->seg[0], e->present[0]);
+                     e->seg[0], e->present[0], e->totq[0], e->totc[0], e->best, e->agree_max);
   WGBM_LAUNCH_CHECK();
-  if (fill_u64(e->totq[0], (int64_t)T * E, 0, st) || fill_u64(e->totc[0], (int64_t)T * E, 0, st))
-    return WGBM_EINVAL;
   hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[0], (int64_t)0, T * E,
                      (const int32_t*)nullptr, e->part_tile_rows, (int32_t)e->max_ptiles, e->ptiles,
                      e->pkts, e->pn, (const uint32_t*)nullptr, 0, 0, (uint32_t*)nullptr,
@@ -294,6 +294,10 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     const int n_tn = T * nodes;
     const int n_keys = n_tn * E;
     const int hcur = d & 1, hprev = hcur ^ 1;
+    // split-pick words of this depth (cleared by the previous depth's
+    // level_finish, or by root_setup at depth 0)
+    unsigned long long* best = e->best + hcur * e->pick_stride;
+    int32_t* agree_max = e->agree_max ? e->agree_max + hcur * e->pick_stride : nullptr;
     if (d < D && e->des_direct) {
       // ---- E > 1, direct: per-era gains of every (node, era) segment
       const int64_t ncand = (int64_t)n_sel * (B - 1);
@@ -301,10 +305,6 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                              e->shifts, e->order[cur], e->seg[cur], E, nodes, e->present[cur],
                              e->local_of, n_sel, mcw, eps, e->sgain, e->sdir);
       if (r) return r;
-      if (fill_u64(e->best, n_tn, 0ull, st)) return WGBM_EINVAL;
-      hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st,
-                         e->agree_max, (int64_t)n_tn, 0);
-      WGBM_LAUNCH_CHECK();
       const int64_t W = (E + kDesEraBlock - 1) / kDesEraBlock;
       hipLaunchKernelGGL(des_alive_kernel, dim3(blocks_for((int64_t)n_tn * W, 256)), dim3(256), 0,
                          st, e->seg[cur], E, n_tn, mcw, e->alive);
@@ -315,14 +315,14 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       WGBM_LAUNCH_CHECK();
       hipLaunchKernelGGL(des_combine_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)),
                          dim3(256), 0, st, e->bsum, e->bdir, E, n_tn, ncand, e->present[cur],
-                         e->alive, e->crit, e->agree, e->agree_max);
+                         e->alive, e->crit, e->agree, agree_max);
       WGBM_LAUNCH_CHECK();
       hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)), dim3(256),
-                         0, st, e->crit, e->agree, e->agree_max, e->present[cur], n_tn, ncand, msg,
-                         e->best);
+                         0, st, e->crit, e->agree, agree_max, e->present[cur], n_tn, ncand, msg,
+                         best);
       WGBM_LAUNCH_CHECK();
       hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)n_tn * E, 256)), dim3(256), 0,
-                         st, e->best, (const int64_t*)nullptr, (const int32_t*)nullptr, F, B, E,
+                         st, best, (const int64_t*)nullptr, (const int32_t*)nullptr, F, B, E,
                          feat_sel, nodes, n_tn, e->shifts, mcw, eps, e->sgain, e->seg[cur], n_sel,
                          e->split_l, e->split_b, e->split_gain);
       WGBM_LAUNCH_CHECK();
@@ -382,59 +382,48 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       if (r) return r;
       // ---- split search + DES selection
       if (E == 1) {
-        if (fill_u64(e->best, n_tn, 0ull, st)) return WGBM_EINVAL;
+        // the pick is decoded by level_finish
         const int bpn = (n_sel + 255) / 256;
         hipLaunchKernelGGL(split_level_e1_kernel, dim3((unsigned)(n_tn * bpn)), dim3(256), 0, st,
                            e->hq[hcur], e->hc[hcur], F, B, feat_sel, n_sel, nodes,
-                           e->present[cur], e->shifts, mcw, eps, msg, e->best);
-        WGBM_LAUNCH_CHECK();
-        hipLaunchKernelGGL(split_decode_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st,
-                           e->best, n_tn, B, e->split_l, e->split_b, e->split_gain);
+                           e->present[cur], e->shifts, mcw, eps, msg, best);
         WGBM_LAUNCH_CHECK();
       } else {
         const int64_t ncand = (int64_t)n_sel * (B - 1);
         const int64_t nacc = (int64_t)n_tn * n_sel * ((B - 1 + kDesChunk - 1) / kDesChunk);
-        if (fill_u64(e->best, n_tn, 0ull, st)) return WGBM_EINVAL;
-        hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st,
-                           e->agree_max, (int64_t)n_tn, 0);
-        WGBM_LAUNCH_CHECK();
         hipLaunchKernelGGL(des_accumulate_kernel, dim3(blocks_for(nacc, 128)), dim3(128), 0, st,
                            e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, n_sel, nodes, n_tn,
                            e->present[cur], e->shifts, mcw, eps, e->crit, e->agree,
-                           e->agree_max);
+                           agree_max);
         WGBM_LAUNCH_CHECK();
         hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)),
-                           dim3(256), 0, st, e->crit, e->agree, e->agree_max, e->present[cur],
-                           n_tn, ncand, msg, e->best);
+                           dim3(256), 0, st, e->crit, e->agree, agree_max, e->present[cur],
+                           n_tn, ncand, msg, best);
         WGBM_LAUNCH_CHECK();
         hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)n_tn * E, 256)), dim3(256),
-                           0, st, e->best, e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, nodes,
+                           0, st, best, e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, nodes,
                            n_tn, e->shifts, mcw, eps, (const float*)nullptr,
                            (const int64_t*)nullptr, n_sel, e->split_l, e->split_b, e->split_gain);
         WGBM_LAUNCH_CHECK();
       }
-    } else {
-      hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks_for(n_tn, 256)), dim3(256), 0, st,
-                         e->split_l, (int64_t)n_tn, -1);
-      WGBM_LAUNCH_CHECK();
     }
-    // ---- leaf values and the tree record of this depth
-    hipLaunchKernelGGL(level_finish_kernel, dim3((unsigned)n_tn), dim3(64), 0, st, d, D, T,
-                       E, e->present[cur], e->split_l, e->split_b, e->split_gain, feat_sel,
-                       e->totq[cur], e->totc[cur], e->shifts, e->leaf_val, rec);
+    // ---- leaf values, the tree record of this depth, cleared words of the
+    // next depth (child totals, split picks)
+    const int nxt = cur ^ 1;
+    const bool e1_pick = d < D && !e->des_direct && E == 1;
+    hipLaunchKernelGGL(level_finish_kernel, dim3((unsigned)n_tn), dim3(64), 0, st, d, D, T, E, B,
+                       e->present[cur], e1_pick ? (const unsigned long long*)best : nullptr,
+                       e->split_l, e->split_b, e->split_gain, feat_sel, e->totq[cur],
+                       e->totc[cur], e->shifts, e->leaf_val, rec, e->totq[nxt], e->totc[nxt],
+                       e->best + (hcur ^ 1) * e->pick_stride,
+                       e->agree_max ? e->agree_max + (hcur ^ 1) * e->pick_stride : nullptr);
     WGBM_LAUNCH_CHECK();
     // ---- partition (or final leaf update)
-    const int nxt = cur ^ 1;
     hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur], (int64_t)0,
                        n_keys, (const int32_t*)nullptr, e->part_tile_rows, (int32_t)e->max_ptiles,
                        e->ptiles, e->pkts, e->pn, (const uint32_t*)nullptr, 0, 0,
                        (uint32_t*)nullptr, (int32_t*)nullptr);
     WGBM_LAUNCH_CHECK();
-    if (d < D) {
-      if (fill_u64(e->totq[nxt], (int64_t)n_keys * 2, 0, st) ||
-          fill_u64(e->totc[nxt], (int64_t)n_keys * 2, 0, st))
-        return WGBM_EINVAL;
-    }
     const int64_t pstride = c.objective == 0 ? 1 : T;
     const int64_t pcol = c.objective == 0 ? 0 : 1;
     hipLaunchKernelGGL(partition_count_kernel, dim3((unsigned)e->max_ptiles), dim3(256), 0, st,

@@ -74,16 +74,25 @@ __global__ void residual_softmax_kernel(const float* __restrict__ logits,
 __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_t n,
                                   int32_t T, const int64_t* __restrict__ era_start, int32_t E,
                                   int32_t* __restrict__ order, int64_t* __restrict__ seg,
-                                  int32_t* __restrict__ present) {
+                                  int32_t* __restrict__ present, int64_t* __restrict__ tot_q,
+                                  int64_t* __restrict__ tot_c, unsigned long long* __restrict__ best,
+                                  int32_t* __restrict__ agree_max) {
+  // root segments, cleared root totals and cleared depth-0 split-pick words
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid < (int64_t)T * n) order[gid] = root_order[gid % n];
   if (gid < (int64_t)T * E) {
     const int t = (int)(gid / E);
     const int e = (int)(gid - (int64_t)t * E);
     seg[gid] = (int64_t)t * n + era_start[e];
+    tot_q[gid] = 0;
+    tot_c[gid] = 0;
   }
   if (gid == 0) seg[(int64_t)T * E] = (int64_t)T * n;
-  if (gid < T) present[gid] = 1;
+  if (gid < T) {
+    present[gid] = 1;
+    best[gid] = 0ull;
+    if (agree_max) agree_max[gid] = 0;
+  }
 }
 
 // sum of quantised residuals and row count per segment (root totals)
@@ -118,16 +127,53 @@ __global__ __launch_bounds__(256) void segment_totals_kernel(
 //   computed from the exact quantised sum: float(ldexp(Sq, -s) / count)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void level_finish_kernel(
-    int32_t depth, int32_t max_depth, int32_t T, int32_t E, const int32_t* __restrict__ present,
-    const int32_t* __restrict__ split_l, const int32_t* __restrict__ split_b,
+    int32_t depth, int32_t max_depth, int32_t T, int32_t E, int32_t B,
+    const int32_t* __restrict__ present, const unsigned long long* __restrict__ best,
+    int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
     const float* __restrict__ split_gain_era, const int32_t* __restrict__ feat_sel,
     const int64_t* __restrict__ tot_q, const int64_t* __restrict__ tot_c,
-    const int32_t* __restrict__ shifts, float* __restrict__ leaf_val, TreeRecord rec) {
-  // one wave per (tree, node); the eras are spread over the lanes
+    const int32_t* __restrict__ shifts, float* __restrict__ leaf_val, TreeRecord rec,
+    int64_t* __restrict__ tot_q_next, int64_t* __restrict__ tot_c_next,
+    unsigned long long* __restrict__ best_next, int32_t* __restrict__ agree_max_next) {
+  // one wave per (tree, node); the eras are spread over the lanes.  The wave
+  // also clears the next depth's words of its two children: their per-era
+  // totals (accumulated by the partition) and their split-pick words.  With
+  // best != null (one era) the packed pick of the split search is decoded here.
   const int nodes = 1 << depth;
   const int tn = blockIdx.x;
   const int lane = threadIdx.x;
   if (tn >= T * nodes) return;
+  if (depth < max_depth) {
+    const int64_t c0 = (int64_t)2 * tn * E;
+    for (int k = lane; k < 2 * E; k += 64) {
+      tot_q_next[c0 + k] = 0;
+      tot_c_next[c0 + k] = 0;
+    }
+    if (depth + 1 < max_depth && lane < 2) {
+      best_next[2 * tn + lane] = 0ull;
+      if (agree_max_next) agree_max_next[2 * tn + lane] = 0;
+    }
+  }
+  int l = -1, b = -1;
+  float g1 = 0.0f;
+  if (depth < max_depth) {
+    if (best) {
+      const unsigned long long k = best[tn];
+      if (k != 0ull) {
+        const int idx = (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
+        l = idx / (B - 1);
+        b = idx - l * (B - 1);
+        g1 = gain_from_key((uint32_t)(k >> 32));
+      }
+      if (lane == 0) {
+        split_l[tn] = l;
+        split_b[tn] = b;
+      }
+    } else {
+      l = split_l[tn];
+      b = split_b[tn];
+    }
+  }
   const int t = tn / nodes;
   const int node = tn - t * nodes;
   const int64_t h = (int64_t)t * rec.H + (nodes - 1) + node;
@@ -149,12 +195,11 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
     sq += __shfl_xor(sq, o, 64);
     sc += __shfl_xor(sc, o, 64);
   }
-  const int l = depth < max_depth ? split_l[tn] : -1;
   if (lane == 0) {
     rec.count[h] = sc;
     if (l >= 0) {
       rec.feat[h] = feat_sel[l];
-      rec.bin[h] = split_b[tn];
+      rec.bin[h] = b;
       rec.leaf[h] = 0.0f;
     } else {
       const float v = (float)(ldexp((double)sq, -shifts[t]) / (double)sc);
@@ -164,8 +209,13 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
       rec.leaf[h] = v;
     }
   }
-  if (l >= 0)
-    for (int e = lane; e < E; e += 64) rec.gain[h * E + e] = split_gain_era[(int64_t)tn * E + e];
+  if (l >= 0) {
+    if (best) {
+      if (lane == 0) rec.gain[h] = g1;
+    } else {
+      for (int e = lane; e < E; e += 64) rec.gain[h * E + e] = split_gain_era[(int64_t)tn * E + e];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------

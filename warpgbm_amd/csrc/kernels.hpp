@@ -103,4 +103,13 @@ void timer_enable(int on);
 int timer_read(const char* tag, double* total_ms, long* count);
 void timer_reset();
 
+// order-preserving map of float bits to uint32 (and back)
+__device__ inline uint32_t gain_key(float g) {
+  const uint32_t u = __float_as_uint(g);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ inline float gain_from_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 }  // namespace wgbm

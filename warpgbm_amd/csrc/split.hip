@@ -97,15 +97,6 @@ __device__ inline bool des_segment_dead(int64_t n, float mcw) {
   return (float)n < 2.0f * mcw;
 }
 
-// order-preserving map of float bits to uint32 (and back)
-__device__ inline uint32_t gain_key(float g) {
-  const uint32_t u = __float_as_uint(g);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ inline float gain_from_key(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
-
 // One lane per (tree-node, local feature); the node's best candidate is kept
 // as a packed key  gain_key(gain) << 32 | (0xffffffff - flat index)  updated
 // with a 64-bit atomicMax, so the larger gain wins and, on equal gains, the
@@ -157,23 +148,6 @@ __global__ __launch_bounds__(256) void split_level_e1_kernel(
   }
 }
 
-// decode the packed best keys of a level into (local feature, bin, gain)
-__global__ void split_decode_kernel(const unsigned long long* __restrict__ best, int32_t n_tn,
-                                    int32_t B, int32_t* __restrict__ split_l,
-                                    int32_t* __restrict__ split_b, float* __restrict__ split_gain) {
-  const int tn = blockIdx.x * blockDim.x + threadIdx.x;
-  if (tn >= n_tn) return;
-  const unsigned long long k = best[tn];
-  if (k == 0ull) {
-    split_l[tn] = -1;
-    split_b[tn] = -1;
-    return;
-  }
-  const int idx = (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
-  split_l[tn] = idx / (B - 1);
-  split_b[tn] = idx % (B - 1);
-  split_gain[tn] = gain_from_key((uint32_t)(k >> 32));
-}
 
 // ---------------------------------------------------------------------------
 // engine: E > 1, without per-era gain/direction arrays.
