@@ -121,9 +121,13 @@ int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride
 
 /* Pre-binned int8 input (warpgbm/core.py:502-505): copy [n, n_feats] with
  * row stride x_stride bytes into the padded row-major and column-major
- * layouts used by wgbm_bin_matrix. */
+ * layouts used by wgbm_bin_matrix.  If over_flag (one int32 on the device) is
+ * not NULL it ends as 1 when some value is >= threshold, else 0: the
+ * reference's "every column max < num_bins" test (core.py:501-503) made in
+ * the same pass. */
 int wgbm_copy_prebinned(const int8_t* X, int64_t n, int32_t n_feats, int64_t x_stride,
-                        int8_t* codes_rm, int64_t codes_stride, int8_t* codes_cm, void* stream);
+                        int8_t* codes_rm, int64_t codes_stride, int8_t* codes_cm,
+                        int32_t threshold, int32_t* over_flag, void* stream);
 
 /* Single-launch ensemble inference over heap-ordered trees (replaces the
  * per-tree launches of warpgbm/core.py:1010-1026 and the single launch of

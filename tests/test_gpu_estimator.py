@@ -43,6 +43,10 @@ def test_c1_regression_bit_exact(gpu):
     p = m.predict(X)
     assert np.array_equal(bits(p), bits(ref.predict_codes(codes)))
     assert np.array_equal(bits(p), bits(ref.train_preds))
+    # tables rebuilt from the tree dicts (what a loaded or edited forest uses)
+    # predict exactly as the ones taken from the engine's records at fit
+    m._heap = None
+    assert np.array_equal(bits(m.predict(X)), bits(p))
     assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
     assert np.corrcoef(p, y)[0, 1] > 0.9
 
@@ -65,6 +69,8 @@ def test_multiclass_bit_exact(gpu):
         assert a == b, f"round {i} differs"
     proba = m.predict_proba(X)
     assert np.array_equal(bits(proba), bits(ref.predict_codes(codes)))
+    m._heap = None
+    assert np.array_equal(bits(m.predict_proba(X)), bits(proba))
     assert np.allclose(proba.sum(axis=1), 1.0, atol=1e-5)
     assert (m.predict(X) == y).mean() > 0.8
 
@@ -88,6 +94,26 @@ def test_era_des_prebinned_bit_exact(gpu):
     assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
     assert m.per_era_feature_importance_.shape == (E, F)
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
+
+
+def test_int8_input_over_num_bins_is_quantile_binned(gpu):
+    """int8 input with a value >= num_bins fails the pre-binned test
+    (warpgbm/core.py:501-503) and is quantile-binned as float32, at fit and
+    at predict."""
+    print_case("estimator", "int8 not pre-binned")
+    rng = np.random.default_rng(5)
+    N, F = 4000, 9
+    X = rng.integers(-4, 5, (N, F)).astype(np.int8)
+    X[N - 1, F - 1] = 7  # one value >= num_bins = 6
+    y = (X[:, 0] * 0.5 + X[:, 1] - X[:, 2] + rng.standard_normal(N)).astype(F32)
+    m = WarpGBM(num_bins=6, max_depth=3, n_estimators=5, learning_rate=0.3)
+    m.fit(X, y)
+    Xf = X.astype(F32)
+    codes = oracle_codes(m, Xf)
+    ref = gbm.Forest(num_bins=6, max_depth=3, n_estimators=5, learning_rate=0.3).fit_codes(codes, y)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
 
 
 @pytest.mark.parametrize("mcw", [1, 20])

@@ -240,6 +240,19 @@ def test_copy_prebinned(gpu):
     assert np.array_equal(rm[:, :300], X.astype(np.int8))
     assert np.all(rm[:, 300:] == -1)
     assert np.array_equal(c.cm.cpu().numpy(), X.astype(np.int8).T)
+    # the in-pass "every value < num_bins" test, at and around the boundary,
+    # against the host's column maxima (warpgbm/core.py:501-503)
+    X8 = rng.integers(-128, 5, (70_001, 129)).astype(np.int8)
+    x8 = D.upload_int8(X8, dev)
+    for thr in (4, 5, 6, 127):
+        c, over = D.codes_from_int8(x8, with_cm=False, threshold=thr)
+        assert over == (not np.all(X8.max(axis=0) < thr)), thr
+        assert np.array_equal(c.rm.cpu().numpy()[:, :129], X8)
+    X8[69_999, 128] = 17
+    c, over = D.codes_from_int8(D.upload_int8(X8, dev), with_cm=True, threshold=17)
+    assert over and np.array_equal(c.cm.cpu().numpy(), X8.T)
+    c, over = D.codes_from_int8(D.upload_int8(X8, dev), with_cm=True, threshold=18)
+    assert not over
 
 
 @pytest.mark.parametrize("B", [2, 5, 32, 127])

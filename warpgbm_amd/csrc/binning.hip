@@ -104,25 +104,34 @@ __global__ void pad_codes_kernel(int8_t* __restrict__ codes_rm, int64_t n, int64
   codes_rm[r * S + from + (gid - r * w)] = (int8_t)-1;
 }
 
-// pre-binned int8 input [n, F] (row stride xs bytes) -> padded row-major + column-major
+// pre-binned int8 input [n, F] (row stride xs bytes) -> padded row-major + column-major.
+// With over != null, a workgroup that copies a value >= threshold stores 1
+// there (plain stores of one value: no atomics; the flag is cleared before).
 __global__ __launch_bounds__(256) void copy_prebinned_kernel(const int8_t* __restrict__ X,
                                                              int64_t n, int32_t F, int64_t xs,
                                                              int8_t* __restrict__ codes_rm,
                                                              int64_t S,
-                                                             int8_t* __restrict__ codes_cm) {
+                                                             int8_t* __restrict__ codes_cm,
+                                                             int32_t threshold,
+                                                             int32_t* __restrict__ over) {
   __shared__ int8_t tcode[BT_F][BT_R + 4];
   const int64_t r0 = (int64_t)blockIdx.x * BT_R;
   const int f0 = blockIdx.y * BT_F;
   const int tid = threadIdx.x;
   const int fl = tid & 63;
   const int f = f0 + fl;
+  int hit = 0;
   for (int k = tid >> 6; k < BT_R; k += 4) {
     const int64_t r = r0 + k;
     int8_t c = -1;
-    if (r < n && f < F) c = X[r * xs + f];
+    if (r < n && f < F) {
+      c = X[r * xs + f];
+      hit |= (int)c >= threshold;
+    }
     tcode[fl][k] = c;
     if (r < n && f < S) codes_rm[r * S + f] = c;
   }
+  if (over && __syncthreads_or(hit) && tid == 0) over[0] = 1;
   __syncthreads();
   if (codes_cm) {
     const int rl = tid & 63;

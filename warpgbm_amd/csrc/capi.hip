@@ -278,14 +278,19 @@ int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride
 }
 
 int wgbm_copy_prebinned(const int8_t* X, int64_t n, int32_t n_feats, int64_t x_stride,
-                        int8_t* codes_rm, int64_t codes_stride, int8_t* codes_cm, void* stream) {
+                        int8_t* codes_rm, int64_t codes_stride, int8_t* codes_cm,
+                        int32_t threshold, int32_t* over_flag, void* stream) {
   WGBM_REQUIRE(n >= 0 && n_feats >= 1 && x_stride >= n_feats && codes_stride >= n_feats,
                "bad copy_prebinned shape");
+  if (over_flag) {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, S(stream), over_flag, (int64_t)1, 0);
+    WGBM_LAUNCH_CHECK();
+  }
   if (n == 0) return 0;
   WGBM_REQUIRE(X && codes_rm, "null pointer");
   dim3 grid(nblocks(n, 64), nblocks(n_feats, 64));
   hipLaunchKernelGGL(copy_prebinned_kernel, grid, dim3(256), 0, S(stream), X, n, n_feats,
-                     x_stride, codes_rm, codes_stride, codes_cm);
+                     x_stride, codes_rm, codes_stride, codes_cm, threshold, over_flag);
   WGBM_LAUNCH_CHECK();
   const int64_t covered = (int64_t)grid.y * 64;
   if (codes_stride > covered) {

@@ -140,7 +140,8 @@ __global__ void bin_matrix_kernel(const float* X, int64_t n, int32_t F, int64_t 
                                   int64_t S, int8_t* codes_cm);
 __global__ void pad_codes_kernel(int8_t* codes_rm, int64_t n, int64_t S, int32_t from);
 __global__ void copy_prebinned_kernel(const int8_t* X, int64_t n, int32_t F, int64_t xs,
-                                      int8_t* codes_rm, int64_t S, int8_t* codes_cm);
+                                      int8_t* codes_rm, int64_t S, int8_t* codes_cm,
+                                      int32_t threshold, int32_t* over);
 __global__ void quantile_edges_kernel(const float* sorted, int64_t n, int32_t F,
                                       const float* q, int32_t nq, float* edges);
 __global__ void transpose_keys_kernel(const float* X, int64_t n, int32_t F, int64_t xs,

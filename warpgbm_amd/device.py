@@ -58,14 +58,31 @@ def upload_prebinned(X: np.ndarray, dev, with_cm: bool) -> Codes:
     """Integer input whose columns are all < num_bins is used as codes directly
     (warpgbm/core.py:499-517); values are cast to int8 like the reference's
     ``bin_indices[:, f] = torch.as_tensor(X[:, f])``."""
-    n, F = X.shape
-    x8 = torch.from_numpy(np.ascontiguousarray(X).astype(np.int8, copy=False)).to(dev)
+    X = np.asarray(X)
+    x8 = upload_int8(X if X.dtype == np.int8 else X.astype(np.int8), dev)
+    return codes_from_int8(x8, with_cm)[0]
+
+
+def upload_int8(X: np.ndarray, dev) -> torch.Tensor:
+    """int8 [n, F] contiguous copy of an int8 host matrix on the device."""
+    return _upload_staged(X, dev, np.int8, torch.int8)
+
+
+def codes_from_int8(x8: torch.Tensor, with_cm: bool, threshold: int | None = None):
+    """Codes from an int8 [n, F] device matrix (``wgbm_copy_prebinned``).
+    With a threshold, also whether some value is >= threshold (found in the
+    same pass over the matrix); else None."""
+    n, F = x8.shape
+    dev = x8.device
     c = _alloc_codes(n, F, dev, with_cm)
+    flag = torch.empty(1, dtype=torch.int32, device=dev) if threshold is not None else None
     lib = _lib.load()
     rc = lib.wgbm_copy_prebinned(x8.data_ptr(), n, F, F, c.rm.data_ptr(), c.stride,
-                                 c.cm.data_ptr() if c.cm is not None else None, _stream(dev))
+                                 c.cm.data_ptr() if c.cm is not None else None,
+                                 int(threshold) if threshold is not None else 0,
+                                 flag.data_ptr() if flag is not None else None, _stream(dev))
     _lib.check(rc, "copy_prebinned")
-    return c
+    return c, (bool(flag.item()) if flag is not None else None)
 
 
 _STAGE_BYTES = 64 << 20   # one pinned staging buffer
@@ -89,17 +106,23 @@ def _staging():
 
 def upload_float(X: np.ndarray, dev) -> torch.Tensor:
     """float32 [n, F] contiguous copy of X on the device (float64 input is
-    rounded to float32 first, as ``torch.as_tensor(..., dtype=float32)``).
+    rounded to float32 first, as ``torch.as_tensor(..., dtype=float32)``)."""
+    return _upload_staged(X, dev, np.float32, torch.float32)
+
+
+def _upload_staged(X: np.ndarray, dev, np_dtype, torch_dtype) -> torch.Tensor:
+    """[n, F] contiguous copy of X on the device in np_dtype.
 
     Large inputs are streamed through pinned staging buffers: host threads
     fill one buffer (converting the dtype on the way) while the DMA engine
     copies the previous ones on a side stream."""
     X = np.asarray(X)
     n, F = X.shape
-    row_bytes = 4 * max(F, 1)
+    esize = np.dtype(np_dtype).itemsize
+    row_bytes = esize * max(F, 1)
     if n * row_bytes < 4 * _STAGE_BYTES or not X.flags.c_contiguous:
-        return torch.from_numpy(np.ascontiguousarray(X, dtype=np.float32)).to(dev)
-    out = torch.empty((n, F), dtype=torch.float32, device=dev)
+        return torch.from_numpy(np.ascontiguousarray(X, dtype=np_dtype)).to(dev)
+    out = torch.empty((n, F), dtype=torch_dtype, device=dev)
     bufs, pool = _staging()
     rows_per = max(1, _STAGE_BYTES // row_bytes)
     side = torch.cuda.Stream(device=dev)
@@ -115,7 +138,7 @@ def upload_float(X: np.ndarray, dev) -> torch.Tensor:
         k = i % len(bufs)
         if events[k] is not None:
             events[k].synchronize()  # the DMA that used this buffer has finished
-        host = bufs[k][: (r1 - r0) * row_bytes].view(torch.float32).view(r1 - r0, F)
+        host = bufs[k][: (r1 - r0) * row_bytes].view(torch_dtype).view(r1 - r0, F)
         dst = host.numpy()
         step = max(1, (r1 - r0 + nthreads - 1) // nthreads)
         list(pool.map(lambda a: fill(dst, a, min(a + step, r1 - r0)), range(0, r1 - r0, step)))
