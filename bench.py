@@ -134,13 +134,13 @@ def main():
     N, F, B = args.rows, args.feats, 32
     print(f"[bench] generating C2 inputs {N}x{F}", file=sys.stderr, flush=True)
     codes_h, grad_h, node_h = c2_inputs(N, F)
-    # the library's code layout: rows padded to a 128-byte multiple with -1
-    # (what the binner writes); algorithmic bytes still count F bytes per row
-    from warpgbm_amd.device import codes_stride
+    # the codes in the library's native layout, made by the pre-binned ingest
+    # (what fit() does with int8 input): rows padded to a 128-byte multiple,
+    # every byte in [0, B + 1]; algorithmic bytes still count F bytes per row
+    from warpgbm_amd import device as D
 
-    S = codes_stride(F)
-    codes = torch.full((N, S), -1, dtype=torch.int8, device=dev)
-    codes[:, :F] = torch.from_numpy(codes_h).to(dev)
+    nat = D.codes_from_int8(torch.from_numpy(codes_h).to(dev), False, B)[0]
+    codes, S = nat.rm, nat.stride
     grad = torch.from_numpy(grad_h).to(dev)
     order16_h = np.argsort(node_h, kind="stable").astype(np.int32)
     seg16_h = np.zeros(17, np.int64)
@@ -154,13 +154,15 @@ def main():
     H16 = torch.zeros_like(G16)
     stream = _lib.current_stream_ptr(dev)
 
+    flags = _lib.CODES_NATIVE
+
     def step():
         _lib.check(lib.wgbm_histogram_segments(codes.data_ptr(), N, S, F, grad.data_ptr(), None,
-                                               seg1.data_ptr(), 1, N, B, G1.data_ptr(),
+                                               seg1.data_ptr(), 1, N, B, flags, G1.data_ptr(),
                                                H1.data_ptr(), stream), "hist root")
         _lib.check(lib.wgbm_histogram_segments(codes.data_ptr(), N, S, F, grad.data_ptr(),
                                                order16.data_ptr(), seg16.data_ptr(), 16, N, B,
-                                               G16.data_ptr(), H16.data_ptr(), stream),
+                                               flags, G16.data_ptr(), H16.data_ptr(), stream),
                    "hist 16 nodes")
 
     for _ in range(args.warmup):
@@ -220,7 +222,7 @@ def main():
                          f"(exact sums), 1 thread, {dt:.2f} s on {cpu_model()}"}
         print(f"[bench] cpu baseline {cpu['value']} GB/s ({dt:.2f} s)", file=sys.stderr, flush=True)
 
-    del codes, grad, order16, G16, H16
+    del nat, codes, grad, order16, G16, H16
     torch.cuda.empty_cache()
 
     e2e = {}
@@ -273,7 +275,7 @@ def main():
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(k_achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(k_achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "hist_tiles_kernel<4,0,32,*>",
+                     "traffic": traffic, "kernel": "hist_tiles_kernel<4,0,32,*,true> (native codes)",
                      "kernel_ms": round(k_ms, 4),
                      # the binding unit in practice: one 64-bit LDS atomic per
                      # (row, feature); peak = wgbm_probe_lds_atomics, measured

@@ -85,16 +85,26 @@ int wgbm_predict_forest(const int8_t* bin_indices, int64_t n, int64_t n_feats,
  * per-node / per-feature / per-tree reference calls named in its comment).
  * ------------------------------------------------------------------------ */
 
+/* Native code layout: codes written by wgbm_bin_matrix (num_bins = n_edges
+ * + 1) or wgbm_copy_prebinned (for num_bins).  Every byte of every row is in
+ * [0, num_bins + 1]: a code c in [0, num_bins) is stored as c, a negative
+ * code as num_bins, a code >= num_bins and every padding byte as
+ * num_bins + 1.  The column-major copy keeps the raw codes. */
+#define WGBM_CODES_NATIVE 1
+
 /* Multi-segment histogram: the positions order[seg[k] .. seg[k+1]) are the
  * rows of segment k (a node; cf. the per-node sample_indices of
  * warpgbm/core.py:551-562).  codes: int8 [n_rows, stride] row-major,
- * features 0..n_feats-1.  G, H: float32 [n_seg, n_feats, num_bins],
+ * features 0..n_feats-1; codes outside [0, num_bins) are skipped.  flags:
+ * 0 for any int8 codes, or WGBM_CODES_NATIVE when the codes are in the native
+ * layout for this num_bins (a faster kernel that relies on every byte being
+ * in [0, num_bins + 1]).  G, H: float32 [n_seg, n_feats, num_bins],
  * accumulated into.  seg is a device int64 array [n_seg + 1]; n_pos is
  * seg[n_seg] (known to the caller). */
 int wgbm_histogram_segments(const int8_t* codes, int64_t n_rows, int64_t stride, int32_t n_feats,
                             const float* residuals, const int32_t* order, const int64_t* seg,
-                            int32_t n_seg, int64_t n_pos, int32_t num_bins, float* G, float* H,
-                            void* stream);
+                            int32_t n_seg, int64_t n_pos, int32_t num_bins, int32_t flags,
+                            float* G, float* H, void* stream);
 
 /* Quantile edges (the torch.quantile call of warpgbm/core.py:529-534) from
  * columns already sorted ascending (NaN last): sorted float32 [n_feats, n];
@@ -113,32 +123,35 @@ int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64
 /* Batched binner (the per-feature loop of warpgbm/core.py:527-538 and
  * 908-913 in one launch).  X float32 [n, n_feats] with row stride x_stride
  * (elements); edges float32 [n_feats, n_edges] sorted per feature.  Writes
- * codes_rm int8 [n, codes_stride] (padding bytes = -1) and, if codes_cm is
- * not NULL, codes_cm int8 [n_feats, n] (column-major copy). */
+ * codes_rm int8 [n, codes_stride] in the native layout for num_bins =
+ * n_edges + 1 (codes in [0, n_edges], padding bytes n_edges + 2) and, if
+ * codes_cm is not NULL, codes_cm int8 [n_feats, n] (column-major copy). */
 int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride,
                     const float* edges, int32_t n_edges, int8_t* codes_rm, int64_t codes_stride,
                     int8_t* codes_cm, void* stream);
 
 /* Pre-binned int8 input (warpgbm/core.py:502-505): copy [n, n_feats] with
- * row stride x_stride bytes into the padded row-major and column-major
- * layouts used by wgbm_bin_matrix.  If over_flag (one int32 on the device) is
- * not NULL it ends as 1 when some value is >= threshold, else 0: the
- * reference's "every column max < num_bins" test (core.py:501-503) made in
- * the same pass. */
+ * row stride x_stride bytes into the native row-major layout for num_bins
+ * (2..127) and the raw column-major copy, as wgbm_bin_matrix.  If over_flag
+ * (one int32 on the device) is not NULL it ends as 1 when some value is
+ * >= num_bins, else 0: the reference's "every column max < num_bins" test
+ * (core.py:501-503) made in the same pass. */
 int wgbm_copy_prebinned(const int8_t* X, int64_t n, int32_t n_feats, int64_t x_stride,
                         int8_t* codes_rm, int64_t codes_stride, int8_t* codes_cm,
-                        int32_t threshold, int32_t* over_flag, void* stream);
+                        int32_t num_bins, int32_t* over_flag, void* stream);
 
 /* Single-launch ensemble inference over heap-ordered trees (replaces the
  * per-tree launches of warpgbm/core.py:1010-1026 and the single launch of
  * :928-930).  Tree t = round * K + k, node h has children 2h+1 / 2h+2;
  * feat[t*H + h] >= 0 splits on that feature (left if code <= bin), -1 is a
  * leaf with value leaf[t*H + h].  out float32 [n, K] row-major, pre-filled
- * with the initial scores; tree contributions added round by round. */
-int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, const int32_t* feat,
-                      const int32_t* bin, const float* leaf, int32_t n_rounds, int32_t K,
-                      int32_t H, int32_t max_depth, float learning_rate, float* out,
-                      void* stream);
+ * with the initial scores; tree contributions added round by round.  codes:
+ * native layout for num_bins (negative codes go left, codes >= num_bins go
+ * right, as the raw int8 compare of the reference). */
+int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int32_t num_bins,
+                      const int32_t* feat, const int32_t* bin, const float* leaf,
+                      int32_t n_rounds, int32_t K, int32_t H, int32_t max_depth,
+                      float learning_rate, float* out, void* stream);
 
 /* In-place row softmax of float32 [n, K] (warpgbm/metrics.py:12-15). */
 int wgbm_softmax_rows(float* x, int64_t n, int32_t K, void* stream);
@@ -163,7 +176,7 @@ typedef struct wgbm_engine_config {
   float min_split_gain;
   float l2_reg;
   float learning_rate;
-  const int8_t* codes_rm;     /* [n_rows, codes_stride] */
+  const int8_t* codes_rm;     /* [n_rows, codes_stride], native layout */
   const int8_t* codes_cm;     /* [n_feats, n_rows] */
   const int32_t* root_order;  /* [n_rows] row ids sorted by era, ascending inside */
   const int64_t* era_start;   /* [num_eras + 1] */

@@ -96,6 +96,33 @@ def test_era_des_prebinned_bit_exact(gpu):
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
 
 
+@pytest.mark.parametrize("E", [1, 3])
+def test_prebinned_negative_and_wrapped_codes_bit_exact(gpu, E):
+    """Pre-binned integer input with negative values: every column max is
+    < num_bins, so it is used as codes (warpgbm/core.py:499-505), cast to
+    int8 (values below -128 wrap, e.g. -200 -> 56 >= num_bins).  Codes outside
+    [0, num_bins) are skipped by the histograms (histogram_kernel.cu:41) and
+    compared as signed int8 by the partition and predict (core.py:629,
+    predict.cu:43): negative codes go left, wrapped ones >= num_bins right."""
+    print_case("estimator", "pre-binned negative codes E", E)
+    rng = np.random.default_rng(8)
+    N, F, B = 5000, 14, 10
+    X = rng.integers(-2, B, (N, F)).astype(np.int64)
+    X[rng.random((N, F)) < 0.05] = -200           # wraps to int8 56
+    era = np.repeat(np.arange(E), N // E + 1)[:N]
+    score = np.clip(X[:, :4], -1, None).sum(axis=1) + rng.standard_normal(N)
+    y = (score / 5.0).astype(F32)
+    kw = dict(num_bins=B, max_depth=4, n_estimators=5, learning_rate=0.4, min_child_weight=5)
+    m = WarpGBM(**kw).fit(X, y, era_id=era)
+    codes = X.astype(np.int8)
+    assert (codes >= B).any() and (codes < 0).any()
+    ref = gbm.Forest(**kw).fit_codes(codes, y, era_id=era)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
+    assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
+
+
 def test_int8_input_over_num_bins_is_quantile_binned(gpu):
     """int8 input with a value >= num_bins fails the pre-binned test
     (warpgbm/core.py:501-503) and is quantile-binned as float32, at fit and

@@ -173,13 +173,29 @@ def test_predict_forest_bit_exact(gpu):
     assert np.array_equal(bits(out.cpu().numpy()), bits(ref))
 
 
-def test_histogram_segments_bit_exact(gpu):
-    print_case("histogram_segments", "16 nodes")
-    rng = np.random.default_rng(5)
-    N, F, B, S = 40000, 200, 32, 16
+def native_layout(raw, num_bins, stride):
+    """The library's native row-major code layout (include/warpgbm_amd.h):
+    codes in [0, B) as is, negative codes B, codes >= B and padding B + 1."""
+    n, F = raw.shape
+    out = np.full((n, stride), num_bins + 1, np.int16)
+    r = raw.astype(np.int16)
+    out[:, :F] = np.where(r < 0, num_bins, np.where(r >= num_bins, num_bins + 1, r))
+    return out.astype(np.uint8).view(np.int8)
+
+
+@pytest.mark.parametrize("B", [32, 5, 50, 126, 127])
+@pytest.mark.parametrize("native", [False, True])
+def test_histogram_segments_bit_exact(gpu, native, B):
+    """16 node segments of raw codes with values outside [0, B) (negative and
+    >= B: skipped, histogram_kernel.cu:41), through the raw-code kernel and
+    through the native layout made by the pre-binned copy; both equal the
+    oracle on the raw codes.  B = 127 has no native-layout kernel (its rows
+    would not fit a byte) and takes the clamping one."""
+    print_case("histogram_segments", "16 nodes", "native" if native else "raw", B)
+    rng = np.random.default_rng(5 + B)
+    N, F, S = 40000, 203, 16
     stride = D.codes_stride(F)
-    codes = np.full((N, stride), -1, np.int8)
-    codes[:, :F] = rng.integers(0, B, (N, F))
+    raw = rng.integers(-3, B + 3, (N, F)).astype(np.int8)
     resid = rng.standard_normal(N).astype(F32)
     node = rng.integers(0, S, N)
     order = np.argsort(node, kind="stable").astype(np.int32)
@@ -190,10 +206,18 @@ def test_histogram_segments_bit_exact(gpu):
     from warpgbm_amd import _lib
 
     lib = _lib.load()
+    if native:
+        c = D.codes_from_int8(t(raw), False, B)[0]
+        assert np.array_equal(c.rm.cpu().numpy(), native_layout(raw, B, stride))
+        codes_d, flags = c.rm, _lib.CODES_NATIVE
+    else:
+        padded = np.full((N, stride), -1, np.int8)
+        padded[:, :F] = raw
+        codes_d, flags = t(padded), 0
     # keep the device tensors alive until the asynchronous call has run
-    codes_d, resid_d, order_d, seg_d = t(codes), t(resid), t(order), t(seg)
+    resid_d, order_d, seg_d = t(resid), t(order), t(seg)
     rc = lib.wgbm_histogram_segments(codes_d.data_ptr(), N, stride, F, resid_d.data_ptr(),
-                                     order_d.data_ptr(), seg_d.data_ptr(), S, N, B,
+                                     order_d.data_ptr(), seg_d.data_ptr(), S, N, B, flags,
                                      G.data_ptr(), H.data_ptr(),
                                      _lib.current_stream_ptr(dev))
     _lib.check(rc, "histogram_segments")
@@ -202,7 +226,7 @@ def test_histogram_segments_bit_exact(gpu):
     q = ops.quantise(resid, s)
     Gc, Hc = G.cpu().numpy(), H.cpu().numpy()
     for k in range(S):
-        Q, C = ops.histogram_exact_q(codes, q, order[seg[k]:seg[k + 1]], np.arange(F), None, 1, B)
+        Q, C = ops.histogram_exact_q(raw, q, order[seg[k]:seg[k + 1]], np.arange(F), None, 1, B)
         assert np.array_equal(Hc[k], C[0].astype(F32))
         assert np.array_equal(bits(Gc[k]), bits(ops.dequantise(Q[0], s)))
 
@@ -226,7 +250,7 @@ def test_quantile_edges_and_bin_matrix(gpu):
     cm = codes.cm.cpu().numpy()
     ref = ops.bin_matrix(X, edges)
     assert np.array_equal(rm[:, :F], ref)
-    assert np.all(rm[:, F:] == -1)
+    assert np.all(rm[:, F:] == B + 1)  # native layout padding
     assert np.array_equal(cm, ref.T)
     assert np.all(ref[:, 5] == 0)
 
@@ -235,23 +259,21 @@ def test_copy_prebinned(gpu):
     print_case("copy_prebinned")
     rng = np.random.default_rng(7)
     X = rng.integers(-3, 5, (5000, 300)).astype(np.int64)
-    c = D.upload_prebinned(X, dev, with_cm=True)
-    rm = c.rm.cpu().numpy()
-    assert np.array_equal(rm[:, :300], X.astype(np.int8))
-    assert np.all(rm[:, 300:] == -1)
-    assert np.array_equal(c.cm.cpu().numpy(), X.astype(np.int8).T)
+    c = D.upload_prebinned(X, dev, with_cm=True, num_bins=5)
+    assert np.array_equal(c.rm.cpu().numpy(), native_layout(X.astype(np.int8), 5, c.stride))
+    assert np.array_equal(c.cm.cpu().numpy(), X.astype(np.int8).T)  # raw codes
     # the in-pass "every value < num_bins" test, at and around the boundary,
     # against the host's column maxima (warpgbm/core.py:501-503)
     X8 = rng.integers(-128, 5, (70_001, 129)).astype(np.int8)
     x8 = D.upload_int8(X8, dev)
     for thr in (4, 5, 6, 127):
-        c, over = D.codes_from_int8(x8, with_cm=False, threshold=thr)
+        c, over = D.codes_from_int8(x8, False, thr, check=True)
         assert over == (not np.all(X8.max(axis=0) < thr)), thr
-        assert np.array_equal(c.rm.cpu().numpy()[:, :129], X8)
+        assert np.array_equal(c.rm.cpu().numpy(), native_layout(X8, thr, c.stride))
     X8[69_999, 128] = 17
-    c, over = D.codes_from_int8(D.upload_int8(X8, dev), with_cm=True, threshold=17)
+    c, over = D.codes_from_int8(D.upload_int8(X8, dev), True, 17, check=True)
     assert over and np.array_equal(c.cm.cpu().numpy(), X8.T)
-    c, over = D.codes_from_int8(D.upload_int8(X8, dev), with_cm=True, threshold=18)
+    c, over = D.codes_from_int8(D.upload_int8(X8, dev), True, 18, check=True)
     assert not over
 
 

@@ -13,6 +13,9 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libwarpgbm_amd.so"
 
+# flags of wgbm_histogram_segments (include/warpgbm_amd.h)
+CODES_NATIVE = 1
+
 _p = C.c_void_p
 _i32 = C.c_int32
 _i64 = C.c_int64
@@ -28,13 +31,13 @@ SIGNATURES = {
     "wgbm_custom_cuda_binner": (C.c_int, [_p, _i64, _p, _i32, _p, _p]),
     "wgbm_predict_forest": (C.c_int, [_p, _i64, _i64, _p, _i64, _i64, _f32, _p, _p]),
     "wgbm_histogram_segments": (C.c_int, [_p, _i64, _i64, _i32, _p, _p, _p, _i32, _i64, _i32,
-                                          _p, _p, _p]),
+                                          _i32, _p, _p, _p]),
     "wgbm_quantile_edges": (C.c_int, [_p, _i64, _i32, _p, _i32, _p, _p]),
     "wgbm_quantile_edges_matrix": (C.c_int, [_p, _i64, _i32, _i64, _p, _i32, _p, _p]),
     "wgbm_bin_matrix": (C.c_int, [_p, _i64, _i32, _i64, _p, _i32, _p, _i64, _p, _p]),
     "wgbm_copy_prebinned": (C.c_int, [_p, _i64, _i32, _i64, _p, _i64, _p, _i32, _p, _p]),
-    "wgbm_predict_heap": (C.c_int, [_p, _i64, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _f32,
-                                    _p, _p]),
+    "wgbm_predict_heap": (C.c_int, [_p, _i64, _i64, _i32, _p, _p, _p, _i32, _i32, _i32, _i32,
+                                    _f32, _p, _p]),
     "wgbm_softmax_rows": (C.c_int, [_p, _i64, _i32, _p]),
     "wgbm_engine_create": (C.c_int, [C.POINTER(_p), _p]),
     "wgbm_engine_round": (C.c_int, [_p, _p, _p, _p, _i32, _p, _p]),

@@ -293,13 +293,13 @@ class WarpGBM(BaseEstimator, RegressorMixin):
             return None, None
         if X_np.dtype == np.int8 and X_np.shape[0] > 0:
             x8 = D.upload_int8(X_np, dev)
-            codes, over = D.codes_from_int8(x8, with_cm, threshold=self.num_bins)
+            codes, over = D.codes_from_int8(x8, with_cm, self.num_bins, check=True)
             if not over:
                 return codes, None
             del codes
             return None, x8.to(torch.float32)
         if X_np.shape[0] == 0 or bool(np.all(X_np.max(axis=0) < self.num_bins)):
-            return D.upload_prebinned(X_np, dev, with_cm), None
+            return D.upload_prebinned(X_np, dev, with_cm, self.num_bins), None
         return None, None
 
     def _new_engine(self, codes, root_order, era_start, n_trees, objective):

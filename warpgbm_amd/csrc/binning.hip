@@ -47,9 +47,22 @@ __device__ inline int count_le(const float* e, int ne, float v) {
 }
 
 // ---------------------------------------------------------------------------
+// The row-major code matrix codes_rm [n, S] is this library's own layout
+// ("native codes"), read by the histogram kernels and the heap predictor:
+// with B = num_bins, every byte is in [0, B + 1]:
+//   a code c of a real feature    -> c        if 0 <= c < B
+//                                 -> B        if c < 0   (routed left)
+//                                 -> B + 1    if c >= B  (routed right)
+//   padding bytes F..S-1          -> B + 1.
+// Histograms drop both B and B + 1 (the reference skips codes outside
+// [0, B): histogram_kernel.cu:41), and a kernel that knows every byte is in
+// range needs no clamp.  The column-major copy codes_cm [F, n] keeps the raw
+// signed codes (the partition compares them as the reference does,
+// core.py:629).
+//
 // batched binner: X [n, F] row-major float32 (row stride xs floats) ->
-//   codes_rm [n, S] int8 (S >= F; bytes F..S-1 set to -1) and, if non-null,
-//   codes_cm [F, n] int8 (column-major, for the row partition).
+//   codes_rm [n, S] (native; the binner's codes are in [0, n_edges] and
+//   num_bins = n_edges + 1) and, if non-null, codes_cm [F, n].
 // workgroup: 64 rows x 64 features; edges of its 64 features staged in LDS.
 // ---------------------------------------------------------------------------
 constexpr int BT_R = 64, BT_F = 64;
@@ -72,15 +85,16 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
   // each thread: feature column fl = tid & 63, rows (tid >> 6) + 4k
   const int fl = tid & 63;
   const int f = f0 + fl;
+  const int8_t pad = (int8_t)(n_edges + 2);  // num_bins + 1
   for (int k = tid >> 6; k < BT_R; k += 4) {
     const int64_t r = r0 + k;
-    int8_t c = -1;
+    int8_t c = pad;
     if (r < n && f < F) {
       const float v = X[r * xs + f];
       c = (int8_t)count_le(sedge + fl * n_edges, n_edges, v);
     }
     tcode[fl][k] = c;
-    if (r < n && f < S) codes_rm[r * S + f] = c;  // padding columns get -1
+    if (r < n && f < S) codes_rm[r * S + f] = c;
   }
   __syncthreads();
   if (codes_cm) {
@@ -96,23 +110,24 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
 
 // padding bytes beyond the last 64-feature tile (S > round_up(F, 64))
 __global__ void pad_codes_kernel(int8_t* __restrict__ codes_rm, int64_t n, int64_t S,
-                                 int32_t from) {
+                                 int32_t from, int8_t value) {
   const int64_t w = S - from;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= n * w) return;
   const int64_t r = gid / w;
-  codes_rm[r * S + from + (gid - r * w)] = (int8_t)-1;
+  codes_rm[r * S + from + (gid - r * w)] = value;
 }
 
-// pre-binned int8 input [n, F] (row stride xs bytes) -> padded row-major + column-major.
-// With over != null, a workgroup that copies a value >= threshold stores 1
-// there (plain stores of one value: no atomics; the flag is cleared before).
+// pre-binned int8 input [n, F] (row stride xs bytes) -> native row-major
+// codes for num_bins B + raw column-major copy.  With over != null, a
+// workgroup that copies a value >= B stores 1 there (plain stores of one
+// value: no atomics; the flag is cleared before).
 __global__ __launch_bounds__(256) void copy_prebinned_kernel(const int8_t* __restrict__ X,
                                                              int64_t n, int32_t F, int64_t xs,
                                                              int8_t* __restrict__ codes_rm,
                                                              int64_t S,
                                                              int8_t* __restrict__ codes_cm,
-                                                             int32_t threshold,
+                                                             int32_t num_bins,
                                                              int32_t* __restrict__ over) {
   __shared__ int8_t tcode[BT_F][BT_R + 4];
   const int64_t r0 = (int64_t)blockIdx.x * BT_R;
@@ -121,15 +136,17 @@ __global__ __launch_bounds__(256) void copy_prebinned_kernel(const int8_t* __res
   const int fl = tid & 63;
   const int f = f0 + fl;
   int hit = 0;
+  const int8_t neg = (int8_t)num_bins, over_b = (int8_t)(num_bins + 1);
   for (int k = tid >> 6; k < BT_R; k += 4) {
     const int64_t r = r0 + k;
-    int8_t c = -1;
+    int8_t c = 0, nat = over_b;  // padding columns: num_bins + 1
     if (r < n && f < F) {
       c = X[r * xs + f];
-      hit |= (int)c >= threshold;
+      hit |= (int)c >= num_bins;
+      nat = c < 0 ? neg : ((int)c >= num_bins ? over_b : c);
     }
     tcode[fl][k] = c;
-    if (r < n && f < S) codes_rm[r * S + f] = c;
+    if (r < n && f < S) codes_rm[r * S + f] = nat;
   }
   if (over && __syncthreads_or(hit) && tid == 0) over[0] = 1;
   __syncthreads();

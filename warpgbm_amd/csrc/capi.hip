@@ -32,7 +32,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
                               int64_t n_pos, const int64_t* seg_dev, int32_t n_seg,
                               const int32_t* era, int32_t num_eras, const int32_t* feat_idx,
                               int32_t n_out_feats, int32_t num_bins, float* G, float* H,
-                              hipStream_t st) {
+                              bool native, hipStream_t st) {
   const int V = hist_pick_v(num_bins);
   const int n_chunks = (n_hist_feats + kHistSlots * V - 1) / (kHistSlots * V);
   // scratch layout (slot 0: control words and the per-block maxima)
@@ -44,8 +44,17 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   int32_t* n_tiles = (int32_t*)(ctl + 32);
   uint32_t* abs_part = ctl + 64;
   const int n_abs = (int)std::max<int64_t>(1, std::min<int64_t>(nblocks(n_pos, 256), kAbsBlocks));
+  // a row list without an era regrouping: the residuals are gathered into
+  // position order in the same pass, so the tile kernel reads them
+  // contiguously instead of one 4-byte gather per row
+  const bool regroup = !seg_dev && num_eras > 1;
+  float* rpos = nullptr;
+  if (rows && !regroup) {
+    rpos = (float*)scratch_get(st, sizeof(float) * std::max<int64_t>(n_pos, 1), 6);
+    WGBM_REQUIRE(rpos, "scratch allocation failed");
+  }
   hipLaunchKernelGGL(absmax_partial_kernel, dim3(n_abs), dim3(256), 0, st, resid, rows, n_pos,
-                     abs_part);
+                     abs_part, rpos);
   WGBM_LAUNCH_CHECK();
   // (the per-block maxima are reduced to the shift by the tile planner below)
 
@@ -101,7 +110,8 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   a.n_rows = n_rows;
   a.stride = stride;
   a.n_feats = n_hist_feats;
-  a.resid = resid;
+  a.resid = rpos ? rpos : resid;
+  a.resid_by_pos = rpos ? 1 : 0;
   a.resid_tree_stride = 0;
   a.shifts = shift;
   a.order = order;
@@ -113,6 +123,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   a.V = V;
   a.n_chunks = n_chunks;
   a.max_tiles = (int32_t)max_tiles;
+  a.native = native ? 1 : 0;
   void* tm = timer_begin("hist_tiles", st);
   int r = launch_hist_tiles(a, st);
   timer_end(tm, st);
@@ -163,18 +174,20 @@ int wgbm_compute_histogram3(const int8_t* bin_indices, int64_t n_rows, int64_t n
   return histogram_pipeline(bin_indices, n_rows, n_feats_master, (int32_t)n_feats_master,
                             residuals, sample_indices, n_samples, nullptr, 1, era_indices,
                             num_eras, feature_indices, (int32_t)n_feats, num_bins, grad_hist,
-                            hess_hist, S(stream));
+                            hess_hist, false, S(stream));
 }
 
 int wgbm_histogram_segments(const int8_t* codes, int64_t n_rows, int64_t stride, int32_t n_feats,
                             const float* residuals, const int32_t* order, const int64_t* seg,
-                            int32_t n_seg, int64_t n_pos, int32_t num_bins, float* G, float* H,
-                            void* stream) {
+                            int32_t n_seg, int64_t n_pos, int32_t num_bins, int32_t flags,
+                            float* G, float* H, void* stream) {
   WGBM_REQUIRE(num_bins >= 1 && num_bins <= 127, "num_bins must be in [1, 127]");
   WGBM_REQUIRE(n_seg >= 1 && seg && codes && residuals && G && H, "bad segment arguments");
   WGBM_REQUIRE(stride >= n_feats && n_feats >= 1, "stride must be >= n_feats >= 1");
+  WGBM_REQUIRE((flags & ~WGBM_CODES_NATIVE) == 0, "unknown histogram flags 0x%x", flags);
   return histogram_pipeline(codes, n_rows, stride, n_feats, residuals, order, n_pos, seg, n_seg,
-                            nullptr, 1, nullptr, n_feats, num_bins, G, H, S(stream));
+                            nullptr, 1, nullptr, n_feats, num_bins, G, H,
+                            (flags & WGBM_CODES_NATIVE) != 0, S(stream));
 }
 
 int wgbm_compute_split(const float* G, const float* H, int32_t num_eras, int32_t n_feats,
@@ -271,7 +284,7 @@ int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride
   if (codes_stride > covered) {
     const int64_t tot = n * (codes_stride - covered);
     hipLaunchKernelGGL(pad_codes_kernel, dim3(nblocks(tot, 256)), dim3(256), 0, S(stream),
-                       codes_rm, n, codes_stride, (int32_t)covered);
+                       codes_rm, n, codes_stride, (int32_t)covered, (int8_t)(n_edges + 2));
     WGBM_LAUNCH_CHECK();
   }
   return 0;
@@ -279,9 +292,10 @@ int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride
 
 int wgbm_copy_prebinned(const int8_t* X, int64_t n, int32_t n_feats, int64_t x_stride,
                         int8_t* codes_rm, int64_t codes_stride, int8_t* codes_cm,
-                        int32_t threshold, int32_t* over_flag, void* stream) {
+                        int32_t num_bins, int32_t* over_flag, void* stream) {
   WGBM_REQUIRE(n >= 0 && n_feats >= 1 && x_stride >= n_feats && codes_stride >= n_feats,
                "bad copy_prebinned shape");
+  WGBM_REQUIRE(num_bins >= 2 && num_bins <= 127, "num_bins must be in [2, 127]");
   if (over_flag) {
     hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, S(stream), over_flag, (int64_t)1, 0);
     WGBM_LAUNCH_CHECK();
@@ -290,30 +304,31 @@ int wgbm_copy_prebinned(const int8_t* X, int64_t n, int32_t n_feats, int64_t x_s
   WGBM_REQUIRE(X && codes_rm, "null pointer");
   dim3 grid(nblocks(n, 64), nblocks(n_feats, 64));
   hipLaunchKernelGGL(copy_prebinned_kernel, grid, dim3(256), 0, S(stream), X, n, n_feats,
-                     x_stride, codes_rm, codes_stride, codes_cm, threshold, over_flag);
+                     x_stride, codes_rm, codes_stride, codes_cm, num_bins, over_flag);
   WGBM_LAUNCH_CHECK();
   const int64_t covered = (int64_t)grid.y * 64;
   if (codes_stride > covered) {
     const int64_t tot = n * (codes_stride - covered);
     hipLaunchKernelGGL(pad_codes_kernel, dim3(nblocks(tot, 256)), dim3(256), 0, S(stream),
-                       codes_rm, n, codes_stride, (int32_t)covered);
+                       codes_rm, n, codes_stride, (int32_t)covered, (int8_t)(num_bins + 1));
     WGBM_LAUNCH_CHECK();
   }
   return 0;
 }
 
-int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, const int32_t* feat,
-                      const int32_t* bin, const float* leaf, int32_t n_rounds, int32_t K,
-                      int32_t H, int32_t max_depth, float learning_rate, float* out,
-                      void* stream) {
+int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int32_t num_bins,
+                      const int32_t* feat, const int32_t* bin, const float* leaf,
+                      int32_t n_rounds, int32_t K, int32_t H, int32_t max_depth,
+                      float learning_rate, float* out, void* stream) {
   WGBM_REQUIRE(n >= 0 && K >= 1 && n_rounds >= 0 && max_depth >= 0 && max_depth <= 20,
                "bad predict_heap shape");
+  WGBM_REQUIRE(num_bins >= 2 && num_bins <= 127, "num_bins must be in [2, 127]");
   WGBM_REQUIRE(H == (1 << (max_depth + 1)) - 1, "H must be 2^(max_depth+1)-1");
   if (n == 0) return 0;
   WGBM_REQUIRE(codes && out && (n_rounds == 0 || (feat && bin && leaf)), "null pointer");
   hipLaunchKernelGGL(predict_heap_kernel, dim3(nblocks(n * K, 256)), dim3(256), 0, S(stream),
-                     codes, n, codes_stride, feat, bin, leaf, n_rounds, K, H, max_depth,
-                     learning_rate, out);
+                     codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds, K, H,
+                     max_depth, learning_rate, out);
   WGBM_LAUNCH_CHECK();
   return 0;
 }

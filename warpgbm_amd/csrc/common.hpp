@@ -100,6 +100,26 @@ __device__ inline __amdgpu_buffer_rsrc_t wgbm_rsrc(const void* base, uint32_t by
                                            (int)bytes, WGBM_RSRC_DW3);
 }
 
+// A 64-bit word in LDS addressed by an integer byte offset (address space 3).
+typedef __attribute__((address_space(3))) unsigned long long wgbm_lds_u64;
+
+// Lane u (0..15) of every row of 16 lanes, broadcast to the whole row (DPP
+// row_newbcast): with the same value in lanes u, u+16, u+32, u+48 this is a
+// wave-wide broadcast of that value in one VALU instruction.  u must be a
+// constant after unrolling.
+__device__ __forceinline__ unsigned long long wgbm_row_bcast(unsigned long long v, int u) {
+  switch (u) {
+#define WGBM_BC(k) \
+  case k:          \
+    return __builtin_amdgcn_mov_dpp(v, 0x150 + k, 0xf, 0xf, false);
+    WGBM_BC(0) WGBM_BC(1) WGBM_BC(2) WGBM_BC(3) WGBM_BC(4) WGBM_BC(5) WGBM_BC(6) WGBM_BC(7)
+    WGBM_BC(8) WGBM_BC(9) WGBM_BC(10) WGBM_BC(11) WGBM_BC(12) WGBM_BC(13) WGBM_BC(14) WGBM_BC(15)
+#undef WGBM_BC
+    default:
+      return v;
+  }
+}
+
 // Order-preserving encoding of a non-negative float's magnitude as uint32
 // (for atomicMax over |r|).  NaN maps above +inf and is reported as an error.
 __device__ inline uint32_t wgbm_abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }

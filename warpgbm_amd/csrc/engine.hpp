@@ -138,10 +138,11 @@ __global__ void bin_column_kernel(const float* x, int64_t n, const float* edges,
 __global__ void bin_matrix_kernel(const float* X, int64_t n, int32_t F, int64_t xs,
                                   const float* edges, int32_t n_edges, int8_t* codes_rm,
                                   int64_t S, int8_t* codes_cm);
-__global__ void pad_codes_kernel(int8_t* codes_rm, int64_t n, int64_t S, int32_t from);
+__global__ void pad_codes_kernel(int8_t* codes_rm, int64_t n, int64_t S, int32_t from,
+                                 int8_t value);
 __global__ void copy_prebinned_kernel(const int8_t* X, int64_t n, int32_t F, int64_t xs,
                                       int8_t* codes_rm, int64_t S, int8_t* codes_cm,
-                                      int32_t threshold, int32_t* over);
+                                      int32_t num_bins, int32_t* over);
 __global__ void quantile_edges_kernel(const float* sorted, int64_t n, int32_t F,
                                       const float* q, int32_t nq, float* edges);
 __global__ void transpose_keys_kernel(const float* X, int64_t n, int32_t F, int64_t xs,
@@ -151,7 +152,7 @@ __global__ void quantile_select_kernel(const uint32_t* keys, int64_t n, int32_t 
 __global__ void predict_table_kernel(const int8_t* codes, int64_t n, int64_t F,
                                      const float* table, int64_t T, int64_t M, float lr,
                                      float* out);
-__global__ void predict_heap_kernel(const int8_t* codes, int64_t n, int64_t S,
+__global__ void predict_heap_kernel(const int8_t* codes, int64_t n, int64_t S, int32_t num_bins,
                                     const int32_t* feat, const int32_t* bin, const float* leaf,
                                     int32_t n_rounds, int32_t K, int32_t H, int32_t max_depth,
                                     float lr, float* out);

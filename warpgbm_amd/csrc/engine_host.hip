@@ -371,6 +371,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       a.V = e->V;
       a.n_chunks = e->n_chunks;
       a.max_tiles = (int32_t)max_tiles;
+      a.native = 1;  // the engine's codes come from the library's binner / pre-binned copy
       void* tm = timer_begin("engine_hist_tiles", st);
       r = launch_hist_tiles(a, st);
       timer_end(tm, st);

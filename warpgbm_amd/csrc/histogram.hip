@@ -36,14 +36,28 @@ namespace wgbm {
 // The residuals of the tile's tree t = key / keys_per_tree are
 // resid + t*resid_tree_stride, quantised with shifts[t].  BT > 0 fixes
 // num_bins at compile time (LDS offsets become immediates).  GATHER: the rows
-// of positions p are order[p] (else p).
+// of positions p are order[p] (else p); RPOS (with GATHER): the residual of
+// position p is resid[p] (a copy already gathered into position order, read
+// contiguously) instead of resid[order[p]].
 //
 // The kernel is bound by the LDS atomic unit (one 64-lane ds_add_u64 per row
-// and feature quad); everything else is arranged to keep that unit fed:
-// 8 waves per SIMD (two workgroups per CU, at most 64 VGPRs), row ids and
-// residuals as wave-uniform scalar loads, the row offset in the scalar
-// offset of the code load, and a branch-free add.
-template <int V, int MODE, int BT, bool GATHER>
+// and feature quad) and by the code stream from HBM; everything else is
+// arranged to keep both fed: 8 waves per SIMD (two workgroups per CU, at most
+// 64 VGPRs), the row offset in the scalar offset of the code load, and a
+// branch-free add.
+//
+// Two LDS layouts, both conflict-free (the lanes of one atomic never share a
+// word or a bank pair, whatever the bins are):
+// * raw codes (NAT = false): word (j, b, lane) at (j*(B+1) + b)*64 + lane; the
+//   bin of a code byte is clamped to the trash bin B (codes outside [0, B)),
+//   two VALU per atomic (a byte-select min, a shift-add).
+// * native codes (NAT = true, every byte in [0, B+1]): 256-byte LDS rows of
+//   32 lane words; lane l writes row j*2H + (l/32)*H + c, H = B + 2, so the
+//   row index of a byte c is c + (l/32)*H (one add per loaded dword, no
+//   carries: c + H <= 2B + 3 <= 255) and the address (row << 8) | (l%32)*8
+//   is a single byte permute of the code dword with the lane offset; rows B
+//   and B+1 of each half are the trash rows.  One VALU per atomic.
+template <int V, int MODE, int BT, bool GATHER, bool NAT, bool RPOS>
 __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void hist_tiles_kernel(
     const int8_t* __restrict__ codes, int64_t n_rows, int64_t stride, int32_t n_feats,
@@ -51,6 +65,8 @@ void hist_tiles_kernel(
     const int32_t* __restrict__ shifts, const int32_t* __restrict__ order,
     const Tile* __restrict__ tiles, const int32_t* __restrict__ n_tiles, int32_t keys_per_tree,
     int32_t num_bins_rt, unsigned long long* __restrict__ part) {
+  // the only LDS of this kernel: with no static LDS it starts at LDS address
+  // 0, so the NAT path can form LDS addresses as plain integers
   extern __shared__ unsigned long long lds[];
   constexpr int CW = kHistSlots * V;  // features per chunk
   const int num_bins = BT > 0 ? BT : num_bins_rt;
@@ -60,7 +76,8 @@ void hist_tiles_kernel(
   if (tile_id >= *n_tiles) return;
   const Tile tl = tiles[tile_id];
   const int Bp = num_bins + 1;
-  const int nent = V * Bp * kHistSlots;
+  const int Hn = num_bins + 2;  // NAT: rows per lane half
+  const int nent = NAT ? V * 2 * Hn * 32 : V * Bp * kHistSlots;
   for (int i = threadIdx.x; i < nent; i += kHistThreads) lds[i] = 0ull;
   __syncthreads();
 
@@ -79,17 +96,23 @@ void hist_tiles_kernel(
   const int32_t* __restrict__ ord = GATHER ? order + tl.begin : nullptr;
   const int n = (int)(tl.end - tl.begin);  // a tile has at most 65536 rows
   // A lane past the last feature adds whatever it reads to its own words,
-  // which belong to no feature and are never read back; the clamp below keeps
-  // every address inside the lane's column (padding bytes and other
-  // out-of-range codes go to the trash bin B).  It reads nothing new: an
-  // out-of-range buffer offset (returns zeros without a memory access), or
-  // the last real feature's offset, whose line the wave fetches anyway.
+  // which belong to no feature and are never read back; every address stays
+  // inside the lane's column (raw codes: out-of-range bytes go to the trash
+  // bin; native codes are in range).  It reads nothing new: an out-of-range
+  // buffer offset (returns zeros without a memory access), or the last real
+  // feature's offset, whose line the wave fetches anyway.
   const int vlast = (n_feats - 1) / V * V;
   const int voff = f_base < n_feats ? f_base : (MODE == kLoadBuffer ? 0x7fffffff : vlast);
   const int n_valid_bytes = f_base < n_feats ? (n_feats - f_base < V ? n_feats - f_base : V) : 0;
   const uint32_t rs_bytes = (MODE == kLoadBuffer) ? (uint32_t)(n_rows * stride) : 0u;
   const __amdgpu_buffer_rsrc_t rs = wgbm_rsrc(codes, rs_bytes);
   unsigned long long* my = lds + lane;
+  // NAT: lane offset inside a 256-byte row, and the row offset of the lane's
+  // half added to every code byte of its dword
+  const uint32_t lane_lo8 = (uint32_t)(lane & 31) * 8u;
+  const uint32_t half_add =
+      (lane >> 5) ? (uint32_t)Hn * (V == 4 ? 0x01010101u : (V == 2 ? 0x0101u : 1u)) : 0u;
+  const uint32_t plane_bytes = (uint32_t)(2 * Hn) * 256u;
 
   // software pipeline: wave w takes the row groups [i, i + U) with
   // i = (w + k*nwaves)*U (tile-relative).  Two register sets alternate: the
@@ -97,16 +120,16 @@ void hist_tiles_kernel(
   // loop is unrolled twice so that neither set is ever copied (a copy would
   // wait for every outstanding load).  Positions past the tile end (last
   // group only) repeat the tile's last row and add nothing.
-  constexpr int U = 8;
+  constexpr int U = 8;  // <= 16: the NAT path broadcasts within 16-lane rows
   constexpr int step = nwaves * U;
   struct Group {
     uint32_t c[U];  // codes of rows 0..U-1 of the group (all lanes)
-    float r;        // lane u < U: residual of row u
+    float r;        // lane l: residual of row l % U
   };
   Group ga, gb;
   const int row0 = (int)tl.begin;  // row ids fit 31 bits (checked by the launcher)
   const int ul = lane & (U - 1);
-  // GATHER: lane u < U holds order[i0 + u] of the next group to issue; read
+  // GATHER: lane l holds order[i0 + l % U] of the next group to issue; read
   // one issue ahead so that turning it into scalar row ids never waits
   int32_t ids = 0;
   auto load_ids = [&](int i0) {
@@ -120,20 +143,20 @@ void hist_tiles_kernel(
 #pragma unroll
     for (int u = 0; u < U; ++u)
       rows[u] = GATHER ? __builtin_amdgcn_readlane(ids, u) : row0 + (i0 + u < n ? i0 + u : n - 1);
-    // residuals: one vector load per group (lane u < U reads row u's)
-    const int my_row = GATHER ? ids : row0 + (i0 + ul < n ? i0 + ul : n - 1);
-    g.r = r_t[my_row];
+    // residuals: one vector load per group (lane l reads row l % U's)
+    const int my_pos = row0 + (i0 + ul < n ? i0 + ul : n - 1);
+    g.r = r_t[(GATHER && !RPOS) ? ids : my_pos];
     if constexpr (GATHER) load_ids(i0 + step);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (MODE == kLoadBuffer) {
         const int so = rows[u] * (int)stride;  // n_rows * stride < 2^31 in this mode
         if constexpr (V == 4)
-          g.c[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, so, kAuxNT);
+          g.c[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, so, kAuxStream);
         else if constexpr (V == 2)
-          g.c[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, voff, so, kAuxNT);
+          g.c[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, voff, so, kAuxStream);
         else
-          g.c[u] = __builtin_amdgcn_raw_buffer_load_b8(rs, voff, so, kAuxNT);
+          g.c[u] = __builtin_amdgcn_raw_buffer_load_b8(rs, voff, so, kAuxStream);
       } else if (MODE == kLoadGlobalAligned) {
         // row stride and chunk offsets are multiples of V bytes: aligned loads
         // that never run past the row (voff + V <= stride)
@@ -156,29 +179,45 @@ void hist_tiles_kernel(
     }
   };
   // branch-free: positions past the tile end add the word 0 (no sum, no
-  // count), selected with a wave-uniform condition where the word is used
+  // count)
   auto add = [&](const Group& g, int i0) {
-    // the group's packed words, quantised once (lane u < U: row u) and
-    // broadcast row by row
+    // the group's packed words, quantised once (lane l: row l % U)
     const int64_t qv = (int64_t)wgbm_quantise(g.r, s);
     const uint64_t pv = (uint64_t)(qv * (int64_t)(1 << WGBM_CBITS) + 1);
-    const uint32_t plo = (uint32_t)pv, phi = (uint32_t)(pv >> 32);
+    if constexpr (NAT) {
+      const unsigned long long pm = i0 + ul < n ? (unsigned long long)pv : 0ull;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      // readlane returns int: widen through uint32_t (no sign extension)
-      const uint64_t wu = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(phi, u) << 32) |
-                          (uint64_t)(uint32_t)__builtin_amdgcn_readlane(plo, u);
-      const unsigned long long w = i0 + u < n ? (unsigned long long)wu : 0ull;
+      for (int u = 0; u < U; ++u) {
+        // row u's word in every lane (DPP broadcast of lane u of each row of 16)
+        const unsigned long long w = wgbm_row_bcast(pm, u);
+        const uint32_t cw = g.c[u] + half_add;
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        uint32_t c = (g.c[u] >> (8 * j)) & 0xffu;
-        // out-of-range code (incl. negative int8, read as >= 128) -> trash bin
-        c = c < (uint32_t)num_bins ? c : (uint32_t)num_bins;
-        atomicAdd(my + (j * Bp + (int)c) * kHistSlots, w);
+        for (int j = 0; j < V; ++j) {
+          const uint32_t addr = __builtin_amdgcn_perm(cw, lane_lo8, 0x0c0c0000u | ((4u + j) << 8));
+          __hip_atomic_fetch_add((wgbm_lds_u64*)(uintptr_t)(addr + (uint32_t)j * plane_bytes), w,
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // one row at a time: hoisting the next rows' work above these atomics
-      // only raises register pressure (the LDS unit is the bottleneck)
-      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      const uint32_t plo = (uint32_t)pv, phi = (uint32_t)(pv >> 32);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        // readlane returns int: widen through uint32_t (no sign extension)
+        const uint64_t wu = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(phi, u) << 32) |
+                            (uint64_t)(uint32_t)__builtin_amdgcn_readlane(plo, u);
+        const unsigned long long w = i0 + u < n ? (unsigned long long)wu : 0ull;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          uint32_t c = (g.c[u] >> (8 * j)) & 0xffu;
+          // out-of-range code (incl. negative int8, read as >= 128) -> trash bin
+          c = c < (uint32_t)num_bins ? c : (uint32_t)num_bins;
+          atomicAdd(my + (j * Bp + (int)c) * kHistSlots, w);
+        }
+        // one row at a time: hoisting the next rows' work above these atomics
+        // only raises register pressure (the LDS unit is the bottleneck)
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   };
   int i = wave * U;
@@ -204,31 +243,40 @@ void hist_tiles_kernel(
   }
   __syncthreads();
 
-  // flush in LDS order: part[tile][chunk][j][b][lane] (trash row dropped); the
-  // packed word (sum * 2^18 + count) is stored as is and unpacked by finalize
+  // flush in the partial layout part[tile][chunk][j][b][lane] (trash rows
+  // dropped); the packed word (sum * 2^18 + count) is stored as is and
+  // unpacked by finalize.  Two words (lanes l, l+1 of one (j, b)) per thread
+  // and store: 16-byte non-temporal stores (every workgroup flushes at the
+  // same time at the end, so the stores should not wait on cache lines)
   const int64_t tile_words = (int64_t)n_chunks * CW * num_bins;
   const int64_t chunk_off = (int64_t)tile_id * tile_words + (int64_t)chunk * CW * num_bins;
-  const int nout = V * num_bins * kHistSlots;
-  for (int k = threadIdx.x; k < nout; k += kHistThreads) {
-    const int sl = k & (kHistSlots - 1);
-    const int jb = k / kHistSlots;  // j*B + b
+  const int npair = V * num_bins * kHistSlots / 2;
+  typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+  for (int k2 = threadIdx.x; k2 < npair; k2 += kHistThreads) {
+    const int k = 2 * k2;
+    const int sl = k & (kHistSlots - 1);  // even: sl and sl + 1 share (j, b) and a lane half
+    const int jb = k / kHistSlots;        // j*B + b
     const int j = jb / num_bins;
     const int b = jb - j * num_bins;
-    part[chunk_off + k] = lds[(j * Bp + b) * kHistSlots + sl];
+    const int src = NAT ? (j * 2 * Hn + (sl >> 5) * Hn + b) * 32 + (sl & 31)
+                        : (j * Bp + b) * kHistSlots + sl;
+    const u64x2 v = *reinterpret_cast<const u64x2*>(lds + src);
+    __builtin_nontemporal_store(v, reinterpret_cast<u64x2*>(part + chunk_off + k));
   }
 }
 
 // unpack a packed tile word into (exact sum, count)
 __device__ inline void unpack_word(unsigned long long P, int64_t& Q, int64_t& C) {
+  // P = q * 2^18 + c with 0 <= c < 2^18: the arithmetic shift is floor(P / 2^18) = q
   C = (int64_t)(P & (unsigned long long)WGBM_CMASK);
-  Q = ((int64_t)P - C) / (int64_t)(1 << WGBM_CBITS);
+  Q = (int64_t)P >> WGBM_CBITS;
 }
 
 // partial-layout index i (within one tile) -> (feature, bin)
-__device__ inline void part_feature_bin(int64_t i, int V, int num_bins, int& f, int& b) {
+__device__ inline void part_feature_bin(int i, int V, int num_bins, int& f, int& b) {
   const int per_chunk = kHistSlots * V * num_bins;
-  const int chunk = (int)(i / per_chunk);
-  const int r = (int)(i - (int64_t)chunk * per_chunk);
+  const int chunk = i / per_chunk;
+  const int r = i - chunk * per_chunk;
   const int sl = r & (kHistSlots - 1);
   const int jb = r / kHistSlots;
   const int j = jb / num_bins;
@@ -250,20 +298,37 @@ __device__ inline void part_feature_bin(int64_t i, int V, int num_bins, int& f, 
 // workgroups); many tiles -> narrow FW (more parallel tile reads).
 template <int FW>
 __device__ inline void finalize_sum(const unsigned long long* __restrict__ part, int64_t tile_words,
-                                    int64_t i, bool ok, int t0, int t1, int64_t& Q, int64_t& C) {
+                                    int i, bool ok, int t0, int t1, int64_t& Q, int64_t& C) {
   constexpr int SPLIT = 256 / FW;
   __shared__ int64_t sq[SPLIT][FW];
   __shared__ int64_t sc[SPLIT][FW];
   const int w = threadIdx.x % FW;
   const int g = threadIdx.x / FW;
   int64_t q = 0, c = 0;
-  if (ok)
-    for (int t = t0 + g; t < t1; t += SPLIT) {
+  if (ok) {
+    // four tiles' loads in flight per step (the partials are read once)
+    const unsigned long long* __restrict__ p = part + i;
+    int t = t0 + g;
+    for (; t + 3 * SPLIT < t1; t += 4 * SPLIT) {
+      unsigned long long P[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        P[u] = __builtin_nontemporal_load(p + (int64_t)(t + u * SPLIT) * tile_words);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        int64_t a, b;
+        unpack_word(P[u], a, b);
+        q += a;
+        c += b;
+      }
+    }
+    for (; t < t1; t += SPLIT) {
       int64_t a, b;
-      unpack_word(part[(int64_t)t * tile_words + i], a, b);
+      unpack_word(__builtin_nontemporal_load(p + (int64_t)t * tile_words), a, b);
       q += a;
       c += b;
     }
+  }
   sq[g][w] = q;
   sc[g][w] = c;
   __syncthreads();
@@ -282,10 +347,11 @@ __global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
     const int32_t* __restrict__ shifts, const uint32_t* __restrict__ absmax_bits,
     const int32_t* __restrict__ n_tiles, int32_t accumulate, float* __restrict__ G,
     float* __restrict__ H) {
-  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
-  const int64_t wpk = (tile_words + FW - 1) / FW;  // workgroups per segment
-  const int k = (int)(blockIdx.x / wpk);
-  const int64_t i = (blockIdx.x - (int64_t)k * wpk) * FW + threadIdx.x % FW;
+  // tile_words < 2^31 (checked by the launcher)
+  const int tile_words = n_chunks * kHistSlots * V * num_bins;
+  const int wpk = (tile_words + FW - 1) / FW;  // workgroups per segment
+  const int k = (int)blockIdx.x / wpk;
+  const int i = ((int)blockIdx.x - k * wpk) * FW + (int)threadIdx.x % FW;
   const bool ok = k < n_keys && i < tile_words;
   int t0 = 0, t1 = 0;
   if (k < n_keys) {
@@ -341,13 +407,14 @@ __global__ __launch_bounds__(256) void hist_finalize_level_kernel(
     int32_t num_bins, int32_t n_feats, int32_t num_eras, int32_t nodes_in_level, int32_t depth,
     const int64_t* __restrict__ parent_q, const int32_t* __restrict__ parent_c,
     const int32_t* __restrict__ n_tiles, int64_t* __restrict__ hq, int32_t* __restrict__ hc) {
-  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
-  const int64_t wpk = (tile_words + FW - 1) / FW;
-  const int kk = (int)(blockIdx.x / wpk);
+  // tile_words < 2^31 (checked by the launcher)
+  const int tile_words = n_chunks * kHistSlots * V * num_bins;
+  const int wpk = (tile_words + FW - 1) / FW;
+  const int kk = (int)blockIdx.x / wpk;
   if (kk >= n_list) return;  // uniform per workgroup
   const int key = key_list ? key_list[kk] : kk;
   if (key < 0) return;  // uniform per workgroup
-  const int64_t i = (blockIdx.x - (int64_t)kk * wpk) * FW + threadIdx.x % FW;
+  const int i = ((int)blockIdx.x - kk * wpk) * FW + (int)threadIdx.x % FW;
   const bool ok = i < tile_words;
   const int t0 = key_tile_start[kk];
   const int t1 = key_tile_start[kk + 1] < *n_tiles ? key_tile_start[kk + 1] : *n_tiles;
@@ -381,12 +448,16 @@ __global__ __launch_bounds__(256) void hist_finalize_level_kernel(
 // --------------------------------------------------------------------------
 __global__ void absmax_partial_kernel(const float* __restrict__ resid,
                                       const int32_t* __restrict__ rows, int64_t n,
-                                      uint32_t* __restrict__ partial) {
+                                      uint32_t* __restrict__ partial,
+                                      float* __restrict__ gathered) {
+  // gathered (with rows): resid[rows[i]] copied into position order on the way
   uint32_t m = 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = rows ? (int64_t)rows[i] : i;
-    const uint32_t b = wgbm_abs_bits(resid[r]);
+    const float v = resid[r];
+    if (gathered) gathered[i] = v;
+    const uint32_t b = wgbm_abs_bits(v);
     m = b > m ? b : m;
   }
   m = wgbm_block_max_u32(m);
@@ -624,6 +695,9 @@ int launch_finalize_f32(int64_t tiles_per_key, const unsigned long long* part,
                         float* G, float* H, hipStream_t st) {
   const int fw = fin_words_for(tiles_per_key);
   const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
+  WGBM_REQUIRE(tile_words < ((int64_t)1 << 31) &&
+                   n_keys * ((tile_words + fw - 1) / fw) < ((int64_t)1 << 31),
+               "finalize: too many histogram words");
   const unsigned wg = (unsigned)(n_keys * ((tile_words + fw - 1) / fw));
 #define WGBM_L(F)                                                                                 \
   hipLaunchKernelGGL(hist_finalize_f32_kernel<F>, dim3(wg), dim3(256), 0, st, part, key_tile_start, \
@@ -643,6 +717,9 @@ int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
                           int64_t* hq, int32_t* hc, hipStream_t st) {
   const int fw = fin_words_for(tiles_per_key);
   const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
+  WGBM_REQUIRE(tile_words < ((int64_t)1 << 31) &&
+                   n_list * ((tile_words + fw - 1) / fw) < ((int64_t)1 << 31),
+               "finalize: too many histogram words");
   const unsigned wg = (unsigned)(n_list * ((tile_words + fw - 1) / fw));
 #define WGBM_L(F)                                                                          \
   hipLaunchKernelGGL(hist_finalize_level_kernel<F>, dim3(wg), dim3(256), 0, st, part,        \
@@ -667,31 +744,42 @@ int hist_pick_v(int num_bins) {
   return 1;
 }
 
-size_t hist_lds_bytes(int V, int num_bins) {
+size_t hist_lds_bytes(int V, int num_bins, bool native) {
+  if (native) return (size_t)V * 2 * (num_bins + 2) * 256;
   return (size_t)V * (num_bins + 1) * kHistSlots * 8;
 }
 
-template <int V, int MODE, int BT, bool GATHER>
+// the native-code layout needs c + H <= 255 for every byte c <= B + 1
+bool hist_native_ok(int num_bins) { return 2 * num_bins + 3 <= 255; }
+
+template <int V, int MODE, int BT, bool GATHER, bool NAT, bool RPOS>
 static int launch_tiles_t(const HistLaunch& a, hipStream_t st) {
   static bool attr_set = false;
-  const size_t lds = hist_lds_bytes(V, a.num_bins);
+  const size_t lds = hist_lds_bytes(V, a.num_bins, NAT);
   if (!attr_set) {
-    WGBM_CHECK(hipFuncSetAttribute((const void*)hist_tiles_kernel<V, MODE, BT, GATHER>,
+    WGBM_CHECK(hipFuncSetAttribute((const void*)hist_tiles_kernel<V, MODE, BT, GATHER, NAT, RPOS>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     attr_set = true;
   }
   dim3 grid((unsigned)((int64_t)a.n_chunks * a.max_tiles));
-  hipLaunchKernelGGL((hist_tiles_kernel<V, MODE, BT, GATHER>), grid, dim3(kHistThreads), lds, st,
-                     a.codes, a.n_rows, a.stride, a.n_feats, a.resid, a.resid_tree_stride,
+  hipLaunchKernelGGL((hist_tiles_kernel<V, MODE, BT, GATHER, NAT, RPOS>), grid, dim3(kHistThreads), lds,
+                     st, a.codes, a.n_rows, a.stride, a.n_feats, a.resid, a.resid_tree_stride,
                      a.shifts, a.order, a.tiles, a.n_tiles, a.keys_per_tree, a.num_bins, a.part);
   WGBM_LAUNCH_CHECK();
   return 0;
 }
 
+template <int V, int MODE, int BT, bool NAT>
+static int launch_tiles_r(const HistLaunch& a, hipStream_t st) {
+  if (!a.order) return launch_tiles_t<V, MODE, BT, false, NAT, false>(a, st);
+  return a.resid_by_pos ? launch_tiles_t<V, MODE, BT, true, NAT, true>(a, st)
+                        : launch_tiles_t<V, MODE, BT, true, NAT, false>(a, st);
+}
+
 template <int V, int MODE, int BT>
 static int launch_tiles_g(const HistLaunch& a, hipStream_t st) {
-  return a.order ? launch_tiles_t<V, MODE, BT, true>(a, st)
-                 : launch_tiles_t<V, MODE, BT, false>(a, st);
+  if (a.native && hist_native_ok(a.num_bins)) return launch_tiles_r<V, MODE, BT, true>(a, st);
+  return launch_tiles_r<V, MODE, BT, false>(a, st);
 }
 
 int hist_load_mode(int64_t n_rows, int64_t stride, int V) {

@@ -24,8 +24,10 @@ constexpr int kDesChunk = 8;
 // eras per block of the DES era sum (float64: in era order inside a block,
 // then block sums in block order); also the width of a live-era mask word
 constexpr int kDesEraBlock = 32;
-// cache-policy bits of a buffer load: non-temporal (streamed once)
+// cache-policy bits of a buffer load: non-temporal (streamed once), plus
+// sc0 for the code stream of the tile histogram (measured faster there)
 constexpr int kAuxNT = 2;
+constexpr int kAuxStream = 3;
 // histogram workgroups per launch the tile sizes aim for (2 per CU)
 constexpr int kHistTargetWG = 512;
 
@@ -46,10 +48,17 @@ struct HistLaunch {
   int32_t V;
   int32_t n_chunks;
   int32_t max_tiles;
+  // codes in the native layout (every byte in [0, num_bins + 1], written by
+  // the library's binner / pre-binned copy): the kernel needs no clamp
+  int32_t native = 0;
+  // with order: resid holds the residuals in position order (resid[p] belongs
+  // to row order[p]) instead of row order
+  int32_t resid_by_pos = 0;
 };
 
 int hist_pick_v(int num_bins);
-size_t hist_lds_bytes(int V, int num_bins);
+size_t hist_lds_bytes(int V, int num_bins, bool native);
+bool hist_native_ok(int num_bins);
 int hist_load_mode(int64_t n_rows, int64_t stride, int V);
 int launch_hist_tiles(const HistLaunch& a, hipStream_t st);
 int probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, hipStream_t st);
@@ -71,7 +80,7 @@ int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
                           const int64_t* parent_q, const int32_t* parent_c, const int32_t* n_tiles,
                           int64_t* hq, int32_t* hc, hipStream_t st);
 __global__ void absmax_partial_kernel(const float* resid, const int32_t* rows, int64_t n,
-                                      uint32_t* partial);
+                                      uint32_t* partial, float* gathered);
 __global__ void absmax_finish_kernel(const uint32_t* partial, int32_t n_part, int32_t qbits,
                                      uint32_t* absmax_bits, int32_t* shifts);
 __global__ void plan_tiles_kernel(const int64_t* seg, int64_t total, int32_t n_keys,

@@ -48,8 +48,12 @@ __global__ void predict_table_kernel(const int8_t* __restrict__ codes, int64_t n
 // compact heap tables written by the engine: node h has children 2h+1, 2h+2.
 //   feat[t][h] >= 0 split feature, -1 leaf; bin[t][h]; leaf[t][h]
 // trees are ordered (round, class); out is [n, K] row-major, pre-initialised.
+// codes are native (bytes in [0, B + 1], B = num_bins): the byte B stands for
+// a negative code, which goes left at every split (a raw int8 code <= bin
+// with bin >= 0), and B + 1 for a code >= B, which goes right; the other
+// bytes are the codes themselves.
 __global__ void predict_heap_kernel(const int8_t* __restrict__ codes, int64_t n, int64_t S,
-                                    const int32_t* __restrict__ feat,
+                                    int32_t num_bins, const int32_t* __restrict__ feat,
                                     const int32_t* __restrict__ bin,
                                     const float* __restrict__ leaf, int32_t n_rounds, int32_t K,
                                     int32_t H, int32_t max_depth, float lr,
@@ -68,7 +72,8 @@ __global__ void predict_heap_kernel(const int8_t* __restrict__ codes, int64_t n,
     for (int d = 0; d < max_depth; ++d) {
       const int f = ft[h];
       if (f < 0) break;
-      h = 2 * h + ((int)row[f] <= bt[h] ? 1 : 2);
+      const int c = (int)(uint8_t)row[f];
+      h = 2 * h + ((c <= bt[h] || c == num_bins) ? 1 : 2);
     }
     acc = acc + lr * leaf[t * H + h];
   }

@@ -39,28 +39,32 @@ def quantile_levels(num_bins: int) -> torch.Tensor:
 
 @dataclass
 class Codes:
-    """Binned matrix on the device: row-major (padded) and column-major copies."""
+    """Binned matrix on the device.  ``rm`` is the library's native row-major
+    layout for ``num_bins`` (every byte in [0, num_bins + 1]: codes in
+    [0, num_bins) as is, negative codes as num_bins, codes >= num_bins and
+    padding as num_bins + 1); ``cm`` the raw column-major copy."""
     rm: torch.Tensor        # int8 [n, stride]
     cm: torch.Tensor | None  # int8 [F, n]
     n: int
     n_feats: int
     stride: int
+    num_bins: int
 
 
-def _alloc_codes(n: int, F: int, dev, with_cm: bool) -> Codes:
+def _alloc_codes(n: int, F: int, dev, with_cm: bool, num_bins: int) -> Codes:
     S = codes_stride(F)
     rm = torch.empty((n, S), dtype=torch.int8, device=dev)
     cm = torch.empty((F, n), dtype=torch.int8, device=dev) if with_cm else None
-    return Codes(rm, cm, n, F, S)
+    return Codes(rm, cm, n, F, S, num_bins)
 
 
-def upload_prebinned(X: np.ndarray, dev, with_cm: bool) -> Codes:
+def upload_prebinned(X: np.ndarray, dev, with_cm: bool, num_bins: int) -> Codes:
     """Integer input whose columns are all < num_bins is used as codes directly
     (warpgbm/core.py:499-517); values are cast to int8 like the reference's
     ``bin_indices[:, f] = torch.as_tensor(X[:, f])``."""
     X = np.asarray(X)
     x8 = upload_int8(X if X.dtype == np.int8 else X.astype(np.int8), dev)
-    return codes_from_int8(x8, with_cm)[0]
+    return codes_from_int8(x8, with_cm, num_bins)[0]
 
 
 def upload_int8(X: np.ndarray, dev) -> torch.Tensor:
@@ -68,18 +72,17 @@ def upload_int8(X: np.ndarray, dev) -> torch.Tensor:
     return _upload_staged(X, dev, np.int8, torch.int8)
 
 
-def codes_from_int8(x8: torch.Tensor, with_cm: bool, threshold: int | None = None):
-    """Codes from an int8 [n, F] device matrix (``wgbm_copy_prebinned``).
-    With a threshold, also whether some value is >= threshold (found in the
-    same pass over the matrix); else None."""
+def codes_from_int8(x8: torch.Tensor, with_cm: bool, num_bins: int, check: bool = False):
+    """Native codes for num_bins from an int8 [n, F] device matrix
+    (``wgbm_copy_prebinned``).  With check, also whether some value is
+    >= num_bins (found in the same pass over the matrix); else None."""
     n, F = x8.shape
     dev = x8.device
-    c = _alloc_codes(n, F, dev, with_cm)
-    flag = torch.empty(1, dtype=torch.int32, device=dev) if threshold is not None else None
+    c = _alloc_codes(n, F, dev, with_cm, num_bins)
+    flag = torch.empty(1, dtype=torch.int32, device=dev) if check else None
     lib = _lib.load()
     rc = lib.wgbm_copy_prebinned(x8.data_ptr(), n, F, F, c.rm.data_ptr(), c.stride,
-                                 c.cm.data_ptr() if c.cm is not None else None,
-                                 int(threshold) if threshold is not None else 0,
+                                 c.cm.data_ptr() if c.cm is not None else None, int(num_bins),
                                  flag.data_ptr() if flag is not None else None, _stream(dev))
     _lib.check(rc, "copy_prebinned")
     return c, (bool(flag.item()) if flag is not None else None)
@@ -192,7 +195,7 @@ def bin_matrix(Xd: torch.Tensor, edges: torch.Tensor, with_cm: bool) -> Codes:
     edges = edges.to(device=Xd.device, dtype=torch.float32).contiguous()
     if edges.shape[0] != F:
         raise ValueError(f"edges for {edges.shape[0]} features, X has {F}")
-    c = _alloc_codes(n, F, Xd.device, with_cm)
+    c = _alloc_codes(n, F, Xd.device, with_cm, edges.shape[1] + 1)
     lib = _lib.load()
     rc = lib.wgbm_bin_matrix(Xd.data_ptr(), n, F, F, edges.data_ptr(), edges.shape[1],
                              c.rm.data_ptr(), c.stride,
@@ -268,9 +271,10 @@ def predict_heap(codes: Codes, feat: torch.Tensor, bin_: torch.Tensor, leaf: tor
     ``out`` [n, K] (one launch; cf. warpgbm/core.py:917-932, 991-1030)."""
     H = (1 << (max_depth + 1)) - 1
     lib = _lib.load()
-    rc = lib.wgbm_predict_heap(codes.rm.data_ptr(), codes.n, codes.stride, feat.data_ptr(),
-                               bin_.data_ptr(), leaf.data_ptr(), n_rounds, K, H, max_depth,
-                               float(learning_rate), out.data_ptr(), _stream(out.device))
+    rc = lib.wgbm_predict_heap(codes.rm.data_ptr(), codes.n, codes.stride, codes.num_bins,
+                               feat.data_ptr(), bin_.data_ptr(), leaf.data_ptr(), n_rounds, K, H,
+                               max_depth, float(learning_rate), out.data_ptr(),
+                               _stream(out.device))
     _lib.check(rc, "predict_heap")
 
 
