@@ -75,6 +75,26 @@ def test_multiclass_bit_exact(gpu):
     assert (m.predict(X) == y).mean() > 0.8
 
 
+def test_multiclass_many_features_bit_exact(gpu):
+    """Many features and K trees per round: the level histograms of the deeper
+    levels have enough (tree, node) segments x feature planes for the plane
+    finalize (exact int64 level sums, sibling = parent - child)."""
+    print_case("estimator", "multiclass K=5, F=300")
+    rng = np.random.default_rng(11)
+    N, F, K = 8000, 300, 5
+    means = rng.standard_normal((K, F)) * 0.4
+    labels = rng.integers(0, K, N)
+    X = (means[labels] + rng.standard_normal((N, F))).astype(F32)
+    kw = dict(objective="multiclass", num_bins=32, max_depth=4, n_estimators=4,
+              learning_rate=0.3, min_child_weight=10)
+    m = WarpGBM(**kw).fit(X, labels)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, labels)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"round {i} differs"
+    assert np.array_equal(bits(m.predict_proba(X)), bits(ref.predict_codes(codes)))
+
+
 def test_era_des_prebinned_bit_exact(gpu):
     print_case("estimator", "DES E=6 prebinned")
     rng = np.random.default_rng(2)

@@ -183,17 +183,19 @@ def native_layout(raw, num_bins, stride):
     return out.astype(np.uint8).view(np.int8)
 
 
-@pytest.mark.parametrize("B", [32, 5, 50, 126, 127])
+@pytest.mark.parametrize("B,F", [(32, 203), (5, 203), (50, 203), (126, 203), (127, 203),
+                                 (32, 1000), (50, 700)])
 @pytest.mark.parametrize("native", [False, True])
-def test_histogram_segments_bit_exact(gpu, native, B):
+def test_histogram_segments_bit_exact(gpu, native, B, F):
     """16 node segments of raw codes with values outside [0, B) (negative and
     >= B: skipped, histogram_kernel.cu:41), through the raw-code kernel and
     through the native layout made by the pre-binned copy; both equal the
     oracle on the raw codes.  B = 127 has no native-layout kernel (its rows
-    would not fit a byte) and takes the clamping one."""
-    print_case("histogram_segments", "16 nodes", "native" if native else "raw", B)
-    rng = np.random.default_rng(5 + B)
-    N, F, S = 40000, 203, 16
+    would not fit a byte) and takes the clamping one.  The wide cases (16
+    segments x 16 or more feature planes) take the plane finalize."""
+    print_case("histogram_segments", "16 nodes", "native" if native else "raw", B, F)
+    rng = np.random.default_rng(5 + B + F)
+    N, S = 40000, 16
     stride = D.codes_stride(F)
     raw = rng.integers(-3, B + 3, (N, F)).astype(np.int8)
     resid = rng.standard_normal(N).astype(F32)

@@ -124,9 +124,8 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   a.n_chunks = n_chunks;
   a.max_tiles = (int32_t)max_tiles;
   a.native = native ? 1 : 0;
-  void* tm = timer_begin("hist_tiles", st);
+  a.timer_tag = "hist_tiles";
   int r = launch_hist_tiles(a, st);
-  timer_end(tm, st);
   if (r) return r;
   // tiles per segment (finalize's tile split): the planner's estimate
   const int64_t tiles_per_key = std::max<int64_t>(1, (n_pos + R - 1) / R / std::max(n_keys, 1));

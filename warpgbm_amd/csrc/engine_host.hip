@@ -372,9 +372,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       a.n_chunks = e->n_chunks;
       a.max_tiles = (int32_t)max_tiles;
       a.native = 1;  // the engine's codes come from the library's binner / pre-binned copy
-      void* tm = timer_begin("engine_hist_tiles", st);
+      a.timer_tag = "engine_hist_tiles";
       r = launch_hist_tiles(a, st);
-      timer_end(tm, st);
       if (r) return r;
       const int64_t tiles_per_key = std::max<int64_t>(1, rows_bound / R / std::max(n_list, 1));
       r = launch_finalize_level(tiles_per_key, e->part, e->hkts, list, n_list, e->n_chunks, e->V,

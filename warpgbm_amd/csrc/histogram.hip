@@ -24,6 +24,8 @@
 // * Each tile writes its partial histogram (exact int64 sum, int32 count) in
 //   the LDS layout; a finalize kernel sums the tiles of a segment (integers, so
 //   in any order) and rounds once to float32.
+#include <hip/hip_ext.h>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -376,6 +378,153 @@ __global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
   }
 }
 
+// --------------------------------------------------------------------------
+// plane finalize: one workgroup (1024 threads) per (segment, plane), where a
+// plane is the B x 64 partial words of one (chunk, j): bins b of the 64
+// features chunk*64V + lane*V + j.  Four thread groups sum every fourth tile
+// of the segment (each thread 1..16 words of the plane, all their loads of
+// one tile in flight together), the groups are combined with LDS integer
+// adds into [b][lane] tables padded to 65 words a row, and the workgroup
+// then writes the outputs in their [feature][bin] order: 32 threads write the
+// B contiguous bins of one feature (coalesced rows, where a word-per-thread
+// finalize stores with a stride of V*B words).  Used when there are many
+// segments, each with few tiles.
+// --------------------------------------------------------------------------
+constexpr int kPlaneThreads = 1024;
+constexpr int kPlaneGroups = 4;
+constexpr int kPlaneMaxBins = 64;  // words per thread: B*64/256 <= 16
+constexpr int kPlaneRow = 65;
+
+__device__ inline void plane_sum(const unsigned long long* __restrict__ part, int64_t tile_words,
+                                 int plane_off, int num_bins, int t0, int t1,
+                                 unsigned long long* sq, unsigned int* sc) {
+  const int W = num_bins * kHistSlots;
+  for (int i = threadIdx.x; i < num_bins * kPlaneRow; i += kPlaneThreads) {
+    sq[i] = 0ull;
+    sc[i] = 0u;
+  }
+  __syncthreads();
+  const int g = threadIdx.x / (kPlaneThreads / kPlaneGroups);
+  const int lt = threadIdx.x % (kPlaneThreads / kPlaneGroups);
+  constexpr int kMaxW = kPlaneMaxBins * kHistSlots / (kPlaneThreads / kPlaneGroups);
+  int64_t q[kMaxW];
+  int64_t c[kMaxW];
+#pragma unroll
+  for (int k = 0; k < kMaxW; ++k) q[k] = c[k] = 0;
+  for (int t = t0 + g; t < t1; t += kPlaneGroups) {
+    const unsigned long long* __restrict__ p = part + (int64_t)t * tile_words + plane_off;
+    unsigned long long P[kMaxW];
+#pragma unroll
+    for (int k = 0; k < kMaxW; ++k) {
+      const int w = lt + k * (kPlaneThreads / kPlaneGroups);
+      P[k] = w < W ? __builtin_nontemporal_load(p + w) : 0ull;
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxW; ++k) {
+      int64_t a, b;
+      unpack_word(P[k], a, b);
+      q[k] += a;
+      c[k] += b;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxW; ++k) {
+    const int w = lt + k * (kPlaneThreads / kPlaneGroups);
+    if (w < W && t1 > t0) {
+      const int li = (w / kHistSlots) * kPlaneRow + (w % kHistSlots);  // [b][lane]
+      atomicAdd(sq + li, (unsigned long long)q[k]);  // two's complement: exact
+      atomicAdd(sc + li, (unsigned int)c[k]);
+    }
+  }
+  __syncthreads();
+}
+
+// G[k, f, b] (+)= float(sum * 2^-s), H[k, f, b] (+)= count
+__global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_f32_kernel(
+    const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
+    int32_t n_keys, int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
+    const int32_t* __restrict__ shifts, const uint32_t* __restrict__ absmax_bits,
+    const int32_t* __restrict__ n_tiles, int32_t accumulate, float* __restrict__ G,
+    float* __restrict__ H) {
+  __shared__ unsigned long long sq[kPlaneMaxBins * kPlaneRow];
+  __shared__ unsigned int sc[kPlaneMaxBins * kPlaneRow];
+  const int P = n_chunks * V;
+  const int k = (int)blockIdx.x / P;
+  const int plane = (int)blockIdx.x - k * P;
+  if (k >= n_keys) return;  // uniform per workgroup
+  const int chunk = plane / V, j = plane - (plane / V) * V;
+  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
+  const int t0 = key_tile_start[k];
+  const int t1 = key_tile_start[k + 1] < *n_tiles ? key_tile_start[k + 1] : *n_tiles;
+  plane_sum(part, tile_words, plane * num_bins * kHistSlots, num_bins, t0, t1, sq, sc);
+  const bool bad = (*absmax_bits) >= 0x7f800000u;  // non-finite residual seen
+  const int s = shifts[0];
+  for (int o = threadIdx.x; o < kHistSlots * num_bins; o += kPlaneThreads) {
+    const int lane = o / num_bins, b = o - lane * num_bins;
+    const int f = chunk * kHistSlots * V + lane * V + j;
+    if (f >= n_feats) continue;
+    const int li = b * kPlaneRow + lane;
+    const float g = bad ? __builtin_nanf("") : wgbm_dequantise((int64_t)sq[li], s);
+    const float h = (float)sc[li];
+    const int64_t out = ((int64_t)k * n_feats + f) * num_bins + b;
+    if (accumulate) {
+      G[out] = G[out] + g;
+      H[out] = H[out] + h;
+    } else {
+      G[out] = g;
+      H[out] = h;
+    }
+  }
+}
+
+// the engine's level arrays (exact int64 sums, int32 counts) and the sibling
+// as parent - computed child; key layout as hist_finalize_level_kernel
+__global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_level_kernel(
+    const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
+    const int32_t* __restrict__ key_list, int32_t n_list, int32_t n_chunks, int32_t V,
+    int32_t num_bins, int32_t n_feats, int32_t num_eras, int32_t nodes_in_level, int32_t depth,
+    const int64_t* __restrict__ parent_q, const int32_t* __restrict__ parent_c,
+    const int32_t* __restrict__ n_tiles, int64_t* __restrict__ hq, int32_t* __restrict__ hc) {
+  __shared__ unsigned long long sq[kPlaneMaxBins * kPlaneRow];
+  __shared__ unsigned int sc[kPlaneMaxBins * kPlaneRow];
+  const int P = n_chunks * V;
+  const int kk = (int)blockIdx.x / P;
+  const int plane = (int)blockIdx.x - kk * P;
+  if (kk >= n_list) return;  // uniform per workgroup
+  const int key = key_list ? key_list[kk] : kk;
+  if (key < 0) return;  // uniform per workgroup
+  const int chunk = plane / V, j = plane - (plane / V) * V;
+  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
+  const int t0 = key_tile_start[kk];
+  const int t1 = key_tile_start[kk + 1] < *n_tiles ? key_tile_start[kk + 1] : *n_tiles;
+  plane_sum(part, tile_words, plane * num_bins * kHistSlots, num_bins, t0, t1, sq, sc);
+  const int64_t per_key = (int64_t)n_feats * num_bins;
+  int64_t pkey = 0, skey = 0;
+  if (depth > 0) {
+    const int era = key % num_eras;
+    const int tn = key / num_eras;
+    const int node = tn % nodes_in_level;
+    const int tree = tn / nodes_in_level;
+    pkey = ((int64_t)tree * (nodes_in_level >> 1) + (node >> 1)) * num_eras + era;
+    skey = ((int64_t)tree * nodes_in_level + (node ^ 1)) * num_eras + era;
+  }
+  for (int o = threadIdx.x; o < kHistSlots * num_bins; o += kPlaneThreads) {
+    const int lane = o / num_bins, b = o - lane * num_bins;
+    const int f = chunk * kHistSlots * V + lane * V + j;
+    if (f >= n_feats) continue;
+    const int li = b * kPlaneRow + lane;
+    const int64_t Q = (int64_t)sq[li];
+    const int32_t C = (int32_t)sc[li];
+    const int64_t fb = (int64_t)f * num_bins + b;
+    hq[(int64_t)key * per_key + fb] = Q;
+    hc[(int64_t)key * per_key + fb] = C;
+    if (depth > 0) {
+      hq[skey * per_key + fb] = parent_q[pkey * per_key + fb] - Q;
+      hc[skey * per_key + fb] = parent_c[pkey * per_key + fb] - C;
+    }
+  }
+}
+
 // out[e, fo, b] += full[e, feat[fo], b]  (feature selection of compute_histogram3)
 __global__ void hist_gather_features_kernel(const float* __restrict__ Gf,
                                             const float* __restrict__ Hf, int32_t n_keys,
@@ -688,11 +837,28 @@ int fin_words_for(int64_t tiles_per_key) {
     default: LAUNCH(256); break;       \
   }
 
+// plane finalize for many segments with few tiles each (coalesced output rows);
+// the word-per-thread kernels otherwise (few segments: their tile split keeps
+// enough loads in flight)
+static bool use_plane_finalize(int64_t tiles_per_key, int64_t n_keys, int n_chunks, int V,
+                               int num_bins) {
+  return num_bins <= kPlaneMaxBins && tiles_per_key <= 64 && n_keys * n_chunks * V >= 128;
+}
+
 int launch_finalize_f32(int64_t tiles_per_key, const unsigned long long* part,
                         const int32_t* key_tile_start, int32_t n_keys, int32_t n_chunks, int32_t V,
                         int32_t num_bins, int32_t n_feats, const int32_t* shifts,
                         const uint32_t* absmax_bits, const int32_t* n_tiles, int32_t accumulate,
                         float* G, float* H, hipStream_t st) {
+  if (use_plane_finalize(tiles_per_key, n_keys, n_chunks, V, num_bins)) {
+    const int64_t wg = (int64_t)n_keys * n_chunks * V;
+    WGBM_REQUIRE(wg < ((int64_t)1 << 31), "finalize: too many segments");
+    hipLaunchKernelGGL(hist_finalize_plane_f32_kernel, dim3((unsigned)wg), dim3(kPlaneThreads), 0,
+                       st, part, key_tile_start, n_keys, n_chunks, V, num_bins, n_feats, shifts,
+                       absmax_bits, n_tiles, accumulate, G, H);
+    WGBM_LAUNCH_CHECK();
+    return 0;
+  }
   const int fw = fin_words_for(tiles_per_key);
   const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
   WGBM_REQUIRE(tile_words < ((int64_t)1 << 31) &&
@@ -715,6 +881,16 @@ int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
                           int32_t num_eras, int32_t nodes_in_level, int32_t depth,
                           const int64_t* parent_q, const int32_t* parent_c, const int32_t* n_tiles,
                           int64_t* hq, int32_t* hc, hipStream_t st) {
+  if (use_plane_finalize(tiles_per_key, n_list, n_chunks, V, num_bins)) {
+    const int64_t wg = (int64_t)n_list * n_chunks * V;
+    WGBM_REQUIRE(wg < ((int64_t)1 << 31), "finalize: too many segments");
+    hipLaunchKernelGGL(hist_finalize_plane_level_kernel, dim3((unsigned)wg), dim3(kPlaneThreads),
+                       0, st, part, key_tile_start, key_list, n_list, n_chunks, V, num_bins,
+                       n_feats, num_eras, nodes_in_level, depth, parent_q, parent_c, n_tiles, hq,
+                       hc);
+    WGBM_LAUNCH_CHECK();
+    return 0;
+  }
   const int fw = fin_words_for(tiles_per_key);
   const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
   WGBM_REQUIRE(tile_words < ((int64_t)1 << 31) &&
@@ -762,9 +938,13 @@ static int launch_tiles_t(const HistLaunch& a, hipStream_t st) {
     attr_set = true;
   }
   dim3 grid((unsigned)((int64_t)a.n_chunks * a.max_tiles));
-  hipLaunchKernelGGL((hist_tiles_kernel<V, MODE, BT, GATHER, NAT, RPOS>), grid, dim3(kHistThreads), lds,
-                     st, a.codes, a.n_rows, a.stride, a.n_feats, a.resid, a.resid_tree_stride,
-                     a.shifts, a.order, a.tiles, a.n_tiles, a.keys_per_tree, a.num_bins, a.part);
+  void* tm = timer_begin(a.timer_tag);
+  hipExtLaunchKernelGGL((hist_tiles_kernel<V, MODE, BT, GATHER, NAT, RPOS>), grid,
+                        dim3(kHistThreads), lds, st, timer_start_event(tm), timer_stop_event(tm), 0,
+                        a.codes, a.n_rows, a.stride, a.n_feats, a.resid, a.resid_tree_stride,
+                        a.shifts, a.order, a.tiles, a.n_tiles, a.keys_per_tree, a.num_bins,
+                        a.part);
+  timer_end(tm);
   WGBM_LAUNCH_CHECK();
   return 0;
 }

@@ -54,6 +54,8 @@ struct HistLaunch {
   // with order: resid holds the residuals in position order (resid[p] belongs
   // to row order[p]) instead of row order
   int32_t resid_by_pos = 0;
+  // timer tag of the tile kernel (nullptr: not timed)
+  const char* timer_tag = nullptr;
 };
 
 int hist_pick_v(int num_bins);
@@ -104,10 +106,14 @@ int fill_u64(void* p, int64_t n, unsigned long long v, hipStream_t st);
 void* scratch_get(hipStream_t st, size_t bytes, int slot);
 void scratch_release_all();
 
-// optional HIP-event timers around selected kernels
+// optional HIP-event timers of selected kernels: timer_begin(tag) gives a
+// handle (nullptr when timing is off) whose start / stop events the launcher
+// passes to hipExtLaunchKernel; timer_end(handle) files the interval
 bool timer_enabled();
-void* timer_begin(const char* tag, hipStream_t st);
-void timer_end(void* h, hipStream_t st);
+void* timer_begin(const char* tag);
+hipEvent_t timer_start_event(void* h);
+hipEvent_t timer_stop_event(void* h);
+void timer_end(void* h);
 void timer_enable(int on);
 int timer_read(const char* tag, double* total_ms, long* count);
 void timer_reset();

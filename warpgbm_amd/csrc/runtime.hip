@@ -94,8 +94,10 @@ int fill_u64(void* p, int64_t n, unsigned long long v, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
-// kernel timers: when enabled, launchers bracket selected kernels with HIP
-// events recorded on the launch stream; wgbm_timer_read sums the intervals.
+// kernel timers: when enabled, the launcher of a timed kernel attaches a pair
+// of HIP events to the kernel's own dispatch (hipExtLaunchKernel start / stop
+// events), so an interval is the kernel's execution alone, without the
+// dispatch of the packet; wgbm_timer_read sums the intervals per tag.
 // ---------------------------------------------------------------------------
 struct TimerRec {
   std::string tag;
@@ -108,21 +110,27 @@ static std::map<std::string, std::pair<double, long>> g_timer_acc;
 
 bool timer_enabled() { return g_timer_on; }
 
-void* timer_begin(const char* tag, hipStream_t st) {
-  if (!g_timer_on) return nullptr;
+void* timer_begin(const char* tag) {
+  if (!g_timer_on || !tag) return nullptr;
   TimerRec* r = new TimerRec{tag, nullptr, nullptr};
-  if (hipEventCreate(&r->a) != hipSuccess || hipEventCreate(&r->b) != hipSuccess) {
+  if (hipEventCreate(&r->a) != hipSuccess) {
     delete r;
     return nullptr;
   }
-  (void)hipEventRecord(r->a, st);
+  if (hipEventCreate(&r->b) != hipSuccess) {
+    (void)hipEventDestroy(r->a);
+    delete r;
+    return nullptr;
+  }
   return r;
 }
 
-void timer_end(void* h, hipStream_t st) {
+hipEvent_t timer_start_event(void* h) { return h ? ((TimerRec*)h)->a : nullptr; }
+hipEvent_t timer_stop_event(void* h) { return h ? ((TimerRec*)h)->b : nullptr; }
+
+void timer_end(void* h) {
   if (!h) return;
   TimerRec* r = (TimerRec*)h;
-  (void)hipEventRecord(r->b, st);
   std::lock_guard<std::mutex> lk(g_timer_mu);
   g_timer_pending.push_back(*r);
   delete r;
