@@ -638,7 +638,8 @@ __global__ void absmax_finish_kernel(const uint32_t* __restrict__ partial, int32
 // nullptr) or the first *n_list entries of key_list.  seg: int64 [n_keys+1]
 // (nullptr => a single segment [0, total)).
 // --------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void plan_tiles_kernel(
+// (blockDim.x == 1024)
+__device__ void plan_tiles_body(
     const int64_t* __restrict__ seg, int64_t total_rows, int32_t n_keys,
     const int32_t* __restrict__ key_list, int32_t tile_rows,
     int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
@@ -723,6 +724,17 @@ __global__ __launch_bounds__(1024) void plan_tiles_kernel(
       write_tile(key, b0, b1, first, j);
   }
 }
+
+__global__ __launch_bounds__(1024) void plan_tiles_kernel(
+    const int64_t* __restrict__ seg, int64_t total_rows, int32_t n_keys,
+    const int32_t* __restrict__ key_list, int32_t tile_rows,
+    int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
+    int32_t* __restrict__ n_tiles, const uint32_t* __restrict__ abs_part, int32_t n_abs,
+    int32_t qbits, uint32_t* __restrict__ absmax_bits, int32_t* __restrict__ shift) {
+  plan_tiles_body(seg, total_rows, n_keys, key_list, tile_rows, max_tiles, tiles, key_tile_start,
+                  n_tiles, abs_part, n_abs, qbits, absmax_bits, shift);
+}
+
 
 // --------------------------------------------------------------------------
 // era sort for the ABI path: rows -> era-grouped positions
