@@ -132,3 +132,29 @@ def test_importance_adds_in_node_order():
         np.add.at(a.T, idx, val)
         _add_in_order(b.T, idx, val)
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), trial
+
+
+def test_era_layout_matches_unique_sort():
+    """The era bookkeeping (warpgbm/core.py:540: sorted unique eras, inverse
+    indices, stable era order, offsets) equals the np.unique + stable argsort
+    restatement, including the linear path for non-decreasing era ids."""
+    from warpgbm_amd import device as D
+
+    def by_sort(era):
+        uniq, inv = np.unique(np.asarray(era), return_inverse=True)
+        inv = inv.astype(np.int32).reshape(-1)
+        order = np.argsort(inv, kind="stable").astype(np.int32)
+        counts = np.bincount(inv, minlength=len(uniq)).astype(np.int64)
+        start = np.zeros(len(uniq) + 1, dtype=np.int64)
+        np.cumsum(counts, out=start[1:])
+        return uniq, inv, order, start
+
+    rng = np.random.default_rng(0)
+    cases = [np.ones(10, np.int32), np.repeat(np.arange(5), 7), np.array([3]),
+             np.repeat([-2, 0, 5, 9], [1, 4, 2, 3]), rng.integers(0, 4, 50),
+             np.sort(rng.integers(0, 9, 100)), np.repeat(np.array(["a", "b", "c"]), 3),
+             np.array([1.5, 1.5, 2.0]), np.array([2, 2, 1, 1])]
+    for era in cases:
+        got, ref = D.era_layout(era), by_sort(era)
+        for a, b in zip(got, ref):
+            assert np.array_equal(a, b) and a.dtype == b.dtype, era

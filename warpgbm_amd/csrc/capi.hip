@@ -325,9 +325,24 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
   WGBM_REQUIRE(H == (1 << (max_depth + 1)) - 1, "H must be 2^(max_depth+1)-1");
   if (n == 0) return 0;
   WGBM_REQUIRE(codes && out && (n_rounds == 0 || (feat && bin && leaf)), "null pointer");
-  hipLaunchKernelGGL(predict_heap_kernel, dim3(nblocks(n * K, 256)), dim3(256), 0, S(stream),
-                     codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds, K, H,
-                     max_depth, learning_rate, out);
+  if (n_rounds == 0) return 0;
+  int32_t RB = 0, TC = 0;
+  size_t lds = 0;
+  if (predict_rows_plan(codes_stride, K, H, n_rounds, &RB, &TC, &lds)) {
+    static bool attr = false;
+    if (!attr) {
+      WGBM_CHECK(hipFuncSetAttribute((const void*)predict_rows_kernel,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      attr = true;
+    }
+    hipLaunchKernelGGL(predict_rows_kernel, dim3(nblocks(n, RB)), dim3(1024), lds, S(stream),
+                       codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds, K, H,
+                       max_depth, learning_rate, RB, TC, out);
+  } else {
+    hipLaunchKernelGGL(predict_heap_kernel, dim3(nblocks(n * K, 256)), dim3(256), 0, S(stream),
+                       codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds, K, H,
+                       max_depth, learning_rate, out);
+  }
   WGBM_LAUNCH_CHECK();
   return 0;
 }

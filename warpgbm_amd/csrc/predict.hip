@@ -9,6 +9,8 @@
 // order, so out[i] = ((out[i] + lr*v_0) + lr*v_1) + ... is deterministic; it is
 // one of the orders the reference's atomics may produce.  Each product lr*v is
 // rounded to float32 before the add, as in the reference.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -78,6 +80,130 @@ __global__ void predict_heap_kernel(const int8_t* __restrict__ codes, int64_t n,
     acc = acc + lr * leaf[t * H + h];
   }
   out[gid] = acc;
+}
+
+// Row-block inference (same results as predict_heap_kernel): a workgroup of
+// 1024 threads stages a block of RB rows of codes in LDS (one coalesced read
+// of the rows instead of a dependent byte gather per tree level) and walks
+// the trees a chunk of TC at a time: the chunk's node words and leaf values
+// are staged in LDS, every (row, tree) pair of the chunk is walked by its own
+// thread (all walks independent: D dependent LDS reads each instead of D per
+// tree in sequence), the products lr * leaf go to an LDS table [row][tree],
+// and one thread per (row, class) adds them in tree order.  TC is a multiple
+// of K, so tree t0 + j belongs to class j % K.
+//   LDS: rows [RB][S + 4] bytes (a 4-byte pad per row spreads the rows of
+//   one wave over the banks), nodes [TC][H] (feature << 8 | bin, or ~0 for a
+//   leaf), leaves [TC][H], vals [RB][TC].
+constexpr int kPredThreads = 1024;
+constexpr int kPredMaxAcc = 4;  // (row, class) accumulators per thread
+constexpr uint32_t kPredLeaf = 0xffffffffu;
+
+__global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
+    const int8_t* __restrict__ codes, int64_t n, int64_t S, int32_t num_bins,
+    const int32_t* __restrict__ feat, const int32_t* __restrict__ bin,
+    const float* __restrict__ leaf, int32_t n_rounds, int32_t K, int32_t H, int32_t max_depth,
+    float lr, int32_t RB, int32_t TC, float* __restrict__ out) {
+  extern __shared__ uint32_t psm[];
+  const int Sp = (int)S + 4;
+  uint8_t* rows_s = reinterpret_cast<uint8_t*>(psm);
+  uint32_t* nodes_s = psm + (RB * Sp) / 4;
+  float* leaves_s = reinterpret_cast<float*>(nodes_s + TC * H);
+  float* vals_s = leaves_s + TC * H;
+  const int64_t row0 = (int64_t)blockIdx.x * RB;
+  const int nr = (int)(n - row0 < RB ? n - row0 : RB);
+  const int tid = threadIdx.x;
+  // stage the row block: 16-byte global loads, 4-byte LDS stores
+  {
+    const int q_per_row = (int)(S / 16);
+    const int nq = nr * q_per_row;
+    for (int q = tid; q < nq; q += kPredThreads) {
+      const int r = q / q_per_row, c = q - r * q_per_row;
+      typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+      const u4 v = __builtin_nontemporal_load(
+          reinterpret_cast<const u4*>(codes + (row0 + r) * S) + c);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(rows_s + r * Sp + c * 16);
+      dst[0] = v.x;
+      dst[1] = v.y;
+      dst[2] = v.z;
+      dst[3] = v.w;
+    }
+  }
+  // accumulators: pair m*1024 + tid = (row, class) = (p % RB, p / RB)
+  float acc[kPredMaxAcc];
+#pragma unroll
+  for (int m = 0; m < kPredMaxAcc; ++m) {
+    const int p = m * kPredThreads + tid;
+    const int r = p % RB, k = p / RB;
+    acc[m] = (k < K && r < nr) ? out[(row0 + r) * K + k] : 0.0f;
+  }
+  const int T = n_rounds * K;
+  for (int t0 = 0; t0 < T; t0 += TC) {
+    const int tc = T - t0 < TC ? T - t0 : TC;
+    __syncthreads();  // rows staged / previous chunk's vals consumed
+    for (int i = tid; i < tc * H; i += kPredThreads) {
+      const int64_t g = (int64_t)t0 * H + i;
+      const int f = feat[g];
+      nodes_s[i] = f < 0 ? kPredLeaf : ((uint32_t)f << 8) | (uint32_t)(bin[g] & 0xff);
+      leaves_s[i] = leaf[g];
+    }
+    __syncthreads();
+    // walks: pair p = (row p % RB, tree p / RB) of the chunk
+    for (int p = tid; p < RB * tc; p += kPredThreads) {
+      const int r = p % RB, tl = p / RB;
+      if (r >= nr) continue;
+      const uint32_t* nd = nodes_s + tl * H;
+      const uint8_t* row = rows_s + r * Sp;
+      int h = 0;
+      uint32_t w = nd[0];
+      for (int d = 0; d < max_depth; ++d) {
+        if (w == kPredLeaf) break;
+        const uint32_t f = w >> 8;
+        const int c = (int)row[f < (uint32_t)S ? f : (uint32_t)S - 1];  // stays in the row
+        const int b = (int)(w & 0xffu);
+        h = 2 * h + ((c <= b || c == num_bins) ? 1 : 2);
+        w = nd[h];
+      }
+      vals_s[r * TC + tl] = lr * leaves_s[tl * H + h];
+    }
+    __syncthreads();
+    // ordered sums: trees t0 + j of class k are j = k, k + K, ... (t0 % K == 0)
+#pragma unroll
+    for (int m = 0; m < kPredMaxAcc; ++m) {
+      const int p = m * kPredThreads + tid;
+      const int r = p % RB, k = p / RB;
+      if (k < K && r < nr) {
+        float a = acc[m];
+        for (int j = k; j < tc; j += K) a = a + vals_s[r * TC + j];
+        acc[m] = a;
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kPredMaxAcc; ++m) {
+    const int p = m * kPredThreads + tid;
+    const int r = p % RB, k = p / RB;
+    if (k < K && r < nr) out[(row0 + r) * K + k] = acc[m];
+  }
+}
+
+// block shape of predict_rows_kernel: 0 when the trees or rows do not fit
+// (then predict_heap_kernel is used)
+int predict_rows_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
+                      int32_t* TC_out, size_t* lds_out) {
+  constexpr int64_t kBudget = 64 * 1024;
+  if (S % 16 != 0 || S >= (1 << 24) || (int64_t)8 * H * K > 32 * 1024) return 0;
+  const int64_t T = (int64_t)n_rounds * K;
+  int64_t m = std::max<int64_t>(1, (16 * 1024) / ((int64_t)8 * H * K));
+  int64_t TC = std::min<int64_t>(m * K, std::max<int64_t>(K, (T + K - 1) / K * K));
+  const int64_t Sp = S + 4;
+  int64_t RB = (kBudget - 8 * TC * H) / (Sp + 4 * TC);
+  RB = std::min<int64_t>(RB, 256);
+  RB = std::min<int64_t>(RB, (int64_t)kPredMaxAcc * kPredThreads / K);
+  if (RB < 16) return 0;
+  *RB_out = (int32_t)RB;
+  *TC_out = (int32_t)TC;
+  *lds_out = (size_t)(RB * Sp + 8 * TC * H + 4 * RB * TC);
+  return 1;
 }
 
 // in-place row softmax over K logits: exp(x - max) / sum, sequential in k

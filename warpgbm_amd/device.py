@@ -206,8 +206,23 @@ def bin_matrix(Xd: torch.Tensor, edges: torch.Tensor, with_cm: bool) -> Codes:
 
 def era_layout(era_id: np.ndarray):
     """Sorted unique eras, era index per row, rows sorted by era (stable) and
-    era offsets (warpgbm/core.py:540: torch.unique(..., return_inverse=True))."""
-    uniq, inv = np.unique(np.asarray(era_id), return_inverse=True)
+    era offsets (warpgbm/core.py:540: torch.unique(..., return_inverse=True)).
+    Era ids that are already non-decreasing (one era, or contiguous eras) take
+    a linear path with the same result as the sort."""
+    era = np.asarray(era_id).reshape(-1)
+    n = era.shape[0]
+    if n > 0 and (n == 1 or bool(np.all(era[1:] >= era[:-1]))):
+        first = np.ones(n, dtype=bool)
+        first[1:] = era[1:] != era[:-1]
+        idx = np.flatnonzero(first)
+        uniq = era[idx]
+        inv = (np.cumsum(first) - 1).astype(np.int32)
+        order = np.arange(n, dtype=np.int32)
+        start = np.empty(len(idx) + 1, dtype=np.int64)
+        start[:-1] = idx
+        start[-1] = n
+        return uniq, inv, order, start
+    uniq, inv = np.unique(era, return_inverse=True)
     inv = inv.astype(np.int32).reshape(-1)
     order = np.argsort(inv, kind="stable").astype(np.int32)
     counts = np.bincount(inv, minlength=len(uniq)).astype(np.int64)
