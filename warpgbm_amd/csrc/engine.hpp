@@ -56,10 +56,6 @@ __global__ void root_setup_kernel(const int32_t* root_order, int64_t n, int32_t 
                                   const int64_t* era_start, int32_t E, int32_t* order,
                                   int64_t* seg, int32_t* present, int64_t* tot_q,
                                   int64_t* tot_c, unsigned long long* best, int32_t* agree_max);
-__global__ void segment_totals_kernel(const Tile* tiles, const int32_t* n_tiles,
-                                      const int32_t* order, const float* resid, int64_t n,
-                                      const int32_t* shifts, int32_t keys_per_tree,
-                                      int64_t* tot_q, int64_t* tot_c);
 __global__ void level_finish_kernel(int32_t depth, int32_t max_depth, int32_t T, int32_t E,
                                     int32_t B, const int32_t* present,
                                     const unsigned long long* best, int32_t* split_l,
@@ -69,25 +65,48 @@ __global__ void level_finish_kernel(int32_t depth, int32_t max_depth, int32_t T,
                                     float* leaf_val, TreeRecord rec, int64_t* tot_q_next,
                                     int64_t* tot_c_next, unsigned long long* best_next,
                                     int32_t* agree_max_next);
-__global__ void partition_count_kernel(
-    const Tile* tiles, const int32_t* n_tiles, const int32_t* order, int32_t E, int32_t nodes,
-    int32_t max_split_depth_ok, const int32_t* split_l, const int32_t* split_b,
-    const int32_t* feat_sel, const int8_t* codes_cm, int64_t n, const float* resid,
-    const int32_t* shifts, const float* leaf_val, float lr, float* pred, int64_t pstride,
-    int64_t pcol, uint8_t* dirbit, int32_t* tile_left, int64_t* tot_q_next,
-    int64_t* tot_c_next);
-__global__ void partition_scan_kernel(int32_t T, int32_t nodes, int32_t E, const int64_t* seg,
-                                      const Tile* tiles, const int32_t* key_tile_start,
-                                      const int32_t* n_tiles, const int32_t* tile_left,
-                                      const int32_t* split_l,
-                                      int64_t* Lk, int64_t* tile_lbase, int64_t* tile_rbase,
-                                      int64_t* seg_next, int32_t* present_next,
-                                      int32_t* key_list_next);
-__global__ void partition_scatter_kernel(const Tile* tiles, const int32_t* n_tiles,
-                                         const int32_t* order, int32_t E,
-                                         const int32_t* split_l, const uint8_t* dirbit,
-                                         const int64_t* tile_lbase, const int64_t* tile_rbase,
-                                         int32_t* order_next);
+// partition over position blocks (engine_kernels.hip)
+constexpr int kPartBlock = 1024;   // positions per block
+constexpr int kPartThreads = 256;
+struct RouteArgs {
+  int32_t mode;  // 0 root totals, 1 split level, 2 last level (leaves only)
+  const int64_t* seg;
+  int32_t n_keys;
+  int64_t n_pos;
+  const int32_t* order;
+  int32_t E, nodes;
+  const int32_t* present;
+  const int32_t* split_l;
+  const int32_t* split_b;
+  const int32_t* feat_sel;
+  const int8_t* codes_cm;
+  int64_t n;
+  const float* resid;
+  const int32_t* shifts;
+  const float* leaf_val;
+  float lr;
+  float* pred;
+  int64_t pstride, pcol;
+  uint8_t* dirbit;
+  int32_t* keyp;
+  int64_t* Lk;
+  int64_t* tot_q;  // mode 0: of the level's keys; mode 1: of the next level's keys
+  int64_t* tot_c;
+  int32_t *blk_fk, *blk_fl, *blk_lk, *blk_ll;
+};
+__global__ void route_kernel(RouteArgs a);
+__global__ void node_scan_kernel(int32_t T, int32_t nodes, int32_t E, int64_t n_pos,
+                                 const int64_t* seg, const int32_t* present,
+                                 const int32_t* split_l, const int64_t* Lk, int64_t* Lk_next,
+                                 int64_t* seg_next, int32_t* present_next,
+                                 int32_t* key_list_next);
+__global__ void block_carry_kernel(int32_t nb, const int32_t* fk, const int32_t* fl,
+                                   const int32_t* lk, const int32_t* ll, int32_t* S,
+                                   int32_t* carry);
+__global__ void scatter_kernel(int64_t n_pos, int32_t E, const int64_t* seg,
+                               const int64_t* seg_next, const int32_t* keyp,
+                               const uint8_t* dirbit, const int32_t* carry,
+                               const int32_t* order, int32_t* order_next);
 __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v);
 
 // split kernels (split.hip)

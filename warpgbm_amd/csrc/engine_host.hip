@@ -26,9 +26,8 @@ struct Engine {
   EngineConfig c;
   int V = 16, n_chunks = 1, qbits = 28;
   int H = 1;
-  int part_tile_rows = 2048;
   int64_t hist_tile_rows = 0;  // 0: automatic
-  int64_t n_keys_max = 0, max_ptiles = 0, max_htiles = 0;
+  int64_t n_keys_max = 0, max_htiles = 0, nb = 0;
   // buffers
   float* resid = nullptr;
   uint32_t* absmax = nullptr;
@@ -39,14 +38,12 @@ struct Engine {
   int64_t* totc[2] = {nullptr, nullptr};
   int32_t* present[2] = {nullptr, nullptr};
   int32_t* key_list[2] = {nullptr, nullptr};
-  uint8_t* dirbit = nullptr;
-  Tile* ptiles = nullptr;
-  int32_t* pkts = nullptr;
-  int32_t* pn = nullptr;
-  int32_t* tile_left = nullptr;
-  int64_t* lbase = nullptr;
-  int64_t* rbase = nullptr;
-  int64_t* Lk = nullptr;
+  // partition over position blocks of kPartBlock positions
+  uint8_t* dirbit = nullptr;            // [T*N] 0 left, 1 right, 2 stays
+  int32_t* keyp = nullptr;              // [T*N] segment key of each position
+  int64_t* Lk[2] = {nullptr, nullptr};  // left rows per segment (level parity)
+  int32_t *blk_fk = nullptr, *blk_fl = nullptr, *blk_lk = nullptr, *blk_ll = nullptr;
+  int32_t *blk_S = nullptr, *blk_carry = nullptr;
   Tile* htiles = nullptr;
   int32_t* hkts = nullptr;
   int32_t* hn = nullptr;
@@ -171,14 +168,16 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     E_ALLOC(e->bdir, T * hist_nodes_max * W * F * (B - 1));
   }
   E_ALLOC(e->dirbit, T * N);
-  e->max_ptiles = T * N / e->part_tile_rows + e->n_keys_max + 1;
-  E_ALLOC(e->ptiles, e->max_ptiles);
-  E_ALLOC(e->pkts, e->n_keys_max + 1);
-  E_ALLOC(e->pn, 1);
-  E_ALLOC(e->tile_left, e->max_ptiles);
-  E_ALLOC(e->lbase, e->max_ptiles);
-  E_ALLOC(e->rbase, e->max_ptiles);
-  E_ALLOC(e->Lk, e->n_keys_max);
+  E_ALLOC(e->keyp, T * N);
+  E_ALLOC(e->Lk[0], e->n_keys_max);
+  E_ALLOC(e->Lk[1], e->n_keys_max);
+  e->nb = (T * N + kPartBlock - 1) / kPartBlock;
+  E_ALLOC(e->blk_fk, e->nb);
+  E_ALLOC(e->blk_fl, e->nb);
+  E_ALLOC(e->blk_lk, e->nb);
+  E_ALLOC(e->blk_ll, e->nb);
+  E_ALLOC(e->blk_S, e->nb);
+  E_ALLOC(e->blk_carry, e->nb);
   E_ALLOC(e->hkts, e->n_keys_max + 1);
   E_ALLOC(e->hn, 1);
   if (E > 1) {
@@ -265,19 +264,46 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
 
   // root segments and totals
   int cur = 0;
-  hipLaunchKernelGGL(root_setup_kernel, dim3(blocks_for(std::max<int64_t>((int64_t)T * N, T * E), 256)),
+  const int64_t n_pos = (int64_t)T * N;
+  hipLaunchKernelGGL(root_setup_kernel, dim3(blocks_for(std::max<int64_t>(n_pos, T * E), 256)),
                      dim3(256), 0, st, c.root_order, N, T, c.era_start, E, e->order[0],
                      e->seg[0], e->present[0], e->totq[0], e->totc[0], e->best, e->agree_max);
   WGBM_LAUNCH_CHECK();
-  hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[0], (int64_t)0, T * E,
-                     (const int32_t*)nullptr, e->part_tile_rows, (int32_t)e->max_ptiles, e->ptiles,
-                     e->pkts, e->pn, (const uint32_t*)nullptr, 0, 0, (uint32_t*)nullptr,
-                     (int32_t*)nullptr);
+  hipLaunchKernelGGL(fill_u64_kernel, dim3(blocks_for((int64_t)T * E, 256)), dim3(256), 0, st,
+                     (unsigned long long*)e->Lk[0], (int64_t)T * E, 0ull);
   WGBM_LAUNCH_CHECK();
-  hipLaunchKernelGGL(segment_totals_kernel, dim3((unsigned)e->max_ptiles), dim3(256), 0, st,
-                     e->ptiles, e->pn, e->order[0], e->resid, N, e->shifts, E, e->totq[0],
-                     e->totc[0]);
-  WGBM_LAUNCH_CHECK();
+  RouteArgs ra{};
+  ra.n_pos = n_pos;
+  ra.E = E;
+  ra.feat_sel = feat_sel;
+  ra.codes_cm = c.codes_cm;
+  ra.n = N;
+  ra.resid = e->resid;
+  ra.shifts = e->shifts;
+  ra.leaf_val = e->leaf_val;
+  ra.lr = c.learning_rate;
+  ra.pred = pred;
+  ra.pstride = c.objective == 0 ? 1 : T;
+  ra.pcol = c.objective == 0 ? 0 : 1;
+  ra.dirbit = e->dirbit;
+  ra.keyp = e->keyp;
+  ra.blk_fk = e->blk_fk;
+  ra.blk_fl = e->blk_fl;
+  ra.blk_lk = e->blk_lk;
+  ra.blk_ll = e->blk_ll;
+  {
+    RouteArgs r0 = ra;
+    r0.mode = 0;
+    r0.seg = e->seg[0];
+    r0.n_keys = T * E;
+    r0.order = e->order[0];
+    r0.nodes = 1;
+    r0.present = e->present[0];
+    r0.tot_q = e->totq[0];
+    r0.tot_c = e->totc[0];
+    hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, r0);
+    WGBM_LAUNCH_CHECK();
+  }
 
   if (e->des_direct) {
     hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks_for(F, 256)), dim3(256), 0, st, e->local_of,
@@ -418,28 +444,34 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                        e->best + (hcur ^ 1) * e->pick_stride,
                        e->agree_max ? e->agree_max + (hcur ^ 1) * e->pick_stride : nullptr);
     WGBM_LAUNCH_CHECK();
-    // ---- partition (or final leaf update)
-    hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur], (int64_t)0,
-                       n_keys, (const int32_t*)nullptr, e->part_tile_rows, (int32_t)e->max_ptiles,
-                       e->ptiles, e->pkts, e->pn, (const uint32_t*)nullptr, 0, 0,
-                       (uint32_t*)nullptr, (int32_t*)nullptr);
-    WGBM_LAUNCH_CHECK();
-    const int64_t pstride = c.objective == 0 ? 1 : T;
-    const int64_t pcol = c.objective == 0 ? 0 : 1;
-    hipLaunchKernelGGL(partition_count_kernel, dim3((unsigned)e->max_ptiles), dim3(256), 0, st,
-                       e->ptiles, e->pn, e->order[cur], E, nodes, d < D ? 1 : 0, e->split_l,
-                       e->split_b, feat_sel, c.codes_cm, N, e->resid, e->shifts, e->leaf_val,
-                       c.learning_rate, pred, pstride, pcol, e->dirbit, e->tile_left,
-                       e->totq[nxt], e->totc[nxt]);
+    // ---- partition (or final leaf update): route every position, then the
+    // next level's segments and the stable scatter
+    RouteArgs rl = ra;
+    rl.mode = d < D ? 1 : 2;
+    rl.seg = e->seg[cur];
+    rl.n_keys = n_keys;
+    rl.order = e->order[cur];
+    rl.nodes = nodes;
+    rl.present = e->present[cur];
+    rl.split_l = e->split_l;
+    rl.split_b = e->split_b;
+    rl.Lk = e->Lk[d & 1];
+    rl.tot_q = e->totq[nxt];
+    rl.tot_c = e->totc[nxt];
+    hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, rl);
     WGBM_LAUNCH_CHECK();
     if (d < D) {
-      hipLaunchKernelGGL(partition_scan_kernel, dim3(1), dim3(1024), 0, st, T, nodes, E,
-                         e->seg[cur], e->ptiles, e->pkts, e->pn, e->tile_left, e->split_l, e->Lk,
-                         e->lbase, e->rbase, e->seg[nxt], e->present[nxt], e->key_list[nxt]);
+      hipLaunchKernelGGL(node_scan_kernel, dim3(blocks_for((int64_t)n_tn, 4)), dim3(256), 0, st, T,
+                         nodes, E, n_pos, e->seg[cur], e->present[cur], e->split_l,
+                         e->Lk[d & 1], e->Lk[(d + 1) & 1], e->seg[nxt], e->present[nxt],
+                         e->key_list[nxt]);
       WGBM_LAUNCH_CHECK();
-      hipLaunchKernelGGL(partition_scatter_kernel, dim3((unsigned)e->max_ptiles), dim3(256), 0, st,
-                         e->ptiles, e->pn, e->order[cur], E, e->split_l, e->dirbit, e->lbase,
-                         e->rbase, e->order[nxt]);
+      hipLaunchKernelGGL(block_carry_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb,
+                         e->blk_fk, e->blk_fl, e->blk_lk, e->blk_ll, e->blk_S, e->blk_carry);
+      WGBM_LAUNCH_CHECK();
+      hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, n_pos,
+                         E, e->seg[cur], e->seg[nxt], e->keyp, e->dirbit, e->blk_carry,
+                         e->order[cur], e->order[nxt]);
       WGBM_LAUNCH_CHECK();
     }
     cur = nxt;

@@ -95,32 +95,6 @@ __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_
   }
 }
 
-// sum of quantised residuals and row count per segment (root totals)
-__global__ __launch_bounds__(256) void segment_totals_kernel(
-    const Tile* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-    const int32_t* __restrict__ order, const float* __restrict__ resid, int64_t n,
-    const int32_t* __restrict__ shifts, int32_t keys_per_tree, int64_t* __restrict__ tot_q,
-    int64_t* __restrict__ tot_c) {
-  const int tile = blockIdx.x;
-  if (tile >= *n_tiles) return;
-  const Tile tl = tiles[tile];
-  const int t = tl.key / keys_per_tree;
-  const int s = shifts[t];
-  const float* r = resid + (int64_t)t * n;
-  int64_t q = 0;
-  for (int64_t p = tl.begin + threadIdx.x; p < tl.end; p += blockDim.x)
-    q += wgbm_quantise(r[order[p]], s);
-  q = wgbm_wave_sum(q);
-  __shared__ int64_t sq[4];
-  if ((threadIdx.x & 63) == 0) sq[threadIdx.x >> 6] = q;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int64_t tq = sq[0] + sq[1] + sq[2] + sq[3];
-    atomicAdd((unsigned long long*)&tot_q[tl.key], (unsigned long long)tq);
-    atomicAdd((unsigned long long*)&tot_c[tl.key], (unsigned long long)(tl.end - tl.begin));
-  }
-}
-
 // ---------------------------------------------------------------------------
 // per-level bookkeeping: leaf values and the tree record
 //   leaf value = mean of the node's residuals (warpgbm/core.py:599, :614),
@@ -219,231 +193,306 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// partition, pass 1: per tile, route rows (code <= bin goes left,
-// warpgbm/core.py:629), count lefts and accumulate child totals.  Tiles of a
-// leaf node instead add lr * leaf to the rows' predictions (core.py:602-605).
+// Partition over position blocks.
+//
+// Rows stay in the position space [0, T*N) of the whole round: a node that
+// does not split (a leaf, or a node under a leaf) keeps its rows where they
+// are -- its left child gets all of them, its right child none -- so the
+// next level's segments of one parent node cover exactly the parent's
+// position range, left child eras first, then right child eras:
+//     next key of (tree t, child 2*node + side, era e) = 2*tn*E + side*E + e,
+// and the next level's offsets come from a scan over the node's own eras
+// (no scan over all segments).  The blocks below are fixed ranges of
+// kPartBlock positions, independent of the segment boundaries, so a level
+// with many small segments (deep DES levels: 2^d nodes x 500 eras) costs the
+// same launches as one with a single segment.
+//
+// route:   direction of every row of a split node (code <= bin goes left,
+//          warpgbm/core.py:629), leaf update of the rows of a node that stops
+//          here (core.py:602-605), per-(block, segment) left counts and child
+//          totals reduced in LDS and added to the segment's words; the key of
+//          every position (for the scatter) and the block's first / last
+//          segment with its left count (for the carry).  Mode 0 only sums the
+//          quantised residuals and rows of every segment (root totals).
+// node_scan: one wave per (tree, node): the next level's segment offsets, the
+//          presence of the children and the histogram key list (the smaller
+//          child of every split, core.py:636-643).
+// carry:   per block, the left rows of its first segment in earlier blocks
+//          (a segmented scan over the blocks).
+// scatter: stable destination of every row: left rank in its segment = left
+//          rows before it in the block (block prefix) - left rows before the
+//          segment's start in the block (+ the carry when the segment began in
+//          an earlier block).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void partition_count_kernel(
-    const Tile* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-    const int32_t* __restrict__ order, int32_t E, int32_t nodes, int32_t max_split_depth_ok,
-    const int32_t* __restrict__ split_l, const int32_t* __restrict__ split_b,
-    const int32_t* __restrict__ feat_sel, const int8_t* __restrict__ codes_cm, int64_t n,
-    const float* __restrict__ resid, const int32_t* __restrict__ shifts,
-    const float* __restrict__ leaf_val, float lr, float* __restrict__ pred, int64_t pstride,
-    int64_t pcol, uint8_t* __restrict__ dirbit, int32_t* __restrict__ tile_left,
-    int64_t* __restrict__ tot_q_next, int64_t* __restrict__ tot_c_next) {
-  const int tile = blockIdx.x;
-  if (tile >= *n_tiles) return;
-  const Tile tl = tiles[tile];
-  const int tn = tl.key / E;
-  const int e = tl.key - tn * E;
-  const int t = tn / nodes;
-  const int node = tn - t * nodes;
-  const int l = max_split_depth_ok ? split_l[tn] : -1;
-  if (l < 0) {
-    const float v = lr * leaf_val[tn];
-    float* pc = pred + (int64_t)t * pcol;
-    for (int64_t p = tl.begin + threadIdx.x; p < tl.end; p += blockDim.x) {
-      const int64_t row = order[p];
-      pc[row * pstride] = pc[row * pstride] + v;
-    }
-    if (threadIdx.x == 0) tile_left[tile] = 0;
-    return;
+__device__ inline int seg_key_of(const int64_t* __restrict__ seg, int lo, int hi, int64_t p) {
+  // the key k in [lo, hi] with seg[k] <= p < seg[k + 1] (segments may be empty)
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (seg[mid] <= p) lo = mid; else hi = mid - 1;
   }
-  const int8_t* col = codes_cm + (int64_t)feat_sel[l] * n;
-  const int sb = split_b[tn];
-  const int s = shifts[t];
-  const float* r = resid + (int64_t)t * n;
-  int64_t ql = 0, qr = 0;
-  int32_t nl = 0, nr = 0;
-  for (int64_t p = tl.begin + threadIdx.x; p < tl.end; p += blockDim.x) {
-    const int32_t row = order[p];
-    const bool right = (int)col[row] > sb;
-    dirbit[p] = right ? 1 : 0;
-    const int64_t q = wgbm_quantise(r[row], s);
-    if (right) {
-      qr += q;
-      ++nr;
-    } else {
-      ql += q;
-      ++nl;
-    }
+  return lo;
+}
+
+__global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
+  // per-segment sums of the block, in the slot of the segment's first
+  // position in the block (distinct for distinct non-empty segments; empty
+  // segments own no position)
+  __shared__ int64_t s_ql[kPartBlock], s_qr[kPartBlock];
+  __shared__ int32_t s_nl[kPartBlock], s_nr[kPartBlock], s_key[kPartBlock];
+  __shared__ int s_k[2];
+  const int tid = threadIdx.x;
+  const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
+  const int64_t p1 = p0 + kPartBlock < a.n_pos ? p0 + kPartBlock : a.n_pos;
+  if (tid == 0) {
+    s_k[0] = seg_key_of(a.seg, 0, a.n_keys - 1, p0);
+    s_k[1] = seg_key_of(a.seg, 0, a.n_keys - 1, p1 - 1);
   }
-  ql = wgbm_wave_sum(ql);
-  qr = wgbm_wave_sum(qr);
-  nl = wgbm_wave_sum(nl);
-  nr = wgbm_wave_sum(nr);
-  __shared__ int64_t s_ql[4], s_qr[4];
-  __shared__ int32_t s_nl[4], s_nr[4];
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    s_ql[w] = ql;
-    s_qr[w] = qr;
-    s_nl[w] = nl;
-    s_nr[w] = nr;
+  for (int i = tid; i < kPartBlock; i += kPartThreads) {
+    s_ql[i] = 0;
+    s_qr[i] = 0;
+    s_nl[i] = 0;
+    s_nr[i] = 0;
+    s_key[i] = -1;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int64_t a = 0, b = 0;
-    int32_t c = 0, d = 0;
-    for (int k = 0; k < 4; ++k) {
-      a += s_ql[k];
-      b += s_qr[k];
-      c += s_nl[k];
-      d += s_nr[k];
+  const int klo = s_k[0], khi = s_k[1];
+  for (int j = 0; j < kPartBlock / kPartThreads; ++j) {
+    const int64_t p = p0 + j * kPartThreads + tid;
+    if (p >= p1) break;
+    const int k = seg_key_of(a.seg, klo, khi, p);
+    const int64_t sk = a.seg[k];
+    const int slot = (int)((sk > p0 ? sk : p0) - p0);
+    const int tn = k / a.E;
+    const int t = tn / a.nodes;
+    const int32_t row = a.order[p];
+    if (a.mode == 0) {
+      const int64_t q = wgbm_quantise(a.resid[(int64_t)t * a.n + row], a.shifts[t]);
+      s_key[slot] = k;
+      atomicAdd((unsigned long long*)&s_ql[slot], (unsigned long long)q);
+      atomicAdd(&s_nl[slot], 1);
+      continue;
     }
-    tile_left[tile] = c;
-    const int64_t kl = (((int64_t)t * 2 * nodes) + 2 * node) * E + e;
-    const int64_t kr = kl + E;
-    atomicAdd((unsigned long long*)&tot_q_next[kl], (unsigned long long)a);
-    atomicAdd((unsigned long long*)&tot_q_next[kr], (unsigned long long)b);
-    atomicAdd((unsigned long long*)&tot_c_next[kl], (unsigned long long)c);
-    atomicAdd((unsigned long long*)&tot_c_next[kr], (unsigned long long)d);
+    a.keyp[p] = k;
+    uint8_t dir = 2;  // stays in place
+    if (a.present[tn]) {
+      const int l = a.mode == 2 ? -1 : a.split_l[tn];
+      if (l < 0) {
+        // the node is a leaf: add lr * leaf to its rows' predictions
+        float* pc = a.pred + (int64_t)t * a.pcol + (int64_t)row * a.pstride;
+        *pc = *pc + a.lr * a.leaf_val[tn];
+      } else {
+        const bool right = (int)a.codes_cm[(int64_t)a.feat_sel[l] * a.n + row] > a.split_b[tn];
+        const int64_t q = wgbm_quantise(a.resid[(int64_t)t * a.n + row], a.shifts[t]);
+        dir = right ? 1 : 0;
+        s_key[slot] = k;
+        if (right) {
+          atomicAdd((unsigned long long*)&s_qr[slot], (unsigned long long)q);
+          atomicAdd(&s_nr[slot], 1);
+        } else {
+          atomicAdd((unsigned long long*)&s_ql[slot], (unsigned long long)q);
+          atomicAdd(&s_nl[slot], 1);
+        }
+      }
+    }
+    a.dirbit[p] = dir;
+  }
+  __syncthreads();
+  for (int i = tid; i < kPartBlock; i += kPartThreads) {
+    const int k = s_key[i];
+    if (k < 0) continue;  // no summed rows start here
+    if (a.mode == 0) {
+      atomicAdd((unsigned long long*)&a.tot_q[k], (unsigned long long)s_ql[i]);
+      atomicAdd((unsigned long long*)&a.tot_c[k], (unsigned long long)(int64_t)s_nl[i]);
+      continue;
+    }
+    const int tn = k / a.E;
+    const int e = k - tn * a.E;
+    const int64_t kl = (int64_t)2 * tn * a.E + e, kr = kl + a.E;
+    atomicAdd((unsigned long long*)&a.Lk[k], (unsigned long long)(int64_t)s_nl[i]);
+    if (s_nl[i]) {
+      atomicAdd((unsigned long long*)&a.tot_q[kl], (unsigned long long)s_ql[i]);
+      atomicAdd((unsigned long long*)&a.tot_c[kl], (unsigned long long)(int64_t)s_nl[i]);
+    }
+    if (s_nr[i]) {
+      atomicAdd((unsigned long long*)&a.tot_q[kr], (unsigned long long)s_qr[i]);
+      atomicAdd((unsigned long long*)&a.tot_c[kr], (unsigned long long)(int64_t)s_nr[i]);
+    }
+  }
+  if (a.mode != 0 && tid == 0) {
+    // the first and last segments of the block and their left rows here
+    const int64_t sl = a.seg[khi];
+    a.blk_fk[blockIdx.x] = klo;
+    a.blk_fl[blockIdx.x] = s_nl[0];
+    a.blk_lk[blockIdx.x] = khi;
+    a.blk_ll[blockIdx.x] = s_nl[(int)((sl > p0 ? sl : p0) - p0)];
   }
 }
 
-// ---------------------------------------------------------------------------
-// partition, pass 2 (one workgroup of 1024): segment sizes of the next level,
-// their offsets, per-tile output bases, next-level presence and the list of
-// segments whose histogram is built at the next level (the smaller child of
-// every split, warpgbm/core.py:636-643; the other child is parent - child).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void partition_scan_kernel(
-    int32_t T, int32_t nodes, int32_t E, const int64_t* __restrict__ seg,
-    const Tile* __restrict__ tiles, const int32_t* __restrict__ key_tile_start,
-    const int32_t* __restrict__ n_tiles_dev, const int32_t* __restrict__ tile_left,
-    const int32_t* __restrict__ split_l, int64_t* __restrict__ Lk,
-    int64_t* __restrict__ tile_lbase, int64_t* __restrict__ tile_rbase,
+// one wave per (tree, node) of the level; four waves per workgroup
+__global__ __launch_bounds__(256) void node_scan_kernel(
+    int32_t T, int32_t nodes, int32_t E, int64_t n_pos, const int64_t* __restrict__ seg,
+    const int32_t* __restrict__ present, const int32_t* __restrict__ split_l,
+    const int64_t* __restrict__ Lk, int64_t* __restrict__ Lk_next,
     int64_t* __restrict__ seg_next, int32_t* __restrict__ present_next,
     int32_t* __restrict__ key_list_next) {
-  __shared__ int64_t wsum[16];
-  __shared__ int64_t sbuf[kScanK * 1024];
-  const int n_keys = T * nodes * E;
-  const int n_tiles = *n_tiles_dev;
-  // phase 1: exclusive scan of the left counts over all tiles (tiles of a
-  // segment are consecutive), kept in tile_lbase for now
-  const int64_t lefts = wgbm_block_scan_tiled(
-      n_tiles, [&](int t) { return (int64_t)tile_left[t]; },
-      [&](int t, int64_t v) { tile_lbase[t] = v; }, wsum, sbuf);
-  __syncthreads();
-  // lefts per segment: difference of the scan at its first tile and the next
-  // segment's first tile
-  for (int k = threadIdx.x; k < n_keys; k += blockDim.x) {
-    const int t0 = key_tile_start[k], t1 = key_tile_start[k + 1];
-    const int64_t a = t0 < n_tiles ? tile_lbase[t0] : lefts;
-    const int64_t b = t1 < n_tiles ? tile_lbase[t1] : lefts;
-    Lk[k] = t1 > t0 ? b - a : 0;
-  }
-  __syncthreads();
-  // phase 2: exclusive scan of next-level segment sizes
-  const int nodes2 = 2 * nodes;
-  const int n_next = T * nodes2 * E;
-  const int64_t total_next = wgbm_block_scan_tiled(
-      n_next,
-      [&](int k2) -> int64_t {
-        const int e = k2 % E;
-        const int tc = k2 / E;
-        const int t = tc / nodes2;
-        const int c = tc - t * nodes2;
-        const int tn = t * nodes + (c >> 1);
-        if (split_l[tn] < 0) return 0;
-        const int k = tn * E + e;
-        const int64_t cnt = seg[k + 1] - seg[k];
-        return (c & 1) ? cnt - Lk[k] : Lk[k];
-      },
-      [&](int k2, int64_t v) { seg_next[k2] = v; }, wsum, sbuf);
-  if (threadIdx.x == 0) seg_next[n_next] = total_next;
-  __syncthreads();
-  // phase 3: per-tile output bases (one thread per tile).  The left prefix
-  // inside the segment is taken first (into tile_rbase) for every tile, since
-  // the bases then overwrite the scan the prefixes are read from.
-  for (int tt = threadIdx.x; tt < n_tiles; tt += blockDim.x)
-    tile_rbase[tt] = tile_lbase[tt] - tile_lbase[key_tile_start[tiles[tt].key]];
-  __syncthreads();
-  for (int tt = threadIdx.x; tt < n_tiles; tt += blockDim.x) {
-    const Tile tl = tiles[tt];
-    const int k = tl.key;
-    const int tn = k / E;
-    if (split_l[tn] < 0) continue;
-    const int e = k - tn * E;
-    const int t = tn / nodes;
-    const int node = tn - t * nodes;
-    const int64_t kl = ((int64_t)t * nodes2 + 2 * node) * E + e;
-    const int64_t kr = kl + E;
-    const int64_t lpre = tile_rbase[tt];
-    const int64_t before = tl.begin - seg[k];
-    tile_lbase[tt] = seg_next[kl] + lpre;
-    tile_rbase[tt] = seg_next[kr] + (before - lpre);
-  }
-  // phase 4: presence and the histogram key list of the next level; one wave
-  // per (tree, node), the eras spread over its lanes
   const int lane = threadIdx.x & 63;
-  for (int tn = threadIdx.x >> 6; tn < T * nodes; tn += blockDim.x >> 6) {
-    const bool sp = split_l[tn] >= 0;
-    const int t = tn / nodes;
-    const int node = tn - t * nodes;
-    if (lane == 0) {
-      present_next[t * nodes2 + 2 * node] = sp;
-      present_next[t * nodes2 + 2 * node + 1] = sp;
-    }
-    int64_t ls = 0, tot = 0;
-    if (sp)
-      for (int e = lane; e < E; e += 64) {
-        const int k = tn * E + e;
-        ls += Lk[k];
-        tot += seg[k + 1] - seg[k];
-      }
-    for (int o = 32; o > 0; o >>= 1) {
-      ls += __shfl_xor(ls, o, 64);
-      tot += __shfl_xor(tot, o, 64);
-    }
-    const int side = (ls <= tot - ls) ? 0 : 1;
-    for (int e = lane; e < E; e += 64)
-      key_list_next[tn * E + e] =
-          sp ? (int32_t)(((int64_t)t * nodes2 + 2 * node + side) * E + e) : -1;
+  const int tn = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tn >= T * nodes) return;  // uniform per wave; no workgroup barriers below
+  const bool sp = present[tn] && split_l[tn] >= 0;
+  const int64_t k0 = (int64_t)tn * E;
+  const int64_t base = seg[k0];
+  const int64_t c0 = 2 * k0;  // next keys of the children: c0 + side * E + e
+  // left rows of the node (all of them when it does not split)
+  int64_t ltot = 0, tot = 0;
+  for (int e = lane; e < E; e += 64) {
+    const int64_t cnt = seg[k0 + e + 1] - seg[k0 + e];
+    ltot += sp ? Lk[k0 + e] : cnt;
+    tot += cnt;
   }
+  for (int o = 32; o > 0; o >>= 1) {
+    ltot += __shfl_xor(ltot, o, 64);
+    tot += __shfl_xor(tot, o, 64);
+  }
+  const int side = (ltot <= tot - ltot) ? 0 : 1;  // the smaller child gets the histogram
+  int64_t carry_l = 0, carry_r = 0;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    int64_t L = 0, R = 0;
+    if (e < E) {
+      const int64_t cnt = seg[k0 + e + 1] - seg[k0 + e];
+      L = sp ? Lk[k0 + e] : cnt;
+      R = cnt - L;
+    }
+    int64_t il = L, ir = R;  // inclusive wave scans
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t yl = __shfl_up(il, o, 64), yr = __shfl_up(ir, o, 64);
+      if (lane >= o) {
+        il += yl;
+        ir += yr;
+      }
+    }
+    if (e < E) {
+      seg_next[c0 + e] = base + carry_l + il - L;
+      seg_next[c0 + E + e] = base + ltot + carry_r + ir - R;
+      Lk_next[c0 + e] = 0;
+      Lk_next[c0 + E + e] = 0;
+      key_list_next[k0 + e] = sp ? (int32_t)(c0 + side * E + e) : -1;
+    }
+    carry_l += __shfl(il, 63, 64);
+    carry_r += __shfl(ir, 63, 64);
+  }
+  if (lane < 2) present_next[2 * tn + lane] = sp;
+  if (tn == T * nodes - 1 && lane == 0) seg_next[(int64_t)2 * T * nodes * E] = n_pos;
 }
 
-// ---------------------------------------------------------------------------
-// partition, pass 3: stable scatter of the rows of split nodes
-__global__ __launch_bounds__(256) void partition_scatter_kernel(
-    const Tile* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-    const int32_t* __restrict__ order, int32_t E, const int32_t* __restrict__ split_l,
-    const uint8_t* __restrict__ dirbit, const int64_t* __restrict__ tile_lbase,
-    const int64_t* __restrict__ tile_rbase, int32_t* __restrict__ order_next) {
-  const int tile = blockIdx.x;
-  if (tile >= *n_tiles) return;
-  const Tile tl = tiles[tile];
-  if (split_l[tl.key / E] < 0) return;
-  __shared__ int32_t wl[4];
-  int64_t lb = tile_lbase[tile], rb = tile_rbase[tile];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int64_t base = tl.begin; base < tl.end; base += blockDim.x) {
-    const int64_t p = base + threadIdx.x;
-    const bool ok = p < tl.end;
-    const bool right = ok && dirbit[p];
-    const bool left = ok && !right;
-    const unsigned long long ml = __ballot(left);
-    const int rank_in_wave = __popcll(ml & __lanemask_lt());
-    if (lane == 0) wl[w] = __popcll(ml);
-    __syncthreads();
-    int pre = 0, tot = 0;
-    for (int k = 0; k < 4; ++k) {
-      if (k < w) pre += wl[k];
-      tot += wl[k];
+// carry[b] = left rows of block b's first segment in the blocks before b: a
+// segmented inclusive scan S of the blocks' last-segment left counts (a run
+// continues through blocks that lie inside one segment), read at b - 1.
+// One workgroup of 1024 threads, tiles of 1024 blocks.
+__global__ __launch_bounds__(1024) void block_carry_kernel(
+    int32_t nb, const int32_t* __restrict__ fk, const int32_t* __restrict__ fl,
+    const int32_t* __restrict__ lk, const int32_t* __restrict__ ll, int32_t* __restrict__ S,
+    int32_t* __restrict__ carry) {
+  (void)fl;
+  __shared__ int64_t sv[1024];
+  __shared__ int sh[1024];
+  __shared__ int64_t s_prev;
+  const int t = threadIdx.x;
+  if (t == 0) s_prev = 0;
+  __syncthreads();
+  for (int b0 = 0; b0 < nb; b0 += 1024) {
+    const int b = b0 + t;
+    int64_t v = 0;
+    int head = 1;
+    if (b < nb) {
+      v = ll[b];
+      // the run of segment lk[b] continues from b - 1 when block b lies inside
+      // that segment and block b - 1 ends in it
+      head = !(fk[b] == lk[b] && b > 0 && lk[b - 1] == lk[b]);
     }
-    const int64_t chunk_n = (tl.end - base) < blockDim.x ? (tl.end - base) : blockDim.x;
-    if (ok) {
-      const int lrank = pre + rank_in_wave;
-      const int64_t idx = p - base;  // position inside the chunk
-      if (left)
-        order_next[lb + lrank] = order[p];
-      else
-        order_next[rb + (idx - lrank)] = order[p];
-    }
-    lb += tot;
-    rb += chunk_n - tot;
+    sv[t] = v;
+    sh[t] = head;
     __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+      int64_t pv = 0;
+      int ph = 0;
+      if (t >= o) {
+        pv = sv[t - o];
+        ph = sh[t - o];
+      }
+      __syncthreads();
+      if (t >= o && !sh[t]) {
+        sv[t] = sv[t] + pv;
+        sh[t] = ph;
+      }
+      __syncthreads();
+    }
+    // elements before the tile's first head continue the previous tile's run
+    int64_t out = sv[t];
+    if (!sh[t]) out += s_prev;
+    if (b < nb) S[b] = (int32_t)out;
+    __syncthreads();
+    if (t == 1023) s_prev = out;
+    __syncthreads();
+  }
+  __syncthreads();
+  for (int b = t; b < nb; b += 1024) carry[b] = (b > 0 && lk[b - 1] == fk[b]) ? S[b - 1] : 0;
+}
+
+__global__ __launch_bounds__(kPartThreads) void scatter_kernel(
+    int64_t n_pos, int32_t E, const int64_t* __restrict__ seg,
+    const int64_t* __restrict__ seg_next, const int32_t* __restrict__ keyp,
+    const uint8_t* __restrict__ dirbit, const int32_t* __restrict__ carry,
+    const int32_t* __restrict__ order, int32_t* __restrict__ order_next) {
+  constexpr int PT = kPartBlock / kPartThreads;  // consecutive positions per thread
+  __shared__ int32_t s_pl[kPartBlock + 1];      // left rows before each block position
+  __shared__ int32_t s_w[kPartThreads / 64];
+  const int tid = threadIdx.x;
+  const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
+  const int64_t pb = p0 + (int64_t)tid * PT;
+  uint8_t d[PT];
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    d[j] = pb + j < n_pos ? dirbit[pb + j] : 2;
+    cnt += d[j] == 0;
+  }
+  // exclusive block scan of the per-thread left counts
+  const int lane = tid & 63, w = tid >> 6;
+  int x = cnt;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) s_w[w] = x;
+  __syncthreads();
+  int pre = 0;
+  for (int k = 0; k < w; ++k) pre += s_w[k];
+  int run = pre + x - cnt;
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    s_pl[tid * PT + j] = run;
+    run += d[j] == 0;
+  }
+  __syncthreads();
+  const int32_t cin = carry[blockIdx.x];
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    const int64_t p = pb + j;
+    if (p >= n_pos) break;
+    const int32_t row = order[p];
+    if (d[j] == 2) {
+      order_next[p] = row;
+      continue;
+    }
+    const int k = keyp[p];
+    const int64_t sk = seg[k];
+    const int64_t s0 = sk > p0 ? sk : p0;
+    const int64_t rl = (int64_t)s_pl[tid * PT + j] - s_pl[s0 - p0] + (sk < p0 ? cin : 0);
+    const int tn = k / E;
+    const int64_t kl = (int64_t)2 * tn * E + (k - (int64_t)tn * E);
+    const int64_t dst = d[j] == 0 ? seg_next[kl] + rl : seg_next[kl + E] + ((p - sk) - rl);
+    order_next[dst] = row;
   }
 }
 
