@@ -54,7 +54,7 @@ __global__ void residual_softmax_kernel(const float* logits, const int32_t* labe
                                         int32_t K, float* r, uint32_t* partial);
 __global__ void root_setup_kernel(const int32_t* root_order, int64_t n, int32_t T,
                                   const int64_t* era_start, int32_t E, int32_t* order,
-                                  int64_t* seg, int32_t* present, int64_t* tot_q,
+                                  int32_t* keyp, int64_t* seg, int32_t* present, int64_t* tot_q,
                                   int64_t* tot_c, unsigned long long* best, int32_t* agree_max);
 __global__ void level_finish_kernel(int32_t depth, int32_t max_depth, int32_t T, int32_t E,
                                     int32_t B, const int32_t* present,
@@ -88,7 +88,7 @@ struct RouteArgs {
   float* pred;
   int64_t pstride, pcol;
   uint8_t* dirbit;
-  int32_t* keyp;
+  const int32_t* keyp;  // segment key of every position
   int64_t* Lk;
   int64_t* tot_q;  // mode 0: of the level's keys; mode 1: of the next level's keys
   int64_t* tot_c;
@@ -106,7 +106,7 @@ __global__ void block_carry_kernel(int32_t nb, const int32_t* fk, const int32_t*
 __global__ void scatter_kernel(int64_t n_pos, int32_t E, const int64_t* seg,
                                const int64_t* seg_next, const int32_t* keyp,
                                const uint8_t* dirbit, const int32_t* carry,
-                               const int32_t* order, int32_t* order_next);
+                               const int32_t* order, int32_t* order_next, int32_t* keyp_next);
 __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v);
 
 // split kernels (split.hip)

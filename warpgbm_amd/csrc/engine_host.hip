@@ -40,7 +40,7 @@ struct Engine {
   int32_t* key_list[2] = {nullptr, nullptr};
   // partition over position blocks of kPartBlock positions
   uint8_t* dirbit = nullptr;            // [T*N] 0 left, 1 right, 2 stays
-  int32_t* keyp = nullptr;              // [T*N] segment key of each position
+  int32_t* keyp[2] = {nullptr, nullptr};  // [T*N] segment key of each position
   int64_t* Lk[2] = {nullptr, nullptr};  // left rows per segment (level parity)
   int32_t *blk_fk = nullptr, *blk_fl = nullptr, *blk_lk = nullptr, *blk_ll = nullptr;
   int32_t *blk_S = nullptr, *blk_carry = nullptr;
@@ -168,7 +168,8 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     E_ALLOC(e->bdir, T * hist_nodes_max * W * F * (B - 1));
   }
   E_ALLOC(e->dirbit, T * N);
-  E_ALLOC(e->keyp, T * N);
+  E_ALLOC(e->keyp[0], T * N);
+  E_ALLOC(e->keyp[1], T * N);
   E_ALLOC(e->Lk[0], e->n_keys_max);
   E_ALLOC(e->Lk[1], e->n_keys_max);
   e->nb = (T * N + kPartBlock - 1) / kPartBlock;
@@ -267,7 +268,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   const int64_t n_pos = (int64_t)T * N;
   hipLaunchKernelGGL(root_setup_kernel, dim3(blocks_for(std::max<int64_t>(n_pos, T * E), 256)),
                      dim3(256), 0, st, c.root_order, N, T, c.era_start, E, e->order[0],
-                     e->seg[0], e->present[0], e->totq[0], e->totc[0], e->best, e->agree_max);
+                     e->keyp[0], e->seg[0], e->present[0], e->totq[0], e->totc[0], e->best,
+                     e->agree_max);
   WGBM_LAUNCH_CHECK();
   hipLaunchKernelGGL(fill_u64_kernel, dim3(blocks_for((int64_t)T * E, 256)), dim3(256), 0, st,
                      (unsigned long long*)e->Lk[0], (int64_t)T * E, 0ull);
@@ -286,7 +288,6 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   ra.pstride = c.objective == 0 ? 1 : T;
   ra.pcol = c.objective == 0 ? 0 : 1;
   ra.dirbit = e->dirbit;
-  ra.keyp = e->keyp;
   ra.blk_fk = e->blk_fk;
   ra.blk_fl = e->blk_fl;
   ra.blk_lk = e->blk_lk;
@@ -297,6 +298,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     r0.seg = e->seg[0];
     r0.n_keys = T * E;
     r0.order = e->order[0];
+    r0.keyp = e->keyp[0];
     r0.nodes = 1;
     r0.present = e->present[0];
     r0.tot_q = e->totq[0];
@@ -451,6 +453,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     rl.seg = e->seg[cur];
     rl.n_keys = n_keys;
     rl.order = e->order[cur];
+    rl.keyp = e->keyp[cur];
     rl.nodes = nodes;
     rl.present = e->present[cur];
     rl.split_l = e->split_l;
@@ -470,8 +473,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                          e->blk_fk, e->blk_fl, e->blk_lk, e->blk_ll, e->blk_S, e->blk_carry);
       WGBM_LAUNCH_CHECK();
       hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, n_pos,
-                         E, e->seg[cur], e->seg[nxt], e->keyp, e->dirbit, e->blk_carry,
-                         e->order[cur], e->order[nxt]);
+                         E, e->seg[cur], e->seg[nxt], e->keyp[cur], e->dirbit, e->blk_carry,
+                         e->order[cur], e->order[nxt], e->keyp[nxt]);
       WGBM_LAUNCH_CHECK();
     }
     cur = nxt;

@@ -73,13 +73,24 @@ __global__ void residual_softmax_kernel(const float* __restrict__ logits,
 // ---------------------------------------------------------------------------
 __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_t n,
                                   int32_t T, const int64_t* __restrict__ era_start, int32_t E,
-                                  int32_t* __restrict__ order, int64_t* __restrict__ seg,
+                                  int32_t* __restrict__ order, int32_t* __restrict__ keyp,
+                                  int64_t* __restrict__ seg,
                                   int32_t* __restrict__ present, int64_t* __restrict__ tot_q,
                                   int64_t* __restrict__ tot_c, unsigned long long* __restrict__ best,
                                   int32_t* __restrict__ agree_max) {
-  // root segments, cleared root totals and cleared depth-0 split-pick words
+  // root order and segment key of every position, root segments, cleared
+  // root totals and cleared depth-0 split-pick words
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid < (int64_t)T * n) order[gid] = root_order[gid % n];
+  if (gid < (int64_t)T * n) {
+    const int64_t t = gid / n, p = gid - t * n;
+    order[gid] = root_order[p];
+    int lo = 0, hi = E - 1;  // the era e with era_start[e] <= p < era_start[e + 1]
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (era_start[mid] <= p) lo = mid; else hi = mid - 1;
+    }
+    keyp[gid] = (int32_t)(t * E + lo);
+  }
   if (gid < (int64_t)T * E) {
     const int t = (int)(gid / E);
     const int e = (int)(gid - (int64_t)t * E);
@@ -207,6 +218,9 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
 // with many small segments (deep DES levels: 2^d nodes x 500 eras) costs the
 // same launches as one with a single segment.
 //
+// Every position also carries its segment key (keyp, written by the root
+// setup and by each level's scatter for the next level).
+//
 // route:   direction of every row of a split node (code <= bin goes left,
 //          warpgbm/core.py:629), leaf update of the rows of a node that stops
 //          here (core.py:602-605), per-(block, segment) left counts and child
@@ -224,15 +238,6 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
 //          segment's start in the block (+ the carry when the segment began in
 //          an earlier block).
 // ---------------------------------------------------------------------------
-__device__ inline int seg_key_of(const int64_t* __restrict__ seg, int lo, int hi, int64_t p) {
-  // the key k in [lo, hi] with seg[k] <= p < seg[k + 1] (segments may be empty)
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (seg[mid] <= p) lo = mid; else hi = mid - 1;
-  }
-  return lo;
-}
-
 __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   // per-segment sums of the block, in the slot of the segment's first
   // position in the block (distinct for distinct non-empty segments; empty
@@ -244,8 +249,8 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
   const int64_t p1 = p0 + kPartBlock < a.n_pos ? p0 + kPartBlock : a.n_pos;
   if (tid == 0) {
-    s_k[0] = seg_key_of(a.seg, 0, a.n_keys - 1, p0);
-    s_k[1] = seg_key_of(a.seg, 0, a.n_keys - 1, p1 - 1);
+    s_k[0] = a.keyp[p0];
+    s_k[1] = a.keyp[p1 - 1];
   }
   for (int i = tid; i < kPartBlock; i += kPartThreads) {
     s_ql[i] = 0;
@@ -256,45 +261,77 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   }
   __syncthreads();
   const int klo = s_k[0], khi = s_k[1];
-  for (int j = 0; j < kPartBlock / kPartThreads; ++j) {
+  // the block's positions, four per thread (strided: coalesced), in phases so
+  // that the loads of the four positions are in flight together
+  constexpr int PJ = kPartBlock / kPartThreads;
+  int key[PJ], slot[PJ], tnv[PJ], lv[PJ];
+  int32_t rowv[PJ];
+  bool ok[PJ];
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
     const int64_t p = p0 + j * kPartThreads + tid;
-    if (p >= p1) break;
-    const int k = seg_key_of(a.seg, klo, khi, p);
-    const int64_t sk = a.seg[k];
-    const int slot = (int)((sk > p0 ? sk : p0) - p0);
-    const int tn = k / a.E;
-    const int t = tn / a.nodes;
-    const int32_t row = a.order[p];
-    if (a.mode == 0) {
-      const int64_t q = wgbm_quantise(a.resid[(int64_t)t * a.n + row], a.shifts[t]);
-      s_key[slot] = k;
-      atomicAdd((unsigned long long*)&s_ql[slot], (unsigned long long)q);
-      atomicAdd(&s_nl[slot], 1);
-      continue;
+    ok[j] = p < p1;
+    key[j] = ok[j] ? a.keyp[p] : klo;
+    rowv[j] = ok[j] ? a.order[p] : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const int64_t sk = a.seg[key[j]];
+    slot[j] = (int)((sk > p0 ? sk : p0) - p0);
+    tnv[j] = key[j] / a.E;
+    // -2: the row stays (node absent), -1: leaf update, >= 0: split feature
+    lv[j] = -2;
+    if (ok[j] && a.present[tnv[j]]) lv[j] = a.mode == 1 ? a.split_l[tnv[j]] : -1;
+  }
+  if (a.mode == 0) {
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      if (!ok[j]) continue;
+      const int t = tnv[j] / a.nodes;
+      const int64_t q = wgbm_quantise(a.resid[(int64_t)t * a.n + rowv[j]], a.shifts[t]);
+      s_key[slot[j]] = key[j];
+      atomicAdd((unsigned long long*)&s_ql[slot[j]], (unsigned long long)q);
+      atomicAdd(&s_nl[slot[j]], 1);
     }
-    a.keyp[p] = k;
-    uint8_t dir = 2;  // stays in place
-    if (a.present[tn]) {
-      const int l = a.mode == 2 ? -1 : a.split_l[tn];
-      if (l < 0) {
-        // the node is a leaf: add lr * leaf to its rows' predictions
-        float* pc = a.pred + (int64_t)t * a.pcol + (int64_t)row * a.pstride;
-        *pc = *pc + a.lr * a.leaf_val[tn];
-      } else {
-        const bool right = (int)a.codes_cm[(int64_t)a.feat_sel[l] * a.n + row] > a.split_b[tn];
-        const int64_t q = wgbm_quantise(a.resid[(int64_t)t * a.n + row], a.shifts[t]);
-        dir = right ? 1 : 0;
-        s_key[slot] = k;
-        if (right) {
-          atomicAdd((unsigned long long*)&s_qr[slot], (unsigned long long)q);
-          atomicAdd(&s_nr[slot], 1);
-        } else {
-          atomicAdd((unsigned long long*)&s_ql[slot], (unsigned long long)q);
-          atomicAdd(&s_nl[slot], 1);
-        }
+  } else {
+    int cv[PJ];
+    float rv[PJ];
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      const int t = tnv[j] / a.nodes;
+      cv[j] = 0;
+      rv[j] = 0.0f;
+      if (lv[j] >= 0) {
+        cv[j] = (int)a.codes_cm[(int64_t)a.feat_sel[lv[j]] * a.n + rowv[j]];
+        rv[j] = a.resid[(int64_t)t * a.n + rowv[j]];
       }
     }
-    a.dirbit[p] = dir;
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      if (!ok[j]) continue;
+      const int64_t p = p0 + j * kPartThreads + tid;
+      const int tn = tnv[j];
+      const int t = tn / a.nodes;
+      uint8_t dir = 2;  // stays in place
+      if (lv[j] == -1) {
+        // the node is a leaf: add lr * leaf to its rows' predictions
+        float* pc = a.pred + (int64_t)t * a.pcol + (int64_t)rowv[j] * a.pstride;
+        *pc = *pc + a.lr * a.leaf_val[tn];
+      } else if (lv[j] >= 0) {
+        const bool right = cv[j] > a.split_b[tn];
+        const int64_t q = wgbm_quantise(rv[j], a.shifts[t]);
+        dir = right ? 1 : 0;
+        s_key[slot[j]] = key[j];
+        if (right) {
+          atomicAdd((unsigned long long*)&s_qr[slot[j]], (unsigned long long)q);
+          atomicAdd(&s_nr[slot[j]], 1);
+        } else {
+          atomicAdd((unsigned long long*)&s_ql[slot[j]], (unsigned long long)q);
+          atomicAdd(&s_nl[slot[j]], 1);
+        }
+      }
+      a.dirbit[p] = dir;
+    }
   }
   __syncthreads();
   for (int i = tid; i < kPartBlock; i += kPartThreads) {
@@ -443,7 +480,8 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
     int64_t n_pos, int32_t E, const int64_t* __restrict__ seg,
     const int64_t* __restrict__ seg_next, const int32_t* __restrict__ keyp,
     const uint8_t* __restrict__ dirbit, const int32_t* __restrict__ carry,
-    const int32_t* __restrict__ order, int32_t* __restrict__ order_next) {
+    const int32_t* __restrict__ order, int32_t* __restrict__ order_next,
+    int32_t* __restrict__ keyp_next) {
   constexpr int PT = kPartBlock / kPartThreads;  // consecutive positions per thread
   __shared__ int32_t s_pl[kPartBlock + 1];      // left rows before each block position
   __shared__ int32_t s_w[kPartThreads / 64];
@@ -481,18 +519,21 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
     const int64_t p = pb + j;
     if (p >= n_pos) break;
     const int32_t row = order[p];
+    const int k = keyp[p];
+    const int tn = k / E;
+    const int64_t kl = (int64_t)2 * tn * E + (k - (int64_t)tn * E);  // left child's key
     if (d[j] == 2) {
+      // a node that does not split: its rows stay, in its left child's segment
       order_next[p] = row;
+      keyp_next[p] = (int32_t)kl;
       continue;
     }
-    const int k = keyp[p];
     const int64_t sk = seg[k];
     const int64_t s0 = sk > p0 ? sk : p0;
     const int64_t rl = (int64_t)s_pl[tid * PT + j] - s_pl[s0 - p0] + (sk < p0 ? cin : 0);
-    const int tn = k / E;
-    const int64_t kl = (int64_t)2 * tn * E + (k - (int64_t)tn * E);
     const int64_t dst = d[j] == 0 ? seg_next[kl] + rl : seg_next[kl + E] + ((p - sk) - rl);
     order_next[dst] = row;
+    keyp_next[dst] = (int32_t)(d[j] == 0 ? kl : kl + E);
   }
 }
 
