@@ -163,21 +163,22 @@ def test_int8_input_over_num_bins_is_quantile_binned(gpu):
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
 
 
-@pytest.mark.parametrize("mcw", [1, 20])
-def test_era_des_colsample_uneven_eras_bit_exact(gpu, mcw):
+@pytest.mark.parametrize("mcw,B", [(1, 12), (20, 12), (1, 7), (20, 3)])
+def test_era_des_colsample_uneven_eras_bit_exact(gpu, mcw, B):
     """Direct era path (every era fits one LDS tile): uneven era sizes, eras
-    that are empty at deeper nodes, a feature subset per tree, a generic bin
-    count; with min_child_weight 20 many (node, era) segments hold fewer than
-    2*20 rows (no candidate can split them) from the root down."""
-    print_case("estimator", "DES E=7 uneven colsample mcw", mcw)
+    that are empty at deeper nodes, a feature subset per tree, generic bin
+    counts (B <= 7: the pair-packed LDS cells); with min_child_weight 20 many
+    (node, era) segments hold fewer than 2*20 rows (no candidate can split
+    them) from the root down."""
+    print_case("estimator", "DES E=7 uneven colsample mcw B", mcw, B)
     rng = np.random.default_rng(5)
     sizes = np.array([900, 40, 1500, 7, 600, 1200, 253])
     E, N, F = len(sizes), int(sizes.sum()), 23
     era = np.repeat(np.arange(E), sizes)
-    X = rng.integers(0, 12, (N, F)).astype(np.int8)
-    score = (X[:, :6] - 5.5).sum(axis=1) * np.where(era % 2 == 0, 1.0, -0.5) + rng.standard_normal(N)
+    X = rng.integers(0, B, (N, F)).astype(np.int8)
+    score = (X[:, :6] - (B - 1) / 2).sum(axis=1) * np.where(era % 2 == 0, 1.0, -0.5) + rng.standard_normal(N)
     y = (score / 10.0).astype(F32)
-    kw = dict(num_bins=12, max_depth=5, n_estimators=5, learning_rate=0.3, min_child_weight=mcw)
+    kw = dict(num_bins=B, max_depth=5, n_estimators=5, learning_rate=0.3, min_child_weight=mcw)
     m = WarpGBM(colsample_bytree=0.6, random_state=11, **kw)
     m.fit(X, y, era_id=era)
     ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era, feat_sets=m.feature_subsets_)

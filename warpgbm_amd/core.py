@@ -318,7 +318,16 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         else:
             sel = torch.arange(F, dtype=torch.int64)
         self.feature_subsets_.append(sel.numpy().astype(np.int32))
-        return sel.to(torch.int32).to(dev)
+        if self.colsample_bytree >= 1.0:
+            # every round uses all features: one device copy for the whole fit
+            cached = getattr(self, "_all_features_dev", None)
+            if cached is None or cached.numel() != F or cached.device != dev:
+                cached = torch.arange(F, dtype=torch.int32, device=dev)
+                self._all_features_dev = cached
+            return cached
+        # a pinned staging copy, so the upload does not wait for the rounds
+        # already queued on the stream
+        return sel.to(torch.int32).pin_memory().to(dev, non_blocking=True)
 
     def _alloc_records(self, n_rounds, n_trees, dev):
         H = (1 << (self.max_depth + 1)) - 1
