@@ -251,7 +251,9 @@ int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64
   WGBM_REQUIRE(X && q && edges, "null pointer");
   hipStream_t st = S(stream);
   // column-major keys of up to `chunk` features at a time (bounded scratch)
-  const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n_feats, (int64_t(1) << 28) / n));
+  // (up to 2^30 keys = 4 GiB of scratch: all features of a 1M-row matrix in
+  // one launch, so that every CU holds several columns)
+  const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n_feats, (int64_t(1) << 30) / n));
   uint32_t* keys = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (size_t)(chunk * n), 8);
   WGBM_REQUIRE(keys, "scratch allocation failed");
   for (int64_t f0 = 0; f0 < n_feats; f0 += chunk) {
