@@ -49,9 +49,9 @@ class _Phases:
             self.items.append((name, now - self.t))
             self.t = now
 
-    def report(self):
+    def report(self, what="fit"):
         if _TIMING:
-            print("fit phases: " + ", ".join(f"{n} {dt * 1e3:.1f} ms" for n, dt in self.items))
+            print(f"{what} phases: " + ", ".join(f"{n} {dt * 1e3:.1f} ms" for n, dt in self.items))
 
 
 class WarpGBM(BaseEstimator, RegressorMixin):
@@ -591,8 +591,12 @@ class WarpGBM(BaseEstimator, RegressorMixin):
     # ------------------------------------------------------------------ binning at predict time
     def bin_data_with_existing_edges(self, X_np):
         dev = torch.device(self.device)
+        ph = _Phases()
         Xd = D.upload_float(X_np, dev)
+        ph.mark("upload")
         codes = D.bin_matrix(Xd, torch.as_tensor(self.bin_edges), with_cm=False)
+        ph.mark("bin")
+        ph.report("binning")
         del Xd
         return codes
 
@@ -669,8 +673,14 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         if self.objective in ("multiclass", "binary"):
             probs = self.predict_proba(X_np)
             return self.label_encoder.inverse_transform(np.argmax(probs, axis=1))
+        ph = _Phases()
         codes = self.bin_inference_data(X_np)
-        preds = self.predict_binned(codes).cpu().numpy()
+        ph.mark("codes")
+        out = self.predict_binned(codes)
+        ph.mark("trees")
+        preds = out.cpu().numpy()
+        ph.mark("copy out")
+        ph.report("predict")
         del codes
         return preds
 
