@@ -53,21 +53,33 @@ __global__ void residual_regression_kernel(const float* y, const float* pred, in
 __global__ void residual_softmax_kernel(const float* logits, const int32_t* label, int64_t n,
                                         int32_t K, float* r, uint32_t* partial);
 __global__ void root_setup_kernel(const int32_t* root_order, int64_t n, int32_t T,
-                                  const int64_t* era_start, int32_t E, int32_t* order,
-                                  int32_t* keyp, int64_t* seg, int32_t* present, int64_t* tot_q,
-                                  int64_t* tot_c, unsigned long long* best, int32_t* agree_max);
+                                  const int64_t* era_start, int32_t E, const float* resid,
+                                  int32_t* order, int32_t* keyp, float* rpos, int64_t* seg,
+                                  int32_t* present, unsigned long long* best, int32_t* agree_max);
 __global__ void level_finish_kernel(int32_t depth, int32_t max_depth, int32_t T, int32_t E,
                                     int32_t B, const int32_t* present,
                                     const unsigned long long* best, int32_t* split_l,
                                     int32_t* split_b, const float* split_gain_era,
                                     const int32_t* feat_sel, const int64_t* tot_q,
                                     const int64_t* tot_c, const int32_t* shifts,
-                                    float* leaf_val, TreeRecord rec, int64_t* tot_q_next,
-                                    int64_t* tot_c_next, unsigned long long* best_next,
-                                    int32_t* agree_max_next);
+                                    float* leaf_val, TreeRecord rec,
+                                    unsigned long long* best_next, int32_t* agree_max_next);
 // partition over position blocks (engine_kernels.hip)
 constexpr int kPartBlock = 1024;   // positions per block
 constexpr int kPartThreads = 256;
+// Per-level left sums of the partition (see route_kernel): words of the
+// segments that lie inside one block, the first- and last-segment partials of
+// every block and their inclusive prefix over the blocks.
+struct PartSums {
+  int64_t* own_q;  // [n_keys]
+  int32_t* own_n;
+  int64_t* bf_q;  // [nb]
+  int32_t* bf_n;
+  int64_t* bl_q;
+  int32_t* bl_n;
+  int64_t* P_q;
+  int64_t* P_n;
+};
 struct RouteArgs {
   int32_t mode;  // 0 root totals, 1 split level, 2 last level (leaves only)
   const int64_t* seg;
@@ -81,7 +93,7 @@ struct RouteArgs {
   const int32_t* feat_sel;
   const int8_t* codes_cm;
   int64_t n;
-  const float* resid;
+  const float* rpos;  // residual of every position's row
   const int32_t* shifts;
   const float* leaf_val;
   float lr;
@@ -89,24 +101,22 @@ struct RouteArgs {
   int64_t pstride, pcol;
   uint8_t* dirbit;
   const int32_t* keyp;  // segment key of every position
-  int64_t* Lk;
-  int64_t* tot_q;  // mode 0: of the level's keys; mode 1: of the next level's keys
-  int64_t* tot_c;
-  int32_t *blk_fk, *blk_fl, *blk_lk, *blk_ll;
+  PartSums ps;
 };
 __global__ void route_kernel(RouteArgs a);
-__global__ void node_scan_kernel(int32_t T, int32_t nodes, int32_t E, int64_t n_pos,
-                                 const int64_t* seg, const int32_t* present,
-                                 const int32_t* split_l, const int64_t* Lk, int64_t* Lk_next,
-                                 int64_t* seg_next, int32_t* present_next,
-                                 int32_t* key_list_next);
-__global__ void block_carry_kernel(int32_t nb, const int32_t* fk, const int32_t* fl,
-                                   const int32_t* lk, const int32_t* ll, int32_t* S,
-                                   int32_t* carry);
+__global__ void block_scan_kernel(int32_t nb, PartSums ps);
+__global__ void root_totals_kernel(int32_t n_keys, const int64_t* seg, PartSums ps,
+                                   int64_t* tot_q, int64_t* tot_c);
+__global__ void node_scan_kernel(int32_t T, int32_t nodes, int32_t E, int32_t wpn,
+                                 int64_t n_pos, const int64_t* seg, const int32_t* present,
+                                 const int32_t* split_l, PartSums ps, const int64_t* tot_q,
+                                 int64_t* seg_next, int64_t* tot_q_next, int64_t* tot_c_next,
+                                 int32_t* present_next, int32_t* key_list_next);
 __global__ void scatter_kernel(int64_t n_pos, int32_t E, const int64_t* seg,
                                const int64_t* seg_next, const int32_t* keyp,
-                               const uint8_t* dirbit, const int32_t* carry,
-                               const int32_t* order, int32_t* order_next, int32_t* keyp_next);
+                               const uint8_t* dirbit, PartSums ps, const int32_t* order,
+                               int32_t* order_next, int32_t* keyp_next, const float* rpos,
+                               float* rpos_next);
 __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v);
 
 // split kernels (split.hip)
@@ -144,8 +154,7 @@ __global__ void des_combine_kernel(const double* bsum, const int32_t* bdir, int3
 __global__ void local_scatter_kernel(const int32_t* feat_sel, int32_t n_sel, int32_t F,
                                      int32_t* local_of);
 int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* codes,
-                   int64_t stride, int32_t F, const float* resid, int64_t resid_tree_stride,
-                   const int32_t* shifts, const int32_t* order, const int64_t* seg, int32_t E,
+                   int64_t stride, int32_t F, const float* rpos, const int32_t* shifts, const int32_t* order, const int64_t* seg, int32_t E,
                    int32_t nodes_in_level,
                    const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
                    float eps, float* gain, int8_t* dir);

@@ -41,9 +41,8 @@ struct Engine {
   // partition over position blocks of kPartBlock positions
   uint8_t* dirbit = nullptr;            // [T*N] 0 left, 1 right, 2 stays
   int32_t* keyp[2] = {nullptr, nullptr};  // [T*N] segment key of each position
-  int64_t* Lk[2] = {nullptr, nullptr};  // left rows per segment (level parity)
-  int32_t *blk_fk = nullptr, *blk_fl = nullptr, *blk_lk = nullptr, *blk_ll = nullptr;
-  int32_t *blk_S = nullptr, *blk_carry = nullptr;
+  float* rpos[2] = {nullptr, nullptr};    // [T*N] residual of each position's row
+  PartSums ps{};  // partition's left sums (own words, block partials, prefix)
   Tile* htiles = nullptr;
   int32_t* hkts = nullptr;
   int32_t* hn = nullptr;
@@ -170,15 +169,17 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->dirbit, T * N);
   E_ALLOC(e->keyp[0], T * N);
   E_ALLOC(e->keyp[1], T * N);
-  E_ALLOC(e->Lk[0], e->n_keys_max);
-  E_ALLOC(e->Lk[1], e->n_keys_max);
+  E_ALLOC(e->rpos[0], T * N);
+  E_ALLOC(e->rpos[1], T * N);
   e->nb = (T * N + kPartBlock - 1) / kPartBlock;
-  E_ALLOC(e->blk_fk, e->nb);
-  E_ALLOC(e->blk_fl, e->nb);
-  E_ALLOC(e->blk_lk, e->nb);
-  E_ALLOC(e->blk_ll, e->nb);
-  E_ALLOC(e->blk_S, e->nb);
-  E_ALLOC(e->blk_carry, e->nb);
+  E_ALLOC(e->ps.own_q, e->n_keys_max);
+  E_ALLOC(e->ps.own_n, e->n_keys_max);
+  E_ALLOC(e->ps.bf_q, e->nb);
+  E_ALLOC(e->ps.bf_n, e->nb);
+  E_ALLOC(e->ps.bl_q, e->nb);
+  E_ALLOC(e->ps.bl_n, e->nb);
+  E_ALLOC(e->ps.P_q, e->nb);
+  E_ALLOC(e->ps.P_n, e->nb);
   E_ALLOC(e->hkts, e->n_keys_max + 1);
   E_ALLOC(e->hn, 1);
   if (E > 1) {
@@ -267,12 +268,9 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   int cur = 0;
   const int64_t n_pos = (int64_t)T * N;
   hipLaunchKernelGGL(root_setup_kernel, dim3(blocks_for(std::max<int64_t>(n_pos, T * E), 256)),
-                     dim3(256), 0, st, c.root_order, N, T, c.era_start, E, e->order[0],
-                     e->keyp[0], e->seg[0], e->present[0], e->totq[0], e->totc[0], e->best,
+                     dim3(256), 0, st, c.root_order, N, T, c.era_start, E, e->resid,
+                     e->order[0], e->keyp[0], e->rpos[0], e->seg[0], e->present[0], e->best,
                      e->agree_max);
-  WGBM_LAUNCH_CHECK();
-  hipLaunchKernelGGL(fill_u64_kernel, dim3(blocks_for((int64_t)T * E, 256)), dim3(256), 0, st,
-                     (unsigned long long*)e->Lk[0], (int64_t)T * E, 0ull);
   WGBM_LAUNCH_CHECK();
   RouteArgs ra{};
   ra.n_pos = n_pos;
@@ -280,7 +278,6 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   ra.feat_sel = feat_sel;
   ra.codes_cm = c.codes_cm;
   ra.n = N;
-  ra.resid = e->resid;
   ra.shifts = e->shifts;
   ra.leaf_val = e->leaf_val;
   ra.lr = c.learning_rate;
@@ -288,10 +285,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   ra.pstride = c.objective == 0 ? 1 : T;
   ra.pcol = c.objective == 0 ? 0 : 1;
   ra.dirbit = e->dirbit;
-  ra.blk_fk = e->blk_fk;
-  ra.blk_fl = e->blk_fl;
-  ra.blk_lk = e->blk_lk;
-  ra.blk_ll = e->blk_ll;
+  ra.ps = e->ps;
   {
     RouteArgs r0 = ra;
     r0.mode = 0;
@@ -299,11 +293,15 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     r0.n_keys = T * E;
     r0.order = e->order[0];
     r0.keyp = e->keyp[0];
+    r0.rpos = e->rpos[0];
     r0.nodes = 1;
     r0.present = e->present[0];
-    r0.tot_q = e->totq[0];
-    r0.tot_c = e->totc[0];
     hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, r0);
+    WGBM_LAUNCH_CHECK();
+    hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
+    WGBM_LAUNCH_CHECK();
+    hipLaunchKernelGGL(root_totals_kernel, dim3(blocks_for((int64_t)T * E, 256)), dim3(256), 0,
+                       st, (int32_t)(T * E), e->seg[0], e->ps, e->totq[0], e->totc[0]);
     WGBM_LAUNCH_CHECK();
   }
 
@@ -329,7 +327,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     if (d < D && e->des_direct) {
       // ---- E > 1, direct: per-era gains of every (node, era) segment
       const int64_t ncand = (int64_t)n_sel * (B - 1);
-      int r = launch_des_era(e->V, B, n_keys, st, c.codes_rm, c.stride, F, e->resid, N,
+      int r = launch_des_era(e->V, B, n_keys, st, c.codes_rm, c.stride, F, e->rpos[cur],
                              e->shifts, e->order[cur], e->seg[cur], E, nodes, e->present[cur],
                              e->local_of, n_sel, mcw, eps, e->sgain, e->sdir);
       if (r) return r;
@@ -387,8 +385,9 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       a.n_rows = N;
       a.stride = c.stride;
       a.n_feats = F;
-      a.resid = e->resid;
-      a.resid_tree_stride = N;
+      a.resid = e->rpos[cur];  // residuals in position order (global positions)
+      a.resid_by_pos = 1;
+      a.resid_tree_stride = 0;
       a.shifts = e->shifts;
       a.order = e->order[cur];
       a.tiles = e->htiles;
@@ -442,7 +441,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     hipLaunchKernelGGL(level_finish_kernel, dim3((unsigned)n_tn), dim3(64), 0, st, d, D, T, E, B,
                        e->present[cur], e1_pick ? (const unsigned long long*)best : nullptr,
                        e->split_l, e->split_b, e->split_gain, feat_sel, e->totq[cur],
-                       e->totc[cur], e->shifts, e->leaf_val, rec, e->totq[nxt], e->totc[nxt],
+                       e->totc[cur], e->shifts, e->leaf_val, rec,
                        e->best + (hcur ^ 1) * e->pick_stride,
                        e->agree_max ? e->agree_max + (hcur ^ 1) * e->pick_stride : nullptr);
     WGBM_LAUNCH_CHECK();
@@ -454,27 +453,26 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     rl.n_keys = n_keys;
     rl.order = e->order[cur];
     rl.keyp = e->keyp[cur];
+    rl.rpos = e->rpos[cur];
     rl.nodes = nodes;
     rl.present = e->present[cur];
     rl.split_l = e->split_l;
     rl.split_b = e->split_b;
-    rl.Lk = e->Lk[d & 1];
-    rl.tot_q = e->totq[nxt];
-    rl.tot_c = e->totc[nxt];
     hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, rl);
     WGBM_LAUNCH_CHECK();
     if (d < D) {
-      hipLaunchKernelGGL(node_scan_kernel, dim3(blocks_for((int64_t)n_tn, 4)), dim3(256), 0, st, T,
-                         nodes, E, n_pos, e->seg[cur], e->present[cur], e->split_l,
-                         e->Lk[d & 1], e->Lk[(d + 1) & 1], e->seg[nxt], e->present[nxt],
+      hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
+      WGBM_LAUNCH_CHECK();
+      const int wpn = E <= 64 ? 1 : (E <= 128 ? 2 : 4);  // waves per node
+      hipLaunchKernelGGL(node_scan_kernel, dim3(blocks_for((int64_t)n_tn, 4 / wpn)), dim3(256), 0,
+                         st, T, nodes, E, wpn, n_pos, e->seg[cur], e->present[cur], e->split_l, e->ps,
+                         e->totq[cur], e->seg[nxt], e->totq[nxt], e->totc[nxt], e->present[nxt],
                          e->key_list[nxt]);
       WGBM_LAUNCH_CHECK();
-      hipLaunchKernelGGL(block_carry_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb,
-                         e->blk_fk, e->blk_fl, e->blk_lk, e->blk_ll, e->blk_S, e->blk_carry);
-      WGBM_LAUNCH_CHECK();
       hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, n_pos,
-                         E, e->seg[cur], e->seg[nxt], e->keyp[cur], e->dirbit, e->blk_carry,
-                         e->order[cur], e->order[nxt], e->keyp[nxt]);
+                         E, e->seg[cur], e->seg[nxt], e->keyp[cur], e->dirbit, e->ps,
+                         e->order[cur], e->order[nxt], e->keyp[nxt], e->rpos[cur],
+                         e->rpos[nxt]);
       WGBM_LAUNCH_CHECK();
     }
     cur = nxt;

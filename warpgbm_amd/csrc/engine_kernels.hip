@@ -73,17 +73,19 @@ __global__ void residual_softmax_kernel(const float* __restrict__ logits,
 // ---------------------------------------------------------------------------
 __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_t n,
                                   int32_t T, const int64_t* __restrict__ era_start, int32_t E,
-                                  int32_t* __restrict__ order, int32_t* __restrict__ keyp,
-                                  int64_t* __restrict__ seg,
-                                  int32_t* __restrict__ present, int64_t* __restrict__ tot_q,
-                                  int64_t* __restrict__ tot_c, unsigned long long* __restrict__ best,
+                                  const float* __restrict__ resid, int32_t* __restrict__ order,
+                                  int32_t* __restrict__ keyp, float* __restrict__ rpos,
+                                  int64_t* __restrict__ seg, int32_t* __restrict__ present,
+                                  unsigned long long* __restrict__ best,
                                   int32_t* __restrict__ agree_max) {
-  // root order and segment key of every position, root segments, cleared
-  // root totals and cleared depth-0 split-pick words
+  // root order, segment key and residual of every position, root segments
+  // and cleared depth-0 split-pick words
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid < (int64_t)T * n) {
     const int64_t t = gid / n, p = gid - t * n;
-    order[gid] = root_order[p];
+    const int32_t row = root_order[p];
+    order[gid] = row;
+    rpos[gid] = resid[t * n + row];
     int lo = 0, hi = E - 1;  // the era e with era_start[e] <= p < era_start[e + 1]
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -95,8 +97,6 @@ __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_
     const int t = (int)(gid / E);
     const int e = (int)(gid - (int64_t)t * E);
     seg[gid] = (int64_t)t * n + era_start[e];
-    tot_q[gid] = 0;
-    tot_c[gid] = 0;
   }
   if (gid == 0) seg[(int64_t)T * E] = (int64_t)T * n;
   if (gid < T) {
@@ -118,26 +118,17 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
     const float* __restrict__ split_gain_era, const int32_t* __restrict__ feat_sel,
     const int64_t* __restrict__ tot_q, const int64_t* __restrict__ tot_c,
     const int32_t* __restrict__ shifts, float* __restrict__ leaf_val, TreeRecord rec,
-    int64_t* __restrict__ tot_q_next, int64_t* __restrict__ tot_c_next,
     unsigned long long* __restrict__ best_next, int32_t* __restrict__ agree_max_next) {
   // one wave per (tree, node); the eras are spread over the lanes.  The wave
-  // also clears the next depth's words of its two children: their per-era
-  // totals (accumulated by the partition) and their split-pick words.  With
+  // also clears the next depth's split-pick words of its two children.  With
   // best != null (one era) the packed pick of the split search is decoded here.
   const int nodes = 1 << depth;
   const int tn = blockIdx.x;
   const int lane = threadIdx.x;
   if (tn >= T * nodes) return;
-  if (depth < max_depth) {
-    const int64_t c0 = (int64_t)2 * tn * E;
-    for (int k = lane; k < 2 * E; k += 64) {
-      tot_q_next[c0 + k] = 0;
-      tot_c_next[c0 + k] = 0;
-    }
-    if (depth + 1 < max_depth && lane < 2) {
-      best_next[2 * tn + lane] = 0ull;
-      if (agree_max_next) agree_max_next[2 * tn + lane] = 0;
-    }
+  if (depth + 1 < max_depth && lane < 2) {
+    best_next[2 * tn + lane] = 0ull;
+    if (agree_max_next) agree_max_next[2 * tn + lane] = 0;
   }
   int l = -1, b = -1;
   float g1 = 0.0f;
@@ -218,49 +209,75 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
 // with many small segments (deep DES levels: 2^d nodes x 500 eras) costs the
 // same launches as one with a single segment.
 //
-// Every position also carries its segment key (keyp, written by the root
-// setup and by each level's scatter for the next level).
+// Every position also carries its segment key (keyp) and its row's residual
+// (rpos), written by the root setup and by each level's scatter for the next
+// level: the kernels of a level read them contiguously instead of gathering
+// by row id.
 //
 // route:   direction of every row of a split node (code <= bin goes left,
-//          warpgbm/core.py:629), leaf update of the rows of a node that stops
-//          here (core.py:602-605), per-(block, segment) left counts and child
-//          totals reduced in LDS and added to the segment's words; the key of
-//          every position (for the scatter) and the block's first / last
-//          segment with its left count (for the carry).  Mode 0 only sums the
-//          quantised residuals and rows of every segment (root totals).
-// node_scan: one wave per (tree, node): the next level's segment offsets, the
-//          presence of the children and the histogram key list (the smaller
-//          child of every split, core.py:636-643).
-// carry:   per block, the left rows of its first segment in earlier blocks
-//          (a segmented scan over the blocks).
+//          warpgbm/core.py:629) and leaf update of the rows of a node that
+//          stops here (core.py:602-605).  The left rows of every segment and
+//          their quantised residual sum are reduced per block in LDS; a
+//          segment that lies inside the block stores them to its key's words
+//          (own_*), and the block stores those of its first and last segments
+//          as block partials (bf_*, bl_*).  Mode 0 counts every row as left
+//          (root totals).  There are no global atomics: every word written
+//          has one writer.
+// block_scan: inclusive prefix P over the blocks of the first-segment
+//          partials.  A segment whose positions span blocks b0 < b1 sums to
+//          bl[b0] + P[b1] - P[b0]: its part in b0 is b0's last segment and it
+//          is the first segment of every block in (b0, b1].
+// node_scan: one to four waves per (tree, node): those sums, the next level's segment
+//          offsets and child totals (left = the sums, right = the parent's
+//          total minus them), the presence of the children and the histogram
+//          key list (the smaller child of every split, core.py:636-643).
 // scatter: stable destination of every row: left rank in its segment = left
-//          rows before it in the block (block prefix) - left rows before the
-//          segment's start in the block (+ the carry when the segment began in
-//          an earlier block).
+//          rows before it in the block (ballot prefix) - left rows before the
+//          segment's start in the block (+ its left rows in earlier blocks,
+//          from the same partial sums, when it began in an earlier block).
 // ---------------------------------------------------------------------------
+__device__ inline void segment_left_sums(int64_t k, const int64_t* __restrict__ seg,
+                                         const PartSums& ps, int64_t& q, int64_t& n) {
+  const int64_t s0 = seg[k], s1 = seg[k + 1];
+  if (s1 <= s0) {
+    q = 0;
+    n = 0;
+    return;
+  }
+  const int64_t b0 = s0 / kPartBlock, b1 = (s1 - 1) / kPartBlock;
+  if (b0 == b1) {
+    q = ps.own_q[k];
+    n = ps.own_n[k];
+  } else {
+    q = ps.bl_q[b0] + ps.P_q[b1] - ps.P_q[b0];
+    n = ps.bl_n[b0] + ps.P_n[b1] - ps.P_n[b0];
+  }
+}
+
 __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
-  // per-segment sums of the block, in the slot of the segment's first
+  // left sums of the block's segments, in the slot of the segment's first
   // position in the block (distinct for distinct non-empty segments; empty
   // segments own no position)
-  __shared__ int64_t s_ql[kPartBlock], s_qr[kPartBlock];
-  __shared__ int32_t s_nl[kPartBlock], s_nr[kPartBlock], s_key[kPartBlock];
+  __shared__ int64_t s_q[kPartBlock];
+  __shared__ int32_t s_n[kPartBlock], s_key[kPartBlock];
   __shared__ int s_k[2];
   const int tid = threadIdx.x;
   const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
   const int64_t p1 = p0 + kPartBlock < a.n_pos ? p0 + kPartBlock : a.n_pos;
+  const bool sums = a.mode != 2;
   if (tid == 0) {
     s_k[0] = a.keyp[p0];
     s_k[1] = a.keyp[p1 - 1];
   }
-  for (int i = tid; i < kPartBlock; i += kPartThreads) {
-    s_ql[i] = 0;
-    s_qr[i] = 0;
-    s_nl[i] = 0;
-    s_nr[i] = 0;
-    s_key[i] = -1;
+  if (sums) {
+    for (int i = tid; i < kPartBlock; i += kPartThreads) {
+      s_q[i] = 0;
+      s_n[i] = 0;
+      s_key[i] = -1;
+    }
   }
   __syncthreads();
-  const int klo = s_k[0], khi = s_k[1];
+  const int khi = s_k[1];
   // the block's positions, four per thread (strided: coalesced), in phases so
   // that the loads of the four positions are in flight together
   constexpr int PJ = kPartBlock / kPartThreads;
@@ -271,7 +288,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   for (int j = 0; j < PJ; ++j) {
     const int64_t p = p0 + j * kPartThreads + tid;
     ok[j] = p < p1;
-    key[j] = ok[j] ? a.keyp[p] : klo;
+    key[j] = ok[j] ? a.keyp[p] : s_k[0];
     rowv[j] = ok[j] ? a.order[p] : 0;
   }
 #pragma unroll
@@ -283,121 +300,212 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     lv[j] = -2;
     if (ok[j] && a.present[tnv[j]]) lv[j] = a.mode == 1 ? a.split_l[tnv[j]] : -1;
   }
+  // Sums go to the LDS slot of the row's segment.  A wave whose rows all lie
+  // in one segment (the common case for large segments) reduces them across
+  // its lanes first and adds once; otherwise every lane adds its own row.
+  auto add_slot = [&](int sl, int k, bool act, int64_t q, int32_t n) {
+    const uint64_t on = __ballot(act);
+    if (on == 0ull) return;
+    const int first = __builtin_ctzll(on);  // wave-uniform
+    const int s0 = __shfl(sl, first, 64);
+    const int k0 = __shfl(k, first, 64);
+    if (__ballot(act && sl != s0) == 0ull) {
+      q = wgbm_wave_sum(act ? q : (int64_t)0);
+      n = wgbm_wave_sum(act ? n : 0);
+      if ((tid & 63) == 0) {
+        s_key[s0] = k0;
+        if (n) {
+          atomicAdd((unsigned long long*)&s_q[s0], (unsigned long long)q);
+          atomicAdd(&s_n[s0], n);
+        }
+      }
+    } else if (act) {
+      s_key[sl] = k;
+      if (n) {
+        atomicAdd((unsigned long long*)&s_q[sl], (unsigned long long)q);
+        atomicAdd(&s_n[sl], n);
+      }
+    }
+  };
+  float rv[PJ];
+#pragma unroll
+  for (int j = 0; j < PJ; ++j)
+    rv[j] = ok[j] && sums ? a.rpos[p0 + j * kPartThreads + tid] : 0.0f;
   if (a.mode == 0) {
 #pragma unroll
     for (int j = 0; j < PJ; ++j) {
-      if (!ok[j]) continue;
       const int t = tnv[j] / a.nodes;
-      const int64_t q = wgbm_quantise(a.resid[(int64_t)t * a.n + rowv[j]], a.shifts[t]);
-      s_key[slot[j]] = key[j];
-      atomicAdd((unsigned long long*)&s_ql[slot[j]], (unsigned long long)q);
-      atomicAdd(&s_nl[slot[j]], 1);
+      const int64_t q = ok[j] ? wgbm_quantise(rv[j], a.shifts[t]) : 0;
+      add_slot(slot[j], key[j], ok[j], q, 1);
     }
   } else {
     int cv[PJ];
-    float rv[PJ];
+#pragma unroll
+    for (int j = 0; j < PJ; ++j)
+      cv[j] = lv[j] >= 0 ? (int)a.codes_cm[(int64_t)a.feat_sel[lv[j]] * a.n + rowv[j]] : 0;
 #pragma unroll
     for (int j = 0; j < PJ; ++j) {
-      const int t = tnv[j] / a.nodes;
-      cv[j] = 0;
-      rv[j] = 0.0f;
-      if (lv[j] >= 0) {
-        cv[j] = (int)a.codes_cm[(int64_t)a.feat_sel[lv[j]] * a.n + rowv[j]];
-        rv[j] = a.resid[(int64_t)t * a.n + rowv[j]];
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < PJ; ++j) {
-      if (!ok[j]) continue;
-      const int64_t p = p0 + j * kPartThreads + tid;
       const int tn = tnv[j];
       const int t = tn / a.nodes;
       uint8_t dir = 2;  // stays in place
+      int64_t q = 0;
       if (lv[j] == -1) {
         // the node is a leaf: add lr * leaf to its rows' predictions
         float* pc = a.pred + (int64_t)t * a.pcol + (int64_t)rowv[j] * a.pstride;
         *pc = *pc + a.lr * a.leaf_val[tn];
       } else if (lv[j] >= 0) {
-        const bool right = cv[j] > a.split_b[tn];
-        const int64_t q = wgbm_quantise(rv[j], a.shifts[t]);
-        dir = right ? 1 : 0;
-        s_key[slot[j]] = key[j];
-        if (right) {
-          atomicAdd((unsigned long long*)&s_qr[slot[j]], (unsigned long long)q);
-          atomicAdd(&s_nr[slot[j]], 1);
-        } else {
-          atomicAdd((unsigned long long*)&s_ql[slot[j]], (unsigned long long)q);
-          atomicAdd(&s_nl[slot[j]], 1);
-        }
+        dir = cv[j] > a.split_b[tn] ? 1 : 0;
+        q = wgbm_quantise(rv[j], a.shifts[t]);
       }
-      a.dirbit[p] = dir;
+      if (sums) add_slot(slot[j], key[j], dir != 2, dir == 0 ? q : 0, dir == 0 ? 1 : 0);
+      if (ok[j] && sums) a.dirbit[p0 + j * kPartThreads + tid] = dir;
     }
   }
+  if (!sums) return;  // uniform over the block
   __syncthreads();
   for (int i = tid; i < kPartBlock; i += kPartThreads) {
     const int k = s_key[i];
     if (k < 0) continue;  // no summed rows start here
-    if (a.mode == 0) {
-      atomicAdd((unsigned long long*)&a.tot_q[k], (unsigned long long)s_ql[i]);
-      atomicAdd((unsigned long long*)&a.tot_c[k], (unsigned long long)(int64_t)s_nl[i]);
-      continue;
-    }
-    const int tn = k / a.E;
-    const int e = k - tn * a.E;
-    const int64_t kl = (int64_t)2 * tn * a.E + e, kr = kl + a.E;
-    atomicAdd((unsigned long long*)&a.Lk[k], (unsigned long long)(int64_t)s_nl[i]);
-    if (s_nl[i]) {
-      atomicAdd((unsigned long long*)&a.tot_q[kl], (unsigned long long)s_ql[i]);
-      atomicAdd((unsigned long long*)&a.tot_c[kl], (unsigned long long)(int64_t)s_nl[i]);
-    }
-    if (s_nr[i]) {
-      atomicAdd((unsigned long long*)&a.tot_q[kr], (unsigned long long)s_qr[i]);
-      atomicAdd((unsigned long long*)&a.tot_c[kr], (unsigned long long)(int64_t)s_nr[i]);
+    if (a.seg[k] >= p0 && a.seg[k + 1] <= p1) {
+      a.ps.own_q[k] = s_q[i];
+      a.ps.own_n[k] = s_n[i];
     }
   }
-  if (a.mode != 0 && tid == 0) {
-    // the first and last segments of the block and their left rows here
+  if (tid == 0) {
+    // the first and last segments of the block: their sums here
     const int64_t sl = a.seg[khi];
-    a.blk_fk[blockIdx.x] = klo;
-    a.blk_fl[blockIdx.x] = s_nl[0];
-    a.blk_lk[blockIdx.x] = khi;
-    a.blk_ll[blockIdx.x] = s_nl[(int)((sl > p0 ? sl : p0) - p0)];
+    const int ls = (int)((sl > p0 ? sl : p0) - p0);
+    a.ps.bf_q[blockIdx.x] = s_q[0];
+    a.ps.bf_n[blockIdx.x] = s_n[0];
+    a.ps.bl_q[blockIdx.x] = s_q[ls];
+    a.ps.bl_n[blockIdx.x] = s_n[ls];
   }
 }
 
-// one wave per (tree, node) of the level; four waves per workgroup
+// inclusive prefix over the blocks of the first-segment partials; one
+// workgroup of 1024 threads, tiles of 1024 blocks
+__global__ __launch_bounds__(1024) void block_scan_kernel(int32_t nb, PartSums ps) {
+  __shared__ int64_t s_wq[16], s_wn[16];
+  __shared__ int64_t s_cq, s_cn;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  if (t == 0) {
+    s_cq = 0;
+    s_cn = 0;
+  }
+  __syncthreads();
+  for (int b0 = 0; b0 < nb; b0 += 1024) {
+    const int b = b0 + t;
+    int64_t q = b < nb ? ps.bf_q[b] : 0, n = b < nb ? ps.bf_n[b] : 0;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t yq = __shfl_up(q, o, 64), yn = __shfl_up(n, o, 64);
+      if (lane >= o) {
+        q += yq;
+        n += yn;
+      }
+    }
+    if (lane == 63) {
+      s_wq[w] = q;
+      s_wn[w] = n;
+    }
+    __syncthreads();
+    int64_t cq = s_cq, cn = s_cn;
+    for (int k = 0; k < w; ++k) {
+      cq += s_wq[k];
+      cn += s_wn[k];
+    }
+    q += cq;
+    n += cn;
+    if (b < nb) {
+      ps.P_q[b] = q;
+      ps.P_n[b] = n;
+    }
+    __syncthreads();  // every thread has read the carry and the wave sums
+    if (t == 1023) {
+      s_cq = q;
+      s_cn = n;
+    }
+    __syncthreads();
+  }
+}
+
+// root totals of every (tree, era) key: quantised residual sum and rows
+__global__ void root_totals_kernel(int32_t n_keys, const int64_t* __restrict__ seg, PartSums ps,
+                                   int64_t* __restrict__ tot_q, int64_t* __restrict__ tot_c) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n_keys) return;
+  int64_t q, n;
+  segment_left_sums(k, seg, ps, q, n);
+  tot_q[k] = q;
+  tot_c[k] = n;
+}
+
+// wpn waves per (tree, node) of the level (1, 2 or 4: the eras are spread
+// over the group's lanes); 4 / wpn nodes per workgroup
 __global__ __launch_bounds__(256) void node_scan_kernel(
-    int32_t T, int32_t nodes, int32_t E, int64_t n_pos, const int64_t* __restrict__ seg,
-    const int32_t* __restrict__ present, const int32_t* __restrict__ split_l,
-    const int64_t* __restrict__ Lk, int64_t* __restrict__ Lk_next,
-    int64_t* __restrict__ seg_next, int32_t* __restrict__ present_next,
+    int32_t T, int32_t nodes, int32_t E, int32_t wpn, int64_t n_pos,
+    const int64_t* __restrict__ seg, const int32_t* __restrict__ present,
+    const int32_t* __restrict__ split_l, PartSums ps, const int64_t* __restrict__ tot_q,
+    int64_t* __restrict__ seg_next, int64_t* __restrict__ tot_q_next,
+    int64_t* __restrict__ tot_c_next, int32_t* __restrict__ present_next,
     int32_t* __restrict__ key_list_next) {
-  const int lane = threadIdx.x & 63;
-  const int tn = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tn >= T * nodes) return;  // uniform per wave; no workgroup barriers below
-  const bool sp = present[tn] && split_l[tn] >= 0;
+  __shared__ int64_t s_a[4], s_b[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = wave / wpn, wg = wave - grp * wpn;
+  const int tn = blockIdx.x * (4 / wpn) + grp;
+  const int gthreads = wpn * 64, gt = wg * 64 + lane;
+  // a group past the last node still takes part in the workgroup barriers
+  const bool live = tn < T * nodes;
+  const bool sp = live && present[tn] && split_l[tn] >= 0;
   const int64_t k0 = (int64_t)tn * E;
-  const int64_t base = seg[k0];
+  const int64_t base = live ? seg[k0] : 0;
   const int64_t c0 = 2 * k0;  // next keys of the children: c0 + side * E + e
-  // left rows of the node (all of them when it does not split)
+  // left rows of a segment of the node (all of them when it does not split)
+  auto left_of = [&](int64_t k, int64_t cnt, int64_t& q) -> int64_t {
+    int64_t L = cnt;
+    q = 0;
+    if (sp) segment_left_sums(k, seg, ps, q, L);
+    return L;
+  };
+  // sum over the group of one value per wave (every thread gets it)
+  auto group_sum = [&](int64_t a, int64_t b, int64_t& ga, int64_t& gb) {
+    if (lane == 63) {
+      s_a[wave] = a;
+      s_b[wave] = b;
+    }
+    __syncthreads();
+    ga = 0;
+    gb = 0;
+    for (int w = grp * wpn; w < (grp + 1) * wpn; ++w) {
+      ga += s_a[w];
+      gb += s_b[w];
+    }
+    __syncthreads();
+  };
   int64_t ltot = 0, tot = 0;
-  for (int e = lane; e < E; e += 64) {
-    const int64_t cnt = seg[k0 + e + 1] - seg[k0 + e];
-    ltot += sp ? Lk[k0 + e] : cnt;
-    tot += cnt;
+  if (live) {
+    for (int e = gt; e < E; e += gthreads) {
+      const int64_t cnt = seg[k0 + e + 1] - seg[k0 + e];
+      int64_t q;
+      ltot += left_of(k0 + e, cnt, q);
+      tot += cnt;
+    }
   }
-  for (int o = 32; o > 0; o >>= 1) {
-    ltot += __shfl_xor(ltot, o, 64);
-    tot += __shfl_xor(tot, o, 64);
+  for (int o = 1; o < 64; o <<= 1) {  // inclusive wave scans: lane 63 holds the sums
+    const int64_t yl = __shfl_up(ltot, o, 64), yt = __shfl_up(tot, o, 64);
+    if (lane >= o) {
+      ltot += yl;
+      tot += yt;
+    }
   }
+  group_sum(ltot, tot, ltot, tot);
   const int side = (ltot <= tot - ltot) ? 0 : 1;  // the smaller child gets the histogram
   int64_t carry_l = 0, carry_r = 0;
-  for (int e0 = 0; e0 < E; e0 += 64) {
-    const int e = e0 + lane;
-    int64_t L = 0, R = 0;
-    if (e < E) {
+  for (int e0 = 0; e0 < E; e0 += gthreads) {
+    const int e = e0 + gt;
+    int64_t L = 0, R = 0, q = 0;
+    if (live && e < E) {
       const int64_t cnt = seg[k0 + e + 1] - seg[k0 + e];
-      L = sp ? Lk[k0 + e] : cnt;
+      L = left_of(k0 + e, cnt, q);
       R = cnt - L;
     }
     int64_t il = L, ir = R;  // inclusive wave scans
@@ -408,132 +516,112 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
         ir += yr;
       }
     }
-    if (e < E) {
+    // earlier waves of the group, and the chunk totals for the carry
+    if (lane == 63) {
+      s_a[wave] = il;
+      s_b[wave] = ir;
+    }
+    __syncthreads();
+    int64_t pl = 0, pr = 0, cl = 0, cr = 0;
+    for (int w = grp * wpn; w < (grp + 1) * wpn; ++w) {
+      if (w < wave) {
+        pl += s_a[w];
+        pr += s_b[w];
+      }
+      cl += s_a[w];
+      cr += s_b[w];
+    }
+    __syncthreads();
+    il += pl;
+    ir += pr;
+    if (live && e < E) {
       seg_next[c0 + e] = base + carry_l + il - L;
       seg_next[c0 + E + e] = base + ltot + carry_r + ir - R;
-      Lk_next[c0 + e] = 0;
-      Lk_next[c0 + E + e] = 0;
+      // child totals (the words of children that do not exist are zero)
+      tot_q_next[c0 + e] = sp ? q : 0;
+      tot_c_next[c0 + e] = sp ? L : 0;
+      tot_q_next[c0 + E + e] = sp ? tot_q[k0 + e] - q : 0;
+      tot_c_next[c0 + E + e] = sp ? R : 0;
       key_list_next[k0 + e] = sp ? (int32_t)(c0 + side * E + e) : -1;
     }
-    carry_l += __shfl(il, 63, 64);
-    carry_r += __shfl(ir, 63, 64);
+    carry_l += cl;
+    carry_r += cr;
   }
-  if (lane < 2) present_next[2 * tn + lane] = sp;
-  if (tn == T * nodes - 1 && lane == 0) seg_next[(int64_t)2 * T * nodes * E] = n_pos;
-}
-
-// carry[b] = left rows of block b's first segment in the blocks before b: a
-// segmented inclusive scan S of the blocks' last-segment left counts (a run
-// continues through blocks that lie inside one segment), read at b - 1.
-// One workgroup of 1024 threads, tiles of 1024 blocks.
-__global__ __launch_bounds__(1024) void block_carry_kernel(
-    int32_t nb, const int32_t* __restrict__ fk, const int32_t* __restrict__ fl,
-    const int32_t* __restrict__ lk, const int32_t* __restrict__ ll, int32_t* __restrict__ S,
-    int32_t* __restrict__ carry) {
-  (void)fl;
-  __shared__ int64_t sv[1024];
-  __shared__ int sh[1024];
-  __shared__ int64_t s_prev;
-  const int t = threadIdx.x;
-  if (t == 0) s_prev = 0;
-  __syncthreads();
-  for (int b0 = 0; b0 < nb; b0 += 1024) {
-    const int b = b0 + t;
-    int64_t v = 0;
-    int head = 1;
-    if (b < nb) {
-      v = ll[b];
-      // the run of segment lk[b] continues from b - 1 when block b lies inside
-      // that segment and block b - 1 ends in it
-      head = !(fk[b] == lk[b] && b > 0 && lk[b - 1] == lk[b]);
-    }
-    sv[t] = v;
-    sh[t] = head;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-      int64_t pv = 0;
-      int ph = 0;
-      if (t >= o) {
-        pv = sv[t - o];
-        ph = sh[t - o];
-      }
-      __syncthreads();
-      if (t >= o && !sh[t]) {
-        sv[t] = sv[t] + pv;
-        sh[t] = ph;
-      }
-      __syncthreads();
-    }
-    // elements before the tile's first head continue the previous tile's run
-    int64_t out = sv[t];
-    if (!sh[t]) out += s_prev;
-    if (b < nb) S[b] = (int32_t)out;
-    __syncthreads();
-    if (t == 1023) s_prev = out;
-    __syncthreads();
-  }
-  __syncthreads();
-  for (int b = t; b < nb; b += 1024) carry[b] = (b > 0 && lk[b - 1] == fk[b]) ? S[b - 1] : 0;
+  if (live && gt < 2) present_next[2 * tn + gt] = sp;
+  if (tn == T * nodes - 1 && gt == 0) seg_next[(int64_t)2 * T * nodes * E] = n_pos;
 }
 
 __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
     int64_t n_pos, int32_t E, const int64_t* __restrict__ seg,
     const int64_t* __restrict__ seg_next, const int32_t* __restrict__ keyp,
-    const uint8_t* __restrict__ dirbit, const int32_t* __restrict__ carry,
-    const int32_t* __restrict__ order, int32_t* __restrict__ order_next,
-    int32_t* __restrict__ keyp_next) {
-  constexpr int PT = kPartBlock / kPartThreads;  // consecutive positions per thread
-  __shared__ int32_t s_pl[kPartBlock + 1];      // left rows before each block position
-  __shared__ int32_t s_w[kPartThreads / 64];
-  const int tid = threadIdx.x;
+    const uint8_t* __restrict__ dirbit, PartSums ps, const int32_t* __restrict__ order,
+    int32_t* __restrict__ order_next, int32_t* __restrict__ keyp_next,
+    const float* __restrict__ rpos, float* __restrict__ rpos_next) {
+  constexpr int PJ = kPartBlock / kPartThreads;  // positions per thread (strided)
+  constexpr int NW = kPartThreads / 64;
+  __shared__ int32_t s_pl[kPartBlock];  // left rows before each block position
+  __shared__ int32_t s_c[PJ * NW];      // left rows of each (phase, wave) group
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
-  const int64_t pb = p0 + (int64_t)tid * PT;
-  uint8_t d[PT];
-  int cnt = 0;
+  uint8_t d[PJ];
+  int32_t rowv[PJ], key[PJ], rank[PJ];
+  float rr[PJ];
 #pragma unroll
-  for (int j = 0; j < PT; ++j) {
-    d[j] = pb + j < n_pos ? dirbit[pb + j] : 2;
-    cnt += d[j] == 0;
+  for (int j = 0; j < PJ; ++j) {
+    const int64_t p = p0 + j * kPartThreads + tid;
+    const bool ok = p < n_pos;
+    d[j] = ok ? dirbit[p] : 2;
+    rowv[j] = ok ? order[p] : 0;
+    key[j] = ok ? keyp[p] : 0;
+    rr[j] = ok ? rpos[p] : 0.0f;
   }
-  // exclusive block scan of the per-thread left counts
-  const int lane = tid & 63, w = tid >> 6;
-  int x = cnt;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  if (lane == 63) s_w[w] = x;
-  __syncthreads();
-  int pre = 0;
-  for (int k = 0; k < w; ++k) pre += s_w[k];
-  int run = pre + x - cnt;
+  // left rows before each position: rank among the wave's lefts plus the
+  // lefts of the (phase, wave) groups before it (position order is phase,
+  // then wave, then lane)
 #pragma unroll
-  for (int j = 0; j < PT; ++j) {
-    s_pl[tid * PT + j] = run;
-    run += d[j] == 0;
+  for (int j = 0; j < PJ; ++j) {
+    const uint64_t m = __ballot(d[j] == 0);
+    rank[j] = (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    if (lane == 0) s_c[j * NW + w] = __builtin_popcountll(m);
   }
   __syncthreads();
-  const int32_t cin = carry[blockIdx.x];
 #pragma unroll
-  for (int j = 0; j < PT; ++j) {
-    const int64_t p = pb + j;
+  for (int j = 0; j < PJ; ++j) {
+    int pre = 0;
+    for (int i = 0; i < j * NW + w; ++i) pre += s_c[i];
+    rank[j] += pre;
+    s_pl[j * kPartThreads + tid] = rank[j];
+  }
+  __syncthreads();
+  // left rows of the block's first segment in earlier blocks
+  const int64_t sf = seg[keyp[p0]];
+  int64_t cin = 0;
+  if (sf < p0) {
+    const int64_t b0 = sf / kPartBlock;
+    cin = ps.bl_n[b0] + ps.P_n[blockIdx.x - 1] - ps.P_n[b0];
+  }
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const int64_t p = p0 + j * kPartThreads + tid;
     if (p >= n_pos) break;
-    const int32_t row = order[p];
-    const int k = keyp[p];
+    const int k = key[j];
     const int tn = k / E;
     const int64_t kl = (int64_t)2 * tn * E + (k - (int64_t)tn * E);  // left child's key
     if (d[j] == 2) {
       // a node that does not split: its rows stay, in its left child's segment
-      order_next[p] = row;
+      order_next[p] = rowv[j];
       keyp_next[p] = (int32_t)kl;
+      rpos_next[p] = rr[j];
       continue;
     }
     const int64_t sk = seg[k];
     const int64_t s0 = sk > p0 ? sk : p0;
-    const int64_t rl = (int64_t)s_pl[tid * PT + j] - s_pl[s0 - p0] + (sk < p0 ? cin : 0);
+    const int64_t rl = (int64_t)rank[j] - s_pl[s0 - p0] + (sk < p0 ? cin : 0);
     const int64_t dst = d[j] == 0 ? seg_next[kl] + rl : seg_next[kl + E] + ((p - sk) - rl);
-    order_next[dst] = row;
+    order_next[dst] = rowv[j];
     keyp_next[dst] = (int32_t)(d[j] == 0 ? kl : kl + E);
+    rpos_next[dst] = rr[j];
   }
 }
 

@@ -379,8 +379,8 @@ template <int V, int BT>
 __global__ __launch_bounds__(kDesEraThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void des_era_kernel(
     const int8_t* __restrict__ codes, int64_t stride, int32_t F,
-    const float* __restrict__ resid, int64_t resid_tree_stride,
-    const int32_t* __restrict__ shifts, const int32_t* __restrict__ order,
+    const float* __restrict__ rpos, const int32_t* __restrict__ shifts,
+    const int32_t* __restrict__ order,
     const int64_t* __restrict__ seg, int32_t E, int32_t n_keys, int32_t nodes_in_level,
     const int32_t* __restrict__ present, const int32_t* __restrict__ local_of, int32_t n_sel,
     int32_t num_bins_rt, float mcw, float eps, float* __restrict__ gain,
@@ -426,14 +426,13 @@ void des_era_kernel(
       const int n = (int)(seg[key + 1] - begin);  // <= 65536 (checked by the engine)
       const int tree = tn / nodes_in_level;
       const int s = shifts[tree];
-      const float* __restrict__ r_t = resid + (int64_t)tree * resid_tree_stride;
       for (int i = threadIdx.x; i < V * Bp * kHistSlots; i += kDesEraThreads) lds[i] = 0ull;
       __syncthreads();
       // software pipeline as in the tile histogram: wave w takes the row
       // groups [i, i + U), i = (w + k*nwaves)*U; two register sets alternate
       // so that the loads of the next group are in flight while this one is
-      // added; row ids and residuals are vector loads (lane u < U: row u of
-      // the group) broadcast with readlane; positions past the end read the
+      // added; row ids and residuals (stored by position) are vector loads
+      // (lane u < U: row u of the group) broadcast with readlane; positions past the end read the
       // segment's last row and add the word 0
       constexpr int U = 8;
       constexpr int step = nwaves * U;
@@ -449,7 +448,7 @@ void des_era_kernel(
         int rows[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) rows[u] = __builtin_amdgcn_readlane(ids, u);
-        g.r = r_t[ids];
+        g.r = rpos[begin + (i0 + ul < n ? i0 + ul : n - 1)];
         load_ids(i0 + step);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -633,8 +632,7 @@ __global__ void local_scatter_kernel(const int32_t* __restrict__ feat_sel, int32
 }
 
 int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* codes,
-                   int64_t stride, int32_t F, const float* resid, int64_t resid_tree_stride,
-                   const int32_t* shifts, const int32_t* order, const int64_t* seg, int32_t E,
+                   int64_t stride, int32_t F, const float* rpos, const int32_t* shifts, const int32_t* order, const int64_t* seg, int32_t E,
                    int32_t nodes_in_level,
                    const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
                    float eps, float* gain, int8_t* dir) {
@@ -652,7 +650,7 @@ int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* c
       attr = true;                                                                             \
     }                                                                                          \
     hipLaunchKernelGGL((des_era_kernel<VV, BB>), grid, dim3(kDesEraThreads), lds, st, codes,   \
-                       stride, F, resid, resid_tree_stride, shifts, order, seg, E, n_keys,     \
+                       stride, F, rpos, shifts, order, seg, E, n_keys,                        \
                        nodes_in_level, present, local_of, n_sel, B, mcw, eps, gain, dir);      \
     WGBM_LAUNCH_CHECK();                                                                       \
     return 0;                                                                                  \
