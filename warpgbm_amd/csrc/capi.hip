@@ -36,14 +36,17 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   const int V = hist_pick_v(num_bins);
   const int n_chunks = (n_hist_feats + kHistSlots * V - 1) / (kHistSlots * V);
   // scratch layout (slot 0: control words and the per-block maxima)
-  constexpr int kAbsBlocks = 512;
+  constexpr int kAbsBlocks = 256;
   uint32_t* ctl = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (64 + kAbsBlocks), 0);
   WGBM_REQUIRE(ctl, "scratch allocation failed");
   uint32_t* absmax = ctl;
   int32_t* shift = (int32_t*)(ctl + 16);
   int32_t* n_tiles = (int32_t*)(ctl + 32);
   uint32_t* abs_part = ctl + 64;
-  const int n_abs = (int)std::max<int64_t>(1, std::min<int64_t>(nblocks(n_pos, 256), kAbsBlocks));
+  // per-block maxima of |residual|: blocks of 1024 threads, at most 256 of
+  // them (every wave of the tile kernel reduces them to the shift)
+  const int n_abs =
+      (int)std::max<int64_t>(1, std::min<int64_t>(nblocks(n_pos, 1024), kAbsBlocks));
   // a row list without an era regrouping: the residuals are gathered into
   // position order in the same pass, so the tile kernel reads them
   // contiguously instead of one 4-byte gather per row
@@ -53,16 +56,31 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
     rpos = (float*)scratch_get(st, sizeof(float) * std::max<int64_t>(n_pos, 1), 6);
     WGBM_REQUIRE(rpos, "scratch allocation failed");
   }
-  hipLaunchKernelGGL(absmax_partial_kernel, dim3(n_abs), dim3(256), 0, st, resid, rows, n_pos,
-                     abs_part, rpos);
-  WGBM_LAUNCH_CHECK();
-  // (the per-block maxima are reduced to the shift by the tile planner below)
-
   // segments: explicit (seg_dev), by era (sort rows by era), or a single one
+  const int n_keys = seg_dev ? n_seg : (regroup ? num_eras : 1);
+
+  // tiles: ~2 workgroups per CU over the whole call
+  int64_t tiles_target = std::max<int64_t>(1, kHistTargetWG / n_chunks);
+  int64_t R = (n_pos + tiles_target - 1) / tiles_target;
+  R = std::min<int64_t>(std::max<int64_t>((R + 255) / 256 * 256, 1024), WGBM_MAX_TILE_ROWS);
+  const int64_t max_tiles = n_pos / R + n_keys + 1;
+  Tile* tiles = (Tile*)scratch_get(st, sizeof(Tile) * max_tiles, 3);
+  int32_t* kts = (int32_t*)scratch_get(st, sizeof(int32_t) * ((size_t)n_keys + 1), 4);
+  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
+  const int64_t words = max_tiles * tile_words;
+  unsigned long long* part =
+      (unsigned long long*)scratch_get(st, sizeof(unsigned long long) * words, 5);
+  WGBM_REQUIRE(tiles && kts && part, "scratch allocation failed (%lld words)", (long long)words);
+
+  // maxima (+ gathered residuals) and, unless the rows are regrouped by era
+  // first, the tile plan: one launch
+  hipLaunchKernelGGL(hist_prep_kernel, dim3(n_abs + (regroup ? 0 : 1)), dim3(1024), 0, st, resid,
+                     rows, n_pos, abs_part, rpos, n_abs, regroup ? 0 : 1, seg_dev, n_keys,
+                     (int32_t)R, (int32_t)max_tiles, tiles, kts, n_tiles);
+  WGBM_LAUNCH_CHECK();
   const int32_t* order = rows;
   const int64_t* seg = seg_dev;
-  int n_keys = n_seg;
-  if (!seg_dev && num_eras > 1) {
+  if (regroup) {
     int64_t* counts = (int64_t*)scratch_get(st, sizeof(int64_t) * (3 * (size_t)num_eras + 2), 1);
     int32_t* sorted = (int32_t*)scratch_get(st, sizeof(int32_t) * std::max<int64_t>(n_pos, 1), 2);
     WGBM_REQUIRE(counts && sorted, "scratch allocation failed");
@@ -83,28 +101,11 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
     WGBM_LAUNCH_CHECK();
     order = sorted;
     seg = starts;
-    n_keys = num_eras;
-  } else if (!seg_dev) {
-    n_keys = 1;
+    hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, seg, n_pos, n_keys,
+                       (const int32_t*)nullptr, (int32_t)R, (int32_t)max_tiles, tiles, kts,
+                       n_tiles);
+    WGBM_LAUNCH_CHECK();
   }
-
-  // tiles: ~2 workgroups per CU over the whole call
-  int64_t tiles_target = std::max<int64_t>(1, kHistTargetWG / n_chunks);
-  int64_t R = (n_pos + tiles_target - 1) / tiles_target;
-  R = std::min<int64_t>(std::max<int64_t>((R + 255) / 256 * 256, 1024), WGBM_MAX_TILE_ROWS);
-  const int64_t max_tiles = n_pos / R + n_keys + 1;
-  Tile* tiles = (Tile*)scratch_get(st, sizeof(Tile) * max_tiles, 3);
-  int32_t* kts = (int32_t*)scratch_get(st, sizeof(int32_t) * ((size_t)n_keys + 1), 4);
-  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
-  const int64_t words = max_tiles * tile_words;
-  unsigned long long* part =
-      (unsigned long long*)scratch_get(st, sizeof(unsigned long long) * words, 5);
-  WGBM_REQUIRE(tiles && kts && part, "scratch allocation failed (%lld words)", (long long)words);
-  hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, seg, n_pos, n_keys,
-                     (const int32_t*)nullptr, (int32_t)R, (int32_t)max_tiles, tiles, kts, n_tiles,
-                     abs_part, n_abs, wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1)), absmax,
-                     shift);
-  WGBM_LAUNCH_CHECK();
   HistLaunch a;
   a.codes = codes;
   a.n_rows = n_rows;
@@ -125,6 +126,11 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   a.max_tiles = (int32_t)max_tiles;
   a.native = native ? 1 : 0;
   a.timer_tag = "hist_tiles";
+  a.sm.partial = abs_part;
+  a.sm.n_part = n_abs;
+  a.sm.qbits = wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1));
+  a.sm.absmax_bits = absmax;
+  a.sm.shift = shift;
   int r = launch_hist_tiles(a, st);
   if (r) return r;
   // tiles per segment (finalize's tile split): the planner's estimate

@@ -66,7 +66,7 @@ void hist_tiles_kernel(
     const float* __restrict__ resid, int64_t resid_tree_stride,
     const int32_t* __restrict__ shifts, const int32_t* __restrict__ order,
     const Tile* __restrict__ tiles, const int32_t* __restrict__ n_tiles, int32_t keys_per_tree,
-    int32_t num_bins_rt, unsigned long long* __restrict__ part) {
+    int32_t num_bins_rt, unsigned long long* __restrict__ part, ShiftFromMax sm) {
   // the only LDS of this kernel: with no static LDS it starts at LDS address
   // 0, so the NAT path can form LDS addresses as plain integers
   extern __shared__ unsigned long long lds[];
@@ -75,6 +75,24 @@ void hist_tiles_kernel(
   const int n_chunks = (n_feats + CW - 1) / CW;
   const int tile_id = blockIdx.x / n_chunks;
   const int chunk = blockIdx.x - tile_id * n_chunks;
+  // sm.partial (one tree): every wave reduces the call's per-block maxima of
+  // |residual| to the shift itself (no separate launch); workgroup 0, which
+  // always exists, stores the maximum and the shift for the finalize
+  int s_call = 0;
+  if (sm.partial) {
+    const int lane0 = threadIdx.x & 63;
+    uint32_t m = 0;
+    for (int i = lane0; i < sm.n_part; i += 64) {
+      const uint32_t v = sm.partial[i];
+      m = v > m ? v : m;
+    }
+    m = wgbm_wave_max_u32(m);
+    s_call = m >= 0x7f800000u ? 0 : wgbm_shift_from_absmax(__uint_as_float(m), sm.qbits);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      *sm.absmax_bits = m;
+      *sm.shift = s_call;
+    }
+  }
   if (tile_id >= *n_tiles) return;
   const Tile tl = tiles[tile_id];
   const int Bp = num_bins + 1;
@@ -93,7 +111,7 @@ void hist_tiles_kernel(
   // wait for the (scalar) load happens once before the loop rather than at
   // the top of every iteration, where it would also drain the wave's
   // outstanding LDS atomics (both share one counter).
-  const int s_raw = shifts[tree];
+  const int s_raw = sm.partial ? __builtin_amdgcn_readfirstlane(s_call) : shifts[tree];
   const int s = s_raw < 0 ? 0 : (s_raw > 255 ? 255 : s_raw);
   const int32_t* __restrict__ ord = GATHER ? order + tl.begin : nullptr;
   const int n = (int)(tl.end - tl.begin);  // a tile has at most 65536 rows
@@ -592,27 +610,6 @@ __global__ __launch_bounds__(256) void hist_finalize_level_kernel(
   }
 }
 
-// --------------------------------------------------------------------------
-// max |residual| over the rows of a call (ABI path)
-// --------------------------------------------------------------------------
-__global__ void absmax_partial_kernel(const float* __restrict__ resid,
-                                      const int32_t* __restrict__ rows, int64_t n,
-                                      uint32_t* __restrict__ partial,
-                                      float* __restrict__ gathered) {
-  // gathered (with rows): resid[rows[i]] copied into position order on the way
-  uint32_t m = 0;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = rows ? (int64_t)rows[i] : i;
-    const float v = resid[r];
-    if (gathered) gathered[i] = v;
-    const uint32_t b = wgbm_abs_bits(v);
-    m = b > m ? b : m;
-  }
-  m = wgbm_block_max_u32(m);
-  if (threadIdx.x == 0) partial[blockIdx.x] = m;
-}
-
 // one workgroup per independent maximum t: reduce partial[t*n_part ...] and
 // turn it into the quantisation shift (0 for an all-zero or non-finite input;
 // absmax_bits keeps the raw maximum so a NaN/inf input can be reported)
@@ -643,20 +640,8 @@ __device__ void plan_tiles_body(
     const int64_t* __restrict__ seg, int64_t total_rows, int32_t n_keys,
     const int32_t* __restrict__ key_list, int32_t tile_rows,
     int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
-    int32_t* __restrict__ n_tiles, const uint32_t* __restrict__ abs_part, int32_t n_abs,
-    int32_t qbits, uint32_t* __restrict__ absmax_bits, int32_t* __restrict__ shift) {
+    int32_t* __restrict__ n_tiles) {
   __shared__ int64_t wsum[16];
-  if (abs_part) {
-    // the quantisation shift of the call from the per-block maxima (what
-    // absmax_finish_kernel does for one tree), folded in to save a launch
-    uint32_t m = 0;
-    for (int i = threadIdx.x; i < n_abs; i += blockDim.x) m = abs_part[i] > m ? abs_part[i] : m;
-    m = wgbm_block_max_u32(m);
-    if (threadIdx.x == 0) {
-      *absmax_bits = m;
-      *shift = m >= 0x7f800000u ? 0 : wgbm_shift_from_absmax(__uint_as_float(m), qbits);
-    }
-  }
   __shared__ int64_t sbuf[kScanK * 1024];
   const int nk = n_keys;  // entries of key_list (or keys 0..n_keys-1)
   auto bounds = [&](int i, int& key, int64_t& b0, int64_t& b1) {
@@ -725,14 +710,42 @@ __device__ void plan_tiles_body(
   }
 }
 
+// One launch for a call's preparation: blocks [0, n_part) write the per-block
+// maxima of |residual| (and, with rows, the residuals in position order), and
+// with plan != 0 block n_part plans the tiles.  The tile kernel turns the
+// maxima into the shift.
+__global__ __launch_bounds__(1024) void hist_prep_kernel(
+    const float* __restrict__ resid, const int32_t* __restrict__ rows, int64_t n,
+    uint32_t* __restrict__ partial, float* __restrict__ gathered, int32_t n_part, int32_t plan,
+    const int64_t* __restrict__ seg, int32_t n_keys, int32_t tile_rows, int32_t max_tiles,
+    Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
+    int32_t* __restrict__ n_tiles) {
+  if ((int)blockIdx.x >= n_part) {
+    if (plan)
+      plan_tiles_body(seg, n, n_keys, nullptr, tile_rows, max_tiles, tiles, key_tile_start,
+                      n_tiles);
+    return;
+  }
+  uint32_t m = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)n_part * blockDim.x) {
+    const int64_t r = rows ? (int64_t)rows[i] : i;
+    const float v = resid[r];
+    if (gathered) gathered[i] = v;
+    const uint32_t b = wgbm_abs_bits(v);
+    m = b > m ? b : m;
+  }
+  m = wgbm_block_max_u32(m);
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
 __global__ __launch_bounds__(1024) void plan_tiles_kernel(
     const int64_t* __restrict__ seg, int64_t total_rows, int32_t n_keys,
     const int32_t* __restrict__ key_list, int32_t tile_rows,
     int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
-    int32_t* __restrict__ n_tiles, const uint32_t* __restrict__ abs_part, int32_t n_abs,
-    int32_t qbits, uint32_t* __restrict__ absmax_bits, int32_t* __restrict__ shift) {
+    int32_t* __restrict__ n_tiles) {
   plan_tiles_body(seg, total_rows, n_keys, key_list, tile_rows, max_tiles, tiles, key_tile_start,
-                  n_tiles, abs_part, n_abs, qbits, absmax_bits, shift);
+                  n_tiles);
 }
 
 
@@ -955,7 +968,7 @@ static int launch_tiles_t(const HistLaunch& a, hipStream_t st) {
                         dim3(kHistThreads), lds, st, timer_start_event(tm), timer_stop_event(tm), 0,
                         a.codes, a.n_rows, a.stride, a.n_feats, a.resid, a.resid_tree_stride,
                         a.shifts, a.order, a.tiles, a.n_tiles, a.keys_per_tree, a.num_bins,
-                        a.part);
+                        a.part, a.sm);
   timer_end(tm);
   WGBM_LAUNCH_CHECK();
   return 0;

@@ -31,6 +31,16 @@ constexpr int kAuxStream = 3;
 // histogram workgroups per launch the tile sizes aim for (2 per CU)
 constexpr int kHistTargetWG = 512;
 
+// The tile kernel's shift from per-block maxima of |residual| (one tree):
+// partial == nullptr means the shifts come from the shifts array instead.
+struct ShiftFromMax {
+  const uint32_t* partial = nullptr;
+  int32_t n_part = 0;
+  int32_t qbits = 0;
+  uint32_t* absmax_bits = nullptr;  // written by workgroup 0
+  int32_t* shift = nullptr;
+};
+
 struct HistLaunch {
   const int8_t* codes;
   int64_t n_rows;
@@ -56,6 +66,7 @@ struct HistLaunch {
   int32_t resid_by_pos = 0;
   // timer tag of the tile kernel (nullptr: not timed)
   const char* timer_tag = nullptr;
+  ShiftFromMax sm;
 };
 
 int hist_pick_v(int num_bins);
@@ -81,15 +92,16 @@ int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
                           int32_t num_eras, int32_t nodes_in_level, int32_t depth,
                           const int64_t* parent_q, const int32_t* parent_c, const int32_t* n_tiles,
                           int64_t* hq, int32_t* hc, hipStream_t st);
-__global__ void absmax_partial_kernel(const float* resid, const int32_t* rows, int64_t n,
-                                      uint32_t* partial, float* gathered);
 __global__ void absmax_finish_kernel(const uint32_t* partial, int32_t n_part, int32_t qbits,
                                      uint32_t* absmax_bits, int32_t* shifts);
 __global__ void plan_tiles_kernel(const int64_t* seg, int64_t total, int32_t n_keys,
-                                  const int32_t* key_list, int32_t tile_rows, int32_t max_tiles, Tile* tiles,
-                                  int32_t* key_tile_start, int32_t* n_tiles,
-                                  const uint32_t* abs_part, int32_t n_abs, int32_t qbits,
-                                  uint32_t* absmax_bits, int32_t* shift);
+                                  const int32_t* key_list, int32_t tile_rows, int32_t max_tiles,
+                                  Tile* tiles, int32_t* key_tile_start, int32_t* n_tiles);
+__global__ void hist_prep_kernel(const float* resid, const int32_t* rows, int64_t n,
+                                 uint32_t* partial, float* gathered, int32_t n_part, int32_t plan,
+                                 const int64_t* seg, int32_t n_keys, int32_t tile_rows,
+                                 int32_t max_tiles, Tile* tiles, int32_t* key_tile_start,
+                                 int32_t* n_tiles);
 __global__ void era_count_kernel(const int32_t* rows, int64_t n, const int32_t* era,
                                  int32_t num_eras, int64_t* counts);
 __global__ void exclusive_scan_i64_kernel(const int64_t* in, int32_t n, int64_t* out);
