@@ -59,10 +59,10 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   // segments: explicit (seg_dev), by era (sort rows by era), or a single one
   const int n_keys = seg_dev ? n_seg : (regroup ? num_eras : 1);
 
-  // tiles: ~2 workgroups per CU over the whole call
-  int64_t tiles_target = std::max<int64_t>(1, kHistTargetWG / n_chunks);
+  // tiles: ~1 workgroup per CU over the whole call
+  int64_t tiles_target = std::max<int64_t>(1, kHistTargetWGCall / n_chunks);
   int64_t R = (n_pos + tiles_target - 1) / tiles_target;
-  R = std::min<int64_t>(std::max<int64_t>((R + 255) / 256 * 256, 1024), WGBM_MAX_TILE_ROWS);
+  R = std::min<int64_t>(std::max<int64_t>(R, 1024), WGBM_MAX_TILE_ROWS);
   const int64_t max_tiles = n_pos / R + n_keys + 1;
   Tile* tiles = (Tile*)scratch_get(st, sizeof(Tile) * max_tiles, 3);
   int32_t* kts = (int32_t*)scratch_get(st, sizeof(int32_t) * ((size_t)n_keys + 1), 4);

@@ -630,8 +630,10 @@ __global__ void absmax_finish_kernel(const uint32_t* __restrict__ partial, int32
 }
 
 // --------------------------------------------------------------------------
-// tile planner: one workgroup scans segment lengths and emits tiles of at most
-// tile_rows rows that never cross a segment.  keys: either all n_keys (list ==
+// tile planner: one workgroup scans segment lengths and splits every segment
+// into round(len / tile_rows) near-equal tiles (at least one, and at most
+// WGBM_MAX_TILE_ROWS rows each) that never cross a segment: no tile is a
+// small remainder, so the workgroups of a launch carry even work.  keys: either all n_keys (list ==
 // nullptr) or the first *n_list entries of key_list.  seg: int64 [n_keys+1]
 // (nullptr => a single segment [0, total)).
 // --------------------------------------------------------------------------
@@ -649,6 +651,12 @@ __device__ void plan_tiles_body(
     b0 = (key >= 0 && seg) ? seg[key] : 0;
     b1 = key < 0 ? 0 : (seg ? seg[key + 1] : total_rows);
   };
+  auto count = [&](int64_t len) -> int64_t {
+    if (len <= 0) return 0;
+    const int64_t k = (len + tile_rows / 2) / tile_rows;
+    const int64_t kmin = (len + WGBM_MAX_TILE_ROWS - 1) / WGBM_MAX_TILE_ROWS;
+    return k > kmin ? k : kmin;
+  };
   // phase 1: exclusive scan of the tile counts -> key_tile_start
   const int64_t total = wgbm_block_scan_tiled(
       nk,
@@ -656,7 +664,7 @@ __device__ void plan_tiles_body(
         int key;
         int64_t b0, b1;
         bounds(i, key, b0, b1);
-        return key < 0 ? 0 : (b1 - b0 + tile_rows - 1) / tile_rows;
+        return key < 0 ? 0 : count(b1 - b0);
       },
       [&](int i, int64_t v) { key_tile_start[i] = (int32_t)v; }, wsum, sbuf);
   const int ntot = total < max_tiles ? (int)total : max_tiles;
@@ -673,11 +681,12 @@ __device__ void plan_tiles_body(
   if (threadIdx.x == 0) n_big = 0;
   __syncthreads();
   auto write_tile = [&](int key, int64_t b0, int64_t b1, int first, int j) {
+    const int64_t nt = count(b1 - b0);
     Tile tl;
     tl.key = key;
     tl.pad = 0;
-    tl.begin = b0 + (int64_t)j * tile_rows;
-    tl.end = tl.begin + tile_rows < b1 ? tl.begin + tile_rows : b1;
+    tl.begin = b0 + (b1 - b0) * j / nt;
+    tl.end = b0 + (b1 - b0) * (j + 1) / nt;
     tiles[first + j] = tl;
   };
   for (int i = threadIdx.x; i < nk; i += blockDim.x) {

@@ -28,8 +28,12 @@ constexpr int kDesEraBlock = 32;
 // sc0 for the code stream of the tile histogram (measured faster there)
 constexpr int kAuxNT = 2;
 constexpr int kAuxStream = 3;
-// histogram workgroups per launch the tile sizes aim for (2 per CU)
+// histogram workgroups per launch the tile sizes aim for: 2 per CU in the
+// engine; 1 per CU for a single call (one 16-wave workgroup already keeps a
+// CU's LDS atomic unit busy, and half the tiles halve the partials that the
+// finalize reads)
 constexpr int kHistTargetWG = 512;
+constexpr int kHistTargetWGCall = 256;
 
 // The tile kernel's shift from per-block maxima of |residual| (one tree):
 // partial == nullptr means the shifts come from the shifts array instead.
