@@ -102,7 +102,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
     order = sorted;
     seg = starts;
     hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, seg, n_pos, n_keys,
-                       (const int32_t*)nullptr, (int32_t)R, (int32_t)max_tiles, tiles, kts,
+                       (const int32_t*)nullptr, (int32_t)R, 1, (int32_t)max_tiles, tiles, kts,
                        n_tiles);
     WGBM_LAUNCH_CHECK();
   }

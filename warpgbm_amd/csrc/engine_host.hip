@@ -377,7 +377,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         e->max_htiles = max_tiles;
       }
       hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur], (int64_t)0,
-                         n_list, list, (int32_t)R, (int32_t)max_tiles, e->htiles, e->hkts, e->hn);
+                         n_list, list, (int32_t)R, 0, (int32_t)max_tiles, e->htiles, e->hkts,
+                         e->hn);
       WGBM_LAUNCH_CHECK();
       HistLaunch a;
       a.codes = c.codes_rm;

@@ -631,16 +631,18 @@ __global__ void absmax_finish_kernel(const uint32_t* __restrict__ partial, int32
 
 // --------------------------------------------------------------------------
 // tile planner: one workgroup scans segment lengths and splits every segment
-// into round(len / tile_rows) near-equal tiles (at least one, and at most
-// WGBM_MAX_TILE_ROWS rows each) that never cross a segment: no tile is a
-// small remainder, so the workgroups of a launch carry even work.  keys: either all n_keys (list ==
+// into near-equal tiles that never cross a segment: ceil(len / tile_rows)
+// tiles (tiles never exceed tile_rows), or with nearest != 0
+// round(len / tile_rows) (at least one, and at most WGBM_MAX_TILE_ROWS rows
+// each: a call sized for one workgroup per CU gets exactly that).  No tile is
+// a small remainder, so the workgroups of a launch carry even work.  keys: either all n_keys (list ==
 // nullptr) or the first *n_list entries of key_list.  seg: int64 [n_keys+1]
 // (nullptr => a single segment [0, total)).
 // --------------------------------------------------------------------------
 // (blockDim.x == 1024)
 __device__ void plan_tiles_body(
     const int64_t* __restrict__ seg, int64_t total_rows, int32_t n_keys,
-    const int32_t* __restrict__ key_list, int32_t tile_rows,
+    const int32_t* __restrict__ key_list, int32_t tile_rows, int32_t nearest,
     int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
     int32_t* __restrict__ n_tiles) {
   __shared__ int64_t wsum[16];
@@ -651,10 +653,14 @@ __device__ void plan_tiles_body(
     b0 = (key >= 0 && seg) ? seg[key] : 0;
     b1 = key < 0 ? 0 : (seg ? seg[key + 1] : total_rows);
   };
-  auto count = [&](int64_t len) -> int64_t {
-    if (len <= 0) return 0;
-    const int64_t k = (len + tile_rows / 2) / tile_rows;
-    const int64_t kmin = (len + WGBM_MAX_TILE_ROWS - 1) / WGBM_MAX_TILE_ROWS;
+  // segment lengths are below 2^31 (positions are int32): 32-bit divisions
+  auto count = [&](int64_t len64) -> int64_t {
+    if (len64 <= 0) return 0;
+    const uint32_t len = (uint32_t)len64;
+    const uint32_t up = (uint32_t)(nearest ? tile_rows / 2 : tile_rows - 1);
+    const uint32_t k = (len + up) / (uint32_t)tile_rows;
+    static_assert(WGBM_MAX_TILE_ROWS == 1 << 16, "tile row bound");
+    const uint32_t kmin = (len + WGBM_MAX_TILE_ROWS - 1) >> 16;
     return k > kmin ? k : kmin;
   };
   // phase 1: exclusive scan of the tile counts -> key_tile_start
@@ -680,13 +686,15 @@ __device__ void plan_tiles_body(
   __shared__ int n_big;
   if (threadIdx.x == 0) n_big = 0;
   __syncthreads();
-  auto write_tile = [&](int key, int64_t b0, int64_t b1, int first, int j) {
-    const int64_t nt = count(b1 - b0);
+  // tile j of a segment split into nt: q = len / nt rows, the first r = len %
+  // nt tiles one more
+  auto write_tile = [&](int key, int64_t b0, uint32_t q, uint32_t r, int first, int j) {
+    const uint32_t uj = (uint32_t)j;
     Tile tl;
     tl.key = key;
     tl.pad = 0;
-    tl.begin = b0 + (b1 - b0) * j / nt;
-    tl.end = b0 + (b1 - b0) * (j + 1) / nt;
+    tl.begin = b0 + (int64_t)(uj * q + (uj < r ? uj : r));
+    tl.end = tl.begin + (int64_t)(q + (uj < r ? 1u : 0u));
     tiles[first + j] = tl;
   };
   for (int i = threadIdx.x; i < nk; i += blockDim.x) {
@@ -703,7 +711,8 @@ __device__ void plan_tiles_body(
         continue;
       }
     }
-    for (int j = 0; j < nt && first + j < ntot; ++j) write_tile(key, b0, b1, first, j);
+    const uint32_t len = (uint32_t)(b1 - b0), q = len / (uint32_t)nt, r = len - q * (uint32_t)nt;
+    for (int j = 0; j < nt && first + j < ntot; ++j) write_tile(key, b0, q, r, first, j);
   }
   __syncthreads();
   const int nb = n_big < kMaxBig ? n_big : kMaxBig;
@@ -714,8 +723,9 @@ __device__ void plan_tiles_body(
     bounds(i, key, b0, b1);
     const int first = key_tile_start[i];
     const int nt = key_tile_start[i + 1] - first;
+    const uint32_t len = (uint32_t)(b1 - b0), q = len / (uint32_t)nt, r = len - q * (uint32_t)nt;
     for (int j = threadIdx.x; j < nt && first + j < ntot; j += blockDim.x)
-      write_tile(key, b0, b1, first, j);
+      write_tile(key, b0, q, r, first, j);
   }
 }
 
@@ -731,7 +741,7 @@ __global__ __launch_bounds__(1024) void hist_prep_kernel(
     int32_t* __restrict__ n_tiles) {
   if ((int)blockIdx.x >= n_part) {
     if (plan)
-      plan_tiles_body(seg, n, n_keys, nullptr, tile_rows, max_tiles, tiles, key_tile_start,
+      plan_tiles_body(seg, n, n_keys, nullptr, tile_rows, 1, max_tiles, tiles, key_tile_start,
                       n_tiles);
     return;
   }
@@ -750,11 +760,11 @@ __global__ __launch_bounds__(1024) void hist_prep_kernel(
 
 __global__ __launch_bounds__(1024) void plan_tiles_kernel(
     const int64_t* __restrict__ seg, int64_t total_rows, int32_t n_keys,
-    const int32_t* __restrict__ key_list, int32_t tile_rows,
+    const int32_t* __restrict__ key_list, int32_t tile_rows, int32_t nearest,
     int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
     int32_t* __restrict__ n_tiles) {
-  plan_tiles_body(seg, total_rows, n_keys, key_list, tile_rows, max_tiles, tiles, key_tile_start,
-                  n_tiles);
+  plan_tiles_body(seg, total_rows, n_keys, key_list, tile_rows, nearest, max_tiles, tiles,
+                  key_tile_start, n_tiles);
 }
 
 

@@ -99,8 +99,9 @@ int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
 __global__ void absmax_finish_kernel(const uint32_t* partial, int32_t n_part, int32_t qbits,
                                      uint32_t* absmax_bits, int32_t* shifts);
 __global__ void plan_tiles_kernel(const int64_t* seg, int64_t total, int32_t n_keys,
-                                  const int32_t* key_list, int32_t tile_rows, int32_t max_tiles,
-                                  Tile* tiles, int32_t* key_tile_start, int32_t* n_tiles);
+                                  const int32_t* key_list, int32_t tile_rows, int32_t nearest,
+                                  int32_t max_tiles, Tile* tiles, int32_t* key_tile_start,
+                                  int32_t* n_tiles);
 __global__ void hist_prep_kernel(const float* resid, const int32_t* rows, int64_t n,
                                  uint32_t* partial, float* gathered, int32_t n_part, int32_t plan,
                                  const int64_t* seg, int32_t n_keys, int32_t tile_rows,
