@@ -184,7 +184,7 @@ def native_layout(raw, num_bins, stride):
 
 
 @pytest.mark.parametrize("B,F", [(32, 203), (5, 203), (50, 203), (126, 203), (127, 203),
-                                 (32, 1000), (50, 700)])
+                                 (32, 1000), (50, 700), (32, 100), (5, 60)])
 @pytest.mark.parametrize("native", [False, True])
 def test_histogram_segments_bit_exact(gpu, native, B, F):
     """16 node segments of raw codes with values outside [0, B) (negative and
@@ -192,7 +192,8 @@ def test_histogram_segments_bit_exact(gpu, native, B, F):
     through the native layout made by the pre-binned copy; both equal the
     oracle on the raw codes.  B = 127 has no native-layout kernel (its rows
     would not fit a byte) and takes the clamping one.  The wide cases (16
-    segments x 16 or more feature planes) take the plane finalize."""
+    segments x 16 or more feature planes) take the plane finalize; 100 and 60
+    features take two and one feature per lane."""
     print_case("histogram_segments", "16 nodes", "native" if native else "raw", B, F)
     rng = np.random.default_rng(5 + B + F)
     N, S = 40000, 16

@@ -33,7 +33,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
                               const int32_t* era, int32_t num_eras, const int32_t* feat_idx,
                               int32_t n_out_feats, int32_t num_bins, float* G, float* H,
                               bool native, hipStream_t st) {
-  const int V = hist_pick_v(num_bins);
+  const int V = hist_pick_v(num_bins, n_hist_feats);
   const int n_chunks = (n_hist_feats + kHistSlots * V - 1) / (kHistSlots * V);
   // scratch layout (slot 0: control words and the per-block maxima)
   constexpr int kAbsBlocks = 256;

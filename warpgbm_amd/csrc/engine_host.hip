@@ -120,7 +120,7 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   const int64_t T = cfg.n_trees, N = cfg.n_rows, E = cfg.num_eras, F = cfg.n_feats,
                 B = cfg.num_bins;
   const int D = cfg.max_depth;
-  e->V = hist_pick_v(cfg.num_bins);
+  e->V = hist_pick_v(cfg.num_bins, F);
   e->n_chunks = (int)((F + kHistSlots * e->V - 1) / (kHistSlots * e->V));
   e->qbits = wgbm_qbits_for_rows(N);
   e->H = (1 << (D + 1)) - 1;

@@ -957,11 +957,16 @@ int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
 // --------------------------------------------------------------------------
 // features per lane: the largest V in {4, 2, 1} whose LDS histogram
 // V*(B+1)*64 words stays within 68 KiB, so that two workgroups fit a CU
-int hist_pick_v(int num_bins) {
+int hist_pick_v(int num_bins, int64_t n_feats) {
   const int bp = num_bins + 1;
-  if (4 * bp <= 136) return 4;  // num_bins <= 33
-  if (2 * bp <= 136) return 2;  // num_bins <= 67
-  return 1;
+  int v = 4 * bp <= 136 ? 4 : (2 * bp <= 136 ? 2 : 1);  // num_bins <= 33 / <= 67 / beyond
+  // a narrower lane (fewer features per lane) as long as the chunk count
+  // stays the same: each row still costs the same load instructions, and
+  // the atomics of lanes past the last feature (every lane adds, for a
+  // branch-free loop) shrink, e.g. 100 features: 4 -> 2 LDS atomics per row
+  auto chunks = [&](int w) { return (n_feats + kHistSlots * w - 1) / (kHistSlots * w); };
+  while (v > 1 && chunks(v / 2) == chunks(v)) v /= 2;
+  return v;
 }
 
 size_t hist_lds_bytes(int V, int num_bins, bool native) {
@@ -1018,6 +1023,10 @@ int launch_hist_tiles(const HistLaunch& a, hipStream_t st) {
   if (a.V == 4 && a.num_bins == 32) {
     if (mode == kLoadBuffer) return launch_tiles_g<4, kLoadBuffer, 32>(a, st);
     if (mode == kLoadGlobalAligned) return launch_tiles_g<4, kLoadGlobalAligned, 32>(a, st);
+  }
+  if (a.V == 2 && a.num_bins == 32) {
+    if (mode == kLoadBuffer) return launch_tiles_g<2, kLoadBuffer, 32>(a, st);
+    if (mode == kLoadGlobalAligned) return launch_tiles_g<2, kLoadGlobalAligned, 32>(a, st);
   }
 #define WGBM_DISPATCH(VV)                                                      \
   if (a.V == VV) {                                                             \

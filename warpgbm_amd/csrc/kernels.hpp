@@ -73,7 +73,7 @@ struct HistLaunch {
   ShiftFromMax sm;
 };
 
-int hist_pick_v(int num_bins);
+int hist_pick_v(int num_bins, int64_t n_feats);
 size_t hist_lds_bytes(int V, int num_bins, bool native);
 bool hist_native_ok(int num_bins);
 int hist_load_mode(int64_t n_rows, int64_t stride, int V);
