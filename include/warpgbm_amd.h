@@ -156,6 +156,16 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
 /* In-place row softmax of float32 [n, K] (warpgbm/metrics.py:12-15). */
 int wgbm_softmax_rows(float* x, int64_t n, int32_t K, void* stream);
 
+/* Per-era split-gain importance (replaces the per-node .item() loop of
+ * warpgbm/core.py:624-627): acc float32 [num_eras, n_feats] (device, in/out)
+ * gets acc[e][f] += gain[node[i] * num_eras + e] for i in [feat_start[f],
+ * feat_start[f+1]), one float32 add after the other in that order.  gain:
+ * float32 rows of num_eras per node; node: int64 gain-row indices grouped by
+ * feature, each group in the order the reference visits the nodes (trees in
+ * order, nodes depth-first, left first); feat_start: int64 [n_feats + 1]. */
+int wgbm_importance_add(float* acc, int32_t n_feats, int32_t num_eras, const float* gain,
+                        const int64_t* node, const int64_t* feat_start, void* stream);
+
 /* ------------------------------------------------------------------------
  * Level-wise boosting engine (the caller of the four operators:
  * warpgbm/core.py grow_forest 692-744, grow_forest_multiclass 746-818,

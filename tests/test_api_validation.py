@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 from warpgbm_amd import WarpGBM
-from warpgbm_amd.core import _add_in_order, _dict_to_heap, _heap_to_dict_lists, _preorder_heap
+from warpgbm_amd.core import _dict_to_heap, _heaps_to_dicts, _preorder_heap
 
 
 @pytest.mark.parametrize("kw,exc", [
@@ -89,8 +89,9 @@ def test_heap_dict_round_trip_and_preorder():
     f, b, v = _dict_to_heap(tree, H)
     assert f.tolist() == [3, 1, -1, -1, -1, -1, -1]
     cnt = np.array([12, 5, 7, 2, 3, 0, 0])
-    back = _heap_to_dict_lists(f.tolist(), b.tolist(), v.tolist(), cnt.tolist())
-    assert back == tree
+    back = _heaps_to_dicts(np.asarray(f)[None], np.asarray(b)[None], np.asarray(v)[None],
+                           cnt[None])
+    assert back == [tree]
     assert _preorder_heap(7).tolist() == [0, 1, 3, 4, 2, 5, 6]
 
     def internal(feat):
@@ -100,11 +101,15 @@ def test_heap_dict_round_trip_and_preorder():
     # engine records mark nodes below a leaf as absent (-2)
     feat = [0, -1, 4, -2, -2, -1, -1]
     assert internal(feat) == [0, 2]
-    assert _heap_to_dict_lists(feat, [2, 0, 1, 0, 0, 0, 0], [0.0, 1.0, 0.0, 0.0, 0.0, -3.5, 2.0],
-                               [9, 4, 5, 0, 0, 4, 1]) == {
-        "feature": 0, "bin": 2, "left": {"leaf_value": 1.0, "samples": 4},
-        "right": {"feature": 4, "bin": 1, "left": {"leaf_value": -3.5, "samples": 4},
-                  "right": {"leaf_value": 2.0, "samples": 1}}}
+    second = {"feature": 0, "bin": 2, "left": {"leaf_value": 1.0, "samples": 4},
+              "right": {"feature": 4, "bin": 1, "left": {"leaf_value": -3.5, "samples": 4},
+                        "right": {"leaf_value": 2.0, "samples": 1}}}
+    # several records in one call ([rounds, trees, H]), an all-absent one included
+    fs = np.array([[f, feat], [[-2] * 7, f]], np.int32)
+    bs = np.array([[b, [2, 0, 1, 0, 0, 0, 0]], [[0] * 7, b]], np.int32)
+    vs = np.array([[v, [0.0, 1.0, 0.0, 0.0, 0.0, -3.5, 2.0]], [[0.0] * 7, v]], np.float32)
+    cs = np.array([[cnt, [9, 4, 5, 0, 0, 4, 1]], [[0] * 7, cnt]], np.int64)
+    assert _heaps_to_dicts(fs, bs, vs, cs) == [tree, second, None, tree]
 
 
 def test_flatten_tree_matches_reference_layout():
@@ -116,22 +121,6 @@ def test_flatten_tree_matches_reference_layout():
     assert flat[1, 4:].tolist() == [1.0, 1.5]
     assert flat[2, :5].tolist() == [0, 1, 3, 4, 0]
     assert np.isnan(flat[5:]).all()
-
-
-def test_importance_adds_in_node_order():
-    """Importance accumulation equals np.add.at's one-by-one float32 adds (the
-    reference's sequential per-node += at warpgbm/core.py:624-627), bit for
-    bit, for repeated, single and absent indices and values of mixed scale."""
-    rng = np.random.default_rng(0)
-    for trial in range(200):
-        F, E, M = int(rng.integers(1, 30)), int(rng.integers(1, 7)), int(rng.integers(0, 300))
-        idx = rng.integers(0, F, M) if trial % 3 else np.full(M, F - 1)
-        val = (rng.standard_normal((M, E)) * 10.0 ** rng.integers(-8, 8, (M, 1))).astype(np.float32)
-        a = rng.standard_normal((E, F)).astype(np.float32)
-        b = a.copy()
-        np.add.at(a.T, idx, val)
-        _add_in_order(b.T, idx, val)
-        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), trial
 
 
 def test_era_layout_matches_unique_sort():

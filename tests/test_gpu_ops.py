@@ -322,6 +322,31 @@ def test_staged_upload_exact(gpu):
     assert torch.equal(D.upload_float(X32, dev).cpu(), torch.from_numpy(X32))
 
 
+def test_importance_add_in_node_order(gpu):
+    """wgbm_importance_add equals np.add.at's one-by-one float32 adds (the
+    reference's sequential per-node += at warpgbm/core.py:624-627), bit for
+    bit, for repeated, single and absent features and values of mixed scale
+    (large then tiny adds expose any reordering)."""
+    print_case("importance_add")
+    rng = np.random.default_rng(0)
+    for trial in range(40):
+        F, E, M = int(rng.integers(1, 30)), int(rng.integers(1, 7)), int(rng.integers(0, 300))
+        idx = rng.integers(0, F, M) if trial % 3 else np.full(M, F - 1)
+        val = (rng.standard_normal((M, E)) * 10.0 ** rng.integers(-8, 8, (M, 1))).astype(F32)
+        acc0 = rng.standard_normal((E, F)).astype(F32)
+        want = acc0.copy()
+        np.add.at(want.T, idx, val)
+        # gain rows stored shuffled; node lists the rows in add order by feature
+        perm = rng.permutation(M)
+        rows = np.empty((max(M, 1), E), F32)
+        rows[perm] = val
+        by_f = np.argsort(idx, kind="stable")
+        fstart = np.searchsorted(idx[by_f], np.arange(F + 1)).astype(np.int64)
+        acc = t(acc0)
+        D.importance_add(acc, t(rows), t(perm[by_f].astype(np.int64)), t(fstart))
+        assert np.array_equal(bits(acc.cpu().numpy()), bits(want)), trial
+
+
 def test_lds_atomic_probe(gpu):
     """The instrumentation probe runs and reports a plausible whole-GPU rate
     of 64-bit LDS atomic adds (between 1e11 and 1e14 per second)."""

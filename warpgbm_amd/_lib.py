@@ -38,6 +38,7 @@ SIGNATURES = {
     "wgbm_copy_prebinned": (C.c_int, [_p, _i64, _i32, _i64, _p, _i64, _p, _i32, _p, _p]),
     "wgbm_predict_heap": (C.c_int, [_p, _i64, _i64, _i32, _p, _p, _p, _i32, _i32, _i32, _i32,
                                     _f32, _p, _p]),
+    "wgbm_importance_add": (C.c_int, [_p, _i32, _i32, _p, _p, _p, _p]),
     "wgbm_softmax_rows": (C.c_int, [_p, _i64, _i32, _p]),
     "wgbm_engine_create": (C.c_int, [C.POINTER(_p), _p]),
     "wgbm_engine_round": (C.c_int, [_p, _p, _p, _p, _i32, _p, _p]),

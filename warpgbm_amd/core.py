@@ -380,6 +380,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         eng = self._new_engine(codes, root_order, era_start, 1, 0)
         n_new = self.n_estimators - start_iter
         rec = self._alloc_records(n_new, 1, dev)
+        self._phases.mark("engine")
         self.stop = False
         eval_pred = None
         if self._eval is not None:
@@ -435,6 +436,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         eng = self._new_engine(codes, root_order, era_start, K, 1)
         n_new = self.n_estimators - start_iter
         rec = self._alloc_records(n_new, K, dev)
+        self._phases.mark("engine")
         self.stop = False
         eval_scores = None
         if self._eval is not None:
@@ -557,28 +559,49 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         tree dicts and accumulate importance in the reference's order: per
         tree, internal nodes in depth-first pre-order, float32 adds
         (warpgbm/core.py:624-627)."""
-        host = {k: v[:done].cpu().numpy() for k, v in rec.items()}
+        host = {}
+        for k in ("feat", "bin", "leaf", "count"):
+            # through pinned memory: one DMA per record
+            v = rec[k][:done]
+            h = torch.empty(v.shape, dtype=v.dtype, pin_memory=True)
+            h.copy_(v)
+            host[k] = h.numpy()
+        self._phases.mark("records copy")
         feat = host["feat"]  # [done, n_trees, H]
         n_trees, H = feat.shape[1], feat.shape[2]
         # importance: every internal node of every tree, trees in order and
-        # nodes in pre-order; np.add.at applies repeated indices one after the
-        # other, so the float32 adds happen in exactly that sequence
+        # nodes in pre-order, one float32 add per node and era in exactly that
+        # sequence; on the device from the per-era gain records (the nodes
+        # grouped by feature, in order, give each (feature, era) word to one
+        # thread)
         po = _preorder_heap(H)
         fp = feat[:, :, po]
         internal = fp >= 0
-        _add_in_order(self.per_era_feature_importance_.T, fp[internal],
-                      host["gain"][:, :, po, :][internal])
-        fl, bl = feat.tolist(), host["bin"].tolist()
-        ll, cl = host["leaf"].tolist(), host["count"].tolist()
+        if internal.any():
+            base = (np.arange(done, dtype=np.int64)[:, None, None] * n_trees
+                    + np.arange(n_trees, dtype=np.int64)[None, :, None]) * H
+            rows = (base + po[None, None, :].astype(np.int64))[internal]
+            fsel = fp[internal]
+            by_f = np.argsort(fsel, kind="stable")
+            F, E = self.num_features, self.num_eras
+            fstart = np.searchsorted(fsel[by_f], np.arange(F + 1)).astype(np.int64)
+            dev = rec["gain"].device
+            acc = torch.from_numpy(np.ascontiguousarray(self.per_era_feature_importance_,
+                                                        dtype=np.float32)).to(dev)
+            D.importance_add(acc, rec["gain"][:done].reshape(-1, E),
+                             torch.from_numpy(rows[by_f]).to(dev),
+                             torch.from_numpy(fstart).to(dev))
+            self.per_era_feature_importance_ = acc.cpu().numpy()
+        self._phases.mark("importance")
         # the tree dicts form no reference cycles; pausing the cyclic
         # collector keeps it from re-walking the growing forest on every
         # allocation threshold (about 4x faster at 2000 trees of depth 6)
         gc_was_on = gc.isenabled()
         gc.disable()
         try:
+            flat = _heaps_to_dicts(feat, host["bin"], host["leaf"], host["count"])
             for j in range(done):
-                trees = [_heap_to_dict_lists(fl[j][t], bl[j][t], ll[j][t], cl[j][t])
-                         for t in range(n_trees)]
+                trees = flat[j * n_trees:(j + 1) * n_trees]
                 if classification:
                     self.forest.append(trees)
                 else:
@@ -811,43 +834,32 @@ class WarpGBM(BaseEstimator, RegressorMixin):
 
 
 # ---------------------------------------------------------------------- tree helpers
-def _heap_to_dict_lists(feat, bin_, leaf, count):
-    """Reference tree dict from one heap record given as Python lists (feat
-    -1 leaf, -2 absent, >= 0 split; children of h at 2h+1 / 2h+2), built
-    bottom-up."""
-    H = len(feat)
-    nodes = [None] * H
-    for h in range(H - 1, -1, -1):
-        f = feat[h]
-        if f >= 0:
-            nodes[h] = {"feature": f, "bin": bin_[h], "left": nodes[2 * h + 1],
-                        "right": nodes[2 * h + 2]}
-        elif f == -1:
-            nodes[h] = {"leaf_value": leaf[h], "samples": count[h]}
-    return nodes[0]
-
-
-def _add_in_order(acc, idx, val):
-    """acc[idx[i]] += val[i] for i = 0, 1, ... in that order (what
-    ``np.add.at(acc, idx, val)`` computes, float adds included), by layers:
-    layer j holds the j-th occurrence of every index, so an index appears at
-    most once per layer and one fancy-indexed add per layer keeps each
-    index's sequence of adds in order."""
-    idx = np.asarray(idx, dtype=np.int64)
-    m = idx.shape[0]
-    if m == 0:
-        return
-    by_idx = np.argsort(idx, kind="stable")
-    sorted_idx = idx[by_idx]
-    first = np.flatnonzero(np.r_[True, sorted_idx[1:] != sorted_idx[:-1]])
-    runs = np.diff(np.r_[first, m])
-    occurrence = np.arange(m) - np.repeat(first, runs)
-    by_occ = np.argsort(occurrence, kind="stable")
-    bounds = np.searchsorted(occurrence[by_occ], np.arange(int(runs.max()) + 1), side="left")
-    bounds = np.r_[bounds, m]
-    for j in range(len(bounds) - 1):
-        sel = by_idx[by_occ[bounds[j]:bounds[j + 1]]]
-        acc[idx[sel]] += val[sel]
+def _heaps_to_dicts(feat, bin_, leaf, count):
+    """Reference tree dicts of many heap records ([..., H] arrays, trees in
+    row-major order; feat -1 leaf, -2 absent, >= 0 split; children of h at
+    2h+1 / 2h+2), each built bottom-up.  Only the present nodes' values are
+    turned into Python objects."""
+    H = feat.shape[-1]
+    f2 = feat.reshape(-1, H)
+    pres = f2 >= -1
+    h_l = np.nonzero(pres)[1].tolist()
+    ends = np.cumsum(np.count_nonzero(pres, axis=1)).tolist()
+    f_l = f2[pres].tolist()
+    b_l = bin_.reshape(-1, H)[pres].tolist()
+    v_l = leaf.reshape(-1, H)[pres].tolist()
+    c_l = count.reshape(-1, H)[pres].tolist()
+    out = []
+    start = 0
+    for end in ends:
+        nodes = [None] * H
+        for i in range(end - 1, start - 1, -1):
+            h, f = h_l[i], f_l[i]
+            nodes[h] = ({"feature": f, "bin": b_l[i], "left": nodes[2 * h + 1],
+                         "right": nodes[2 * h + 2]} if f >= 0
+                        else {"leaf_value": v_l[i], "samples": c_l[i]})
+        out.append(nodes[0])
+        start = end
+    return out
 
 
 def _preorder_heap(H):

@@ -364,6 +364,16 @@ int wgbm_softmax_rows(float* x, int64_t n, int32_t K, void* stream) {
   return 0;
 }
 
+int wgbm_importance_add(float* acc, int32_t n_feats, int32_t num_eras, const float* gain,
+                        const int64_t* node, const int64_t* feat_start, void* stream) {
+  WGBM_REQUIRE(n_feats >= 1 && num_eras >= 1, "bad importance shape");
+  WGBM_REQUIRE(acc && feat_start, "null pointer");
+  hipLaunchKernelGGL(importance_add_kernel, dim3(nblocks((int64_t)n_feats * num_eras, 256)),
+                     dim3(256), 0, S(stream), acc, n_feats, num_eras, gain, node, feat_start);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
 // ---------------------------------------------------------------------------
 // engine
 // ---------------------------------------------------------------------------

@@ -222,4 +222,25 @@ __global__ void softmax_rows_kernel(float* __restrict__ x, int64_t n, int32_t K)
   for (int k = 0; k < K; ++k) r[k] = r[k] / s;
 }
 
+// ---------------------------------------------------------------------------
+// per-era split-gain importance (warpgbm/core.py:624-627): every internal node
+// adds its per-era gains to acc[e][feature] with one float32 add per era, the
+// nodes in the order the reference visits them.  node / fstart: the gain rows
+// of the nodes grouped by feature (group f = node[fstart[f] .. fstart[f+1]),
+// in visiting order), so each (feature, era) word is one thread's sequential
+// sum and no two threads touch the same word.
+// ---------------------------------------------------------------------------
+__global__ void importance_add_kernel(float* __restrict__ acc, int32_t F, int32_t E,
+                                      const float* __restrict__ gain,
+                                      const int64_t* __restrict__ node,
+                                      const int64_t* __restrict__ fstart) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)F * E) return;
+  const int f = (int)(gid / E), e = (int)(gid - (int64_t)f * E);
+  float* w = acc + (int64_t)e * F + f;
+  float s = *w;
+  for (int64_t i = fstart[f]; i < fstart[f + 1]; ++i) s = s + gain[node[i] * E + e];
+  *w = s;
+}
+
 }  // namespace wgbm

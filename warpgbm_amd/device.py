@@ -293,6 +293,21 @@ def predict_heap(codes: Codes, feat: torch.Tensor, bin_: torch.Tensor, leaf: tor
     _lib.check(rc, "predict_heap")
 
 
+def importance_add(acc: torch.Tensor, gain: torch.Tensor, node: torch.Tensor,
+                   feat_start: torch.Tensor) -> None:
+    """acc [E, F] float32 += the gain rows ``gain`` [*, E] of ``node`` (int64,
+    grouped by feature: group f = node[feat_start[f]:feat_start[f+1]]), in
+    order, one float32 add at a time (cf. warpgbm/core.py:624-627)."""
+    E, F = acc.shape
+    assert acc.is_contiguous() and gain.is_contiguous() and acc.dtype == torch.float32
+    assert node.dtype == torch.int64 and feat_start.dtype == torch.int64
+    assert feat_start.numel() == F + 1
+    lib = _lib.load()
+    rc = lib.wgbm_importance_add(acc.data_ptr(), F, E, gain.data_ptr(), node.data_ptr(),
+                                 feat_start.data_ptr(), _stream(acc.device))
+    _lib.check(rc, "importance_add")
+
+
 def softmax_rows(x: torch.Tensor) -> None:
     lib = _lib.load()
     n, K = x.shape
