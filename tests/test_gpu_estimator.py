@@ -187,6 +187,32 @@ def test_era_des_colsample_uneven_eras_bit_exact(gpu, mcw, B):
     assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
 
 
+def test_era_des_many_eras_blocks_bit_exact(gpu):
+    """More eras than one 32-era block of the DES era sum (70 ids: two full
+    blocks and a partial one), uneven sizes with tiny eras, an id with no
+    rows and a feature subset: the oracle's trees, importances and
+    predictions."""
+    print_case("estimator", "DES E=70 era blocks")
+    rng = np.random.default_rng(12)
+    E, F, B = 70, 37, 5
+    sizes = rng.integers(2, 160, E)
+    sizes[[3, 40, 69]] = [1, 0, 300]
+    N = int(sizes.sum())
+    era = np.repeat(np.arange(E), sizes)
+    X = rng.integers(0, B, (N, F)).astype(np.int8)
+    flip = np.where(rng.random(E) < 0.5, -1.0, 1.0)
+    score = (X[:, :4] - 2).sum(axis=1) + flip[era] * (X[:, 4] - 2) + rng.standard_normal(N)
+    y = (score / 4.0).astype(F32)
+    kw = dict(num_bins=B, max_depth=4, n_estimators=4, learning_rate=0.4, min_child_weight=6)
+    m = WarpGBM(colsample_bytree=0.8, random_state=3, **kw)
+    m.fit(X, y, era_id=era)
+    ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era, feat_sets=m.feature_subsets_)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
+
+
 def test_era_des_large_eras_histogram_path_bit_exact(gpu):
     """Eras larger than one LDS tile (65536 rows) take the per-era histogram
     path (tile partials, exact sibling subtraction, era accumulation)."""
