@@ -322,6 +322,24 @@ def test_staged_upload_exact(gpu):
     assert torch.equal(D.upload_float(X32, dev).cpu(), torch.from_numpy(X32))
 
 
+def test_streamed_binning_exact(gpu):
+    """Predict-time binning that bins each uploaded chunk as it lands
+    (upload_and_bin) writes the same native codes as binning the whole
+    uploaded matrix, over several chunks and a ragged last one, float64 input
+    and NaN included."""
+    print_case("upload_and_bin")
+    rng = np.random.default_rng(10)
+    n, F, B = 300_001, 230, 32
+    X = rng.standard_normal((n, F))                   # float64: rounded while staging
+    X[rng.random((n, F)) < 1e-4] = np.nan
+    Xd = D.upload_float(X, dev)
+    edges = D.quantile_edges(Xd, B)
+    want = D.bin_matrix(Xd, edges, with_cm=False)
+    got = D.upload_and_bin(X, edges, dev)
+    assert got.stride == want.stride and got.num_bins == want.num_bins
+    assert torch.equal(got.rm, want.rm)
+
+
 def test_importance_add_in_node_order(gpu):
     """wgbm_importance_add equals np.add.at's one-by-one float32 adds (the
     reference's sequential per-node += at warpgbm/core.py:624-627), bit for

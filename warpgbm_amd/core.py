@@ -615,12 +615,9 @@ class WarpGBM(BaseEstimator, RegressorMixin):
     def bin_data_with_existing_edges(self, X_np):
         dev = torch.device(self.device)
         ph = _Phases()
-        Xd = D.upload_float(X_np, dev)
-        ph.mark("upload")
-        codes = D.bin_matrix(Xd, torch.as_tensor(self.bin_edges), with_cm=False)
-        ph.mark("bin")
+        codes = D.upload_and_bin(X_np, torch.as_tensor(self.bin_edges), dev)
+        ph.mark("upload+bin")
         ph.report("binning")
-        del Xd
         return codes
 
     def bin_inference_data(self, X_np):

@@ -158,6 +158,65 @@ def _upload_staged(X: np.ndarray, dev, np_dtype, torch_dtype) -> torch.Tensor:
     return out
 
 
+def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev) -> Codes:
+    """Row-major native codes of a host float matrix for known edges
+    [F, num_bins - 1] (predict-time binning, warpgbm/core.py:902-915): the rows
+    stream through the pinned staging buffers and a few device chunk buffers,
+    and each chunk is binned as soon as its copy lands, so the float matrix is
+    never whole on the device and the binning overlaps the transfer."""
+    X = np.asarray(X)
+    n, F = X.shape
+    row_bytes = 4 * max(F, 1)
+    if n * row_bytes < 4 * _STAGE_BYTES or not X.flags.c_contiguous:
+        return bin_matrix(upload_float(X, dev), edges, with_cm=False)
+    edges = edges.to(device=dev, dtype=torch.float32).contiguous()
+    if edges.shape[0] != F:
+        raise ValueError(f"edges for {edges.shape[0]} features, X has {F}")
+    c = _alloc_codes(n, F, dev, False, edges.shape[1] + 1)
+    bufs, pool = _staging()
+    rows_per = max(1, _STAGE_BYTES // row_bytes)
+    dbufs = [torch.empty((rows_per, F), dtype=torch.float32, device=dev)
+             for _ in range(len(bufs))]
+    lib = _lib.load()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    side_ptr = side.cuda_stream
+    events = [None] * len(bufs)
+    nthreads = pool._max_workers
+
+    def fill(dst, lo, hi):
+        np.copyto(dst[lo:hi], X[r0 + lo:r0 + hi], casting="same_kind")
+
+    for i, r0 in enumerate(range(0, n, rows_per)):
+        r1 = min(n, r0 + rows_per)
+        k = i % len(bufs)
+        if events[k] is not None:
+            events[k].synchronize()  # the copy that used this staging buffer is done
+        host = bufs[k][: (r1 - r0) * row_bytes].view(torch.float32).view(r1 - r0, F)
+        dst = host.numpy()
+        step = max(1, (r1 - r0 + nthreads - 1) // nthreads)
+        list(pool.map(lambda a: fill(dst, a, min(a + step, r1 - r0)), range(0, r1 - r0, step)))
+        with torch.cuda.stream(side):
+            # device buffer k was last read by the binning of chunk i - len(bufs),
+            # earlier on this same stream
+            dbufs[k][: r1 - r0].copy_(host, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(side)
+        events[k] = ev
+        rc = lib.wgbm_bin_matrix(dbufs[k].data_ptr(), r1 - r0, F, F, edges.data_ptr(),
+                                 edges.shape[1], c.rm.data_ptr() + r0 * c.stride, c.stride, None,
+                                 side_ptr)
+        _lib.check(rc, "bin_matrix")
+    torch.cuda.current_stream(dev).wait_stream(side)
+    c.rm.record_stream(side)
+    for b in dbufs:
+        b.record_stream(side)
+    for ev in events:
+        if ev is not None:
+            ev.synchronize()  # staging buffers are reused by the next upload
+    return c
+
+
 def quantile_edges(Xd: torch.Tensor, num_bins: int) -> torch.Tensor:
     """Per-feature quantile edges [F, num_bins - 1] (the torch.quantile call of
     warpgbm/core.py:529-534), by radix selection on the device
