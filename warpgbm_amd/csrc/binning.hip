@@ -63,9 +63,14 @@ __device__ inline int count_le(const float* e, int ne, float v) {
 // batched binner: X [n, F] row-major float32 (row stride xs floats) ->
 //   codes_rm [n, S] (native; the binner's codes are in [0, n_edges] and
 //   num_bins = n_edges + 1) and, if non-null, codes_cm [F, n].
-// workgroup: 64 rows x 64 features; edges of its 64 features staged in LDS.
+// workgroup: 64 features x BT_R rows; the edges of its 64 features staged in
+// LDS once.  Lane l of every wave owns feature f0 + l (coalesced 256-byte row
+// loads, 64-byte code stores); each thread issues the loads of 8 rows before
+// it searches them, so several rows are in flight.  The column-major copy is
+// transposed through LDS and written as BT_R-byte runs per feature.
 // ---------------------------------------------------------------------------
-constexpr int BT_R = 64, BT_F = 64;
+constexpr int BT_F = kBinTileFeats, BT_R = kBinTileRows, BT_U = 8;
+static_assert(BT_F == 64 && BT_R == 256, "lane = feature, thread = row of the transposed copy");
 
 __global__ __launch_bounds__(256) void bin_matrix_kernel(
     const float* __restrict__ X, int64_t n, int32_t F, int64_t xs,
@@ -82,29 +87,34 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
     sedge[i] = f < F ? edges[(int64_t)f * n_edges + (i - fl * n_edges)] : 0.0f;
   }
   __syncthreads();
-  // each thread: feature column fl = tid & 63, rows (tid >> 6) + 4k
   const int fl = tid & 63;
+  const int rq = tid >> 6;  // rows rq, rq + 4, ... of the tile
   const int f = f0 + fl;
+  const float* e = sedge + fl * n_edges;
   const int8_t pad = (int8_t)(n_edges + 2);  // num_bins + 1
-  for (int k = tid >> 6; k < BT_R; k += 4) {
-    const int64_t r = r0 + k;
-    int8_t c = pad;
-    if (r < n && f < F) {
-      const float v = X[r * xs + f];
-      c = (int8_t)count_le(sedge + fl * n_edges, n_edges, v);
+  for (int k0 = 0; k0 < BT_R; k0 += 4 * BT_U) {
+    float v[BT_U];
+#pragma unroll
+    for (int u = 0; u < BT_U; ++u) {
+      const int64_t r = r0 + k0 + rq + 4 * u;
+      v[u] = (r < n && f < F) ? X[r * xs + f] : 0.0f;
     }
-    tcode[fl][k] = c;
-    if (r < n && f < S) codes_rm[r * S + f] = c;
+#pragma unroll
+    for (int u = 0; u < BT_U; ++u) {
+      const int k = k0 + rq + 4 * u;
+      const int64_t r = r0 + k;
+      const int8_t c = f < F ? (int8_t)count_le(e, n_edges, v[u]) : pad;
+      tcode[fl][k] = c;
+      if (r < n && f < S) codes_rm[r * S + f] = c;
+    }
   }
+  if (!codes_cm) return;  // uniform over the workgroup
   __syncthreads();
-  if (codes_cm) {
-    // column-major: thread writes rows (tid & 63) of features (tid >> 6) + 4k
-    const int rl = tid & 63;
-    const int64_t r = r0 + rl;
-    for (int k = tid >> 6; k < BT_F; k += 4) {
-      const int ff = f0 + k;
-      if (r < n && ff < F) codes_cm[(int64_t)ff * n + r] = tcode[k][rl];
-    }
+  // column-major: thread t writes row r0 + t of every feature of the tile
+  const int64_t r = r0 + tid;
+  if (r < n) {
+    for (int k = 0; k < BT_F && f0 + k < F; ++k)
+      codes_cm[(int64_t)(f0 + k) * n + r] = tcode[k][tid];
   }
 }
 
@@ -134,29 +144,38 @@ __global__ __launch_bounds__(256) void copy_prebinned_kernel(const int8_t* __res
   const int f0 = blockIdx.y * BT_F;
   const int tid = threadIdx.x;
   const int fl = tid & 63;
+  const int rq = tid >> 6;  // rows rq, rq + 4, ... of the tile
   const int f = f0 + fl;
   int hit = 0;
   const int8_t neg = (int8_t)num_bins, over_b = (int8_t)(num_bins + 1);
-  for (int k = tid >> 6; k < BT_R; k += 4) {
-    const int64_t r = r0 + k;
-    int8_t c = 0, nat = over_b;  // padding columns: num_bins + 1
-    if (r < n && f < F) {
-      c = X[r * xs + f];
-      hit |= (int)c >= num_bins;
-      nat = c < 0 ? neg : ((int)c >= num_bins ? over_b : c);
+  for (int k0 = 0; k0 < BT_R; k0 += 4 * BT_U) {
+    int8_t c[BT_U];
+#pragma unroll
+    for (int u = 0; u < BT_U; ++u) {
+      const int64_t r = r0 + k0 + rq + 4 * u;
+      c[u] = (r < n && f < F) ? X[r * xs + f] : (int8_t)0;
     }
-    tcode[fl][k] = c;
-    if (r < n && f < S) codes_rm[r * S + f] = nat;
+#pragma unroll
+    for (int u = 0; u < BT_U; ++u) {
+      const int k = k0 + rq + 4 * u;
+      const int64_t r = r0 + k;
+      int8_t nat = over_b;  // padding columns: num_bins + 1
+      if (r < n && f < F) {
+        hit |= (int)c[u] >= num_bins;
+        nat = c[u] < 0 ? neg : ((int)c[u] >= num_bins ? over_b : c[u]);
+      }
+      tcode[fl][k] = c[u];
+      if (r < n && f < S) codes_rm[r * S + f] = nat;
+    }
   }
   if (over && __syncthreads_or(hit) && tid == 0) over[0] = 1;
+  if (!codes_cm) return;  // uniform over the workgroup
   __syncthreads();
-  if (codes_cm) {
-    const int rl = tid & 63;
-    const int64_t r = r0 + rl;
-    for (int k = tid >> 6; k < BT_F; k += 4) {
-      const int ff = f0 + k;
-      if (r < n && ff < F) codes_cm[(int64_t)ff * n + r] = tcode[k][rl];
-    }
+  // column-major raw codes: thread t writes row r0 + t of every feature
+  const int64_t r = r0 + tid;
+  if (r < n) {
+    for (int k = 0; k < BT_F && f0 + k < F; ++k)
+      codes_cm[(int64_t)(f0 + k) * n + r] = tcode[k][tid];
   }
 }
 

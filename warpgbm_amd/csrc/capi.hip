@@ -283,11 +283,11 @@ int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride
   if (n == 0) return 0;
   WGBM_REQUIRE(X && codes_rm && (n_edges == 0 || edges), "null pointer");
   const size_t lds = sizeof(float) * 64 * std::max(n_edges, 1);
-  dim3 grid(nblocks(n, 64), nblocks(n_feats, 64));
+  dim3 grid(nblocks(n, kBinTileRows), nblocks(n_feats, kBinTileFeats));
   hipLaunchKernelGGL(bin_matrix_kernel, grid, dim3(256), lds, S(stream), X, n, n_feats, x_stride,
                      edges, n_edges, codes_rm, codes_stride, codes_cm);
   WGBM_LAUNCH_CHECK();
-  const int64_t covered = (int64_t)grid.y * 64;
+  const int64_t covered = (int64_t)grid.y * kBinTileFeats;
   if (codes_stride > covered) {
     const int64_t tot = n * (codes_stride - covered);
     hipLaunchKernelGGL(pad_codes_kernel, dim3(nblocks(tot, 256)), dim3(256), 0, S(stream),
@@ -309,11 +309,11 @@ int wgbm_copy_prebinned(const int8_t* X, int64_t n, int32_t n_feats, int64_t x_s
   }
   if (n == 0) return 0;
   WGBM_REQUIRE(X && codes_rm, "null pointer");
-  dim3 grid(nblocks(n, 64), nblocks(n_feats, 64));
+  dim3 grid(nblocks(n, kBinTileRows), nblocks(n_feats, kBinTileFeats));
   hipLaunchKernelGGL(copy_prebinned_kernel, grid, dim3(256), 0, S(stream), X, n, n_feats,
                      x_stride, codes_rm, codes_stride, codes_cm, num_bins, over_flag);
   WGBM_LAUNCH_CHECK();
-  const int64_t covered = (int64_t)grid.y * 64;
+  const int64_t covered = (int64_t)grid.y * kBinTileFeats;
   if (codes_stride > covered) {
     const int64_t tot = n * (codes_stride - covered);
     hipLaunchKernelGGL(pad_codes_kernel, dim3(nblocks(tot, 256)), dim3(256), 0, S(stream),
