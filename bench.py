@@ -20,6 +20,9 @@ Metric: histogram GB/s (% HBM peak) + train/infer seconds,
 * train_s / infer_s: end-to-end fit / predict wall seconds on config C3
   (1M x 1000 float32 features, 100 trees, depth 5, 32 bins, lr 0.01; predict
   on 1M held-out rows), including host->device copies and binning.
+* kernels: achieved HBM bandwidth of quantile edges, binning and inference on
+  C3's held-out matrix resident on the device (algorithmic bytes / median
+  call time).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
 """
@@ -260,6 +263,8 @@ def main():
                "heldout_corr": round(corr, 4), "e2e_workload": f"C3 {n}x{F}, {args.e2e_trees} trees"}
         print(f"[bench] C3 train {train_s:.2f} s, infer {infer_s:.2f} s, corr {corr:.4f}",
               file=sys.stderr, flush=True)
+        e2e["kernels"] = c3_kernel_rooflines(m, Xt)
+        del Xt
 
     # HBM bytes per hist_tiles launch from the committed rocprofv3 PMC summary
     # (FETCH_SIZE / WRITE_SIZE runs of this same workload, scaled by a copy of
@@ -302,6 +307,59 @@ def main():
     for cfg in [c for c in args.extra.split(",") if c]:
         out.update(run_extra(cfg))
     print(json.dumps(out))
+
+
+def c3_kernel_rooflines(m, Xt):
+    """Achieved HBM bandwidth of the other three operators on C3's held-out
+    matrix (1M x 1000 float32, resident on the device): quantile edges,
+    binning, and inference of the fitted 100 trees.  Each is timed with torch
+    events on the current stream (the stream the library launches on), median
+    of 5 calls after one warm-up; bytes are the algorithmic ones (every input
+    byte read once, every output byte written once)."""
+    import torch
+
+    from warpgbm_amd import device as D
+
+    dev = torch.device("cuda:0")
+    Xd = D.upload_float(Xt, dev)
+    n, F = Xd.shape
+    B = m.num_bins
+
+    def timed(fn):
+        fn()
+        ts = []
+        for _ in range(5):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return sorted(ts)[2]
+
+    out = {}
+
+    def put(name, ms, nbytes, what):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 4), "bytes": int(nbytes), "GB/s": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_are": what}
+
+    edges = D.quantile_edges(Xd, B)
+    put("quantile_edges", timed(lambda: D.quantile_edges(Xd, B)), n * F * 4 + F * (B - 1) * 4,
+        "X read once + edges (the selection reads X in 4 radix passes)")
+    put("bin_matrix", timed(lambda: D.bin_matrix(Xd, edges, with_cm=False)),
+        n * F * 4 + n * F + F * (B - 1) * 4, "X + codes (row-major) + edges")
+    codes = D.bin_matrix(Xd, edges, with_cm=False)
+    del Xd
+    feat, bin_, leaf, nt = m._cached_heap()
+    pred = torch.zeros((n, 1), dtype=torch.float32, device=dev)
+    put("predict_heap", timed(lambda: D.predict_heap(codes, feat, bin_, leaf, nt, 1, m.max_depth,
+                                                       m.learning_rate, pred)),
+        n * F + 8 * n, "codes + predictions read and written (tables are in LDS)")
+    for k, v in out.items():
+        print(f"[bench] {k}: {v['ms']:.3f} ms, {v['GB/s']:.0f} GB/s ({100 * v['frac']:.1f}% of HBM)",
+              file=sys.stderr, flush=True)
+    return out
 
 
 def run_extra(cfg):
