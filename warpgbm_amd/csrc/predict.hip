@@ -93,7 +93,7 @@ __global__ void predict_heap_kernel(const int8_t* __restrict__ codes, int64_t n,
 // of K, so tree t0 + j belongs to class j % K.
 //   LDS: rows [RB][S + 4] bytes (a 4-byte pad per row spreads the rows of
 //   one wave over the banks), nodes [TC][H] (feature << 8 | bin, or ~0 for a
-//   leaf), leaves [TC][H], vals [RB][TC].
+//   leaf), leaves [TC][H], vals [RB][TC + 1] (odd row stride: no bank conflicts).
 constexpr int kPredThreads = 1024;
 constexpr int kPredMaxAcc = 4;  // (row, class) accumulators per thread
 constexpr uint32_t kPredLeaf = 0xffffffffu;
@@ -147,23 +147,38 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
       leaves_s[i] = leaf[g];
     }
     __syncthreads();
-    // walks: pair p = (row p % RB, tree p / RB) of the chunk
-    for (int p = tid; p < RB * tc; p += kPredThreads) {
-      const int r = p % RB, tl = p / RB;
-      if (r >= nr) continue;
-      const uint32_t* nd = nodes_s + tl * H;
-      const uint8_t* row = rows_s + r * Sp;
-      int h = 0;
-      uint32_t w = nd[0];
-      for (int d = 0; d < max_depth; ++d) {
-        if (w == kPredLeaf) break;
-        const uint32_t f = w >> 8;
-        const int c = (int)row[f < (uint32_t)S ? f : (uint32_t)S - 1];  // stays in the row
-        const int b = (int)(w & 0xffu);
-        h = 2 * h + ((c <= b || c == num_bins) ? 1 : 2);
-        w = nd[h];
+    // walks: pair p = (row p % RB, tree p / RB) of the chunk; each thread
+    // advances two walks (p and p + kPredThreads) step by step, so the LDS
+    // reads of one walk overlap those of the other
+    for (int p0 = tid; p0 < RB * tc; p0 += 2 * kPredThreads) {
+      int r[2], tl[2], h[2];
+      bool on[2];
+      uint32_t w[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int p = p0 + k * kPredThreads;
+        r[k] = p % RB;
+        tl[k] = p / RB;
+        on[k] = p < RB * tc && r[k] < nr;
+        h[k] = 0;
+        w[k] = on[k] ? nodes_s[tl[k] * H] : kPredLeaf;
       }
-      vals_s[r * TC + tl] = lr * leaves_s[tl * H + h];
+      for (int d = 0; d < max_depth; ++d) {
+        if (w[0] == kPredLeaf && w[1] == kPredLeaf) break;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          if (w[k] == kPredLeaf) continue;
+          const uint32_t f = w[k] >> 8;
+          const uint8_t* row = rows_s + r[k] * Sp;
+          const int c = (int)row[f < (uint32_t)S ? f : (uint32_t)S - 1];  // stays in the row
+          const int b = (int)(w[k] & 0xffu);
+          h[k] = 2 * h[k] + ((c <= b || c == num_bins) ? 1 : 2);
+          w[k] = nodes_s[tl[k] * H + h[k]];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (on[k]) vals_s[r[k] * (TC + 1) + tl[k]] = lr * leaves_s[tl[k] * H + h[k]];
     }
     __syncthreads();
     // ordered sums: trees t0 + j of class k are j = k, k + K, ... (t0 % K == 0)
@@ -173,7 +188,7 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
       const int r = p % RB, k = p / RB;
       if (k < K && r < nr) {
         float a = acc[m];
-        for (int j = k; j < tc; j += K) a = a + vals_s[r * TC + j];
+        for (int j = k; j < tc; j += K) a = a + vals_s[r * (TC + 1) + j];
         acc[m] = a;
       }
     }
@@ -196,13 +211,13 @@ int predict_rows_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t
   int64_t m = std::max<int64_t>(1, (16 * 1024) / ((int64_t)8 * H * K));
   int64_t TC = std::min<int64_t>(m * K, std::max<int64_t>(K, (T + K - 1) / K * K));
   const int64_t Sp = S + 4;
-  int64_t RB = (kBudget - 8 * TC * H) / (Sp + 4 * TC);
+  int64_t RB = (kBudget - 8 * TC * H) / (Sp + 4 * (TC + 1));
   RB = std::min<int64_t>(RB, 256);
   RB = std::min<int64_t>(RB, (int64_t)kPredMaxAcc * kPredThreads / K);
   if (RB < 16) return 0;
   *RB_out = (int32_t)RB;
   *TC_out = (int32_t)TC;
-  *lds_out = (size_t)(RB * Sp + 8 * TC * H + 4 * RB * TC);
+  *lds_out = (size_t)(RB * Sp + 8 * TC * H + 4 * RB * (TC + 1));
   return 1;
 }
 
