@@ -315,6 +315,40 @@ def test_native_quantile_selection_bit_exact(gpu, B):
         assert np.array_equal(bits(got2[:5]), bits(ref[:5])), n
 
 
+@pytest.mark.parametrize("B", [5, 32, 127])
+def test_quantile_selection_value_buckets_bit_exact(gpu, B):
+    """Columns large enough for the value-bucket first pass: smooth data (the
+    target buckets go to the buffer), heavy ties and outliers that stretch
+    the range (the buffer would overflow: radix over the whole column),
+    infinities, a constant -0.0 column and a NaN column; all equal the
+    oracle, and torch.quantile where no signed zero is involved."""
+    print_case("quantile_edges value buckets", B)
+    rng = np.random.default_rng(100 + B)
+    n = 300_001
+    X = np.empty((n, 9), F32)
+    X[:, 0] = rng.standard_normal(n)
+    X[:, 1] = rng.uniform(1.0, 2.0, n)
+    X[:, 2] = rng.integers(0, 4, n)                  # heavy ties
+    X[:, 3] = rng.standard_normal(n)
+    X[7, 3] = 1e30                                   # outlier stretches the range
+    X[:, 4] = rng.standard_normal(n)
+    X[11, 4] = np.inf
+    X[:, 5] = rng.standard_normal(n)
+    X[13, 5] = -np.inf
+    X[:, 6] = rng.exponential(1.0, n) ** 3           # heavy tail
+    X[:, 7] = -0.0                                   # constant negative zero
+    X[:, 8] = rng.standard_normal(n)
+    X[n // 3, 8] = np.nan
+    Xd = D.upload_float(X, dev)
+    got = D.quantile_edges(Xd, B).cpu().numpy()
+    ref = ops.quantile_edges(X, B)
+    assert np.array_equal(bits(got), bits(ref))
+    cols = [0, 1, 3, 4, 5, 6]
+    tq = torch.quantile(torch.from_numpy(X[:, cols]), torch.from_numpy(ops.quantile_levels(B)),
+                        dim=0).numpy().T
+    assert np.array_equal(bits(got[cols]), bits(tq))
+
+
 def test_staged_upload_exact(gpu):
     """The pinned, multi-threaded upload reproduces X (float64 input rounded
     to float32) exactly, including a ragged last chunk."""

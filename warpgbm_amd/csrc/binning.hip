@@ -227,146 +227,337 @@ __device__ inline float key_to_float(uint32_t k) {
   return __uint_as_float(u);
 }
 
-// X [n, F] float32 (row stride xs) -> keys [F, n]; 64 x 64 tiles through LDS
+// X [n, F] float32 (row stride xs) -> keys [F, n]: a workgroup moves 64
+// features x kTransRows rows in 64 x 64 tiles through LDS, and keeps the
+// smallest and largest key of each of its features (a NaN key is the
+// largest), merged into kmin / kmax [F] with one atomic per feature.
 __global__ __launch_bounds__(256) void transpose_keys_kernel(const float* __restrict__ X,
                                                              int64_t n, int32_t F, int64_t xs,
-                                                             uint32_t* __restrict__ keys) {
+                                                             uint32_t* __restrict__ keys,
+                                                             uint32_t* __restrict__ kmin,
+                                                             uint32_t* __restrict__ kmax) {
   __shared__ uint32_t t[64][65];
-  const int64_t r0 = (int64_t)blockIdx.x * 64;
+  __shared__ uint32_t s_mn[4][64], s_mx[4][64];
   const int f0 = blockIdx.y * 64;
   const int c = threadIdx.x & 63;
-  for (int k = threadIdx.x >> 6; k < 64; k += 4) {
-    const int64_t r = r0 + k;
-    t[k][c] = (r < n && f0 + c < F) ? float_to_key(X[r * xs + f0 + c]) : 0u;
+  const int rq = threadIdx.x >> 6;
+  uint32_t mn = 0xffffffffu, mx = 0u;
+  for (int64_t r0 = (int64_t)blockIdx.x * kTransRows;
+       r0 < n && r0 < (int64_t)(blockIdx.x + 1) * kTransRows; r0 += 64) {
+    __syncthreads();  // the previous tile has been written out
+    for (int k = rq; k < 64; k += 4) {
+      const int64_t r = r0 + k;
+      uint32_t key = 0u;
+      if (r < n && f0 + c < F) {
+        key = float_to_key(X[r * xs + f0 + c]);
+        mn = key < mn ? key : mn;
+        mx = key > mx ? key : mx;
+      }
+      t[k][c] = key;
+    }
+    __syncthreads();
+    for (int k = rq; k < 64; k += 4) {
+      const int f = f0 + k;
+      const int64_t r = r0 + c;
+      if (f < F && r < n) keys[(int64_t)f * n + r] = t[c][k];
+    }
   }
+  s_mn[rq][c] = mn;
+  s_mx[rq][c] = mx;
   __syncthreads();
-  for (int k = threadIdx.x >> 6; k < 64; k += 4) {
-    const int f = f0 + k;
-    const int64_t r = r0 + c;
-    if (f < F && r < n) keys[(int64_t)f * n + r] = t[c][k];
+  if (threadIdx.x < 64 && f0 + c < F) {
+    for (int w = 1; w < 4; ++w) {
+      mn = s_mn[w][c] < mn ? s_mn[w][c] : mn;
+      mx = s_mx[w][c] > mx ? s_mx[w][c] : mx;
+    }
+    atomicMin(&kmin[f0 + c], mn);
+    atomicMax(&kmax[f0 + c], mx);
   }
 }
 
-constexpr int kSelThreads = 1024;
+constexpr int kSelThreads = 512;
 constexpr int kSelMaxTargets = 256;   // 2 * 126 ranks at most (num_bins <= 127)
-constexpr int kSelGroup = 48;         // distinct prefixes histogrammed per column pass
+constexpr int kSelGroup = 32;         // distinct prefixes histogrammed per scan
+constexpr int kSelBuckets = 4096;     // value buckets of the first pass
 
+// One workgroup per feature (512 threads, ~37 KB of LDS: four per CU, so a
+// 1000-feature matrix runs in one round).  The order statistics at ranks
+// floor / ceil(q (n-1)) are found in two scans of the column plus work on a
+// small buffer:
+//   1. histogram of kSelBuckets equal-width value buckets between the
+//      column's smallest and largest value (monotone in the value, so each
+//      bucket is a contiguous run of the sorted column);
+//   2. the keys of the buckets that hold a target rank are copied to a
+//      per-feature buffer (the whole buckets, so a target's rank inside the
+//      buffer is the buffer keys of lower buckets plus its rank inside its
+//      bucket);
+//   3. radix selection (four byte passes) over the buffer.
+// A column whose target buckets exceed the buffer (heavy ties, outliers that
+// stretch the range, infinities) runs the radix selection over the whole
+// column instead; a column holding a NaN gets NaN edges (torch.quantile) and
+// a constant column its value.
 __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
     const uint32_t* __restrict__ keys, int64_t n, int32_t F, const float* __restrict__ q,
-    int32_t nq, float* __restrict__ edges) {
-  __shared__ uint32_t hist[kSelGroup][256];        // 48 KB
+    int32_t nq, float* __restrict__ edges, const uint32_t* __restrict__ kmin,
+    const uint32_t* __restrict__ kmax, uint32_t* __restrict__ cbuf, int64_t ccap) {
+  __shared__ uint32_t hist[kSelGroup][256];        // 32 KB (also the value buckets)
   __shared__ uint32_t tprefix[kSelMaxTargets];      // known key bits of each target
   __shared__ int64_t trank[kSelMaxTargets];         // rank still to find within the prefix
   __shared__ uint32_t dist[kSelMaxTargets];         // distinct prefixes of this pass (sorted)
-  __shared__ int s_nd, s_nan;
+  __shared__ uint32_t tbucket[kSelMaxTargets];      // value bucket of each target
+  __shared__ uint32_t tfirst[kSelMaxTargets];       // first occurrence of its prefix
+  __shared__ uint32_t marked[kSelBuckets / 32];     // buckets copied to the buffer
+  __shared__ uint32_t wsum[kSelThreads / 64];
+  __shared__ int s_nd;
+  __shared__ uint32_t s_tot;
+  __shared__ uint32_t s_cnt;
+  constexpr int nwaves = kSelThreads / 64;
   const int f = blockIdx.x;
   if (f >= F) return;
   const uint32_t* col = keys + (int64_t)f * n;
+  uint32_t* cb = cbuf + (int64_t)f * ccap;
   const int nt = 2 * nq;
   const int64_t last = n - 1;
-  for (int t = threadIdx.x; t < nt; t += kSelThreads) {
-    const float rank = q[t >> 1] * (float)last;
-    int64_t r = (t & 1) ? (int64_t)ceilf(rank) : (int64_t)rank;
-    r = r < 0 ? 0 : (r > last ? last : r);
-    trank[t] = r;
-    tprefix[t] = 0;
-  }
-  if (threadIdx.x == 0) s_nan = 0;
-  // pass 1: histogram of the top byte (per-wave copies in hist rows 0..15)
-  for (int i = threadIdx.x; i < 16 * 256; i += kSelThreads) (&hist[0][0])[i] = 0;
-  __syncthreads();
-  {
-    const int w = threadIdx.x >> 6;
-    int nan_local = 0;
-    for (int64_t i = threadIdx.x; i < n; i += kSelThreads) {
-      const uint32_t k = col[i];
-      nan_local += k == 0xffffffffu;
-      atomicAdd(&hist[w][k >> 24], 1u);
-    }
-    if (nan_local) atomicAdd(&s_nan, nan_local);
-  }
-  __syncthreads();
-  if (s_nan) {  // torch.quantile: a NaN anywhere makes every quantile NaN
-    for (int j = threadIdx.x; j < nq; j += kSelThreads)
-      edges[(int64_t)f * nq + j] = __builtin_nanf("");
+  const int tid = threadIdx.x;
+  const uint32_t kmn = kmin[f], kmx = kmax[f];
+  float* out = edges + (int64_t)f * nq;
+  if (kmx == 0xffffffffu) {  // a NaN anywhere makes every quantile NaN
+    for (int j = tid; j < nq; j += kSelThreads) out[j] = __builtin_nanf("");
     return;
   }
-  for (int b = threadIdx.x; b < 256; b += kSelThreads) {
-    uint32_t s = 0;
-    for (int w = 0; w < 16; ++w) s += hist[w][b];
-    hist[16][b] = s;
-  }
-  __syncthreads();
-  for (int t = threadIdx.x; t < nt; t += kSelThreads) {
-    int64_t r = trank[t];
-    int b = 0;
-    while (r >= (int64_t)hist[16][b]) r -= hist[16][b++];
-    tprefix[t] = (uint32_t)b;
-    trank[t] = r;
-  }
-  __syncthreads();
-  // passes 2..4: next byte of the keys that share a target's prefix
-  for (int pass = 1; pass < 4; ++pass) {
-    const int sh = 32 - 8 * pass;  // prefix = key >> sh
-    if (threadIdx.x == 0) {
-      // sorted distinct prefixes (insertion sort of <= 252 values)
-      int nd = 0;
-      for (int t = 0; t < nt; ++t) {
-        const uint32_t v = tprefix[t];
-        int pos = nd;
-        while (pos > 0 && dist[pos - 1] > v) --pos;
-        if (pos > 0 && dist[pos - 1] == v) continue;
-        for (int m = nd; m > pos; --m) dist[m] = dist[m - 1];
-        dist[pos] = v;
-        ++nd;
+  // a constant column: every order statistic is its value (interpolated
+  // below like any other, which fixes the sign of a zero as torch does)
+  const bool constant = kmn == kmx;
+  for (int t = tid; t < nt; t += kSelThreads) tprefix[t] = kmn;
+  if (!constant) {
+    for (int t = tid; t < nt; t += kSelThreads) {
+      const float rank = q[t >> 1] * (float)last;
+      int64_t r = (t & 1) ? (int64_t)ceilf(rank) : (int64_t)rank;
+      r = r < 0 ? 0 : (r > last ? last : r);
+      trank[t] = r;
+      tprefix[t] = 0;
+    }
+    // ---- value buckets
+    const float lo = key_to_float(kmn), hi = key_to_float(kmx);
+    const float scale = (float)kSelBuckets / (hi - lo);
+    auto bucket = [&](uint32_t k) -> int {
+      // non-decreasing in the value; inf / NaN intermediates fall into bucket 0
+      const float v = (key_to_float(k) - lo) * scale;
+      return v >= (float)(kSelBuckets - 1) ? kSelBuckets - 1 : (v > 0.0f ? (int)v : 0);
+    };
+    uint32_t* H = &hist[0][0];  // [kSelBuckets]
+    for (int i = tid; i < kSelBuckets; i += kSelThreads) H[i] = 0;
+    for (int i = tid; i < kSelBuckets / 32; i += kSelThreads) marked[i] = 0;
+    if (tid == 0) s_cnt = 0;
+    __syncthreads();
+    // four independent loads in flight per thread
+    for (int64_t i0 = tid; i0 < n; i0 += 4 * kSelThreads) {
+      uint32_t k[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t i = i0 + u * kSelThreads;
+        k[u] = i < n ? col[i] : 0u;
       }
-      s_nd = nd;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (i0 + u * kSelThreads < n) atomicAdd(&H[bucket(k[u])], 1u);
     }
     __syncthreads();
-    const int nd = s_nd;
-    for (int g0 = 0; g0 < nd; g0 += kSelGroup) {
-      const int gn = nd - g0 < kSelGroup ? nd - g0 : kSelGroup;
-      for (int i = threadIdx.x; i < gn * 256; i += kSelThreads) (&hist[0][0])[i] = 0;
+    // exclusive prefix of the buckets, in place: thread t owns buckets
+    // [8t, 8t + 8)
+    constexpr int per = kSelBuckets / kSelThreads;
+    static_assert(per * kSelThreads == kSelBuckets, "buckets per thread");
+    auto block_exclusive_scan = [&](uint32_t* a) {
+      uint32_t v[per], sum = 0;
+#pragma unroll
+      for (int k = 0; k < per; ++k) {
+        v[k] = a[tid * per + k];
+        sum += v[k];
+      }
+      const int lane = tid & 63, w = tid >> 6;
+      uint32_t inc = sum;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += y;
+      }
+      if (lane == 63) wsum[w] = inc;
       __syncthreads();
-      const uint32_t lo_p = dist[g0], hi_p = dist[g0 + gn - 1];
-      for (int64_t i = threadIdx.x; i < n; i += kSelThreads) {
-        const uint32_t k = col[i];
-        const uint32_t pre = k >> sh;
-        if (pre < lo_p || pre > hi_p) continue;
-        int lo = g0, hi = g0 + gn - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (dist[mid] < pre) lo = mid + 1; else hi = mid;
-        }
-        if (dist[lo] == pre) atomicAdd(&hist[lo - g0][(k >> (sh - 8)) & 255u], 1u);
+      uint32_t base = inc - sum;
+      for (int k = 0; k < w; ++k) base += wsum[k];
+#pragma unroll
+      for (int k = 0; k < per; ++k) {
+        a[tid * per + k] = base;
+        base += v[k];
       }
       __syncthreads();
-      for (int t = threadIdx.x; t < nt; t += kSelThreads) {
-        int lo = g0, hi = g0 + gn - 1;
-        const uint32_t pre = tprefix[t];
-        if (pre < dist[g0] || pre > dist[g0 + gn - 1]) continue;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (dist[mid] < pre) lo = mid + 1; else hi = mid;
+    };
+    // sizes are needed again below: keep them in the buffer-rank scan's input
+    uint32_t* C = H;  // exclusive prefix (C[b] = keys in buckets < b)
+    uint32_t sz[per];
+#pragma unroll
+    for (int k = 0; k < per; ++k) sz[k] = H[tid * per + k];
+    block_exclusive_scan(C);
+    // bucket of every target (last bucket b with C[b] <= rank)
+    for (int t = tid; t < nt; t += kSelThreads) {
+      const int64_t r = trank[t];
+      int a = 0, b = kSelBuckets - 1;
+      while (a < b) {
+        const int m = (a + b + 1) >> 1;
+        if ((int64_t)C[m] <= r) a = m; else b = m - 1;
+      }
+      tbucket[t] = (uint32_t)a;
+      atomicOr(&marked[a >> 5], 1u << (a & 31));
+    }
+    __syncthreads();
+    // buffer ranks: keys of marked buckets below the target's bucket + rank
+    // inside the bucket (M = exclusive prefix of the marked buckets' sizes)
+    {
+      uint32_t* M = &hist[16][0];  // [kSelBuckets] words after C
+#pragma unroll
+      for (int k = 0; k < per; ++k) {
+        const int b = tid * per + k;
+        M[b] = ((marked[b >> 5] >> (b & 31)) & 1u) ? sz[k] : 0u;
+      }
+      __syncthreads();
+      if (tid == kSelThreads - 1) {
+        uint32_t tl = 0;
+        for (int k = 0; k < per; ++k) tl += M[tid * per + k];
+        s_tot = tl;  // completed by the scan below
+      }
+      __syncthreads();
+      block_exclusive_scan(M);
+      if (tid == kSelThreads - 1) s_tot += M[kSelBuckets - per];
+      __syncthreads();
+      if ((int64_t)s_tot <= ccap) {
+        for (int t = tid; t < nt; t += kSelThreads) {
+          const int b = (int)tbucket[t];
+          trank[t] = (int64_t)M[b] + (trank[t] - (int64_t)C[b]);
         }
-        int64_t r = trank[t];
-        int b = 0;
-        while (b < 255 && r >= (int64_t)hist[lo - g0][b]) r -= hist[lo - g0][b++];
-        tprefix[t] = (pre << 8) | (uint32_t)b;
-        trank[t] = r;
       }
       __syncthreads();
     }
-  }
+    const uint32_t* src = col;  // the keys the radix selection scans
+    int64_t ns = n;
+    if ((int64_t)s_tot <= ccap) {
+      // one buffer reservation per wave: a ballot of the lanes that keep
+      // their key, lane ranks by mbcnt
+      const int lane = tid & 63;
+      for (int64_t i0 = 0; i0 < n; i0 += kSelThreads) {  // same trip count for all
+        const int64_t i = i0 + tid;
+        uint32_t k = 0u;
+        bool take = false;
+        if (i < n) {
+          k = col[i];
+          const int b = bucket(k);
+          take = (marked[b >> 5] >> (b & 31)) & 1u;
+        }
+        const uint64_t m = __ballot(take);
+        if (m) {
+          const int first = __builtin_ctzll(m);
+          uint32_t base = 0;
+          if (lane == first) base = atomicAdd(&s_cnt, (uint32_t)__builtin_popcountll(m));
+          base = __shfl(base, first, 64);
+          const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
+              (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+          if (take) cb[base + rank] = k;  // base + rank < s_tot <= ccap
+        }
+      }
+      __syncthreads();
+      src = cb;
+      ns = (int64_t)s_tot;
+    }
+    // ---- radix selection over src (ranks in trank are ranks within src)
+    for (int i = tid; i < nwaves * 256; i += kSelThreads) (&hist[0][0])[i] = 0;
+    __syncthreads();
+    {
+      const int w = tid >> 6;
+      for (int64_t i = tid; i < ns; i += kSelThreads) atomicAdd(&hist[w][src[i] >> 24], 1u);
+    }
+    __syncthreads();
+    for (int b = tid; b < 256; b += kSelThreads) {
+      uint32_t sum = 0;
+      for (int w = 0; w < nwaves; ++w) sum += hist[w][b];
+      hist[nwaves][b] = sum;
+    }
+    __syncthreads();
+    for (int t = tid; t < nt; t += kSelThreads) {
+      int64_t r = trank[t];
+      int b = 0;
+      while (r >= (int64_t)hist[nwaves][b]) r -= hist[nwaves][b++];
+      tprefix[t] = (uint32_t)b;
+      trank[t] = r;
+    }
+    __syncthreads();
+    // index of prefix pre in the sorted dist[lo..hi] (or where it would be)
+    auto find = [&](uint32_t pre, int a, int b) {
+      while (a < b) {
+        const int mid = (a + b) >> 1;
+        if (dist[mid] < pre) a = mid + 1; else b = mid;
+      }
+      return a;
+    };
+    // passes 2..4: next byte of the keys that share a target's prefix
+    for (int pass = 1; pass < 4; ++pass) {
+      const int sh = 32 - 8 * pass;  // prefix = key >> sh
+      // sorted distinct prefixes, in parallel (a serial sort on one thread
+      // waits on every LDS access behind the other waves' atomics): thread
+      // t marks whether it holds the first occurrence of its value, then a
+      // first occurrence stores its value at the count of distinct values
+      // below it
+      if (tid == 0) s_nd = 0;
+      if (tid < nt) {
+        const uint32_t v = tprefix[tid];
+        bool first = true;
+        for (int u = 0; u < tid; ++u) first = first && tprefix[u] != v;
+        tfirst[tid] = first ? 1u : 0u;
+      }
+      __syncthreads();
+      if (tid < nt && tfirst[tid]) {
+        const uint32_t v = tprefix[tid];
+        int below = 0;
+        for (int u = 0; u < nt; ++u) below += (tfirst[u] && tprefix[u] < v) ? 1 : 0;
+        dist[below] = v;
+        atomicAdd(&s_nd, 1);
+      }
+      __syncthreads();
+      const int nd = s_nd;
+      for (int g0 = 0; g0 < nd; g0 += kSelGroup) {
+        const int gn = nd - g0 < kSelGroup ? nd - g0 : kSelGroup;
+        for (int i = tid; i < gn * 256; i += kSelThreads) (&hist[0][0])[i] = 0;
+        __syncthreads();
+        const uint32_t lo_p = dist[g0], hi_p = dist[g0 + gn - 1];
+        for (int64_t i = tid; i < ns; i += kSelThreads) {
+          const uint32_t k = src[i];
+          const uint32_t pre = k >> sh;
+          if (pre < lo_p || pre > hi_p) continue;
+          const int g = find(pre, g0, g0 + gn - 1);
+          if (dist[g] == pre) atomicAdd(&hist[g - g0][(k >> (sh - 8)) & 255u], 1u);
+        }
+        __syncthreads();
+        for (int t = tid; t < nt; t += kSelThreads) {
+          const uint32_t pre = tprefix[t];
+          if (pre < dist[g0] || pre > dist[g0 + gn - 1]) continue;
+          const int g = find(pre, g0, g0 + gn - 1);
+          int64_t r = trank[t];
+          int b = 0;
+          while (b < 255 && r >= (int64_t)hist[g - g0][b]) r -= hist[g - g0][b++];
+          tprefix[t] = (pre << 8) | (uint32_t)b;
+          trank[t] = r;
+        }
+        __syncthreads();
+      }
+    }
+  }  // !constant
+  __syncthreads();
   // interpolate (torch.quantile, linear): see quantile_edges_kernel
-  for (int j = threadIdx.x; j < nq; j += kSelThreads) {
+  for (int j = tid; j < nq; j += kSelThreads) {
     const float rank = q[j] * (float)last;
-    const int64_t lo = (int64_t)rank;
-    const float w = rank - (float)lo;
+    const int64_t lo_r = (int64_t)rank;
+    const float w = rank - (float)lo_r;
     const float a = key_to_float(tprefix[2 * j]);
     const float b = key_to_float(tprefix[2 * j + 1]);
     const float d = b - a;
-    edges[(int64_t)f * nq + j] = w < 0.5f ? fmaf(w, d, a) : fmaf(w - 1.0f, d, b);
+    out[j] = w < 0.5f ? fmaf(w, d, a) : fmaf(w - 1.0f, d, b);
   }
 }
 

@@ -261,14 +261,22 @@ int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64
   // one launch, so that every CU holds several columns)
   const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n_feats, (int64_t(1) << 30) / n));
   uint32_t* keys = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (size_t)(chunk * n), 8);
-  WGBM_REQUIRE(keys, "scratch allocation failed");
+  // per-feature buffer of the keys left after the 16-bit prefix pass (a
+  // quarter of the column; a column with more falls back to full scans)
+  const int64_t ccap = std::max<int64_t>(1024, n / 4);
+  uint32_t* cbuf = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (size_t)(chunk * ccap), 10);
+  uint32_t* kmm = (uint32_t*)scratch_get(st, sizeof(uint32_t) * 2 * (size_t)chunk, 11);
+  WGBM_REQUIRE(keys && cbuf && kmm, "scratch allocation failed");
+  uint32_t *kmin = kmm, *kmax = kmm + chunk;
   for (int64_t f0 = 0; f0 < n_feats; f0 += chunk) {
     const int32_t fc = (int32_t)std::min<int64_t>(chunk, n_feats - f0);
-    dim3 tg(nblocks(n, 64), nblocks(fc, 64));
-    hipLaunchKernelGGL(transpose_keys_kernel, tg, dim3(256), 0, st, X + f0, n, fc, x_stride, keys);
+    if (fill_u32(kmin, fc, 0xffffffffu, st) || fill_u32(kmax, fc, 0u, st)) return WGBM_EINVAL;
+    dim3 tg(nblocks(n, kTransRows), nblocks(fc, 64));
+    hipLaunchKernelGGL(transpose_keys_kernel, tg, dim3(256), 0, st, X + f0, n, fc, x_stride, keys,
+                       kmin, kmax);
     WGBM_LAUNCH_CHECK();
-    hipLaunchKernelGGL(quantile_select_kernel, dim3(fc), dim3(1024), 0, st, keys, n, fc, q, nq,
-                       edges + f0 * nq);
+    hipLaunchKernelGGL(quantile_select_kernel, dim3(fc), dim3(512), 0, st, keys, n, fc, q, nq,
+                       edges + f0 * nq, kmin, kmax, cbuf, ccap);
     WGBM_LAUNCH_CHECK();
   }
   return 0;

@@ -30,6 +30,8 @@ constexpr int kAuxNT = 2;
 constexpr int kAuxStream = 3;
 // tile of the binner and the pre-binned copy: rows x features per workgroup
 constexpr int kBinTileRows = 256, kBinTileFeats = 64;
+// rows per workgroup of the key transpose of the quantile selection
+constexpr int kTransRows = 1024;
 // histogram workgroups per launch the tile sizes aim for: 2 per CU in the
 // engine; 1 per CU for a single call (one 16-wave workgroup already keeps a
 // CU's LDS atomic unit busy, and half the tiles halve the partials that the
