@@ -344,7 +344,22 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
   if (n_rounds == 0) return 0;
   int32_t RB = 0, TC = 0;
   size_t lds = 0;
-  if (predict_rows_plan(codes_stride, K, H, n_rounds, &RB, &TC, &lds)) {
+  int dev = 0, n_cu = 0;
+  WGBM_CHECK(hipGetDevice(&dev));
+  WGBM_CHECK(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+  if (predict_resident_plan(codes_stride, K, H, n_rounds, &RB, &lds)) {
+    static bool attr_r = false;
+    if (!attr_r) {
+      WGBM_CHECK(hipFuncSetAttribute((const void*)predict_resident_kernel,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      attr_r = true;
+    }
+    // one persistent workgroup per CU (fewer when there are fewer blocks)
+    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(n_cu, nblocks(n, RB)));
+    hipLaunchKernelGGL(predict_resident_kernel, dim3((unsigned)grid), dim3(1024), lds, S(stream),
+                       codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds * K, K, H,
+                       max_depth, learning_rate, RB, out);
+  } else if (predict_rows_plan(codes_stride, K, H, n_rounds, &RB, &TC, &lds)) {
     static bool attr = false;
     if (!attr) {
       WGBM_CHECK(hipFuncSetAttribute((const void*)predict_rows_kernel,

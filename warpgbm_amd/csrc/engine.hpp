@@ -192,6 +192,13 @@ __global__ void predict_rows_kernel(const int8_t* codes, int64_t n, int64_t S, i
                                     float lr, int32_t RB, int32_t TC, float* out);
 int predict_rows_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
                       int32_t* TC_out, size_t* lds_out);
+__global__ void predict_resident_kernel(const int8_t* codes, int64_t n, int64_t S,
+                                        int32_t num_bins, const int32_t* feat,
+                                        const int32_t* bin, const float* leaf, int32_t T,
+                                        int32_t K, int32_t H, int32_t max_depth, float lr,
+                                        int32_t RB, float* out);
+int predict_resident_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
+                          size_t* lds_out);
 __global__ void softmax_rows_kernel(float* x, int64_t n, int32_t K);
 __global__ void importance_add_kernel(float* acc, int32_t F, int32_t E, const float* gain,
                                       const int64_t* node, const int64_t* fstart);

@@ -201,6 +201,172 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Resident-tree inference, for ensembles whose node tables fit in LDS next to
+// a row block (same results as predict_rows_kernel).  Persistent workgroups
+// (one per CU) load every tree once, then stride over blocks of RB rows:
+//   * the next block's codes are loaded into registers while the current one
+//     is walked (QPT 16-byte loads per thread), then stored to the LDS row
+//     buffer after the walks;
+//   * waves 1..15 walk the (row, tree) pairs of the block, two per thread
+//     in lock-step, and write lr * leaf to a per-block value table [RB][T + 1];
+//   * wave 0 meanwhile adds the previous block's table to `out` in tree
+//     order (one lane per (row, class)), so the ordered sums run beside the
+//     walks; the value tables alternate between two buffers.
+// ---------------------------------------------------------------------------
+constexpr int kResThreads = 1024;
+constexpr int kResMaxQ = 4;  // 16-byte row loads per thread and block
+constexpr int kResWalks = 2;  // walks a walker thread advances in lock-step
+
+__global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
+    const int8_t* __restrict__ codes, int64_t n, int64_t S, int32_t num_bins,
+    const int32_t* __restrict__ feat, const int32_t* __restrict__ bin,
+    const float* __restrict__ leaf, int32_t T, int32_t K, int32_t H, int32_t max_depth,
+    float lr, int32_t RB, float* __restrict__ out) {
+  extern __shared__ uint32_t psm[];
+  const int Sp = (int)S + 4;
+  const int TV = T + 1;  // value-table row stride (odd or even, see below)
+  uint32_t* nodes_s = psm;
+  float* leaves_s = reinterpret_cast<float*>(nodes_s + T * H);
+  uint8_t* rows_s = reinterpret_cast<uint8_t*>(leaves_s + T * H);
+  float* vals_s = reinterpret_cast<float*>(rows_s + RB * Sp);  // 2 x [RB][TV]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  for (int i = tid; i < T * H; i += kResThreads) {
+    const int f = feat[i];
+    nodes_s[i] = f < 0 ? kPredLeaf : ((uint32_t)f << 8) | (uint32_t)(bin[i] & 0xff);
+    leaves_s[i] = leaf[i];
+  }
+  const int64_t nblk = (n + RB - 1) / RB;
+  const int qpr = (int)(S / 16);  // 16-byte quads per row
+  const int nq = RB * qpr;
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  u4 pre[kResMaxQ];
+  auto prefetch = [&](int64_t b) {
+#pragma unroll
+    for (int u = 0; u < kResMaxQ; ++u) {
+      const int q = u * kResThreads + tid;
+      const int r = q / qpr, c = q - r * qpr;
+      const int64_t row = b * RB + r;
+      pre[u] = u4{0u, 0u, 0u, 0u};
+      if (q < nq && row < n)
+        pre[u] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(codes + row * S) + c);
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int u = 0; u < kResMaxQ; ++u) {
+      const int q = u * kResThreads + tid;
+      if (q < nq) {
+        const int r = q / qpr, c = q - r * qpr;
+        uint32_t* dst = reinterpret_cast<uint32_t*>(rows_s + r * Sp + c * 16);
+        dst[0] = pre[u].x;
+        dst[1] = pre[u].y;
+        dst[2] = pre[u].z;
+        dst[3] = pre[u].w;
+      }
+    }
+  };
+  // ordered sums of a finished block (wave 0): lane per (row, class)
+  auto sums = [&](int64_t b, const float* vt) {
+    const int64_t row0 = b * RB;
+    const int nr = (int)(n - row0 < RB ? n - row0 : RB);
+    for (int p = lane; p < RB * K; p += 64) {
+      const int r = p % RB, k = p / RB;
+      if (r >= nr) continue;
+      float* o = out + (row0 + r) * K + k;
+      const float* v = vt + r * TV;
+      float a = *o;
+      // tree order; eight loads issued ahead of their sequential adds
+      int j = k;
+      for (; j + 7 * K < T; j += 8 * K) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = v[j + u * K];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a = a + x[u];
+      }
+      for (; j < T; j += K) a = a + v[j];
+      *o = a;
+    }
+  };
+  int64_t b = blockIdx.x;
+  if (b < nblk) prefetch(b);
+  int64_t prev = -1;
+  for (int it = 0; b < nblk; b += gridDim.x, ++it) {
+    stash();
+    __syncthreads();  // rows of block b (and the tables) in LDS; last walks done
+    if (b + gridDim.x < nblk) prefetch(b + gridDim.x);
+    float* vt = vals_s + (it & 1) * RB * TV;
+    if (tid < 64) {
+      if (prev >= 0) sums(prev, vals_s + ((it & 1) ^ 1) * RB * TV);
+    } else {
+      const int64_t row0 = b * RB;
+      const int nr = (int)(n - row0 < RB ? n - row0 : RB);
+      const int np = RB * T;
+      constexpr int kWalkers = kResThreads - 64;
+      for (int p0 = tid - 64; p0 < np; p0 += kResWalks * kWalkers) {
+        int r[kResWalks], tl[kResWalks], h[kResWalks];
+        bool on[kResWalks];
+        uint32_t w[kResWalks];
+#pragma unroll
+        for (int k = 0; k < kResWalks; ++k) {
+          const int p = p0 + k * kWalkers;
+          r[k] = p % RB;
+          tl[k] = p / RB;
+          on[k] = p < np && r[k] < nr;
+          h[k] = 0;
+          w[k] = on[k] ? nodes_s[tl[k] * H] : kPredLeaf;
+        }
+        for (int d = 0; d < max_depth; ++d) {
+          bool any = false;
+#pragma unroll
+          for (int k = 0; k < kResWalks; ++k) any = any || w[k] != kPredLeaf;
+          if (!any) break;
+#pragma unroll
+          for (int k = 0; k < kResWalks; ++k) {
+            if (w[k] == kPredLeaf) continue;
+            const uint32_t f = w[k] >> 8;
+            const uint8_t* row = rows_s + r[k] * Sp;
+            const int c = (int)row[f < (uint32_t)S ? f : (uint32_t)S - 1];  // stays in the row
+            const int bb = (int)(w[k] & 0xffu);
+            h[k] = 2 * h[k] + ((c <= bb || c == num_bins) ? 1 : 2);
+            w[k] = nodes_s[tl[k] * H + h[k]];
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < kResWalks; ++k)
+          if (on[k]) vt[r[k] * TV + tl[k]] = lr * leaves_s[tl[k] * H + h[k]];
+      }
+    }
+    prev = b;
+    __syncthreads();  // the walks are done: the row buffer can be refilled
+  }
+  if (prev >= 0 && tid < 64) {
+    // the last block: its table is the one the last iteration wrote
+    int it_last = 0;
+    for (int64_t bb = blockIdx.x; bb + gridDim.x < nblk; bb += gridDim.x) ++it_last;
+    sums(prev, vals_s + (it_last & 1) * RB * TV);
+  }
+}
+
+// block shape of predict_resident_kernel: 0 when the trees do not fit
+int predict_resident_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
+                          size_t* lds_out) {
+  constexpr int64_t kBudget = 150 * 1024;
+  const int64_t T = (int64_t)n_rounds * K;
+  if (S % 16 != 0 || S >= (1 << 20) || T * H * 8 > 64 * 1024) return 0;
+  const int64_t Sp = S + 4;
+  // RB rows: the row buffer, two value tables and at most kResMaxQ loads per thread
+  int64_t RB = (kBudget - 8 * T * H) / (Sp + 8 * (T + 1));
+  RB = std::min<int64_t>(RB, (int64_t)kResMaxQ * kResThreads * 16 / S);
+  RB = std::min<int64_t>(RB, 256);
+  if (RB < 8) return 0;
+  *RB_out = (int32_t)RB;
+  *lds_out = (size_t)(8 * T * H + RB * Sp + 8 * RB * (T + 1));
+  return 1;
+}
+
 // block shape of predict_rows_kernel: 0 when the trees or rows do not fit
 // (then predict_heap_kernel is used)
 int predict_rows_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
