@@ -105,6 +105,14 @@ struct RouteArgs {
 };
 __global__ void route_kernel(RouteArgs a);
 __global__ void block_scan_kernel(int32_t nb, PartSums ps);
+constexpr int kLevelScanMaxNodes = 64;  // (tree, node)s of a level for level_scan_kernel
+__global__ void level_scan_kernel(int32_t nb, PartSums ps, int32_t T, int32_t nodes, int32_t E,
+                                  int64_t n_pos, const int64_t* seg, const int32_t* present,
+                                  const int32_t* split_l, const int64_t* tot_q,
+                                  int64_t* seg_next, int64_t* tot_q_next, int64_t* tot_c_next,
+                                  int32_t* present_next, int32_t* key_list_next, int32_t n_list,
+                                  int32_t tile_rows, int32_t max_tiles, Tile* tiles,
+                                  int32_t* key_tile_start, int32_t* n_tiles);
 __global__ void root_totals_kernel(int32_t n_keys, const int64_t* seg, PartSums ps,
                                    int64_t* tot_q, int64_t* tot_c);
 __global__ void node_scan_kernel(int32_t T, int32_t nodes, int32_t E, int32_t wpn,

@@ -238,6 +238,41 @@ static int ensure_partials(Engine* e, int64_t max_tiles) {
   return 0;
 }
 
+// histogram tiles of level d (the root, or the smaller child of every split):
+// tile rows, the tile bound, and buffers that hold them
+struct LevelPlan {
+  int32_t n_list = 0;
+  int64_t rows_bound = 0, R = 0, max_tiles = 0;
+};
+
+static int level_plan(Engine* e, int d, LevelPlan* lp) {
+  const int64_t T = e->c.n_trees, N = e->c.n_rows, E = e->c.num_eras;
+  const int64_t nodes = int64_t(1) << d;
+  lp->n_list = (int32_t)(d == 0 ? T * nodes * E : T * (nodes / 2) * E);
+  lp->rows_bound = d == 0 ? T * N : (T * N) / 2;
+  lp->R = pick_tile_rows(e, lp->rows_bound);
+  lp->max_tiles = lp->rows_bound / lp->R + lp->n_list + 1;
+  int r = ensure_partials(e, lp->max_tiles);
+  if (r) return r;
+  if (lp->max_tiles > e->max_htiles) {
+    if (e->htiles) {
+      // tile lists are only reused within the stream; grow after a sync
+      WGBM_CHECK(hipDeviceSynchronize());
+      for (auto it = e->allocs.begin(); it != e->allocs.end(); ++it)
+        if (*it == e->htiles) {
+          (void)hipFree(*it);
+          e->allocs.erase(it);
+          break;
+        }
+      e->htiles = nullptr;
+    }
+    r = dalloc(e, &e->htiles, lp->max_tiles);
+    if (r) return r;
+    e->max_htiles = lp->max_tiles;
+  }
+  return 0;
+}
+
 static inline unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
 int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat_sel,
@@ -315,6 +350,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   }
 
   const float mcw = c.min_child_weight, eps = c.l2_reg, msg = c.min_split_gain;
+  bool planned = false;  // this level's histogram tiles were planned by the previous level
   for (int d = 0; d <= D; ++d) {
     const int nodes = 1 << d;
     const int n_tn = T * nodes;
@@ -354,32 +390,18 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       WGBM_LAUNCH_CHECK();
     } else if (d < D) {
       // ---- histograms of the computed segments
-      const int n_list = d == 0 ? n_keys : T * (nodes / 2) * E;
       const int32_t* list = d == 0 ? nullptr : e->key_list[cur];
-      const int64_t rows_bound = d == 0 ? (int64_t)T * N : ((int64_t)T * N) / 2;
-      const int64_t R = pick_tile_rows(e, rows_bound);
-      const int64_t max_tiles = rows_bound / R + n_list + 1;
-      int r = ensure_partials(e, max_tiles);
+      LevelPlan lp;
+      int r = level_plan(e, d, &lp);
       if (r) return r;
-      if (max_tiles > e->max_htiles) {
-        if (e->htiles) {
-          WGBM_CHECK(hipDeviceSynchronize());
-          for (auto it = e->allocs.begin(); it != e->allocs.end(); ++it)
-            if (*it == e->htiles) {
-              (void)hipFree(*it);
-              e->allocs.erase(it);
-              break;
-            }
-          e->htiles = nullptr;
-        }
-        r = dalloc(e, &e->htiles, max_tiles);
-        if (r) return r;
-        e->max_htiles = max_tiles;
+      const int n_list = lp.n_list;
+      const int64_t R = lp.R, max_tiles = lp.max_tiles, rows_bound = lp.rows_bound;
+      if (!planned) {  // else planned by the previous level's level_scan_kernel
+        hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur], (int64_t)0,
+                           n_list, list, (int32_t)R, 0, (int32_t)max_tiles, e->htiles, e->hkts,
+                           e->hn);
+        WGBM_LAUNCH_CHECK();
       }
-      hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur], (int64_t)0,
-                         n_list, list, (int32_t)R, 0, (int32_t)max_tiles, e->htiles, e->hkts,
-                         e->hn);
-      WGBM_LAUNCH_CHECK();
       HistLaunch a;
       a.codes = c.codes_rm;
       a.n_rows = N;
@@ -460,7 +482,24 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     rl.split_b = e->split_b;
     hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, rl);
     WGBM_LAUNCH_CHECK();
-    if (d < D) {
+    planned = false;
+    if (d < D && E <= 64 && n_tn <= kLevelScanMaxNodes) {
+      // few keys: block prefix, node scan and the next level's tile plan in
+      // one workgroup
+      LevelPlan lp;
+      const bool next_hist = d + 1 < D && !e->des_direct;
+      if (next_hist) {
+        const int r = level_plan(e, d + 1, &lp);
+        if (r) return r;
+      }
+      hipLaunchKernelGGL(level_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps, T,
+                         nodes, E, n_pos, e->seg[cur], e->present[cur], e->split_l, e->totq[cur],
+                         e->seg[nxt], e->totq[nxt], e->totc[nxt], e->present[nxt],
+                         e->key_list[nxt], next_hist ? lp.n_list : 0, (int32_t)lp.R,
+                         (int32_t)lp.max_tiles, e->htiles, e->hkts, e->hn);
+      WGBM_LAUNCH_CHECK();
+      planned = next_hist;
+    } else if (d < D) {
       hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
       WGBM_LAUNCH_CHECK();
       const int wpn = E <= 64 ? 1 : (E <= 128 ? 2 : 4);  // waves per node
@@ -469,6 +508,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                          e->totq[cur], e->seg[nxt], e->totq[nxt], e->totc[nxt], e->present[nxt],
                          e->key_list[nxt]);
       WGBM_LAUNCH_CHECK();
+    }
+    if (d < D) {
       hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, n_pos,
                          E, e->seg[cur], e->seg[nxt], e->keyp[cur], e->dirbit, e->ps,
                          e->order[cur], e->order[nxt], e->keyp[nxt], e->rpos[cur],

@@ -11,6 +11,7 @@
 #include "common.hpp"
 #include "engine.hpp"
 #include "kernels.hpp"
+#include "plan.hpp"
 
 namespace wgbm {
 
@@ -384,7 +385,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
 
 // inclusive prefix over the blocks of the first-segment partials; one
 // workgroup of 1024 threads, tiles of 1024 blocks
-__global__ __launch_bounds__(1024) void block_scan_kernel(int32_t nb, PartSums ps) {
+__device__ inline void block_scan_body(int32_t nb, const PartSums& ps) {
   __shared__ int64_t s_wq[16], s_wn[16];
   __shared__ int64_t s_cq, s_cn;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -426,6 +427,10 @@ __global__ __launch_bounds__(1024) void block_scan_kernel(int32_t nb, PartSums p
     }
     __syncthreads();
   }
+}
+
+__global__ __launch_bounds__(1024) void block_scan_kernel(int32_t nb, PartSums ps) {
+  block_scan_body(nb, ps);
 }
 
 // root totals of every (tree, era) key: quantised residual sum and rows
@@ -623,6 +628,67 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
     keyp_next[dst] = (int32_t)(d[j] == 0 ? kl : kl + E);
     rpos_next[dst] = rr[j];
   }
+}
+
+// The three steps between route and scatter of a level with few keys (at
+// most 64 eras), in one workgroup of 1024 threads: the block prefix, the node
+// scan with one wave per node (wave w takes nodes w, w + 16, ...), and the
+// tile plan of the next level's histogram (the smaller child of every split,
+// the first n_list entries of key_list_next; skipped when n_list is 0).  The
+// prefix and the node scan's outputs are read back by the same workgroup
+// after a barrier.
+__global__ __launch_bounds__(1024) void level_scan_kernel(
+    int32_t nb, PartSums ps, int32_t T, int32_t nodes, int32_t E, int64_t n_pos,
+    const int64_t* __restrict__ seg, const int32_t* __restrict__ present,
+    const int32_t* __restrict__ split_l, const int64_t* __restrict__ tot_q,
+    int64_t* __restrict__ seg_next, int64_t* __restrict__ tot_q_next,
+    int64_t* __restrict__ tot_c_next, int32_t* __restrict__ present_next,
+    int32_t* __restrict__ key_list_next, int32_t n_list, int32_t tile_rows, int32_t max_tiles,
+    Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
+    int32_t* __restrict__ n_tiles) {
+  block_scan_body(nb, ps);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int tn = wave; tn < T * nodes; tn += 16) {
+    const bool sp = present[tn] && split_l[tn] >= 0;
+    const int64_t k0 = (int64_t)tn * E;
+    const int64_t base = seg[k0];
+    const int64_t c0 = 2 * k0;
+    // E <= 64: era e on lane e
+    int64_t L = 0, R = 0, q = 0;
+    if (lane < E) {
+      const int64_t cnt = seg[k0 + lane + 1] - seg[k0 + lane];
+      L = cnt;
+      if (sp) segment_left_sums(k0 + lane, seg, ps, q, L);
+      R = cnt - L;
+    }
+    int64_t il = L, ir = R;  // inclusive wave scans
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t yl = __shfl_up(il, o, 64), yr = __shfl_up(ir, o, 64);
+      if (lane >= o) {
+        il += yl;
+        ir += yr;
+      }
+    }
+    const int64_t ltot = __shfl(il, 63, 64), rtot = __shfl(ir, 63, 64);
+    const int side = (ltot <= rtot) ? 0 : 1;  // the smaller child gets the histogram
+    if (lane < E) {
+      seg_next[c0 + lane] = base + il - L;
+      seg_next[c0 + E + lane] = base + ltot + ir - R;
+      // child totals (the words of children that do not exist are zero)
+      tot_q_next[c0 + lane] = sp ? q : 0;
+      tot_c_next[c0 + lane] = sp ? L : 0;
+      tot_q_next[c0 + E + lane] = sp ? tot_q[k0 + lane] - q : 0;
+      tot_c_next[c0 + E + lane] = sp ? R : 0;
+      key_list_next[k0 + lane] = sp ? (int32_t)(c0 + side * E + lane) : -1;
+    }
+    if (lane < 2) present_next[2 * tn + lane] = sp;
+    if (tn == T * nodes - 1 && lane == 0) seg_next[(int64_t)2 * T * nodes * E] = n_pos;
+  }
+  if (n_list <= 0) return;  // uniform
+  __syncthreads();
+  plan_tiles_body(seg_next, 0, n_list, key_list_next, tile_rows, 0, max_tiles, tiles,
+                  key_tile_start, n_tiles);
 }
 
 __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
