@@ -54,6 +54,64 @@ class _Phases:
             print(f"{what} phases: " + ", ".join(f"{n} {dt * 1e3:.1f} ms" for n, dt in self.items))
 
 
+class _RecordStream:
+    """The engine's per-round tree records (device heaps [rounds, trees, H])
+    copied to pinned host memory in blocks of rounds while later rounds run,
+    each finished block turned into reference tree dicts on the host: the
+    dict building overlaps the GPU's work instead of following it."""
+
+    BLOCK = 8  # rounds per copy
+
+    def __init__(self, rec):
+        self.rec = rec
+        self.host = {k: torch.empty(rec[k].shape, dtype=rec[k].dtype, pin_memory=True)
+                     for k in ("feat", "bin", "leaf", "count")}
+        self.pending = []   # (first round, end round, event) of issued copies
+        self.copied = 0     # rounds whose copy has been issued
+        self.trees = []     # per finished round: its list of tree dicts
+
+    def round_done(self, j):
+        """Round j has been enqueued: issue a block copy every BLOCK rounds
+        and convert the blocks whose copies have landed."""
+        if (j + 1) % self.BLOCK == 0:
+            self.issue(j + 1)
+        self.drain(wait=False)
+
+    def issue(self, end):
+        if end <= self.copied:
+            return
+        r0 = self.copied
+        for k, h in self.host.items():
+            h[r0:end].copy_(self.rec[k][r0:end], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.pending.append((r0, end, ev))
+        self.copied = end
+
+    def drain(self, wait):
+        # the tree dicts form no reference cycles; pausing the cyclic
+        # collector keeps it from re-walking the growing forest on every
+        # allocation threshold (about 4x faster at 2000 trees of depth 6)
+        gc_was_on = gc.isenabled()
+        gc.disable()
+        try:
+            while self.pending and (wait or self.pending[0][2].query()):
+                r0, r1, ev = self.pending.pop(0)
+                ev.synchronize()
+                h = {k: v[r0:r1].numpy() for k, v in self.host.items()}
+                n_trees = h["feat"].shape[1]
+                flat = _heaps_to_dicts(h["feat"], h["bin"], h["leaf"], h["count"])
+                for j in range(r1 - r0):
+                    self.trees.append(flat[j * n_trees:(j + 1) * n_trees])
+        finally:
+            if gc_was_on:
+                gc.enable()
+
+    def finish(self, done):
+        self.issue(done)
+        self.drain(wait=True)
+
+
 class WarpGBM(BaseEstimator, RegressorMixin):
     def __init__(
         self,
@@ -389,12 +447,14 @@ class WarpGBM(BaseEstimator, RegressorMixin):
             if start_iter > 0:
                 self._predict_codes_into(self._eval["codes"], eval_pred, self.forest[:start_iter])
         done = 0
+        stream = _RecordStream(rec)
         with torch.no_grad():
             for j in range(n_new):
                 i = start_iter + j
                 feat_sel = self._feature_subset(dev)
                 eng.round(Y_gpu, preds, feat_sel, {k: v[j] for k, v in rec.items()})
                 done = j + 1
+                stream.round_done(j)
                 if self._eval is not None:
                     D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
                                    rec["leaf"][j], 1, 1, self.max_depth, self.learning_rate,
@@ -402,9 +462,10 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                     self._compute_eval_regression(i, Y_gpu, preds, eval_pred[:, 0])
                     if self.stop:
                         break
+        stream.finish(done)
         self._phases.mark("rounds")
         eng.close()
-        self._absorb_records(rec, done, start_iter, classification=False)
+        self._absorb_records(rec, stream, done, start_iter, classification=False)
         self._phases.mark("records")
         self._phases.report()
         self.feature_importance_ = self.per_era_feature_importance_.sum(axis=0)
@@ -445,12 +506,14 @@ class WarpGBM(BaseEstimator, RegressorMixin):
             if start_iter > 0:
                 self._predict_codes_into(self._eval["codes"], eval_scores, self.forest[:start_iter])
         done = 0
+        stream = _RecordStream(rec)
         with torch.no_grad():
             for j in range(n_new):
                 i = start_iter + j
                 feat_sel = self._feature_subset(dev)
                 eng.round(labels, scores, feat_sel, {k: v[j] for k, v in rec.items()})
                 done = j + 1
+                stream.round_done(j)
                 if self._eval is not None:
                     D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
                                    rec["leaf"][j], 1, K, self.max_depth, self.learning_rate,
@@ -458,9 +521,10 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                     self._compute_eval_multiclass(i, labels, scores, eval_scores)
                     if self.stop:
                         break
+        stream.finish(done)
         self._phases.mark("rounds")
         eng.close()
-        self._absorb_records(rec, done, start_iter, classification=True)
+        self._absorb_records(rec, stream, done, start_iter, classification=True)
         self._phases.mark("records")
         self._phases.report()
         self.feature_importance_ = self.per_era_feature_importance_.sum(axis=0)
@@ -554,20 +618,12 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                   f"Train LogLoss: {train_loss:.6f} | Eval {self.eval_metric}: {eval_loss:.6f}")
 
     # ------------------------------------------------------------------ records -> forest
-    def _absorb_records(self, rec, done, start_iter, classification):
-        """Convert the engine's heap records of ``done`` rounds into reference
-        tree dicts and accumulate importance in the reference's order: per
-        tree, internal nodes in depth-first pre-order, float32 adds
-        (warpgbm/core.py:624-627)."""
-        host = {}
-        for k in ("feat", "bin", "leaf", "count"):
-            # through pinned memory: one DMA per record
-            v = rec[k][:done]
-            h = torch.empty(v.shape, dtype=v.dtype, pin_memory=True)
-            h.copy_(v)
-            host[k] = h.numpy()
-        self._phases.mark("records copy")
-        feat = host["feat"]  # [done, n_trees, H]
+    def _absorb_records(self, rec, stream, done, start_iter, classification):
+        """Reference tree dicts of the ``done`` rounds (built by the record
+        stream during training) into the forest, and importance in the
+        reference's order: per tree, internal nodes in depth-first pre-order,
+        float32 adds (warpgbm/core.py:624-627)."""
+        feat = stream.host["feat"][:done].numpy()  # [done, n_trees, H]
         n_trees, H = feat.shape[1], feat.shape[2]
         # importance: every internal node of every tree, trees in order and
         # nodes in pre-order, one float32 add per node and era in exactly that
@@ -593,22 +649,11 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                              torch.from_numpy(fstart).to(dev))
             self.per_era_feature_importance_ = acc.cpu().numpy()
         self._phases.mark("importance")
-        # the tree dicts form no reference cycles; pausing the cyclic
-        # collector keeps it from re-walking the growing forest on every
-        # allocation threshold (about 4x faster at 2000 trees of depth 6)
-        gc_was_on = gc.isenabled()
-        gc.disable()
-        try:
-            flat = _heaps_to_dicts(feat, host["bin"], host["leaf"], host["count"])
-            for j in range(done):
-                trees = flat[j * n_trees:(j + 1) * n_trees]
-                if classification:
-                    self.forest.append(trees)
-                else:
-                    self.forest[start_iter + j] = trees[0]
-        finally:
-            if gc_was_on:
-                gc.enable()
+        for j in range(done):
+            if classification:
+                self.forest.append(stream.trees[j])
+            else:
+                self.forest[start_iter + j] = stream.trees[j][0]
         self._trees_trained = start_iter + done
 
     # ------------------------------------------------------------------ binning at predict time

@@ -420,7 +420,17 @@ __global__ void importance_add_kernel(float* __restrict__ acc, int32_t F, int32_
   const int f = (int)(gid / E), e = (int)(gid - (int64_t)f * E);
   float* w = acc + (int64_t)e * F + f;
   float s = *w;
-  for (int64_t i = fstart[f]; i < fstart[f + 1]; ++i) s = s + gain[node[i] * E + e];
+  const int64_t i1 = fstart[f + 1];
+  int64_t i = fstart[f];
+  // eight gathers in flight ahead of their (sequential) adds
+  for (; i + 8 <= i1; i += 8) {
+    float g[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) g[u] = gain[node[i + u] * E + e];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s = s + g[u];
+  }
+  for (; i < i1; ++i) s = s + gain[node[i] * E + e];
   *w = s;
 }
 
