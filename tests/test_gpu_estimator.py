@@ -95,8 +95,14 @@ def test_multiclass_many_features_bit_exact(gpu):
     assert np.array_equal(bits(m.predict_proba(X)), bits(ref.predict_codes(codes)))
 
 
-def test_era_des_prebinned_bit_exact(gpu):
-    print_case("estimator", "DES E=6 prebinned")
+# era code layouts (engine tuning key 2): the int8 codes, or the pair-code
+# copy (num_bins <= 7; the int8 codes above that)
+LAYOUTS = [0, 1]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_era_des_prebinned_bit_exact(gpu, layout):
+    print_case("estimator", "DES E=6 prebinned layout", layout)
     rng = np.random.default_rng(2)
     N, F, E = 6000, 30, 6
     X = rng.integers(0, 5, (N, F)).astype(np.int8)
@@ -106,6 +112,7 @@ def test_era_des_prebinned_bit_exact(gpu):
     score = ((X[:, :10] - 2) * sign[era]).sum(axis=1) + rng.standard_normal(N)
     y = np.digitize(score, np.quantile(score, [0.2, 0.4, 0.6, 0.8])) / 4.0
     m = WarpGBM(num_bins=5, max_depth=4, n_estimators=6, learning_rate=0.5)
+    m._engine_tuning = {2: layout}
     m.fit(X, y.astype(F32), era_id=era)
     ref = gbm.Forest(num_bins=5, max_depth=4, n_estimators=6, learning_rate=0.5).fit_codes(
         X, y.astype(F32), era_id=era)
@@ -116,17 +123,17 @@ def test_era_des_prebinned_bit_exact(gpu):
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
 
 
-@pytest.mark.parametrize("E", [1, 3])
-def test_prebinned_negative_and_wrapped_codes_bit_exact(gpu, E):
+@pytest.mark.parametrize("E,B", [(1, 10), (3, 10), (3, 5)])
+def test_prebinned_negative_and_wrapped_codes_bit_exact(gpu, E, B):
     """Pre-binned integer input with negative values: every column max is
     < num_bins, so it is used as codes (warpgbm/core.py:499-505), cast to
     int8 (values below -128 wrap, e.g. -200 -> 56 >= num_bins).  Codes outside
     [0, num_bins) are skipped by the histograms (histogram_kernel.cu:41) and
     compared as signed int8 by the partition and predict (core.py:629,
     predict.cu:43): negative codes go left, wrapped ones >= num_bins right."""
-    print_case("estimator", "pre-binned negative codes E", E)
+    print_case("estimator", "pre-binned negative codes E B", E, B)
     rng = np.random.default_rng(8)
-    N, F, B = 5000, 14, 10
+    N, F = 5000, 14
     X = rng.integers(-2, B, (N, F)).astype(np.int64)
     X[rng.random((N, F)) < 0.05] = -200           # wraps to int8 56
     era = np.repeat(np.arange(E), N // E + 1)[:N]
@@ -163,14 +170,16 @@ def test_int8_input_over_num_bins_is_quantile_binned(gpu):
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
 
 
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("mcw,B", [(1, 12), (20, 12), (1, 7), (20, 3)])
-def test_era_des_colsample_uneven_eras_bit_exact(gpu, mcw, B):
+def test_era_des_colsample_uneven_eras_bit_exact(gpu, mcw, B, layout):
     """Direct era path (every era fits one LDS tile): uneven era sizes, eras
     that are empty at deeper nodes, a feature subset per tree, generic bin
-    counts (B <= 7: the pair-packed LDS cells); with min_child_weight 20 many
+    counts (B <= 7 with layout 1: pair codes and pair tables); with
+    min_child_weight 20 many
     (node, era) segments hold fewer than 2*20 rows (no candidate can split
     them) from the root down."""
-    print_case("estimator", "DES E=7 uneven colsample mcw B", mcw, B)
+    print_case("estimator", "DES E=7 uneven colsample mcw B layout", mcw, B, layout)
     rng = np.random.default_rng(5)
     sizes = np.array([900, 40, 1500, 7, 600, 1200, 253])
     E, N, F = len(sizes), int(sizes.sum()), 23
@@ -180,6 +189,7 @@ def test_era_des_colsample_uneven_eras_bit_exact(gpu, mcw, B):
     y = (score / 10.0).astype(F32)
     kw = dict(num_bins=B, max_depth=5, n_estimators=5, learning_rate=0.3, min_child_weight=mcw)
     m = WarpGBM(colsample_bytree=0.6, random_state=11, **kw)
+    m._engine_tuning = {2: layout}
     m.fit(X, y, era_id=era)
     ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era, feat_sets=m.feature_subsets_)
     for i, (a, b) in enumerate(zip(m.forest, ref.forest)):

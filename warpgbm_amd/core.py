@@ -361,9 +361,13 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         return None, None
 
     def _new_engine(self, codes, root_order, era_start, n_trees, objective):
-        return D.Engine(codes, root_order, era_start, self.num_bins, self.num_eras,
-                        self.max_depth, n_trees, objective, self.min_child_weight,
-                        self.min_split_gain, self.L2_reg, self.learning_rate)
+        eng = D.Engine(codes, root_order, era_start, self.num_bins, self.num_eras,
+                       self.max_depth, n_trees, objective, self.min_child_weight,
+                       self.min_split_gain, self.L2_reg, self.learning_rate)
+        # engine knobs (wgbm_engine_set_tuning keys); none changes the model
+        for key, value in getattr(self, "_engine_tuning", {}).items():
+            eng.set_tuning(int(key), int(value))
+        return eng
 
     def _feature_subset(self, dev):
         """Features of one round: randperm(F)[:k], k = max(1, int(colsample * F))

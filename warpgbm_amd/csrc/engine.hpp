@@ -161,11 +161,23 @@ __global__ void des_combine_kernel(const double* bsum, const int32_t* bdir, int3
                                    int32_t* agree_max);
 __global__ void local_scatter_kernel(const int32_t* feat_sel, int32_t n_sel, int32_t F,
                                      int32_t* local_of);
+// pcodes: the pair-code copy of the codes (num_bins <= 7; n_rows rows of
+// pstride bytes, under 4 GiB) or null for the int8 codes
 int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* codes,
-                   int64_t stride, int32_t F, const float* rpos, const int32_t* shifts, const int32_t* order, const int64_t* seg, int32_t E,
-                   int32_t nodes_in_level,
+                   int64_t stride, int32_t F, const float* rpos, const int32_t* shifts,
+                   const int32_t* order, const int64_t* seg, int32_t E, int32_t nodes_in_level,
                    const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
-                   float eps, float* gain, int8_t* dir);
+                   float eps, float* gain, int8_t* dir, const uint8_t* pcodes, int64_t n_rows,
+                   int64_t pstride);
+// levels whose mean (node, era) segment holds at least this many rows use
+// the pair codes: below it the int8 kernel's smaller LDS tables keep more
+// segments (and so more row loads) in flight per CU
+constexpr int kDesPairMinRows = 96;
+int launch_pack_pairs(hipStream_t st, const int8_t* codes, int64_t stride, int32_t F, int64_t n,
+                      int32_t B, uint8_t* out, int64_t pstride);
+// row stride of the pair codes: one byte per feature pair, whole 8-byte
+// words of 8 pairs, rows 256-byte aligned
+inline int64_t pair_stride(int32_t F) { return ((int64_t)(F + 15) / 16 * 8 + 255) / 256 * 256; }
 
 
 // binning / predict kernels

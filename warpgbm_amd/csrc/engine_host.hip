@@ -60,6 +60,12 @@ struct Engine {
   float* sgain = nullptr;       // staged per-era gains [tn][E][n_sel][B-1]
   int8_t* sdir = nullptr;       // staged per-era directions
   int32_t* local_of = nullptr;  // [F] local index in the round's subset, or -1
+  // num_bins <= 7: pair-code copy of codes_rm for the era path (made by the
+  // first round); des_codes 0 = read the int8 codes, 1 = pair codes (default)
+  uint8_t* pcodes = nullptr;
+  int64_t pstride = 0;
+  bool pcodes_ready = false;
+  int des_codes = 1;
   uint32_t* alive = nullptr;    // [tn][W] segments that can hold a split, W = ceil(E/32)
   double* bsum = nullptr;       // [tn][W][n_sel*(B-1)] era-block gain sums
   int32_t* bdir = nullptr;      // [tn][W][n_sel*(B-1)] era-block direction sums
@@ -161,6 +167,10 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     E_ALLOC(e->sgain, T * hist_nodes_max * E * F * (B - 1));
     E_ALLOC(e->sdir, T * hist_nodes_max * E * F * (B - 1));
     E_ALLOC(e->local_of, F);
+    if (B <= 7 && N * pair_stride((int32_t)F) <= (int64_t)0xffffffffll) {
+      e->pstride = pair_stride((int32_t)F);
+      E_ALLOC(e->pcodes, N * e->pstride);
+    }
     const int64_t W = (E + kDesEraBlock - 1) / kDesEraBlock;
     E_ALLOC(e->alive, T * hist_nodes_max * W);
     E_ALLOC(e->bsum, T * hist_nodes_max * W * F * (B - 1));
@@ -202,6 +212,11 @@ int engine_set_tuning(Engine* e, int key, int64_t value) {
     WGBM_REQUIRE(value == 0 || (value >= 256 && value <= WGBM_MAX_TILE_ROWS),
                  "hist tile rows must be 0 or in [256, %d]", WGBM_MAX_TILE_ROWS);
     e->hist_tile_rows = value;
+    return 0;
+  }
+  if (key == 2) {
+    WGBM_REQUIRE(value == 0 || value == 1, "era code layout must be 0 or 1");
+    e->des_codes = (int)value;
     return 0;
   }
   wgbm_set_error("engine_set_tuning: unknown key %d", key);
@@ -363,9 +378,18 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     if (d < D && e->des_direct) {
       // ---- E > 1, direct: per-era gains of every (node, era) segment
       const int64_t ncand = (int64_t)n_sel * (B - 1);
+      // pair codes for levels of large segments (mean rows per (node, era))
+      const bool use_pairs = e->pcodes && e->des_codes == 1 &&
+                             N >= (int64_t)kDesPairMinRows * nodes * E;
+      if (use_pairs && !e->pcodes_ready) {
+        int r = launch_pack_pairs(st, c.codes_rm, c.stride, F, N, B, e->pcodes, e->pstride);
+        if (r) return r;
+        e->pcodes_ready = true;
+      }
       int r = launch_des_era(e->V, B, n_keys, st, c.codes_rm, c.stride, F, e->rpos[cur],
                              e->shifts, e->order[cur], e->seg[cur], E, nodes, e->present[cur],
-                             e->local_of, n_sel, mcw, eps, e->sgain, e->sdir);
+                             e->local_of, n_sel, mcw, eps, e->sgain, e->sdir,
+                             use_pairs ? e->pcodes : nullptr, N, e->pstride);
       if (r) return r;
       const int64_t W = (E + kDesEraBlock - 1) / kDesEraBlock;
       hipLaunchKernelGGL(des_alive_kernel, dim3(blocks_for((int64_t)n_tn * W, 256)), dim3(256), 0,

@@ -525,6 +525,234 @@ void des_era_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// des_pair: the direct era path for num_bins <= 7 on pair codes, for levels
+// whose (node, era) segments are large (the engine picks it by the mean
+// segment size; see kDesPairMinRows).
+//   Pair codes (made once per engine by pack_pairs_kernel): byte k of a row
+//   is c(2k) * (B+1) + c(2k+1) for the features 2k, 2k+1, each code clamped
+//   to the trash bin B (a code >= B or negative, and the padding past the
+//   last feature); a row of F features takes ceil(F/2) bytes.
+//   LDS: per lane (lane-owned columns as in the tile histogram) one
+//   (B+1) x (B+1) table per feature pair, indexed by the pair code, so a row
+//   costs one LDS add per pair of features instead of one per feature.  A
+//   feature's column is its table summed over the partner's codes (all B+1,
+//   the trash bin included): the same packed words as a one-feature
+//   histogram, since packed words add exactly.
+//   A lane covers 2 pairs (4 features, one 16-bit load per row); the
+//   workgroup's 64 lanes cover a chunk of 256 features.  Code loads are
+//   buffer loads with the row offset in a scalar register (the engine keeps
+//   the copy under 4 GiB), so a row costs no vector address arithmetic.
+// Outputs and key order as des_era_kernel (staged gain / dir per (key,
+// local feature, bin)).  Each key's scan clears the table words it read, so
+// the next key starts from zero without a pass of its own.
+// The tables (36 KB at B = 5) allow 4 workgroups per CU: per row of a
+// small segment fewer bytes are in flight than with the int8 codes' 12 KB
+// tables, which is why deep levels keep des_era_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kDesPairThreads = 512;
+constexpr int kDesPairLanePairs = 2;                                 // pairs per lane
+constexpr int kDesPairChunk = kHistSlots * 2 * kDesPairLanePairs;  // features per workgroup
+
+template <int BT>
+__global__ __launch_bounds__(kDesPairThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void des_pair_kernel(
+    const uint8_t* __restrict__ pcodes, uint32_t pbytes, uint32_t pstride, int32_t F,
+    const float* __restrict__ rpos, const int32_t* __restrict__ shifts,
+    const int32_t* __restrict__ order, const int64_t* __restrict__ seg, int32_t E,
+    int32_t n_keys, int32_t nodes_in_level, const int32_t* __restrict__ present,
+    const int32_t* __restrict__ local_of, int32_t n_sel, float mcw, float eps,
+    float* __restrict__ gain, int8_t* __restrict__ dir) {
+  static_assert(BT >= 2 && BT <= 7, "pair tables: num_bins in [2, 7]");
+  constexpr int Bp = BT + 1, P = Bp * Bp;
+  constexpr int LP = kDesPairLanePairs;
+  constexpr int CW = kDesPairChunk;
+  constexpr int nwaves = kDesPairThreads / 64;
+  constexpr int U = 8;  // rows per group
+  constexpr int step = nwaves * U;
+  constexpr int nb = BT - 1;
+  extern __shared__ unsigned long long lds[];
+  const int n_chunks = (F + CW - 1) / CW;
+  const int slots = gridDim.x / n_chunks;
+  const int slot = blockIdx.x / n_chunks;
+  const int chunk = blockIdx.x - slot * n_chunks;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ul = lane & (U - 1);
+  const int f_base = chunk * CW + lane * 2 * LP;
+  // lanes past the last feature re-read the last real pair word; their
+  // words are never evaluated
+  const uint32_t voff = (uint32_t)((f_base < F ? f_base : (F - 1) / (2 * LP) * (2 * LP)) / 2);
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)pcodes, (short)0, (int)pbytes, 0x00020000);
+  // byte address of this lane's word 0 of pair table 0: lane * 8
+  const uint32_t lbase = (uint32_t)lane * 8u;
+
+  for (int i = threadIdx.x; i < LP * P * kHistSlots; i += kDesPairThreads) lds[i] = 0ull;
+  __syncthreads();
+
+  for (int kb = slot; kb < n_keys; kb += 64 * slots) {
+    const int kl = kb + lane * slots;
+    bool live = false;
+    if (kl < n_keys) live = present[kl / E] && !des_segment_dead(seg[kl + 1] - seg[kl], mcw);
+    uint64_t todo = __ballot(live);
+    while (todo) {
+      const int l0 = __builtin_ctzll(todo);
+      todo &= todo - 1;
+      const int key = kb + l0 * slots;
+      const int64_t begin = seg[key];
+      const int n = (int)(seg[key + 1] - begin);  // <= 65536 (checked by the engine)
+      const int s = shifts[(key / E) / nodes_in_level];
+
+      // rows: wave w takes groups [i, i + U), i = (w + k*nwaves)*U; lane
+      // u < U loads row u's id and residual; two register sets alternate so
+      // that the next group's loads are in flight while one is added;
+      // positions past the end read the segment's last row and add the word 0
+      struct Group {
+        uint32_t c[U];
+        int32_t q;  // lane u < U: quantised residual of row u
+      };
+      int32_t ids = 0;
+      auto load_ids = [&](int i0) { ids = order[begin + (i0 + ul < n ? i0 + ul : n - 1)]; };
+      auto issue = [&](Group& g, int i0) {
+        uint32_t rows[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) rows[u] = (uint32_t)__builtin_amdgcn_readlane(ids, u);
+        g.q = wgbm_quantise(rpos[begin + (i0 + ul < n ? i0 + ul : n - 1)], s);
+        load_ids(i0 + step);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          g.c[u] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, voff, rows[u] * pstride, 0);
+      };
+      auto add = [&](const Group& g, int i0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t qr = __builtin_amdgcn_readlane(g.q, u);
+          const unsigned long long w =
+              i0 + u < n ? (unsigned long long)(qr * (int64_t)(1 << WGBM_CBITS) + 1) : 0ull;
+#pragma unroll
+          for (int p = 0; p < LP; ++p) {
+            const uint32_t idx = (g.c[u] >> (8 * p)) & 0xffu;
+            const uint32_t addr = (idx << 9) + lbase + (uint32_t)(p * P * kHistSlots * 8);
+            atomicAdd(
+                reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(lds) + addr), w);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      Group ga, gb;
+      int i = wave * U;
+      if (i < n) {
+        load_ids(i);
+        issue(ga, i);
+        while (i + 2 * step < n) {
+          issue(gb, i + step);
+          add(ga, i);
+          issue(ga, i + 2 * step);
+          add(gb, i + step);
+          i += 2 * step;
+        }
+        if (i + step < n) {
+          issue(gb, i + step);
+          add(ga, i);
+          add(gb, i + step);
+        } else {
+          add(ga, i);
+        }
+      }
+      __syncthreads();
+
+      // thread per feature pair: one sweep of the pair's table, row by row,
+      // clears it and gives the columns of its first feature (row sums,
+      // stored back at word (a, 0) of row a < B) and second feature (column
+      // sums, stored in the trash row: word (B, b)); both are scanned from
+      // there and cleared
+      for (int pi = threadIdx.x; pi < CW / 2; pi += kDesPairThreads) {
+        const int pl = pi / LP, p = pi % LP;  // lane, pair of the lane
+        unsigned long long* t = lds + p * P * kHistSlots + pl;
+        unsigned long long c1[BT];
+#pragma unroll
+        for (int b = 0; b < BT; ++b) c1[b] = 0ull;
+#pragma unroll
+        for (int a = 0; a < Bp; ++a) {
+          unsigned long long row = 0ull;
+#pragma unroll
+          for (int b = 0; b < Bp; ++b) {
+            const unsigned long long w = t[(a * Bp + b) * kHistSlots];
+            row += w;
+            if (b < BT) c1[b] += w;
+            t[(a * Bp + b) * kHistSlots] = 0ull;
+          }
+          if (a < BT) t[a * Bp * kHistSlots] = row;
+          __builtin_amdgcn_sched_barrier(0);  // one row of words live at a time
+        }
+#pragma unroll
+        for (int b = 0; b < BT; ++b) t[(BT * Bp + b) * kHistSlots] = c1[b];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          // column word b of the feature: h = 0 at (b, 0), h = 1 at (B, b)
+          unsigned long long* col = t + (h ? BT * Bp * kHistSlots : 0);
+          const int cs = (h ? 1 : Bp) * kHistSlots;
+          const int f = chunk * CW + pl * 2 * LP + 2 * p + h;
+          const int l = f < F ? local_of[f] : -1;
+          if (l >= 0) {
+            const int64_t out = ((int64_t)key * n_sel + l) * nb;
+            scan_bins(
+                BT, mcw, eps,
+                [&](int b) { return wgbm_dequantise((int64_t)col[b * cs] >> WGBM_CBITS, s); },
+                [&](int b) {
+                  return (float)(int32_t)(col[b * cs] & (unsigned long long)WGBM_CMASK);
+                },
+                [&](int b, float gn, float d) {
+                  gain[out + b] = gn;
+                  dir[out + b] = (int8_t)d;
+                });
+          }
+#pragma unroll
+          for (int b = 0; b < BT; ++b) col[b * cs] = 0ull;
+        }
+      }
+      __syncthreads();  // the table is zero again for the next key
+    }
+  }
+}
+
+// pair codes for des_pair (num_bins <= 7): thread per (row, 4 output bytes
+// = 8 features); byte k of a row = c(2k) * (B+1) + c(2k+1), each code
+// clamped to B (a code >= B or negative, and the padding past the last
+// feature)
+__global__ void pack_pairs_kernel(const int8_t* __restrict__ codes, int64_t stride, int32_t F,
+                                  int64_t n, int32_t B, uint8_t* __restrict__ out,
+                                  int64_t pstride) {
+  const int64_t wpr = pstride / 4;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n * wpr) return;
+  const int64_t row = gid / wpr;
+  const int w = (int)(gid - row * wpr);
+  const int f0 = w * 8;
+  const int8_t* src = codes + row * stride;
+  // one 8-byte load where the row holds all 8 (stride % 16 == 0, f0 % 8 == 0)
+  uint64_t v = 0;
+  if (f0 + 8 <= stride) {
+    v = *reinterpret_cast<const uint64_t*>(src + f0);
+  } else {
+    for (int j = 0; j < 8 && f0 + j < stride; ++j) v |= (uint64_t)(uint8_t)src[f0 + j] << (8 * j);
+  }
+  uint32_t word = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t c[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * k + h;
+      uint32_t x = f0 + j < F ? (uint32_t)(v >> (8 * j)) & 0xffu : (uint32_t)B;
+      c[h] = x < (uint32_t)B ? x : (uint32_t)B;
+    }
+    word |= (c[0] * (uint32_t)(B + 1) + c[1]) << (8 * k);
+  }
+  reinterpret_cast<uint32_t*>(out + row * pstride)[w] = word;
+}
+
 // live-era bit masks: bit (e % 32) of alive[tn * W + e / 32] is set when the
 // (tn, era e) segment can hold a split (not des_segment_dead); W = ceil(E/32)
 // (one mask word per era block)
@@ -632,10 +860,46 @@ __global__ void local_scatter_kernel(const int32_t* __restrict__ feat_sel, int32
 }
 
 int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* codes,
-                   int64_t stride, int32_t F, const float* rpos, const int32_t* shifts, const int32_t* order, const int64_t* seg, int32_t E,
-                   int32_t nodes_in_level,
+                   int64_t stride, int32_t F, const float* rpos, const int32_t* shifts,
+                   const int32_t* order, const int64_t* seg, int32_t E, int32_t nodes_in_level,
                    const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
-                   float eps, float* gain, int8_t* dir) {
+                   float eps, float* gain, int8_t* dir, const uint8_t* pcodes, int64_t n_rows,
+                   int64_t pstride) {
+  if (pcodes) {
+    WGBM_REQUIRE(B >= 2 && B <= 7, "launch_des_era: pair codes need num_bins in [2, 7]");
+    WGBM_REQUIRE(pstride > 0 && pstride % 8 == 0 && pstride * 2 >= ((F + 15) / 16) * 16,
+                 "launch_des_era: bad pair stride %lld", (long long)pstride);
+    WGBM_REQUIRE(n_rows * pstride <= (int64_t)0xffffffffll,
+                 "launch_des_era: pair codes must stay under 4 GiB");
+    const size_t lds = (size_t)kDesPairLanePairs * (B + 1) * (B + 1) * kHistSlots * 8;
+    const int n_chunks = (F + kDesPairChunk - 1) / kDesPairChunk;
+    const int slots = std::max(1, std::min(n_keys, kDesEraMaxWG / n_chunks));
+    const dim3 grid((unsigned)(slots * n_chunks));
+    const uint32_t pbytes = (uint32_t)(n_rows * pstride);
+#define WGBM_DES_PAIR(BB)                                                                      \
+  do {                                                                                         \
+    static bool attr = false;                                                                  \
+    if (!attr) {                                                                               \
+      WGBM_CHECK(hipFuncSetAttribute((const void*)des_pair_kernel<BB>,                          \
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024)); \
+      attr = true;                                                                             \
+    }                                                                                          \
+    hipLaunchKernelGGL((des_pair_kernel<BB>), grid, dim3(kDesPairThreads), lds, st, pcodes,    \
+                       pbytes, (uint32_t)pstride, F, rpos, shifts, order, seg, E, n_keys,      \
+                       nodes_in_level, present, local_of, n_sel, mcw, eps, gain, dir);         \
+    WGBM_LAUNCH_CHECK();                                                                       \
+    return 0;                                                                                  \
+  } while (0)
+    switch (B) {
+      case 2: WGBM_DES_PAIR(2);
+      case 3: WGBM_DES_PAIR(3);
+      case 4: WGBM_DES_PAIR(4);
+      case 5: WGBM_DES_PAIR(5);
+      case 6: WGBM_DES_PAIR(6);
+      default: WGBM_DES_PAIR(7);
+    }
+#undef WGBM_DES_PAIR
+  }
   const size_t lds = (size_t)V * (B + 1) * kHistSlots * 8;
   // at most kDesEraMaxWG workgroups; each strides over the keys of its chunk
   const int n_chunks = (F + kHistSlots * V - 1) / (kHistSlots * V);
@@ -662,6 +926,18 @@ int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* c
 #undef WGBM_DES_ERA
   wgbm_set_error("launch_des_era: bad V=%d", V);
   return WGBM_EINVAL;
+}
+
+int launch_pack_pairs(hipStream_t st, const int8_t* codes, int64_t stride, int32_t F, int64_t n,
+                      int32_t B, uint8_t* out, int64_t pstride) {
+  WGBM_REQUIRE(B >= 2 && B <= 7, "pack_pairs: num_bins must be in [2, 7]");
+  WGBM_REQUIRE(pstride > 0 && pstride % 8 == 0 && pstride * 2 >= ((F + 15) / 16) * 16,
+               "pack_pairs: bad pair stride %lld", (long long)pstride);
+  const int64_t threads = n * (pstride / 4);
+  hipLaunchKernelGGL(pack_pairs_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                     codes, stride, F, n, B, out, pstride);
+  WGBM_LAUNCH_CHECK();
+  return 0;
 }
 
 }  // namespace wgbm
