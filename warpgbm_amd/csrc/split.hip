@@ -836,11 +836,27 @@ __global__ __launch_bounds__(256) void des_combine_kernel(
     const uint32_t* al = alive + (int64_t)tn * W;
     double acc = 0.0;
     int ds = 0;
-    for (int b = 0; b < W; ++b) {
-      if (al[b] == 0) continue;
-      const int64_t o = ((int64_t)tn * W + b) * ncand + c;
-      acc += bsum[o];  // block order
-      ds += bdir[o];
+    // blocks in groups of 8: the loads of a group are issued together (a
+    // block without a live era was never written; its value is loaded and
+    // not added)
+    constexpr int G = 8;
+    for (int b0 = 0; b0 < W; b0 += G) {
+      double v[G];
+      int dv[G];
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        const int b = b0 + k < W ? b0 + k : W - 1;
+        const int64_t o = ((int64_t)tn * W + b) * ncand + c;
+        v[k] = bsum[o];
+        dv[k] = bdir[o];
+      }
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        if (b0 + k < W && al[b0 + k] != 0) {
+          acc += v[k];  // block order
+          ds += dv[k];
+        }
+      }
     }
     crit[gid] = (float)(acc / (double)E);
     a = ds < 0 ? -ds : ds;
