@@ -19,6 +19,7 @@ from __future__ import annotations
 
 import gc
 import pickle
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import torch
@@ -57,8 +58,9 @@ class _Phases:
 class _RecordStream:
     """The engine's per-round tree records (device heaps [rounds, trees, H])
     copied to pinned host memory in blocks of rounds while later rounds run,
-    each finished block turned into reference tree dicts on the host: the
-    dict building overlaps the GPU's work instead of following it."""
+    each landed block turned into reference tree dicts by a worker thread:
+    the dict building overlaps the launches of later rounds (which release
+    the interpreter lock while in the library) and the GPU's work."""
 
     BLOCK = 8  # rounds per copy
 
@@ -68,11 +70,18 @@ class _RecordStream:
                      for k in ("feat", "bin", "leaf", "count")}
         self.pending = []   # (first round, end round, event) of issued copies
         self.copied = 0     # rounds whose copy has been issued
+        self.blocks = []    # futures of per-block lists of per-round tree lists
         self.trees = []     # per finished round: its list of tree dicts
+        self.pool = ThreadPoolExecutor(max_workers=1)
+        # the tree dicts form no reference cycles; pausing the cyclic
+        # collector keeps it from re-walking the growing forest on every
+        # allocation threshold (about 4x faster at 2000 trees of depth 6)
+        self.gc_was_on = gc.isenabled()
+        gc.disable()
 
     def round_done(self, j):
         """Round j has been enqueued: issue a block copy every BLOCK rounds
-        and convert the blocks whose copies have landed."""
+        and hand the blocks whose copies have landed to the worker."""
         if (j + 1) % self.BLOCK == 0:
             self.issue(j + 1)
         self.drain(wait=False)
@@ -88,28 +97,34 @@ class _RecordStream:
         self.pending.append((r0, end, ev))
         self.copied = end
 
+    def _convert(self, r0, r1):
+        h = {k: v[r0:r1].numpy() for k, v in self.host.items()}
+        n_trees = h["feat"].shape[1]
+        flat = _heaps_to_dicts(h["feat"], h["bin"], h["leaf"], h["count"])
+        return [flat[j * n_trees:(j + 1) * n_trees] for j in range(r1 - r0)]
+
     def drain(self, wait):
-        # the tree dicts form no reference cycles; pausing the cyclic
-        # collector keeps it from re-walking the growing forest on every
-        # allocation threshold (about 4x faster at 2000 trees of depth 6)
-        gc_was_on = gc.isenabled()
-        gc.disable()
-        try:
-            while self.pending and (wait or self.pending[0][2].query()):
-                r0, r1, ev = self.pending.pop(0)
-                ev.synchronize()
-                h = {k: v[r0:r1].numpy() for k, v in self.host.items()}
-                n_trees = h["feat"].shape[1]
-                flat = _heaps_to_dicts(h["feat"], h["bin"], h["leaf"], h["count"])
-                for j in range(r1 - r0):
-                    self.trees.append(flat[j * n_trees:(j + 1) * n_trees])
-        finally:
-            if gc_was_on:
-                gc.enable()
+        while self.pending and (wait or self.pending[0][2].query()):
+            r0, r1, ev = self.pending.pop(0)
+            ev.synchronize()
+            self.blocks.append(self.pool.submit(self._convert, r0, r1))
 
     def finish(self, done):
-        self.issue(done)
-        self.drain(wait=True)
+        try:
+            self.issue(done)
+            self.drain(wait=True)
+            for f in self.blocks:  # block order
+                self.trees.extend(f.result())
+        finally:
+            self.close()
+
+    def close(self):
+        """Stop the worker and restore the collector (also after an error)."""
+        if self.pool is not None:
+            self.pool.shutdown(wait=True)
+            self.pool = None
+            if self.gc_was_on:
+                gc.enable()
 
 
 class WarpGBM(BaseEstimator, RegressorMixin):
@@ -452,21 +467,24 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                 self._predict_codes_into(self._eval["codes"], eval_pred, self.forest[:start_iter])
         done = 0
         stream = _RecordStream(rec)
-        with torch.no_grad():
-            for j in range(n_new):
-                i = start_iter + j
-                feat_sel = self._feature_subset(dev)
-                eng.round(Y_gpu, preds, feat_sel, {k: v[j] for k, v in rec.items()})
-                done = j + 1
-                stream.round_done(j)
-                if self._eval is not None:
-                    D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
-                                   rec["leaf"][j], 1, 1, self.max_depth, self.learning_rate,
-                                   eval_pred)
-                    self._compute_eval_regression(i, Y_gpu, preds, eval_pred[:, 0])
-                    if self.stop:
-                        break
-        stream.finish(done)
+        try:
+            with torch.no_grad():
+                for j in range(n_new):
+                    i = start_iter + j
+                    feat_sel = self._feature_subset(dev)
+                    eng.round(Y_gpu, preds, feat_sel, {k: v[j] for k, v in rec.items()})
+                    done = j + 1
+                    stream.round_done(j)
+                    if self._eval is not None:
+                        D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
+                                       rec["leaf"][j], 1, 1, self.max_depth, self.learning_rate,
+                                       eval_pred)
+                        self._compute_eval_regression(i, Y_gpu, preds, eval_pred[:, 0])
+                        if self.stop:
+                            break
+            stream.finish(done)
+        finally:
+            stream.close()
         self._phases.mark("rounds")
         eng.close()
         self._absorb_records(rec, stream, done, start_iter, classification=False)
@@ -511,21 +529,24 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                 self._predict_codes_into(self._eval["codes"], eval_scores, self.forest[:start_iter])
         done = 0
         stream = _RecordStream(rec)
-        with torch.no_grad():
-            for j in range(n_new):
-                i = start_iter + j
-                feat_sel = self._feature_subset(dev)
-                eng.round(labels, scores, feat_sel, {k: v[j] for k, v in rec.items()})
-                done = j + 1
-                stream.round_done(j)
-                if self._eval is not None:
-                    D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
-                                   rec["leaf"][j], 1, K, self.max_depth, self.learning_rate,
-                                   eval_scores)
-                    self._compute_eval_multiclass(i, labels, scores, eval_scores)
-                    if self.stop:
-                        break
-        stream.finish(done)
+        try:
+            with torch.no_grad():
+                for j in range(n_new):
+                    i = start_iter + j
+                    feat_sel = self._feature_subset(dev)
+                    eng.round(labels, scores, feat_sel, {k: v[j] for k, v in rec.items()})
+                    done = j + 1
+                    stream.round_done(j)
+                    if self._eval is not None:
+                        D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
+                                       rec["leaf"][j], 1, K, self.max_depth, self.learning_rate,
+                                       eval_scores)
+                        self._compute_eval_multiclass(i, labels, scores, eval_scores)
+                        if self.stop:
+                            break
+            stream.finish(done)
+        finally:
+            stream.close()
         self._phases.mark("rounds")
         eng.close()
         self._absorb_records(rec, stream, done, start_iter, classification=True)

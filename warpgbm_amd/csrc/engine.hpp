@@ -131,11 +131,11 @@ __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v);
 __global__ void split_f32_kernel(const float* G, const float* H, int32_t E, int32_t F,
                                  int32_t B, float mcw, float eps, float* gain_out,
                                  float* dir_out);
-__global__ void split_level_e1_kernel(const int64_t* hq, const int32_t* hc, int32_t F,
-                                      int32_t B, const int32_t* feat_sel, int32_t n_sel,
-                                      int32_t nodes_in_level, const int32_t* present,
-                                      const int32_t* shifts, float mcw, float eps,
-                                      float min_split_gain, unsigned long long* best);
+// split_level_e1_kernel over n_tn tree-nodes (a compile-time bin count for B = 32)
+int launch_split_level_e1(int n_tn, hipStream_t st, const int64_t* hq, const int32_t* hc,
+                          int32_t F, int32_t B, const int32_t* feat_sel, int32_t n_sel,
+                          int32_t nodes_in_level, const int32_t* present, const int32_t* shifts,
+                          float mcw, float eps, float min_split_gain, unsigned long long* best);
 __global__ void des_accumulate_kernel(const int64_t* hq, const int32_t* hc, int32_t F, int32_t B,
                                       int32_t E, const int32_t* feat_sel, int32_t n_sel,
                                       int32_t nodes_in_level, int32_t n_tn,

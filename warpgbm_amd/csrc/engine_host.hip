@@ -456,11 +456,9 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       // ---- split search + DES selection
       if (E == 1) {
         // the pick is decoded by level_finish
-        const int bpn = (n_sel + 255) / 256;
-        hipLaunchKernelGGL(split_level_e1_kernel, dim3((unsigned)(n_tn * bpn)), dim3(256), 0, st,
-                           e->hq[hcur], e->hc[hcur], F, B, feat_sel, n_sel, nodes,
-                           e->present[cur], e->shifts, mcw, eps, msg, best);
-        WGBM_LAUNCH_CHECK();
+        int r = launch_split_level_e1(n_tn, st, e->hq[hcur], e->hc[hcur], F, B, feat_sel, n_sel,
+                                      nodes, e->present[cur], e->shifts, mcw, eps, msg, best);
+        if (r) return r;
       } else {
         const int64_t ncand = (int64_t)n_sel * (B - 1);
         const int64_t nacc = (int64_t)n_tn * n_sel * ((B - 1 + kDesChunk - 1) / kDesChunk);

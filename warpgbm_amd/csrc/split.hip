@@ -39,12 +39,14 @@ struct ScanOut {
 template <typename LoadG, typename LoadH, typename Emit>
 __device__ inline void scan_bins(int B, float mcw, float eps, LoadG g, LoadH h, Emit emit) {
   float Gt = 0.0f, Ht = 0.0f;
+#pragma unroll
   for (int b = 0; b < B; ++b) {
     Gt = Gt + g(b);
     Ht = Ht + h(b);
   }
   float GL = 0.0f, HL = 0.0f;
   const float tot = (Gt * Gt) / (Ht + eps);
+#pragma unroll
   for (int b = 0; b < B - 1; ++b) {
     GL = GL + g(b);
     HL = HL + h(b);
@@ -103,11 +105,15 @@ __device__ inline bool des_segment_dead(int64_t n, float mcw) {
 // smaller flat index (torch.argmax takes the first).  Integer atomics make
 // the result independent of execution order.  best[tn] == 0: no split (every
 // real key is nonzero: gain_key(-inf) = 0x007fffff).
+// BT > 0: B known at compile time, and every bin of the lane's histogram is
+// loaded before the scan (one round trip instead of one per bin)
+template <int BT>
 __global__ __launch_bounds__(256) void split_level_e1_kernel(
-    const int64_t* __restrict__ hq, const int32_t* __restrict__ hc, int32_t F, int32_t B,
+    const int64_t* __restrict__ hq, const int32_t* __restrict__ hc, int32_t F, int32_t B_rt,
     const int32_t* __restrict__ feat_sel, int32_t n_sel, int32_t nodes_in_level,
     const int32_t* __restrict__ present, const int32_t* __restrict__ shifts, float mcw,
     float eps, float min_split_gain, unsigned long long* __restrict__ best) {
+  const int B = BT > 0 ? BT : B_rt;
   const int blocks_per_node = (n_sel + 255) / 256;
   const int tn = blockIdx.x / blocks_per_node;
   const int l = (blockIdx.x - tn * blocks_per_node) * 256 + threadIdx.x;
@@ -121,17 +127,28 @@ __global__ __launch_bounds__(256) void split_level_e1_kernel(
     const int64_t base = ((int64_t)tn * F + f) * B;
     const int64_t* q = hq + base;
     const int32_t* c = hc + base;
-    scan_bins(
-        B, mcw, eps, [&](int b) { return wgbm_dequantise(q[b], s); },
-        [&](int b) { return (float)c[b]; },
-        [&](int b, float gn, float d) {
-          (void)d;
-          const int idx = l * (B - 1) + b;
-          if (gn > min_split_gain && better(gn, idx, bg, bi)) {
-            bg = gn;
-            bi = idx;
-          }
-        });
+    auto emit = [&](int b, float gn, float d) {
+      (void)d;
+      const int idx = l * (B - 1) + b;
+      if (gn > min_split_gain && better(gn, idx, bg, bi)) {
+        bg = gn;
+        bi = idx;
+      }
+    };
+    if constexpr (BT > 0) {
+      float g[BT], h[BT];
+#pragma unroll
+      for (int b = 0; b < BT; ++b) {
+        g[b] = wgbm_dequantise(q[b], s);
+        h[b] = (float)c[b];
+      }
+      scan_bins(
+          BT, mcw, eps, [&](int b) { return g[b]; }, [&](int b) { return h[b]; }, emit);
+    } else {
+      scan_bins(
+          B, mcw, eps, [&](int b) { return wgbm_dequantise(q[b], s); },
+          [&](int b) { return (float)c[b]; }, emit);
+    }
   }
   for (int o = 32; o > 0; o >>= 1) {
     const float og = __shfl_xor(bg, o, 64);
@@ -873,6 +890,21 @@ __global__ void local_scatter_kernel(const int32_t* __restrict__ feat_sel, int32
     const int f = feat_sel[l];
     if (f >= 0 && f < F) local_of[f] = l;
   }
+}
+
+int launch_split_level_e1(int n_tn, hipStream_t st, const int64_t* hq, const int32_t* hc,
+                          int32_t F, int32_t B, const int32_t* feat_sel, int32_t n_sel,
+                          int32_t nodes_in_level, const int32_t* present, const int32_t* shifts,
+                          float mcw, float eps, float min_split_gain, unsigned long long* best) {
+  const dim3 grid((unsigned)(n_tn * ((n_sel + 255) / 256)));
+  if (B == 32)
+    hipLaunchKernelGGL(split_level_e1_kernel<32>, grid, dim3(256), 0, st, hq, hc, F, B, feat_sel,
+                       n_sel, nodes_in_level, present, shifts, mcw, eps, min_split_gain, best);
+  else
+    hipLaunchKernelGGL(split_level_e1_kernel<0>, grid, dim3(256), 0, st, hq, hc, F, B, feat_sel,
+                       n_sel, nodes_in_level, present, shifts, mcw, eps, min_split_gain, best);
+  WGBM_LAUNCH_CHECK();
+  return 0;
 }
 
 int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* codes,
