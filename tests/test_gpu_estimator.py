@@ -171,7 +171,7 @@ def test_int8_input_over_num_bins_is_quantile_binned(gpu):
 
 
 @pytest.mark.parametrize("layout", LAYOUTS)
-@pytest.mark.parametrize("mcw,B", [(1, 12), (20, 12), (1, 7), (20, 3)])
+@pytest.mark.parametrize("mcw,B", [(1, 12), (20, 12), (1, 7), (20, 3), (1, 2)])
 def test_era_des_colsample_uneven_eras_bit_exact(gpu, mcw, B, layout):
     """Direct era path (every era fits one LDS tile): uneven era sizes, eras
     that are empty at deeper nodes, a feature subset per tree, generic bin
