@@ -600,6 +600,9 @@ void des_pair_kernel(
   // lanes past the last feature re-read the last real pair word; their
   // words are never evaluated
   const uint32_t voff = (uint32_t)((f_base < F ? f_base : (F - 1) / (2 * LP) * (2 * LP)) / 2);
+  // raw buffer over the whole copy: stride 0, pbytes records (loads past
+  // them return 0), word 3 = 0x00020000 (DATA_FORMAT 32-bit: untyped buffer
+  // loads need a nonzero data format on gfx9-family targets)
   const __amdgpu_buffer_rsrc_t rsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)pcodes, (short)0, (int)pbytes, 0x00020000);
   // byte address of this lane's word 0 of pair table 0: lane * 8
