@@ -390,7 +390,7 @@ __global__ void des_finish_kernel(const unsigned long long* __restrict__ best,
 //     sum in double in era order (same values and order as des_accumulate).
 // ---------------------------------------------------------------------------
 constexpr int kDesEraThreads = 256;
-constexpr int kDesEraMaxWG = 4096;  // des_era grid bound (about 16 workgroups per CU)
+constexpr int kDesEraMaxWG = 8192;  // era kernels grid bound (32 workgroups per CU; 4096 and 16384 measured slower)
 
 template <int V, int BT>
 __global__ __launch_bounds__(kDesEraThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
