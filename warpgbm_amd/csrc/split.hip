@@ -585,7 +585,7 @@ void des_pair_kernel(
   constexpr int LP = kDesPairLanePairs;
   constexpr int CW = kDesPairChunk;
   constexpr int nwaves = kDesPairThreads / 64;
-  constexpr int U = 8;  // rows per group
+  constexpr int U = 16;  // rows per group
   constexpr int step = nwaves * U;
   constexpr int nb = BT - 1;
   extern __shared__ unsigned long long lds[];
