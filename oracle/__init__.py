@@ -15,7 +15,14 @@ Modules
   clib -- ctypes loader of ``csrc/oracle.c`` (gcc): exact histograms for
           large inputs and the fma-based exp used by the softmax residuals
 
-How each function is pinned (checked against something other than itself)
-is listed in tests/test_oracle_pins.py; a function without such a check
-would be marked "parity unpinned" here.  Currently: none.
+How each function is pinned (checked against something other than itself:
+brute force, the torch routine the reference calls, closed forms,
+invariants) is listed in the header of tests/test_oracle_pins.py, which
+covers every function here, including the start values of the fit
+(base_score, class_prior_logits, uniform_prior_logits) against torch's own
+float32 / float64 evaluation of the reference's expressions.  The literal
+float32 growth mode (gbm.Forest(..., literal_f32=True)) is the one part not
+held to bit equality: the reference's float32 atomics have no fixed order,
+so it is compared tree for tree with the exact mode, every difference
+required to be a near-tie.
 """

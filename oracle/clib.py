@@ -25,6 +25,10 @@ def lib():
         L.oracle_softmax_residual.argtypes = [p, p, i64, i32, p]
         L.oracle_softmax_rows.argtypes = [p, i64, i32]
         L.oracle_quantile_sorted.argtypes = [p, i64, p, i32, p]
+        L.oracle_quantile_edges_matrix.argtypes = [p, i64, i64, i64, p, i32, p]
+        L.oracle_bin_matrix.argtypes = [p, i64, i64, i64, p, i32, p, i64]
+        L.oracle_predict_tables.argtypes = [p, i64, i64, p, i32, i32, p, i32, C.c_float, p]
+        L.oracle_split_scan_q.argtypes = [p, p, i64, i32, i32, C.c_float, C.c_float, p, p]
         _lib = L
     return _lib
 
@@ -78,3 +82,55 @@ def softmax_rows(x):
     n, K = x.shape
     lib().oracle_softmax_rows(_ptr(x), n, K)
     return x
+
+
+def quantile_edges_matrix(X, num_bins):
+    """[F, B-1] torch.quantile edges of every column of the row-major float32
+    matrix X (the C loop of ops.quantile_edges, for full-size inputs)."""
+    from . import ops
+
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    n, F = X.shape
+    q = np.ascontiguousarray(ops.quantile_levels(num_bins), dtype=np.float32)
+    out = np.empty((F, num_bins - 1), np.float32)
+    lib().oracle_quantile_edges_matrix(_ptr(X), n, F, F, _ptr(q), len(q), _ptr(out))
+    return out
+
+
+def bin_matrix(X, edges):
+    """int8 codes [n, F] of X against edges [F, B-1] (ops.bin_matrix in C)."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    edges = np.ascontiguousarray(edges, dtype=np.float32)
+    n, F = X.shape
+    assert edges.shape[0] == F
+    out = np.empty((n, F), np.int8)
+    lib().oracle_bin_matrix(_ptr(X), n, F, F, _ptr(edges), edges.shape[1], _ptr(out), F)
+    return out
+
+
+def predict_tables(codes, tables, lr, out, cls=None):
+    """ops.predict_table in C over many trees: out [n, K] (or [n]) is updated
+    in tree order with float32(lr * leaf); tree t adds to column cls[t]."""
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    tables = np.ascontiguousarray(tables, dtype=np.float32)
+    T, M, _ = tables.shape
+    o = np.array(out, dtype=np.float32, copy=True, order="C")
+    K = 1 if o.ndim == 1 else o.shape[1]
+    c = None if cls is None else np.ascontiguousarray(cls, dtype=np.int32)
+    assert c is None or len(c) == T
+    lib().oracle_predict_tables(_ptr(codes), codes.shape[0], codes.shape[1], _ptr(tables), T, M,
+                                _ptr(c), K, np.float32(lr), _ptr(o))
+    return o
+
+
+def split_scan_q(Q, Cn, s, min_child_samples, eps):
+    """ops.split_scan(ops.dequantise(Q, s), float32(Cn), ...) in one C loop:
+    gain, dir [E, F, B-1] from exact histograms Q, Cn [E, F, B]."""
+    Q = np.ascontiguousarray(Q, dtype=np.int64)
+    Cn = np.ascontiguousarray(Cn, dtype=np.int64)
+    E, F, B = Q.shape
+    gain = np.empty((E, F, B - 1), np.float32)
+    dirn = np.empty((E, F, B - 1), np.float32)
+    lib().oracle_split_scan_q(_ptr(Q), _ptr(Cn), E * F, B, int(s), np.float32(min_child_samples),
+                              np.float32(eps), _ptr(gain), _ptr(dirn))
+    return gain, dirn

@@ -10,10 +10,19 @@
  *    degree-7 Taylor polynomial in Horner form with fmaf, ldexpf scaling)
  *    so that results are reproducible to the bit on any IEEE machine.
  *
- * Built by oracle/build.py with gcc -O2 -ffp-contract=off.
+ *  - oracle_quantile_edges_matrix / oracle_bin_matrix / oracle_predict_tables:
+ *    the quantile edges of core.py:527-533 (torch.quantile over each sorted
+ *    column), binner.cu:12-25 and predict.cu:13-44, for full-size checks.
+ *
+ * The loops over independent features / columns / rows run on OpenMP
+ * threads; every output element is produced by one thread in a fixed order,
+ * so results do not depend on the thread count.
+ *
+ * Built by oracle/build.py with gcc -O2 -fopenmp -ffp-contract=off.
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 void oracle_hist_exact(const int8_t* codes, int64_t stride, const int32_t* q,
@@ -21,21 +30,31 @@ void oracle_hist_exact(const int8_t* codes, int64_t stride, const int32_t* q,
                        int32_t n_feats, const int32_t* era, int32_t num_eras, int32_t num_bins,
                        int64_t* Q, int64_t* C) {
   const int64_t per_era = (int64_t)n_feats * num_bins;
-  memset(Q, 0, sizeof(int64_t) * per_era * num_eras);
-  memset(C, 0, sizeof(int64_t) * per_era * num_eras);
-  for (int64_t p = 0; p < n_rows; ++p) {
-    const int64_t s = rows ? rows[p] : p;
-    const int e = num_eras == 1 ? 0 : era[s];
-    if (e < 0 || e >= num_eras) continue;
-    const int8_t* row = codes + s * stride;
-    const int64_t qs = q[s];
-    int64_t* Qe = Q + e * per_era;
-    int64_t* Ce = C + e * per_era;
-    for (int32_t f = 0; f < n_feats; ++f) {
-      const int b = row[feats ? feats[f] : f];
-      if (b < 0 || b >= num_bins) continue;
-      Qe[(int64_t)f * num_bins + b] += qs;
-      Ce[(int64_t)f * num_bins + b] += 1;
+  /* each thread owns a range of features: it reads those bytes of every row
+   * and is the only writer of their bins */
+  const int32_t fblk = 32;
+  const int32_t nblk = (n_feats + fblk - 1) / fblk;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int32_t kb = 0; kb < nblk; ++kb) {
+    const int32_t f0 = kb * fblk, f1 = f0 + fblk < n_feats ? f0 + fblk : n_feats;
+    for (int e = 0; e < num_eras; ++e) {
+      memset(Q + e * per_era + (int64_t)f0 * num_bins, 0, sizeof(int64_t) * (f1 - f0) * num_bins);
+      memset(C + e * per_era + (int64_t)f0 * num_bins, 0, sizeof(int64_t) * (f1 - f0) * num_bins);
+    }
+    for (int64_t p = 0; p < n_rows; ++p) {
+      const int64_t s = rows ? rows[p] : p;
+      const int e = num_eras == 1 ? 0 : era[s];
+      if (e < 0 || e >= num_eras) continue;
+      const int8_t* row = codes + s * stride;
+      const int64_t qs = q[s];
+      int64_t* Qe = Q + e * per_era;
+      int64_t* Ce = C + e * per_era;
+      for (int32_t f = f0; f < f1; ++f) {
+        const int b = row[feats ? feats[f] : f];
+        if (b < 0 || b >= num_bins) continue;
+        Qe[(int64_t)f * num_bins + b] += qs;
+        Ce[(int64_t)f * num_bins + b] += 1;
+      }
     }
   }
 }
@@ -112,5 +131,128 @@ void oracle_softmax_rows(float* x, int64_t n, int32_t K) {
       s = s + v[k];
     }
     for (int k = 0; k < K; ++k) v[k] = v[k] / s;
+  }
+}
+
+/* ---- full-size helpers ------------------------------------------------- */
+
+/* order-preserving key of a float (NaN above +inf, -0.0 just below +0.0) */
+static inline uint32_t f32_key(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if (x != x) return 0xffffffffu;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+/* ascending sort of n floats by their key (LSD radix, 4 passes of 8 bits) */
+static void sort_f32(float* a, float* tmp, int64_t n) {
+  for (int pass = 0; pass < 4; ++pass) {
+    int64_t cnt[257];
+    memset(cnt, 0, sizeof(cnt));
+    const int sh = pass * 8;
+    for (int64_t i = 0; i < n; ++i) cnt[((f32_key(a[i]) >> sh) & 255u) + 1]++;
+    for (int k = 0; k < 256; ++k) cnt[k + 1] += cnt[k];
+    for (int64_t i = 0; i < n; ++i) tmp[cnt[(f32_key(a[i]) >> sh) & 255u]++] = a[i];
+    memcpy(a, tmp, sizeof(float) * n);
+  }
+}
+
+/* edges[f, j] = torch.quantile(X[:, f], q[j]) for every column f of the
+ * row-major X [n, ldx]: the column sorted (NaN last), then the linear
+ * interpolation of oracle_quantile_sorted */
+void oracle_quantile_edges_matrix(const float* X, int64_t n, int64_t F, int64_t ldx,
+                                  const float* q, int32_t nq, float* edges) {
+  if (n <= 0) {
+    for (int64_t k = 0; k < F * nq; ++k) edges[k] = NAN;
+    return;
+  }
+#pragma omp parallel
+  {
+    float* col = (float*)malloc(sizeof(float) * (n > 0 ? n : 1));
+    float* tmp = (float*)malloc(sizeof(float) * (n > 0 ? n : 1));
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t f = 0; f < F; ++f) {
+      for (int64_t i = 0; i < n; ++i) col[i] = X[i * ldx + f];
+      sort_f32(col, tmp, n);
+      oracle_quantile_sorted(col, n, q, nq, edges + f * nq);
+    }
+    free(col);
+    free(tmp);
+  }
+}
+
+/* codes[i, f] = number of leading edges e[f, j] with x >= e (binner.cu:17-23:
+ * the scan stops at the first edge x is below; NaN -> 0) */
+void oracle_bin_matrix(const float* X, int64_t n, int64_t F, int64_t ldx, const float* edges,
+                       int32_t ne, int8_t* codes, int64_t ldc) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    for (int64_t f = 0; f < F; ++f) {
+      const float x = X[i * ldx + f];
+      const float* e = edges + f * ne;
+      int b = 0;
+      while (b < ne && x >= e[b]) ++b;
+      codes[i * ldc + f] = (int8_t)b;
+    }
+  }
+}
+
+/* out[i, cls[t]] = out[i, cls[t]] + lr * leaf_t(i) for t = 0..T-1 in order,
+ * leaf_t(i) found by walking the pre-order table tables[t] [M, 6]
+ * (feature, bin, left, right, is_leaf, value): while is_leaf <= 0.5,
+ * code <= bin goes left (predict.cu:23-44) */
+void oracle_predict_tables(const int8_t* codes, int64_t n, int64_t ldc, const float* tables,
+                           int32_t T, int32_t M, const int32_t* cls, int32_t K, float lr,
+                           float* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    const int8_t* row = codes + i * ldc;
+    for (int32_t t = 0; t < T; ++t) {
+      const float* tb = tables + (int64_t)t * M * 6;
+      int32_t nd = 0;
+      int guard = 0;
+      while (tb[nd * 6 + 4] <= 0.5f && guard++ <= M) {
+        const int32_t f = (int32_t)tb[nd * 6 + 0];
+        const int32_t b = (int32_t)tb[nd * 6 + 1];
+        nd = (int32_t)(row[f] <= b ? tb[nd * 6 + 2] : tb[nd * 6 + 3]);
+      }
+      const float v = lr * tb[nd * 6 + 5];
+      float* o = out + i * K + (cls ? cls[t] : 0);
+      *o = *o + v;
+    }
+  }
+}
+
+/* Per-era gain and direction of best_split_kernel.cu:25-54 (the restatement
+ * of ops.split_scan) straight from exact histograms: G = float(ldexp(Q, -s)),
+ * H = float(C), then sequential float32 totals and prefix; gain/dir are
+ * [EF, B-1] for the EF (era, feature) rows of Q, C [EF, B]. */
+void oracle_split_scan_q(const int64_t* Q, const int64_t* Cn, int64_t EF, int32_t B, int32_t s,
+                         float mcw, float eps, float* gain, float* dirn) {
+#pragma omp parallel for schedule(static)
+  for (int64_t k = 0; k < EF; ++k) {
+    const int64_t* q = Q + k * B;
+    const int64_t* c = Cn + k * B;
+    float Gt = 0.0f, Ht = 0.0f;
+    for (int32_t b = 0; b < B; ++b) {
+      Gt = Gt + (float)ldexp((double)q[b], -s);
+      Ht = Ht + (float)c[b];
+    }
+    const float tot = (Gt * Gt) / (Ht + eps);
+    float GL = 0.0f, HL = 0.0f;
+    for (int32_t b = 0; b + 1 < B; ++b) {
+      GL = GL + (float)ldexp((double)q[b], -s);
+      HL = HL + (float)c[b];
+      const float GR = Gt - GL, HR = Ht - HL;
+      float g = 0.0f, d = 0.0f;
+      if (HL >= mcw && HR >= mcw) {
+        const float a = (GL * GL) / (HL + eps);
+        const float r = (GR * GR) / (HR + eps);
+        g = (a + r) - tot;
+        d = GL / (HL + eps) > GR / (HR + eps) ? 1.0f : -1.0f;
+      }
+      gain[k * (B - 1) + b] = g;
+      dirn[k * (B - 1) + b] = d;
+    }
   }
 }

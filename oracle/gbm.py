@@ -22,7 +22,7 @@ class TreeGrower:
     """Grows one tree given the residual of the tree (fixed, core.py:719)."""
 
     def __init__(self, codes, era_idx, E, B, max_depth, min_child_weight, min_split_gain,
-                 L2_reg, feat_sel, qbits, hist=None):
+                 L2_reg, feat_sel, qbits, hist=None, scan=None):
         self.codes = codes
         self.era = era_idx
         self.E = E
@@ -34,6 +34,9 @@ class TreeGrower:
         self.feat_sel = np.asarray(feat_sel, dtype=np.int64)
         self.qbits = qbits
         self.hist = hist or ops.histogram_exact_q
+        # (Q, C, shift) -> per-era gain, dir; clib.split_scan_q is the same in C
+        self.scan = scan or (lambda Q, C, s, mcw, eps: ops.split_scan(
+            ops.dequantise(Q, s), C.astype(F32), mcw, eps))
         self.splits = []  # (global feature, per-era gains) in DFS pre-order
 
     def grow(self, resid, rows):
@@ -55,9 +58,7 @@ class TreeGrower:
     def _node(self, Q, C, rows, depth):
         if depth == self.max_depth:
             return self._leaf(rows)
-        G = ops.dequantise(Q, self.s)
-        H = C.astype(F32)
-        gain, dirn = ops.split_scan(G, H, self.mcw, self.eps)
+        gain, dirn = self.scan(Q, C, self.s, self.mcw, self.eps)
         lf, b = ops.des_select(gain, dirn, self.msg)
         if lf == -1:
             return self._leaf(rows)
@@ -105,12 +106,12 @@ class Forest:
         self.msg = min_split_gain
         self.eps = L2_reg
 
-    def fit_codes(self, codes, y, era_id=None, feat_sets=None, hist=None):
+    def fit_codes(self, codes, y, era_id=None, feat_sets=None, hist=None, scan=None):
         codes = np.asarray(codes)
         N, F = codes.shape
         if era_id is None:
             era_id = np.ones(N, dtype=np.int32)
-        uniq, inv = np.unique(era_id, return_inverse=True)
+        uniq, inv = np.unique(era_ids_int32(era_id), return_inverse=True)
         self.E = len(uniq)
         era = inv.astype(np.int64).reshape(-1)
         self.num_features = F
@@ -120,13 +121,13 @@ class Forest:
         self.forest = []
         if self.objective == "regression":
             Y = np.asarray(y, dtype=F32)
-            self.base = F32(np.mean(Y, dtype=np.float64))
+            self.base = base_score(Y)
             preds = np.full(N, self.base, F32)
             for i in range(self.n_estimators):
                 fs = np.arange(F) if feat_sets is None else feat_sets[i]
                 resid = Y - preds
                 g = TreeGrower(codes, era, self.E, self.B, self.max_depth, self.mcw, self.msg,
-                               self.eps, fs, qbits, hist)
+                               self.eps, fs, qbits, hist, scan)
                 tree = g.grow(resid, rows)
                 for rws, v in g.leaf_rows:
                     preds[rws] = preds[rws] + F32(self.lr) * v
@@ -144,7 +145,7 @@ class Forest:
                 trees = []
                 for k in range(K):
                     g = TreeGrower(codes, era, self.E, self.B, self.max_depth, self.mcw,
-                                   self.msg, self.eps, fs, qbits, hist)
+                                   self.msg, self.eps, fs, qbits, hist, scan)
                     tree = g.grow(res[k], rows)
                     for rws, v in g.leaf_rows:
                         scores[rws, k] = scores[rws, k] + F32(self.lr) * v
@@ -177,9 +178,26 @@ class Forest:
         return clib.softmax_rows(out)
 
 
+def era_ids_int32(era_id):
+    """The era ids after the reference's ``.type(torch.int32)`` (core.py:493):
+    a C cast -- floats truncated toward zero, wider integers wrapped to 32
+    bits, bools 0/1."""
+    return np.asarray(era_id).reshape(-1).astype(np.int32, casting="unsafe")
+
+
+def base_score(Y):
+    """The regression start value Y.mean() (core.py:387) as the float32
+    nearest the exact mean of the float32 targets (float64 pairwise sum, one
+    division, one rounding).  The reference's torch float32 reduction is
+    within a few ulps of it in an order no other device reproduces."""
+    return F32(np.mean(np.asarray(Y, dtype=F32), dtype=np.float64))
+
+
 def class_prior_logits(labels, K):
-    """log(prior_k + 1e-10), prior_k = float32(count_k) / float32(n)
-    (core.py:452-456)."""
+    """log(prior_k + 1e-10) for every class present, 0 for an absent class
+    (core.py:450-456): prior_k = float32(count_k) / float32(n), + 1e-10 in
+    float32, and the float32 nearest the natural log of that (torch.log is
+    within 1 ulp of it)."""
     n = F32(len(labels))
     out = np.zeros(K, F32)
     for k in range(K):
@@ -190,5 +208,7 @@ def class_prior_logits(labels, K):
 
 
 def uniform_prior_logits(K):
-    """log(float32(1/K + 1e-10)) (core.py:1004-1007)."""
-    return np.full(K, F32(np.log(np.float64(F32(1.0 / K + 1e-10)))), F32)
+    """The start logits of predict_proba (core.py:1003-1007): 1/K + 1e-10 and
+    its log in float64 (a numpy float64 wrapped by torch.tensor), rounded to
+    float32 once when stored into the float32 score matrix."""
+    return np.full(K, F32(np.log(np.float64(1.0) / np.float64(K) + 1e-10)), F32)

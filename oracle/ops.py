@@ -288,10 +288,13 @@ def predict_table(codes, table, lr, out):
             active &= ~is_leaf
             if not active.any():
                 break
-            feat = nd[:, 0].astype(np.int64)
-            sb = nd[:, 1].astype(np.int64)
+            # rows already at a leaf (or on NaN padding) read column 0 and
+            # keep their node: only the active rows' fields are cast
+            nd_act = np.where(active[:, None], nd, F32(0))
+            feat = nd_act[:, 0].astype(np.int64)
+            sb = nd_act[:, 1].astype(np.int64)
             c = codes[np.arange(N), np.clip(feat, 0, codes.shape[1] - 1)].astype(np.int64)
-            nxt = np.where(c <= sb, nd[:, 2], nd[:, 3]).astype(np.int64)
+            nxt = np.where(c <= sb, nd_act[:, 2], nd_act[:, 3]).astype(np.int64)
             node = np.where(active, nxt, node)
         out = out + lr * leafv
     return out.astype(F32)

@@ -124,14 +124,19 @@ def test_flatten_tree_matches_reference_layout():
 
 
 def test_era_layout_matches_unique_sort():
-    """The era bookkeeping (warpgbm/core.py:540: sorted unique eras, inverse
-    indices, stable era order, offsets) equals the np.unique + stable argsort
-    restatement, including the linear path for non-decreasing era ids."""
+    """The era bookkeeping (warpgbm/core.py:493 and :540: era ids cast to
+    int32, then sorted unique eras, inverse indices, stable era order,
+    offsets) equals torch's own cast + torch.unique followed by a stable
+    argsort, including the linear path for non-decreasing era ids."""
+    import torch
+
     from warpgbm_amd import device as D
 
     def by_sort(era):
-        uniq, inv = np.unique(np.asarray(era), return_inverse=True)
-        inv = inv.astype(np.int32).reshape(-1)
+        t = torch.from_numpy(np.asarray(era)).type(torch.int32)
+        uniq, inv = torch.unique(t, sorted=True, return_inverse=True)
+        uniq = uniq.numpy()
+        inv = inv.numpy().astype(np.int32).reshape(-1)
         order = np.argsort(inv, kind="stable").astype(np.int32)
         counts = np.bincount(inv, minlength=len(uniq)).astype(np.int64)
         start = np.zeros(len(uniq) + 1, dtype=np.int64)
@@ -141,9 +146,32 @@ def test_era_layout_matches_unique_sort():
     rng = np.random.default_rng(0)
     cases = [np.ones(10, np.int32), np.repeat(np.arange(5), 7), np.array([3]),
              np.repeat([-2, 0, 5, 9], [1, 4, 2, 3]), rng.integers(0, 4, 50),
-             np.sort(rng.integers(0, 9, 100)), np.repeat(np.array(["a", "b", "c"]), 3),
-             np.array([1.5, 1.5, 2.0]), np.array([2, 2, 1, 1])]
+             np.sort(rng.integers(0, 9, 100)), np.array([1.5, 1.5, 2.0]), np.array([2, 2, 1, 1]),
+             np.array([1.2, 1.7, 0.4, -0.6, 2.9]), np.array([2**32 + 5, 5, -1], np.int64),
+             np.array([True, False, True]), rng.integers(0, 3, 40).astype(np.uint8)]
     for era in cases:
         got, ref = D.era_layout(era), by_sort(era)
         for a, b in zip(got, ref):
             assert np.array_equal(a, b) and a.dtype == b.dtype, era
+    # the reference's float -> int32 truncation: 1.2 and 1.7 are one era
+    assert len(D.era_layout(np.array([1.2, 1.7]))[0]) == 1
+    # int64 ids wrap to 32 bits as in torch: 2^32 + 5 and 5 are one era
+    assert len(D.era_layout(np.array([2**32 + 5, 5], np.int64))[0]) == 1
+    # torch.from_numpy refuses strings, as the reference's fit does
+    with pytest.raises(TypeError):
+        D.era_layout(np.array(["a", "b"]))
+
+
+def test_oracle_era_cast_matches_torch():
+    """The oracle's era cast (numpy C cast) equals torch's .type(torch.int32)
+    (warpgbm/core.py:493) on floats, wide and unsigned integers and bools."""
+    import torch
+
+    from oracle import gbm
+
+    rng = np.random.default_rng(1)
+    for era in (rng.standard_normal(200) * 50, np.array([1.2, 1.7, -0.5, -1.9]),
+                rng.integers(-2**40, 2**40, 100), rng.integers(0, 200, 64).astype(np.uint8),
+                np.array([True, False]), rng.integers(0, 9, 30).astype(np.int16)):
+        want = torch.from_numpy(np.asarray(era)).type(torch.int32).numpy()
+        assert np.array_equal(gbm.era_ids_int32(era), want), era.dtype

@@ -3,14 +3,21 @@
 C2: root and 16-node histograms of 1,000,000 x 1,000 int8 codes, bit-exact
 (exact integer sums, one float32 rounding), plus size-independent invariants:
 every feature counts every row, and the 16 nodes add up to the root exactly.
-C4: 500,000 x 2,000 pre-binned codes with 500 eras (the benchmark's own
-inputs), two trees of depth 2 grown by the direct era path, tree for tree and
-importance bit for bit equal to the oracle's recursive growth."""
+C3 (1M x 1000 float32, 32 bins, depth 5, 100 trees, lr 0.01): quantile edges
+and codes bit-exact, the first 3 trees identical to the oracle's recursive
+growth, and the predictions of all 100 trees on the training rows and on 1M
+held-out rows bit-exact against the oracle's traversal of the fitted forest.
+C4 (500k x 2000 pre-binned, 500 eras): two trees at the config's full depth 8
+through the era path, tree for tree and importance bit for bit.
+C5 (200k x 100, 10 classes, depth 6, 200 rounds): edges, codes and the first 2
+rounds (20 trees) identical; predict_proba of all 2000 trees on 1M rows
+bit-exact against the oracle's traversal + uniform prior + softmax.
+"""
 import numpy as np
 import pytest
 import torch
 
-from bench import c2_inputs, c4_inputs
+from bench import c2_inputs, c3_inputs, c4_inputs, c5_inputs
 from oracle import clib, gbm, ops
 from tests.conftest import print_case
 from warpgbm_amd import WarpGBM, _lib
@@ -84,19 +91,95 @@ def test_c2_full_size_histograms_bit_exact(gpu):
     torch.cuda.empty_cache()
 
 
-def test_c4_full_size_first_levels_bit_exact(gpu):
-    print_case("fullsize", "C4 500k x 2000, 500 eras, 2 trees depth 2")
+def _leaf_rows(node):
+    if "leaf_value" in node:
+        return node["samples"]
+    return _leaf_rows(node["left"]) + _leaf_rows(node["right"])
+
+
+def _gpu_codes(m, X):
+    """The codes fit bins X to: the library's binner with the model's edges."""
+    Xd = D.upload_float(X, torch.device("cuda:0"))
+    c = D.bin_matrix(Xd, torch.as_tensor(m.bin_edges), with_cm=False)
+    out = c.rm[:, :X.shape[1]].cpu().numpy()
+    del Xd, c
+    return out
+
+
+def _tables(trees, max_depth):
+    return np.stack([ops.flatten_tree(t, 2 ** (max_depth + 1)) for t in trees])
+
+
+@pytest.fixture(scope="module")
+def c3_fit(gpu):
+    print_case("fullsize", "C3 fit 1M x 1000, 100 trees depth 5")
+    X, y = c3_inputs(1_000_000, 1000, 0)
+    m = WarpGBM(num_bins=32, max_depth=5, n_estimators=100, learning_rate=0.01)
+    m.fit(X, y)
+    edges = clib.quantile_edges_matrix(X, 32)
+    codes = clib.bin_matrix(X, edges)
+    return X, y, m, edges, codes
+
+
+def test_c3_full_size_edges_codes_and_first_trees(c3_fit):
+    X, y, m, edges, codes = c3_fit
+    print_case("fullsize", "C3 edges, codes, first 3 trees")
+    assert np.array_equal(bits(torch.as_tensor(m.bin_edges).cpu().numpy()), bits(edges))
+    assert np.array_equal(_gpu_codes(m, X), codes)
+    ref = gbm.Forest(num_bins=32, max_depth=5, n_estimators=3, learning_rate=0.01).fit_codes(
+        codes, y, hist=clib.hist_exact_q, scan=clib.split_scan_q)
+    assert m.base_prediction == float(ref.base)
+    for i in range(3):
+        assert m.forest[i] == ref.forest[i], f"tree {i} differs"
+        assert _leaf_rows(m.forest[i]) == len(y)
+
+
+def test_c3_full_size_predictions_bit_exact(c3_fit):
+    X, y, m, edges, codes = c3_fit
+    print_case("fullsize", "C3 predictions, training rows and 1M held-out rows")
+    tabs = _tables(m.forest, 5)
+    base = np.full(len(y), np.float32(m.base_prediction), F32)
+    want = clib.predict_tables(codes, tabs, 0.01, base)
+    assert np.array_equal(bits(m.predict(X)), bits(want))
+    Xt, yt = c3_inputs(1_000_000, 1000, 1)
+    got = m.predict(Xt)
+    want_t = clib.predict_tables(clib.bin_matrix(Xt, edges), tabs, 0.01, base)
+    assert np.array_equal(bits(got), bits(want_t))
+    assert np.corrcoef(got, yt)[0, 1] > 0.7
+
+
+def test_c4_full_size_depth8_bit_exact(gpu):
+    print_case("fullsize", "C4 500k x 2000, 500 eras, 2 trees depth 8")
     X, y, era = c4_inputs()
-    kw = dict(num_bins=5, max_depth=2, n_estimators=2, learning_rate=0.5)
+    kw = dict(num_bins=5, max_depth=8, n_estimators=2, learning_rate=0.1)
     m = WarpGBM(**kw).fit(X, y, era_id=era)
-    ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era, hist=clib.hist_exact_q)
+    ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era, hist=clib.hist_exact_q,
+                                     scan=clib.split_scan_q)
     for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
         assert a == b, f"tree {i} differs"
+        assert _leaf_rows(a) == len(y)  # every row in one leaf
     assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
 
-    def leaf_rows(node):
-        if "leaf_value" in node:
-            return node["samples"]
-        return leaf_rows(node["left"]) + leaf_rows(node["right"])
 
-    assert all(leaf_rows(tree) == len(y) for tree in m.forest)  # every row in one leaf
+def test_c5_full_size_rounds_and_predict_proba_bit_exact(gpu):
+    print_case("fullsize", "C5 200k x 100, K=10, depth 6, 200 rounds")
+    X, lab = c5_inputs()
+    kw = dict(objective="multiclass", num_bins=32, max_depth=6, learning_rate=0.1)
+    m = WarpGBM(n_estimators=200, **kw).fit(X, lab)
+    edges = clib.quantile_edges_matrix(X, 32)
+    assert np.array_equal(bits(torch.as_tensor(m.bin_edges).cpu().numpy()), bits(edges))
+    codes = clib.bin_matrix(X, edges)
+    assert np.array_equal(_gpu_codes(m, X), codes)
+    ref = gbm.Forest(n_estimators=2, **kw).fit_codes(codes, lab, hist=clib.hist_exact_q,
+                                                     scan=clib.split_scan_q)
+    for i in range(2):
+        assert m.forest[i] == ref.forest[i], f"round {i} differs"
+    print_case("fullsize", "C5 predict_proba on 1M rows")
+    Xt, lt = c5_inputs(rows_per_class=100_000, seed=1)
+    got = m.predict_proba(Xt)
+    trees = [t for rnd in m.forest for t in rnd]
+    cls = np.tile(np.arange(10, dtype=np.int32), len(m.forest))
+    start = np.tile(gbm.uniform_prior_logits(10), (len(lt), 1))
+    logits = clib.predict_tables(clib.bin_matrix(Xt, edges), _tables(trees, 6), 0.1, start, cls)
+    assert np.array_equal(bits(got), bits(clib.softmax_rows(logits)))
+    assert (got.argmax(axis=1) == lt).mean() > 0.95

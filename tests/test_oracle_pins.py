@@ -21,6 +21,16 @@ off-by-one bin or transposed index fails.
   gbm.Forest / TreeGrower   planted split found; leaf = group mean; train
                             preds == predict; min_child respected
   clib.expf / softmax       numpy float64 exp within 2 ulp; rows sum to 1
+  gbm.base_score            float32 nearest the exact rational mean; torch's
+                            CPU float32 Y.mean() within 4 ulp
+  gbm.class_prior_logits    torch CPU float32 log((y == k).float().mean()
+                            + 1e-10) within 1 ulp; hand values; absent class 0
+  gbm.uniform_prior_logits  torch evaluating core.py:1003-1007 literally
+                            (float64 log, float32 store), bit-exact, K=2..3000
+  gbm.era_ids_int32         torch .type(torch.int32) (test_api_validation.py)
+  clib.quantile_edges_matrix / bin_matrix / predict_tables / split_scan_q
+                            (the C loops of the full-size checks) equal to the
+                            pinned numpy restatements above, bit for bit
 """
 import math
 from fractions import Fraction
@@ -464,3 +474,154 @@ def test_softmax_rows_sum_to_one():
     ref /= ref.sum(axis=1, keepdims=True)
     assert np.allclose(p.sum(axis=1), 1.0, atol=1e-6)
     assert np.allclose(p, ref, rtol=1e-5, atol=1e-7)
+
+
+# --------------------------------------------------------------------------- start values
+def _f32_nearest(fr):
+    """The float32 nearest the rational fr (ties to even), by exact comparison
+    of the neighbours of a first guess."""
+    x = F32(float(fr))
+    cands = [np.nextafter(x, F32(-np.inf)), x, np.nextafter(x, F32(np.inf))]
+    best = min(cands, key=lambda c: (abs(Fraction(float(c)) - fr),
+                                     int(np.asarray(c, F32).view(np.uint32)) & 1))
+    return F32(best)
+
+
+def _ulps(a, b):
+    ia = np.asarray(a, F32).view(np.int32).astype(np.int64)
+    ib = np.asarray(b, F32).view(np.int32).astype(np.int64)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("n,loc,seed", [(1, 0.0, 0), (7, 3.0, 1), (1000, 1000.0, 2),
+                                        (200_000, 0.0, 3), (200_000, 1000.0, 4)])
+def test_base_score_is_nearest_float_to_exact_mean(n, loc, seed):
+    """Y.mean() (core.py:387): the float32 nearest the exact mean.  A float32
+    running sum -- a plausible slip -- is off by many ulps on the offset
+    targets (loc = 1000), and a dropped row changes the mean."""
+    rng = np.random.default_rng(seed)
+    y = (loc + rng.standard_normal(n)).astype(F32)
+    exact = sum((Fraction(float(v)) for v in y), Fraction(0)) / n
+    want = _f32_nearest(exact)
+    assert gbm.base_score(y) == want
+    if n >= 1000 and loc != 0.0:
+        run = F32(0)
+        for v in y[:20000]:
+            run = F32(run + v)
+        sub_exact = _f32_nearest(sum((Fraction(float(v)) for v in y[:20000]), Fraction(0)) / 20000)
+        assert run / F32(20000) != sub_exact  # the slip is caught by this check
+
+
+def test_base_score_vs_torch_float32_mean():
+    """torch's own float32 mean (the reference's call, on the CPU here) agrees
+    within 4 ulp up to 2M rows; it reduces in float32 in its own order, so
+    equality is not expected."""
+    rng = np.random.default_rng(5)
+    for n in (10, 1000, 123_457, 2_000_000):
+        y = (rng.standard_normal(n) * 7.0 + 3.0).astype(F32)
+        t = F32(torch.from_numpy(y).mean().item())
+        assert _ulps(gbm.base_score(y), t) <= 4, n
+
+
+def test_class_prior_logits_vs_torch():
+    """log((y == k).float().mean() + 1e-10) per present class (core.py:450-456)
+    against torch's CPU float32 evaluation: within 1 ulp everywhere (torch's
+    float32 log is not correctly rounded) and identical almost everywhere.
+    A uniform prior, a log10, or a log of an absent class (-23.03 instead of
+    the 0 the reference leaves) would fail."""
+    rng = np.random.default_rng(6)
+    diff = total = 0
+    for _ in range(300):
+        n = int(rng.integers(2, 50_000))
+        K = int(rng.integers(2, 12))
+        p = rng.dirichlet(np.ones(K))
+        lab = rng.choice(K, size=n, p=p).astype(np.int32)
+        lab[lab == K - 1] = 0  # class K-1 absent
+        got = gbm.class_prior_logits(lab, K)
+        t = torch.from_numpy(lab)
+        want = np.zeros(K, F32)
+        for k in range(K):
+            pk = (t == k).float().mean()
+            if pk > 0:
+                want[k] = F32(torch.log(pk + 1e-10).item())
+        assert got[K - 1] == 0.0
+        u = _ulps(got, want)
+        assert u.max() <= 1
+        diff += int(np.count_nonzero(u))
+        total += K
+    assert diff <= total // 500
+    # hand values: a 3:1 split
+    v = gbm.class_prior_logits(np.array([0, 0, 0, 1], np.int32), 2)
+    assert v[0] == F32(math.log(0.75)) and v[1] == F32(math.log(0.25))
+
+
+def test_uniform_prior_logits_vs_reference_expression():
+    """predict_proba's start logits, evaluated as core.py:1003-1007 writes
+    them (numpy 1/K, + 1e-10, torch.tensor -> float64 log, stored into a
+    float32 tensor), bit-exact for K = 2..3000.  Rounding 1/K + 1e-10 to
+    float32 before the log (a plausible slip) differs at K = 47."""
+    for K in range(2, 3001):
+        classes = np.arange(K)
+        F = torch.zeros((1, K), dtype=torch.float32)
+        for k in (0, K - 1):
+            prior_k = (classes == classes[k]).sum() / len(classes)
+            F[:, k] = torch.log(torch.tensor(prior_k + 1e-10))
+        got = gbm.uniform_prior_logits(K)
+        assert got[0] == F[0, 0].item() and got[-1] == F[0, K - 1].item(), K
+    slip = F32(np.log(np.float64(F32(1.0 / 47 + 1e-10))))
+    assert slip != gbm.uniform_prior_logits(47)[0]
+
+
+# --------------------------------------------------------------------------- full-size C loops
+def test_clib_edges_and_codes_equal_numpy_restatement():
+    rng = np.random.default_rng(11)
+    X = rng.standard_normal((3001, 23)).astype(F32)
+    X[:, 2] = np.round(X[:, 2])            # heavy ties
+    X[::50, 4] = np.nan                    # a NaN column: all edges NaN
+    X[:, 5] = 7.0                          # constant column
+    X[:, 6] = np.abs(X[:, 6]) + 1.0        # positive only
+    for B in (2, 5, 32, 127):
+        e_np = ops.quantile_edges(X, B)
+        e_c = clib.quantile_edges_matrix(X, B)
+        # bit-exact, except that an edge on a zero may carry either sign: a
+        # comparison sort leaves -0.0 and +0.0 in input order, the radix key
+        # (the GPU's) puts -0.0 first; the codes cannot differ
+        same = (e_np.view(np.uint32) == e_c.view(np.uint32)) | ((e_np == 0) & (e_c == 0))
+        assert same.all(), B
+        assert np.array_equal(ops.bin_matrix(X, e_np), clib.bin_matrix(X, e_np)), B
+
+
+def test_clib_split_scan_q_equals_numpy():
+    rng = np.random.default_rng(12)
+    for _ in range(25):
+        E, F, B = int(rng.integers(1, 5)), int(rng.integers(1, 30)), int(rng.integers(2, 40))
+        C = rng.integers(0, 60, (E, F, B))
+        Q = rng.integers(-2**27, 2**27, (E, F, B)) * C
+        s = int(rng.integers(8, 30))
+        mcw = float(rng.integers(1, 40))
+        g1, d1 = ops.split_scan(ops.dequantise(Q, s), C.astype(F32), mcw, 1e-6)
+        g2, d2 = clib.split_scan_q(Q, C, s, mcw, 1e-6)
+        assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32))
+        assert np.array_equal(d1, d2)
+
+
+def test_clib_predict_tables_equals_numpy_and_dict_walk():
+    rng = np.random.default_rng(13)
+    N, F, B, K = 700, 9, 8, 3
+    X = rng.standard_normal((N, F)).astype(F32)
+    codes = ops.bin_matrix(X, ops.quantile_edges(X, B))
+    y = rng.integers(0, K, N)
+    f = gbm.Forest(objective="multiclass", num_bins=B, max_depth=3, n_estimators=3,
+                   learning_rate=0.3, min_child_weight=5).fit_codes(codes, y)
+    trees = [t for rnd in f.forest for t in rnd]
+    tabs = np.stack([ops.flatten_tree(t, 16) for t in trees])
+    cls = np.tile(np.arange(K, dtype=np.int32), 3)
+    start = np.tile(gbm.uniform_prior_logits(K), (N, 1))
+    got = clib.predict_tables(codes, tabs, 0.3, start, cls)
+    want = start.copy()
+    for t, k in zip(range(len(trees)), cls):
+        want[:, k] = ops.predict_table(codes, tabs[t:t + 1], 0.3, want[:, k])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(clib.softmax_rows(got), f.predict_codes(codes))
+    one = clib.predict_tables(codes, tabs[:1], 0.3, np.zeros(N, F32))
+    assert np.array_equal(one, F32(0.3) * ops.predict_tree_dict(codes, trees[0]))

@@ -574,10 +574,12 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         return out
 
     def _uniform_prior_logits(self):
-        """log(float32(1/K + 1e-10)) for every class: the prior predict_proba
-        starts from (warpgbm/core.py:1003-1007)."""
+        """The start logits of predict_proba (warpgbm/core.py:1003-1007):
+        1/K + 1e-10 is a float64 there (numpy division, wrapped by
+        torch.tensor), so its log is taken in float64 and rounded to float32
+        once, when it lands in the float32 score matrix."""
         K = self.num_classes
-        v = np.float32(np.log(np.float64(np.float32(1.0 / K + 1e-10))))
+        v = np.float32(np.log(np.float64(1.0) / np.float64(K) + 1e-10))
         return np.full(K, v, dtype=np.float32)
 
     # ------------------------------------------------------------------ eval

@@ -263,12 +263,24 @@ def bin_matrix(Xd: torch.Tensor, edges: torch.Tensor, with_cm: bool) -> Codes:
     return c
 
 
+def era_id_int32(era_id: np.ndarray) -> np.ndarray:
+    """The era ids as the reference sees them: torch.from_numpy(era_id)
+    .type(torch.int32) (warpgbm/core.py:493), i.e. floats truncated toward
+    zero (1.2 and 1.7 are one era), wider integers wrapped to 32 bits, bools
+    0/1; dtypes torch cannot take (strings, objects) raise TypeError as there."""
+    era = np.asarray(era_id).reshape(-1)
+    if era.dtype == np.int32:
+        return era
+    return torch.from_numpy(np.ascontiguousarray(era)).type(torch.int32).numpy()
+
+
 def era_layout(era_id: np.ndarray):
     """Sorted unique eras, era index per row, rows sorted by era (stable) and
-    era offsets (warpgbm/core.py:540: torch.unique(..., return_inverse=True)).
-    Era ids that are already non-decreasing (one era, or contiguous eras) take
-    a linear path with the same result as the sort."""
-    era = np.asarray(era_id).reshape(-1)
+    era offsets (warpgbm/core.py:540: torch.unique(..., return_inverse=True)
+    over the int32 era ids of :493).  Era ids that are already non-decreasing
+    (one era, or contiguous eras) take a linear path with the same result as
+    the sort."""
+    era = era_id_int32(era_id)
     n = era.shape[0]
     if n > 0 and (n == 1 or bool(np.all(era[1:] >= era[:-1]))):
         first = np.ones(n, dtype=bool)
