@@ -6,7 +6,9 @@ Conventions
 * "exact" histograms use the arithmetic of the HIP library: each residual is
   quantised to q = rint(r * 2^s) (exact scaling by a power of two), sums of q
   are exact integers, and a float32 value is produced once by rounding
-  ldexp(sum, -s).  The shift s comes from max|r| (see shift_from_absmax).
+  ldexp(sum, -s).  The shift s comes from max|r| (see shift_from_absmax); in
+  tree growth each node has its own (node_shift), and leaf means use a wider
+  quantisation (leaf_value63).
 """
 from __future__ import annotations
 
@@ -47,6 +49,47 @@ def leaf_value(sq: int, count: int, s: int) -> np.float32:
     float64 arithmetic (the reference's residual[node_indices].mean(),
     warpgbm/core.py:599 and :614)."""
     return F32(np.ldexp(np.float64(sq), -s) / np.float64(count))
+
+
+# Leaf values and node totals use a second, wide quantisation: q63 =
+# rint(r * 2^s63) with s63 = s + 62 - qbits (|q63| < 2^62), so every residual
+# down to max|r| * 2^-38 keeps all 24 bits and a leaf's mean is exact to
+# float64 precision relative to its own residuals, however small they are
+# next to the tree's largest.  Sums of q63 are exact integers, carried on the
+# device as two int64 words per sum: hi = q63 >> 32 (arithmetic) and
+# lo = q63 & (2^32 - 1).
+def shift63(s: int, qbits: int) -> int:
+    return int(s) + 62 - int(qbits)
+
+
+def leaf_value63(q63_rows, count: int, s63: int) -> np.float32:
+    """float32 mean of a leaf from its rows' q63 values, in the device's exact
+    steps: H = sum(hi) + (sum(lo) >> 32), L = sum(lo) & (2^32 - 1) (so that
+    sum q63 = H * 2^32 + L), v = float64(H) * 2^32 + float64(L) (one rounding
+    when |H| < 2^53), leaf = float32(ldexp(v, -s63) / float64(count))."""
+    q = np.asarray(q63_rows, dtype=np.int64)
+    hi = int((q >> 32).sum())
+    lo = int((q & 0xFFFFFFFF).sum())
+    H = hi + (lo >> 32)
+    L = lo & 0xFFFFFFFF
+    v = np.float64(H) * np.float64(4294967296.0) + np.float64(L)
+    return F32(np.ldexp(v, -int(s63)) / np.float64(count))
+
+
+# A node's histogram shift: the root takes the tree's shift s; a child keeps
+# its parent's shift unless the shift of its own max|r| is at least
+# NODE_SHIFT_STEP larger (its residuals are all below 2^-8 of the parent's
+# scale), in which case it takes its own.  Every node's histogram is the exact
+# integer histogram of its rows at its shift (so G is within count * max|r of
+# the node| * 2^(NODE_SHIFT_STEP - 30) of the real sum); a sibling is taken
+# as parent - child only when both children keep the parent's shift, where
+# that subtraction is exact.
+NODE_SHIFT_STEP = 8
+
+
+def node_shift(max_abs, parent_shift: int, qbits: int) -> int:
+    s_own = shift_from_absmax(max_abs, qbits)
+    return s_own if s_own - int(parent_shift) >= NODE_SHIFT_STEP else int(parent_shift)
 
 
 # --------------------------------------------------------------------------- histogram

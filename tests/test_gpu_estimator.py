@@ -306,3 +306,61 @@ def test_binary_objective(gpu):
                 learning_rate=0.3).fit(X, y)
     assert m.predict_proba(X).shape == (3000, 2)
     assert (m.predict(X) == y).mean() > 0.9
+
+
+def _heavy_targets(rng, n, signal):
+    """+-1e-3 targets (sign of ``signal``) with +1e6 and -1e6 on two rows."""
+    y = np.where(signal > 0, 1e-3, -1e-3).astype(F32)
+    y[0], y[1] = 1e6, -1e6
+    return y
+
+
+def _small_leaves(tree, out):
+    if "leaf_value" in tree:
+        out.append(tree["leaf_value"])
+    else:
+        _small_leaves(tree["left"], out)
+        _small_leaves(tree["right"], out)
+    return out
+
+
+@pytest.mark.parametrize("seed,depth", [(0, 3), (2, 4), (3, 3), (5, 4)])
+def test_heavy_tailed_regression_bit_exact(gpu, seed, depth):
+    """Residuals of 1e-3 next to +-1e6: nodes whose residuals are all small
+    take their own histogram shift (both children histogrammed), leaves use
+    the wide sums, so the small rows get their own means and splits -- bit
+    for bit the oracle's arithmetic (whose agreement with the reference's
+    float32 arithmetic is checked in test_literal_f32.py)."""
+    print_case("estimator", "heavy-tailed regression seed depth", seed, depth)
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((2000, 4)).astype(F32)
+    y = _heavy_targets(rng, 2000, X[:, 1])
+    kw = dict(num_bins=4, max_depth=depth, n_estimators=3, learning_rate=0.1,
+              min_child_weight=5)
+    m = WarpGBM(**kw).fit(X, y)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, y)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
+    small = [v for v in _small_leaves(m.forest[0], []) if abs(v) < 1e-2]
+    assert small and all(v != 0.0 for v in small)  # the small rows' own means
+
+
+@pytest.mark.parametrize("N,E", [(6000, 4), (140_000, 2)])
+def test_heavy_tailed_eras_bit_exact(gpu, N, E):
+    """The same targets through the era paths: direct per-(node, era) LDS
+    histograms (eras <= 65536 rows) and the per-era histogram path with exact
+    subtraction (larger eras)."""
+    print_case("estimator", "heavy-tailed eras N E", N, E)
+    rng = np.random.default_rng(9)
+    X = rng.integers(0, 5, (N, 6)).astype(np.int8)
+    era = np.repeat(np.arange(E), N // E)
+    y = _heavy_targets(rng, N, X[:, 2].astype(np.float64) - 2 + 0.5 * (era % 2))
+    kw = dict(num_bins=5, max_depth=4, n_estimators=2, learning_rate=0.1, min_child_weight=5)
+    m = WarpGBM(**kw).fit(X, y, era_id=era)
+    ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))

@@ -55,13 +55,15 @@ __global__ void residual_softmax_kernel(const float* logits, const int32_t* labe
 __global__ void root_setup_kernel(const int32_t* root_order, int64_t n, int32_t T,
                                   const int64_t* era_start, int32_t E, const float* resid,
                                   int32_t* order, int32_t* keyp, float* rpos, int64_t* seg,
-                                  int32_t* present, unsigned long long* best, int32_t* agree_max);
+                                  int32_t* present, unsigned long long* best, int32_t* agree_max,
+                                  const int32_t* shifts, int32_t* node_shift);
 __global__ void level_finish_kernel(int32_t depth, int32_t max_depth, int32_t T, int32_t E,
                                     int32_t B, const int32_t* present,
                                     const unsigned long long* best, int32_t* split_l,
                                     int32_t* split_b, const float* split_gain_era,
-                                    const int32_t* feat_sel, const int64_t* tot_q,
-                                    const int64_t* tot_c, const int32_t* shifts,
+                                    const int32_t* feat_sel, const int64_t* tot_qh,
+                                    const int64_t* tot_ql, const int64_t* tot_c,
+                                    const int32_t* shifts, int32_t s63_add,
                                     float* leaf_val, TreeRecord rec,
                                     unsigned long long* best_next, int32_t* agree_max_next);
 // partition over position blocks (engine_kernels.hip)
@@ -69,17 +71,44 @@ constexpr int kPartBlock = 1024;   // positions per block
 constexpr int kPartThreads = 256;
 // Per-level left sums of the partition (see route_kernel): words of the
 // segments that lie inside one block, the first- and last-segment partials of
-// every block and their inclusive prefix over the blocks.
+// every block and their inclusive prefix over the blocks.  A residual sum is
+// two words, qh = sum of (q63 >> 32) and ql = sum of (q63 & (2^32 - 1)), with
+// q63 the wide quantisation of the leaf sums (sum q63 = qh * 2^32 + ql).
+// Node maxima of |residual| of the left and right rows of every split node
+// (float bits), per node: words of nodes inside one block, and the block's
+// first- and last-node partials.
 struct PartSums {
-  int64_t* own_q;  // [n_keys]
+  int64_t* own_qh;  // [n_keys]
+  int64_t* own_ql;
   int32_t* own_n;
-  int64_t* bf_q;  // [nb]
+  int64_t* bf_qh;  // [nb]
+  int64_t* bf_ql;
   int32_t* bf_n;
-  int64_t* bl_q;
+  int64_t* bl_qh;
+  int64_t* bl_ql;
   int32_t* bl_n;
-  int64_t* P_q;
+  int64_t* P_qh;
+  int64_t* P_ql;
   int64_t* P_n;
+  uint32_t* own_ml;  // [T * nodes] left-child max of a node inside one block
+  uint32_t* own_mr;  //             right-child max
+  uint32_t* bf_ml;   // [nb] of the block's first node
+  uint32_t* bf_mr;
+  uint32_t* bl_ml;   // [nb] of the block's last node
+  uint32_t* bl_mr;
 };
+
+// A child node keeps its parent's histogram shift unless the shift of its
+// own max|r| is at least this much larger (all its residuals below 2^-8 of
+// the parent's scale); then it takes its own, and both children of that
+// split are histogrammed directly instead of one by subtraction.
+constexpr int kNodeShiftStep = 8;
+__device__ inline int node_shift_rule(uint32_t absmax_bits, int parent_shift,
+                                               int qbits) {
+  if (absmax_bits >= 0x7f800000u) return parent_shift;  // inf / NaN residuals
+  const int s_own = wgbm_shift_from_absmax(__uint_as_float(absmax_bits), qbits);
+  return s_own - parent_shift >= kNodeShiftStep ? s_own : parent_shift;
+}
 struct RouteArgs {
   int32_t mode;  // 0 root totals, 1 split level, 2 last level (leaves only)
   const int64_t* seg;
@@ -94,7 +123,8 @@ struct RouteArgs {
   const int8_t* codes_cm;
   int64_t n;
   const float* rpos;  // residual of every position's row
-  const int32_t* shifts;
+  const int32_t* shifts;  // per tree
+  int32_t s63_add;        // wide leaf-sum shift = shifts[t] + s63_add
   const float* leaf_val;
   float lr;
   float* pred;
@@ -106,20 +136,34 @@ struct RouteArgs {
 __global__ void route_kernel(RouteArgs a);
 __global__ void block_scan_kernel(int32_t nb, PartSums ps);
 constexpr int kLevelScanMaxNodes = 64;  // (tree, node)s of a level for level_scan_kernel
+// Per split level: the children's segments and totals, their histogram
+// shifts (node_shift_rule from the node maxima) and the histogram key list of
+// the next level, two entries per (parent, era): the smaller child and -1
+// (the sibling by subtraction), or both children when a child's shift
+// differs from the parent's.
+struct LevelNext {
+  const int64_t* tot_qh;
+  const int64_t* tot_ql;
+  const int32_t* node_shift;  // [T * nodes] of this level
+  int32_t qbits;
+  int64_t* seg_next;
+  int64_t* tot_qh_next;
+  int64_t* tot_ql_next;
+  int64_t* tot_c_next;
+  int32_t* present_next;
+  int32_t* key_list_next;   // [2 * T * nodes * E]
+  int32_t* node_shift_next;  // [2 * T * nodes]
+};
 __global__ void level_scan_kernel(int32_t nb, PartSums ps, int32_t T, int32_t nodes, int32_t E,
                                   int64_t n_pos, const int64_t* seg, const int32_t* present,
-                                  const int32_t* split_l, const int64_t* tot_q,
-                                  int64_t* seg_next, int64_t* tot_q_next, int64_t* tot_c_next,
-                                  int32_t* present_next, int32_t* key_list_next, int32_t n_list,
+                                  const int32_t* split_l, LevelNext nx, int32_t n_list,
                                   int32_t tile_rows, int32_t max_tiles, Tile* tiles,
                                   int32_t* key_tile_start, int32_t* n_tiles);
 __global__ void root_totals_kernel(int32_t n_keys, const int64_t* seg, PartSums ps,
-                                   int64_t* tot_q, int64_t* tot_c);
+                                   int64_t* tot_qh, int64_t* tot_ql, int64_t* tot_c);
 __global__ void node_scan_kernel(int32_t T, int32_t nodes, int32_t E, int32_t wpn,
                                  int64_t n_pos, const int64_t* seg, const int32_t* present,
-                                 const int32_t* split_l, PartSums ps, const int64_t* tot_q,
-                                 int64_t* seg_next, int64_t* tot_q_next, int64_t* tot_c_next,
-                                 int32_t* present_next, int32_t* key_list_next);
+                                 const int32_t* split_l, PartSums ps, LevelNext nx);
 __global__ void scatter_kernel(int64_t n_pos, int32_t E, const int64_t* seg,
                                const int64_t* seg_next, const int32_t* keyp,
                                const uint8_t* dirbit, PartSums ps, const int32_t* order,
@@ -127,27 +171,31 @@ __global__ void scatter_kernel(int64_t n_pos, int32_t E, const int64_t* seg,
                                float* rpos_next);
 __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v);
 
-// split kernels (split.hip)
+// split kernels (split.hip); node_shift: the histogram shift of every
+// (tree, node) of the level, indexed by tree * nodes_in_level + node
 __global__ void split_f32_kernel(const float* G, const float* H, int32_t E, int32_t F,
                                  int32_t B, float mcw, float eps, float* gain_out,
                                  float* dir_out);
 // split_level_e1_kernel over n_tn tree-nodes (a compile-time bin count for B = 32)
 int launch_split_level_e1(int n_tn, hipStream_t st, const int64_t* hq, const int32_t* hc,
                           int32_t F, int32_t B, const int32_t* feat_sel, int32_t n_sel,
-                          int32_t nodes_in_level, const int32_t* present, const int32_t* shifts,
-                          float mcw, float eps, float min_split_gain, unsigned long long* best);
+                          int32_t nodes_in_level, const int32_t* present,
+                          const int32_t* node_shift, float mcw, float eps, float min_split_gain,
+                          unsigned long long* best);
 __global__ void des_accumulate_kernel(const int64_t* hq, const int32_t* hc, int32_t F, int32_t B,
                                       int32_t E, const int32_t* feat_sel, int32_t n_sel,
                                       int32_t nodes_in_level, int32_t n_tn,
-                                      const int32_t* present, const int32_t* shifts, float mcw,
-                                      float eps, float* crit, int32_t* agree, int32_t* agree_max);
+                                      const int32_t* present, const int32_t* node_shift,
+                                      float mcw, float eps, float* crit, int32_t* agree,
+                                      int32_t* agree_max);
 __global__ void des_pick_kernel(const float* crit, const int32_t* agree, const int32_t* agree_max,
                                 const int32_t* present, int32_t n_tn, int64_t ncand,
                                 float min_split_gain, unsigned long long* best);
 __global__ void des_finish_kernel(const unsigned long long* best, const int64_t* hq,
                                   const int32_t* hc, int32_t F, int32_t B, int32_t E,
                                   const int32_t* feat_sel, int32_t nodes_in_level, int32_t n_tn,
-                                  const int32_t* shifts, float mcw, float eps, const float* staged,
+                                  const int32_t* node_shift, float mcw, float eps,
+                                  const float* staged,
                                   const int64_t* seg, int32_t n_sel, int32_t* split_l,
                                   int32_t* split_b, float* split_gain_era);
 __global__ void des_alive_kernel(const int64_t* seg, int32_t E, int32_t n_tn, float mcw,
@@ -164,7 +212,7 @@ __global__ void local_scatter_kernel(const int32_t* feat_sel, int32_t n_sel, int
 // pcodes: the pair-code copy of the codes (num_bins <= 7; n_rows rows of
 // pstride bytes, under 4 GiB) or null for the int8 codes
 int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* codes,
-                   int64_t stride, int32_t F, const float* rpos, const int32_t* shifts,
+                   int64_t stride, int32_t F, const float* rpos, const int32_t* node_shift,
                    const int32_t* order, const int64_t* seg, int32_t E, int32_t nodes_in_level,
                    const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
                    float eps, float* gain, int8_t* dir, const uint8_t* pcodes, int64_t n_rows,

@@ -10,7 +10,8 @@
 // on one stream and no host synchronisation inside a round:
 //   residuals -> shifts -> root segments/totals ->
 //   for depth d: histograms of the smaller children (+ siblings by
-//   subtraction) -> split/DES -> leaf values + record -> partition.
+//   subtraction; both children when one takes a finer histogram shift) ->
+//   split/DES -> leaf values + record -> partition.
 #include <algorithm>
 #include <vector>
 
@@ -34,10 +35,12 @@ struct Engine {
   int32_t* shifts = nullptr;
   int32_t* order[2] = {nullptr, nullptr};
   int64_t* seg[2] = {nullptr, nullptr};
-  int64_t* totq[2] = {nullptr, nullptr};
+  int64_t* totqh[2] = {nullptr, nullptr};  // wide leaf sums, two words (see PartSums)
+  int64_t* totql[2] = {nullptr, nullptr};
   int64_t* totc[2] = {nullptr, nullptr};
   int32_t* present[2] = {nullptr, nullptr};
-  int32_t* key_list[2] = {nullptr, nullptr};
+  int32_t* node_shift[2] = {nullptr, nullptr};  // histogram shift per (tree, node)
+  int32_t* key_list[2] = {nullptr, nullptr};    // histogram key pairs per (parent, era)
   // partition over position blocks of kPartBlock positions
   uint8_t* dirbit = nullptr;            // [T*N] 0 left, 1 right, 2 stays
   int32_t* keyp[2] = {nullptr, nullptr};  // [T*N] segment key of each position
@@ -154,10 +157,12 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   for (int k = 0; k < 2; ++k) {
     E_ALLOC(e->order[k], T * N);
     E_ALLOC(e->seg[k], e->n_keys_max + 1);
-    E_ALLOC(e->totq[k], e->n_keys_max);
+    E_ALLOC(e->totqh[k], e->n_keys_max);
+    E_ALLOC(e->totql[k], e->n_keys_max);
     E_ALLOC(e->totc[k], e->n_keys_max);
     E_ALLOC(e->present[k], T * nodes_max);
-    E_ALLOC(e->key_list[k], e->n_keys_max);
+    E_ALLOC(e->node_shift[k], T * nodes_max);
+    E_ALLOC(e->key_list[k], 2 * e->n_keys_max);
     if (!e->des_direct) {
       E_ALLOC(e->hq[k], T * hist_nodes_max * E * F * B);
       E_ALLOC(e->hc[k], T * hist_nodes_max * E * F * B);
@@ -182,14 +187,24 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->rpos[0], T * N);
   E_ALLOC(e->rpos[1], T * N);
   e->nb = (T * N + kPartBlock - 1) / kPartBlock;
-  E_ALLOC(e->ps.own_q, e->n_keys_max);
+  E_ALLOC(e->ps.own_qh, e->n_keys_max);
+  E_ALLOC(e->ps.own_ql, e->n_keys_max);
   E_ALLOC(e->ps.own_n, e->n_keys_max);
-  E_ALLOC(e->ps.bf_q, e->nb);
+  E_ALLOC(e->ps.bf_qh, e->nb);
+  E_ALLOC(e->ps.bf_ql, e->nb);
   E_ALLOC(e->ps.bf_n, e->nb);
-  E_ALLOC(e->ps.bl_q, e->nb);
+  E_ALLOC(e->ps.bl_qh, e->nb);
+  E_ALLOC(e->ps.bl_ql, e->nb);
   E_ALLOC(e->ps.bl_n, e->nb);
-  E_ALLOC(e->ps.P_q, e->nb);
+  E_ALLOC(e->ps.P_qh, e->nb);
+  E_ALLOC(e->ps.P_ql, e->nb);
   E_ALLOC(e->ps.P_n, e->nb);
+  E_ALLOC(e->ps.own_ml, T * nodes_max);
+  E_ALLOC(e->ps.own_mr, T * nodes_max);
+  E_ALLOC(e->ps.bf_ml, e->nb);
+  E_ALLOC(e->ps.bf_mr, e->nb);
+  E_ALLOC(e->ps.bl_ml, e->nb);
+  E_ALLOC(e->ps.bl_mr, e->nb);
   E_ALLOC(e->hkts, e->n_keys_max + 1);
   E_ALLOC(e->hn, 1);
   if (E > 1) {
@@ -253,8 +268,9 @@ static int ensure_partials(Engine* e, int64_t max_tiles) {
   return 0;
 }
 
-// histogram tiles of level d (the root, or the smaller child of every split):
-// tile rows, the tile bound, and buffers that hold them
+// histogram tiles of level d (the root, or the key pairs of every split: the
+// smaller child, or both children when one takes a finer shift): tile rows,
+// the tile bound, and buffers that hold them
 struct LevelPlan {
   int32_t n_list = 0;
   int64_t rows_bound = 0, R = 0, max_tiles = 0;
@@ -263,10 +279,12 @@ struct LevelPlan {
 static int level_plan(Engine* e, int d, LevelPlan* lp) {
   const int64_t T = e->c.n_trees, N = e->c.n_rows, E = e->c.num_eras;
   const int64_t nodes = int64_t(1) << d;
-  lp->n_list = (int32_t)(d == 0 ? T * nodes * E : T * (nodes / 2) * E);
+  lp->n_list = (int32_t)(d == 0 ? T * nodes * E : 2 * T * (nodes / 2) * E);
+  // tiles are sized for the smaller children (half the rows); the bound
+  // holds the rare level where every split histograms both children
   lp->rows_bound = d == 0 ? T * N : (T * N) / 2;
   lp->R = pick_tile_rows(e, lp->rows_bound);
-  lp->max_tiles = lp->rows_bound / lp->R + lp->n_list + 1;
+  lp->max_tiles = (T * N) / lp->R + lp->n_list + 1;
   int r = ensure_partials(e, lp->max_tiles);
   if (r) return r;
   if (lp->max_tiles > e->max_htiles) {
@@ -320,7 +338,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   hipLaunchKernelGGL(root_setup_kernel, dim3(blocks_for(std::max<int64_t>(n_pos, T * E), 256)),
                      dim3(256), 0, st, c.root_order, N, T, c.era_start, E, e->resid,
                      e->order[0], e->keyp[0], e->rpos[0], e->seg[0], e->present[0], e->best,
-                     e->agree_max);
+                     e->agree_max, e->shifts, e->node_shift[0]);
   WGBM_LAUNCH_CHECK();
   RouteArgs ra{};
   ra.n_pos = n_pos;
@@ -329,6 +347,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   ra.codes_cm = c.codes_cm;
   ra.n = N;
   ra.shifts = e->shifts;
+  ra.s63_add = 62 - e->qbits;
   ra.leaf_val = e->leaf_val;
   ra.lr = c.learning_rate;
   ra.pred = pred;
@@ -351,7 +370,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
     WGBM_LAUNCH_CHECK();
     hipLaunchKernelGGL(root_totals_kernel, dim3(blocks_for((int64_t)T * E, 256)), dim3(256), 0,
-                       st, (int32_t)(T * E), e->seg[0], e->ps, e->totq[0], e->totc[0]);
+                       st, (int32_t)(T * E), e->seg[0], e->ps, e->totqh[0], e->totql[0],
+                       e->totc[0]);
     WGBM_LAUNCH_CHECK();
   }
 
@@ -387,7 +407,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         e->pcodes_ready = true;
       }
       int r = launch_des_era(e->V, B, n_keys, st, c.codes_rm, c.stride, F, e->rpos[cur],
-                             e->shifts, e->order[cur], e->seg[cur], E, nodes, e->present[cur],
+                             e->node_shift[cur], e->order[cur], e->seg[cur], E, nodes,
+                             e->present[cur],
                              e->local_of, n_sel, mcw, eps, e->sgain, e->sdir,
                              use_pairs ? e->pcodes : nullptr, N, e->pstride);
       if (r) return r;
@@ -409,7 +430,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       WGBM_LAUNCH_CHECK();
       hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)n_tn * E, 256)), dim3(256), 0,
                          st, best, (const int64_t*)nullptr, (const int32_t*)nullptr, F, B, E,
-                         feat_sel, nodes, n_tn, e->shifts, mcw, eps, e->sgain, e->seg[cur], n_sel,
+                         feat_sel, nodes, n_tn, e->node_shift[cur], mcw, eps, e->sgain,
+                         e->seg[cur], n_sel,
                          e->split_l, e->split_b, e->split_gain);
       WGBM_LAUNCH_CHECK();
     } else if (d < D) {
@@ -434,11 +456,12 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       a.resid = e->rpos[cur];  // residuals in position order (global positions)
       a.resid_by_pos = 1;
       a.resid_tree_stride = 0;
-      a.shifts = e->shifts;
+      // quantised with the histogram shift of each tile's (tree, node)
+      a.shifts = e->node_shift[cur];
       a.order = e->order[cur];
       a.tiles = e->htiles;
       a.n_tiles = e->hn;
-      a.keys_per_tree = nodes * E;
+      a.keys_per_tree = E;
       a.num_bins = B;
       a.part = e->part;
       a.V = e->V;
@@ -448,7 +471,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       a.timer_tag = "engine_hist_tiles";
       r = launch_hist_tiles(a, st);
       if (r) return r;
-      const int64_t tiles_per_key = std::max<int64_t>(1, rows_bound / R / std::max(n_list, 1));
+      const int64_t tiles_per_key =
+          std::max<int64_t>(1, rows_bound / R / std::max(d == 0 ? n_list : n_list / 2, 1));
       r = launch_finalize_level(tiles_per_key, e->part, e->hkts, list, n_list, e->n_chunks, e->V,
                                 B, F, E, nodes, d, e->hq[hprev], e->hc[hprev], e->hn, e->hq[hcur],
                                 e->hc[hcur], st);
@@ -457,14 +481,15 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       if (E == 1) {
         // the pick is decoded by level_finish
         int r = launch_split_level_e1(n_tn, st, e->hq[hcur], e->hc[hcur], F, B, feat_sel, n_sel,
-                                      nodes, e->present[cur], e->shifts, mcw, eps, msg, best);
+                                      nodes, e->present[cur], e->node_shift[cur], mcw, eps, msg,
+                                      best);
         if (r) return r;
       } else {
         const int64_t ncand = (int64_t)n_sel * (B - 1);
         const int64_t nacc = (int64_t)n_tn * n_sel * ((B - 1 + kDesChunk - 1) / kDesChunk);
         hipLaunchKernelGGL(des_accumulate_kernel, dim3(blocks_for(nacc, 128)), dim3(128), 0, st,
                            e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, n_sel, nodes, n_tn,
-                           e->present[cur], e->shifts, mcw, eps, e->crit, e->agree,
+                           e->present[cur], e->node_shift[cur], mcw, eps, e->crit, e->agree,
                            agree_max);
         WGBM_LAUNCH_CHECK();
         hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)),
@@ -473,7 +498,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         WGBM_LAUNCH_CHECK();
         hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)n_tn * E, 256)), dim3(256),
                            0, st, best, e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, nodes,
-                           n_tn, e->shifts, mcw, eps, (const float*)nullptr,
+                           n_tn, e->node_shift[cur], mcw, eps, (const float*)nullptr,
                            (const int64_t*)nullptr, n_sel, e->split_l, e->split_b, e->split_gain);
         WGBM_LAUNCH_CHECK();
       }
@@ -484,8 +509,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     const bool e1_pick = d < D && !e->des_direct && E == 1;
     hipLaunchKernelGGL(level_finish_kernel, dim3((unsigned)n_tn), dim3(64), 0, st, d, D, T, E, B,
                        e->present[cur], e1_pick ? (const unsigned long long*)best : nullptr,
-                       e->split_l, e->split_b, e->split_gain, feat_sel, e->totq[cur],
-                       e->totc[cur], e->shifts, e->leaf_val, rec,
+                       e->split_l, e->split_b, e->split_gain, feat_sel, e->totqh[cur],
+                       e->totql[cur], e->totc[cur], e->shifts, 62 - e->qbits, e->leaf_val, rec,
                        e->best + (hcur ^ 1) * e->pick_stride,
                        e->agree_max ? e->agree_max + (hcur ^ 1) * e->pick_stride : nullptr);
     WGBM_LAUNCH_CHECK();
@@ -505,6 +530,18 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, rl);
     WGBM_LAUNCH_CHECK();
     planned = false;
+    LevelNext nx;
+    nx.tot_qh = e->totqh[cur];
+    nx.tot_ql = e->totql[cur];
+    nx.node_shift = e->node_shift[cur];
+    nx.qbits = e->qbits;
+    nx.seg_next = e->seg[nxt];
+    nx.tot_qh_next = e->totqh[nxt];
+    nx.tot_ql_next = e->totql[nxt];
+    nx.tot_c_next = e->totc[nxt];
+    nx.present_next = e->present[nxt];
+    nx.key_list_next = e->key_list[nxt];
+    nx.node_shift_next = e->node_shift[nxt];
     if (d < D && E <= 64 && n_tn <= kLevelScanMaxNodes) {
       // few keys: block prefix, node scan and the next level's tile plan in
       // one workgroup
@@ -515,10 +552,9 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         if (r) return r;
       }
       hipLaunchKernelGGL(level_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps, T,
-                         nodes, E, n_pos, e->seg[cur], e->present[cur], e->split_l, e->totq[cur],
-                         e->seg[nxt], e->totq[nxt], e->totc[nxt], e->present[nxt],
-                         e->key_list[nxt], next_hist ? lp.n_list : 0, (int32_t)lp.R,
-                         (int32_t)lp.max_tiles, e->htiles, e->hkts, e->hn);
+                         nodes, E, n_pos, e->seg[cur], e->present[cur], e->split_l, nx,
+                         next_hist ? lp.n_list : 0, (int32_t)lp.R, (int32_t)lp.max_tiles,
+                         e->htiles, e->hkts, e->hn);
       WGBM_LAUNCH_CHECK();
       planned = next_hist;
     } else if (d < D) {
@@ -526,9 +562,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       WGBM_LAUNCH_CHECK();
       const int wpn = E <= 64 ? 1 : (E <= 128 ? 2 : 4);  // waves per node
       hipLaunchKernelGGL(node_scan_kernel, dim3(blocks_for((int64_t)n_tn, 4 / wpn)), dim3(256), 0,
-                         st, T, nodes, E, wpn, n_pos, e->seg[cur], e->present[cur], e->split_l, e->ps,
-                         e->totq[cur], e->seg[nxt], e->totq[nxt], e->totc[nxt], e->present[nxt],
-                         e->key_list[nxt]);
+                         st, T, nodes, E, wpn, n_pos, e->seg[cur], e->present[cur], e->split_l,
+                         e->ps, nx);
       WGBM_LAUNCH_CHECK();
     }
     if (d < D) {

@@ -78,9 +78,12 @@ __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_
                                   int32_t* __restrict__ keyp, float* __restrict__ rpos,
                                   int64_t* __restrict__ seg, int32_t* __restrict__ present,
                                   unsigned long long* __restrict__ best,
-                                  int32_t* __restrict__ agree_max) {
-  // root order, segment key and residual of every position, root segments
-  // and cleared depth-0 split-pick words
+                                  int32_t* __restrict__ agree_max,
+                                  const int32_t* __restrict__ shifts,
+                                  int32_t* __restrict__ node_shift) {
+  // root order, segment key and residual of every position, root segments,
+  // the roots' histogram shifts (the trees' own) and cleared depth-0
+  // split-pick words
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid < (int64_t)T * n) {
     const int64_t t = gid / n, p = gid - t * n;
@@ -102,6 +105,7 @@ __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_
   if (gid == 0) seg[(int64_t)T * E] = (int64_t)T * n;
   if (gid < T) {
     present[gid] = 1;
+    node_shift[gid] = shifts[gid];
     best[gid] = 0ull;
     if (agree_max) agree_max[gid] = 0;
   }
@@ -110,15 +114,19 @@ __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_
 // ---------------------------------------------------------------------------
 // per-level bookkeeping: leaf values and the tree record
 //   leaf value = mean of the node's residuals (warpgbm/core.py:599, :614),
-//   computed from the exact quantised sum: float(ldexp(Sq, -s) / count)
+//   from the exact sum of the wide quantisation q63 = rint(r * 2^s63),
+//   s63 = s + s63_add (|q63| < 2^62), held as qh = sum (q63 >> 32) and
+//   ql = sum (q63 & (2^32 - 1)):  H = qh + (ql >> 32), L = ql mod 2^32,
+//   leaf = float(ldexp(double(H) * 2^32 + double(L), -s63) / count)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void level_finish_kernel(
     int32_t depth, int32_t max_depth, int32_t T, int32_t E, int32_t B,
     const int32_t* __restrict__ present, const unsigned long long* __restrict__ best,
     int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
     const float* __restrict__ split_gain_era, const int32_t* __restrict__ feat_sel,
-    const int64_t* __restrict__ tot_q, const int64_t* __restrict__ tot_c,
-    const int32_t* __restrict__ shifts, float* __restrict__ leaf_val, TreeRecord rec,
+    const int64_t* __restrict__ tot_qh, const int64_t* __restrict__ tot_ql,
+    const int64_t* __restrict__ tot_c, const int32_t* __restrict__ shifts, int32_t s63_add,
+    float* __restrict__ leaf_val, TreeRecord rec,
     unsigned long long* __restrict__ best_next, int32_t* __restrict__ agree_max_next) {
   // one wave per (tree, node); the eras are spread over the lanes.  The wave
   // also clears the next depth's split-pick words of its two children.  With
@@ -163,13 +171,15 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
     }
     return;
   }
-  int64_t sq = 0, sc = 0;
+  int64_t sqh = 0, sql = 0, sc = 0;
   for (int e = lane; e < E; e += 64) {
-    sq += tot_q[(int64_t)tn * E + e];
+    sqh += tot_qh[(int64_t)tn * E + e];
+    sql += tot_ql[(int64_t)tn * E + e];
     sc += tot_c[(int64_t)tn * E + e];
   }
   for (int o = 32; o > 0; o >>= 1) {
-    sq += __shfl_xor(sq, o, 64);
+    sqh += __shfl_xor(sqh, o, 64);
+    sql += __shfl_xor(sql, o, 64);
     sc += __shfl_xor(sc, o, 64);
   }
   if (lane == 0) {
@@ -179,7 +189,10 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
       rec.bin[h] = b;
       rec.leaf[h] = 0.0f;
     } else {
-      const float v = (float)(ldexp((double)sq, -shifts[t]) / (double)sc);
+      const int64_t hi = sqh + (sql >> 32);
+      const int64_t lo = sql & 0xffffffffll;
+      const double sum = (double)hi * 4294967296.0 + (double)lo;
+      const float v = (float)(ldexp(sum, -(shifts[t] + s63_add)) / (double)sc);
       leaf_val[tn] = v;
       rec.feat[h] = -1;
       rec.bin[h] = -1;
@@ -238,43 +251,87 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
 //          from the same partial sums, when it began in an earlier block).
 // ---------------------------------------------------------------------------
 __device__ inline void segment_left_sums(int64_t k, const int64_t* __restrict__ seg,
-                                         const PartSums& ps, int64_t& q, int64_t& n) {
+                                         const PartSums& ps, int64_t& qh, int64_t& ql,
+                                         int64_t& n) {
   const int64_t s0 = seg[k], s1 = seg[k + 1];
   if (s1 <= s0) {
-    q = 0;
+    qh = 0;
+    ql = 0;
     n = 0;
     return;
   }
   const int64_t b0 = s0 / kPartBlock, b1 = (s1 - 1) / kPartBlock;
   if (b0 == b1) {
-    q = ps.own_q[k];
+    qh = ps.own_qh[k];
+    ql = ps.own_ql[k];
     n = ps.own_n[k];
   } else {
-    q = ps.bl_q[b0] + ps.P_q[b1] - ps.P_q[b0];
+    qh = ps.bl_qh[b0] + ps.P_qh[b1] - ps.P_qh[b0];
+    ql = ps.bl_ql[b0] + ps.P_ql[b1] - ps.P_ql[b0];
     n = ps.bl_n[b0] + ps.P_n[b1] - ps.P_n[b0];
   }
 }
 
+// Max of the left (ml) and right (mr) residual magnitudes (float bits) of
+// the rows of split node tn, whose positions are [P0, P1): its own words
+// when it lies inside one block, else the last-node partial of its first
+// block and the first-node partials of the blocks after it (the node is
+// their first node).  The gthreads threads of a group share the blocks; the
+// caller reduces the maximum over the group.
+__device__ inline void node_child_max(int tn, int64_t P0, int64_t P1, const PartSums& ps,
+                                      int gt, int gthreads, uint32_t& ml, uint32_t& mr) {
+  ml = 0;
+  mr = 0;
+  if (P1 <= P0) return;
+  const int64_t b0 = P0 / kPartBlock, b1 = (P1 - 1) / kPartBlock;
+  if (b0 == b1) {
+    if (gt == 0) {
+      ml = ps.own_ml[tn];
+      mr = ps.own_mr[tn];
+    }
+    return;
+  }
+  if (gt == 0) {
+    ml = ps.bl_ml[b0];
+    mr = ps.bl_mr[b0];
+  }
+  for (int64_t b = b0 + 1 + gt; b <= b1; b += gthreads) {
+    const uint32_t l = ps.bf_ml[b], r = ps.bf_mr[b];
+    ml = l > ml ? l : ml;
+    mr = r > mr ? r : mr;
+  }
+}
+
 __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
-  // left sums of the block's segments, in the slot of the segment's first
+  // Left sums of the block's segments, in the slot of the segment's first
   // position in the block (distinct for distinct non-empty segments; empty
-  // segments own no position)
-  __shared__ int64_t s_q[kPartBlock];
-  __shared__ int32_t s_n[kPartBlock], s_key[kPartBlock];
+  // segments own no position): s_qn packs the qh sum with the row count
+  // (qh_sum * 2^11 + rows: at most kPartBlock < 2^11 rows, |q63 >> 32| <=
+  // 2^30 per row), s_ql holds the ql sum.  With mode 1 also the largest
+  // |residual| (float bits) of each split node's left and right rows, in the
+  // slot of the node's first position in the block (the slot of its first
+  // segment there).
+  __shared__ int64_t s_qn[kPartBlock];
+  __shared__ int64_t s_ql[kPartBlock];
+  __shared__ int32_t s_key[kPartBlock];
+  __shared__ uint32_t s_ml[kPartBlock], s_mr[kPartBlock];
   __shared__ int s_k[2];
   const int tid = threadIdx.x;
   const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
   const int64_t p1 = p0 + kPartBlock < a.n_pos ? p0 + kPartBlock : a.n_pos;
   const bool sums = a.mode != 2;
+  const bool maxes = a.mode == 1;
   if (tid == 0) {
     s_k[0] = a.keyp[p0];
     s_k[1] = a.keyp[p1 - 1];
   }
   if (sums) {
     for (int i = tid; i < kPartBlock; i += kPartThreads) {
-      s_q[i] = 0;
-      s_n[i] = 0;
+      s_qn[i] = 0;
+      s_ql[i] = 0;
       s_key[i] = -1;
+      s_ml[i] = 0u;
+      s_mr[i] = 0u;
     }
   }
   __syncthreads();
@@ -282,7 +339,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   // the block's positions, four per thread (strided: coalesced), in phases so
   // that the loads of the four positions are in flight together
   constexpr int PJ = kPartBlock / kPartThreads;
-  int key[PJ], slot[PJ], tnv[PJ], lv[PJ];
+  int key[PJ], slot[PJ], nslot[PJ], tnv[PJ], lv[PJ];
   int32_t rowv[PJ];
   bool ok[PJ];
 #pragma unroll
@@ -297,6 +354,11 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     const int64_t sk = a.seg[key[j]];
     slot[j] = (int)((sk > p0 ? sk : p0) - p0);
     tnv[j] = key[j] / a.E;
+    nslot[j] = 0;
+    if (maxes) {
+      const int64_t sn = a.seg[(int64_t)tnv[j] * a.E];
+      nslot[j] = (int)((sn > p0 ? sn : p0) - p0);
+    }
     // -2: the row stays (node absent), -1: leaf update, >= 0: split feature
     lv[j] = -2;
     if (ok[j] && a.present[tnv[j]]) lv[j] = a.mode == 1 ? a.split_l[tnv[j]] : -1;
@@ -304,29 +366,49 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   // Sums go to the LDS slot of the row's segment.  A wave whose rows all lie
   // in one segment (the common case for large segments) reduces them across
   // its lanes first and adds once; otherwise every lane adds its own row.
-  auto add_slot = [&](int sl, int k, bool act, int64_t q, int32_t n) {
+  auto add_slot = [&](int sl, int k, bool act, int64_t qn, int64_t ql) {
     const uint64_t on = __ballot(act);
     if (on == 0ull) return;
     const int first = __builtin_ctzll(on);  // wave-uniform
     const int s0 = __shfl(sl, first, 64);
     const int k0 = __shfl(k, first, 64);
     if (__ballot(act && sl != s0) == 0ull) {
-      q = wgbm_wave_sum(act ? q : (int64_t)0);
-      n = wgbm_wave_sum(act ? n : 0);
+      qn = wgbm_wave_sum(act ? qn : (int64_t)0);
+      ql = wgbm_wave_sum(act ? ql : (int64_t)0);
       if ((tid & 63) == 0) {
         s_key[s0] = k0;
-        if (n) {
-          atomicAdd((unsigned long long*)&s_q[s0], (unsigned long long)q);
-          atomicAdd(&s_n[s0], n);
-        }
+        if (qn) atomicAdd((unsigned long long*)&s_qn[s0], (unsigned long long)qn);
+        if (ql) atomicAdd((unsigned long long*)&s_ql[s0], (unsigned long long)ql);
       }
     } else if (act) {
       s_key[sl] = k;
-      if (n) {
-        atomicAdd((unsigned long long*)&s_q[sl], (unsigned long long)q);
-        atomicAdd(&s_n[sl], n);
-      }
+      if (qn) atomicAdd((unsigned long long*)&s_qn[sl], (unsigned long long)qn);
+      if (ql) atomicAdd((unsigned long long*)&s_ql[sl], (unsigned long long)ql);
     }
+  };
+  // node maxima likewise, per node slot
+  auto max_slot = [&](int sl, bool act, uint32_t ml, uint32_t mr) {
+    const uint64_t on = __ballot(act);
+    if (on == 0ull) return;
+    const int first = __builtin_ctzll(on);
+    const int s0 = __shfl(sl, first, 64);
+    if (__ballot(act && sl != s0) == 0ull) {
+      ml = wgbm_wave_max_u32(act ? ml : 0u);
+      mr = wgbm_wave_max_u32(act ? mr : 0u);
+      if ((tid & 63) == 0) {
+        if (ml) atomicMax(&s_ml[s0], ml);
+        if (mr) atomicMax(&s_mr[s0], mr);
+      }
+    } else if (act) {
+      if (ml) atomicMax(&s_ml[sl], ml);
+      if (mr) atomicMax(&s_mr[sl], mr);
+    }
+  };
+  // one row's wide quantisation, split into (hi word * 2^11 + 1, lo word)
+  auto q63_words = [&](float r, int t, int64_t& qn, int64_t& ql) {
+    const int64_t q = (int64_t)rintf(ldexpf(r, a.shifts[t] + a.s63_add));
+    qn = (q >> 32) * 2048 + 1;
+    ql = q & 0xffffffffll;
   };
   float rv[PJ];
 #pragma unroll
@@ -336,8 +418,9 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
 #pragma unroll
     for (int j = 0; j < PJ; ++j) {
       const int t = tnv[j] / a.nodes;
-      const int64_t q = ok[j] ? wgbm_quantise(rv[j], a.shifts[t]) : 0;
-      add_slot(slot[j], key[j], ok[j], q, 1);
+      int64_t qn = 0, ql = 0;
+      if (ok[j]) q63_words(rv[j], t, qn, ql);
+      add_slot(slot[j], key[j], ok[j], qn, ql);
     }
   } else {
     int cv[PJ];
@@ -349,80 +432,126 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
       const int tn = tnv[j];
       const int t = tn / a.nodes;
       uint8_t dir = 2;  // stays in place
-      int64_t q = 0;
+      int64_t qn = 0, ql = 0;
       if (lv[j] == -1) {
         // the node is a leaf: add lr * leaf to its rows' predictions
         float* pc = a.pred + (int64_t)t * a.pcol + (int64_t)rowv[j] * a.pstride;
         *pc = *pc + a.lr * a.leaf_val[tn];
       } else if (lv[j] >= 0) {
         dir = cv[j] > a.split_b[tn] ? 1 : 0;
-        q = wgbm_quantise(rv[j], a.shifts[t]);
+        if (dir == 0) q63_words(rv[j], t, qn, ql);
       }
-      if (sums) add_slot(slot[j], key[j], dir != 2, dir == 0 ? q : 0, dir == 0 ? 1 : 0);
+      if (sums) add_slot(slot[j], key[j], dir != 2, qn, ql);
+      if (maxes) {
+        const uint32_t m = wgbm_abs_bits(rv[j]);
+        max_slot(nslot[j], dir != 2, dir == 0 ? m : 0u, dir == 1 ? m : 0u);
+      }
       if (ok[j] && sums) a.dirbit[p0 + j * kPartThreads + tid] = dir;
     }
   }
   if (!sums) return;  // uniform over the block
   __syncthreads();
+  // decode a slot's packed word: rows in the low 11 bits, the hi sum above
+  auto unpack = [](int64_t qn, int64_t& qh, int32_t& n) {
+    n = (int32_t)(qn & 2047);
+    qh = qn >> 11;
+  };
   for (int i = tid; i < kPartBlock; i += kPartThreads) {
     const int k = s_key[i];
     if (k < 0) continue;  // no summed rows start here
     if (a.seg[k] >= p0 && a.seg[k + 1] <= p1) {
-      a.ps.own_q[k] = s_q[i];
-      a.ps.own_n[k] = s_n[i];
+      int64_t qh;
+      int32_t n;
+      unpack(s_qn[i], qh, n);
+      a.ps.own_qh[k] = qh;
+      a.ps.own_ql[k] = s_ql[i];
+      a.ps.own_n[k] = n;
+    }
+    if (maxes) {
+      // a node inside the block: its maxima are complete here
+      const int tn = k / a.E;
+      const int64_t n0 = a.seg[(int64_t)tn * a.E], n1 = a.seg[(int64_t)(tn + 1) * a.E];
+      if (n0 >= p0 && n1 <= p1 && n0 - p0 == i) {
+        a.ps.own_ml[tn] = s_ml[i];
+        a.ps.own_mr[tn] = s_mr[i];
+      }
     }
   }
   if (tid == 0) {
     // the first and last segments of the block: their sums here
     const int64_t sl = a.seg[khi];
     const int ls = (int)((sl > p0 ? sl : p0) - p0);
-    a.ps.bf_q[blockIdx.x] = s_q[0];
-    a.ps.bf_n[blockIdx.x] = s_n[0];
-    a.ps.bl_q[blockIdx.x] = s_q[ls];
-    a.ps.bl_n[blockIdx.x] = s_n[ls];
+    int64_t qh;
+    int32_t n;
+    unpack(s_qn[0], qh, n);
+    a.ps.bf_qh[blockIdx.x] = qh;
+    a.ps.bf_ql[blockIdx.x] = s_ql[0];
+    a.ps.bf_n[blockIdx.x] = n;
+    unpack(s_qn[ls], qh, n);
+    a.ps.bl_qh[blockIdx.x] = qh;
+    a.ps.bl_ql[blockIdx.x] = s_ql[ls];
+    a.ps.bl_n[blockIdx.x] = n;
+    if (maxes) {
+      // the first and last nodes of the block: their maxima here
+      const int64_t sn = a.seg[(int64_t)(khi / a.E) * a.E];
+      const int lns = (int)((sn > p0 ? sn : p0) - p0);
+      a.ps.bf_ml[blockIdx.x] = s_ml[0];
+      a.ps.bf_mr[blockIdx.x] = s_mr[0];
+      a.ps.bl_ml[blockIdx.x] = s_ml[lns];
+      a.ps.bl_mr[blockIdx.x] = s_mr[lns];
+    }
   }
 }
 
 // inclusive prefix over the blocks of the first-segment partials; one
 // workgroup of 1024 threads, tiles of 1024 blocks
 __device__ inline void block_scan_body(int32_t nb, const PartSums& ps) {
-  __shared__ int64_t s_wq[16], s_wn[16];
-  __shared__ int64_t s_cq, s_cn;
+  __shared__ int64_t s_wh[16], s_wl[16], s_wn[16];
+  __shared__ int64_t s_ch, s_cl, s_cn;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   if (t == 0) {
-    s_cq = 0;
+    s_ch = 0;
+    s_cl = 0;
     s_cn = 0;
   }
   __syncthreads();
   for (int b0 = 0; b0 < nb; b0 += 1024) {
     const int b = b0 + t;
-    int64_t q = b < nb ? ps.bf_q[b] : 0, n = b < nb ? ps.bf_n[b] : 0;
+    int64_t qh = b < nb ? ps.bf_qh[b] : 0, ql = b < nb ? ps.bf_ql[b] : 0,
+            n = b < nb ? ps.bf_n[b] : 0;
     for (int o = 1; o < 64; o <<= 1) {
-      const int64_t yq = __shfl_up(q, o, 64), yn = __shfl_up(n, o, 64);
+      const int64_t yh = __shfl_up(qh, o, 64), yl = __shfl_up(ql, o, 64),
+                    yn = __shfl_up(n, o, 64);
       if (lane >= o) {
-        q += yq;
+        qh += yh;
+        ql += yl;
         n += yn;
       }
     }
     if (lane == 63) {
-      s_wq[w] = q;
+      s_wh[w] = qh;
+      s_wl[w] = ql;
       s_wn[w] = n;
     }
     __syncthreads();
-    int64_t cq = s_cq, cn = s_cn;
+    int64_t ch = s_ch, cl = s_cl, cn = s_cn;
     for (int k = 0; k < w; ++k) {
-      cq += s_wq[k];
+      ch += s_wh[k];
+      cl += s_wl[k];
       cn += s_wn[k];
     }
-    q += cq;
+    qh += ch;
+    ql += cl;
     n += cn;
     if (b < nb) {
-      ps.P_q[b] = q;
+      ps.P_qh[b] = qh;
+      ps.P_ql[b] = ql;
       ps.P_n[b] = n;
     }
     __syncthreads();  // every thread has read the carry and the wave sums
     if (t == 1023) {
-      s_cq = q;
+      s_ch = qh;
+      s_cl = ql;
       s_cn = n;
     }
     __syncthreads();
@@ -435,12 +564,14 @@ __global__ __launch_bounds__(1024) void block_scan_kernel(int32_t nb, PartSums p
 
 // root totals of every (tree, era) key: quantised residual sum and rows
 __global__ void root_totals_kernel(int32_t n_keys, const int64_t* __restrict__ seg, PartSums ps,
-                                   int64_t* __restrict__ tot_q, int64_t* __restrict__ tot_c) {
+                                   int64_t* __restrict__ tot_qh, int64_t* __restrict__ tot_ql,
+                                   int64_t* __restrict__ tot_c) {
   const int k = blockIdx.x * blockDim.x + threadIdx.x;
   if (k >= n_keys) return;
-  int64_t q, n;
-  segment_left_sums(k, seg, ps, q, n);
-  tot_q[k] = q;
+  int64_t qh, ql, n;
+  segment_left_sums(k, seg, ps, qh, ql, n);
+  tot_qh[k] = qh;
+  tot_ql[k] = ql;
   tot_c[k] = n;
 }
 
@@ -449,10 +580,7 @@ __global__ void root_totals_kernel(int32_t n_keys, const int64_t* __restrict__ s
 __global__ __launch_bounds__(256) void node_scan_kernel(
     int32_t T, int32_t nodes, int32_t E, int32_t wpn, int64_t n_pos,
     const int64_t* __restrict__ seg, const int32_t* __restrict__ present,
-    const int32_t* __restrict__ split_l, PartSums ps, const int64_t* __restrict__ tot_q,
-    int64_t* __restrict__ seg_next, int64_t* __restrict__ tot_q_next,
-    int64_t* __restrict__ tot_c_next, int32_t* __restrict__ present_next,
-    int32_t* __restrict__ key_list_next) {
+    const int32_t* __restrict__ split_l, PartSums ps, LevelNext nx) {
   __shared__ int64_t s_a[4], s_b[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / wpn, wg = wave - grp * wpn;
@@ -465,14 +593,15 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
   const int64_t base = live ? seg[k0] : 0;
   const int64_t c0 = 2 * k0;  // next keys of the children: c0 + side * E + e
   // left rows of a segment of the node (all of them when it does not split)
-  auto left_of = [&](int64_t k, int64_t cnt, int64_t& q) -> int64_t {
+  auto left_of = [&](int64_t k, int64_t cnt, int64_t& qh, int64_t& ql) -> int64_t {
     int64_t L = cnt;
-    q = 0;
-    if (sp) segment_left_sums(k, seg, ps, q, L);
+    qh = 0;
+    ql = 0;
+    if (sp) segment_left_sums(k, seg, ps, qh, ql, L);
     return L;
   };
-  // sum over the group of one value per wave (every thread gets it)
-  auto group_sum = [&](int64_t a, int64_t b, int64_t& ga, int64_t& gb) {
+  // sum (or max) over the group of one value per wave (every thread gets it)
+  auto group_sum = [&](int64_t a, int64_t b, int64_t& ga, int64_t& gb, bool is_max) {
     if (lane == 63) {
       s_a[wave] = a;
       s_b[wave] = b;
@@ -481,8 +610,13 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
     ga = 0;
     gb = 0;
     for (int w = grp * wpn; w < (grp + 1) * wpn; ++w) {
-      ga += s_a[w];
-      gb += s_b[w];
+      if (is_max) {
+        ga = s_a[w] > ga ? s_a[w] : ga;
+        gb = s_b[w] > gb ? s_b[w] : gb;
+      } else {
+        ga += s_a[w];
+        gb += s_b[w];
+      }
     }
     __syncthreads();
   };
@@ -490,8 +624,8 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
   if (live) {
     for (int e = gt; e < E; e += gthreads) {
       const int64_t cnt = seg[k0 + e + 1] - seg[k0 + e];
-      int64_t q;
-      ltot += left_of(k0 + e, cnt, q);
+      int64_t qh, ql;
+      ltot += left_of(k0 + e, cnt, qh, ql);
       tot += cnt;
     }
   }
@@ -502,15 +636,30 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
       tot += yt;
     }
   }
-  group_sum(ltot, tot, ltot, tot);
+  group_sum(ltot, tot, ltot, tot, false);
   const int side = (ltot <= tot - ltot) ? 0 : 1;  // the smaller child gets the histogram
+  // the children's histogram shifts from their largest |residual|
+  uint32_t ml = 0, mr = 0;
+  if (sp) node_child_max(tn, base, seg[k0 + E], ps, gt, gthreads, ml, mr);
+  ml = wgbm_wave_max_u32(ml);
+  mr = wgbm_wave_max_u32(mr);
+  {
+    int64_t gml, gmr;
+    group_sum((int64_t)ml, (int64_t)mr, gml, gmr, true);
+    ml = (uint32_t)gml;
+    mr = (uint32_t)gmr;
+  }
+  const int hs = live ? nx.node_shift[tn] : 0;
+  const int hs_l = sp ? node_shift_rule(ml, hs, nx.qbits) : hs;
+  const int hs_r = sp ? node_shift_rule(mr, hs, nx.qbits) : hs;
+  const bool both = sp && (hs_l != hs || hs_r != hs);  // both children histogrammed
   int64_t carry_l = 0, carry_r = 0;
   for (int e0 = 0; e0 < E; e0 += gthreads) {
     const int e = e0 + gt;
-    int64_t L = 0, R = 0, q = 0;
+    int64_t L = 0, R = 0, qh = 0, ql = 0;
     if (live && e < E) {
       const int64_t cnt = seg[k0 + e + 1] - seg[k0 + e];
-      L = left_of(k0 + e, cnt, q);
+      L = left_of(k0 + e, cnt, qh, ql);
       R = cnt - L;
     }
     int64_t il = L, ir = R;  // inclusive wave scans
@@ -540,20 +689,27 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
     il += pl;
     ir += pr;
     if (live && e < E) {
-      seg_next[c0 + e] = base + carry_l + il - L;
-      seg_next[c0 + E + e] = base + ltot + carry_r + ir - R;
+      nx.seg_next[c0 + e] = base + carry_l + il - L;
+      nx.seg_next[c0 + E + e] = base + ltot + carry_r + ir - R;
       // child totals (the words of children that do not exist are zero)
-      tot_q_next[c0 + e] = sp ? q : 0;
-      tot_c_next[c0 + e] = sp ? L : 0;
-      tot_q_next[c0 + E + e] = sp ? tot_q[k0 + e] - q : 0;
-      tot_c_next[c0 + E + e] = sp ? R : 0;
-      key_list_next[k0 + e] = sp ? (int32_t)(c0 + side * E + e) : -1;
+      nx.tot_qh_next[c0 + e] = sp ? qh : 0;
+      nx.tot_ql_next[c0 + e] = sp ? ql : 0;
+      nx.tot_c_next[c0 + e] = sp ? L : 0;
+      nx.tot_qh_next[c0 + E + e] = sp ? nx.tot_qh[k0 + e] - qh : 0;
+      nx.tot_ql_next[c0 + E + e] = sp ? nx.tot_ql[k0 + e] - ql : 0;
+      nx.tot_c_next[c0 + E + e] = sp ? R : 0;
+      nx.key_list_next[2 * (k0 + e)] =
+          sp ? (int32_t)(c0 + (both ? 0 : side * E) + e) : -1;
+      nx.key_list_next[2 * (k0 + e) + 1] = both ? (int32_t)(c0 + E + e) : -1;
     }
     carry_l += cl;
     carry_r += cr;
   }
-  if (live && gt < 2) present_next[2 * tn + gt] = sp;
-  if (tn == T * nodes - 1 && gt == 0) seg_next[(int64_t)2 * T * nodes * E] = n_pos;
+  if (live && gt < 2) {
+    nx.present_next[2 * tn + gt] = sp;
+    nx.node_shift_next[2 * tn + gt] = gt == 0 ? hs_l : hs_r;
+  }
+  if (tn == T * nodes - 1 && gt == 0) nx.seg_next[(int64_t)2 * T * nodes * E] = n_pos;
 }
 
 __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
@@ -633,18 +789,15 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
 // The three steps between route and scatter of a level with few keys (at
 // most 64 eras), in one workgroup of 1024 threads: the block prefix, the node
 // scan with one wave per node (wave w takes nodes w, w + 16, ...), and the
-// tile plan of the next level's histogram (the smaller child of every split,
-// the first n_list entries of key_list_next; skipped when n_list is 0).  The
+// tile plan of the next level's histogram (the key pairs of every split, the
+// first n_list entries of key_list_next; skipped when n_list is 0).  The
 // prefix and the node scan's outputs are read back by the same workgroup
 // after a barrier.
 __global__ __launch_bounds__(1024) void level_scan_kernel(
     int32_t nb, PartSums ps, int32_t T, int32_t nodes, int32_t E, int64_t n_pos,
     const int64_t* __restrict__ seg, const int32_t* __restrict__ present,
-    const int32_t* __restrict__ split_l, const int64_t* __restrict__ tot_q,
-    int64_t* __restrict__ seg_next, int64_t* __restrict__ tot_q_next,
-    int64_t* __restrict__ tot_c_next, int32_t* __restrict__ present_next,
-    int32_t* __restrict__ key_list_next, int32_t n_list, int32_t tile_rows, int32_t max_tiles,
-    Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
+    const int32_t* __restrict__ split_l, LevelNext nx, int32_t n_list, int32_t tile_rows,
+    int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
     int32_t* __restrict__ n_tiles) {
   block_scan_body(nb, ps);
   __syncthreads();
@@ -655,11 +808,11 @@ __global__ __launch_bounds__(1024) void level_scan_kernel(
     const int64_t base = seg[k0];
     const int64_t c0 = 2 * k0;
     // E <= 64: era e on lane e
-    int64_t L = 0, R = 0, q = 0;
+    int64_t L = 0, R = 0, qh = 0, ql = 0;
     if (lane < E) {
       const int64_t cnt = seg[k0 + lane + 1] - seg[k0 + lane];
       L = cnt;
-      if (sp) segment_left_sums(k0 + lane, seg, ps, q, L);
+      if (sp) segment_left_sums(k0 + lane, seg, ps, qh, ql, L);
       R = cnt - L;
     }
     int64_t il = L, ir = R;  // inclusive wave scans
@@ -672,22 +825,37 @@ __global__ __launch_bounds__(1024) void level_scan_kernel(
     }
     const int64_t ltot = __shfl(il, 63, 64), rtot = __shfl(ir, 63, 64);
     const int side = (ltot <= rtot) ? 0 : 1;  // the smaller child gets the histogram
+    uint32_t ml = 0, mr = 0;
+    if (sp) node_child_max(tn, base, seg[k0 + E], ps, lane, 64, ml, mr);
+    ml = wgbm_wave_max_u32(ml);
+    mr = wgbm_wave_max_u32(mr);
+    const int hs = nx.node_shift[tn];
+    const int hs_l = sp ? node_shift_rule(ml, hs, nx.qbits) : hs;
+    const int hs_r = sp ? node_shift_rule(mr, hs, nx.qbits) : hs;
+    const bool both = sp && (hs_l != hs || hs_r != hs);  // both children histogrammed
     if (lane < E) {
-      seg_next[c0 + lane] = base + il - L;
-      seg_next[c0 + E + lane] = base + ltot + ir - R;
+      nx.seg_next[c0 + lane] = base + il - L;
+      nx.seg_next[c0 + E + lane] = base + ltot + ir - R;
       // child totals (the words of children that do not exist are zero)
-      tot_q_next[c0 + lane] = sp ? q : 0;
-      tot_c_next[c0 + lane] = sp ? L : 0;
-      tot_q_next[c0 + E + lane] = sp ? tot_q[k0 + lane] - q : 0;
-      tot_c_next[c0 + E + lane] = sp ? R : 0;
-      key_list_next[k0 + lane] = sp ? (int32_t)(c0 + side * E + lane) : -1;
+      nx.tot_qh_next[c0 + lane] = sp ? qh : 0;
+      nx.tot_ql_next[c0 + lane] = sp ? ql : 0;
+      nx.tot_c_next[c0 + lane] = sp ? L : 0;
+      nx.tot_qh_next[c0 + E + lane] = sp ? nx.tot_qh[k0 + lane] - qh : 0;
+      nx.tot_ql_next[c0 + E + lane] = sp ? nx.tot_ql[k0 + lane] - ql : 0;
+      nx.tot_c_next[c0 + E + lane] = sp ? R : 0;
+      nx.key_list_next[2 * (k0 + lane)] =
+          sp ? (int32_t)(c0 + (both ? 0 : side * E) + lane) : -1;
+      nx.key_list_next[2 * (k0 + lane) + 1] = both ? (int32_t)(c0 + E + lane) : -1;
     }
-    if (lane < 2) present_next[2 * tn + lane] = sp;
-    if (tn == T * nodes - 1 && lane == 0) seg_next[(int64_t)2 * T * nodes * E] = n_pos;
+    if (lane < 2) {
+      nx.present_next[2 * tn + lane] = sp;
+      nx.node_shift_next[2 * tn + lane] = lane == 0 ? hs_l : hs_r;
+    }
+    if (tn == T * nodes - 1 && lane == 0) nx.seg_next[(int64_t)2 * T * nodes * E] = n_pos;
   }
   if (n_list <= 0) return;  // uniform
   __syncthreads();
-  plan_tiles_body(seg_next, 0, n_list, key_list_next, tile_rows, 0, max_tiles, tiles,
+  plan_tiles_body(nx.seg_next, 0, n_list, nx.key_list_next, tile_rows, 0, max_tiles, tiles,
                   key_tile_start, n_tiles);
 }
 

@@ -497,7 +497,8 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_f32_kernel(
 }
 
 // the engine's level arrays (exact int64 sums, int32 counts) and the sibling
-// as parent - computed child; key layout as hist_finalize_level_kernel
+// as parent - computed child; key layout and list pairs as
+// hist_finalize_level_kernel
 __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_level_kernel(
     const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
     const int32_t* __restrict__ key_list, int32_t n_list, int32_t n_chunks, int32_t V,
@@ -519,7 +520,10 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_level_kerne
   plane_sum(part, tile_words, plane * num_bins * kHistSlots, num_bins, t0, t1, sq, sc);
   const int64_t per_key = (int64_t)n_feats * num_bins;
   int64_t pkey = 0, skey = 0;
-  if (depth > 0) {
+  // the sibling by subtraction unless it is histogrammed itself (the second
+  // entry of the list pair)
+  const bool derive = depth > 0 && key_list[kk ^ 1] < 0;
+  if (derive) {
     const int era = key % num_eras;
     const int tn = key / num_eras;
     const int node = tn % nodes_in_level;
@@ -537,7 +541,7 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_level_kerne
     const int64_t fb = (int64_t)f * num_bins + b;
     hq[(int64_t)key * per_key + fb] = Q;
     hc[(int64_t)key * per_key + fb] = C;
-    if (depth > 0) {
+    if (derive) {
       hq[skey * per_key + fb] = parent_q[pkey * per_key + fb] - Q;
       hc[skey * per_key + fb] = parent_c[pkey * per_key + fb] - C;
     }
@@ -567,6 +571,9 @@ __global__ void hist_gather_features_kernel(const float* __restrict__ Gf,
 // plus the sibling histogram as (parent - computed child), also exact.
 //   computed key k = (tree, node, era) with node = 2*parent + side
 //   hq/hc layout: [tree][node][era][F][B]
+// Below the root the key list holds pairs (entries 2j, 2j + 1): the computed
+// child and -1 (its sibling is derived here), or both children (each
+// histogrammed at its own shift; nothing is derived).
 // --------------------------------------------------------------------------
 template <int FW>
 __global__ __launch_bounds__(256) void hist_finalize_level_kernel(
@@ -596,7 +603,7 @@ __global__ __launch_bounds__(256) void hist_finalize_level_kernel(
   const int64_t fb = (int64_t)f * num_bins + b;
   hq[(int64_t)key * per_key + fb] = Q;
   hc[(int64_t)key * per_key + fb] = (int32_t)C;
-  if (depth > 0) {
+  if (depth > 0 && key_list[kk ^ 1] < 0) {
     // key = ((tree*nodes + node)*E + era)
     const int era = key % num_eras;
     const int tn = key / num_eras;

@@ -111,15 +111,14 @@ template <int BT>
 __global__ __launch_bounds__(256) void split_level_e1_kernel(
     const int64_t* __restrict__ hq, const int32_t* __restrict__ hc, int32_t F, int32_t B_rt,
     const int32_t* __restrict__ feat_sel, int32_t n_sel, int32_t nodes_in_level,
-    const int32_t* __restrict__ present, const int32_t* __restrict__ shifts, float mcw,
+    const int32_t* __restrict__ present, const int32_t* __restrict__ node_shift, float mcw,
     float eps, float min_split_gain, unsigned long long* __restrict__ best) {
   const int B = BT > 0 ? BT : B_rt;
   const int blocks_per_node = (n_sel + 255) / 256;
   const int tn = blockIdx.x / blocks_per_node;
   const int l = (blockIdx.x - tn * blocks_per_node) * 256 + threadIdx.x;
   if (!present[tn]) return;  // uniform per workgroup
-  const int tree = tn / nodes_in_level;
-  const int s = shifts[tree];
+  const int s = node_shift[tn];
   float bg = -__builtin_inff();
   int bi = 0x7fffffff;
   if (l < n_sel) {
@@ -215,7 +214,7 @@ __device__ inline void atomic_max_grouped_u64(unsigned long long* base, int key,
 __global__ __launch_bounds__(128) void des_accumulate_kernel(
     const int64_t* __restrict__ hq, const int32_t* __restrict__ hc, int32_t F, int32_t B,
     int32_t E, const int32_t* __restrict__ feat_sel, int32_t n_sel, int32_t nodes_in_level,
-    int32_t n_tn, const int32_t* __restrict__ present, const int32_t* __restrict__ shifts,
+    int32_t n_tn, const int32_t* __restrict__ present, const int32_t* __restrict__ node_shift,
     float mcw, float eps, float* __restrict__ crit, int32_t* __restrict__ agree,
     int32_t* __restrict__ agree_max) {
   const int nb = B - 1;
@@ -232,7 +231,7 @@ __global__ __launch_bounds__(128) void des_accumulate_kernel(
   }
   int amax = 0;
   if (active) {
-    const int s = shifts[tn / nodes_in_level];
+    const int s = node_shift[tn];
     const int f = feat_sel[l];
     const int b0 = ch * kDesChunk;
     double gs[kDesChunk];
@@ -331,8 +330,8 @@ __global__ void des_finish_kernel(const unsigned long long* __restrict__ best,
                                   const int64_t* __restrict__ hq, const int32_t* __restrict__ hc,
                                   int32_t F, int32_t B, int32_t E,
                                   const int32_t* __restrict__ feat_sel, int32_t nodes_in_level,
-                                  int32_t n_tn, const int32_t* __restrict__ shifts, float mcw,
-                                  float eps, const float* __restrict__ staged,
+                                  int32_t n_tn, const int32_t* __restrict__ node_shift,
+                                  float mcw, float eps, const float* __restrict__ staged,
                                   const int64_t* __restrict__ seg, int32_t n_sel,
                                   int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
                                   float* __restrict__ split_gain_era) {
@@ -363,7 +362,7 @@ __global__ void des_finish_kernel(const unsigned long long* __restrict__ best,
                               : staged[k2 * ((int64_t)n_sel * nb) + idx];
     return;
   }
-  const int s = shifts[tn / nodes_in_level];
+  const int s = node_shift[tn];
   const int64_t base = (((int64_t)tn * E + e) * F + feat_sel[l]) * B;
   const int64_t* q = hq + base;
   const int32_t* c = hc + base;
@@ -396,7 +395,7 @@ template <int V, int BT>
 __global__ __launch_bounds__(kDesEraThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void des_era_kernel(
     const int8_t* __restrict__ codes, int64_t stride, int32_t F,
-    const float* __restrict__ rpos, const int32_t* __restrict__ shifts,
+    const float* __restrict__ rpos, const int32_t* __restrict__ node_shift,
     const int32_t* __restrict__ order,
     const int64_t* __restrict__ seg, int32_t E, int32_t n_keys, int32_t nodes_in_level,
     const int32_t* __restrict__ present, const int32_t* __restrict__ local_of, int32_t n_sel,
@@ -441,8 +440,7 @@ void des_era_kernel(
       const int tn = key / E;
       const int64_t begin = seg[key];
       const int n = (int)(seg[key + 1] - begin);  // <= 65536 (checked by the engine)
-      const int tree = tn / nodes_in_level;
-      const int s = shifts[tree];
+      const int s = node_shift[tn];
       for (int i = threadIdx.x; i < V * Bp * kHistSlots; i += kDesEraThreads) lds[i] = 0ull;
       __syncthreads();
       // software pipeline as in the tile histogram: wave w takes the row
@@ -575,7 +573,7 @@ template <int BT>
 __global__ __launch_bounds__(kDesPairThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void des_pair_kernel(
     const uint8_t* __restrict__ pcodes, uint32_t pbytes, uint32_t pstride, int32_t F,
-    const float* __restrict__ rpos, const int32_t* __restrict__ shifts,
+    const float* __restrict__ rpos, const int32_t* __restrict__ node_shift,
     const int32_t* __restrict__ order, const int64_t* __restrict__ seg, int32_t E,
     int32_t n_keys, int32_t nodes_in_level, const int32_t* __restrict__ present,
     const int32_t* __restrict__ local_of, int32_t n_sel, float mcw, float eps,
@@ -622,7 +620,7 @@ void des_pair_kernel(
       const int key = kb + l0 * slots;
       const int64_t begin = seg[key];
       const int n = (int)(seg[key + 1] - begin);  // <= 65536 (checked by the engine)
-      const int s = shifts[(key / E) / nodes_in_level];
+      const int s = node_shift[key / E];
 
       // rows: wave w takes groups [i, i + U), i = (w + k*nwaves)*U; lane
       // u < U loads row u's id and residual; two register sets alternate so
@@ -897,21 +895,24 @@ __global__ void local_scatter_kernel(const int32_t* __restrict__ feat_sel, int32
 
 int launch_split_level_e1(int n_tn, hipStream_t st, const int64_t* hq, const int32_t* hc,
                           int32_t F, int32_t B, const int32_t* feat_sel, int32_t n_sel,
-                          int32_t nodes_in_level, const int32_t* present, const int32_t* shifts,
-                          float mcw, float eps, float min_split_gain, unsigned long long* best) {
+                          int32_t nodes_in_level, const int32_t* present,
+                          const int32_t* node_shift, float mcw, float eps, float min_split_gain,
+                          unsigned long long* best) {
   const dim3 grid((unsigned)(n_tn * ((n_sel + 255) / 256)));
   if (B == 32)
     hipLaunchKernelGGL(split_level_e1_kernel<32>, grid, dim3(256), 0, st, hq, hc, F, B, feat_sel,
-                       n_sel, nodes_in_level, present, shifts, mcw, eps, min_split_gain, best);
+                       n_sel, nodes_in_level, present, node_shift, mcw, eps, min_split_gain,
+                       best);
   else
     hipLaunchKernelGGL(split_level_e1_kernel<0>, grid, dim3(256), 0, st, hq, hc, F, B, feat_sel,
-                       n_sel, nodes_in_level, present, shifts, mcw, eps, min_split_gain, best);
+                       n_sel, nodes_in_level, present, node_shift, mcw, eps, min_split_gain,
+                       best);
   WGBM_LAUNCH_CHECK();
   return 0;
 }
 
 int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* codes,
-                   int64_t stride, int32_t F, const float* rpos, const int32_t* shifts,
+                   int64_t stride, int32_t F, const float* rpos, const int32_t* node_shift,
                    const int32_t* order, const int64_t* seg, int32_t E, int32_t nodes_in_level,
                    const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
                    float eps, float* gain, int8_t* dir, const uint8_t* pcodes, int64_t n_rows,
@@ -936,7 +937,7 @@ int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* c
       attr = true;                                                                             \
     }                                                                                          \
     hipLaunchKernelGGL((des_pair_kernel<BB>), grid, dim3(kDesPairThreads), lds, st, pcodes,    \
-                       pbytes, (uint32_t)pstride, F, rpos, shifts, order, seg, E, n_keys,      \
+                       pbytes, (uint32_t)pstride, F, rpos, node_shift, order, seg, E, n_keys,  \
                        nodes_in_level, present, local_of, n_sel, mcw, eps, gain, dir);         \
     WGBM_LAUNCH_CHECK();                                                                       \
     return 0;                                                                                  \
@@ -965,7 +966,7 @@ int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* c
       attr = true;                                                                             \
     }                                                                                          \
     hipLaunchKernelGGL((des_era_kernel<VV, BB>), grid, dim3(kDesEraThreads), lds, st, codes,   \
-                       stride, F, rpos, shifts, order, seg, E, n_keys,                        \
+                       stride, F, rpos, node_shift, order, seg, E, n_keys,                    \
                        nodes_in_level, present, local_of, n_sel, B, mcw, eps, gain, dir);      \
     WGBM_LAUNCH_CHECK();                                                                       \
     return 0;                                                                                  \
