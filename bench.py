@@ -9,22 +9,31 @@ Metric: histogram GB/s (% HBM peak) + train/infer seconds,
   assigned uniformly at random to 16 depth-4 nodes), inputs resident in HBM.
   Algorithmic bytes per launch: R*F + 4R (gradients) + 4R (row indices, node
   case only) + nodes*F*B*8 (G and H written).
+* Before the warm-up steps the step runs for --settle-ms of wall time: the
+  GPU's clocks take tens of milliseconds of sustained load to settle, and a
+  short run would otherwise time the ramp.
 * roofline: the dominant kernel (hist_tiles), its average launch duration
-  measured with HIP events attached to its dispatches (start / stop events of
-  hipExtLaunchKernel on its launch stream) in every 8th step of the timed
-  region.  An attached event pair adds ~11 us of dispatch gap around its
-  kernel, so only a sample of the steps carries them (1/8 of that gap is in
-  the whole-op value).
-* cpu_baseline: the CPU oracle's exact histogram (C loop, one thread) on the
-  C2 root, on this machine's host.
+  from HIP events recorded on its launch stream right before and right
+  after every one of its dispatches in the timed region (wgbm_timer_enable(1):
+  the interval is the kernel plus the dispatch of its packet, a few
+  microseconds).  The same steps without events are timed too
+  (ms_per_step_no_events): each event pair adds that dispatch time again.
+* cpu_baseline: the CPU oracle (C loops on all OpenMP threads) running the
+  same C2 step, 1 warm-up then the median of 5; plus C1 end to end (quantile
+  edges, binning, 20 trees) on the CPU, median of 3.
+* dropin: the reference-shaped op, node_kernel.compute_histogram3, on C2 in
+  the reference's call pattern (root with sample_indices = all rows, then one
+  call per node with that node's rows), raw [N, F] int8 codes.
 * train_s / infer_s: end-to-end fit / predict wall seconds on config C3
   (1M x 1000 float32 features, 100 trees, depth 5, 32 bins, lr 0.01; predict
-  on 1M held-out rows), including host->device copies and binning.
+  on 1M held-out rows), including host->device copies and binning; C4 (era
+  DES) and C5 (softmax) likewise, C1 fit seconds on the GPU.
 * kernels: achieved HBM bandwidth of quantile edges, binning and inference on
   C3's held-out matrix resident on the device (algorithmic bytes / median
   call time).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-ms MS]
+                       [--no-e2e] [--no-cpu] [--no-extra] [--no-dropin]
 """
 from __future__ import annotations
 
@@ -93,6 +102,17 @@ def c5_inputs(rows_per_class=20_000, feats=100, K=10, seed=0):
     return X, lab
 
 
+def c1_inputs(n=10000, f=50, seed=0):
+    """Config C1: X ~ N(0,1) float32, y = X.w (10 nonzero) + 0.1 N(0,1)."""
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((n, f), dtype=np.float32)
+    w = np.zeros(f, np.float32)
+    idx = rng.choice(f, 10, replace=False)
+    w[idx] = rng.standard_normal(10)
+    y = (X @ w + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    return X, y
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -106,17 +126,18 @@ def cpu_model():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # the GPU's clocks settle over the first tens of milliseconds of sustained
-    # load: 40 warm-up steps (~20 ms), then 200 timed steps (~0.1 s)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="wall time the step runs before the warm-up steps (clock ramp)")
     ap.add_argument("--rows", type=int, default=1_000_000)
     ap.add_argument("--feats", type=int, default=1000)
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--e2e-rows", type=int, default=1_000_000)
     ap.add_argument("--e2e-trees", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--extra", default="", help="comma list of extra end-to-end configs: c4,c5")
+    ap.add_argument("--no-extra", action="store_true", help="skip C4 / C5 / C1 end to end")
+    ap.add_argument("--no-dropin", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -141,14 +162,15 @@ def main():
         del src, dst
         torch.cuda.empty_cache()
     N, F, B = args.rows, args.feats, 32
-    print(f"[bench] generating C2 inputs {N}x{F}", file=sys.stderr, flush=True)
+    log(f"generating C2 inputs {N}x{F}")
     codes_h, grad_h, node_h = c2_inputs(N, F)
     # the codes in the library's native layout, made by the pre-binned ingest
     # (what fit() does with int8 input): rows padded to a 128-byte multiple,
     # every byte in [0, B + 1]; algorithmic bytes still count F bytes per row
     from warpgbm_amd import device as D
 
-    nat = D.codes_from_int8(torch.from_numpy(codes_h).to(dev), False, B)[0]
+    raw = torch.from_numpy(codes_h).to(dev)
+    nat = D.codes_from_int8(raw, False, B)[0]
     codes, S = nat.rm, nat.stride
     grad = torch.from_numpy(grad_h).to(dev)
     order16_h = np.argsort(node_h, kind="stable").astype(np.int32)
@@ -162,7 +184,6 @@ def main():
     G16 = torch.zeros((16, F, B), device=dev)
     H16 = torch.zeros_like(G16)
     stream = _lib.current_stream_ptr(dev)
-
     flags = _lib.CODES_NATIVE
 
     def step():
@@ -174,77 +195,86 @@ def main():
                                                flags, G16.data_ptr(), H16.data_ptr(), stream),
                    "hist 16 nodes")
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    # sanity: exact counts (H accumulates over the warmup calls)
-    H1.zero_(), H16.zero_(), G1.zero_(), G16.zero_()
+    # sanity first: exact counts.  Its first-use torch reductions load code
+    # objects for ~0.1 s; done here, that idle time does not fall between the
+    # settle and the timed region (the clocks ramp again after ~0.1 s idle).
     step()
     torch.cuda.synchronize()
     assert torch.all(H1.sum(dim=2) == N), "root histogram counts are wrong"
     assert torch.equal(H16.sum(dim=0), H1[0]), "16-node counts do not add up to the root"
-    lib.wgbm_timer_reset()
-    timer_every = 8
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     e0.record()
-    for i in range(args.steps):
-        timed = i % timer_every == 0
-        if timed:
-            lib.wgbm_timer_enable(1)
-        step()
-        if timed:
-            lib.wgbm_timer_enable(0)
     e1.record()
     torch.cuda.synchronize()
-    ms_step = e0.elapsed_time(e1) / args.steps
-    import ctypes
+    # the clock ramp: the step runs for settle_ms of wall time (the clocks
+    # reach their steady state after ~20 ms of sustained load), then the
+    # warm-up steps lead straight into the timed region
+    n_settle, t0 = 0, time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
+        n_settle += 20
+    settle_ms = (time.perf_counter() - t0) * 1e3
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
 
-    tot = ctypes.c_double()
-    cnt = ctypes.c_int64()
-    lib.wgbm_timer_read(b"hist_tiles", ctypes.byref(tot), ctypes.byref(cnt))
+    def run_steps(with_events):
+        lib.wgbm_timer_reset()
+        lib.wgbm_timer_enable(1 if with_events else 0)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        lib.wgbm_timer_enable(0)
+        return e0.elapsed_time(e1) / args.steps
+
+    # the timed region: every hist_tiles dispatch carries a HIP event pair
+    ms_step = run_steps(True)
+    tot = C.c_double()
+    cnt = C.c_int64()
+    lib.wgbm_timer_read(b"hist_tiles", C.byref(tot), C.byref(cnt))
     k_ms = tot.value / max(cnt.value, 1)
+    assert cnt.value == 2 * args.steps, (cnt.value, args.steps)
+    # the same steps with no events attached (their dispatch overhead)
+    ms_step_plain = run_steps(False)
     bytes_root = N * F + 4 * N + 1 * F * B * 8
     bytes_16 = N * F + 4 * N + 4 * N + 16 * F * B * 8
     gbs = (bytes_root + bytes_16) / (ms_step * 1e-3) / 1e9
     k_achieved = ((bytes_root + bytes_16) / 2) / (k_ms * 1e-3) / 1e9
-    print(f"[bench] histogram step {ms_step:.3f} ms ({gbs:.1f} GB/s); hist_tiles "
-          f"{k_ms:.3f} ms/launch over {cnt.value} launches ({k_achieved:.1f} GB/s)",
-          file=sys.stderr, flush=True)
+    log(f"histogram step {ms_step:.4f} ms ({gbs:.1f} GB/s), {ms_step_plain:.4f} ms without "
+        f"events; hist_tiles {k_ms:.4f} ms/launch over {cnt.value} launches "
+        f"({k_achieved:.1f} GB/s); settle {n_settle} steps in {settle_ms:.0f} ms")
     # ceiling of the kernel's LDS stage: 64-bit LDS atomic adds per second in
     # the same LDS layout with no global traffic (measured live, after the
     # timed region so that its heavy LDS load does not precede the timing)
     lds_peak = C.c_double(0.0)
     _lib.check(lib.wgbm_probe_lds_atomics(512, 500, C.byref(lds_peak), stream), "lds probe")
     lds_peak = lds_peak.value
-    print(f"[bench] LDS atomic probe: {lds_peak:.3e} 64-bit adds/s", file=sys.stderr, flush=True)
+    log(f"LDS atomic probe: {lds_peak:.3e} 64-bit adds/s")
+
+    dropin = None
+    if not args.no_dropin:
+        dropin = dropin_leg(raw, grad, order16, seg16_h, N, F, B, dev)
+    del nat, codes, G16, H16, raw
+    torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
-        from oracle import clib, ops
-
-        rows_s = min(N, 1_000_000)
-        t0 = time.perf_counter()
-        s = ops.shift_from_absmax(np.max(np.abs(grad_h[:rows_s])), ops.qbits_for_rows(rows_s))
-        q = ops.quantise(grad_h[:rows_s], s)
-        clib.hist_exact_q(codes_h[:rows_s], q, None, np.arange(F), None, 1, B)
-        dt = time.perf_counter() - t0
-        cb = rows_s * F + 4 * rows_s + F * B * 8
-        cpu = {"value": round(cb / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"C2 root histogram, {rows_s}x{F} int8 codes, oracle C loop "
-                         f"(exact sums), 1 thread, {dt:.2f} s on {cpu_model()}"}
-        print(f"[bench] cpu baseline {cpu['value']} GB/s ({dt:.2f} s)", file=sys.stderr, flush=True)
-
-    del nat, codes, grad, order16, G16, H16
-    torch.cuda.empty_cache()
+        cpu = cpu_baseline_leg(codes_h, grad_h, order16_h, seg16_h, N, F, B,
+                               bytes_root + bytes_16, run_c1=not args.no_extra)
+    del grad, order16
 
     e2e = {}
     if not args.no_e2e:
         from warpgbm_amd import WarpGBM
 
         n = args.e2e_rows
-        print(f"[bench] generating C3 inputs {n}x{F}", file=sys.stderr, flush=True)
+        log(f"generating C3 inputs {n}x{F}")
         X, y = c3_inputs(n, F, 0)
         m = WarpGBM(num_bins=32, max_depth=5, n_estimators=args.e2e_trees, learning_rate=0.01)
         torch.cuda.synchronize()
@@ -261,8 +291,7 @@ def main():
         corr = float(np.corrcoef(p, yt)[0, 1])
         e2e = {"train_s": round(train_s, 3), "infer_s": round(infer_s, 3),
                "heldout_corr": round(corr, 4), "e2e_workload": f"C3 {n}x{F}, {args.e2e_trees} trees"}
-        print(f"[bench] C3 train {train_s:.2f} s, infer {infer_s:.2f} s, corr {corr:.4f}",
-              file=sys.stderr, flush=True)
+        log(f"C3 train {train_s:.3f} s, infer {infer_s:.3f} s, corr {corr:.4f}")
         e2e["kernels"] = c3_kernel_rooflines(m, Xt)
         del Xt
 
@@ -288,13 +317,17 @@ def main():
         "data": "synthetic (numpy default_rng(0); C2 histogram and C3 end-to-end workloads)",
         "config": {"workload": f"C2 histogram: root + 16 nodes, {N}x{F} int8, 32 bins, 1 era",
                    "rows": N, "features": F, "bins": B, "nodes": [1, 16], "row_stride": S},
+        "warmup_state": {"settle_ms": round(settle_ms, 1), "settle_steps": n_settle,
+                         "warmup_steps": args.warmup},
+        "ms_per_step_no_events": round(ms_step_plain, 4),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(k_achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(k_achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel": "hist_tiles_kernel<4,0,32,*,true> (native codes)",
                      "kernel_ms": round(k_ms, 4),
-                     "kernel_timing": f"HIP events on {cnt.value} launches (every "
-                                      f"{timer_every}th step of the timed region)",
+                     "kernel_timing": f"HIP events recorded around all {cnt.value} launches "
+                                      f"of the timed region ({args.steps} steps x 2) on the "
+                                      f"kernel's stream",
                      # the binding unit in practice: one 64-bit LDS atomic per
                      # (row, feature); peak = wgbm_probe_lds_atomics, measured
                      # above on this GPU
@@ -302,11 +335,114 @@ def main():
                                      "peak_per_s": round(lds_peak),
                                      "frac": round(N * F / (k_ms * 1e-3) / lds_peak, 4)}},
         "cpu_baseline": cpu,
+        "dropin": dropin,
     }
     out.update(e2e)
-    for cfg in [c for c in args.extra.split(",") if c]:
-        out.update(run_extra(cfg))
+    if not args.no_extra:
+        for cfg in ("c1", "c4", "c5"):
+            out.update(run_extra(cfg))
     print(json.dumps(out))
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def dropin_leg(raw, grad, order16, seg16_h, N, F, B, dev):
+    """The reference-shaped op in the reference's call pattern on C2:
+    node_kernel.compute_histogram3 on the raw [N, F] int8 codes, once for the
+    root (sample_indices = every row) and once per node (that node's rows),
+    as warpgbm/core.py:543-563 calls it; the outputs accumulate (the
+    reference's per-call torch.zeros is the caller's and is not timed).
+    Median of 5 steps after one warm-up, torch events on the current stream."""
+    import torch
+
+    from warpgbm_amd import node_kernel as nk
+
+    feats = torch.arange(F, dtype=torch.int32, device=dev)
+    era = torch.zeros(N, dtype=torch.int32, device=dev)
+    rows_all = torch.arange(N, dtype=torch.int32, device=dev)
+    node_rows = [order16[int(seg16_h[k]):int(seg16_h[k + 1])] for k in range(16)]
+    G = torch.zeros((17, 1, F, B), device=dev)
+    H = torch.zeros_like(G)
+
+    def dstep():
+        nk.compute_histogram3(raw, grad, rows_all, feats, era, G[0], H[0], B)
+        for k in range(16):
+            nk.compute_histogram3(raw, grad, node_rows[k], feats, era, G[k + 1], H[k + 1], B)
+
+    dstep()
+    ts = []
+    for _ in range(5):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dstep()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ms = sorted(ts)[2]
+    # root: codes + gradients + row ids; nodes: the same per row; outputs
+    nbytes = (N * F + 8 * N + F * B * 8) + (N * F + 8 * N + 16 * F * B * 8)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"drop-in compute_histogram3, C2 root + 16 per-node calls: {ms:.3f} ms ({gbs:.0f} GB/s)")
+    return {"op": "node_kernel.compute_histogram3", "calls_per_step": 17,
+            "ms_per_step": round(ms, 4), "bytes": int(nbytes), "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "pattern": "root (sample_indices = all rows) + one call per node, raw [N, F] int8 "
+                       "codes, all features, 1 era"}
+
+
+def cpu_baseline_leg(codes_h, grad_h, order16_h, seg16_h, N, F, B, step_bytes, run_c1):
+    """The CPU oracle (test infrastructure, the checker of the GPU path) on
+    the host: the same C2 step (root + 16 nodes, exact sums) with its C loops
+    on every OpenMP thread, 1 warm-up then the median of 5; C1 end to end
+    (quantile edges, binning, 20 trees of depth 5) median of 3."""
+    from oracle import clib, gbm, ops
+
+    threads = clib.num_threads()
+    feats = np.arange(F)
+    qbits = ops.qbits_for_rows(N)
+
+    def cstep():
+        s = ops.shift_from_absmax(np.max(np.abs(grad_h)), qbits)
+        q = ops.quantise(grad_h, s)
+        clib.hist_exact_q(codes_h, q, None, feats, None, 1, B)
+        for k in range(16):
+            clib.hist_exact_q(codes_h, q, order16_h[seg16_h[k]:seg16_h[k + 1]], feats, None, 1, B)
+
+    cstep()
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        cstep()
+        ts.append(time.perf_counter() - t0)
+    dt = sorted(ts)[2]
+    cpu = {"value": round(step_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+           "kind": "port", "host_cpus": os.cpu_count(), "cpu_model": cpu_model(),
+           "sample": f"the full C2 step (root + 16 nodes, {N}x{F} int8 codes, exact sums) by the "
+                     f"oracle's C loops on {threads} OpenMP threads; 1 warm-up, median of 5: "
+                     f"{dt:.3f} s per step"}
+    log(f"cpu baseline {cpu['value']} GB/s ({dt:.3f} s per step, {threads} threads)")
+    if run_c1:
+        X, y = c1_inputs()
+
+        def c1_fit():
+            edges = clib.quantile_edges_matrix(X, 32)
+            codes = clib.bin_matrix(X, edges)
+            gbm.Forest(num_bins=32, max_depth=5, n_estimators=20, learning_rate=0.1).fit_codes(
+                codes, y, hist=clib.hist_exact_q, scan=clib.split_scan_q)
+
+        c1_fit()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            c1_fit()
+            ts.append(time.perf_counter() - t0)
+        cpu["c1_train_s"] = round(sorted(ts)[1], 3)
+        cpu["c1_sample"] = ("C1 end to end: 10000x50 float32, edges + binning + 20 trees of depth 5 "
+                            "(32 bins), oracle growth with the C loops; median of 3")
+        log(f"cpu C1 train {cpu['c1_train_s']} s")
+    return cpu
 
 
 def c3_kernel_rooflines(m, Xt):
@@ -363,11 +499,25 @@ def c3_kernel_rooflines(m, Xt):
 
 
 def run_extra(cfg):
-    """End-to-end seconds of configs C4 (era-aware DES) and C5 (softmax)."""
+    """End-to-end seconds of configs C1 (fit only), C4 (era-aware DES) and C5
+    (softmax)."""
     import torch
 
     from warpgbm_amd import WarpGBM
 
+    if cfg == "c1":
+        X, y = c1_inputs()
+        WarpGBM(num_bins=32, max_depth=5, n_estimators=20, learning_rate=0.1).fit(X, y)
+        ts = []
+        for _ in range(3):
+            m = WarpGBM(num_bins=32, max_depth=5, n_estimators=20, learning_rate=0.1)
+            t0 = time.perf_counter()
+            m.fit(X, y)
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        tr = sorted(ts)[1]
+        log(f"C1 train {tr:.3f} s (median of 3)")
+        return {"c1_train_s": round(tr, 3)}
     if cfg == "c4":
         print("[bench] generating C4 inputs", file=sys.stderr, flush=True)
         X, y, era = c4_inputs()

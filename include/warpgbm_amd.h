@@ -220,9 +220,12 @@ void wgbm_engine_destroy(wgbm_engine* eng);
 
 /* ------------------------------------------------------------------------
  * Instrumentation: HIP-event timing of selected kernels (tags
- * "hist_tiles", "engine_hist_tiles").  Reading synchronises the events.
+ * "hist_tiles", "engine_hist_tiles").  mode 0 off; 1: events recorded on the
+ * kernel's stream right before and after its launch; 2: events attached to
+ * the kernel's dispatch (hipExtLaunchKernel).  Reading synchronises the
+ * events.
  * ------------------------------------------------------------------------ */
-void wgbm_timer_enable(int32_t on);
+void wgbm_timer_enable(int32_t mode);
 int wgbm_timer_read(const char* tag, double* total_ms, int64_t* count);
 void wgbm_timer_reset(void);
 /* Rate of 64-bit LDS atomic adds (per second, whole GPU) in the tile

@@ -28,6 +28,7 @@ def lib():
         L.oracle_quantile_edges_matrix.argtypes = [p, i64, i64, i64, p, i32, p]
         L.oracle_bin_matrix.argtypes = [p, i64, i64, i64, p, i32, p, i64]
         L.oracle_predict_tables.argtypes = [p, i64, i64, p, i32, i32, p, i32, C.c_float, p]
+        L.oracle_num_threads.restype = C.c_int
         L.oracle_split_scan_q.argtypes = [p, p, i64, i32, i32, C.c_float, C.c_float, p, p]
         _lib = L
     return _lib
@@ -134,3 +135,8 @@ def split_scan_q(Q, Cn, s, min_child_samples, eps):
     lib().oracle_split_scan_q(_ptr(Q), _ptr(Cn), E * F, B, int(s), np.float32(min_child_samples),
                               np.float32(eps), _ptr(gain), _ptr(dirn))
     return gain, dirn
+
+
+def num_threads():
+    """Threads of the OpenMP loops (OMP_NUM_THREADS, else every core)."""
+    return int(lib().oracle_num_threads())

@@ -21,41 +21,82 @@
  * Built by oracle/build.py with gcc -O2 -fopenmp -ffp-contract=off.
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+
+/* threads the OpenMP loops below use (OMP_NUM_THREADS, else all cores) */
+int oracle_num_threads(void) { return omp_get_max_threads(); }
+
+/* rows [p0, p1) of the call into Q, C restricted to features [f0, f1) */
+static void hist_rows(const int8_t* codes, int64_t stride, const int32_t* q, const int32_t* rows,
+                      int64_t p0, int64_t p1, const int32_t* feats, int32_t f0, int32_t f1,
+                      const int32_t* era, int32_t num_eras, int32_t num_bins, int64_t per_era,
+                      int64_t* Q, int64_t* C) {
+  for (int64_t p = p0; p < p1; ++p) {
+    const int64_t s = rows ? rows[p] : p;
+    const int e = num_eras == 1 ? 0 : era[s];
+    if (e < 0 || e >= num_eras) continue;
+    const int8_t* row = codes + s * stride;
+    const int64_t qs = q[s];
+    int64_t* Qe = Q + e * per_era;
+    int64_t* Ce = C + e * per_era;
+    for (int32_t f = f0; f < f1; ++f) {
+      const int b = row[feats ? feats[f] : f];
+      if (b < 0 || b >= num_bins) continue;
+      Qe[(int64_t)f * num_bins + b] += qs;
+      Ce[(int64_t)f * num_bins + b] += 1;
+    }
+  }
+}
 
 void oracle_hist_exact(const int8_t* codes, int64_t stride, const int32_t* q,
                        const int32_t* rows, int64_t n_rows, const int32_t* feats,
                        int32_t n_feats, const int32_t* era, int32_t num_eras, int32_t num_bins,
                        int64_t* Q, int64_t* C) {
   const int64_t per_era = (int64_t)n_feats * num_bins;
-  /* each thread owns a range of features: it reads those bytes of every row
-   * and is the only writer of their bins */
-  const int32_t fblk = 32;
-  const int32_t nblk = (n_feats + fblk - 1) / fblk;
-#pragma omp parallel for schedule(dynamic, 1)
-  for (int32_t kb = 0; kb < nblk; ++kb) {
-    const int32_t f0 = kb * fblk, f1 = f0 + fblk < n_feats ? f0 + fblk : n_feats;
-    for (int e = 0; e < num_eras; ++e) {
-      memset(Q + e * per_era + (int64_t)f0 * num_bins, 0, sizeof(int64_t) * (f1 - f0) * num_bins);
-      memset(C + e * per_era + (int64_t)f0 * num_bins, 0, sizeof(int64_t) * (f1 - f0) * num_bins);
-    }
-    for (int64_t p = 0; p < n_rows; ++p) {
-      const int64_t s = rows ? rows[p] : p;
-      const int e = num_eras == 1 ? 0 : era[s];
-      if (e < 0 || e >= num_eras) continue;
-      const int8_t* row = codes + s * stride;
-      const int64_t qs = q[s];
-      int64_t* Qe = Q + e * per_era;
-      int64_t* Ce = C + e * per_era;
-      for (int32_t f = f0; f < f1; ++f) {
-        const int b = row[feats ? feats[f] : f];
-        if (b < 0 || b >= num_bins) continue;
-        Qe[(int64_t)f * num_bins + b] += qs;
-        Ce[(int64_t)f * num_bins + b] += 1;
+  const int64_t words = per_era * num_eras;
+  const int nt = omp_get_max_threads();
+  memset(Q, 0, sizeof(int64_t) * words);
+  memset(C, 0, sizeof(int64_t) * words);
+  if (nt > 1 && words * 16 <= (int64_t)8 << 20 && n_rows >= 4096) {
+    /* small histograms: rows split over the threads, each into a private
+     * copy, then the copies added (integer sums: the order is immaterial) */
+    int64_t* priv = (int64_t*)calloc((size_t)nt * 2 * words, sizeof(int64_t));
+    if (priv) {
+#pragma omp parallel num_threads(nt)
+      {
+        const int t = omp_get_thread_num();
+        const int64_t p0 = n_rows * t / nt, p1 = n_rows * (t + 1) / nt;
+        int64_t* Qt = priv + (int64_t)t * 2 * words;
+        hist_rows(codes, stride, q, rows, p0, p1, feats, 0, n_feats, era, num_eras, num_bins,
+                  per_era, Qt, Qt + words);
       }
+#pragma omp parallel for schedule(static)
+      for (int64_t w = 0; w < words; ++w) {
+        int64_t a = 0, c = 0;
+        for (int t = 0; t < nt; ++t) {
+          a += priv[(int64_t)t * 2 * words + w];
+          c += priv[(int64_t)t * 2 * words + words + w];
+        }
+        Q[w] = a;
+        C[w] = c;
+      }
+      free(priv);
+      return;
     }
+  }
+  /* large histograms: each thread owns one contiguous range of features,
+   * reads those bytes of every row and is the only writer of their bins */
+#pragma omp parallel num_threads(nt)
+  {
+    const int t = omp_get_thread_num();
+    const int32_t f0 = (int32_t)((int64_t)n_feats * t / nt);
+    const int32_t f1 = (int32_t)((int64_t)n_feats * (t + 1) / nt);
+    if (f1 > f0)
+      hist_rows(codes, stride, q, rows, 0, n_rows, feats, f0, f1, era, num_eras, num_bins,
+                per_era, Q, C);
   }
 }
 

@@ -455,7 +455,7 @@ void wgbm_engine_destroy(wgbm_engine* eng) {
   delete eng;
 }
 
-void wgbm_timer_enable(int32_t on) { timer_enable(on); }
+void wgbm_timer_enable(int32_t mode) { timer_enable(mode); }
 int wgbm_timer_read(const char* tag, double* total_ms, int64_t* count) {
   long c = 0;
   int r = timer_read(tag, total_ms, &c);

@@ -111,6 +111,7 @@ __device__ inline int node_shift_rule(uint32_t absmax_bits, int parent_shift,
 }
 struct RouteArgs {
   int32_t mode;  // 0 root totals, 1 split level, 2 last level (leaves only)
+  int32_t want_max;  // mode 1: gather the children's max|r| (their level has histograms)
   const int64_t* seg;
   int32_t n_keys;
   int64_t n_pos;
@@ -134,6 +135,11 @@ struct RouteArgs {
   PartSums ps;
 };
 __global__ void route_kernel(RouteArgs a);
+// dynamic LDS of route_kernel: the slot sums, plus the node maxima
+inline size_t route_lds_bytes(const RouteArgs& a) {
+  if (a.mode == 2) return 0;
+  return (size_t)kPartBlock * (16 + (a.mode == 1 && a.want_max ? 8 : 0));
+}
 __global__ void block_scan_kernel(int32_t nb, PartSums ps);
 constexpr int kLevelScanMaxNodes = 64;  // (tree, node)s of a level for level_scan_kernel
 // Per split level: the children's segments and totals, their histogram
@@ -146,6 +152,7 @@ struct LevelNext {
   const int64_t* tot_ql;
   const int32_t* node_shift;  // [T * nodes] of this level
   int32_t qbits;
+  int32_t have_max;  // the route gathered the children's max|r| (else no shift changes)
   int64_t* seg_next;
   int64_t* tot_qh_next;
   int64_t* tot_ql_next;

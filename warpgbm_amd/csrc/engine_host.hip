@@ -365,7 +365,9 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     r0.rpos = e->rpos[0];
     r0.nodes = 1;
     r0.present = e->present[0];
-    hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, r0);
+    r0.want_max = 0;
+    hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads),
+                       route_lds_bytes(r0), st, r0);
     WGBM_LAUNCH_CHECK();
     hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
     WGBM_LAUNCH_CHECK();
@@ -527,7 +529,11 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     rl.present = e->present[cur];
     rl.split_l = e->split_l;
     rl.split_b = e->split_b;
-    hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, rl);
+    // the children's max|r| decides their histogram shifts; children at the
+    // last depth are leaves and need none
+    rl.want_max = d + 1 < D ? 1 : 0;
+    hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads),
+                       route_lds_bytes(rl), st, rl);
     WGBM_LAUNCH_CHECK();
     planned = false;
     LevelNext nx;
@@ -535,6 +541,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     nx.tot_ql = e->totql[cur];
     nx.node_shift = e->node_shift[cur];
     nx.qbits = e->qbits;
+    nx.have_max = d + 1 < D ? 1 : 0;
     nx.seg_next = e->seg[nxt];
     nx.tot_qh_next = e->totqh[nxt];
     nx.tot_ql_next = e->totql[nxt];

@@ -303,24 +303,25 @@ __device__ inline void node_child_max(int tn, int64_t P0, int64_t P1, const Part
 }
 
 __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
-  // Left sums of the block's segments, in the slot of the segment's first
-  // position in the block (distinct for distinct non-empty segments; empty
-  // segments own no position): s_qn packs the qh sum with the row count
-  // (qh_sum * 2^11 + rows: at most kPartBlock < 2^11 rows, |q63 >> 32| <=
-  // 2^30 per row), s_ql holds the ql sum.  With mode 1 also the largest
-  // |residual| (float bits) of each split node's left and right rows, in the
-  // slot of the node's first position in the block (the slot of its first
-  // segment there).
-  __shared__ int64_t s_qn[kPartBlock];
-  __shared__ int64_t s_ql[kPartBlock];
-  __shared__ int32_t s_key[kPartBlock];
-  __shared__ uint32_t s_ml[kPartBlock], s_mr[kPartBlock];
+  // Dynamic LDS (route_lds_bytes): left sums of the block's segments, in the
+  // slot of the segment's first position in the block (distinct for
+  // distinct non-empty segments; empty segments own no position): s_qn packs
+  // the qh sum with the row count (qh_sum * 2^11 + rows: at most kPartBlock
+  // < 2^11 rows, |q63 >> 32| <= 2^30 per row), s_ql holds the ql sum.  With
+  // a.want_max also the largest |residual| (float bits) of each split node's
+  // left and right rows, in the slot of the node's first position in the
+  // block (the slot of its first segment there).
+  extern __shared__ int64_t s_dyn[];
+  int64_t* s_qn = s_dyn;
+  int64_t* s_ql = s_dyn + kPartBlock;
+  uint32_t* s_ml = (uint32_t*)(s_dyn + 2 * kPartBlock);
+  uint32_t* s_mr = s_ml + kPartBlock;
   __shared__ int s_k[2];
   const int tid = threadIdx.x;
   const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
   const int64_t p1 = p0 + kPartBlock < a.n_pos ? p0 + kPartBlock : a.n_pos;
   const bool sums = a.mode != 2;
-  const bool maxes = a.mode == 1;
+  const bool maxes = a.mode == 1 && a.want_max;
   if (tid == 0) {
     s_k[0] = a.keyp[p0];
     s_k[1] = a.keyp[p1 - 1];
@@ -329,9 +330,10 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     for (int i = tid; i < kPartBlock; i += kPartThreads) {
       s_qn[i] = 0;
       s_ql[i] = 0;
-      s_key[i] = -1;
-      s_ml[i] = 0u;
-      s_mr[i] = 0u;
+      if (maxes) {
+        s_ml[i] = 0u;
+        s_mr[i] = 0u;
+      }
     }
   }
   __syncthreads();
@@ -366,22 +368,19 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   // Sums go to the LDS slot of the row's segment.  A wave whose rows all lie
   // in one segment (the common case for large segments) reduces them across
   // its lanes first and adds once; otherwise every lane adds its own row.
-  auto add_slot = [&](int sl, int k, bool act, int64_t qn, int64_t ql) {
+  auto add_slot = [&](int sl, bool act, int64_t qn, int64_t ql) {
     const uint64_t on = __ballot(act);
     if (on == 0ull) return;
     const int first = __builtin_ctzll(on);  // wave-uniform
     const int s0 = __shfl(sl, first, 64);
-    const int k0 = __shfl(k, first, 64);
     if (__ballot(act && sl != s0) == 0ull) {
       qn = wgbm_wave_sum(act ? qn : (int64_t)0);
       ql = wgbm_wave_sum(act ? ql : (int64_t)0);
       if ((tid & 63) == 0) {
-        s_key[s0] = k0;
         if (qn) atomicAdd((unsigned long long*)&s_qn[s0], (unsigned long long)qn);
         if (ql) atomicAdd((unsigned long long*)&s_ql[s0], (unsigned long long)ql);
       }
     } else if (act) {
-      s_key[sl] = k;
       if (qn) atomicAdd((unsigned long long*)&s_qn[sl], (unsigned long long)qn);
       if (ql) atomicAdd((unsigned long long*)&s_ql[sl], (unsigned long long)ql);
     }
@@ -420,7 +419,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
       const int t = tnv[j] / a.nodes;
       int64_t qn = 0, ql = 0;
       if (ok[j]) q63_words(rv[j], t, qn, ql);
-      add_slot(slot[j], key[j], ok[j], qn, ql);
+      add_slot(slot[j], ok[j], qn, ql);
     }
   } else {
     int cv[PJ];
@@ -441,7 +440,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
         dir = cv[j] > a.split_b[tn] ? 1 : 0;
         if (dir == 0) q63_words(rv[j], t, qn, ql);
       }
-      if (sums) add_slot(slot[j], key[j], dir != 2, qn, ql);
+      if (sums) add_slot(slot[j], dir == 0, qn, ql);
       if (maxes) {
         const uint32_t m = wgbm_abs_bits(rv[j]);
         max_slot(nslot[j], dir != 2, dir == 0 ? m : 0u, dir == 1 ? m : 0u);
@@ -456,9 +455,11 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     n = (int32_t)(qn & 2047);
     qh = qn >> 11;
   };
-  for (int i = tid; i < kPartBlock; i += kPartThreads) {
-    const int k = s_key[i];
-    if (k < 0) continue;  // no summed rows start here
+  for (int i = tid; i < (int)(p1 - p0); i += kPartThreads) {
+    // slot i opens a segment when its position's key differs from the one
+    // before it (block boundaries: the first slot always does)
+    const int k = a.keyp[p0 + i];
+    if (i > 0 && a.keyp[p0 + i - 1] == k) continue;
     if (a.seg[k] >= p0 && a.seg[k + 1] <= p1) {
       int64_t qh;
       int32_t n;
@@ -640,7 +641,7 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
   const int side = (ltot <= tot - ltot) ? 0 : 1;  // the smaller child gets the histogram
   // the children's histogram shifts from their largest |residual|
   uint32_t ml = 0, mr = 0;
-  if (sp) node_child_max(tn, base, seg[k0 + E], ps, gt, gthreads, ml, mr);
+  if (sp && nx.have_max) node_child_max(tn, base, seg[k0 + E], ps, gt, gthreads, ml, mr);
   ml = wgbm_wave_max_u32(ml);
   mr = wgbm_wave_max_u32(mr);
   {
@@ -650,8 +651,8 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
     mr = (uint32_t)gmr;
   }
   const int hs = live ? nx.node_shift[tn] : 0;
-  const int hs_l = sp ? node_shift_rule(ml, hs, nx.qbits) : hs;
-  const int hs_r = sp ? node_shift_rule(mr, hs, nx.qbits) : hs;
+  const int hs_l = sp && nx.have_max ? node_shift_rule(ml, hs, nx.qbits) : hs;
+  const int hs_r = sp && nx.have_max ? node_shift_rule(mr, hs, nx.qbits) : hs;
   const bool both = sp && (hs_l != hs || hs_r != hs);  // both children histogrammed
   int64_t carry_l = 0, carry_r = 0;
   for (int e0 = 0; e0 < E; e0 += gthreads) {
@@ -826,12 +827,12 @@ __global__ __launch_bounds__(1024) void level_scan_kernel(
     const int64_t ltot = __shfl(il, 63, 64), rtot = __shfl(ir, 63, 64);
     const int side = (ltot <= rtot) ? 0 : 1;  // the smaller child gets the histogram
     uint32_t ml = 0, mr = 0;
-    if (sp) node_child_max(tn, base, seg[k0 + E], ps, lane, 64, ml, mr);
+    if (sp && nx.have_max) node_child_max(tn, base, seg[k0 + E], ps, lane, 64, ml, mr);
     ml = wgbm_wave_max_u32(ml);
     mr = wgbm_wave_max_u32(mr);
     const int hs = nx.node_shift[tn];
-    const int hs_l = sp ? node_shift_rule(ml, hs, nx.qbits) : hs;
-    const int hs_r = sp ? node_shift_rule(mr, hs, nx.qbits) : hs;
+    const int hs_l = sp && nx.have_max ? node_shift_rule(ml, hs, nx.qbits) : hs;
+    const int hs_r = sp && nx.have_max ? node_shift_rule(mr, hs, nx.qbits) : hs;
     const bool both = sp && (hs_l != hs || hs_r != hs);  // both children histogrammed
     if (lane < E) {
       nx.seg_next[c0 + lane] = base + il - L;

@@ -896,11 +896,14 @@ static int launch_tiles_t(const HistLaunch& a, hipStream_t st) {
   }
   dim3 grid((unsigned)((int64_t)a.n_chunks * a.max_tiles));
   void* tm = timer_begin(a.timer_tag);
+  const bool marks = tm && timer_mode() == 1;
+  if (marks) WGBM_CHECK(hipEventRecord(timer_start_event(tm), st));
   hipExtLaunchKernelGGL((hist_tiles_kernel<V, MODE, BT, GATHER, NAT, RPOS>), grid,
-                        dim3(kHistThreads), lds, st, timer_start_event(tm), timer_stop_event(tm), 0,
-                        a.codes, a.n_rows, a.stride, a.n_feats, a.resid, a.resid_tree_stride,
-                        a.shifts, a.order, a.tiles, a.n_tiles, a.keys_per_tree, a.num_bins,
-                        a.part, a.sm);
+                        dim3(kHistThreads), lds, st, marks ? nullptr : timer_start_event(tm),
+                        marks ? nullptr : timer_stop_event(tm), 0, a.codes, a.n_rows, a.stride,
+                        a.n_feats, a.resid, a.resid_tree_stride, a.shifts, a.order, a.tiles,
+                        a.n_tiles, a.keys_per_tree, a.num_bins, a.part, a.sm);
+  if (marks) WGBM_CHECK(hipEventRecord(timer_stop_event(tm), st));
   timer_end(tm);
   WGBM_LAUNCH_CHECK();
   return 0;

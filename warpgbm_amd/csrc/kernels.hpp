@@ -128,9 +128,11 @@ void* scratch_get(hipStream_t st, size_t bytes, int slot);
 void scratch_release_all();
 
 // optional HIP-event timers of selected kernels: timer_begin(tag) gives a
-// handle (nullptr when timing is off) whose start / stop events the launcher
-// passes to hipExtLaunchKernel; timer_end(handle) files the interval
+// handle (null when timers are off) whose two events the launcher records
+// around the launch on its stream (timer_mode() 1) or passes to
+// hipExtLaunchKernel (mode 2); timer_end(handle) files the interval
 bool timer_enabled();
+int timer_mode();
 void* timer_begin(const char* tag);
 hipEvent_t timer_start_event(void* h);
 hipEvent_t timer_stop_event(void* h);

@@ -94,24 +94,27 @@ int fill_u64(void* p, int64_t n, unsigned long long v, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
-// kernel timers: when enabled, the launcher of a timed kernel attaches a pair
-// of HIP events to the kernel's own dispatch (hipExtLaunchKernel start / stop
-// events), so an interval is the kernel's execution alone, without the
-// dispatch of the packet; wgbm_timer_read sums the intervals per tag.
+// kernel timers, wgbm_timer_enable(mode): mode 1 records a HIP event on the
+// kernel's stream right before and right after the launch of a timed kernel
+// (hipEventRecord markers: the interval is the kernel's execution plus the
+// dispatch of its packet); mode 2 attaches the pair to the kernel's own
+// dispatch (hipExtLaunchKernel start / stop events).  wgbm_timer_read sums
+// the intervals per tag.
 // ---------------------------------------------------------------------------
 struct TimerRec {
   std::string tag;
   hipEvent_t a, b;
 };
 static std::mutex g_timer_mu;
-static bool g_timer_on = false;
+static int g_timer_mode = 0;
 static std::vector<TimerRec> g_timer_pending;
 static std::map<std::string, std::pair<double, long>> g_timer_acc;
 
-bool timer_enabled() { return g_timer_on; }
+bool timer_enabled() { return g_timer_mode != 0; }
+int timer_mode() { return g_timer_mode; }
 
 void* timer_begin(const char* tag) {
-  if (!g_timer_on || !tag) return nullptr;
+  if (!g_timer_mode || !tag) return nullptr;
   TimerRec* r = new TimerRec{tag, nullptr, nullptr};
   if (hipEventCreate(&r->a) != hipSuccess) {
     delete r;
@@ -136,9 +139,9 @@ void timer_end(void* h) {
   delete r;
 }
 
-void timer_enable(int on) {
+void timer_enable(int mode) {
   std::lock_guard<std::mutex> lk(g_timer_mu);
-  g_timer_on = on != 0;
+  g_timer_mode = mode == 1 || mode == 2 ? mode : 0;
 }
 
 int timer_read(const char* tag, double* total_ms, long* count) {
