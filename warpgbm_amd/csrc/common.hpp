@@ -120,6 +120,71 @@ __device__ __forceinline__ unsigned long long wgbm_row_bcast(unsigned long long 
   }
 }
 
+// Wave-wide reductions on DPP moves (VALU; no LDS crossbar traffic): a
+// Hillis-Steele scan inside each row of 16 lanes (row_shr 1, 2, 4, 8; lanes
+// with no source read 0), then the rows combined with row_bcast:15 (rows 1
+// and 3) and row_bcast:31 (rows 2 and 3).  Lane 63 then holds the reduction
+// over the wave; it is read out as a wave-uniform value.  0 is the identity
+// (sums, and maxima of unsigned values).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint32_t wgbm_dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xf, true);
+}
+
+__device__ __forceinline__ uint32_t wgbm_wave_reduce_max_u32(uint32_t x) {
+#define WGBM_MAXSTEP(C, M)              \
+  {                                     \
+    const uint32_t y = wgbm_dpp_u32<C, M>(x); \
+    x = y > x ? y : x;                  \
+  }
+  WGBM_MAXSTEP(0x111, 0xf)
+  WGBM_MAXSTEP(0x112, 0xf)
+  WGBM_MAXSTEP(0x114, 0xf)
+  WGBM_MAXSTEP(0x118, 0xf)
+  WGBM_MAXSTEP(0x142, 0xa)
+  WGBM_MAXSTEP(0x143, 0xc)
+#undef WGBM_MAXSTEP
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+__device__ __forceinline__ int64_t wgbm_wave_reduce_add_i64(int64_t x) {
+#define WGBM_ADDSTEP(C, M)                                                     \
+  {                                                                            \
+    const uint32_t lo = wgbm_dpp_u32<C, M>((uint32_t)(uint64_t)x);             \
+    const uint32_t hi = wgbm_dpp_u32<C, M>((uint32_t)((uint64_t)x >> 32));     \
+    x += (int64_t)(((uint64_t)hi << 32) | lo);                                 \
+  }
+  WGBM_ADDSTEP(0x111, 0xf)
+  WGBM_ADDSTEP(0x112, 0xf)
+  WGBM_ADDSTEP(0x114, 0xf)
+  WGBM_ADDSTEP(0x118, 0xf)
+  WGBM_ADDSTEP(0x142, 0xa)
+  WGBM_ADDSTEP(0x143, 0xc)
+#undef WGBM_ADDSTEP
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)x, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)x >> 32), 63);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Inclusive prefix sum over the wave's lanes (lane i: lanes 0..i), the same
+// DPP sequence without the read-out.
+__device__ __forceinline__ int64_t wgbm_wave_incl_scan_i64(int64_t x) {
+#define WGBM_SCANSTEP(C, M)                                                    \
+  {                                                                            \
+    const uint32_t lo = wgbm_dpp_u32<C, M>((uint32_t)(uint64_t)x);             \
+    const uint32_t hi = wgbm_dpp_u32<C, M>((uint32_t)((uint64_t)x >> 32));     \
+    x += (int64_t)(((uint64_t)hi << 32) | lo);                                 \
+  }
+  WGBM_SCANSTEP(0x111, 0xf)
+  WGBM_SCANSTEP(0x112, 0xf)
+  WGBM_SCANSTEP(0x114, 0xf)
+  WGBM_SCANSTEP(0x118, 0xf)
+  WGBM_SCANSTEP(0x142, 0xa)
+  WGBM_SCANSTEP(0x143, 0xc)
+#undef WGBM_SCANSTEP
+  return x;
+}
+
 // Order-preserving encoding of a non-negative float's magnitude as uint32
 // (for atomicMax over |r|).  NaN maps above +inf and is reported as an error.
 __device__ inline uint32_t wgbm_abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }

@@ -356,8 +356,8 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     const int64_t sk = a.seg[key[j]];
     slot[j] = (int)((sk > p0 ? sk : p0) - p0);
     tnv[j] = key[j] / a.E;
-    nslot[j] = 0;
-    if (maxes) {
+    nslot[j] = slot[j];  // one era: the node is the segment
+    if (maxes && a.E > 1) {
       const int64_t sn = a.seg[(int64_t)tnv[j] * a.E];
       nslot[j] = (int)((sn > p0 ? sn : p0) - p0);
     }
@@ -372,10 +372,10 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     const uint64_t on = __ballot(act);
     if (on == 0ull) return;
     const int first = __builtin_ctzll(on);  // wave-uniform
-    const int s0 = __shfl(sl, first, 64);
+    const int s0 = __builtin_amdgcn_readlane(sl, first);
     if (__ballot(act && sl != s0) == 0ull) {
-      qn = wgbm_wave_sum(act ? qn : (int64_t)0);
-      ql = wgbm_wave_sum(act ? ql : (int64_t)0);
+      qn = wgbm_wave_reduce_add_i64(act ? qn : (int64_t)0);
+      ql = wgbm_wave_reduce_add_i64(act ? ql : (int64_t)0);
       if ((tid & 63) == 0) {
         if (qn) atomicAdd((unsigned long long*)&s_qn[s0], (unsigned long long)qn);
         if (ql) atomicAdd((unsigned long long*)&s_ql[s0], (unsigned long long)ql);
@@ -390,10 +390,10 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     const uint64_t on = __ballot(act);
     if (on == 0ull) return;
     const int first = __builtin_ctzll(on);
-    const int s0 = __shfl(sl, first, 64);
+    const int s0 = __builtin_amdgcn_readlane(sl, first);
     if (__ballot(act && sl != s0) == 0ull) {
-      ml = wgbm_wave_max_u32(act ? ml : 0u);
-      mr = wgbm_wave_max_u32(act ? mr : 0u);
+      ml = wgbm_wave_reduce_max_u32(act ? ml : 0u);
+      mr = wgbm_wave_reduce_max_u32(act ? mr : 0u);
       if ((tid & 63) == 0) {
         if (ml) atomicMax(&s_ml[s0], ml);
         if (mr) atomicMax(&s_mr[s0], mr);
@@ -520,15 +520,9 @@ __device__ inline void block_scan_body(int32_t nb, const PartSums& ps) {
     const int b = b0 + t;
     int64_t qh = b < nb ? ps.bf_qh[b] : 0, ql = b < nb ? ps.bf_ql[b] : 0,
             n = b < nb ? ps.bf_n[b] : 0;
-    for (int o = 1; o < 64; o <<= 1) {
-      const int64_t yh = __shfl_up(qh, o, 64), yl = __shfl_up(ql, o, 64),
-                    yn = __shfl_up(n, o, 64);
-      if (lane >= o) {
-        qh += yh;
-        ql += yl;
-        n += yn;
-      }
-    }
+    qh = wgbm_wave_incl_scan_i64(qh);
+    ql = wgbm_wave_incl_scan_i64(ql);
+    n = wgbm_wave_incl_scan_i64(n);
     if (lane == 63) {
       s_wh[w] = qh;
       s_wl[w] = ql;
@@ -630,20 +624,15 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
       tot += cnt;
     }
   }
-  for (int o = 1; o < 64; o <<= 1) {  // inclusive wave scans: lane 63 holds the sums
-    const int64_t yl = __shfl_up(ltot, o, 64), yt = __shfl_up(tot, o, 64);
-    if (lane >= o) {
-      ltot += yl;
-      tot += yt;
-    }
-  }
+  ltot = wgbm_wave_incl_scan_i64(ltot);  // inclusive wave scans: lane 63 holds the sums
+  tot = wgbm_wave_incl_scan_i64(tot);
   group_sum(ltot, tot, ltot, tot, false);
   const int side = (ltot <= tot - ltot) ? 0 : 1;  // the smaller child gets the histogram
   // the children's histogram shifts from their largest |residual|
   uint32_t ml = 0, mr = 0;
   if (sp && nx.have_max) node_child_max(tn, base, seg[k0 + E], ps, gt, gthreads, ml, mr);
-  ml = wgbm_wave_max_u32(ml);
-  mr = wgbm_wave_max_u32(mr);
+  ml = wgbm_wave_reduce_max_u32(ml);
+  mr = wgbm_wave_reduce_max_u32(mr);
   {
     int64_t gml, gmr;
     group_sum((int64_t)ml, (int64_t)mr, gml, gmr, true);
@@ -663,14 +652,7 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
       L = left_of(k0 + e, cnt, qh, ql);
       R = cnt - L;
     }
-    int64_t il = L, ir = R;  // inclusive wave scans
-    for (int o = 1; o < 64; o <<= 1) {
-      const int64_t yl = __shfl_up(il, o, 64), yr = __shfl_up(ir, o, 64);
-      if (lane >= o) {
-        il += yl;
-        ir += yr;
-      }
-    }
+    int64_t il = wgbm_wave_incl_scan_i64(L), ir = wgbm_wave_incl_scan_i64(R);
     // earlier waves of the group, and the chunk totals for the carry
     if (lane == 63) {
       s_a[wave] = il;
@@ -816,20 +798,13 @@ __global__ __launch_bounds__(1024) void level_scan_kernel(
       if (sp) segment_left_sums(k0 + lane, seg, ps, qh, ql, L);
       R = cnt - L;
     }
-    int64_t il = L, ir = R;  // inclusive wave scans
-    for (int o = 1; o < 64; o <<= 1) {
-      const int64_t yl = __shfl_up(il, o, 64), yr = __shfl_up(ir, o, 64);
-      if (lane >= o) {
-        il += yl;
-        ir += yr;
-      }
-    }
+    int64_t il = wgbm_wave_incl_scan_i64(L), ir = wgbm_wave_incl_scan_i64(R);
     const int64_t ltot = __shfl(il, 63, 64), rtot = __shfl(ir, 63, 64);
     const int side = (ltot <= rtot) ? 0 : 1;  // the smaller child gets the histogram
     uint32_t ml = 0, mr = 0;
     if (sp && nx.have_max) node_child_max(tn, base, seg[k0 + E], ps, lane, 64, ml, mr);
-    ml = wgbm_wave_max_u32(ml);
-    mr = wgbm_wave_max_u32(mr);
+    ml = wgbm_wave_reduce_max_u32(ml);
+    mr = wgbm_wave_reduce_max_u32(mr);
     const int hs = nx.node_shift[tn];
     const int hs_l = sp && nx.have_max ? node_shift_rule(ml, hs, nx.qbits) : hs;
     const int hs_r = sp && nx.have_max ? node_shift_rule(mr, hs, nx.qbits) : hs;
