@@ -106,6 +106,25 @@ int wgbm_histogram_segments(const int8_t* codes, int64_t n_rows, int64_t stride,
                             int32_t n_seg, int64_t n_pos, int32_t num_bins, int32_t flags,
                             float* G, float* H, void* stream);
 
+/* wgbm_histogram_segments that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as wgbm_histogram_segments; the
+ * call's working memory (tile plan, partial histograms, gathered residuals)
+ * is a fixed device array of WGBM_NOALLOC_SCRATCH_BYTES that every GPU the
+ * library runs on holds until the process ends.  A call needing more (about
+ * 4 bytes per row of a row list plus 256 KiB per histogram tile of 1000
+ * features at 32 bins; the 1M x 1000 root + 16-node calls need ~25 MiB)
+ * returns WGBM_EINVAL with the sizes in wgbm_last_error().  Calls that
+ * overlap on one GPU (other streams, other threads) share the array and
+ * race: serialise them. */
+#define WGBM_NOALLOC_SCRATCH_BYTES (64 * 1024 * 1024)
+int wgbm_histogram_segments_noalloc(const int8_t* codes, int64_t n_rows, int64_t stride,
+                                    int32_t n_feats, const float* residuals, const int32_t* order,
+                                    const int64_t* seg, int32_t n_seg, int64_t n_pos,
+                                    int32_t num_bins, int32_t flags, float* G, float* H,
+                                    void* stream);
+
 /* Quantile edges (the torch.quantile call of warpgbm/core.py:529-534) from
  * columns already sorted ascending (NaN last): sorted float32 [n_feats, n];
  * q float32 [nq]; edges float32 [n_feats, nq]. */

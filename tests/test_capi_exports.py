@@ -53,3 +53,17 @@ def test_error_reporting_without_gpu_work():
     rc = lib.wgbm_compute_histogram3(None, 10, 5, None, None, 4, None, 5, None, 1, None, None,
                                      200, 64, 4, None)
     assert rc == 1000 and "num_bins" in lib.wgbm_last_error().decode()
+
+
+def test_noalloc_size_check_without_gpu_work():
+    """The no-allocation entry point refuses a call whose working memory
+    exceeds its fixed array before any HIP call, naming both sizes."""
+    from warpgbm_amd import _lib
+
+    lib = _lib.load()
+    one = ctypes.c_void_p(1)  # never dereferenced: the size check comes first
+    rc = lib.wgbm_histogram_segments_noalloc(one, 1 << 24, 1024, 1000, one, one, one, 1, 1 << 24,
+                                             32, 0, one, one, None)
+    assert rc == 1000
+    msg = lib.wgbm_last_error().decode()
+    assert "needs" in msg and str(64 * 1024 * 1024) in msg

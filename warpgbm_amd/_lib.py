@@ -32,6 +32,8 @@ SIGNATURES = {
     "wgbm_predict_forest": (C.c_int, [_p, _i64, _i64, _p, _i64, _i64, _f32, _p, _p]),
     "wgbm_histogram_segments": (C.c_int, [_p, _i64, _i64, _i32, _p, _p, _p, _i32, _i64, _i32,
                                           _i32, _p, _p, _p]),
+    "wgbm_histogram_segments_noalloc": (C.c_int, [_p, _i64, _i64, _i32, _p, _p, _p, _i32, _i64,
+                                                  _i32, _i32, _p, _p, _p]),
     "wgbm_quantile_edges": (C.c_int, [_p, _i64, _i32, _p, _i32, _p, _p]),
     "wgbm_quantile_edges_matrix": (C.c_int, [_p, _i64, _i32, _i64, _p, _i32, _p, _p]),
     "wgbm_bin_matrix": (C.c_int, [_p, _i64, _i32, _i64, _p, _i32, _p, _i64, _p, _p]),

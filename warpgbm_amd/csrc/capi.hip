@@ -1,5 +1,6 @@
 // extern "C" boundary of the library (declared in include/warpgbm_amd.h).
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/warpgbm_amd.h"
 #include "common.hpp"
@@ -12,6 +13,8 @@ using namespace wgbm;
 
 static inline hipStream_t S(void* s) { return (hipStream_t)s; }
 static inline unsigned nblocks(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+constexpr int kMaxDevices = 64;  // devices the no-allocation entry point keeps addresses for
 
 extern "C" {
 
@@ -27,49 +30,97 @@ const char* wgbm_last_error(void) { return wgbm_last_error_impl(); }
 // ---------------------------------------------------------------------------
 // shared histogram pipeline: shift -> (era sort) -> tiles -> partials -> f32
 // ---------------------------------------------------------------------------
+// Working memory of one call: the library's arena (scratch_get, grows on
+// demand), or one fixed buffer carved into 256-byte-aligned pieces (the
+// no-allocation entry point).  Every piece is written before it is read.
+struct HistScratch {
+  hipStream_t st;
+  unsigned char* base = nullptr;
+  size_t cap = 0, used = 0;
+  void* get(size_t bytes, int slot) {
+    if (!base) return scratch_get(st, bytes, slot);
+    const size_t off = (used + 255) & ~(size_t)255;
+    if (off > cap || bytes > cap - off) return nullptr;
+    used = off + bytes;
+    return base + off;
+  }
+};
+
+constexpr int kAbsBlocks = 256;  // per-block |residual| maxima of one call, at most
+
+// sizes of one call, shared by the pipeline and the no-allocation size check
+struct HistPlan {
+  int V = 1, n_chunks = 1, n_abs = 1, n_keys = 1;
+  bool regroup = false, gather_resid = false;
+  int64_t R = 1024, max_tiles = 1, tile_words = 0;
+};
+
+static HistPlan hist_plan(int32_t n_hist_feats, int32_t num_bins, int64_t n_pos,
+                          const int32_t* rows, const int64_t* seg_dev, int32_t n_seg,
+                          int32_t num_eras) {
+  HistPlan p;
+  p.V = hist_pick_v(num_bins, n_hist_feats);
+  p.n_chunks = (n_hist_feats + kHistSlots * p.V - 1) / (kHistSlots * p.V);
+  // per-block maxima of |residual|: blocks of 1024 threads, at most 256 of
+  // them (every wave of the tile kernel reduces them to the shift)
+  p.n_abs = (int)std::max<int64_t>(1, std::min<int64_t>(nblocks(n_pos, 1024), kAbsBlocks));
+  // a row list without an era regrouping: the residuals are gathered into
+  // position order in the same pass, so the tile kernel reads them
+  // contiguously instead of one 4-byte gather per row
+  p.regroup = !seg_dev && num_eras > 1;
+  p.gather_resid = rows && !p.regroup;
+  // segments: explicit (seg_dev), by era (sort rows by era), or a single one
+  p.n_keys = seg_dev ? n_seg : (p.regroup ? num_eras : 1);
+  // tiles: ~1 workgroup per CU over the whole call
+  const int64_t tiles_target = std::max<int64_t>(1, kHistTargetWGCall / p.n_chunks);
+  int64_t R = (n_pos + tiles_target - 1) / tiles_target;
+  p.R = std::min<int64_t>(std::max<int64_t>(R, 1024), WGBM_MAX_TILE_ROWS);
+  p.max_tiles = n_pos / p.R + p.n_keys + 1;
+  p.tile_words = (int64_t)p.n_chunks * kHistSlots * p.V * num_bins;
+  return p;
+}
+
+// bytes of the pieces a call without era regrouping or feature selection
+// takes (control words, gathered residuals, tiles, tile starts, partials),
+// each rounded up to 256 bytes as HistScratch carves them
+static size_t hist_scratch_bytes(const HistPlan& p, int64_t n_pos) {
+  auto r = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  size_t b = r(sizeof(uint32_t) * (64 + kAbsBlocks));
+  if (p.gather_resid) b += r(sizeof(float) * (size_t)std::max<int64_t>(n_pos, 1));
+  b += r(sizeof(Tile) * (size_t)p.max_tiles);
+  b += r(sizeof(int32_t) * ((size_t)p.n_keys + 1));
+  b += r(sizeof(unsigned long long) * (size_t)(p.max_tiles * p.tile_words));
+  return b;
+}
+
 static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t stride,
                               int32_t n_hist_feats, const float* resid, const int32_t* rows,
                               int64_t n_pos, const int64_t* seg_dev, int32_t n_seg,
                               const int32_t* era, int32_t num_eras, const int32_t* feat_idx,
                               int32_t n_out_feats, int32_t num_bins, float* G, float* H,
-                              bool native, hipStream_t st) {
-  const int V = hist_pick_v(num_bins, n_hist_feats);
-  const int n_chunks = (n_hist_feats + kHistSlots * V - 1) / (kHistSlots * V);
-  // scratch layout (slot 0: control words and the per-block maxima)
-  constexpr int kAbsBlocks = 256;
-  uint32_t* ctl = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (64 + kAbsBlocks), 0);
+                              bool native, HistScratch& sc) {
+  hipStream_t st = sc.st;
+  const HistPlan pl = hist_plan(n_hist_feats, num_bins, n_pos, rows, seg_dev, n_seg, num_eras);
+  const int V = pl.V, n_chunks = pl.n_chunks, n_abs = pl.n_abs, n_keys = pl.n_keys;
+  const bool regroup = pl.regroup;
+  const int64_t R = pl.R, max_tiles = pl.max_tiles, tile_words = pl.tile_words;
+  // control words and the per-block maxima
+  uint32_t* ctl = (uint32_t*)sc.get(sizeof(uint32_t) * (64 + kAbsBlocks), 0);
   WGBM_REQUIRE(ctl, "scratch allocation failed");
   uint32_t* absmax = ctl;
   int32_t* shift = (int32_t*)(ctl + 16);
   int32_t* n_tiles = (int32_t*)(ctl + 32);
   uint32_t* abs_part = ctl + 64;
-  // per-block maxima of |residual|: blocks of 1024 threads, at most 256 of
-  // them (every wave of the tile kernel reduces them to the shift)
-  const int n_abs =
-      (int)std::max<int64_t>(1, std::min<int64_t>(nblocks(n_pos, 1024), kAbsBlocks));
-  // a row list without an era regrouping: the residuals are gathered into
-  // position order in the same pass, so the tile kernel reads them
-  // contiguously instead of one 4-byte gather per row
-  const bool regroup = !seg_dev && num_eras > 1;
   float* rpos = nullptr;
-  if (rows && !regroup) {
-    rpos = (float*)scratch_get(st, sizeof(float) * std::max<int64_t>(n_pos, 1), 6);
+  if (pl.gather_resid) {
+    rpos = (float*)sc.get(sizeof(float) * std::max<int64_t>(n_pos, 1), 6);
     WGBM_REQUIRE(rpos, "scratch allocation failed");
   }
-  // segments: explicit (seg_dev), by era (sort rows by era), or a single one
-  const int n_keys = seg_dev ? n_seg : (regroup ? num_eras : 1);
-
-  // tiles: ~1 workgroup per CU over the whole call
-  int64_t tiles_target = std::max<int64_t>(1, kHistTargetWGCall / n_chunks);
-  int64_t R = (n_pos + tiles_target - 1) / tiles_target;
-  R = std::min<int64_t>(std::max<int64_t>(R, 1024), WGBM_MAX_TILE_ROWS);
-  const int64_t max_tiles = n_pos / R + n_keys + 1;
-  Tile* tiles = (Tile*)scratch_get(st, sizeof(Tile) * max_tiles, 3);
-  int32_t* kts = (int32_t*)scratch_get(st, sizeof(int32_t) * ((size_t)n_keys + 1), 4);
-  const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
+  Tile* tiles = (Tile*)sc.get(sizeof(Tile) * max_tiles, 3);
+  int32_t* kts = (int32_t*)sc.get(sizeof(int32_t) * ((size_t)n_keys + 1), 4);
   const int64_t words = max_tiles * tile_words;
   unsigned long long* part =
-      (unsigned long long*)scratch_get(st, sizeof(unsigned long long) * words, 5);
+      (unsigned long long*)sc.get(sizeof(unsigned long long) * words, 5);
   WGBM_REQUIRE(tiles && kts && part, "scratch allocation failed (%lld words)", (long long)words);
 
   // maxima (+ gathered residuals) and, unless the rows are regrouped by era
@@ -81,8 +132,8 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   const int32_t* order = rows;
   const int64_t* seg = seg_dev;
   if (regroup) {
-    int64_t* counts = (int64_t*)scratch_get(st, sizeof(int64_t) * (3 * (size_t)num_eras + 2), 1);
-    int32_t* sorted = (int32_t*)scratch_get(st, sizeof(int32_t) * std::max<int64_t>(n_pos, 1), 2);
+    int64_t* counts = (int64_t*)sc.get(sizeof(int64_t) * (3 * (size_t)num_eras + 2), 1);
+    int32_t* sorted = (int32_t*)sc.get(sizeof(int32_t) * std::max<int64_t>(n_pos, 1), 2);
     WGBM_REQUIRE(counts && sorted, "scratch allocation failed");
     int64_t* starts = counts + num_eras;
     unsigned long long* cursor = (unsigned long long*)(starts + num_eras + 1);
@@ -125,7 +176,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   a.n_chunks = n_chunks;
   a.max_tiles = (int32_t)max_tiles;
   a.native = native ? 1 : 0;
-  a.timer_tag = "hist_tiles";
+  a.timer_tag = sc.base ? nullptr : "hist_tiles";  // timers create events: not without allocation
   a.sm.partial = abs_part;
   a.sm.n_part = n_abs;
   a.sm.qbits = wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1));
@@ -143,7 +194,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   } else {
     // full-width histogram in scratch, then the requested features
     const int64_t full = (int64_t)n_keys * n_hist_feats * num_bins;
-    float* Gf = (float*)scratch_get(st, sizeof(float) * 2 * full, 7);
+    float* Gf = (float*)sc.get(sizeof(float) * 2 * full, 7);
     WGBM_REQUIRE(Gf, "scratch allocation failed");
     float* Hf = Gf + full;
     r = launch_finalize_f32(tiles_per_key, part, kts, n_keys, n_chunks, V, num_bins, n_hist_feats,
@@ -176,10 +227,11 @@ int wgbm_compute_histogram3(const int8_t* bin_indices, int64_t n_rows, int64_t n
   WGBM_REQUIRE(n_feats == 0 || (feature_indices && grad_hist && hess_hist), "null output pointer");
   WGBM_REQUIRE(num_eras == 1 || era_indices, "era_indices required when num_eras > 1");
   if (n_feats == 0) return 0;
+  HistScratch sc{S(stream)};
   return histogram_pipeline(bin_indices, n_rows, n_feats_master, (int32_t)n_feats_master,
                             residuals, sample_indices, n_samples, nullptr, 1, era_indices,
                             num_eras, feature_indices, (int32_t)n_feats, num_bins, grad_hist,
-                            hess_hist, false, S(stream));
+                            hess_hist, false, sc);
 }
 
 int wgbm_histogram_segments(const int8_t* codes, int64_t n_rows, int64_t stride, int32_t n_feats,
@@ -190,9 +242,64 @@ int wgbm_histogram_segments(const int8_t* codes, int64_t n_rows, int64_t stride,
   WGBM_REQUIRE(n_seg >= 1 && seg && codes && residuals && G && H, "bad segment arguments");
   WGBM_REQUIRE(stride >= n_feats && n_feats >= 1, "stride must be >= n_feats >= 1");
   WGBM_REQUIRE((flags & ~WGBM_CODES_NATIVE) == 0, "unknown histogram flags 0x%x", flags);
+  HistScratch sc{S(stream)};
   return histogram_pipeline(codes, n_rows, stride, n_feats, residuals, order, n_pos, seg, n_seg,
                             nullptr, 1, nullptr, n_feats, num_bins, G, H,
-                            (flags & WGBM_CODES_NATIVE) != 0, S(stream));
+                            (flags & WGBM_CODES_NATIVE) != 0, sc);
+}
+
+// ---------------------------------------------------------------------------
+// wgbm_histogram_segments without allocation: the call's working memory is
+// carved from g_noalloc_scratch, a fixed device array every GPU the library
+// runs on holds until the process ends.  Its address on each device comes
+// from hipGetSymbolAddress, fetched once per device on the first call made
+// with that device current; the host name of the array is a stand-in and is
+// never passed to a kernel.  Calls that overlap on one GPU share the array
+// and race; each call writes every piece before reading it.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char g_noalloc_scratch[WGBM_NOALLOC_SCRATCH_BYTES];
+static std::mutex g_noalloc_mu;
+static void* g_noalloc_ptr[kMaxDevices] = {};
+
+static int noalloc_scratch_ptr(unsigned char** out) {
+  int dev = 0;
+  WGBM_CHECK(hipGetDevice(&dev));
+  WGBM_REQUIRE(dev >= 0 && dev < kMaxDevices, "histogram_segments_noalloc: device %d beyond %d",
+               dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    WGBM_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(g_noalloc_scratch)));
+    WGBM_REQUIRE(p, "histogram_segments_noalloc: no device address for the scratch array");
+    g_noalloc_ptr[dev] = p;
+  }
+  *out = (unsigned char*)g_noalloc_ptr[dev];
+  return 0;
+}
+
+int wgbm_histogram_segments_noalloc(const int8_t* codes, int64_t n_rows, int64_t stride,
+                                    int32_t n_feats, const float* residuals, const int32_t* order,
+                                    const int64_t* seg, int32_t n_seg, int64_t n_pos,
+                                    int32_t num_bins, int32_t flags, float* G, float* H,
+                                    void* stream) {
+  WGBM_REQUIRE(num_bins >= 1 && num_bins <= 127, "num_bins must be in [1, 127]");
+  WGBM_REQUIRE(n_seg >= 1 && seg && codes && residuals && G && H, "bad segment arguments");
+  WGBM_REQUIRE(stride >= n_feats && n_feats >= 1, "stride must be >= n_feats >= 1");
+  WGBM_REQUIRE(n_pos >= 0, "n_pos must be >= 0");
+  WGBM_REQUIRE((flags & ~WGBM_CODES_NATIVE) == 0, "unknown histogram flags 0x%x", flags);
+  const HistPlan pl = hist_plan(n_feats, num_bins, n_pos, order, seg, n_seg, 1);
+  const size_t need = hist_scratch_bytes(pl, n_pos);
+  WGBM_REQUIRE(need <= (size_t)WGBM_NOALLOC_SCRATCH_BYTES,
+               "histogram_segments_noalloc: this call needs %zu bytes of scratch, the fixed "
+               "array holds %zu (fewer rows, features or segments per call)",
+               need, (size_t)WGBM_NOALLOC_SCRATCH_BYTES);
+  HistScratch sc{S(stream)};
+  int r = noalloc_scratch_ptr(&sc.base);
+  if (r) return r;
+  sc.cap = WGBM_NOALLOC_SCRATCH_BYTES;
+  return histogram_pipeline(codes, n_rows, stride, n_feats, residuals, order, n_pos, seg, n_seg,
+                            nullptr, 1, nullptr, n_feats, num_bins, G, H,
+                            (flags & WGBM_CODES_NATIVE) != 0, sc);
 }
 
 int wgbm_compute_split(const float* G, const float* H, int32_t num_eras, int32_t n_feats,
