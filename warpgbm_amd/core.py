@@ -281,49 +281,68 @@ class WarpGBM(BaseEstimator, RegressorMixin):
             early_stopping_rounds=None, eval_metric="mse"):
         early_stopping_rounds = self.validate_fit_params(
             X, y, era_id, X_eval, y_eval, eval_every_n_trees, early_stopping_rounds, eval_metric)
-        # colsample_bytree feature subsets come from this generator (host RNG,
-        # reproducible for a given random_state)
-        seed = self.random_state if self.random_state is not None else int(
-            np.random.SeedSequence().generate_state(1)[0])
-        self._gen = torch.Generator().manual_seed(int(seed))
+        # random_state seeds the global RNGs as the reference does
+        # (warpgbm/core.py:308-314); colsample_bytree subsets are then drawn
+        # with torch.randperm on the device (core.py:722, 778)
         if self.random_state is not None:
+            torch.manual_seed(self.random_state)
             np.random.seed(self.random_state)
+            if torch.cuda.is_available():
+                torch.cuda.manual_seed(self.random_state)
+                torch.cuda.manual_seed_all(self.random_state)
 
-        if not self.warm_start or not self._is_fitted:
-            self._is_fitted = False
-            self._trees_trained = 0
-            self.forest = [{} for _ in range(self.n_estimators)] if self.objective == "regression" else []
-            self.training_loss = []
-            self.eval_loss = []
-        else:
-            if X.shape[1] != self.num_features:
-                raise ValueError(
-                    f"X has {X.shape[1]} features, but model was trained with {self.num_features} features.")
-            if self._trees_trained >= self.n_estimators:
-                print(f"Model already has {self._trees_trained} trees (n_estimators={self.n_estimators}). No additional training needed.")
-                return self
+        fresh = not (self.warm_start and self._is_fitted)
+        if fresh:
+            self._reset_training_state()
+        elif X.shape[1] != self.num_features:
+            raise ValueError(
+                f"X has {X.shape[1]} features, but model was trained with {self.num_features} features.")
+        elif self._trees_trained >= self.n_estimators:
+            print(f"Model already has {self._trees_trained} trees (n_estimators={self.n_estimators}). No additional training needed.")
+            return self
 
         if era_id is None:
             era_id = np.ones(X.shape[0], dtype="int32")
-        self.feature_subsets_ = []
+        self._subsets_dev = []
         self._phases = _Phases()
+        try:
+            if self.objective in ("multiclass", "binary"):
+                y_encoded = self._encode_labels(y, refit=fresh)
+                self._check_class_count()
+                return self._fit_classification(X, y_encoded, era_id, X_eval, y_eval,
+                                                eval_every_n_trees, early_stopping_rounds,
+                                                eval_metric)
+            return self._fit_regression(X, y, era_id, X_eval, y_eval, eval_every_n_trees,
+                                        early_stopping_rounds, eval_metric)
+        finally:
+            # the subsets drawn on the device, on the host once the fit is done
+            self.feature_subsets_ = [t if isinstance(t, np.ndarray) else
+                                     t.cpu().numpy().astype(np.int32) for t in self._subsets_dev]
+            self._subsets_dev = []
 
-        if self.objective in ("multiclass", "binary"):
-            if not self.warm_start or not self._is_fitted:
-                self.label_encoder = LabelEncoder()
-                y_encoded = self.label_encoder.fit_transform(y)
-                self.classes_ = self.label_encoder.classes_
-                self.num_classes = len(self.classes_)
-            else:
-                y_encoded = self.label_encoder.transform(y)
-            if self.objective == "binary" and self.num_classes != 2:
-                raise ValueError(f"binary objective requires exactly 2 classes, got {self.num_classes}")
-            if self.objective == "multiclass" and self.num_classes < 2:
-                raise ValueError(f"multiclass objective requires at least 2 classes, got {self.num_classes}")
-            return self._fit_classification(X, y_encoded, era_id, X_eval, y_eval,
-                                            eval_every_n_trees, early_stopping_rounds, eval_metric)
-        return self._fit_regression(X, y, era_id, X_eval, y_eval, eval_every_n_trees,
-                                    early_stopping_rounds, eval_metric)
+    def _reset_training_state(self):
+        """A fresh fit: no trees, no loss history (warpgbm/core.py:317-324)."""
+        self._is_fitted = False
+        self._trees_trained = 0
+        self.forest = [{} for _ in range(self.n_estimators)] if self.objective == "regression" else []
+        self.training_loss = []
+        self.eval_loss = []
+
+    def _encode_labels(self, y, refit):
+        """Class labels as 0..K-1 by sklearn's LabelEncoder (warpgbm/core.py:341-352):
+        fitted on a fresh start, the fitted one reused on a warm start."""
+        if refit:
+            self.label_encoder = LabelEncoder().fit(y)
+            self.classes_ = self.label_encoder.classes_
+            self.num_classes = len(self.classes_)
+        return self.label_encoder.transform(y)
+
+    def _check_class_count(self):
+        K = self.num_classes
+        if self.objective == "binary" and K != 2:
+            raise ValueError(f"binary objective requires exactly 2 classes, got {K}")
+        if self.objective == "multiclass" and K < 2:
+            raise ValueError(f"multiclass objective requires at least 2 classes, got {K}")
 
     def preprocess_gpu_data(self, X_np, Y_np, era_id_np):
         """Codes, era layout and targets on the device (warpgbm/core.py:487-541)."""
@@ -385,26 +404,24 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         return eng
 
     def _feature_subset(self, dev):
-        """Features of one round: randperm(F)[:k], k = max(1, int(colsample * F))
-        (warpgbm/core.py:702-703, 721-722, 777-778); the subsets drawn in the
-        last fit are kept in ``feature_subsets_``."""
+        """Features of one round: torch.randperm(F)[:k] on the device,
+        k = max(1, int(colsample * F)) (warpgbm/core.py:702-703, 721-722,
+        777-778); the subsets of the last fit are kept in ``feature_subsets_``
+        (copied to the host when the fit ends, so no round waits for them)."""
         F = self.num_features
         if self.colsample_bytree < 1.0:
             k = max(1, int(self.colsample_bytree * F))
-            sel = torch.randperm(F, generator=self._gen, dtype=torch.int64)[:k]
-        else:
-            sel = torch.arange(F, dtype=torch.int64)
-        self.feature_subsets_.append(sel.numpy().astype(np.int32))
-        if self.colsample_bytree >= 1.0:
-            # every round uses all features: one device copy for the whole fit
-            cached = getattr(self, "_all_features_dev", None)
-            if cached is None or cached.numel() != F or cached.device != dev:
-                cached = torch.arange(F, dtype=torch.int32, device=dev)
-                self._all_features_dev = cached
-            return cached
-        # a pinned staging copy, so the upload does not wait for the rounds
-        # already queued on the stream
-        return sel.to(torch.int32).pin_memory().to(dev, non_blocking=True)
+            sel = torch.randperm(F, device=dev, dtype=torch.int32)[:k]
+            self._subsets_dev.append(sel)
+            return sel
+        # every round uses all features: one device copy for the whole fit
+        cached = getattr(self, "_all_features_dev", None)
+        if cached is None or cached.numel() != F or cached.device != dev:
+            cached = torch.arange(F, dtype=torch.int32, device=dev)
+            self._all_features_dev = cached
+            self._all_features_host = np.arange(F, dtype=np.int32)
+        self._subsets_dev.append(self._all_features_host)
+        return cached
 
     def _alloc_records(self, n_rounds, n_trees, dev):
         H = (1 << (self.max_depth + 1)) - 1
@@ -603,15 +620,20 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         self.eval_every_n_trees = eval_every_n_trees
         self.early_stopping_rounds = early_stopping_rounds
 
+    _REGRESSION_METRICS = {
+        # mean squared error
+        "mse": lambda t, p: ((t - p) ** 2).mean(),
+        # one minus Pearson's r of targets and predictions
+        "corr": lambda t, p: 1 - torch.corrcoef(torch.vstack([t, p]))[0, 1],
+        "rmsle": lambda t, p: rmsle_torch(t, p),
+    }
+
     def get_eval_metric(self, y_true, y_pred):
-        if self.eval_metric == "mse":
-            return ((y_true - y_pred) ** 2).mean().item()
-        elif self.eval_metric == "corr":
-            return 1 - torch.corrcoef(torch.vstack([y_true, y_pred]))[0, 1].item()
-        elif self.eval_metric == "rmsle":
-            return rmsle_torch(y_true, y_pred).item()
-        else:
+        """Regression eval loss of warpgbm/core.py:660-668 (lower is better)."""
+        fn = self._REGRESSION_METRICS.get(self.eval_metric)
+        if fn is None:
             raise ValueError(f"Invalid eval_metric: {self.eval_metric}.")
+        return fn(y_true, y_pred).item()
 
     def _compute_eval_regression(self, i, Y_gpu, preds, eval_preds):
         """warpgbm/core.py:670-690."""
@@ -785,41 +807,31 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         del codes
         return probs
 
-    # ------------------------------------------------------------------ reference op helpers
-    def compute_histograms(self, sample_indices, feature_indices, residual, bin_indices,
-                           era_indices):
-        """Per-node histograms through the reference op (warpgbm/core.py:543-563)."""
-        E = int(era_indices.max().item()) + 1 if era_indices.numel() else 1
-        g = torch.zeros((E, len(feature_indices), self.num_bins), device=residual.device)
-        h = torch.zeros_like(g)
-        node_kernel.compute_histogram3(bin_indices, residual, sample_indices, feature_indices,
-                                       era_indices, g, h, self.num_bins, self.threads_per_block,
-                                       self.rows_per_thread)
-        return g, h
-
     # ------------------------------------------------------------------ importance
+    @staticmethod
+    def _share_of_total(a):
+        """Each row of ``a`` (float32) divided by its own sum; all-zero rows
+        stay zero."""
+        tot = a.sum(axis=-1, keepdims=True)
+        return np.where(tot > 0, a / np.where(tot > 0, tot, 1), a).astype(a.dtype)
+
     def get_feature_importance(self, importance_type="gain", normalize=True):
-        """warpgbm/core.py:1032-1065."""
+        """Summed split gain per feature over all eras (warpgbm/core.py:1032-1065),
+        as fractions of the total with ``normalize``."""
         if self.feature_importance_ is None:
             raise ValueError("Model has not been fitted yet.")
         if importance_type != "gain":
             raise ValueError(f"importance_type '{importance_type}' not supported. Use 'gain'.")
-        importance = self.feature_importance_.copy()
-        if normalize and importance.sum() > 0:
-            importance = importance / importance.sum()
-        return importance
+        imp = np.array(self.feature_importance_, copy=True)
+        return self._share_of_total(imp) if normalize else imp
 
     def get_per_era_feature_importance(self, normalize=True):
-        """warpgbm/core.py:1067-1101."""
+        """Split gain per (era, feature) (warpgbm/core.py:1067-1101); with
+        ``normalize`` every era's row sums to 1 (eras without gain stay 0)."""
         if self.per_era_feature_importance_ is None:
             raise ValueError("Model has not been fitted yet.")
-        importance = self.per_era_feature_importance_.copy()
-        if normalize:
-            for era_idx in range(importance.shape[0]):
-                era_sum = importance[era_idx].sum()
-                if era_sum > 0:
-                    importance[era_idx] /= era_sum
-        return importance
+        imp = np.array(self.per_era_feature_importance_, copy=True)
+        return self._share_of_total(imp) if normalize else imp
 
     # ------------------------------------------------------------------ persistence
     def save_model(self, path):

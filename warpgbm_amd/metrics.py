@@ -7,11 +7,10 @@ import torch
 
 
 def rmsle_torch(y_true, y_pred, eps=1e-7):
-    y_true = torch.clamp(y_true, min=0)
-    y_pred = torch.clamp(y_pred, min=0)
-    log_true = torch.log1p(y_true + eps)
-    log_pred = torch.log1p(y_pred + eps)
-    return torch.sqrt(torch.mean((log_true - log_pred) ** 2))
+    """Root mean squared difference of log1p(max(v, 0) + eps) between
+    targets and predictions (negative values count as 0)."""
+    d = torch.log1p(y_true.clamp(min=0) + eps) - torch.log1p(y_pred.clamp(min=0) + eps)
+    return d.pow(2).mean().sqrt()
 
 
 def softmax(logits, dim=-1):
