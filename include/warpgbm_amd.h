@@ -209,6 +209,14 @@ typedef struct wgbm_engine_config {
   const int8_t* codes_cm;     /* [n_feats, n_rows] */
   const int32_t* root_order;  /* [n_rows] row ids sorted by era, ascending inside */
   const int64_t* era_start;   /* [num_eras + 1] */
+  /* device bytes for the per-level split buffers (level histograms, staged
+   * per-era gains, era-block sums, criteria); 0 = 4 GiB.  A depth with more
+   * (tree, node)s than fit is processed in chunks of nodes, each histogrammed
+   * directly; the trees do not depend on it.  max_depth is limited only by
+   * int32 node and segment numbering (n_trees * 2^max_depth * num_eras <
+   * 2^31) and by the device memory of the per-node bookkeeping, which
+   * wgbm_engine_create checks against the free memory. */
+  int64_t level_bytes;
 } wgbm_engine_config;
 
 /* Heap-ordered record of the trees grown in one round; H = 2^(max_depth+1)-1.

@@ -364,3 +364,98 @@ def test_heavy_tailed_eras_bit_exact(gpu, N, E):
         assert a == b, f"tree {i} differs"
     assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
+
+
+@pytest.mark.parametrize("level_bytes", [0, 1])
+def test_chunked_levels_regression_bit_exact(gpu, level_bytes):
+    """A level budget of 1 byte leaves room for one (tree, node) at a time:
+    every level below the root is processed node by node, each histogrammed
+    directly.  The trees are the same as with the whole-level path."""
+    print_case("estimator", "chunked levels regression, level_bytes", level_bytes)
+    X, y = c1_data(4000, 12)
+    kw = dict(num_bins=16, max_depth=6, n_estimators=3, learning_rate=0.3, min_child_weight=10)
+    m = WarpGBM(**kw)
+    m._engine_level_bytes = level_bytes
+    m.fit(X, y)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, y)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
+
+
+def test_chunked_levels_multiclass_and_eras_bit_exact(gpu):
+    print_case("estimator", "chunked levels multiclass / DES direct / large eras")
+    # softmax, 4 class trees per round: chunks of nodes across trees
+    rng = np.random.default_rng(3)
+    N, F, K = 3000, 8, 4
+    labels = rng.integers(0, K, N)
+    X = (rng.standard_normal((K, F))[labels] * 1.5 + rng.standard_normal((N, F))).astype(F32)
+    kw = dict(objective="multiclass", num_bins=12, max_depth=4, n_estimators=2,
+              learning_rate=0.3, min_child_weight=5)
+    m = WarpGBM(**kw)
+    m._engine_level_bytes = 40_000  # a few (tree, node)s per chunk
+    m.fit(X, labels)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, labels)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"round {i} differs"
+    # direct era path (every era <= 65536 rows) and the per-era histogram path
+    for N, E, lb in ((6000, 6, 1), (140_000, 2, 1)):
+        rng = np.random.default_rng(4)
+        X = rng.integers(0, 5, (N, 10)).astype(np.int8)
+        era = np.repeat(np.arange(E), N // E)
+        score = (X[:, 0] - 2) + np.where(era % 2 == 0, 1.0, -1.0) * (X[:, 1] - 2)
+        y = (score + rng.standard_normal(N)).astype(F32) / 4
+        kw = dict(num_bins=5, max_depth=4, n_estimators=2, learning_rate=0.5)
+        m = WarpGBM(**kw)
+        m._engine_level_bytes = lb
+        m.fit(X, y, era_id=era)
+        ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era)
+        for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+            assert a == b, f"E={E} tree {i} differs"
+        assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
+
+
+def test_127_bins_depth_10_bit_exact(gpu):
+    """The reference demo's shape (127 bins, depth 10): the one-feature-per-
+    lane histogram variant, deep heaps in the predictor."""
+    print_case("estimator", "127 bins depth 10")
+    rng = np.random.default_rng(5)
+    N = 30_000
+    t = rng.uniform(0, 4 * np.pi, N)
+    X = np.stack([t * np.cos(t), t * np.sin(t), rng.standard_normal(N),
+                  rng.standard_normal(N)], axis=1).astype(F32) + 0.3 * rng.standard_normal((N, 4)).astype(F32)
+    y = (np.sin(t) + 0.1 * rng.standard_normal(N)).astype(F32)
+    kw = dict(num_bins=127, max_depth=10, n_estimators=4, learning_rate=0.3, min_child_weight=5)
+    m = WarpGBM(**kw).fit(X, y)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, y)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
+    assert max(_depth(t) for t in m.forest) == 10
+
+
+def _depth(node):
+    if "leaf_value" in node:
+        return 0
+    return 1 + max(_depth(node["left"]), _depth(node["right"]))
+
+
+def test_depth_beyond_twenty_bit_exact(gpu):
+    """max_depth 22 (the engine used to stop at 20): with min_child_weight 1
+    the trees reach their full depth on a small set."""
+    print_case("estimator", "max_depth 22")
+    rng = np.random.default_rng(6)
+    N = 3000
+    X = rng.standard_normal((N, 5)).astype(F32)
+    y = (X[:, 0] * 3 + np.sin(5 * X[:, 1]) + rng.standard_normal(N)).astype(F32)
+    kw = dict(num_bins=64, max_depth=22, n_estimators=2, learning_rate=0.5, min_child_weight=1)
+    m = WarpGBM(**kw).fit(X, y)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, y)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
+    assert max(_depth(t) for t in m.forest) > 12

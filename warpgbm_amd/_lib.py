@@ -72,6 +72,7 @@ class EngineConfig(C.Structure):
         ("codes_cm", _p),
         ("root_order", _p),
         ("era_start", _p),
+        ("level_bytes", _i64),
     ]
 
 

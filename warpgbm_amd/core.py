@@ -395,9 +395,12 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         return None, None
 
     def _new_engine(self, codes, root_order, era_start, n_trees, objective):
+        # _engine_level_bytes (0: the library's default) bounds the per-level
+        # split buffers; a smaller bound only changes how levels are chunked
         eng = D.Engine(codes, root_order, era_start, self.num_bins, self.num_eras,
                        self.max_depth, n_trees, objective, self.min_child_weight,
-                       self.min_split_gain, self.L2_reg, self.learning_rate)
+                       self.min_split_gain, self.L2_reg, self.learning_rate,
+                       getattr(self, "_engine_level_bytes", 0))
         # engine knobs (wgbm_engine_set_tuning keys); none changes the model
         for key, value in getattr(self, "_engine_tuning", {}).items():
             eng.set_tuning(int(key), int(value))
@@ -425,6 +428,13 @@ class WarpGBM(BaseEstimator, RegressorMixin):
 
     def _alloc_records(self, n_rounds, n_trees, dev):
         H = (1 << (self.max_depth + 1)) - 1
+        need = n_rounds * n_trees * H * (20 + 4 * self.num_eras)
+        free, _ = torch.cuda.mem_get_info(dev)
+        if need > free:
+            raise MemoryError(
+                f"max_depth={self.max_depth} with {n_rounds} rounds x {n_trees} trees needs "
+                f"{need / 2**30:.1f} GiB of device memory for the tree records "
+                f"({free / 2**30:.1f} GiB free); reduce max_depth or n_estimators")
         return {
             "feat": torch.empty((n_rounds, n_trees, H), dtype=torch.int32, device=dev),
             "bin": torch.empty((n_rounds, n_trees, H), dtype=torch.int32, device=dev),

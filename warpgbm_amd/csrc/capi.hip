@@ -442,8 +442,8 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
                       const int32_t* feat, const int32_t* bin, const float* leaf,
                       int32_t n_rounds, int32_t K, int32_t H, int32_t max_depth,
                       float learning_rate, float* out, void* stream) {
-  WGBM_REQUIRE(n >= 0 && K >= 1 && n_rounds >= 0 && max_depth >= 0 && max_depth <= 20,
-               "bad predict_heap shape");
+  WGBM_REQUIRE(n >= 0 && K >= 1 && n_rounds >= 0 && max_depth >= 0 && max_depth <= 29,
+               "bad predict_heap shape");  // heap indices below 2^30: int32
   WGBM_REQUIRE(num_bins >= 2 && num_bins <= 127, "num_bins must be in [2, 127]");
   WGBM_REQUIRE(H == (1 << (max_depth + 1)) - 1, "H must be 2^(max_depth+1)-1");
   if (n == 0) return 0;
@@ -530,6 +530,7 @@ int wgbm_engine_create(wgbm_engine** out, const wgbm_engine_config* cfg) {
   c.codes_cm = cfg->codes_cm;
   c.root_order = cfg->root_order;
   c.era_start = cfg->era_start;
+  c.level_bytes = cfg->level_bytes;
   Engine* e = nullptr;
   int r = engine_create(&e, c);
   if (r) return r;

@@ -36,6 +36,7 @@ struct EngineConfig {
   const int8_t* codes_cm;  // [n_feats, n_rows]
   const int32_t* root_order;  // [n_rows] rows sorted by era (ascending row id inside)
   const int64_t* era_start;   // [E + 1]
+  int64_t level_bytes;        // per-level split buffers (0: default)
 };
 
 struct Engine;
@@ -177,6 +178,9 @@ __global__ void scatter_kernel(int64_t n_pos, int32_t E, const int64_t* seg,
                                int32_t* order_next, int32_t* keyp_next, const float* rpos,
                                float* rpos_next);
 __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v);
+// histogram keys of a chunk of n (tree, node)s: list[i] = i when node i / E
+// is present, else -1 (keys relative to the chunk's first node)
+__global__ void chunk_keys_kernel(const int32_t* present, int32_t E, int32_t n, int32_t* list);
 
 // split kernels (split.hip); node_shift: the histogram shift of every
 // (tree, node) of the level, indexed by tree * nodes_in_level + node

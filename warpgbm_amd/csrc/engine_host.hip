@@ -27,6 +27,10 @@ struct Engine {
   EngineConfig c;
   int V = 16, n_chunks = 1, qbits = 28;
   int H = 1;
+  // (tree, node)s the per-level split buffers hold: a depth with more is
+  // processed in chunks of nodes, each histogrammed directly
+  int64_t nc_max = 1;
+  bool stored_prev = false;  // hq[previous depth] holds that whole level (for subtraction)
   int64_t hist_tile_rows = 0;  // 0: automatic
   int64_t n_keys_max = 0, max_htiles = 0, nb = 0;
   // buffers
@@ -118,8 +122,13 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
                "engine: codes stride must be >= n_feats and a multiple of 16");
   WGBM_REQUIRE(cfg.num_bins >= 2 && cfg.num_bins <= 127, "engine: num_bins must be in [2, 127]");
   WGBM_REQUIRE(cfg.num_eras >= 1, "engine: num_eras must be >= 1");
-  WGBM_REQUIRE(cfg.max_depth >= 1 && cfg.max_depth <= 20, "engine: max_depth must be in [1, 20]");
+  WGBM_REQUIRE(cfg.max_depth >= 1 && cfg.max_depth <= 29, "engine: max_depth must be in [1, 29]");
   WGBM_REQUIRE(cfg.n_trees >= 1, "engine: n_trees must be >= 1");
+  WGBM_REQUIRE(cfg.num_eras >= 1 &&
+                   ((int64_t)cfg.n_trees << cfg.max_depth) * cfg.num_eras < (int64_t(1) << 31),
+               "engine: n_trees * 2^max_depth * num_eras = %lld segments exceeds the int32 "
+               "segment numbering; reduce max_depth",
+               (long long)(((int64_t)cfg.n_trees << cfg.max_depth) * cfg.num_eras));
   WGBM_REQUIRE(cfg.objective == 0 || cfg.objective == 1, "engine: bad objective");
   WGBM_REQUIRE(cfg.objective == 1 || cfg.n_trees == 1, "engine: regression grows one tree per round");
   WGBM_REQUIRE(cfg.codes_rm && cfg.codes_cm && cfg.root_order && cfg.era_start,
@@ -154,6 +163,42 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     for (int64_t k = 0; k < E; ++k) mx = std::max<int64_t>(mx, es[k + 1] - es[k]);
     e->des_direct = mx <= WGBM_MAX_TILE_ROWS;
   }
+  // per-level split buffers for nc_max (tree, node)s: every node of the
+  // deepest split level when that fits the budget, else the largest power of
+  // two of nodes that does (deeper levels are then processed in chunks)
+  const int64_t W = (E + kDesEraBlock - 1) / kDesEraBlock;
+  const int64_t per_node =
+      e->des_direct ? E * F * (B - 1) * 5 + W * (4 + F * (B - 1) * 12) + F * (B - 1) * 8
+                    : 2 * E * F * B * 12 + (E > 1 ? F * (B - 1) * 8 : 0);
+  const int64_t budget = cfg.level_bytes > 0 ? cfg.level_bytes : (int64_t)4 << 30;
+  if (T * hist_nodes_max * per_node <= budget) {
+    e->nc_max = T * hist_nodes_max;
+  } else {
+    e->nc_max = 1;
+    while (e->nc_max * 2 <= T * hist_nodes_max && e->nc_max * 2 * per_node <= budget)
+      e->nc_max *= 2;
+  }
+  {
+    // device memory of the rest, against what is free (a clear error rather
+    // than an allocation failure halfway)
+    // positions: order, keyp, rpos (two levels each), residual, direction
+    // byte; segments: offsets, wide sums and counts (two levels), key pairs,
+    // partition words; nodes: flags, shifts, maxima, picks, leaf values and
+    // the chosen split's per-era gains; the pair codes; 64 MiB of slack
+    const int64_t keys = e->n_keys_max, tn = T * nodes_max;
+    const int64_t pcodes = (e->des_direct && B <= 7) ? N * pair_stride((int32_t)F) : 0;
+    const int64_t need = e->nc_max * per_node + T * N * 29 + keys * 100 + tn * 60 + tn * E * 4 +
+                         pcodes + ((int64_t)64 << 20);
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) == hipSuccess && (size_t)need > free_b) {
+      wgbm_set_error("engine: needs about %.1f GiB of device memory (max_depth=%d, %d eras, "
+                     "%lld rows x %d trees), %.1f GiB free; reduce max_depth or the data",
+                     need / 1073741824.0, D, (int)E, (long long)N, (int)T,
+                     free_b / 1073741824.0);
+      engine_destroy(e);
+      return WGBM_ENOMEM;
+    }
+  }
   for (int k = 0; k < 2; ++k) {
     E_ALLOC(e->order[k], T * N);
     E_ALLOC(e->seg[k], e->n_keys_max + 1);
@@ -164,22 +209,21 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     E_ALLOC(e->node_shift[k], T * nodes_max);
     E_ALLOC(e->key_list[k], 2 * e->n_keys_max);
     if (!e->des_direct) {
-      E_ALLOC(e->hq[k], T * hist_nodes_max * E * F * B);
-      E_ALLOC(e->hc[k], T * hist_nodes_max * E * F * B);
+      E_ALLOC(e->hq[k], e->nc_max * E * F * B);
+      E_ALLOC(e->hc[k], e->nc_max * E * F * B);
     }
   }
   if (e->des_direct) {
-    E_ALLOC(e->sgain, T * hist_nodes_max * E * F * (B - 1));
-    E_ALLOC(e->sdir, T * hist_nodes_max * E * F * (B - 1));
+    E_ALLOC(e->sgain, e->nc_max * E * F * (B - 1));
+    E_ALLOC(e->sdir, e->nc_max * E * F * (B - 1));
     E_ALLOC(e->local_of, F);
     if (B <= 7 && N * pair_stride((int32_t)F) <= (int64_t)0xffffffffll) {
       e->pstride = pair_stride((int32_t)F);
       E_ALLOC(e->pcodes, N * e->pstride);
     }
-    const int64_t W = (E + kDesEraBlock - 1) / kDesEraBlock;
-    E_ALLOC(e->alive, T * hist_nodes_max * W);
-    E_ALLOC(e->bsum, T * hist_nodes_max * W * F * (B - 1));
-    E_ALLOC(e->bdir, T * hist_nodes_max * W * F * (B - 1));
+    E_ALLOC(e->alive, e->nc_max * W);
+    E_ALLOC(e->bsum, e->nc_max * W * F * (B - 1));
+    E_ALLOC(e->bdir, e->nc_max * W * F * (B - 1));
   }
   E_ALLOC(e->dirbit, T * N);
   E_ALLOC(e->keyp[0], T * N);
@@ -208,8 +252,8 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->hkts, e->n_keys_max + 1);
   E_ALLOC(e->hn, 1);
   if (E > 1) {
-    E_ALLOC(e->crit, T * hist_nodes_max * F * (B - 1));
-    E_ALLOC(e->agree, T * hist_nodes_max * F * (B - 1));
+    E_ALLOC(e->crit, e->nc_max * F * (B - 1));
+    E_ALLOC(e->agree, e->nc_max * F * (B - 1));
     E_ALLOC(e->agree_max, 2 * T * nodes_max);
   }
   E_ALLOC(e->split_l, T * nodes_max);
@@ -268,6 +312,29 @@ static int ensure_partials(Engine* e, int64_t max_tiles) {
   return 0;
 }
 
+// room for max_tiles histogram tiles (tile list and partials)
+static int ensure_tiles(Engine* e, int64_t max_tiles) {
+  int r = ensure_partials(e, max_tiles);
+  if (r) return r;
+  if (max_tiles > e->max_htiles) {
+    if (e->htiles) {
+      // tile lists are only reused within the stream; grow after a sync
+      WGBM_CHECK(hipDeviceSynchronize());
+      for (auto it = e->allocs.begin(); it != e->allocs.end(); ++it)
+        if (*it == e->htiles) {
+          (void)hipFree(*it);
+          e->allocs.erase(it);
+          break;
+        }
+      e->htiles = nullptr;
+    }
+    r = dalloc(e, &e->htiles, max_tiles);
+    if (r) return r;
+    e->max_htiles = max_tiles;
+  }
+  return 0;
+}
+
 // histogram tiles of level d (the root, or the key pairs of every split: the
 // smaller child, or both children when one takes a finer shift): tile rows,
 // the tile bound, and buffers that hold them
@@ -285,25 +352,18 @@ static int level_plan(Engine* e, int d, LevelPlan* lp) {
   lp->rows_bound = d == 0 ? T * N : (T * N) / 2;
   lp->R = pick_tile_rows(e, lp->rows_bound);
   lp->max_tiles = (T * N) / lp->R + lp->n_list + 1;
-  int r = ensure_partials(e, lp->max_tiles);
-  if (r) return r;
-  if (lp->max_tiles > e->max_htiles) {
-    if (e->htiles) {
-      // tile lists are only reused within the stream; grow after a sync
-      WGBM_CHECK(hipDeviceSynchronize());
-      for (auto it = e->allocs.begin(); it != e->allocs.end(); ++it)
-        if (*it == e->htiles) {
-          (void)hipFree(*it);
-          e->allocs.erase(it);
-          break;
-        }
-      e->htiles = nullptr;
-    }
-    r = dalloc(e, &e->htiles, lp->max_tiles);
-    if (r) return r;
-    e->max_htiles = lp->max_tiles;
-  }
-  return 0;
+  return ensure_tiles(e, lp->max_tiles);
+}
+
+// histogram tiles of one chunk of a level (n_list keys, the chunk's present
+// nodes histogrammed directly; the level split into n_chunk such chunks)
+static int chunk_plan(Engine* e, int64_t n_list, int n_chunk, LevelPlan* lp) {
+  const int64_t TN = (int64_t)e->c.n_trees * e->c.n_rows;
+  lp->n_list = (int32_t)n_list;
+  lp->rows_bound = TN;
+  lp->R = pick_tile_rows(e, std::max<int64_t>(1, TN / std::max(n_chunk, 1)));
+  lp->max_tiles = TN / lp->R + n_list + 1;
+  return ensure_tiles(e, lp->max_tiles);
 }
 
 static inline unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
@@ -397,6 +457,10 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     // level_finish, or by root_setup at depth 0)
     unsigned long long* best = e->best + hcur * e->pick_stride;
     int32_t* agree_max = e->agree_max ? e->agree_max + hcur * e->pick_stride : nullptr;
+    // the (tree, node)s of this depth go through the split buffers whole, or
+    // in chunks of nc_max nodes when they do not fit (chunk nodes are
+    // histogrammed directly: their parents' histograms are not kept)
+    const bool whole = n_tn <= e->nc_max;
     if (d < D && e->des_direct) {
       // ---- E > 1, direct: per-era gains of every (node, era) segment
       const int64_t ncand = (int64_t)n_sel * (B - 1);
@@ -408,102 +472,127 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         if (r) return r;
         e->pcodes_ready = true;
       }
-      int r = launch_des_era(e->V, B, n_keys, st, c.codes_rm, c.stride, F, e->rpos[cur],
-                             e->node_shift[cur], e->order[cur], e->seg[cur], E, nodes,
-                             e->present[cur],
-                             e->local_of, n_sel, mcw, eps, e->sgain, e->sdir,
-                             use_pairs ? e->pcodes : nullptr, N, e->pstride);
-      if (r) return r;
       const int64_t W = (E + kDesEraBlock - 1) / kDesEraBlock;
-      hipLaunchKernelGGL(des_alive_kernel, dim3(blocks_for((int64_t)n_tn * W, 256)), dim3(256), 0,
-                         st, e->seg[cur], E, n_tn, mcw, e->alive);
-      WGBM_LAUNCH_CHECK();
-      hipLaunchKernelGGL(des_block_kernel, dim3(blocks_for((int64_t)n_tn * W * ncand, 256)),
-                         dim3(256), 0, st, e->sgain, e->sdir, E, n_tn, ncand, e->present[cur],
-                         e->alive, e->bsum, e->bdir);
-      WGBM_LAUNCH_CHECK();
-      hipLaunchKernelGGL(des_combine_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)),
-                         dim3(256), 0, st, e->bsum, e->bdir, E, n_tn, ncand, e->present[cur],
-                         e->alive, e->crit, e->agree, agree_max);
-      WGBM_LAUNCH_CHECK();
-      hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)), dim3(256),
-                         0, st, e->crit, e->agree, agree_max, e->present[cur], n_tn, ncand, msg,
-                         best);
-      WGBM_LAUNCH_CHECK();
-      hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)n_tn * E, 256)), dim3(256), 0,
-                         st, best, (const int64_t*)nullptr, (const int32_t*)nullptr, F, B, E,
-                         feat_sel, nodes, n_tn, e->node_shift[cur], mcw, eps, e->sgain,
-                         e->seg[cur], n_sel,
-                         e->split_l, e->split_b, e->split_gain);
-      WGBM_LAUNCH_CHECK();
-    } else if (d < D) {
-      // ---- histograms of the computed segments
-      const int32_t* list = d == 0 ? nullptr : e->key_list[cur];
-      LevelPlan lp;
-      int r = level_plan(e, d, &lp);
-      if (r) return r;
-      const int n_list = lp.n_list;
-      const int64_t R = lp.R, max_tiles = lp.max_tiles, rows_bound = lp.rows_bound;
-      if (!planned) {  // else planned by the previous level's level_scan_kernel
-        hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur], (int64_t)0,
-                           n_list, list, (int32_t)R, 0, (int32_t)max_tiles, e->htiles, e->hkts,
-                           e->hn);
-        WGBM_LAUNCH_CHECK();
-      }
-      HistLaunch a;
-      a.codes = c.codes_rm;
-      a.n_rows = N;
-      a.stride = c.stride;
-      a.n_feats = F;
-      a.resid = e->rpos[cur];  // residuals in position order (global positions)
-      a.resid_by_pos = 1;
-      a.resid_tree_stride = 0;
-      // quantised with the histogram shift of each tile's (tree, node)
-      a.shifts = e->node_shift[cur];
-      a.order = e->order[cur];
-      a.tiles = e->htiles;
-      a.n_tiles = e->hn;
-      a.keys_per_tree = E;
-      a.num_bins = B;
-      a.part = e->part;
-      a.V = e->V;
-      a.n_chunks = e->n_chunks;
-      a.max_tiles = (int32_t)max_tiles;
-      a.native = 1;  // the engine's codes come from the library's binner / pre-binned copy
-      a.timer_tag = "engine_hist_tiles";
-      r = launch_hist_tiles(a, st);
-      if (r) return r;
-      const int64_t tiles_per_key =
-          std::max<int64_t>(1, rows_bound / R / std::max(d == 0 ? n_list : n_list / 2, 1));
-      r = launch_finalize_level(tiles_per_key, e->part, e->hkts, list, n_list, e->n_chunks, e->V,
-                                B, F, E, nodes, d, e->hq[hprev], e->hc[hprev], e->hn, e->hq[hcur],
-                                e->hc[hcur], st);
-      if (r) return r;
-      // ---- split search + DES selection
-      if (E == 1) {
-        // the pick is decoded by level_finish
-        int r = launch_split_level_e1(n_tn, st, e->hq[hcur], e->hc[hcur], F, B, feat_sel, n_sel,
-                                      nodes, e->present[cur], e->node_shift[cur], mcw, eps, msg,
-                                      best);
+      for (int c0 = 0; c0 < n_tn; c0 += (int)e->nc_max) {
+        // nodes [c0, c0 + nc): every node-indexed argument starts at c0
+        const int nc = (int)std::min<int64_t>(e->nc_max, n_tn - c0);
+        const int64_t k0 = (int64_t)c0 * E;
+        int r = launch_des_era(e->V, B, nc * E, st, c.codes_rm, c.stride, F, e->rpos[cur],
+                               e->node_shift[cur] + c0, e->order[cur], e->seg[cur] + k0, E, nodes,
+                               e->present[cur] + c0, e->local_of, n_sel, mcw, eps, e->sgain,
+                               e->sdir, use_pairs ? e->pcodes : nullptr, N, e->pstride);
         if (r) return r;
-      } else {
-        const int64_t ncand = (int64_t)n_sel * (B - 1);
-        const int64_t nacc = (int64_t)n_tn * n_sel * ((B - 1 + kDesChunk - 1) / kDesChunk);
-        hipLaunchKernelGGL(des_accumulate_kernel, dim3(blocks_for(nacc, 128)), dim3(128), 0, st,
-                           e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, n_sel, nodes, n_tn,
-                           e->present[cur], e->node_shift[cur], mcw, eps, e->crit, e->agree,
-                           agree_max);
+        hipLaunchKernelGGL(des_alive_kernel, dim3(blocks_for((int64_t)nc * W, 256)), dim3(256), 0,
+                           st, e->seg[cur] + k0, E, nc, mcw, e->alive);
         WGBM_LAUNCH_CHECK();
-        hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)n_tn * ncand, 256)),
-                           dim3(256), 0, st, e->crit, e->agree, agree_max, e->present[cur],
-                           n_tn, ncand, msg, best);
+        hipLaunchKernelGGL(des_block_kernel, dim3(blocks_for((int64_t)nc * W * ncand, 256)),
+                           dim3(256), 0, st, e->sgain, e->sdir, E, nc, ncand,
+                           e->present[cur] + c0, e->alive, e->bsum, e->bdir);
         WGBM_LAUNCH_CHECK();
-        hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)n_tn * E, 256)), dim3(256),
-                           0, st, best, e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, nodes,
-                           n_tn, e->node_shift[cur], mcw, eps, (const float*)nullptr,
-                           (const int64_t*)nullptr, n_sel, e->split_l, e->split_b, e->split_gain);
+        hipLaunchKernelGGL(des_combine_kernel, dim3(blocks_for((int64_t)nc * ncand, 256)),
+                           dim3(256), 0, st, e->bsum, e->bdir, E, nc, ncand, e->present[cur] + c0,
+                           e->alive, e->crit, e->agree, agree_max + c0);
+        WGBM_LAUNCH_CHECK();
+        hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)nc * ncand, 256)),
+                           dim3(256), 0, st, e->crit, e->agree, agree_max + c0,
+                           e->present[cur] + c0, nc, ncand, msg, best + c0);
+        WGBM_LAUNCH_CHECK();
+        hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)nc * E, 256)), dim3(256),
+                           0, st, best + c0, (const int64_t*)nullptr, (const int32_t*)nullptr, F,
+                           B, E, feat_sel, nodes, nc, e->node_shift[cur] + c0, mcw, eps,
+                           e->sgain, e->seg[cur] + k0, n_sel, e->split_l + c0, e->split_b + c0,
+                           e->split_gain + k0);
         WGBM_LAUNCH_CHECK();
       }
+    } else if (d < D) {
+      // ---- histograms of the computed segments, then split search + DES
+      // selection.  Whole level (and the previous one kept): the smaller
+      // child of every split, the sibling by subtraction.  Otherwise each
+      // chunk's present nodes directly.
+      const bool subtract = whole && (d == 0 || e->stored_prev);
+      const int n_chunk = subtract ? 1 : (int)((n_tn + e->nc_max - 1) / e->nc_max);
+      for (int ch = 0; ch < n_chunk; ++ch) {
+        const int c0 = subtract ? 0 : (int)(ch * e->nc_max);
+        const int nc = subtract ? n_tn : (int)std::min<int64_t>(e->nc_max, n_tn - c0);
+        const int64_t k0 = (int64_t)c0 * E;
+        LevelPlan lp;
+        int r = subtract ? level_plan(e, d, &lp) : chunk_plan(e, (int64_t)nc * E, n_chunk, &lp);
+        if (r) return r;
+        const int n_list = lp.n_list;
+        const int64_t R = lp.R, max_tiles = lp.max_tiles, rows_bound = lp.rows_bound;
+        // keys: the level's pairs (depth > 0), every root key, or the chunk's
+        // present nodes (relative to the chunk)
+        const int32_t* list = nullptr;
+        if (!subtract) {
+          hipLaunchKernelGGL(chunk_keys_kernel, dim3(blocks_for((int64_t)nc * E, 256)),
+                             dim3(256), 0, st, e->present[cur] + c0, E, nc, e->key_list[cur]);
+          WGBM_LAUNCH_CHECK();
+          list = e->key_list[cur];
+        } else if (d > 0) {
+          list = e->key_list[cur];
+        }
+        if (!(subtract && planned)) {  // else planned by the previous level's level_scan_kernel
+          hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur] + k0,
+                             (int64_t)0, n_list, list, (int32_t)R, 0, (int32_t)max_tiles,
+                             e->htiles, e->hkts, e->hn);
+          WGBM_LAUNCH_CHECK();
+        }
+        HistLaunch a;
+        a.codes = c.codes_rm;
+        a.n_rows = N;
+        a.stride = c.stride;
+        a.n_feats = F;
+        a.resid = e->rpos[cur];  // residuals in position order (global positions)
+        a.resid_by_pos = 1;
+        a.resid_tree_stride = 0;
+        // quantised with the histogram shift of each tile's (tree, node)
+        a.shifts = e->node_shift[cur] + c0;
+        a.order = e->order[cur];
+        a.tiles = e->htiles;
+        a.n_tiles = e->hn;
+        a.keys_per_tree = E;
+        a.num_bins = B;
+        a.part = e->part;
+        a.V = e->V;
+        a.n_chunks = e->n_chunks;
+        a.max_tiles = (int32_t)max_tiles;
+        a.native = 1;  // the engine's codes come from the library's binner / pre-binned copy
+        a.timer_tag = "engine_hist_tiles";
+        r = launch_hist_tiles(a, st);
+        if (r) return r;
+        const int64_t pairs = (subtract && d > 0) ? n_list / 2 : n_list;
+        const int64_t tiles_per_key = std::max<int64_t>(1, rows_bound / R / std::max<int64_t>(pairs, 1));
+        r = launch_finalize_level(tiles_per_key, e->part, e->hkts, list, n_list, e->n_chunks, e->V,
+                                  B, F, E, nodes, subtract ? d : 0, e->hq[hprev], e->hc[hprev],
+                                  e->hn, e->hq[hcur], e->hc[hcur], st);
+        if (r) return r;
+        if (E == 1) {
+          // the pick is decoded by level_finish
+          r = launch_split_level_e1(nc, st, e->hq[hcur], e->hc[hcur], F, B, feat_sel, n_sel, nodes,
+                                    e->present[cur] + c0, e->node_shift[cur] + c0, mcw, eps, msg,
+                                    best + c0);
+          if (r) return r;
+        } else {
+          const int64_t ncand = (int64_t)n_sel * (B - 1);
+          const int64_t nacc = (int64_t)nc * n_sel * ((B - 1 + kDesChunk - 1) / kDesChunk);
+          hipLaunchKernelGGL(des_accumulate_kernel, dim3(blocks_for(nacc, 128)), dim3(128), 0, st,
+                             e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, n_sel, nodes, nc,
+                             e->present[cur] + c0, e->node_shift[cur] + c0, mcw, eps, e->crit,
+                             e->agree, agree_max + c0);
+          WGBM_LAUNCH_CHECK();
+          hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)nc * ncand, 256)),
+                             dim3(256), 0, st, e->crit, e->agree, agree_max + c0,
+                             e->present[cur] + c0, nc, ncand, msg, best + c0);
+          WGBM_LAUNCH_CHECK();
+          hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)nc * E, 256)), dim3(256),
+                             0, st, best + c0, e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, nodes,
+                             nc, e->node_shift[cur] + c0, mcw, eps, (const float*)nullptr,
+                             e->seg[cur] + k0, n_sel, e->split_l + c0, e->split_b + c0,
+                             e->split_gain + k0);
+          WGBM_LAUNCH_CHECK();
+        }
+      }
+      e->stored_prev = subtract;
     }
     // ---- leaf values, the tree record of this depth, cleared words of the
     // next depth (child totals, split picks)
@@ -553,7 +642,10 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       // few keys: block prefix, node scan and the next level's tile plan in
       // one workgroup
       LevelPlan lp;
-      const bool next_hist = d + 1 < D && !e->des_direct;
+      // the next level's tiles are planned here when it takes the subtraction
+      // path (all its nodes fit and this level's histograms are kept)
+      const bool next_hist = d + 1 < D && !e->des_direct && 2 * (int64_t)n_tn <= e->nc_max &&
+                             e->stored_prev;
       if (next_hist) {
         const int r = level_plan(e, d + 1, &lp);
         if (r) return r;

@@ -835,6 +835,12 @@ __global__ __launch_bounds__(1024) void level_scan_kernel(
                   key_tile_start, n_tiles);
 }
 
+__global__ void chunk_keys_kernel(const int32_t* __restrict__ present, int32_t E, int32_t n,
+                                  int32_t* __restrict__ list) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < (int64_t)n * E) list[i] = present[i / E] ? (int32_t)i : -1;
+}
+
 __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;

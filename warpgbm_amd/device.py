@@ -308,7 +308,7 @@ class Engine:
     def __init__(self, codes: Codes, root_order: torch.Tensor, era_start: torch.Tensor,
                  num_bins: int, num_eras: int, max_depth: int, n_trees: int, objective: int,
                  min_child_weight: float, min_split_gain: float, l2_reg: float,
-                 learning_rate: float):
+                 learning_rate: float, level_bytes: int = 0):
         self.lib = _lib.load()
         self._keep = (codes, root_order, era_start)
         cfg = _lib.EngineConfig(
@@ -317,7 +317,8 @@ class Engine:
             min_child_weight=float(min_child_weight), min_split_gain=float(min_split_gain),
             l2_reg=float(l2_reg), learning_rate=float(learning_rate),
             codes_rm=codes.rm.data_ptr(), codes_cm=codes.cm.data_ptr(),
-            root_order=root_order.data_ptr(), era_start=era_start.data_ptr())
+            root_order=root_order.data_ptr(), era_start=era_start.data_ptr(),
+            level_bytes=int(level_bytes))
         h = C.c_void_p()
         _lib.check(self.lib.wgbm_engine_create(C.byref(h), C.byref(cfg)), "engine_create")
         self.h = h
