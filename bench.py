@@ -354,42 +354,56 @@ def dropin_leg(raw, grad, order16, seg16_h, N, F, B, dev):
     root (sample_indices = every row) and once per node (that node's rows),
     as warpgbm/core.py:543-563 calls it; the outputs accumulate (the
     reference's per-call torch.zeros is the caller's and is not timed).
-    Median of 5 steps after one warm-up, torch events on the current stream."""
+    Two feature choices: every feature (colsample_bytree = 1, the reference's
+    arange) and a random half (colsample_bytree = 0.5, the reference's
+    randperm(F)[:k], core.py:722).  Median of 5 steps after one warm-up,
+    torch events on the current stream."""
     import torch
 
     from warpgbm_amd import node_kernel as nk
 
-    feats = torch.arange(F, dtype=torch.int32, device=dev)
     era = torch.zeros(N, dtype=torch.int32, device=dev)
     rows_all = torch.arange(N, dtype=torch.int32, device=dev)
     node_rows = [order16[int(seg16_h[k]):int(seg16_h[k + 1])] for k in range(16)]
-    G = torch.zeros((17, 1, F, B), device=dev)
-    H = torch.zeros_like(G)
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    choices = {"all": torch.arange(F, dtype=torch.int32),
+               "half": torch.randperm(F, generator=gen, dtype=torch.int32)[:F // 2]}
+    out = {"op": "node_kernel.compute_histogram3", "calls_per_step": 17,
+           "pattern": "root (sample_indices = all rows) + one call per node, raw [N, F] int8 "
+                      "codes, 1 era"}
+    for name, fsel in choices.items():
+        feats = fsel.to(dev)
+        k = feats.numel()
+        G = torch.zeros((17, 1, k, B), device=dev)
+        H = torch.zeros_like(G)
 
-    def dstep():
-        nk.compute_histogram3(raw, grad, rows_all, feats, era, G[0], H[0], B)
-        for k in range(16):
-            nk.compute_histogram3(raw, grad, node_rows[k], feats, era, G[k + 1], H[k + 1], B)
+        def dstep():
+            nk.compute_histogram3(raw, grad, rows_all, feats, era, G[0], H[0], B)
+            for j in range(16):
+                nk.compute_histogram3(raw, grad, node_rows[j], feats, era, G[j + 1], H[j + 1], B)
 
-    dstep()
-    ts = []
-    for _ in range(5):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
         dstep()
-        b.record()
-        torch.cuda.synchronize()
-        ts.append(a.elapsed_time(b))
-    ms = sorted(ts)[2]
-    # root: codes + gradients + row ids; nodes: the same per row; outputs
-    nbytes = (N * F + 8 * N + F * B * 8) + (N * F + 8 * N + 16 * F * B * 8)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"drop-in compute_histogram3, C2 root + 16 per-node calls: {ms:.3f} ms ({gbs:.0f} GB/s)")
-    return {"op": "node_kernel.compute_histogram3", "calls_per_step": 17,
-            "ms_per_step": round(ms, 4), "bytes": int(nbytes), "GB/s": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "pattern": "root (sample_indices = all rows) + one call per node, raw [N, F] int8 "
-                       "codes, all features, 1 era"}
+        ts = []
+        for _ in range(5):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            dstep()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        ms = sorted(ts)[2]
+        # root and nodes: the selected codes, gradient and row id of every row; outputs
+        nbytes = 2 * (N * k + 8 * N) + 17 * k * B * 8
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        log(f"drop-in compute_histogram3 ({name} features, {k}), C2 root + 16 per-node calls: "
+            f"{ms:.3f} ms ({gbs:.0f} GB/s)")
+        key = "" if name == "all" else "half_"
+        out[key + "features"] = k
+        out[key + "ms_per_step"] = round(ms, 4)
+        out[key + "bytes"] = int(nbytes)
+        out[key + "GB/s"] = round(gbs, 1)
+        out[key + "frac"] = round(gbs / HBM_PEAK_GBS, 4)
+    return out
 
 
 def cpu_baseline_leg(codes_h, grad_h, order16_h, seg16_h, N, F, B, step_bytes, run_c1):

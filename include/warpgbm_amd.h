@@ -46,7 +46,10 @@ const char* wgbm_last_error(void);
  * if 0 <= b < num_bins:  grad_hist[e,f,b] += residual[s];  hess_hist[e,f,b] += 1.
  * grad_hist / hess_hist: float32 [num_eras, n_feats, num_bins], ACCUMULATED
  * into (the caller zeroes them, as the reference's caller does).  Rows whose
- * era is outside [0, num_eras) are skipped.  threads_per_block and
+ * era is outside [0, num_eras) are skipped, and so are feature indices
+ * outside [0, n_feats_master) (their outputs keep their values; the
+ * reference reads such codes out of bounds).  Only the selected columns are
+ * histogrammed (in any order, repeats allowed).  threads_per_block and
  * rows_per_thread are accepted for signature compatibility and ignored. */
 int wgbm_compute_histogram3(const int8_t* bin_indices, int64_t n_rows, int64_t n_feats_master,
                             const float* residuals, const int32_t* sample_indices,

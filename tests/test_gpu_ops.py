@@ -89,6 +89,105 @@ def test_compute_histogram3_bit_exact(gpu, case):
         assert np.all(np.abs(Gc.astype(np.float64) - Gs) <= tol)
 
 
+def _feats(kind, Fm, rng):
+    if kind == "sorted_run":          # aligned run: one V-byte load per row
+        return np.arange(100, 612)
+    if kind == "unaligned_run":       # consecutive but not V-aligned: byte loads
+        return np.arange(101, 613)
+    if kind == "reversed":
+        return np.arange(Fm)[::-1].copy()
+    if kind == "dups":                # repeated indices: each output gets the column
+        f = rng.permutation(Fm)[:60]
+        return np.concatenate([f, f[:17], f[5:9]])
+    if kind == "identity":
+        return np.arange(Fm)
+    return rng.permutation(Fm)[:int(kind)]
+
+
+FMAP_CASES = [
+    # name, N, Fm, B, E, feature choice
+    ("sorted_run", 20000, 1000, 32, 1, "sorted_run"),
+    ("unaligned_run", 20000, 1000, 32, 1, "unaligned_run"),
+    ("half_random_c2_like", 30000, 1000, 32, 1, "500"),
+    ("reversed", 12000, 203, 32, 1, "reversed"),
+    ("dups", 12000, 203, 17, 2, "dups"),
+    ("bytes_mode_identity", 9000, 131, 32, 1, "identity"),
+    ("bytes_mode_subset", 9000, 131, 32, 1, "100"),
+    ("eras_40_subset", 20000, 64, 16, 40, "30"),
+    ("eras_9000_two_windows", 30000, 8, 4, 9000, "identity"),
+]
+
+
+@pytest.mark.parametrize("case", FMAP_CASES, ids=[c[0] for c in FMAP_CASES])
+def test_compute_histogram3_feature_maps(gpu, case):
+    """Feature indices in any order, with repeats, runs and random subsets:
+    only the selected columns are histogrammed and every output o receives
+    column feature_indices[o]; eras regrouped in LDS windows (E > 8192 takes
+    two).  Bit-exact against the oracle."""
+    name, N, Fm, B, E, kind = case
+    print_case("compute_histogram3 feature map", name)
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    codes = rng.integers(-2, B + 2, (N, Fm)).astype(np.int8)
+    resid = rng.standard_normal(N).astype(F32)
+    rows = np.sort(rng.choice(N, N * 3 // 4, replace=False))
+    feats = _feats(kind, Fm, rng)
+    era = rng.integers(0, E, N).astype(np.int32)
+    G = torch.zeros((E, len(feats), B), device=dev)
+    H = torch.zeros_like(G)
+    node_kernel.compute_histogram3(t(codes), t(resid), t(rows, torch.int32),
+                                   t(feats, torch.int32), t(era), G, H, B)
+    Gr, Hr = ops.histogram_exact(codes, resid, rows, feats, era, E, B)
+    assert np.array_equal(H.cpu().numpy(), Hr)
+    assert np.array_equal(bits(G.cpu().numpy()), bits(Gr))
+
+
+def test_compute_histogram3_out_of_range_features(gpu):
+    """Feature indices outside [0, n_feats) (which the reference would read
+    out of bounds) contribute nothing: those outputs keep their values; the
+    others are exact."""
+    print_case("compute_histogram3", "out-of-range feature indices")
+    rng = np.random.default_rng(11)
+    N, Fm, B = 6000, 70, 8
+    codes = rng.integers(0, B, (N, Fm)).astype(np.int8)
+    resid = rng.standard_normal(N).astype(F32)
+    feats = np.array([3, -1, 69, 70, 5, 1 << 20, 3, -(1 << 30)], np.int64)
+    valid = (feats >= 0) & (feats < Fm)
+    era = np.zeros(N, np.int32)
+    G = torch.full((1, len(feats), B), 7.0, device=dev)
+    H = torch.full((1, len(feats), B), 7.0, device=dev)
+    node_kernel.compute_histogram3(t(codes), t(resid), t(np.arange(N), torch.int32),
+                                   t(feats, torch.int32), t(era), G, H, B)
+    Gr, Hr = ops.histogram_exact(codes, resid, np.arange(N), feats[valid], era, 1, B)
+    Gc, Hc = G.cpu().numpy(), H.cpu().numpy()
+    assert np.all(Gc[:, ~valid] == 7.0) and np.all(Hc[:, ~valid] == 7.0)
+    assert np.array_equal(Hc[:, valid], Hr + F32(7.0))
+    assert np.array_equal(bits(Gc[:, valid]), bits(Gr + F32(7.0)))
+
+
+@pytest.mark.parametrize("scale", [1e9, 1e12, 1e30])
+def test_compute_histogram3_huge_residuals(gpu, scale):
+    """Residuals of magnitude 2^qbits and above give a negative shift (the
+    sums are kept in units of 2^-s > 1); the tile kernel must quantise with
+    that shift, not clamp it to 0."""
+    print_case("compute_histogram3", "huge residuals", scale)
+    rng = np.random.default_rng(int(math.log10(scale)))
+    N, Fm, B, E = 9000, 40, 16, 2
+    codes = rng.integers(-1, B + 1, (N, Fm)).astype(np.int8)
+    resid = (rng.standard_normal(N) * scale).astype(F32)
+    rows = np.sort(rng.choice(N, 7000, replace=False))
+    feats = rng.permutation(Fm)[:31]
+    era = rng.integers(0, E, N).astype(np.int32)
+    s = ops.shift_from_absmax(np.max(np.abs(resid[rows])), ops.qbits_for_rows(len(rows)))
+    assert s < 0
+    G = torch.zeros((E, len(feats), B), device=dev)
+    H = torch.zeros_like(G)
+    node_kernel.compute_histogram3(t(codes), t(resid), t(rows, torch.int32),
+                                   t(feats, torch.int32), t(era), G, H, B)
+    Gr, Hr = ops.histogram_exact(codes, resid, rows, feats, era, E, B)
+    assert np.array_equal(H.cpu().numpy(), Hr)
+    assert np.array_equal(bits(G.cpu().numpy()), bits(Gr))
+
+
 def test_compute_histogram3_accumulates_and_handles_empty(gpu):
     print_case("compute_histogram3", "accumulate/empty")
     rng = np.random.default_rng(1)

@@ -93,6 +93,10 @@ static size_t hist_scratch_bytes(const HistPlan& p, int64_t n_pos) {
   return b;
 }
 
+// n_hist_feats: code columns histogrammed (feat_idx == nullptr: outputs
+// [key][n_hist_feats][B]), or the code columns of a row that feat_idx
+// selects from (outputs [key][n_out_feats][B], output o = column
+// feat_idx[o]; only the selected columns are histogrammed)
 static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t stride,
                               int32_t n_hist_feats, const float* resid, const int32_t* rows,
                               int64_t n_pos, const int64_t* seg_dev, int32_t n_seg,
@@ -100,7 +104,11 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
                               int32_t n_out_feats, int32_t num_bins, float* G, float* H,
                               bool native, HistScratch& sc) {
   hipStream_t st = sc.st;
-  const HistPlan pl = hist_plan(n_hist_feats, num_bins, n_pos, rows, seg_dev, n_seg, num_eras);
+  const bool fsel = feat_idx != nullptr;
+  WGBM_REQUIRE(!fsel || (rows && !native), "feature selection needs a row list and raw codes");
+  // histogram features: the distinct selected columns, at most this many
+  const int32_t width = fsel ? std::min(n_out_feats, n_hist_feats) : n_hist_feats;
+  const HistPlan pl = hist_plan(width, num_bins, n_pos, rows, seg_dev, n_seg, num_eras);
   const int V = pl.V, n_chunks = pl.n_chunks, n_abs = pl.n_abs, n_keys = pl.n_keys;
   const bool regroup = pl.regroup;
   const int64_t R = pl.R, max_tiles = pl.max_tiles, tile_words = pl.tile_words;
@@ -110,6 +118,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   uint32_t* absmax = ctl;
   int32_t* shift = (int32_t*)(ctl + 16);
   int32_t* n_tiles = (int32_t*)(ctl + 32);
+  int32_t* n_sel = (int32_t*)(ctl + 48);
   uint32_t* abs_part = ctl + 64;
   float* rpos = nullptr;
   if (pl.gather_resid) {
@@ -122,36 +131,58 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   unsigned long long* part =
       (unsigned long long*)sc.get(sizeof(unsigned long long) * words, 5);
   WGBM_REQUIRE(tiles && kts && part, "scratch allocation failed (%lld words)", (long long)words);
+  FeatMapArgs fm;
+  if (fsel) {
+    // mark [n_master], next [n_out], list and head [width], run [n_chunks]
+    const size_t ints =
+        (size_t)n_hist_feats + (size_t)n_out_feats + 2 * (size_t)width + (size_t)n_chunks;
+    int32_t* m = (int32_t*)sc.get(sizeof(int32_t) * ints, 7);
+    WGBM_REQUIRE(m, "scratch allocation failed");
+    fm.feat_idx = feat_idx;
+    fm.n_out = n_out_feats;
+    fm.n_master = n_hist_feats;
+    fm.V = V;
+    fm.n_chunks = n_chunks;
+    fm.mark = m;
+    fm.next = m + n_hist_feats;
+    fm.list = fm.next + n_out_feats;
+    fm.head = fm.list + width;
+    fm.run = fm.head + width;
+    fm.count = n_sel;
+  }
 
-  // maxima (+ gathered residuals) and, unless the rows are regrouped by era
-  // first, the tile plan: one launch
-  hipLaunchKernelGGL(hist_prep_kernel, dim3(n_abs + (regroup ? 0 : 1)), dim3(1024), 0, st, resid,
-                     rows, n_pos, abs_part, rpos, n_abs, regroup ? 0 : 1, seg_dev, n_keys,
-                     (int32_t)R, (int32_t)max_tiles, tiles, kts, n_tiles);
+  // maxima (+ gathered residuals), the tile plan unless the rows are
+  // regrouped by era first, and the feature map: one launch
+  const unsigned prep_blocks = (unsigned)(n_abs + (regroup ? 0 : 1) + (fsel ? 1 : 0));
+  hipLaunchKernelGGL(hist_prep_kernel, dim3(prep_blocks), dim3(1024), 0, st, resid, rows, n_pos,
+                     abs_part, rpos, n_abs, regroup ? 0 : 1, seg_dev, n_keys, (int32_t)R,
+                     (int32_t)max_tiles, tiles, kts, n_tiles, fm);
   WGBM_LAUNCH_CHECK();
   const int32_t* order = rows;
   const int64_t* seg = seg_dev;
   if (regroup) {
-    int64_t* counts = (int64_t*)sc.get(sizeof(int64_t) * (3 * (size_t)num_eras + 2), 1);
+    // blocks of about 8192 positions, at most 1024, and at most 2^24 count words
+    int64_t nb = std::min<int64_t>(std::max<int64_t>((n_pos + 8191) / 8192, 1), 1024);
+    nb = std::max<int64_t>(1, std::min<int64_t>(nb, ((int64_t)1 << 24) / num_eras));
+    const int64_t per_block = std::max<int64_t>(1, (n_pos + nb - 1) / nb);
+    int32_t* counts = (int32_t*)sc.get(sizeof(int32_t) * (size_t)(num_eras * nb), 1);
+    int64_t* era_tot = (int64_t*)sc.get(sizeof(int64_t) * ((size_t)num_eras + 1), 12);
     int32_t* sorted = (int32_t*)sc.get(sizeof(int32_t) * std::max<int64_t>(n_pos, 1), 2);
-    WGBM_REQUIRE(counts && sorted, "scratch allocation failed");
-    int64_t* starts = counts + num_eras;
-    unsigned long long* cursor = (unsigned long long*)(starts + num_eras + 1);
-    if (fill_u64(counts, num_eras, 0, st)) return WGBM_EINVAL;
-    const unsigned g = std::min<int64_t>(nblocks(std::max<int64_t>(n_pos, 1), 256), 2048);
-    hipLaunchKernelGGL(era_count_kernel, dim3(g), dim3(256), 0, st, rows, n_pos, era, num_eras,
-                       counts);
+    WGBM_REQUIRE(counts && era_tot && sorted, "scratch allocation failed");
+    hipLaunchKernelGGL(era_block_count_kernel, dim3((unsigned)nb), dim3(1024), 0, st, rows, n_pos,
+                       era, num_eras, per_block, counts);
     WGBM_LAUNCH_CHECK();
-    hipLaunchKernelGGL(exclusive_scan_i64_kernel, dim3(1), dim3(1), 0, st, counts, num_eras,
-                       starts);
+    hipLaunchKernelGGL(era_row_scan_kernel, dim3((unsigned)((num_eras + 15) / 16)), dim3(1024), 0,
+                       st, counts, num_eras, (int32_t)nb, era_tot);
     WGBM_LAUNCH_CHECK();
-    WGBM_CHECK(hipMemcpyAsync(cursor, starts, sizeof(int64_t) * num_eras,
-                              hipMemcpyDeviceToDevice, st));
-    hipLaunchKernelGGL(era_scatter_kernel, dim3(g), dim3(256), 0, st, rows, n_pos, era, num_eras,
-                       cursor, sorted);
+    hipLaunchKernelGGL(era_start_scan_kernel, dim3(1), dim3(1024), 0, st, era_tot, num_eras);
+    WGBM_LAUNCH_CHECK();
+    hipLaunchKernelGGL(era_block_scatter_kernel, dim3((unsigned)nb), dim3(1024), 0, st, rows,
+                       n_pos, era, num_eras, per_block, (const int32_t*)counts,
+                       (const int64_t*)era_tot, sorted);
     WGBM_LAUNCH_CHECK();
     order = sorted;
-    seg = starts;
+    seg = era_tot;
     hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, seg, n_pos, n_keys,
                        (const int32_t*)nullptr, (int32_t)R, 1, (int32_t)max_tiles, tiles, kts,
                        n_tiles);
@@ -161,7 +192,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   a.codes = codes;
   a.n_rows = n_rows;
   a.stride = stride;
-  a.n_feats = n_hist_feats;
+  a.n_feats = width;
   a.resid = rpos ? rpos : resid;
   a.resid_by_pos = rpos ? 1 : 0;
   a.resid_tree_stride = 0;
@@ -182,30 +213,27 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   a.sm.qbits = wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1));
   a.sm.absmax_bits = absmax;
   a.sm.shift = shift;
+  if (fsel) {
+    a.fs.list = fm.list;
+    a.fs.count = n_sel;
+    a.fs.run = fm.run;
+    a.fs.n_master = n_hist_feats;
+  }
   int r = launch_hist_tiles(a, st);
   if (r) return r;
   // tiles per segment (finalize's tile split): the planner's estimate
   const int64_t tiles_per_key = std::max<int64_t>(1, (n_pos + R - 1) / R / std::max(n_keys, 1));
-  if (!feat_idx) {
-    // identity feature map: finalize straight into the (accumulated) outputs
-    r = launch_finalize_f32(tiles_per_key, part, kts, n_keys, n_chunks, V, num_bins, n_hist_feats,
-                            shift, absmax, n_tiles, 1, G, H, st);
-    if (r) return r;
-  } else {
-    // full-width histogram in scratch, then the requested features
-    const int64_t full = (int64_t)n_keys * n_hist_feats * num_bins;
-    float* Gf = (float*)sc.get(sizeof(float) * 2 * full, 7);
-    WGBM_REQUIRE(Gf, "scratch allocation failed");
-    float* Hf = Gf + full;
-    r = launch_finalize_f32(tiles_per_key, part, kts, n_keys, n_chunks, V, num_bins, n_hist_feats,
-                            shift, absmax, n_tiles, 0, Gf, Hf, st);
-    if (r) return r;
-    const int64_t nout = (int64_t)n_keys * n_out_feats * num_bins;
-    hipLaunchKernelGGL(hist_gather_features_kernel, dim3(nblocks(nout, 256)), dim3(256), 0, st, Gf,
-                       Hf, n_keys, n_hist_feats, num_bins, feat_idx, n_out_feats, G, H);
-    WGBM_LAUNCH_CHECK();
+  // straight into the (accumulated) outputs, through the feature map if any
+  FeatOut fo;
+  if (fsel) {
+    fo.head = fm.head;
+    fo.next = fm.next;
+    fo.count = n_sel;
+    fo.run = fm.run;
+    fo.n_out = n_out_feats;
   }
-  return 0;
+  return launch_finalize_f32(tiles_per_key, part, kts, n_keys, n_chunks, V, num_bins, width,
+                             shift, absmax, n_tiles, 1, fo, G, H, st);
 }
 
 int wgbm_compute_histogram3(const int8_t* bin_indices, int64_t n_rows, int64_t n_feats_master,
@@ -226,7 +254,7 @@ int wgbm_compute_histogram3(const int8_t* bin_indices, int64_t n_rows, int64_t n
                "null input pointer");
   WGBM_REQUIRE(n_feats == 0 || (feature_indices && grad_hist && hess_hist), "null output pointer");
   WGBM_REQUIRE(num_eras == 1 || era_indices, "era_indices required when num_eras > 1");
-  if (n_feats == 0) return 0;
+  if (n_feats == 0 || n_samples == 0) return 0;  // nothing to add
   HistScratch sc{S(stream)};
   return histogram_pipeline(bin_indices, n_rows, n_feats_master, (int32_t)n_feats_master,
                             residuals, sample_indices, n_samples, nullptr, 1, era_indices,

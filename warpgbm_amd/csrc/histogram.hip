@@ -60,14 +60,25 @@ namespace wgbm {
 //   carries: c + H <= 2B + 3 <= 255) and the address (row << 8) | (l%32)*8
 //   is a single byte permute of the code dword with the lane offset; rows B
 //   and B+1 of each half are the trash rows.  One VALU per atomic.
-template <int V, int MODE, int BT, bool GATHER, bool NAT, bool RPOS>
+//
+// FS (selected features, raw codes, row order): histogram feature h <
+// *fs.count reads code column fs.list[h] (ascending).  A chunk whose lanes
+// all own aligned runs of V consecutive columns (fs.run[chunk]: every
+// feature selected, or sorted ranges) is loaded as above, lane l owning h =
+// chunk*64*V + l*V + j, with one V-byte load per row.  Otherwise lane l owns
+// h = chunk*64*V + j*64 + l and loads its V columns with V byte loads per
+// row, each instruction covering 64 consecutive selected columns (few cache
+// lines); U = 8/V rows per group, so the group's registers match the run
+// path's.
+template <int V, int MODE, int BT, bool GATHER, bool NAT, bool RPOS, bool FS>
 __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void hist_tiles_kernel(
     const int8_t* __restrict__ codes, int64_t n_rows, int64_t stride, int32_t n_feats,
     const float* __restrict__ resid, int64_t resid_tree_stride,
     const int32_t* __restrict__ shifts, const int32_t* __restrict__ order,
     const Tile* __restrict__ tiles, const int32_t* __restrict__ n_tiles, int32_t keys_per_tree,
-    int32_t num_bins_rt, unsigned long long* __restrict__ part, ShiftFromMax sm) {
+    int32_t num_bins_rt, unsigned long long* __restrict__ part, ShiftFromMax sm, FeatSel fs) {
+  static_assert(!FS || (GATHER && !NAT), "feature selection: row order and raw codes");
   // the only LDS of this kernel: with no static LDS it starts at LDS address
   // 0, so the NAT path can form LDS addresses as plain integers
   extern __shared__ unsigned long long lds[];
@@ -95,6 +106,10 @@ void hist_tiles_kernel(
     }
   }
   if (tile_id >= *n_tiles) return;
+  // FS: chunks past the selected features (the grid is sized for the
+  // host's bound) have nothing to do; their partials are never read
+  const int n_sel = FS ? *fs.count : n_feats;
+  if (FS && chunk * CW >= n_sel) return;
   const Tile tl = tiles[tile_id];
   const int Bp = num_bins + 1;
   const int Hn = num_bins + 2;  // NAT: rows per lane half
@@ -108,12 +123,15 @@ void hist_tiles_kernel(
   const int f_base = chunk * CW + lane * V;
   const int tree = tl.key / keys_per_tree;
   const float* __restrict__ r_t = resid + (int64_t)tree * resid_tree_stride;
-  // Shifts lie in [0, 177]; clamping consumes the loaded value here, so the
-  // wait for the (scalar) load happens once before the loop rather than at
-  // the top of every iteration, where it would also drain the wave's
-  // outstanding LDS atomics (both share one counter).
+  // Shifts lie in [qbits - 128, qbits + 149] = [-120, 177] (frexp exponent of
+  // a finite float32 maximum); negative ones quantise residuals of magnitude
+  // 2^qbits and above.  The clamp to a wider range changes no shift: it
+  // consumes the loaded value here, so the wait for the (scalar) load happens
+  // once before the loop rather than at the top of every iteration, where it
+  // would also drain the wave's outstanding LDS atomics (both share one
+  // counter).
   const int s_raw = sm.partial ? __builtin_amdgcn_readfirstlane(s_call) : shifts[tree];
-  const int s = s_raw < 0 ? 0 : (s_raw > 255 ? 255 : s_raw);
+  const int s = s_raw < -160 ? -160 : (s_raw > 255 ? 255 : s_raw);
   const int32_t* __restrict__ ord = GATHER ? order + tl.begin : nullptr;
   const int n = (int)(tl.end - tl.begin);  // a tile has at most 65536 rows
   // A lane past the last feature adds whatever it reads to its own words,
@@ -122,9 +140,27 @@ void hist_tiles_kernel(
   // bin; native codes are in range).  It reads nothing new: an out-of-range
   // buffer offset (returns zeros without a memory access), or the last real
   // feature's offset, whose line the wave fetches anyway.
-  const int vlast = (n_feats - 1) / V * V;
-  const int voff = f_base < n_feats ? f_base : (MODE == kLoadBuffer ? 0x7fffffff : vlast);
-  const int n_valid_bytes = f_base < n_feats ? (n_feats - f_base < V ? n_feats - f_base : V) : 0;
+  // FS: the chunk's lane ownership and the lane's code columns (-1 past the
+  // selected features).  In a run chunk the V-byte load starts at the lane's
+  // first column and may cover unselected columns past the last selected
+  // one, whose words belong to histogram features >= n_sel and are never
+  // read back.
+  int mcol[V];
+  bool run_ok = true;
+  if constexpr (FS) {
+    run_ok = fs.run[chunk] != 0;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int h = chunk * CW + (run_ok ? lane * V + j : j * kHistSlots + lane);
+      mcol[j] = h < n_sel ? fs.list[h] : -1;
+    }
+  }
+  const int n_cols = FS ? fs.n_master : n_feats;  // code columns of a row
+  const int lane_col = FS ? mcol[0] : (f_base < n_feats ? f_base : -1);
+  const int vlast = (n_cols - 1) / V * V;
+  const int voff = lane_col >= 0 ? lane_col : (MODE == kLoadBuffer ? 0x7fffffff : vlast);
+  const int n_valid_bytes =
+      lane_col >= 0 ? (n_cols - lane_col < V ? n_cols - lane_col : V) : 0;
   const uint32_t rs_bytes = (MODE == kLoadBuffer) ? (uint32_t)(n_rows * stride) : 0u;
   const __amdgpu_buffer_rsrc_t rs = wgbm_rsrc(codes, rs_bytes);
   unsigned long long* my = lds + lane;
@@ -241,26 +277,102 @@ void hist_tiles_kernel(
       }
     }
   };
-  int i = wave * U;
-  if (i < n) {
-    load_ids(i);
-    issue(ga, i);
-    // steady state without conditional loads, so that every add waits for
-    // exactly its own group (the other group's loads stay in flight)
-    while (i + 2 * step < n) {
-      issue(gb, i + step);
-      add(ga, i);
-      issue(ga, i + 2 * step);
-      add(gb, i + step);
-      i += 2 * step;
+  // the software pipeline over the wave's row groups (group size UU)
+  auto pipeline = [&](auto& a, auto& b, int uu, auto&& first_ids, auto&& iss, auto&& ad) {
+    const int stp = nwaves * uu;
+    int i = wave * uu;
+    if (i < n) {
+      first_ids(i);
+      iss(a, i);
+      // steady state without conditional loads, so that every add waits for
+      // exactly its own group (the other group's loads stay in flight)
+      while (i + 2 * stp < n) {
+        iss(b, i + stp);
+        ad(a, i);
+        iss(a, i + 2 * stp);
+        ad(b, i + stp);
+        i += 2 * stp;
+      }
+      if (i + stp < n) {
+        iss(b, i + stp);
+        ad(a, i);
+        ad(b, i + stp);
+      } else {
+        ad(a, i);
+      }
     }
-    if (i + step < n) {
-      issue(gb, i + step);
-      add(ga, i);
-      add(gb, i + step);
-    } else {
-      add(ga, i);
+  };
+  if (!FS || run_ok) {
+    pipeline(ga, gb, U, load_ids, issue, add);
+  } else if constexpr (FS) {
+    // per-column byte loads: UG rows per group, V bytes each
+    constexpr int UG = 8 / V;
+    constexpr int stepg = nwaves * UG;
+    struct GroupB {
+      uint32_t c[UG][V];  // zero-extended code bytes
+      float r;            // lane l: residual of row l % UG
+    };
+    GroupB ha, hb;
+    // buffer mode (row stride a multiple of 4, out-of-range offsets read
+    // zeros): the dword that holds the column, the byte taken by a shift;
+    // otherwise byte loads
+    const int col_fill = MODE == kLoadBuffer ? 0x7ffffffc : fs.list[n_sel - 1];
+    int vcol[V];
+    uint32_t vsh[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int cj = mcol[j] >= 0 ? mcol[j] : col_fill;
+      vcol[j] = MODE == kLoadBuffer ? (cj & ~3) : cj;
+      vsh[j] = MODE == kLoadBuffer ? (uint32_t)(cj & 3) * 8u : 0u;
     }
+    const int ug = lane & (UG - 1);
+    int32_t idg = 0;
+    auto load_idg = [&](int i0) {
+      const int iu = i0 + ug < n ? i0 + ug : n - 1;
+      idg = ord[iu];
+    };
+    auto issue_b = [&](GroupB& g, int i0) {
+      int rows[UG];
+#pragma unroll
+      for (int u = 0; u < UG; ++u) rows[u] = __builtin_amdgcn_readlane(idg, u);
+      const int my_pos = row0 + (i0 + ug < n ? i0 + ug : n - 1);
+      g.r = r_t[RPOS ? my_pos : idg];
+      load_idg(i0 + stepg);
+#pragma unroll
+      for (int u = 0; u < UG; ++u) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          if (MODE == kLoadBuffer) {
+            g.c[u][j] = __builtin_amdgcn_raw_buffer_load_b32(rs, vcol[j], rows[u] * (int)stride,
+                                                             kAuxStream);
+          } else {
+            const uint8_t* src =
+                reinterpret_cast<const uint8_t*>(codes) + (int64_t)rows[u] * stride + vcol[j];
+            g.c[u][j] = __builtin_nontemporal_load(src);
+          }
+        }
+      }
+    };
+    auto add_b = [&](const GroupB& g, int i0) {
+      const int64_t qv = (int64_t)wgbm_quantise(g.r, s);
+      const uint64_t pv = (uint64_t)(qv * (int64_t)(1 << WGBM_CBITS) + 1);
+      const uint32_t plo = (uint32_t)pv, phi = (uint32_t)(pv >> 32);
+#pragma unroll
+      for (int u = 0; u < UG; ++u) {
+        const uint64_t wu = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(phi, u) << 32) |
+                            (uint64_t)(uint32_t)__builtin_amdgcn_readlane(plo, u);
+        const unsigned long long w = i0 + u < n ? (unsigned long long)wu : 0ull;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          // out-of-range code (incl. negative int8, read as >= 128) -> trash bin
+          uint32_t c = (g.c[u][j] >> vsh[j]) & 0xffu;
+          c = c < (uint32_t)num_bins ? c : (uint32_t)num_bins;
+          atomicAdd(my + (j * Bp + (int)c) * kHistSlots, w);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    pipeline(ha, hb, UG, load_idg, issue_b, add_b);
   }
   __syncthreads();
 
@@ -303,6 +415,22 @@ __device__ inline void part_feature_bin(int i, int V, int num_bins, int& f, int&
   const int j = jb / num_bins;
   b = jb - j * num_bins;
   f = chunk * kHistSlots * V + sl * V + j;
+}
+
+// the same with the lane ownership of selected-feature chunks (run ==
+// nullptr or run[chunk] != 0: lane-major as above; else feature chunk*64*V
+// + j*64 + lane)
+__device__ inline void part_feature_bin_sel(int i, int V, int num_bins,
+                                            const int32_t* __restrict__ run, int& f, int& b) {
+  const int per_chunk = kHistSlots * V * num_bins;
+  const int chunk = i / per_chunk;
+  const int r = i - chunk * per_chunk;
+  const int sl = r & (kHistSlots - 1);
+  const int jb = r / kHistSlots;
+  const int j = jb / num_bins;
+  b = jb - j * num_bins;
+  const bool lane_major = run == nullptr || run[chunk] != 0;
+  f = chunk * kHistSlots * V + (lane_major ? sl * V + j : j * kHistSlots + sl);
 }
 
 // --------------------------------------------------------------------------
@@ -366,14 +494,20 @@ __global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
     const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
     int32_t n_keys, int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
     const int32_t* __restrict__ shifts, const uint32_t* __restrict__ absmax_bits,
-    const int32_t* __restrict__ n_tiles, int32_t accumulate, float* __restrict__ G,
+    const int32_t* __restrict__ n_tiles, int32_t accumulate, FeatOut fo, float* __restrict__ G,
     float* __restrict__ H) {
   // tile_words < 2^31 (checked by the launcher)
   const int tile_words = n_chunks * kHistSlots * V * num_bins;
   const int wpk = (tile_words + FW - 1) / FW;  // workgroups per segment
   const int k = (int)blockIdx.x / wpk;
   const int i = ((int)blockIdx.x - k * wpk) * FW + (int)threadIdx.x % FW;
-  const bool ok = k < n_keys && i < tile_words;
+  const int n_hist = fo.head ? *fo.count : n_feats;  // histogram features with outputs
+  int f = 0, b = 0;
+  bool ok = k < n_keys && i < tile_words;
+  if (ok) {
+    part_feature_bin_sel(i, V, num_bins, fo.run, f, b);
+    ok = f < n_hist;
+  }
   int t0 = 0, t1 = 0;
   if (k < n_keys) {
     t0 = key_tile_start[k];
@@ -382,18 +516,19 @@ __global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
   int64_t Q, C;
   finalize_sum<FW>(part, tile_words, i, ok, t0, t1, Q, C);
   if (!ok || threadIdx.x >= FW) return;
-  int f, b;
-  part_feature_bin(i, V, num_bins, f, b);
-  if (f >= n_feats) return;
   const bool bad = (*absmax_bits) >= 0x7f800000u;  // non-finite residual seen
   const float g = bad ? __builtin_nanf("") : wgbm_dequantise(Q, shifts[0]);
-  const int64_t o = ((int64_t)k * n_feats + f) * num_bins + b;
-  if (accumulate) {
-    G[o] = G[o] + g;
-    H[o] = H[o] + (float)C;
-  } else {
-    G[o] = g;
-    H[o] = (float)C;
+  const float h = (float)C;
+  const int n_out = fo.head ? fo.n_out : n_feats;
+  for (int of = fo.head ? fo.head[f] : f; of >= 0; of = fo.head ? fo.next[of] : -1) {
+    const int64_t o = ((int64_t)k * n_out + of) * num_bins + b;
+    if (accumulate) {
+      G[o] = G[o] + g;
+      H[o] = H[o] + h;
+    } else {
+      G[o] = g;
+      H[o] = h;
+    }
   }
 }
 
@@ -463,7 +598,7 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_f32_kernel(
     const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
     int32_t n_keys, int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
     const int32_t* __restrict__ shifts, const uint32_t* __restrict__ absmax_bits,
-    const int32_t* __restrict__ n_tiles, int32_t accumulate, float* __restrict__ G,
+    const int32_t* __restrict__ n_tiles, int32_t accumulate, FeatOut fo, float* __restrict__ G,
     float* __restrict__ H) {
   __shared__ unsigned long long sq[kPlaneMaxBins * kPlaneRow];
   __shared__ unsigned int sc[kPlaneMaxBins * kPlaneRow];
@@ -472,26 +607,32 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_f32_kernel(
   const int plane = (int)blockIdx.x - k * P;
   if (k >= n_keys) return;  // uniform per workgroup
   const int chunk = plane / V, j = plane - (plane / V) * V;
+  const int n_hist = fo.head ? *fo.count : n_feats;  // histogram features with outputs
+  if (chunk * kHistSlots * V >= n_hist) return;     // uniform per workgroup
   const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
   const int t0 = key_tile_start[k];
   const int t1 = key_tile_start[k + 1] < *n_tiles ? key_tile_start[k + 1] : *n_tiles;
   plane_sum(part, tile_words, plane * num_bins * kHistSlots, num_bins, t0, t1, sq, sc);
   const bool bad = (*absmax_bits) >= 0x7f800000u;  // non-finite residual seen
   const int s = shifts[0];
+  const int n_out = fo.head ? fo.n_out : n_feats;
+  const bool lane_major = fo.run == nullptr || fo.run[chunk] != 0;
   for (int o = threadIdx.x; o < kHistSlots * num_bins; o += kPlaneThreads) {
     const int lane = o / num_bins, b = o - lane * num_bins;
-    const int f = chunk * kHistSlots * V + lane * V + j;
-    if (f >= n_feats) continue;
+    const int f = chunk * kHistSlots * V + (lane_major ? lane * V + j : j * kHistSlots + lane);
+    if (f >= n_hist) continue;
     const int li = b * kPlaneRow + lane;
     const float g = bad ? __builtin_nanf("") : wgbm_dequantise((int64_t)sq[li], s);
     const float h = (float)sc[li];
-    const int64_t out = ((int64_t)k * n_feats + f) * num_bins + b;
-    if (accumulate) {
-      G[out] = G[out] + g;
-      H[out] = H[out] + h;
-    } else {
-      G[out] = g;
-      H[out] = h;
+    for (int of = fo.head ? fo.head[f] : f; of >= 0; of = fo.head ? fo.next[of] : -1) {
+      const int64_t out = ((int64_t)k * n_out + of) * num_bins + b;
+      if (accumulate) {
+        G[out] = G[out] + g;
+        H[out] = H[out] + h;
+      } else {
+        G[out] = g;
+        H[out] = h;
+      }
     }
   }
 }
@@ -546,24 +687,6 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_level_kerne
       hc[skey * per_key + fb] = parent_c[pkey * per_key + fb] - C;
     }
   }
-}
-
-// out[e, fo, b] += full[e, feat[fo], b]  (feature selection of compute_histogram3)
-__global__ void hist_gather_features_kernel(const float* __restrict__ Gf,
-                                            const float* __restrict__ Hf, int32_t n_keys,
-                                            int32_t n_feats_full, int32_t num_bins,
-                                            const int32_t* __restrict__ feat_idx,
-                                            int32_t n_out, float* __restrict__ G,
-                                            float* __restrict__ H) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (int64_t)n_keys * n_out * num_bins) return;
-  const int b = (int)(gid % num_bins);
-  const int fo = (int)((gid / num_bins) % n_out);
-  const int k = (int)(gid / ((int64_t)num_bins * n_out));
-  const int f = feat_idx[fo];
-  const int64_t src = ((int64_t)k * n_feats_full + f) * num_bins + b;
-  G[gid] = G[gid] + Gf[src];
-  H[gid] = H[gid] + Hf[src];
 }
 
 // --------------------------------------------------------------------------
@@ -637,20 +760,72 @@ __global__ void absmax_finish_kernel(const uint32_t* __restrict__ partial, int32
   }
 }
 
+// The feature map of a call with feature indices (one workgroup of 1024):
+// every requested column f in [0, n_master) gets the list of its outputs
+// (mark[f] = first, next[o] = following, -1 ends; indices outside the
+// columns have no list and contribute nothing), and the columns that have
+// one are numbered in ascending order: list[h] = column, head[h] = its
+// first output, *count = how many.
+__device__ void feature_map_body(const FeatMapArgs& fm) {
+  __shared__ int64_t wsum[16];
+  __shared__ int64_t sbuf[kScanK * 1024];
+  for (int f = threadIdx.x; f < fm.n_master; f += blockDim.x) fm.mark[f] = -1;
+  __syncthreads();
+  for (int o = threadIdx.x; o < fm.n_out; o += blockDim.x) {
+    const int f = fm.feat_idx[o];
+    fm.next[o] = (f >= 0 && f < fm.n_master) ? atomicExch(&fm.mark[f], o) : -1;
+  }
+  __syncthreads();
+  // the exchanged heads live in L2: read them with device-scope loads
+  auto head_of = [&](int f) {
+    return __hip_atomic_load(&fm.mark[f], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  const int64_t tot = wgbm_block_scan_tiled(
+      fm.n_master, [&](int f) -> int64_t { return head_of(f) >= 0 ? 1 : 0; },
+      [&](int f, int64_t h) {
+        const int m = head_of(f);
+        if (m >= 0) {
+          fm.list[h] = f;
+          fm.head[h] = m;
+        }
+      },
+      wsum, sbuf);
+  // lane ownership per chunk: a run chunk needs every lane's selected
+  // features to be V consecutive columns starting at a multiple of V (a
+  // lane with none, past the end, does not matter)
+  const int n_sel = (int)tot;
+  for (int c = threadIdx.x; c < fm.n_chunks; c += blockDim.x) fm.run[c] = 1;
+  __syncthreads();
+  for (int g = threadIdx.x; g < fm.n_chunks * kHistSlots; g += blockDim.x) {
+    const int h0 = g * fm.V;
+    if (h0 >= n_sel) continue;
+    auto col = [&](int h) {
+      return __hip_atomic_load(&fm.list[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    const int c0 = col(h0);
+    bool ok = c0 % fm.V == 0;
+    for (int j = 1; j < fm.V && h0 + j < n_sel; ++j) ok = ok && col(h0 + j) == c0 + j;
+    if (!ok) fm.run[g / kHistSlots] = 0;
+  }
+  if (threadIdx.x == 0) *fm.count = n_sel;
+}
+
 // One launch for a call's preparation: blocks [0, n_part) write the per-block
-// maxima of |residual| (and, with rows, the residuals in position order), and
-// with plan != 0 block n_part plans the tiles.  The tile kernel turns the
-// maxima into the shift.
+// maxima of |residual| (and, with rows, the residuals in position order);
+// then, with plan != 0, one block plans the tiles and, with a feature map,
+// one block builds it.  The tile kernel turns the maxima into the shift.
 __global__ __launch_bounds__(1024) void hist_prep_kernel(
     const float* __restrict__ resid, const int32_t* __restrict__ rows, int64_t n,
     uint32_t* __restrict__ partial, float* __restrict__ gathered, int32_t n_part, int32_t plan,
     const int64_t* __restrict__ seg, int32_t n_keys, int32_t tile_rows, int32_t max_tiles,
     Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
-    int32_t* __restrict__ n_tiles) {
+    int32_t* __restrict__ n_tiles, FeatMapArgs fm) {
   if ((int)blockIdx.x >= n_part) {
-    if (plan)
+    if (plan && (int)blockIdx.x == n_part)
       plan_tiles_body(seg, n, n_keys, nullptr, tile_rows, 1, max_tiles, tiles, key_tile_start,
                       n_tiles);
+    else if (fm.feat_idx)
+      feature_map_body(fm);
     return;
   }
   uint32_t m = 0;
@@ -677,7 +852,94 @@ __global__ __launch_bounds__(1024) void plan_tiles_kernel(
 
 
 // --------------------------------------------------------------------------
-// era sort for the ABI path: rows -> era-grouped positions
+// era regrouping for the ABI path: row list -> era-grouped positions.
+// Positions are split into nb contiguous blocks of per_block; block b counts
+// its rows per era in LDS (kEraWindow eras per pass), the counts [era][block]
+// are scanned per era (offsets inside the era) and across eras (era starts),
+// and block b scatters its rows from LDS cursors at start[e] + offset[e][b].
+// Rows with an era outside [0, num_eras) are dropped.  The order of rows
+// inside an era follows LDS atomics (the histogram sums are exact integers,
+// so it does not change a result).
+// --------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void era_block_count_kernel(
+    const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ era,
+    int32_t num_eras, int64_t per_block, int32_t* __restrict__ counts) {
+  __shared__ uint32_t c[kEraWindow];
+  const int nb = gridDim.x;
+  const int64_t p0 = (int64_t)blockIdx.x * per_block;
+  const int64_t p1 = p0 + per_block < n ? p0 + per_block : n;
+  for (int w0 = 0; w0 < num_eras; w0 += kEraWindow) {
+    const int wn = num_eras - w0 < kEraWindow ? num_eras - w0 : kEraWindow;
+    for (int i = threadIdx.x; i < wn; i += blockDim.x) c[i] = 0u;
+    __syncthreads();
+    for (int64_t p = p0 + threadIdx.x; p < p1; p += blockDim.x) {
+      const int e = era[rows ? rows[p] : (int32_t)p] - w0;
+      if ((unsigned)e < (unsigned)wn) atomicAdd(&c[e], 1u);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < wn; i += blockDim.x)
+      counts[(int64_t)(w0 + i) * nb + blockIdx.x] = (int32_t)c[i];
+    __syncthreads();
+  }
+}
+
+// one wave per era: counts[e][0..nb) -> exclusive offsets in place, era_tot[e]
+// = the era's rows
+__global__ __launch_bounds__(1024) void era_row_scan_kernel(int32_t* __restrict__ counts,
+                                                            int32_t num_eras, int32_t nb,
+                                                            int64_t* __restrict__ era_tot) {
+  const int e = (int)blockIdx.x * 16 + (int)(threadIdx.x >> 6);
+  if (e >= num_eras) return;
+  const int lane = threadIdx.x & 63;
+  int32_t* row = counts + (int64_t)e * nb;
+  int64_t carry = 0;
+  for (int b0 = 0; b0 < nb; b0 += 64) {
+    const int b = b0 + lane;
+    const int64_t v = b < nb ? row[b] : 0;
+    const int64_t inc = wgbm_wave_incl_scan_i64(v);
+    if (b < nb) row[b] = (int32_t)(carry + inc - v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)inc, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)inc >> 32), 63);
+    carry += (int64_t)(((uint64_t)hi << 32) | lo);
+  }
+  if (lane == 0) era_tot[e] = carry;
+}
+
+// one workgroup: era_tot[0..E) -> exclusive era starts in place, era_tot[E] =
+// the total (the segment bounds of the regrouped positions)
+__global__ __launch_bounds__(1024) void era_start_scan_kernel(int64_t* __restrict__ era_tot,
+                                                              int32_t num_eras) {
+  __shared__ int64_t wsum[16];
+  __shared__ int64_t sbuf[kScanK * 1024];
+  const int64_t tot = wgbm_block_scan_tiled(
+      num_eras, [&](int i) -> int64_t { return era_tot[i]; },
+      [&](int i, int64_t v) { era_tot[i] = v; }, wsum, sbuf);
+  if (threadIdx.x == 0) era_tot[num_eras] = tot;
+}
+
+__global__ __launch_bounds__(1024) void era_block_scatter_kernel(
+    const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ era,
+    int32_t num_eras, int64_t per_block, const int32_t* __restrict__ offs,
+    const int64_t* __restrict__ seg, int32_t* __restrict__ out) {
+  __shared__ uint32_t cur[kEraWindow];
+  const int nb = gridDim.x;
+  const int64_t p0 = (int64_t)blockIdx.x * per_block;
+  const int64_t p1 = p0 + per_block < n ? p0 + per_block : n;
+  for (int w0 = 0; w0 < num_eras; w0 += kEraWindow) {
+    const int wn = num_eras - w0 < kEraWindow ? num_eras - w0 : kEraWindow;
+    // positions < 2^31: 32-bit cursors
+    for (int i = threadIdx.x; i < wn; i += blockDim.x)
+      cur[i] = (uint32_t)(seg[w0 + i] + offs[(int64_t)(w0 + i) * nb + blockIdx.x]);
+    __syncthreads();
+    for (int64_t p = p0 + threadIdx.x; p < p1; p += blockDim.x) {
+      const int32_t r = rows ? rows[p] : (int32_t)p;
+      const int e = era[r] - w0;
+      if ((unsigned)e < (unsigned)wn) out[atomicAdd(&cur[e], 1u)] = r;
+    }
+    __syncthreads();
+  }
+}
+
 // --------------------------------------------------------------------------
 __global__ void era_count_kernel(const int32_t* __restrict__ rows, int64_t n,
                                  const int32_t* __restrict__ era, int32_t num_eras,
@@ -801,13 +1063,13 @@ int launch_finalize_f32(int64_t tiles_per_key, const unsigned long long* part,
                         const int32_t* key_tile_start, int32_t n_keys, int32_t n_chunks, int32_t V,
                         int32_t num_bins, int32_t n_feats, const int32_t* shifts,
                         const uint32_t* absmax_bits, const int32_t* n_tiles, int32_t accumulate,
-                        float* G, float* H, hipStream_t st) {
+                        FeatOut fo, float* G, float* H, hipStream_t st) {
   if (use_plane_finalize(tiles_per_key, n_keys, n_chunks, V, num_bins)) {
     const int64_t wg = (int64_t)n_keys * n_chunks * V;
     WGBM_REQUIRE(wg < ((int64_t)1 << 31), "finalize: too many segments");
     hipLaunchKernelGGL(hist_finalize_plane_f32_kernel, dim3((unsigned)wg), dim3(kPlaneThreads), 0,
                        st, part, key_tile_start, n_keys, n_chunks, V, num_bins, n_feats, shifts,
-                       absmax_bits, n_tiles, accumulate, G, H);
+                       absmax_bits, n_tiles, accumulate, fo, G, H);
     WGBM_LAUNCH_CHECK();
     return 0;
   }
@@ -820,7 +1082,7 @@ int launch_finalize_f32(int64_t tiles_per_key, const unsigned long long* part,
 #define WGBM_L(F)                                                                                 \
   hipLaunchKernelGGL(hist_finalize_f32_kernel<F>, dim3(wg), dim3(256), 0, st, part, key_tile_start, \
                      n_keys, n_chunks, V, num_bins, n_feats, shifts, absmax_bits, n_tiles,          \
-                     accumulate, G, H)
+                     accumulate, fo, G, H)
   WGBM_FIN_DISPATCH(fw, WGBM_L)
 #undef WGBM_L
   WGBM_LAUNCH_CHECK();
@@ -885,24 +1147,25 @@ size_t hist_lds_bytes(int V, int num_bins, bool native) {
 // the native-code layout needs c + H <= 255 for every byte c <= B + 1
 bool hist_native_ok(int num_bins) { return 2 * num_bins + 3 <= 255; }
 
-template <int V, int MODE, int BT, bool GATHER, bool NAT, bool RPOS>
+template <int V, int MODE, int BT, bool GATHER, bool NAT, bool RPOS, bool FS = false>
 static int launch_tiles_t(const HistLaunch& a, hipStream_t st) {
   static bool attr_set = false;
   const size_t lds = hist_lds_bytes(V, a.num_bins, NAT);
   if (!attr_set) {
-    WGBM_CHECK(hipFuncSetAttribute((const void*)hist_tiles_kernel<V, MODE, BT, GATHER, NAT, RPOS>,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    WGBM_CHECK(hipFuncSetAttribute(
+        (const void*)hist_tiles_kernel<V, MODE, BT, GATHER, NAT, RPOS, FS>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     attr_set = true;
   }
   dim3 grid((unsigned)((int64_t)a.n_chunks * a.max_tiles));
   void* tm = timer_begin(a.timer_tag);
   const bool marks = tm && timer_mode() == 1;
   if (marks) WGBM_CHECK(hipEventRecord(timer_start_event(tm), st));
-  hipExtLaunchKernelGGL((hist_tiles_kernel<V, MODE, BT, GATHER, NAT, RPOS>), grid,
+  hipExtLaunchKernelGGL((hist_tiles_kernel<V, MODE, BT, GATHER, NAT, RPOS, FS>), grid,
                         dim3(kHistThreads), lds, st, marks ? nullptr : timer_start_event(tm),
                         marks ? nullptr : timer_stop_event(tm), 0, a.codes, a.n_rows, a.stride,
                         a.n_feats, a.resid, a.resid_tree_stride, a.shifts, a.order, a.tiles,
-                        a.n_tiles, a.keys_per_tree, a.num_bins, a.part, a.sm);
+                        a.n_tiles, a.keys_per_tree, a.num_bins, a.part, a.sm, a.fs);
   if (marks) WGBM_CHECK(hipEventRecord(timer_stop_event(tm), st));
   timer_end(tm);
   WGBM_LAUNCH_CHECK();
@@ -912,6 +1175,11 @@ static int launch_tiles_t(const HistLaunch& a, hipStream_t st) {
 template <int V, int MODE, int BT, bool NAT>
 static int launch_tiles_r(const HistLaunch& a, hipStream_t st) {
   if (!a.order) return launch_tiles_t<V, MODE, BT, false, NAT, false>(a, st);
+  if constexpr (!NAT) {
+    if (a.fs.list)
+      return a.resid_by_pos ? launch_tiles_t<V, MODE, BT, true, false, true, true>(a, st)
+                            : launch_tiles_t<V, MODE, BT, true, false, false, true>(a, st);
+  }
   return a.resid_by_pos ? launch_tiles_t<V, MODE, BT, true, NAT, true>(a, st)
                         : launch_tiles_t<V, MODE, BT, true, NAT, false>(a, st);
 }
@@ -930,6 +1198,9 @@ int hist_load_mode(int64_t n_rows, int64_t stride, int V) {
 
 int launch_hist_tiles(const HistLaunch& a, hipStream_t st) {
   WGBM_REQUIRE(a.n_rows < ((int64_t)1 << 31), "histogram: at most 2^31 - 1 rows");
+  WGBM_REQUIRE(!a.fs.list || (a.order && a.fs.count && a.fs.run && !a.native &&
+                                a.fs.n_master <= a.stride),
+               "histogram: feature selection needs a row list and raw codes");
   const int mode = hist_load_mode(a.n_rows, a.stride, a.V);
   if (a.V == 4 && a.num_bins == 32) {
     if (mode == kLoadBuffer) return launch_tiles_g<4, kLoadBuffer, 32>(a, st);

@@ -49,6 +49,51 @@ struct ShiftFromMax {
   int32_t* shift = nullptr;
 };
 
+// Feature selection of a histogram call (compute_histogram3's feature
+// indices): histogram feature h < *count reads code column list[h] of each
+// row (list ascending, distinct).  list == nullptr: feature h is column h.
+// Per chunk of 64*V histogram features, run[c] != 0 when every lane's V
+// features are an aligned run of V consecutive columns (lane l owns features
+// c*64*V + l*V + j, loaded with one V-byte load per row); otherwise lane l
+// owns features c*64*V + j*64 + l (V byte loads per row, each covering 64
+// consecutive selected columns).
+struct FeatSel {
+  const int32_t* list = nullptr;
+  const int32_t* count = nullptr;
+  const int32_t* run = nullptr;
+  int32_t n_master = 0;  // code columns per row
+};
+
+// Outputs of a selected histogram feature h: head[h] is the first output
+// index o (feature_indices[o] == list[h]), next[o] the following one or -1.
+// head == nullptr: feature h is output h (f < n_feats).
+struct FeatOut {
+  const int32_t* head = nullptr;
+  const int32_t* next = nullptr;
+  const int32_t* count = nullptr;
+  const int32_t* run = nullptr;  // lane ownership per chunk, as FeatSel
+  int32_t n_out = 0;  // features of the output layout [key][n_out][B]
+};
+
+// The map from requested features to histogram features, built on the
+// device by one workgroup of the preparation launch: mark [n_master] and
+// next [n_out] hold the per-column output lists, list/head [min(n_out,
+// n_master)] and *count the distinct requested columns in ascending order,
+// run [n_chunks] the lane ownership of each chunk (FeatSel).
+struct FeatMapArgs {
+  const int32_t* feat_idx = nullptr;  // nullptr: no map
+  int32_t n_out = 0;
+  int32_t n_master = 0;
+  int32_t V = 1;
+  int32_t n_chunks = 0;
+  int32_t* mark = nullptr;
+  int32_t* next = nullptr;
+  int32_t* list = nullptr;
+  int32_t* head = nullptr;
+  int32_t* count = nullptr;
+  int32_t* run = nullptr;
+};
+
 struct HistLaunch {
   const int8_t* codes;
   int64_t n_rows;
@@ -75,6 +120,9 @@ struct HistLaunch {
   // timer tag of the tile kernel (nullptr: not timed)
   const char* timer_tag = nullptr;
   ShiftFromMax sm;
+  // selected features (fs.list != nullptr: n_feats bounds *fs.count; row
+  // order required, raw codes only)
+  FeatSel fs;
 };
 
 int hist_pick_v(int num_bins, int64_t n_feats);
@@ -89,11 +137,7 @@ int launch_finalize_f32(int64_t tiles_per_key, const unsigned long long* part,
                         const int32_t* key_tile_start, int32_t n_keys, int32_t n_chunks, int32_t V,
                         int32_t num_bins, int32_t n_feats, const int32_t* shifts,
                         const uint32_t* absmax_bits, const int32_t* n_tiles, int32_t accumulate,
-                        float* G, float* H, hipStream_t st);
-__global__ void hist_gather_features_kernel(const float* Gf, const float* Hf, int32_t n_keys,
-                                            int32_t n_feats_full, int32_t num_bins,
-                                            const int32_t* feat_idx, int32_t n_out, float* G,
-                                            float* H);
+                        FeatOut fo, float* G, float* H, hipStream_t st);
 int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
                           const int32_t* key_tile_start, const int32_t* key_list, int32_t n_list,
                           int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
@@ -110,12 +154,18 @@ __global__ void hist_prep_kernel(const float* resid, const int32_t* rows, int64_
                                  uint32_t* partial, float* gathered, int32_t n_part, int32_t plan,
                                  const int64_t* seg, int32_t n_keys, int32_t tile_rows,
                                  int32_t max_tiles, Tile* tiles, int32_t* key_tile_start,
-                                 int32_t* n_tiles);
-__global__ void era_count_kernel(const int32_t* rows, int64_t n, const int32_t* era,
-                                 int32_t num_eras, int64_t* counts);
-__global__ void exclusive_scan_i64_kernel(const int64_t* in, int32_t n, int64_t* out);
-__global__ void era_scatter_kernel(const int32_t* rows, int64_t n, const int32_t* era,
-                                   int32_t num_eras, unsigned long long* cursor, int32_t* out);
+                                 int32_t* n_tiles, FeatMapArgs fm);
+// era regrouping of a row list (compute_histogram3 with eras): block counts,
+// per-era scans, era starts, block scatter; no device-scope atomics
+constexpr int kEraWindow = 8192;  // eras counted per LDS pass
+__global__ void era_block_count_kernel(const int32_t* rows, int64_t n, const int32_t* era,
+                                       int32_t num_eras, int64_t per_block, int32_t* counts);
+__global__ void era_row_scan_kernel(int32_t* counts, int32_t num_eras, int32_t nb,
+                                    int64_t* era_tot);
+__global__ void era_start_scan_kernel(int64_t* era_tot, int32_t num_eras);
+__global__ void era_block_scatter_kernel(const int32_t* rows, int64_t n, const int32_t* era,
+                                         int32_t num_eras, int64_t per_block,
+                                         const int32_t* offs, const int64_t* seg, int32_t* out);
 
 // generic fills (graph-safe replacement for memset)
 __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v);
