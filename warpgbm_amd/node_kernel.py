@@ -127,3 +127,19 @@ def predict_forest(bin_indices, tree_tensor, learning_rate, out) -> None:
                                  float(learning_rate), out.data_ptr(),
                                  _lib.current_stream_ptr(out.device))
     _lib.check(rc, "predict_forest")
+
+
+def install_as_reference_module() -> None:
+    """Serve this module as ``warpgbm.cuda.node_kernel``, the name the
+    reference estimator imports it by (``from warpgbm.cuda import
+    node_kernel``, warpgbm/core.py:7), so that the reference's own Python
+    runs on these kernels without an edit.  Call it before the reference's
+    ``warpgbm.core`` is imported; the reference's ``warpgbm`` package itself
+    must still be importable (only its compiled op module is replaced)."""
+    import sys
+
+    me = sys.modules[__name__]
+    sys.modules["warpgbm.cuda.node_kernel"] = me
+    parent = sys.modules.get("warpgbm.cuda")
+    if parent is not None:
+        setattr(parent, "node_kernel", me)
