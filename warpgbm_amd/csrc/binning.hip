@@ -63,8 +63,9 @@ __device__ inline int count_le(const float* e, int ne, float v) {
 // batched binner: X [n, F] row-major float32 (row stride xs floats) ->
 //   codes_rm [n, S] (native; the binner's codes are in [0, n_edges] and
 //   num_bins = n_edges + 1) and, if non-null, codes_cm [F, n].
-// workgroup: 64 features x BT_R rows; the edges of its 64 features staged in
-// LDS once.  Lane l of every wave owns feature f0 + l (coalesced 256-byte row
+// workgroup: 64 features x BT_R rows (the feature tiles of a row block
+// consecutive in the XCD work order, so a cache line shared by two tiles is
+// fetched once); the edges of its 64 features staged in LDS once.  Lane l of every wave owns feature f0 + l (coalesced 256-byte row
 // loads, 64-byte code stores); each thread issues the loads of 8 rows before
 // it searches them, so several rows are in flight.  The column-major copy is
 // transposed through LDS and written as BT_R-byte runs per feature.
@@ -78,8 +79,12 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
     int8_t* __restrict__ codes_cm) {
   extern __shared__ float sedge[];  // [BT_F][n_edges]
   __shared__ int8_t tcode[BT_F][BT_R + 4];
-  const int64_t r0 = (int64_t)blockIdx.x * BT_R;
-  const int f0 = blockIdx.y * BT_F;
+  const int nft = (F + BT_F - 1) / BT_F;
+  const int64_t n_work = (n + BT_R - 1) / BT_R * nft;
+  const int64_t w = wgbm_xcd_work(blockIdx.x, n_work);
+  if (w >= n_work) return;  // uniform over the workgroup
+  const int64_t r0 = w / nft * BT_R;
+  const int f0 = (int)(w % nft) * BT_F;
   const int tid = threadIdx.x;
   for (int i = tid; i < BT_F * n_edges; i += blockDim.x) {
     const int fl = i / n_edges;
@@ -140,8 +145,13 @@ __global__ __launch_bounds__(256) void copy_prebinned_kernel(const int8_t* __res
                                                              int32_t num_bins,
                                                              int32_t* __restrict__ over) {
   __shared__ int8_t tcode[BT_F][BT_R + 4];
-  const int64_t r0 = (int64_t)blockIdx.x * BT_R;
-  const int f0 = blockIdx.y * BT_F;
+  // tiles in the XCD work order, as bin_matrix_kernel
+  const int nft = (F + BT_F - 1) / BT_F;
+  const int64_t n_work = (n + BT_R - 1) / BT_R * nft;
+  const int64_t w = wgbm_xcd_work(blockIdx.x, n_work);
+  if (w >= n_work) return;  // uniform over the workgroup
+  const int64_t r0 = w / nft * BT_R;
+  const int f0 = (int)(w % nft) * BT_F;
   const int tid = threadIdx.x;
   const int fl = tid & 63;
   const int rq = tid >> 6;  // rows rq, rq + 4, ... of the tile
@@ -227,53 +237,120 @@ __device__ inline float key_to_float(uint32_t k) {
   return __uint_as_float(u);
 }
 
-// X [n, F] float32 (row stride xs) -> keys [F, n]: a workgroup moves 64
-// features x kTransRows rows in 64 x 64 tiles through LDS, and keeps the
-// smallest and largest key of each of its features (a NaN key is the
-// largest), merged into kmin / kmax [F] with one atomic per feature.
+// X [n, F] float32 (row stride xs) -> keys [F][ks] (ks >= n, a multiple of
+// 4, so every column starts on 16 bytes): a workgroup moves 64 features x
+// kTransRows rows in 64 x 64 tiles through LDS, and keeps the smallest and
+// largest key of each of its features (a NaN key is the largest), merged
+// into kmin / kmax [F] with one atomic per feature.  Loads: 16 threads read
+// one row's 64 values as four-value quads (VEC: 16-byte loads, when the
+// rows are 16-byte aligned; a quad past the last feature reads its valid
+// values one by one); stores: 16 threads write one feature's 64 rows as
+// 16-byte quads.
+template <bool VEC>
 __global__ __launch_bounds__(256) void transpose_keys_kernel(const float* __restrict__ X,
                                                              int64_t n, int32_t F, int64_t xs,
+                                                             int64_t ks,
                                                              uint32_t* __restrict__ keys,
                                                              uint32_t* __restrict__ kmin,
                                                              uint32_t* __restrict__ kmax) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   __shared__ uint32_t t[64][65];
-  __shared__ uint32_t s_mn[4][64], s_mx[4][64];
-  const int f0 = blockIdx.y * 64;
-  const int c = threadIdx.x & 63;
-  const int rq = threadIdx.x >> 6;
-  uint32_t mn = 0xffffffffu, mx = 0u;
-  for (int64_t r0 = (int64_t)blockIdx.x * kTransRows;
-       r0 < n && r0 < (int64_t)(blockIdx.x + 1) * kTransRows; r0 += 64) {
+  __shared__ uint32_t s_mn[16][64], s_mx[16][64];
+  // (row block, feature tile) in the XCD work order, feature tiles of a row
+  // block consecutive: rows are not line-aligned, and the neighbouring tiles
+  // that share a row's lines then read them from the same L2
+  const int nft = (F + 63) / 64;
+  const int64_t n_work = (n + kTransRows - 1) / kTransRows * nft;
+  const int64_t wk = wgbm_xcd_work(blockIdx.x, n_work);
+  if (wk >= n_work) return;  // uniform over the workgroup
+  const int64_t rb = wk / nft;
+  const int f0 = (int)(wk % nft) * 64;
+  const int g = threadIdx.x >> 4;  // load: row group; store: feature group
+  const int qd = threadIdx.x & 15;  // load: feature quad; store: row quad
+  const int fq = f0 + 4 * qd;      // first feature of the load quad
+  const int nvf = F - fq < 4 ? (F - fq > 0 ? F - fq : 0) : 4;  // valid features of the quad
+  uint32_t mn[4], mx[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    mn[c] = 0xffffffffu;
+    mx[c] = 0u;
+  }
+  for (int64_t r0 = rb * kTransRows; r0 < n && r0 < (rb + 1) * kTransRows; r0 += 64) {
     __syncthreads();  // the previous tile has been written out
-    for (int k = rq; k < 64; k += 4) {
-      const int64_t r = r0 + k;
-      uint32_t key = 0u;
-      if (r < n && f0 + c < F) {
-        key = float_to_key(X[r * xs + f0 + c]);
-        mn = key < mn ? key : mn;
-        mx = key > mx ? key : mx;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int rr = g + 16 * k;
+      const int64_t r = r0 + rr;
+      float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      const bool row_ok = r < n;
+      if (row_ok) {
+        const float* src = X + r * xs + fq;
+        if (VEC && nvf == 4) {
+          const f32x4 w = *reinterpret_cast<const f32x4*>(src);
+          v[0] = w.x;
+          v[1] = w.y;
+          v[2] = w.z;
+          v[3] = w.w;
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (c < nvf) v[c] = src[c];
+        }
       }
-      t[k][c] = key;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        uint32_t key = 0u;
+        if (row_ok && c < nvf) {
+          key = float_to_key(v[c]);
+          mn[c] = key < mn[c] ? key : mn[c];
+          mx[c] = key > mx[c] ? key : mx[c];
+        }
+        t[rr][4 * qd + c] = key;
+      }
     }
     __syncthreads();
-    for (int k = rq; k < 64; k += 4) {
-      const int f = f0 + k;
-      const int64_t r = r0 + c;
-      if (f < F && r < n) keys[(int64_t)f * n + r] = t[c][k];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int fl = g + 16 * k;  // feature within the tile
+      const int f = f0 + fl;
+      const int64_t r = r0 + 4 * qd;
+      if (f >= F || r >= n) continue;
+      uint32_t* dst = keys + (int64_t)f * ks + r;
+      if (r + 3 < n) {
+        u32x4 w;
+        w.x = t[4 * qd + 0][fl];
+        w.y = t[4 * qd + 1][fl];
+        w.z = t[4 * qd + 2][fl];
+        w.w = t[4 * qd + 3][fl];
+        *reinterpret_cast<u32x4*>(dst) = w;  // ks and r are multiples of 4
+      } else {
+        for (int c = 0; r + c < n; ++c) dst[c] = t[4 * qd + c][fl];
+      }
     }
   }
-  s_mn[rq][c] = mn;
-  s_mx[rq][c] = mx;
+  // per-feature extremes: thread (g, qd) holds features fq..fq+3 of row group g
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    s_mn[g][4 * qd + c] = mn[c];
+    s_mx[g][4 * qd + c] = mx[c];
+  }
   __syncthreads();
-  if (threadIdx.x < 64 && f0 + c < F) {
-    for (int w = 1; w < 4; ++w) {
-      mn = s_mn[w][c] < mn ? s_mn[w][c] : mn;
-      mx = s_mx[w][c] > mx ? s_mx[w][c] : mx;
+  if (threadIdx.x < 64 && f0 + (int)threadIdx.x < F) {
+    const int c = threadIdx.x;
+    uint32_t a = s_mn[0][c], b = s_mx[0][c];
+    for (int w = 1; w < 16; ++w) {
+      a = s_mn[w][c] < a ? s_mn[w][c] : a;
+      b = s_mx[w][c] > b ? s_mx[w][c] : b;
     }
-    atomicMin(&kmin[f0 + c], mn);
-    atomicMax(&kmax[f0 + c], mx);
+    atomicMin(&kmin[f0 + c], a);
+    atomicMax(&kmax[f0 + c], b);
   }
 }
+template __global__ void transpose_keys_kernel<true>(const float*, int64_t, int32_t, int64_t,
+                                                     int64_t, uint32_t*, uint32_t*, uint32_t*);
+template __global__ void transpose_keys_kernel<false>(const float*, int64_t, int32_t, int64_t,
+                                                      int64_t, uint32_t*, uint32_t*, uint32_t*);
 
 constexpr int kSelThreads = 512;
 constexpr int kSelMaxTargets = 256;   // 2 * 126 ranks at most (num_bins <= 127)
@@ -296,10 +373,15 @@ constexpr int kSelBuckets = 4096;     // value buckets of the first pass
 // stretch the range, infinities) runs the radix selection over the whole
 // column instead; a column holding a NaN gets NaN edges (torch.quantile) and
 // a constant column its value.
+//
+// The two column scans read 16-byte quads of keys (columns start on 16
+// bytes: ks is a multiple of 4), several per thread in flight.
 __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
-    const uint32_t* __restrict__ keys, int64_t n, int32_t F, const float* __restrict__ q,
-    int32_t nq, float* __restrict__ edges, const uint32_t* __restrict__ kmin,
-    const uint32_t* __restrict__ kmax, uint32_t* __restrict__ cbuf, int64_t ccap) {
+    const uint32_t* __restrict__ keys, int64_t n, int64_t ks, int32_t F,
+    const float* __restrict__ q, int32_t nq, float* __restrict__ edges,
+    const uint32_t* __restrict__ kmin, const uint32_t* __restrict__ kmax,
+    uint32_t* __restrict__ cbuf, int64_t ccap) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   __shared__ uint32_t hist[kSelGroup][256];        // 32 KB (also the value buckets)
   __shared__ uint32_t tprefix[kSelMaxTargets];      // known key bits of each target
   __shared__ int64_t trank[kSelMaxTargets];         // rank still to find within the prefix
@@ -314,7 +396,9 @@ __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
   constexpr int nwaves = kSelThreads / 64;
   const int f = blockIdx.x;
   if (f >= F) return;
-  const uint32_t* col = keys + (int64_t)f * n;
+  const uint32_t* col = keys + (int64_t)f * ks;
+  const u32x4* col4 = reinterpret_cast<const u32x4*>(col);
+  const int64_t n4 = n >> 2;  // whole quads; keys [4 * n4, n) are the tail
   uint32_t* cb = cbuf + (int64_t)f * ccap;
   const int nt = 2 * nq;
   const int64_t last = n - 1;
@@ -350,18 +434,25 @@ __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
     for (int i = tid; i < kSelBuckets / 32; i += kSelThreads) marked[i] = 0;
     if (tid == 0) s_cnt = 0;
     __syncthreads();
-    // four independent loads in flight per thread
-    for (int64_t i0 = tid; i0 < n; i0 += 4 * kSelThreads) {
-      uint32_t k[4];
+    // four 16-byte loads in flight per thread
+    for (int64_t i0 = tid; i0 < n4; i0 += 4 * kSelThreads) {
+      u32x4 k[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int64_t i = i0 + u * kSelThreads;
-        k[u] = i < n ? col[i] : 0u;
+        k[u] = i < n4 ? col4[i] : u32x4{0u, 0u, 0u, 0u};
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (i0 + u * kSelThreads < n) atomicAdd(&H[bucket(k[u])], 1u);
+      for (int u = 0; u < 4; ++u) {
+        if (i0 + u * kSelThreads < n4) {
+          atomicAdd(&H[bucket(k[u].x)], 1u);
+          atomicAdd(&H[bucket(k[u].y)], 1u);
+          atomicAdd(&H[bucket(k[u].z)], 1u);
+          atomicAdd(&H[bucket(k[u].w)], 1u);
+        }
+      }
     }
+    for (int64_t i = 4 * n4 + tid; i < n; i += kSelThreads) atomicAdd(&H[bucket(col[i])], 1u);
     __syncthreads();
     // exclusive prefix of the buckets, in place: thread t owns buckets
     // [8t, 8t + 8)
@@ -442,12 +533,9 @@ __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
       // one buffer reservation per wave: a ballot of the lanes that keep
       // their key, lane ranks by mbcnt
       const int lane = tid & 63;
-      for (int64_t i0 = 0; i0 < n; i0 += kSelThreads) {  // same trip count for all
-        const int64_t i = i0 + tid;
-        uint32_t k = 0u;
+      auto keep = [&](uint32_t k, bool valid) {
         bool take = false;
-        if (i < n) {
-          k = col[i];
+        if (valid) {
           const int b = bucket(k);
           take = (marked[b >> 5] >> (b & 31)) & 1u;
         }
@@ -461,6 +549,24 @@ __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
               (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
           if (take) cb[base + rank] = k;  // base + rank < s_tot <= ccap
         }
+      };
+      // two 16-byte loads per thread in flight; the same trip count for all
+      for (int64_t i0 = 0; i0 < n4; i0 += 2 * kSelThreads) {
+        const int64_t ia = i0 + tid, ib = ia + kSelThreads;
+        const u32x4 ka = ia < n4 ? col4[ia] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 kb = ib < n4 ? col4[ib] : u32x4{0u, 0u, 0u, 0u};
+        keep(ka.x, ia < n4);
+        keep(ka.y, ia < n4);
+        keep(ka.z, ia < n4);
+        keep(ka.w, ia < n4);
+        keep(kb.x, ib < n4);
+        keep(kb.y, ib < n4);
+        keep(kb.z, ib < n4);
+        keep(kb.w, ib < n4);
+      }
+      {
+        const int64_t i = 4 * n4 + tid;  // the tail: fewer than 4 keys
+        keep(i < n ? col[i] : 0u, i < n);
       }
       __syncthreads();
       src = cb;

@@ -394,8 +394,11 @@ int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64
   // column-major keys of up to `chunk` features at a time (bounded scratch)
   // (up to 2^30 keys = 4 GiB of scratch: all features of a 1M-row matrix in
   // one launch, so that every CU holds several columns)
-  const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n_feats, (int64_t(1) << 30) / n));
-  uint32_t* keys = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (size_t)(chunk * n), 8);
+  // key columns padded to a multiple of 32 keys (128-byte lines; the
+  // kernels need 16-byte aligned quads)
+  const int64_t ks = (n + 31) / 32 * 32;
+  const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n_feats, (int64_t(1) << 30) / ks));
+  uint32_t* keys = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (size_t)(chunk * ks), 8);
   // per-feature buffer of the keys left after the 16-bit prefix pass (a
   // quarter of the column; a column with more falls back to full scans)
   const int64_t ccap = std::max<int64_t>(1024, n / 4);
@@ -406,11 +409,17 @@ int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64
   for (int64_t f0 = 0; f0 < n_feats; f0 += chunk) {
     const int32_t fc = (int32_t)std::min<int64_t>(chunk, n_feats - f0);
     if (fill_u32(kmin, fc, 0xffffffffu, st) || fill_u32(kmax, fc, 0u, st)) return WGBM_EINVAL;
-    dim3 tg(nblocks(n, kTransRows), nblocks(fc, 64));
-    hipLaunchKernelGGL(transpose_keys_kernel, tg, dim3(256), 0, st, X + f0, n, fc, x_stride, keys,
-                       kmin, kmax);
+    const dim3 tg((unsigned)wgbm_xcd_grid((int64_t)nblocks(n, kTransRows) * nblocks(fc, 64)));
+    // 16-byte row loads when every row of the chunk starts on 16 bytes
+    const bool vec = ((uintptr_t)(X + f0) % 16) == 0 && x_stride % 4 == 0;
+    if (vec)
+      hipLaunchKernelGGL(transpose_keys_kernel<true>, tg, dim3(256), 0, st, X + f0, n, fc,
+                         x_stride, ks, keys, kmin, kmax);
+    else
+      hipLaunchKernelGGL(transpose_keys_kernel<false>, tg, dim3(256), 0, st, X + f0, n, fc,
+                         x_stride, ks, keys, kmin, kmax);
     WGBM_LAUNCH_CHECK();
-    hipLaunchKernelGGL(quantile_select_kernel, dim3(fc), dim3(512), 0, st, keys, n, fc, q, nq,
+    hipLaunchKernelGGL(quantile_select_kernel, dim3(fc), dim3(512), 0, st, keys, n, ks, fc, q, nq,
                        edges + f0 * nq, kmin, kmax, cbuf, ccap);
     WGBM_LAUNCH_CHECK();
   }
@@ -426,11 +435,12 @@ int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride
   if (n == 0) return 0;
   WGBM_REQUIRE(X && codes_rm && (n_edges == 0 || edges), "null pointer");
   const size_t lds = sizeof(float) * 64 * std::max(n_edges, 1);
-  dim3 grid(nblocks(n, kBinTileRows), nblocks(n_feats, kBinTileFeats));
+  const int64_t nft = nblocks(n_feats, kBinTileFeats);
+  const dim3 grid((unsigned)wgbm_xcd_grid((int64_t)nblocks(n, kBinTileRows) * nft));
   hipLaunchKernelGGL(bin_matrix_kernel, grid, dim3(256), lds, S(stream), X, n, n_feats, x_stride,
                      edges, n_edges, codes_rm, codes_stride, codes_cm);
   WGBM_LAUNCH_CHECK();
-  const int64_t covered = (int64_t)grid.y * kBinTileFeats;
+  const int64_t covered = nft * kBinTileFeats;
   if (codes_stride > covered) {
     const int64_t tot = n * (codes_stride - covered);
     hipLaunchKernelGGL(pad_codes_kernel, dim3(nblocks(tot, 256)), dim3(256), 0, S(stream),
@@ -452,11 +462,12 @@ int wgbm_copy_prebinned(const int8_t* X, int64_t n, int32_t n_feats, int64_t x_s
   }
   if (n == 0) return 0;
   WGBM_REQUIRE(X && codes_rm, "null pointer");
-  dim3 grid(nblocks(n, kBinTileRows), nblocks(n_feats, kBinTileFeats));
+  const int64_t nft = nblocks(n_feats, kBinTileFeats);
+  const dim3 grid((unsigned)wgbm_xcd_grid((int64_t)nblocks(n, kBinTileRows) * nft));
   hipLaunchKernelGGL(copy_prebinned_kernel, grid, dim3(256), 0, S(stream), X, n, n_feats,
                      x_stride, codes_rm, codes_stride, codes_cm, num_bins, over_flag);
   WGBM_LAUNCH_CHECK();
-  const int64_t covered = (int64_t)grid.y * kBinTileFeats;
+  const int64_t covered = nft * kBinTileFeats;
   if (codes_stride > covered) {
     const int64_t tot = n * (codes_stride - covered);
     hipLaunchKernelGGL(pad_codes_kernel, dim3(nblocks(tot, 256)), dim3(256), 0, S(stream),

@@ -185,6 +185,22 @@ __device__ __forceinline__ int64_t wgbm_wave_incl_scan_i64(int64_t x) {
   return x;
 }
 
+// Work order that keeps neighbouring work items on one XCD.  The hardware
+// deals consecutive workgroup ids round-robin over the 8 XCDs, each with its
+// own L2; work item w = (id % 8) * per + id / 8 (per = ceil(n_work / 8))
+// gives every XCD a contiguous run of work items, so tiles that share cache
+// lines (the feature tiles of one row block) run on the same L2 at about the
+// same time.  Launch wgbm_xcd_grid(n_work) workgroups; ids whose work item
+// is >= n_work have nothing to do.
+constexpr int kXcds = 8;
+__host__ __device__ inline int64_t wgbm_xcd_grid(int64_t n_work) {
+  return (n_work + kXcds - 1) / kXcds * kXcds;
+}
+__device__ inline int64_t wgbm_xcd_work(int64_t id, int64_t n_work) {
+  const int64_t per = (n_work + kXcds - 1) / kXcds;
+  return (id % kXcds) * per + id / kXcds;
+}
+
 // Order-preserving encoding of a non-negative float's magnitude as uint32
 // (for atomicMax over |r|).  NaN maps above +inf and is reported as an error.
 __device__ inline uint32_t wgbm_abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
