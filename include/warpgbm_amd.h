@@ -236,9 +236,11 @@ typedef struct wgbm_tree_record {
 
 int wgbm_engine_create(wgbm_engine** out, const wgbm_engine_config* cfg);
 /* One boosting round.  target: float32 y [n_rows] (regression) or int32
- * labels [n_rows] (softmax); pred: float32 [n_rows] or [n_rows, K],
- * updated in place; feat_sel: int32 [n_sel] features of this round's trees
- * (colsample_bytree subset, local order). */
+ * labels [n_rows] (softmax); pred: float32 [n_rows] (regression) or
+ * class-major [K, n_rows] (softmax: the scores of class k are row k, so each
+ * class tree's leaf updates stay inside one row), updated in place;
+ * feat_sel: int32 [n_sel] features of this round's trees (colsample_bytree
+ * subset, local order). */
 int wgbm_engine_round(wgbm_engine* eng, const void* target, float* pred, const int32_t* feat_sel,
                       int32_t n_sel, const wgbm_tree_record* rec, void* stream);
 /* Tuning knobs: key 1 = histogram tile rows (0 = automatic); key 2 = codes

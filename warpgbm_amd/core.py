@@ -532,9 +532,12 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         labels = torch.from_numpy(np.asarray(y_encoded).astype(np.int32)).to(dev)
         start_iter = self._trees_trained if (self.warm_start and self._is_fitted) else 0
         init = self._class_prior_logits(np.asarray(y_encoded))
-        scores = torch.from_numpy(np.tile(init, (self.num_samples, 1))).to(dev)
+        # the engine keeps the training scores class-major, [K, n]
+        scores_rm = torch.from_numpy(np.tile(init, (self.num_samples, 1))).to(dev)
         if start_iter > 0:
-            self._predict_codes_into(codes, scores, self.forest[:start_iter])
+            self._predict_codes_into(codes, scores_rm, self.forest[:start_iter])
+        scores = scores_rm.t().contiguous()
+        del scores_rm
         self._setup_eval(X_eval, y_eval, eval_every_n_trees, early_stopping_rounds, eval_metric,
                          classification=True)
         if not hasattr(self, "training_loss") or not self.warm_start or not self._is_fitted:
@@ -568,7 +571,8 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                         D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
                                        rec["leaf"][j], 1, K, self.max_depth, self.learning_rate,
                                        eval_scores)
-                        self._compute_eval_multiclass(i, labels, scores, eval_scores)
+                        self._compute_eval_multiclass(i, labels, scores.t().contiguous(),
+                                                      eval_scores)
                         if self.stop:
                             break
             stream.finish(done)

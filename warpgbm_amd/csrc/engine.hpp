@@ -58,6 +58,16 @@ __global__ void root_setup_kernel(const int32_t* root_order, int64_t n, int32_t 
                                   int32_t* order, int32_t* keyp, float* rpos, int64_t* seg,
                                   int32_t* present, unsigned long long* best, int32_t* agree_max,
                                   const int32_t* shifts, int32_t* node_shift);
+// What the partition needs of a (tree, node) of the level, written by
+// level_finish_kernel: col = the split's code column (-1: the node is a
+// leaf, -2: absent), bin = the split bin, leaf = the leaf value, s63 = the
+// wide leaf-sum shift of the node's tree.  One 16-byte load per position.
+struct alignas(16) NodeRoute {
+  int32_t col;
+  int32_t bin;
+  float leaf;
+  int32_t s63;
+};
 __global__ void level_finish_kernel(int32_t depth, int32_t max_depth, int32_t T, int32_t E,
                                     int32_t B, const int32_t* present,
                                     const unsigned long long* best, int32_t* split_l,
@@ -66,7 +76,8 @@ __global__ void level_finish_kernel(int32_t depth, int32_t max_depth, int32_t T,
                                     const int64_t* tot_ql, const int64_t* tot_c,
                                     const int32_t* shifts, int32_t s63_add,
                                     float* leaf_val, TreeRecord rec,
-                                    unsigned long long* best_next, int32_t* agree_max_next);
+                                    unsigned long long* best_next, int32_t* agree_max_next,
+                                    NodeRoute* nroute);
 // partition over position blocks (engine_kernels.hip)
 constexpr int kPartBlock = 1024;   // positions per block
 constexpr int kPartThreads = 256;
@@ -128,6 +139,7 @@ struct RouteArgs {
   const int32_t* shifts;  // per tree
   int32_t s63_add;        // wide leaf-sum shift = shifts[t] + s63_add
   const float* leaf_val;
+  const NodeRoute* nroute;  // modes 1, 2: the level's nodes (level_finish_kernel)
   float lr;
   float* pred;
   int64_t pstride, pcol;

@@ -78,6 +78,7 @@ struct Engine {
   int32_t* bdir = nullptr;      // [tn][W][n_sel*(B-1)] era-block direction sums
   int32_t* split_l = nullptr;
   int32_t* split_b = nullptr;
+  NodeRoute* nroute = nullptr;  // [T*nodes] the level's route records
   float* split_gain = nullptr;
   float* leaf_val = nullptr;
   unsigned long long* best = nullptr;  // packed split picks, two depths (parity)
@@ -187,7 +188,7 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     // the chosen split's per-era gains; the pair codes; 64 MiB of slack
     const int64_t keys = e->n_keys_max, tn = T * nodes_max;
     const int64_t pcodes = (e->des_direct && B <= 7) ? N * pair_stride((int32_t)F) : 0;
-    const int64_t need = e->nc_max * per_node + T * N * 29 + keys * 100 + tn * 60 + tn * E * 4 +
+    const int64_t need = e->nc_max * per_node + T * N * 29 + keys * 100 + tn * 76 + tn * E * 4 +
                          pcodes + ((int64_t)64 << 20);
     size_t free_b = 0, total_b = 0;
     if (hipMemGetInfo(&free_b, &total_b) == hipSuccess && (size_t)need > free_b) {
@@ -260,6 +261,7 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->split_b, T * nodes_max);
   E_ALLOC(e->split_gain, T * nodes_max * E);
   E_ALLOC(e->leaf_val, T * nodes_max);
+  E_ALLOC(e->nroute, T * nodes_max);
   E_ALLOC(e->best, 2 * T * nodes_max);
   e->pick_stride = T * nodes_max;
   *out = e;
@@ -411,8 +413,9 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   ra.leaf_val = e->leaf_val;
   ra.lr = c.learning_rate;
   ra.pred = pred;
-  ra.pstride = c.objective == 0 ? 1 : T;
-  ra.pcol = c.objective == 0 ? 0 : 1;
+  // scores: [N] (one tree per round) or class-major [K][N] (tree t = class t)
+  ra.pstride = 1;
+  ra.pcol = c.objective == 0 ? 0 : N;
   ra.dirbit = e->dirbit;
   ra.ps = e->ps;
   {
@@ -603,7 +606,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                        e->split_l, e->split_b, e->split_gain, feat_sel, e->totqh[cur],
                        e->totql[cur], e->totc[cur], e->shifts, 62 - e->qbits, e->leaf_val, rec,
                        e->best + (hcur ^ 1) * e->pick_stride,
-                       e->agree_max ? e->agree_max + (hcur ^ 1) * e->pick_stride : nullptr);
+                       e->agree_max ? e->agree_max + (hcur ^ 1) * e->pick_stride : nullptr,
+                       e->nroute);
     WGBM_LAUNCH_CHECK();
     // ---- partition (or final leaf update): route every position, then the
     // next level's segments and the stable scatter
@@ -618,6 +622,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     rl.present = e->present[cur];
     rl.split_l = e->split_l;
     rl.split_b = e->split_b;
+    rl.nroute = e->nroute;
     // the children's max|r| decides their histogram shifts; children at the
     // last depth are leaves and need none
     rl.want_max = d + 1 < D ? 1 : 0;

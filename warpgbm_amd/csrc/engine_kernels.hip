@@ -37,7 +37,7 @@ __global__ void residual_regression_kernel(const float* __restrict__ y,
 // softmax: p = softmax(F[i, :]); residual_k = -(p_k - onehot_k)
 // (warpgbm/core.py:186-214 and :782; metrics.py:12-15).
 // partial[k * gridDim.x + block] = max_i |residual_k|
-__global__ void residual_softmax_kernel(const float* __restrict__ logits,
+__global__ void residual_softmax_kernel(const float* __restrict__ logits /* [K][n] */,
                                         const int32_t* __restrict__ label, int64_t n, int32_t K,
                                         float* __restrict__ r /* [K][n] */,
                                         uint32_t* __restrict__ partial) {
@@ -46,15 +46,16 @@ __global__ void residual_softmax_kernel(const float* __restrict__ logits,
     uint32_t m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-      const float* x = logits + i * K;
+      // the row's K logits, class-major (one coalesced read per class)
+      const float* x = logits + i;
       const int lab = label[i];
       float mx = x[0];
-      for (int k = 1; k < K; ++k) mx = x[k] > mx ? x[k] : mx;
+      for (int k = 1; k < K; ++k) mx = x[k * n] > mx ? x[k * n] : mx;
       float s = 0.0f;
-      for (int k = 0; k < K; ++k) s = s + wgbm_expf(x[k] - mx);
+      for (int k = 0; k < K; ++k) s = s + wgbm_expf(x[k * n] - mx);
       for (int kk = 0; kk < 8 && k0 + kk < K; ++kk) {
         const int k = k0 + kk;
-        const float p = wgbm_expf(x[k] - mx) / s;
+        const float p = wgbm_expf(x[k * n] - mx) / s;
         const float g = p - (k == lab ? 1.0f : 0.0f);
         const float v = -g;
         r[(int64_t)k * n + i] = v;
@@ -127,7 +128,8 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
     const int64_t* __restrict__ tot_qh, const int64_t* __restrict__ tot_ql,
     const int64_t* __restrict__ tot_c, const int32_t* __restrict__ shifts, int32_t s63_add,
     float* __restrict__ leaf_val, TreeRecord rec,
-    unsigned long long* __restrict__ best_next, int32_t* __restrict__ agree_max_next) {
+    unsigned long long* __restrict__ best_next, int32_t* __restrict__ agree_max_next,
+    NodeRoute* __restrict__ nroute) {
   // one wave per (tree, node); the eras are spread over the lanes.  The wave
   // also clears the next depth's split-pick words of its two children.  With
   // best != null (one era) the packed pick of the split search is decoded here.
@@ -168,6 +170,7 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
       rec.bin[h] = -1;
       rec.leaf[h] = 0.0f;
       rec.count[h] = 0;
+      nroute[tn] = NodeRoute{-2, -1, 0.0f, 0};
     }
     return;
   }
@@ -184,19 +187,23 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
   }
   if (lane == 0) {
     rec.count[h] = sc;
+    const int32_t s63 = shifts[t] + s63_add;
     if (l >= 0) {
-      rec.feat[h] = feat_sel[l];
+      const int32_t col = feat_sel[l];
+      rec.feat[h] = col;
       rec.bin[h] = b;
       rec.leaf[h] = 0.0f;
+      nroute[tn] = NodeRoute{col, b, 0.0f, s63};
     } else {
       const int64_t hi = sqh + (sql >> 32);
       const int64_t lo = sql & 0xffffffffll;
       const double sum = (double)hi * 4294967296.0 + (double)lo;
-      const float v = (float)(ldexp(sum, -(shifts[t] + s63_add)) / (double)sc);
+      const float v = (float)(ldexp(sum, -s63) / (double)sc);
       leaf_val[tn] = v;
       rec.feat[h] = -1;
       rec.bin[h] = -1;
       rec.leaf[h] = v;
+      nroute[tn] = NodeRoute{-1, -1, v, s63};
     }
   }
   if (l >= 0) {
@@ -316,15 +323,53 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   int64_t* s_ql = s_dyn + kPartBlock;
   uint32_t* s_ml = (uint32_t*)(s_dyn + 2 * kPartBlock);
   uint32_t* s_mr = s_ml + kPartBlock;
-  __shared__ int s_k[2];
+  __shared__ int s_wlast[kPartThreads / 64];  // key of each wave's last position
+  __shared__ int s_khi;                        // key of the block's last position
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
   const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
   const int64_t p1 = p0 + kPartBlock < a.n_pos ? p0 + kPartBlock : a.n_pos;
   const bool sums = a.mode != 2;
   const bool maxes = a.mode == 1 && a.want_max;
-  if (tid == 0) {
-    s_k[0] = a.keyp[p0];
-    s_k[1] = a.keyp[p1 - 1];
+  // Thread t owns the PJ consecutive positions pl0 .. pl0 + PJ - 1 of the
+  // block (16-byte loads of keys, rows and residuals; rows of one segment
+  // are usually combined in registers before the wave reduction).  Issued
+  // before the LDS is cleared, so that their latency overlaps it.  A position
+  // past the end takes the block's last key (it adds nothing).
+  constexpr int PJ = kPartBlock / kPartThreads;
+  static_assert(PJ == 4, "four positions per thread");
+  typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int pl0 = tid * PJ;
+  const int64_t pb = p0 + pl0;
+  int key[PJ], slot[PJ], nslot[PJ], tnv[PJ], lv[PJ];
+  int32_t rowv[PJ];
+  float rv[PJ];
+  bool ok[PJ];
+  const bool vec = pb + PJ <= p1 &&
+                   (((uintptr_t)a.keyp | (uintptr_t)a.order | (uintptr_t)a.rpos) & 15u) == 0 &&
+                   ((uintptr_t)a.dirbit & 3u) == 0;
+  if (vec) {
+    const i32x4 k4 = *reinterpret_cast<const i32x4*>(a.keyp + pb);
+    const i32x4 o4 = *reinterpret_cast<const i32x4*>(a.order + pb);
+    f32x4 r4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (sums) r4 = *reinterpret_cast<const f32x4*>(a.rpos + pb);
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      ok[j] = true;
+      key[j] = k4[j];
+      rowv[j] = o4[j];
+      rv[j] = r4[j];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      const int64_t p = pb + j;
+      ok[j] = p < p1;
+      key[j] = a.keyp[ok[j] ? p : p1 - 1];
+      rowv[j] = ok[j] ? a.order[p] : 0;
+      rv[j] = ok[j] && sums ? a.rpos[p] : 0.0f;
+    }
   }
   if (sums) {
     for (int i = tid; i < kPartBlock; i += kPartThreads) {
@@ -335,35 +380,33 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
         s_mr[i] = 0u;
       }
     }
+    if (lane == 63) s_wlast[tid >> 6] = key[PJ - 1];
+#pragma unroll
+    for (int j = 0; j < PJ; ++j)
+      if (pb + j == p1 - 1) s_khi = key[j];
   }
   __syncthreads();
-  const int khi = s_k[1];
-  // the block's positions, four per thread (strided: coalesced), in phases so
-  // that the loads of the four positions are in flight together
-  constexpr int PJ = kPartBlock / kPartThreads;
-  int key[PJ], slot[PJ], nslot[PJ], tnv[PJ], lv[PJ];
-  int32_t rowv[PJ];
-  bool ok[PJ];
+  // Everything a position needs of its segment and node, in one round of
+  // independent loads: the segment's bounds, the node's bounds (several
+  // eras) and its route record.  col: -2 the row stays (node absent), -1
+  // leaf update, >= 0 the split's code column.
+  bool seg_in[PJ], node_in[PJ];  // the segment / node lies inside the block
+  NodeRoute nr[PJ];
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
-    const int64_t p = p0 + j * kPartThreads + tid;
-    ok[j] = p < p1;
-    key[j] = ok[j] ? a.keyp[p] : s_k[0];
-    rowv[j] = ok[j] ? a.order[p] : 0;
-  }
-#pragma unroll
-  for (int j = 0; j < PJ; ++j) {
-    const int64_t sk = a.seg[key[j]];
+    const int64_t sk = a.seg[key[j]], se = a.seg[key[j] + 1];
     slot[j] = (int)((sk > p0 ? sk : p0) - p0);
+    seg_in[j] = sk >= p0 && se <= p1;
     tnv[j] = key[j] / a.E;
-    nslot[j] = slot[j];  // one era: the node is the segment
+    int64_t nb = sk, ne = se;  // one era: the node is the segment
     if (maxes && a.E > 1) {
-      const int64_t sn = a.seg[(int64_t)tnv[j] * a.E];
-      nslot[j] = (int)((sn > p0 ? sn : p0) - p0);
+      nb = a.seg[(int64_t)tnv[j] * a.E];
+      ne = a.seg[(int64_t)(tnv[j] + 1) * a.E];
     }
-    // -2: the row stays (node absent), -1: leaf update, >= 0: split feature
-    lv[j] = -2;
-    if (ok[j] && a.present[tnv[j]]) lv[j] = a.mode == 1 ? a.split_l[tnv[j]] : -1;
+    nslot[j] = (int)((nb > p0 ? nb : p0) - p0);
+    node_in[j] = nb >= p0 && ne <= p1;
+    if (a.mode != 0) nr[j] = a.nroute[tnv[j]];
+    lv[j] = (ok[j] && a.mode != 0) ? nr[j].col : -2;
   }
   // Sums go to the LDS slot of the row's segment.  A wave whose rows all lie
   // in one segment (the common case for large segments) reduces them across
@@ -376,7 +419,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     if (__ballot(act && sl != s0) == 0ull) {
       qn = wgbm_wave_reduce_add_i64(act ? qn : (int64_t)0);
       ql = wgbm_wave_reduce_add_i64(act ? ql : (int64_t)0);
-      if ((tid & 63) == 0) {
+      if (lane == 0) {
         if (qn) atomicAdd((unsigned long long*)&s_qn[s0], (unsigned long long)qn);
         if (ql) atomicAdd((unsigned long long*)&s_ql[s0], (unsigned long long)ql);
       }
@@ -394,7 +437,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     if (__ballot(act && sl != s0) == 0ull) {
       ml = wgbm_wave_reduce_max_u32(act ? ml : 0u);
       mr = wgbm_wave_reduce_max_u32(act ? mr : 0u);
-      if ((tid & 63) == 0) {
+      if (lane == 0) {
         if (ml) atomicMax(&s_ml[s0], ml);
         if (mr) atomicMax(&s_mr[s0], mr);
       }
@@ -403,49 +446,101 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
       if (mr) atomicMax(&s_mr[sl], mr);
     }
   };
-  // one row's wide quantisation, split into (hi word * 2^11 + 1, lo word)
-  auto q63_words = [&](float r, int t, int64_t& qn, int64_t& ql) {
-    const int64_t q = (int64_t)rintf(ldexpf(r, a.shifts[t] + a.s63_add));
+  // one row's wide quantisation at shift s63, split into (hi word * 2^11 +
+  // 1, lo word)
+  auto q63_words = [&](float r, int s63, int64_t& qn, int64_t& ql) {
+    const int64_t q = (int64_t)rintf(ldexpf(r, s63));
     qn = (q >> 32) * 2048 + 1;
     ql = q & 0xffffffffll;
   };
-  float rv[PJ];
+  // the thread's positions lie in one segment (then also in one node): their
+  // sums and maxima are combined here and reduced once per wave, when every
+  // thread of the wave can do so
+  bool one = true;
 #pragma unroll
-  for (int j = 0; j < PJ; ++j)
-    rv[j] = ok[j] && sums ? a.rpos[p0 + j * kPartThreads + tid] : 0.0f;
+  for (int j = 1; j < PJ; ++j) one = one && key[j] == key[0];
+  const bool wave_one = __ballot(!one) == 0ull;
+  uint8_t dirs[PJ];
+  int s63v[PJ];  // the wide shift of each position's tree
   if (a.mode == 0) {
 #pragma unroll
     for (int j = 0; j < PJ; ++j) {
-      const int t = tnv[j] / a.nodes;
-      int64_t qn = 0, ql = 0;
-      if (ok[j]) q63_words(rv[j], t, qn, ql);
-      add_slot(slot[j], ok[j], qn, ql);
+      s63v[j] = a.shifts[tnv[j] / a.nodes] + a.s63_add;
+      dirs[j] = ok[j] ? 0 : 2;
     }
   } else {
     int cv[PJ];
 #pragma unroll
     for (int j = 0; j < PJ; ++j)
-      cv[j] = lv[j] >= 0 ? (int)a.codes_cm[(int64_t)a.feat_sel[lv[j]] * a.n + rowv[j]] : 0;
+      cv[j] = lv[j] >= 0 ? (int)a.codes_cm[(int64_t)lv[j] * a.n + rowv[j]] : 0;
 #pragma unroll
     for (int j = 0; j < PJ; ++j) {
-      const int tn = tnv[j];
-      const int t = tn / a.nodes;
+      const int t = tnv[j] / a.nodes;
       uint8_t dir = 2;  // stays in place
-      int64_t qn = 0, ql = 0;
       if (lv[j] == -1) {
         // the node is a leaf: add lr * leaf to its rows' predictions
         float* pc = a.pred + (int64_t)t * a.pcol + (int64_t)rowv[j] * a.pstride;
-        *pc = *pc + a.lr * a.leaf_val[tn];
+        *pc = *pc + a.lr * nr[j].leaf;
       } else if (lv[j] >= 0) {
-        dir = cv[j] > a.split_b[tn] ? 1 : 0;
-        if (dir == 0) q63_words(rv[j], t, qn, ql);
+        dir = cv[j] > nr[j].bin ? 1 : 0;
       }
-      if (sums) add_slot(slot[j], dir == 0, qn, ql);
-      if (maxes) {
+      dirs[j] = dir;
+      s63v[j] = nr[j].s63;
+    }
+  }
+  if (sums) {
+    if (wave_one) {
+      int64_t qn = 0, ql = 0;
+      bool act = false;
+#pragma unroll
+      for (int j = 0; j < PJ; ++j) {
+        if (dirs[j] == 0) {
+          int64_t n1, l1;
+          q63_words(rv[j], s63v[j], n1, l1);
+          qn += n1;
+          ql += l1;
+          act = true;
+        }
+      }
+      add_slot(slot[0], act, qn, ql);
+    } else {
+#pragma unroll
+      for (int j = 0; j < PJ; ++j) {
+        int64_t n1 = 0, l1 = 0;
+        if (dirs[j] == 0) q63_words(rv[j], s63v[j], n1, l1);
+        add_slot(slot[j], dirs[j] == 0, n1, l1);
+      }
+    }
+  }
+  if (maxes) {
+    if (wave_one) {
+      uint32_t ml = 0u, mr = 0u;
+      bool act = false;
+#pragma unroll
+      for (int j = 0; j < PJ; ++j) {
         const uint32_t m = wgbm_abs_bits(rv[j]);
-        max_slot(nslot[j], dir != 2, dir == 0 ? m : 0u, dir == 1 ? m : 0u);
+        if (dirs[j] == 0) ml = m > ml ? m : ml;
+        if (dirs[j] == 1) mr = m > mr ? m : mr;
+        act = act || dirs[j] != 2;
       }
-      if (ok[j] && sums) a.dirbit[p0 + j * kPartThreads + tid] = dir;
+      max_slot(nslot[0], act, ml, mr);
+    } else {
+#pragma unroll
+      for (int j = 0; j < PJ; ++j) {
+        const uint32_t m = wgbm_abs_bits(rv[j]);
+        max_slot(nslot[j], dirs[j] != 2, dirs[j] == 0 ? m : 0u, dirs[j] == 1 ? m : 0u);
+      }
+    }
+  }
+  if (a.mode != 0 && sums) {
+    if (vec) {
+      const uint32_t w = (uint32_t)dirs[0] | ((uint32_t)dirs[1] << 8) |
+                         ((uint32_t)dirs[2] << 16) | ((uint32_t)dirs[3] << 24);
+      *reinterpret_cast<uint32_t*>(a.dirbit + pb) = w;  // pb is a multiple of 4
+    } else {
+#pragma unroll
+      for (int j = 0; j < PJ; ++j)
+        if (ok[j]) a.dirbit[pb + j] = dirs[j];
     }
   }
   if (!sums) return;  // uniform over the block
@@ -455,12 +550,20 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     n = (int32_t)(qn & 2047);
     qh = qn >> 11;
   };
-  for (int i = tid; i < (int)(p1 - p0); i += kPartThreads) {
-    // slot i opens a segment when its position's key differs from the one
-    // before it (block boundaries: the first slot always does)
-    const int k = a.keyp[p0 + i];
-    if (i > 0 && a.keyp[p0 + i - 1] == k) continue;
-    if (a.seg[k] >= p0 && a.seg[k + 1] <= p1) {
+  // the key of the position before the thread's first: the previous lane's
+  // last (lane 0: the previous wave's last; the block's first position has
+  // none)
+  int prev = __shfl_up(key[PJ - 1], 1, 64);
+  if (lane == 0) prev = tid > 0 ? s_wlast[(tid >> 6) - 1] : -1;
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    // position pl0 + j opens a segment when its key differs from the one
+    // before it (the block's first position always does)
+    const int i = pl0 + j;
+    const int k = key[j];
+    const int kp = j == 0 ? prev : key[j - 1];
+    if (!ok[j] || (i > 0 && kp == k)) continue;
+    if (seg_in[j]) {
       int64_t qh;
       int32_t n;
       unpack(s_qn[i], qh, n);
@@ -470,16 +573,15 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     }
     if (maxes) {
       // a node inside the block: its maxima are complete here
-      const int tn = k / a.E;
-      const int64_t n0 = a.seg[(int64_t)tn * a.E], n1 = a.seg[(int64_t)(tn + 1) * a.E];
-      if (n0 >= p0 && n1 <= p1 && n0 - p0 == i) {
-        a.ps.own_ml[tn] = s_ml[i];
-        a.ps.own_mr[tn] = s_mr[i];
+      if (node_in[j] && nslot[j] == i) {
+        a.ps.own_ml[tnv[j]] = s_ml[i];
+        a.ps.own_mr[tnv[j]] = s_mr[i];
       }
     }
   }
   if (tid == 0) {
     // the first and last segments of the block: their sums here
+    const int khi = s_khi;
     const int64_t sl = a.seg[khi];
     const int ls = (int)((sl > p0 ? sl : p0) - p0);
     int64_t qh;
