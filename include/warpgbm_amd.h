@@ -117,7 +117,8 @@ int wgbm_histogram_segments(const int8_t* codes, int64_t n_rows, int64_t stride,
  * is a fixed device array of WGBM_NOALLOC_SCRATCH_BYTES that every GPU the
  * library runs on holds until the process ends.  A call needing more (about
  * 4 bytes per row of a row list plus 256 KiB per histogram tile of 1000
- * features at 32 bins; the 1M x 1000 root + 16-node calls need ~25 MiB)
+ * features at 32 bins; the 1M x 1000 root and 16-node calls need 32 and
+ * 40 MiB)
  * returns WGBM_EINVAL with the sizes in wgbm_last_error().  Calls that
  * overlap on one GPU (other streams, other threads) share the array and
  * race: serialise them. */
