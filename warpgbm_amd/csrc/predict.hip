@@ -137,6 +137,10 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
     acc[m] = (k < K && r < nr) ? out[(row0 + r) * K + k] : 0.0f;
   }
   const int T = n_rounds * K;
+  const int G = kPredThreads / RB;  // RB <= 256: G >= 4
+  const bool walker = tid < G * RB;
+  const int wr = walker ? tid % RB : 0;
+  const int wt0 = walker ? tid / RB : 0;
   for (int t0 = 0; t0 < T; t0 += TC) {
     const int tc = T - t0 < TC ? T - t0 : TC;
     __syncthreads();  // rows staged / previous chunk's vals consumed
@@ -147,38 +151,40 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
       leaves_s[i] = leaf[g];
     }
     __syncthreads();
-    // walks: pair p = (row p % RB, tree p / RB) of the chunk; each thread
-    // advances two walks (p and p + kPredThreads) step by step, so the LDS
-    // reads of one walk overlap those of the other
-    for (int p0 = tid; p0 < RB * tc; p0 += 2 * kPredThreads) {
-      int r[2], tl[2], h[2];
-      bool on[2];
-      uint32_t w[2];
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int p = p0 + k * kPredThreads;
-        r[k] = p % RB;
-        tl[k] = p / RB;
-        on[k] = p < RB * tc && r[k] < nr;
-        h[k] = 0;
-        w[k] = on[k] ? nodes_s[tl[k] * H] : kPredLeaf;
-      }
-      for (int d = 0; d < max_depth; ++d) {
-        if (w[0] == kPredLeaf && w[1] == kPredLeaf) break;
+    // walks: thread w < G * RB owns row wr = w % RB and the chunk's trees
+    // wt0, wt0 + G, ... (G = threads / RB row groups, no division per walk),
+    // two in lock-step so that the LDS reads of one overlap those of the
+    // other; max_depth branch-free steps (a walk at a leaf reloads its own
+    // node word and keeps its index)
+    if (walker) {
+      const bool row_on = wr < nr;
+      const uint8_t* row = rows_s + wr * Sp;
+      for (int j0 = wt0; j0 < tc; j0 += 2 * G) {
+        int tl[2], h[2];
+        bool on[2];
+        uint32_t w[2];
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-          if (w[k] == kPredLeaf) continue;
-          const uint32_t f = w[k] >> 8;
-          const uint8_t* row = rows_s + r[k] * Sp;
-          const int c = (int)row[f < (uint32_t)S ? f : (uint32_t)S - 1];  // stays in the row
-          const int b = (int)(w[k] & 0xffu);
-          h[k] = 2 * h[k] + ((c <= b || c == num_bins) ? 1 : 2);
-          w[k] = nodes_s[tl[k] * H + h[k]];
+          on[k] = row_on && j0 + k * G < tc;
+          tl[k] = on[k] ? j0 + k * G : 0;  // an idle walk reads tree 0 and stores nothing
+          h[k] = 0;
+          w[k] = on[k] ? nodes_s[tl[k] * H] : kPredLeaf;
         }
-      }
+        for (int d = 0; d < max_depth; ++d) {
 #pragma unroll
-      for (int k = 0; k < 2; ++k)
-        if (on[k]) vals_s[r[k] * (TC + 1) + tl[k]] = lr * leaves_s[tl[k] * H + h[k]];
+          for (int k = 0; k < 2; ++k) {
+            const uint32_t f = w[k] >> 8;
+            const int c = (int)row[f < (uint32_t)S ? f : (uint32_t)S - 1];  // stays in the row
+            const int b = (int)(w[k] & 0xffu);
+            const bool leaf = w[k] == kPredLeaf;
+            h[k] = leaf ? h[k] : 2 * h[k] + ((c <= b || c == num_bins) ? 1 : 2);
+            w[k] = nodes_s[tl[k] * H + h[k]];
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+          if (on[k]) vals_s[wr * (TC + 1) + tl[k]] = lr * leaves_s[tl[k] * H + h[k]];
+      }
     }
     __syncthreads();
     // ordered sums: trees t0 + j of class k are j = k, k + K, ... (t0 % K == 0)
@@ -290,6 +296,15 @@ __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
       *o = a;
     }
   };
+  // walkers (waves 1..15): thread w owns row wr = w % RB of every block and
+  // the trees wt0, wt0 + G, ... (G = walkers / RB row groups), so no walk
+  // divides; the kWalkers - G * RB threads left over idle
+  constexpr int kWalkers = kResThreads - 64;
+  const int G = kWalkers / RB;  // RB <= 256: G >= 3
+  const int wid = tid - 64;
+  const bool walker = wid >= 0 && wid < G * RB;
+  const int wr = walker ? wid % RB : 0;
+  const int wt0 = walker ? wid / RB : 0;
   int64_t b = blockIdx.x;
   if (b < nblk) prefetch(b);
   int64_t prev = -1;
@@ -300,43 +315,39 @@ __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
     float* vt = vals_s + (it & 1) * RB * TV;
     if (tid < 64) {
       if (prev >= 0) sums(prev, vals_s + ((it & 1) ^ 1) * RB * TV);
-    } else {
+    } else if (walker) {
       const int64_t row0 = b * RB;
       const int nr = (int)(n - row0 < RB ? n - row0 : RB);
-      const int np = RB * T;
-      constexpr int kWalkers = kResThreads - 64;
-      for (int p0 = tid - 64; p0 < np; p0 += kResWalks * kWalkers) {
-        int r[kResWalks], tl[kResWalks], h[kResWalks];
+      const bool row_on = wr < nr;
+      const uint8_t* row = rows_s + wr * Sp;
+      float* vrow = vt + wr * TV;
+      for (int t0 = wt0; t0 < T; t0 += kResWalks * G) {
+        int tl[kResWalks], h[kResWalks];
         bool on[kResWalks];
         uint32_t w[kResWalks];
 #pragma unroll
         for (int k = 0; k < kResWalks; ++k) {
-          const int p = p0 + k * kWalkers;
-          r[k] = p % RB;
-          tl[k] = p / RB;
-          on[k] = p < np && r[k] < nr;
+          on[k] = row_on && t0 + k * G < T;
+          tl[k] = on[k] ? t0 + k * G : 0;  // an idle walk reads tree 0 and stores nothing
           h[k] = 0;
           w[k] = on[k] ? nodes_s[tl[k] * H] : kPredLeaf;
         }
+        // max_depth steps, branch-free: a walk at a leaf reloads its own
+        // node word (kPredLeaf) and keeps its index
         for (int d = 0; d < max_depth; ++d) {
-          bool any = false;
-#pragma unroll
-          for (int k = 0; k < kResWalks; ++k) any = any || w[k] != kPredLeaf;
-          if (!any) break;
 #pragma unroll
           for (int k = 0; k < kResWalks; ++k) {
-            if (w[k] == kPredLeaf) continue;
             const uint32_t f = w[k] >> 8;
-            const uint8_t* row = rows_s + r[k] * Sp;
             const int c = (int)row[f < (uint32_t)S ? f : (uint32_t)S - 1];  // stays in the row
             const int bb = (int)(w[k] & 0xffu);
-            h[k] = 2 * h[k] + ((c <= bb || c == num_bins) ? 1 : 2);
+            const bool leaf = w[k] == kPredLeaf;
+            h[k] = leaf ? h[k] : 2 * h[k] + ((c <= bb || c == num_bins) ? 1 : 2);
             w[k] = nodes_s[tl[k] * H + h[k]];
           }
         }
 #pragma unroll
         for (int k = 0; k < kResWalks; ++k)
-          if (on[k]) vt[r[k] * TV + tl[k]] = lr * leaves_s[tl[k] * H + h[k]];
+          if (on[k]) vrow[tl[k]] = lr * leaves_s[tl[k] * H + h[k]];
       }
     }
     prev = b;
