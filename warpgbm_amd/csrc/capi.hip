@@ -493,7 +493,22 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
   int dev = 0, n_cu = 0;
   WGBM_CHECK(hipGetDevice(&dev));
   WGBM_CHECK(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
-  if (predict_resident_plan(codes_stride, K, H, n_rounds, &RB, &lds)) {
+  const bool resident = predict_resident_plan(codes_stride, K, H, n_rounds, &RB, &lds) != 0;
+  const bool rows = !resident && predict_rows_plan(codes_stride, K, H, n_rounds, &RB, &TC, &lds);
+  uint32_t* cnode = nullptr;
+  float* cleaf = nullptr;
+  if (resident || rows) {
+    // the complete-tree tables the LDS predictors walk (H words per tree)
+    const int64_t T = (int64_t)n_rounds * K;
+    cnode = (uint32_t*)scratch_get(S(stream), sizeof(uint32_t) * (size_t)(T * H), 13);
+    WGBM_REQUIRE(cnode, "scratch allocation failed");
+    cleaf = reinterpret_cast<float*>(cnode + T * ((H - 1) / 2));
+    const int64_t work = T * H;
+    hipLaunchKernelGGL(complete_tables_kernel, dim3(nblocks(work, 256)), dim3(256), 0,
+                       S(stream), feat, bin, leaf, T, max_depth, codes_stride, cnode, cleaf);
+    WGBM_LAUNCH_CHECK();
+  }
+  if (resident) {
     static bool attr_r = false;
     if (!attr_r) {
       WGBM_CHECK(hipFuncSetAttribute((const void*)predict_resident_kernel,
@@ -503,9 +518,9 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
     // one persistent workgroup per CU (fewer when there are fewer blocks)
     const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(n_cu, nblocks(n, RB)));
     hipLaunchKernelGGL(predict_resident_kernel, dim3((unsigned)grid), dim3(1024), lds, S(stream),
-                       codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds * K, K, H,
-                       max_depth, learning_rate, RB, out);
-  } else if (predict_rows_plan(codes_stride, K, H, n_rounds, &RB, &TC, &lds)) {
+                       codes, n, codes_stride, num_bins, (const uint32_t*)cnode,
+                       (const float*)cleaf, n_rounds * K, K, max_depth, learning_rate, RB, out);
+  } else if (rows) {
     static bool attr = false;
     if (!attr) {
       WGBM_CHECK(hipFuncSetAttribute((const void*)predict_rows_kernel,
@@ -513,8 +528,8 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
       attr = true;
     }
     hipLaunchKernelGGL(predict_rows_kernel, dim3(nblocks(n, RB)), dim3(1024), lds, S(stream),
-                       codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds, K, H,
-                       max_depth, learning_rate, RB, TC, out);
+                       codes, n, codes_stride, num_bins, (const uint32_t*)cnode,
+                       (const float*)cleaf, n_rounds, K, max_depth, learning_rate, RB, TC, out);
   } else {
     hipLaunchKernelGGL(predict_heap_kernel, dim3(nblocks(n * K, 256)), dim3(256), 0, S(stream),
                        codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds, K, H,

@@ -82,33 +82,78 @@ __global__ void predict_heap_kernel(const int8_t* __restrict__ codes, int64_t n,
   out[gid] = acc;
 }
 
+// Complete-tree tables for the LDS predictors.  Per tree: (2^D - 1) node
+// words for the levels above the last, feature << 8 | bin for a split whose
+// ancestors are all splits, else (a leaf, an absent node, or any position
+// under one) the always-left word 255 (every code byte is <= 255); and 2^D
+// last-level values, slot s = the leaf value of the first node on the path
+// from the root to heap node 2^D - 1 + s that is not a split (or of that node
+// itself).  A walk then takes exactly D steps with no leaf test and reaches
+// the value the heap walk stops at.  Features are clamped into the row
+// (S - 1), as the walkers clamp them.
+__global__ void complete_tables_kernel(const int32_t* __restrict__ feat,
+                                       const int32_t* __restrict__ bin,
+                                       const float* __restrict__ leaf, int64_t T, int32_t D,
+                                       int64_t S, uint32_t* __restrict__ cnode,
+                                       float* __restrict__ cleaf) {
+  const int Hi = (1 << D) - 1, L = 1 << D, H = 2 * L - 1;
+  const int64_t per = (int64_t)Hi + L;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= T * per) return;
+  const int64_t t = gid / per;
+  const int j = (int)(gid - t * per);
+  const int32_t* ft = feat + t * H;
+  if (j < Hi) {
+    const int dj = 31 - __builtin_clz((unsigned)(j + 1));  // depth of node j
+    bool split = true;
+    for (int k = 0; k <= dj && split; ++k) split = ft[((j + 1) >> (dj - k)) - 1] >= 0;
+    uint32_t w = 255u;
+    if (split) {
+      const int64_t f = ft[j] < S ? ft[j] : S - 1;
+      w = ((uint32_t)f << 8) | ((uint32_t)bin[t * H + j] & 0xffu);
+    }
+    cnode[t * Hi + j] = w;
+  } else {
+    const int sl = j - Hi;
+    const int h = Hi + sl;  // heap node at depth D
+    int a = h;
+    for (int k = 0; k < D; ++k) {
+      const int ak = ((h + 1) >> (D - k)) - 1;
+      if (ft[ak] < 0) {
+        a = ak;
+        break;
+      }
+    }
+    cleaf[t * L + sl] = leaf[t * H + a];
+  }
+}
+
 // Row-block inference (same results as predict_heap_kernel): a workgroup of
 // 1024 threads stages a block of RB rows of codes in LDS (one coalesced read
 // of the rows instead of a dependent byte gather per tree level) and walks
-// the trees a chunk of TC at a time: the chunk's node words and leaf values
-// are staged in LDS, every (row, tree) pair of the chunk is walked by its own
-// thread (all walks independent: D dependent LDS reads each instead of D per
-// tree in sequence), the products lr * leaf go to an LDS table [row][tree],
-// and one thread per (row, class) adds them in tree order.  TC is a multiple
-// of K, so tree t0 + j belongs to class j % K.
+// the trees a chunk of TC at a time: the chunk's complete-tree tables
+// (complete_tables_kernel) are staged in LDS, every (row, tree) pair of the
+// chunk is walked by its own thread (all walks independent: D dependent LDS
+// reads each instead of D per tree in sequence), the products lr * leaf go to
+// an LDS table [row][tree], and one thread per (row, class) adds them in tree
+// order.  TC is a multiple of K, so tree t0 + j belongs to class j % K.
 //   LDS: rows [RB][S + 4] bytes (a 4-byte pad per row spreads the rows of
-//   one wave over the banks), nodes [TC][H] (feature << 8 | bin, or ~0 for a
-//   leaf), leaves [TC][H], vals [RB][TC + 1] (odd row stride: no bank conflicts).
+//   one wave over the banks), node words [TC][2^D - 1], last-level values
+//   [TC][2^D], vals [RB][TC + 1] (odd row stride: no bank conflicts).
 constexpr int kPredThreads = 1024;
 constexpr int kPredMaxAcc = 4;  // (row, class) accumulators per thread
-constexpr uint32_t kPredLeaf = 0xffffffffu;
 
 __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
     const int8_t* __restrict__ codes, int64_t n, int64_t S, int32_t num_bins,
-    const int32_t* __restrict__ feat, const int32_t* __restrict__ bin,
-    const float* __restrict__ leaf, int32_t n_rounds, int32_t K, int32_t H, int32_t max_depth,
-    float lr, int32_t RB, int32_t TC, float* __restrict__ out) {
+    const uint32_t* __restrict__ cnode, const float* __restrict__ cleaf, int32_t n_rounds,
+    int32_t K, int32_t max_depth, float lr, int32_t RB, int32_t TC, float* __restrict__ out) {
   extern __shared__ uint32_t psm[];
   const int Sp = (int)S + 4;
+  const int Hi = (1 << max_depth) - 1, L = 1 << max_depth;  // complete-table widths
   uint8_t* rows_s = reinterpret_cast<uint8_t*>(psm);
   uint32_t* nodes_s = psm + (RB * Sp) / 4;
-  float* leaves_s = reinterpret_cast<float*>(nodes_s + TC * H);
-  float* vals_s = leaves_s + TC * H;
+  float* leaves_s = reinterpret_cast<float*>(nodes_s + TC * Hi);
+  float* vals_s = leaves_s + TC * L;
   const int64_t row0 = (int64_t)blockIdx.x * RB;
   const int nr = (int)(n - row0 < RB ? n - row0 : RB);
   const int tid = threadIdx.x;
@@ -144,46 +189,36 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
   for (int t0 = 0; t0 < T; t0 += TC) {
     const int tc = T - t0 < TC ? T - t0 : TC;
     __syncthreads();  // rows staged / previous chunk's vals consumed
-    for (int i = tid; i < tc * H; i += kPredThreads) {
-      const int64_t g = (int64_t)t0 * H + i;
-      const int f = feat[g];
-      nodes_s[i] = f < 0 ? kPredLeaf : ((uint32_t)f << 8) | (uint32_t)(bin[g] & 0xff);
-      leaves_s[i] = leaf[g];
-    }
+    for (int i = tid; i < tc * Hi; i += kPredThreads) nodes_s[i] = cnode[(int64_t)t0 * Hi + i];
+    for (int i = tid; i < tc * L; i += kPredThreads) leaves_s[i] = cleaf[(int64_t)t0 * L + i];
     __syncthreads();
     // walks: thread w < G * RB owns row wr = w % RB and the chunk's trees
     // wt0, wt0 + G, ... (G = threads / RB row groups, no division per walk),
     // two in lock-step so that the LDS reads of one overlap those of the
-    // other; max_depth branch-free steps (a walk at a leaf reloads its own
-    // node word and keeps its index)
+    // other; max_depth steps on the complete tables (no leaf test)
     if (walker) {
       const bool row_on = wr < nr;
       const uint8_t* row = rows_s + wr * Sp;
       for (int j0 = wt0; j0 < tc; j0 += 2 * G) {
         int tl[2], h[2];
         bool on[2];
-        uint32_t w[2];
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           on[k] = row_on && j0 + k * G < tc;
           tl[k] = on[k] ? j0 + k * G : 0;  // an idle walk reads tree 0 and stores nothing
           h[k] = 0;
-          w[k] = on[k] ? nodes_s[tl[k] * H] : kPredLeaf;
         }
         for (int d = 0; d < max_depth; ++d) {
 #pragma unroll
           for (int k = 0; k < 2; ++k) {
-            const uint32_t f = w[k] >> 8;
-            const int c = (int)row[f < (uint32_t)S ? f : (uint32_t)S - 1];  // stays in the row
-            const int b = (int)(w[k] & 0xffu);
-            const bool leaf = w[k] == kPredLeaf;
-            h[k] = leaf ? h[k] : 2 * h[k] + ((c <= b || c == num_bins) ? 1 : 2);
-            w[k] = nodes_s[tl[k] * H + h[k]];
+            const uint32_t w = nodes_s[tl[k] * Hi + h[k]];
+            const int c = (int)row[w >> 8];
+            h[k] = 2 * h[k] + ((c <= (int)(w & 0xffu) || c == num_bins) ? 1 : 2);
           }
         }
 #pragma unroll
         for (int k = 0; k < 2; ++k)
-          if (on[k]) vals_s[wr * (TC + 1) + tl[k]] = lr * leaves_s[tl[k] * H + h[k]];
+          if (on[k]) vals_s[wr * (TC + 1) + tl[k]] = lr * leaves_s[tl[k] * L + h[k] - Hi];
       }
     }
     __syncthreads();
@@ -208,9 +243,10 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Resident-tree inference, for ensembles whose node tables fit in LDS next to
-// a row block (same results as predict_rows_kernel).  Persistent workgroups
-// (one per CU) load every tree once, then stride over blocks of RB rows:
+// Resident-tree inference, for ensembles whose complete-tree tables fit in
+// LDS next to a row block (same results as predict_rows_kernel).  Persistent
+// workgroups (one per CU) load every tree once, then stride over blocks of RB
+// rows:
 //   * the next block's codes are loaded into registers while the current one
 //     is walked (QPT 16-byte loads per thread), then stored to the LDS row
 //     buffer after the walks;
@@ -226,23 +262,20 @@ constexpr int kResWalks = 2;  // walks a walker thread advances in lock-step
 
 __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
     const int8_t* __restrict__ codes, int64_t n, int64_t S, int32_t num_bins,
-    const int32_t* __restrict__ feat, const int32_t* __restrict__ bin,
-    const float* __restrict__ leaf, int32_t T, int32_t K, int32_t H, int32_t max_depth,
-    float lr, int32_t RB, float* __restrict__ out) {
+    const uint32_t* __restrict__ cnode, const float* __restrict__ cleaf, int32_t T, int32_t K,
+    int32_t max_depth, float lr, int32_t RB, float* __restrict__ out) {
   extern __shared__ uint32_t psm[];
   const int Sp = (int)S + 4;
   const int TV = T + 1;  // value-table row stride (odd or even, see below)
+  const int Hi = (1 << max_depth) - 1, L = 1 << max_depth;  // complete-table widths
   uint32_t* nodes_s = psm;
-  float* leaves_s = reinterpret_cast<float*>(nodes_s + T * H);
-  uint8_t* rows_s = reinterpret_cast<uint8_t*>(leaves_s + T * H);
+  float* leaves_s = reinterpret_cast<float*>(nodes_s + T * Hi);
+  uint8_t* rows_s = reinterpret_cast<uint8_t*>(leaves_s + T * L);
   float* vals_s = reinterpret_cast<float*>(rows_s + RB * Sp);  // 2 x [RB][TV]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  for (int i = tid; i < T * H; i += kResThreads) {
-    const int f = feat[i];
-    nodes_s[i] = f < 0 ? kPredLeaf : ((uint32_t)f << 8) | (uint32_t)(bin[i] & 0xff);
-    leaves_s[i] = leaf[i];
-  }
+  for (int i = tid; i < T * Hi; i += kResThreads) nodes_s[i] = cnode[i];
+  for (int i = tid; i < T * L; i += kResThreads) leaves_s[i] = cleaf[i];
   const int64_t nblk = (n + RB - 1) / RB;
   const int qpr = (int)(S / 16);  // 16-byte quads per row
   const int nq = RB * qpr;
@@ -324,30 +357,24 @@ __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
       for (int t0 = wt0; t0 < T; t0 += kResWalks * G) {
         int tl[kResWalks], h[kResWalks];
         bool on[kResWalks];
-        uint32_t w[kResWalks];
 #pragma unroll
         for (int k = 0; k < kResWalks; ++k) {
           on[k] = row_on && t0 + k * G < T;
           tl[k] = on[k] ? t0 + k * G : 0;  // an idle walk reads tree 0 and stores nothing
           h[k] = 0;
-          w[k] = on[k] ? nodes_s[tl[k] * H] : kPredLeaf;
         }
-        // max_depth steps, branch-free: a walk at a leaf reloads its own
-        // node word (kPredLeaf) and keeps its index
+        // max_depth steps on the complete tables (no leaf test)
         for (int d = 0; d < max_depth; ++d) {
 #pragma unroll
           for (int k = 0; k < kResWalks; ++k) {
-            const uint32_t f = w[k] >> 8;
-            const int c = (int)row[f < (uint32_t)S ? f : (uint32_t)S - 1];  // stays in the row
-            const int bb = (int)(w[k] & 0xffu);
-            const bool leaf = w[k] == kPredLeaf;
-            h[k] = leaf ? h[k] : 2 * h[k] + ((c <= bb || c == num_bins) ? 1 : 2);
-            w[k] = nodes_s[tl[k] * H + h[k]];
+            const uint32_t w = nodes_s[tl[k] * Hi + h[k]];
+            const int c = (int)row[w >> 8];
+            h[k] = 2 * h[k] + ((c <= (int)(w & 0xffu) || c == num_bins) ? 1 : 2);
           }
         }
 #pragma unroll
         for (int k = 0; k < kResWalks; ++k)
-          if (on[k]) vrow[tl[k]] = lr * leaves_s[tl[k] * H + h[k]];
+          if (on[k]) vrow[tl[k]] = lr * leaves_s[tl[k] * L + h[k] - Hi];
       }
     }
     prev = b;
@@ -366,15 +393,16 @@ int predict_resident_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int
                           size_t* lds_out) {
   constexpr int64_t kBudget = 150 * 1024;
   const int64_t T = (int64_t)n_rounds * K;
-  if (S % 16 != 0 || S >= (1 << 20) || T * H * 8 > 64 * 1024) return 0;
+  // complete tables: (H - 1) / 2 node words and (H + 1) / 2 values per tree
+  if (S % 16 != 0 || S >= (1 << 20) || T * H * 4 > 64 * 1024) return 0;
   const int64_t Sp = S + 4;
   // RB rows: the row buffer, two value tables and at most kResMaxQ loads per thread
-  int64_t RB = (kBudget - 8 * T * H) / (Sp + 8 * (T + 1));
+  int64_t RB = (kBudget - 4 * T * H) / (Sp + 8 * (T + 1));
   RB = std::min<int64_t>(RB, (int64_t)kResMaxQ * kResThreads * 16 / S);
   RB = std::min<int64_t>(RB, 256);
   if (RB < 8) return 0;
   *RB_out = (int32_t)RB;
-  *lds_out = (size_t)(8 * T * H + RB * Sp + 8 * RB * (T + 1));
+  *lds_out = (size_t)(4 * T * H + RB * Sp + 8 * RB * (T + 1));
   return 1;
 }
 
@@ -383,18 +411,19 @@ int predict_resident_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int
 int predict_rows_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
                       int32_t* TC_out, size_t* lds_out) {
   constexpr int64_t kBudget = 64 * 1024;
-  if (S % 16 != 0 || S >= (1 << 24) || (int64_t)8 * H * K > 32 * 1024) return 0;
+  // complete tables: (H - 1) / 2 node words and (H + 1) / 2 values per tree
+  if (S % 16 != 0 || S >= (1 << 24) || (int64_t)4 * H * K > 32 * 1024) return 0;
   const int64_t T = (int64_t)n_rounds * K;
-  int64_t m = std::max<int64_t>(1, (16 * 1024) / ((int64_t)8 * H * K));
+  int64_t m = std::max<int64_t>(1, (16 * 1024) / ((int64_t)4 * H * K));
   int64_t TC = std::min<int64_t>(m * K, std::max<int64_t>(K, (T + K - 1) / K * K));
   const int64_t Sp = S + 4;
-  int64_t RB = (kBudget - 8 * TC * H) / (Sp + 4 * (TC + 1));
+  int64_t RB = (kBudget - 4 * TC * H) / (Sp + 4 * (TC + 1));
   RB = std::min<int64_t>(RB, 256);
   RB = std::min<int64_t>(RB, (int64_t)kPredMaxAcc * kPredThreads / K);
   if (RB < 16) return 0;
   *RB_out = (int32_t)RB;
   *TC_out = (int32_t)TC;
-  *lds_out = (size_t)(RB * Sp + 8 * TC * H + 4 * RB * (TC + 1));
+  *lds_out = (size_t)(RB * Sp + 4 * TC * H + 4 * RB * (TC + 1));
   return 1;
 }
 
