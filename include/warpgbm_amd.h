@@ -246,8 +246,10 @@ int wgbm_engine_round(wgbm_engine* eng, const void* target, float* pred, const i
                       int32_t n_sel, const wgbm_tree_record* rec, void* stream);
 /* Tuning knobs: key 1 = histogram tile rows (0 = automatic); key 2 = codes
  * read by the era path when num_bins <= 7 (0 = the int8 codes, 1 = a
- * pair-code copy, one byte per feature pair; default 1).  Set before the
- * first round; every setting grows the same trees. */
+ * pair-code copy, one byte per feature pair; default 1); key 3 = the
+ * per-level node scan of one-era fits (1 = a thread per node, default; 0 = a
+ * wave per node).  Set before the first round; every setting grows the same
+ * trees. */
 int wgbm_engine_set_tuning(wgbm_engine* eng, int32_t key, int64_t value);
 void wgbm_engine_destroy(wgbm_engine* eng);
 

@@ -459,3 +459,43 @@ def test_depth_beyond_twenty_bit_exact(gpu):
         assert a == b, f"tree {i} differs"
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
     assert max(_depth(t) for t in m.forest) > 12
+
+
+@pytest.mark.parametrize("scan", [1, 0])
+def test_one_era_level_scans_bit_exact(gpu, scan):
+    """The two per-level node scans of one-era fits (engine tuning key 3: a
+    thread per node, or a wave per node) grow the oracle's trees.  Heavy
+    tails on 60000 rows: nodes spanning many partition blocks whose child
+    maxima move their histogram shift (both children histogrammed); depth 12
+    (2048 nodes at the last split level, past the 1024 planned from
+    registers); softmax with 5 class trees and 640 nodes at depth 7."""
+    print_case("estimator", "one-era level scan", scan)
+    rng = np.random.default_rng(12)
+    N = 60_000
+    X = rng.standard_normal((N, 5)).astype(F32)
+    y = _heavy_targets(rng, N, X[:, 1])
+    y[2:200] *= 1e4  # a band of mid-sized residuals
+    kw = dict(num_bins=8, max_depth=12, n_estimators=2, learning_rate=0.3, min_child_weight=1)
+    m = WarpGBM(**kw)
+    m._engine_tuning = {3: scan}
+    m.fit(X, y)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, y)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
+    assert max(_depth(t) for t in m.forest) == 12
+    # softmax: 5 trees per round, 640 (tree, node)s at depth 7
+    N, F, K = 30_000, 6, 5
+    labels = rng.integers(0, K, N)
+    X = (rng.standard_normal((K, F))[labels] + rng.standard_normal((N, F))).astype(F32)
+    kw = dict(objective="multiclass", num_bins=16, max_depth=8, n_estimators=2,
+              learning_rate=0.3, min_child_weight=2)
+    m = WarpGBM(**kw)
+    m._engine_tuning = {3: scan}
+    m.fit(X, labels)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, labels)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"round {i} differs"
+    assert np.array_equal(bits(m.predict_proba(X)), bits(ref.predict_codes(codes)))

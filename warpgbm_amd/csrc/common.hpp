@@ -166,6 +166,67 @@ __device__ __forceinline__ int64_t wgbm_wave_reduce_add_i64(int64_t x) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// One DPP step of a 64-bit sum: x + (x of the source lane, 0 where none).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ int64_t wgbm_dpp_add_i64(int64_t x) {
+  const uint32_t lo = wgbm_dpp_u32<CTRL, ROWMASK>((uint32_t)(uint64_t)x);
+  const uint32_t hi = wgbm_dpp_u32<CTRL, ROWMASK>((uint32_t)((uint64_t)x >> 32));
+  return x + (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Workgroup barrier that orders LDS accesses only: global stores issued
+// before it need not have completed (__syncthreads waits for them, a memory
+// round trip).  Use it where the threads exchange data through LDS alone.
+__device__ __forceinline__ void wgbm_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// A 64-bit value of one lane (lane wave-uniform).
+__device__ __forceinline__ int64_t wgbm_readlane_i64(int64_t x, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)x, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)x >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Inclusive prefix sum inside each row of 16 lanes (lane 16 r + i: lanes
+// 16 r .. 16 r + i).
+__device__ __forceinline__ int64_t wgbm_row_incl_scan_i64(int64_t x) {
+  x = wgbm_dpp_add_i64<0x111, 0xf>(x);
+  x = wgbm_dpp_add_i64<0x112, 0xf>(x);
+  x = wgbm_dpp_add_i64<0x114, 0xf>(x);
+  x = wgbm_dpp_add_i64<0x118, 0xf>(x);
+  return x;
+}
+
+// Segmented inclusive maxima over the lanes: (f, a, b) triples, f set where
+// a run opens, combined as (f1, a1, b1) . (f2, a2, b2) = (f1 | f2, f2 ? a2 :
+// max(a1, a2), f2 ? b2 : max(b1, b2)); a lane with no source reads (0, 0, 0),
+// the identity.  The row steps alone scan each row of 16 lanes.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ void wgbm_dpp_segmax_step(uint32_t& f, uint32_t& a, uint32_t& b) {
+  const uint32_t yf = wgbm_dpp_u32<CTRL, ROWMASK>(f);
+  const uint32_t ya = wgbm_dpp_u32<CTRL, ROWMASK>(a);
+  const uint32_t yb = wgbm_dpp_u32<CTRL, ROWMASK>(b);
+  if (!f) {
+    a = ya > a ? ya : a;
+    b = yb > b ? yb : b;
+  }
+  f |= yf;
+}
+__device__ __forceinline__ void wgbm_row_segmax_scan(uint32_t& f, uint32_t& a, uint32_t& b) {
+  wgbm_dpp_segmax_step<0x111, 0xf>(f, a, b);
+  wgbm_dpp_segmax_step<0x112, 0xf>(f, a, b);
+  wgbm_dpp_segmax_step<0x114, 0xf>(f, a, b);
+  wgbm_dpp_segmax_step<0x118, 0xf>(f, a, b);
+}
+__device__ __forceinline__ void wgbm_wave_segmax_scan(uint32_t& f, uint32_t& a, uint32_t& b) {
+  wgbm_row_segmax_scan(f, a, b);
+  wgbm_dpp_segmax_step<0x142, 0xa>(f, a, b);
+  wgbm_dpp_segmax_step<0x143, 0xc>(f, a, b);
+}
+
 // Inclusive prefix sum over the wave's lanes (lane i: lanes 0..i), the same
 // DPP sequence without the read-out.
 __device__ __forceinline__ int64_t wgbm_wave_incl_scan_i64(int64_t x) {
@@ -265,22 +326,16 @@ __host__ __device__ inline float wgbm_expf(float x) {
 // exclusive scan of one value per thread; *total = sum over the workgroup
 __device__ inline int64_t wgbm_block_excl_scan(int64_t v, int64_t* wsum /*[16]*/,
                                                int64_t* total) {
+  // 1024 threads: the wave totals, scanned over lanes 0..15 of every wave
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int64_t x = v;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int64_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  const int64_t x = wgbm_wave_incl_scan_i64(v);
   if (lane == 63) wsum[w] = x;
   __syncthreads();
-  int64_t pre = 0, tot = 0;
-  for (int k = 0; k < 16; ++k) {
-    if (k < w) pre += wsum[k];
-    tot += wsum[k];
-  }
+  const int64_t s = wgbm_row_incl_scan_i64(lane < 16 ? wsum[lane] : 0);
+  const int64_t pre = wgbm_readlane_i64(s, w > 0 ? w - 1 : 0);
+  *total = wgbm_readlane_i64(s, 15);
   __syncthreads();
-  *total = tot;
-  return pre + x - v;
+  return (w > 0 ? pre : 0) + x - v;
 }
 
 // Exclusive scan of n values get(i) by one workgroup, kScanK * 1024 values

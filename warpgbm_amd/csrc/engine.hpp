@@ -108,6 +108,9 @@ struct PartSums {
   uint32_t* bf_mr;
   uint32_t* bl_ml;   // [nb] of the block's last node
   uint32_t* bl_mr;
+  int32_t* bf_node;  // [nb] (tree, node) of the block's first position
+  uint32_t* pm_l;    // [nb] segmented maxima of bf_ml / bf_mr over runs of
+  uint32_t* pm_r;    //      blocks with one first node (block_scan_body)
 };
 
 // A child node keeps its parent's histogram shift unless the shift of its
@@ -179,6 +182,14 @@ __global__ void level_scan_kernel(int32_t nb, PartSums ps, int32_t T, int32_t no
                                   const int32_t* split_l, LevelNext nx, int32_t n_list,
                                   int32_t tile_rows, int32_t max_tiles, Tile* tiles,
                                   int32_t* key_tile_start, int32_t* n_tiles);
+// One-era levels: level_scan_kernel's work with a thread per (tree, node),
+// up to kLevelScanE1MaxNodes of them, and the next level's tile plan.
+constexpr int kLevelScanE1MaxNodes = 2048;
+__global__ void level_scan_e1_kernel(int32_t nb, PartSums ps, int32_t n_tn, int64_t n_pos,
+                                     const int64_t* seg, const int32_t* present,
+                                     const int32_t* split_l, LevelNext nx, int32_t plan,
+                                     int32_t tile_rows, int32_t max_tiles, Tile* tiles,
+                                     int32_t* key_tile_start, int32_t* n_tiles);
 __global__ void root_totals_kernel(int32_t n_keys, const int64_t* seg, PartSums ps,
                                    int64_t* tot_qh, int64_t* tot_ql, int64_t* tot_c);
 __global__ void node_scan_kernel(int32_t T, int32_t nodes, int32_t E, int32_t wpn,

@@ -73,6 +73,9 @@ struct Engine {
   int64_t pstride = 0;
   bool pcodes_ready = false;
   int des_codes = 1;
+  // one-era levels: 1 = level_scan_e1_kernel (a thread per node), 0 = the
+  // wave-per-node kernels
+  int lscan_e1 = 1;
   uint32_t* alive = nullptr;    // [tn][W] segments that can hold a split, W = ceil(E/32)
   double* bsum = nullptr;       // [tn][W][n_sel*(B-1)] era-block gain sums
   int32_t* bdir = nullptr;      // [tn][W][n_sel*(B-1)] era-block direction sums
@@ -250,6 +253,9 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->ps.bf_mr, e->nb);
   E_ALLOC(e->ps.bl_ml, e->nb);
   E_ALLOC(e->ps.bl_mr, e->nb);
+  E_ALLOC(e->ps.bf_node, e->nb);
+  E_ALLOC(e->ps.pm_l, e->nb);
+  E_ALLOC(e->ps.pm_r, e->nb);
   E_ALLOC(e->hkts, e->n_keys_max + 1);
   E_ALLOC(e->hn, 1);
   if (E > 1) {
@@ -278,6 +284,11 @@ int engine_set_tuning(Engine* e, int key, int64_t value) {
   if (key == 2) {
     WGBM_REQUIRE(value == 0 || value == 1, "era code layout must be 0 or 1");
     e->des_codes = (int)value;
+    return 0;
+  }
+  if (key == 3) {
+    WGBM_REQUIRE(value == 0 || value == 1, "one-era level scan must be 0 or 1");
+    e->lscan_e1 = (int)value;
     return 0;
   }
   wgbm_set_error("engine_set_tuning: unknown key %d", key);
@@ -643,7 +654,9 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     nx.present_next = e->present[nxt];
     nx.key_list_next = e->key_list[nxt];
     nx.node_shift_next = e->node_shift[nxt];
-    if (d < D && E <= 64 && n_tn <= kLevelScanMaxNodes) {
+    const bool one_wg = E == 1 ? n_tn <= kLevelScanE1MaxNodes
+                               : (E <= 64 && n_tn <= kLevelScanMaxNodes);
+    if (d < D && one_wg) {
       // few keys: block prefix, node scan and the next level's tile plan in
       // one workgroup
       LevelPlan lp;
@@ -655,12 +668,28 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         const int r = level_plan(e, d + 1, &lp);
         if (r) return r;
       }
-      hipLaunchKernelGGL(level_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps, T,
-                         nodes, E, n_pos, e->seg[cur], e->present[cur], e->split_l, nx,
-                         next_hist ? lp.n_list : 0, (int32_t)lp.R, (int32_t)lp.max_tiles,
-                         e->htiles, e->hkts, e->hn);
-      WGBM_LAUNCH_CHECK();
-      planned = next_hist;
+      if (E == 1 && e->lscan_e1) {
+        hipLaunchKernelGGL(level_scan_e1_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb,
+                           e->ps, (int32_t)n_tn, n_pos, e->seg[cur], e->present[cur], e->split_l,
+                           nx, next_hist ? 1 : 0, (int32_t)lp.R, (int32_t)lp.max_tiles, e->htiles,
+                           e->hkts, e->hn);
+        WGBM_LAUNCH_CHECK();
+        planned = next_hist;
+      } else if (n_tn <= kLevelScanMaxNodes) {
+        hipLaunchKernelGGL(level_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps,
+                           T, nodes, E, n_pos, e->seg[cur], e->present[cur], e->split_l, nx,
+                           next_hist ? lp.n_list : 0, (int32_t)lp.R, (int32_t)lp.max_tiles,
+                           e->htiles, e->hkts, e->hn);
+        WGBM_LAUNCH_CHECK();
+        planned = next_hist;
+      } else {
+        hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
+        WGBM_LAUNCH_CHECK();
+        hipLaunchKernelGGL(node_scan_kernel, dim3(blocks_for((int64_t)n_tn, 4)), dim3(256), 0,
+                           st, T, nodes, E, 1, n_pos, e->seg[cur], e->present[cur], e->split_l,
+                           e->ps, nx);
+        WGBM_LAUNCH_CHECK();
+      }
     } else if (d < D) {
       hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
       WGBM_LAUNCH_CHECK();

@@ -596,6 +596,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     a.ps.bl_n[blockIdx.x] = n;
     if (maxes) {
       // the first and last nodes of the block: their maxima here
+      a.ps.bf_node[blockIdx.x] = key[0] / a.E;  // thread 0 holds the block's first position
       const int64_t sn = a.seg[(int64_t)(khi / a.E) * a.E];
       const int lns = (int)((sn > p0 ? sn : p0) - p0);
       a.ps.bf_ml[blockIdx.x] = s_ml[0];
@@ -606,36 +607,95 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   }
 }
 
+// LDS copies of the block prefixes (level_scan_e1_kernel, at most
+// kScanLdsBlocks blocks)
+constexpr int kScanLdsBlocks = 2048;
+struct ScanLds {
+  int64_t* qh;
+  int64_t* ql;
+  int32_t* n;
+  uint32_t* ml;
+  uint32_t* mr;
+};
+
 // inclusive prefix over the blocks of the first-segment partials; one
-// workgroup of 1024 threads, tiles of 1024 blocks
-__device__ inline void block_scan_body(int32_t nb, const PartSums& ps) {
-  __shared__ int64_t s_wh[16], s_wl[16], s_wn[16];
-  __shared__ int64_t s_ch, s_cl, s_cn;
+// workgroup of 1024 threads, tiles of 1024 blocks.  The words of the first
+// two tiles are loaded before pre() runs (work of the caller that does not
+// need the prefixes), later tiles one tile ahead.  Wave totals are scanned
+// with DPP over lanes 0..15 and double-buffered by tile parity (one barrier
+// per tile); the carries between tiles stay in registers.  With seg_max
+// also the segmented inclusive maxima of the first nodes' child maxima:
+// pm_l[b] = max of bf_ml over the run of consecutive blocks, ending at b,
+// whose first node is bf_node[b] (every such block starts inside that
+// node).  With to_lds the prefixes are also left in LDS (nb <=
+// kScanLdsBlocks).
+struct NoPre {
+  __device__ void operator()() const {}
+};
+template <typename Pre = NoPre>
+__device__ inline void block_scan_body(int32_t nb, const PartSums& ps, bool seg_max = false,
+                                       bool to_lds = false, ScanLds lds = ScanLds{},
+                                       Pre pre = Pre{}) {
+  __shared__ int64_t s_wh[2][16], s_wl[2][16], s_wn[2][16];
+  __shared__ uint32_t s_mf[2][16], s_ml[2][16], s_mr[2][16];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  if (t == 0) {
-    s_ch = 0;
-    s_cl = 0;
-    s_cn = 0;
-  }
-  __syncthreads();
-  for (int b0 = 0; b0 < nb; b0 += 1024) {
-    const int b = b0 + t;
-    int64_t qh = b < nb ? ps.bf_qh[b] : 0, ql = b < nb ? ps.bf_ql[b] : 0,
-            n = b < nb ? ps.bf_n[b] : 0;
-    qh = wgbm_wave_incl_scan_i64(qh);
-    ql = wgbm_wave_incl_scan_i64(ql);
-    n = wgbm_wave_incl_scan_i64(n);
-    if (lane == 63) {
-      s_wh[w] = qh;
-      s_wl[w] = ql;
-      s_wn[w] = n;
+  // one block's words (blocks past the end: zero, and a run opens there).
+  // Loads only: the run test compares the first nodes when the words are
+  // used, so that the loads of both tiles are in flight together.
+  struct Words {
+    int64_t qh, ql;
+    int32_t n;  // widened where used (a conversion here would wait for the load)
+    uint32_t vl, vr;
+    int32_t nd, ndp;  // first node of the block and of the block before
+  };
+  auto load = [&](int b) {
+    Words x{0, 0, 0, 0u, 0u, -1, -2};
+    if (b < nb) {
+      x.qh = ps.bf_qh[b];
+      x.ql = ps.bf_ql[b];
+      x.n = ps.bf_n[b];
+      if (seg_max) {
+        x.vl = ps.bf_ml[b];
+        x.vr = ps.bf_mr[b];
+        x.nd = ps.bf_node[b];
+        x.ndp = b > 0 ? ps.bf_node[b - 1] : -2;
+      }
     }
-    __syncthreads();
-    int64_t ch = s_ch, cl = s_cl, cn = s_cn;
-    for (int k = 0; k < w; ++k) {
-      ch += s_wh[k];
-      cl += s_wl[k];
-      cn += s_wn[k];
+    return x;
+  };
+  Words nxt = load(t), nxt2 = load(t + 1024);
+  pre();
+  int64_t ch = 0, cl = 0, cn = 0;  // prefix before the tile (workgroup-uniform)
+  uint32_t cml = 0u, cmr = 0u;     // maxima of the run open before the tile
+  int par = 0;
+  for (int b0 = 0; b0 < nb; b0 += 1024, par ^= 1) {
+    const int b = b0 + t;
+    const Words cur = nxt;
+    nxt = nxt2;
+    if (b0 + 2048 < nb) nxt2 = load(b + 2048);
+    int64_t qh = wgbm_wave_incl_scan_i64(cur.qh);
+    int64_t ql = wgbm_wave_incl_scan_i64(cur.ql);
+    int64_t n = wgbm_wave_incl_scan_i64((int64_t)cur.n);
+    uint32_t f = cur.nd != cur.ndp ? 1u : 0u, vl = cur.vl, vr = cur.vr;
+    if (seg_max) wgbm_wave_segmax_scan(f, vl, vr);
+    if (lane == 63) {
+      s_wh[par][w] = qh;
+      s_wl[par][w] = ql;
+      s_wn[par][w] = n;
+      s_mf[par][w] = f;
+      s_ml[par][w] = vl;
+      s_mr[par][w] = vr;
+    }
+    wgbm_lds_barrier();  // the wave totals are read from LDS only
+    // the wave totals scanned over lanes 0..15: lane w - 1 holds waves 0..w-1
+    const int src = w > 0 ? w - 1 : 0;
+    const int64_t gh = wgbm_row_incl_scan_i64(lane < 16 ? s_wh[par][lane] : 0);
+    const int64_t gl = wgbm_row_incl_scan_i64(lane < 16 ? s_wl[par][lane] : 0);
+    const int64_t gn = wgbm_row_incl_scan_i64(lane < 16 ? s_wn[par][lane] : 0);
+    if (w > 0) {
+      qh += wgbm_readlane_i64(gh, src);
+      ql += wgbm_readlane_i64(gl, src);
+      n += wgbm_readlane_i64(gn, src);
     }
     qh += ch;
     ql += cl;
@@ -644,15 +704,50 @@ __device__ inline void block_scan_body(int32_t nb, const PartSums& ps) {
       ps.P_qh[b] = qh;
       ps.P_ql[b] = ql;
       ps.P_n[b] = n;
+      if (to_lds) {
+        lds.qh[b] = qh;
+        lds.ql[b] = ql;
+        lds.n[b] = (int32_t)n;
+      }
     }
-    __syncthreads();  // every thread has read the carry and the wave sums
-    if (t == 1023) {
-      s_ch = qh;
-      s_cl = ql;
-      s_cn = n;
+    ch += wgbm_readlane_i64(gh, 15);
+    cl += wgbm_readlane_i64(gl, 15);
+    cn += wgbm_readlane_i64(gn, 15);
+    if (seg_max) {
+      uint32_t mf = lane < 16 ? s_mf[par][lane] : 0u;
+      uint32_t ma = lane < 16 ? s_ml[par][lane] : 0u;
+      uint32_t mb = lane < 16 ? s_mr[par][lane] : 0u;
+      wgbm_row_segmax_scan(mf, ma, mb);
+      // the open run's maxima before this wave: the tile carry, then waves
+      // 0..w-1 (a run opening among them restarts it)
+      uint32_t pl = cml, pr = cmr;
+      if (w > 0) {
+        const uint32_t F = (uint32_t)__builtin_amdgcn_readlane((int)mf, src);
+        const uint32_t A = (uint32_t)__builtin_amdgcn_readlane((int)ma, src);
+        const uint32_t B = (uint32_t)__builtin_amdgcn_readlane((int)mb, src);
+        pl = F ? A : (A > pl ? A : pl);
+        pr = F ? B : (B > pr ? B : pr);
+      }
+      if (!f) {
+        vl = pl > vl ? pl : vl;
+        vr = pr > vr ? pr : vr;
+      }
+      if (b < nb) {
+        ps.pm_l[b] = vl;
+        ps.pm_r[b] = vr;
+        if (to_lds) {
+          lds.ml[b] = vl;
+          lds.mr[b] = vr;
+        }
+      }
+      const uint32_t F = (uint32_t)__builtin_amdgcn_readlane((int)mf, 15);
+      const uint32_t A = (uint32_t)__builtin_amdgcn_readlane((int)ma, 15);
+      const uint32_t B = (uint32_t)__builtin_amdgcn_readlane((int)mb, 15);
+      cml = F ? A : (A > cml ? A : cml);
+      cmr = F ? B : (B > cmr ? B : cmr);
     }
-    __syncthreads();
   }
+  if (to_lds) wgbm_lds_barrier();  // the LDS prefixes are read by other threads
 }
 
 __global__ __launch_bounds__(1024) void block_scan_kernel(int32_t nb, PartSums ps) {
@@ -935,6 +1030,228 @@ __global__ __launch_bounds__(1024) void level_scan_kernel(
   __syncthreads();
   plan_tiles_body(nx.seg_next, 0, n_list, nx.key_list_next, tile_rows, 0, max_tiles, tiles,
                   key_tile_start, n_tiles);
+}
+
+// The tiles of one list entry: a segment [b0, b0 + len) split into nt tiles
+// of len / nt rows, the first len % nt one more (tile ids below ntot).
+__device__ inline void write_entry_tiles(int key, int64_t b0, uint32_t len, int first, int nt,
+                                         int j0, int dj, int ntot, Tile* __restrict__ tiles) {
+  const uint32_t q = len / (uint32_t)nt, r = len - q * (uint32_t)nt;
+  for (int j = j0; j < nt && first + j < ntot; j += dj) {
+    const uint32_t uj = (uint32_t)j;
+    Tile tl;
+    tl.key = key;
+    tl.pad = 0;
+    tl.begin = b0 + (int64_t)(uj * q + (uj < r ? uj : r));
+    tl.end = tl.begin + (int64_t)(q + (uj < r ? 1u : 0u));
+    tiles[first + j] = tl;
+  }
+}
+
+// One-era levels (E == 1): a thread per (tree, node).  The node's words
+// that do not depend on the block prefix (flags, bounds, its route partials)
+// are loaded before the prefix scan, which leaves its prefixes in LDS; the
+// node's left / right child maxima come from the segmented block maxima, so
+// each node costs a fixed number of loads whatever its size.  The next
+// level's list entries are 2 tn (left child) and 2 tn + 1 (right child);
+// with at most 1024 nodes their tiles are planned from registers, else from
+// the words just written (plan_tiles_body).  Same outputs as
+// level_scan_kernel.
+__global__ __launch_bounds__(1024) void level_scan_e1_kernel(
+    int32_t nb, PartSums ps, int32_t n_tn, int64_t n_pos, const int64_t* __restrict__ seg,
+    const int32_t* __restrict__ present, const int32_t* __restrict__ split_l, LevelNext nx,
+    int32_t plan, int32_t tile_rows, int32_t max_tiles, Tile* __restrict__ tiles,
+    int32_t* __restrict__ key_tile_start, int32_t* __restrict__ n_tiles) {
+  __shared__ int64_t l_qh[kScanLdsBlocks], l_ql[kScanLdsBlocks];
+  __shared__ int32_t l_n[kScanLdsBlocks];
+  __shared__ uint32_t l_ml[kScanLdsBlocks], l_mr[kScanLdsBlocks];
+  const int t = threadIdx.x;
+  const bool have_max = nx.have_max != 0;
+  // a node's words that do not need the prefix scan: q0 / q1 are its first
+  // and last blocks; for a node inside one block its own partials, else the
+  // partials of its part of the first block
+  struct NodeWords {
+    int32_t pr, sl, hs;
+    int64_t base, end, tqh, tql;
+    int64_t oqh, oql, bqh, bql;  // own partials, and those of the first block
+    int32_t on, bn;
+    uint32_t oml, omr, bml, bmr;
+  };
+  // (every load is unconditional and the words are used only after the
+  // block scan, so that one round trip brings the flags and bounds and a
+  // second the partials, both overlapping the scan)
+  auto load_node = [&](int tn) {
+    NodeWords x;
+    x.pr = present[tn];
+    x.sl = split_l[tn];
+    x.base = seg[tn];
+    x.end = seg[tn + 1];
+    x.hs = nx.node_shift[tn];
+    x.tqh = nx.tot_qh[tn];
+    x.tql = nx.tot_ql[tn];
+    const int64_t q0 = x.base / kPartBlock;
+    const int64_t qb = q0 < nb ? q0 : nb - 1;  // an empty node may start at n_pos
+    x.oqh = ps.own_qh[tn];
+    x.oql = ps.own_ql[tn];
+    x.on = ps.own_n[tn];
+    x.bqh = ps.bl_qh[qb];
+    x.bql = ps.bl_ql[qb];
+    x.bn = ps.bl_n[qb];
+    x.oml = x.omr = x.bml = x.bmr = 0u;
+    if (have_max) {
+      x.oml = ps.own_ml[tn];
+      x.omr = ps.own_mr[tn];
+      x.bml = ps.bl_ml[qb];
+      x.bmr = ps.bl_mr[qb];
+    }
+    return x;
+  };
+  NodeWords first{};
+  const bool in_lds = nb <= kScanLdsBlocks;
+  // the node's own words load while the block prefixes are scanned
+  block_scan_body(nb, ps, have_max, in_lds, ScanLds{l_qh, l_ql, l_n, l_ml, l_mr}, [&]() {
+    if (t < n_tn) first = load_node(t);
+  });
+  if (!in_lds) __syncthreads();  // the prefixes are read back from global memory
+  // the entries of this thread's node (when n_tn <= 1024): keys and bounds
+  int32_t ka = -1, kb = -1;
+  int64_t a0 = 0, a1 = 0, b1 = 0;
+  auto finish_node = [&](int tn, const NodeWords& x) {
+    const int64_t cnt = x.end - x.base;
+    const bool sp = x.pr && x.sl >= 0;
+    const int64_t xq0 = x.base / kPartBlock, xq1 = cnt > 0 ? (x.end - 1) / kPartBlock : xq0;
+    const bool inside = xq0 == xq1;
+    const bool use = sp && cnt > 0;
+    int64_t L = cnt, qh = 0, ql = 0;
+    uint32_t ml = use ? (inside ? x.oml : x.bml) : 0u;
+    uint32_t mr = use ? (inside ? x.omr : x.bmr) : 0u;
+    if (sp) {
+      L = use ? (int64_t)(inside ? x.on : x.bn) : 0;
+      qh = use ? (inside ? x.oqh : x.bqh) : 0;
+      ql = use ? (inside ? x.oql : x.bql) : 0;
+      if (use && !inside) {
+        // the first blocks' partials of blocks q0 + 1 .. q1 (all start inside
+        // the node), and the maxima of the run of blocks ending at q1
+        const int q0 = (int)xq0, q1 = (int)xq1;
+        if (in_lds) {
+          L += (int64_t)(l_n[q1] - l_n[q0]);
+          qh += l_qh[q1] - l_qh[q0];
+          ql += l_ql[q1] - l_ql[q0];
+        } else {
+          L += ps.P_n[q1] - ps.P_n[q0];
+          qh += ps.P_qh[q1] - ps.P_qh[q0];
+          ql += ps.P_ql[q1] - ps.P_ql[q0];
+        }
+        if (have_max) {
+          const uint32_t rl = in_lds ? l_ml[q1] : ps.pm_l[q1];
+          const uint32_t rr = in_lds ? l_mr[q1] : ps.pm_r[q1];
+          ml = rl > ml ? rl : ml;
+          mr = rr > mr ? rr : mr;
+        }
+      }
+    }
+    const int64_t R = cnt - L;
+    const int side = L <= R ? 0 : 1;  // the smaller child gets the histogram
+    const int hs = x.hs;
+    const int hs_l = sp && have_max ? node_shift_rule(ml, hs, nx.qbits) : hs;
+    const int hs_r = sp && have_max ? node_shift_rule(mr, hs, nx.qbits) : hs;
+    const bool both = sp && (hs_l != hs || hs_r != hs);  // both children histogrammed
+    const int64_t c0 = 2 * (int64_t)tn;
+    const int64_t base = x.base;
+    nx.seg_next[c0] = base;
+    nx.seg_next[c0 + 1] = base + L;
+    // child totals (the words of children that do not exist are zero)
+    nx.tot_qh_next[c0] = sp ? qh : 0;
+    nx.tot_ql_next[c0] = sp ? ql : 0;
+    nx.tot_c_next[c0] = sp ? L : 0;
+    nx.tot_qh_next[c0 + 1] = sp ? x.tqh - qh : 0;
+    nx.tot_ql_next[c0 + 1] = sp ? x.tql - ql : 0;
+    nx.tot_c_next[c0 + 1] = sp ? R : 0;
+    ka = sp ? (int32_t)(c0 + (both ? 0 : side)) : -1;
+    kb = both ? (int32_t)(c0 + 1) : -1;
+    nx.key_list_next[c0] = ka;
+    nx.key_list_next[c0 + 1] = kb;
+    nx.present_next[c0] = sp;
+    nx.present_next[c0 + 1] = sp;
+    nx.node_shift_next[c0] = hs_l;
+    nx.node_shift_next[c0 + 1] = hs_r;
+    a0 = base;
+    a1 = base + L;
+    b1 = x.end;
+  };
+  if (t < n_tn) finish_node(t, first);
+  for (int tn = t + 1024; tn < n_tn; tn += 1024) finish_node(tn, load_node(tn));
+  if (t == 0) nx.seg_next[2 * (int64_t)n_tn] = n_pos;
+  if (!plan) return;  // uniform
+  if (n_tn > 1024) {
+    __syncthreads();
+    plan_tiles_body(nx.seg_next, 0, 2 * n_tn, nx.key_list_next, tile_rows, 0, max_tiles, tiles,
+                    key_tile_start, n_tiles);
+    return;
+  }
+  // tiles per entry (plan_tiles_body's count, rounding up); key c0 spans
+  // [a0, a1), key c0 + 1 spans [a1, b1)
+  auto count = [&](int32_t key) -> int {
+    if (key < 0) return 0;
+    const uint32_t len = (uint32_t)((key & 1) ? b1 - a1 : a1 - a0);
+    if (len == 0) return 0;
+    const uint32_t k = (len + (uint32_t)tile_rows - 1) / (uint32_t)tile_rows;
+    static_assert(WGBM_MAX_TILE_ROWS == 1 << 16, "tile row bound");
+    const uint32_t kmin = (len + WGBM_MAX_TILE_ROWS - 1) >> 16;
+    return (int)(k > kmin ? k : kmin);
+  };
+  __shared__ int64_t s_wsum[16];
+  __shared__ int s_nbig;
+  const bool live = t < n_tn;
+  const int na = live ? count(ka) : 0, nbt = live ? count(kb) : 0;
+  // exclusive scan of the node's tile counts (wave totals through LDS)
+  const int lane = t & 63, w = t >> 6;
+  const int64_t v = na + nbt;
+  const int64_t x = wgbm_wave_incl_scan_i64(v);
+  if (lane == 63) s_wsum[w] = x;
+  if (t == 0) s_nbig = 0;
+  wgbm_lds_barrier();
+  const int64_t sw = wgbm_row_incl_scan_i64(lane < 16 ? s_wsum[lane] : 0);
+  const int64_t total = wgbm_readlane_i64(sw, 15);
+  const int64_t pre = wgbm_readlane_i64(sw, w > 0 ? w - 1 : 0);
+  const int64_t ex = (w > 0 ? pre : 0) + x - v;
+  const int ntot = total < max_tiles ? (int)total : max_tiles;
+  if (live) {
+    key_tile_start[2 * t] = (int32_t)ex;
+    key_tile_start[2 * t + 1] = (int32_t)(ex + na);
+  }
+  if (t == 0) {
+    key_tile_start[2 * n_tn] = (int32_t)total;
+    *n_tiles = ntot;
+  }
+  // entries with many tiles are written by the whole workgroup afterwards
+  constexpr int kMaxBig = 256, kSmall = 8;
+  __shared__ int64_t s_b0[kMaxBig];
+  __shared__ int s_bkey[kMaxBig], s_blen[kMaxBig], s_bfirst[kMaxBig], s_bnt[kMaxBig];
+  for (int s2 = 0; s2 < 2 && live; ++s2) {
+    const int32_t key = s2 ? kb : ka;
+    const int nt = s2 ? nbt : na;
+    if (nt == 0) continue;
+    const int64_t e0 = (key & 1) ? a1 : a0, e1 = (key & 1) ? b1 : a1;
+    const int first = (int)ex + (s2 ? na : 0);
+    if (nt > kSmall) {
+      const int slot = atomicAdd(&s_nbig, 1);
+      if (slot < kMaxBig) {
+        s_b0[slot] = e0;
+        s_bkey[slot] = key;
+        s_blen[slot] = (int)(e1 - e0);
+        s_bfirst[slot] = first;
+        s_bnt[slot] = nt;
+        continue;
+      }
+    }
+    write_entry_tiles(key, e0, (uint32_t)(e1 - e0), first, nt, 0, 1, ntot, tiles);
+  }
+  wgbm_lds_barrier();  // the large entries are listed in LDS
+  const int nbig = s_nbig < kMaxBig ? s_nbig : kMaxBig;
+  for (int k = 0; k < nbig; ++k)
+    write_entry_tiles(s_bkey[k], s_b0[k], (uint32_t)s_blen[k], s_bfirst[k], s_bnt[k], t, 1024,
+                      ntot, tiles);
 }
 
 __global__ void chunk_keys_kernel(const int32_t* __restrict__ present, int32_t E, int32_t n,
