@@ -324,7 +324,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   uint32_t* s_ml = (uint32_t*)(s_dyn + 2 * kPartBlock);
   uint32_t* s_mr = s_ml + kPartBlock;
   __shared__ int s_wlast[kPartThreads / 64];  // key of each wave's last position
-  __shared__ int s_khi;                        // key of the block's last position
+  __shared__ int64_t s_sl, s_sn;  // start of the block's last segment, and of its node
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
@@ -381,11 +381,8 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
       }
     }
     if (lane == 63) s_wlast[tid >> 6] = key[PJ - 1];
-#pragma unroll
-    for (int j = 0; j < PJ; ++j)
-      if (pb + j == p1 - 1) s_khi = key[j];
   }
-  __syncthreads();
+  wgbm_lds_barrier();  // the LDS words are cleared (the loads stay in flight)
   // Everything a position needs of its segment and node, in one round of
   // independent loads: the segment's bounds, the node's bounds (several
   // eras) and its route record.  col: -2 the row stays (node absent), -1
@@ -405,6 +402,11 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     }
     nslot[j] = (int)((nb > p0 ? nb : p0) - p0);
     node_in[j] = nb >= p0 && ne <= p1;
+    if (sums && pb + j == p1 - 1) {
+      // the block's last position: where its segment and node start
+      s_sl = sk;
+      s_sn = nb;  // (the segment itself unless maxes with several eras)
+    }
     if (a.mode != 0) nr[j] = a.nroute[tnv[j]];
     lv[j] = (ok[j] && a.mode != 0) ? nr[j].col : -2;
   }
@@ -544,7 +546,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     }
   }
   if (!sums) return;  // uniform over the block
-  __syncthreads();
+  wgbm_lds_barrier();  // the block's sums are in LDS (the stores above need not land)
   // decode a slot's packed word: rows in the low 11 bits, the hi sum above
   auto unpack = [](int64_t qn, int64_t& qh, int32_t& n) {
     n = (int32_t)(qn & 2047);
@@ -581,8 +583,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   }
   if (tid == 0) {
     // the first and last segments of the block: their sums here
-    const int khi = s_khi;
-    const int64_t sl = a.seg[khi];
+    const int64_t sl = s_sl;
     const int ls = (int)((sl > p0 ? sl : p0) - p0);
     int64_t qh;
     int32_t n;
@@ -597,7 +598,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     if (maxes) {
       // the first and last nodes of the block: their maxima here
       a.ps.bf_node[blockIdx.x] = key[0] / a.E;  // thread 0 holds the block's first position
-      const int64_t sn = a.seg[(int64_t)(khi / a.E) * a.E];
+      const int64_t sn = s_sn;
       const int lns = (int)((sn > p0 ? sn : p0) - p0);
       a.ps.bf_ml[blockIdx.x] = s_ml[0];
       a.ps.bf_mr[blockIdx.x] = s_mr[0];
@@ -613,7 +614,7 @@ constexpr int kScanLdsBlocks = 2048;
 struct ScanLds {
   int64_t* qh;
   int64_t* ql;
-  int32_t* n;
+  int64_t* n;
   uint32_t* ml;
   uint32_t* mr;
 };
@@ -707,7 +708,7 @@ __device__ inline void block_scan_body(int32_t nb, const PartSums& ps, bool seg_
       if (to_lds) {
         lds.qh[b] = qh;
         lds.ql[b] = ql;
-        lds.n[b] = (int32_t)n;
+        lds.n[b] = n;
       }
     }
     ch += wgbm_readlane_i64(gh, 15);
@@ -798,7 +799,7 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
       s_a[wave] = a;
       s_b[wave] = b;
     }
-    __syncthreads();
+    wgbm_lds_barrier();
     ga = 0;
     gb = 0;
     for (int w = grp * wpn; w < (grp + 1) * wpn; ++w) {
@@ -810,7 +811,7 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
         gb += s_b[w];
       }
     }
-    __syncthreads();
+    wgbm_lds_barrier();
   };
   int64_t ltot = 0, tot = 0;
   if (live) {
@@ -855,7 +856,7 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
       s_a[wave] = il;
       s_b[wave] = ir;
     }
-    __syncthreads();
+    wgbm_lds_barrier();
     int64_t pl = 0, pr = 0, cl = 0, cr = 0;
     for (int w = grp * wpn; w < (grp + 1) * wpn; ++w) {
       if (w < wave) {
@@ -865,7 +866,7 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
       cl += s_a[w];
       cr += s_b[w];
     }
-    __syncthreads();
+    wgbm_lds_barrier();
     il += pl;
     ir += pr;
     if (live && e < E) {
@@ -907,15 +908,37 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
   uint8_t d[PJ];
   int32_t rowv[PJ], key[PJ], rank[PJ];
   float rr[PJ];
+  bool ok[PJ];
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
     const int64_t p = p0 + j * kPartThreads + tid;
-    const bool ok = p < n_pos;
-    d[j] = ok ? dirbit[p] : 2;
-    rowv[j] = ok ? order[p] : 0;
-    key[j] = ok ? keyp[p] : 0;
-    rr[j] = ok ? rpos[p] : 0.0f;
+    ok[j] = p < n_pos;
+    d[j] = ok[j] ? dirbit[p] : 2;
+    rowv[j] = ok[j] ? order[p] : 0;
+    key[j] = ok[j] ? keyp[p] : 0;
+    rr[j] = ok[j] ? rpos[p] : 0.0f;
   }
+  // Every global word the positions need is loaded here, ahead of the LDS
+  // rank work: the segment bounds and child starts of each position's key,
+  // and the left rows of the block's first segment in earlier blocks.
+  // Kept in 32 bits relative to the block and the segment: a segment and
+  // the node around it hold fewer than 2^31 positions.
+  const int kf = keyp[p0];
+  int32_t sk[PJ], nd[PJ];  // segment start - p0; row's child segment start - segment start
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const int k = key[j];
+    const int tn = k / E;
+    const int64_t kl = (int64_t)2 * tn * E + (k - (int64_t)tn * E);  // left child's key
+    const int64_t s_k = seg[k];
+    sk[j] = (int32_t)(s_k - p0);
+    nd[j] = (int32_t)(seg_next[d[j] == 1 ? kl + E : kl] - s_k);
+  }
+  const int64_t sf = seg[kf];
+  const int64_t b0 = (sf < p0 ? sf : p0) / kPartBlock;
+  const int64_t bl0 = ps.bl_n[b0];
+  const int64_t pb0 = ps.P_n[b0];
+  const int64_t pprev = blockIdx.x > 0 ? ps.P_n[blockIdx.x - 1] : 0;
   // left rows before each position: rank among the wave's lefts plus the
   // lefts of the (phase, wave) groups before it (position order is phase,
   // then wave, then lane)
@@ -926,7 +949,7 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
     if (lane == 0) s_c[j * NW + w] = __builtin_popcountll(m);
   }
-  __syncthreads();
+  wgbm_lds_barrier();
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
     int pre = 0;
@@ -934,18 +957,13 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
     rank[j] += pre;
     s_pl[j * kPartThreads + tid] = rank[j];
   }
-  __syncthreads();
+  wgbm_lds_barrier();
   // left rows of the block's first segment in earlier blocks
-  const int64_t sf = seg[keyp[p0]];
-  int64_t cin = 0;
-  if (sf < p0) {
-    const int64_t b0 = sf / kPartBlock;
-    cin = ps.bl_n[b0] + ps.P_n[blockIdx.x - 1] - ps.P_n[b0];
-  }
+  const int64_t cin = sf < p0 ? bl0 + pprev - pb0 : 0;
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
     const int64_t p = p0 + j * kPartThreads + tid;
-    if (p >= n_pos) break;
+    if (!ok[j]) break;
     const int k = key[j];
     const int tn = k / E;
     const int64_t kl = (int64_t)2 * tn * E + (k - (int64_t)tn * E);  // left child's key
@@ -956,10 +974,11 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
       rpos_next[p] = rr[j];
       continue;
     }
-    const int64_t sk = seg[k];
-    const int64_t s0 = sk > p0 ? sk : p0;
-    const int64_t rl = (int64_t)rank[j] - s_pl[s0 - p0] + (sk < p0 ? cin : 0);
-    const int64_t dst = d[j] == 0 ? seg_next[kl] + rl : seg_next[kl + E] + ((p - sk) - rl);
+    const int64_t skj = p0 + sk[j];
+    const int s0 = sk[j] > 0 ? sk[j] : 0;  // the segment's first position in the block
+    const int64_t rl = (int64_t)rank[j] - s_pl[s0] + (sk[j] < 0 ? cin : 0);
+    const int64_t cs = skj + nd[j];
+    const int64_t dst = d[j] == 0 ? cs + rl : cs + ((p - skj) - rl);
     order_next[dst] = rowv[j];
     keyp_next[dst] = (int32_t)(d[j] == 0 ? kl : kl + E);
     rpos_next[dst] = rr[j];
@@ -1063,7 +1082,7 @@ __global__ __launch_bounds__(1024) void level_scan_e1_kernel(
     int32_t plan, int32_t tile_rows, int32_t max_tiles, Tile* __restrict__ tiles,
     int32_t* __restrict__ key_tile_start, int32_t* __restrict__ n_tiles) {
   __shared__ int64_t l_qh[kScanLdsBlocks], l_ql[kScanLdsBlocks];
-  __shared__ int32_t l_n[kScanLdsBlocks];
+  __shared__ int64_t l_n[kScanLdsBlocks];
   __shared__ uint32_t l_ml[kScanLdsBlocks], l_mr[kScanLdsBlocks];
   const int t = threadIdx.x;
   const bool have_max = nx.have_max != 0;
@@ -1134,7 +1153,7 @@ __global__ __launch_bounds__(1024) void level_scan_e1_kernel(
         // the node), and the maxima of the run of blocks ending at q1
         const int q0 = (int)xq0, q1 = (int)xq1;
         if (in_lds) {
-          L += (int64_t)(l_n[q1] - l_n[q0]);
+          L += l_n[q1] - l_n[q0];
           qh += l_qh[q1] - l_qh[q0];
           ql += l_ql[q1] - l_ql[q0];
         } else {
