@@ -234,7 +234,9 @@ def main():
         return e0.elapsed_time(e1) / args.steps
 
     # the timed region: every hist_tiles dispatch carries a HIP event pair
+    mark("c2 timed")
     ms_step = run_steps(True)
+    mark("c2 plain")
     tot = C.c_double()
     cnt = C.c_int64()
     lib.wgbm_timer_read(b"hist_tiles", C.byref(tot), C.byref(cnt))
@@ -242,6 +244,7 @@ def main():
     assert cnt.value == 2 * args.steps, (cnt.value, args.steps)
     # the same steps with no events attached (their dispatch overhead)
     ms_step_plain = run_steps(False)
+    mark("c2 end")
     bytes_root = N * F + 4 * N + 1 * F * B * 8
     bytes_16 = N * F + 4 * N + 4 * N + 16 * F * B * 8
     gbs = (bytes_root + bytes_16) / (ms_step * 1e-3) / 1e9
@@ -276,22 +279,36 @@ def main():
         n = args.e2e_rows
         log(f"generating C3 inputs {n}x{F}")
         X, y = c3_inputs(n, F, 0)
-        m = WarpGBM(num_bins=32, max_depth=5, n_estimators=args.e2e_trees, learning_rate=0.01)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        m.fit(X, y)
-        torch.cuda.synchronize()
-        train_s = time.perf_counter() - t0
-        del X, y
         Xt, yt = c3_inputs(n, F, 1)
-        t0 = time.perf_counter()
-        p = m.predict(Xt)
-        torch.cuda.synchronize()
-        infer_s = time.perf_counter() - t0
+        # two identical fits / predicts: the first in this process pays the
+        # one-time costs (first large staged upload, first launch of each
+        # kernel), the second is the steady state reported as train_s / infer_s
+        runs = []
+        for run in range(2):
+            m = WarpGBM(num_bins=32, max_depth=5, n_estimators=args.e2e_trees,
+                        learning_rate=0.01)
+            torch.cuda.synchronize()
+            mark(f"c3 fit {run}")
+            t0 = time.perf_counter()
+            m.fit(X, y)
+            torch.cuda.synchronize()
+            tr = time.perf_counter() - t0
+            mark(f"c3 predict {run}")
+            t0 = time.perf_counter()
+            p = m.predict(Xt)
+            torch.cuda.synchronize()
+            runs.append((tr, time.perf_counter() - t0, p))
+            mark(f"c3 end {run}")
+        del X, y
+        (train_cold, infer_cold, _), (train_s, infer_s, p) = runs
         corr = float(np.corrcoef(p, yt)[0, 1])
         e2e = {"train_s": round(train_s, 3), "infer_s": round(infer_s, 3),
-               "heldout_corr": round(corr, 4), "e2e_workload": f"C3 {n}x{F}, {args.e2e_trees} trees"}
-        log(f"C3 train {train_s:.3f} s, infer {infer_s:.3f} s, corr {corr:.4f}")
+               "train_cold_s": round(train_cold, 3), "infer_cold_s": round(infer_cold, 3),
+               "heldout_corr": round(corr, 4), "e2e_workload": f"C3 {n}x{F}, {args.e2e_trees} trees",
+               "e2e_timing": "second of two identical fit + predict runs in this process "
+                             "(the first, *_cold_s, includes one-time setup)"}
+        log(f"C3 train {train_s:.3f} s (first run {train_cold:.3f}), infer {infer_s:.3f} s "
+            f"(first run {infer_cold:.3f}), corr {corr:.4f}")
         e2e["kernels"] = c3_kernel_rooflines(m, Xt)
         del Xt
 
@@ -341,11 +358,28 @@ def main():
     if not args.no_extra:
         for cfg in ("c1", "c4", "c5"):
             out.update(run_extra(cfg))
+    write_marks()
     print(json.dumps(out))
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# Phase marks on CLOCK_MONOTONIC (the clock of rocprofv3's kernel
+# timestamps), written to $WGBM_BENCH_MARKS as JSON when that is set, so a
+# kernel trace of this run can be split into its legs.
+_MARKS: list = []
+
+
+def mark(label):
+    _MARKS.append((label, time.clock_gettime_ns(time.CLOCK_MONOTONIC)))
+
+
+def write_marks():
+    path = os.environ.get("WGBM_BENCH_MARKS")
+    if path:
+        Path(path).write_text(json.dumps(_MARKS))
 
 
 def dropin_leg(raw, grad, order16, seg16_h, N, F, B, dev):
@@ -535,35 +569,53 @@ def run_extra(cfg):
     if cfg == "c4":
         print("[bench] generating C4 inputs", file=sys.stderr, flush=True)
         X, y, era = c4_inputs()
-        m = WarpGBM(num_bins=5, max_depth=8, n_estimators=100, learning_rate=0.1)
-        t0 = time.perf_counter()
-        m.fit(X, y, era_id=era)
-        torch.cuda.synchronize()
-        tr = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        p = m.predict(X)
-        inf = time.perf_counter() - t0
+        runs = []
+        for run in range(2):  # the second run is the steady state (see the C3 leg)
+            m = WarpGBM(num_bins=5, max_depth=8, n_estimators=100, learning_rate=0.1)
+            torch.cuda.synchronize()
+            mark(f"c4 fit {run}")
+            t0 = time.perf_counter()
+            m.fit(X, y, era_id=era)
+            torch.cuda.synchronize()
+            tr = time.perf_counter() - t0
+            mark(f"c4 predict {run}")
+            t0 = time.perf_counter()
+            p = m.predict(X)
+            runs.append((tr, time.perf_counter() - t0, p))
+            mark(f"c4 end {run}")
+        (tr0, inf0, _), (tr, inf, p) = runs
         corr = float(np.corrcoef(p, y)[0, 1])
-        print(f"[bench] C4 train {tr:.2f} s, infer {inf:.2f} s, in-sample corr {corr:.4f}",
-              file=sys.stderr, flush=True)
-        return {"c4_train_s": round(tr, 3), "c4_infer_s": round(inf, 3), "c4_corr": round(corr, 4)}
+        print(f"[bench] C4 train {tr:.3f} s (first run {tr0:.3f}), infer {inf:.3f} s "
+              f"(first run {inf0:.3f}), in-sample corr {corr:.4f}", file=sys.stderr, flush=True)
+        return {"c4_train_s": round(tr, 3), "c4_infer_s": round(inf, 3),
+                "c4_train_cold_s": round(tr0, 3), "c4_infer_cold_s": round(inf0, 3),
+                "c4_corr": round(corr, 4)}
     if cfg == "c5":
         print("[bench] generating C5 inputs", file=sys.stderr, flush=True)
         X, lab = c5_inputs()
         Xt, labt = c5_inputs(rows_per_class=100_000, seed=1)
-        m = WarpGBM(objective="multiclass", num_bins=32, max_depth=6, n_estimators=200,
-                    learning_rate=0.1)
-        t0 = time.perf_counter()
-        m.fit(X, lab)
-        torch.cuda.synchronize()
-        tr = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        proba = m.predict_proba(Xt)
-        inf = time.perf_counter() - t0
+        runs = []
+        for run in range(2):  # the second run is the steady state (see the C3 leg)
+            m = WarpGBM(objective="multiclass", num_bins=32, max_depth=6, n_estimators=200,
+                        learning_rate=0.1)
+            torch.cuda.synchronize()
+            mark(f"c5 fit {run}")
+            t0 = time.perf_counter()
+            m.fit(X, lab)
+            torch.cuda.synchronize()
+            tr = time.perf_counter() - t0
+            mark(f"c5 predict {run}")
+            t0 = time.perf_counter()
+            proba = m.predict_proba(Xt)
+            runs.append((tr, time.perf_counter() - t0, proba))
+            mark(f"c5 end {run}")
+        (tr0, inf0, _), (tr, inf, proba) = runs
         acc = float((np.argmax(proba, axis=1) == labt).mean())
-        print(f"[bench] C5 train {tr:.2f} s, predict_proba {inf:.2f} s, acc {acc:.4f}",
-              file=sys.stderr, flush=True)
-        return {"c5_train_s": round(tr, 3), "c5_infer_s": round(inf, 3), "c5_acc": round(acc, 4)}
+        print(f"[bench] C5 train {tr:.3f} s (first run {tr0:.3f}), predict_proba {inf:.3f} s "
+              f"(first run {inf0:.3f}), acc {acc:.4f}", file=sys.stderr, flush=True)
+        return {"c5_train_s": round(tr, 3), "c5_infer_s": round(inf, 3),
+                "c5_train_cold_s": round(tr0, 3), "c5_infer_cold_s": round(inf0, 3),
+                "c5_acc": round(acc, 4)}
     raise SystemExit(f"unknown extra config {cfg}")
 
 

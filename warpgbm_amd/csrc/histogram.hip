@@ -480,7 +480,7 @@ __device__ inline void finalize_sum(const unsigned long long* __restrict__ part,
   }
   sq[g][w] = q;
   sc[g][w] = c;
-  __syncthreads();
+  wgbm_lds_barrier();
   Q = 0;
   C = 0;
   for (int k = 0; k < SPLIT; ++k) {
@@ -549,6 +549,8 @@ constexpr int kPlaneGroups = 4;
 constexpr int kPlaneMaxBins = 64;  // words per thread: B*64/256 <= 16
 constexpr int kPlaneRow = 65;
 
+// MB: the largest num_bins of the instance (register arrays are sized by it)
+template <int MB = kPlaneMaxBins>
 __device__ inline void plane_sum(const unsigned long long* __restrict__ part, int64_t tile_words,
                                  int plane_off, int num_bins, int t0, int t1,
                                  unsigned long long* sq, unsigned int* sc) {
@@ -557,10 +559,10 @@ __device__ inline void plane_sum(const unsigned long long* __restrict__ part, in
     sq[i] = 0ull;
     sc[i] = 0u;
   }
-  __syncthreads();
+  wgbm_lds_barrier();
   const int g = threadIdx.x / (kPlaneThreads / kPlaneGroups);
   const int lt = threadIdx.x % (kPlaneThreads / kPlaneGroups);
-  constexpr int kMaxW = kPlaneMaxBins * kHistSlots / (kPlaneThreads / kPlaneGroups);
+  constexpr int kMaxW = MB * kHistSlots / (kPlaneThreads / kPlaneGroups);
   int64_t q[kMaxW];
   int64_t c[kMaxW];
 #pragma unroll
@@ -590,7 +592,7 @@ __device__ inline void plane_sum(const unsigned long long* __restrict__ part, in
       atomicAdd(sc + li, (unsigned int)c[k]);
     }
   }
-  __syncthreads();
+  wgbm_lds_barrier();
 }
 
 // G[k, f, b] (+)= float(sum * 2^-s), H[k, f, b] (+)= count
@@ -640,6 +642,7 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_f32_kernel(
 // the engine's level arrays (exact int64 sums, int32 counts) and the sibling
 // as parent - computed child; key layout and list pairs as
 // hist_finalize_level_kernel
+template <int MB>
 __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_level_kernel(
     const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
     const int32_t* __restrict__ key_list, int32_t n_list, int32_t n_chunks, int32_t V,
@@ -652,18 +655,19 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_level_kerne
   const int kk = (int)blockIdx.x / P;
   const int plane = (int)blockIdx.x - kk * P;
   if (kk >= n_list) return;  // uniform per workgroup
+  // the list words in one round of loads (the tile range does not depend on
+  // the key), the parent words of a derived sibling with the partials
   const int key = key_list ? key_list[kk] : kk;
+  const int pair = depth > 0 ? key_list[kk ^ 1] : 0;
+  const int ts0 = key_tile_start[kk], ts1 = key_tile_start[kk + 1], ntl = *n_tiles;
   if (key < 0) return;  // uniform per workgroup
   const int chunk = plane / V, j = plane - (plane / V) * V;
   const int64_t tile_words = (int64_t)n_chunks * kHistSlots * V * num_bins;
-  const int t0 = key_tile_start[kk];
-  const int t1 = key_tile_start[kk + 1] < *n_tiles ? key_tile_start[kk + 1] : *n_tiles;
-  plane_sum(part, tile_words, plane * num_bins * kHistSlots, num_bins, t0, t1, sq, sc);
   const int64_t per_key = (int64_t)n_feats * num_bins;
   int64_t pkey = 0, skey = 0;
   // the sibling by subtraction unless it is histogrammed itself (the second
   // entry of the list pair)
-  const bool derive = depth > 0 && key_list[kk ^ 1] < 0;
+  const bool derive = depth > 0 && pair < 0;
   if (derive) {
     const int era = key % num_eras;
     const int tn = key / num_eras;
@@ -672,7 +676,33 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_level_kerne
     pkey = ((int64_t)tree * (nodes_in_level >> 1) + (node >> 1)) * num_eras + era;
     skey = ((int64_t)tree * nodes_in_level + (node ^ 1)) * num_eras + era;
   }
-  for (int o = threadIdx.x; o < kHistSlots * num_bins; o += kPlaneThreads) {
+  // this thread's outputs (o = threadIdx.x + m * kPlaneThreads) and their
+  // parent words, loaded with the partials (up to 32 bins; beyond, the
+  // registers go to the partial sums and the parents load afterwards)
+  constexpr int kOut = MB * kHistSlots / kPlaneThreads;
+  constexpr bool kPre = MB <= 32;
+  int64_t pq[kOut];
+  int32_t pc[kOut];
+#pragma unroll
+  for (int m = 0; m < kOut; ++m) {
+    const int o = threadIdx.x + m * kPlaneThreads;
+    const int lane = o / num_bins, b = o - lane * num_bins;
+    const int f = chunk * kHistSlots * V + lane * V + j;
+    pq[m] = 0;
+    pc[m] = 0;
+    if (kPre && derive && o < kHistSlots * num_bins && f < n_feats) {
+      const int64_t fb = (int64_t)f * num_bins + b;
+      pq[m] = parent_q[pkey * per_key + fb];
+      pc[m] = parent_c[pkey * per_key + fb];
+    }
+  }
+  const int t0 = ts0;
+  const int t1 = ts1 < ntl ? ts1 : ntl;
+  plane_sum<MB>(part, tile_words, plane * num_bins * kHistSlots, num_bins, t0, t1, sq, sc);
+#pragma unroll
+  for (int m = 0; m < kOut; ++m) {
+    const int o = threadIdx.x + m * kPlaneThreads;
+    if (o >= kHistSlots * num_bins) break;
     const int lane = o / num_bins, b = o - lane * num_bins;
     const int f = chunk * kHistSlots * V + lane * V + j;
     if (f >= n_feats) continue;
@@ -683,8 +713,10 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_level_kerne
     hq[(int64_t)key * per_key + fb] = Q;
     hc[(int64_t)key * per_key + fb] = C;
     if (derive) {
-      hq[skey * per_key + fb] = parent_q[pkey * per_key + fb] - Q;
-      hc[skey * per_key + fb] = parent_c[pkey * per_key + fb] - C;
+      const int64_t pqm = kPre ? pq[m] : parent_q[pkey * per_key + fb];
+      const int32_t pcm = kPre ? pc[m] : parent_c[pkey * per_key + fb];
+      hq[skey * per_key + fb] = pqm - Q;
+      hc[skey * per_key + fb] = pcm - C;
     }
   }
 }
@@ -710,34 +742,44 @@ __global__ __launch_bounds__(256) void hist_finalize_level_kernel(
   const int wpk = (tile_words + FW - 1) / FW;
   const int kk = (int)blockIdx.x / wpk;
   if (kk >= n_list) return;  // uniform per workgroup
+  // the list words in one round of loads (the tile range does not depend on
+  // the key), the parent words of a derived sibling with the partials
   const int key = key_list ? key_list[kk] : kk;
+  const int pair = depth > 0 ? key_list[kk ^ 1] : 0;
+  const int ts0 = key_tile_start[kk], ts1 = key_tile_start[kk + 1], ntl = *n_tiles;
   if (key < 0) return;  // uniform per workgroup
   const int i = ((int)blockIdx.x - kk * wpk) * FW + (int)threadIdx.x % FW;
   const bool ok = i < tile_words;
-  const int t0 = key_tile_start[kk];
-  const int t1 = key_tile_start[kk + 1] < *n_tiles ? key_tile_start[kk + 1] : *n_tiles;
-  int64_t Q, C;
-  finalize_sum<FW>(part, tile_words, i, ok, t0, t1, Q, C);
-  if (!ok || threadIdx.x >= FW) return;
-  int f, b;
-  part_feature_bin(i, V, num_bins, f, b);
-  if (f >= n_feats) return;
+  int f = 0, b = 0;
+  if (ok) part_feature_bin(i, V, num_bins, f, b);
   const int64_t per_key = (int64_t)n_feats * num_bins;
   const int64_t fb = (int64_t)f * num_bins + b;
-  hq[(int64_t)key * per_key + fb] = Q;
-  hc[(int64_t)key * per_key + fb] = (int32_t)C;
-  if (depth > 0 && key_list[kk ^ 1] < 0) {
+  // the sibling by subtraction unless it is histogrammed itself
+  const bool derive = depth > 0 && pair < 0;
+  int64_t skey = 0, pq = 0;
+  int32_t pc = 0;
+  if (derive && ok && threadIdx.x < FW && f < n_feats) {
     // key = ((tree*nodes + node)*E + era)
     const int era = key % num_eras;
     const int tn = key / num_eras;
     const int node = tn % nodes_in_level;
     const int tree = tn / nodes_in_level;
-    const int sib = node ^ 1;
-    const int parent = node >> 1;
-    const int64_t pkey = ((int64_t)tree * (nodes_in_level >> 1) + parent) * num_eras + era;
-    const int64_t skey = ((int64_t)tree * nodes_in_level + sib) * num_eras + era;
-    hq[skey * per_key + fb] = parent_q[pkey * per_key + fb] - Q;
-    hc[skey * per_key + fb] = parent_c[pkey * per_key + fb] - (int32_t)C;
+    const int64_t pkey = ((int64_t)tree * (nodes_in_level >> 1) + (node >> 1)) * num_eras + era;
+    skey = ((int64_t)tree * nodes_in_level + (node ^ 1)) * num_eras + era;
+    pq = parent_q[pkey * per_key + fb];
+    pc = parent_c[pkey * per_key + fb];
+  }
+  const int t0 = ts0;
+  const int t1 = ts1 < ntl ? ts1 : ntl;
+  int64_t Q, C;
+  finalize_sum<FW>(part, tile_words, i, ok, t0, t1, Q, C);
+  if (!ok || threadIdx.x >= FW) return;
+  if (f >= n_feats) return;
+  hq[(int64_t)key * per_key + fb] = Q;
+  hc[(int64_t)key * per_key + fb] = (int32_t)C;
+  if (derive) {
+    hq[skey * per_key + fb] = pq - Q;
+    hc[skey * per_key + fb] = pc - (int32_t)C;
   }
 }
 
@@ -1098,10 +1140,16 @@ int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
   if (use_plane_finalize(tiles_per_key, n_list, n_chunks, V, num_bins)) {
     const int64_t wg = (int64_t)n_list * n_chunks * V;
     WGBM_REQUIRE(wg < ((int64_t)1 << 31), "finalize: too many segments");
-    hipLaunchKernelGGL(hist_finalize_plane_level_kernel, dim3((unsigned)wg), dim3(kPlaneThreads),
-                       0, st, part, key_tile_start, key_list, n_list, n_chunks, V, num_bins,
-                       n_feats, num_eras, nodes_in_level, depth, parent_q, parent_c, n_tiles, hq,
-                       hc);
+    if (num_bins <= 32)
+      hipLaunchKernelGGL(hist_finalize_plane_level_kernel<32>, dim3((unsigned)wg),
+                         dim3(kPlaneThreads), 0, st, part, key_tile_start, key_list, n_list,
+                         n_chunks, V, num_bins, n_feats, num_eras, nodes_in_level, depth,
+                         parent_q, parent_c, n_tiles, hq, hc);
+    else
+      hipLaunchKernelGGL(hist_finalize_plane_level_kernel<kPlaneMaxBins>, dim3((unsigned)wg),
+                         dim3(kPlaneThreads), 0, st, part, key_tile_start, key_list, n_list,
+                         n_chunks, V, num_bins, n_feats, num_eras, nodes_in_level, depth,
+                         parent_q, parent_c, n_tiles, hq, hc);
     WGBM_LAUNCH_CHECK();
     return 0;
   }
