@@ -248,8 +248,9 @@ int wgbm_engine_round(wgbm_engine* eng, const void* target, float* pred, const i
  * read by the era path when num_bins <= 7 (0 = the int8 codes, 1 = a
  * pair-code copy, one byte per feature pair; default 1); key 3 = the
  * per-level node scan of one-era fits (1 = a thread per node, default; 0 = a
- * wave per node).  Set before the first round; every setting grows the same
- * trees. */
+ * wave per node); key 4 = one-era split search and leaf / record step (1 =
+ * one fused launch, default; 0 = two launches).  Set before the first round;
+ * every setting grows the same trees. */
 int wgbm_engine_set_tuning(wgbm_engine* eng, int32_t key, int64_t value);
 void wgbm_engine_destroy(wgbm_engine* eng);
 

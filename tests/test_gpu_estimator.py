@@ -461,15 +461,18 @@ def test_depth_beyond_twenty_bit_exact(gpu):
     assert max(_depth(t) for t in m.forest) > 12
 
 
-@pytest.mark.parametrize("scan", [1, 0])
-def test_one_era_level_scans_bit_exact(gpu, scan):
-    """The two per-level node scans of one-era fits (engine tuning key 3: a
-    thread per node, or a wave per node) grow the oracle's trees.  Heavy
-    tails on 60000 rows: nodes spanning many partition blocks whose child
-    maxima move their histogram shift (both children histogrammed); depth 12
-    (2048 nodes at the last split level, past the 1024 planned from
-    registers); softmax with 5 class trees and 640 nodes at depth 7."""
-    print_case("estimator", "one-era level scan", scan)
+@pytest.mark.parametrize("scan,fuse", [(1, 1), (0, 0), (1, 0)])
+def test_one_era_level_scans_bit_exact(gpu, scan, fuse):
+    """The per-level kernels of one-era fits in each setting (engine tuning
+    key 3: node scan with a thread or a wave per node; key 4: split search
+    and leaf step fused or not) grow the oracle's trees.  Heavy tails on
+    60000 rows: nodes spanning many partition blocks whose child maxima move
+    their histogram shift (both children histogrammed); depth 12 (2048 nodes
+    at the last split level, past the 1024 planned from registers); softmax
+    with 5 class trees and 640 nodes at depth 7; 300 features (two split
+    workgroups per node, the fused step's last-arrival path)."""
+    print_case("estimator", "one-era level scan, fused finish", scan, fuse)
+    tuning = {3: scan, 4: fuse}
     rng = np.random.default_rng(12)
     N = 60_000
     X = rng.standard_normal((N, 5)).astype(F32)
@@ -477,7 +480,7 @@ def test_one_era_level_scans_bit_exact(gpu, scan):
     y[2:200] *= 1e4  # a band of mid-sized residuals
     kw = dict(num_bins=8, max_depth=12, n_estimators=2, learning_rate=0.3, min_child_weight=1)
     m = WarpGBM(**kw)
-    m._engine_tuning = {3: scan}
+    m._engine_tuning = tuning
     m.fit(X, y)
     codes = oracle_codes(m, X)
     ref = gbm.Forest(**kw).fit_codes(codes, y)
@@ -492,10 +495,23 @@ def test_one_era_level_scans_bit_exact(gpu, scan):
     kw = dict(objective="multiclass", num_bins=16, max_depth=8, n_estimators=2,
               learning_rate=0.3, min_child_weight=2)
     m = WarpGBM(**kw)
-    m._engine_tuning = {3: scan}
+    m._engine_tuning = tuning
     m.fit(X, labels)
     codes = oracle_codes(m, X)
     ref = gbm.Forest(**kw).fit_codes(codes, labels)
     for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
         assert a == b, f"round {i} differs"
     assert np.array_equal(bits(m.predict_proba(X)), bits(ref.predict_codes(codes)))
+    # 300 features: n_sel > 256, several split workgroups per node
+    N, F = 20_000, 300
+    X = rng.standard_normal((N, F)).astype(F32)
+    y = (X[:, 7] + 0.5 * (X[:, 280] > 0) + 0.3 * rng.standard_normal(N)).astype(F32)
+    kw = dict(num_bins=16, max_depth=5, n_estimators=3, learning_rate=0.3, min_child_weight=5)
+    m = WarpGBM(**kw)
+    m._engine_tuning = tuning
+    m.fit(X, y)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, y)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"300-feature tree {i} differs"
+    assert "'feature': 280" in str(m.forest[0]) or "'feature': 7" in str(m.forest[0])

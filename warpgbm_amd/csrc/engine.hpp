@@ -216,6 +216,33 @@ int launch_split_level_e1(int n_tn, hipStream_t st, const int64_t* hq, const int
                           int32_t nodes_in_level, const int32_t* present,
                           const int32_t* node_shift, float mcw, float eps, float min_split_gain,
                           unsigned long long* best);
+// What the leaf / record step of a one-era level needs besides the pick
+// (level-wide arrays, indexed by the node's index in the level).
+struct FinishE1 {
+  int32_t depth, max_depth, T, B;
+  const int32_t* present;
+  int32_t* split_l;
+  int32_t* split_b;
+  const int32_t* feat_sel;
+  const int64_t* tot_qh;
+  const int64_t* tot_ql;
+  const int64_t* tot_c;
+  const int32_t* shifts;
+  int32_t s63_add;
+  float* leaf_val;
+  TreeRecord rec;
+  unsigned long long* best_next;
+  NodeRoute* nroute;
+};
+// split_level_e1_kernel fused with the level's leaf / record step (one era):
+// nodes c0 .. c0 + n_tn - 1 of the level; hq / hc hold the chunk's nodes from
+// 0.  A node searched by several workgroups is finished by the last of them
+// (done: per-node arrival counters, zero between launches).
+int launch_split_finish_e1(int n_tn, int32_t c0, hipStream_t st, const int64_t* hq,
+                           const int32_t* hc, int32_t F, int32_t n_sel,
+                           const int32_t* node_shift, float mcw, float eps,
+                           float min_split_gain, unsigned long long* best, uint32_t* done,
+                           const FinishE1& fa);
 __global__ void des_accumulate_kernel(const int64_t* hq, const int32_t* hc, int32_t F, int32_t B,
                                       int32_t E, const int32_t* feat_sel, int32_t n_sel,
                                       int32_t nodes_in_level, int32_t n_tn,

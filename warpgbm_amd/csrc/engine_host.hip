@@ -76,6 +76,10 @@ struct Engine {
   // one-era levels: 1 = level_scan_e1_kernel (a thread per node), 0 = the
   // wave-per-node kernels
   int lscan_e1 = 1;
+  // one-era levels: 1 = split search and leaf / record step fused
+  // (split_finish_e1_kernel), 0 = split_level_e1_kernel + level_finish_kernel
+  int fuse_finish = 1;
+  uint32_t* done = nullptr;  // [T * nodes_max] arrival counters (zero between launches)
   uint32_t* alive = nullptr;    // [tn][W] segments that can hold a split, W = ceil(E/32)
   double* bsum = nullptr;       // [tn][W][n_sel*(B-1)] era-block gain sums
   int32_t* bdir = nullptr;      // [tn][W][n_sel*(B-1)] era-block direction sums
@@ -270,6 +274,15 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->nroute, T * nodes_max);
   E_ALLOC(e->best, 2 * T * nodes_max);
   e->pick_stride = T * nodes_max;
+  E_ALLOC(e->done, T * nodes_max);
+  {
+    const hipError_t err = hipMemset(e->done, 0, sizeof(uint32_t) * T * nodes_max);
+    if (err != hipSuccess) {
+      wgbm_set_error("engine: clearing the arrival counters failed: %s", hipGetErrorString(err));
+      engine_destroy(e);
+      return (int)err;
+    }
+  }
   *out = e;
   return 0;
 }
@@ -289,6 +302,11 @@ int engine_set_tuning(Engine* e, int key, int64_t value) {
   if (key == 3) {
     WGBM_REQUIRE(value == 0 || value == 1, "one-era level scan must be 0 or 1");
     e->lscan_e1 = (int)value;
+    return 0;
+  }
+  if (key == 4) {
+    WGBM_REQUIRE(value == 0 || value == 1, "fused split / leaf step must be 0 or 1");
+    e->fuse_finish = (int)value;
     return 0;
   }
   wgbm_set_error("engine_set_tuning: unknown key %d", key);
@@ -580,7 +598,30 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                                   B, F, E, nodes, subtract ? d : 0, e->hq[hprev], e->hc[hprev],
                                   e->hn, e->hq[hcur], e->hc[hcur], st);
         if (r) return r;
-        if (E == 1) {
+        if (E == 1 && e->fuse_finish) {
+          // split search and the level's leaf / record step in one launch
+          FinishE1 fa;
+          fa.depth = d;
+          fa.max_depth = D;
+          fa.T = T;
+          fa.B = B;
+          fa.present = e->present[cur];
+          fa.split_l = e->split_l;
+          fa.split_b = e->split_b;
+          fa.feat_sel = feat_sel;
+          fa.tot_qh = e->totqh[cur];
+          fa.tot_ql = e->totql[cur];
+          fa.tot_c = e->totc[cur];
+          fa.shifts = e->shifts;
+          fa.s63_add = 62 - e->qbits;
+          fa.leaf_val = e->leaf_val;
+          fa.rec = rec;
+          fa.best_next = e->best + (hcur ^ 1) * e->pick_stride;
+          fa.nroute = e->nroute;
+          r = launch_split_finish_e1(nc, c0, st, e->hq[hcur], e->hc[hcur], F, n_sel,
+                                     e->node_shift[cur], mcw, eps, msg, best, e->done, fa);
+          if (r) return r;
+        } else if (E == 1) {
           // the pick is decoded by level_finish
           r = launch_split_level_e1(nc, st, e->hq[hcur], e->hc[hcur], F, B, feat_sel, n_sel, nodes,
                                     e->present[cur] + c0, e->node_shift[cur] + c0, mcw, eps, msg,
@@ -612,14 +653,16 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     // next depth (child totals, split picks)
     const int nxt = cur ^ 1;
     const bool e1_pick = d < D && !e->des_direct && E == 1;
-    hipLaunchKernelGGL(level_finish_kernel, dim3((unsigned)n_tn), dim3(64), 0, st, d, D, T, E, B,
-                       e->present[cur], e1_pick ? (const unsigned long long*)best : nullptr,
-                       e->split_l, e->split_b, e->split_gain, feat_sel, e->totqh[cur],
-                       e->totql[cur], e->totc[cur], e->shifts, 62 - e->qbits, e->leaf_val, rec,
-                       e->best + (hcur ^ 1) * e->pick_stride,
-                       e->agree_max ? e->agree_max + (hcur ^ 1) * e->pick_stride : nullptr,
-                       e->nroute);
-    WGBM_LAUNCH_CHECK();
+    if (!(e1_pick && e->fuse_finish)) {  // (else done by split_finish_e1_kernel)
+      hipLaunchKernelGGL(level_finish_kernel, dim3((unsigned)n_tn), dim3(64), 0, st, d, D, T, E,
+                         B, e->present[cur], e1_pick ? (const unsigned long long*)best : nullptr,
+                         e->split_l, e->split_b, e->split_gain, feat_sel, e->totqh[cur],
+                         e->totql[cur], e->totc[cur], e->shifts, 62 - e->qbits, e->leaf_val, rec,
+                         e->best + (hcur ^ 1) * e->pick_stride,
+                         e->agree_max ? e->agree_max + (hcur ^ 1) * e->pick_stride : nullptr,
+                         e->nroute);
+      WGBM_LAUNCH_CHECK();
+    }
     // ---- partition (or final leaf update): route every position, then the
     // next level's segments and the stable scatter
     RouteArgs rl = ra;

@@ -12,6 +12,7 @@
 #include "engine.hpp"
 #include "kernels.hpp"
 #include "plan.hpp"
+#include "split_scan.hpp"
 
 namespace wgbm {
 
@@ -120,32 +121,31 @@ __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_
 //   ql = sum (q63 & (2^32 - 1)):  H = qh + (ql >> 32), L = ql mod 2^32,
 //   leaf = float(ldexp(double(H) * 2^32 + double(L), -s63) / count)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void level_finish_kernel(
-    int32_t depth, int32_t max_depth, int32_t T, int32_t E, int32_t B,
-    const int32_t* __restrict__ present, const unsigned long long* __restrict__ best,
-    int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
-    const float* __restrict__ split_gain_era, const int32_t* __restrict__ feat_sel,
-    const int64_t* __restrict__ tot_qh, const int64_t* __restrict__ tot_ql,
-    const int64_t* __restrict__ tot_c, const int32_t* __restrict__ shifts, int32_t s63_add,
-    float* __restrict__ leaf_val, TreeRecord rec,
-    unsigned long long* __restrict__ best_next, int32_t* __restrict__ agree_max_next,
-    NodeRoute* __restrict__ nroute) {
-  // one wave per (tree, node); the eras are spread over the lanes.  The wave
-  // also clears the next depth's split-pick words of its two children.  With
-  // best != null (one era) the packed pick of the split search is decoded here.
+// The leaf / record step of one (tree, node), by one wave (lane = 0..63).
+// have_key: the packed pick of the one-era split search is `key` (the fused
+// split kernel's own result); else it is read from best (one era), or the
+// era path's split_l / split_b are used.
+__device__ inline void finish_node(
+    int tn, int lane, int32_t depth, int32_t max_depth, int32_t T, int32_t E, int32_t B,
+    const int32_t* __restrict__ present, bool have_key, unsigned long long key,
+    const unsigned long long* __restrict__ best, int32_t* __restrict__ split_l,
+    int32_t* __restrict__ split_b, const float* __restrict__ split_gain_era,
+    const int32_t* __restrict__ feat_sel, const int64_t* __restrict__ tot_qh,
+    const int64_t* __restrict__ tot_ql, const int64_t* __restrict__ tot_c,
+    const int32_t* __restrict__ shifts, int32_t s63_add, float* __restrict__ leaf_val,
+    const TreeRecord& rec, unsigned long long* __restrict__ best_next,
+    int32_t* __restrict__ agree_max_next, NodeRoute* __restrict__ nroute) {
   const int nodes = 1 << depth;
-  const int tn = blockIdx.x;
-  const int lane = threadIdx.x;
-  if (tn >= T * nodes) return;
   if (depth + 1 < max_depth && lane < 2) {
     best_next[2 * tn + lane] = 0ull;
     if (agree_max_next) agree_max_next[2 * tn + lane] = 0;
   }
   int l = -1, b = -1;
   float g1 = 0.0f;
+  const bool one_era_pick = have_key || best;
   if (depth < max_depth) {
-    if (best) {
-      const unsigned long long k = best[tn];
+    if (one_era_pick) {
+      const unsigned long long k = have_key ? key : best[tn];
       if (k != 0ull) {
         const int idx = (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
         l = idx / (B - 1);
@@ -207,12 +207,32 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
     }
   }
   if (l >= 0) {
-    if (best) {
+    if (one_era_pick) {
       if (lane == 0) rec.gain[h] = g1;
     } else {
       for (int e = lane; e < E; e += 64) rec.gain[h * E + e] = split_gain_era[(int64_t)tn * E + e];
     }
   }
+}
+
+__global__ __launch_bounds__(64) void level_finish_kernel(
+    int32_t depth, int32_t max_depth, int32_t T, int32_t E, int32_t B,
+    const int32_t* __restrict__ present, const unsigned long long* __restrict__ best,
+    int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
+    const float* __restrict__ split_gain_era, const int32_t* __restrict__ feat_sel,
+    const int64_t* __restrict__ tot_qh, const int64_t* __restrict__ tot_ql,
+    const int64_t* __restrict__ tot_c, const int32_t* __restrict__ shifts, int32_t s63_add,
+    float* __restrict__ leaf_val, TreeRecord rec,
+    unsigned long long* __restrict__ best_next, int32_t* __restrict__ agree_max_next,
+    NodeRoute* __restrict__ nroute) {
+  // one wave per (tree, node); the eras are spread over the lanes.  The wave
+  // also clears the next depth's split-pick words of its two children.  With
+  // best != null (one era) the packed pick of the split search is decoded here.
+  const int tn = blockIdx.x;
+  if (tn >= T * (1 << depth)) return;
+  finish_node(tn, threadIdx.x, depth, max_depth, T, E, B, present, false, 0ull, best, split_l,
+              split_b, split_gain_era, feat_sel, tot_qh, tot_ql, tot_c, shifts, s63_add,
+              leaf_val, rec, best_next, agree_max_next, nroute);
 }
 
 // ---------------------------------------------------------------------------
@@ -1049,6 +1069,118 @@ __global__ __launch_bounds__(1024) void level_scan_kernel(
   __syncthreads();
   plan_tiles_body(nx.seg_next, 0, n_list, nx.key_list_next, tile_rows, 0, max_tiles, tiles,
                   key_tile_start, n_tiles);
+}
+
+// One-era split search fused with the leaf / record step: one lane per
+// (node, local feature) scans the node's histogram as split_level_e1_kernel
+// does (split.hip); the workgroup's best candidate is the max of the packed
+// keys gain_key(gain) << 32 | (0xffffffff - flat index) of its waves.  With
+// one workgroup per node that key is the node's pick and the workgroup's
+// first wave finishes the node directly; otherwise every workgroup adds its
+// key to best[tn] (atomicMax) and counts itself in done[tn], and the last
+// one to arrive reads the final pick back and finishes the node (a release
+// fence before the count, an acquire fence after; no workgroup waits for
+// another).  Saves level_finish_kernel's launch on one-era levels.
+template <int BT>
+__global__ __launch_bounds__(256) void split_finish_e1_kernel(
+    const int64_t* __restrict__ hq, const int32_t* __restrict__ hc, int32_t F, int32_t B_rt,
+    int32_t n_sel, int32_t c0, const int32_t* __restrict__ node_shift, float mcw, float eps,
+    float min_split_gain, unsigned long long* __restrict__ best, uint32_t* __restrict__ done,
+    FinishE1 fa) {
+  __shared__ unsigned long long s_key[4];
+  __shared__ int s_last;
+  const int B = BT > 0 ? BT : B_rt;
+  const int bpn = (n_sel + 255) / 256;
+  const int tl = blockIdx.x / bpn;  // node within the chunk (histogram index)
+  const int tn = c0 + tl;           // node within the level
+  const int l = (blockIdx.x - tl * bpn) * 256 + threadIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const bool pres = fa.present[tn] != 0;
+  float bg = -__builtin_inff();
+  int bi = 0x7fffffff;
+  if (pres && l < n_sel) {
+    const int s = node_shift[tn];
+    const int f = fa.feat_sel[l];
+    const int64_t base = ((int64_t)tl * F + f) * B;
+    const int64_t* q = hq + base;
+    const int32_t* c = hc + base;
+    auto emit = [&](int b, float gn, float d) {
+      (void)d;
+      const int idx = l * (B - 1) + b;
+      if (gn > min_split_gain && better(gn, idx, bg, bi)) {
+        bg = gn;
+        bi = idx;
+      }
+    };
+    if constexpr (BT > 0) {
+      float g[BT], h[BT];
+#pragma unroll
+      for (int b = 0; b < BT; ++b) {
+        g[b] = wgbm_dequantise(q[b], s);
+        h[b] = (float)c[b];
+      }
+      scan_bins(
+          BT, mcw, eps, [&](int b) { return g[b]; }, [&](int b) { return h[b]; }, emit);
+    } else {
+      scan_bins(
+          B, mcw, eps, [&](int b) { return wgbm_dequantise(q[b], s); },
+          [&](int b) { return (float)c[b]; }, emit);
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float og = __shfl_xor(bg, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (better(og, oi, bg, bi)) {
+      bg = og;
+      bi = oi;
+    }
+  }
+  if (lane == 0)
+    s_key[w] = bi != 0x7fffffff ? (((unsigned long long)gain_key(bg) << 32) |
+                                   (unsigned long long)(0xffffffffu - (uint32_t)bi))
+                                : 0ull;
+  wgbm_lds_barrier();
+  unsigned long long k = 0ull;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) k = s_key[i] > k ? s_key[i] : k;
+  if (bpn > 1) {
+    if (threadIdx.x == 0) {
+      if (k) atomicMax(best + tn, k);
+      __threadfence();  // the key is visible before the arrival is counted
+      const uint32_t prev = atomicAdd(done + tn, 1u);
+      const bool last = prev == (uint32_t)(bpn - 1);
+      if (last) {
+        __threadfence();  // every other workgroup's key is visible
+        k = __hip_atomic_load(best + tn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        done[tn] = 0u;    // ready for the next level
+      }
+      s_last = last ? 1 : 0;
+      s_key[0] = k;
+    }
+    __syncthreads();
+    if (!s_last) return;  // uniform
+    k = s_key[0];
+  }
+  if (w == 0)
+    finish_node(tn, lane, fa.depth, fa.max_depth, fa.T, 1, fa.B, fa.present, true, k, nullptr,
+                fa.split_l, fa.split_b, nullptr, fa.feat_sel, fa.tot_qh, fa.tot_ql, fa.tot_c,
+                fa.shifts, fa.s63_add, fa.leaf_val, fa.rec, fa.best_next, nullptr, fa.nroute);
+}
+
+int launch_split_finish_e1(int n_tn, int32_t c0, hipStream_t st, const int64_t* hq,
+                           const int32_t* hc, int32_t F, int32_t n_sel,
+                           const int32_t* node_shift, float mcw, float eps,
+                           float min_split_gain, unsigned long long* best, uint32_t* done,
+                           const FinishE1& fa) {
+  const dim3 grid((unsigned)(n_tn * ((n_sel + 255) / 256)));
+  if (fa.B == 32)
+    hipLaunchKernelGGL(split_finish_e1_kernel<32>, grid, dim3(256), 0, st, hq, hc, F, fa.B,
+                       n_sel, c0, node_shift, mcw, eps, min_split_gain, best, done, fa);
+  else
+    hipLaunchKernelGGL(split_finish_e1_kernel<0>, grid, dim3(256), 0, st, hq, hc, F, fa.B,
+                       n_sel, c0, node_shift, mcw, eps, min_split_gain, best, done, fa);
+  WGBM_LAUNCH_CHECK();
+  return 0;
 }
 
 // The tiles of one list entry: a segment [b0, b0 + len) split into nt tiles

@@ -27,41 +27,9 @@
 #include <algorithm>
 #include "common.hpp"
 #include "kernels.hpp"
+#include "split_scan.hpp"
 
 namespace wgbm {
-
-struct ScanOut {
-  float gain;
-  float dir;
-};
-
-// sequential scan of one (era, feature) histogram; calls emit(b, gain, dir)
-template <typename LoadG, typename LoadH, typename Emit>
-__device__ inline void scan_bins(int B, float mcw, float eps, LoadG g, LoadH h, Emit emit) {
-  float Gt = 0.0f, Ht = 0.0f;
-#pragma unroll
-  for (int b = 0; b < B; ++b) {
-    Gt = Gt + g(b);
-    Ht = Ht + h(b);
-  }
-  float GL = 0.0f, HL = 0.0f;
-  const float tot = (Gt * Gt) / (Ht + eps);
-#pragma unroll
-  for (int b = 0; b < B - 1; ++b) {
-    GL = GL + g(b);
-    HL = HL + h(b);
-    const float GR = Gt - GL;
-    const float HR = Ht - HL;
-    float gain = 0.0f, dir = 0.0f;
-    if (HL >= mcw && HR >= mcw) {
-      gain = (GL * GL) / (HL + eps) + (GR * GR) / (HR + eps) - tot;
-      const float lv = GL / (HL + eps);
-      const float rv = GR / (HR + eps);
-      dir = lv > rv ? 1.0f : -1.0f;
-    }
-    emit(b, gain, dir);
-  }
-}
 
 // ---------------------------------------------------------------------------
 // reference-compatible compute_split: one lane per (era, feature)
@@ -88,9 +56,6 @@ __global__ void split_f32_kernel(const float* __restrict__ G, const float* __res
 //   hq/hc: [tree][node][F][B] exact sums; feat_sel: local -> global feature
 // outputs per (tree, node): split_l (local feature or -1), split_b, best gain
 // ---------------------------------------------------------------------------
-__device__ inline bool better(float g, int i, float bg, int bi) {
-  return g > bg || (g == bg && i < bi);
-}
 
 // A (node, era) segment of n rows where every candidate split has gain 0 and
 // direction 0: HL >= mcw && HR >= mcw needs HL + HR >= 2*mcw, and HL + HR
