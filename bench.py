@@ -530,7 +530,7 @@ def c3_kernel_rooflines(m, Xt):
 
     edges = D.quantile_edges(Xd, B)
     put("quantile_edges", timed(lambda: D.quantile_edges(Xd, B)), n * F * 4 + F * (B - 1) * 4,
-        "X read once + edges (the selection reads X in 4 radix passes)")
+        "X read once + edges (moved: X read and its values written transposed, then two scans of each transposed column)")
     put("bin_matrix", timed(lambda: D.bin_matrix(Xd, edges, with_cm=False)),
         n * F * 4 + n * F + F * (B - 1) * 4, "X + codes (row-major) + edges")
     codes = D.bin_matrix(Xd, edges, with_cm=False)

@@ -232,25 +232,29 @@ __device__ inline uint32_t float_to_key(float x) {
   if (x != x) return 0xffffffffu;
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+// the key of a value's bits, the value not a NaN
+__device__ inline uint32_t bits_to_key(uint32_t u) {
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
 __device__ inline float key_to_float(uint32_t k) {
   const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
   return __uint_as_float(u);
 }
 
-// X [n, F] float32 (row stride xs) -> keys [F][ks] (ks >= n, a multiple of
-// 4, so every column starts on 16 bytes): a workgroup moves 64 features x
-// kTransRows rows in 64 x 64 tiles through LDS, and keeps the smallest and
-// largest key of each of its features (a NaN key is the largest), merged
-// into kmin / kmax [F] with one atomic per feature.  Loads: 16 threads read
+// X [n, F] float32 (row stride xs) -> vals [F][ks] (the values' bits; ks >=
+// n, a multiple of 4, so every column starts on 16 bytes): a workgroup moves
+// 64 features x kTransRows rows in 64 x 64 tiles through LDS, and keeps the
+// smallest and largest key of each of its features (a NaN key is the
+// largest), merged into kmin / kmax [F] with one atomic per feature.  Loads: 16 threads read
 // one row's 64 values as four-value quads (VEC: 16-byte loads, when the
 // rows are 16-byte aligned; a quad past the last feature reads its valid
 // values one by one); stores: 16 threads write one feature's 64 rows as
 // 16-byte quads.
 template <bool VEC>
-__global__ __launch_bounds__(256) void transpose_keys_kernel(const float* __restrict__ X,
-                                                             int64_t n, int32_t F, int64_t xs,
-                                                             int64_t ks,
-                                                             uint32_t* __restrict__ keys,
+__global__ __launch_bounds__(256) void transpose_values_kernel(const float* __restrict__ X,
+                                                               int64_t n, int32_t F, int64_t xs,
+                                                               int64_t ks,
+                                                               uint32_t* __restrict__ keys,
                                                              uint32_t* __restrict__ kmin,
                                                              uint32_t* __restrict__ kmax) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -300,13 +304,12 @@ __global__ __launch_bounds__(256) void transpose_keys_kernel(const float* __rest
       }
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        uint32_t key = 0u;
         if (row_ok && c < nvf) {
-          key = float_to_key(v[c]);
+          const uint32_t key = float_to_key(v[c]);
           mn[c] = key < mn[c] ? key : mn[c];
           mx[c] = key > mx[c] ? key : mx[c];
         }
-        t[rr][4 * qd + c] = key;
+        t[rr][4 * qd + c] = __float_as_uint(v[c]);
       }
     }
     __syncthreads();
@@ -347,9 +350,9 @@ __global__ __launch_bounds__(256) void transpose_keys_kernel(const float* __rest
     atomicMax(&kmax[f0 + c], b);
   }
 }
-template __global__ void transpose_keys_kernel<true>(const float*, int64_t, int32_t, int64_t,
+template __global__ void transpose_values_kernel<true>(const float*, int64_t, int32_t, int64_t,
                                                      int64_t, uint32_t*, uint32_t*, uint32_t*);
-template __global__ void transpose_keys_kernel<false>(const float*, int64_t, int32_t, int64_t,
+template __global__ void transpose_values_kernel<false>(const float*, int64_t, int32_t, int64_t,
                                                       int64_t, uint32_t*, uint32_t*, uint32_t*);
 
 constexpr int kSelThreads = 512;
@@ -361,9 +364,11 @@ constexpr int kSelBuckets = 4096;     // value buckets of the first pass
 // 1000-feature matrix runs in one round).  The order statistics at ranks
 // floor / ceil(q (n-1)) are found in two scans of the column plus work on a
 // small buffer:
-//   1. histogram of kSelBuckets equal-width value buckets between the
-//      column's smallest and largest value (monotone in the value, so each
-//      bucket is a contiguous run of the sorted column);
+//   1. histogram of kSelBuckets value buckets between the column's smallest
+//      and largest value, bucket = clamp(int(fma(v, scale, offset))): any
+//      function non-decreasing in the value works (each bucket is then a
+//      contiguous run of the sorted column), this one costs three VALU
+//      operations a value, which is what the scan is bound by;
 //   2. the keys of the buckets that hold a target rank are copied to a
 //      per-feature buffer (the whole buckets, so a target's rank inside the
 //      buffer is the buffer keys of lower buckets plus its rank inside its
@@ -374,8 +379,10 @@ constexpr int kSelBuckets = 4096;     // value buckets of the first pass
 // column instead; a column holding a NaN gets NaN edges (torch.quantile) and
 // a constant column its value.
 //
-// The two column scans read 16-byte quads of keys (columns start on 16
-// bytes: ks is a multiple of 4), several per thread in flight.
+// The columns hold the values' bits (transpose_values_kernel); the buffer and
+// the radix selection use the order-preserving keys.  The two column scans
+// read 16-byte quads (columns start on 16 bytes: ks is a multiple of 4),
+// several per thread in flight.
 __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
     const uint32_t* __restrict__ keys, int64_t n, int64_t ks, int32_t F,
     const float* __restrict__ q, int32_t nq, float* __restrict__ edges,
@@ -423,33 +430,49 @@ __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
     }
     // ---- value buckets
     const float lo = key_to_float(kmn), hi = key_to_float(kmx);
-    const float scale = (float)kSelBuckets / (hi - lo);
-    auto bucket = [&](uint32_t k) -> int {
-      // non-decreasing in the value; inf / NaN intermediates fall into bucket 0
-      const float v = (key_to_float(k) - lo) * scale;
-      return v >= (float)(kSelBuckets - 1) ? kSelBuckets - 1 : (v > 0.0f ? (int)v : 0);
+    float scale = (float)kSelBuckets / (hi - lo);
+    if (!(scale < __builtin_inff())) scale = 0.0f;  // infinite ends: everything in bucket 0
+    const float off = -lo * scale;
+    auto bucket = [&](uint32_t bits) -> int {
+      // non-decreasing in the value: a correctly rounded fma is monotone in v
+      // for scale >= 0, and so is the clamp (fmaxf maps a NaN to 0)
+      const float v = __builtin_fmaf(__uint_as_float(bits), scale, off);
+      return (int)fminf(fmaxf(v, 0.0f), (float)(kSelBuckets - 1));
     };
     uint32_t* H = &hist[0][0];  // [kSelBuckets]
     for (int i = tid; i < kSelBuckets; i += kSelThreads) H[i] = 0;
     for (int i = tid; i < kSelBuckets / 32; i += kSelThreads) marked[i] = 0;
     if (tid == 0) s_cnt = 0;
     __syncthreads();
-    // four 16-byte loads in flight per thread
-    for (int64_t i0 = tid; i0 < n4; i0 += 4 * kSelThreads) {
-      u32x4 k[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t i = i0 + u * kSelThreads;
-        k[u] = i < n4 ? col4[i] : u32x4{0u, 0u, 0u, 0u};
+    // The column in batches of two 16-byte quads per thread (quads i and
+    // i + kSelThreads); two batches alternate so that the next batch's loads
+    // are in flight while this one is counted (a thread that loaded, waited
+    // and counted left the memory idle half the time).  Quads past the end
+    // are not read.
+    constexpr int64_t kQ = kSelThreads;
+    // quads past the end read the last quad (straight-line loads, so that the
+    // wait before a batch covers only its own loads); their keys are not used
+    auto ld4 = [&](int64_t i) { return col4[i < n4 ? i : n4 - 1]; };
+    auto count4 = [&](const u32x4& k, bool v) {
+      if (v) {
+        atomicAdd(&H[bucket(k.x)], 1u);
+        atomicAdd(&H[bucket(k.y)], 1u);
+        atomicAdd(&H[bucket(k.z)], 1u);
+        atomicAdd(&H[bucket(k.w)], 1u);
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (i0 + u * kSelThreads < n4) {
-          atomicAdd(&H[bucket(k[u].x)], 1u);
-          atomicAdd(&H[bucket(k[u].y)], 1u);
-          atomicAdd(&H[bucket(k[u].z)], 1u);
-          atomicAdd(&H[bucket(k[u].w)], 1u);
-        }
+    };
+    if (n4 > 0) {
+      int64_t i0 = tid;
+      u32x4 a0 = ld4(i0), a1 = ld4(i0 + kQ);
+      for (; i0 < n4; i0 += 4 * kQ) {
+        const int64_t j0 = i0 + 2 * kQ;
+        const u32x4 b0 = ld4(j0), b1 = ld4(j0 + kQ);
+        count4(a0, true);
+        count4(a1, i0 + kQ < n4);
+        a0 = ld4(j0 + 2 * kQ);
+        a1 = ld4(j0 + 3 * kQ);
+        count4(b0, j0 < n4);
+        count4(b1, j0 + kQ < n4);
       }
     }
     for (int64_t i = 4 * n4 + tid; i < n; i += kSelThreads) atomicAdd(&H[bucket(col[i])], 1u);
@@ -527,57 +550,115 @@ __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
       }
       __syncthreads();
     }
-    const uint32_t* src = col;  // the keys the radix selection scans
-    int64_t ns = n;
+    const uint32_t* src = col;  // what the radix selection scans: the column's
+    int64_t ns = n;             // values, or the buffer's keys
     if ((int64_t)s_tot <= ccap) {
-      // one buffer reservation per wave: a ballot of the lanes that keep
-      // their key, lane ranks by mbcnt
+      // Batches of two quads per thread (8 keys, double-buffered as in the
+      // first scan): a thread marks the keys it keeps, a DPP scan over the
+      // wave gives each lane its offset, and one LDS reservation per wave
+      // and batch places them (the order inside the buffer is free: the
+      // selection below only counts).
       const int lane = tid & 63;
-      auto keep = [&](uint32_t k, bool valid) {
-        bool take = false;
-        if (valid) {
-          const int b = bucket(k);
-          take = (marked[b >> 5] >> (b & 31)) & 1u;
-        }
-        const uint64_t m = __ballot(take);
-        if (m) {
-          const int first = __builtin_ctzll(m);
-          uint32_t base = 0;
-          if (lane == first) base = atomicAdd(&s_cnt, (uint32_t)__builtin_popcountll(m));
-          base = __shfl(base, first, 64);
-          const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
-              (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-          if (take) cb[base + rank] = k;  // base + rank < s_tot <= ccap
-        }
+      auto take = [&](uint32_t k) -> uint32_t {
+        const int b = bucket(k);
+        return (marked[b >> 5] >> (b & 31)) & 1u;
       };
-      // two 16-byte loads per thread in flight; the same trip count for all
-      for (int64_t i0 = 0; i0 < n4; i0 += 2 * kSelThreads) {
-        const int64_t ia = i0 + tid, ib = ia + kSelThreads;
-        const u32x4 ka = ia < n4 ? col4[ia] : u32x4{0u, 0u, 0u, 0u};
-        const u32x4 kb = ib < n4 ? col4[ib] : u32x4{0u, 0u, 0u, 0u};
-        keep(ka.x, ia < n4);
-        keep(ka.y, ia < n4);
-        keep(ka.z, ia < n4);
-        keep(ka.w, ia < n4);
-        keep(kb.x, ib < n4);
-        keep(kb.y, ib < n4);
-        keep(kb.z, ib < n4);
-        keep(kb.w, ib < n4);
+      auto keep8 = [&](const u32x4& x, bool vx, const u32x4& y, bool vy) {
+        uint32_t bits = 0;
+        if (vx) bits |= take(x.x) | take(x.y) << 1 | take(x.z) << 2 | take(x.w) << 3;
+        if (vy) bits |= take(y.x) << 4 | take(y.y) << 5 | take(y.z) << 6 | take(y.w) << 7;
+        const int64_t cnt = __builtin_popcount(bits);
+        const int64_t inc = wgbm_wave_incl_scan_i64(cnt);
+        const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)inc, 63);
+        if (tot == 0) return;  // wave-uniform
+        uint32_t base = 0;
+        if (lane == 63) base = atomicAdd(&s_cnt, tot);
+        base = (uint32_t)__builtin_amdgcn_readlane((int)base, 63);
+        uint32_t o = base + (uint32_t)(inc - cnt);  // < s_tot <= ccap
+        const uint32_t kk[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if ((bits >> j) & 1u) cb[o++] = bits_to_key(kk[j]);
+      };
+      if (n4 > 0) {
+        // the same trip count for every thread: keep8's wave scan and lane
+        // 63's reservation need the whole wave
+        u32x4 a0 = ld4(tid), a1 = ld4(tid + kQ);
+        for (int64_t q0 = 0; q0 < n4; q0 += 4 * kQ) {
+          const int64_t i0 = q0 + tid, j0 = i0 + 2 * kQ;
+          const u32x4 b0 = ld4(j0), b1 = ld4(j0 + kQ);
+          keep8(a0, i0 < n4, a1, i0 + kQ < n4);
+          a0 = ld4(j0 + 2 * kQ);
+          a1 = ld4(j0 + 3 * kQ);
+          keep8(b0, j0 < n4, b1, j0 + kQ < n4);
+        }
       }
       {
-        const int64_t i = 4 * n4 + tid;  // the tail: fewer than 4 keys
-        keep(i < n ? col[i] : 0u, i < n);
+        // the tail: fewer than 4 keys, one per thread
+        const int64_t i = 4 * n4 + tid;
+        const uint32_t k = i < n ? col[i] : 0u;
+        const uint32_t bit = (i < n && take(k)) ? 1u : 0u;
+        const int64_t inc = wgbm_wave_incl_scan_i64((int64_t)bit);
+        const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)inc, 63);
+        if (tot) {
+          uint32_t base = 0;
+          if (lane == 63) base = atomicAdd(&s_cnt, tot);
+          base = (uint32_t)__builtin_amdgcn_readlane((int)base, 63);
+          if (bit) cb[base + (uint32_t)inc - 1u] = bits_to_key(k);
+        }
       }
       __syncthreads();
       src = cb;
       ns = (int64_t)s_tot;
     }
     // ---- radix selection over src (ranks in trank are ranks within src)
+    // src is read in batches of 8 keys per thread in flight (the column's
+    // values are turned into keys here)
+    const bool src_vals = src == col;
+    auto for_src = [&](auto fn) {
+      for (int64_t i0 = tid; i0 < ns; i0 += 8 * kSelThreads) {
+        uint32_t k[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int64_t i = i0 + u * kSelThreads;
+          k[u] = src[i < ns ? i : ns - 1];  // (i0 < ns, so ns >= 1)
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (i0 + u * kSelThreads < ns) fn(src_vals ? bits_to_key(k[u]) : k[u]);
+      }
+    };
+    // a 256-bin row of counts -> inclusive prefix, in place (one wave, 4 bins
+    // a lane)
+    auto row_prefix = [&](uint32_t* row) {
+      const int ln = tid & 63;
+      uint32_t v[4];
+      uint32_t t = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        t += row[4 * ln + j];
+        v[j] = t;
+      }
+      const uint32_t base = (uint32_t)(wgbm_wave_incl_scan_i64((int64_t)t) - t);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) row[4 * ln + j] = base + v[j];
+    };
+    // first bin whose inclusive prefix exceeds r (bins 0..255; 255 when none
+    // below does), and r made relative to that bin
+    auto pick_bin = [&](const uint32_t* P, int64_t& r) {
+      int a = 0, b = 255;
+      while (a < b) {
+        const int mid = (a + b) >> 1;
+        if ((int64_t)P[mid] > r) b = mid; else a = mid + 1;
+      }
+      if (a > 0) r -= P[a - 1];
+      return a;
+    };
     for (int i = tid; i < nwaves * 256; i += kSelThreads) (&hist[0][0])[i] = 0;
     __syncthreads();
     {
       const int w = tid >> 6;
-      for (int64_t i = tid; i < ns; i += kSelThreads) atomicAdd(&hist[w][src[i] >> 24], 1u);
+      for_src([&](uint32_t k) { atomicAdd(&hist[w][k >> 24], 1u); });
     }
     __syncthreads();
     for (int b = tid; b < 256; b += kSelThreads) {
@@ -586,10 +667,11 @@ __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
       hist[nwaves][b] = sum;
     }
     __syncthreads();
+    if (tid < 64) row_prefix(hist[nwaves]);
+    __syncthreads();
     for (int t = tid; t < nt; t += kSelThreads) {
       int64_t r = trank[t];
-      int b = 0;
-      while (r >= (int64_t)hist[nwaves][b]) r -= hist[nwaves][b++];
+      const int b = pick_bin(hist[nwaves], r);
       tprefix[t] = (uint32_t)b;
       trank[t] = r;
     }
@@ -632,21 +714,21 @@ __global__ __launch_bounds__(kSelThreads) void quantile_select_kernel(
         for (int i = tid; i < gn * 256; i += kSelThreads) (&hist[0][0])[i] = 0;
         __syncthreads();
         const uint32_t lo_p = dist[g0], hi_p = dist[g0 + gn - 1];
-        for (int64_t i = tid; i < ns; i += kSelThreads) {
-          const uint32_t k = src[i];
+        for_src([&](uint32_t k) {
           const uint32_t pre = k >> sh;
-          if (pre < lo_p || pre > hi_p) continue;
+          if (pre < lo_p || pre > hi_p) return;
           const int g = find(pre, g0, g0 + gn - 1);
           if (dist[g] == pre) atomicAdd(&hist[g - g0][(k >> (sh - 8)) & 255u], 1u);
-        }
+        });
+        __syncthreads();
+        for (int g = tid >> 6; g < gn; g += nwaves) row_prefix(hist[g]);
         __syncthreads();
         for (int t = tid; t < nt; t += kSelThreads) {
           const uint32_t pre = tprefix[t];
           if (pre < dist[g0] || pre > dist[g0 + gn - 1]) continue;
           const int g = find(pre, g0, g0 + gn - 1);
           int64_t r = trank[t];
-          int b = 0;
-          while (b < 255 && r >= (int64_t)hist[g - g0][b]) r -= hist[g - g0][b++];
+          const int b = pick_bin(hist[g - g0], r);
           tprefix[t] = (pre << 8) | (uint32_t)b;
           trank[t] = r;
         }

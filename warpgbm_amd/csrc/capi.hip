@@ -394,7 +394,7 @@ int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64
   // column-major keys of up to `chunk` features at a time (bounded scratch)
   // (up to 2^30 keys = 4 GiB of scratch: all features of a 1M-row matrix in
   // one launch, so that every CU holds several columns)
-  // key columns padded to a multiple of 32 keys (128-byte lines; the
+  // value columns padded to a multiple of 32 values (128-byte lines; the
   // kernels need 16-byte aligned quads)
   const int64_t ks = (n + 31) / 32 * 32;
   const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n_feats, (int64_t(1) << 30) / ks));
@@ -413,10 +413,10 @@ int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64
     // 16-byte row loads when every row of the chunk starts on 16 bytes
     const bool vec = ((uintptr_t)(X + f0) % 16) == 0 && x_stride % 4 == 0;
     if (vec)
-      hipLaunchKernelGGL(transpose_keys_kernel<true>, tg, dim3(256), 0, st, X + f0, n, fc,
+      hipLaunchKernelGGL(transpose_values_kernel<true>, tg, dim3(256), 0, st, X + f0, n, fc,
                          x_stride, ks, keys, kmin, kmax);
     else
-      hipLaunchKernelGGL(transpose_keys_kernel<false>, tg, dim3(256), 0, st, X + f0, n, fc,
+      hipLaunchKernelGGL(transpose_values_kernel<false>, tg, dim3(256), 0, st, X + f0, n, fc,
                          x_stride, ks, keys, kmin, kmax);
     WGBM_LAUNCH_CHECK();
     hipLaunchKernelGGL(quantile_select_kernel, dim3(fc), dim3(512), 0, st, keys, n, ks, fc, q, nq,

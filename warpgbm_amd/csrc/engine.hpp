@@ -303,7 +303,7 @@ __global__ void copy_prebinned_kernel(const int8_t* X, int64_t n, int32_t F, int
 __global__ void quantile_edges_kernel(const float* sorted, int64_t n, int32_t F,
                                       const float* q, int32_t nq, float* edges);
 template <bool VEC>
-__global__ void transpose_keys_kernel(const float* X, int64_t n, int32_t F, int64_t xs,
+__global__ void transpose_values_kernel(const float* X, int64_t n, int32_t F, int64_t xs,
                                       int64_t ks, uint32_t* keys, uint32_t* kmin,
                                       uint32_t* kmax);
 __global__ void quantile_select_kernel(const uint32_t* keys, int64_t n, int64_t ks, int32_t F,
