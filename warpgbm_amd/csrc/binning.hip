@@ -65,20 +65,25 @@ __device__ inline int count_le(const float* e, int ne, float v) {
 //   num_bins = n_edges + 1) and, if non-null, codes_cm [F, n].
 // workgroup: 64 features x BT_R rows (the feature tiles of a row block
 // consecutive in the XCD work order, so a cache line shared by two tiles is
-// fetched once); the edges of its 64 features staged in LDS once.  Lane l of every wave owns feature f0 + l (coalesced 256-byte row
-// loads, 64-byte code stores); each thread issues the loads of 8 rows before
-// it searches them, so several rows are in flight.  The column-major copy is
-// transposed through LDS and written as BT_R-byte runs per feature.
+// fetched once); the edges of its 64 features staged in LDS once.  Thread
+// (row group g = t / 16, quad q = t % 16) owns features f0 + 4q .. + 3 of
+// rows g, g + 16, ...: one 16-byte load per row when the rows are 16-byte
+// aligned (VEC), and the row's four codes stored as one 32-bit word when the
+// code rows allow it (rm_words); four rows' loads are issued before they are
+// searched.  The column-major copy is transposed through LDS and written as
+// 32-bit words of four rows (when n and the pointer allow; bytes otherwise).
 // ---------------------------------------------------------------------------
-constexpr int BT_F = kBinTileFeats, BT_R = kBinTileRows, BT_U = 8;
-static_assert(BT_F == 64 && BT_R == 256, "lane = feature, thread = row of the transposed copy");
+constexpr int BT_F = kBinTileFeats, BT_R = kBinTileRows, BT_U = 4;
+static_assert(BT_F == 64 && BT_R == 256, "16 feature quads x 16 row groups per step");
 
+template <bool VEC>
 __global__ __launch_bounds__(256) void bin_matrix_kernel(
     const float* __restrict__ X, int64_t n, int32_t F, int64_t xs,
     const float* __restrict__ edges, int32_t n_edges, int8_t* __restrict__ codes_rm, int64_t S,
     int8_t* __restrict__ codes_cm) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
   extern __shared__ float sedge[];  // [BT_F][n_edges]
-  __shared__ int8_t tcode[BT_F][BT_R + 4];
+  __shared__ __align__(4) int8_t tcode[BT_F][BT_R + 4];
   const int nft = (F + BT_F - 1) / BT_F;
   const int64_t n_work = (n + BT_R - 1) / BT_R * nft;
   const int64_t w = wgbm_xcd_work(blockIdx.x, n_work);
@@ -92,36 +97,77 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
     sedge[i] = f < F ? edges[(int64_t)f * n_edges + (i - fl * n_edges)] : 0.0f;
   }
   __syncthreads();
-  const int fl = tid & 63;
-  const int rq = tid >> 6;  // rows rq, rq + 4, ... of the tile
-  const int f = f0 + fl;
-  const float* e = sedge + fl * n_edges;
-  const int8_t pad = (int8_t)(n_edges + 2);  // num_bins + 1
-  for (int k0 = 0; k0 < BT_R; k0 += 4 * BT_U) {
-    float v[BT_U];
+  const int q = tid & 15, g = tid >> 4;
+  const int fq = f0 + 4 * q;  // first feature of the thread's quad
+  const int nvf = F - fq < 4 ? (F - fq > 0 ? F - fq : 0) : 4;  // its real features
+  const int8_t pad = (int8_t)(n_edges + 2);                     // num_bins + 1
+  const bool rm_words = (S & 3) == 0 && ((uintptr_t)codes_rm & 3) == 0;
+  for (int k0 = 0; k0 < BT_R; k0 += 16 * BT_U) {
+    float v[BT_U][4];
 #pragma unroll
     for (int u = 0; u < BT_U; ++u) {
-      const int64_t r = r0 + k0 + rq + 4 * u;
-      v[u] = (r < n && f < F) ? X[r * xs + f] : 0.0f;
+      const int64_t r = r0 + k0 + g + 16 * u;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[u][c] = 0.0f;
+      if (r < n) {
+        const float* src = X + r * xs + fq;
+        if (VEC && nvf == 4) {
+          const f32x4 x4 = *reinterpret_cast<const f32x4*>(src);
+          v[u][0] = x4.x;
+          v[u][1] = x4.y;
+          v[u][2] = x4.z;
+          v[u][3] = x4.w;
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (c < nvf) v[u][c] = src[c];
+        }
+      }
     }
 #pragma unroll
     for (int u = 0; u < BT_U; ++u) {
-      const int k = k0 + rq + 4 * u;
+      const int k = k0 + g + 16 * u;
       const int64_t r = r0 + k;
-      const int8_t c = f < F ? (int8_t)count_le(e, n_edges, v[u]) : pad;
-      tcode[fl][k] = c;
-      if (r < n && f < S) codes_rm[r * S + f] = c;
+      uint32_t word = 0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int8_t code =
+            c < nvf ? (int8_t)count_le(sedge + (4 * q + c) * n_edges, n_edges, v[u][c]) : pad;
+        tcode[4 * q + c][k] = code;
+        word |= (uint32_t)(uint8_t)code << (8 * c);
+      }
+      if (r < n && fq < S) {
+        int8_t* dst = codes_rm + r * S + fq;
+        if (rm_words && fq + 4 <= S) {
+          *reinterpret_cast<uint32_t*>(dst) = word;
+        } else {
+          for (int c = 0; c < 4 && fq + c < S; ++c) dst[c] = (int8_t)(word >> (8 * c));
+        }
+      }
     }
   }
   if (!codes_cm) return;  // uniform over the workgroup
   __syncthreads();
-  // column-major: thread t writes row r0 + t of every feature of the tile
-  const int64_t r = r0 + tid;
+  // column-major: lane l of wave wv writes rows r0 + 4l .. 4l + 3 of features
+  // wv, wv + 4, ... of the tile
+  const int l = tid & 63, wv = tid >> 6;
+  const int64_t r = r0 + 4 * l;
+  const bool cm_words = (n & 3) == 0 && ((uintptr_t)codes_cm & 3) == 0;
   if (r < n) {
-    for (int k = 0; k < BT_F && f0 + k < F; ++k)
-      codes_cm[(int64_t)(f0 + k) * n + r] = tcode[k][tid];
+    for (int k = wv; k < BT_F && f0 + k < F; k += 4) {
+      int8_t* dst = codes_cm + (int64_t)(f0 + k) * n + r;
+      if (cm_words) {  // r + 3 < n: n and r are multiples of 4
+        *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(&tcode[k][4 * l]);
+      } else {
+        for (int c = 0; c < 4 && r + c < n; ++c) dst[c] = tcode[k][4 * l + c];
+      }
+    }
   }
 }
+template __global__ void bin_matrix_kernel<true>(const float*, int64_t, int32_t, int64_t,
+                                                 const float*, int32_t, int8_t*, int64_t, int8_t*);
+template __global__ void bin_matrix_kernel<false>(const float*, int64_t, int32_t, int64_t,
+                                                  const float*, int32_t, int8_t*, int64_t, int8_t*);
 
 // padding bytes beyond the last 64-feature tile (S > round_up(F, 64))
 __global__ void pad_codes_kernel(int8_t* __restrict__ codes_rm, int64_t n, int64_t S,
