@@ -533,11 +533,13 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         start_iter = self._trees_trained if (self.warm_start and self._is_fitted) else 0
         init = self._class_prior_logits(np.asarray(y_encoded))
         # the engine keeps the training scores class-major, [K, n]
-        scores_rm = torch.from_numpy(np.tile(init, (self.num_samples, 1))).to(dev)
         if start_iter > 0:
+            scores_rm = D.rows_of(init, self.num_samples, dev)
             self._predict_codes_into(codes, scores_rm, self.forest[:start_iter])
-        scores = scores_rm.t().contiguous()
-        del scores_rm
+            scores = scores_rm.t().contiguous()
+            del scores_rm
+        else:
+            scores = D.cols_of(init, self.num_samples, dev)
         self._setup_eval(X_eval, y_eval, eval_every_n_trees, early_stopping_rounds, eval_metric,
                          classification=True)
         if not hasattr(self, "training_loss") or not self.warm_start or not self._is_fitted:
@@ -553,8 +555,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         self.stop = False
         eval_scores = None
         if self._eval is not None:
-            eval_scores = torch.from_numpy(
-                np.tile(self._uniform_prior_logits(), (self._eval["codes"].n, 1))).to(dev)
+            eval_scores = D.rows_of(self._uniform_prior_logits(), self._eval["codes"].n, dev)
             if start_iter > 0:
                 self._predict_codes_into(self._eval["codes"], eval_scores, self.forest[:start_iter])
         done = 0
@@ -788,7 +789,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
 
     def predict_proba_binned(self, codes):
         dev = torch.device(self.device)
-        scores = torch.from_numpy(np.tile(self._uniform_prior_logits(), (codes.n, 1))).to(dev)
+        scores = D.rows_of(self._uniform_prior_logits(), codes.n, dev)
         feat, bin_, leaf, n = self._cached_heap()
         if n:
             D.predict_heap(codes, feat, bin_, leaf, n, self.num_classes, self.max_depth,
@@ -806,7 +807,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         ph.mark("codes")
         out = self.predict_binned(codes)
         ph.mark("trees")
-        preds = out.cpu().numpy()
+        preds = D.to_host(out)
         ph.mark("copy out")
         ph.report("predict")
         del codes
@@ -817,7 +818,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         if self.objective not in ["multiclass", "binary"]:
             raise ValueError("predict_proba only available for classification objectives")
         codes = self.bin_inference_data(X_np)
-        probs = self.predict_proba_binned(codes).cpu().numpy()
+        probs = D.to_host(self.predict_proba_binned(codes))
         del codes
         return probs
 

@@ -380,6 +380,31 @@ def importance_add(acc: torch.Tensor, gain: torch.Tensor, node: torch.Tensor,
     _lib.check(rc, "importance_add")
 
 
+def rows_of(values: np.ndarray, n: int, dev) -> torch.Tensor:
+    """float32 [n, K] on the device, every row equal to ``values`` [K] (a
+    broadcast on the device: no host-side tile and no n * K upload)."""
+    v = torch.from_numpy(np.ascontiguousarray(values, dtype=np.float32)).to(dev)
+    return v.reshape(1, -1).expand(n, v.numel()).contiguous()
+
+
+def cols_of(values: np.ndarray, n: int, dev) -> torch.Tensor:
+    """float32 [K, n] on the device, row k filled with ``values[k]`` (the
+    class-major layout of rows_of)."""
+    v = torch.from_numpy(np.ascontiguousarray(values, dtype=np.float32)).to(dev)
+    return v.reshape(-1, 1).expand(v.numel(), n).contiguous()
+
+
+def to_host(t: torch.Tensor) -> np.ndarray:
+    """A device tensor as a numpy array, copied through page-locked memory
+    (a DMA at full link speed; a plain ``.cpu()`` stages pageable memory at a
+    fraction of it).  The array keeps its page-locked block until it is freed."""
+    if not t.is_cuda:
+        return t.numpy()
+    h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+    h.copy_(t)
+    return h.numpy()
+
+
 def softmax_rows(x: torch.Tensor) -> None:
     lib = _lib.load()
     n, K = x.shape
