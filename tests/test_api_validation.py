@@ -94,6 +94,20 @@ def test_heap_dict_round_trip_and_preorder():
     assert back == [tree]
     assert _preorder_heap(7).tolist() == [0, 1, 3, 4, 2, 5, 6]
 
+    # complete heaps (computed level by level) against a depth-first walk,
+    # and heaps that are not complete
+    def walk(H):
+        out, stack = [], [0]
+        while stack:
+            h = stack.pop()
+            if h < H:
+                out.append(h)
+                stack += [2 * h + 2, 2 * h + 1]
+        return out
+
+    for H in [1, 3, 15, 63, 1023, 4095, 2, 6, 100]:
+        assert _preorder_heap(H).tolist() == walk(H), H
+
     def internal(feat):
         return [int(h) for h in _preorder_heap(len(feat)) if feat[h] >= 0]
 

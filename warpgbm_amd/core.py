@@ -687,30 +687,30 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         stream during training) into the forest, and importance in the
         reference's order: per tree, internal nodes in depth-first pre-order,
         float32 adds (warpgbm/core.py:624-627)."""
-        feat = stream.host["feat"][:done].numpy()  # [done, n_trees, H]
-        n_trees, H = feat.shape[1], feat.shape[2]
+        dev = rec["gain"].device
+        featd = rec["feat"][:done]  # [done, n_trees, H] on the device
+        n_trees, H = featd.shape[1], featd.shape[2]
         # importance: every internal node of every tree, trees in order and
         # nodes in pre-order, one float32 add per node and era in exactly that
         # sequence; on the device from the per-era gain records (the nodes
-        # grouped by feature, in order, give each (feature, era) word to one
-        # thread)
-        po = _preorder_heap(H)
-        fp = feat[:, :, po]
+        # grouped by feature with a stable sort, in order, give each (feature,
+        # era) word to one thread)
+        po = torch.from_numpy(_preorder_heap(H).astype(np.int64)).to(dev)
+        fp = featd[:, :, po]
         internal = fp >= 0
-        if internal.any():
-            base = (np.arange(done, dtype=np.int64)[:, None, None] * n_trees
-                    + np.arange(n_trees, dtype=np.int64)[None, :, None]) * H
-            rows = (base + po[None, None, :].astype(np.int64))[internal]
+        if bool(internal.any()):
+            base = (torch.arange(done, dtype=torch.int64, device=dev)[:, None, None] * n_trees
+                    + torch.arange(n_trees, dtype=torch.int64, device=dev)[None, :, None]) * H
+            rows = (base + po[None, None, :])[internal]
             fsel = fp[internal]
-            by_f = np.argsort(fsel, kind="stable")
+            fsorted, by_f = torch.sort(fsel, stable=True)
             F, E = self.num_features, self.num_eras
-            fstart = np.searchsorted(fsel[by_f], np.arange(F + 1)).astype(np.int64)
-            dev = rec["gain"].device
+            fstart = torch.searchsorted(
+                fsorted, torch.arange(F + 1, dtype=fsorted.dtype, device=dev)).to(torch.int64)
             acc = torch.from_numpy(np.ascontiguousarray(self.per_era_feature_importance_,
                                                         dtype=np.float32)).to(dev)
-            D.importance_add(acc, rec["gain"][:done].reshape(-1, E),
-                             torch.from_numpy(rows[by_f]).to(dev),
-                             torch.from_numpy(fstart).to(dev))
+            D.importance_add(acc, rec["gain"][:done].reshape(-1, E), rows[by_f].contiguous(),
+                             fstart.contiguous())
             self.per_era_feature_importance_ = acc.cpu().numpy()
         self._phases.mark("importance")
         for j in range(done):
@@ -959,15 +959,29 @@ def _heaps_to_dicts(feat, bin_, leaf, count):
 
 
 def _preorder_heap(H):
-    """All heap indices < H in depth-first pre-order (left first)."""
-    out, stack = [], [0]
-    while stack:
-        h = stack.pop()
-        if h < H:
-            out.append(h)
-            stack.append(2 * h + 2)
-            stack.append(2 * h + 1)
-    return np.asarray(out, dtype=np.int64)
+    """All heap indices < H in depth-first pre-order (left first).  For a
+    complete heap (H = 2^(D+1) - 1) the pre-order position of a node follows
+    from its parent's: left child = parent + 1, right child = parent + 1 + the
+    size of the left child's subtree; computed level by level."""
+    D = int(H + 1).bit_length() - 2
+    if H < 1 or (1 << (D + 1)) - 1 != H:
+        out, stack = [], [0]
+        while stack:
+            h = stack.pop()
+            if h < H:
+                out.append(h)
+                stack.append(2 * h + 2)
+                stack.append(2 * h + 1)
+        return np.asarray(out, dtype=np.int64)
+    pos = np.zeros(H, dtype=np.int64)
+    for d in range(D):
+        par = np.arange((1 << d) - 1, (1 << (d + 1)) - 1, dtype=np.int64)
+        sub = (1 << (D - d)) - 1  # nodes under a child of a depth-d node
+        pos[2 * par + 1] = pos[par] + 1
+        pos[2 * par + 2] = pos[par] + 1 + sub
+    out = np.empty(H, dtype=np.int64)
+    out[pos] = np.arange(H, dtype=np.int64)
+    return out
 
 
 def _dict_to_heap(tree, H):

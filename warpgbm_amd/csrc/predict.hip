@@ -462,13 +462,25 @@ __global__ void importance_add_kernel(float* __restrict__ acc, int32_t F, int32_
   float s = *w;
   const int64_t i1 = fstart[f + 1];
   int64_t i = fstart[f];
-  // eight gathers in flight ahead of their (sequential) adds
-  for (; i + 8 <= i1; i += 8) {
-    float g[8];
+  // batches of 16 gathers in flight ahead of their (sequential) adds, the
+  // node indices of the next batch loaded with this batch's gains (one
+  // memory round trip per batch; a feature can hold thousands of nodes)
+  constexpr int U = 16;
+  int64_t nx[U];
+  if (i + U <= i1) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) g[u] = gain[node[i + u] * E + e];
+    for (int u = 0; u < U; ++u) nx[u] = node[i + u];
+  }
+  for (; i + U <= i1; i += U) {
+    float g[U];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) s = s + g[u];
+    for (int u = 0; u < U; ++u) g[u] = gain[nx[u] * E + e];
+    if (i + 2 * U <= i1) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) nx[u] = node[i + U + u];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) s = s + g[u];
   }
   for (; i < i1; ++i) s = s + gain[node[i] * E + e];
   *w = s;
