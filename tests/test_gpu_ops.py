@@ -272,6 +272,66 @@ def test_predict_forest_bit_exact(gpu):
     assert np.array_equal(bits(out.cpu().numpy()), bits(ref))
 
 
+def _random_heap(rng, R, K, depth, F, B):
+    """R rounds x K heap-ordered trees (node h: children 2h+1, 2h+2; feat -1
+    = leaf) of depth <= ``depth``, with garbage below every leaf (the
+    predictors must never read it) and the reference table of each tree."""
+    H = (1 << (depth + 1)) - 1
+    feat = rng.integers(-1, F, (R, K, H)).astype(np.int32)   # garbage everywhere first
+    binv = rng.integers(0, B - 1, (R, K, H)).astype(np.int32)
+    leaf = rng.standard_normal((R, K, H)).astype(F32)
+    tables = np.zeros((R * K, H, 6), F32)
+    for r in range(R):
+        for k in range(K):
+            f, b, lv, tb = feat[r, k], binv[r, k], leaf[r, k], tables[r * K + k]
+            stack = [(0, 0)]
+            while stack:
+                h, d = stack.pop()
+                if d == depth or rng.random() < 0.25:
+                    f[h] = -1
+                    tb[h] = (0, 0, 0, 0, 1, lv[h])
+                else:
+                    f[h] = rng.integers(F)
+                    tb[h] = (f[h], b[h], 2 * h + 1, 2 * h + 2, 0, 0)
+                    stack += [(2 * h + 1, d + 1), (2 * h + 2, d + 1)]
+    return feat, binv, leaf, tables
+
+
+# name, rows, features, bins, classes, rounds, depth: the LDS-resident
+# predictor (also with single-leaf trees and blocks of 9 rows), the row-block
+# predictor (partial last tree chunk and row block, deep trees, one round
+# per tree chunk) and the heap walker
+PRED_CASES = [
+    ("resident", 5000, 40, 16, 1, 30, 5),
+    ("rows_partial_chunk", 7001, 100, 32, 10, 23, 6),
+    ("rows_deep", 3000, 20, 8, 1, 50, 9),
+    ("rows_one_round_per_chunk", 2000, 30, 8, 3, 4, 10),
+    ("resident_depth0", 500, 10, 4, 10, 200, 0),
+    ("heap", 3000, 30, 8, 10, 3, 10),
+    ("heap_depth0", 500, 10, 4, 10, 2000, 0),
+]
+
+
+@pytest.mark.parametrize("case", PRED_CASES, ids=[c[0] for c in PRED_CASES])
+def test_predict_heap_paths_bit_exact(gpu, case):
+    """wgbm_predict_heap (the estimator's predictor) on raw codes with values
+    outside [0, B) equals the reference-table walk (warpgbm/cuda/predict.cu:
+    23-44, trees added in (round, class) order) bit for bit, whichever of its
+    three kernels the shape selects."""
+    name, N, F, B, K, R, depth = case
+    print_case("predict_heap", name)
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    raw = rng.integers(-2, B + 3, (N, F)).astype(np.int8)
+    feat, binv, leaf, tables = _random_heap(rng, R, K, depth, F, B)
+    out0 = rng.standard_normal((N, K)).astype(F32)
+    codes = D.codes_from_int8(D.upload_int8(raw, dev), False, B)[0]
+    out = t(out0)
+    D.predict_heap(codes, t(feat), t(binv), t(leaf), R, K, depth, 0.1, out)
+    cls = np.tile(np.arange(K, dtype=np.int32), R)
+    ref = clib.predict_tables(raw, tables, F32(0.1), out0, cls)
+    assert np.array_equal(bits(out.cpu().numpy()), bits(ref))
+
+
 def native_layout(raw, num_bins, stride):
     """The library's native row-major code layout (include/warpgbm_amd.h):
     codes in [0, B) as is, negative codes B, codes >= B and padding B + 1."""

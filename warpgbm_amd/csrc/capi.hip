@@ -510,7 +510,8 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
     cleaf = reinterpret_cast<float*>(cnode + T * ((H - 1) / 2));
     const int64_t work = T * H;
     hipLaunchKernelGGL(complete_tables_kernel, dim3(nblocks(work, 256)), dim3(256), 0,
-                       S(stream), feat, bin, leaf, T, max_depth, codes_stride, cnode, cleaf);
+                       S(stream), feat, bin, leaf, T, max_depth, codes_stride, learning_rate,
+                       cnode, cleaf);
     WGBM_LAUNCH_CHECK();
   }
   if (resident) {
@@ -524,7 +525,7 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
     const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(n_cu, nblocks(n, RB)));
     hipLaunchKernelGGL(predict_resident_kernel, dim3((unsigned)grid), dim3(1024), lds, S(stream),
                        codes, n, codes_stride, num_bins, (const uint32_t*)cnode,
-                       (const float*)cleaf, n_rounds * K, K, max_depth, learning_rate, RB, out);
+                       (const float*)cleaf, n_rounds * K, K, max_depth, RB, out);
   } else if (rows) {
     static bool attr = false;
     if (!attr) {
@@ -534,7 +535,7 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
     }
     hipLaunchKernelGGL(predict_rows_kernel, dim3(nblocks(n, RB)), dim3(1024), lds, S(stream),
                        codes, n, codes_stride, num_bins, (const uint32_t*)cnode,
-                       (const float*)cleaf, n_rounds, K, max_depth, learning_rate, RB, TC, out);
+                       (const float*)cleaf, n_rounds, K, max_depth, RB, TC, out);
   } else {
     hipLaunchKernelGGL(predict_heap_kernel, dim3(nblocks(n * K, 256)), dim3(256), 0, S(stream),
                        codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds, K, H,

@@ -319,18 +319,18 @@ __global__ void predict_heap_kernel(const int8_t* codes, int64_t n, int64_t S, i
                                     int32_t n_rounds, int32_t K, int32_t H, int32_t max_depth,
                                     float lr, float* out);
 __global__ void complete_tables_kernel(const int32_t* feat, const int32_t* bin, const float* leaf,
-                                       int64_t T, int32_t D, int64_t S, uint32_t* cnode,
-                                       float* cleaf);
+                                       int64_t T, int32_t D, int64_t S, float lr,
+                                       uint32_t* cnode, float* cleaf);
 __global__ void predict_rows_kernel(const int8_t* codes, int64_t n, int64_t S, int32_t num_bins,
                                     const uint32_t* cnode, const float* cleaf, int32_t n_rounds,
-                                    int32_t K, int32_t max_depth, float lr, int32_t RB, int32_t TC,
+                                    int32_t K, int32_t max_depth, int32_t RB, int32_t TC,
                                     float* out);
 int predict_rows_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
                       int32_t* TC_out, size_t* lds_out);
 __global__ void predict_resident_kernel(const int8_t* codes, int64_t n, int64_t S,
                                         int32_t num_bins, const uint32_t* cnode,
                                         const float* cleaf, int32_t T, int32_t K,
-                                        int32_t max_depth, float lr, int32_t RB, float* out);
+                                        int32_t max_depth, int32_t RB, float* out);
 int predict_resident_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
                           size_t* lds_out);
 __global__ void softmax_rows_kernel(float* x, int64_t n, int32_t K);

@@ -83,18 +83,19 @@ __global__ void predict_heap_kernel(const int8_t* __restrict__ codes, int64_t n,
 }
 
 // Complete-tree tables for the LDS predictors.  Per tree: (2^D - 1) node
-// words for the levels above the last, feature << 8 | bin for a split whose
+// words for the levels above the last, feature << 16 | bin for a split whose
 // ancestors are all splits, else (a leaf, an absent node, or any position
 // under one) the always-left word 255 (every code byte is <= 255); and 2^D
-// last-level values, slot s = the leaf value of the first node on the path
-// from the root to heap node 2^D - 1 + s that is not a split (or of that node
-// itself).  A walk then takes exactly D steps with no leaf test and reaches
+// last-level values, slot s = lr times the leaf value of the first node on
+// the path from the root to heap node 2^D - 1 + s that is not a split (or of
+// that node itself), rounded to float32 as the walkers' per-tree products
+// are.  A walk then takes exactly D steps with no leaf test and reaches
 // the value the heap walk stops at.  Features are clamped into the row
-// (S - 1), as the walkers clamp them.
+// (S - 1 < 65536), as the walkers clamp them.
 __global__ void complete_tables_kernel(const int32_t* __restrict__ feat,
                                        const int32_t* __restrict__ bin,
                                        const float* __restrict__ leaf, int64_t T, int32_t D,
-                                       int64_t S, uint32_t* __restrict__ cnode,
+                                       int64_t S, float lr, uint32_t* __restrict__ cnode,
                                        float* __restrict__ cleaf) {
   const int Hi = (1 << D) - 1, L = 1 << D, H = 2 * L - 1;
   const int64_t per = (int64_t)Hi + L;
@@ -110,7 +111,7 @@ __global__ void complete_tables_kernel(const int32_t* __restrict__ feat,
     uint32_t w = 255u;
     if (split) {
       const int64_t f = ft[j] < S ? ft[j] : S - 1;
-      w = ((uint32_t)f << 8) | ((uint32_t)bin[t * H + j] & 0xffu);
+      w = ((uint32_t)f << 16) | ((uint32_t)bin[t * H + j] & 0xffu);
     }
     cnode[t * Hi + j] = w;
   } else {
@@ -124,7 +125,88 @@ __global__ void complete_tables_kernel(const int32_t* __restrict__ feat,
         break;
       }
     }
-    cleaf[t * L + sl] = leaf[t * H + a];
+    cleaf[t * L + sl] = lr * leaf[t * H + a];
+  }
+}
+
+// Code bytes as the LDS walkers read them: a native byte equal to num_bins (a
+// negative code, left at every split) becomes 0, which also goes left at
+// every split (split bins are >= 0), so a walk step is one compare: right iff
+// code > bin.  bb = num_bins * 0x01010101.
+__device__ __forceinline__ uint32_t walk_bytes(uint32_t x, uint32_t bb) {
+  const uint32_t t = x ^ bb;  // zero bytes where x has num_bins
+  // 0x80 in every byte of t that is not zero (no carries between bytes)
+  const uint32_t nz = (((t & 0x7f7f7f7fu) + 0x7f7f7f7fu) | t) & 0x80808080u;
+  return x & ((nz >> 7) * 0xffu);
+}
+
+// A walk over a complete table held in LDS, stepped by LDS byte address: the
+// tree's node words start at `base`, node g (1-based heap index, children 2g
+// and 2g + 1) sits at a = base + 4 (g - 1), so the step to child 2g + x is
+// a' = 2a + 4 + 4x - base (mod 2^32): one compare, one select, one shift-add
+// and the row byte's address per step.
+typedef __attribute__((address_space(3))) uint32_t lds_u32_t;
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_u8_t*)p;
+}
+
+struct Walk {
+  uint32_t a, k0, k1;  // node address; step offsets for left / right
+  __device__ __forceinline__ void start(uint32_t base) {
+    a = base;
+    k0 = 4u - base;
+    k1 = 8u - base;
+    // opaque to the optimiser, which would otherwise fold the select back into
+    // select(4, 8) - base, one more instruction per step
+    __asm__("" : "+v"(k0), "+v"(k1));
+  }
+  // row: LDS address of the row's first code byte
+  __device__ __forceinline__ void step(uint32_t row) {
+    const uint32_t w = *(const lds_u32_t*)(uintptr_t)a;
+    const uint32_t c = *(const lds_u8_t*)(uintptr_t)(row + (w >> 16));
+    a = 2u * a + (c > (w & 0xffu) ? k1 : k0);
+  }
+};
+
+typedef __attribute__((address_space(3))) float lds_f32_t;
+
+// Walks the trees j = j_first, j_first + G, ... (j < n_trees) of one row, NW
+// in lock-step, and stores each tree's value at out_a + 4j.  LDS byte
+// addresses: row_a = the row's code bytes, nodes_a = tree 0's node words (Hi
+// per tree), values_a = tree 0's last-level values (Hi + 1 per tree).  After
+// D steps a walk of tree j sits at a = nodes_a + 4 (j Hi + g - 1) with g =
+// 2^D + slot, so its value is at a + c0 + 4j, c0 = values_a - nodes_a + 4 -
+// 4 (Hi + 1): every address is an add, and the trees' node words advance by
+// a uniform stride.  An idle walk (past n_trees, or row_on false) walks tree
+// 0 and stores nothing.
+template <int NW>
+__device__ __forceinline__ void walk_trees(int j_first, int n_trees, int G, bool row_on,
+                                           uint32_t row_a, uint32_t nodes_a, uint32_t values_a,
+                                           int Hi, int D, uint32_t out_a) {
+  const uint32_t hi4 = 4u * (uint32_t)Hi, nstep = hi4 * (uint32_t)G;
+  const uint32_t c0 = values_a - nodes_a + 4u - 4u * (uint32_t)(Hi + 1);
+  uint32_t nb = nodes_a + hi4 * (uint32_t)j_first;  // node words of tree j0
+  for (int j0 = j_first; j0 < n_trees; j0 += NW * G, nb += NW * nstep) {
+    Walk wk[NW];
+    uint32_t t4[NW];
+    bool on[NW];
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
+      on[k] = row_on && j0 + k * G < n_trees;
+      t4[k] = on[k] ? 4u * (uint32_t)(j0 + k * G) : 0u;
+      wk[k].start(on[k] ? nb + (uint32_t)k * nstep : nodes_a);
+    }
+    for (int d = 0; d < D; ++d) {
+#pragma unroll
+      for (int k = 0; k < NW; ++k) wk[k].step(row_a);
+    }
+#pragma unroll
+    for (int k = 0; k < NW; ++k)
+      if (on[k])
+        *(lds_f32_t*)(uintptr_t)(out_a + t4[k]) =
+            *(const lds_f32_t*)(uintptr_t)(wk[k].a + c0 + t4[k]);
   }
 }
 
@@ -134,19 +216,20 @@ __global__ void complete_tables_kernel(const int32_t* __restrict__ feat,
 // the trees a chunk of TC at a time: the chunk's complete-tree tables
 // (complete_tables_kernel) are staged in LDS, every (row, tree) pair of the
 // chunk is walked by its own thread (all walks independent: D dependent LDS
-// reads each instead of D per tree in sequence), the products lr * leaf go to
-// an LDS table [row][tree], and one thread per (row, class) adds them in tree
-// order.  TC is a multiple of K, so tree t0 + j belongs to class j % K.
+// reads each instead of D per tree in sequence), the products lr * leaf (the
+// tables hold them) go to an LDS table [row][tree], and one thread per (row,
+// class) adds them in tree order.  TC is a multiple of K, so tree t0 + j belongs to class j % K.
 //   LDS: rows [RB][S + 4] bytes (a 4-byte pad per row spreads the rows of
 //   one wave over the banks), node words [TC][2^D - 1], last-level values
 //   [TC][2^D], vals [RB][TC + 1] (odd row stride: no bank conflicts).
 constexpr int kPredThreads = 1024;
 constexpr int kPredMaxAcc = 4;  // (row, class) accumulators per thread
+constexpr int kPredWalks = 2;   // walks a thread advances in lock-step
 
 __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
     const int8_t* __restrict__ codes, int64_t n, int64_t S, int32_t num_bins,
     const uint32_t* __restrict__ cnode, const float* __restrict__ cleaf, int32_t n_rounds,
-    int32_t K, int32_t max_depth, float lr, int32_t RB, int32_t TC, float* __restrict__ out) {
+    int32_t K, int32_t max_depth, int32_t RB, int32_t TC, float* __restrict__ out) {
   extern __shared__ uint32_t psm[];
   const int Sp = (int)S + 4;
   const int Hi = (1 << max_depth) - 1, L = 1 << max_depth;  // complete-table widths
@@ -157,6 +240,7 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
   const int64_t row0 = (int64_t)blockIdx.x * RB;
   const int nr = (int)(n - row0 < RB ? n - row0 : RB);
   const int tid = threadIdx.x;
+  const uint32_t bb = (uint32_t)num_bins * 0x01010101u;
   // stage the row block: 16-byte global loads, 4-byte LDS stores
   {
     const int q_per_row = (int)(S / 16);
@@ -167,10 +251,10 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
       const u4 v = __builtin_nontemporal_load(
           reinterpret_cast<const u4*>(codes + (row0 + r) * S) + c);
       uint32_t* dst = reinterpret_cast<uint32_t*>(rows_s + r * Sp + c * 16);
-      dst[0] = v.x;
-      dst[1] = v.y;
-      dst[2] = v.z;
-      dst[3] = v.w;
+      dst[0] = walk_bytes(v.x, bb);
+      dst[1] = walk_bytes(v.y, bb);
+      dst[2] = walk_bytes(v.z, bb);
+      dst[3] = walk_bytes(v.w, bb);
     }
   }
   // accumulators: pair m*1024 + tid = (row, class) = (p % RB, p / RB)
@@ -196,31 +280,9 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
     // wt0, wt0 + G, ... (G = threads / RB row groups, no division per walk),
     // two in lock-step so that the LDS reads of one overlap those of the
     // other; max_depth steps on the complete tables (no leaf test)
-    if (walker) {
-      const bool row_on = wr < nr;
-      const uint8_t* row = rows_s + wr * Sp;
-      for (int j0 = wt0; j0 < tc; j0 += 2 * G) {
-        int tl[2], h[2];
-        bool on[2];
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          on[k] = row_on && j0 + k * G < tc;
-          tl[k] = on[k] ? j0 + k * G : 0;  // an idle walk reads tree 0 and stores nothing
-          h[k] = 0;
-        }
-        for (int d = 0; d < max_depth; ++d) {
-#pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            const uint32_t w = nodes_s[tl[k] * Hi + h[k]];
-            const int c = (int)row[w >> 8];
-            h[k] = 2 * h[k] + ((c <= (int)(w & 0xffu) || c == num_bins) ? 1 : 2);
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-          if (on[k]) vals_s[wr * (TC + 1) + tl[k]] = lr * leaves_s[tl[k] * L + h[k] - Hi];
-      }
-    }
+    if (walker)
+      walk_trees<kPredWalks>(wt0, tc, G, wr < nr, lds_addr(rows_s + wr * Sp), lds_addr(nodes_s),
+                             lds_addr(leaves_s), Hi, max_depth, lds_addr(vals_s + wr * (TC + 1)));
     __syncthreads();
     // ordered sums: trees t0 + j of class k are j = k, k + K, ... (t0 % K == 0)
 #pragma unroll
@@ -251,7 +313,8 @@ __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
 //     is walked (QPT 16-byte loads per thread), then stored to the LDS row
 //     buffer after the walks;
 //   * waves 1..15 walk the (row, tree) pairs of the block, two per thread
-//     in lock-step, and write lr * leaf to a per-block value table [RB][T + 1];
+//     in lock-step, and write lr * leaf (from the tables) to a per-block value
+//     table [RB][T + 1];
 //   * wave 0 meanwhile adds the previous block's table to `out` in tree
 //     order (one lane per (row, class)), so the ordered sums run beside the
 //     walks; the value tables alternate between two buffers.
@@ -263,7 +326,7 @@ constexpr int kResWalks = 2;  // walks a walker thread advances in lock-step
 __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
     const int8_t* __restrict__ codes, int64_t n, int64_t S, int32_t num_bins,
     const uint32_t* __restrict__ cnode, const float* __restrict__ cleaf, int32_t T, int32_t K,
-    int32_t max_depth, float lr, int32_t RB, float* __restrict__ out) {
+    int32_t max_depth, int32_t RB, float* __restrict__ out) {
   extern __shared__ uint32_t psm[];
   const int Sp = (int)S + 4;
   const int TV = T + 1;  // value-table row stride (odd or even, see below)
@@ -274,6 +337,7 @@ __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
   float* vals_s = reinterpret_cast<float*>(rows_s + RB * Sp);  // 2 x [RB][TV]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  const uint32_t bb = (uint32_t)num_bins * 0x01010101u;
   for (int i = tid; i < T * Hi; i += kResThreads) nodes_s[i] = cnode[i];
   for (int i = tid; i < T * L; i += kResThreads) leaves_s[i] = cleaf[i];
   const int64_t nblk = (n + RB - 1) / RB;
@@ -299,10 +363,10 @@ __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
       if (q < nq) {
         const int r = q / qpr, c = q - r * qpr;
         uint32_t* dst = reinterpret_cast<uint32_t*>(rows_s + r * Sp + c * 16);
-        dst[0] = pre[u].x;
-        dst[1] = pre[u].y;
-        dst[2] = pre[u].z;
-        dst[3] = pre[u].w;
+        dst[0] = walk_bytes(pre[u].x, bb);
+        dst[1] = walk_bytes(pre[u].y, bb);
+        dst[2] = walk_bytes(pre[u].z, bb);
+        dst[3] = walk_bytes(pre[u].w, bb);
       }
     }
   };
@@ -351,31 +415,8 @@ __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
     } else if (walker) {
       const int64_t row0 = b * RB;
       const int nr = (int)(n - row0 < RB ? n - row0 : RB);
-      const bool row_on = wr < nr;
-      const uint8_t* row = rows_s + wr * Sp;
-      float* vrow = vt + wr * TV;
-      for (int t0 = wt0; t0 < T; t0 += kResWalks * G) {
-        int tl[kResWalks], h[kResWalks];
-        bool on[kResWalks];
-#pragma unroll
-        for (int k = 0; k < kResWalks; ++k) {
-          on[k] = row_on && t0 + k * G < T;
-          tl[k] = on[k] ? t0 + k * G : 0;  // an idle walk reads tree 0 and stores nothing
-          h[k] = 0;
-        }
-        // max_depth steps on the complete tables (no leaf test)
-        for (int d = 0; d < max_depth; ++d) {
-#pragma unroll
-          for (int k = 0; k < kResWalks; ++k) {
-            const uint32_t w = nodes_s[tl[k] * Hi + h[k]];
-            const int c = (int)row[w >> 8];
-            h[k] = 2 * h[k] + ((c <= (int)(w & 0xffu) || c == num_bins) ? 1 : 2);
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < kResWalks; ++k)
-          if (on[k]) vrow[tl[k]] = lr * leaves_s[tl[k] * L + h[k] - Hi];
-      }
+      walk_trees<kResWalks>(wt0, T, G, wr < nr, lds_addr(rows_s + wr * Sp), lds_addr(nodes_s),
+                            lds_addr(leaves_s), Hi, max_depth, lds_addr(vt + wr * TV));
     }
     prev = b;
     __syncthreads();  // the walks are done: the row buffer can be refilled
@@ -394,7 +435,7 @@ int predict_resident_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int
   constexpr int64_t kBudget = 150 * 1024;
   const int64_t T = (int64_t)n_rounds * K;
   // complete tables: (H - 1) / 2 node words and (H + 1) / 2 values per tree
-  if (S % 16 != 0 || S >= (1 << 20) || T * H * 4 > 64 * 1024) return 0;
+  if (S % 16 != 0 || S > (1 << 16) || T * H * 4 > 64 * 1024) return 0;
   const int64_t Sp = S + 4;
   // RB rows: the row buffer, two value tables and at most kResMaxQ loads per thread
   int64_t RB = (kBudget - 4 * T * H) / (Sp + 8 * (T + 1));
@@ -412,7 +453,7 @@ int predict_rows_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t
                       int32_t* TC_out, size_t* lds_out) {
   constexpr int64_t kBudget = 64 * 1024;
   // complete tables: (H - 1) / 2 node words and (H + 1) / 2 values per tree
-  if (S % 16 != 0 || S >= (1 << 24) || (int64_t)4 * H * K > 32 * 1024) return 0;
+  if (S % 16 != 0 || S > (1 << 16) || (int64_t)4 * H * K > 32 * 1024) return 0;
   const int64_t T = (int64_t)n_rounds * K;
   int64_t m = std::max<int64_t>(1, (16 * 1024) / ((int64_t)4 * H * K));
   int64_t TC = std::min<int64_t>(m * K, std::max<int64_t>(K, (T + K - 1) / K * K));
