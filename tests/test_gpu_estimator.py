@@ -515,3 +515,48 @@ def test_one_era_level_scans_bit_exact(gpu, scan, fuse):
     for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
         assert a == b, f"300-feature tree {i} differs"
     assert "'feature': 280" in str(m.forest[0]) or "'feature': 7" in str(m.forest[0])
+
+
+def test_predict_reads_split_columns_only(gpu):
+    """Inputs of >= 65536 rows are binned only in the columns the forest
+    splits on (gathered on the host, uploaded and binned as a narrow code
+    matrix): the predictions equal the full binning path and the oracle's,
+    bit for bit, for float32, float64 and non-contiguous input, regression
+    and multiclass."""
+    print_case("estimator", "predict from split columns")
+    rng = np.random.default_rng(11)
+    N, F = 20000, 300
+    X = rng.standard_normal((N, F)).astype(F32)
+    y = (2.0 * X[:, 7] - X[:, 150] + 0.5 * X[:, 299] + 0.1 * rng.standard_normal(N)).astype(F32)
+    m = WarpGBM(num_bins=32, max_depth=4, n_estimators=10, learning_rate=0.1)
+    m.fit(X, y)
+    cols, _ = m._used_features()
+    assert 2 * len(cols) <= F and {7, 150} <= set(cols.tolist())
+    Xt = rng.standard_normal((70_001, F)).astype(F32)
+    p = m.predict(Xt)
+    full = m.predict_binned(m.bin_inference_data(Xt)).cpu().numpy()
+    assert np.array_equal(bits(p), bits(full))
+    ref = gbm.Forest(num_bins=32, max_depth=4, n_estimators=10, learning_rate=0.1,
+                     min_child_weight=20, min_split_gain=0.0, L2_reg=1e-6)
+    ref.forest, ref.base = m.forest, F32(m.base_prediction)
+    codes_t = ops.bin_matrix(Xt, torch.as_tensor(m.bin_edges).cpu().numpy())
+    assert np.array_equal(bits(p), bits(ref.predict_codes(codes_t)))
+    assert np.array_equal(bits(m.predict(Xt.astype(np.float64))), bits(p))
+    assert np.array_equal(bits(m.predict(np.asfortranarray(Xt))), bits(p))
+
+    K = 3
+    lab = rng.integers(0, K, N)
+    Xc = rng.standard_normal((N, F)).astype(F32)
+    Xc[:, 11] += 2.0 * lab
+    Xc[:, 201] -= 1.5 * lab
+    mc = WarpGBM(objective="multiclass", num_bins=16, max_depth=3, n_estimators=6,
+                 learning_rate=0.2)
+    mc.fit(Xc, lab)
+    cols, _ = mc._used_features()
+    assert 2 * len(cols) <= F
+    Xct = rng.standard_normal((66_000, F)).astype(F32)
+    Xct[:, 11] += 2.0 * rng.integers(0, K, len(Xct))
+    pr = mc.predict_proba(Xct)
+    full = mc.predict_proba_binned(mc.bin_inference_data(Xct)).cpu().numpy()
+    assert np.array_equal(bits(pr), bits(full))
+    assert np.array_equal(mc.predict(Xct), mc.classes_[np.argmax(full, axis=1)])

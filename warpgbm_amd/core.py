@@ -34,6 +34,8 @@ from . import node_kernel
 from .metrics import accuracy_torch, log_loss_torch, rmsle_torch, softmax
 
 _TIMING = os.environ.get("WGBM_TIMING", "") not in ("", "0")
+# predict inputs from this many rows on read only the forest's split columns
+_NARROW_MIN_ROWS = 1 << 16
 
 
 class _Phases:
@@ -188,6 +190,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         self._is_fitted = False
         self._trees_trained = 0
         self._heap = None  # device heap tables of the fitted forest (cache)
+        self._heap_used = None  # (heap, split features, tables over them) (cache)
 
     # ------------------------------------------------------------------ validation
     def _validate_hyperparams(self, **kwargs):
@@ -779,23 +782,65 @@ class WarpGBM(BaseEstimator, RegressorMixin):
             self._heap = self._heap_tables(self.forest)
         return self._heap
 
-    def predict_binned(self, codes):
+    def _used_features(self):
+        """The features the fitted forest splits on (sorted) and its heap
+        tables with every split feature replaced by its index in that list.
+        Cached with the tables they were derived from."""
+        heap = self._cached_heap()
+        if self._heap_used is None or self._heap_used[0] is not heap:
+            feat = heap[0]
+            used = torch.unique(feat[feat >= 0])  # sorted
+            if used.numel() == 0:
+                used = torch.zeros(1, dtype=feat.dtype, device=feat.device)
+            lut = torch.full((self.num_features,), -1, dtype=feat.dtype, device=feat.device)
+            lut[used.long()] = torch.arange(used.numel(), dtype=feat.dtype, device=feat.device)
+            local = torch.where(feat >= 0, lut[feat.clamp(min=0).long()], feat).contiguous()
+            self._heap_used = (heap, used.cpu().numpy().astype(np.intp),
+                               (local, heap[1], heap[2], heap[3]))
+        return self._heap_used[1], self._heap_used[2]
+
+    def _inference_codes(self, X_np):
+        """Codes of new data and the heap tables that walk them.  A prediction
+        reads only the codes of the features the forest splits on: for float
+        input (binned with the training edges, warpgbm/core.py:902-915) where
+        those are at most half of the columns, only their columns are gathered
+        on the host, uploaded and binned, and the tables index that narrow
+        code matrix.  The codes of the features read are the same as in the
+        full matrix, so the predictions are identical."""
+        X_np = np.asarray(X_np)
+        heap = self._cached_heap()
+        if (heap[3] and X_np.ndim == 2 and np.issubdtype(X_np.dtype, np.floating)
+                and X_np.shape[1] == self.num_features and X_np.shape[0] >= _NARROW_MIN_ROWS):
+            cols, tables = self._used_features()
+            if 2 * len(cols) <= X_np.shape[1]:
+                codes = D.upload_and_bin(X_np, torch.as_tensor(self.bin_edges),
+                                         torch.device(self.device), cols=cols)
+                return codes, tables
+        return self.bin_inference_data(X_np), heap
+
+    def _predict_values(self, codes, tables):
         out = torch.full((codes.n, 1), np.float32(self.base_prediction), dtype=torch.float32,
                          device=torch.device(self.device))
-        feat, bin_, leaf, n = self._cached_heap()
+        feat, bin_, leaf, n = tables
         if n:
             D.predict_heap(codes, feat, bin_, leaf, n, 1, self.max_depth, self.learning_rate, out)
         return out[:, 0]
 
-    def predict_proba_binned(self, codes):
+    def _predict_scores(self, codes, tables):
         dev = torch.device(self.device)
         scores = D.rows_of(self._uniform_prior_logits(), codes.n, dev)
-        feat, bin_, leaf, n = self._cached_heap()
+        feat, bin_, leaf, n = tables
         if n:
             D.predict_heap(codes, feat, bin_, leaf, n, self.num_classes, self.max_depth,
                            self.learning_rate, scores)
         D.softmax_rows(scores)
         return scores
+
+    def predict_binned(self, codes):
+        return self._predict_values(codes, self._cached_heap())
+
+    def predict_proba_binned(self, codes):
+        return self._predict_scores(codes, self._cached_heap())
 
     def predict(self, X_np):
         """Regression values, or class labels for classification (warpgbm/core.py:957-974)."""
@@ -803,9 +848,9 @@ class WarpGBM(BaseEstimator, RegressorMixin):
             probs = self.predict_proba(X_np)
             return self.label_encoder.inverse_transform(np.argmax(probs, axis=1))
         ph = _Phases()
-        codes = self.bin_inference_data(X_np)
+        codes, tables = self._inference_codes(X_np)
         ph.mark("codes")
-        out = self.predict_binned(codes)
+        out = self._predict_values(codes, tables)
         ph.mark("trees")
         preds = D.to_host(out)
         ph.mark("copy out")
@@ -817,8 +862,8 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         """Class probabilities (warpgbm/core.py:976-989)."""
         if self.objective not in ["multiclass", "binary"]:
             raise ValueError("predict_proba only available for classification objectives")
-        codes = self.bin_inference_data(X_np)
-        probs = D.to_host(self.predict_proba_binned(codes))
+        codes, tables = self._inference_codes(X_np)
+        probs = D.to_host(self._predict_scores(codes, tables))
         del codes
         return probs
 

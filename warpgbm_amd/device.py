@@ -90,6 +90,7 @@ def codes_from_int8(x8: torch.Tensor, with_cm: bool, num_bins: int, check: bool 
 
 _STAGE_BYTES = 64 << 20   # one pinned staging buffer
 _STAGE_COUNT = 4          # buffers in rotation
+_NARROW_CHUNK_ROWS = 131072  # rows per chunk of a column-subset upload
 _stage_lock = threading.Lock()
 _stage_bufs: list = []
 _pool = None
@@ -158,24 +159,37 @@ def _upload_staged(X: np.ndarray, dev, np_dtype, torch_dtype) -> torch.Tensor:
     return out
 
 
-def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev) -> Codes:
+def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev, cols=None) -> Codes:
     """Row-major native codes of a host float matrix for known edges
     [F, num_bins - 1] (predict-time binning, warpgbm/core.py:902-915): the rows
     stream through the pinned staging buffers and a few device chunk buffers,
     and each chunk is binned as soon as its copy lands, so the float matrix is
-    never whole on the device and the binning overlaps the transfer."""
+    never whole on the device and the binning overlaps the transfer.
+
+    With ``cols`` (feature indices) only those columns are gathered (host
+    threads, straight into the staging buffers), uploaded and binned: code
+    column j holds feature cols[j]."""
     X = np.asarray(X)
     n, F = X.shape
-    row_bytes = 4 * max(F, 1)
-    if n * row_bytes < 4 * _STAGE_BYTES or not X.flags.c_contiguous:
-        return bin_matrix(upload_float(X, dev), edges, with_cm=False)
     edges = edges.to(device=dev, dtype=torch.float32).contiguous()
     if edges.shape[0] != F:
         raise ValueError(f"edges for {edges.shape[0]} features, X has {F}")
-    c = _alloc_codes(n, F, dev, False, edges.shape[1] + 1)
+    if cols is not None:
+        cols = np.ascontiguousarray(cols, dtype=np.intp)
+        if cols.ndim != 1 or len(cols) == 0 or cols.min() < 0 or cols.max() >= F:
+            raise ValueError("cols must be a non-empty list of feature indices")
+        edges = edges[torch.from_numpy(cols).to(dev)].contiguous()
+    Fw = F if cols is None else len(cols)
+    row_bytes = 4 * max(Fw, 1)
+    if (n * 4 * max(F, 1) < 4 * _STAGE_BYTES and cols is None) or not X.flags.c_contiguous:
+        Xs = X if cols is None else np.take(X, cols, axis=1)
+        return bin_matrix(upload_float(Xs, dev), edges, with_cm=False)
+    c = _alloc_codes(n, Fw, dev, False, edges.shape[1] + 1)
     bufs, pool = _staging()
     rows_per = max(1, _STAGE_BYTES // row_bytes)
-    dbufs = [torch.empty((rows_per, F), dtype=torch.float32, device=dev)
+    if cols is not None:
+        rows_per = min(rows_per, _NARROW_CHUNK_ROWS)  # several chunks in flight
+    dbufs = [torch.empty((rows_per, Fw), dtype=torch.float32, device=dev)
              for _ in range(len(bufs))]
     lib = _lib.load()
     side = torch.cuda.Stream(device=dev)
@@ -185,14 +199,20 @@ def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev) -> Codes:
     nthreads = pool._max_workers
 
     def fill(dst, lo, hi):
-        np.copyto(dst[lo:hi], X[r0 + lo:r0 + hi], casting="same_kind")
+        src = X[r0 + lo:r0 + hi]
+        if cols is None:
+            np.copyto(dst[lo:hi], src, casting="same_kind")
+        elif X.dtype == np.float32:
+            np.take(src, cols, axis=1, out=dst[lo:hi], mode="clip")  # cols are in range
+        else:
+            np.copyto(dst[lo:hi], np.take(src, cols, axis=1), casting="same_kind")
 
     for i, r0 in enumerate(range(0, n, rows_per)):
         r1 = min(n, r0 + rows_per)
         k = i % len(bufs)
         if events[k] is not None:
             events[k].synchronize()  # the copy that used this staging buffer is done
-        host = bufs[k][: (r1 - r0) * row_bytes].view(torch.float32).view(r1 - r0, F)
+        host = bufs[k][: (r1 - r0) * row_bytes].view(torch.float32).view(r1 - r0, Fw)
         dst = host.numpy()
         step = max(1, (r1 - r0 + nthreads - 1) // nthreads)
         list(pool.map(lambda a: fill(dst, a, min(a + step, r1 - r0)), range(0, r1 - r0, step)))
@@ -203,7 +223,7 @@ def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev) -> Codes:
             ev = torch.cuda.Event()
             ev.record(side)
         events[k] = ev
-        rc = lib.wgbm_bin_matrix(dbufs[k].data_ptr(), r1 - r0, F, F, edges.data_ptr(),
+        rc = lib.wgbm_bin_matrix(dbufs[k].data_ptr(), r1 - r0, Fw, Fw, edges.data_ptr(),
                                  edges.shape[1], c.rm.data_ptr() + r0 * c.stride, c.stride, None,
                                  side_ptr)
         _lib.check(rc, "bin_matrix")
