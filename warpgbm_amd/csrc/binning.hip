@@ -102,11 +102,15 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
   const int nvf = F - fq < 4 ? (F - fq > 0 ? F - fq : 0) : 4;  // its real features
   const int8_t pad = (int8_t)(n_edges + 2);                     // num_bins + 1
   const bool rm_words = (S & 3) == 0 && ((uintptr_t)codes_rm & 3) == 0;
+  // thread (g, q) bins rows k0 + BT_U g + u (u < BT_U) of its feature quad, so
+  // that its codes of one feature for those rows form one 32-bit word of the
+  // transposed tile (lanes of a wave then store to distinct banks)
+  static_assert(BT_U == 4, "a transposed word holds the codes of four rows");
   for (int k0 = 0; k0 < BT_R; k0 += 16 * BT_U) {
     float v[BT_U][4];
 #pragma unroll
     for (int u = 0; u < BT_U; ++u) {
-      const int64_t r = r0 + k0 + g + 16 * u;
+      const int64_t r = r0 + k0 + BT_U * g + u;
 #pragma unroll
       for (int c = 0; c < 4; ++c) v[u][c] = 0.0f;
       if (r < n) {
@@ -124,16 +128,17 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
         }
       }
     }
+    uint32_t tw[4] = {0u, 0u, 0u, 0u};  // feature c's codes of the thread's rows
 #pragma unroll
     for (int u = 0; u < BT_U; ++u) {
-      const int k = k0 + g + 16 * u;
+      const int k = k0 + BT_U * g + u;
       const int64_t r = r0 + k;
       uint32_t word = 0;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int8_t code =
             c < nvf ? (int8_t)count_le(sedge + (4 * q + c) * n_edges, n_edges, v[u][c]) : pad;
-        tcode[4 * q + c][k] = code;
+        tw[c] |= (uint32_t)(uint8_t)code << (8 * u);
         word |= (uint32_t)(uint8_t)code << (8 * c);
       }
       if (r < n && fq < S) {
@@ -145,6 +150,9 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
         }
       }
     }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *reinterpret_cast<uint32_t*>(&tcode[4 * q + c][k0 + BT_U * g]) = tw[c];
   }
   if (!codes_cm) return;  // uniform over the workgroup
   __syncthreads();
