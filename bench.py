@@ -137,6 +137,11 @@ def main():
     ap.add_argument("--e2e-trees", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip C4 / C5 / C1 end to end")
+    ap.add_argument("--runs", type=int, default=2, choices=(1, 2),
+                    help="fit + predict runs per end-to-end config (the last is reported; "
+                         "with 2 the first is reported as *_cold_s)")
+    ap.add_argument("--extra", default="c1,c4,c5",
+                    help="the end-to-end configs run after C3 (comma list of c1, c4, c5)")
     ap.add_argument("--no-dropin", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates HBM byte counters)")
@@ -284,7 +289,7 @@ def main():
         # one-time costs (first large staged upload, first launch of each
         # kernel), the second is the steady state reported as train_s / infer_s
         runs = []
-        for run in range(2):
+        for run in range(args.runs):
             m = WarpGBM(num_bins=32, max_depth=5, n_estimators=args.e2e_trees,
                         learning_rate=0.01)
             torch.cuda.synchronize()
@@ -300,7 +305,7 @@ def main():
             runs.append((tr, time.perf_counter() - t0, p))
             mark(f"c3 end {run}")
         del X, y
-        (train_cold, infer_cold, _), (train_s, infer_s, p) = runs
+        (train_cold, infer_cold, _), (train_s, infer_s, p) = runs[0], runs[-1]
         corr = float(np.corrcoef(p, yt)[0, 1])
         e2e = {"train_s": round(train_s, 3), "infer_s": round(infer_s, 3),
                "train_cold_s": round(train_cold, 3), "infer_cold_s": round(infer_cold, 3),
@@ -357,7 +362,8 @@ def main():
     out.update(e2e)
     if not args.no_extra:
         for cfg in ("c1", "c4", "c5"):
-            out.update(run_extra(cfg))
+            if cfg in args.extra.split(","):
+                out.update(run_extra(cfg, args.runs))
     write_marks()
     print(json.dumps(out))
 
@@ -546,7 +552,7 @@ def c3_kernel_rooflines(m, Xt):
     return out
 
 
-def run_extra(cfg):
+def run_extra(cfg, n_runs=2):
     """End-to-end seconds of configs C1 (fit only), C4 (era-aware DES) and C5
     (softmax)."""
     import torch
@@ -570,7 +576,7 @@ def run_extra(cfg):
         print("[bench] generating C4 inputs", file=sys.stderr, flush=True)
         X, y, era = c4_inputs()
         runs = []
-        for run in range(2):  # the second run is the steady state (see the C3 leg)
+        for run in range(n_runs):  # the second run is the steady state (see the C3 leg)
             m = WarpGBM(num_bins=5, max_depth=8, n_estimators=100, learning_rate=0.1)
             torch.cuda.synchronize()
             mark(f"c4 fit {run}")
@@ -583,7 +589,7 @@ def run_extra(cfg):
             p = m.predict(X)
             runs.append((tr, time.perf_counter() - t0, p))
             mark(f"c4 end {run}")
-        (tr0, inf0, _), (tr, inf, p) = runs
+        (tr0, inf0, _), (tr, inf, p) = runs[0], runs[-1]
         corr = float(np.corrcoef(p, y)[0, 1])
         print(f"[bench] C4 train {tr:.3f} s (first run {tr0:.3f}), infer {inf:.3f} s "
               f"(first run {inf0:.3f}), in-sample corr {corr:.4f}", file=sys.stderr, flush=True)
@@ -595,7 +601,7 @@ def run_extra(cfg):
         X, lab = c5_inputs()
         Xt, labt = c5_inputs(rows_per_class=100_000, seed=1)
         runs = []
-        for run in range(2):  # the second run is the steady state (see the C3 leg)
+        for run in range(n_runs):  # the second run is the steady state (see the C3 leg)
             m = WarpGBM(objective="multiclass", num_bins=32, max_depth=6, n_estimators=200,
                         learning_rate=0.1)
             torch.cuda.synchronize()
@@ -609,7 +615,7 @@ def run_extra(cfg):
             proba = m.predict_proba(Xt)
             runs.append((tr, time.perf_counter() - t0, proba))
             mark(f"c5 end {run}")
-        (tr0, inf0, _), (tr, inf, proba) = runs
+        (tr0, inf0, _), (tr, inf, proba) = runs[0], runs[-1]
         acc = float((np.argmax(proba, axis=1) == labt).mean())
         print(f"[bench] C5 train {tr:.3f} s (first run {tr0:.3f}), predict_proba {inf:.3f} s "
               f"(first run {inf0:.3f}), acc {acc:.4f}", file=sys.stderr, flush=True)
