@@ -35,6 +35,32 @@ __global__ void bin_column_kernel(const float* __restrict__ x, int64_t n,
 }
 
 // #{j < ne : e[j] <= v} for sorted e (branch-free lower bound on the predicate)
+// The binner's edge lists in LDS are in breadth-first (Eytzinger) order:
+// node p of the complete search tree of 2^k - 1 nodes (k levels, the
+// smallest with 2^k - 1 >= ne) holds sorted edge (2j + 1) 2^(k-1-d) - 1,
+// d = depth of p, j = p + 1 - 2^d (edges past ne are +inf).  The search
+// descends k levels without a branch; every lane of a step reads within one
+// level, and feature lists start 1 mod 16 words apart (eytz_stride), so
+// the 16 features a wave searches at a time fall in different banks at the
+// top levels.  count = #{edges <= v} as count_le: a +inf value also counts
+// the +inf padding, hence the clamp to ne; NaN compares false: 0.
+__host__ __device__ inline int eytz_levels(int ne) {
+  int k = 0;
+  while ((1 << k) - 1 < ne) ++k;
+  return k;
+}
+__host__ __device__ inline int eytz_stride(int ne) {
+  const int nodes = (1 << eytz_levels(ne)) - 1;
+  const int m = nodes > 1 ? nodes : 1;
+  return (m - 1 + 15) / 16 * 16 + 1;
+}
+__device__ inline int eytz_count(const float* e, int k, int ne, float v) {
+  uint32_t idx = 0;
+  for (int s = 0; s < k; ++s) idx = 2u * idx + 1u + (v >= e[idx] ? 1u : 0u);
+  const int c = (int)idx - ((1 << k) - 1);
+  return c < ne ? c : ne;
+}
+
 __device__ inline int count_le(const float* e, int ne, float v) {
   int lo = 0, len = ne;
   while (len > 0) {
@@ -82,7 +108,7 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
     const float* __restrict__ edges, int32_t n_edges, int8_t* __restrict__ codes_rm, int64_t S,
     int8_t* __restrict__ codes_cm) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
-  extern __shared__ float sedge[];  // [BT_F][n_edges]
+  extern __shared__ float sedge[];  // [BT_F][eytz_stride(n_edges)], breadth-first order
   __shared__ __align__(4) int8_t tcode[BT_F][BT_R + 4];
   const int nft = (F + BT_F - 1) / BT_F;
   const int64_t n_work = (n + BT_R - 1) / BT_R * nft;
@@ -91,10 +117,20 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
   const int64_t r0 = w / nft * BT_R;
   const int f0 = (int)(w % nft) * BT_F;
   const int tid = threadIdx.x;
-  for (int i = tid; i < BT_F * n_edges; i += blockDim.x) {
-    const int fl = i / n_edges;
+  const int ek = eytz_levels(n_edges), es = eytz_stride(n_edges);
+  const int enodes = (1 << ek) - 1;
+  for (int i = tid; i < BT_F * es; i += blockDim.x) {
+    const int fl = i / es;
+    const int p = i - fl * es;
     const int f = f0 + fl;
-    sedge[i] = f < F ? edges[(int64_t)f * n_edges + (i - fl * n_edges)] : 0.0f;
+    float val = __builtin_inff();
+    if (p < enodes) {
+      const int d = 31 - __builtin_clz((unsigned)(p + 1));
+      const int j = p + 1 - (1 << d);
+      const int si = ((2 * j + 1) << (ek - 1 - d)) - 1;
+      if (f < F && si < n_edges) val = edges[(int64_t)f * n_edges + si];
+    }
+    sedge[i] = val;
   }
   __syncthreads();
   const int q = tid & 15, g = tid >> 4;
@@ -137,7 +173,7 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int8_t code =
-            c < nvf ? (int8_t)count_le(sedge + (4 * q + c) * n_edges, n_edges, v[u][c]) : pad;
+            c < nvf ? (int8_t)eytz_count(sedge + (4 * q + c) * es, ek, n_edges, v[u][c]) : pad;
         tw[c] |= (uint32_t)(uint8_t)code << (8 * u);
         word |= (uint32_t)(uint8_t)code << (8 * c);
       }
@@ -172,6 +208,8 @@ __global__ __launch_bounds__(256) void bin_matrix_kernel(
     }
   }
 }
+int bin_edge_stride(int32_t n_edges) { return eytz_stride(n_edges); }
+
 template __global__ void bin_matrix_kernel<true>(const float*, int64_t, int32_t, int64_t,
                                                  const float*, int32_t, int8_t*, int64_t, int8_t*);
 template __global__ void bin_matrix_kernel<false>(const float*, int64_t, int32_t, int64_t,

@@ -434,7 +434,7 @@ int wgbm_bin_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride
   WGBM_REQUIRE(n_edges >= 0 && n_edges <= 126, "n_edges must be in [0, 126]");
   if (n == 0) return 0;
   WGBM_REQUIRE(X && codes_rm && (n_edges == 0 || edges), "null pointer");
-  const size_t lds = sizeof(float) * 64 * std::max(n_edges, 1);
+  const size_t lds = sizeof(float) * kBinTileFeats * bin_edge_stride(n_edges);
   const int64_t nft = nblocks(n_feats, kBinTileFeats);
   const dim3 grid((unsigned)wgbm_xcd_grid((int64_t)nblocks(n, kBinTileRows) * nft));
   // 16-byte loads when every row starts on 16 bytes

@@ -292,6 +292,9 @@ inline int64_t pair_stride(int32_t F) { return ((int64_t)(F + 15) / 16 * 8 + 255
 // binning / predict kernels
 __global__ void bin_column_kernel(const float* x, int64_t n, const float* edges,
                                   int32_t n_edges, int8_t* out);
+// words per feature of bin_matrix_kernel's LDS edge lists (dynamic LDS =
+// 4 * kBinTileFeats * this)
+int bin_edge_stride(int32_t n_edges);
 template <bool VEC>
 __global__ void bin_matrix_kernel(const float* X, int64_t n, int32_t F, int64_t xs,
                                   const float* edges, int32_t n_edges, int8_t* codes_rm,
