@@ -393,7 +393,7 @@ def test_histogram_segments_bit_exact(gpu, native, B, F):
         assert np.array_equal(bits(Gc[k]), bits(ops.dequantise(Q[0], s)))
 
 
-@pytest.mark.parametrize("B", [32, 2, 127])
+@pytest.mark.parametrize("B", [32, 2, 127, 5, 100])
 def test_quantile_edges_and_bin_matrix(gpu, B):
     print_case("quantile_edges/bin_matrix B", B)
     rng = np.random.default_rng(6)
@@ -405,6 +405,7 @@ def test_quantile_edges_and_bin_matrix(gpu, B):
     # the torch cross-check below would see a zero of the other sign
     X[:, 3] = np.round(X[:, 3]) + F32(0.0)
     X[::997, 5] = np.nan          # NaN column -> all edges NaN -> all codes 0
+    X[17, 9], X[18, 9] = np.inf, -np.inf  # +inf counts every edge (past the search's padding)
     Xd = D.upload_float(X, dev)
     edges = D.quantile_edges(Xd, B).cpu().numpy()
     ref_edges = ops.quantile_edges(X, B)
