@@ -799,24 +799,50 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                                (local, heap[1], heap[2], heap[3]))
         return self._heap_used[1], self._heap_used[2]
 
-    def _inference_codes(self, X_np):
-        """Codes of new data and the heap tables that walk them.  A prediction
-        reads only the codes of the features the forest splits on: for float
-        input (binned with the training edges, warpgbm/core.py:902-915) where
-        those are at most half of the columns, only their columns are gathered
-        on the host, uploaded and binned, and the tables index that narrow
-        code matrix.  The codes of the features read are the same as in the
-        full matrix, so the predictions are identical."""
+    def _infer(self, X_np, K):
+        """Raw scores [n, K] of new data: the start values plus every tree,
+        added in tree order.  Float input (binned with the training edges,
+        warpgbm/core.py:902-915) is streamed: each chunk of rows is walked
+        as soon as it is binned, on the device, while the next chunk is
+        copied.  A prediction reads only the codes of the features the forest
+        splits on: where those are at most half of the columns of an input of
+        _NARROW_MIN_ROWS rows or more, only their columns are gathered on the
+        host, uploaded and binned, and the tables index that narrow code
+        matrix.  The codes of the features read are the same as in the full
+        matrix, so the predictions are identical either way."""
         X_np = np.asarray(X_np)
+        dev = torch.device(self.device)
         heap = self._cached_heap()
-        if (heap[3] and X_np.ndim == 2 and np.issubdtype(X_np.dtype, np.floating)
-                and X_np.shape[1] == self.num_features and X_np.shape[0] >= _NARROW_MIN_ROWS):
-            cols, tables = self._used_features()
-            if 2 * len(cols) <= X_np.shape[1]:
-                codes = D.upload_and_bin(X_np, torch.as_tensor(self.bin_edges),
-                                         torch.device(self.device), cols=cols)
-                return codes, tables
-        return self.bin_inference_data(X_np), heap
+        n = X_np.shape[0]
+        if K == 1:
+            out = torch.full((n, 1), np.float32(self.base_prediction), dtype=torch.float32,
+                             device=dev)
+        else:
+            out = D.rows_of(self._uniform_prior_logits(), n, dev)
+        if (X_np.ndim == 2 and np.issubdtype(X_np.dtype, np.floating)
+                and X_np.shape[1] == self.num_features):
+            cols, tables = None, heap
+            if heap[3] and n >= _NARROW_MIN_ROWS:
+                used, narrow = self._used_features()
+                if 2 * len(used) <= X_np.shape[1]:
+                    cols, tables = used, narrow
+            feat, bin_, leaf, n_rounds = tables
+
+            def walk(codes, r0, r1):
+                if n_rounds:
+                    D.predict_heap(codes, feat, bin_, leaf, n_rounds, K, self.max_depth,
+                                   self.learning_rate, out[r0:r1])
+
+            D.upload_and_bin(X_np, torch.as_tensor(self.bin_edges), dev, cols=cols,
+                             on_chunk=walk)
+            return out
+        codes = self.bin_inference_data(X_np)
+        feat, bin_, leaf, n_rounds = heap
+        if n_rounds:
+            D.predict_heap(codes, feat, bin_, leaf, n_rounds, K, self.max_depth,
+                           self.learning_rate, out)
+        del codes
+        return out
 
     def _predict_values(self, codes, tables):
         out = torch.full((codes.n, 1), np.float32(self.base_prediction), dtype=torch.float32,
@@ -848,24 +874,20 @@ class WarpGBM(BaseEstimator, RegressorMixin):
             probs = self.predict_proba(X_np)
             return self.label_encoder.inverse_transform(np.argmax(probs, axis=1))
         ph = _Phases()
-        codes, tables = self._inference_codes(X_np)
-        ph.mark("codes")
-        out = self._predict_values(codes, tables)
-        ph.mark("trees")
-        preds = D.to_host(out)
+        out = self._infer(X_np, 1)
+        ph.mark("codes + trees")
+        preds = D.to_host(out[:, 0])
         ph.mark("copy out")
         ph.report("predict")
-        del codes
         return preds
 
     def predict_proba(self, X_np):
         """Class probabilities (warpgbm/core.py:976-989)."""
         if self.objective not in ["multiclass", "binary"]:
             raise ValueError("predict_proba only available for classification objectives")
-        codes, tables = self._inference_codes(X_np)
-        probs = D.to_host(self._predict_scores(codes, tables))
-        del codes
-        return probs
+        scores = self._infer(X_np, self.num_classes)
+        D.softmax_rows(scores)
+        return D.to_host(scores)
 
     # ------------------------------------------------------------------ importance
     @staticmethod

@@ -159,16 +159,20 @@ def _upload_staged(X: np.ndarray, dev, np_dtype, torch_dtype) -> torch.Tensor:
     return out
 
 
-def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev, cols=None) -> Codes:
+def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev, cols=None, on_chunk=None) -> Codes:
     """Row-major native codes of a host float matrix for known edges
     [F, num_bins - 1] (predict-time binning, warpgbm/core.py:902-915): the rows
-    stream through the pinned staging buffers and a few device chunk buffers,
-    and each chunk is binned as soon as its copy lands, so the float matrix is
-    never whole on the device and the binning overlaps the transfer.
+    stream through the pinned staging buffers and a few device chunk buffers;
+    the copies run back to back on a copy stream and each chunk is binned on
+    a compute stream as soon as its copy lands, so the float matrix is never
+    whole on the device and the binning overlaps the transfer.
 
     With ``cols`` (feature indices) only those columns are gathered (host
     threads, straight into the staging buffers), uploaded and binned: code
-    column j holds feature cols[j]."""
+    column j holds feature cols[j].  ``on_chunk(codes_rows, r0, r1)`` is
+    called after each chunk's binning is enqueued, with the compute stream
+    current, so work on those rows (the predictors) overlaps the next copies;
+    when the input is not streamed it is called once for all rows."""
     X = np.asarray(X)
     n, F = X.shape
     edges = edges.to(device=dev, dtype=torch.float32).contiguous()
@@ -183,7 +187,10 @@ def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev, cols=None) -> Codes:
     row_bytes = 4 * max(Fw, 1)
     if (n * 4 * max(F, 1) < 4 * _STAGE_BYTES and cols is None) or not X.flags.c_contiguous:
         Xs = X if cols is None else np.take(X, cols, axis=1)
-        return bin_matrix(upload_float(Xs, dev), edges, with_cm=False)
+        c = bin_matrix(upload_float(Xs, dev), edges, with_cm=False)
+        if on_chunk is not None:
+            on_chunk(c, 0, n)
+        return c
     c = _alloc_codes(n, Fw, dev, False, edges.shape[1] + 1)
     bufs, pool = _staging()
     rows_per = max(1, _STAGE_BYTES // row_bytes)
@@ -192,10 +199,17 @@ def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev, cols=None) -> Codes:
     dbufs = [torch.empty((rows_per, Fw), dtype=torch.float32, device=dev)
              for _ in range(len(bufs))]
     lib = _lib.load()
-    side = torch.cuda.Stream(device=dev)
-    side.wait_stream(torch.cuda.current_stream(dev))
-    side_ptr = side.cuda_stream
-    events = [None] * len(bufs)
+    # copies on one stream, binning (and on_chunk's work) on another: chunk
+    # i's copy waits for the binning that last read its device buffer, chunk
+    # i's binning for its copy
+    cur = torch.cuda.current_stream(dev)
+    copy_st = torch.cuda.Stream(device=dev)
+    comp_st = torch.cuda.Stream(device=dev)
+    copy_st.wait_stream(cur)
+    comp_st.wait_stream(cur)
+    comp_ptr = comp_st.cuda_stream
+    events = [None] * len(bufs)   # copy done: the staging buffer can be refilled
+    freed = [None] * len(bufs)    # binning done: the device buffer can be overwritten
     nthreads = pool._max_workers
 
     def fill(dst, lo, hi):
@@ -216,21 +230,30 @@ def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev, cols=None) -> Codes:
         dst = host.numpy()
         step = max(1, (r1 - r0 + nthreads - 1) // nthreads)
         list(pool.map(lambda a: fill(dst, a, min(a + step, r1 - r0)), range(0, r1 - r0, step)))
-        with torch.cuda.stream(side):
-            # device buffer k was last read by the binning of chunk i - len(bufs),
-            # earlier on this same stream
+        with torch.cuda.stream(copy_st):
+            if freed[k] is not None:
+                copy_st.wait_event(freed[k])  # the binning of chunk i - len(bufs) read it
             dbufs[k][: r1 - r0].copy_(host, non_blocking=True)
             ev = torch.cuda.Event()
-            ev.record(side)
+            ev.record(copy_st)
         events[k] = ev
+        comp_st.wait_event(ev)
         rc = lib.wgbm_bin_matrix(dbufs[k].data_ptr(), r1 - r0, Fw, Fw, edges.data_ptr(),
                                  edges.shape[1], c.rm.data_ptr() + r0 * c.stride, c.stride, None,
-                                 side_ptr)
+                                 comp_ptr)
         _lib.check(rc, "bin_matrix")
-    torch.cuda.current_stream(dev).wait_stream(side)
-    c.rm.record_stream(side)
+        fe = torch.cuda.Event()
+        fe.record(comp_st)
+        freed[k] = fe
+        if on_chunk is not None:
+            with torch.cuda.stream(comp_st):
+                on_chunk(Codes(c.rm[r0:r1], None, r1 - r0, Fw, c.stride, c.num_bins), r0, r1)
+    cur.wait_stream(comp_st)
+    cur.wait_stream(copy_st)
+    c.rm.record_stream(comp_st)
     for b in dbufs:
-        b.record_stream(side)
+        b.record_stream(copy_st)
+        b.record_stream(comp_st)
     for ev in events:
         if ev is not None:
             ev.synchronize()  # staging buffers are reused by the next upload
