@@ -176,6 +176,10 @@ struct LevelNext {
   int32_t* present_next;
   int32_t* key_list_next;   // [2 * T * nodes * E]
   int32_t* node_shift_next;  // [2 * T * nodes]
+  // node_scan_kernel: the next level's live-era masks (des_alive_kernel's
+  // output for the children, [2 * T * nodes][ceil(E / 32)]), or null
+  uint32_t* alive_next;
+  float mcw;
 };
 __global__ void level_scan_kernel(int32_t nb, PartSums ps, int32_t T, int32_t nodes, int32_t E,
                                   int64_t n_pos, const int64_t* seg, const int32_t* present,

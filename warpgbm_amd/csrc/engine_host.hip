@@ -480,6 +480,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
 
   const float mcw = c.min_child_weight, eps = c.l2_reg, msg = c.min_split_gain;
   bool planned = false;  // this level's histogram tiles were planned by the previous level
+  bool alive_ready = false;  // this level's live-era masks were written by the previous scan
   for (int d = 0; d <= D; ++d) {
     const int nodes = 1 << d;
     const int n_tn = T * nodes;
@@ -514,9 +515,11 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                                e->present[cur] + c0, e->local_of, n_sel, mcw, eps, e->sgain,
                                e->sdir, use_pairs ? e->pcodes : nullptr, N, e->pstride);
         if (r) return r;
-        hipLaunchKernelGGL(des_alive_kernel, dim3(blocks_for((int64_t)nc * W, 256)), dim3(256), 0,
-                           st, e->seg[cur] + k0, E, nc, mcw, e->alive);
-        WGBM_LAUNCH_CHECK();
+        if (!(alive_ready && nc == n_tn)) {
+          hipLaunchKernelGGL(des_alive_kernel, dim3(blocks_for((int64_t)nc * W, 256)), dim3(256),
+                             0, st, e->seg[cur] + k0, E, nc, mcw, e->alive);
+          WGBM_LAUNCH_CHECK();
+        }
         hipLaunchKernelGGL(des_block_kernel, dim3(blocks_for((int64_t)nc * W * ncand, 256)),
                            dim3(256), 0, st, e->sgain, e->sdir, E, nc, ncand,
                            e->present[cur] + c0, e->alive, e->bsum, e->bdir);
@@ -684,6 +687,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                        route_lds_bytes(rl), st, rl);
     WGBM_LAUNCH_CHECK();
     planned = false;
+    alive_ready = false;
     LevelNext nx;
     nx.tot_qh = e->totqh[cur];
     nx.tot_ql = e->totql[cur];
@@ -697,6 +701,11 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     nx.present_next = e->present[nxt];
     nx.key_list_next = e->key_list[nxt];
     nx.node_shift_next = e->node_shift[nxt];
+    // the next era level's live-era masks, when it runs whole: written by
+    // node_scan_kernel (no des_alive_kernel launch there)
+    const bool next_alive = d + 1 < D && e->des_direct && 2 * (int64_t)n_tn <= e->nc_max;
+    nx.alive_next = nullptr;
+    nx.mcw = mcw;
     const bool one_wg = E == 1 ? n_tn <= kLevelScanE1MaxNodes
                                : (E <= 64 && n_tn <= kLevelScanMaxNodes);
     if (d < D && one_wg) {
@@ -728,19 +737,23 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       } else {
         hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
         WGBM_LAUNCH_CHECK();
+        nx.alive_next = next_alive ? e->alive : nullptr;
         hipLaunchKernelGGL(node_scan_kernel, dim3(blocks_for((int64_t)n_tn, 4)), dim3(256), 0,
                            st, T, nodes, E, 1, n_pos, e->seg[cur], e->present[cur], e->split_l,
                            e->ps, nx);
         WGBM_LAUNCH_CHECK();
+        alive_ready = next_alive;
       }
     } else if (d < D) {
       hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
       WGBM_LAUNCH_CHECK();
       const int wpn = E <= 64 ? 1 : (E <= 128 ? 2 : 4);  // waves per node
+      nx.alive_next = next_alive ? e->alive : nullptr;
       hipLaunchKernelGGL(node_scan_kernel, dim3(blocks_for((int64_t)n_tn, 4 / wpn)), dim3(256), 0,
                          st, T, nodes, E, wpn, n_pos, e->seg[cur], e->present[cur], e->split_l,
                          e->ps, nx);
       WGBM_LAUNCH_CHECK();
+      alive_ready = next_alive;
     }
     if (d < D) {
       hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, n_pos,

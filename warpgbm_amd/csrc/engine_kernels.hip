@@ -889,6 +889,27 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
     wgbm_lds_barrier();
     il += pl;
     ir += pr;
+    if (nx.alive_next) {
+      // the children's live eras (des_alive_kernel's bits: a segment of at
+      // least 2 * mcw rows), one ballot per child and wave: the wave's 64
+      // eras are two mask words
+      const bool in = live && e < E;
+      const uint64_t bl = __ballot(in && !des_segment_dead(L, nx.mcw));
+      const uint64_t br = __ballot(in && !des_segment_dead(R, nx.mcw));
+      static_assert(kDesEraBlock == 32, "a wave's 64 eras are two mask words");
+      const int W = (E + kDesEraBlock - 1) / kDesEraBlock;
+      const int w0 = (e0 + wg * 64) / kDesEraBlock;
+      if (live && lane == 0 && w0 < W) {
+        uint32_t* al = nx.alive_next + (int64_t)(2 * tn) * W;
+        uint32_t* ar = al + W;
+        al[w0] = (uint32_t)bl;
+        ar[w0] = (uint32_t)br;
+        if (w0 + 1 < W) {
+          al[w0 + 1] = (uint32_t)(bl >> 32);
+          ar[w0 + 1] = (uint32_t)(br >> 32);
+        }
+      }
+    }
     if (live && e < E) {
       nx.seg_next[c0 + e] = base + carry_l + il - L;
       nx.seg_next[c0 + E + e] = base + ltot + carry_r + ir - R;

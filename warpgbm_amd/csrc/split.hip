@@ -57,13 +57,6 @@ __global__ void split_f32_kernel(const float* __restrict__ G, const float* __res
 // outputs per (tree, node): split_l (local feature or -1), split_b, best gain
 // ---------------------------------------------------------------------------
 
-// A (node, era) segment of n rows where every candidate split has gain 0 and
-// direction 0: HL >= mcw && HR >= mcw needs HL + HR >= 2*mcw, and HL + HR
-// counts at most the n rows (exact small integers in float).
-__device__ inline bool des_segment_dead(int64_t n, float mcw) {
-  return (float)n < 2.0f * mcw;
-}
-
 // One lane per (tree-node, local feature); the node's best candidate is kept
 // as a packed key  gain_key(gain) << 32 | (0xffffffff - flat index)  updated
 // with a 64-bit atomicMax, so the larger gain wins and, on equal gains, the

@@ -5,6 +5,14 @@
 
 namespace wgbm {
 
+// A (node, era) segment of n rows where every candidate split has gain 0 and
+// direction 0: HL >= mcw && HR >= mcw needs HL + HR >= 2*mcw, and HL + HR
+// counts at most the n rows (exact small integers in float).
+__device__ inline bool des_segment_dead(int64_t n, float mcw) {
+  return (float)n < 2.0f * mcw;
+}
+
+
 struct ScanOut {
   float gain;
   float dir;
