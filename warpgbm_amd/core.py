@@ -72,8 +72,11 @@ class _RecordStream:
                      for k in ("feat", "bin", "leaf", "count")}
         self.pending = []   # (first round, end round, event) of issued copies
         self.copied = 0     # rounds whose copy has been issued
-        self.blocks = []    # futures of per-block lists of per-round tree lists
+        self.blocks = []    # futures of per-block (tree lists, importance nodes)
         self.trees = []     # per finished round: its list of tree dicts
+        # per finished block: the records' rows of its internal nodes (rounds,
+        # then trees in order, nodes in pre-order) and their split features
+        self.nodes = []
         self.pool = ThreadPoolExecutor(max_workers=1)
         # the tree dicts form no reference cycles; pausing the cyclic
         # collector keeps it from re-walking the growing forest on every
@@ -101,9 +104,16 @@ class _RecordStream:
 
     def _convert(self, r0, r1):
         h = {k: v[r0:r1].numpy() for k, v in self.host.items()}
-        n_trees = h["feat"].shape[1]
+        n_trees, H = h["feat"].shape[1], h["feat"].shape[2]
         flat = _heaps_to_dicts(h["feat"], h["bin"], h["leaf"], h["count"])
-        return [flat[j * n_trees:(j + 1) * n_trees] for j in range(r1 - r0)]
+        # the block's internal nodes in the importance order
+        po = _preorder_heap(H).astype(np.int64)
+        fp = h["feat"][:, :, po]
+        internal = fp >= 0
+        base = (np.arange(r0, r1, dtype=np.int64)[:, None, None] * n_trees
+                + np.arange(n_trees, dtype=np.int64)[None, :, None]) * H
+        nodes = ((base + po[None, None, :])[internal], fp[internal])
+        return [flat[j * n_trees:(j + 1) * n_trees] for j in range(r1 - r0)], nodes
 
     def drain(self, wait):
         while self.pending and (wait or self.pending[0][2].query()):
@@ -116,7 +126,9 @@ class _RecordStream:
             self.issue(done)
             self.drain(wait=True)
             for f in self.blocks:  # block order
-                self.trees.extend(f.result())
+                trees, nodes = f.result()
+                self.trees.extend(trees)
+                self.nodes.append(nodes)
         finally:
             self.close()
 
@@ -691,29 +703,26 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         reference's order: per tree, internal nodes in depth-first pre-order,
         float32 adds (warpgbm/core.py:624-627)."""
         dev = rec["gain"].device
-        featd = rec["feat"][:done]  # [done, n_trees, H] on the device
-        n_trees, H = featd.shape[1], featd.shape[2]
         # importance: every internal node of every tree, trees in order and
         # nodes in pre-order, one float32 add per node and era in exactly that
-        # sequence; on the device from the per-era gain records (the nodes
-        # grouped by feature with a stable sort, in order, give each (feature,
-        # era) word to one thread)
-        po = torch.from_numpy(_preorder_heap(H).astype(np.int64)).to(dev)
-        fp = featd[:, :, po]
-        internal = fp >= 0
-        if bool(internal.any()):
-            base = (torch.arange(done, dtype=torch.int64, device=dev)[:, None, None] * n_trees
-                    + torch.arange(n_trees, dtype=torch.int64, device=dev)[None, :, None]) * H
-            rows = (base + po[None, None, :])[internal]
-            fsel = fp[internal]
-            fsorted, by_f = torch.sort(fsel, stable=True)
+        # sequence, on the device from the per-era gain records; the nodes
+        # (listed by the record stream's worker, block by block while later
+        # rounds ran) are grouped by feature here (a stable sort keeps their
+        # order), so each (feature, era) word is one device thread's sum
+        rows = (np.concatenate([r for r, _ in stream.nodes]) if stream.nodes
+                else np.zeros(0, np.int64))
+        fsel = (np.concatenate([f for _, f in stream.nodes]) if stream.nodes
+                else np.zeros(0, np.int32))
+        if rows.size:
             F, E = self.num_features, self.num_eras
-            fstart = torch.searchsorted(
-                fsorted, torch.arange(F + 1, dtype=fsorted.dtype, device=dev)).to(torch.int64)
+            # (16-bit keys sort by radix: several times faster than 32-bit)
+            by_f = np.argsort(fsel.astype(np.int16) if F < (1 << 15) else fsel, kind="stable")
+            fstart = np.searchsorted(fsel[by_f], np.arange(F + 1)).astype(np.int64)
             acc = torch.from_numpy(np.ascontiguousarray(self.per_era_feature_importance_,
                                                         dtype=np.float32)).to(dev)
-            D.importance_add(acc, rec["gain"][:done].reshape(-1, E), rows[by_f].contiguous(),
-                             fstart.contiguous())
+            D.importance_add(acc, rec["gain"][:done].reshape(-1, E),
+                             torch.from_numpy(np.ascontiguousarray(rows[by_f])).to(dev),
+                             torch.from_numpy(fstart).to(dev))
             self.per_era_feature_importance_ = acc.cpu().numpy()
         self._phases.mark("importance")
         for j in range(done):
@@ -789,14 +798,15 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         heap = self._cached_heap()
         if self._heap_used is None or self._heap_used[0] is not heap:
             feat = heap[0]
-            used = torch.unique(feat[feat >= 0])  # sorted
-            if used.numel() == 0:
-                used = torch.zeros(1, dtype=feat.dtype, device=feat.device)
-            lut = torch.full((self.num_features,), -1, dtype=feat.dtype, device=feat.device)
-            lut[used.long()] = torch.arange(used.numel(), dtype=feat.dtype, device=feat.device)
-            local = torch.where(feat >= 0, lut[feat.clamp(min=0).long()], feat).contiguous()
-            self._heap_used = (heap, used.cpu().numpy().astype(np.intp),
-                               (local, heap[1], heap[2], heap[3]))
+            fh = feat.cpu().numpy()  # (small: trees x heap nodes)
+            used = np.unique(fh[fh >= 0])  # sorted
+            if used.size == 0:
+                used = np.zeros(1, dtype=fh.dtype)
+            lut = np.full(self.num_features, -1, dtype=fh.dtype)
+            lut[used] = np.arange(used.size, dtype=fh.dtype)
+            local = np.where(fh >= 0, lut[np.maximum(fh, 0)], fh)
+            local_d = torch.from_numpy(np.ascontiguousarray(local)).to(feat.device)
+            self._heap_used = (heap, used.astype(np.intp), (local_d, heap[1], heap[2], heap[3]))
         return self._heap_used[1], self._heap_used[2]
 
     def _infer(self, X_np, K):
