@@ -189,3 +189,25 @@ def test_iris_multiclass(gpu):
     ref = gbm.Forest(**kw).fit_codes(codes, labels)
     assert m.forest == ref.forest
     assert np.array_equal(bits(m.predict_proba(X)), bits(ref.predict_codes(codes)))
+
+
+def test_predict_zero_rows(gpu):
+    """A prediction over no rows returns empty arrays of the right shapes
+    (regression values, class labels, class probabilities) and leaves the
+    model usable: the next prediction matches one made before it."""
+    print_case("behaviour", "predict on zero rows")
+    X, y = c1_data(n=2000, f=12, seed=5)
+    m = WarpGBM(num_bins=16, max_depth=3, n_estimators=5, learning_rate=0.2)
+    m.fit(X, y)
+    p = m.predict(X)
+    z = m.predict(X[:0])
+    assert z.shape == (0,)
+    assert np.array_equal(bits(m.predict(X)), bits(p))
+    Xc, labels = blobs(1500, 6, 3, seed=8)
+    c = WarpGBM(objective="multiclass", num_bins=16, max_depth=3, n_estimators=4,
+                learning_rate=0.3)
+    c.fit(Xc, labels)
+    pr = c.predict_proba(Xc)
+    assert c.predict(Xc[:0]).shape == (0,)
+    assert c.predict_proba(Xc[:0]).shape == (0, 3)
+    assert np.array_equal(bits(c.predict_proba(Xc)), bits(pr))
