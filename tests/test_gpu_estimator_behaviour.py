@@ -211,3 +211,20 @@ def test_predict_zero_rows(gpu):
     assert c.predict(Xc[:0]).shape == (0,)
     assert c.predict_proba(Xc[:0]).shape == (0, 3)
     assert np.array_equal(bits(c.predict_proba(Xc)), bits(pr))
+
+
+@pytest.mark.parametrize("value", [0.0, 2.5, -1024.0])
+def test_constant_target_grows_no_splits(gpu, value):
+    """A constant target (values whose running sums are exact in float32, so
+    the base prediction, warpgbm/core.py:387, is the value itself) leaves every
+    residual exactly zero: every candidate's gain is 0, which does not pass
+    the strict gain > min_split_gain test (warpgbm/core.py:579-583), so no tree
+    splits, every leaf value is 0 and every prediction is the target."""
+    print_case("behaviour", f"constant target {value}")
+    X, _ = c1_data(n=3000, f=12, seed=9)
+    y = np.full(len(X), value, F32)
+    m = WarpGBM(num_bins=16, max_depth=4, n_estimators=6, learning_rate=0.3)
+    m.fit(X, y)
+    assert np.float32(m.base_prediction) == np.float32(value)
+    assert np.array_equal(bits(m.predict(X)), bits(np.full(len(X), value, F32)))
+    assert float(np.sum(m.get_feature_importance(normalize=False))) == 0.0
