@@ -10,9 +10,17 @@
  *
  * Arithmetic contract (see the reference semantics cited at each entry):
  *  - histogram gradient sums are exact sums of the residuals quantised to
- *    q = rint(r * 2^s) with a power-of-two scale chosen from max|r| of the
- *    call (at most 28 significant bits per value), rounded once to float32;
- *    counts are exact.  Results do not depend on row order or launch shape.
+ *    q = rint(r * 2^s) with a power-of-two scale s chosen from a maximum
+ *    |r| M (at most 28 significant bits per value), rounded once to
+ *    float32; counts are exact.  Results do not depend on row order or
+ *    launch shape.  M is taken per output block: the whole call when it has
+ *    one segment and one era, else each segment / each era separately (an
+ *    era or segment of small residuals keeps its precision next to another
+ *    one's outliers).  Within one such block a bin's error is at most
+ *    count * M * 2^-29, so a bin that holds only residuals far below M (e.g.
+ *    1e-3 values in the same era as a 1e6 one) can lose them, where the
+ *    reference's float32 atomics keep ~24 bits of that bin's own scale.  A
+ *    non-finite residual makes its block's sums NaN.
  *  - split gains/directions are bit-identical to a sequential float32 scan.
  *  - predictions add trees in tree order (deterministic).
  */

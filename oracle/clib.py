@@ -29,7 +29,8 @@ def lib():
         L.oracle_bin_matrix.argtypes = [p, i64, i64, i64, p, i32, p, i64]
         L.oracle_predict_tables.argtypes = [p, i64, i64, p, i32, i32, p, i32, C.c_float, p]
         L.oracle_num_threads.restype = C.c_int
-        L.oracle_split_scan_q.argtypes = [p, p, i64, i32, i32, C.c_float, C.c_float, p, p]
+        L.oracle_split_scan_q.argtypes = [p, p, i64, i32, i32, p, C.c_float, C.c_float, p, p]
+        L.oracle_era_absmax.argtypes = [p, p, i64, p, i32, p]
         _lib = L
     return _lib
 
@@ -126,15 +127,29 @@ def predict_tables(codes, tables, lr, out, cls=None):
 
 def split_scan_q(Q, Cn, s, min_child_samples, eps):
     """ops.split_scan(ops.dequantise(Q, s), float32(Cn), ...) in one C loop:
-    gain, dir [E, F, B-1] from exact histograms Q, Cn [E, F, B]."""
+    gain, dir [E, F, B-1] from exact histograms Q, Cn [E, F, B]; s is one
+    shift for every era or an array of E per-era shifts."""
     Q = np.ascontiguousarray(Q, dtype=np.int64)
     Cn = np.ascontiguousarray(Cn, dtype=np.int64)
     E, F, B = Q.shape
+    s_era = np.ascontiguousarray(np.broadcast_to(np.asarray(s, dtype=np.int32).reshape(-1), (E,)),
+                                 dtype=np.int32)
     gain = np.empty((E, F, B - 1), np.float32)
     dirn = np.empty((E, F, B - 1), np.float32)
-    lib().oracle_split_scan_q(_ptr(Q), _ptr(Cn), E * F, B, int(s), np.float32(min_child_samples),
-                              np.float32(eps), _ptr(gain), _ptr(dirn))
+    lib().oracle_split_scan_q(_ptr(Q), _ptr(Cn), E * F, B, F, _ptr(s_era),
+                              np.float32(min_child_samples), np.float32(eps), _ptr(gain), _ptr(dirn))
     return gain, dirn
+
+
+def era_absmax(r, rows, era, E):
+    """[E] largest |r| over the rows of each era among ``rows`` (float32),
+    computed by a C loop (ops.era_absmax is the same in numpy)."""
+    r = np.ascontiguousarray(r, dtype=np.float32)
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    era = np.ascontiguousarray(era, dtype=np.int32)
+    out = np.empty(E, np.uint32)
+    lib().oracle_era_absmax(_ptr(r), _ptr(rows), len(rows), _ptr(era), E, _ptr(out))
+    return out.view(np.float32)
 
 
 def num_threads():

@@ -268,10 +268,11 @@ void oracle_predict_tables(const int8_t* codes, int64_t n, int64_t ldc, const fl
  * of ops.split_scan) straight from exact histograms: G = float(ldexp(Q, -s)),
  * H = float(C), then sequential float32 totals and prefix; gain/dir are
  * [EF, B-1] for the EF (era, feature) rows of Q, C [EF, B]. */
-void oracle_split_scan_q(const int64_t* Q, const int64_t* Cn, int64_t EF, int32_t B, int32_t s,
-                         float mcw, float eps, float* gain, float* dirn) {
+void oracle_split_scan_q(const int64_t* Q, const int64_t* Cn, int64_t EF, int32_t B, int32_t F,
+                         const int32_t* s_era, float mcw, float eps, float* gain, float* dirn) {
 #pragma omp parallel for schedule(static)
   for (int64_t k = 0; k < EF; ++k) {
+    const int32_t s = s_era[k / F]; /* the shift of row k's era */
     const int64_t* q = Q + k * B;
     const int64_t* c = Cn + k * B;
     float Gt = 0.0f, Ht = 0.0f;
@@ -295,5 +296,22 @@ void oracle_split_scan_q(const int64_t* Q, const int64_t* Cn, int64_t EF, int32_
       gain[k * (B - 1) + b] = g;
       dirn[k * (B - 1) + b] = d;
     }
+  }
+}
+
+/* largest |r| of the rows of each era among rows[0..n) (float bits of
+ * |r|, as an unsigned compare orders non-negative floats; a NaN compares
+ * above every finite value and +inf): out[e] for e < num_eras */
+void oracle_era_absmax(const float* r, const int32_t* rows, int64_t n, const int32_t* era,
+                       int32_t num_eras, uint32_t* out) {
+  memset(out, 0, sizeof(uint32_t) * (size_t)num_eras);
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t s = rows[i];
+    const int e = era[s];
+    if (e < 0 || e >= num_eras) continue;
+    uint32_t b;
+    memcpy(&b, &r[s], sizeof b);
+    b &= 0x7fffffffu;
+    if (b > out[e]) out[e] = b;
   }
 }

@@ -6,12 +6,16 @@ predict drivers (917-932, 991-1030) -- recursively, depth first, left child
 first, smaller child's histogram computed and the sibling obtained by
 subtraction, exactly the reference's control flow.  Histogram arithmetic is
 the exact quantised form of ``ops``: per tree a shift s from max|residual|
-over all rows; per node a histogram shift (ops.node_shift: the parent's,
-unless the node's own residuals are all below 2^-8 of the parent's scale);
-exact integer sums, and the sibling by exact subtraction when both children
-keep the parent's shift (else both children histogrammed directly); one
-rounding to float32 before the split scan.  Leaf means come from the wide
-quantisation of ops.leaf_value63.
+over all rows.  One era: per node a histogram shift (ops.node_shift: the
+parent's, unless the node's own residuals are all below 2^-8 of the
+parent's scale); exact integer sums, and the sibling by exact subtraction
+when both children keep the parent's shift (else both children histogrammed
+directly).  Several eras: every (node, era) segment at the shift of its own
+largest |residual| (ops.key_shift), the sibling's segment of an era by
+subtraction where the parent's and both children's shifts of that era are
+equal (else histogrammed directly).  One rounding to float32 per era before
+the split scan.  Leaf means come from the wide quantisation of
+ops.leaf_value63.
 """
 from __future__ import annotations
 
@@ -38,7 +42,8 @@ class TreeGrower:
         self.feat_sel = np.asarray(feat_sel, dtype=np.int64)
         self.qbits = qbits
         self.hist = hist or ops.histogram_exact_q
-        # (Q, C, shift) -> per-era gain, dir; clib.split_scan_q is the same in C
+        # (Q, C, shift or per-era shifts) -> per-era gain, dir; clib.split_scan_q
+        # is the same in C
         self.scan = scan or (lambda Q, C, s, mcw, eps: ops.split_scan(
             ops.dequantise(Q, s), C.astype(F32), mcw, eps))
         self.splits = []  # (global feature, per-era gains) in DFS pre-order
@@ -53,8 +58,56 @@ class TreeGrower:
         self.q63 = ops.quantise(r, self.s63)
         self._qcache = {}
         self.leaf_rows = []  # (rows, leaf value)
+        if self.E > 1:
+            S = self._key_shifts(rows)
+            Q, C = self._hist_era(rows, S)
+            return self._node_era(Q, C, rows, 0, S)
         Q, C = self._hist(rows, self.s)
         return self._node(Q, C, rows, 0, self.s)
+
+    # ---- several eras: per-(node, era) shifts
+    def _key_shifts(self, rows):
+        from . import clib
+
+        m = clib.era_absmax(self.r, rows, self.era, self.E)
+        return np.array([ops.key_shift(v, self.qbits) for v in m], np.int64)
+
+    def _hist_era(self, rows, S):
+        q = ops.quantise_by_era(self.r, rows, self.era, S)
+        return self.hist(self.codes, q, rows, self.feat_sel, self.era, self.E, self.B)
+
+    def _node_era(self, Q, C, rows, depth, S):
+        if depth == self.max_depth:
+            return self._leaf(rows)
+        gain, dirn = self.scan(Q, C, S, self.mcw, self.eps)
+        lf, b = ops.des_select(gain, dirn, self.msg)
+        if lf == -1:
+            return self._leaf(rows)
+        gf = int(self.feat_sel[lf])
+        self.splits.append((gf, gain[:, lf, b].copy()))
+        go_left = self.codes[rows, gf].astype(np.int64) <= b
+        left, right = rows[go_left], rows[~go_left]
+        QL = CL = QR = CR = SL = SR = None
+        if depth + 1 < self.max_depth:  # (children at max_depth are leaves)
+            SL, SR = self._key_shifts(left), self._key_shifts(right)
+            same = (SL == S) & (SR == S)  # eras where the sibling is parent - child
+            small_left = len(left) <= len(right)
+            small, other = (left, right) if small_left else (right, left)
+            Qs, Cs = self._hist_era(small, SL if small_left else SR)
+            Qo, Co = Q - Qs, C - Cs
+            if not same.all():
+                # the other child's segments of those eras, directly
+                sel = other[~same[self.era[other]]]
+                Qd, Cd = self._hist_era(sel, SR if small_left else SL)
+                Qo[~same] = Qd[~same]
+                Co[~same] = Cd[~same]
+            QL, CL, QR, CR = (Qs, Cs, Qo, Co) if small_left else (Qo, Co, Qs, Cs)
+        return {
+            "feature": gf,
+            "bin": int(b),
+            "left": self._node_era(QL, CL, left, depth + 1, SL),
+            "right": self._node_era(QR, CR, right, depth + 1, SR),
+        }
 
     def _q(self, hs):
         if hs not in self._qcache:

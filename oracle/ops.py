@@ -39,9 +39,14 @@ def quantise(r: np.ndarray, s: int) -> np.ndarray:
     return np.rint(np.ldexp(np.asarray(r, dtype=F32), s)).astype(np.int64)
 
 
-def dequantise(Q, s: int) -> np.ndarray:
-    """float32(ldexp(Q, -s)): one rounding of an exact value (|Q| < 2^53)."""
-    return np.ldexp(np.asarray(Q, dtype=np.int64).astype(np.float64), -s).astype(F32)
+def dequantise(Q, s) -> np.ndarray:
+    """float32(ldexp(Q, -s)): one rounding of an exact value (|Q| < 2^53).  s
+    is one shift, or an array of per-era shifts for Q of shape [E, ...]."""
+    Q = np.asarray(Q, dtype=np.int64)
+    s = np.asarray(s, dtype=np.int64)
+    if s.ndim == 1:
+        s = s.reshape((-1,) + (1,) * (Q.ndim - 1))
+    return np.ldexp(Q.astype(np.float64), -s).astype(F32)
 
 
 def leaf_value(sq: int, count: int, s: int) -> np.float32:
@@ -92,6 +97,48 @@ def node_shift(max_abs, parent_shift: int, qbits: int) -> int:
     return s_own if s_own - int(parent_shift) >= NODE_SHIFT_STEP else int(parent_shift)
 
 
+# Several eras (E > 1): the histogram of every (node, era) segment is
+# quantised at the shift of its own largest |residual| (key_shift), so the
+# sums of an era whose residuals are far smaller than another era's keep
+# their precision (the reference sums each era's bins in float32 of their
+# own scale, warpgbm/cuda/histogram_kernel.cu:38-45, and DES votes per era,
+# warpgbm/core.py:580-583).  A sibling segment is parent - child only where
+# the parent's and both children's shifts of that era are equal (the
+# subtraction is then exact); otherwise both children's segments of that
+# era are histogrammed directly.
+def key_shift(max_abs, qbits: int) -> int:
+    """Shift of one (node, era) segment from its largest |residual|: 0 for
+    an empty segment, an all-zero one or a non-finite maximum."""
+    m = F32(max_abs)
+    if not np.isfinite(m):
+        return 0
+    return shift_from_absmax(m, qbits)
+
+
+def era_absmax(r, rows, era, E: int) -> np.ndarray:
+    """[E] largest |r| of the rows of each era among ``rows`` (0 for an era
+    without rows; NaN when an era holds a NaN)."""
+    rows = np.asarray(rows, dtype=np.int64)
+    out = np.zeros(E, F32)
+    a = np.abs(np.asarray(r, dtype=F32)[rows])
+    e = np.asarray(era, np.int64)[rows]
+    nan = np.isnan(a)
+    np.maximum.at(out, e[~nan], a[~nan])
+    out[np.unique(e[nan])] = F32(np.nan)
+    return out
+
+
+def quantise_by_era(r, rows, era, shifts) -> np.ndarray:
+    """Full-length int64 q with q[s] = rint(r[s] * 2^shifts[era[s]]) for s in
+    rows (0 elsewhere)."""
+    rows = np.asarray(rows, dtype=np.int64)
+    q = np.zeros(len(r), np.int64)
+    if len(rows):
+        sh = np.asarray(shifts, np.int64)[np.asarray(era, np.int64)[rows]]
+        q[rows] = np.rint(np.ldexp(np.asarray(r, dtype=F32)[rows], sh)).astype(np.int64)
+    return q
+
+
 # --------------------------------------------------------------------------- histogram
 def histogram_exact_q(codes, q, rows, feats, era, E: int, B: int):
     """Exact integer histogram (restates warpgbm/cuda/histogram_kernel.cu:33-59
@@ -121,13 +168,58 @@ def histogram_exact_q(codes, q, rows, feats, era, E: int, B: int):
 
 def histogram_exact(codes, resid, rows, feats, era, E: int, B: int, qbits=None):
     """float32 G, H of one compute_histogram3 call in the HIP library's
-    arithmetic: scale from max|resid| over ``rows``, exact sums, one rounding."""
+    arithmetic: exact sums of residuals quantised at one shift from
+    max|resid| over ``rows`` (E == 1) or, with several eras, at each era's
+    own shift from max|resid| over the call's rows of that era (key_shift),
+    then one rounding.  qbits follows the call's row count.  Sums over a
+    non-finite residual are NaN (the whole call, or the era's)."""
     rows = np.asarray(rows, dtype=np.int64)
     r = np.asarray(resid, dtype=F32)
-    m = np.max(np.abs(r[rows])) if len(rows) else F32(0)
-    s = shift_from_absmax(m, qbits_for_rows(max(len(rows), 1)) if qbits is None else qbits)
-    Q, C = histogram_exact_q(codes, quantise(r, s), rows, feats, era, E, B)
-    return dequantise(Q, s), C.astype(F32)
+    qb = qbits_for_rows(max(len(rows), 1)) if qbits is None else qbits
+    if E == 1:
+        m = np.max(np.abs(r[rows])) if len(rows) else F32(0)
+        if not np.isfinite(m):
+            Q, C = histogram_exact_q(codes, np.zeros(len(r), np.int64), rows, feats, era, E, B)
+            return np.full(Q.shape, np.nan, F32), C.astype(F32)
+        s = shift_from_absmax(m, qb)
+        Q, C = histogram_exact_q(codes, quantise(r, s), rows, feats, era, E, B)
+        return dequantise(Q, s), C.astype(F32)
+    e = np.asarray(era, np.int64)
+    ok = rows[(e[rows] >= 0) & (e[rows] < E)]
+    mx = era_absmax(r, ok, e, E)
+    S = np.array([key_shift(v, qb) for v in mx], np.int64)
+    q = quantise_by_era(np.where(np.isfinite(r), r, F32(0)), ok, e, S)
+    Q, C = histogram_exact_q(codes, q, rows, feats, era, E, B)
+    G = dequantise(Q, S)
+    G[~np.isfinite(mx)] = np.nan
+    return G, C.astype(F32)
+
+
+def histogram_segments_exact(codes, resid, order, seg, feats, B: int, n_pos=None):
+    """G, H [S, F, B] of one wgbm_histogram_segments call: segment k holds
+    positions seg[k] .. seg[k+1]-1, whose rows are order[p] (residual
+    resid[order[p]]).  One segment: one shift from max|r| over the call's
+    n_pos positions; several: each segment at its own shift (key_shift of
+    its largest |r|).  qbits follows n_pos."""
+    order = np.asarray(order, np.int64)
+    seg = np.asarray(seg, np.int64)
+    r = np.asarray(resid, dtype=F32)
+    S = len(seg) - 1
+    n_pos = int(seg[-1]) if n_pos is None else int(n_pos)
+    qb = qbits_for_rows(max(n_pos, 1))
+    F = len(feats)
+    G = np.zeros((S, F, B), F32)
+    H = np.zeros((S, F, B), F32)
+    for k in range(S):
+        rows = order[seg[k]:seg[k + 1]]
+        pool = order[:n_pos] if S == 1 else rows
+        m = np.max(np.abs(r[pool])) if len(pool) else F32(0)
+        s = key_shift(m, qb)
+        Q, C = histogram_exact_q(codes, quantise(np.where(np.isfinite(r), r, F32(0)), s), rows,
+                                 feats, None, 1, B)
+        G[k] = dequantise(Q[0], s) if np.isfinite(m) else np.nan
+        H[k] = C[0]
+    return G, H
 
 
 def histogram_f32_seq(codes, resid, rows, feats, era, E: int, B: int):

@@ -366,6 +366,29 @@ def test_heavy_tailed_eras_bit_exact(gpu, N, E):
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
 
 
+@pytest.mark.parametrize("N,E", [(4000, 4), (140_000, 2)])
+@pytest.mark.parametrize("big", [1e4, 1e6])
+def test_eras_of_different_scales_bit_exact(gpu, N, E, big):
+    """Eras whose residual scales differ by up to 1e9 (+-1e-3 targets, two
+    +-big rows in era 0): every (node, era) segment is quantised at its own
+    shift, on the direct era path (eras <= 65536 rows) and on the per-era
+    histogram path (larger eras, the sibling subtracted per era only where
+    the shifts agree).  Trees, importances and predictions bit-exact against
+    the oracle, whose agreement with the reference's float32 DES picks on
+    this data is checked in test_literal_f32.py."""
+    from tests.test_literal_f32 import HEAVY_ERA_KW, heavy_tailed_eras
+
+    print_case("estimator", "eras of different scales N E big", N, E, big)
+    X, y, era = heavy_tailed_eras(3, big, n=N, E=E)
+    m = WarpGBM(**HEAVY_ERA_KW).fit(X, y, era_id=era)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**HEAVY_ERA_KW).fit_codes(codes, y, era_id=era)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
+
+
 @pytest.mark.parametrize("level_bytes", [0, 1])
 def test_chunked_levels_regression_bit_exact(gpu, level_bytes):
     """A level budget of 1 byte leaves room for one (tree, node) at a time:

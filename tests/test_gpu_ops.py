@@ -82,7 +82,14 @@ def test_compute_histogram3_bit_exact(gpu, case):
         # with 2^-23); the library's sum is the true sum of residuals rounded to
         # multiples of 2^-s (error <= count * 2^-(s+1), s from max|r| of the call)
         # plus one final float32 rounding
-        s = ops.shift_from_absmax(np.max(np.abs(resid[rows])), ops.qbits_for_rows(len(rows)))
+        # (s from max|r| of the call, or of the era's rows with several eras)
+        qb = ops.qbits_for_rows(len(rows))
+        if E == 1:
+            s = np.array([ops.shift_from_absmax(np.max(np.abs(resid[rows])), qb)])
+        else:
+            s = np.array([ops.key_shift(m, qb)
+                          for m in ops.era_absmax(resid, rows, era, E)])
+        s = s.reshape(-1, 1, 1).astype(np.float64)
         Gc = G.cpu().numpy()
         tol = (Hs.astype(np.float64) * 2.0**-23 * absum + Hs.astype(np.float64) * 2.0**(-s - 1)
                + np.spacing(np.abs(Gc)).astype(np.float64))
@@ -384,13 +391,89 @@ def test_histogram_segments_bit_exact(gpu, native, B, F):
                                      _lib.current_stream_ptr(dev))
     _lib.check(rc, "histogram_segments")
     torch.cuda.synchronize()
-    s = ops.shift_from_absmax(np.max(np.abs(resid)), ops.qbits_for_rows(N))
-    q = ops.quantise(resid, s)
+    Gr, Hr = ops.histogram_segments_exact(raw, resid, order, seg, np.arange(F), B)
     Gc, Hc = G.cpu().numpy(), H.cpu().numpy()
-    for k in range(S):
-        Q, C = ops.histogram_exact_q(raw, q, order[seg[k]:seg[k + 1]], np.arange(F), None, 1, B)
-        assert np.array_equal(Hc[k], C[0].astype(F32))
-        assert np.array_equal(bits(Gc[k]), bits(ops.dequantise(Q[0], s)))
+    assert np.array_equal(Hc, Hr)
+    assert np.array_equal(bits(Gc), bits(Gr))
+
+
+def _rel_ok(G, codes, r, rows, key_of_row, n_keys, feats, B, skip_key):
+    """|G - float64 sum| <= 1e-5 * sum|r| for every (key, feature, bin) but
+    skip_key's (the key of the outlier)."""
+    kr = key_of_row[rows]
+    for fi, f in enumerate(feats):
+        b = codes[rows, f].astype(np.int64)
+        ok = (b >= 0) & (b < B)
+        idx = kr[ok] * B + b[ok]
+        true = np.bincount(idx, weights=r[rows[ok]].astype(np.float64), minlength=n_keys * B)
+        absum = np.bincount(idx, weights=np.abs(r[rows[ok]]).astype(np.float64),
+                            minlength=n_keys * B)
+        err = np.abs(G[:, fi, :].reshape(-1).astype(np.float64) - true)
+        keep = np.repeat(np.arange(n_keys) != skip_key, B)
+        assert np.all(err[keep] <= 1e-5 * absum[keep])
+
+
+def test_compute_histogram3_era_outlier(gpu):
+    """A 1e6 residual in era 0 next to eras of 1e-3 residuals: each era is
+    quantised at the shift of its own largest |r|, so the small eras' sums
+    hold to 1e-5 of their bins' sum of |r| (bit-exact against the oracle)."""
+    print_case("compute_histogram3", "era outlier")
+    rng = np.random.default_rng(31)
+    N, Fm, B, E = 30000, 64, 16, 5
+    codes = rng.integers(-1, B + 1, (N, Fm)).astype(np.int8)
+    era = rng.integers(0, E, N).astype(np.int32)
+    resid = (1e-3 * rng.standard_normal(N)).astype(F32)
+    big = np.flatnonzero(era == 0)[:3]
+    resid[big] = F32(1e6) * np.array([1, -1, 0.5], F32)
+    rows = np.sort(rng.choice(N, 25000, replace=False))
+    rows = np.union1d(rows, big)
+    feats = rng.permutation(Fm)[:50]
+    G = torch.zeros((E, len(feats), B), device=dev)
+    H = torch.zeros_like(G)
+    node_kernel.compute_histogram3(t(codes), t(resid), t(rows, torch.int32),
+                                   t(feats, torch.int32), t(era), G, H, B)
+    Gr, Hr = ops.histogram_exact(codes, resid, rows, feats, era, E, B)
+    Gc = G.cpu().numpy()
+    assert np.array_equal(H.cpu().numpy(), Hr)
+    assert np.array_equal(bits(Gc), bits(Gr))
+    _rel_ok(Gc, codes, resid, rows, era.astype(np.int64), E, feats, B, skip_key=0)
+
+
+def test_histogram_segments_segment_outlier(gpu):
+    """Segments: a 1e6 residual in segment 2 leaves the other segments'
+    sums of 1e-3 residuals at their own scale (1e-5 of sum|r| per bin), and
+    the no-allocation entry point gives the same bits."""
+    print_case("histogram_segments", "segment outlier")
+    rng = np.random.default_rng(32)
+    N, F, B, S = 40000, 203, 32, 16
+    stride = D.codes_stride(F)
+    raw = rng.integers(-2, B + 2, (N, F)).astype(np.int8)
+    resid = (1e-3 * rng.standard_normal(N)).astype(F32)
+    node = rng.integers(0, S, N)
+    resid[np.flatnonzero(node == 2)[:2]] = F32(1e6)
+    order = np.argsort(node, kind="stable").astype(np.int32)
+    seg = np.zeros(S + 1, np.int64)
+    seg[1:] = np.cumsum(np.bincount(node, minlength=S))
+    padded = np.full((N, stride), -1, np.int8)
+    padded[:, :F] = raw
+    lib = _lib.load()
+    codes_d, resid_d, order_d, seg_d = t(padded), t(resid), t(order), t(seg)
+    out = []
+    for fn in (lib.wgbm_histogram_segments, lib.wgbm_histogram_segments_noalloc):
+        G = torch.zeros((S, F, B), device=dev)
+        H = torch.zeros_like(G)
+        rc = fn(codes_d.data_ptr(), N, stride, F, resid_d.data_ptr(), order_d.data_ptr(),
+                seg_d.data_ptr(), S, N, B, 0, G.data_ptr(), H.data_ptr(),
+                _lib.current_stream_ptr(dev))
+        _lib.check(rc, "histogram_segments")
+        torch.cuda.synchronize()
+        out.append((G.cpu().numpy(), H.cpu().numpy()))
+    Gr, Hr = ops.histogram_segments_exact(raw, resid, order, seg, np.arange(F), B)
+    for Gc, Hc in out:
+        assert np.array_equal(Hc, Hr)
+        assert np.array_equal(bits(Gc), bits(Gr))
+    _rel_ok(out[0][0], raw, resid, order.astype(np.int64), node, S, np.arange(F), B,
+            skip_key=2)
 
 
 @pytest.mark.parametrize("B", [32, 2, 127, 5, 100])

@@ -1,7 +1,8 @@
 """The exact arithmetic against the reference's literal float32 arithmetic.
 
 The oracle's exact mode (the HIP library's arithmetic: quantised residuals,
-exact integer histogram sums, per-node histogram shifts, wide leaf sums) and
+exact integer histogram sums, per-node histogram shifts with one era and
+per-(node, era) shifts with several, wide leaf sums) and
 its literal mode (gbm.LiteralF32Grower: float32 histograms accumulated in
 position order, float32 sibling subtraction as warpgbm/core.py:638-643,
 float32 leaf means as core.py:599) grow forests on the same data, and
@@ -110,3 +111,55 @@ def test_node_shift_rule():
     assert ops.quantise(r, s_parent).sum() == 0  # below the tree's histogram step
     v = ops.leaf_value63(ops.quantise(r, s63), len(r), s63)
     assert abs(float(v) - 1e-3) <= 1e-3 * 2**-23
+
+
+def heavy_tailed_eras(seed, big, n=4000, E=4):
+    """Eras whose residual scales differ: +-1e-3 targets (sign of x1) plus
+    1e-4 noise on E equal eras, and +big, -big on two rows of era 0."""
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((n, 6)).astype(F32)
+    y = (np.where(X[:, 1] > 0, 1e-3, -1e-3) + 1e-4 * rng.standard_normal(n)).astype(F32)
+    y[0], y[1] = big, -big
+    era = np.repeat(np.arange(E), n // E)
+    return X, y, era
+
+
+HEAVY_ERA_KW = dict(num_bins=8, max_depth=3, n_estimators=2, learning_rate=0.1,
+                    min_child_weight=5)
+
+
+@pytest.mark.parametrize("big", [1e4, 1e5, 1e6])
+def test_heavy_tailed_eras_exact_vs_literal(big):
+    """Every (node, era) segment is quantised at its own shift, so eras 1-3
+    keep their sums and their direction votes next to era 0's outliers: the
+    exact mode's picks are admissible under the float64 DES rule in every
+    seed (one shift per node fails 2/8 seeds at 1e4 and all at 1e6)."""
+    for seed in range(8):
+        X, y, era = heavy_tailed_eras(seed, big)
+        codes = ops.bin_matrix(X, ops.quantile_edges(X, 8))
+        exact = gbm.Forest(**HEAVY_ERA_KW).fit_codes(codes, y, era_id=era)
+        literal = gbm.Forest(**HEAVY_ERA_KW).fit_codes(codes, y, era_id=era, literal_f32=True)
+        gbm.compare_growth(exact, literal, codes, exact_may_win=True)
+
+
+def test_heavy_tailed_eras_check_catches_one_shift_per_node(monkeypatch):
+    """Planted in the oracle: every era of a node quantised at the node's
+    shift (from its largest |r| over all eras).  Eras 1-3 then round to zero
+    next to era 0's 1e6 outliers and vote -1 everywhere; the comparison must
+    reject the resulting picks."""
+    def node_wide(self, rows):
+        m = np.max(np.abs(self.r[rows])) if len(rows) else F32(0)
+        return np.full(self.E, ops.key_shift(m, self.qbits), np.int64)
+
+    monkeypatch.setattr(gbm.TreeGrower, "_key_shifts", node_wide)
+    failed = 0
+    for seed in range(8):
+        X, y, era = heavy_tailed_eras(seed, 1e6)
+        codes = ops.bin_matrix(X, ops.quantile_edges(X, 8))
+        exact = gbm.Forest(**HEAVY_ERA_KW).fit_codes(codes, y, era_id=era)
+        literal = gbm.Forest(**HEAVY_ERA_KW).fit_codes(codes, y, era_id=era, literal_f32=True)
+        try:
+            gbm.compare_growth(exact, literal, codes, exact_may_win=True)
+        except AssertionError:
+            failed += 1
+    assert failed >= 6

@@ -13,7 +13,11 @@ off-by-one bin or transposed index fails.
   ops.quantise/dequantise   lossless for |r| >= max|r|*2^(24-qbits); error <= 2^-(s+1)
   ops.histogram_exact_q     brute-force integer dict; count invariants;
                             child + sibling == parent
-  ops.histogram_exact       |G - fsum(r)| <= n 2^-(s+1) + ulp; vs f32 sequential
+  ops.histogram_exact       |G - fsum(r)| <= n 2^-(s+1) + ulp; vs f32 sequential;
+                            several eras: within 1e-5 of sum|r| per bin next to
+                            another era's outlier, equal to per-era calls
+  ops.histogram_segments_exact  per segment equal to one-segment calls
+  ops.era_absmax / key_shift  hand values, NaN / inf / empty eras
   ops.histogram_f32_seq     per-row float32 loop
   ops.split_scan            scalar float32 loop; hand KAT; gain >= 0 identity
   ops.des_select            hand-built DES cases; first-index ties
@@ -214,6 +218,84 @@ def test_histogram_exact_vs_true_sum_and_f32_sequential():
             # float32 sequential accumulation error bound ~ n * eps * sum|r|
             absum = math.fsum(abs(float(v)) for v in r[sel])
             assert abs(float(Gs[0, f, b]) - true) <= len(sel) * 2**-24 * absum + 1e-30
+
+
+def _bin_true_sums(codes, r, rows, era, E, B, f):
+    """float64 (fsum) sum and sum of |r| of every (era, bin) of feature f."""
+    true = np.zeros((E, B))
+    absum = np.zeros((E, B))
+    for e in range(E):
+        for b in range(B):
+            sel = rows[(codes[rows, f] == b) & (era[rows] == e)]
+            true[e, b] = math.fsum(float(v) for v in r[sel])
+            absum[e, b] = math.fsum(abs(float(v)) for v in r[sel])
+    return true, absum
+
+
+def test_histogram_exact_eras_keep_their_own_scale():
+    """Several eras: each era's sums are quantised at the shift of its own
+    largest |r|, so an era of 1e-3 residuals next to an era holding a 1e6
+    outlier is summed to within 1e-5 of its bins' sum of |r| (a single shift
+    for the call would round every 1e-3 residual to 0: planted below)."""
+    rng = np.random.default_rng(21)
+    N, Fm, B, E = 4000, 3, 8, 4
+    codes = rng.integers(0, B, (N, Fm)).astype(np.int8)
+    era = np.repeat(np.arange(E), N // E).astype(np.int32)
+    r = (1e-3 * rng.standard_normal(N)).astype(F32)
+    r[5] = F32(1e6)  # era 0
+    rows = np.arange(N)
+    G, H = ops.histogram_exact(codes, r, rows, np.arange(Fm), era, E, B)
+    for f in range(Fm):
+        true, absum = _bin_true_sums(codes, r, rows, era, E, B, f)
+        err = np.abs(G[1:, f, :].astype(np.float64) - true[1:])
+        assert np.all(err <= 1e-5 * absum[1:])
+    # the same eras through the one-era path, era by era, at the call's qbits
+    qb = ops.qbits_for_rows(N)
+    for e in range(E):
+        Ge, He = ops.histogram_exact(codes, r, rows[era == e], np.arange(Fm), None, 1, B, qbits=qb)
+        assert np.array_equal(Ge[0], G[e]) and np.array_equal(He[0], H[e])
+    # planted: one shift for the whole call (step 2^-8 next to the outlier)
+    # rounds the 1e-3 residuals of eras 1..3 away and fails the same bound
+    s = ops.shift_from_absmax(np.max(np.abs(r)), qb)
+    Q1, _ = ops.histogram_exact_q(codes, ops.quantise(r, s), rows, np.arange(Fm), era, E, B)
+    G1 = ops.dequantise(Q1, s)
+    true, absum = _bin_true_sums(codes, r, rows, era, E, B, 0)
+    assert np.any(np.abs(G1[1:, 0, :].astype(np.float64) - true[1:]) > 1e-5 * absum[1:])
+
+
+def test_histogram_segments_exact_per_segment_shift():
+    """Several segments: each at the shift of its own largest |r|, equal to
+    the one-segment histogram of its rows at the call's qbits; one segment:
+    the shift of the call's positions."""
+    rng = np.random.default_rng(22)
+    N, Fm, B, S = 3000, 4, 6, 5
+    codes = rng.integers(-1, B + 1, (N, Fm)).astype(np.int8)
+    r = (rng.standard_normal(N) * 10.0 ** rng.integers(-4, 3, N)).astype(F32)
+    order = rng.permutation(N).astype(np.int32)
+    seg = np.array([0, 700, 700, 1500, 2900, 3000], np.int64)  # one empty segment
+    G, H = ops.histogram_segments_exact(codes, r, order, seg, np.arange(Fm), B)
+    qb = ops.qbits_for_rows(N)
+    for k in range(S):
+        rows = order[seg[k]:seg[k + 1]]
+        Gk, Hk = ops.histogram_exact(codes, r, rows, np.arange(Fm), None, 1, B, qbits=qb)
+        assert np.array_equal(G[k], Gk[0]) and np.array_equal(H[k], Hk[0])
+    G1, H1 = ops.histogram_segments_exact(codes, r, order, np.array([0, 2000]), np.arange(Fm), B,
+                                          n_pos=N)
+    s = ops.shift_from_absmax(np.max(np.abs(r)), qb)  # over all N positions
+    Q, C = ops.histogram_exact_q(codes, ops.quantise(r, s), order[:2000], np.arange(Fm), None, 1, B)
+    assert np.array_equal(G1[0], ops.dequantise(Q[0], s)) and np.array_equal(H1[0], C[0])
+
+
+def test_era_absmax_and_key_shift():
+    r = np.array([1.0, -3.0, 2.0, np.nan, 5.0, -0.0], F32)
+    era = np.array([0, 0, 1, 2, 1, 3])
+    m = ops.era_absmax(r, np.arange(6), era, 5)
+    assert m[0] == 3 and m[1] == 5 and np.isnan(m[2]) and m[3] == 0 and m[4] == 0
+    assert np.array_equal(np.nan_to_num(clib.era_absmax(r, np.arange(6), era, 5), nan=-1),
+                          np.nan_to_num(m, nan=-1))
+    assert ops.key_shift(F32(0), 28) == 0 and ops.key_shift(F32(np.inf), 28) == 0
+    assert ops.key_shift(F32(np.nan), 28) == 0
+    assert ops.key_shift(F32(3.0), 28) == 26  # 3 = 0.75 * 2^2: 3 * 2^26 < 2^28
 
 
 def test_histogram_f32_seq_matches_row_loop():

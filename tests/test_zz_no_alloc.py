@@ -61,12 +61,28 @@ def test_noalloc_matches_allocating_entry_point(gpu):
 
 
 def test_noalloc_rejects_calls_beyond_its_scratch(gpu):
-    """16M rows in one row-list call need more than the fixed array; the
-    call is refused before any work, with both sizes in the message."""
+    """300 segments of 1000 features need a tile of partials each (256 KiB
+    at 32 bins), 75 MiB in all, more than the fixed array: the call is
+    refused before any work, with both sizes in the message.  Every pointer
+    is a real device buffer of the call's shape, so a size check that ran
+    late would compute a histogram (and fail the return code check) rather
+    than touch memory outside the buffers."""
+    dev = torch.device("cuda:0")
     lib = _lib.load()
-    one = C.c_void_p(1)  # never dereferenced: the size check comes first
-    rc = lib.wgbm_histogram_segments_noalloc(one, 1 << 24, 1024, 1000, one, one, one, 1, 1 << 24,
-                                             32, 0, one, one, None)
+    st = _lib.current_stream_ptr(dev)
+    N, F, B, n_seg = 600, 1000, 32, 300
+    rng = np.random.default_rng(3)
+    codes = torch.from_numpy(rng.integers(0, B, (N, F), dtype=np.int8)).to(dev)
+    grad = torch.from_numpy(rng.standard_normal(N).astype(F32)).to(dev)
+    order = torch.arange(N, dtype=torch.int32, device=dev)
+    seg = torch.from_numpy(np.arange(n_seg + 1, dtype=np.int64) * 2).to(dev)
+    G = torch.zeros((n_seg, F, B), device=dev)
+    H = torch.zeros_like(G)
+    rc = lib.wgbm_histogram_segments_noalloc(codes.data_ptr(), N, F, F, grad.data_ptr(),
+                                             order.data_ptr(), seg.data_ptr(), n_seg, N, B, 0,
+                                             G.data_ptr(), H.data_ptr(), st)
+    torch.cuda.synchronize()
     assert rc == 1000
     msg = lib.wgbm_last_error().decode()
     assert "needs" in msg and str(64 * 1024 * 1024) in msg
+    assert float(H.sum()) == 0.0  # nothing ran

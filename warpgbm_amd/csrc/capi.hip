@@ -51,7 +51,9 @@ constexpr int kAbsBlocks = 256;  // per-block |residual| maxima of one call, at 
 // sizes of one call, shared by the pipeline and the no-allocation size check
 struct HistPlan {
   int V = 1, n_chunks = 1, n_abs = 1, n_keys = 1;
-  bool regroup = false, gather_resid = false;
+  // per_key: several segments (or eras), each quantised at the shift of its
+  // own largest |residual|; else one shift for the call
+  bool regroup = false, gather_resid = false, per_key = false;
   int64_t R = 1024, max_tiles = 1, tile_words = 0;
 };
 
@@ -71,6 +73,7 @@ static HistPlan hist_plan(int32_t n_hist_feats, int32_t num_bins, int64_t n_pos,
   p.gather_resid = rows && !p.regroup;
   // segments: explicit (seg_dev), by era (sort rows by era), or a single one
   p.n_keys = seg_dev ? n_seg : (p.regroup ? num_eras : 1);
+  p.per_key = p.n_keys > 1;
   // tiles: ~1 workgroup per CU over the whole call
   const int64_t tiles_target = std::max<int64_t>(1, kHistTargetWGCall / p.n_chunks);
   int64_t R = (n_pos + tiles_target - 1) / tiles_target;
@@ -90,6 +93,7 @@ static size_t hist_scratch_bytes(const HistPlan& p, int64_t n_pos) {
   b += r(sizeof(Tile) * (size_t)p.max_tiles);
   b += r(sizeof(int32_t) * ((size_t)p.n_keys + 1));
   b += r(sizeof(unsigned long long) * (size_t)(p.max_tiles * p.tile_words));
+  if (p.per_key) b += r(sizeof(uint32_t) * (size_t)p.n_keys);
   return b;
 }
 
@@ -131,6 +135,11 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   unsigned long long* part =
       (unsigned long long*)sc.get(sizeof(unsigned long long) * words, 5);
   WGBM_REQUIRE(tiles && kts && part, "scratch allocation failed (%lld words)", (long long)words);
+  uint32_t* key_max = nullptr;
+  if (pl.per_key) {
+    key_max = (uint32_t*)sc.get(sizeof(uint32_t) * (size_t)n_keys, 13);
+    WGBM_REQUIRE(key_max, "scratch allocation failed");
+  }
   FeatMapArgs fm;
   if (fsel) {
     // mark [n_master], next [n_out], list and head [width], run [n_chunks]
@@ -156,7 +165,7 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   const unsigned prep_blocks = (unsigned)(n_abs + (regroup ? 0 : 1) + (fsel ? 1 : 0));
   hipLaunchKernelGGL(hist_prep_kernel, dim3(prep_blocks), dim3(1024), 0, st, resid, rows, n_pos,
                      abs_part, rpos, n_abs, regroup ? 0 : 1, seg_dev, n_keys, (int32_t)R,
-                     (int32_t)max_tiles, tiles, kts, n_tiles, fm);
+                     (int32_t)max_tiles, tiles, kts, n_tiles, fm, key_max);
   WGBM_LAUNCH_CHECK();
   const int32_t* order = rows;
   const int64_t* seg = seg_dev;
@@ -188,6 +197,13 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
                        n_tiles);
     WGBM_LAUNCH_CHECK();
   }
+  const int qbits = wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1));
+  if (pl.per_key) {
+    // each key's largest |residual| (its shift) over its tiles' positions
+    hipLaunchKernelGGL(hist_key_max_kernel, dim3((unsigned)max_tiles), dim3(256), 0, st, tiles,
+                       n_tiles, rpos ? rpos : resid, order, rpos ? 1 : 0, key_max);
+    WGBM_LAUNCH_CHECK();
+  }
   HistLaunch a;
   a.codes = codes;
   a.n_rows = n_rows;
@@ -208,11 +224,15 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
   a.max_tiles = (int32_t)max_tiles;
   a.native = native ? 1 : 0;
   a.timer_tag = sc.base ? nullptr : "hist_tiles";  // timers create events: not without allocation
-  a.sm.partial = abs_part;
-  a.sm.n_part = n_abs;
-  a.sm.qbits = wgbm_qbits_for_rows(std::max<int64_t>(n_pos, 1));
-  a.sm.absmax_bits = absmax;
-  a.sm.shift = shift;
+  a.sm.qbits = qbits;
+  if (pl.per_key) {
+    a.sm.key_max = key_max;
+  } else {
+    a.sm.partial = abs_part;
+    a.sm.n_part = n_abs;
+    a.sm.absmax_bits = absmax;
+    a.sm.shift = shift;
+  }
   if (fsel) {
     a.fs.list = fm.list;
     a.fs.count = n_sel;
@@ -233,7 +253,8 @@ static int histogram_pipeline(const int8_t* codes, int64_t n_rows, int64_t strid
     fo.n_out = n_out_feats;
   }
   return launch_finalize_f32(tiles_per_key, part, kts, n_keys, n_chunks, V, num_bins, width,
-                             shift, absmax, n_tiles, 1, fo, G, H, st);
+                             pl.per_key ? key_max : absmax, pl.per_key ? 1 : 0, qbits, n_tiles,
+                             1, fo, G, H, st);
 }
 
 int wgbm_compute_histogram3(const int8_t* bin_indices, int64_t n_rows, int64_t n_feats_master,

@@ -75,6 +75,15 @@ __host__ __device__ inline int wgbm_shift_from_absmax(float m, int qbits) {
   return qbits - e;
 }
 
+// the shift of a maximum given as float bits: 0 for a non-finite one (a NaN
+// or infinite residual; the caller reports it)
+__host__ __device__ inline int wgbm_shift_from_bits(uint32_t absmax_bits, int qbits) {
+  if (absmax_bits >= 0x7f800000u) return 0;
+  float m;
+  __builtin_memcpy(&m, &absmax_bits, sizeof m);
+  return wgbm_shift_from_absmax(m, qbits);
+}
+
 __host__ __device__ inline int32_t wgbm_quantise(float r, int s) {
   return (int32_t)rintf(ldexpf(r, s));
 }

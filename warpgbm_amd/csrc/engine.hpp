@@ -102,15 +102,15 @@ struct PartSums {
   int64_t* P_qh;
   int64_t* P_ql;
   int64_t* P_n;
-  uint32_t* own_ml;  // [T * nodes] left-child max of a node inside one block
-  uint32_t* own_mr;  //             right-child max
-  uint32_t* bf_ml;   // [nb] of the block's first node
+  uint32_t* own_ml;  // [keys] left-child max|r| of a segment inside one block
+  uint32_t* own_mr;  //        right-child max
+  uint32_t* bf_ml;   // [nb] of the block's first segment
   uint32_t* bf_mr;
-  uint32_t* bl_ml;   // [nb] of the block's last node
+  uint32_t* bl_ml;   // [nb] of the block's last segment
   uint32_t* bl_mr;
-  int32_t* bf_node;  // [nb] (tree, node) of the block's first position
+  int32_t* bf_node;  // [nb] segment key of the block's first position (one era: its node)
   uint32_t* pm_l;    // [nb] segmented maxima of bf_ml / bf_mr over runs of
-  uint32_t* pm_r;    //      blocks with one first node (block_scan_body)
+  uint32_t* pm_r;    //      blocks with one first segment (block_scan_body)
 };
 
 // A child node keeps its parent's histogram shift unless the shift of its
@@ -124,9 +124,15 @@ __device__ inline int node_shift_rule(uint32_t absmax_bits, int parent_shift,
   const int s_own = wgbm_shift_from_absmax(__uint_as_float(absmax_bits), qbits);
   return s_own - parent_shift >= kNodeShiftStep ? s_own : parent_shift;
 }
+// Several eras: the histogram shift of one (node, era) segment from the
+// float bits of its largest |residual| (0 for an empty, all-zero or
+// non-finite segment)
+__device__ inline int key_shift_of(uint32_t absmax_bits, int qbits) {
+  return wgbm_shift_from_bits(absmax_bits, qbits);
+}
 struct RouteArgs {
   int32_t mode;  // 0 root totals, 1 split level, 2 last level (leaves only)
-  int32_t want_max;  // mode 1: gather the children's max|r| (their level has histograms)
+  int32_t want_max;  // gather each segment's left / right max|r| (the next level's shifts)
   const int64_t* seg;
   int32_t n_keys;
   int64_t n_pos;
@@ -154,7 +160,7 @@ __global__ void route_kernel(RouteArgs a);
 // dynamic LDS of route_kernel: the slot sums, plus the node maxima
 inline size_t route_lds_bytes(const RouteArgs& a) {
   if (a.mode == 2) return 0;
-  return (size_t)kPartBlock * (16 + (a.mode == 1 && a.want_max ? 8 : 0));
+  return (size_t)kPartBlock * (16 + (a.want_max ? 8 : 0));
 }
 __global__ void block_scan_kernel(int32_t nb, PartSums ps);
 constexpr int kLevelScanMaxNodes = 64;  // (tree, node)s of a level for level_scan_kernel
@@ -166,7 +172,9 @@ constexpr int kLevelScanMaxNodes = 64;  // (tree, node)s of a level for level_sc
 struct LevelNext {
   const int64_t* tot_qh;
   const int64_t* tot_ql;
-  const int32_t* node_shift;  // [T * nodes] of this level
+  // histogram shifts of this level: one era [T * nodes], several eras per
+  // (node, era) key [T * nodes * E]
+  const int32_t* node_shift;
   int32_t qbits;
   int32_t have_max;  // the route gathered the children's max|r| (else no shift changes)
   int64_t* seg_next;
@@ -175,7 +183,7 @@ struct LevelNext {
   int64_t* tot_c_next;
   int32_t* present_next;
   int32_t* key_list_next;   // [2 * T * nodes * E]
-  int32_t* node_shift_next;  // [2 * T * nodes]
+  int32_t* node_shift_next;  // the next level's, indexed likewise
   // node_scan_kernel: the next level's live-era masks (des_alive_kernel's
   // output for the children, [2 * T * nodes][ceil(E / 32)]), or null
   uint32_t* alive_next;
@@ -195,7 +203,8 @@ __global__ void level_scan_e1_kernel(int32_t nb, PartSums ps, int32_t n_tn, int6
                                      int32_t tile_rows, int32_t max_tiles, Tile* tiles,
                                      int32_t* key_tile_start, int32_t* n_tiles);
 __global__ void root_totals_kernel(int32_t n_keys, const int64_t* seg, PartSums ps,
-                                   int64_t* tot_qh, int64_t* tot_ql, int64_t* tot_c);
+                                   int64_t* tot_qh, int64_t* tot_ql, int64_t* tot_c,
+                                   int32_t qbits, int32_t* key_shift);
 __global__ void node_scan_kernel(int32_t T, int32_t nodes, int32_t E, int32_t wpn,
                                  int64_t n_pos, const int64_t* seg, const int32_t* present,
                                  const int32_t* split_l, PartSums ps, LevelNext nx);

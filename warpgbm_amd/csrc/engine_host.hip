@@ -43,7 +43,9 @@ struct Engine {
   int64_t* totql[2] = {nullptr, nullptr};
   int64_t* totc[2] = {nullptr, nullptr};
   int32_t* present[2] = {nullptr, nullptr};
-  int32_t* node_shift[2] = {nullptr, nullptr};  // histogram shift per (tree, node)
+  // histogram shift per (tree, node) with one era, per (tree, node, era)
+  // segment key with several eras
+  int32_t* node_shift[2] = {nullptr, nullptr};
   int32_t* key_list[2] = {nullptr, nullptr};    // histogram key pairs per (parent, era)
   // partition over position blocks of kPartBlock positions
   uint8_t* dirbit = nullptr;            // [T*N] 0 left, 1 right, 2 stays
@@ -214,7 +216,7 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     E_ALLOC(e->totql[k], e->n_keys_max);
     E_ALLOC(e->totc[k], e->n_keys_max);
     E_ALLOC(e->present[k], T * nodes_max);
-    E_ALLOC(e->node_shift[k], T * nodes_max);
+    E_ALLOC(e->node_shift[k], e->n_keys_max);
     E_ALLOC(e->key_list[k], 2 * e->n_keys_max);
     if (!e->des_direct) {
       E_ALLOC(e->hq[k], e->nc_max * E * F * B);
@@ -251,8 +253,8 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->ps.P_qh, e->nb);
   E_ALLOC(e->ps.P_ql, e->nb);
   E_ALLOC(e->ps.P_n, e->nb);
-  E_ALLOC(e->ps.own_ml, T * nodes_max);
-  E_ALLOC(e->ps.own_mr, T * nodes_max);
+  E_ALLOC(e->ps.own_ml, e->n_keys_max);
+  E_ALLOC(e->ps.own_mr, e->n_keys_max);
   E_ALLOC(e->ps.bf_ml, e->nb);
   E_ALLOC(e->ps.bf_mr, e->nb);
   E_ALLOC(e->ps.bl_ml, e->nb);
@@ -457,7 +459,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     r0.rpos = e->rpos[0];
     r0.nodes = 1;
     r0.present = e->present[0];
-    r0.want_max = 0;
+    r0.want_max = E > 1 ? 1 : 0;  // several eras: every root key's own shift
     hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads),
                        route_lds_bytes(r0), st, r0);
     WGBM_LAUNCH_CHECK();
@@ -465,7 +467,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     WGBM_LAUNCH_CHECK();
     hipLaunchKernelGGL(root_totals_kernel, dim3(blocks_for((int64_t)T * E, 256)), dim3(256), 0,
                        st, (int32_t)(T * E), e->seg[0], e->ps, e->totqh[0], e->totql[0],
-                       e->totc[0]);
+                       e->totc[0], e->qbits, E > 1 ? e->node_shift[0] : (int32_t*)nullptr);
     WGBM_LAUNCH_CHECK();
   }
 
@@ -511,7 +513,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         const int nc = (int)std::min<int64_t>(e->nc_max, n_tn - c0);
         const int64_t k0 = (int64_t)c0 * E;
         int r = launch_des_era(e->V, B, nc * E, st, c.codes_rm, c.stride, F, e->rpos[cur],
-                               e->node_shift[cur] + c0, e->order[cur], e->seg[cur] + k0, E, nodes,
+                               e->node_shift[cur] + k0, e->order[cur], e->seg[cur] + k0, E, nodes,
                                e->present[cur] + c0, e->local_of, n_sel, mcw, eps, e->sgain,
                                e->sdir, use_pairs ? e->pcodes : nullptr, N, e->pstride);
         if (r) return r;
@@ -534,7 +536,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         WGBM_LAUNCH_CHECK();
         hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)nc * E, 256)), dim3(256),
                            0, st, best + c0, (const int64_t*)nullptr, (const int32_t*)nullptr, F,
-                           B, E, feat_sel, nodes, nc, e->node_shift[cur] + c0, mcw, eps,
+                           B, E, feat_sel, nodes, nc, e->node_shift[cur] + k0, mcw, eps,
                            e->sgain, e->seg[cur] + k0, n_sel, e->split_l + c0, e->split_b + c0,
                            e->split_gain + k0);
         WGBM_LAUNCH_CHECK();
@@ -580,12 +582,13 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         a.resid = e->rpos[cur];  // residuals in position order (global positions)
         a.resid_by_pos = 1;
         a.resid_tree_stride = 0;
-        // quantised with the histogram shift of each tile's (tree, node)
-        a.shifts = e->node_shift[cur] + c0;
+        // quantised with the histogram shift of each tile's key (the (tree,
+        // node) with one era, the (tree, node, era) segment with several)
+        a.shifts = e->node_shift[cur] + k0;
         a.order = e->order[cur];
         a.tiles = e->htiles;
         a.n_tiles = e->hn;
-        a.keys_per_tree = E;
+        a.keys_per_tree = 1;
         a.num_bins = B;
         a.part = e->part;
         a.V = e->V;
@@ -635,7 +638,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
           const int64_t nacc = (int64_t)nc * n_sel * ((B - 1 + kDesChunk - 1) / kDesChunk);
           hipLaunchKernelGGL(des_accumulate_kernel, dim3(blocks_for(nacc, 128)), dim3(128), 0, st,
                              e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, n_sel, nodes, nc,
-                             e->present[cur] + c0, e->node_shift[cur] + c0, mcw, eps, e->crit,
+                             e->present[cur] + c0, e->node_shift[cur] + k0, mcw, eps, e->crit,
                              e->agree, agree_max + c0);
           WGBM_LAUNCH_CHECK();
           hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)nc * ncand, 256)),
@@ -644,7 +647,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
           WGBM_LAUNCH_CHECK();
           hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)nc * E, 256)), dim3(256),
                              0, st, best + c0, e->hq[hcur], e->hc[hcur], F, B, E, feat_sel, nodes,
-                             nc, e->node_shift[cur] + c0, mcw, eps, (const float*)nullptr,
+                             nc, e->node_shift[cur] + k0, mcw, eps, (const float*)nullptr,
                              e->seg[cur] + k0, n_sel, e->split_l + c0, e->split_b + c0,
                              e->split_gain + k0);
           WGBM_LAUNCH_CHECK();

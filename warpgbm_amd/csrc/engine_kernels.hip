@@ -107,7 +107,9 @@ __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_
   if (gid == 0) seg[(int64_t)T * E] = (int64_t)T * n;
   if (gid < T) {
     present[gid] = 1;
-    node_shift[gid] = shifts[gid];
+    // one era: the root's key is its tree; several eras: root_totals_kernel
+    // writes every (tree, era) key's own shift
+    if (E == 1) node_shift[gid] = shifts[gid];
     best[gid] = 0ull;
     if (agree_max) agree_max[gid] = 0;
   }
@@ -300,21 +302,21 @@ __device__ inline void segment_left_sums(int64_t k, const int64_t* __restrict__ 
 }
 
 // Max of the left (ml) and right (mr) residual magnitudes (float bits) of
-// the rows of split node tn, whose positions are [P0, P1): its own words
-// when it lies inside one block, else the last-node partial of its first
-// block and the first-node partials of the blocks after it (the node is
-// their first node).  The gthreads threads of a group share the blocks; the
-// caller reduces the maximum over the group.
-__device__ inline void node_child_max(int tn, int64_t P0, int64_t P1, const PartSums& ps,
-                                      int gt, int gthreads, uint32_t& ml, uint32_t& mr) {
+// the rows of segment k (one era: the node), whose positions are [P0, P1):
+// its own words when it lies inside one block, else the last-segment
+// partial of its first block and the first-segment partials of the blocks
+// after it (the segment is their first segment).  The gthreads threads of a
+// group share the blocks; the caller reduces the maximum over the group.
+__device__ inline void seg_child_max(int64_t k, int64_t P0, int64_t P1, const PartSums& ps,
+                                     int gt, int gthreads, uint32_t& ml, uint32_t& mr) {
   ml = 0;
   mr = 0;
   if (P1 <= P0) return;
   const int64_t b0 = P0 / kPartBlock, b1 = (P1 - 1) / kPartBlock;
   if (b0 == b1) {
     if (gt == 0) {
-      ml = ps.own_ml[tn];
-      mr = ps.own_mr[tn];
+      ml = ps.own_ml[k];
+      mr = ps.own_mr[k];
     }
     return;
   }
@@ -335,22 +337,22 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   // distinct non-empty segments; empty segments own no position): s_qn packs
   // the qh sum with the row count (qh_sum * 2^11 + rows: at most kPartBlock
   // < 2^11 rows, |q63 >> 32| <= 2^30 per row), s_ql holds the ql sum.  With
-  // a.want_max also the largest |residual| (float bits) of each split node's
-  // left and right rows, in the slot of the node's first position in the
-  // block (the slot of its first segment there).
+  // a.want_max also the largest |residual| (float bits) of each segment's
+  // left and right rows (mode 0: all its rows are "left"), in the same slot:
+  // per (node, era) segment, so per node when there is one era.
   extern __shared__ int64_t s_dyn[];
   int64_t* s_qn = s_dyn;
   int64_t* s_ql = s_dyn + kPartBlock;
   uint32_t* s_ml = (uint32_t*)(s_dyn + 2 * kPartBlock);
   uint32_t* s_mr = s_ml + kPartBlock;
   __shared__ int s_wlast[kPartThreads / 64];  // key of each wave's last position
-  __shared__ int64_t s_sl, s_sn;  // start of the block's last segment, and of its node
+  __shared__ int64_t s_sl;  // start of the block's last segment
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
   const int64_t p1 = p0 + kPartBlock < a.n_pos ? p0 + kPartBlock : a.n_pos;
   const bool sums = a.mode != 2;
-  const bool maxes = a.mode == 1 && a.want_max;
+  const bool maxes = sums && a.want_max;
   // Thread t owns the PJ consecutive positions pl0 .. pl0 + PJ - 1 of the
   // block (16-byte loads of keys, rows and residuals; rows of one segment
   // are usually combined in registers before the wave reduction).  Issued
@@ -362,7 +364,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int pl0 = tid * PJ;
   const int64_t pb = p0 + pl0;
-  int key[PJ], slot[PJ], nslot[PJ], tnv[PJ], lv[PJ];
+  int key[PJ], slot[PJ], tnv[PJ], lv[PJ];
   int32_t rowv[PJ];
   float rv[PJ];
   bool ok[PJ];
@@ -404,10 +406,10 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   }
   wgbm_lds_barrier();  // the LDS words are cleared (the loads stay in flight)
   // Everything a position needs of its segment and node, in one round of
-  // independent loads: the segment's bounds, the node's bounds (several
-  // eras) and its route record.  col: -2 the row stays (node absent), -1
-  // leaf update, >= 0 the split's code column.
-  bool seg_in[PJ], node_in[PJ];  // the segment / node lies inside the block
+  // independent loads: the segment's bounds and its node's route record.
+  // col: -2 the row stays (node absent), -1 leaf update, >= 0 the split's
+  // code column.
+  bool seg_in[PJ];  // the segment lies inside the block
   NodeRoute nr[PJ];
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
@@ -415,18 +417,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     slot[j] = (int)((sk > p0 ? sk : p0) - p0);
     seg_in[j] = sk >= p0 && se <= p1;
     tnv[j] = key[j] / a.E;
-    int64_t nb = sk, ne = se;  // one era: the node is the segment
-    if (maxes && a.E > 1) {
-      nb = a.seg[(int64_t)tnv[j] * a.E];
-      ne = a.seg[(int64_t)(tnv[j] + 1) * a.E];
-    }
-    nslot[j] = (int)((nb > p0 ? nb : p0) - p0);
-    node_in[j] = nb >= p0 && ne <= p1;
-    if (sums && pb + j == p1 - 1) {
-      // the block's last position: where its segment and node start
-      s_sl = sk;
-      s_sn = nb;  // (the segment itself unless maxes with several eras)
-    }
+    if (sums && pb + j == p1 - 1) s_sl = sk;  // the block's last position: its segment's start
     if (a.mode != 0) nr[j] = a.nroute[tnv[j]];
     lv[j] = (ok[j] && a.mode != 0) ? nr[j].col : -2;
   }
@@ -450,7 +441,7 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
       if (ql) atomicAdd((unsigned long long*)&s_ql[sl], (unsigned long long)ql);
     }
   };
-  // node maxima likewise, per node slot
+  // segment maxima likewise, per segment slot
   auto max_slot = [&](int sl, bool act, uint32_t ml, uint32_t mr) {
     const uint64_t on = __ballot(act);
     if (on == 0ull) return;
@@ -545,12 +536,12 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
         if (dirs[j] == 1) mr = m > mr ? m : mr;
         act = act || dirs[j] != 2;
       }
-      max_slot(nslot[0], act, ml, mr);
+      max_slot(slot[0], act, ml, mr);
     } else {
 #pragma unroll
       for (int j = 0; j < PJ; ++j) {
         const uint32_t m = wgbm_abs_bits(rv[j]);
-        max_slot(nslot[j], dirs[j] != 2, dirs[j] == 0 ? m : 0u, dirs[j] == 1 ? m : 0u);
+        max_slot(slot[j], dirs[j] != 2, dirs[j] == 0 ? m : 0u, dirs[j] == 1 ? m : 0u);
       }
     }
   }
@@ -586,18 +577,16 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     const int kp = j == 0 ? prev : key[j - 1];
     if (!ok[j] || (i > 0 && kp == k)) continue;
     if (seg_in[j]) {
+      // a segment inside the block: its sums (and maxima) are complete here
       int64_t qh;
       int32_t n;
       unpack(s_qn[i], qh, n);
       a.ps.own_qh[k] = qh;
       a.ps.own_ql[k] = s_ql[i];
       a.ps.own_n[k] = n;
-    }
-    if (maxes) {
-      // a node inside the block: its maxima are complete here
-      if (node_in[j] && nslot[j] == i) {
-        a.ps.own_ml[tnv[j]] = s_ml[i];
-        a.ps.own_mr[tnv[j]] = s_mr[i];
+      if (maxes) {
+        a.ps.own_ml[k] = s_ml[i];
+        a.ps.own_mr[k] = s_mr[i];
       }
     }
   }
@@ -616,14 +605,12 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
     a.ps.bl_ql[blockIdx.x] = s_ql[ls];
     a.ps.bl_n[blockIdx.x] = n;
     if (maxes) {
-      // the first and last nodes of the block: their maxima here
-      a.ps.bf_node[blockIdx.x] = key[0] / a.E;  // thread 0 holds the block's first position
-      const int64_t sn = s_sn;
-      const int lns = (int)((sn > p0 ? sn : p0) - p0);
+      // the first and last segments of the block: their maxima here
+      a.ps.bf_node[blockIdx.x] = key[0];  // thread 0 holds the block's first position
       a.ps.bf_ml[blockIdx.x] = s_ml[0];
       a.ps.bf_mr[blockIdx.x] = s_mr[0];
-      a.ps.bl_ml[blockIdx.x] = s_ml[lns];
-      a.ps.bl_mr[blockIdx.x] = s_mr[lns];
+      a.ps.bl_ml[blockIdx.x] = s_ml[ls];
+      a.ps.bl_mr[blockIdx.x] = s_mr[ls];
     }
   }
 }
@@ -775,10 +762,13 @@ __global__ __launch_bounds__(1024) void block_scan_kernel(int32_t nb, PartSums p
   block_scan_body(nb, ps);
 }
 
-// root totals of every (tree, era) key: quantised residual sum and rows
+// root totals of every (tree, era) key: quantised residual sum and rows;
+// with key_shift (several eras) also the key's histogram shift from its
+// largest |residual| (the root route ran with want_max)
 __global__ void root_totals_kernel(int32_t n_keys, const int64_t* __restrict__ seg, PartSums ps,
                                    int64_t* __restrict__ tot_qh, int64_t* __restrict__ tot_ql,
-                                   int64_t* __restrict__ tot_c) {
+                                   int64_t* __restrict__ tot_c, int32_t qbits,
+                                   int32_t* __restrict__ key_shift) {
   const int k = blockIdx.x * blockDim.x + threadIdx.x;
   if (k >= n_keys) return;
   int64_t qh, ql, n;
@@ -786,6 +776,34 @@ __global__ void root_totals_kernel(int32_t n_keys, const int64_t* __restrict__ s
   tot_qh[k] = qh;
   tot_ql[k] = ql;
   tot_c[k] = n;
+  if (key_shift) {
+    uint32_t m = 0, unused = 0;
+    seg_child_max(k, seg[k], seg[k + 1], ps, 0, 1, m, unused);
+    key_shift[k] = key_shift_of(m, qbits);
+  }
+}
+
+// Several eras: the histogram shifts of one split's two children's segments
+// of an era (keys kl, kr of the next level; k the parent's segment), each from
+// its own largest |residual| (key_shift_of), and whether both are
+// histogrammed: the sibling's segment is parent - child only when the
+// parent's and both children's shifts are equal (the subtraction is then
+// exact).  A node that does not split has no children: their words are 0.
+__device__ inline void era_child_shifts(int64_t k, int64_t kl, int64_t kr, bool sp,
+                                        const PartSums& ps, const int64_t* __restrict__ seg,
+                                        const LevelNext& nx, bool& both) {
+  int sl = 0, sr = 0;
+  both = false;
+  if (sp && nx.have_max) {
+    uint32_t ml = 0, mr = 0;
+    seg_child_max(k, seg[k], seg[k + 1], ps, 0, 1, ml, mr);
+    sl = key_shift_of(ml, nx.qbits);
+    sr = key_shift_of(mr, nx.qbits);
+    const int sp_k = nx.node_shift[k];
+    both = sl != sp_k || sr != sp_k;
+  }
+  nx.node_shift_next[kl] = sl;
+  nx.node_shift_next[kr] = sr;
 }
 
 // wpn waves per (tree, node) of the level (1, 2 or 4: the eras are spread
@@ -846,21 +864,26 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
   tot = wgbm_wave_incl_scan_i64(tot);
   group_sum(ltot, tot, ltot, tot, false);
   const int side = (ltot <= tot - ltot) ? 0 : 1;  // the smaller child gets the histogram
-  // the children's histogram shifts from their largest |residual|
-  uint32_t ml = 0, mr = 0;
-  if (sp && nx.have_max) node_child_max(tn, base, seg[k0 + E], ps, gt, gthreads, ml, mr);
-  ml = wgbm_wave_reduce_max_u32(ml);
-  mr = wgbm_wave_reduce_max_u32(mr);
-  {
-    int64_t gml, gmr;
-    group_sum((int64_t)ml, (int64_t)mr, gml, gmr, true);
-    ml = (uint32_t)gml;
-    mr = (uint32_t)gmr;
+  // One era: the children's histogram shifts from their largest |residual|
+  // (node_shift_rule).  Several eras: per (child, era) segment, below.
+  int hs = 0, hs_l = 0, hs_r = 0;
+  bool both = false;  // both children histogrammed
+  if (E == 1) {
+    uint32_t ml = 0, mr = 0;
+    if (sp && nx.have_max) seg_child_max(tn, base, seg[k0 + E], ps, gt, gthreads, ml, mr);
+    ml = wgbm_wave_reduce_max_u32(ml);
+    mr = wgbm_wave_reduce_max_u32(mr);
+    {
+      int64_t gml, gmr;
+      group_sum((int64_t)ml, (int64_t)mr, gml, gmr, true);
+      ml = (uint32_t)gml;
+      mr = (uint32_t)gmr;
+    }
+    hs = live ? nx.node_shift[tn] : 0;
+    hs_l = sp && nx.have_max ? node_shift_rule(ml, hs, nx.qbits) : hs;
+    hs_r = sp && nx.have_max ? node_shift_rule(mr, hs, nx.qbits) : hs;
+    both = sp && (hs_l != hs || hs_r != hs);
   }
-  const int hs = live ? nx.node_shift[tn] : 0;
-  const int hs_l = sp && nx.have_max ? node_shift_rule(ml, hs, nx.qbits) : hs;
-  const int hs_r = sp && nx.have_max ? node_shift_rule(mr, hs, nx.qbits) : hs;
-  const bool both = sp && (hs_l != hs || hs_r != hs);  // both children histogrammed
   int64_t carry_l = 0, carry_r = 0;
   for (int e0 = 0; e0 < E; e0 += gthreads) {
     const int e = e0 + gt;
@@ -920,16 +943,18 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
       nx.tot_qh_next[c0 + E + e] = sp ? nx.tot_qh[k0 + e] - qh : 0;
       nx.tot_ql_next[c0 + E + e] = sp ? nx.tot_ql[k0 + e] - ql : 0;
       nx.tot_c_next[c0 + E + e] = sp ? R : 0;
+      bool both_e = both;
+      if (E > 1) era_child_shifts(k0 + e, c0 + e, c0 + E + e, sp, ps, seg, nx, both_e);
       nx.key_list_next[2 * (k0 + e)] =
-          sp ? (int32_t)(c0 + (both ? 0 : side * E) + e) : -1;
-      nx.key_list_next[2 * (k0 + e) + 1] = both ? (int32_t)(c0 + E + e) : -1;
+          sp ? (int32_t)(c0 + (both_e ? 0 : side * E) + e) : -1;
+      nx.key_list_next[2 * (k0 + e) + 1] = both_e ? (int32_t)(c0 + E + e) : -1;
     }
     carry_l += cl;
     carry_r += cr;
   }
   if (live && gt < 2) {
     nx.present_next[2 * tn + gt] = sp;
-    nx.node_shift_next[2 * tn + gt] = gt == 0 ? hs_l : hs_r;
+    if (E == 1) nx.node_shift_next[2 * tn + gt] = gt == 0 ? hs_l : hs_r;
   }
   if (tn == T * nodes - 1 && gt == 0) nx.seg_next[(int64_t)2 * T * nodes * E] = n_pos;
 }
@@ -1058,14 +1083,20 @@ __global__ __launch_bounds__(1024) void level_scan_kernel(
     int64_t il = wgbm_wave_incl_scan_i64(L), ir = wgbm_wave_incl_scan_i64(R);
     const int64_t ltot = __shfl(il, 63, 64), rtot = __shfl(ir, 63, 64);
     const int side = (ltot <= rtot) ? 0 : 1;  // the smaller child gets the histogram
-    uint32_t ml = 0, mr = 0;
-    if (sp && nx.have_max) node_child_max(tn, base, seg[k0 + E], ps, lane, 64, ml, mr);
-    ml = wgbm_wave_reduce_max_u32(ml);
-    mr = wgbm_wave_reduce_max_u32(mr);
-    const int hs = nx.node_shift[tn];
-    const int hs_l = sp && nx.have_max ? node_shift_rule(ml, hs, nx.qbits) : hs;
-    const int hs_r = sp && nx.have_max ? node_shift_rule(mr, hs, nx.qbits) : hs;
-    const bool both = sp && (hs_l != hs || hs_r != hs);  // both children histogrammed
+    // one era: the children's shifts by node_shift_rule; several eras: per
+    // (child, era) segment (era_child_shifts)
+    int hs = 0, hs_l = 0, hs_r = 0;
+    bool both = false;  // both children histogrammed
+    if (E == 1) {
+      uint32_t ml = 0, mr = 0;
+      if (sp && nx.have_max) seg_child_max(tn, base, seg[k0 + E], ps, lane, 64, ml, mr);
+      ml = wgbm_wave_reduce_max_u32(ml);
+      mr = wgbm_wave_reduce_max_u32(mr);
+      hs = nx.node_shift[tn];
+      hs_l = sp && nx.have_max ? node_shift_rule(ml, hs, nx.qbits) : hs;
+      hs_r = sp && nx.have_max ? node_shift_rule(mr, hs, nx.qbits) : hs;
+      both = sp && (hs_l != hs || hs_r != hs);
+    }
     if (lane < E) {
       nx.seg_next[c0 + lane] = base + il - L;
       nx.seg_next[c0 + E + lane] = base + ltot + ir - R;
@@ -1076,13 +1107,15 @@ __global__ __launch_bounds__(1024) void level_scan_kernel(
       nx.tot_qh_next[c0 + E + lane] = sp ? nx.tot_qh[k0 + lane] - qh : 0;
       nx.tot_ql_next[c0 + E + lane] = sp ? nx.tot_ql[k0 + lane] - ql : 0;
       nx.tot_c_next[c0 + E + lane] = sp ? R : 0;
+      bool both_e = both;
+      if (E > 1) era_child_shifts(k0 + lane, c0 + lane, c0 + E + lane, sp, ps, seg, nx, both_e);
       nx.key_list_next[2 * (k0 + lane)] =
-          sp ? (int32_t)(c0 + (both ? 0 : side * E) + lane) : -1;
-      nx.key_list_next[2 * (k0 + lane) + 1] = both ? (int32_t)(c0 + E + lane) : -1;
+          sp ? (int32_t)(c0 + (both_e ? 0 : side * E) + lane) : -1;
+      nx.key_list_next[2 * (k0 + lane) + 1] = both_e ? (int32_t)(c0 + E + lane) : -1;
     }
     if (lane < 2) {
       nx.present_next[2 * tn + lane] = sp;
-      nx.node_shift_next[2 * tn + lane] = lane == 0 ? hs_l : hs_r;
+      if (E == 1) nx.node_shift_next[2 * tn + lane] = lane == 0 ? hs_l : hs_r;
     }
     if (tn == T * nodes - 1 && lane == 0) nx.seg_next[(int64_t)2 * T * nodes * E] = n_pos;
   }

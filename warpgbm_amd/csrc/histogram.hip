@@ -130,7 +130,9 @@ void hist_tiles_kernel(
   // once before the loop rather than at the top of every iteration, where it
   // would also drain the wave's outstanding LDS atomics (both share one
   // counter).
-  const int s_raw = sm.partial ? __builtin_amdgcn_readfirstlane(s_call) : shifts[tree];
+  const int s_raw = sm.partial   ? __builtin_amdgcn_readfirstlane(s_call)
+                    : sm.key_max ? wgbm_shift_from_bits(sm.key_max[tl.key], sm.qbits)
+                                 : shifts[tree];
   const int s = s_raw < -160 ? -160 : (s_raw > 255 ? 255 : s_raw);
   const int32_t* __restrict__ ord = GATHER ? order + tl.begin : nullptr;
   const int n = (int)(tl.end - tl.begin);  // a tile has at most 65536 rows
@@ -493,7 +495,7 @@ template <int FW>
 __global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
     const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
     int32_t n_keys, int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
-    const int32_t* __restrict__ shifts, const uint32_t* __restrict__ absmax_bits,
+    const uint32_t* __restrict__ absmax_bits, int32_t key_stride, int32_t qbits,
     const int32_t* __restrict__ n_tiles, int32_t accumulate, FeatOut fo, float* __restrict__ G,
     float* __restrict__ H) {
   // tile_words < 2^31 (checked by the launcher)
@@ -516,8 +518,9 @@ __global__ __launch_bounds__(256) void hist_finalize_f32_kernel(
   int64_t Q, C;
   finalize_sum<FW>(part, tile_words, i, ok, t0, t1, Q, C);
   if (!ok || threadIdx.x >= FW) return;
-  const bool bad = (*absmax_bits) >= 0x7f800000u;  // non-finite residual seen
-  const float g = bad ? __builtin_nanf("") : wgbm_dequantise(Q, shifts[0]);
+  const uint32_t mb = absmax_bits[key_stride ? k : 0];
+  const bool bad = mb >= 0x7f800000u;  // non-finite residual seen
+  const float g = bad ? __builtin_nanf("") : wgbm_dequantise(Q, wgbm_shift_from_bits(mb, qbits));
   const float h = (float)C;
   const int n_out = fo.head ? fo.n_out : n_feats;
   for (int of = fo.head ? fo.head[f] : f; of >= 0; of = fo.head ? fo.next[of] : -1) {
@@ -600,7 +603,7 @@ __device__ inline void plane_sum(const unsigned long long* __restrict__ part, in
 __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_f32_kernel(
     const unsigned long long* __restrict__ part, const int32_t* __restrict__ key_tile_start,
     int32_t n_keys, int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
-    const int32_t* __restrict__ shifts, const uint32_t* __restrict__ absmax_bits,
+    const uint32_t* __restrict__ absmax_bits, int32_t key_stride, int32_t qbits,
     const int32_t* __restrict__ n_tiles, int32_t accumulate, FeatOut fo, float* __restrict__ G,
     float* __restrict__ H) {
   __shared__ unsigned long long sq[kPlaneMaxBins * kPlaneRow];
@@ -616,8 +619,9 @@ __global__ __launch_bounds__(kPlaneThreads) void hist_finalize_plane_f32_kernel(
   const int t0 = key_tile_start[k];
   const int t1 = key_tile_start[k + 1] < *n_tiles ? key_tile_start[k + 1] : *n_tiles;
   plane_sum(part, tile_words, plane * num_bins * kHistSlots, num_bins, t0, t1, sq, sc);
-  const bool bad = (*absmax_bits) >= 0x7f800000u;  // non-finite residual seen
-  const int s = shifts[0];
+  const uint32_t mb = absmax_bits[key_stride ? k : 0];
+  const bool bad = mb >= 0x7f800000u;  // non-finite residual seen
+  const int s = wgbm_shift_from_bits(mb, qbits);
   const int n_out = fo.head ? fo.n_out : n_feats;
   const bool lane_major = fo.run == nullptr || fo.run[chunk] != 0;
   for (int o = threadIdx.x; o < kHistSlots * num_bins; o += kPlaneThreads) {
@@ -862,7 +866,7 @@ __global__ __launch_bounds__(1024) void hist_prep_kernel(
     uint32_t* __restrict__ partial, float* __restrict__ gathered, int32_t n_part, int32_t plan,
     const int64_t* __restrict__ seg, int32_t n_keys, int32_t tile_rows, int32_t max_tiles,
     Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
-    int32_t* __restrict__ n_tiles, FeatMapArgs fm) {
+    int32_t* __restrict__ n_tiles, FeatMapArgs fm, uint32_t* __restrict__ key_max) {
   if ((int)blockIdx.x >= n_part) {
     if (plan && (int)blockIdx.x == n_part)
       plan_tiles_body(seg, n, n_keys, nullptr, tile_rows, 1, max_tiles, tiles, key_tile_start,
@@ -870,6 +874,11 @@ __global__ __launch_bounds__(1024) void hist_prep_kernel(
     else if (fm.feat_idx)
       feature_map_body(fm);
     return;
+  }
+  if (key_max) {
+    // the per-key maxima of hist_key_max_kernel start from zero
+    for (int k = blockIdx.x * blockDim.x + threadIdx.x; k < n_keys; k += n_part * blockDim.x)
+      key_max[k] = 0u;
   }
   uint32_t m = 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -882,6 +891,22 @@ __global__ __launch_bounds__(1024) void hist_prep_kernel(
   }
   m = wgbm_block_max_u32(m);
   if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(256) void hist_key_max_kernel(
+    const Tile* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
+    const float* __restrict__ resid, const int32_t* __restrict__ order, int32_t by_pos,
+    uint32_t* __restrict__ key_max) {
+  if ((int)blockIdx.x >= *n_tiles) return;  // uniform per workgroup
+  const Tile tl = tiles[blockIdx.x];
+  uint32_t m = 0;
+  for (int64_t p = tl.begin + threadIdx.x; p < tl.end; p += blockDim.x) {
+    const int64_t r = (by_pos || !order) ? p : (int64_t)order[p];
+    const uint32_t b = wgbm_abs_bits(resid[r]);
+    m = b > m ? b : m;
+  }
+  m = wgbm_block_max_u32(m);
+  if (threadIdx.x == 0 && m) atomicMax(key_max + tl.key, m);
 }
 
 __global__ __launch_bounds__(1024) void plan_tiles_kernel(
@@ -1104,15 +1129,15 @@ static bool use_plane_finalize(int64_t tiles_per_key, int64_t n_keys, int n_chun
 
 int launch_finalize_f32(int64_t tiles_per_key, const unsigned long long* part,
                         const int32_t* key_tile_start, int32_t n_keys, int32_t n_chunks, int32_t V,
-                        int32_t num_bins, int32_t n_feats, const int32_t* shifts,
-                        const uint32_t* absmax_bits, const int32_t* n_tiles, int32_t accumulate,
-                        FeatOut fo, float* G, float* H, hipStream_t st) {
+                        int32_t num_bins, int32_t n_feats, const uint32_t* absmax_bits,
+                        int32_t key_stride, int32_t qbits, const int32_t* n_tiles,
+                        int32_t accumulate, FeatOut fo, float* G, float* H, hipStream_t st) {
   if (use_plane_finalize(tiles_per_key, n_keys, n_chunks, V, num_bins)) {
     const int64_t wg = (int64_t)n_keys * n_chunks * V;
     WGBM_REQUIRE(wg < ((int64_t)1 << 31), "finalize: too many segments");
     hipLaunchKernelGGL(hist_finalize_plane_f32_kernel, dim3((unsigned)wg), dim3(kPlaneThreads), 0,
-                       st, part, key_tile_start, n_keys, n_chunks, V, num_bins, n_feats, shifts,
-                       absmax_bits, n_tiles, accumulate, fo, G, H);
+                       st, part, key_tile_start, n_keys, n_chunks, V, num_bins, n_feats,
+                       absmax_bits, key_stride, qbits, n_tiles, accumulate, fo, G, H);
     WGBM_LAUNCH_CHECK();
     return 0;
   }
@@ -1124,8 +1149,8 @@ int launch_finalize_f32(int64_t tiles_per_key, const unsigned long long* part,
   const unsigned wg = (unsigned)(n_keys * ((tile_words + fw - 1) / fw));
 #define WGBM_L(F)                                                                                 \
   hipLaunchKernelGGL(hist_finalize_f32_kernel<F>, dim3(wg), dim3(256), 0, st, part, key_tile_start, \
-                     n_keys, n_chunks, V, num_bins, n_feats, shifts, absmax_bits, n_tiles,          \
-                     accumulate, fo, G, H)
+                     n_keys, n_chunks, V, num_bins, n_feats, absmax_bits, key_stride, qbits,        \
+                     n_tiles, accumulate, fo, G, H)
   WGBM_FIN_DISPATCH(fw, WGBM_L)
 #undef WGBM_L
   WGBM_LAUNCH_CHECK();

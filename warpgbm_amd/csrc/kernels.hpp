@@ -47,6 +47,9 @@ struct ShiftFromMax {
   int32_t qbits = 0;
   uint32_t* absmax_bits = nullptr;  // written by workgroup 0
   int32_t* shift = nullptr;
+  // per key (partial == nullptr): the float bits of each key's largest
+  // |residual| (hist_key_max_kernel); a tile takes its key's shift from them
+  const uint32_t* key_max = nullptr;
 };
 
 // Feature selection of a histogram call (compute_histogram3's feature
@@ -133,11 +136,13 @@ int launch_hist_tiles(const HistLaunch& a, hipStream_t st);
 int probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, hipStream_t st);
 
 // kernels launched directly from other translation units
+// absmax_bits: the call's largest |residual| (float bits; key_stride 0), or
+// each key's (key_stride 1); the shift follows from them and qbits
 int launch_finalize_f32(int64_t tiles_per_key, const unsigned long long* part,
                         const int32_t* key_tile_start, int32_t n_keys, int32_t n_chunks, int32_t V,
-                        int32_t num_bins, int32_t n_feats, const int32_t* shifts,
-                        const uint32_t* absmax_bits, const int32_t* n_tiles, int32_t accumulate,
-                        FeatOut fo, float* G, float* H, hipStream_t st);
+                        int32_t num_bins, int32_t n_feats, const uint32_t* absmax_bits,
+                        int32_t key_stride, int32_t qbits, const int32_t* n_tiles,
+                        int32_t accumulate, FeatOut fo, float* G, float* H, hipStream_t st);
 int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
                           const int32_t* key_tile_start, const int32_t* key_list, int32_t n_list,
                           int32_t n_chunks, int32_t V, int32_t num_bins, int32_t n_feats,
@@ -154,7 +159,13 @@ __global__ void hist_prep_kernel(const float* resid, const int32_t* rows, int64_
                                  uint32_t* partial, float* gathered, int32_t n_part, int32_t plan,
                                  const int64_t* seg, int32_t n_keys, int32_t tile_rows,
                                  int32_t max_tiles, Tile* tiles, int32_t* key_tile_start,
-                                 int32_t* n_tiles, FeatMapArgs fm);
+                                 int32_t* n_tiles, FeatMapArgs fm, uint32_t* key_max);
+// the largest |residual| (float bits) of every key of a tile plan: one
+// workgroup per tile, atomicMax into key_max (cleared by hist_prep_kernel);
+// the residual of position p is resid[p] (by_pos), resid[order[p]], or
+// resid[p] without an order
+__global__ void hist_key_max_kernel(const Tile* tiles, const int32_t* n_tiles, const float* resid,
+                                    const int32_t* order, int32_t by_pos, uint32_t* key_max);
 // era regrouping of a row list (compute_histogram3 with eras): block counts,
 // per-era scans, era starts, block scatter; no device-scope atomics
 constexpr int kEraWindow = 8192;  // eras counted per LDS pass

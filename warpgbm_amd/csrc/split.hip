@@ -172,7 +172,7 @@ __device__ inline void atomic_max_grouped_u64(unsigned long long* base, int key,
 __global__ __launch_bounds__(128) void des_accumulate_kernel(
     const int64_t* __restrict__ hq, const int32_t* __restrict__ hc, int32_t F, int32_t B,
     int32_t E, const int32_t* __restrict__ feat_sel, int32_t n_sel, int32_t nodes_in_level,
-    int32_t n_tn, const int32_t* __restrict__ present, const int32_t* __restrict__ node_shift,
+    int32_t n_tn, const int32_t* __restrict__ present, const int32_t* __restrict__ key_shift,
     float mcw, float eps, float* __restrict__ crit, int32_t* __restrict__ agree,
     int32_t* __restrict__ agree_max) {
   const int nb = B - 1;
@@ -189,7 +189,6 @@ __global__ __launch_bounds__(128) void des_accumulate_kernel(
   }
   int amax = 0;
   if (active) {
-    const int s = node_shift[tn];
     const int f = feat_sel[l];
     const int b0 = ch * kDesChunk;
     double gs[kDesChunk];
@@ -203,6 +202,7 @@ __global__ __launch_bounds__(128) void des_accumulate_kernel(
 #pragma unroll
     for (int k = 0; k < kDesChunk; ++k) bs[k] = 0.0;
     for (int e = 0; e < E; ++e) {
+      const int s = key_shift[(int64_t)tn * E + e];  // the (node, era) segment's shift
       const int64_t base = (((int64_t)tn * E + e) * F + f) * B;
       const int64_t* q = hq + base;
       const int32_t* c = hc + base;
@@ -288,7 +288,7 @@ __global__ void des_finish_kernel(const unsigned long long* __restrict__ best,
                                   const int64_t* __restrict__ hq, const int32_t* __restrict__ hc,
                                   int32_t F, int32_t B, int32_t E,
                                   const int32_t* __restrict__ feat_sel, int32_t nodes_in_level,
-                                  int32_t n_tn, const int32_t* __restrict__ node_shift,
+                                  int32_t n_tn, const int32_t* __restrict__ key_shift,
                                   float mcw, float eps, const float* __restrict__ staged,
                                   const int64_t* __restrict__ seg, int32_t n_sel,
                                   int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
@@ -320,7 +320,7 @@ __global__ void des_finish_kernel(const unsigned long long* __restrict__ best,
                               : staged[k2 * ((int64_t)n_sel * nb) + idx];
     return;
   }
-  const int s = node_shift[tn];
+  const int s = key_shift[gid];  // the (node, era) segment's shift
   const int64_t base = (((int64_t)tn * E + e) * F + feat_sel[l]) * B;
   const int64_t* q = hq + base;
   const int32_t* c = hc + base;
@@ -353,7 +353,7 @@ template <int V, int BT>
 __global__ __launch_bounds__(kDesEraThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void des_era_kernel(
     const int8_t* __restrict__ codes, int64_t stride, int32_t F,
-    const float* __restrict__ rpos, const int32_t* __restrict__ node_shift,
+    const float* __restrict__ rpos, const int32_t* __restrict__ key_shift,
     const int32_t* __restrict__ order,
     const int64_t* __restrict__ seg, int32_t E, int32_t n_keys, int32_t nodes_in_level,
     const int32_t* __restrict__ present, const int32_t* __restrict__ local_of, int32_t n_sel,
@@ -395,10 +395,9 @@ void des_era_kernel(
       const int l0 = __builtin_ctzll(todo);
       todo &= todo - 1;
       const int key = kb + l0 * slots;
-      const int tn = key / E;
       const int64_t begin = seg[key];
       const int n = (int)(seg[key + 1] - begin);  // <= 65536 (checked by the engine)
-      const int s = node_shift[tn];
+      const int s = key_shift[key];                // the segment's own shift
       for (int i = threadIdx.x; i < V * Bp * kHistSlots; i += kDesEraThreads) lds[i] = 0ull;
       __syncthreads();
       // software pipeline as in the tile histogram: wave w takes the row
@@ -531,7 +530,7 @@ template <int BT>
 __global__ __launch_bounds__(kDesPairThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void des_pair_kernel(
     const uint8_t* __restrict__ pcodes, uint32_t pbytes, uint32_t pstride, int32_t F,
-    const float* __restrict__ rpos, const int32_t* __restrict__ node_shift,
+    const float* __restrict__ rpos, const int32_t* __restrict__ key_shift,
     const int32_t* __restrict__ order, const int64_t* __restrict__ seg, int32_t E,
     int32_t n_keys, int32_t nodes_in_level, const int32_t* __restrict__ present,
     const int32_t* __restrict__ local_of, int32_t n_sel, float mcw, float eps,
@@ -578,7 +577,7 @@ void des_pair_kernel(
       const int key = kb + l0 * slots;
       const int64_t begin = seg[key];
       const int n = (int)(seg[key + 1] - begin);  // <= 65536 (checked by the engine)
-      const int s = node_shift[key / E];
+      const int s = key_shift[key];  // the segment's own shift
 
       // rows: wave w takes groups [i, i + U), i = (w + k*nwaves)*U; lane
       // u < U loads row u's id and residual; two register sets alternate so
@@ -870,7 +869,7 @@ int launch_split_level_e1(int n_tn, hipStream_t st, const int64_t* hq, const int
 }
 
 int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* codes,
-                   int64_t stride, int32_t F, const float* rpos, const int32_t* node_shift,
+                   int64_t stride, int32_t F, const float* rpos, const int32_t* key_shift,
                    const int32_t* order, const int64_t* seg, int32_t E, int32_t nodes_in_level,
                    const int32_t* present, const int32_t* local_of, int32_t n_sel, float mcw,
                    float eps, float* gain, int8_t* dir, const uint8_t* pcodes, int64_t n_rows,
@@ -895,7 +894,7 @@ int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* c
       attr = true;                                                                             \
     }                                                                                          \
     hipLaunchKernelGGL((des_pair_kernel<BB>), grid, dim3(kDesPairThreads), lds, st, pcodes,    \
-                       pbytes, (uint32_t)pstride, F, rpos, node_shift, order, seg, E, n_keys,  \
+                       pbytes, (uint32_t)pstride, F, rpos, key_shift, order, seg, E, n_keys,   \
                        nodes_in_level, present, local_of, n_sel, mcw, eps, gain, dir);         \
     WGBM_LAUNCH_CHECK();                                                                       \
     return 0;                                                                                  \
@@ -924,7 +923,7 @@ int launch_des_era(int V, int B, int32_t n_keys, hipStream_t st, const int8_t* c
       attr = true;                                                                             \
     }                                                                                          \
     hipLaunchKernelGGL((des_era_kernel<VV, BB>), grid, dim3(kDesEraThreads), lds, st, codes,   \
-                       stride, F, rpos, node_shift, order, seg, E, n_keys,                    \
+                       stride, F, rpos, key_shift, order, seg, E, n_keys,                     \
                        nodes_in_level, present, local_of, n_sel, B, mcw, eps, gain, dir);      \
     WGBM_LAUNCH_CHECK();                                                                       \
     return 0;                                                                                  \
