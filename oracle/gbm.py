@@ -339,7 +339,7 @@ class Forest:
         self.eps = L2_reg
 
     def fit_codes(self, codes, y, era_id=None, feat_sets=None, hist=None, scan=None,
-                  literal_f32=False):
+                  literal_f32=False, progress=None):
         codes = np.asarray(codes)
         N, F = codes.shape
         if era_id is None:
@@ -369,6 +369,8 @@ class Forest:
                     preds[rws] = preds[rws] + F32(self.lr) * v
                 self._importance(g)
                 self.forest.append(tree)
+                if progress:
+                    progress(i)
             self.train_preds = preds
         else:
             labels = np.asarray(y).astype(np.int32)
@@ -389,6 +391,8 @@ class Forest:
                     self._importance(g)
                     trees.append(tree)
                 self.forest.append(trees)
+                if progress:
+                    progress(i)
             self.train_scores = scores
         self.feature_importance = self.imp.sum(axis=0)
         return self

@@ -389,6 +389,50 @@ def test_eras_of_different_scales_bit_exact(gpu, N, E, big):
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
 
 
+def _des_gate_data(N=8000, E=4, seed=12):
+    """Four eras: feature 0 moves the target a little in the same direction
+    in every era, feature 1 a lot but with opposite signs in eras {0, 1} and
+    {2, 3}; features 2, 3 are noise."""
+    rng = np.random.default_rng(seed)
+    X = rng.integers(0, 5, (N, 4)).astype(np.int8)
+    era = np.repeat(np.arange(E), N // E)
+    sgn = np.where(era < E // 2, 1.0, -1.0)
+    y = (0.01 * (X[:, 0] - 2) + sgn * (X[:, 1] - 2) + 0.001 * rng.standard_normal(N))
+    return X, y.astype(F32), era
+
+
+def test_des_leaf_when_max_agreement_candidates_fail_min_split_gain(gpu):
+    """core.py:583-586: the DES mask is (agree == max agree) & (crit >
+    min_split_gain); when every max-agreement candidate fails the gain
+    threshold the node is a leaf, although lower-agreement candidates (here
+    feature 1, whose sign flips between eras and whose criterion is some 500
+    times larger) pass it.  min_split_gain is set between the two, from the
+    oracle's root criteria; without it the root splits."""
+    print_case("estimator", "DES leaf by min_split_gain")
+    X, y, era = _des_gate_data()
+    E, B = 4, 5
+    r = y - gbm.base_score(y)
+    qb = ops.qbits_for_rows(len(y))
+    S = np.array([ops.key_shift(m, qb) for m in ops.era_absmax(r, np.arange(len(y)), era, E)])
+    Q, C = ops.histogram_exact_q(X, ops.quantise_by_era(r, np.arange(len(y)), era, S),
+                                 np.arange(len(y)), np.arange(4), era, E, B)
+    gain, dirn = ops.split_scan(ops.dequantise(Q, S), C.astype(F32), 20, 1e-6)
+    crit, agree = ops.des_criterion(gain, dirn)
+    top = agree == agree.max()
+    a, b = float(crit[top].max()), float(crit.max())
+    assert b > 100 * a  # the gate lies between the two
+    msg = float(np.sqrt(a * b))
+    for gate, expect_leaf in ((0.0, False), (msg, True)):
+        kw = dict(num_bins=B, max_depth=3, n_estimators=2, learning_rate=0.1,
+                  min_split_gain=gate)
+        m = WarpGBM(**kw).fit(X, y, era_id=era)
+        ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era)
+        assert ("leaf_value" in ref.forest[0]) == expect_leaf
+        for i, (ta, tb) in enumerate(zip(m.forest, ref.forest)):
+            assert ta == tb, f"gate {gate}: tree {i} differs"
+        assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
+
+
 @pytest.mark.parametrize("level_bytes", [0, 1])
 def test_chunked_levels_regression_bit_exact(gpu, level_bytes):
     """A level budget of 1 byte leaves room for one (tree, node) at a time:

@@ -4,14 +4,19 @@ C2: root and 16-node histograms of 1,000,000 x 1,000 int8 codes, bit-exact
 (exact integer sums, one float32 rounding), plus size-independent invariants:
 every feature counts every row, and the 16 nodes add up to the root exactly.
 C3 (1M x 1000 float32, 32 bins, depth 5, 100 trees, lr 0.01): quantile edges
-and codes bit-exact, the first 3 trees identical to the oracle's recursive
-growth, and the predictions of all 100 trees on the training rows and on 1M
-held-out rows bit-exact against the oracle's traversal of the fitted forest.
-C4 (500k x 2000 pre-binned, 500 eras): two trees at the config's full depth 8
-through the era path, tree for tree and importance bit for bit.
-C5 (200k x 100, 10 classes, depth 6, 200 rounds): edges, codes and the first 2
-rounds (20 trees) identical; predict_proba of all 2000 trees on 1M rows
-bit-exact against the oracle's traversal + uniform prior + softmax.
+and codes bit-exact, all 100 trees identical to the oracle's recursive growth
+(in four chunks of 25 trees: a chunk starts from the training scores of the
+trees before it, which equal the oracle's when those trees are identical),
+and the predictions of all 100 trees on the training rows and on 1M held-out
+rows bit-exact against the oracle's traversal of the fitted forest.
+C4 (500k x 2000 pre-binned, 500 eras, depth 8): two trees grown by the oracle
+here, and all 100 trees, the per-era importance and the training predictions
+against the digests of the oracle's forest committed in
+tests/golden/c4_forest_digest.json (made by tests/golden/make_c4_digest.py).
+C5 (200k x 100, 10 classes, depth 6, 200 rounds): edges, codes and all 200
+rounds (2000 trees, four chunks of 50 rounds) identical; predict_proba of all
+2000 trees on 1M rows bit-exact against the oracle's traversal + uniform
+prior + softmax.
 """
 import numpy as np
 import pytest
@@ -121,17 +126,68 @@ def c3_fit(gpu):
     return X, y, m, edges, codes
 
 
-def test_c3_full_size_edges_codes_and_first_trees(c3_fit):
+def test_c3_full_size_edges_and_codes(c3_fit):
     X, y, m, edges, codes = c3_fit
-    print_case("fullsize", "C3 edges, codes, first 3 trees")
+    print_case("fullsize", "C3 edges, codes")
     assert np.array_equal(bits(torch.as_tensor(m.bin_edges).cpu().numpy()), bits(edges))
     assert np.array_equal(_gpu_codes(m, X), codes)
-    ref = gbm.Forest(num_bins=32, max_depth=5, n_estimators=3, learning_rate=0.01).fit_codes(
-        codes, y, hist=clib.hist_exact_q, scan=clib.split_scan_q)
-    assert m.base_prediction == float(ref.base)
-    for i in range(3):
-        assert m.forest[i] == ref.forest[i], f"tree {i} differs"
-        assert _leaf_rows(m.forest[i]) == len(y)
+    assert m.base_prediction == float(gbm.base_score(y))
+
+
+def _grow_chunk(codes, targets, start, era, E, kw, n, on_tree):
+    """Grow n trees (or rounds) with the oracle from the scores `start`:
+    regression (targets = y, start [N]) or softmax (targets = labels, start
+    [N, K]), in the arithmetic of gbm.Forest.fit_codes; on_tree(i, trees)
+    after each."""
+    N, F = codes.shape
+    qbits = ops.qbits_for_rows(N)
+    rows = np.arange(N)
+    scores = np.array(start, dtype=F32, copy=True)
+
+    def grower():
+        return gbm.TreeGrower(codes, era, E, kw["num_bins"], kw["max_depth"],
+                              kw.get("min_child_weight", 20), kw.get("min_split_gain", 0.0),
+                              kw.get("L2_reg", 1e-6), np.arange(F), qbits,
+                              clib.hist_exact_q, clib.split_scan_q)
+
+    lr = F32(kw["learning_rate"])
+    for i in range(n):
+        if scores.ndim == 1:
+            g = grower()
+            tree = g.grow(np.asarray(targets, F32) - scores, rows)
+            for rws, v in g.leaf_rows:
+                scores[rws] = scores[rws] + lr * v
+            on_tree(i, tree)
+        else:
+            res = gbm.softmax_residuals(scores, targets)
+            trees = []
+            for k in range(scores.shape[1]):
+                g = grower()
+                trees.append(g.grow(res[k], rows))
+                for rws, v in g.leaf_rows:
+                    scores[rws, k] = scores[rws, k] + lr * v
+            on_tree(i, trees)
+    return scores
+
+
+C3_KW = dict(num_bins=32, max_depth=5, learning_rate=0.01)
+
+
+@pytest.mark.parametrize("chunk", range(4))
+def test_c3_full_size_all_trees_identical(c3_fit, chunk):
+    """Trees 25*chunk .. 25*chunk + 24 against the oracle, grown from the
+    training scores of the GPU's trees before them."""
+    X, y, m, edges, codes = c3_fit
+    t0 = 25 * chunk
+    print_case("fullsize", "C3 trees", t0, "to", t0 + 24)
+    base = np.full(len(y), F32(m.base_prediction), F32)
+    start = base if t0 == 0 else clib.predict_tables(codes, _tables(m.forest[:t0], 5), 0.01, base)
+
+    def check(i, tree):
+        assert m.forest[t0 + i] == tree, f"tree {t0 + i} differs"
+        assert _leaf_rows(tree) == len(y)
+
+    _grow_chunk(codes, y, start, np.zeros(len(y), np.int64), 1, C3_KW, 25, check)
 
 
 def test_c3_full_size_predictions_bit_exact(c3_fit):
@@ -161,25 +217,105 @@ def test_c4_full_size_depth8_bit_exact(gpu):
     assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
 
 
-def test_c5_full_size_rounds_and_predict_proba_bit_exact(gpu):
-    print_case("fullsize", "C5 200k x 100, K=10, depth 6, 200 rounds")
+def test_c4_full_size_100_trees_against_digests(gpu):
+    """The benchmark's whole C4 forest: every tree's digest (structure,
+    features, bins, leaf counts, leaf value bits), the per-era importance and
+    the training predictions against the oracle's, committed as a fixture."""
+    import json
+    from pathlib import Path
+
+    from tests.golden.forest_digest import array_digest, tree_digest
+
+    print_case("fullsize", "C4 100 trees depth 8 against the oracle's digests")
+    fixture = Path(__file__).parent / "golden" / "c4_forest_digest.json"
+    if not fixture.exists():
+        pytest.skip("tests/golden/c4_forest_digest.json not generated "
+                    "(python tests/golden/make_c4_digest.py)")
+    ref = json.loads(fixture.read_text())
+    X, y, era = c4_inputs()
+    m = WarpGBM(num_bins=5, max_depth=8, n_estimators=100, learning_rate=0.1)
+    m.fit(X, y, era_id=era)
+    got = [tree_digest(t) for t in m.forest]
+    bad = [i for i, (a, b) in enumerate(zip(got, ref["trees"])) if a != b]
+    assert len(got) == len(ref["trees"]) == 100 and not bad, f"trees differ: {bad[:10]}"
+    assert array_digest(m.per_era_feature_importance_) == ref["per_era_importance"]
+    assert array_digest(m.predict(X)) == ref["train_preds"]
+
+
+def test_native_codes_beyond_2gib_bit_exact(gpu):
+    """2.2M x 1000 pre-binned codes: the native matrix (2.2M x 1024 bytes)
+    is past 2^31 bytes, so the histogram tile kernel loads codes with 64-bit
+    global addresses (kLoadGlobalAligned, 4 codes per lane) instead of 32-bit
+    buffer offsets; one tree of depth 3 against the oracle, and its training
+    predictions."""
+    print_case("fullsize", "2.2M x 1000 pre-binned, native codes beyond 2 GiB")
+    rng = np.random.default_rng(7)
+    N, F, B = 2_200_000, 1000, 32
+    X = rng.integers(0, B, (N, F), dtype=np.int8)
+    y = ((X[:, 3] > 15) + 0.5 * (X[:, 700] > 20) + 0.1 * rng.standard_normal(N)).astype(F32)
+    assert N * D.codes_stride(F) >= 2**31
+    kw = dict(num_bins=B, max_depth=3, n_estimators=1, learning_rate=0.5)
+    m = WarpGBM(**kw).fit(X, y)
+    ref = gbm.Forest(**kw).fit_codes(X, y, hist=clib.hist_exact_q, scan=clib.split_scan_q)
+    assert m.forest[0] == ref.forest[0]
+    assert str(ref.forest[0]).count("'feature'") == 7  # a full tree of depth 3
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
+    del X
+    torch.cuda.empty_cache()
+
+
+C5_KW = dict(objective="multiclass", num_bins=32, max_depth=6, learning_rate=0.1)
+
+
+@pytest.fixture(scope="module")
+def c5_fit(gpu):
+    print_case("fullsize", "C5 fit 200k x 100, K=10, depth 6, 200 rounds")
     X, lab = c5_inputs()
-    kw = dict(objective="multiclass", num_bins=32, max_depth=6, learning_rate=0.1)
-    m = WarpGBM(n_estimators=200, **kw).fit(X, lab)
+    m = WarpGBM(n_estimators=200, **C5_KW).fit(X, lab)
     edges = clib.quantile_edges_matrix(X, 32)
-    assert np.array_equal(bits(torch.as_tensor(m.bin_edges).cpu().numpy()), bits(edges))
     codes = clib.bin_matrix(X, edges)
+    return X, lab, m, edges, codes
+
+
+def test_c5_full_size_edges_and_codes(c5_fit):
+    X, lab, m, edges, codes = c5_fit
+    print_case("fullsize", "C5 edges, codes")
+    assert np.array_equal(bits(torch.as_tensor(m.bin_edges).cpu().numpy()), bits(edges))
     assert np.array_equal(_gpu_codes(m, X), codes)
-    ref = gbm.Forest(n_estimators=2, **kw).fit_codes(codes, lab, hist=clib.hist_exact_q,
-                                                     scan=clib.split_scan_q)
-    for i in range(2):
-        assert m.forest[i] == ref.forest[i], f"round {i} differs"
+
+
+def _class_tables(rounds):
+    trees = [t for rnd in rounds for t in rnd]
+    cls = np.tile(np.arange(10, dtype=np.int32), len(rounds))
+    return _tables(trees, 6), cls
+
+
+@pytest.mark.parametrize("chunk", range(4))
+def test_c5_full_size_all_rounds_identical(c5_fit, chunk):
+    """Rounds 50*chunk .. 50*chunk + 49 (10 class trees each) against the
+    oracle, grown from the training scores of the GPU's rounds before them
+    (the training priors, then every earlier tree in round and class order)."""
+    X, lab, m, edges, codes = c5_fit
+    r0 = 50 * chunk
+    print_case("fullsize", "C5 rounds", r0, "to", r0 + 49)
+    start = np.tile(gbm.class_prior_logits(lab, 10), (len(lab), 1)).astype(F32)
+    if r0:
+        tabs, cls = _class_tables(m.forest[:r0])
+        start = clib.predict_tables(codes, tabs, 0.1, start, cls)
+
+    def check(i, trees):
+        assert m.forest[r0 + i] == trees, f"round {r0 + i} differs"
+
+    _grow_chunk(codes, lab, start, np.zeros(len(lab), np.int64), 1, C5_KW, 50, check)
+
+
+def test_c5_full_size_predict_proba_bit_exact(c5_fit):
+    X, lab, m, edges, codes = c5_fit
     print_case("fullsize", "C5 predict_proba on 1M rows")
     Xt, lt = c5_inputs(rows_per_class=100_000, seed=1)
     got = m.predict_proba(Xt)
-    trees = [t for rnd in m.forest for t in rnd]
-    cls = np.tile(np.arange(10, dtype=np.int32), len(m.forest))
+    tabs, cls = _class_tables(m.forest)
     start = np.tile(gbm.uniform_prior_logits(10), (len(lt), 1))
-    logits = clib.predict_tables(clib.bin_matrix(Xt, edges), _tables(trees, 6), 0.1, start, cls)
+    logits = clib.predict_tables(clib.bin_matrix(Xt, edges), tabs, 0.1, start, cls)
     assert np.array_equal(bits(got), bits(clib.softmax_rows(logits)))
     assert (got.argmax(axis=1) == lt).mean() > 0.95

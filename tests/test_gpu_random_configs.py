@@ -5,9 +5,12 @@ recursive growth (warpgbm/core.py:597-658, 692-818).
 Each case draws its shape from its seed: rows (a few dozen to several
 thousand: partial position blocks, segments smaller and larger than a wave),
 features (1 to 300), bins (2 to 127), depth (1 to 7), eras (regression only),
-colsample_bytree, min_child_weight, float or pre-binned int8 input, and the
-objective (regression, or softmax with 3 classes).  Bar: identical tree
-dicts, bit-exact predictions and importances."""
+colsample_bytree, min_child_weight, min_split_gain (0, small, large: the
+engine's `crit > min_split_gain` masks, and the DES rule that a node whose
+max-agreement candidates all fail it is a leaf), L2_reg (0, the default,
+1), float or pre-binned int8 input, and the objective (regression, or
+softmax with 3 classes).  Bar: identical tree dicts, bit-exact predictions
+and importances."""
 import numpy as np
 import pytest
 
@@ -37,10 +40,15 @@ def draw_case(seed):
         prebinned=bool(rng.random() < 0.3),
     )
     c["E"] = int(rng.choice([1, 1, 3, 17])) if c["objective"] == "regression" else 1
+    # drawn from their own stream, so that the shapes above stay those of
+    # the first 48 seeds whatever is added here
+    knob = np.random.default_rng(5000 + seed)
+    c["msg"] = float(knob.choice([0.0, 0.0, 0.05, 5.0]))
+    c["l2"] = float(knob.choice([1e-6, 1e-6, 0.0, 1.0]))
     return c, rng
 
 
-CASES = list(range(48))
+CASES = list(range(64))
 
 
 @pytest.mark.parametrize("seed", CASES)
@@ -58,7 +66,8 @@ def test_random_config_bit_exact(gpu, seed):
         signal = signal + 0.5 * (X[:, 1].astype(np.float64) > 0)
     era = rng.integers(0, E, N).astype(np.int32) if E > 1 else None
     kw = dict(num_bins=B, max_depth=c["depth"], n_estimators=c["trees"], learning_rate=0.3,
-              min_child_weight=c["mcw"], colsample_bytree=c["colsample"])
+              min_child_weight=c["mcw"], colsample_bytree=c["colsample"],
+              min_split_gain=c["msg"], L2_reg=c["l2"])
     if c["objective"] == "regression":
         y = (signal + 0.3 * rng.standard_normal(N)).astype(F32)
         m = WarpGBM(random_state=seed, **kw).fit(X, y, era_id=era)
@@ -74,7 +83,7 @@ def test_random_config_bit_exact(gpu, seed):
         edges = ops.quantile_edges(X, B)
         codes = ops.bin_matrix(X, edges)
     ref_kw = dict(num_bins=B, max_depth=c["depth"], n_estimators=c["trees"], learning_rate=0.3,
-                  min_child_weight=c["mcw"])
+                  min_child_weight=c["mcw"], min_split_gain=c["msg"], L2_reg=c["l2"])
     if c["objective"] != "regression":
         ref_kw["objective"] = "multiclass"
     subsets = m.feature_subsets_ if c["colsample"] < 1.0 else None
@@ -86,7 +95,7 @@ def test_random_config_bit_exact(gpu, seed):
     # the comparison is not vacuous: some tree splits wherever the rows allow
     splits = sum(str(t).count("'feature'") for t in ref.forest)
     print("splits", splits, flush=True)
-    if N >= 700:
+    if N >= 700 and c["msg"] == 0.0:
         assert splits > 0
     assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
     if c["objective"] == "regression":
