@@ -264,10 +264,17 @@ def main():
     _lib.check(lib.wgbm_probe_lds_atomics(512, 500, C.byref(lds_peak), stream), "lds probe")
     lds_peak = lds_peak.value
     log(f"LDS atomic probe: {lds_peak:.3e} 64-bit adds/s")
+    # achievable HBM read rate: 16-byte streaming loads over the same codes
+    # buffer (N x S bytes), ten launches back to back
+    hbm_probe = C.c_double(0.0)
+    _lib.check(lib.wgbm_probe_hbm_read(codes.data_ptr(), N * S, 10, C.byref(hbm_probe), stream),
+               "hbm probe")
+    hbm_probe = hbm_probe.value / 1e9
+    log(f"HBM read probe: {hbm_probe:.1f} GB/s ({N * S} bytes, 16-byte loads)")
 
     dropin = None
     if not args.no_dropin:
-        dropin = dropin_leg(raw, grad, order16, seg16_h, N, F, B, dev)
+        dropin = {"compute_histogram3": dropin_leg(raw, grad, order16, seg16_h, N, F, B, dev)}
     del nat, codes, G16, H16, raw
     torch.cuda.empty_cache()
 
@@ -304,6 +311,8 @@ def main():
             torch.cuda.synchronize()
             runs.append((tr, time.perf_counter() - t0, p))
             mark(f"c3 end {run}")
+        if cpu is not None:
+            cpu.update(cpu_train_estimate("c3", X, y))
         del X, y
         (train_cold, infer_cold, _), (train_s, infer_s, p) = runs[0], runs[-1]
         corr = float(np.corrcoef(p, yt)[0, 1])
@@ -314,7 +323,7 @@ def main():
                              "(the first, *_cold_s, includes one-time setup)"}
         log(f"C3 train {train_s:.3f} s (first run {train_cold:.3f}), infer {infer_s:.3f} s "
             f"(first run {infer_cold:.3f}), corr {corr:.4f}")
-        e2e["kernels"] = c3_kernel_rooflines(m, Xt)
+        e2e["kernels"] = c3_kernel_rooflines(m, Xt, dropin)
         del Xt
 
     # HBM bytes per hist_tiles launch from the committed rocprofv3 PMC summary
@@ -353,6 +362,10 @@ def main():
                      # the binding unit in practice: one 64-bit LDS atomic per
                      # (row, feature); peak = wgbm_probe_lds_atomics, measured
                      # above on this GPU
+                     # the practical HBM ceiling: a pure 16-byte streaming read
+                     "hbm_read_probe": {"GB/s": round(hbm_probe, 1),
+                                        "frac_of_peak": round(hbm_probe / HBM_PEAK_GBS, 4),
+                                        "kernel_frac_of_probe": round(k_achieved / hbm_probe, 4)},
                      "lds_atomics": {"updates": N * F, "achieved_per_s": round(N * F / (k_ms * 1e-3)),
                                      "peak_per_s": round(lds_peak),
                                      "frac": round(N * F / (k_ms * 1e-3) / lds_peak, 4)}},
@@ -363,7 +376,7 @@ def main():
     if not args.no_extra:
         for cfg in ("c1", "c4", "c5"):
             if cfg in args.extra.split(","):
-                out.update(run_extra(cfg, args.runs))
+                out.update(run_extra(cfg, args.runs, cpu))
     write_marks()
     print(json.dumps(out))
 
@@ -408,7 +421,7 @@ def dropin_leg(raw, grad, order16, seg16_h, N, F, B, dev):
     gen = torch.Generator(device="cpu").manual_seed(7)
     choices = {"all": torch.arange(F, dtype=torch.int32),
                "half": torch.randperm(F, generator=gen, dtype=torch.int32)[:F // 2]}
-    out = {"op": "node_kernel.compute_histogram3", "calls_per_step": 17,
+    out = {"calls_per_step": 17,
            "pattern": "root (sample_indices = all rows) + one call per node, raw [N, F] int8 "
                       "codes, 1 era"}
     for name, fsel in choices.items():
@@ -499,7 +512,42 @@ def cpu_baseline_leg(codes_h, grad_h, order16_h, seg16_h, N, F, B, step_bytes, r
     return cpu
 
 
-def c3_kernel_rooflines(m, Xt):
+def cpu_train_estimate(cfg, X, y, era=None):
+    """The CPU oracle on an end-to-end config, per BASELINE.md's plan: the
+    one-time work (quantile edges and binning of the float32 matrix, none for
+    C4's pre-binned codes) timed once, plus ONE tree (C3, C4) or one round
+    of K class trees (C5) grown with the oracle's C loops on every OpenMP
+    thread; the whole fit is estimated as one-time + trees x that (labelled
+    as an estimate: the trees of a fit differ in size, the first is timed)."""
+    from oracle import clib, gbm
+
+    threads = clib.num_threads()
+    t0 = time.perf_counter()
+    if cfg == "c4":
+        codes, prep = X, 0.0
+        kw, n = dict(num_bins=5, max_depth=8, learning_rate=0.1), 100
+    else:
+        B = 32
+        edges = clib.quantile_edges_matrix(X, B)
+        codes = clib.bin_matrix(X, edges)
+        prep = time.perf_counter() - t0
+        kw, n = ((dict(num_bins=32, max_depth=5, learning_rate=0.01), 100) if cfg == "c3" else
+                 (dict(objective="multiclass", num_bins=32, max_depth=6, learning_rate=0.1), 200))
+    t1 = time.perf_counter()
+    gbm.Forest(n_estimators=1, **kw).fit_codes(codes, y, era_id=era, hist=clib.hist_exact_q,
+                                               scan=clib.split_scan_q)
+    one = time.perf_counter() - t1
+    unit = "round of 10 class trees" if cfg == "c5" else "tree"
+    log(f"cpu {cfg.upper()}: one-time {prep:.2f} s, one {unit} {one:.2f} s "
+        f"({threads} threads) -> estimated fit {prep + n * one:.1f} s")
+    return {f"{cfg}_train_est_s": round(prep + n * one, 2),
+            f"{cfg}_sample": f"{cfg.upper()} on the CPU oracle ({threads} threads): quantile edges + "
+                             f"binning {prep:.2f} s (timed once) + {n} x one {unit} "
+                             f"{one:.2f} s (the first {unit} of the fit, timed; the x{n} is an "
+                             f"estimate)"}
+
+
+def c3_kernel_rooflines(m, Xt, dropin=None):
     """Achieved HBM bandwidth of the other three operators on C3's held-out
     matrix (1M x 1000 float32, resident on the device): quantile edges,
     binning, and inference of the fitted 100 trees.  Each is timed with torch
@@ -540,6 +588,8 @@ def c3_kernel_rooflines(m, Xt):
     put("bin_matrix", timed(lambda: D.bin_matrix(Xd, edges, with_cm=False)),
         n * F * 4 + n * F + F * (B - 1) * 4, "X + codes (row-major) + edges")
     codes = D.bin_matrix(Xd, edges, with_cm=False)
+    if dropin is not None:
+        dropin.update(dropin_ops_leg(m, Xd, codes))
     del Xd
     feat, bin_, leaf, nt = m._cached_heap()
     pred = torch.zeros((n, 1), dtype=torch.float32, device=dev)
@@ -552,9 +602,185 @@ def c3_kernel_rooflines(m, Xt):
     return out
 
 
-def run_extra(cfg, n_runs=2):
+def dropin_ops_leg(m, Xd, codes):
+    """The other three reference-shaped ops of warpgbm.cuda.node_kernel, each
+    in the reference's own call pattern, timed like c3_kernel_rooflines
+    (median of 5 after a warm-up, torch events on the current stream), with
+    algorithmic bytes:
+    * compute_split (best_split_kernel.cu:61-88) at a C4 node's shape, E=500
+      eras x F=2000 features x B=5 bins: G and H read, per-era gain and
+      direction written (E*F*B*8 + E*F*(B-1)*8 bytes);
+    * predict_forest (predict.cu:48-76) of C3's 100 fitted trees as the
+      reference's flatten_tree tables ([100, 2^(depth+1), 6], core.py:917-932)
+      on C3's 1M held-out rows as raw [N, F] int8 codes (N*F + 8N bytes);
+    * custom_cuda_binner (binner.cu:27-52) once per feature column, as the
+      reference's quantile-binning loop calls it (core.py:527-537): F calls,
+      each on one resident contiguous float32 column of C3's held-out matrix
+      (N*F*4 + N*F bytes + edges)."""
+    import torch
+
+    from warpgbm_amd import node_kernel as nk
+
+    dev = torch.device("cuda:0")
+
+    def timed(fn):
+        fn()
+        ts = []
+        for _ in range(5):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return sorted(ts)[2]
+
+    out = {}
+
+    def put(name, ms, nbytes, shape):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 4), "bytes": int(nbytes), "GB/s": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "shape": shape}
+        log(f"drop-in {name} ({shape}): {ms:.3f} ms, {gbs:.0f} GB/s")
+
+    # compute_split at a C4 node: a real-looking histogram (counts of 500,000
+    # rows over 500 eras and 5 bins, residual sums)
+    E, F4, B4 = 500, 2000, 5
+    gen = torch.Generator(device="cpu").manual_seed(11)
+    Hh = torch.randint(0, 400, (E, F4, B4), generator=gen).float().to(dev)
+    Gh = (torch.randn((E, F4, B4), generator=gen) * Hh.cpu().sqrt()).to(dev)
+    gain = torch.empty((E, F4, B4 - 1), device=dev)
+    dirn = torch.empty_like(gain)
+    put("compute_split", timed(lambda: nk.compute_split(Gh, Hh, 0.0, 20.0, 1e-6, gain, dirn)),
+        E * F4 * B4 * 8 + E * F4 * (B4 - 1) * 8, "E=500 x F=2000 x B=5 (a C4 node)")
+    del Gh, Hh, gain, dirn
+
+    # predict_forest: the reference's flat tables of C3's forest
+    n, F = Xd.shape
+    M = 2 ** (m.max_depth + 1)
+    tt = torch.stack([m.flatten_tree(t, M) for t in m.forest]).to(dev)
+    raw = codes.rm[:, :F].contiguous()
+    pred = torch.zeros(n, device=dev)
+    put("predict_forest", timed(lambda: nk.predict_forest(raw, tt, m.learning_rate, pred)),
+        n * F + 8 * n, f"{len(m.forest)} trees x {M} nodes on {n}x{F} int8 codes")
+    del raw, pred
+
+    # custom_cuda_binner per column
+    XT = Xd.t().contiguous()
+    edges = torch.as_tensor(m.bin_edges).to(dev)
+    cols = torch.empty((F, n), dtype=torch.int8, device=dev)
+
+    def bin_loop():
+        for f in range(F):
+            nk.custom_cuda_binner(XT[f], edges[f], cols[f])
+
+    put("custom_cuda_binner", timed(bin_loop), n * F * 5 + F * (m.num_bins - 1) * 4,
+        f"{F} per-column calls of {n} values, {m.num_bins} bins")
+    del XT, cols
+    torch.cuda.empty_cache()
+    return out
+
+
+def des_level_rooflines(lib, X, y, era, trees=100):
+    """Achieved HBM bandwidth of the era path (DES) on C4, per depth: one
+    more 100-tree fit with the library's event timers on ("des_rows_L<d>":
+    the per-era gain kernel, pair codes or int8 codes; "des_sums_L<d>": era
+    sums, pick and finish), against algorithmic bytes counted from the
+    fitted forest by routing every row through each tree on the host:
+    * rows kernel: every row of a live (node, era) segment (one that can
+      hold a split: at least 2 x min_child_weight rows) read once -- its
+      codes (F/2 bytes as pair codes on the levels that use them, F bytes
+      as int8 codes) plus its row id and residual (8 bytes) -- and the
+      segment's gains and directions staged (5 bytes per candidate);
+    * sums: the staged values read once, each live 32-era block's float64
+      sums and direction counts written and read (12 bytes per candidate
+      each way), and per present node the criterion and agreement written
+      and read (16 bytes per candidate)."""
+    import torch
+
+    from warpgbm_amd import WarpGBM
+
+    kw = dict(num_bins=5, max_depth=8, n_estimators=trees, learning_rate=0.1)
+    lib.wgbm_timer_reset()
+    lib.wgbm_timer_enable(1)
+    m = WarpGBM(**kw).fit(X, y, era_id=era)
+    torch.cuda.synchronize()
+    lib.wgbm_timer_enable(0)
+    N, F = X.shape
+    B, D, mcw = m.num_bins, m.max_depth, float(m.min_child_weight)
+    eras = np.unique(era, return_inverse=True)[1].astype(np.int64)
+    E = int(eras.max()) + 1
+    W = (E + 31) // 32
+    ncand = F * (B - 1)
+    # the routing runs on the device with torch (bookkeeping for the byte
+    # counts, outside every timed region)
+    dev = torch.device("cuda:0")
+    feat, bin_, _, _ = m._cached_heap()
+    feat, bin_ = feat[:, 0].long(), bin_[:, 0].long()
+    Xd = torch.from_numpy(X).to(dev)
+    ed = torch.from_numpy(eras).to(dev)
+    rows_alive = np.zeros(D, np.int64)
+    segs_alive = np.zeros(D, np.int64)
+    blocks_live = np.zeros(D, np.int64)
+    present = np.zeros(D, np.int64)
+    for t in range(feat.shape[0]):
+        idx = torch.arange(N, device=dev)
+        h = torch.zeros(N, dtype=torch.long, device=dev)
+        for d in range(D):
+            base = (1 << d) - 1
+            key = (h - base) * E + ed[idx]
+            cnt = torch.bincount(key, minlength=(1 << d) * E).reshape(1 << d, E)
+            live = cnt >= 2.0 * mcw
+            pad = torch.zeros((1 << d, W * 32), dtype=torch.bool, device=dev)
+            pad[:, :E] = live
+            st = torch.stack([(cnt * live).sum(), live.sum(),
+                              pad.reshape(1 << d, W, 32).any(dim=2).sum(),
+                              (cnt.sum(dim=1) > 0).sum()]).cpu().numpy()
+            rows_alive[d] += int(st[0])
+            segs_alive[d] += int(st[1])
+            blocks_live[d] += int(st[2])
+            present[d] += int(st[3])
+            f = feat[t, h]
+            keep = f >= 0
+            idx, h, f = idx[keep], h[keep], f[keep]
+            right = Xd[idx, f].long() > bin_[t, h]
+            h = 2 * h + 1 + right.long()
+    del Xd, ed
+    levels = []
+    tot_ms = tot_bytes = 0.0
+    for d in range(D):
+        pairs = N >= 96 * (1 << d) * E  # the engine's pair-code rule (kDesPairMinRows)
+        rb = rows_alive[d] * ((F + 1) // 2 + 8 if pairs else F + 8) + segs_alive[d] * ncand * 5
+        sb = segs_alive[d] * ncand * 5 + blocks_live[d] * ncand * 24 + present[d] * ncand * 16
+        ent = {"depth": d, "codes": "pair" if pairs else "int8"}
+        for name, nbytes in (("rows", rb), ("sums", sb)):
+            tot = C.c_double()
+            cnt = C.c_int64()
+            lib.wgbm_timer_read(f"des_{name}_L{d}".encode(), C.byref(tot), C.byref(cnt))
+            ms = tot.value
+            gbs = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+            ent[name] = {"ms": round(ms, 3), "bytes": int(nbytes), "GB/s": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": int(cnt.value)}
+            tot_ms += ms
+            tot_bytes += nbytes
+        levels.append(ent)
+        log(f"C4 DES depth {d} ({ent['codes']}): rows {ent['rows']['ms']:.2f} ms "
+            f"{ent['rows']['GB/s']:.0f} GB/s, sums {ent['sums']['ms']:.2f} ms "
+            f"{ent['sums']['GB/s']:.0f} GB/s")
+    gbs = tot_bytes / (tot_ms * 1e-3) / 1e9
+    log(f"C4 DES total {tot_ms:.1f} ms for {trees} trees, {gbs:.0f} GB/s")
+    return {"ms": round(tot_ms, 2), "bytes": int(tot_bytes), "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "trees": trees, "levels": levels,
+            "bytes_are": "per depth, summed over the trees: live (node, era) segments' rows "
+                         "(codes + row id + residual) and staged per-era gains (rows); staged "
+                         "gains read, 32-era block sums written and read, per-node criteria "
+                         "(sums); timed with HIP events around the launches"}
+
+
+def run_extra(cfg, n_runs=2, cpu=None):
     """End-to-end seconds of configs C1 (fit only), C4 (era-aware DES) and C5
-    (softmax)."""
+    (softmax); with a cpu_baseline dict, the CPU oracle's estimate of the same
+    fit is added to it."""
     import torch
 
     from warpgbm_amd import WarpGBM
@@ -591,11 +817,15 @@ def run_extra(cfg, n_runs=2):
             mark(f"c4 end {run}")
         (tr0, inf0, _), (tr, inf, p) = runs[0], runs[-1]
         corr = float(np.corrcoef(p, y)[0, 1])
+        if cpu is not None:
+            cpu.update(cpu_train_estimate("c4", X, y, era))
+        from warpgbm_amd import _lib
+        des = des_level_rooflines(_lib.load(), X, y, era)
         print(f"[bench] C4 train {tr:.3f} s (first run {tr0:.3f}), infer {inf:.3f} s "
               f"(first run {inf0:.3f}), in-sample corr {corr:.4f}", file=sys.stderr, flush=True)
         return {"c4_train_s": round(tr, 3), "c4_infer_s": round(inf, 3),
                 "c4_train_cold_s": round(tr0, 3), "c4_infer_cold_s": round(inf0, 3),
-                "c4_corr": round(corr, 4)}
+                "c4_corr": round(corr, 4), "c4_des": des}
     if cfg == "c5":
         print("[bench] generating C5 inputs", file=sys.stderr, flush=True)
         X, lab = c5_inputs()
@@ -617,6 +847,8 @@ def run_extra(cfg, n_runs=2):
             mark(f"c5 end {run}")
         (tr0, inf0, _), (tr, inf, proba) = runs[0], runs[-1]
         acc = float((np.argmax(proba, axis=1) == labt).mean())
+        if cpu is not None:
+            cpu.update(cpu_train_estimate("c5", X, lab))
         print(f"[bench] C5 train {tr:.3f} s (first run {tr0:.3f}), predict_proba {inf:.3f} s "
               f"(first run {inf0:.3f}), acc {acc:.4f}", file=sys.stderr, flush=True)
         return {"c5_train_s": round(tr, 3), "c5_infer_s": round(inf, 3),

@@ -264,7 +264,9 @@ void wgbm_engine_destroy(wgbm_engine* eng);
 
 /* ------------------------------------------------------------------------
  * Instrumentation: HIP-event timing of selected kernels (tags
- * "hist_tiles", "engine_hist_tiles").  mode 0 off; 1: events recorded on the
+ * "hist_tiles", "engine_hist_tiles"; in mode 1 also the engine's era path
+ * per depth d: "des_rows_L<d>", the per-era gain kernel, and "des_sums_L<d>",
+ * the era sums, pick and finish).  mode 0 off; 1: events recorded on the
  * kernel's stream right before and after its launch; 2: events attached to
  * the kernel's dispatch (hipExtLaunchKernel).  Reading synchronises the
  * events.
@@ -276,6 +278,13 @@ void wgbm_timer_reset(void);
  * histogram's LDS layout with synthetic bins and no global traffic: the
  * ceiling of the histogram kernel's LDS stage.  Synchronises `stream`. */
 int wgbm_probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, void* stream);
+/* Achievable HBM read rate (bytes per second, whole GPU): `iters` launches
+ * that each stream the device buffer `buf` (16-byte aligned, `bytes` long;
+ * the last bytes % 16 are not read) once with 16-byte loads and no other
+ * memory traffic: the practical ceiling of a read-bound kernel.  No
+ * counterpart in the reference.  Synchronises `stream`. */
+int wgbm_probe_hbm_read(const void* buf, int64_t bytes, int32_t iters, double* bytes_per_s,
+                        void* stream);
 /* Free the library's scratch buffers (all devices / streams). */
 void wgbm_release_scratch(void);
 

@@ -126,6 +126,27 @@ def test_heap_dict_round_trip_and_preorder():
     assert _heaps_to_dicts(fs, bs, vs, cs) == [tree, second, None, tree]
 
 
+def test_heap_of_tensor_features():
+    """Trees the reference's fit wrote hold a split's feature as a 0-d int64
+    tensor (warpgbm/core.py:653-654): the heap tables and the flat predict
+    table take them as the integers they hold."""
+    import torch
+
+    plain = {"feature": 7, "bin": 2,
+             "left": {"leaf_value": 0.5, "samples": 3},
+             "right": {"feature": 1, "bin": 0, "left": {"leaf_value": -1.0, "samples": 2},
+                       "right": {"leaf_value": 2.5, "samples": 1}}}
+    tens = {"feature": torch.tensor(7), "bin": 2,
+            "left": {"leaf_value": 0.5, "samples": 3},
+            "right": {"feature": torch.tensor(1), "bin": 0,
+                      "left": {"leaf_value": -1.0, "samples": 2},
+                      "right": {"leaf_value": 2.5, "samples": 1}}}
+    for a, b in zip(_dict_to_heap(tens, 7), _dict_to_heap(plain, 7)):
+        assert np.array_equal(a, b)
+    fa, fb = WarpGBM().flatten_tree(tens, 8), WarpGBM().flatten_tree(plain, 8)
+    assert torch.allclose(fa, fb, rtol=0, atol=0, equal_nan=True)
+
+
 def test_flatten_tree_matches_reference_layout():
     tree = {"feature": 3, "bin": 5, "left": {"leaf_value": 1.5, "samples": 2},
             "right": {"feature": 0, "bin": 1, "left": {"leaf_value": 0.5, "samples": 1},

@@ -197,6 +197,36 @@ def test_era_des_colsample_uneven_eras_bit_exact(gpu, mcw, B, layout):
     assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
 
 
+@pytest.mark.parametrize("E,B", [(3, 2), (70, 5), (40, 7), (33, 8), (5, 16)])
+def test_era_des_bins_and_blocks_bit_exact(gpu, E, B):
+    """The era path (pair codes for num_bins <= 7, int8 codes above) against
+    the oracle: uneven era sizes (empty, tiny and dead eras, more than one
+    32-era block), more than one feature chunk, a feature subset,
+    min_split_gain > 0 and negative codes."""
+    print_case("estimator", "DES bins / blocks E B", E, B)
+    rng = np.random.default_rng(40 + E + B)
+    F = 300 if B < 8 else 150
+    sizes = rng.integers(0, 200, E)
+    sizes[0] = 1
+    N = int(sizes.sum())
+    era = np.repeat(np.arange(E), sizes)
+    X = rng.integers(0, B, (N, F)).astype(np.int8)
+    X[rng.random((N, F)) < 0.01] = -1  # outside [0, num_bins): no bin (still pre-binned)
+    flip = np.where(rng.random(E) < 0.5, -1.0, 1.0)
+    score = ((X[:, :6].astype(np.float64) - B / 2).sum(axis=1)
+             + flip[era] * (X[:, 6] - B / 2) + rng.standard_normal(N))
+    y = (score / 4.0).astype(F32)
+    kw = dict(num_bins=B, max_depth=5, n_estimators=3, learning_rate=0.4, min_child_weight=4,
+              min_split_gain=0.01)
+    m = WarpGBM(colsample_bytree=0.7, random_state=5, **kw).fit(X, y, era_id=era)
+    ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era, feat_sets=m.feature_subsets_)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs from the oracle"
+    assert sum(str(t).count("'feature'") for t in m.forest) > 0
+    assert np.array_equal(bits(m.per_era_feature_importance_), bits(ref.imp))
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
+
+
 def test_era_des_many_eras_blocks_bit_exact(gpu):
     """More eras than one 32-era block of the DES era sum (70 ids: two full
     blocks and a partial one), uneven sizes with tiny eras, an id with no

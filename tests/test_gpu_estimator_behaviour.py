@@ -228,3 +228,58 @@ def test_constant_target_grows_no_splits(gpu, value):
     assert np.float32(m.base_prediction) == np.float32(value)
     assert np.array_equal(bits(m.predict(X)), bits(np.full(len(X), value, F32)))
     assert float(np.sum(m.get_feature_importance(normalize=False))) == 0.0
+
+
+def _as_reference_forest(forest, dev):
+    """The forest as the reference's fit leaves it: a split's "feature" is
+    feat_indices_tree[local_feature], a 0-d int64 tensor on the device
+    (warpgbm/core.py:653-654); "bin" and the leaf values are Python numbers
+    (.item(), core.py:590-594, 606)."""
+    import torch
+
+    def conv(node):
+        if "leaf_value" in node:
+            return dict(node)
+        return {"feature": torch.tensor(int(node["feature"]), dtype=torch.int64, device=dev),
+                "bin": node["bin"], "left": conv(node["left"]), "right": conv(node["right"])}
+
+    return [[conv(t) for t in r] if isinstance(r, list) else conv(r) for r in forest]
+
+
+@pytest.mark.parametrize("objective", ["regression", "multiclass"])
+def test_load_reference_written_pickle(gpu, tmp_path, objective):
+    """A pickle in the reference's save_model layout (warpgbm/core.py:1122-1153)
+    whose trees hold device-tensor features and whose bin_edges is a device
+    tensor loads through load_model and predicts exactly as the model it was
+    made from."""
+    import pickle
+
+    import torch
+
+    print_case("behaviour", "reference-written pickle", objective)
+    dev = torch.device("cuda:0")
+    if objective == "regression":
+        X, y = c1_data(n=3000, f=12, seed=31)
+        m = WarpGBM(num_bins=16, max_depth=3, n_estimators=8).fit(X, y)
+    else:
+        X, labels = blobs(2000, 6, 3, seed=32)
+        m = WarpGBM(objective="multiclass", num_bins=16, max_depth=3, n_estimators=5,
+                    learning_rate=0.3, min_child_weight=5).fit(X, labels)
+    path = tmp_path / "ref.pkl"
+    m.save_model(str(path))
+    with open(path, "rb") as f:
+        state = pickle.load(f)  # written by this test just above
+    state["forest"] = _as_reference_forest(m.forest, dev)
+    state["bin_edges"] = torch.as_tensor(m.bin_edges).to(dev)
+    with open(path, "wb") as f:
+        pickle.dump(state, f)
+    loaded = WarpGBM().load_model(str(path))
+    if objective == "regression":
+        assert np.array_equal(bits(loaded.predict(X)), bits(m.predict(X)))
+    else:
+        assert np.array_equal(bits(loaded.predict_proba(X)), bits(m.predict_proba(X)))
+        assert (loaded.predict(X) == m.predict(X)).all()
+    # the reference's flat predict table of a loaded tree equals the original's
+    first = (lambda mm: mm.forest[0][0] if objective == "multiclass" else mm.forest[0])
+    a, b = loaded.flatten_tree(first(loaded), 64), m.flatten_tree(first(m), 64)
+    assert torch.allclose(a, b, rtol=0, atol=0, equal_nan=True)

@@ -50,6 +50,7 @@ SIGNATURES = {
     "wgbm_timer_read": (C.c_int, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(_i64)]),
     "wgbm_timer_reset": (None, []),
     "wgbm_probe_lds_atomics": (C.c_int, [_i32, _i32, C.POINTER(C.c_double), _p]),
+    "wgbm_probe_hbm_read": (C.c_int, [_p, _i64, _i32, C.POINTER(C.c_double), _p]),
     "wgbm_release_scratch": (None, []),
 }
 

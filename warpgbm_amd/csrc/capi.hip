@@ -24,6 +24,15 @@ int wgbm_probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, voi
   return probe_lds_atomics(blocks, iters, ops_per_s, S(stream));
 }
 
+int wgbm_probe_hbm_read(const void* buf, int64_t bytes, int32_t iters, double* bytes_per_s,
+                        void* stream) {
+  WGBM_REQUIRE(buf && bytes >= 16 && ((uintptr_t)buf & 15) == 0 && iters >= 1 && iters <= 1000 &&
+                   bytes_per_s,
+               "probe_hbm_read: bad arguments (buffer %p, %lld bytes, %d iterations)", buf,
+               (long long)bytes, iters);
+  return probe_hbm_read(buf, bytes, iters, bytes_per_s, S(stream));
+}
+
 const char* wgbm_version(void) { return "warpgbm_amd 0.1.0 (gfx950)"; }
 const char* wgbm_last_error(void) { return wgbm_last_error_impl(); }
 

@@ -12,6 +12,8 @@
 //   for depth d: histograms of the smaller children (+ siblings by
 //   subtraction; both children when one takes a finer histogram shift) ->
 //   split/DES -> leaf values + record -> partition.
+#include <stdio.h>
+
 #include <algorithm>
 #include <vector>
 
@@ -512,11 +514,25 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         // nodes [c0, c0 + nc): every node-indexed argument starts at c0
         const int nc = (int)std::min<int64_t>(e->nc_max, n_tn - c0);
         const int64_t k0 = (int64_t)c0 * E;
+        // optional event timers (wgbm_timer_enable(1)): the per-era kernel of
+        // the level ("des_rows_L<d>") and the era sums, pick and finish
+        // ("des_sums_L<d>")
+        char tag[32];
+        snprintf(tag, sizeof tag, "des_rows_L%d", d);
+        void* tm = timer_mode() == 1 ? timer_begin(tag) : nullptr;
+        if (tm) WGBM_CHECK(hipEventRecord(timer_start_event(tm), st));
         int r = launch_des_era(e->V, B, nc * E, st, c.codes_rm, c.stride, F, e->rpos[cur],
                                e->node_shift[cur] + k0, e->order[cur], e->seg[cur] + k0, E, nodes,
                                e->present[cur] + c0, e->local_of, n_sel, mcw, eps, e->sgain,
                                e->sdir, use_pairs ? e->pcodes : nullptr, N, e->pstride);
         if (r) return r;
+        if (tm) {
+          WGBM_CHECK(hipEventRecord(timer_stop_event(tm), st));
+          timer_end(tm);
+          snprintf(tag, sizeof tag, "des_sums_L%d", d);
+          tm = timer_begin(tag);
+          if (tm) WGBM_CHECK(hipEventRecord(timer_start_event(tm), st));
+        }
         if (!(alive_ready && nc == n_tn)) {
           hipLaunchKernelGGL(des_alive_kernel, dim3(blocks_for((int64_t)nc * W, 256)), dim3(256),
                              0, st, e->seg[cur] + k0, E, nc, mcw, e->alive);
@@ -540,6 +556,10 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                            e->sgain, e->seg[cur] + k0, n_sel, e->split_l + c0, e->split_b + c0,
                            e->split_gain + k0);
         WGBM_LAUNCH_CHECK();
+        if (tm) {
+          WGBM_CHECK(hipEventRecord(timer_stop_event(tm), st));
+          timer_end(tm);
+        }
       }
     } else if (d < D) {
       // ---- histograms of the computed segments, then split search + DES

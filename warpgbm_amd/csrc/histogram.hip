@@ -1102,6 +1102,63 @@ int probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, hipStrea
 }
 
 // --------------------------------------------------------------------------
+// instrumentation: the achievable HBM read rate.  Every lane streams 16-byte
+// loads over a caller's buffer (grid-stride, four loads in flight per lane,
+// non-temporal like the histogram's code loads) and folds them into one
+// word per lane, stored to a per-workgroup sink so the loads stay live.
+// The buffer is read whole once per launch; nothing else touches memory.
+// --------------------------------------------------------------------------
+typedef uint32_t wgbm_u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void hbm_read_probe_kernel(const wgbm_u32x4* __restrict__ src,
+                                                             int64_t n16,
+                                                             uint32_t* __restrict__ sink) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    wgbm_u32x4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = __builtin_nontemporal_load(src + i + k * stride);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+  }
+  for (; i < n16; i += stride) {
+    const wgbm_u32x4 v = __builtin_nontemporal_load(src + i);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  sink[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
+int probe_hbm_read(const void* buf, int64_t bytes, int32_t iters, double* bytes_per_s,
+                   hipStream_t st) {
+  const int64_t n16 = bytes / 16;
+  constexpr int kBlocks = 2048;  // 8 workgroups of 256 lanes per CU
+  uint32_t* sink = (uint32_t*)scratch_get(st, sizeof(uint32_t) * kBlocks * 256, 9);
+  WGBM_REQUIRE(sink, "scratch allocation failed");
+  hipEvent_t a, b;
+  WGBM_CHECK(hipEventCreate(&a));
+  WGBM_CHECK(hipEventCreate(&b));
+  // one untimed launch, then `iters` timed ones back to back
+  hipLaunchKernelGGL(hbm_read_probe_kernel, dim3(kBlocks), dim3(256), 0, st,
+                     (const wgbm_u32x4*)buf, n16, sink);
+  WGBM_LAUNCH_CHECK();
+  WGBM_CHECK(hipEventRecord(a, st));
+  for (int it = 0; it < iters; ++it) {
+    hipLaunchKernelGGL(hbm_read_probe_kernel, dim3(kBlocks), dim3(256), 0, st,
+                       (const wgbm_u32x4*)buf, n16, sink);
+    WGBM_LAUNCH_CHECK();
+  }
+  WGBM_CHECK(hipEventRecord(b, st));
+  WGBM_CHECK(hipEventSynchronize(b));
+  float ms = 0.0f;
+  WGBM_CHECK(hipEventElapsedTime(&ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  *bytes_per_s = (double)n16 * 16.0 * iters / (ms * 1e-3);
+  return 0;
+}
+
+// --------------------------------------------------------------------------
 // finalize launchers: words per workgroup from the expected tiles per segment
 // --------------------------------------------------------------------------
 int fin_words_for(int64_t tiles_per_key) {

@@ -134,6 +134,8 @@ bool hist_native_ok(int num_bins);
 int hist_load_mode(int64_t n_rows, int64_t stride, int V);
 int launch_hist_tiles(const HistLaunch& a, hipStream_t st);
 int probe_lds_atomics(int32_t blocks, int32_t iters, double* ops_per_s, hipStream_t st);
+int probe_hbm_read(const void* buf, int64_t bytes, int32_t iters, double* bytes_per_s,
+                   hipStream_t st);
 
 // kernels launched directly from other translation units
 // absmax_bits: the call's largest |residual| (float bits; key_stride 0), or

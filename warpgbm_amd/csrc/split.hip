@@ -607,7 +607,13 @@ void des_pair_kernel(
               i0 + u < n ? (unsigned long long)(qr * (int64_t)(1 << WGBM_CBITS) + 1) : 0ull;
 #pragma unroll
           for (int p = 0; p < LP; ++p) {
-            const uint32_t idx = (g.c[u] >> (8 * p)) & 0xffu;
+            // the pair code is at most P - 1 already (pack_pairs_kernel clamps
+            // each code): for the low byte the min lets the byte select be one
+            // SDWA instruction, the top byte of the 16-bit load is one byte
+            // permute; either way one more instruction adds shift and lane
+            static_assert(LP == 2, "one 16-bit code load per row and lane");
+            const uint32_t idx = p == 0 ? min(g.c[u] & 0xffu, (uint32_t)(P - 1))
+                                        : __builtin_amdgcn_perm(0u, g.c[u], 0x0c0c0c01u);
             const uint32_t addr = (idx << 9) + lbase + (uint32_t)(p * P * kHistSlots * 8);
             atomicAdd(
                 reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(lds) + addr), w);
