@@ -20,10 +20,14 @@ Metric: histogram GB/s (% HBM peak) + train/infer seconds,
   (ms_per_step_no_events): each event pair adds that dispatch time again.
 * cpu_baseline: the CPU oracle (C loops on all OpenMP threads) running the
   same C2 step, 1 warm-up then the median of 5; plus C1 end to end (quantile
-  edges, binning, 20 trees) on the CPU, median of 3.
-* dropin: the reference-shaped op, node_kernel.compute_histogram3, on C2 in
-  the reference's call pattern (root with sample_indices = all rows, then one
-  call per node with that node's rows), raw [N, F] int8 codes.
+  edges, binning, 20 trees) on the CPU, median of 3; and estimates of the
+  C3, C4 and C5 fits (edges + binning timed, one tree or round timed, times
+  the trees or rounds of the config).
+* dropin: the reference-shaped ops of node_kernel in the reference's call
+  patterns: compute_histogram3 on C2 (root with sample_indices = all rows,
+  then one call per node with that node's rows, raw [N, F] int8 codes);
+  compute_split at a C4 node's shape; predict_forest of C3's 100 trees as
+  flatten_tree tables; custom_cuda_binner once per C3 column.
 * train_s / infer_s: end-to-end fit / predict wall seconds on config C3
   (1M x 1000 float32 features, 100 trees, depth 5, 32 bins, lr 0.01; predict
   on 1M held-out rows), including host->device copies and binning; C4 (era
@@ -32,8 +36,15 @@ Metric: histogram GB/s (% HBM peak) + train/infer seconds,
   C3's held-out matrix resident on the device (algorithmic bytes / median
   call time).
 
+* c4_des: the era path (DES) on C4 per depth: per-era gain kernel ("rows")
+  and era sums + pick ("sums"), HIP-event times against algorithmic bytes
+  counted from the fitted forest.
+* roofline.hbm_read_probe: a pure 16-byte streaming read of the C2 codes
+  buffer, the practical HBM ceiling of a read-bound kernel on this GPU.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-ms MS]
                        [--no-e2e] [--no-cpu] [--no-extra] [--no-dropin]
+                       [--only-extra --extra c4 --c4-trees T]   (profiling driver)
 """
 from __future__ import annotations
 
@@ -145,6 +156,11 @@ def main():
     ap.add_argument("--no-dropin", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates HBM byte counters)")
+    ap.add_argument("--only-extra", action="store_true",
+                    help="run only the --extra configs (no C2 step, probes, drop-in, CPU or C3): "
+                         "a short driver for profiling those fits")
+    ap.add_argument("--c4-trees", type=int, default=100,
+                    help="trees of the C4 fits (100 is the config; fewer for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -166,6 +182,14 @@ def main():
         torch.cuda.synchronize()
         del src, dst
         torch.cuda.empty_cache()
+    if args.only_extra:
+        out = {"metric": "end-to-end fits of the --extra configs only (a profiling driver)",
+               "config": {"workload": args.extra, "c4_trees": args.c4_trees}}
+        for cfg in ("c1", "c4", "c5"):
+            if cfg in args.extra.split(","):
+                out.update(run_extra(cfg, args.runs, None, args.c4_trees))
+        print(json.dumps(out))
+        return
     N, F, B = args.rows, args.feats, 32
     log(f"generating C2 inputs {N}x{F}")
     codes_h, grad_h, node_h = c2_inputs(N, F)
@@ -376,7 +400,7 @@ def main():
     if not args.no_extra:
         for cfg in ("c1", "c4", "c5"):
             if cfg in args.extra.split(","):
-                out.update(run_extra(cfg, args.runs, cpu))
+                out.update(run_extra(cfg, args.runs, cpu, args.c4_trees))
     write_marks()
     print(json.dumps(out))
 
@@ -777,7 +801,7 @@ def des_level_rooflines(lib, X, y, era, trees=100):
                          "(sums); timed with HIP events around the launches"}
 
 
-def run_extra(cfg, n_runs=2, cpu=None):
+def run_extra(cfg, n_runs=2, cpu=None, c4_trees=100):
     """End-to-end seconds of configs C1 (fit only), C4 (era-aware DES) and C5
     (softmax); with a cpu_baseline dict, the CPU oracle's estimate of the same
     fit is added to it."""
@@ -803,7 +827,7 @@ def run_extra(cfg, n_runs=2, cpu=None):
         X, y, era = c4_inputs()
         runs = []
         for run in range(n_runs):  # the second run is the steady state (see the C3 leg)
-            m = WarpGBM(num_bins=5, max_depth=8, n_estimators=100, learning_rate=0.1)
+            m = WarpGBM(num_bins=5, max_depth=8, n_estimators=c4_trees, learning_rate=0.1)
             torch.cuda.synchronize()
             mark(f"c4 fit {run}")
             t0 = time.perf_counter()
@@ -820,7 +844,7 @@ def run_extra(cfg, n_runs=2, cpu=None):
         if cpu is not None:
             cpu.update(cpu_train_estimate("c4", X, y, era))
         from warpgbm_amd import _lib
-        des = des_level_rooflines(_lib.load(), X, y, era)
+        des = des_level_rooflines(_lib.load(), X, y, era, c4_trees)
         print(f"[bench] C4 train {tr:.3f} s (first run {tr0:.3f}), infer {inf:.3f} s "
               f"(first run {inf0:.3f}), in-sample corr {corr:.4f}", file=sys.stderr, flush=True)
         return {"c4_train_s": round(tr, 3), "c4_infer_s": round(inf, 3),
