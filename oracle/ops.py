@@ -405,7 +405,10 @@ def flatten_tree(tree, max_nodes: int) -> np.ndarray:
 
 def predict_table(codes, table, lr, out):
     """warpgbm/cuda/predict.cu:23-44 with the trees added in tree order:
-    out[i] = out[i] + float32(lr * leaf_t), t = 0..T-1.  Returns a new array."""
+    out[i] = out[i] + float32(lr * leaf_t), t = 0..T-1.  Returns a new array.
+    A walk that would leave the table -- a split feature outside [0, F), a
+    child index outside [0, M), or more than M steps -- contributes NaN (the
+    reference reads out of bounds there; this build's kernels define NaN)."""
     codes = np.asarray(codes)
     table = np.asarray(table, dtype=F32)
     out = np.array(out, dtype=F32, copy=True)
@@ -428,8 +431,10 @@ def predict_table(codes, table, lr, out):
             nd_act = np.where(active[:, None], nd, F32(0))
             feat = nd_act[:, 0].astype(np.int64)
             sb = nd_act[:, 1].astype(np.int64)
+            active &= (feat >= 0) & (feat < codes.shape[1])  # leaves the row: NaN
             c = codes[np.arange(N), np.clip(feat, 0, codes.shape[1] - 1)].astype(np.int64)
             nxt = np.where(c <= sb, nd_act[:, 2], nd_act[:, 3]).astype(np.int64)
+            active &= (nxt >= 0) & (nxt < M)  # leaves the table: NaN
             node = np.where(active, nxt, node)
         out = out + lr * leafv
     return out.astype(F32)

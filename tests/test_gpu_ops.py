@@ -279,6 +279,70 @@ def test_predict_forest_bit_exact(gpu):
     assert np.array_equal(bits(out.cpu().numpy()), bits(ref))
 
 
+def _chain_tree(rng, depth, F, B):
+    """A split at every level down one side: depth `depth` in 2*depth + 1 nodes."""
+    if depth == 0:
+        return {"leaf_value": float(F32(rng.standard_normal())), "samples": 1}
+    return {"feature": int(rng.integers(F)), "bin": int(rng.integers(0, B)),
+            "left": {"leaf_value": float(F32(rng.standard_normal())), "samples": 1},
+            "right": _chain_tree(rng, depth - 1, F, B)}
+
+
+@pytest.mark.parametrize("case", ["plain", "big_bins", "bad_nodes", "deep", "neg_bin", "few"])
+def test_predict_forest_heap_path_bit_exact(gpu, case):
+    """predict_forest with enough trees and rows takes the heap path (flat
+    tables -> heap tables, a native copy of the codes, the LDS predictors);
+    tables it cannot hold fall back to the flat walk on the device.  Every
+    case against the oracle's flat walk (warpgbm/cuda/predict.cu:13-44):
+    * plain: depth-5 trees in 64-slot tables, codes -128..127 (negative codes
+      go left at every split, 127 right at every bin <= 126);
+    * big_bins: split bins 127..300 (every int8 code goes left);
+    * bad_nodes: features outside [0, F) and child indices outside [0, M)
+      (the flat walk's NaN), which the heap holds as NaN leaves;
+    * deep: one tree deeper than its table's heap (fallback);
+    * neg_bin: a negative split bin (fallback);
+    * few: fewer trees than the heap path takes (the flat walk alone)."""
+    print_case("predict_forest heap path", case)
+    rng = np.random.default_rng(20 + len(case))
+    N, F, B, D_ = 9000, 300, 32, 5
+    M = 2 ** (D_ + 1)
+    codes = rng.integers(-3, B + 2, (N, F)).astype(np.int8)
+    codes[rng.random((N, F)) < 0.01] = 127
+    codes[rng.random((N, F)) < 0.01] = -128
+    T = 3 if case == "few" else 40
+    trees = [_random_tree(rng, 0, D_, F, B) for _ in range(T)]
+    for tr in trees:  # bins in [0, B): _random_tree draws -1 too
+        stack = [tr]
+        while stack:
+            nd = stack.pop()
+            if "feature" in nd:
+                nd["bin"] = max(nd["bin"], 0)
+                stack += [nd["left"], nd["right"]]
+    if case == "deep":
+        trees[7] = _chain_tree(rng, D_ + 3, F, B)
+    table = np.stack([ops.flatten_tree(tr, M) for tr in trees])
+    splits = np.argwhere(table[:, :, 4] == 0)
+    if case == "big_bins":
+        pick = splits[rng.random(len(splits)) < 0.2]
+        table[pick[:, 0], pick[:, 1], 1] = rng.integers(127, 301, len(pick))
+    if case == "bad_nodes":
+        pick = splits[rng.random(len(splits)) < 0.05]
+        table[pick[:, 0], pick[:, 1], 0] = F + 5
+        pick = splits[rng.random(len(splits)) < 0.05]
+        table[pick[:, 0], pick[:, 1], 2] = M + 3
+        pick = splits[rng.random(len(splits)) < 0.05]
+        table[pick[:, 0], pick[:, 1], 3] = -1
+    if case == "neg_bin":
+        table[splits[0][0], splits[0][1], 1] = -1
+    out = torch.full((N,), 0.25, device=dev)
+    node_kernel.predict_forest(t(codes), t(table), 0.1, out)
+    ref = ops.predict_table(codes, table, 0.1, np.full(N, F32(0.25)))
+    got = out.cpu().numpy()
+    assert np.array_equal(bits(got), bits(ref))
+    if case == "bad_nodes":
+        assert np.isnan(ref).any()
+
+
 def _random_heap(rng, R, K, depth, F, B):
     """R rounds x K heap-ordered trees (node h: children 2h+1, 2h+2; feat -1
     = leaf) of depth <= ``depth``, with garbage below every leaf (the

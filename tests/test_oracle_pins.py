@@ -478,6 +478,31 @@ def test_predict_stump_closed_form():
     assert got.tolist() == [-1.0, -1.0, 2.5, 2.5]
 
 
+def test_predict_table_malformed_walks_are_nan():
+    """Known answers of the NaN rule: a split on a feature outside [0, F), an
+    edge to a child outside [0, M), and a cycle (more than M steps) give NaN
+    for the rows that take them and leave the other rows' values alone."""
+    codes = np.array([[0, 0], [5, 0], [5, 9], [0, 9]], np.int8)
+    nan = np.nan
+    #        feature bin left right leaf value
+    table = np.array([[[0, 3, 1, 2, 0, nan],      # node 0: code0 <= 3 -> 1 else 2
+                       [7, 0, 3, 3, 0, nan],      # node 1: feature 7 >= F=2 -> NaN
+                       [1, 4, 3, 9, 0, nan],      # node 2: code1 <= 4 -> 3 else child 9 >= M
+                       [0, 0, 0, 0, 1, 1.5]],     # node 3: leaf 1.5
+                      [[1, 4, 1, 2, 0, nan],      # tree 2, node 0: code1 <= 4 -> 1 else 2
+                       [0, 9, 0, 0, 0, nan],      # node 1: back to 0 forever (cycle)
+                       [0, 0, 0, 0, 1, -2.0],     # node 2: leaf -2
+                       [0, 0, 0, 0, 1, 0.0]]], F32)
+    got = ops.predict_table(codes, table, 1.0, np.zeros(4, F32))
+    # row 0: tree 1 -> node 1 (NaN); row 1: node 2 -> node 3: 1.5, tree 2 cycle: NaN
+    # row 2: node 2 -> child 9: NaN; row 3: tree 1 NaN (node 1), tree 2 -> leaf -2
+    assert np.isnan(got).tolist() == [True, True, True, True]
+    one = ops.predict_table(codes, table[:1], 1.0, np.zeros(4, F32))
+    assert np.isnan(one).tolist() == [True, False, True, True] and one[1] == F32(1.5)
+    two = ops.predict_table(codes, table[1:], 1.0, np.zeros(4, F32))
+    assert np.isnan(two).tolist() == [True, True, False, False] and two[2] == F32(-2.0)
+
+
 # --------------------------------------------------------------------------- tree growth
 def test_gbm_finds_planted_split_and_group_means():
     rng = np.random.default_rng(4)

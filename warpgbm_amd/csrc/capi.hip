@@ -15,6 +15,8 @@ static inline hipStream_t S(void* s) { return (hipStream_t)s; }
 static inline unsigned nblocks(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
 constexpr int kMaxDevices = 64;  // devices the no-allocation entry point keeps addresses for
+// wgbm_predict_forest takes the heap path from this many trees on
+constexpr int64_t kForestHeapMinTrees = 8;
 
 extern "C" {
 
@@ -388,14 +390,118 @@ int wgbm_custom_cuda_binner(const float* X, int64_t n, const float* bin_edges, i
   return 0;
 }
 
+}  // extern "C"
+
+static int predict_heap_impl(const int8_t* codes, int64_t n, int64_t codes_stride,
+                             int32_t num_bins, const int32_t* feat, const int32_t* bin,
+                             const float* leaf, int32_t n_rounds, int32_t K, int32_t H,
+                             int32_t max_depth, float learning_rate, float* out, void* stream,
+                             const int32_t* skip) {
+  WGBM_REQUIRE(n >= 0 && K >= 1 && n_rounds >= 0 && max_depth >= 0 && max_depth <= 29,
+               "bad predict_heap shape");  // heap indices below 2^30: int32
+  WGBM_REQUIRE(num_bins >= 2 && num_bins <= 127, "num_bins must be in [2, 127]");
+  WGBM_REQUIRE(H == (1 << (max_depth + 1)) - 1, "H must be 2^(max_depth+1)-1");
+  if (n == 0) return 0;
+  WGBM_REQUIRE(codes && out && (n_rounds == 0 || (feat && bin && leaf)), "null pointer");
+  if (n_rounds == 0) return 0;
+  int32_t RB = 0, TC = 0;
+  size_t lds = 0;
+  int dev = 0, n_cu = 0;
+  WGBM_CHECK(hipGetDevice(&dev));
+  WGBM_CHECK(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+  const bool resident = predict_resident_plan(codes_stride, K, H, n_rounds, &RB, &lds) != 0;
+  const bool rows = !resident && predict_rows_plan(codes_stride, K, H, n_rounds, &RB, &TC, &lds);
+  uint32_t* cnode = nullptr;
+  float* cleaf = nullptr;
+  if (resident || rows) {
+    // the complete-tree tables the LDS predictors walk (H words per tree)
+    const int64_t T = (int64_t)n_rounds * K;
+    cnode = (uint32_t*)scratch_get(S(stream), sizeof(uint32_t) * (size_t)(T * H), 13);
+    WGBM_REQUIRE(cnode, "scratch allocation failed");
+    cleaf = reinterpret_cast<float*>(cnode + T * ((H - 1) / 2));
+    const int64_t work = T * H;
+    hipLaunchKernelGGL(complete_tables_kernel, dim3(nblocks(work, 256)), dim3(256), 0,
+                       S(stream), feat, bin, leaf, T, max_depth, codes_stride, learning_rate,
+                       cnode, cleaf);
+    WGBM_LAUNCH_CHECK();
+  }
+  if (resident) {
+    static bool attr_r = false;
+    if (!attr_r) {
+      WGBM_CHECK(hipFuncSetAttribute((const void*)predict_resident_kernel,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      attr_r = true;
+    }
+    // one persistent workgroup per CU (fewer when there are fewer blocks)
+    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(n_cu, nblocks(n, RB)));
+    hipLaunchKernelGGL(predict_resident_kernel, dim3((unsigned)grid), dim3(1024), lds, S(stream),
+                       codes, n, codes_stride, num_bins, (const uint32_t*)cnode,
+                       (const float*)cleaf, n_rounds * K, K, max_depth, RB, out, skip);
+  } else if (rows) {
+    static bool attr = false;
+    if (!attr) {
+      WGBM_CHECK(hipFuncSetAttribute((const void*)predict_rows_kernel,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      attr = true;
+    }
+    hipLaunchKernelGGL(predict_rows_kernel, dim3(nblocks(n, RB)), dim3(1024), lds, S(stream),
+                       codes, n, codes_stride, num_bins, (const uint32_t*)cnode,
+                       (const float*)cleaf, n_rounds, K, max_depth, RB, TC, out, skip);
+  } else {
+    hipLaunchKernelGGL(predict_heap_kernel, dim3(nblocks(n * K, 256)), dim3(256), 0, S(stream),
+                       codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds, K, H,
+                       max_depth, learning_rate, out, skip);
+  }
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" {
+
 int wgbm_predict_forest(const int8_t* bin_indices, int64_t n, int64_t n_feats,
                         const float* tree_tensor, int64_t n_trees, int64_t max_nodes,
                         float learning_rate, float* out, void* stream) {
   WGBM_REQUIRE(n >= 0 && n_feats >= 0 && n_trees >= 0 && max_nodes >= 1, "bad predict shape");
   if (n == 0) return 0;
   WGBM_REQUIRE(bin_indices && out && (n_trees == 0 || tree_tensor), "null pointer");
-  hipLaunchKernelGGL(predict_table_kernel, dim3(nblocks(n, 256)), dim3(256), 0, S(stream),
-                     bin_indices, n, n_feats, tree_tensor, n_trees, max_nodes, learning_rate, out);
+  hipStream_t st = S(stream);
+  // Heap path, for enough trees and rows to pay for a copy of the codes: the
+  // flat tables become heap tables of depth D = floor(log2(max_nodes)) - 1
+  // (flatten_tree's max_nodes = 2^(max_depth+1)) and the codes a native
+  // copy (num_bins 127: a negative code becomes the byte 127, which every
+  // split sends left; 127 becomes 128, which every split bin <= 126 sends
+  // right; the other codes stay), then the LDS predictors walk them.  A
+  // table the heap cannot hold sets a device flag: the heap walk is skipped
+  // and the flat walk below runs instead; otherwise the flat walk exits.
+  int D = 0;
+  while ((int64_t(4) << D) <= max_nodes) ++D;  // 2^(D+1) <= max_nodes < 2^(D+2)
+  const bool heap_path = n_trees >= kForestHeapMinTrees && n >= 4096 && n_feats >= 1 &&
+                         n_feats <= 65535 && max_nodes >= 2 && D <= 12 &&
+                         n_trees * ((int64_t(2) << D) - 1) <= (int64_t(1) << 28);
+  const int32_t* flag = nullptr;
+  if (heap_path) {
+    const int64_t H = (int64_t(2) << D) - 1, Sn = (n_feats + 127) / 128 * 128;
+    int32_t* fl = (int32_t*)scratch_get(st, sizeof(int32_t) * 64, 14);
+    int32_t* feat = (int32_t*)scratch_get(st, sizeof(int32_t) * (size_t)(n_trees * H), 15);
+    int32_t* bin = (int32_t*)scratch_get(st, sizeof(int32_t) * (size_t)(n_trees * H), 16);
+    float* leaf = (float*)scratch_get(st, sizeof(float) * (size_t)(n_trees * H), 17);
+    int8_t* nat = (int8_t*)scratch_get(st, (size_t)(n * Sn), 18);
+    WGBM_REQUIRE(fl && feat && bin && leaf && nat, "scratch allocation failed");
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, fl, (int64_t)1, 0);
+    WGBM_LAUNCH_CHECK();
+    hipLaunchKernelGGL(flat_to_heap_kernel, dim3(nblocks(n_trees * H, 256)), dim3(256), 0, st,
+                       tree_tensor, n_trees, max_nodes, n_feats, (int32_t)D, feat, bin, leaf, fl);
+    WGBM_LAUNCH_CHECK();
+    int r = wgbm_copy_prebinned(bin_indices, n, (int32_t)n_feats, n_feats, nat, Sn, nullptr, 127,
+                                nullptr, stream);
+    if (r) return r;
+    r = predict_heap_impl(nat, n, Sn, 127, feat, bin, leaf, (int32_t)n_trees, 1, (int32_t)H, D,
+                          learning_rate, out, stream, fl);
+    if (r) return r;
+    flag = fl;
+  }
+  hipLaunchKernelGGL(predict_table_kernel, dim3(nblocks(n, 256)), dim3(256), 0, st, bin_indices,
+                     n, n_feats, tree_tensor, n_trees, max_nodes, learning_rate, out, flag);
   WGBM_LAUNCH_CHECK();
   return 0;
 }
@@ -516,63 +622,8 @@ int wgbm_predict_heap(const int8_t* codes, int64_t n, int64_t codes_stride, int3
                       const int32_t* feat, const int32_t* bin, const float* leaf,
                       int32_t n_rounds, int32_t K, int32_t H, int32_t max_depth,
                       float learning_rate, float* out, void* stream) {
-  WGBM_REQUIRE(n >= 0 && K >= 1 && n_rounds >= 0 && max_depth >= 0 && max_depth <= 29,
-               "bad predict_heap shape");  // heap indices below 2^30: int32
-  WGBM_REQUIRE(num_bins >= 2 && num_bins <= 127, "num_bins must be in [2, 127]");
-  WGBM_REQUIRE(H == (1 << (max_depth + 1)) - 1, "H must be 2^(max_depth+1)-1");
-  if (n == 0) return 0;
-  WGBM_REQUIRE(codes && out && (n_rounds == 0 || (feat && bin && leaf)), "null pointer");
-  if (n_rounds == 0) return 0;
-  int32_t RB = 0, TC = 0;
-  size_t lds = 0;
-  int dev = 0, n_cu = 0;
-  WGBM_CHECK(hipGetDevice(&dev));
-  WGBM_CHECK(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
-  const bool resident = predict_resident_plan(codes_stride, K, H, n_rounds, &RB, &lds) != 0;
-  const bool rows = !resident && predict_rows_plan(codes_stride, K, H, n_rounds, &RB, &TC, &lds);
-  uint32_t* cnode = nullptr;
-  float* cleaf = nullptr;
-  if (resident || rows) {
-    // the complete-tree tables the LDS predictors walk (H words per tree)
-    const int64_t T = (int64_t)n_rounds * K;
-    cnode = (uint32_t*)scratch_get(S(stream), sizeof(uint32_t) * (size_t)(T * H), 13);
-    WGBM_REQUIRE(cnode, "scratch allocation failed");
-    cleaf = reinterpret_cast<float*>(cnode + T * ((H - 1) / 2));
-    const int64_t work = T * H;
-    hipLaunchKernelGGL(complete_tables_kernel, dim3(nblocks(work, 256)), dim3(256), 0,
-                       S(stream), feat, bin, leaf, T, max_depth, codes_stride, learning_rate,
-                       cnode, cleaf);
-    WGBM_LAUNCH_CHECK();
-  }
-  if (resident) {
-    static bool attr_r = false;
-    if (!attr_r) {
-      WGBM_CHECK(hipFuncSetAttribute((const void*)predict_resident_kernel,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-      attr_r = true;
-    }
-    // one persistent workgroup per CU (fewer when there are fewer blocks)
-    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(n_cu, nblocks(n, RB)));
-    hipLaunchKernelGGL(predict_resident_kernel, dim3((unsigned)grid), dim3(1024), lds, S(stream),
-                       codes, n, codes_stride, num_bins, (const uint32_t*)cnode,
-                       (const float*)cleaf, n_rounds * K, K, max_depth, RB, out);
-  } else if (rows) {
-    static bool attr = false;
-    if (!attr) {
-      WGBM_CHECK(hipFuncSetAttribute((const void*)predict_rows_kernel,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-      attr = true;
-    }
-    hipLaunchKernelGGL(predict_rows_kernel, dim3(nblocks(n, RB)), dim3(1024), lds, S(stream),
-                       codes, n, codes_stride, num_bins, (const uint32_t*)cnode,
-                       (const float*)cleaf, n_rounds, K, max_depth, RB, TC, out);
-  } else {
-    hipLaunchKernelGGL(predict_heap_kernel, dim3(nblocks(n * K, 256)), dim3(256), 0, S(stream),
-                       codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds, K, H,
-                       max_depth, learning_rate, out);
-  }
-  WGBM_LAUNCH_CHECK();
-  return 0;
+  return predict_heap_impl(codes, n, codes_stride, num_bins, feat, bin, leaf, n_rounds, K, H,
+                           max_depth, learning_rate, out, stream, nullptr);
 }
 
 int wgbm_softmax_rows(float* x, int64_t n, int32_t K, void* stream) {

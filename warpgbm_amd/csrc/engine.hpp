@@ -327,26 +327,32 @@ __global__ void quantile_select_kernel(const uint32_t* keys, int64_t n, int64_t 
                                        const float* q, int32_t nq, float* edges,
                                        const uint32_t* kmin, const uint32_t* kmax,
                                        uint32_t* cbuf, int64_t ccap);
+// skip / run_if (optional, null: none): device flags that switch a kernel
+// off (skip nonzero) or on (run_if nonzero), for wgbm_predict_forest
 __global__ void predict_table_kernel(const int8_t* codes, int64_t n, int64_t F,
                                      const float* table, int64_t T, int64_t M, float lr,
-                                     float* out);
+                                     float* out, const int32_t* run_if);
+__global__ void flat_to_heap_kernel(const float* table, int64_t T, int64_t M, int64_t F,
+                                    int32_t D, int32_t* feat, int32_t* bin, float* leaf,
+                                    int32_t* fallback);
 __global__ void predict_heap_kernel(const int8_t* codes, int64_t n, int64_t S, int32_t num_bins,
                                     const int32_t* feat, const int32_t* bin, const float* leaf,
                                     int32_t n_rounds, int32_t K, int32_t H, int32_t max_depth,
-                                    float lr, float* out);
+                                    float lr, float* out, const int32_t* skip);
 __global__ void complete_tables_kernel(const int32_t* feat, const int32_t* bin, const float* leaf,
                                        int64_t T, int32_t D, int64_t S, float lr,
                                        uint32_t* cnode, float* cleaf);
 __global__ void predict_rows_kernel(const int8_t* codes, int64_t n, int64_t S, int32_t num_bins,
                                     const uint32_t* cnode, const float* cleaf, int32_t n_rounds,
                                     int32_t K, int32_t max_depth, int32_t RB, int32_t TC,
-                                    float* out);
+                                    float* out, const int32_t* skip);
 int predict_rows_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
                       int32_t* TC_out, size_t* lds_out);
 __global__ void predict_resident_kernel(const int8_t* codes, int64_t n, int64_t S,
                                         int32_t num_bins, const uint32_t* cnode,
                                         const float* cleaf, int32_t T, int32_t K,
-                                        int32_t max_depth, int32_t RB, float* out);
+                                        int32_t max_depth, int32_t RB, float* out,
+                                        const int32_t* skip);
 int predict_resident_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
                           size_t* lds_out);
 __global__ void softmax_rows_kernel(float* x, int64_t n, int32_t K);

@@ -18,9 +18,13 @@ namespace wgbm {
 
 // reference table format, walk bounded by M steps (malformed tables cannot
 // loop forever; a walk that leaves the table contributes NaN)
+// run_if (optional): the walk runs only when *run_if is nonzero (the fallback
+// of wgbm_predict_forest's heap path, decided on the device)
 __global__ void predict_table_kernel(const int8_t* __restrict__ codes, int64_t n, int64_t F,
                                      const float* __restrict__ table, int64_t T, int64_t M,
-                                     float lr, float* __restrict__ out) {
+                                     float lr, float* __restrict__ out,
+                                     const int32_t* __restrict__ run_if) {
+  if (run_if && *run_if == 0) return;  // uniform
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int8_t* row = codes + i * F;
@@ -47,6 +51,82 @@ __global__ void predict_table_kernel(const int8_t* __restrict__ codes, int64_t n
   out[i] = acc;
 }
 
+// The reference's flat tables [T, M, 6] as heap tables of depth D (H =
+// 2^(D+1) - 1 slots per tree), for wgbm_predict_forest's heap path: one
+// thread per (tree, heap node h) walks from node 0 along h's path and
+// writes what the flat walk of predict_table_kernel meets there: a leaf
+// (feat -1, its value), a split (feature, bin), an absent node (-2, under a
+// leaf) or -- where that walk would stop with NaN (a feature outside [0, F),
+// a child index outside [0, M)) -- a leaf of value NaN, so the heap walk
+// returns the same value.  A split on the last heap level (a deeper tree), a
+// negative bin or a feature >= 65536 cannot be held: then *fallback is set
+// and the caller's flat walk runs instead.  Bins of 127 and above hold as
+// 255: every int8 code is <= such a bin, and every code byte of the native
+// copy (127 and 128 included) is <= 255.
+__global__ void flat_to_heap_kernel(const float* __restrict__ table, int64_t T, int64_t M,
+                                    int64_t F, int32_t D, int32_t* __restrict__ feat,
+                                    int32_t* __restrict__ bin, float* __restrict__ leaf,
+                                    int32_t* __restrict__ fallback) {
+  const int64_t H = (int64_t(2) << D) - 1;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= T * H) return;
+  const int64_t t = gid / H;
+  const int h = (int)(gid - t * H);
+  const float* tree = table + t * M * 6;
+  const int d = 31 - __builtin_clz((unsigned)(h + 1));  // depth of heap node h
+  int32_t f_out = -2, b_out = 0;
+  float v_out = 0.0f;
+  int64_t node = 0;
+  bool reached = true;
+  for (int k = 0; k < d && reached; ++k) {
+    const float* nd = tree + node * 6;
+    if (nd[4] > 0.5f) {  // a leaf above h: h is absent
+      reached = false;
+      break;
+    }
+    const int f = (int)nd[0];
+    if (f < 0 || f >= F) {  // the walk stops here (NaN): h is absent
+      reached = false;
+      break;
+    }
+    const int right = ((h + 1) >> (d - 1 - k)) & 1;
+    const int nxt = right ? (int)nd[3] : (int)nd[2];
+    if (nxt < 0 || nxt >= M) {
+      // the walk stops (NaN) on this edge: a NaN leaf if it leads to h
+      if (k == d - 1) {
+        f_out = -1;
+        v_out = __builtin_nanf("");
+      }
+      reached = false;
+      break;
+    }
+    node = nxt;
+  }
+  if (reached) {
+    const float* nd = tree + node * 6;
+    if (nd[4] > 0.5f) {
+      f_out = -1;
+      v_out = nd[5];
+    } else {
+      const int f = (int)nd[0];
+      const int sb = (int)nd[1];
+      if (f < 0 || f >= F) {
+        f_out = -1;
+        v_out = __builtin_nanf("");
+      } else if (d == D || sb < 0 || f > 65535) {
+        *fallback = 1;
+        f_out = -1;
+      } else {
+        f_out = f;
+        b_out = sb < 127 ? sb : 255;
+      }
+    }
+  }
+  feat[gid] = f_out;
+  bin[gid] = b_out;
+  leaf[gid] = v_out;
+}
+
 // compact heap tables written by the engine: node h has children 2h+1, 2h+2.
 //   feat[t][h] >= 0 split feature, -1 leaf; bin[t][h]; leaf[t][h]
 // trees are ordered (round, class); out is [n, K] row-major, pre-initialised.
@@ -59,7 +139,8 @@ __global__ void predict_heap_kernel(const int8_t* __restrict__ codes, int64_t n,
                                     const int32_t* __restrict__ bin,
                                     const float* __restrict__ leaf, int32_t n_rounds, int32_t K,
                                     int32_t H, int32_t max_depth, float lr,
-                                    float* __restrict__ out) {
+                                    float* __restrict__ out, const int32_t* __restrict__ skip) {
+  if (skip && *skip) return;  // uniform: the caller's fallback runs instead
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= n * K) return;
   const int64_t i = gid / K;
@@ -229,7 +310,9 @@ constexpr int kPredWalks = 2;   // walks a thread advances in lock-step
 __global__ __launch_bounds__(kPredThreads) void predict_rows_kernel(
     const int8_t* __restrict__ codes, int64_t n, int64_t S, int32_t num_bins,
     const uint32_t* __restrict__ cnode, const float* __restrict__ cleaf, int32_t n_rounds,
-    int32_t K, int32_t max_depth, int32_t RB, int32_t TC, float* __restrict__ out) {
+    int32_t K, int32_t max_depth, int32_t RB, int32_t TC, float* __restrict__ out,
+    const int32_t* __restrict__ skip) {
+  if (skip && *skip) return;  // uniform: the caller's fallback runs instead
   extern __shared__ uint32_t psm[];
   const int Sp = (int)S + 4;
   const int Hi = (1 << max_depth) - 1, L = 1 << max_depth;  // complete-table widths
@@ -326,7 +409,9 @@ constexpr int kResWalks = 2;  // walks a walker thread advances in lock-step
 __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
     const int8_t* __restrict__ codes, int64_t n, int64_t S, int32_t num_bins,
     const uint32_t* __restrict__ cnode, const float* __restrict__ cleaf, int32_t T, int32_t K,
-    int32_t max_depth, int32_t RB, float* __restrict__ out) {
+    int32_t max_depth, int32_t RB, float* __restrict__ out,
+    const int32_t* __restrict__ skip) {
+  if (skip && *skip) return;  // uniform: the caller's fallback runs instead
   extern __shared__ uint32_t psm[];
   const int Sp = (int)S + 4;
   const int TV = T + 1;  // value-table row stride (odd or even, see below)
