@@ -68,7 +68,7 @@ struct Engine {
   // E > 1 with every era <= 65536 rows: per-era gains straight from LDS
   // histograms of every (node, era) segment (no per-era histogram arrays)
   bool des_direct = false;
-  float* sgain = nullptr;       // staged per-era gains [tn][E][n_sel][B-1]
+  float* sgain = nullptr;       // staged per-era gains (des_stage_slot layout)
   int8_t* sdir = nullptr;       // staged per-era directions
   int32_t* local_of = nullptr;  // [F] local index in the round's subset, or -1
   // num_bins <= 7: pair-code copy of codes_rm for the era path (made by the
@@ -180,7 +180,8 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   // two of nodes that does (deeper levels are then processed in chunks)
   const int64_t W = (E + kDesEraBlock - 1) / kDesEraBlock;
   const int64_t per_node =
-      e->des_direct ? E * F * (B - 1) * 5 + W * (4 + F * (B - 1) * 12) + F * (B - 1) * 8
+      e->des_direct ? des_stage_words(1, (int32_t)W, F * (B - 1)) * 5 +
+                          W * (4 + F * (B - 1) * 12) + F * (B - 1) * 8
                     : 2 * E * F * B * 12 + (E > 1 ? F * (B - 1) * 8 : 0);
   const int64_t budget = cfg.level_bytes > 0 ? cfg.level_bytes : (int64_t)4 << 30;
   if (T * hist_nodes_max * per_node <= budget) {
@@ -226,8 +227,8 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     }
   }
   if (e->des_direct) {
-    E_ALLOC(e->sgain, e->nc_max * E * F * (B - 1));
-    E_ALLOC(e->sdir, e->nc_max * E * F * (B - 1));
+    E_ALLOC(e->sgain, des_stage_words(e->nc_max, (int32_t)W, F * (B - 1)));
+    E_ALLOC(e->sdir, des_stage_words(e->nc_max, (int32_t)W, F * (B - 1)));
     E_ALLOC(e->local_of, F);
     if (B <= 7 && N * pair_stride((int32_t)F) <= (int64_t)0xffffffffll) {
       e->pstride = pair_stride((int32_t)F);

@@ -38,6 +38,7 @@ __global__ void residual_regression_kernel(const float* __restrict__ y,
 // softmax: p = softmax(F[i, :]); residual_k = -(p_k - onehot_k)
 // (warpgbm/core.py:186-214 and :782; metrics.py:12-15).
 // partial[k * gridDim.x + block] = max_i |residual_k|
+constexpr int kSoftmaxRegK = 16;  // classes whose logits a thread holds in registers
 __global__ void residual_softmax_kernel(const float* __restrict__ logits /* [K][n] */,
                                         const int32_t* __restrict__ label, int64_t n, int32_t K,
                                         float* __restrict__ r /* [K][n] */,
@@ -50,18 +51,39 @@ __global__ void residual_softmax_kernel(const float* __restrict__ logits /* [K][
       // the row's K logits, class-major (one coalesced read per class)
       const float* x = logits + i;
       const int lab = label[i];
-      float mx = x[0];
-      for (int k = 1; k < K; ++k) mx = x[k * n] > mx ? x[k * n] : mx;
-      float s = 0.0f;
-      for (int k = 0; k < K; ++k) s = s + wgbm_expf(x[k * n] - mx);
-      for (int kk = 0; kk < 8 && k0 + kk < K; ++kk) {
+      auto emit = [&](int kk, float p) {
         const int k = k0 + kk;
-        const float p = wgbm_expf(x[k * n] - mx) / s;
         const float g = p - (k == lab ? 1.0f : 0.0f);
         const float v = -g;
         r[(int64_t)k * n + i] = v;
         const uint32_t b = wgbm_abs_bits(v);
         m[kk] = b > m[kk] ? b : m[kk];
+      };
+      if (K <= kSoftmaxRegK) {
+        // the logits loaded together into registers (fully unrolled: no
+        // dynamic register index), then the same operations in the same
+        // order as the general loop below
+        float xr[kSoftmaxRegK];
+#pragma unroll
+        for (int k = 0; k < kSoftmaxRegK; ++k) xr[k] = x[(k < K ? k : 0) * n];
+        float mx = xr[0];
+#pragma unroll
+        for (int k = 1; k < kSoftmaxRegK; ++k)
+          if (k < K) mx = xr[k] > mx ? xr[k] : mx;
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kSoftmaxRegK; ++k)
+          if (k < K) s = s + wgbm_expf(xr[k] - mx);
+#pragma unroll
+        for (int k = 0; k < kSoftmaxRegK; ++k)
+          if (k >= k0 && k < k0 + 8 && k < K) emit(k - k0, wgbm_expf(xr[k] - mx) / s);
+      } else {
+        float mx = x[0];
+        for (int k = 1; k < K; ++k) mx = x[k * n] > mx ? x[k * n] : mx;
+        float s = 0.0f;
+        for (int k = 0; k < K; ++k) s = s + wgbm_expf(x[k * n] - mx);
+        for (int kk = 0; kk < 8 && k0 + kk < K; ++kk)
+          emit(kk, wgbm_expf(x[(k0 + kk) * n] - mx) / s);
       }
     }
     for (int kk = 0; kk < 8 && k0 + kk < K; ++kk) {

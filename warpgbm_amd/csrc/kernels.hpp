@@ -24,6 +24,20 @@ constexpr int kDesChunk = 8;
 // eras per block of the DES era sum (float64: in era order inside a block,
 // then block sums in block order); also the width of a live-era mask word
 constexpr int kDesEraBlock = 32;
+// Staged per-era gains / directions of the direct era path, block-major: for
+// (tree-node tn, era e, candidate c = local feature * (B-1) + bin) the slot
+// (((tn * W + e / 32) * C64 + c / 64) * 32 + e % 32) * 64 + c % 64, with W =
+// ceil(E / 32) era blocks and C64 = ceil(ncand / 64) groups of 64
+// candidates: the 32 eras of one block and 64 candidates are 8 KB of
+// consecutive floats, which one wave of des_block_kernel reads front to back.
+__host__ __device__ inline int64_t des_stage_slot(int64_t tn, int32_t e, int32_t W,
+                                                  int64_t c64, int64_t c) {
+  return (((tn * W + e / 32) * c64 + c / 64) * 32 + e % 32) * 64 + c % 64;
+}
+// slots of nc tree-nodes
+__host__ __device__ inline int64_t des_stage_words(int64_t nc, int32_t W, int64_t ncand) {
+  return nc * W * ((ncand + 63) / 64) * 32 * 64;
+}
 // cache-policy bits of a buffer load: non-temporal (streamed once), plus
 // sc0 for the code stream of the tile histogram (measured faster there)
 constexpr int kAuxNT = 2;

@@ -315,9 +315,11 @@ __global__ void des_finish_kernel(const unsigned long long* __restrict__ best,
   if (staged) {
     // staged per-era gains [tn][E][n_sel][B-1]; none for dead segments
     const int64_t k2 = (int64_t)tn * E + e;
-    split_gain_era[gid] = des_segment_dead(seg[k2 + 1] - seg[k2], mcw)
-                              ? 0.0f
-                              : staged[k2 * ((int64_t)n_sel * nb) + idx];
+    const int W = (E + kDesEraBlock - 1) / kDesEraBlock;
+    split_gain_era[gid] =
+        des_segment_dead(seg[k2 + 1] - seg[k2], mcw)
+            ? 0.0f
+            : staged[des_stage_slot(tn, e, W, ((int64_t)n_sel * nb + 63) / 64, idx)];
     return;
   }
   const int s = key_shift[gid];  // the (node, era) segment's shift
@@ -366,6 +368,7 @@ void des_era_kernel(
   const int Bp = B + 1;
   const int nb = B - 1;
   const int n_chunks = (F + CW - 1) / CW;
+  const int W = (E + kDesEraBlock - 1) / kDesEraBlock;  // era blocks (staging layout)
   const int slots = gridDim.x / n_chunks;  // workgroups per chunk; keys stride by it
   const int slot = blockIdx.x / n_chunks;
   const int chunk = blockIdx.x - slot * n_chunks;
@@ -480,7 +483,8 @@ void des_era_kernel(
         const int l = local_of[f];
         if (l < 0) continue;
         const unsigned long long* col = lds + (fs % V) * Bp * kHistSlots + fs / V;
-        const int64_t out = ((int64_t)key * n_sel + l) * nb;
+        const int64_t c64 = ((int64_t)n_sel * nb + 63) / 64;
+        const int tnk = key / E, ek = key - (key / E) * E;
         scan_bins(
             B, mcw, eps,
             [&](int b) { return wgbm_dequantise((int64_t)col[b * kHistSlots] >> WGBM_CBITS, s); },
@@ -488,8 +492,9 @@ void des_era_kernel(
               return (float)(int32_t)(col[b * kHistSlots] & (unsigned long long)WGBM_CMASK);
             },
             [&](int b, float gn, float d) {
-              gain[out + b] = gn;
-              dir[out + b] = (int8_t)d;
+              const int64_t o = des_stage_slot(tnk, ek, W, c64, (int64_t)l * nb + b);
+              gain[o] = gn;
+              dir[o] = (int8_t)d;
             });
       }
       __syncthreads();  // before the next key's histogram reuses the LDS
@@ -545,6 +550,7 @@ void des_pair_kernel(
   constexpr int nb = BT - 1;
   extern __shared__ unsigned long long lds[];
   const int n_chunks = (F + CW - 1) / CW;
+  const int W = (E + kDesEraBlock - 1) / kDesEraBlock;  // era blocks (staging layout)
   const int slots = gridDim.x / n_chunks;
   const int slot = blockIdx.x / n_chunks;
   const int chunk = blockIdx.x - slot * n_chunks;
@@ -677,7 +683,8 @@ void des_pair_kernel(
           const int f = chunk * CW + pl * 2 * LP + 2 * p + h;
           const int l = f < F ? local_of[f] : -1;
           if (l >= 0) {
-            const int64_t out = ((int64_t)key * n_sel + l) * nb;
+            const int64_t c64 = ((int64_t)n_sel * nb + 63) / 64;
+            const int tnk = key / E, ek = key - (key / E) * E;
             scan_bins(
                 BT, mcw, eps,
                 [&](int b) { return wgbm_dequantise((int64_t)col[b * cs] >> WGBM_CBITS, s); },
@@ -685,8 +692,9 @@ void des_pair_kernel(
                   return (float)(int32_t)(col[b * cs] & (unsigned long long)WGBM_CMASK);
                 },
                 [&](int b, float gn, float d) {
-                  gain[out + b] = gn;
-                  dir[out + b] = (int8_t)d;
+                  const int64_t o = des_stage_slot(tnk, ek, W, c64, (int64_t)l * nb + b);
+                  gain[o] = gn;
+                  dir[o] = (int8_t)d;
                 });
           }
 #pragma unroll
@@ -746,10 +754,19 @@ __global__ void des_alive_kernel(const int64_t* __restrict__ seg, int32_t E, int
   const int tn = (int)(gid / W);
   const int w = (int)(gid - (int64_t)tn * W);
   const int64_t* sg = seg + (int64_t)tn * E;
+  // the block's 33 segment offsets, loaded unconditionally (indices clamped
+  // to the node's E + 1 offsets) so that the loads are issued together
+  int64_t o[kDesEraBlock + 1];
+#pragma unroll
+  for (int b = 0; b <= kDesEraBlock; ++b) {
+    const int e = w * kDesEraBlock + b;
+    o[b] = sg[e < E ? e : E];
+  }
   uint32_t m = 0;
+#pragma unroll
   for (int b = 0; b < kDesEraBlock; ++b) {
     const int e = w * kDesEraBlock + b;
-    if (e < E && !des_segment_dead(sg[e + 1] - sg[e], mcw)) m |= 1u << b;
+    if (e < E && !des_segment_dead(o[b + 1] - o[b], mcw)) m |= 1u << b;
   }
   alive[gid] = m;
 }
@@ -774,7 +791,9 @@ __global__ __launch_bounds__(256) void des_block_kernel(
   if (!present[tn]) return;
   const uint32_t m = alive[tb];
   if (m == 0) return;
-  const int64_t base = ((int64_t)tn * E + (int64_t)blk * kDesEraBlock) * ncand + c;
+  // this block's 32 eras of the candidate: slots base + 64 * k (block-major
+  // staging layout)
+  const int64_t base = des_stage_slot(tn, blk * kDesEraBlock, W, (ncand + 63) / 64, c);
   double acc = 0.0;
   int ds = 0;
   constexpr int kHalf = kDesEraBlock / 2;
@@ -782,17 +801,22 @@ __global__ __launch_bounds__(256) void des_block_kernel(
   for (int h = 0; h < 2; ++h) {
     float gv[kHalf];
     int dv[kHalf];
+    // every slot of the block exists (the layout has 32 per block), so the
+    // loads are unconditional and issued together; a dead era's slot was
+    // never written and its value is not added (a predicated load would
+    // become a branch with a wait after every load)
 #pragma unroll
     for (int k = 0; k < kHalf; ++k) {
       const int kk = h * kHalf + k;
-      const bool live = (m >> kk) & 1u;  // implies the era exists
-      gv[k] = live ? gain[base + (int64_t)kk * ncand] : 0.0f;
-      dv[k] = live ? (int)dir[base + (int64_t)kk * ncand] : 0;
+      gv[k] = gain[base + (int64_t)kk * 64];
+      dv[k] = (int)dir[base + (int64_t)kk * 64];
     }
 #pragma unroll
     for (int k = 0; k < kHalf; ++k) {
-      if ((m >> (h * kHalf + k)) & 1u) acc += (double)gv[k];  // era order
-      ds += dv[k];
+      if ((m >> (h * kHalf + k)) & 1u) {  // a live era (it exists)
+        acc += (double)gv[k];  // era order
+        ds += dv[k];
+      }
     }
   }
   bsum[gid] = acc;
