@@ -277,10 +277,14 @@ __global__ void des_alive_kernel(const int64_t* seg, int32_t E, int32_t n_tn, fl
 __global__ void des_block_kernel(const float* gain, const int8_t* dir, int32_t E, int32_t n_tn,
                                  int64_t ncand, const int32_t* present, const uint32_t* alive,
                                  double* bsum, int32_t* bdir);
-__global__ void des_combine_kernel(const double* bsum, const int32_t* bdir, int32_t E,
-                                   int32_t n_tn, int64_t ncand, const int32_t* present,
-                                   const uint32_t* alive, float* crit, int32_t* agree,
-                                   int32_t* agree_max);
+__global__ void des_combine_pick_kernel(const double* bsum, const int32_t* bdir, int32_t E,
+                                        int32_t n_tn, int64_t ncand, const int32_t* present,
+                                        const uint32_t* alive, float min_split_gain,
+                                        int32_t* wg_agree, unsigned long long* wg_key,
+                                        unsigned long long* best, uint32_t* done,
+                                        const float* staged, const int64_t* seg, float mcw,
+                                        int32_t nb, int32_t n_sel, int32_t* split_l,
+                                        int32_t* split_b, float* split_gain_era);
 __global__ void local_scatter_kernel(const int32_t* feat_sel, int32_t n_sel, int32_t F,
                                      int32_t* local_of);
 // pcodes: the pair-code copy of the codes (num_bins <= 7; n_rows rows of

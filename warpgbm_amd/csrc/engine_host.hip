@@ -70,6 +70,8 @@ struct Engine {
   bool des_direct = false;
   float* sgain = nullptr;       // staged per-era gains (des_stage_slot layout)
   int8_t* sdir = nullptr;       // staged per-era directions
+  int32_t* wg_agree = nullptr;  // per-workgroup summaries of des_combine_pick_kernel
+  unsigned long long* wg_key = nullptr;
   int32_t* local_of = nullptr;  // [F] local index in the round's subset, or -1
   // num_bins <= 7: pair-code copy of codes_rm for the era path (made by the
   // first round); des_codes 0 = read the int8 codes, 1 = pair codes (default)
@@ -235,6 +237,8 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
       E_ALLOC(e->pcodes, N * e->pstride);
     }
     E_ALLOC(e->alive, e->nc_max * W);
+    E_ALLOC(e->wg_agree, e->nc_max * ((F * (B - 1) + 255) / 256));
+    E_ALLOC(e->wg_key, e->nc_max * ((F * (B - 1) + 255) / 256));
     E_ALLOC(e->bsum, e->nc_max * W * F * (B - 1));
     E_ALLOC(e->bdir, e->nc_max * W * F * (B - 1));
   }
@@ -543,19 +547,15 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                            dim3(256), 0, st, e->sgain, e->sdir, E, nc, ncand,
                            e->present[cur] + c0, e->alive, e->bsum, e->bdir);
         WGBM_LAUNCH_CHECK();
-        hipLaunchKernelGGL(des_combine_kernel, dim3(blocks_for((int64_t)nc * ncand, 256)),
-                           dim3(256), 0, st, e->bsum, e->bdir, E, nc, ncand, e->present[cur] + c0,
-                           e->alive, e->crit, e->agree, agree_max + c0);
-        WGBM_LAUNCH_CHECK();
-        hipLaunchKernelGGL(des_pick_kernel, dim3(blocks_for((int64_t)nc * ncand, 256)),
-                           dim3(256), 0, st, e->crit, e->agree, agree_max + c0,
-                           e->present[cur] + c0, nc, ncand, msg, best + c0);
-        WGBM_LAUNCH_CHECK();
-        hipLaunchKernelGGL(des_finish_kernel, dim3(blocks_for((int64_t)nc * E, 256)), dim3(256),
-                           0, st, best + c0, (const int64_t*)nullptr, (const int32_t*)nullptr, F,
-                           B, E, feat_sel, nodes, nc, e->node_shift[cur] + k0, mcw, eps,
-                           e->sgain, e->seg[cur] + k0, n_sel, e->split_l + c0, e->split_b + c0,
-                           e->split_gain + k0);
+        // block sums in block order, the pick and the record in one launch
+        // (the last workgroup of each node picks from the workgroups'
+        // summaries and finishes the node)
+        hipLaunchKernelGGL(des_combine_pick_kernel,
+                           dim3((unsigned)((int64_t)nc * ((ncand + 255) / 256))), dim3(256), 0,
+                           st, e->bsum, e->bdir, E, nc, ncand, e->present[cur] + c0, e->alive,
+                           msg, e->wg_agree, e->wg_key, best + c0, e->done + c0, e->sgain,
+                           e->seg[cur] + k0, mcw, (int32_t)(B - 1), n_sel, e->split_l + c0,
+                           e->split_b + c0, e->split_gain + k0);
         WGBM_LAUNCH_CHECK();
         if (tm) {
           WGBM_CHECK(hipEventRecord(timer_stop_event(tm), st));

@@ -773,8 +773,8 @@ __global__ void des_alive_kernel(const int64_t* __restrict__ seg, int32_t E, int
 
 // Era sums in the DES order: float64, each block of kDesEraBlock consecutive
 // eras summed in era order (des_block_kernel, one lane per (node, block,
-// candidate)), then the block sums in block order (des_combine_kernel, one
-// lane per (node, candidate)).  Dead segments add gain 0 and direction 0
+// candidate)), then the block sums in block order (des_combine_pick_kernel,
+// one lane per (node, candidate)).  Dead segments add gain 0 and direction 0
 // (acc + 0.0 == acc exactly): their staged values are never read, and a block
 // without a live era is skipped.
 __global__ __launch_bounds__(256) void des_block_kernel(
@@ -823,51 +823,166 @@ __global__ __launch_bounds__(256) void des_block_kernel(
   bdir[gid] = ds;
 }
 
-__global__ __launch_bounds__(256) void des_combine_kernel(
+// The block sums, the pick and the record in one launch (the staged era
+// path).  bpn = ceil(ncand / 256) workgroups per (tree-node); each thread
+// combines its candidate's block sums in block order (crit = float(sum /
+// E), agree = |sum of directions|), and each workgroup leaves a summary:
+// its largest agreement a_w and, among its candidates with agree == a_w and
+// crit > min_split_gain, the packed key of the largest crit (first flat
+// index on ties; gain_key(crit) << 32 | ~index, 0 if none).  The node's
+// pick is then the largest key among the workgroups whose a_w is the node's
+// largest agreement: a candidate qualifies only with agree == max agree,
+// and a workgroup holding one has a_w == max agree.  The last workgroup of
+// the node to arrive (done[tn], a release fence before the count, an
+// acquire fence after; no workgroup waits for another) reads the bpn
+// summaries, stores the pick to best[tn], resets done[tn], and writes
+// split_l / split_b and the chosen split's staged gain of every era (0 for
+// a dead segment), as des_finish_kernel.
+__global__ __launch_bounds__(256) void des_combine_pick_kernel(
     const double* __restrict__ bsum, const int32_t* __restrict__ bdir, int32_t E, int32_t n_tn,
     int64_t ncand, const int32_t* __restrict__ present, const uint32_t* __restrict__ alive,
-    float* __restrict__ crit, int32_t* __restrict__ agree, int32_t* __restrict__ agree_max) {
+    float min_split_gain, int32_t* __restrict__ wg_agree, unsigned long long* __restrict__ wg_key,
+    unsigned long long* __restrict__ best, uint32_t* __restrict__ done,
+    const float* __restrict__ staged, const int64_t* __restrict__ seg, float mcw, int32_t nb,
+    int32_t n_sel, int32_t* __restrict__ split_l, int32_t* __restrict__ split_b,
+    float* __restrict__ split_gain_era) {
+  __shared__ int s_a[4];
+  __shared__ unsigned long long s_k[4];
+  __shared__ int s_last;
   const int W = (E + kDesEraBlock - 1) / kDesEraBlock;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int tn = 0;
-  bool active = gid < (int64_t)n_tn * ncand;
-  int a = 0;
-  if (active) {
-    tn = (int)(gid / ncand);
-    active = present[tn] != 0;
+  const int bpn = (int)((ncand + 255) / 256);
+  const int tn = blockIdx.x / bpn;
+  const int wg = blockIdx.x - tn * bpn;
+  const int64_t c = (int64_t)wg * 256 + threadIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (!present[tn]) {  // uniform: the node is absent (no split, as des_finish_kernel)
+    if (c == 0) {
+      split_l[tn] = -1;
+      split_b[tn] = -1;
+    }
+    return;
   }
-  if (active) {
-    const int64_t c = gid - (int64_t)tn * ncand;
-    const uint32_t* al = alive + (int64_t)tn * W;
+  const uint32_t* al = alive + (int64_t)tn * W;
+  int a = -1;
+  float cr = 0.0f;
+  if (c < ncand) {
     double acc = 0.0;
     int ds = 0;
-    // blocks in groups of 8: the loads of a group are issued together (a
-    // block without a live era was never written; its value is loaded and
-    // not added)
+    // blocks in groups of 8, the group's loads issued together (a block
+    // without a live era was never written: its words are loaded and not
+    // added)
     constexpr int G = 8;
     for (int b0 = 0; b0 < W; b0 += G) {
       double v[G];
       int dv[G];
 #pragma unroll
       for (int k = 0; k < G; ++k) {
-        const int b = b0 + k < W ? b0 + k : W - 1;
-        const int64_t o = ((int64_t)tn * W + b) * ncand + c;
+        const int bk = b0 + k < W ? b0 + k : W - 1;
+        const int64_t o = ((int64_t)tn * W + bk) * ncand + c;
         v[k] = bsum[o];
         dv[k] = bdir[o];
       }
 #pragma unroll
       for (int k = 0; k < G; ++k) {
-        if (b0 + k < W && al[b0 + k] != 0) {
+        if (b0 + k < W && al[b0 + k] != 0u) {
           acc += v[k];  // block order
           ds += dv[k];
         }
       }
     }
-    crit[gid] = (float)(acc / (double)E);
+    cr = (float)(acc / (double)E);
     a = ds < 0 ? -ds : ds;
-    agree[gid] = a;
   }
-  atomic_max_grouped_i32(agree_max, tn, active, a);
+  // the workgroup's largest agreement
+  int am = a;
+  for (int off = 32; off > 0; off >>= 1) {
+    const int y = __shfl_xor(am, off, 64);
+    am = y > am ? y : am;
+  }
+  if (lane == 0) s_a[w] = am;
+  __syncthreads();
+  am = s_a[0];
+  for (int i = 1; i < 4; ++i) am = s_a[i] > am ? s_a[i] : am;
+  // its best candidate at that agreement
+  unsigned long long key = 0ull;
+  if (c < ncand && a == am && cr > min_split_gain)
+    key = ((unsigned long long)gain_key(cr) << 32) |
+          (unsigned long long)(0xffffffffu - (uint32_t)c);
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long y = __shfl_xor(key, off, 64);
+    key = y > key ? y : key;
+  }
+  if (lane == 0) s_k[w] = key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long k = s_k[0];
+    for (int i = 1; i < 4; ++i) k = s_k[i] > k ? s_k[i] : k;
+    const int64_t slot = (int64_t)tn * bpn + wg;
+    wg_agree[slot] = am;
+    wg_key[slot] = k;
+    __threadfence();  // the summary is visible before the arrival is counted
+    const uint32_t prev = atomicAdd(done + tn, 1u);
+    const bool last = prev == (uint32_t)(bpn - 1);
+    if (last) {
+      __threadfence();  // every other workgroup's summary is visible
+      done[tn] = 0u;    // ready for the next level
+    }
+    s_last = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;  // uniform
+  // the node's pick from the bpn summaries (one wave)
+  if (w == 0) {
+    int ma = -1;
+    unsigned long long mk = 0ull;
+    for (int i = lane; i < bpn; i += 64) {
+      const int ai = __hip_atomic_load(wg_agree + (int64_t)tn * bpn + i, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned long long ki = __hip_atomic_load(wg_key + (int64_t)tn * bpn + i,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (ai > ma) {
+        ma = ai;
+        mk = ki;
+      } else if (ai == ma) {
+        mk = ki > mk ? ki : mk;
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const int ya = __shfl_xor(ma, off, 64);
+      const unsigned long long yk = __shfl_xor(mk, off, 64);
+      if (ya > ma) {
+        ma = ya;
+        mk = yk;
+      } else if (ya == ma) {
+        mk = yk > mk ? yk : mk;
+      }
+    }
+    if (lane == 0) s_k[0] = mk;
+  }
+  __syncthreads();
+  const unsigned long long pick = s_k[0];
+  if (threadIdx.x == 0) best[tn] = pick;
+  if (pick == 0ull) {
+    if (threadIdx.x == 0) {
+      split_l[tn] = -1;
+      split_b[tn] = -1;
+    }
+    return;
+  }
+  const int idx = (int)(0xffffffffu - (uint32_t)(pick & 0xffffffffull));
+  if (threadIdx.x == 0) {
+    split_l[tn] = idx / nb;
+    split_b[tn] = idx - (idx / nb) * nb;
+  }
+  // the chosen split's per-era gains (record gain [tn][E]) from the staged
+  // values; none for dead segments
+  const int64_t c64 = ((int64_t)n_sel * nb + 63) / 64;
+  for (int e = threadIdx.x; e < E; e += 256) {
+    const int64_t k2 = (int64_t)tn * E + e;
+    split_gain_era[k2] = des_segment_dead(seg[k2 + 1] - seg[k2], mcw)
+                             ? 0.0f
+                             : staged[des_stage_slot(tn, e, W, c64, idx)];
+  }
 }
 
 // local index of every feature of the round's subset (local_of is -1 elsewhere)
