@@ -276,8 +276,8 @@ __global__ void des_alive_kernel(const int64_t* seg, int32_t E, int32_t n_tn, fl
                                  uint32_t* alive);
 __global__ void des_block_kernel(const float* gain, const int8_t* dir, int32_t E, int32_t n_tn,
                                  int64_t ncand, const int32_t* present, const uint32_t* alive,
-                                 double* bsum, int32_t* bdir);
-__global__ void des_combine_pick_kernel(const double* bsum, const int32_t* bdir, int32_t E,
+                                 double* bsum, int8_t* bdir);
+__global__ void des_combine_pick_kernel(const double* bsum, const int8_t* bdir, int32_t E,
                                         int32_t n_tn, int64_t ncand, const int32_t* present,
                                         const uint32_t* alive, float min_split_gain,
                                         int32_t* wg_agree, unsigned long long* wg_key,

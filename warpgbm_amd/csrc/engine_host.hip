@@ -88,7 +88,7 @@ struct Engine {
   uint32_t* done = nullptr;  // [T * nodes_max] arrival counters (zero between launches)
   uint32_t* alive = nullptr;    // [tn][W] segments that can hold a split, W = ceil(E/32)
   double* bsum = nullptr;       // [tn][W][n_sel*(B-1)] era-block gain sums
-  int32_t* bdir = nullptr;      // [tn][W][n_sel*(B-1)] era-block direction sums
+  int8_t* bdir = nullptr;       // [tn][W][n_sel*(B-1)] era-block direction sums (|.| <= 32)
   int32_t* split_l = nullptr;
   int32_t* split_b = nullptr;
   NodeRoute* nroute = nullptr;  // [T*nodes] the level's route records
@@ -183,7 +183,7 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   const int64_t W = (E + kDesEraBlock - 1) / kDesEraBlock;
   const int64_t per_node =
       e->des_direct ? des_stage_words(1, (int32_t)W, F * (B - 1)) * 5 +
-                          W * (4 + F * (B - 1) * 12) + F * (B - 1) * 8
+                          W * (4 + F * (B - 1) * 9) + F * (B - 1) * 8
                     : 2 * E * F * B * 12 + (E > 1 ? F * (B - 1) * 8 : 0);
   const int64_t budget = cfg.level_bytes > 0 ? cfg.level_bytes : (int64_t)4 << 30;
   if (T * hist_nodes_max * per_node <= budget) {

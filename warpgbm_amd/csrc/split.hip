@@ -780,7 +780,7 @@ __global__ void des_alive_kernel(const int64_t* __restrict__ seg, int32_t E, int
 __global__ __launch_bounds__(256) void des_block_kernel(
     const float* __restrict__ gain, const int8_t* __restrict__ dir, int32_t E, int32_t n_tn,
     int64_t ncand, const int32_t* __restrict__ present, const uint32_t* __restrict__ alive,
-    double* __restrict__ bsum, int32_t* __restrict__ bdir) {
+    double* __restrict__ bsum, int8_t* __restrict__ bdir) {
   const int W = (E + kDesEraBlock - 1) / kDesEraBlock;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (int64_t)n_tn * W * ncand) return;
@@ -820,7 +820,7 @@ __global__ __launch_bounds__(256) void des_block_kernel(
     }
   }
   bsum[gid] = acc;
-  bdir[gid] = ds;
+  bdir[gid] = (int8_t)ds;  // |ds| <= 32: the eras of one block
 }
 
 // The block sums, the pick and the record in one launch (the staged era
@@ -839,7 +839,7 @@ __global__ __launch_bounds__(256) void des_block_kernel(
 // split_l / split_b and the chosen split's staged gain of every era (0 for
 // a dead segment), as des_finish_kernel.
 __global__ __launch_bounds__(256) void des_combine_pick_kernel(
-    const double* __restrict__ bsum, const int32_t* __restrict__ bdir, int32_t E, int32_t n_tn,
+    const double* __restrict__ bsum, const int8_t* __restrict__ bdir, int32_t E, int32_t n_tn,
     int64_t ncand, const int32_t* __restrict__ present, const uint32_t* __restrict__ alive,
     float min_split_gain, int32_t* __restrict__ wg_agree, unsigned long long* __restrict__ wg_key,
     unsigned long long* __restrict__ best, uint32_t* __restrict__ done,
@@ -873,6 +873,12 @@ __global__ __launch_bounds__(256) void des_combine_pick_kernel(
     // added)
     constexpr int G = 8;
     for (int b0 = 0; b0 < W; b0 += G) {
+      // a group whose blocks are all dead is skipped (the alive words are
+      // the same for the whole workgroup: a uniform branch)
+      uint32_t any = 0u;
+#pragma unroll
+      for (int k = 0; k < G; ++k) any |= b0 + k < W ? al[b0 + k] : 0u;
+      if (any == 0u) continue;
       double v[G];
       int dv[G];
 #pragma unroll
@@ -880,7 +886,7 @@ __global__ __launch_bounds__(256) void des_combine_pick_kernel(
         const int bk = b0 + k < W ? b0 + k : W - 1;
         const int64_t o = ((int64_t)tn * W + bk) * ncand + c;
         v[k] = bsum[o];
-        dv[k] = bdir[o];
+        dv[k] = (int)bdir[o];
       }
 #pragma unroll
       for (int k = 0; k < G; ++k) {
