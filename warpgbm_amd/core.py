@@ -433,10 +433,12 @@ class WarpGBM(BaseEstimator, RegressorMixin):
             self._subsets_dev.append(sel)
             return sel
         # every round uses all features: one device copy for the whole fit
+        # (keyed by the device as given: torch.device("cuda") != "cuda:0")
         cached = getattr(self, "_all_features_dev", None)
-        if cached is None or cached.numel() != F or cached.device != dev:
+        if cached is None or cached.numel() != F or getattr(self, "_all_features_on", None) != dev:
             cached = torch.arange(F, dtype=torch.int32, device=dev)
             self._all_features_dev = cached
+            self._all_features_on = dev
             self._all_features_host = np.arange(F, dtype=np.int32)
         self._subsets_dev.append(self._all_features_host)
         return cached
