@@ -717,9 +717,8 @@ def des_level_rooflines(lib, X, y, era, trees=100):
       as int8 codes) plus its row id and residual (8 bytes) -- and the
       segment's gains and directions staged (5 bytes per candidate);
     * sums: the staged values read once, each live 32-era block's float64
-      sums and direction counts written and read (12 bytes per candidate
-      each way), and per present node the criterion and agreement written
-      and read (16 bytes per candidate)."""
+      sum and int8 direction count written and read (9 bytes per candidate
+      each way); the criterion, agreement and pick stay on chip."""
     import torch
 
     from warpgbm_amd import WarpGBM
@@ -775,7 +774,7 @@ def des_level_rooflines(lib, X, y, era, trees=100):
     for d in range(D):
         pairs = N >= 96 * (1 << d) * E  # the engine's pair-code rule (kDesPairMinRows)
         rb = rows_alive[d] * ((F + 1) // 2 + 8 if pairs else F + 8) + segs_alive[d] * ncand * 5
-        sb = segs_alive[d] * ncand * 5 + blocks_live[d] * ncand * 24 + present[d] * ncand * 16
+        sb = segs_alive[d] * ncand * 5 + blocks_live[d] * ncand * 18
         ent = {"depth": d, "codes": "pair" if pairs else "int8"}
         for name, nbytes in (("rows", rb), ("sums", sb)):
             tot = C.c_double()
@@ -797,8 +796,8 @@ def des_level_rooflines(lib, X, y, era, trees=100):
             "frac": round(gbs / HBM_PEAK_GBS, 4), "trees": trees, "levels": levels,
             "bytes_are": "per depth, summed over the trees: live (node, era) segments' rows "
                          "(codes + row id + residual) and staged per-era gains (rows); staged "
-                         "gains read, 32-era block sums written and read, per-node criteria "
-                         "(sums); timed with HIP events around the launches"}
+                         "gains read, 32-era block sums written and read (sums); timed with "
+                         "HIP events around the launches"}
 
 
 def run_extra(cfg, n_runs=2, cpu=None, c4_trees=100):

@@ -543,7 +543,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                              0, st, e->seg[cur] + k0, E, nc, mcw, e->alive);
           WGBM_LAUNCH_CHECK();
         }
-        hipLaunchKernelGGL(des_block_kernel, dim3(blocks_for((int64_t)nc * W * ncand, 256)),
+        hipLaunchKernelGGL(des_block_kernel,
+                           dim3(blocks_for((int64_t)nc * W * ((ncand + 63) / 64) * 64, 256)),
                            dim3(256), 0, st, e->sgain, e->sdir, E, nc, ncand,
                            e->present[cur] + c0, e->alive, e->bsum, e->bdir);
         WGBM_LAUNCH_CHECK();

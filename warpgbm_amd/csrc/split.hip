@@ -782,18 +782,36 @@ __global__ __launch_bounds__(256) void des_block_kernel(
     int64_t ncand, const int32_t* __restrict__ present, const uint32_t* __restrict__ alive,
     double* __restrict__ bsum, int8_t* __restrict__ bdir) {
   const int W = (E + kDesEraBlock - 1) / kDesEraBlock;
+  const int64_t c64 = (ncand + 63) / 64;
+  // thread per (tree-node, block, candidate) with the candidates padded to
+  // whole groups of 64: every wave is one (tree-node, block, 64-group)
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (int64_t)n_tn * W * ncand) return;
-  const int64_t c = gid % ncand;
-  const int64_t tb = gid / ncand;  // tn * W + block
+  if (gid >= (int64_t)n_tn * W * c64 * 64) return;  // whole waves
+  const int64_t tb = gid / (c64 * 64);  // tn * W + block
+  const int64_t c = gid - tb * (c64 * 64);
   const int tn = (int)(tb / W);
   const int blk = (int)(tb - (int64_t)tn * W);
-  if (!present[tn]) return;
+  if (!present[tn]) return;  // wave-uniform
   const uint32_t m = alive[tb];
   if (m == 0) return;
   // this block's 32 eras of the candidate: slots base + 64 * k (block-major
-  // staging layout)
-  const int64_t base = des_stage_slot(tn, blk * kDesEraBlock, W, (ncand + 63) / 64, c);
+  // staging layout).  The loads go through raw buffer descriptors over the
+  // candidate's 64-group of the block (32 x 64 slots): a dead era's load
+  // gets an offset past the descriptor's size, which returns 0 without a
+  // memory access, so no load is a branch (a predicated load would become a
+  // branch with a wait after every load) and dead eras cost no bytes.
+  // the wave's 64 candidates are one group (c % 64 == lane): its slot base
+  // is wave-uniform (stated to the compiler, which the descriptor needs)
+  const int tnu = __builtin_amdgcn_readfirstlane(tn);
+  const int blku = __builtin_amdgcn_readfirstlane(blk);
+  const int64_t cw = (int64_t)__builtin_amdgcn_readfirstlane((int)(c - c % 64));
+  const int64_t g0 = des_stage_slot(tnu, blku * kDesEraBlock, W, c64, cw);
+  const uint32_t cl = (uint32_t)(c % 64);
+  const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(gain + g0), (short)0, (int)(kDesEraBlock * 64 * sizeof(float)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(dir + g0), (short)0, (int)(kDesEraBlock * 64), 0x00020000);
+  constexpr uint32_t kPast = 0x80000000u;  // beyond either descriptor
   double acc = 0.0;
   int ds = 0;
   constexpr int kHalf = kDesEraBlock / 2;
@@ -801,16 +819,16 @@ __global__ __launch_bounds__(256) void des_block_kernel(
   for (int h = 0; h < 2; ++h) {
     float gv[kHalf];
     int dv[kHalf];
-    // every slot of the block exists (the layout has 32 per block), so the
-    // loads are unconditional and issued together; a dead era's slot was
-    // never written and its value is not added (a predicated load would
-    // become a branch with a wait after every load)
 #pragma unroll
     for (int k = 0; k < kHalf; ++k) {
       const int kk = h * kHalf + k;
-      gv[k] = gain[base + (int64_t)kk * 64];
-      dv[k] = (int)dir[base + (int64_t)kk * 64];
+      const bool live = (m >> kk) & 1u;  // implies the era exists
+      const uint32_t slot = (uint32_t)kk * 64u + cl;
+      gv[k] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rg, live ? slot * 4u : kPast, 0, 0));
+      dv[k] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rd, live ? slot : kPast, 0, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);  // the half's loads are all issued before its adds
 #pragma unroll
     for (int k = 0; k < kHalf; ++k) {
       if ((m >> (h * kHalf + k)) & 1u) {  // a live era (it exists)
@@ -819,8 +837,10 @@ __global__ __launch_bounds__(256) void des_block_kernel(
       }
     }
   }
-  bsum[gid] = acc;
-  bdir[gid] = (int8_t)ds;  // |ds| <= 32: the eras of one block
+  if (c < ncand) {  // padding lanes of the last group store nothing
+    bsum[tb * ncand + c] = acc;
+    bdir[tb * ncand + c] = (int8_t)ds;  // |ds| <= 32: the eras of one block
+  }
 }
 
 // The block sums, the pick and the record in one launch (the staged era
