@@ -210,3 +210,45 @@ def test_oracle_era_cast_matches_torch():
                 np.array([True, False]), rng.integers(0, 9, 30).astype(np.int16)):
         want = torch.from_numpy(np.asarray(era)).type(torch.int32).numpy()
         assert np.array_equal(gbm.era_ids_int32(era), want), era.dtype
+
+
+def test_heaps_to_dicts_random_records():
+    """The C tree builder against a recursive walk of the heap records on
+    random trees of depth 1-8: absent roots (None), absent children of a
+    split (None), NaN leaves, counts beyond 32 bits, and leaves below a leaf
+    (ignored)."""
+    rng = np.random.default_rng(3)
+
+    def walk(f, b, v, c, h):
+        if h >= len(f) or f[h] < -1:
+            return None
+        if f[h] == -1:
+            return {"leaf_value": float(v[h]), "samples": int(c[h])}
+        return {"feature": int(f[h]), "bin": int(b[h]), "left": walk(f, b, v, c, 2 * h + 1),
+                "right": walk(f, b, v, c, 2 * h + 2)}
+
+    for D in (1, 3, 6, 8):
+        H = (1 << (D + 1)) - 1
+        M = 60
+        feat = rng.choice([-2, -1, 0, 5, 77], size=(M, H), p=[0.2, 0.3, 0.2, 0.2, 0.1])
+        feat = feat.astype(np.int32)
+        feat[:, (H - 1) // 2:] = np.minimum(feat[:, (H - 1) // 2:], -1)  # no split at depth D
+        bin_ = rng.integers(-5, 127, (M, H)).astype(np.int32)
+        leaf = rng.standard_normal((M, H)).astype(np.float32)
+        leaf[rng.random((M, H)) < 0.05] = np.nan
+        cnt = rng.integers(0, 2**40, (M, H)).astype(np.int64)
+        got = _heaps_to_dicts(feat.reshape(3, M // 3, H), bin_.reshape(3, M // 3, H),
+                              leaf.reshape(3, M // 3, H), cnt.reshape(3, M // 3, H))
+        want = [walk(feat[t], bin_[t], leaf[t], cnt[t], 0) for t in range(M)]
+        # repr: NaN leaves compare equal as text; key order is the reference's
+        assert repr(got) == repr(want), D
+    with pytest.raises(ValueError, match="no child slots"):
+        _heaps_to_dicts(np.array([[-1, 2, -1]], np.int32), np.zeros((1, 3), np.int32),
+                        np.zeros((1, 3), np.float32), np.zeros((1, 3), np.int64))
+    from warpgbm_amd import _trees
+    with pytest.raises(ValueError, match="different lengths"):
+        _trees.heaps_to_dicts(np.zeros(7, np.int32), np.zeros(7, np.int32),
+                              np.zeros(6, np.float32), np.zeros(7, np.int64), 7)
+    with pytest.raises(TypeError):
+        _trees.heaps_to_dicts(np.zeros(7, np.int64), np.zeros(7, np.int32),
+                              np.zeros(7, np.float32), np.zeros(7, np.int64), 7)

@@ -1,10 +1,12 @@
-"""Build the HIP library ``warpgbm_amd/libwarpgbm_amd.so`` for gfx950.
+"""Build the HIP library ``warpgbm_amd/libwarpgbm_amd.so`` for gfx950 and the
+host extension ``warpgbm_amd._trees``.
 
 Every ``csrc/*.hip`` file is compiled by hipcc to an object in ``_build/`` and
 the objects are linked into one shared library that exports the C ABI of
-``include/warpgbm_amd.h``.  Run ``python -m warpgbm_amd.build`` (or call
-:func:`build`); the library is written in-tree so that it travels with the
-source tree.
+``include/warpgbm_amd.h``.  ``csrc/trees.c`` (tree records -> the reference's
+tree dicts, a CPython extension) is compiled by the host C compiler.  Run
+``python -m warpgbm_amd.build`` (or call :func:`build`); both are written
+in-tree so that they travel with the source tree.
 """
 from __future__ import annotations
 
@@ -13,6 +15,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -52,8 +55,28 @@ def _compile(src: Path) -> Path:
     return out
 
 
+def build_trees(verbose: bool = False) -> Path:
+    """Compile the ``_trees`` CPython extension (plain C, no GPU code)."""
+    out = PKG / ("_trees" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("no host C compiler (gcc) found to build warpgbm_amd._trees")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}",
+           str(CSRC / "trees.c"), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"gcc failed for trees.c:\n{r.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile all HIP sources and link the shared library; returns its path."""
+    """Compile all HIP sources and link the shared library (returns its
+    path), then the ``_trees`` host extension."""
+    build_trees(verbose)
     OBJ.mkdir(parents=True, exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
     jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))

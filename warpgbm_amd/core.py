@@ -19,7 +19,6 @@ from __future__ import annotations
 
 import gc
 import pickle
-from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import torch
@@ -57,14 +56,32 @@ class _Phases:
             print(f"{what} phases: " + ", ".join(f"{n} {dt * 1e3:.1f} ms" for n, dt in self.items))
 
 
+_SIDE_STREAMS = {}
+
+
+def _side_stream(dev):
+    """One side stream per device for the record copies, created once (a
+    stream's creation can take milliseconds)."""
+    dev = torch.device(dev)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=key)
+    return _SIDE_STREAMS[key]
+
+
 class _RecordStream:
     """The engine's per-round tree records (device heaps [rounds, trees, H])
     copied to pinned host memory in blocks of rounds while later rounds run,
-    each landed block turned into reference tree dicts by a worker thread:
-    the dict building overlaps the launches of later rounds (which release
-    the interpreter lock while in the library) and the GPU's work."""
+    and each landed block turned into reference tree dicts (by the C
+    extension ``_trees``) on the launching thread, a few trees at a time, only
+    while the GPU still has the previous round queued: the conversion uses
+    the host's slack between launches and never holds the interpreter lock
+    against them (a converter thread did, and left the GPU idle at round
+    starts).  What remains when the last round is enqueued is converted by
+    ``finish``."""
 
-    BLOCK = 8  # rounds per copy
+    BLOCK = 8   # rounds per copy
+    CHUNK = 16  # trees per conversion step (~0.3 ms of host time at depth 6)
 
     def __init__(self, rec):
         self.rec = rec
@@ -72,71 +89,110 @@ class _RecordStream:
                      for k in ("feat", "bin", "leaf", "count")}
         self.pending = []   # (first round, end round, event) of issued copies
         self.copied = 0     # rounds whose copy has been issued
-        self.blocks = []    # futures of per-block (tree lists, importance nodes)
+        self.landed = []    # [r0, r1, trees converted so far] of landed blocks, in order
+        self.flat = []      # tree dicts of the converted trees, rounds then trees
         self.trees = []     # per finished round: its list of tree dicts
-        # per finished block: the records' rows of its internal nodes (rounds,
+        # per converted block: the records' rows of its internal nodes (rounds,
         # then trees in order, nodes in pre-order) and their split features
         self.nodes = []
-        self.pool = ThreadPoolExecutor(max_workers=1)
+        self.prev_ev = None  # completion of the round before the last enqueued one
+        self.last_ev = None
+        self.side = None     # the copies' stream
         # the tree dicts form no reference cycles; pausing the cyclic
         # collector keeps it from re-walking the growing forest on every
         # allocation threshold (about 4x faster at 2000 trees of depth 6)
         self.gc_was_on = gc.isenabled()
+        self.closed = False
         gc.disable()
 
-    def round_done(self, j):
-        """Round j has been enqueued: issue a block copy every BLOCK rounds
-        and hand the blocks whose copies have landed to the worker."""
-        if (j + 1) % self.BLOCK == 0:
+    def round_done(self, j, n_rounds):
+        """Round j of n_rounds has been enqueued: issue a block copy every
+        BLOCK rounds (every round in the last block, so that little is left
+        to convert when the GPU finishes), then convert landed trees while
+        the GPU is still busy with round j - 1 (so round j stays queued
+        behind it)."""
+        if (j + 1) % self.BLOCK == 0 or j + self.BLOCK >= n_rounds:
             self.issue(j + 1)
-        self.drain(wait=False)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.prev_ev, self.last_ev = self.last_ev, ev
+        while self.prev_ev is not None and not self.prev_ev.query():
+            if not self._step():
+                break
 
     def issue(self, end):
+        """Copy rounds [copied, end) to the host on a side stream (after the
+        compute stream's work so far), so that the copies' host-visible
+        writes never stall the compute stream."""
         if end <= self.copied:
             return
         r0 = self.copied
-        for k, h in self.host.items():
-            h[r0:end].copy_(self.rec[k][r0:end], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
+        if self.side is None:
+            self.side = _side_stream(self.rec["feat"].device)
+        ready = torch.cuda.Event()
+        ready.record()
+        with torch.cuda.stream(self.side):
+            self.side.wait_event(ready)
+            for k, h in self.host.items():
+                h[r0:end].copy_(self.rec[k][r0:end], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(self.side)
         self.pending.append((r0, end, ev))
         self.copied = end
 
-    def _convert(self, r0, r1):
-        h = {k: v[r0:r1].numpy() for k, v in self.host.items()}
-        n_trees, H = h["feat"].shape[1], h["feat"].shape[2]
-        flat = _heaps_to_dicts(h["feat"], h["bin"], h["leaf"], h["count"])
-        # the block's internal nodes in the importance order
+    def _step(self, wait=False):
+        """Convert up to CHUNK trees of the oldest landed block; False when
+        no landed block has trees left."""
+        # landed copies; with wait, block for the oldest one only when none
+        # has landed (the rest keep landing while this one is converted)
+        while self.pending and (self.pending[0][2].query() or (wait and not self.landed)):
+            r0, r1, ev = self.pending.pop(0)
+            ev.synchronize()
+            self.landed.append([r0, r1, 0])
+        if not self.landed:
+            return False
+        blk = self.landed[0]
+        r0, r1, done = blk
+        n_trees, H = self.host["feat"].shape[1], self.host["feat"].shape[2]
+        total = (r1 - r0) * n_trees
+        hi = min(total, done + self.CHUNK)
+        t0, t1 = r0 * n_trees + done, r0 * n_trees + hi
+        h = {k: v.view(-1, H)[t0:t1].numpy() for k, v in self.host.items()}
+        self.flat.extend(_heaps_to_dicts(h["feat"], h["bin"], h["leaf"], h["count"]))
+        blk[2] = hi
+        if hi == total:
+            self.landed.pop(0)
+            self.nodes.append(self._block_nodes(r0, r1))
+        return True
+
+    def _block_nodes(self, r0, r1):
+        """The block's internal nodes in the importance order."""
+        feat = self.host["feat"][r0:r1].numpy()
+        n_trees, H = feat.shape[1], feat.shape[2]
         po = _preorder_heap(H).astype(np.int64)
-        fp = h["feat"][:, :, po]
+        fp = feat[:, :, po]
         internal = fp >= 0
         base = (np.arange(r0, r1, dtype=np.int64)[:, None, None] * n_trees
                 + np.arange(n_trees, dtype=np.int64)[None, :, None]) * H
-        nodes = ((base + po[None, None, :])[internal], fp[internal])
-        return [flat[j * n_trees:(j + 1) * n_trees] for j in range(r1 - r0)], nodes
-
-    def drain(self, wait):
-        while self.pending and (wait or self.pending[0][2].query()):
-            r0, r1, ev = self.pending.pop(0)
-            ev.synchronize()
-            self.blocks.append(self.pool.submit(self._convert, r0, r1))
+        return (base + po[None, None, :])[internal], fp[internal]
 
     def finish(self, done):
         try:
             self.issue(done)
-            self.drain(wait=True)
-            for f in self.blocks:  # block order
-                trees, nodes = f.result()
-                self.trees.extend(trees)
-                self.nodes.append(nodes)
+            while self._step(wait=True):
+                pass
+            n_trees = self.host["feat"].shape[1]
+            self.trees = [self.flat[j * n_trees:(j + 1) * n_trees] for j in range(done)]
         finally:
             self.close()
 
     def close(self):
-        """Stop the worker and restore the collector (also after an error)."""
-        if self.pool is not None:
-            self.pool.shutdown(wait=True)
-            self.pool = None
+        """Restore the collector (also after an error, once the copies in
+        flight have landed)."""
+        if not self.closed:
+            self.closed = True
+            for _, _, ev in self.pending:
+                ev.synchronize()
             if self.gc_was_on:
                 gc.enable()
 
@@ -518,7 +574,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                     feat_sel = self._feature_subset(dev)
                     eng.round(Y_gpu, preds, feat_sel, {k: v[j] for k, v in rec.items()})
                     done = j + 1
-                    stream.round_done(j)
+                    stream.round_done(j, n_new)
                     if self._eval is not None:
                         D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
                                        rec["leaf"][j], 1, 1, self.max_depth, self.learning_rate,
@@ -584,7 +640,7 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                     feat_sel = self._feature_subset(dev)
                     eng.round(labels, scores, feat_sel, {k: v[j] for k, v in rec.items()})
                     done = j + 1
-                    stream.round_done(j)
+                    stream.round_done(j, n_new)
                     if self._eval is not None:
                         D.predict_heap(self._eval["codes"], rec["feat"][j], rec["bin"][j],
                                        rec["leaf"][j], 1, K, self.max_depth, self.learning_rate,
@@ -708,8 +764,8 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         # importance: every internal node of every tree, trees in order and
         # nodes in pre-order, one float32 add per node and era in exactly that
         # sequence, on the device from the per-era gain records; the nodes
-        # (listed by the record stream's worker, block by block while later
-        # rounds ran) are grouped by feature here (a stable sort keeps their
+        # (listed by the record stream block by block while later rounds
+        # ran) are grouped by feature here (a stable sort keeps their
         # order), so each (feature, era) word is one device thread's sum
         rows = (np.concatenate([r for r, _ in stream.nodes]) if stream.nodes
                 else np.zeros(0, np.int64))
@@ -1012,29 +1068,18 @@ class WarpGBM(BaseEstimator, RegressorMixin):
 def _heaps_to_dicts(feat, bin_, leaf, count):
     """Reference tree dicts of many heap records ([..., H] arrays, trees in
     row-major order; feat -1 leaf, -2 absent, >= 0 split; children of h at
-    2h+1 / 2h+2), each built bottom-up.  Only the present nodes' values are
-    turned into Python objects."""
+    2h+1 / 2h+2), each built bottom-up by the C extension ``_trees``.  A tree
+    with no root is None, as is an absent child of a split."""
+    try:
+        from . import _trees
+    except ImportError as e:  # built with the HIP library by warpgbm_amd.build
+        raise ImportError("warpgbm_amd._trees is not built; run `python -m warpgbm_amd.build`") \
+            from e
     H = feat.shape[-1]
-    f2 = feat.reshape(-1, H)
-    pres = f2 >= -1
-    h_l = np.nonzero(pres)[1].tolist()
-    ends = np.cumsum(np.count_nonzero(pres, axis=1)).tolist()
-    f_l = f2[pres].tolist()
-    b_l = bin_.reshape(-1, H)[pres].tolist()
-    v_l = leaf.reshape(-1, H)[pres].tolist()
-    c_l = count.reshape(-1, H)[pres].tolist()
-    out = []
-    start = 0
-    for end in ends:
-        nodes = [None] * H
-        for i in range(end - 1, start - 1, -1):
-            h, f = h_l[i], f_l[i]
-            nodes[h] = ({"feature": f, "bin": b_l[i], "left": nodes[2 * h + 1],
-                         "right": nodes[2 * h + 2]} if f >= 0
-                        else {"leaf_value": v_l[i], "samples": c_l[i]})
-        out.append(nodes[0])
-        start = end
-    return out
+    return _trees.heaps_to_dicts(np.ascontiguousarray(feat, dtype=np.int32),
+                                 np.ascontiguousarray(bin_, dtype=np.int32),
+                                 np.ascontiguousarray(leaf, dtype=np.float32),
+                                 np.ascontiguousarray(count, dtype=np.int64), H)
 
 
 def _preorder_heap(H):

@@ -383,7 +383,7 @@ struct LevelPlan {
   int64_t rows_bound = 0, R = 0, max_tiles = 0;
 };
 
-static int level_plan(Engine* e, int d, LevelPlan* lp) {
+static void level_plan_sizes(const Engine* e, int d, LevelPlan* lp) {
   const int64_t T = e->c.n_trees, N = e->c.n_rows, E = e->c.num_eras;
   const int64_t nodes = int64_t(1) << d;
   lp->n_list = (int32_t)(d == 0 ? T * nodes * E : 2 * T * (nodes / 2) * E);
@@ -392,7 +392,27 @@ static int level_plan(Engine* e, int d, LevelPlan* lp) {
   lp->rows_bound = d == 0 ? T * N : (T * N) / 2;
   lp->R = pick_tile_rows(e, lp->rows_bound);
   lp->max_tiles = (T * N) / lp->R + lp->n_list + 1;
+}
+
+static int level_plan(Engine* e, int d, LevelPlan* lp) {
+  level_plan_sizes(e, d, lp);
   return ensure_tiles(e, lp->max_tiles);
+}
+
+// the tile buffers of every whole level a round histograms, sized once before
+// the first round's launches: growing them level by level would synchronise
+// the device (a buffer in use is freed only after a sync) at each depth
+static int presize_levels(Engine* e) {
+  if (e->des_direct) return 0;
+  int64_t mt = 0;
+  for (int d = 0; d < e->c.max_depth; ++d) {
+    // levels take the subtraction path while every level so far fits whole
+    if (((int64_t)e->c.n_trees << d) > e->nc_max) break;
+    LevelPlan lp;
+    level_plan_sizes(e, d, &lp);
+    mt = std::max(mt, lp.max_tiles);
+  }
+  return mt > 0 ? ensure_tiles(e, mt) : 0;
 }
 
 // histogram tiles of one chunk of a level (n_list keys, the chunk's present
@@ -416,6 +436,10 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   WGBM_REQUIRE(rec.H == e->H, "engine_round: record has H=%d, expected %d", rec.H, e->H);
   const int T = c.n_trees, E = c.num_eras, F = c.n_feats, B = c.num_bins, D = c.max_depth;
   const int64_t N = c.n_rows;
+  if (!e->part) {
+    const int r = presize_levels(e);
+    if (r) return r;
+  }
 
   // residuals and quantisation shifts (per-workgroup maxima, then one
   // workgroup per tree reduces them)
