@@ -34,7 +34,8 @@ Metric: histogram GB/s (% HBM peak) + train/infer seconds,
   DES) and C5 (softmax) likewise, C1 fit seconds on the GPU.
 * kernels: achieved HBM bandwidth of quantile edges, binning and inference on
   C3's held-out matrix resident on the device (algorithmic bytes / median
-  call time).
+  call time); quantile_select_staged is the part of the edges that a fit runs
+  after its upload (the column staging rides on the transfer).
 
 * c4_des: the era path (DES) on C4 per depth: per-era gain kernel ("rows")
   and era sums + pick ("sums"), HIP-event times against algorithmic bytes
@@ -609,6 +610,18 @@ def c3_kernel_rooflines(m, Xt, dropin=None):
     edges = D.quantile_edges(Xd, B)
     put("quantile_edges", timed(lambda: D.quantile_edges(Xd, B)), n * F * 4 + F * (B - 1) * 4,
         "X read once + edges (moved: X read and its values written transposed, then two scans of each transposed column)")
+    # the fit's split of the same work: the staging (X's values transposed
+    # into columns) runs block by block on the copy stream while the upload
+    # is in flight, and only the selection over the staged columns follows
+    # the transfer
+    stq = D.QuantileStage(n, F, dev)
+    stq.stage(Xd, 0, n)
+    e2 = stq.edges(B)
+    assert torch.equal(e2.view(torch.int32), edges.view(torch.int32)), "staged edges differ"
+    put("quantile_select_staged", timed(lambda: stq.edges(B)), n * F * 4 + F * (B - 1) * 4,
+        "X's values read once + edges (moved: two scans of each staged column; the fit stages "
+        "the columns behind the PCIe upload, wgbm_quantile_stage_rows per row block)")
+    del stq, e2
     put("bin_matrix", timed(lambda: D.bin_matrix(Xd, edges, with_cm=False)),
         n * F * 4 + n * F + F * (B - 1) * 4, "X + codes (row-major) + edges")
     codes = D.bin_matrix(Xd, edges, with_cm=False)

@@ -151,6 +151,27 @@ int wgbm_quantile_edges(const float* sorted, int64_t n, int32_t n_feats, const f
 int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride,
                                const float* q, int32_t nq, float* edges, void* stream);
 
+/* wgbm_quantile_edges_matrix in two steps, for a matrix that reaches the
+ * device in row blocks (the staged upload of warpgbm/core.py:527-534's input,
+ * whose torch.quantile call needs the whole column): each block's values are
+ * staged as soon as it lands, the edges taken once every row is staged.
+ *
+ * stage_rows: rows [row0, row0 + rows) of the matrix, X pointing at the first
+ * of them (row stride x_stride elements), into the column-major staging array
+ * cols uint32 [n_feats][cols_stride] at column offset row0, and the running
+ * per-column extremes kmin / kmax uint32 [n_feats] (order-preserving keys;
+ * the caller sets them to 0xffffffff / 0 before the first block).  row0 is a
+ * multiple of 4; cols_stride is a multiple of 32 and at least the final row
+ * count n.  Blocks may be staged in any order, on one stream.
+ * edges_staged: the edges of all n staged rows, bit-identical to
+ * wgbm_quantile_edges_matrix on the whole matrix.  n <= 2^24. */
+int wgbm_quantile_stage_rows(const float* X, int64_t rows, int32_t n_feats, int64_t x_stride,
+                             int64_t row0, uint32_t* cols, int64_t cols_stride, uint32_t* kmin,
+                             uint32_t* kmax, void* stream);
+int wgbm_quantile_edges_staged(const uint32_t* cols, int64_t n, int32_t n_feats,
+                               int64_t cols_stride, const uint32_t* kmin, const uint32_t* kmax,
+                               const float* q, int32_t nq, float* edges, void* stream);
+
 /* Batched binner (the per-feature loop of warpgbm/core.py:527-538 and
  * 908-913 in one launch).  X float32 [n, n_feats] with row stride x_stride
  * (elements); edges float32 [n_feats, n_edges] sorted per feature.  Writes

@@ -656,6 +656,61 @@ def test_quantile_selection_value_buckets_bit_exact(gpu, B):
     assert np.array_equal(bits(got[cols]), bits(tq))
 
 
+@pytest.mark.parametrize("B", [5, 32, 127])
+def test_staged_quantile_edges_bit_exact(gpu, B):
+    """Edges taken from columns staged block by block during the upload
+    (upload_float_with_edges: several blocks, a ragged last one, float64
+    input rounded while staging) equal those of the whole resident matrix and
+    the oracle, with ties, outliers, infinities, a constant column and a NaN
+    column; the device copy is X itself."""
+    print_case("upload_float_with_edges", B)
+    rng = np.random.default_rng(200 + B)
+    n, F = 300_001, 12
+    X = rng.standard_normal((n, F))                  # float64: rounded while staging
+    X[:, 1] = rng.integers(0, 4, n)                  # heavy ties
+    X[7, 2] = 1e30                                   # outlier stretches the range
+    X[11, 3] = np.inf
+    X[13, 4] = -np.inf
+    X[:, 5] = 2.5                                    # constant
+    X[n // 3, 6] = np.nan                            # NaN column -> NaN edges
+    X[:, 7] = rng.exponential(1.0, n) ** 3           # heavy tail
+    saved = D._STAGE_BYTES
+    # the pinned staging buffers are allocated once at the current size:
+    # dropped before and after, so that they are re-made at each size
+    with D._stage_lock:
+        D._stage_bufs.clear()
+    try:
+        D._STAGE_BYTES = 1 << 20                     # ~22 blocks of 21,824 rows
+        assert D._streams(X, 4)
+        Xd, got = D.upload_float_with_edges(X, dev, B)
+    finally:
+        D._STAGE_BYTES = saved
+        torch.cuda.synchronize()
+        with D._stage_lock:
+            D._stage_bufs.clear()
+    X32 = X.astype(F32)
+    assert np.array_equal(bits(Xd.cpu().numpy()), bits(X32))  # NaN included
+    whole = D.quantile_edges(D.upload_float(X32, dev), B).cpu().numpy()
+    got = got.cpu().numpy()
+    assert np.array_equal(bits(got), bits(whole))
+    assert np.array_equal(bits(got), bits(ops.quantile_edges(X32, B)))
+
+
+def test_staged_quantile_rows_validation(gpu):
+    """The staging entry point refuses rows that do not start on a multiple
+    of 4 or that run past the column stride (host checks, no launch)."""
+    lib = _lib.load()
+    X = torch.zeros((64, 3), dtype=torch.float32, device=dev)
+    cols = torch.zeros((3, 64), dtype=torch.int32, device=dev)
+    km = torch.zeros(6, dtype=torch.int32, device=dev)
+    args = (X.data_ptr(), 8, 3, 3)
+    tail = (cols.data_ptr(), 64, km.data_ptr(), km[3:].data_ptr(), None)
+    assert lib.wgbm_quantile_stage_rows(*args, 2, *tail) != 0
+    assert lib.wgbm_quantile_stage_rows(*args, 60, *tail) != 0
+    assert lib.wgbm_quantile_stage_rows(*args, 56, *tail) == 0
+    torch.cuda.synchronize()
+
+
 def test_staged_upload_exact(gpu):
     """The pinned, multi-threaded upload reproduces X (float64 input rounded
     to float32) exactly, including a ragged last chunk."""

@@ -36,6 +36,8 @@ SIGNATURES = {
                                                   _i32, _i32, _p, _p, _p]),
     "wgbm_quantile_edges": (C.c_int, [_p, _i64, _i32, _p, _i32, _p, _p]),
     "wgbm_quantile_edges_matrix": (C.c_int, [_p, _i64, _i32, _i64, _p, _i32, _p, _p]),
+    "wgbm_quantile_stage_rows": (C.c_int, [_p, _i64, _i32, _i64, _i64, _p, _i64, _p, _p, _p]),
+    "wgbm_quantile_edges_staged": (C.c_int, [_p, _i64, _i32, _i64, _p, _p, _p, _i32, _p, _p]),
     "wgbm_bin_matrix": (C.c_int, [_p, _i64, _i32, _i64, _p, _i32, _p, _i64, _p, _p]),
     "wgbm_copy_prebinned": (C.c_int, [_p, _i64, _i32, _i64, _p, _i64, _p, _i32, _p, _p]),
     "wgbm_predict_heap": (C.c_int, [_p, _i64, _i64, _i32, _p, _p, _p, _i32, _i32, _i32, _i32,

@@ -428,9 +428,13 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         else:
             print("quantile binning.")
             if Xd is None:
-                Xd = D.upload_float(X_np, dev)
-            ph.mark("upload")
-            bin_edges = D.quantile_edges(Xd, self.num_bins)
+                # the selection's staging rides on the upload (edges are
+                # ready shortly after the last row block lands)
+                Xd, bin_edges = D.upload_float_with_edges(X_np, dev, self.num_bins)
+                ph.mark("upload")
+            else:
+                ph.mark("upload")
+                bin_edges = D.quantile_edges(Xd, self.num_bins)
             ph.mark("edges")
             codes = D.bin_matrix(Xd, bin_edges, with_cm=True)
             ph.mark("bin")

@@ -519,6 +519,66 @@ int wgbm_quantile_edges(const float* sorted, int64_t n, int32_t n_feats, const f
   return 0;
 }
 
+// values of rows [0, rows) of X (row stride x_stride) into the column-major
+// key array keys (column f at keys + f * ks; the caller offsets keys by the
+// first row), and the columns' extremes into kmin / kmax
+static int launch_stage_rows(const float* X, int64_t rows, int32_t fc, int64_t x_stride,
+                             uint32_t* keys, int64_t ks, uint32_t* kmin, uint32_t* kmax,
+                             hipStream_t st) {
+  const dim3 tg((unsigned)wgbm_xcd_grid((int64_t)nblocks(rows, kTransRows) * nblocks(fc, 64)));
+  // 16-byte row loads when every row starts on 16 bytes
+  const bool vec = ((uintptr_t)X % 16) == 0 && x_stride % 4 == 0;
+  if (vec)
+    hipLaunchKernelGGL(transpose_values_kernel<true>, tg, dim3(256), 0, st, X, rows, fc, x_stride,
+                       ks, keys, kmin, kmax);
+  else
+    hipLaunchKernelGGL(transpose_values_kernel<false>, tg, dim3(256), 0, st, X, rows, fc,
+                       x_stride, ks, keys, kmin, kmax);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+// the selection over staged columns (per-feature buffers from the scratch pool)
+static int launch_select(const uint32_t* keys, int64_t n, int64_t ks, int32_t fc, const float* q,
+                         int32_t nq, float* edges, const uint32_t* kmin, const uint32_t* kmax,
+                         hipStream_t st) {
+  // per-feature buffer of the keys of the target buckets (a quarter of the
+  // column; a column with more falls back to full scans)
+  const int64_t ccap = std::max<int64_t>(1024, n / 4);
+  uint32_t* cbuf = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (size_t)((int64_t)fc * ccap), 10);
+  WGBM_REQUIRE(cbuf, "scratch allocation failed");
+  hipLaunchKernelGGL(quantile_select_kernel, dim3(fc), dim3(512), 0, st, keys, n, ks, fc, q, nq,
+                     edges, kmin, kmax, cbuf, ccap);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
+int wgbm_quantile_stage_rows(const float* X, int64_t rows, int32_t n_feats, int64_t x_stride,
+                             int64_t row0, uint32_t* cols, int64_t cols_stride, uint32_t* kmin,
+                             uint32_t* kmax, void* stream) {
+  WGBM_REQUIRE(rows >= 0 && n_feats >= 0 && x_stride >= n_feats && row0 >= 0,
+               "bad quantile staging shape");
+  WGBM_REQUIRE(row0 % 4 == 0 && cols_stride % 32 == 0 && row0 + rows <= cols_stride,
+               "staged rows must start on a multiple of 4 inside the column stride "
+               "(a multiple of 32)");
+  WGBM_REQUIRE(cols_stride <= (int64_t(1) << 24) + 32, "quantile input too large (n > 2^24)");
+  if (rows == 0 || n_feats == 0) return 0;
+  WGBM_REQUIRE(X && cols && kmin && kmax, "null pointer");
+  return launch_stage_rows(X, rows, n_feats, x_stride, cols + row0, cols_stride, kmin, kmax,
+                           S(stream));
+}
+
+int wgbm_quantile_edges_staged(const uint32_t* cols, int64_t n, int32_t n_feats,
+                               int64_t cols_stride, const uint32_t* kmin, const uint32_t* kmax,
+                               const float* q, int32_t nq, float* edges, void* stream) {
+  WGBM_REQUIRE(n >= 1 && n_feats >= 0 && nq >= 0 && nq <= 126, "bad quantile shape");
+  WGBM_REQUIRE(n <= (int64_t(1) << 24), "quantile input too large (n > 2^24), as torch.quantile");
+  WGBM_REQUIRE(cols_stride % 32 == 0 && cols_stride >= n, "bad staged column stride");
+  if ((int64_t)n_feats * nq == 0) return 0;
+  WGBM_REQUIRE(cols && kmin && kmax && q && edges, "null pointer");
+  return launch_select(cols, n, cols_stride, n_feats, q, nq, edges, kmin, kmax, S(stream));
+}
+
 int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64_t x_stride,
                                const float* q, int32_t nq, float* edges, void* stream) {
   WGBM_REQUIRE(n >= 1 && n_feats >= 0 && nq >= 0 && nq <= 126 && x_stride >= n_feats,
@@ -535,29 +595,16 @@ int wgbm_quantile_edges_matrix(const float* X, int64_t n, int32_t n_feats, int64
   const int64_t ks = (n + 31) / 32 * 32;
   const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n_feats, (int64_t(1) << 30) / ks));
   uint32_t* keys = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (size_t)(chunk * ks), 8);
-  // per-feature buffer of the keys left after the 16-bit prefix pass (a
-  // quarter of the column; a column with more falls back to full scans)
-  const int64_t ccap = std::max<int64_t>(1024, n / 4);
-  uint32_t* cbuf = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (size_t)(chunk * ccap), 10);
   uint32_t* kmm = (uint32_t*)scratch_get(st, sizeof(uint32_t) * 2 * (size_t)chunk, 11);
-  WGBM_REQUIRE(keys && cbuf && kmm, "scratch allocation failed");
+  WGBM_REQUIRE(keys && kmm, "scratch allocation failed");
   uint32_t *kmin = kmm, *kmax = kmm + chunk;
   for (int64_t f0 = 0; f0 < n_feats; f0 += chunk) {
     const int32_t fc = (int32_t)std::min<int64_t>(chunk, n_feats - f0);
     if (fill_u32(kmin, fc, 0xffffffffu, st) || fill_u32(kmax, fc, 0u, st)) return WGBM_EINVAL;
-    const dim3 tg((unsigned)wgbm_xcd_grid((int64_t)nblocks(n, kTransRows) * nblocks(fc, 64)));
-    // 16-byte row loads when every row of the chunk starts on 16 bytes
-    const bool vec = ((uintptr_t)(X + f0) % 16) == 0 && x_stride % 4 == 0;
-    if (vec)
-      hipLaunchKernelGGL(transpose_values_kernel<true>, tg, dim3(256), 0, st, X + f0, n, fc,
-                         x_stride, ks, keys, kmin, kmax);
-    else
-      hipLaunchKernelGGL(transpose_values_kernel<false>, tg, dim3(256), 0, st, X + f0, n, fc,
-                         x_stride, ks, keys, kmin, kmax);
-    WGBM_LAUNCH_CHECK();
-    hipLaunchKernelGGL(quantile_select_kernel, dim3(fc), dim3(512), 0, st, keys, n, ks, fc, q, nq,
-                       edges + f0 * nq, kmin, kmax, cbuf, ccap);
-    WGBM_LAUNCH_CHECK();
+    int r = launch_stage_rows(X + f0, n, fc, x_stride, keys, ks, kmin, kmax, st);
+    if (r) return r;
+    r = launch_select(keys, n, ks, fc, q, nq, edges + f0 * nq, kmin, kmax, st);
+    if (r) return r;
   }
   return 0;
 }

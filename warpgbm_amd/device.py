@@ -114,21 +114,32 @@ def upload_float(X: np.ndarray, dev) -> torch.Tensor:
     return _upload_staged(X, dev, np.float32, torch.float32)
 
 
-def _upload_staged(X: np.ndarray, dev, np_dtype, torch_dtype) -> torch.Tensor:
+def _streams(X: np.ndarray, esize: int) -> bool:
+    """Whether _upload_staged streams X through the staging buffers."""
+    n, F = X.shape
+    return n * esize * max(F, 1) >= 4 * _STAGE_BYTES and X.flags.c_contiguous
+
+
+def _upload_staged(X: np.ndarray, dev, np_dtype, torch_dtype, on_chunk=None,
+                   row_align: int = 1) -> torch.Tensor:
     """[n, F] contiguous copy of X on the device in np_dtype.
 
     Large inputs are streamed through pinned staging buffers: host threads
     fill one buffer (converting the dtype on the way) while the DMA engine
-    copies the previous ones on a side stream."""
+    copies the previous ones on a side stream.  ``on_chunk(out, r0, r1,
+    stream)`` (streamed inputs only) enqueues work on rows [r0, r1) of the
+    device copy on that side stream right after their copy; chunks then
+    start on multiples of ``row_align`` rows."""
     X = np.asarray(X)
     n, F = X.shape
     esize = np.dtype(np_dtype).itemsize
     row_bytes = esize * max(F, 1)
-    if n * row_bytes < 4 * _STAGE_BYTES or not X.flags.c_contiguous:
+    if not _streams(X, esize):
         return torch.from_numpy(np.ascontiguousarray(X, dtype=np_dtype)).to(dev)
     out = torch.empty((n, F), dtype=torch_dtype, device=dev)
     bufs, pool = _staging()
     rows_per = max(1, _STAGE_BYTES // row_bytes)
+    rows_per = max(row_align, rows_per // row_align * row_align)
     side = torch.cuda.Stream(device=dev)
     side.wait_stream(torch.cuda.current_stream(dev))
     events = [None] * len(bufs)
@@ -150,6 +161,8 @@ def _upload_staged(X: np.ndarray, dev, np_dtype, torch_dtype) -> torch.Tensor:
             out[r0:r1].copy_(host, non_blocking=True)
             ev = torch.cuda.Event()
             ev.record(side)
+            if on_chunk is not None:
+                on_chunk(out, r0, r1, side.cuda_stream)
         events[k] = ev
     torch.cuda.current_stream(dev).wait_stream(side)
     out.record_stream(side)
@@ -258,6 +271,61 @@ def upload_and_bin(X: np.ndarray, edges: torch.Tensor, dev, cols=None, on_chunk=
         if ev is not None:
             ev.synchronize()  # staging buffers are reused by the next upload
     return c
+
+
+def upload_float_with_edges(X: np.ndarray, dev, num_bins: int):
+    """float32 device copy of X and its quantile edges [F, num_bins - 1]
+    (warpgbm/core.py:519-534).  A streamed upload stages each row block's
+    values for the selection as soon as the block lands
+    (``wgbm_quantile_stage_rows`` on the copy stream, hidden behind the
+    transfer of the next blocks); the edges are then taken from the staged
+    columns (``wgbm_quantile_edges_staged``), bit-identical to
+    ``quantile_edges`` of the whole copy."""
+    X = np.asarray(X)
+    n, F = X.shape
+    if not _streams(X, 4) or F == 0 or num_bins < 2:
+        Xd = upload_float(X, dev)
+        return Xd, quantile_edges(Xd, num_bins)
+    st = QuantileStage(n, F, dev)
+    Xd = _upload_staged(X, dev, np.float32, torch.float32,
+                        on_chunk=lambda out, r0, r1, sp: st.stage(out, r0, r1, sp), row_align=32)
+    return Xd, st.edges(num_bins)
+
+
+class QuantileStage:
+    """Column-major staging of an [n, F] float32 matrix for the quantile
+    selection (``wgbm_quantile_stage_rows`` per row block, in any order),
+    then the edges of all n rows (``wgbm_quantile_edges_staged``)."""
+
+    def __init__(self, n: int, F: int, dev):
+        if n > (1 << 24):
+            raise ValueError("quantile() input tensor is too large (more than 2^24 rows per "
+                             "feature)")
+        self.n, self.F, self.dev = n, F, dev
+        self.ks = (n + 31) // 32 * 32
+        self.cols = torch.empty((F, self.ks), dtype=torch.int32, device=dev)
+        self.kmin = torch.full((F,), -1, dtype=torch.int32, device=dev)  # 0xffffffff
+        self.kmax = torch.zeros((F,), dtype=torch.int32, device=dev)
+        self.lib = _lib.load()
+
+    def stage(self, Xd: torch.Tensor, r0: int, r1: int, stream_ptr=None) -> None:
+        """Rows [r0, r1) of the device matrix Xd (r0 a multiple of 4)."""
+        sp = _stream(self.dev) if stream_ptr is None else stream_ptr
+        rc = self.lib.wgbm_quantile_stage_rows(Xd[r0].data_ptr(), r1 - r0, self.F,
+                                               Xd.stride(0), r0, self.cols.data_ptr(), self.ks,
+                                               self.kmin.data_ptr(), self.kmax.data_ptr(), sp)
+        _lib.check(rc, "quantile_stage_rows")
+
+    def edges(self, num_bins: int) -> torch.Tensor:
+        q = quantile_levels(num_bins).to(self.dev)
+        nq = num_bins - 1
+        edges = torch.empty((self.F, nq), dtype=torch.float32, device=self.dev)
+        rc = self.lib.wgbm_quantile_edges_staged(self.cols.data_ptr(), self.n, self.F, self.ks,
+                                                 self.kmin.data_ptr(), self.kmax.data_ptr(),
+                                                 q.data_ptr(), nq, edges.data_ptr(),
+                                                 _stream(self.dev))
+        _lib.check(rc, "quantile_edges_staged")
+        return edges
 
 
 def quantile_edges(Xd: torch.Tensor, num_bins: int) -> torch.Tensor:
