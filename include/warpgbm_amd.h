@@ -278,8 +278,11 @@ int wgbm_engine_round(wgbm_engine* eng, const void* target, float* pred, const i
  * pair-code copy, one byte per feature pair; default 1); key 3 = the
  * per-level node scan of one-era fits (1 = a thread per node, default; 0 = a
  * wave per node); key 4 = one-era split search and leaf / record step (1 =
- * one fused launch, default; 0 = two launches).  Set before the first round;
- * every setting grows the same trees. */
+ * one fused launch, default; 0 = two launches); key 5 = the one-era root
+ * (1 = its positions and totals in one launch and the root level's
+ * histogram tiles planned once per engine, default; 0 = a root partition
+ * pass, block scan and totals launch, and a plan per round).  Set before the
+ * first round; every setting grows the same trees. */
 int wgbm_engine_set_tuning(wgbm_engine* eng, int32_t key, int64_t value);
 void wgbm_engine_destroy(wgbm_engine* eng);
 

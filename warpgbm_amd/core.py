@@ -56,6 +56,28 @@ class _Phases:
             print(f"{what} phases: " + ", ".join(f"{n} {dt * 1e3:.1f} ms" for n, dt in self.items))
 
 
+def _record_round_bytes(n_trees, H):
+    """Bytes of one round's tree records (count, feature, bin, leaf of each
+    tree's H heap nodes), rounded up to 16 bytes."""
+    return (20 * n_trees * H + 15) // 16 * 16
+
+
+def _record_views(raw, n_trees, H):
+    """The record fields as [rounds, trees, H] views of one round-major byte
+    buffer raw [rounds, _record_round_bytes]: a round's records are one
+    contiguous range (one copy for a block of rounds), and within a round
+    each field is contiguous (the engine's per-round pointers)."""
+    th = n_trees * H
+    R = raw.shape[0]
+
+    def field(lo, hi, dtype):
+        return raw[:, lo:hi].view(dtype).view(R, n_trees, H)
+
+    return {"count": field(0, 8 * th, torch.int64), "feat": field(8 * th, 12 * th, torch.int32),
+            "bin": field(12 * th, 16 * th, torch.int32),
+            "leaf": field(16 * th, 20 * th, torch.float32), "raw": raw}
+
+
 _SIDE_STREAMS = {}
 
 
@@ -85,11 +107,13 @@ class _RecordStream:
 
     def __init__(self, rec):
         self.rec = rec
-        self.host = {k: torch.empty(rec[k].shape, dtype=rec[k].dtype, pin_memory=True)
-                     for k in ("feat", "bin", "leaf", "count")}
+        n_trees, H = rec["feat"].shape[1], rec["feat"].shape[2]
+        self.host_raw = torch.empty(rec["raw"].shape, dtype=torch.uint8, pin_memory=True)
+        self.host = {k: v for k, v in _record_views(self.host_raw, n_trees, H).items()
+                     if k != "raw"}
         self.pending = []   # (first round, end round, event) of issued copies
         self.copied = 0     # rounds whose copy has been issued
-        self.landed = []    # [r0, r1, trees converted so far] of landed blocks, in order
+        self.landed = []    # [r0, r1, trees converted so far, fields] of landed blocks, in order
         self.flat = []      # tree dicts of the converted trees, rounds then trees
         self.trees = []     # per finished round: its list of tree dicts
         # per converted block: the records' rows of its internal nodes (rounds,
@@ -133,8 +157,8 @@ class _RecordStream:
         ready.record()
         with torch.cuda.stream(self.side):
             self.side.wait_event(ready)
-            for k, h in self.host.items():
-                h[r0:end].copy_(self.rec[k][r0:end], non_blocking=True)
+            # the rounds' records are one contiguous range: one copy
+            self.host_raw[r0:end].copy_(self.rec["raw"][r0:end], non_blocking=True)
             ev = torch.cuda.Event()
             ev.record(self.side)
         self.pending.append((r0, end, ev))
@@ -145,20 +169,22 @@ class _RecordStream:
         no landed block has trees left."""
         # landed copies; with wait, block for the oldest one only when none
         # has landed (the rest keep landing while this one is converted)
+        n_trees, H = self.host["feat"].shape[1], self.host["feat"].shape[2]
         while self.pending and (self.pending[0][2].query() or (wait and not self.landed)):
             r0, r1, ev = self.pending.pop(0)
             ev.synchronize()
-            self.landed.append([r0, r1, 0])
+            # the block's fields as contiguous [trees of the block, H] arrays
+            f = {k: np.ascontiguousarray(v[r0:r1].numpy()).reshape(-1, H)
+                 for k, v in self.host.items()}
+            self.landed.append([r0, r1, 0, f])
         if not self.landed:
             return False
         blk = self.landed[0]
-        r0, r1, done = blk
-        n_trees, H = self.host["feat"].shape[1], self.host["feat"].shape[2]
+        r0, r1, done, f = blk
         total = (r1 - r0) * n_trees
         hi = min(total, done + self.CHUNK)
-        t0, t1 = r0 * n_trees + done, r0 * n_trees + hi
-        h = {k: v.view(-1, H)[t0:t1].numpy() for k, v in self.host.items()}
-        self.flat.extend(_heaps_to_dicts(h["feat"], h["bin"], h["leaf"], h["count"]))
+        self.flat.extend(_heaps_to_dicts(f["feat"][done:hi], f["bin"][done:hi],
+                                         f["leaf"][done:hi], f["count"][done:hi]))
         blk[2] = hi
         if hi == total:
             self.landed.pop(0)
@@ -512,14 +538,11 @@ class WarpGBM(BaseEstimator, RegressorMixin):
                 f"max_depth={self.max_depth} with {n_rounds} rounds x {n_trees} trees needs "
                 f"{need / 2**30:.1f} GiB of device memory for the tree records "
                 f"({free / 2**30:.1f} GiB free); reduce max_depth or n_estimators")
-        return {
-            "feat": torch.empty((n_rounds, n_trees, H), dtype=torch.int32, device=dev),
-            "bin": torch.empty((n_rounds, n_trees, H), dtype=torch.int32, device=dev),
-            "leaf": torch.empty((n_rounds, n_trees, H), dtype=torch.float32, device=dev),
-            "count": torch.empty((n_rounds, n_trees, H), dtype=torch.int64, device=dev),
-            "gain": torch.empty((n_rounds, n_trees, H, self.num_eras), dtype=torch.float32,
-                                device=dev),
-        }
+        rec = _record_views(torch.empty((n_rounds, _record_round_bytes(n_trees, H)),
+                                        dtype=torch.uint8, device=dev), n_trees, H)
+        rec["gain"] = torch.empty((n_rounds, n_trees, H, self.num_eras), dtype=torch.float32,
+                                  device=dev)
+        return rec
 
     @staticmethod
     def _records_heap(rec, done):
@@ -529,7 +552,8 @@ class WarpGBM(BaseEstimator, RegressorMixin):
         so the first predict need not rebuild them from the dicts."""
         if done == 0:
             return None
-        return (rec["feat"][:done], rec["bin"][:done], rec["leaf"][:done], done)
+        return (rec["feat"][:done].contiguous(), rec["bin"][:done].contiguous(),
+                rec["leaf"][:done].contiguous(), done)
 
     def _fit_regression(self, X, y, era_id, X_eval, y_eval, eval_every_n_trees,
                         early_stopping_rounds, eval_metric):

@@ -58,6 +58,13 @@ __global__ void root_setup_kernel(const int32_t* root_order, int64_t n, int32_t 
                                   int32_t* order, int32_t* keyp, float* rpos, int64_t* seg,
                                   int32_t* present, unsigned long long* best, int32_t* agree_max,
                                   const int32_t* shifts, int32_t* node_shift);
+constexpr int kRootE1Span = 4096;  // positions per workgroup of root_setup_e1_kernel
+__global__ void root_setup_e1_kernel(const int32_t* root_order, int64_t n, int32_t T,
+                                     const float* resid, int32_t* order, int32_t* keyp,
+                                     float* rpos, int64_t* seg, int32_t* present,
+                                     unsigned long long* best, const int32_t* shifts,
+                                     int32_t s63_add, int32_t* node_shift, int64_t* tot_qh,
+                                     int64_t* tot_ql);
 // What the partition needs of a (tree, node) of the level, written by
 // level_finish_kernel: col = the split's code column (-1: the node is a
 // leaf, -2: absent), bin = the split bin, leaf = the leaf value, s63 = the

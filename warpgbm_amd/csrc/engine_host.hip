@@ -86,6 +86,16 @@ struct Engine {
   // (split_finish_e1_kernel), 0 = split_level_e1_kernel + level_finish_kernel
   int fuse_finish = 1;
   uint32_t* done = nullptr;  // [T * nodes_max] arrival counters (zero between launches)
+  // one era: 1 = the root's words and totals in one launch (root_setup_e1_kernel)
+  // and the root level's histogram tiles planned once (the root segments
+  // are the same every round); 0 = root_setup + root route + block scan +
+  // root totals and a plan per round
+  int root_path = 1;
+  Tile* root_tiles = nullptr;     // the root level's tile plan (planned by the first round)
+  int32_t* root_kts = nullptr;
+  int32_t* root_hn = nullptr;
+  int64_t root_tiles_cap = 0;
+  bool root_tiles_ready = false;
   uint32_t* alive = nullptr;    // [tn][W] segments that can hold a split, W = ceil(E/32)
   double* bsum = nullptr;       // [tn][W][n_sel*(B-1)] era-block gain sums
   int8_t* bdir = nullptr;       // [tn][W][n_sel*(B-1)] era-block direction sums (|.| <= 32)
@@ -301,6 +311,12 @@ int engine_set_tuning(Engine* e, int key, int64_t value) {
     WGBM_REQUIRE(value == 0 || (value >= 256 && value <= WGBM_MAX_TILE_ROWS),
                  "hist tile rows must be 0 or in [256, %d]", WGBM_MAX_TILE_ROWS);
     e->hist_tile_rows = value;
+    e->root_tiles_ready = false;  // the root plan depends on the tile rows
+    return 0;
+  }
+  if (key == 5) {
+    WGBM_REQUIRE(value == 0 || value == 1, "one-era root path must be 0 or 1");
+    e->root_path = (int)value;
     return 0;
   }
   if (key == 2) {
@@ -452,17 +468,30 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                        (const int32_t*)target, N, T, e->resid, e->abs_part);
   }
   WGBM_LAUNCH_CHECK();
+  // one era, fused root: the root totals words are cleared here for the
+  // root's atomic sums
+  const bool root_e1 = E == 1 && e->root_path;
   hipLaunchKernelGGL(absmax_finish_kernel, dim3(T), dim3(256), 0, st, e->abs_part, nres, e->qbits,
-                     e->absmax, e->shifts);
+                     e->absmax, e->shifts, root_e1 ? e->totqh[0] : (int64_t*)nullptr,
+                     e->totql[0], e->totc[0], N);
   WGBM_LAUNCH_CHECK();
 
   // root segments and totals
   int cur = 0;
   const int64_t n_pos = (int64_t)T * N;
-  hipLaunchKernelGGL(root_setup_kernel, dim3(blocks_for(std::max<int64_t>(n_pos, T * E), 256)),
-                     dim3(256), 0, st, c.root_order, N, T, c.era_start, E, e->resid,
-                     e->order[0], e->keyp[0], e->rpos[0], e->seg[0], e->present[0], e->best,
-                     e->agree_max, e->shifts, e->node_shift[0]);
+  if (root_e1) {
+    hipLaunchKernelGGL(root_setup_e1_kernel, dim3(blocks_for(N, kRootE1Span), (unsigned)T),
+                       dim3(1024), 0,
+                       st, c.root_order, N, T, e->resid, e->order[0], e->keyp[0], e->rpos[0],
+                       e->seg[0], e->present[0], e->best, e->shifts, 62 - e->qbits,
+                       e->node_shift[0], e->totqh[0], e->totql[0]);
+  } else {
+    hipLaunchKernelGGL(root_setup_kernel,
+                       dim3(blocks_for(std::max<int64_t>(n_pos, T * E), 256)), dim3(256), 0, st,
+                       c.root_order, N, T, c.era_start, E, e->resid, e->order[0], e->keyp[0],
+                       e->rpos[0], e->seg[0], e->present[0], e->best, e->agree_max, e->shifts,
+                       e->node_shift[0]);
+  }
   WGBM_LAUNCH_CHECK();
   RouteArgs ra{};
   ra.n_pos = n_pos;
@@ -480,7 +509,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
   ra.pcol = c.objective == 0 ? 0 : N;
   ra.dirbit = e->dirbit;
   ra.ps = e->ps;
-  {
+  if (!root_e1) {
     RouteArgs r0 = ra;
     r0.mode = 0;
     r0.seg = e->seg[0];
@@ -614,7 +643,35 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         } else if (d > 0) {
           list = e->key_list[cur];
         }
-        if (!(subtract && planned)) {  // else planned by the previous level's level_scan_kernel
+        // the level's tile plan: the cached root plan, the previous level's
+        // (level_scan_kernel), or planned here
+        Tile* tl_d = e->htiles;
+        int32_t* kts_d = e->hkts;
+        int32_t* hn_d = e->hn;
+        if (d == 0 && subtract && root_e1) {
+          if (!e->root_tiles_ready) {
+            if (max_tiles > e->root_tiles_cap) {
+              // a larger plan (new tile rows): fresh buffers, the old ones stay
+              // allocated until the engine is destroyed (no sync needed)
+              e->root_tiles = nullptr;
+              e->root_kts = nullptr;
+              e->root_hn = nullptr;
+              int ra2 = dalloc(e, &e->root_tiles, max_tiles);
+              if (!ra2) ra2 = dalloc(e, &e->root_kts, (int64_t)n_list + 1);
+              if (!ra2) ra2 = dalloc(e, &e->root_hn, 1);
+              if (ra2) return ra2;
+              e->root_tiles_cap = max_tiles;
+            }
+            hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur],
+                               (int64_t)0, n_list, list, (int32_t)R, 0, (int32_t)max_tiles,
+                               e->root_tiles, e->root_kts, e->root_hn);
+            WGBM_LAUNCH_CHECK();
+            e->root_tiles_ready = true;
+          }
+          tl_d = e->root_tiles;
+          kts_d = e->root_kts;
+          hn_d = e->root_hn;
+        } else if (!(subtract && planned)) {
           hipLaunchKernelGGL(plan_tiles_kernel, dim3(1), dim3(1024), 0, st, e->seg[cur] + k0,
                              (int64_t)0, n_list, list, (int32_t)R, 0, (int32_t)max_tiles,
                              e->htiles, e->hkts, e->hn);
@@ -632,8 +689,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         // node) with one era, the (tree, node, era) segment with several)
         a.shifts = e->node_shift[cur] + k0;
         a.order = e->order[cur];
-        a.tiles = e->htiles;
-        a.n_tiles = e->hn;
+        a.tiles = tl_d;
+        a.n_tiles = hn_d;
         a.keys_per_tree = 1;
         a.num_bins = B;
         a.part = e->part;
@@ -646,9 +703,9 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         if (r) return r;
         const int64_t pairs = (subtract && d > 0) ? n_list / 2 : n_list;
         const int64_t tiles_per_key = std::max<int64_t>(1, rows_bound / R / std::max<int64_t>(pairs, 1));
-        r = launch_finalize_level(tiles_per_key, e->part, e->hkts, list, n_list, e->n_chunks, e->V,
+        r = launch_finalize_level(tiles_per_key, e->part, kts_d, list, n_list, e->n_chunks, e->V,
                                   B, F, E, nodes, subtract ? d : 0, e->hq[hprev], e->hc[hprev],
-                                  e->hn, e->hq[hcur], e->hc[hcur], st);
+                                  hn_d, e->hq[hcur], e->hc[hcur], st);
         if (r) return r;
         if (E == 1 && e->fuse_finish) {
           // split search and the level's leaf / record step in one launch

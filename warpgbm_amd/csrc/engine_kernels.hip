@@ -137,6 +137,79 @@ __global__ void root_setup_kernel(const int32_t* __restrict__ root_order, int64_
   }
 }
 
+// One era (E == 1): root_setup_kernel's words, and each tree's root totals
+// in the same launch: the exact sums over the tree's rows of the wide
+// quantisation q63 = rint(r * 2^s63), s63 = shifts[t] + s63_add, held as
+// qh = sum (q63 >> 32) and ql = sum (q63 & (2^32 - 1)) (the words the root
+// route + block scan + root_totals_kernel give).  Grid (ceil(n /
+// kRootE1Span), T): a workgroup holds kRootE1Span positions of one tree and
+// adds its sums to the tree's words with one relaxed atomic each (integer
+// sums: any order gives the same words); absmax_finish_kernel cleared them
+// and set the row count.  No fence: the next launch sees the sums.
+__global__ __launch_bounds__(1024) void root_setup_e1_kernel(
+    const int32_t* __restrict__ root_order, int64_t n, int32_t T, const float* __restrict__ resid,
+    int32_t* __restrict__ order, int32_t* __restrict__ keyp, float* __restrict__ rpos,
+    int64_t* __restrict__ seg, int32_t* __restrict__ present, unsigned long long* __restrict__ best,
+    const int32_t* __restrict__ shifts, int32_t s63_add, int32_t* __restrict__ node_shift,
+    int64_t* __restrict__ tot_qh, int64_t* __restrict__ tot_ql) {
+  constexpr int kThreads = 1024, kWaves = kThreads / 64;
+  constexpr int PJ = kRootE1Span / kThreads;  // positions per thread, loads issued together
+  __shared__ int64_t s_qh[kWaves], s_ql[kWaves];
+  const int t = (int)blockIdx.y;
+  const int tid = (int)threadIdx.x;
+  const int s63 = shifts[t] + s63_add;
+  const int64_t p0 = (int64_t)blockIdx.x * kRootE1Span;
+  const int64_t tb = (int64_t)t * n;
+  int32_t rows[PJ];
+  float rv[PJ];
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const int64_t p = p0 + j * kThreads + tid;
+    rows[j] = p < n ? root_order[p] : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const int64_t p = p0 + j * kThreads + tid;
+    rv[j] = p < n ? resid[tb + rows[j]] : 0.0f;
+  }
+  int64_t qh = 0, ql = 0;
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const int64_t p = p0 + j * kThreads + tid;
+    if (p < n) {
+      order[tb + p] = rows[j];
+      rpos[tb + p] = rv[j];
+      keyp[tb + p] = t;
+      const int64_t q = (int64_t)rintf(ldexpf(rv[j], s63));
+      qh += q >> 32;
+      ql += q & 0xffffffffll;
+    }
+  }
+  if (blockIdx.x == 0 && tid == 0) {
+    seg[t] = tb;
+    if (t == 0) seg[T] = (int64_t)T * n;
+    present[t] = 1;
+    node_shift[t] = shifts[t];
+    best[t] = 0ull;
+  }
+  qh = wgbm_wave_reduce_add_i64(qh);
+  ql = wgbm_wave_reduce_add_i64(ql);
+  if ((tid & 63) == 0) {
+    s_qh[tid >> 6] = qh;
+    s_ql[tid >> 6] = ql;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int64_t a = 0, b = 0;
+    for (int k = 0; k < kWaves; ++k) {
+      a += s_qh[k];
+      b += s_ql[k];
+    }
+    if (a) atomicAdd((unsigned long long*)(tot_qh + t), (unsigned long long)a);
+    if (b) atomicAdd((unsigned long long*)(tot_ql + t), (unsigned long long)b);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // per-level bookkeeping: leaf values and the tree record
 //   leaf value = mean of the node's residuals (warpgbm/core.py:599, :614),

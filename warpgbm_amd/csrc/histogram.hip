@@ -790,11 +790,20 @@ __global__ __launch_bounds__(256) void hist_finalize_level_kernel(
 
 // one workgroup per independent maximum t: reduce partial[t*n_part ...] and
 // turn it into the quantisation shift (0 for an all-zero or non-finite input;
-// absmax_bits keeps the raw maximum so a NaN/inf input can be reported)
+// absmax_bits keeps the raw maximum so a NaN/inf input can be reported).
+// With tot_qh, also tree t's root totals words made ready for the root's
+// atomic sums (root_setup_e1_kernel): sums 0, count n_rows.
 __global__ void absmax_finish_kernel(const uint32_t* __restrict__ partial, int32_t n_part,
                                      int32_t qbits, uint32_t* __restrict__ absmax_bits,
-                                     int32_t* __restrict__ shifts) {
+                                     int32_t* __restrict__ shifts, int64_t* __restrict__ tot_qh,
+                                     int64_t* __restrict__ tot_ql, int64_t* __restrict__ tot_c,
+                                     int64_t n_rows) {
   const int t = blockIdx.x;
+  if (tot_qh && threadIdx.x == 0) {
+    tot_qh[t] = 0;
+    tot_ql[t] = 0;
+    tot_c[t] = n_rows;
+  }
   uint32_t m = 0;
   for (int i = threadIdx.x; i < n_part; i += blockDim.x) {
     const uint32_t b = partial[(int64_t)t * n_part + i];

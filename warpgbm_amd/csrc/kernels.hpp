@@ -166,7 +166,8 @@ int launch_finalize_level(int64_t tiles_per_key, const unsigned long long* part,
                           const int64_t* parent_q, const int32_t* parent_c, const int32_t* n_tiles,
                           int64_t* hq, int32_t* hc, hipStream_t st);
 __global__ void absmax_finish_kernel(const uint32_t* partial, int32_t n_part, int32_t qbits,
-                                     uint32_t* absmax_bits, int32_t* shifts);
+                                     uint32_t* absmax_bits, int32_t* shifts, int64_t* tot_qh,
+                                     int64_t* tot_ql, int64_t* tot_c, int64_t n_rows);
 __global__ void plan_tiles_kernel(const int64_t* seg, int64_t total, int32_t n_keys,
                                   const int32_t* key_list, int32_t tile_rows, int32_t nearest,
                                   int32_t max_tiles, Tile* tiles, int32_t* key_tile_start,
