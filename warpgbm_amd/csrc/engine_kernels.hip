@@ -43,6 +43,61 @@ __global__ void residual_softmax_kernel(const float* __restrict__ logits /* [K][
                                         const int32_t* __restrict__ label, int64_t n, int32_t K,
                                         float* __restrict__ r /* [K][n] */,
                                         uint32_t* __restrict__ partial) {
+  if (K <= kSoftmaxRegK) {
+    // one pass: a row's K logits in registers (fully unrolled: no dynamic
+    // register index), max, the exponentials (each computed once, used for
+    // the sum and the probability: the same values), every class's
+    // residual; then every class's block maximum with one LDS exchange
+    uint32_t m[kSoftmaxRegK];
+#pragma unroll
+    for (int k = 0; k < kSoftmaxRegK; ++k) m[k] = 0u;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+      const float* x = logits + i;
+      const int lab = label[i];
+      float xr[kSoftmaxRegK];
+#pragma unroll
+      for (int k = 0; k < kSoftmaxRegK; ++k) xr[k] = x[(k < K ? k : 0) * n];
+      float mx = xr[0];
+#pragma unroll
+      for (int k = 1; k < kSoftmaxRegK; ++k)
+        if (k < K) mx = xr[k] > mx ? xr[k] : mx;
+      float ex[kSoftmaxRegK];
+      float sum = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kSoftmaxRegK; ++k) {
+        ex[k] = k < K ? wgbm_expf(xr[k] - mx) : 0.0f;
+        if (k < K) sum = sum + ex[k];
+      }
+#pragma unroll
+      for (int k = 0; k < kSoftmaxRegK; ++k) {
+        if (k < K) {
+          const float g = ex[k] / sum - (k == lab ? 1.0f : 0.0f);
+          const float v = -g;
+          r[(int64_t)k * n + i] = v;
+          const uint32_t b = wgbm_abs_bits(v);
+          m[k] = b > m[k] ? b : m[k];
+        }
+      }
+    }
+    __shared__ uint32_t s_m[kSoftmaxRegK][16];  // [class][wave]
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+    for (int k = 0; k < kSoftmaxRegK; ++k) {
+      if (k < K) {
+        const uint32_t wm = wgbm_wave_max_u32(m[k]);
+        if ((threadIdx.x & 63) == 0) s_m[k][w] = wm;
+      }
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < K) {
+      const int k = threadIdx.x;
+      uint32_t bm = 0u;
+      for (int j = 0; j < nw; ++j) bm = s_m[k][j] > bm ? s_m[k][j] : bm;
+      partial[(int64_t)k * gridDim.x + blockIdx.x] = bm;
+    }
+    return;
+  }
   for (int k0 = 0; k0 < K; k0 += 8) {
     // up to 8 class maxima per pass over the rows
     uint32_t m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -51,39 +106,17 @@ __global__ void residual_softmax_kernel(const float* __restrict__ logits /* [K][
       // the row's K logits, class-major (one coalesced read per class)
       const float* x = logits + i;
       const int lab = label[i];
-      auto emit = [&](int kk, float p) {
+      float mx = x[0];
+      for (int k = 1; k < K; ++k) mx = x[k * n] > mx ? x[k * n] : mx;
+      float s = 0.0f;
+      for (int k = 0; k < K; ++k) s = s + wgbm_expf(x[k * n] - mx);
+      for (int kk = 0; kk < 8 && k0 + kk < K; ++kk) {
         const int k = k0 + kk;
-        const float g = p - (k == lab ? 1.0f : 0.0f);
+        const float g = wgbm_expf(x[k * n] - mx) / s - (k == lab ? 1.0f : 0.0f);
         const float v = -g;
         r[(int64_t)k * n + i] = v;
         const uint32_t b = wgbm_abs_bits(v);
         m[kk] = b > m[kk] ? b : m[kk];
-      };
-      if (K <= kSoftmaxRegK) {
-        // the logits loaded together into registers (fully unrolled: no
-        // dynamic register index), then the same operations in the same
-        // order as the general loop below
-        float xr[kSoftmaxRegK];
-#pragma unroll
-        for (int k = 0; k < kSoftmaxRegK; ++k) xr[k] = x[(k < K ? k : 0) * n];
-        float mx = xr[0];
-#pragma unroll
-        for (int k = 1; k < kSoftmaxRegK; ++k)
-          if (k < K) mx = xr[k] > mx ? xr[k] : mx;
-        float s = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kSoftmaxRegK; ++k)
-          if (k < K) s = s + wgbm_expf(xr[k] - mx);
-#pragma unroll
-        for (int k = 0; k < kSoftmaxRegK; ++k)
-          if (k >= k0 && k < k0 + 8 && k < K) emit(k - k0, wgbm_expf(xr[k] - mx) / s);
-      } else {
-        float mx = x[0];
-        for (int k = 1; k < K; ++k) mx = x[k * n] > mx ? x[k * n] : mx;
-        float s = 0.0f;
-        for (int k = 0; k < K; ++k) s = s + wgbm_expf(x[k * n] - mx);
-        for (int kk = 0; kk < 8 && k0 + kk < K; ++kk)
-          emit(kk, wgbm_expf(x[(k0 + kk) * n] - mx) / s);
       }
     }
     for (int kk = 0; kk < 8 && k0 + kk < K; ++kk) {
