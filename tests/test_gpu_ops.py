@@ -288,12 +288,15 @@ def _chain_tree(rng, depth, F, B):
             "right": _chain_tree(rng, depth - 1, F, B)}
 
 
+@pytest.mark.parametrize("F", [296, 300])
 @pytest.mark.parametrize("case", ["plain", "big_bins", "bad_nodes", "deep", "neg_bin", "few"])
-def test_predict_forest_heap_path_bit_exact(gpu, case):
+def test_predict_forest_heap_path_bit_exact(gpu, case, F):
     """predict_forest with enough trees and rows takes the heap path (flat
-    tables -> heap tables, a native copy of the codes, the LDS predictors);
-    tables it cannot hold fall back to the flat walk on the device.  Every
-    case against the oracle's flat walk (warpgbm/cuda/predict.cu:13-44):
+    tables -> heap tables, then the LDS predictor over the raw codes when
+    rows are a multiple of 8 bytes (F = 296), or over a native copy of the
+    codes (F = 300)); tables it cannot hold fall back to the flat walk on the
+    device.  Every case against the oracle's flat walk
+    (warpgbm/cuda/predict.cu:13-44):
     * plain: depth-5 trees in 64-slot tables, codes -128..127 (negative codes
       go left at every split, 127 right at every bin <= 126);
     * big_bins: split bins 127..300 (every int8 code goes left);
@@ -302,9 +305,9 @@ def test_predict_forest_heap_path_bit_exact(gpu, case):
     * deep: one tree deeper than its table's heap (fallback);
     * neg_bin: a negative split bin (fallback);
     * few: fewer trees than the heap path takes (the flat walk alone)."""
-    print_case("predict_forest heap path", case)
-    rng = np.random.default_rng(20 + len(case))
-    N, F, B, D_ = 9000, 300, 32, 5
+    print_case("predict_forest heap path", case, F)
+    rng = np.random.default_rng(20 + len(case) + F)
+    N, B, D_ = 9000, 32, 5
     M = 2 ** (D_ + 1)
     codes = rng.integers(-3, B + 2, (N, F)).astype(np.int8)
     codes[rng.random((N, F)) < 0.01] = 127

@@ -428,14 +428,14 @@ static int predict_heap_impl(const int8_t* codes, int64_t n, int64_t codes_strid
   if (resident) {
     static bool attr_r = false;
     if (!attr_r) {
-      WGBM_CHECK(hipFuncSetAttribute((const void*)predict_resident_kernel,
+      WGBM_CHECK(hipFuncSetAttribute((const void*)predict_resident_kernel<false>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
       attr_r = true;
     }
     // one persistent workgroup per CU (fewer when there are fewer blocks)
     const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(n_cu, nblocks(n, RB)));
-    hipLaunchKernelGGL(predict_resident_kernel, dim3((unsigned)grid), dim3(1024), lds, S(stream),
-                       codes, n, codes_stride, num_bins, (const uint32_t*)cnode,
+    hipLaunchKernelGGL(predict_resident_kernel<false>, dim3((unsigned)grid), dim3(1024), lds,
+                       S(stream), codes, n, codes_stride, num_bins, (const uint32_t*)cnode,
                        (const float*)cleaf, n_rounds * K, K, max_depth, RB, out, skip);
   } else if (rows) {
     static bool attr = false;
@@ -456,6 +456,43 @@ static int predict_heap_impl(const int8_t* codes, int64_t n, int64_t codes_strid
   return 0;
 }
 
+// predict_forest's heap tables walked straight over the raw codes (no native
+// copy): rows of stride n_feats (a multiple of 8, 8-byte aligned), the
+// resident predictor only.  Returns -1 without launching when that does not
+// fit (the caller then copies the codes to the native layout).
+static int predict_forest_raw(const int8_t* raw, int64_t n, int64_t n_feats,
+                              const int32_t* feat, const int32_t* bin, const float* leaf,
+                              int32_t n_trees, int32_t H, int32_t D, float learning_rate,
+                              float* out, hipStream_t st, const int32_t* skip) {
+  int32_t RB = 0;
+  size_t lds = 0;
+  if (n_feats % 8 != 0 || ((uintptr_t)raw % 8) != 0 ||
+      !predict_resident_plan(n_feats, 1, H, n_trees, &RB, &lds, true))
+    return -1;
+  int dev = 0, n_cu = 0;
+  WGBM_CHECK(hipGetDevice(&dev));
+  WGBM_CHECK(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+  uint32_t* cnode = (uint32_t*)scratch_get(st, sizeof(uint32_t) * (size_t)n_trees * H, 13);
+  WGBM_REQUIRE(cnode, "scratch allocation failed");
+  float* cleaf = reinterpret_cast<float*>(cnode + (int64_t)n_trees * ((H - 1) / 2));
+  const int64_t work = (int64_t)n_trees * H;
+  hipLaunchKernelGGL(complete_tables_kernel, dim3(nblocks(work, 256)), dim3(256), 0, st, feat,
+                     bin, leaf, (int64_t)n_trees, D, n_feats, learning_rate, cnode, cleaf);
+  WGBM_LAUNCH_CHECK();
+  static bool attr = false;
+  if (!attr) {
+    WGBM_CHECK(hipFuncSetAttribute((const void*)predict_resident_kernel<true>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr = true;
+  }
+  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(n_cu, nblocks(n, RB)));
+  hipLaunchKernelGGL(predict_resident_kernel<true>, dim3((unsigned)grid), dim3(1024), lds, st,
+                     raw, n, n_feats, 127, (const uint32_t*)cnode, (const float*)cleaf, n_trees,
+                     1, D, RB, out, skip);
+  WGBM_LAUNCH_CHECK();
+  return 0;
+}
+
 extern "C" {
 
 int wgbm_predict_forest(const int8_t* bin_indices, int64_t n, int64_t n_feats,
@@ -465,12 +502,14 @@ int wgbm_predict_forest(const int8_t* bin_indices, int64_t n, int64_t n_feats,
   if (n == 0) return 0;
   WGBM_REQUIRE(bin_indices && out && (n_trees == 0 || tree_tensor), "null pointer");
   hipStream_t st = S(stream);
-  // Heap path, for enough trees and rows to pay for a copy of the codes: the
-  // flat tables become heap tables of depth D = floor(log2(max_nodes)) - 1
-  // (flatten_tree's max_nodes = 2^(max_depth+1)) and the codes a native
-  // copy (num_bins 127: a negative code becomes the byte 127, which every
-  // split sends left; 127 becomes 128, which every split bin <= 126 sends
-  // right; the other codes stay), then the LDS predictors walk them.  A
+  // Heap path, for enough trees and rows: the flat tables become heap tables
+  // of depth D = floor(log2(max_nodes)) - 1 (flatten_tree's max_nodes =
+  // 2^(max_depth+1)), walked by the LDS predictors.  Rows of a multiple of 8
+  // bytes are read as they are by the resident predictor (a negative code
+  // read as 0, which every split sends left); otherwise the codes get a
+  // native copy (num_bins 127: a negative code becomes the byte 127, which
+  // every split sends left; 127 becomes 128, which every split bin <= 126
+  // sends right; the other codes stay).  A
   // table the heap cannot hold sets a device flag: the heap walk is skipped
   // and the flat walk below runs instead; otherwise the flat walk exits.
   int D = 0;
@@ -485,19 +524,27 @@ int wgbm_predict_forest(const int8_t* bin_indices, int64_t n, int64_t n_feats,
     int32_t* feat = (int32_t*)scratch_get(st, sizeof(int32_t) * (size_t)(n_trees * H), 15);
     int32_t* bin = (int32_t*)scratch_get(st, sizeof(int32_t) * (size_t)(n_trees * H), 16);
     float* leaf = (float*)scratch_get(st, sizeof(float) * (size_t)(n_trees * H), 17);
-    int8_t* nat = (int8_t*)scratch_get(st, (size_t)(n * Sn), 18);
-    WGBM_REQUIRE(fl && feat && bin && leaf && nat, "scratch allocation failed");
+    WGBM_REQUIRE(fl && feat && bin && leaf, "scratch allocation failed");
     hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, fl, (int64_t)1, 0);
     WGBM_LAUNCH_CHECK();
     hipLaunchKernelGGL(flat_to_heap_kernel, dim3(nblocks(n_trees * H, 256)), dim3(256), 0, st,
                        tree_tensor, n_trees, max_nodes, n_feats, (int32_t)D, feat, bin, leaf, fl);
     WGBM_LAUNCH_CHECK();
-    int r = wgbm_copy_prebinned(bin_indices, n, (int32_t)n_feats, n_feats, nat, Sn, nullptr, 127,
-                                nullptr, stream);
-    if (r) return r;
-    r = predict_heap_impl(nat, n, Sn, 127, feat, bin, leaf, (int32_t)n_trees, 1, (int32_t)H, D,
-                          learning_rate, out, stream, fl);
-    if (r) return r;
+    // the raw codes walked as they are when the resident predictor can read
+    // them; else a native copy for the LDS predictors
+    int r = predict_forest_raw(bin_indices, n, n_feats, feat, bin, leaf, (int32_t)n_trees,
+                               (int32_t)H, D, learning_rate, out, st, fl);
+    if (r > 0) return r;
+    if (r < 0) {
+      int8_t* nat = (int8_t*)scratch_get(st, (size_t)(n * Sn), 18);
+      WGBM_REQUIRE(nat, "scratch allocation failed");
+      r = wgbm_copy_prebinned(bin_indices, n, (int32_t)n_feats, n_feats, nat, Sn, nullptr, 127,
+                              nullptr, stream);
+      if (r) return r;
+      r = predict_heap_impl(nat, n, Sn, 127, feat, bin, leaf, (int32_t)n_trees, 1, (int32_t)H, D,
+                            learning_rate, out, stream, fl);
+      if (r) return r;
+    }
     flag = fl;
   }
   hipLaunchKernelGGL(predict_table_kernel, dim3(nblocks(n, 256)), dim3(256), 0, st, bin_indices,

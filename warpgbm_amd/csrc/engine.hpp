@@ -359,13 +359,14 @@ __global__ void predict_rows_kernel(const int8_t* codes, int64_t n, int64_t S, i
                                     float* out, const int32_t* skip);
 int predict_rows_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
                       int32_t* TC_out, size_t* lds_out);
+template <bool RAW>
 __global__ void predict_resident_kernel(const int8_t* codes, int64_t n, int64_t S,
                                         int32_t num_bins, const uint32_t* cnode,
                                         const float* cleaf, int32_t T, int32_t K,
                                         int32_t max_depth, int32_t RB, float* out,
                                         const int32_t* skip);
 int predict_resident_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
-                          size_t* lds_out);
+                          size_t* lds_out, bool raw = false);
 __global__ void softmax_rows_kernel(float* x, int64_t n, int32_t K);
 __global__ void importance_add_kernel(float* acc, int32_t F, int32_t E, const float* gain,
                                       const int64_t* node, const int64_t* fstart);

@@ -221,6 +221,14 @@ __device__ __forceinline__ uint32_t walk_bytes(uint32_t x, uint32_t bb) {
   return x & ((nz >> 7) * 0xffu);
 }
 
+// Raw int8 codes (the reference's bin_indices, any value) as the walkers
+// read them: a negative code becomes 0, which goes left at every split as the
+// reference's signed `code <= bin` sends it (split bins >= 0); 0..127 stay,
+// so right iff code > bin as there.
+__device__ __forceinline__ uint32_t raw_walk_bytes(uint32_t x) {
+  return x & ~(((x >> 7) & 0x01010101u) * 0xffu);
+}
+
 // A walk over a complete table held in LDS, stepped by LDS byte address: the
 // tree's node words start at `base`, node g (1-based heap index, children 2g
 // and 2g + 1) sits at a = base + 4 (g - 1), so the step to child 2g + x is
@@ -406,6 +414,10 @@ constexpr int kResThreads = 1024;
 constexpr int kResMaxQ = 4;  // 16-byte row loads per thread and block
 constexpr int kResWalks = 2;  // walks a walker thread advances in lock-step
 
+// RAW: the rows are raw int8 codes of stride S (a multiple of 8, read with
+// 8-byte loads, twice as many per thread) mapped by raw_walk_bytes, instead
+// of native codes (S a multiple of 16) mapped by walk_bytes.
+template <bool RAW>
 __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
     const int8_t* __restrict__ codes, int64_t n, int64_t S, int32_t num_bins,
     const uint32_t* __restrict__ cnode, const float* __restrict__ cleaf, int32_t T, int32_t K,
@@ -426,32 +438,33 @@ __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
   for (int i = tid; i < T * Hi; i += kResThreads) nodes_s[i] = cnode[i];
   for (int i = tid; i < T * L; i += kResThreads) leaves_s[i] = cleaf[i];
   const int64_t nblk = (n + RB - 1) / RB;
-  const int qpr = (int)(S / 16);  // 16-byte quads per row
+  constexpr int QW = RAW ? 2 : 4;            // 32-bit words per load
+  constexpr int NQ = kResMaxQ * 4 / QW;      // loads per thread and block
+  const int qpr = (int)(S / (4 * QW));       // loads per row
   const int nq = RB * qpr;
-  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-  u4 pre[kResMaxQ];
+  typedef uint32_t uq __attribute__((ext_vector_type(QW)));
+  uq pre[NQ];
   auto prefetch = [&](int64_t b) {
 #pragma unroll
-    for (int u = 0; u < kResMaxQ; ++u) {
+    for (int u = 0; u < NQ; ++u) {
       const int q = u * kResThreads + tid;
       const int r = q / qpr, c = q - r * qpr;
       const int64_t row = b * RB + r;
-      pre[u] = u4{0u, 0u, 0u, 0u};
+      pre[u] = uq{};
       if (q < nq && row < n)
-        pre[u] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(codes + row * S) + c);
+        pre[u] = __builtin_nontemporal_load(reinterpret_cast<const uq*>(codes + row * S) + c);
     }
   };
   auto stash = [&]() {
 #pragma unroll
-    for (int u = 0; u < kResMaxQ; ++u) {
+    for (int u = 0; u < NQ; ++u) {
       const int q = u * kResThreads + tid;
       if (q < nq) {
         const int r = q / qpr, c = q - r * qpr;
-        uint32_t* dst = reinterpret_cast<uint32_t*>(rows_s + r * Sp + c * 16);
-        dst[0] = walk_bytes(pre[u].x, bb);
-        dst[1] = walk_bytes(pre[u].y, bb);
-        dst[2] = walk_bytes(pre[u].z, bb);
-        dst[3] = walk_bytes(pre[u].w, bb);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(rows_s + r * Sp + c * 4 * QW);
+#pragma unroll
+        for (int k = 0; k < QW; ++k)
+          dst[k] = RAW ? raw_walk_bytes(pre[u][k]) : walk_bytes(pre[u][k], bb);
       }
     }
   };
@@ -514,13 +527,23 @@ __global__ __launch_bounds__(kResThreads) void predict_resident_kernel(
   }
 }
 
-// block shape of predict_resident_kernel: 0 when the trees do not fit
+template __global__ void predict_resident_kernel<false>(const int8_t*, int64_t, int64_t, int32_t,
+                                                        const uint32_t*, const float*, int32_t,
+                                                        int32_t, int32_t, int32_t, float*,
+                                                        const int32_t*);
+template __global__ void predict_resident_kernel<true>(const int8_t*, int64_t, int64_t, int32_t,
+                                                       const uint32_t*, const float*, int32_t,
+                                                       int32_t, int32_t, int32_t, float*,
+                                                       const int32_t*);
+
+// block shape of predict_resident_kernel: 0 when the trees do not fit (raw:
+// rows of raw codes, S a multiple of 8; else native rows, S a multiple of 16)
 int predict_resident_plan(int64_t S, int32_t K, int32_t H, int32_t n_rounds, int32_t* RB_out,
-                          size_t* lds_out) {
+                          size_t* lds_out, bool raw) {
   constexpr int64_t kBudget = 150 * 1024;
   const int64_t T = (int64_t)n_rounds * K;
   // complete tables: (H - 1) / 2 node words and (H + 1) / 2 values per tree
-  if (S % 16 != 0 || S > (1 << 16) || T * H * 4 > 64 * 1024) return 0;
+  if (S % (raw ? 8 : 16) != 0 || S > (1 << 16) || T * H * 4 > 64 * 1024) return 0;
   const int64_t Sp = S + 4;
   // RB rows: the row buffer, two value tables and at most kResMaxQ loads per thread
   int64_t RB = (kBudget - 4 * T * H) / (Sp + 8 * (T + 1));
