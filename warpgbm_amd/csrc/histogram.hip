@@ -85,8 +85,27 @@ void hist_tiles_kernel(
   constexpr int CW = kHistSlots * V;  // features per chunk
   const int num_bins = BT > 0 ? BT : num_bins_rt;
   const int n_chunks = (n_feats + CW - 1) / CW;
-  const int tile_id = blockIdx.x / n_chunks;
-  const int chunk = blockIdx.x - tile_id * n_chunks;
+  // raw codes: (tile, chunk) work items in the XCD work order over the
+  // planned tiles, so the chunks of a tile share an XCD and its L2 (a raw
+  // row's chunks straddle 128-byte lines that the neighbouring chunk reads
+  // too), each XCD with an even share of the planned work.  Native rows are
+  // line-aligned: tile-major order, chunks round-robin over the XCDs.
+  const int nt = *n_tiles;
+  int tile_id, chunk;
+  bool have;
+  if constexpr (!NAT) {
+    const int64_t n_work = (int64_t)nt * n_chunks;
+    const int64_t per = (n_work + kXcds - 1) / kXcds;
+    const int64_t xid = blockIdx.x;
+    const int64_t wk = (xid % kXcds) * per + xid / kXcds;
+    have = xid / kXcds < per && wk < n_work;
+    tile_id = have ? (int)(wk / n_chunks) : nt;
+    chunk = have ? (int)(wk - (int64_t)tile_id * n_chunks) : 0;
+  } else {
+    tile_id = blockIdx.x / n_chunks;
+    chunk = blockIdx.x - tile_id * n_chunks;
+    have = tile_id < nt;
+  }
   // sm.partial (one tree): every wave reduces the call's per-block maxima of
   // |residual| to the shift itself (no separate launch); workgroup 0, which
   // always exists, stores the maximum and the shift for the finalize
@@ -105,7 +124,7 @@ void hist_tiles_kernel(
       *sm.shift = s_call;
     }
   }
-  if (tile_id >= *n_tiles) return;
+  if (!have) return;
   // FS: chunks past the selected features (the grid is sized for the
   // host's bound) have nothing to do; their partials are never read
   const int n_sel = FS ? *fs.count : n_feats;
@@ -1301,7 +1320,10 @@ static int launch_tiles_t(const HistLaunch& a, hipStream_t st) {
         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     attr_set = true;
   }
-  dim3 grid((unsigned)((int64_t)a.n_chunks * a.max_tiles));
+  // raw codes: a multiple of 8 workgroups, so that every XCD's share of the
+  // work is covered
+  const int64_t n_wg = (int64_t)a.n_chunks * a.max_tiles;
+  dim3 grid((unsigned)(NAT ? n_wg : wgbm_xcd_grid(n_wg)));
   void* tm = timer_begin(a.timer_tag);
   const bool marks = tm && timer_mode() == 1;
   if (marks) WGBM_CHECK(hipEventRecord(timer_start_event(tm), st));
