@@ -95,15 +95,15 @@ class _RecordStream:
     """The engine's per-round tree records (device heaps [rounds, trees, H])
     copied to pinned host memory in blocks of rounds while later rounds run,
     and each landed block turned into reference tree dicts (by the C
-    extension ``_trees``) on the launching thread, a few trees at a time, only
-    while the GPU still has the previous round queued: the conversion uses
+    extension ``_trees``) on the launching thread, a few thousand heap nodes
+    at a time, only while the GPU still has the previous round queued: the conversion uses
     the host's slack between launches and never holds the interpreter lock
     against them (a converter thread did, and left the GPU idle at round
     starts).  What remains when the last round is enqueued is converted by
     ``finish``."""
 
-    BLOCK = 8   # rounds per copy
-    CHUNK = 16  # trees per conversion step (~0.3 ms of host time at depth 6)
+    BLOCK = 8          # rounds per copy
+    CHUNK_NODES = 2048  # heap nodes per conversion step (~0.3-0.4 ms of host time)
 
     def __init__(self, rec):
         self.rec = rec
@@ -165,7 +165,7 @@ class _RecordStream:
         self.copied = end
 
     def _step(self, wait=False):
-        """Convert up to CHUNK trees of the oldest landed block; False when
+        """Convert a few trees (CHUNK_NODES heap nodes) of the oldest landed block; False when
         no landed block has trees left."""
         # landed copies; with wait, block for the oldest one only when none
         # has landed (the rest keep landing while this one is converted)
@@ -182,7 +182,7 @@ class _RecordStream:
         blk = self.landed[0]
         r0, r1, done, f = blk
         total = (r1 - r0) * n_trees
-        hi = min(total, done + self.CHUNK)
+        hi = min(total, done + max(1, self.CHUNK_NODES // H))
         self.flat.extend(_heaps_to_dicts(f["feat"][done:hi], f["bin"][done:hi],
                                          f["leaf"][done:hi], f["count"][done:hi]))
         blk[2] = hi
