@@ -26,7 +26,7 @@ def _need(t: torch.Tensor, name: str, dtype: torch.dtype, ndim: int | None = Non
         raise RuntimeError(f"{name} must be a torch.Tensor")
     if t.dtype != dtype:
         raise RuntimeError(f"{name} must have dtype {dtype}, got {t.dtype}")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise RuntimeError(f"{name} must be a GPU tensor, got device {t.device}")
     if not t.is_contiguous():
         raise RuntimeError(f"{name} must be contiguous")
