@@ -96,11 +96,11 @@ class _RecordStream:
     copied to pinned host memory in blocks of rounds while later rounds run,
     and each landed block turned into reference tree dicts (by the C
     extension ``_trees``) on the launching thread, a few thousand heap nodes
-    at a time, only while the GPU still has the previous round queued: the conversion uses
-    the host's slack between launches and never holds the interpreter lock
-    against them (a converter thread did, and left the GPU idle at round
-    starts).  What remains when the last round is enqueued is converted by
-    ``finish``."""
+    at a time, only while the GPU still has the previous round queued: the
+    conversion uses the host's slack between launches and never holds the
+    interpreter lock against them (a converter thread did, and left the GPU
+    idle at round starts).  What remains when the last round is enqueued is
+    converted by ``finish``."""
 
     BLOCK = 8          # rounds per copy
     CHUNK_NODES = 2048  # heap nodes per conversion step (~0.3-0.4 ms of host time)
@@ -165,8 +165,8 @@ class _RecordStream:
         self.copied = end
 
     def _step(self, wait=False):
-        """Convert a few trees (CHUNK_NODES heap nodes) of the oldest landed block; False when
-        no landed block has trees left."""
+        """Convert a few trees (CHUNK_NODES heap nodes) of the oldest landed
+        block; False when no landed block has trees left."""
         # landed copies; with wait, block for the oldest one only when none
         # has landed (the rest keep landing while this one is converted)
         n_trees, H = self.host["feat"].shape[1], self.host["feat"].shape[2]
