@@ -344,6 +344,16 @@ def test_predict_forest_heap_path_bit_exact(gpu, case, F):
     assert np.array_equal(bits(got), bits(ref))
     if case == "bad_nodes":
         assert np.isnan(ref).any()
+    if case == "plain":
+        # the same codes at an address that is not 8-byte aligned: the raw
+        # read does not apply, the native copy does
+        buf = torch.empty(N * F + 4, dtype=torch.int8, device=dev)
+        cod = buf[4:].view(N, F)
+        cod.copy_(t(codes))
+        assert cod.data_ptr() % 8 == 4 and cod.is_contiguous()
+        out2 = torch.full((N,), 0.25, device=dev)
+        node_kernel.predict_forest(cod, t(table), 0.1, out2)
+        assert np.array_equal(bits(out2.cpu().numpy()), bits(ref))
 
 
 def _random_heap(rng, R, K, depth, F, B):
