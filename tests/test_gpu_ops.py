@@ -230,8 +230,12 @@ def test_compute_histogram3_rejects_bad_input(gpu):
         node_kernel.compute_histogram3(codes.cpu(), r, rows, feats, era, G, G.clone(), 8)
 
 
-@pytest.mark.parametrize("E,F,B", [(1, 300, 32), (4, 50, 2), (7, 33, 17), (1, 5, 127)])
+@pytest.mark.parametrize("E,F,B", [(1, 300, 32), (4, 50, 2), (7, 33, 17), (13, 157, 5),
+                                   (1, 5, 127), (2, 70, 33)])
 def test_compute_split_bit_exact(gpu, E, F, B):
+    """Per-era gains and directions of best_split_kernel.cu:61-88 for 2 to
+    127 bins, including pair counts that leave the last workgroup partly
+    empty (300, 200, 231, 2041, 140 pairs)."""
     print_case("compute_split", E, F, B)
     rng = np.random.default_rng(E * 1000 + F)
     H = rng.integers(0, 60, (E, F, B)).astype(F32)
