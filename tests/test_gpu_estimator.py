@@ -558,20 +558,25 @@ def test_depth_beyond_twenty_bit_exact(gpu):
     assert max(_depth(t) for t in m.forest) > 12
 
 
-@pytest.mark.parametrize("scan,fuse,root", [(1, 1, 1), (0, 0, 1), (1, 0, 1), (1, 1, 0)])
-def test_one_era_level_scans_bit_exact(gpu, scan, fuse, root):
+@pytest.mark.parametrize("scan,fuse,root,part", [(1, 1, 1, 2), (1, 1, 1, 0), (0, 0, 1, 2),
+                                                  (1, 0, 1, 2), (1, 1, 0, 1)])
+def test_one_era_level_scans_bit_exact(gpu, scan, fuse, root, part):
     """The per-level kernels of one-era fits in each setting (engine tuning
     key 3: node scan with a thread or a wave per node; key 4: split search
     and leaf step fused or not; key 5: the root's positions and totals in one
     launch with a root tile plan made once, or the root partition pass and a
-    plan per round) grow the oracle's trees.  Heavy tails on
+    plan per round; key 6: split levels partitioned in one pass with
+    reserved child ranges -- 2 on every level of up to 1024 nodes, 1 where
+    nodes are small -- or route + block prefix + stable scatter) grow the
+    oracle's trees.  Heavy tails on
     60000 rows: nodes spanning many partition blocks whose child maxima move
     their histogram shift (both children histogrammed); depth 12 (2048 nodes
     at the last split level, past the 1024 planned from registers); softmax
     with 5 class trees and 640 nodes at depth 7; 300 features (two split
     workgroups per node, the fused step's last-arrival path)."""
-    print_case("estimator", "one-era level scan, fused finish, root path", scan, fuse, root)
-    tuning = {3: scan, 4: fuse, 5: root}
+    print_case("estimator", "one-era level scan, fused finish, root path, one-pass partition",
+               scan, fuse, root, part)
+    tuning = {3: scan, 4: fuse, 5: root, 6: part}
     rng = np.random.default_rng(12)
     N = 60_000
     X = rng.standard_normal((N, 5)).astype(F32)

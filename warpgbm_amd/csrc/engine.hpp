@@ -201,11 +201,37 @@ __global__ void level_scan_kernel(int32_t nb, PartSums ps, int32_t T, int32_t no
                                   const int32_t* split_l, LevelNext nx, int32_t n_list,
                                   int32_t tile_rows, int32_t max_tiles, Tile* tiles,
                                   int32_t* key_tile_start, int32_t* n_tiles);
+// Per-node words of the one-era single-pass partition (partition_e1_kernel):
+// what a split node's rows add to its left child (row counts of both
+// children, the left rows' wide residual sums, both children's max|r|).
+// Zero outside a level's partition -> level scan window: the level scan
+// reads and clears them.
+struct KeyWords {
+  unsigned long long* cnt;  // left rows * 2^32 + right rows
+  int64_t* qh;              // left rows' sum of (q63 >> 32)
+  int64_t* ql;              // left rows' sum of (q63 & (2^32 - 1))
+  uint32_t* ml;             // left rows' max|r| (float bits)
+  uint32_t* mr;             // right rows' max|r|
+};
+// One-era split levels in one pass: route, rank and place every position
+// (route_kernel + scatter_kernel without the block prefix between them), for
+// levels of at most kPartition1MaxNodes (tree, node)s.
+constexpr int kPartition1MaxNodes = 1024;
+// Nodes that span many blocks make the blocks that share them queue on their
+// words' atomics: by default the one pass runs where a level's nodes average
+// at most this many positions.
+constexpr int64_t kPartition1AutoSpan = 32 * kPartBlock;
+__global__ void partition_e1_kernel(RouteArgs a, KeyWords kw, int32_t n_slots,
+                                    int32_t* order_next, int32_t* keyp_next, float* rpos_next);
+// its dynamic LDS: 28 bytes per (tree, node) slot
+inline size_t partition1_lds_bytes(int64_t n_slots) { return (size_t)n_slots * 28; }
 // One-era levels: level_scan_kernel's work with a thread per (tree, node),
-// up to kLevelScanE1MaxNodes of them, and the next level's tile plan.
+// up to kLevelScanE1MaxNodes of them, and the next level's tile plan.  With
+// kw.cnt set, the children's counts, sums and maxima come from the
+// single-pass partition's words (no block prefix; the words are cleared).
 constexpr int kLevelScanE1MaxNodes = 2048;
-__global__ void level_scan_e1_kernel(int32_t nb, PartSums ps, int32_t n_tn, int64_t n_pos,
-                                     const int64_t* seg, const int32_t* present,
+__global__ void level_scan_e1_kernel(int32_t nb, PartSums ps, KeyWords kw, int32_t n_tn,
+                                     int64_t n_pos, const int64_t* seg, const int32_t* present,
                                      const int32_t* split_l, LevelNext nx, int32_t plan,
                                      int32_t tile_rows, int32_t max_tiles, Tile* tiles,
                                      int32_t* key_tile_start, int32_t* n_tiles);

@@ -91,6 +91,12 @@ struct Engine {
   // are the same every round); 0 = root_setup + root route + block scan +
   // root totals and a plan per round
   int root_path = 1;
+  // one era: split levels partitioned in one pass (partition_e1_kernel and
+  // the level scan over its node words) instead of route + level scan +
+  // scatter: 1 = levels whose nodes average at most kPartition1AutoSpan
+  // positions, 2 = every level of at most kPartition1MaxNodes nodes, 0 = none
+  int part1 = 1;
+  KeyWords kw{};  // [n_keys_max] each, zero between levels
   Tile* root_tiles = nullptr;     // the root level's tile plan (planned by the first round)
   int32_t* root_kts = nullptr;
   int32_t* root_hn = nullptr;
@@ -281,6 +287,13 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->ps.pm_r, e->nb);
   E_ALLOC(e->hkts, e->n_keys_max + 1);
   E_ALLOC(e->hn, 1);
+  if (E == 1) {
+    E_ALLOC(e->kw.cnt, e->n_keys_max);
+    E_ALLOC(e->kw.qh, e->n_keys_max);
+    E_ALLOC(e->kw.ql, e->n_keys_max);
+    E_ALLOC(e->kw.ml, e->n_keys_max);
+    E_ALLOC(e->kw.mr, e->n_keys_max);
+  }
   if (E > 1) {
     E_ALLOC(e->crit, e->nc_max * F * (B - 1));
     E_ALLOC(e->agree, e->nc_max * F * (B - 1));
@@ -295,9 +308,18 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   e->pick_stride = T * nodes_max;
   E_ALLOC(e->done, T * nodes_max);
   {
-    const hipError_t err = hipMemset(e->done, 0, sizeof(uint32_t) * T * nodes_max);
+    hipError_t err = hipMemset(e->done, 0, sizeof(uint32_t) * T * nodes_max);
+    if (err == hipSuccess && E == 1) {
+      const size_t k = (size_t)e->n_keys_max;
+      err = hipMemset(e->kw.cnt, 0, k * sizeof(unsigned long long));
+      if (err == hipSuccess) err = hipMemset(e->kw.qh, 0, k * sizeof(int64_t));
+      if (err == hipSuccess) err = hipMemset(e->kw.ql, 0, k * sizeof(int64_t));
+      if (err == hipSuccess) err = hipMemset(e->kw.ml, 0, k * sizeof(uint32_t));
+      if (err == hipSuccess) err = hipMemset(e->kw.mr, 0, k * sizeof(uint32_t));
+    }
     if (err != hipSuccess) {
-      wgbm_set_error("engine: clearing the arrival counters failed: %s", hipGetErrorString(err));
+      wgbm_set_error("engine: clearing the arrival counters and node words failed: %s",
+                     hipGetErrorString(err));
       engine_destroy(e);
       return (int)err;
     }
@@ -317,6 +339,11 @@ int engine_set_tuning(Engine* e, int key, int64_t value) {
   if (key == 5) {
     WGBM_REQUIRE(value == 0 || value == 1, "one-era root path must be 0 or 1");
     e->root_path = (int)value;
+    return 0;
+  }
+  if (key == 6) {
+    WGBM_REQUIRE(value >= 0 && value <= 2, "one-era single-pass partition must be 0, 1 or 2");
+    e->part1 = (int)value;
     return 0;
   }
   if (key == 2) {
@@ -789,8 +816,18 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     // the children's max|r| decides their histogram shifts; children at the
     // last depth are leaves and need none
     rl.want_max = d + 1 < D ? 1 : 0;
-    hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads),
-                       route_lds_bytes(rl), st, rl);
+    // one era: route and place every position in one pass, the level scan
+    // then reads the node words
+    const bool one_pass = d < D && E == 1 && e->lscan_e1 && n_tn <= kPartition1MaxNodes &&
+                          (e->part1 == 2 || (e->part1 == 1 && n_pos <= kPartition1AutoSpan * n_tn));
+    if (one_pass) {
+      hipLaunchKernelGGL(partition_e1_kernel, dim3((unsigned)e->nb), dim3(kPartThreads),
+                         partition1_lds_bytes(n_tn), st, rl, e->kw, (int32_t)n_tn,
+                         e->order[nxt], e->keyp[nxt], e->rpos[nxt]);
+    } else {
+      hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads),
+                         route_lds_bytes(rl), st, rl);
+    }
     WGBM_LAUNCH_CHECK();
     planned = false;
     alive_ready = false;
@@ -828,7 +865,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       }
       if (E == 1 && e->lscan_e1) {
         hipLaunchKernelGGL(level_scan_e1_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb,
-                           e->ps, (int32_t)n_tn, n_pos, e->seg[cur], e->present[cur], e->split_l,
+                           e->ps, one_pass ? e->kw : KeyWords{}, (int32_t)n_tn, n_pos,
+                           e->seg[cur], e->present[cur], e->split_l,
                            nx, next_hist ? 1 : 0, (int32_t)lp.R, (int32_t)lp.max_tiles, e->htiles,
                            e->hkts, e->hn);
         WGBM_LAUNCH_CHECK();
@@ -861,7 +899,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       WGBM_LAUNCH_CHECK();
       alive_ready = next_alive;
     }
-    if (d < D) {
+    if (d < D && !one_pass) {
       hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, n_pos,
                          E, e->seg[cur], e->seg[nxt], e->keyp[cur], e->dirbit, e->ps,
                          e->order[cur], e->order[nxt], e->keyp[nxt], e->rpos[cur],

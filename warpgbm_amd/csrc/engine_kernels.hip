@@ -1179,6 +1179,222 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
   }
 }
 
+// One-era split level in one pass (E == 1, mode 1, at most
+// kPartition1MaxNodes (tree, node)s): every position of a block of
+// kPartBlock is routed (route_kernel's directions, leaf updates, left sums
+// and maxima) and placed in the next level's arrays at once.  Its node's
+// left rows fill the left child's range from the node's first position
+// upwards, its right rows the right child's range from the node's last
+// position downwards, so the children's bounds need not be known when a row
+// is placed.  A node inside the block takes the block's ranks directly and
+// stores its words (kw) plainly; a node that crosses the block's edges --
+// only the block's first and last nodes can -- reserves the block's part of
+// both ranges with one atomic add on its packed row counts (left * 2^32 +
+// right) and adds its sums and maxima with relaxed atomics.  Every sum is
+// an exact integer and rows inside a node have no order that any result
+// depends on, so the order in which blocks reserve changes no output;
+// level_scan_e1_kernel then reads the whole words (and clears them).
+// Positions are strided over the threads (position j * kPartThreads + tid
+// of the block), so that the rows of one child taken by one store
+// instruction land on consecutive addresses.  The block's nodes are
+// consecutive keys from its first position's key kf: node k's LDS slot is
+// k - kf (< n_slots = the level's (tree, node)s).
+__global__ __launch_bounds__(kPartThreads) void partition_e1_kernel(
+    RouteArgs a, KeyWords kw, int32_t n_slots, int32_t* __restrict__ order_next,
+    int32_t* __restrict__ keyp_next, float* __restrict__ rpos_next) {
+  constexpr int PJ = kPartBlock / kPartThreads;
+  constexpr int NW = kPartThreads / 64;
+  // per slot: the left rows' (q63 >> 32) sum * 2^11 + their count (at most
+  // kPartBlock < 2^11 rows, |q63 >> 32| <= 2^30 per row), the (q63 mod 2^32)
+  // sum, both children's max|r|, and the block's lefts before the node's
+  // first position (partition1_lds_bytes)
+  extern __shared__ int64_t s_dyn[];
+  int64_t* s_qn = s_dyn;
+  int64_t* s_ql = s_dyn + n_slots;
+  uint32_t* s_ml = (uint32_t*)(s_dyn + 2 * n_slots);
+  uint32_t* s_mr = s_ml + n_slots;
+  int32_t* s_lb = (int32_t*)(s_mr + n_slots);
+  __shared__ int32_t s_c[PJ * NW];          // left positions of each (phase, wave) group
+  __shared__ unsigned long long s_base[2];  // reserved bases of the first / last node
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
+  const int64_t p1 = p0 + kPartBlock < a.n_pos ? p0 + kPartBlock : a.n_pos;
+  const bool maxes = a.want_max != 0;
+  const int kf = a.keyp[p0];
+  int key[PJ];
+  int32_t rowv[PJ];
+  float rv[PJ];
+  bool ok[PJ];
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const int64_t p = p0 + j * kPartThreads + tid;
+    ok[j] = p < p1;
+    key[j] = a.keyp[ok[j] ? p : p1 - 1];
+    rowv[j] = ok[j] ? a.order[p] : 0;
+    rv[j] = ok[j] ? a.rpos[p] : 0.0f;
+  }
+  // the node's bounds and route record (one round of independent loads)
+  int64_t sk[PJ], se[PJ];
+  NodeRoute nr[PJ];
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    sk[j] = a.seg[key[j]];
+    se[j] = a.seg[key[j] + 1];
+    nr[j] = a.nroute[key[j]];
+  }
+  int cv[PJ];
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const int col = ok[j] ? nr[j].col : -2;
+    cv[j] = col >= 0 ? (int)a.codes_cm[(int64_t)col * a.n + rowv[j]] : 0;
+  }
+  uint8_t dirs[PJ];  // 0 left, 1 right, 2 stays (the node does not split)
+  bool opens[PJ];    // the node's first position in the block
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const int col = ok[j] ? nr[j].col : -2;
+    uint8_t dir = 2;
+    if (col == -1) {
+      // the node is a leaf: add lr * leaf to its rows' predictions
+      const int t = key[j] / a.nodes;
+      float* pc = a.pred + (int64_t)t * a.pcol + (int64_t)rowv[j] * a.pstride;
+      *pc = *pc + a.lr * nr[j].leaf;
+    } else if (col >= 0) {
+      dir = cv[j] > nr[j].bin ? 1 : 0;
+    }
+    dirs[j] = dir;
+    const int64_t first = sk[j] > p0 ? sk[j] : p0;
+    opens[j] = ok[j] && dir != 2 && first - p0 == j * kPartThreads + tid;
+    if (opens[j]) {
+      const int sl = key[j] - kf;
+      s_qn[sl] = 0;
+      s_ql[sl] = 0;
+      s_ml[sl] = 0u;
+      s_mr[sl] = 0u;
+    }
+  }
+  // left positions before each one: rank among the wave's lefts plus the
+  // lefts of the (phase, wave) groups before it
+  int32_t rank[PJ];
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const uint64_t m = __ballot(dirs[j] == 0);
+    rank[j] = (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    if (lane == 0) s_c[j * NW + w] = __builtin_popcountll(m);
+  }
+  wgbm_lds_barrier();  // group counts and cleared slots
+  // sums and maxima per node slot (a wave whose active lanes share a slot
+  // reduces first and adds once)
+  auto add_slot = [&](int sl, bool act, int64_t qn, int64_t ql, uint32_t ml, uint32_t mr) {
+    const uint64_t on = __ballot(act);
+    if (on == 0ull) return;
+    const int s0 = __builtin_amdgcn_readlane(sl, __builtin_ctzll(on));
+    if (__ballot(act && sl != s0) == 0ull) {
+      qn = wgbm_wave_reduce_add_i64(act ? qn : (int64_t)0);
+      ql = wgbm_wave_reduce_add_i64(act ? ql : (int64_t)0);
+      if (maxes) {
+        ml = wgbm_wave_reduce_max_u32(act ? ml : 0u);
+        mr = wgbm_wave_reduce_max_u32(act ? mr : 0u);
+      }
+      if (lane == 0) {
+        if (qn) atomicAdd((unsigned long long*)&s_qn[s0], (unsigned long long)qn);
+        if (ql) atomicAdd((unsigned long long*)&s_ql[s0], (unsigned long long)ql);
+        if (ml) atomicMax(&s_ml[s0], ml);
+        if (mr) atomicMax(&s_mr[s0], mr);
+      }
+    } else if (act) {
+      if (qn) atomicAdd((unsigned long long*)&s_qn[sl], (unsigned long long)qn);
+      if (ql) atomicAdd((unsigned long long*)&s_ql[sl], (unsigned long long)ql);
+      if (ml) atomicMax(&s_ml[sl], ml);
+      if (mr) atomicMax(&s_mr[sl], mr);
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    int pre = 0;
+    for (int i = 0; i < j * NW + w; ++i) pre += s_c[i];
+    rank[j] += pre;
+    if (opens[j]) s_lb[key[j] - kf] = rank[j];
+    int64_t qn = 0, ql = 0;
+    uint32_t ml = 0u, mr = 0u;
+    if (dirs[j] == 0) {
+      const int64_t q = (int64_t)rintf(ldexpf(rv[j], nr[j].s63));
+      qn = (q >> 32) * 2048 + 1;
+      ql = q & 0xffffffffll;
+    }
+    if (maxes) {
+      const uint32_t m = wgbm_abs_bits(rv[j]);
+      ml = dirs[j] == 0 ? m : 0u;
+      mr = dirs[j] == 1 ? m : 0u;
+    }
+    add_slot(key[j] - kf, dirs[j] != 2, qn, ql, ml, mr);
+  }
+  wgbm_lds_barrier();  // slot sums, maxima and left bases are complete
+  // the node words: the thread of a split node's first position in the
+  // block stores them (a node inside the block) or adds them and reserves
+  // the block's part of the children's ranges (a node crossing its edges)
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    if (!opens[j]) continue;
+    const int k = key[j], sl = k - kf;
+    const int64_t qn = s_qn[sl];
+    const int32_t nl = (int32_t)(qn & 2047);
+    const int64_t qh = qn >> 11, ql = s_ql[sl];
+    const int64_t b0 = sk[j] > p0 ? sk[j] : p0, b1 = se[j] < p1 ? se[j] : p1;
+    const int32_t nrr = (int32_t)(b1 - b0) - nl;
+    const unsigned long long packed = ((unsigned long long)(uint32_t)nl << 32) | (uint32_t)nrr;
+    if (sk[j] >= p0 && se[j] <= p1) {
+      kw.cnt[k] = packed;
+      kw.qh[k] = qh;
+      kw.ql[k] = ql;
+      if (maxes) {
+        kw.ml[k] = s_ml[sl];
+        kw.mr[k] = s_mr[sl];
+      }
+    } else {
+      s_base[b0 == p0 ? 0 : 1] = atomicAdd(kw.cnt + k, packed);
+      if (qh) atomicAdd((unsigned long long*)(kw.qh + k), (unsigned long long)qh);
+      if (ql) atomicAdd((unsigned long long*)(kw.ql + k), (unsigned long long)ql);
+      if (maxes) {
+        if (s_ml[sl]) atomicMax(kw.ml + k, s_ml[sl]);
+        if (s_mr[sl]) atomicMax(kw.mr + k, s_mr[sl]);
+      }
+    }
+  }
+  wgbm_lds_barrier();  // the reserved bases
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    if (!ok[j]) continue;
+    const int64_t p = p0 + j * kPartThreads + tid;
+    const int kl = 2 * key[j];  // the left child's key (one era)
+    if (dirs[j] == 2) {
+      // a node that does not split: its rows stay, in its left child's segment
+      order_next[p] = rowv[j];
+      keyp_next[p] = kl;
+      rpos_next[p] = rv[j];
+      continue;
+    }
+    const int64_t b0 = sk[j] > p0 ? sk[j] : p0;
+    const bool cross = sk[j] < p0 || se[j] > p1;
+    const unsigned long long base = cross ? s_base[b0 == p0 ? 0 : 1] : 0ull;
+    const int32_t rl = rank[j] - s_lb[key[j] - kf];  // the node's lefts before p in the block
+    int64_t dst;
+    if (dirs[j] == 0) {
+      dst = sk[j] + (int64_t)(base >> 32) + rl;
+    } else {
+      const int32_t rr = (int32_t)(p - b0) - rl;  // its rights before p
+      dst = se[j] - 1 - (int64_t)(base & 0xffffffffull) - rr;
+    }
+    // (always inside the node while its words start at zero; the test keeps
+    // a broken invariant from writing past it)
+    if (dst < sk[j] || dst >= se[j]) continue;
+    order_next[dst] = rowv[j];
+    keyp_next[dst] = kl + dirs[j];
+    rpos_next[dst] = rv[j];
+  }
+}
+
 // The three steps between route and scatter of a level with few keys (at
 // most 64 eras), in one workgroup of 1024 threads: the block prefix, the node
 // scan with one wave per node (wave w takes nodes w, w + 16, ...), and the
@@ -1391,15 +1607,17 @@ __device__ inline void write_entry_tiles(int key, int64_t b0, uint32_t len, int 
 // the words just written (plan_tiles_body).  Same outputs as
 // level_scan_kernel.
 __global__ __launch_bounds__(1024) void level_scan_e1_kernel(
-    int32_t nb, PartSums ps, int32_t n_tn, int64_t n_pos, const int64_t* __restrict__ seg,
-    const int32_t* __restrict__ present, const int32_t* __restrict__ split_l, LevelNext nx,
-    int32_t plan, int32_t tile_rows, int32_t max_tiles, Tile* __restrict__ tiles,
-    int32_t* __restrict__ key_tile_start, int32_t* __restrict__ n_tiles) {
+    int32_t nb, PartSums ps, KeyWords kw, int32_t n_tn, int64_t n_pos,
+    const int64_t* __restrict__ seg, const int32_t* __restrict__ present,
+    const int32_t* __restrict__ split_l, LevelNext nx, int32_t plan, int32_t tile_rows,
+    int32_t max_tiles, Tile* __restrict__ tiles, int32_t* __restrict__ key_tile_start,
+    int32_t* __restrict__ n_tiles) {
   __shared__ int64_t l_qh[kScanLdsBlocks], l_ql[kScanLdsBlocks];
   __shared__ int64_t l_n[kScanLdsBlocks];
   __shared__ uint32_t l_ml[kScanLdsBlocks], l_mr[kScanLdsBlocks];
   const int t = threadIdx.x;
   const bool have_max = nx.have_max != 0;
+  const bool one_pass = kw.cnt != nullptr;  // uniform
   // a node's words that do not need the prefix scan: q0 / q1 are its first
   // and last blocks; for a node inside one block its own partials, else the
   // partials of its part of the first block
@@ -1422,6 +1640,25 @@ __global__ __launch_bounds__(1024) void level_scan_e1_kernel(
     x.hs = nx.node_shift[tn];
     x.tqh = nx.tot_qh[tn];
     x.tql = nx.tot_ql[tn];
+    x.bqh = x.bql = 0;
+    x.bn = 0;
+    x.oml = x.omr = x.bml = x.bmr = 0u;
+    if (one_pass) {
+      // the node's whole left sums (the partition's words), then cleared
+      x.on = (int32_t)(kw.cnt[tn] >> 32);
+      x.oqh = kw.qh[tn];
+      x.oql = kw.ql[tn];
+      if (have_max) {
+        x.oml = kw.ml[tn];
+        x.omr = kw.mr[tn];
+      }
+      kw.cnt[tn] = 0ull;
+      kw.qh[tn] = 0;
+      kw.ql[tn] = 0;
+      kw.ml[tn] = 0u;
+      kw.mr[tn] = 0u;
+      return x;
+    }
     const int64_t q0 = x.base / kPartBlock;
     const int64_t qb = q0 < nb ? q0 : nb - 1;  // an empty node may start at n_pos
     x.oqh = ps.own_qh[tn];
@@ -1430,7 +1667,6 @@ __global__ __launch_bounds__(1024) void level_scan_e1_kernel(
     x.bqh = ps.bl_qh[qb];
     x.bql = ps.bl_ql[qb];
     x.bn = ps.bl_n[qb];
-    x.oml = x.omr = x.bml = x.bmr = 0u;
     if (have_max) {
       x.oml = ps.own_ml[tn];
       x.omr = ps.own_mr[tn];
@@ -1441,11 +1677,15 @@ __global__ __launch_bounds__(1024) void level_scan_e1_kernel(
   };
   NodeWords first{};
   const bool in_lds = nb <= kScanLdsBlocks;
-  // the node's own words load while the block prefixes are scanned
-  block_scan_body(nb, ps, have_max, in_lds, ScanLds{l_qh, l_ql, l_n, l_ml, l_mr}, [&]() {
+  if (one_pass) {
     if (t < n_tn) first = load_node(t);
-  });
-  if (!in_lds) __syncthreads();  // the prefixes are read back from global memory
+  } else {
+    // the node's own words load while the block prefixes are scanned
+    block_scan_body(nb, ps, have_max, in_lds, ScanLds{l_qh, l_ql, l_n, l_ml, l_mr}, [&]() {
+      if (t < n_tn) first = load_node(t);
+    });
+    if (!in_lds) __syncthreads();  // the prefixes are read back from global memory
+  }
   // the entries of this thread's node (when n_tn <= 1024): keys and bounds
   int32_t ka = -1, kb = -1;
   int64_t a0 = 0, a1 = 0, b1 = 0;
@@ -1453,7 +1693,7 @@ __global__ __launch_bounds__(1024) void level_scan_e1_kernel(
     const int64_t cnt = x.end - x.base;
     const bool sp = x.pr && x.sl >= 0;
     const int64_t xq0 = x.base / kPartBlock, xq1 = cnt > 0 ? (x.end - 1) / kPartBlock : xq0;
-    const bool inside = xq0 == xq1;
+    const bool inside = one_pass || xq0 == xq1;  // (one pass: the node's words are whole)
     const bool use = sp && cnt > 0;
     int64_t L = cnt, qh = 0, ql = 0;
     uint32_t ml = use ? (inside ? x.oml : x.bml) : 0u;
