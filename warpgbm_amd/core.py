@@ -17,7 +17,6 @@ on its own rows, and histogram sums are exact (see include/warpgbm_amd.h).
 """
 from __future__ import annotations
 
-import gc
 import pickle
 
 import numpy as np
@@ -122,12 +121,7 @@ class _RecordStream:
         self.prev_ev = None  # completion of the round before the last enqueued one
         self.last_ev = None
         self.side = None     # the copies' stream
-        # the tree dicts form no reference cycles; pausing the cyclic
-        # collector keeps it from re-walking the growing forest on every
-        # allocation threshold (about 4x faster at 2000 trees of depth 6)
-        self.gc_was_on = gc.isenabled()
         self.closed = False
-        gc.disable()
 
     def round_done(self, j, n_rounds):
         """Round j of n_rounds has been enqueued: issue a block copy every
@@ -213,14 +207,12 @@ class _RecordStream:
             self.close()
 
     def close(self):
-        """Restore the collector (also after an error, once the copies in
-        flight have landed)."""
+        """Wait for the copies in flight (also after an error: the pinned
+        buffer must outlive them)."""
         if not self.closed:
             self.closed = True
             for _, _, ev in self.pending:
                 ev.synchronize()
-            if self.gc_was_on:
-                gc.enable()
 
 
 class WarpGBM(BaseEstimator, RegressorMixin):
