@@ -825,7 +825,8 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
                          partition1_lds_bytes(n_tn), st, rl, e->kw, (int32_t)n_tn,
                          e->order[nxt], e->keyp[nxt], e->rpos[nxt]);
     } else {
-      hipLaunchKernelGGL(route_kernel, dim3((unsigned)e->nb), dim3(kPartThreads),
+      const int64_t grid = rl.mode == 2 ? wgbm_xcd_grid(e->nb) : e->nb;
+      hipLaunchKernelGGL(route_kernel, dim3((unsigned)grid), dim3(kPartThreads),
                          route_lds_bytes(rl), st, rl);
     }
     WGBM_LAUNCH_CHECK();

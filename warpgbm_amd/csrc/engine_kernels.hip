@@ -477,7 +477,17 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   __shared__ int64_t s_sl;  // start of the block's last segment
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
+  // Mode 2 (leaf updates only) takes its blocks in the XCD work order
+  // (grid wgbm_xcd_grid(blocks)): each XCD a contiguous range of positions,
+  // so a tree's random prediction updates stay in one or two XCDs' L2
+  // instead of pulling the tree's lines into all eight.
+  int64_t bx = blockIdx.x;
+  if (a.mode == 2) {
+    const int64_t nbk = (a.n_pos + kPartBlock - 1) / kPartBlock;
+    bx = wgbm_xcd_work(blockIdx.x, nbk);
+    if (bx >= nbk) return;  // uniform per workgroup
+  }
+  const int64_t p0 = bx * kPartBlock;
   const int64_t p1 = p0 + kPartBlock < a.n_pos ? p0 + kPartBlock : a.n_pos;
   const bool sums = a.mode != 2;
   const bool maxes = sums && a.want_max;
