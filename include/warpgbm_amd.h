@@ -282,11 +282,11 @@ int wgbm_engine_round(wgbm_engine* eng, const void* target, float* pred, const i
  * (1 = its positions and totals in one launch and the root level's
  * histogram tiles planned once per engine, default; 0 = a root partition
  * pass, block scan and totals launch, and a plan per round); key 6 = the
- * one-era split levels' partition: one pass that routes and places every
- * row, each node's children filled from its two ends (2 = on every level of
- * at most 1024 nodes; 1 = on those whose nodes average at most 32768
- * positions, default), or route, block prefix and a stable scatter (0).
- * Set before the first round; every setting grows the same trees. */
+ * one-era split levels' partition (1 = one pass that routes and places every
+ * row, each node's children filled from its two ends, on levels of at most
+ * 1024 (tree, node)s, default; 0 = route, block prefix and a stable
+ * scatter).  Set before the first round; every setting grows the same
+ * trees. */
 int wgbm_engine_set_tuning(wgbm_engine* eng, int32_t key, int64_t value);
 void wgbm_engine_destroy(wgbm_engine* eng);
 

@@ -558,17 +558,16 @@ def test_depth_beyond_twenty_bit_exact(gpu):
     assert max(_depth(t) for t in m.forest) > 12
 
 
-@pytest.mark.parametrize("scan,fuse,root,part", [(1, 1, 1, 2), (1, 1, 1, 0), (0, 0, 1, 2),
-                                                  (1, 0, 1, 2), (1, 1, 0, 1)])
+@pytest.mark.parametrize("scan,fuse,root,part", [(1, 1, 1, 1), (1, 1, 1, 0), (0, 0, 1, 1),
+                                                  (1, 0, 1, 1), (1, 1, 0, 1)])
 def test_one_era_level_scans_bit_exact(gpu, scan, fuse, root, part):
     """The per-level kernels of one-era fits in each setting (engine tuning
     key 3: node scan with a thread or a wave per node; key 4: split search
     and leaf step fused or not; key 5: the root's positions and totals in one
     launch with a root tile plan made once, or the root partition pass and a
-    plan per round; key 6: split levels partitioned in one pass with
-    reserved child ranges -- 2 on every level of up to 1024 nodes, 1 where
-    nodes are small -- or route + block prefix + stable scatter) grow the
-    oracle's trees.  Heavy tails on
+    plan per round; key 6: split levels of up to 1024 nodes partitioned
+    in one pass with reserved child ranges, or route + block prefix + stable
+    scatter) grow the oracle's trees.  Heavy tails on
     60000 rows: nodes spanning many partition blocks whose child maxima move
     their histogram shift (both children histogrammed); depth 12 (2048 nodes
     at the last split level, past the 1024 planned from registers); softmax

@@ -162,6 +162,7 @@ struct RouteArgs {
   uint8_t* dirbit;
   const int32_t* keyp;  // segment key of every position
   PartSums ps;
+  int32_t xcd_order;  // mode 2: blocks in the XCD work order (grid wgbm_xcd_grid)
 };
 __global__ void route_kernel(RouteArgs a);
 // dynamic LDS of route_kernel: the slot sums, plus the node maxima
@@ -218,9 +219,10 @@ struct KeyWords {
 // levels of at most kPartition1MaxNodes (tree, node)s.
 constexpr int kPartition1MaxNodes = 1024;
 // Nodes that span many blocks make the blocks that share them queue on their
-// words' atomics: by default the one pass runs where a level's nodes average
-// at most this many positions.
-constexpr int64_t kPartition1AutoSpan = 32 * kPartBlock;
+// words' atomics: levels whose nodes average more than kPartition1WideSpan
+// positions take blocks of 4096 positions (a quarter of the blocks).
+constexpr int64_t kPartition1WideSpan = 16 * 1024;
+template <int NT>  // threads per block: 4 NT positions
 __global__ void partition_e1_kernel(RouteArgs a, KeyWords kw, int32_t n_slots,
                                     int32_t* order_next, int32_t* keyp_next, float* rpos_next);
 // its dynamic LDS: 28 bytes per (tree, node) slot

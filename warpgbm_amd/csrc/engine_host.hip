@@ -91,10 +91,9 @@ struct Engine {
   // are the same every round); 0 = root_setup + root route + block scan +
   // root totals and a plan per round
   int root_path = 1;
-  // one era: split levels partitioned in one pass (partition_e1_kernel and
-  // the level scan over its node words) instead of route + level scan +
-  // scatter: 1 = levels whose nodes average at most kPartition1AutoSpan
-  // positions, 2 = every level of at most kPartition1MaxNodes nodes, 0 = none
+  // one era: 1 = split levels of at most kPartition1MaxNodes (tree, node)s
+  // partitioned in one pass (partition_e1_kernel and the level scan over its
+  // node words), 0 = route + level scan + scatter
   int part1 = 1;
   KeyWords kw{};  // [n_keys_max] each, zero between levels
   Tile* root_tiles = nullptr;     // the root level's tile plan (planned by the first round)
@@ -342,7 +341,7 @@ int engine_set_tuning(Engine* e, int key, int64_t value) {
     return 0;
   }
   if (key == 6) {
-    WGBM_REQUIRE(value >= 0 && value <= 2, "one-era single-pass partition must be 0, 1 or 2");
+    WGBM_REQUIRE(value == 0 || value == 1, "one-era single-pass partition must be 0 or 1");
     e->part1 = (int)value;
     return 0;
   }
@@ -818,14 +817,22 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     rl.want_max = d + 1 < D ? 1 : 0;
     // one era: route and place every position in one pass, the level scan
     // then reads the node words
-    const bool one_pass = d < D && E == 1 && e->lscan_e1 && n_tn <= kPartition1MaxNodes &&
-                          (e->part1 == 2 || (e->part1 == 1 && n_pos <= kPartition1AutoSpan * n_tn));
+    const bool one_pass =
+        d < D && E == 1 && e->lscan_e1 && e->part1 && n_tn <= kPartition1MaxNodes;
     if (one_pass) {
-      hipLaunchKernelGGL(partition_e1_kernel, dim3((unsigned)e->nb), dim3(kPartThreads),
-                         partition1_lds_bytes(n_tn), st, rl, e->kw, (int32_t)n_tn,
-                         e->order[nxt], e->keyp[nxt], e->rpos[nxt]);
+      const size_t lds = partition1_lds_bytes(n_tn);
+      if (n_pos > kPartition1WideSpan * n_tn) {
+        hipLaunchKernelGGL(partition_e1_kernel<1024>, dim3((unsigned)((n_pos + 4095) / 4096)),
+                           dim3(1024), lds, st, rl, e->kw, (int32_t)n_tn, e->order[nxt],
+                           e->keyp[nxt], e->rpos[nxt]);
+      } else {
+        hipLaunchKernelGGL(partition_e1_kernel<256>, dim3((unsigned)((n_pos + 1023) / 1024)),
+                           dim3(256), lds, st, rl, e->kw, (int32_t)n_tn, e->order[nxt],
+                           e->keyp[nxt], e->rpos[nxt]);
+      }
     } else {
-      const int64_t grid = rl.mode == 2 ? wgbm_xcd_grid(e->nb) : e->nb;
+      rl.xcd_order = rl.mode == 2 && T > 1 ? 1 : 0;
+      const int64_t grid = rl.xcd_order ? wgbm_xcd_grid(e->nb) : e->nb;
       hipLaunchKernelGGL(route_kernel, dim3((unsigned)grid), dim3(kPartThreads),
                          route_lds_bytes(rl), st, rl);
     }

@@ -477,12 +477,12 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   __shared__ int64_t s_sl;  // start of the block's last segment
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  // Mode 2 (leaf updates only) takes its blocks in the XCD work order
-  // (grid wgbm_xcd_grid(blocks)): each XCD a contiguous range of positions,
-  // so a tree's random prediction updates stay in one or two XCDs' L2
-  // instead of pulling the tree's lines into all eight.
+  // Mode 2 (leaf updates only) of several trees takes its blocks in the XCD
+  // work order (grid wgbm_xcd_grid(blocks)): each XCD a contiguous range of
+  // positions, so a tree's random prediction updates stay in one or two
+  // XCDs' L2 instead of pulling the tree's lines into all eight.
   int64_t bx = blockIdx.x;
-  if (a.mode == 2) {
+  if (a.xcd_order) {
     const int64_t nbk = (a.n_pos + kPartBlock - 1) / kPartBlock;
     bx = wgbm_xcd_work(blockIdx.x, nbk);
     if (bx >= nbk) return;  // uniform per workgroup
@@ -1190,8 +1190,8 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
 }
 
 // One-era split level in one pass (E == 1, mode 1, at most
-// kPartition1MaxNodes (tree, node)s): every position of a block of
-// kPartBlock is routed (route_kernel's directions, leaf updates, left sums
+// kPartition1MaxNodes (tree, node)s): every position of a block of 4 NT
+// positions (NT threads) is routed (route_kernel's directions, leaf updates, left sums
 // and maxima) and placed in the next level's arrays at once.  Its node's
 // left rows fill the left child's range from the node's first position
 // upwards, its right rows the right child's range from the node's last
@@ -1204,18 +1204,24 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
 // an exact integer and rows inside a node have no order that any result
 // depends on, so the order in which blocks reserve changes no output;
 // level_scan_e1_kernel then reads the whole words (and clears them).
-// Positions are strided over the threads (position j * kPartThreads + tid
-// of the block), so that the rows of one child taken by one store
+// Positions are strided over the threads (position j * NT + tid of the
+// block), so that the rows of one child taken by one store
 // instruction land on consecutive addresses.  The block's nodes are
 // consecutive keys from its first position's key kf: node k's LDS slot is
 // k - kf (< n_slots = the level's (tree, node)s).
-__global__ __launch_bounds__(kPartThreads) void partition_e1_kernel(
-    RouteArgs a, KeyWords kw, int32_t n_slots, int32_t* __restrict__ order_next,
-    int32_t* __restrict__ keyp_next, float* __restrict__ rpos_next) {
-  constexpr int PJ = kPartBlock / kPartThreads;
-  constexpr int NW = kPartThreads / 64;
-  // per slot: the left rows' (q63 >> 32) sum * 2^11 + their count (at most
-  // kPartBlock < 2^11 rows, |q63 >> 32| <= 2^30 per row), the (q63 mod 2^32)
+template <int NT>
+__global__ __launch_bounds__(NT) void partition_e1_kernel(RouteArgs a, KeyWords kw,
+                                                          int32_t n_slots,
+                                                          int32_t* __restrict__ order_next,
+                                                          int32_t* __restrict__ keyp_next,
+                                                          float* __restrict__ rpos_next) {
+  constexpr int PJ = 4;              // positions per thread
+  constexpr int PB = PJ * NT;        // positions per block
+  constexpr int NW = NT / 64;
+  constexpr int kCountBits = 13;     // row counts packed below the hi sums
+  static_assert(PB < (1 << kCountBits), "block rows fit the count field");
+  // per slot: the left rows' (q63 >> 32) sum * 2^13 + their count (at most
+  // PB < 2^13 rows, |q63 >> 32| <= 2^30 per row), the (q63 mod 2^32)
   // sum, both children's max|r|, and the block's lefts before the node's
   // first position (partition1_lds_bytes)
   extern __shared__ int64_t s_dyn[];
@@ -1227,8 +1233,8 @@ __global__ __launch_bounds__(kPartThreads) void partition_e1_kernel(
   __shared__ int32_t s_c[PJ * NW];          // left positions of each (phase, wave) group
   __shared__ unsigned long long s_base[2];  // reserved bases of the first / last node
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t p0 = (int64_t)blockIdx.x * kPartBlock;
-  const int64_t p1 = p0 + kPartBlock < a.n_pos ? p0 + kPartBlock : a.n_pos;
+  const int64_t p0 = (int64_t)blockIdx.x * PB;
+  const int64_t p1 = p0 + PB < a.n_pos ? p0 + PB : a.n_pos;
   const bool maxes = a.want_max != 0;
   const int kf = a.keyp[p0];
   int key[PJ];
@@ -1237,7 +1243,7 @@ __global__ __launch_bounds__(kPartThreads) void partition_e1_kernel(
   bool ok[PJ];
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
-    const int64_t p = p0 + j * kPartThreads + tid;
+    const int64_t p = p0 + j * NT + tid;
     ok[j] = p < p1;
     key[j] = a.keyp[ok[j] ? p : p1 - 1];
     rowv[j] = ok[j] ? a.order[p] : 0;
@@ -1274,7 +1280,7 @@ __global__ __launch_bounds__(kPartThreads) void partition_e1_kernel(
     }
     dirs[j] = dir;
     const int64_t first = sk[j] > p0 ? sk[j] : p0;
-    opens[j] = ok[j] && dir != 2 && first - p0 == j * kPartThreads + tid;
+    opens[j] = ok[j] && dir != 2 && first - p0 == j * NT + tid;
     if (opens[j]) {
       const int sl = key[j] - kf;
       s_qn[sl] = 0;
@@ -1320,17 +1326,20 @@ __global__ __launch_bounds__(kPartThreads) void partition_e1_kernel(
       if (mr) atomicMax(&s_mr[sl], mr);
     }
   };
+  // the groups' exclusive prefix, scanned by every wave over lanes 0 ..
+  // PJ * NW - 1 (at most 64 groups)
+  static_assert(PJ * NW <= 64, "one lane per (phase, wave) group");
+  const int64_t gcount = lane < PJ * NW ? s_c[lane] : 0;
+  const int64_t gexcl = wgbm_wave_incl_scan_i64(gcount) - gcount;
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
-    int pre = 0;
-    for (int i = 0; i < j * NW + w; ++i) pre += s_c[i];
-    rank[j] += pre;
+    rank[j] += (int32_t)wgbm_readlane_i64(gexcl, j * NW + w);
     if (opens[j]) s_lb[key[j] - kf] = rank[j];
     int64_t qn = 0, ql = 0;
     uint32_t ml = 0u, mr = 0u;
     if (dirs[j] == 0) {
       const int64_t q = (int64_t)rintf(ldexpf(rv[j], nr[j].s63));
-      qn = (q >> 32) * 2048 + 1;
+      qn = (q >> 32) * (1 << kCountBits) + 1;
       ql = q & 0xffffffffll;
     }
     if (maxes) {
@@ -1349,8 +1358,8 @@ __global__ __launch_bounds__(kPartThreads) void partition_e1_kernel(
     if (!opens[j]) continue;
     const int k = key[j], sl = k - kf;
     const int64_t qn = s_qn[sl];
-    const int32_t nl = (int32_t)(qn & 2047);
-    const int64_t qh = qn >> 11, ql = s_ql[sl];
+    const int32_t nl = (int32_t)(qn & ((1 << kCountBits) - 1));
+    const int64_t qh = qn >> kCountBits, ql = s_ql[sl];
     const int64_t b0 = sk[j] > p0 ? sk[j] : p0, b1 = se[j] < p1 ? se[j] : p1;
     const int32_t nrr = (int32_t)(b1 - b0) - nl;
     const unsigned long long packed = ((unsigned long long)(uint32_t)nl << 32) | (uint32_t)nrr;
@@ -1376,7 +1385,7 @@ __global__ __launch_bounds__(kPartThreads) void partition_e1_kernel(
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
     if (!ok[j]) continue;
-    const int64_t p = p0 + j * kPartThreads + tid;
+    const int64_t p = p0 + j * NT + tid;
     const int kl = 2 * key[j];  // the left child's key (one era)
     if (dirs[j] == 2) {
       // a node that does not split: its rows stay, in its left child's segment
@@ -1404,6 +1413,10 @@ __global__ __launch_bounds__(kPartThreads) void partition_e1_kernel(
     rpos_next[dst] = rv[j];
   }
 }
+template __global__ void partition_e1_kernel<256>(RouteArgs, KeyWords, int32_t, int32_t*,
+                                                  int32_t*, float*);
+template __global__ void partition_e1_kernel<1024>(RouteArgs, KeyWords, int32_t, int32_t*,
+                                                   int32_t*, float*);
 
 // The three steps between route and scatter of a level with few keys (at
 // most 64 eras), in one workgroup of 1024 threads: the block prefix, the node
