@@ -909,13 +909,32 @@ __global__ __launch_bounds__(1024) void hist_prep_kernel(
       key_max[k] = 0u;
   }
   uint32_t m = 0;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)n_part * blockDim.x) {
-    const int64_t r = rows ? (int64_t)rows[i] : i;
-    const float v = resid[r];
-    if (gathered) gathered[i] = v;
-    const uint32_t b = wgbm_abs_bits(v);
-    m = b > m ? b : m;
+  // U positions per thread and round, the row loads, then the residual
+  // loads, issued together (a position past the end re-reads the last one
+  // and stores nothing)
+  constexpr int U = 4;
+  const int64_t stride = (int64_t)n_part * blockDim.x;
+  for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < n; i0 += U * stride) {
+    int64_t r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + u * stride;
+      r[u] = i < n ? i : n - 1;
+    }
+    if (rows) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) r[u] = (int64_t)rows[r[u]];
+    }
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = resid[r[u]];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + u * stride;
+      if (gathered && i < n) gathered[i] = v[u];
+      const uint32_t b = wgbm_abs_bits(v[u]);
+      m = b > m ? b : m;
+    }
   }
   m = wgbm_block_max_u32(m);
   if (threadIdx.x == 0) partial[blockIdx.x] = m;
@@ -928,10 +947,29 @@ __global__ __launch_bounds__(256) void hist_key_max_kernel(
   if ((int)blockIdx.x >= *n_tiles) return;  // uniform per workgroup
   const Tile tl = tiles[blockIdx.x];
   uint32_t m = 0;
-  for (int64_t p = tl.begin + threadIdx.x; p < tl.end; p += blockDim.x) {
-    const int64_t r = (by_pos || !order) ? p : (int64_t)order[p];
-    const uint32_t b = wgbm_abs_bits(resid[r]);
-    m = b > m ? b : m;
+  if (tl.end > tl.begin) {
+    // U positions per thread and round, their loads issued together (a
+    // position past the tile re-reads the tile's last one: no branch, and
+    // the maximum is unchanged)
+    constexpr int U = 8;
+    const int64_t last = tl.end - 1;
+    for (int64_t p0 = tl.begin + threadIdx.x; p0 < tl.end; p0 += (int64_t)U * blockDim.x) {
+      int64_t r[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t p = p0 + (int64_t)u * blockDim.x;
+        r[u] = p < tl.end ? p : last;
+      }
+      if (!(by_pos || !order)) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) r[u] = (int64_t)order[r[u]];
+      }
+      uint32_t b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = wgbm_abs_bits(resid[r[u]]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) m = b[u] > m ? b[u] : m;
+    }
   }
   m = wgbm_block_max_u32(m);
   if (threadIdx.x == 0 && m) atomicMax(key_max + tl.key, m);
