@@ -305,10 +305,29 @@ __device__ inline void finish_node(
     return;
   }
   int64_t sqh = 0, sql = 0, sc = 0;
-  for (int e = lane; e < E; e += 64) {
-    sqh += tot_qh[(int64_t)tn * E + e];
-    sql += tot_ql[(int64_t)tn * E + e];
-    sc += tot_c[(int64_t)tn * E + e];
+  {
+    // the node's era words, U per lane and round with their loads issued
+    // together (an era past the end re-reads the node's first and adds 0)
+    constexpr int U = 4;
+    const int64_t k0 = (int64_t)tn * E;
+    for (int e0 = lane; e0 < E; e0 += U * 64) {
+      int64_t a[U], b[U], c[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + u * 64;
+        const int64_t k = k0 + (e < E ? e : 0);
+        a[u] = tot_qh[k];
+        b[u] = tot_ql[k];
+        c[u] = tot_c[k];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool in = e0 + u * 64 < E;
+        sqh += in ? a[u] : 0;
+        sql += in ? b[u] : 0;
+        sc += in ? c[u] : 0;
+      }
+    }
   }
   for (int o = 32; o > 0; o >>= 1) {
     sqh += __shfl_xor(sqh, o, 64);
@@ -407,10 +426,18 @@ __global__ __launch_bounds__(64) void level_finish_kernel(
 //          segment's start in the block (+ its left rows in earlier blocks,
 //          from the same partial sums, when it began in an earlier block).
 // ---------------------------------------------------------------------------
+__device__ inline void segment_left_sums_at(int64_t k, int64_t s0, int64_t s1,
+                                            const PartSums& ps, int64_t& qh, int64_t& ql,
+                                            int64_t& n);
 __device__ inline void segment_left_sums(int64_t k, const int64_t* __restrict__ seg,
                                          const PartSums& ps, int64_t& qh, int64_t& ql,
                                          int64_t& n) {
-  const int64_t s0 = seg[k], s1 = seg[k + 1];
+  segment_left_sums_at(k, seg[k], seg[k + 1], ps, qh, ql, n);
+}
+// the same, for segment k at positions [s0, s1)
+__device__ inline void segment_left_sums_at(int64_t k, int64_t s0, int64_t s1,
+                                            const PartSums& ps, int64_t& qh, int64_t& ql,
+                                            int64_t& n) {
   if (s1 <= s0) {
     qh = 0;
     ql = 0;
@@ -990,7 +1017,74 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
     wgbm_lds_barrier();
   };
   int64_t ltot = 0, tot = 0;
-  if (live) {
+  // With at most NE eras per thread (C4: 500 eras over 256 lanes) the
+  // thread's era words are loaded once, in one round per kind of word, and
+  // kept for the prefix loop below; else they are loaded in each loop.
+  constexpr int NE = 4;
+  const bool keep = E <= NE * gthreads;  // uniform
+  int64_t eL[NE], eR[NE], eQh[NE], eQl[NE];
+  if (live && keep) {
+    int64_t s0[NE], s1[NE];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int e = gt + i * gthreads;
+      const int ec = e < E ? e : E - 1;
+      s0[i] = seg[k0 + ec];
+      s1[i] = seg[k0 + ec + 1];
+    }
+    // both kinds of left sums of every kept era, loaded in one round
+    // (segment_left_sums_at picks one: a segment inside one block has its
+    // own words, else its first block's and the block prefix), block
+    // indices clamped so that the unused kind stays in bounds
+    const int64_t bmax = n_pos > 0 ? (n_pos - 1) / kPartBlock : 0;
+    int64_t oq[NE], ol[NE], bq[NE], bl[NE], pq1[NE], pl1[NE], pq0[NE], pl0[NE];
+    int32_t on[NE], bn[NE];
+    int64_t pn1[NE], pn0[NE];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int e = gt + i * gthreads;
+      const int64_t k = k0 + (e < E ? e : E - 1);
+      const int64_t b0 = s0[i] / kPartBlock < bmax ? s0[i] / kPartBlock : bmax;
+      const int64_t b1 = s1[i] > s0[i] ? (s1[i] - 1) / kPartBlock : b0;
+      oq[i] = ps.own_qh[k];
+      ol[i] = ps.own_ql[k];
+      on[i] = ps.own_n[k];
+      bq[i] = ps.bl_qh[b0];
+      bl[i] = ps.bl_ql[b0];
+      bn[i] = ps.bl_n[b0];
+      pq1[i] = ps.P_qh[b1];
+      pl1[i] = ps.P_ql[b1];
+      pn1[i] = ps.P_n[b1];
+      pq0[i] = ps.P_qh[b0];
+      pl0[i] = ps.P_ql[b0];
+      pn0[i] = ps.P_n[b0];
+    }
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int e = gt + i * gthreads;
+      const int64_t cnt = e < E ? s1[i] - s0[i] : 0;
+      int64_t L = cnt, qh = 0, ql = 0;
+      if (sp) {
+        if (cnt <= 0) {
+          L = 0;
+        } else if (s0[i] / kPartBlock == (s1[i] - 1) / kPartBlock) {
+          qh = oq[i];
+          ql = ol[i];
+          L = on[i];
+        } else {
+          qh = bq[i] + pq1[i] - pq0[i];
+          ql = bl[i] + pl1[i] - pl0[i];
+          L = bn[i] + pn1[i] - pn0[i];
+        }
+      }
+      eQh[i] = qh;
+      eQl[i] = ql;
+      eL[i] = L;
+      eR[i] = cnt - L;
+      ltot += L;
+      tot += cnt;
+    }
+  } else if (live) {
     for (int e = gt; e < E; e += gthreads) {
       const int64_t cnt = seg[k0 + e + 1] - seg[k0 + e];
       int64_t qh, ql;
@@ -1023,10 +1117,22 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
     both = sp && (hs_l != hs || hs_r != hs);
   }
   int64_t carry_l = 0, carry_r = 0;
-  for (int e0 = 0; e0 < E; e0 += gthreads) {
+  for (int e0 = 0, i = 0; e0 < E; e0 += gthreads, ++i) {
     const int e = e0 + gt;
     int64_t L = 0, R = 0, qh = 0, ql = 0;
-    if (live && e < E) {
+    if (keep) {
+      // the kept words of round i (a fixed-index select: no indexed
+      // register access)
+#pragma unroll
+      for (int j = 0; j < NE; ++j) {
+        if (j == i && live) {
+          L = eL[j];
+          R = eR[j];
+          qh = eQh[j];
+          ql = eQl[j];
+        }
+      }
+    } else if (live && e < E) {
       const int64_t cnt = seg[k0 + e + 1] - seg[k0 + e];
       L = left_of(k0 + e, cnt, qh, ql);
       R = cnt - L;
