@@ -372,11 +372,8 @@ int wgbm_compute_split(const float* G, const float* H, int32_t num_eras, int32_t
   const int64_t n = (int64_t)num_eras * n_feats;
   if (n == 0) return 0;
   WGBM_REQUIRE(G && H && per_era_gain && per_era_direction, "null pointer");
-  hipLaunchKernelGGL(split_f32_kernel, dim3(nblocks(n, 256)), dim3(256), 0, S(stream), G, H,
-                     num_eras, n_feats, num_bins, min_child_samples, eps, per_era_gain,
-                     per_era_direction);
-  WGBM_LAUNCH_CHECK();
-  return 0;
+  return launch_split_f32(G, H, num_eras, n_feats, num_bins, min_child_samples, eps,
+                          per_era_gain, per_era_direction, S(stream));
 }
 
 int wgbm_custom_cuda_binner(const float* X, int64_t n, const float* bin_edges, int32_t n_edges,

@@ -255,9 +255,10 @@ __global__ void chunk_keys_kernel(const int32_t* present, int32_t E, int32_t n, 
 
 // split kernels (split.hip); node_shift: the histogram shift of every
 // (tree, node) of the level, indexed by tree * nodes_in_level + node
-__global__ void split_f32_kernel(const float* G, const float* H, int32_t E, int32_t F,
-                                 int32_t B, float mcw, float eps, float* gain_out,
-                                 float* dir_out);
+// per-era gains and directions of every (era, feature) (the drop-in op;
+// split_f32_kernel, a compile-time bin count for common B)
+int launch_split_f32(const float* G, const float* H, int32_t E, int32_t F, int32_t B, float mcw,
+                     float eps, float* gain_out, float* dir_out, hipStream_t st);
 // split_level_e1_kernel over n_tn tree-nodes (a compile-time bin count for B = 32)
 int launch_split_level_e1(int n_tn, hipStream_t st, const int64_t* hq, const int32_t* hc,
                           int32_t F, int32_t B, const int32_t* feat_sel, int32_t n_sel,

@@ -34,21 +34,70 @@ namespace wgbm {
 // ---------------------------------------------------------------------------
 // reference-compatible compute_split: one lane per (era, feature)
 // ---------------------------------------------------------------------------
-__global__ void split_f32_kernel(const float* __restrict__ G, const float* __restrict__ H,
-                                 int32_t E, int32_t F, int32_t B, float mcw, float eps,
-                                 float* __restrict__ gain_out, float* __restrict__ dir_out) {
+// BT > 0: B known at compile time, and every bin of the thread's (era,
+// feature) is loaded before the scan (one memory round trip; with the bin
+// count known only at run time the scan's sequential sums wait for each
+// bin's load in turn)
+template <int BT>
+__global__ __launch_bounds__(256) void split_f32_kernel(const float* __restrict__ G,
+                                                        const float* __restrict__ H, int32_t E,
+                                                        int32_t F, int32_t B_rt, float mcw,
+                                                        float eps, float* __restrict__ gain_out,
+                                                        float* __restrict__ dir_out) {
+  const int B = BT > 0 ? BT : B_rt;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (int64_t)E * F) return;
   const float* g = G + gid * B;
   const float* h = H + gid * B;
   float* go = gain_out + gid * (B - 1);
   float* dout = dir_out + gid * (B - 1);
-  scan_bins(
-      B, mcw, eps, [&](int b) { return g[b]; }, [&](int b) { return h[b]; },
-      [&](int b, float gn, float d) {
-        go[b] = gn;
-        dout[b] = d;
-      });
+  auto emit = [&](int b, float gn, float d) {
+    go[b] = gn;
+    dout[b] = d;
+  };
+  if constexpr (BT > 0) {
+    float gv[BT], hv[BT];
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+      gv[b] = g[b];
+      hv[b] = h[b];
+    }
+    scan_bins(
+        BT, mcw, eps, [&](int b) { return gv[b]; }, [&](int b) { return hv[b]; }, emit);
+  } else {
+    scan_bins(
+        B, mcw, eps, [&](int b) { return g[b]; }, [&](int b) { return h[b]; }, emit);
+  }
+}
+
+int launch_split_f32(const float* G, const float* H, int32_t E, int32_t F, int32_t B, float mcw,
+                     float eps, float* gain_out, float* dir_out, hipStream_t st) {
+  const int64_t n = (int64_t)E * F;
+  const dim3 grid((unsigned)((n + 255) / 256)), blk(256);
+#define WGBM_SPLIT_F32(BT)                                                                    \
+  case BT:                                                                                    \
+    hipLaunchKernelGGL(split_f32_kernel<BT>, grid, blk, 0, st, G, H, E, F, B, mcw, eps,        \
+                       gain_out, dir_out);                                                    \
+    break;
+  switch (B) {
+    WGBM_SPLIT_F32(2)
+    WGBM_SPLIT_F32(3)
+    WGBM_SPLIT_F32(4)
+    WGBM_SPLIT_F32(5)
+    WGBM_SPLIT_F32(6)
+    WGBM_SPLIT_F32(7)
+    WGBM_SPLIT_F32(8)
+    WGBM_SPLIT_F32(10)
+    WGBM_SPLIT_F32(16)
+    WGBM_SPLIT_F32(32)
+    WGBM_SPLIT_F32(64)
+    default:
+      hipLaunchKernelGGL(split_f32_kernel<0>, grid, blk, 0, st, G, H, E, F, B, mcw, eps,
+                         gain_out, dir_out);
+  }
+#undef WGBM_SPLIT_F32
+  WGBM_LAUNCH_CHECK();
+  return 0;
 }
 
 // ---------------------------------------------------------------------------
