@@ -51,6 +51,33 @@ def test_c1_regression_bit_exact(gpu):
     assert np.corrcoef(p, y)[0, 1] > 0.9
 
 
+@pytest.mark.parametrize("B", [5, 8, 10, 16, 64])
+def test_one_era_bin_counts_bit_exact(gpu, B):
+    """The one-era split step's compile-time bin counts (10 is the
+    estimator's default) grow the oracle's trees: regression on 6000 rows
+    and a 3-class softmax, depth 4."""
+    print_case("estimator", "one-era bin count", B)
+    rng = np.random.default_rng(40 + B)
+    N, F = 6000, 12
+    X = rng.standard_normal((N, F)).astype(F32)
+    y = (X[:, 0] - 0.5 * X[:, 3] ** 2 + 0.1 * rng.standard_normal(N)).astype(F32)
+    kw = dict(num_bins=B, max_depth=4, n_estimators=3, learning_rate=0.3, min_child_weight=5)
+    m = WarpGBM(**kw).fit(X, y)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, y)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(codes)))
+    labels = (X[:, 1] > 0).astype(np.int64) + (X[:, 2] > 0.5)
+    kw = dict(objective="multiclass", num_bins=B, max_depth=4, n_estimators=2,
+              learning_rate=0.3, min_child_weight=5)
+    m = WarpGBM(**kw).fit(X, labels)
+    codes = oracle_codes(m, X)
+    ref = gbm.Forest(**kw).fit_codes(codes, labels)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"round {i} differs"
+
+
 def test_multiclass_bit_exact(gpu):
     print_case("estimator", "multiclass K=4")
     rng = np.random.default_rng(1)

@@ -1700,12 +1700,25 @@ int launch_split_finish_e1(int n_tn, int32_t c0, hipStream_t st, const int64_t* 
                            float min_split_gain, unsigned long long* best, uint32_t* done,
                            const FinishE1& fa) {
   const dim3 grid((unsigned)(n_tn * ((n_sel + 255) / 256)));
-  if (fa.B == 32)
-    hipLaunchKernelGGL(split_finish_e1_kernel<32>, grid, dim3(256), 0, st, hq, hc, F, fa.B,
-                       n_sel, c0, node_shift, mcw, eps, min_split_gain, best, done, fa);
-  else
-    hipLaunchKernelGGL(split_finish_e1_kernel<0>, grid, dim3(256), 0, st, hq, hc, F, fa.B,
-                       n_sel, c0, node_shift, mcw, eps, min_split_gain, best, done, fa);
+  // a compile-time bin count (every bin loaded before the scan) for the
+  // common ones: 10 is the estimator's default, 32 the benchmarks'
+#define WGBM_FINISH_E1(BT)                                                                    \
+  case BT:                                                                                    \
+    hipLaunchKernelGGL(split_finish_e1_kernel<BT>, grid, dim3(256), 0, st, hq, hc, F, fa.B,    \
+                       n_sel, c0, node_shift, mcw, eps, min_split_gain, best, done, fa);      \
+    break;
+  switch (fa.B) {
+    WGBM_FINISH_E1(5)
+    WGBM_FINISH_E1(8)
+    WGBM_FINISH_E1(10)
+    WGBM_FINISH_E1(16)
+    WGBM_FINISH_E1(32)
+    WGBM_FINISH_E1(64)
+    default:
+      hipLaunchKernelGGL(split_finish_e1_kernel<0>, grid, dim3(256), 0, st, hq, hc, F, fa.B,
+                         n_sel, c0, node_shift, mcw, eps, min_split_gain, best, done, fa);
+  }
+#undef WGBM_FINISH_E1
   WGBM_LAUNCH_CHECK();
   return 0;
 }
