@@ -224,7 +224,12 @@ constexpr int kPartition1MaxNodes = 1024;
 constexpr int64_t kPartition1WideSpan = 16 * 1024;
 template <int NT>  // threads per block: 4 NT positions
 __global__ void partition_e1_kernel(RouteArgs a, KeyWords kw, int32_t n_slots,
-                                    int32_t* order_next, int32_t* keyp_next, float* rpos_next);
+                                    int32_t* order_next, int32_t* keyp_next, float* rpos_next,
+                                    int32_t* leaf_key);
+// the last level's leaf updates by row, from the rows' leaf keys
+__global__ void leaf_rows_kernel(const int32_t* leaf_key, int64_t n, int32_t T,
+                                 const NodeRoute* nroute, float lr, float* pred, int64_t pstride,
+                                 int64_t pcol);
 // its dynamic LDS: 28 bytes per (tree, node) slot
 inline size_t partition1_lds_bytes(int64_t n_slots) { return (size_t)n_slots * 28; }
 // One-era levels: level_scan_kernel's work with a thread per (tree, node),

@@ -568,6 +568,9 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
 
   const float mcw = c.min_child_weight, eps = c.l2_reg, msg = c.min_split_gain;
   bool planned = false;  // this level's histogram tiles were planned by the previous level
+  // the last split level wrote every row's leaf key (keyp[cur] by row):
+  // the last level updates predictions in row order (leaf_rows_kernel)
+  bool leaf_keys = false;
   bool alive_ready = false;  // this level's live-era masks were written by the previous scan
   for (int d = 0; d <= D; ++d) {
     const int nodes = 1 << d;
@@ -819,16 +822,23 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     // then reads the node words
     const bool one_pass =
         d < D && E == 1 && e->lscan_e1 && e->part1 && n_tn <= kPartition1MaxNodes;
-    if (one_pass) {
+    if (d == D && leaf_keys) {
+      hipLaunchKernelGGL(leaf_rows_kernel, dim3((unsigned)blocks_for(n_pos, 1024)), dim3(256), 0,
+                         st, e->keyp[cur], rl.n, T, rl.nroute, rl.lr, rl.pred, rl.pstride,
+                         rl.pcol);
+    } else if (one_pass) {
+      // the last split level writes each row's leaf key instead of placing it
+      leaf_keys = d + 1 == D;
+      int32_t* lk = leaf_keys ? e->keyp[nxt] : nullptr;
       const size_t lds = partition1_lds_bytes(n_tn);
       if (n_pos > kPartition1WideSpan * n_tn) {
         hipLaunchKernelGGL(partition_e1_kernel<1024>, dim3((unsigned)((n_pos + 4095) / 4096)),
                            dim3(1024), lds, st, rl, e->kw, (int32_t)n_tn, e->order[nxt],
-                           e->keyp[nxt], e->rpos[nxt]);
+                           e->keyp[nxt], e->rpos[nxt], lk);
       } else {
         hipLaunchKernelGGL(partition_e1_kernel<256>, dim3((unsigned)((n_pos + 1023) / 1024)),
                            dim3(256), lds, st, rl, e->kw, (int32_t)n_tn, e->order[nxt],
-                           e->keyp[nxt], e->rpos[nxt]);
+                           e->keyp[nxt], e->rpos[nxt], lk);
       }
     } else {
       rl.xcd_order = rl.mode == 2 && T > 1 ? 1 : 0;

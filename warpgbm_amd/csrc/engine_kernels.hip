@@ -1315,12 +1315,18 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
 // instruction land on consecutive addresses.  The block's nodes are
 // consecutive keys from its first position's key kf: node k's LDS slot is
 // k - kf (< n_slots = the level's (tree, node)s).
+//
+// With leaf_key (the last split level) no position is placed: the next level
+// only updates predictions, so each row's child key is written by row
+// instead, leaf_key[tree * n + row] (leaf_rows_kernel then reads it in row
+// order).
 template <int NT>
 __global__ __launch_bounds__(NT) void partition_e1_kernel(RouteArgs a, KeyWords kw,
                                                           int32_t n_slots,
                                                           int32_t* __restrict__ order_next,
                                                           int32_t* __restrict__ keyp_next,
-                                                          float* __restrict__ rpos_next) {
+                                                          float* __restrict__ rpos_next,
+                                                          int32_t* __restrict__ leaf_key) {
   constexpr int PJ = 4;              // positions per thread
   constexpr int PB = PJ * NT;        // positions per block
   constexpr int NW = NT / 64;
@@ -1493,6 +1499,11 @@ __global__ __launch_bounds__(NT) void partition_e1_kernel(RouteArgs a, KeyWords 
     if (!ok[j]) continue;
     const int64_t p = p0 + j * NT + tid;
     const int kl = 2 * key[j];  // the left child's key (one era)
+    if (leaf_key) {
+      const int t = key[j] / a.nodes;
+      leaf_key[(int64_t)t * a.n + rowv[j]] = kl + (dirs[j] == 1 ? 1 : 0);
+      continue;
+    }
     if (dirs[j] == 2) {
       // a node that does not split: its rows stay, in its left child's segment
       order_next[p] = rowv[j];
@@ -1520,9 +1531,40 @@ __global__ __launch_bounds__(NT) void partition_e1_kernel(RouteArgs a, KeyWords 
   }
 }
 template __global__ void partition_e1_kernel<256>(RouteArgs, KeyWords, int32_t, int32_t*,
-                                                  int32_t*, float*);
+                                                  int32_t*, float*, int32_t*);
 template __global__ void partition_e1_kernel<1024>(RouteArgs, KeyWords, int32_t, int32_t*,
-                                                   int32_t*, float*);
+                                                   int32_t*, float*, int32_t*);
+
+// The last level's leaf updates in row order (after partition_e1_kernel
+// wrote every row's leaf key): pred[t][row] += lr * leaf of the row's node
+// in tree t, as route_kernel's mode 2 does by position.  Four rows per
+// thread, their key loads issued together.
+__global__ __launch_bounds__(256) void leaf_rows_kernel(const int32_t* __restrict__ leaf_key,
+                                                        int64_t n, int32_t T,
+                                                        const NodeRoute* __restrict__ nroute,
+                                                        float lr, float* __restrict__ pred,
+                                                        int64_t pstride, int64_t pcol) {
+  constexpr int U = 4;
+  const int64_t total = (int64_t)T * n;
+  const int64_t i0 = ((int64_t)blockIdx.x * 256) * U + threadIdx.x;
+  int32_t k[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = i0 + u * 256;
+    k[u] = i < total ? leaf_key[i] : 0;
+  }
+  NodeRoute nr[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) nr[u] = nroute[k[u]];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = i0 + u * 256;
+    if (i >= total || nr[u].col != -1) continue;
+    const int64_t t = i / n, row = i - t * n;
+    float* pc = pred + t * pcol + row * pstride;
+    *pc = *pc + lr * nr[u].leaf;
+  }
+}
 
 // The three steps between route and scatter of a level with few keys (at
 // most 64 eras), in one workgroup of 1024 threads: the block prefix, the node
