@@ -254,8 +254,11 @@ def test_custom_cuda_binner_bit_exact(gpu):
     rng = np.random.default_rng(3)
     x = rng.standard_normal(100003).astype(F32)
     x[::101] = np.nan
+    x[7::997] = np.inf
+    x[11::991] = -np.inf
     for edges in (np.sort(rng.standard_normal(31)).astype(F32), rng.standard_normal(9).astype(F32),
-                  np.full(5, np.nan, F32), np.zeros(0, F32)):
+                  np.full(5, np.nan, F32), np.zeros(0, F32),
+                  np.sort(rng.standard_normal(126)).astype(F32)):
         x[:len(edges)] = edges
         out = torch.empty(len(x), dtype=torch.int8, device=dev)
         node_kernel.custom_cuda_binner(t(x), t(edges), out)

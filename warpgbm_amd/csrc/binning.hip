@@ -23,15 +23,54 @@ namespace wgbm {
 // ---------------------------------------------------------------------------
 // reference-compatible single-column binner: literal linear scan
 // ---------------------------------------------------------------------------
-__global__ void bin_column_kernel(const float* __restrict__ x, int64_t n,
-                                  const float* __restrict__ edges, int32_t n_edges,
-                                  int8_t* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float v = x[i];
-  int b = 0;
-  while (b < n_edges && v >= edges[b]) ++b;
-  out[i] = (int8_t)b;
+// bin = the length of the longest prefix of the edges that the value is >=
+// (the reference's `while (bin < ne && v >= edges[bin]) ++bin`, any edge
+// order, NaN stopping the prefix), for kBinColumnU values per thread.  The
+// edges are walked in the same order by every lane (a uniform index: scalar
+// loads, eight per wave and step) and each value keeps a running "still in
+// the prefix" flag instead of leaving the loop, so no lane waits on a load
+// of its own; the walk ends when no value of the wave is still in it.
+__global__ __launch_bounds__(256) void bin_column_kernel(const float* __restrict__ x, int64_t n,
+                                                         const float* __restrict__ edges,
+                                                         int32_t n_edges,
+                                                         int8_t* __restrict__ out) {
+  constexpr int U = kBinColumnU;
+  const int64_t i0 = (int64_t)blockIdx.x * 256 * U + threadIdx.x;
+  float v[U];
+  int bin[U];
+  bool in[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = i0 + (int64_t)u * 256;
+    v[u] = i < n ? x[i] : 0.0f;
+    bin[u] = 0;
+    in[u] = i < n;
+  }
+  // eight edges per step, their (uniform) loads issued together
+  constexpr int EB = 8;
+  for (int b0 = 0; b0 < n_edges; b0 += EB) {
+    bool any = false;
+#pragma unroll
+    for (int u = 0; u < U; ++u) any = any || in[u];
+    if (__ballot(any) == 0ull) break;  // uniform: every value of the wave has stopped
+    float e[EB];
+#pragma unroll
+    for (int k = 0; k < EB; ++k) e[k] = edges[b0 + k < n_edges ? b0 + k : n_edges - 1];
+#pragma unroll
+    for (int k = 0; k < EB; ++k) {
+      if (b0 + k >= n_edges) break;  // uniform
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        in[u] = in[u] && v[u] >= e[k];
+        bin[u] += in[u] ? 1 : 0;
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = i0 + (int64_t)u * 256;
+    if (i < n) out[i] = (int8_t)bin[u];
+  }
 }
 
 // #{j < ne : e[j] <= v} for sorted e (branch-free lower bound on the predicate)

@@ -381,8 +381,8 @@ int wgbm_custom_cuda_binner(const float* X, int64_t n, const float* bin_edges, i
   WGBM_REQUIRE(n >= 0 && n_edges >= 0, "negative size");
   if (n == 0) return 0;
   WGBM_REQUIRE(X && bin_indices && (n_edges == 0 || bin_edges), "null pointer");
-  hipLaunchKernelGGL(bin_column_kernel, dim3(nblocks(n, 256)), dim3(256), 0, S(stream), X, n,
-                     bin_edges, n_edges, bin_indices);
+  hipLaunchKernelGGL(bin_column_kernel, dim3(nblocks(n, 256 * kBinColumnU)), dim3(256), 0,
+                     S(stream), X, n, bin_edges, n_edges, bin_indices);
   WGBM_LAUNCH_CHECK();
   return 0;
 }

@@ -347,7 +347,7 @@ int launch_pack_pairs(hipStream_t st, const int8_t* codes, int64_t stride, int32
 inline int64_t pair_stride(int32_t F) { return ((int64_t)(F + 15) / 16 * 8 + 255) / 256 * 256; }
 
 
-// binning / predict kernels
+// binning / predict kernels (bin_column_kernel: kBinColumnU values per thread)
 __global__ void bin_column_kernel(const float* x, int64_t n, const float* edges,
                                   int32_t n_edges, int8_t* out);
 // words per feature of bin_matrix_kernel's LDS edge lists (dynamic LDS =

@@ -5,6 +5,9 @@
 
 namespace wgbm {
 
+// values per thread of the per-column binner (bin_column_kernel)
+constexpr int kBinColumnU = 4;
+
 // A run of row-order positions [begin, end) that all belong to segment `key`.
 struct Tile {
   int32_t key;
