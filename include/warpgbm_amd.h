@@ -285,8 +285,10 @@ int wgbm_engine_round(wgbm_engine* eng, const void* target, float* pred, const i
  * one-era split levels' partition (1 = one pass that routes and places every
  * row, each node's children filled from its two ends, on levels of at most
  * 1024 (tree, node)s, default; 0 = route, block prefix and a stable
- * scatter).  Set before the first round; every setting grows the same
- * trees. */
+ * scatter); key 7 = the era levels' partition (1 = the route reserves each
+ * (node, era) segment's child ranges and leaves its sums for the node scan,
+ * no block prefix, default; 0 = route, block prefix, node scan, scatter).
+ * Set before the first round; every setting grows the same trees. */
 int wgbm_engine_set_tuning(wgbm_engine* eng, int32_t key, int64_t value);
 void wgbm_engine_destroy(wgbm_engine* eng);
 

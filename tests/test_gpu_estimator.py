@@ -280,6 +280,35 @@ def test_era_des_many_eras_blocks_bit_exact(gpu):
     assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
 
 
+@pytest.mark.parametrize("E,part", [(130, 1), (130, 0), (1100, 1)])
+def test_era_level_partition_modes_bit_exact(gpu, E, part):
+    """Era levels with the route reserving each segment's child ranges
+    (engine tuning key 7 = 1: no block prefix; segments of 300-700 rows
+    cross partition blocks) and with the block prefix (0) grow the oracle's
+    trees; 1100 eras take the node scan's loop over more eras than a
+    thread keeps in registers.  Heavy-tailed residuals move the children's
+    per-era histogram shifts (the segment maxima)."""
+    print_case("estimator", "era level partition", E, part)
+    rng = np.random.default_rng(50 + E + part)
+    F, B = 9, 5
+    sizes = rng.integers(300, 700, E) if E < 1000 else rng.integers(5, 40, E)
+    N = int(sizes.sum())
+    era = np.repeat(np.arange(E), sizes)
+    X = rng.integers(0, B, (N, F)).astype(np.int8)
+    flip = np.where(rng.random(E) < 0.5, -1.0, 1.0)
+    score = (X[:, :3] - 2).sum(axis=1) + flip[era] * (X[:, 3] - 2) + rng.standard_normal(N)
+    y = (score / 4.0).astype(F32)
+    y[rng.integers(0, N, 5)] *= 1e4
+    kw = dict(num_bins=B, max_depth=5, n_estimators=2, learning_rate=0.4, min_child_weight=4)
+    m = WarpGBM(**kw)
+    m._engine_tuning = {7: part}
+    m.fit(X, y, era_id=era)
+    ref = gbm.Forest(**kw).fit_codes(X, y, era_id=era)
+    for i, (a, b) in enumerate(zip(m.forest, ref.forest)):
+        assert a == b, f"tree {i} differs"
+    assert np.array_equal(bits(m.predict(X)), bits(ref.predict_codes(X)))
+
+
 def test_era_des_large_eras_histogram_path_bit_exact(gpu):
     """Eras larger than one LDS tile (65536 rows) take the per-era histogram
     path (tile partials, exact sibling subtraction, era accumulation)."""

@@ -137,6 +137,18 @@ __device__ inline int node_shift_rule(uint32_t absmax_bits, int parent_shift,
 __device__ inline int key_shift_of(uint32_t absmax_bits, int qbits) {
   return wgbm_shift_from_bits(absmax_bits, qbits);
 }
+// Per-segment words of the partitions that reserve child ranges
+// (partition_e1_kernel for one era, route_kernel with kw set for several):
+// what a split segment's rows add to its children (row counts of both, the
+// left rows' wide residual sums, both children's max|r|).  Zero outside a
+// level's partition -> scan window: the level's scan reads and clears them.
+struct KeyWords {
+  unsigned long long* cnt;  // left rows * 2^32 + right rows
+  int64_t* qh;              // left rows' sum of (q63 >> 32)
+  int64_t* ql;              // left rows' sum of (q63 & (2^32 - 1))
+  uint32_t* ml;             // left rows' max|r| (float bits)
+  uint32_t* mr;             // right rows' max|r|
+};
 struct RouteArgs {
   int32_t mode;  // 0 root totals, 1 split level, 2 last level (leaves only)
   int32_t want_max;  // gather each segment's left / right max|r| (the next level's shifts)
@@ -163,6 +175,14 @@ struct RouteArgs {
   const int32_t* keyp;  // segment key of every position
   PartSums ps;
   int32_t xcd_order;  // mode 2: blocks in the XCD work order (grid wgbm_xcd_grid)
+  // mode 1 with kw.cnt set (several eras): the segments' words go to kw
+  // instead of the block partials, a segment crossing the block's edges
+  // reserves the block's part of its children's ranges (res[2 b] for the
+  // block's first segment, res[2 b + 1] for its last: left * 2^32 + right
+  // rows of the segment in earlier-reserving blocks), and no block prefix is
+  // needed
+  KeyWords kw;
+  unsigned long long* res;
 };
 __global__ void route_kernel(RouteArgs a);
 // dynamic LDS of route_kernel: the slot sums, plus the node maxima
@@ -202,18 +222,6 @@ __global__ void level_scan_kernel(int32_t nb, PartSums ps, int32_t T, int32_t no
                                   const int32_t* split_l, LevelNext nx, int32_t n_list,
                                   int32_t tile_rows, int32_t max_tiles, Tile* tiles,
                                   int32_t* key_tile_start, int32_t* n_tiles);
-// Per-node words of the one-era single-pass partition (partition_e1_kernel):
-// what a split node's rows add to its left child (row counts of both
-// children, the left rows' wide residual sums, both children's max|r|).
-// Zero outside a level's partition -> level scan window: the level scan
-// reads and clears them.
-struct KeyWords {
-  unsigned long long* cnt;  // left rows * 2^32 + right rows
-  int64_t* qh;              // left rows' sum of (q63 >> 32)
-  int64_t* ql;              // left rows' sum of (q63 & (2^32 - 1))
-  uint32_t* ml;             // left rows' max|r| (float bits)
-  uint32_t* mr;             // right rows' max|r|
-};
 // One-era split levels in one pass: route, rank and place every position
 // (route_kernel + scatter_kernel without the block prefix between them), for
 // levels of at most kPartition1MaxNodes (tree, node)s.
@@ -245,14 +253,18 @@ __global__ void level_scan_e1_kernel(int32_t nb, PartSums ps, KeyWords kw, int32
 __global__ void root_totals_kernel(int32_t n_keys, const int64_t* seg, PartSums ps,
                                    int64_t* tot_qh, int64_t* tot_ql, int64_t* tot_c,
                                    int32_t qbits, int32_t* key_shift);
+// with kw.cnt set (several eras): the segments' words come from the route's
+// kw words (no block prefix), and are cleared
 __global__ void node_scan_kernel(int32_t T, int32_t nodes, int32_t E, int32_t wpn,
                                  int64_t n_pos, const int64_t* seg, const int32_t* present,
-                                 const int32_t* split_l, PartSums ps, LevelNext nx);
+                                 const int32_t* split_l, PartSums ps, LevelNext nx, KeyWords kw);
+// with res set: the ranks of a segment crossing the block's edges start at
+// the route's reserved bases (RouteArgs::res) instead of the block prefix
 __global__ void scatter_kernel(int64_t n_pos, int32_t E, const int64_t* seg,
                                const int64_t* seg_next, const int32_t* keyp,
                                const uint8_t* dirbit, PartSums ps, const int32_t* order,
                                int32_t* order_next, int32_t* keyp_next, const float* rpos,
-                               float* rpos_next);
+                               float* rpos_next, const unsigned long long* res);
 __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v);
 // histogram keys of a chunk of n (tree, node)s: list[i] = i when node i / E
 // is present, else -1 (keys relative to the chunk's first node)

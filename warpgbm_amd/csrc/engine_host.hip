@@ -96,6 +96,11 @@ struct Engine {
   // node words), 0 = route + level scan + scatter
   int part1 = 1;
   KeyWords kw{};  // [n_keys_max] each, zero between levels
+  // several eras: 1 = levels scanned by node_scan_kernel reserve their
+  // segments' child ranges in the route (kw words, res bases, no block
+  // prefix), 0 = route + block prefix + node scan + scatter
+  int part_era = 1;
+  unsigned long long* res = nullptr;  // [2 nb] reserved bases of the blocks' first / last segments
   Tile* root_tiles = nullptr;     // the root level's tile plan (planned by the first round)
   int32_t* root_kts = nullptr;
   int32_t* root_hn = nullptr;
@@ -217,7 +222,7 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
     // the chosen split's per-era gains; the pair codes; 64 MiB of slack
     const int64_t keys = e->n_keys_max, tn = T * nodes_max;
     const int64_t pcodes = (e->des_direct && B <= 7) ? N * pair_stride((int32_t)F) : 0;
-    const int64_t need = e->nc_max * per_node + T * N * 29 + keys * 100 + tn * 76 + tn * E * 4 +
+    const int64_t need = e->nc_max * per_node + T * N * 29 + keys * 132 + tn * 76 + tn * E * 4 +
                          pcodes + ((int64_t)64 << 20);
     size_t free_b = 0, total_b = 0;
     if (hipMemGetInfo(&free_b, &total_b) == hipSuccess && (size_t)need > free_b) {
@@ -286,13 +291,12 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->ps.pm_r, e->nb);
   E_ALLOC(e->hkts, e->n_keys_max + 1);
   E_ALLOC(e->hn, 1);
-  if (E == 1) {
-    E_ALLOC(e->kw.cnt, e->n_keys_max);
-    E_ALLOC(e->kw.qh, e->n_keys_max);
-    E_ALLOC(e->kw.ql, e->n_keys_max);
-    E_ALLOC(e->kw.ml, e->n_keys_max);
-    E_ALLOC(e->kw.mr, e->n_keys_max);
-  }
+  E_ALLOC(e->kw.cnt, e->n_keys_max);
+  E_ALLOC(e->kw.qh, e->n_keys_max);
+  E_ALLOC(e->kw.ql, e->n_keys_max);
+  E_ALLOC(e->kw.ml, e->n_keys_max);
+  E_ALLOC(e->kw.mr, e->n_keys_max);
+  if (E > 1) E_ALLOC(e->res, 2 * e->nb);
   if (E > 1) {
     E_ALLOC(e->crit, e->nc_max * F * (B - 1));
     E_ALLOC(e->agree, e->nc_max * F * (B - 1));
@@ -308,7 +312,7 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
   E_ALLOC(e->done, T * nodes_max);
   {
     hipError_t err = hipMemset(e->done, 0, sizeof(uint32_t) * T * nodes_max);
-    if (err == hipSuccess && E == 1) {
+    if (err == hipSuccess) {
       const size_t k = (size_t)e->n_keys_max;
       err = hipMemset(e->kw.cnt, 0, k * sizeof(unsigned long long));
       if (err == hipSuccess) err = hipMemset(e->kw.qh, 0, k * sizeof(int64_t));
@@ -343,6 +347,11 @@ int engine_set_tuning(Engine* e, int key, int64_t value) {
   if (key == 6) {
     WGBM_REQUIRE(value == 0 || value == 1, "one-era single-pass partition must be 0 or 1");
     e->part1 = (int)value;
+    return 0;
+  }
+  if (key == 7) {
+    WGBM_REQUIRE(value == 0 || value == 1, "era-level range reservation must be 0 or 1");
+    e->part_era = (int)value;
     return 0;
   }
   if (key == 2) {
@@ -822,6 +831,12 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     // then reads the node words
     const bool one_pass =
         d < D && E == 1 && e->lscan_e1 && e->part1 && n_tn <= kPartition1MaxNodes;
+    const bool one_wg = E == 1 ? n_tn <= kLevelScanE1MaxNodes
+                               : (E <= 64 && n_tn <= kLevelScanMaxNodes);
+    // several eras, levels scanned by node_scan_kernel: the route reserves
+    // the segments' child ranges and leaves their words in kw (no block
+    // prefix launch)
+    const bool era_res = d < D && E > 1 && !one_wg && e->part_era;
     if (d == D && leaf_keys) {
       hipLaunchKernelGGL(leaf_rows_kernel, dim3((unsigned)blocks_for(n_pos, 1024)), dim3(256), 0,
                          st, e->keyp[cur], rl.n, T, rl.nroute, rl.lr, rl.pred, rl.pstride,
@@ -842,6 +857,10 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       }
     } else {
       rl.xcd_order = rl.mode == 2 && T > 1 ? 1 : 0;
+      if (era_res) {
+        rl.kw = e->kw;
+        rl.res = e->res;
+      }
       const int64_t grid = rl.xcd_order ? wgbm_xcd_grid(e->nb) : e->nb;
       hipLaunchKernelGGL(route_kernel, dim3((unsigned)grid), dim3(kPartThreads),
                          route_lds_bytes(rl), st, rl);
@@ -867,8 +886,6 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
     const bool next_alive = d + 1 < D && e->des_direct && 2 * (int64_t)n_tn <= e->nc_max;
     nx.alive_next = nullptr;
     nx.mcw = mcw;
-    const bool one_wg = E == 1 ? n_tn <= kLevelScanE1MaxNodes
-                               : (E <= 64 && n_tn <= kLevelScanMaxNodes);
     if (d < D && one_wg) {
       // few keys: block prefix, node scan and the next level's tile plan in
       // one workgroup
@@ -902,18 +919,20 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
         nx.alive_next = next_alive ? e->alive : nullptr;
         hipLaunchKernelGGL(node_scan_kernel, dim3(blocks_for((int64_t)n_tn, 4)), dim3(256), 0,
                            st, T, nodes, E, 1, n_pos, e->seg[cur], e->present[cur], e->split_l,
-                           e->ps, nx);
+                           e->ps, nx, KeyWords{});
         WGBM_LAUNCH_CHECK();
         alive_ready = next_alive;
       }
     } else if (d < D) {
-      hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
-      WGBM_LAUNCH_CHECK();
+      if (!era_res) {
+        hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(1024), 0, st, (int32_t)e->nb, e->ps);
+        WGBM_LAUNCH_CHECK();
+      }
       const int wpn = E <= 64 ? 1 : (E <= 128 ? 2 : 4);  // waves per node
       nx.alive_next = next_alive ? e->alive : nullptr;
       hipLaunchKernelGGL(node_scan_kernel, dim3(blocks_for((int64_t)n_tn, 4 / wpn)), dim3(256), 0,
                          st, T, nodes, E, wpn, n_pos, e->seg[cur], e->present[cur], e->split_l,
-                         e->ps, nx);
+                         e->ps, nx, era_res ? e->kw : KeyWords{});
       WGBM_LAUNCH_CHECK();
       alive_ready = next_alive;
     }
@@ -921,7 +940,7 @@ int engine_round(Engine* e, const void* target, float* pred, const int32_t* feat
       hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)e->nb), dim3(kPartThreads), 0, st, n_pos,
                          E, e->seg[cur], e->seg[nxt], e->keyp[cur], e->dirbit, e->ps,
                          e->order[cur], e->order[nxt], e->keyp[nxt], e->rpos[cur],
-                         e->rpos[nxt]);
+                         e->rpos[nxt], era_res ? (const unsigned long long*)e->res : nullptr);
       WGBM_LAUNCH_CHECK();
     }
     cur = nxt;

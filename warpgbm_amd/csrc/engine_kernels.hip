@@ -575,10 +575,12 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   // col: -2 the row stays (node absent), -1 leaf update, >= 0 the split's
   // code column.
   bool seg_in[PJ];  // the segment lies inside the block
+  int64_t sev[PJ];  // the segment's end
   NodeRoute nr[PJ];
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
     const int64_t sk = a.seg[key[j]], se = a.seg[key[j] + 1];
+    sev[j] = se;
     slot[j] = (int)((sk > p0 ? sk : p0) - p0);
     seg_in[j] = sk >= p0 && se <= p1;
     tnv[j] = key[j] / a.E;
@@ -733,6 +735,45 @@ __global__ __launch_bounds__(kPartThreads) void route_kernel(RouteArgs a) {
   // none)
   int prev = __shfl_up(key[PJ - 1], 1, 64);
   if (lane == 0) prev = tid > 0 ? s_wlast[(tid >> 6) - 1] : -1;
+  if (a.kw.cnt) {
+    // the segments' words (split segments only): stored by the thread of a
+    // segment's first position in the block when it lies inside the block;
+    // a segment crossing the block's edges (the block's first or last) adds
+    // its part with atomics and reserves its rows' place in the children
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      const int i = pl0 + j;
+      const int k = key[j];
+      const int kp = j == 0 ? prev : key[j - 1];
+      if (!ok[j] || (i > 0 && kp == k) || lv[j] < 0) continue;
+      int64_t qh;
+      int32_t n;
+      unpack(s_qn[i], qh, n);
+      const int64_t e_loc = (sev[j] < p1 ? sev[j] : p1) - p0;
+      const int32_t nrt = (int32_t)(e_loc - i) - n;
+      const unsigned long long packed =
+          ((unsigned long long)(uint32_t)n << 32) | (uint32_t)nrt;
+      if (seg_in[j]) {
+        a.kw.cnt[k] = packed;
+        a.kw.qh[k] = qh;
+        a.kw.ql[k] = s_ql[i];
+        if (maxes) {
+          a.kw.ml[k] = s_ml[i];
+          a.kw.mr[k] = s_mr[i];
+        }
+      } else {
+        a.res[2 * (int64_t)blockIdx.x + (i == 0 ? 0 : 1)] = atomicAdd(a.kw.cnt + k, packed);
+        const int64_t ql = s_ql[i];
+        if (qh) atomicAdd((unsigned long long*)(a.kw.qh + k), (unsigned long long)qh);
+        if (ql) atomicAdd((unsigned long long*)(a.kw.ql + k), (unsigned long long)ql);
+        if (maxes) {
+          if (s_ml[i]) atomicMax(a.kw.ml + k, s_ml[i]);
+          if (s_mr[i]) atomicMax(a.kw.mr + k, s_mr[i]);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
     // position pl0 + j opens a segment when its key differs from the one
@@ -956,12 +997,17 @@ __global__ void root_totals_kernel(int32_t n_keys, const int64_t* __restrict__ s
 // exact).  A node that does not split has no children: their words are 0.
 __device__ inline void era_child_shifts(int64_t k, int64_t kl, int64_t kr, bool sp,
                                         const PartSums& ps, const int64_t* __restrict__ seg,
-                                        const LevelNext& nx, bool& both) {
+                                        const LevelNext& nx, const KeyWords& kw, bool& both) {
   int sl = 0, sr = 0;
   both = false;
   if (sp && nx.have_max) {
     uint32_t ml = 0, mr = 0;
-    seg_child_max(k, seg[k], seg[k + 1], ps, 0, 1, ml, mr);
+    if (kw.cnt) {
+      ml = kw.ml[k];
+      mr = kw.mr[k];
+    } else {
+      seg_child_max(k, seg[k], seg[k + 1], ps, 0, 1, ml, mr);
+    }
     sl = key_shift_of(ml, nx.qbits);
     sr = key_shift_of(mr, nx.qbits);
     const int sp_k = nx.node_shift[k];
@@ -976,7 +1022,8 @@ __device__ inline void era_child_shifts(int64_t k, int64_t kl, int64_t kr, bool 
 __global__ __launch_bounds__(256) void node_scan_kernel(
     int32_t T, int32_t nodes, int32_t E, int32_t wpn, int64_t n_pos,
     const int64_t* __restrict__ seg, const int32_t* __restrict__ present,
-    const int32_t* __restrict__ split_l, PartSums ps, LevelNext nx) {
+    const int32_t* __restrict__ split_l, PartSums ps, LevelNext nx, KeyWords kw) {
+  const bool kwm = kw.cnt != nullptr;  // uniform: the segments' words are in kw
   __shared__ int64_t s_a[4], s_b[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / wpn, wg = wave - grp * wpn;
@@ -993,7 +1040,15 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
     int64_t L = cnt;
     qh = 0;
     ql = 0;
-    if (sp) segment_left_sums(k, seg, ps, qh, ql, L);
+    if (sp && kwm) {
+      if (cnt > 0) {
+        L = (int64_t)(kw.cnt[k] >> 32);
+        qh = kw.qh[k];
+        ql = kw.ql[k];
+      }
+    } else if (sp) {
+      segment_left_sums(k, seg, ps, qh, ql, L);
+    }
     return L;
   };
   // sum (or max) over the group of one value per wave (every thread gets it)
@@ -1040,24 +1095,38 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
     int64_t oq[NE], ol[NE], bq[NE], bl[NE], pq1[NE], pl1[NE], pq0[NE], pl0[NE];
     int32_t on[NE], bn[NE];
     int64_t pn1[NE], pn0[NE];
+    if (kwm) {
+      // the route's words of each kept era: whole sums, no block prefix
 #pragma unroll
-    for (int i = 0; i < NE; ++i) {
-      const int e = gt + i * gthreads;
-      const int64_t k = k0 + (e < E ? e : E - 1);
-      const int64_t b0 = s0[i] / kPartBlock < bmax ? s0[i] / kPartBlock : bmax;
-      const int64_t b1 = s1[i] > s0[i] ? (s1[i] - 1) / kPartBlock : b0;
-      oq[i] = ps.own_qh[k];
-      ol[i] = ps.own_ql[k];
-      on[i] = ps.own_n[k];
-      bq[i] = ps.bl_qh[b0];
-      bl[i] = ps.bl_ql[b0];
-      bn[i] = ps.bl_n[b0];
-      pq1[i] = ps.P_qh[b1];
-      pl1[i] = ps.P_ql[b1];
-      pn1[i] = ps.P_n[b1];
-      pq0[i] = ps.P_qh[b0];
-      pl0[i] = ps.P_ql[b0];
-      pn0[i] = ps.P_n[b0];
+      for (int i = 0; i < NE; ++i) {
+        const int e = gt + i * gthreads;
+        const int64_t k = k0 + (e < E ? e : E - 1);
+        const unsigned long long c = kw.cnt[k];
+        oq[i] = kw.qh[k];
+        ol[i] = kw.ql[k];
+        on[i] = (int32_t)(c >> 32);
+      }
+    }
+    if (!kwm) {
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        const int e = gt + i * gthreads;
+        const int64_t k = k0 + (e < E ? e : E - 1);
+        const int64_t b0 = s0[i] / kPartBlock < bmax ? s0[i] / kPartBlock : bmax;
+        const int64_t b1 = s1[i] > s0[i] ? (s1[i] - 1) / kPartBlock : b0;
+        oq[i] = ps.own_qh[k];
+        ol[i] = ps.own_ql[k];
+        on[i] = ps.own_n[k];
+        bq[i] = ps.bl_qh[b0];
+        bl[i] = ps.bl_ql[b0];
+        bn[i] = ps.bl_n[b0];
+        pq1[i] = ps.P_qh[b1];
+        pl1[i] = ps.P_ql[b1];
+        pn1[i] = ps.P_n[b1];
+        pq0[i] = ps.P_qh[b0];
+        pl0[i] = ps.P_ql[b0];
+        pn0[i] = ps.P_n[b0];
+      }
     }
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
@@ -1067,7 +1136,7 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
       if (sp) {
         if (cnt <= 0) {
           L = 0;
-        } else if (s0[i] / kPartBlock == (s1[i] - 1) / kPartBlock) {
+        } else if (kwm || s0[i] / kPartBlock == (s1[i] - 1) / kPartBlock) {
           qh = oq[i];
           ql = ol[i];
           L = on[i];
@@ -1188,7 +1257,15 @@ __global__ __launch_bounds__(256) void node_scan_kernel(
       nx.tot_ql_next[c0 + E + e] = sp ? nx.tot_ql[k0 + e] - ql : 0;
       nx.tot_c_next[c0 + E + e] = sp ? R : 0;
       bool both_e = both;
-      if (E > 1) era_child_shifts(k0 + e, c0 + e, c0 + E + e, sp, ps, seg, nx, both_e);
+      if (E > 1) era_child_shifts(k0 + e, c0 + e, c0 + E + e, sp, ps, seg, nx, kw, both_e);
+      if (kwm) {
+        // read: ready for the next level
+        kw.cnt[k0 + e] = 0ull;
+        kw.qh[k0 + e] = 0;
+        kw.ql[k0 + e] = 0;
+        kw.ml[k0 + e] = 0u;
+        kw.mr[k0 + e] = 0u;
+      }
       nx.key_list_next[2 * (k0 + e)] =
           sp ? (int32_t)(c0 + (both_e ? 0 : side * E) + e) : -1;
       nx.key_list_next[2 * (k0 + e) + 1] = both_e ? (int32_t)(c0 + E + e) : -1;
@@ -1208,7 +1285,8 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
     const int64_t* __restrict__ seg_next, const int32_t* __restrict__ keyp,
     const uint8_t* __restrict__ dirbit, PartSums ps, const int32_t* __restrict__ order,
     int32_t* __restrict__ order_next, int32_t* __restrict__ keyp_next,
-    const float* __restrict__ rpos, float* __restrict__ rpos_next) {
+    const float* __restrict__ rpos, float* __restrict__ rpos_next,
+    const unsigned long long* __restrict__ res) {
   constexpr int PJ = kPartBlock / kPartThreads;  // positions per thread (strided)
   constexpr int NW = kPartThreads / 64;
   __shared__ int32_t s_pl[kPartBlock];  // left rows before each block position
@@ -1234,7 +1312,9 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
   // Kept in 32 bits relative to the block and the segment: a segment and
   // the node around it hold fewer than 2^31 positions.
   const int kf = keyp[p0];
+  const int64_t p1 = p0 + kPartBlock < n_pos ? p0 + kPartBlock : n_pos;
   int32_t sk[PJ], nd[PJ];  // segment start - p0; row's child segment start - segment start
+  bool past[PJ];           // (with res) the segment ends past the block
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
     const int k = key[j];
@@ -1243,12 +1323,17 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
     const int64_t s_k = seg[k];
     sk[j] = (int32_t)(s_k - p0);
     nd[j] = (int32_t)(seg_next[d[j] == 1 ? kl + E : kl] - s_k);
+    past[j] = res ? seg[k + 1] > p1 : false;
   }
+  // the block prefix words (without res)
   const int64_t sf = seg[kf];
   const int64_t b0 = (sf < p0 ? sf : p0) / kPartBlock;
-  const int64_t bl0 = ps.bl_n[b0];
-  const int64_t pb0 = ps.P_n[b0];
-  const int64_t pprev = blockIdx.x > 0 ? ps.P_n[blockIdx.x - 1] : 0;
+  const int64_t bl0 = res ? 0 : ps.bl_n[b0];
+  const int64_t pb0 = res ? 0 : ps.P_n[b0];
+  const int64_t pprev = !res && blockIdx.x > 0 ? ps.P_n[blockIdx.x - 1] : 0;
+  // the route's reserved bases of the block's first and last segments
+  const unsigned long long rb0 = res ? res[2 * (int64_t)blockIdx.x] : 0ull;
+  const unsigned long long rb1 = res ? res[2 * (int64_t)blockIdx.x + 1] : 0ull;
   // left rows before each position: rank among the wave's lefts plus the
   // lefts of the (phase, wave) groups before it (position order is phase,
   // then wave, then lane)
@@ -1286,6 +1371,21 @@ __global__ __launch_bounds__(kPartThreads) void scatter_kernel(
     }
     const int64_t skj = p0 + sk[j];
     const int s0 = sk[j] > 0 ? sk[j] : 0;  // the segment's first position in the block
+    if (res) {
+      // ranks in the block's part of the segment, after the part of the
+      // blocks that reserved before it (a segment inside the block: none)
+      const bool cross = sk[j] < 0 || past[j];
+      const unsigned long long base = cross ? (s0 == 0 ? rb0 : rb1) : 0ull;
+      const int64_t rlb = (int64_t)rank[j] - s_pl[s0];
+      const int64_t csr = skj + nd[j];
+      const int64_t dst = d[j] == 0 ? csr + (int64_t)(base >> 32) + rlb
+                                    : csr + (int64_t)(base & 0xffffffffull) +
+                                          ((p - (p0 + s0)) - rlb);
+      order_next[dst] = rowv[j];
+      keyp_next[dst] = (int32_t)(d[j] == 0 ? kl : kl + E);
+      rpos_next[dst] = rr[j];
+      continue;
+    }
     const int64_t rl = (int64_t)rank[j] - s_pl[s0] + (sk[j] < 0 ? cin : 0);
     const int64_t cs = skj + nd[j];
     const int64_t dst = d[j] == 0 ? cs + rl : cs + ((p - skj) - rl);
@@ -1623,7 +1723,8 @@ __global__ __launch_bounds__(1024) void level_scan_kernel(
       nx.tot_ql_next[c0 + E + lane] = sp ? nx.tot_ql[k0 + lane] - ql : 0;
       nx.tot_c_next[c0 + E + lane] = sp ? R : 0;
       bool both_e = both;
-      if (E > 1) era_child_shifts(k0 + lane, c0 + lane, c0 + E + lane, sp, ps, seg, nx, both_e);
+      if (E > 1)
+        era_child_shifts(k0 + lane, c0 + lane, c0 + E + lane, sp, ps, seg, nx, KeyWords{}, both_e);
       nx.key_list_next[2 * (k0 + lane)] =
           sp ? (int32_t)(c0 + (both_e ? 0 : side * E) + lane) : -1;
       nx.key_list_next[2 * (k0 + lane) + 1] = both_e ? (int32_t)(c0 + E + lane) : -1;
