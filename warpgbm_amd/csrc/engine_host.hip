@@ -117,11 +117,22 @@ struct Engine {
   unsigned long long* best = nullptr;  // packed split picks, two depths (parity)
   int64_t pick_stride = 0;             // words per depth in best / agree_max
   std::vector<void*> allocs;
+  // one allocation for the buffers sized at creation (hipMalloc and hipFree
+  // cost ~5 and ~20 us each here: ~60 buffers took ~1.5 ms per fit)
+  char* arena = nullptr;
+  size_t arena_size = 0, arena_used = 0;
 };
 
 template <typename T>
 static int dalloc(Engine* e, T** p, int64_t n) {
   if (n < 1) n = 1;
+  // from the engine's arena while it has room (256-byte aligned pieces)
+  const size_t bytes = ((size_t)n * sizeof(T) + 255) / 256 * 256;
+  if (e->arena && e->arena_used + bytes <= e->arena_size) {
+    *p = (T*)(e->arena + e->arena_used);
+    e->arena_used += bytes;
+    return 0;
+  }
   void* q = nullptr;
   hipError_t err = hipMalloc(&q, (size_t)n * sizeof(T));
   if (err != hipSuccess) {
@@ -232,6 +243,16 @@ int engine_create(Engine** out, const EngineConfig& cfg) {
                      free_b / 1073741824.0);
       engine_destroy(e);
       return WGBM_ENOMEM;
+    }
+    // the estimate (with its slack) as one arena; without it every buffer
+    // is its own allocation
+    void* a = nullptr;
+    if (hipMalloc(&a, (size_t)need) == hipSuccess) {
+      e->allocs.push_back(a);
+      e->arena = (char*)a;
+      e->arena_size = (size_t)need;
+    } else {
+      (void)hipGetLastError();
     }
   }
   for (int k = 0; k < 2; ++k) {
