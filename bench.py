@@ -538,7 +538,7 @@ def cpu_baseline_leg(codes_h, grad_h, order16_h, seg16_h, N, F, B, step_bytes, r
 
 
 def cpu_train_estimate(cfg, X, y, era=None):
-    """The CPU oracle on an end-to-end config, per BASELINE.md's plan: the
+    """The CPU oracle on an end-to-end config: the
     one-time work (quantile edges and binning of the float32 matrix, none for
     C4's pre-binned codes) timed once, plus ONE tree (C3, C4) or one round
     of K class trees (C5) grown with the oracle's C loops on every OpenMP

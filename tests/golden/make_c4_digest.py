@@ -1,5 +1,5 @@
 """Writes tests/golden/c4_forest_digest.json: the oracle's 100-tree C4 forest
-(500,000 x 2,000 pre-binned int8 codes in {0..4}, 500
+(benchmark config C4: 500,000 x 2,000 pre-binned int8 codes in {0..4}, 500
 eras, num_bins 5, depth 8, lr 0.1; inputs from bench.c4_inputs, numpy
 default_rng(0)), grown by oracle.gbm.Forest with the C loops, as per-tree
 digests (forest_digest.tree_digest) plus digests of the per-era importance
